@@ -1,0 +1,190 @@
+"""ctypes binding of libmx355.so — the MI355X batched-decode-step library.
+
+This module is a thin host-side harness over the C ABI declared in
+include/mx355.h; it is used by the tests and by bench.py.  It never falls back
+to another implementation: if the native library is missing or fails to load,
+importing this module raises.
+
+The package directory name contains a hyphen, so load it with
+``load_package()`` below (or importlib) rather than a plain import.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmx355.so")
+
+MX_OK = 0
+MX_EINVAL = 1
+MX_EUNSUPPORTED = 2
+MX_EHIP = 3
+MX_ENOMEM = 4
+MX_ESTATE = 5
+
+
+class MxError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"mx error {code}: {msg}")
+        self.code = code
+
+
+class QWeightC(C.Structure):
+    _fields_ = [
+        ("codes", C.c_void_p),
+        ("scales", C.c_void_p),
+        ("biases", C.c_void_p),
+        ("n", C.c_int32),
+        ("k", C.c_int32),
+        ("bits", C.c_int32),
+        ("group_size", C.c_int32),
+    ]
+
+
+def _load() -> C.CDLL:
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is not built; run __graft_entry__.build() (make -C rust-mlx_amd/csrc)"
+        )
+    lib = C.CDLL(LIB_PATH)
+    vp, sz, i32, i64, u64, f32 = C.c_void_p, C.c_size_t, C.c_int32, C.c_int64, C.c_uint64, C.c_float
+    sig = {
+        "mx_last_error": ([], C.c_char_p),
+        "mx_abi_version": ([], i32),
+        "mx_malloc": ([C.POINTER(vp), sz], i32),
+        "mx_free": ([vp], i32),
+        "mx_memcpy_htod": ([vp, vp, sz], i32),
+        "mx_memcpy_dtoh": ([vp, vp, sz], i32),
+        "mx_memcpy_dtod": ([vp, vp, sz, vp], i32),
+        "mx_memset": ([vp, C.c_int, sz, vp], i32),
+        "mx_stream_create": ([C.POINTER(vp)], i32),
+        "mx_stream_destroy": ([vp], i32),
+        "mx_stream_sync": ([vp], i32),
+        "mx_device_sync": ([], i32),
+        "mx_event_create": ([C.POINTER(vp)], i32),
+        "mx_event_destroy": ([vp], i32),
+        "mx_event_record": ([vp, vp], i32),
+        "mx_event_elapsed_ms": ([vp, vp, C.POINTER(f32)], i32),
+        "mx_fill_bf16": ([vp, sz, u64, i32, f32, f32, vp], i32),
+        "mx_fill_codes": ([vp, i64, i32, i32, u64, vp], i32),
+        "mx_eval_math": ([i32, vp, vp, i64, vp], i32),
+        "mx_qmv": ([C.POINTER(QWeightC), vp, i32, vp, vp], i32),
+        "mx_dequant_rows": ([C.POINTER(QWeightC), vp, i32, vp, vp], i32),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    return lib
+
+
+lib = _load()
+
+
+def check(rc: int) -> None:
+    if rc != MX_OK:
+        raise MxError(rc, (lib.mx_last_error() or b"").decode())
+
+
+def declared_symbols(header: str) -> list[str]:
+    """Names of every function the C header declares (for export checks)."""
+    import re
+
+    text = open(header).read()
+    return sorted(set(re.findall(r"\b(mx_[a-z0-9_]+)\s*\(", text)))
+
+
+class DeviceArray:
+    """A device allocation with a numpy dtype/shape view for tests and bench."""
+
+    def __init__(self, shape, dtype, zero: bool = False):
+        self.shape = tuple(int(s) for s in (shape if isinstance(shape, (tuple, list)) else (shape,)))
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+        p = C.c_void_p()
+        check(lib.mx_malloc(C.byref(p), max(self.nbytes, 1)))
+        self.ptr = p.value
+        if zero:
+            check(lib.mx_memset(self.ptr, 0, self.nbytes, None))
+
+    @classmethod
+    def from_numpy(cls, a: np.ndarray) -> "DeviceArray":
+        a = np.ascontiguousarray(a)
+        d = cls(a.shape, a.dtype)
+        check(lib.mx_memcpy_htod(d.ptr, a.ctypes.data, d.nbytes))
+        return d
+
+    def upload(self, a: np.ndarray) -> None:
+        a = np.ascontiguousarray(a, dtype=self.dtype)
+        assert a.nbytes == self.nbytes, (a.nbytes, self.nbytes)
+        check(lib.mx_memcpy_htod(self.ptr, a.ctypes.data, self.nbytes))
+
+    def numpy(self) -> np.ndarray:
+        out = np.empty(self.shape, self.dtype)
+        check(lib.mx_memcpy_dtoh(out.ctypes.data, self.ptr, self.nbytes))
+        return out
+
+    def free(self) -> None:
+        if self.ptr:
+            check(lib.mx_free(self.ptr))
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+@dataclass
+class QWeight:
+    """An affine-quantised matrix resident on the device (MLX layout)."""
+
+    codes: DeviceArray
+    scales: DeviceArray
+    biases: DeviceArray
+    n: int
+    k: int
+    bits: int
+    group_size: int
+
+    def c(self) -> QWeightC:
+        return QWeightC(self.codes.ptr, self.scales.ptr, self.biases.ptr, self.n, self.k,
+                        self.bits, self.group_size)
+
+    @classmethod
+    def random(cls, n: int, k: int, bits: int, gs: int, seed: int,
+               s_range=(0.005, 0.03), b_range=(-0.2, 0.2)) -> "QWeight":
+        """Random codes, scales ~ U(s_range), biases ~ U(b_range), on device."""
+        codes = DeviceArray((n, k * bits // 32), np.uint32)
+        scales = DeviceArray((n, k // gs), np.uint16)
+        biases = DeviceArray((n, k // gs), np.uint16)
+        check(lib.mx_fill_codes(codes.ptr, n, k, bits, seed, None))
+        check(lib.mx_fill_bf16(scales.ptr, scales.nbytes // 2, seed + 1, 0, s_range[0], s_range[1], None))
+        check(lib.mx_fill_bf16(biases.ptr, biases.nbytes // 2, seed + 2, 0, b_range[0], b_range[1], None))
+        return cls(codes, scales, biases, n, k, bits, gs)
+
+    def host(self):
+        return self.codes.numpy(), self.scales.numpy(), self.biases.numpy()
+
+
+def qmv(w: QWeight, x: DeviceArray, m: int, y: DeviceArray, stream=None) -> None:
+    qc = w.c()
+    check(lib.mx_qmv(C.byref(qc), x.ptr, m, y.ptr, stream))
+
+
+def dequant_rows(w: QWeight, ids: DeviceArray, count: int, out: DeviceArray, stream=None) -> None:
+    qc = w.c()
+    check(lib.mx_dequant_rows(C.byref(qc), ids.ptr, count, out.ptr, stream))
+
+
+def fill_bf16(d: DeviceArray, seed: int, dist: int, a: float, b: float) -> None:
+    check(lib.mx_fill_bf16(d.ptr, d.nbytes // 2, seed, dist, a, b, None))
+
+
+def sync() -> None:
+    check(lib.mx_device_sync())
