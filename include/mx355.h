@@ -50,6 +50,30 @@ typedef struct mx_qweight {
   int32_t group_size;  /* 32, 64 or 128 */
 } mx_qweight;
 
+/* A bank of equally shaped expert matrices stored back to back (MLX
+ * SwitchLinear layout, reference src/hybrid.rs:129-143 `switch_mlp.*_proj`):
+ * codes [experts, n, k*bits/32], scales/biases bf16 [experts, n, k/group_size]. */
+typedef struct mx_qbank {
+  const uint32_t* codes;
+  const uint16_t* scales;
+  const uint16_t* biases;
+  int32_t experts;
+  int32_t n;
+  int32_t k;
+  int32_t bits;
+  int32_t group_size;
+} mx_qbank;
+
+/* GatedDeltaNet geometry (reference src/hybrid.rs:12-38 HybridConfig
+ * linear_num_{key,value}_heads, linear_{key,value}_head_dim, linear_conv_kernel_dim). */
+typedef struct mx_gdn_dims {
+  int32_t hk;      /* key heads */
+  int32_t hv;      /* value heads (a multiple of hk) */
+  int32_t dk;      /* key head dim (128) */
+  int32_t dv;      /* value head dim (128) */
+  int32_t conv_k;  /* depthwise conv taps */
+} mx_gdn_dims;
+
 /* ---- errors / version -------------------------------------------------- */
 const char* mx_last_error(void);
 int32_t mx_abi_version(void);
@@ -97,6 +121,115 @@ mx_status mx_qmv(const mx_qweight* w, const uint16_t* x, int32_t m, uint16_t* y,
  * (src/weights.rs:203-226: take_axis + ops::dequantize). */
 mx_status mx_dequant_rows(const mx_qweight* w, const uint32_t* ids, int32_t count,
                           uint16_t* out, void* stream);
+
+/* ---- A6: MoE routing tail -----------------------------------------------
+ * Per row: softmax of `experts` bf16 logits (fp32), bf16 gates, top_k by the
+ * (bf16 gate, expert id) key — ids[row, k-1] is the largest, as the reference
+ * slices the last k of an ascending sort — bf16 renormalised scores, and
+ * factor = bf16 sigmoid(shared_logit).  Rows are `logit_stride` /
+ * `shared_stride` elements apart, so both may point into one fused projection
+ * output.  Replaces moe_route::tail (src/moe_route.rs:25-70,
+ * kernels/moe_route_tail.{h,metal}) and the native softmax / argpartition /
+ * renormalise of MoE::parts (src/hybrid.rs:217-222, 284). */
+mx_status mx_moe_route(const uint16_t* logits, int64_t logit_stride, const uint16_t* shared_logit,
+                       int64_t shared_stride, int32_t rows, int32_t experts, int32_t top_k,
+                       uint32_t* ids, uint16_t* scores, uint16_t* factor, void* stream);
+
+/* ---- A7+A8: gathered expert MLPs ------------------------------------------
+ * For every row r and slot j < top_k, expert e = ids[r, j]:
+ *   h = bf16(bf16(silu(bf16(gate_e x))) * bf16(up_e x)),
+ *   partial[r, j] = bf16(bf16(down_e h) * scores[r, j]);
+ * slot top_k holds the shared expert's bf16(down(h)), unweighted.
+ * partial is bf16 [rows, top_k + 1, hidden]; workspace holds
+ * mx_moe_workspace_bytes(rows, top_k, max(inter, shared inter)) bytes.
+ * Routes naming the same expert are served together, so each selected
+ * expert's weights stream once per call.  Replaces moe_kernel::gate_up
+ * (src/moe_kernel.rs:10-118), the gather_qmm gate/up/down of MoE::parts
+ * (src/hybrid.rs:245-271), moe_down::reduce's expert QMV + score product
+ * (src/moe_down.rs:34-137) and the shared Mlp (src/dense.rs:292-298). */
+size_t mx_moe_workspace_bytes(int32_t rows, int32_t top_k, int32_t inter);
+mx_status mx_moe_experts(const uint16_t* x, const uint32_t* ids, const uint16_t* scores,
+                         int32_t rows, int32_t top_k, const mx_qbank* gate, const mx_qbank* up,
+                         const mx_qbank* down, const mx_qweight* shared_gate,
+                         const mx_qweight* shared_up, const mx_qweight* shared_down,
+                         void* workspace, uint16_t* partial, void* stream);
+/* routed[r] = bf16 sum of partial[r, 0..top_k-1] in the reference's slot
+ * order (kernels/moe_down_tail.h:20, moe_down_tail.metal:83-99). */
+mx_status mx_moe_reduce(const uint16_t* partial, int32_t rows, int32_t top_k, int32_t hidden,
+                        uint16_t* routed, void* stream);
+
+/* ---- A9: MoE hyper-connection epilogue ------------------------------------
+ * out[r, s, c] = bf16(residual[r, s, c] + bf16(bf16(routed + bf16(shared * factor[r]))
+ *                                               * gate[r, s]))
+ * Replaces moe_epilogue::apply (src/moe_epilogue.rs:17-73,
+ * kernels/moe_hc_epilogue.metal) / HyperConnection::write after MoE::forward
+ * (src/hybrid.rs:100-105, 292-307).  out may alias residual. */
+mx_status mx_moe_hc_epilogue(const uint16_t* routed, const uint16_t* shared,
+                             const uint16_t* factor, const uint16_t* residual,
+                             const uint16_t* gate, int32_t rows, int32_t hc, int32_t hidden,
+                             uint16_t* out, void* stream);
+/* mx_moe_reduce followed by mx_moe_hc_epilogue with shared = partial[r, top_k],
+ * in one pass (same bits). */
+mx_status mx_moe_reduce_hc_epilogue(const uint16_t* partial, const uint16_t* factor,
+                                    const uint16_t* residual, const uint16_t* gate, int32_t rows,
+                                    int32_t top_k, int32_t hc, int32_t hidden, uint16_t* out,
+                                    void* stream);
+
+/* ---- A14: greedy head ------------------------------------------------------
+ * tokens[m] = argmax_n bf16(head_n . x_m): largest value, lowest id on ties,
+ * NaN never wins, 0 when nothing exceeds -inf.  Logits are reduced on chip
+ * and never written.  workspace: mx_head_workspace_bytes(n, k, m) bytes.
+ * Replaces greedy_head::project (src/greedy_head.rs:40-126,
+ * kernels/greedy_{head,reduce}.metal) and the default
+ * argmax_axis(head.forward_rows(x)) (src/bin/batch-bench.rs:118-120). */
+size_t mx_head_workspace_bytes(int32_t n, int32_t k, int32_t m);
+mx_status mx_head_argmax(const mx_qweight* w, const uint16_t* x, int32_t m, uint32_t* tokens,
+                         void* workspace, void* stream);
+/* argmax over bf16 logits [rows, n] with the same rule (MLX argmax_axis). */
+mx_status mx_argmax_bf16(const uint16_t* logits, int32_t rows, int32_t n, uint32_t* tokens,
+                         void* stream);
+
+/* ---- A10/A11/A12: GatedDeltaNet -------------------------------------------
+ * Rows are `groups` sequences of `t` consecutive tokens (row = g*t + i);
+ * slots[g] (device int32) selects the group's cached conv window and state.
+ *
+ * mx_gdn_conv: causal depthwise conv of the cached window and the new qkv
+ * rows, then SiLU; out[row] = bf16(silu(bf16(sum_j x_j * w[j]))) per channel.
+ * conv_state bf16 [slots, conv_k-1, channels] is updated in place; conv_w is
+ * fp32 [conv_k, channels]; window_history (nullable) receives the full window
+ * bf16 [groups, conv_k-1+t, channels] for verify rollback.  Replaces
+ * compiled::decode_conv + silu and the conv-state slice of
+ * Gdn::forward_reference (src/compiled.rs:88-95, src/hybrid.rs:374-400). */
+mx_status mx_gdn_conv(const uint16_t* qkv, int64_t row_stride, int32_t groups, int32_t t,
+                      const int32_t* slots, uint16_t* conv_state, const float* conv_w,
+                      int32_t channels, int32_t conv_k, uint16_t* out, int64_t out_stride,
+                      uint16_t* window_history, void* stream);
+/* mx_gdn_recurrence: q/k L2 norm (q scaled by dk^-1/2), beta = sigmoid(b),
+ * g = exp(-exp(a_log) * softplus(a + dt_bias)), the delta rule on the fp32
+ * state, and the gated RMS norm y = rms_norm(o, norm_w, eps) * sigmoid(z).
+ * conv_out rows hold [q (hk*dk) | k (hk*dk) | v (hv*dv)]; z, a, b rows are
+ * zab_stride elements apart.  state fp32 [slots, hv, dk, dv] is updated in
+ * place (note: dk-major, the transpose of MLX's [B, Hv, Dv, Dk]); history
+ * (nullable) receives the state after every token, fp32 [groups*t, hv, dk, dv].
+ * y is bf16 [groups*t, hv*dv].  Replaces gdn_kernel::recurrent /
+ * recurrent_with_history (src/gdn_kernel.rs:7-142, kernels/gated_delta{,_history}.metal)
+ * with the surrounding ops of Gdn::forward_reference (src/hybrid.rs:401-453). */
+mx_status mx_gdn_recurrence(const uint16_t* conv_out, int64_t conv_stride, const uint16_t* z,
+                            const uint16_t* a, const uint16_t* b, int64_t zab_stride,
+                            const float* a_log, const uint16_t* dt_bias, const uint16_t* norm_w,
+                            float eps, const mx_gdn_dims* dims, int32_t groups, int32_t t,
+                            const int32_t* slots, float* state, float* history, uint16_t* y,
+                            void* stream);
+
+/* mx_gdn_scan: the delta rule alone, on given inputs — the reference's
+ * gdn_kernel::recurrent / recurrent_with_history interface (src/gdn_kernel.rs:7-142):
+ * q, k bf16 [groups*t, hk, dk] (already normalised), v bf16 [groups*t, hv, dv],
+ * g fp32 [groups*t, hv], beta bf16 [groups*t, hv]; y = bf16(state . q)
+ * [groups*t, hv, dv]; state / history as for mx_gdn_recurrence. */
+mx_status mx_gdn_scan(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
+                      const uint16_t* beta, const mx_gdn_dims* dims, int32_t groups, int32_t t,
+                      const int32_t* slots, float* state, float* history, uint16_t* y,
+                      void* stream);
 
 #ifdef __cplusplus
 }

@@ -207,44 +207,49 @@ static int lanes_per_row(int k) {
   return L;
 }
 
-/* Affine QMV, restating MLX's  s*sum(x q) + b*sum(x)  per group (reference
- * kernels/verify_qmv.h:112, verify_qmv.metal:30-64) in the build's fixed
- * order: 32-value chunks (fma chain over j, sequential sum of x), per-chunk
- * fma(s, acc, b*sx), lane l of L sums chunks c = l mod L in ascending order,
- * xor butterfly over L lanes, bf16 round. */
-void mxo_qmv(const uint32_t* codes, const uint16_t* scales, const uint16_t* biases, int n, int k,
-             int bits, int gs, const uint16_t* x, int m, uint16_t* y) {
+/* One output row of the affine QMV before the final bf16 rounding, restating
+ * MLX's  s*sum(x q) + b*sum(x)  per group (reference kernels/verify_qmv.h:112,
+ * verify_qmv.metal:30-64) in the build's fixed order: 32-value chunks (fma
+ * chain over j from +0, sequential sum of x), per-chunk fma(s, acc, b*sx),
+ * lane l of L sums chunks c = l mod L in ascending order, xor butterfly over
+ * the L lanes (offsets L/2 .. 1).  L depends on k only, so the value of a row
+ * never depends on how many activation rows share the weight stream. */
+float mxo_qmv_row(const uint32_t* rw, const uint16_t* srow, const uint16_t* brow, int k, int bits,
+                  int gs, const uint16_t* xr) {
   const int chunks = k / 32;
   const int L = lanes_per_row(k);
+  float lane[64], tmp[64];
+  for (int l = 0; l < L; ++l) lane[l] = 0.0f;
+  for (int c = 0; c < chunks; ++c) {
+    float acc = 0.0f, sx = 0.0f;
+    for (int j = 0; j < 32; ++j) {
+      const float xv = mxo_bf16_to_f32(xr[32 * c + j]);
+      const float q = (float)mxo_code(rw, 32 * c + j, bits);
+      acc = fmaf(xv, q, acc);
+      sx = sx + xv;
+    }
+    const int g = (32 * c) / gs;
+    const float s = mxo_bf16_to_f32(srow[g]);
+    const float b = mxo_bf16_to_f32(brow[g]);
+    lane[c % L] = lane[c % L] + fmaf(s, acc, b * sx);
+  }
+  for (int o = L >> 1; o > 0; o >>= 1) {
+    for (int l = 0; l < L; ++l) tmp[l] = lane[l] + lane[l ^ o];
+    for (int l = 0; l < L; ++l) lane[l] = tmp[l];
+  }
+  return lane[0];
+}
+
+void mxo_qmv(const uint32_t* codes, const uint16_t* scales, const uint16_t* biases, int n, int k,
+             int bits, int gs, const uint16_t* x, int m, uint16_t* y) {
   const int64_t wpr = ((int64_t)k * bits) >> 5;
   const int gpr = k / gs;
 #pragma omp parallel for schedule(static)
   for (int row = 0; row < n; ++row) {
-    const uint32_t* rw = codes + (int64_t)row * wpr;
-    for (int mm = 0; mm < m; ++mm) {
-      const uint16_t* xr = x + (int64_t)mm * k;
-      float lane[64];
-      float tmp[64];
-      for (int l = 0; l < L; ++l) lane[l] = 0.0f;
-      for (int c = 0; c < chunks; ++c) {
-        float acc = 0.0f, sx = 0.0f;
-        for (int j = 0; j < 32; ++j) {
-          const float xv = mxo_bf16_to_f32(xr[32 * c + j]);
-          const float q = (float)mxo_code(rw, 32 * c + j, bits);
-          acc = fmaf(xv, q, acc);
-          sx = sx + xv;
-        }
-        const int g = (32 * c) / gs;
-        const float s = mxo_bf16_to_f32(scales[(int64_t)row * gpr + g]);
-        const float b = mxo_bf16_to_f32(biases[(int64_t)row * gpr + g]);
-        lane[c % L] = lane[c % L] + fmaf(s, acc, b * sx);
-      }
-      for (int o = L >> 1; o > 0; o >>= 1) {
-        for (int l = 0; l < L; ++l) tmp[l] = lane[l] + lane[l ^ o];
-        for (int l = 0; l < L; ++l) lane[l] = tmp[l];
-      }
-      y[(int64_t)mm * n + row] = mxo_f32_to_bf16(lane[0]);
-    }
+    for (int mm = 0; mm < m; ++mm)
+      y[(int64_t)mm * n + row] =
+          mxo_f32_to_bf16(mxo_qmv_row(codes + (int64_t)row * wpr, scales + (int64_t)row * gpr,
+                                      biases + (int64_t)row * gpr, k, bits, gs, x + (int64_t)mm * k));
   }
 }
 

@@ -40,10 +40,58 @@ uint32_t mxo_code(const uint32_t* row_words, int k, int bits);
 void mxo_dequant_rows(const uint32_t* codes, const uint16_t* scales, const uint16_t* biases,
                       int n, int k, int bits, int gs, const uint32_t* ids, int count,
                       uint16_t* out);
+float mxo_qmv_row(const uint32_t* row_words, const uint16_t* scale_row, const uint16_t* bias_row,
+                  int k, int bits, int gs, const uint16_t* x);
 void mxo_qmv(const uint32_t* codes, const uint16_t* scales, const uint16_t* biases, int n, int k,
              int bits, int gs, const uint16_t* x, int m, uint16_t* y);
 void mxo_qmv_f64(const uint32_t* codes, const uint16_t* scales, const uint16_t* biases, int n,
                  int k, int bits, int gs, const uint16_t* x, int m, double* y);
+
+/* ---- quantised weights as plain structs ---- */
+typedef struct mxo_qw {
+  const uint32_t* codes;
+  const uint16_t* scales;
+  const uint16_t* biases;
+  int n, k, bits, gs;
+} mxo_qw;
+typedef struct mxo_qbank {
+  const uint32_t* codes;
+  const uint16_t* scales;
+  const uint16_t* biases;
+  int experts, n, k, bits, gs;
+} mxo_qbank;
+
+/* ---- A6-A9: MoE ---- */
+float mxo_sigmoid_bf16(float x);
+float mxo_softplus_bf16(float x);
+void mxo_moe_route(const uint16_t* logits, int64_t logit_stride, const uint16_t* shared_logit,
+                   int64_t shared_stride, int rows, int experts, int top_k, uint32_t* ids,
+                   uint16_t* scores, uint16_t* factor);
+void mxo_moe_experts(const uint16_t* x, const uint32_t* ids, const uint16_t* scores, int rows,
+                     int top_k, const mxo_qbank* gate, const mxo_qbank* up, const mxo_qbank* down,
+                     const mxo_qw* sgate, const mxo_qw* sup, const mxo_qw* sdown, uint16_t* p);
+void mxo_moe_reduce(const uint16_t* p, int rows, int top_k, int hidden, uint16_t* routed);
+void mxo_moe_hc_epilogue(const uint16_t* routed, const uint16_t* shared, const uint16_t* factor,
+                         const uint16_t* residual, const uint16_t* gate, int rows, int hc,
+                         int hidden, uint16_t* out);
+
+/* ---- A10-A12: GatedDeltaNet ---- */
+void mxo_gdn_conv(const uint16_t* qkv, int64_t row_stride, int groups, int t, const int32_t* slots,
+                  uint16_t* conv_state, const float* w, int channels, int taps, uint16_t* out,
+                  int64_t out_stride, uint16_t* window_history);
+void mxo_gdn_recurrence(const uint16_t* conv_out, int64_t conv_stride, const uint16_t* z,
+                        const uint16_t* a, const uint16_t* b, int64_t zab_stride,
+                        const float* a_log, const uint16_t* dt_bias, const uint16_t* norm_w,
+                        float eps, int hk_heads, int hv_heads, int groups, int t,
+                        const int32_t* slots, float* state, float* history, uint16_t* y);
+
+void mxo_gdn_scan(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
+                  const uint16_t* beta, int hk_heads, int hv_heads, int groups, int t,
+                  const int32_t* slots, float* state, float* history, uint16_t* y);
+
+/* ---- A14: greedy head ---- */
+void mxo_argmax_bf16(const uint16_t* logits, int rows, int n, uint32_t* tokens);
+void mxo_head_argmax(const mxo_qw* w, const uint16_t* x, int m, uint32_t* tokens, float* scratch);
 
 int mxo_num_threads(void);
 

@@ -45,6 +45,24 @@ class QWeightC(C.Structure):
     ]
 
 
+class QBankC(C.Structure):
+    _fields_ = [
+        ("codes", C.c_void_p),
+        ("scales", C.c_void_p),
+        ("biases", C.c_void_p),
+        ("experts", C.c_int32),
+        ("n", C.c_int32),
+        ("k", C.c_int32),
+        ("bits", C.c_int32),
+        ("group_size", C.c_int32),
+    ]
+
+
+class GdnDimsC(C.Structure):
+    _fields_ = [("hk", C.c_int32), ("hv", C.c_int32), ("dk", C.c_int32), ("dv", C.c_int32),
+                ("conv_k", C.c_int32)]
+
+
 def _load() -> C.CDLL:
     if not os.path.exists(LIB_PATH):
         raise ImportError(
@@ -74,6 +92,22 @@ def _load() -> C.CDLL:
         "mx_eval_math": ([i32, vp, vp, i64, vp], i32),
         "mx_qmv": ([C.POINTER(QWeightC), vp, i32, vp, vp], i32),
         "mx_dequant_rows": ([C.POINTER(QWeightC), vp, i32, vp, vp], i32),
+        "mx_moe_route": ([vp, i64, vp, i64, i32, i32, i32, vp, vp, vp, vp], i32),
+        "mx_moe_workspace_bytes": ([i32, i32, i32], sz),
+        "mx_moe_experts": ([vp, vp, vp, i32, i32, C.POINTER(QBankC), C.POINTER(QBankC),
+                            C.POINTER(QBankC), C.POINTER(QWeightC), C.POINTER(QWeightC),
+                            C.POINTER(QWeightC), vp, vp, vp], i32),
+        "mx_moe_reduce": ([vp, i32, i32, i32, vp, vp], i32),
+        "mx_moe_hc_epilogue": ([vp, vp, vp, vp, vp, i32, i32, i32, vp, vp], i32),
+        "mx_moe_reduce_hc_epilogue": ([vp, vp, vp, vp, i32, i32, i32, i32, vp, vp], i32),
+        "mx_head_workspace_bytes": ([i32, i32, i32], sz),
+        "mx_head_argmax": ([C.POINTER(QWeightC), vp, i32, vp, vp, vp], i32),
+        "mx_argmax_bf16": ([vp, i32, i32, vp, vp], i32),
+        "mx_gdn_conv": ([vp, i64, i32, i32, vp, vp, vp, i32, i32, vp, i64, vp, vp], i32),
+        "mx_gdn_recurrence": ([vp, i64, vp, vp, vp, i64, vp, vp, vp, f32, C.POINTER(GdnDimsC),
+                               i32, i32, vp, vp, vp, vp, vp], i32),
+        "mx_gdn_scan": ([vp, vp, vp, vp, vp, C.POINTER(GdnDimsC), i32, i32, vp, vp, vp, vp,
+                         vp], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -167,6 +201,34 @@ class QWeight:
         check(lib.mx_fill_bf16(scales.ptr, scales.nbytes // 2, seed + 1, 0, s_range[0], s_range[1], None))
         check(lib.mx_fill_bf16(biases.ptr, biases.nbytes // 2, seed + 2, 0, b_range[0], b_range[1], None))
         return cls(codes, scales, biases, n, k, bits, gs)
+
+    def host(self):
+        return self.codes.numpy(), self.scales.numpy(), self.biases.numpy()
+
+
+@dataclass
+class QBank:
+    """A bank of equally shaped quantised expert matrices on the device."""
+
+    codes: DeviceArray
+    scales: DeviceArray
+    biases: DeviceArray
+    experts: int
+    n: int
+    k: int
+    bits: int
+    group_size: int
+
+    def c(self) -> QBankC:
+        return QBankC(self.codes.ptr, self.scales.ptr, self.biases.ptr, self.experts, self.n,
+                      self.k, self.bits, self.group_size)
+
+    @classmethod
+    def random(cls, experts: int, n: int, k: int, bits: int, gs: int, seed: int,
+               s_range=(0.005, 0.03), b_range=(-0.2, 0.2)) -> "QBank":
+        """Same streams as QWeight.random of an [experts*n, k] matrix."""
+        q = QWeight.random(experts * n, k, bits, gs, seed, s_range, b_range)
+        return cls(q.codes, q.scales, q.biases, experts, n, k, bits, gs)
 
     def host(self):
         return self.codes.numpy(), self.scales.numpy(), self.biases.numpy()

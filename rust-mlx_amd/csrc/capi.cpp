@@ -177,3 +177,194 @@ MX_ABI mx_status mx_dequant_rows(const mx_qweight* w, const uint32_t* ids, int32
   MX_CHECK(count <= 65535, MX_EUNSUPPORTED, "mx_dequant_rows: count must be <= 65535");
   return finish(dequant_rows(q, ids, count, out, hipStream_t(stream)), "mx_dequant_rows");
 }
+
+// ---- MoE ------------------------------------------------------------------
+namespace {
+const char* check_bank(const QBank& b) {
+  if (b.experts <= 0) return "bank needs at least one expert";
+  const QWeight w{b.codes, b.scales, b.biases, b.n, b.k, b.bits, b.group_size};
+  return check_qweight(w);
+}
+}  // namespace
+
+MX_ABI mx_status mx_moe_route(const uint16_t* logits, int64_t logit_stride,
+                              const uint16_t* shared_logit, int64_t shared_stride, int32_t rows,
+                              int32_t experts, int32_t top_k, uint32_t* ids, uint16_t* scores,
+                              uint16_t* factor, void* stream) {
+  MX_CHECK(rows >= 0, MX_EINVAL, "mx_moe_route: negative rows");
+  if (rows == 0) return MX_OK;
+  MX_CHECK(logits && shared_logit && ids && scores && factor, MX_EINVAL,
+           "mx_moe_route: null pointer");
+  MX_CHECK(experts % 64 == 0 && (experts / 64 == 1 || experts / 64 == 2 || experts / 64 == 4 ||
+                                 experts / 64 == 8 || experts / 64 == 16),
+           MX_EUNSUPPORTED, "mx_moe_route: experts must be 64, 128, 256, 512 or 1024");
+  MX_CHECK(top_k >= 1 && top_k <= 16, MX_EUNSUPPORTED, "mx_moe_route: top_k must be in 1..16");
+  MX_CHECK(logit_stride >= experts && shared_stride >= 1, MX_EINVAL,
+           "mx_moe_route: row strides too small");
+  return finish(moe_route(logits, logit_stride, shared_logit, shared_stride, rows, experts, top_k,
+                          ids, scores, factor, hipStream_t(stream)),
+                "mx_moe_route");
+}
+
+MX_ABI size_t mx_moe_workspace_bytes(int32_t rows, int32_t top_k, int32_t inter) {
+  if (rows <= 0 || top_k <= 0 || inter <= 0) return 0;
+  return size_t(rows) * (top_k + 1) * inter * sizeof(uint16_t);
+}
+
+MX_ABI mx_status mx_moe_experts(const uint16_t* x, const uint32_t* ids, const uint16_t* scores,
+                                int32_t rows, int32_t top_k, const mx_qbank* gate,
+                                const mx_qbank* up, const mx_qbank* down,
+                                const mx_qweight* shared_gate, const mx_qweight* shared_up,
+                                const mx_qweight* shared_down, void* workspace, uint16_t* partial,
+                                void* stream) {
+  MX_CHECK(x && ids && scores && gate && up && down && shared_gate && shared_up && shared_down &&
+               workspace && partial,
+           MX_EINVAL, "mx_moe_experts: null pointer");
+  MX_CHECK(rows >= 1 && rows <= 8, MX_EUNSUPPORTED, "mx_moe_experts: rows must be in 1..8");
+  MX_CHECK(top_k >= 1 && top_k <= 16, MX_EUNSUPPORTED, "mx_moe_experts: top_k must be in 1..16");
+  const QBank g = to_qbank(*gate), u = to_qbank(*up), d = to_qbank(*down);
+  const QWeight sg = to_qweight(*shared_gate), su = to_qweight(*shared_up),
+                sd = to_qweight(*shared_down);
+  for (const QBank* b : {&g, &u, &d})
+    if (const char* err = check_bank(*b))
+      return mx_status(set_error(MX_EINVAL, std::string("mx_moe_experts: ") + err));
+  for (const QWeight* w : {&sg, &su, &sd})
+    if (const char* err = check_qweight(*w))
+      return mx_status(set_error(MX_EINVAL, std::string("mx_moe_experts: shared ") + err));
+  MX_CHECK(g.n == u.n && g.k == u.k && d.k == g.n && d.n == g.k && g.experts == u.experts &&
+               g.experts == d.experts && g.bits == u.bits && g.group_size == u.group_size,
+           MX_EINVAL, "mx_moe_experts: gate/up/down banks disagree in shape");
+  MX_CHECK(sg.n == su.n && sg.k == g.k && su.k == g.k && sd.k == sg.n && sd.n == g.k &&
+               sg.bits == su.bits && sg.group_size == su.group_size && sd.bits == d.bits &&
+               sd.group_size == d.group_size && sg.bits == g.bits &&
+               sg.group_size == g.group_size,
+           MX_EINVAL, "mx_moe_experts: shared expert disagrees with the banks");
+  return finish(moe_experts(x, ids, scores, rows, top_k, g, u, d, sg, su, sd,
+                            static_cast<uint16_t*>(workspace), partial, hipStream_t(stream)),
+                "mx_moe_experts");
+}
+
+MX_ABI mx_status mx_moe_reduce(const uint16_t* partial, int32_t rows, int32_t top_k,
+                               int32_t hidden, uint16_t* routed, void* stream) {
+  MX_CHECK(rows >= 0 && hidden > 0 && top_k >= 1, MX_EINVAL, "mx_moe_reduce: bad shape");
+  if (rows == 0) return MX_OK;
+  MX_CHECK(partial && routed, MX_EINVAL, "mx_moe_reduce: null pointer");
+  return finish(moe_reduce(partial, rows, top_k, hidden, routed, hipStream_t(stream)),
+                "mx_moe_reduce");
+}
+
+MX_ABI mx_status mx_moe_hc_epilogue(const uint16_t* routed, const uint16_t* shared,
+                                    const uint16_t* factor, const uint16_t* residual,
+                                    const uint16_t* gate, int32_t rows, int32_t hc,
+                                    int32_t hidden, uint16_t* out, void* stream) {
+  MX_CHECK(rows >= 0 && hc >= 1 && hidden > 0, MX_EINVAL, "mx_moe_hc_epilogue: bad shape");
+  if (rows == 0) return MX_OK;
+  MX_CHECK(routed && shared && factor && residual && gate && out, MX_EINVAL,
+           "mx_moe_hc_epilogue: null pointer");
+  return finish(moe_hc_epilogue(routed, shared, factor, residual, gate, rows, hc, hidden, out,
+                                hipStream_t(stream)),
+                "mx_moe_hc_epilogue");
+}
+
+MX_ABI mx_status mx_moe_reduce_hc_epilogue(const uint16_t* partial, const uint16_t* factor,
+                                           const uint16_t* residual, const uint16_t* gate,
+                                           int32_t rows, int32_t top_k, int32_t hc,
+                                           int32_t hidden, uint16_t* out, void* stream) {
+  MX_CHECK(rows >= 0 && hc >= 1 && hidden > 0 && top_k >= 1, MX_EINVAL,
+           "mx_moe_reduce_hc_epilogue: bad shape");
+  if (rows == 0) return MX_OK;
+  MX_CHECK(partial && factor && residual && gate && out, MX_EINVAL,
+           "mx_moe_reduce_hc_epilogue: null pointer");
+  return finish(moe_reduce_hc_epilogue(partial, factor, residual, gate, rows, top_k, hc, hidden,
+                                       out, hipStream_t(stream)),
+                "mx_moe_reduce_hc_epilogue");
+}
+
+// ---- greedy head ----------------------------------------------------------
+MX_ABI size_t mx_head_workspace_bytes(int32_t n, int32_t k, int32_t m) {
+  if (n <= 0 || k <= 0 || m <= 0) return 0;
+  return size_t(head_parts(n, k)) * m * (sizeof(float) + sizeof(uint32_t));
+}
+
+MX_ABI mx_status mx_head_argmax(const mx_qweight* w, const uint16_t* x, int32_t m,
+                                uint32_t* tokens, void* workspace, void* stream) {
+  MX_CHECK(w && x && tokens && workspace, MX_EINVAL, "mx_head_argmax: null pointer");
+  const QWeight q = to_qweight(*w);
+  if (const char* err = check_qweight(q))
+    return mx_status(set_error(MX_EINVAL, std::string("mx_head_argmax: ") + err));
+  MX_CHECK(m >= 1 && m <= 8, MX_EUNSUPPORTED, "mx_head_argmax: m must be in 1..8");
+  const int parts = head_parts(q.n, q.k);
+  float* maxima = static_cast<float*>(workspace);
+  uint32_t* indices = reinterpret_cast<uint32_t*>(maxima + size_t(parts) * m);
+  int got = 0;
+  int rc = head_partials(q, x, m, maxima, indices, &got, hipStream_t(stream));
+  if (rc != MX_OK) return finish(rc, "mx_head_argmax");
+  return finish(argmax_reduce(maxima, indices, m, parts, tokens, hipStream_t(stream)),
+                "mx_head_argmax");
+}
+
+MX_ABI mx_status mx_argmax_bf16(const uint16_t* logits, int32_t rows, int32_t n, uint32_t* tokens,
+                                void* stream) {
+  MX_CHECK(rows >= 0 && n > 0, MX_EINVAL, "mx_argmax_bf16: bad shape");
+  if (rows == 0) return MX_OK;
+  MX_CHECK(logits && tokens, MX_EINVAL, "mx_argmax_bf16: null pointer");
+  return finish(argmax_bf16(logits, rows, n, tokens, hipStream_t(stream)), "mx_argmax_bf16");
+}
+
+// ---- GatedDeltaNet --------------------------------------------------------
+MX_ABI mx_status mx_gdn_conv(const uint16_t* qkv, int64_t row_stride, int32_t groups, int32_t t,
+                             const int32_t* slots, uint16_t* conv_state, const float* conv_w,
+                             int32_t channels, int32_t conv_k, uint16_t* out, int64_t out_stride,
+                             uint16_t* window_history, void* stream) {
+  MX_CHECK(groups >= 0 && t >= 1 && channels > 0, MX_EINVAL, "mx_gdn_conv: bad shape");
+  if (groups == 0) return MX_OK;
+  MX_CHECK(qkv && slots && conv_state && conv_w && out, MX_EINVAL, "mx_gdn_conv: null pointer");
+  MX_CHECK(conv_k >= 2 && conv_k <= 8, MX_EUNSUPPORTED, "mx_gdn_conv: conv_k must be in 2..8");
+  MX_CHECK(row_stride >= channels && out_stride >= channels, MX_EINVAL,
+           "mx_gdn_conv: row strides too small");
+  return finish(gdn_conv(qkv, row_stride, groups, t, slots, conv_state, conv_w, channels, conv_k,
+                         out, out_stride, window_history, hipStream_t(stream)),
+                "mx_gdn_conv");
+}
+
+MX_ABI mx_status mx_gdn_recurrence(const uint16_t* conv_out, int64_t conv_stride,
+                                   const uint16_t* z, const uint16_t* a, const uint16_t* b,
+                                   int64_t zab_stride, const float* a_log,
+                                   const uint16_t* dt_bias, const uint16_t* norm_w, float eps,
+                                   const mx_gdn_dims* dims, int32_t groups, int32_t t,
+                                   const int32_t* slots, float* state, float* history,
+                                   uint16_t* y, void* stream) {
+  MX_CHECK(dims != nullptr, MX_EINVAL, "mx_gdn_recurrence: null dims");
+  MX_CHECK(groups >= 0 && t >= 1, MX_EINVAL, "mx_gdn_recurrence: bad shape");
+  if (groups == 0) return MX_OK;
+  MX_CHECK(conv_out && z && a && b && a_log && dt_bias && norm_w && slots && state && y,
+           MX_EINVAL, "mx_gdn_recurrence: null pointer");
+  const GdnDims d{dims->hk, dims->hv, dims->dk, dims->dv, dims->conv_k};
+  MX_CHECK(d.hk > 0 && d.hv > 0 && d.hv % d.hk == 0, MX_EINVAL,
+           "mx_gdn_recurrence: value heads must be a multiple of key heads");
+  MX_CHECK(d.dk == 128 && d.dv == 128, MX_EUNSUPPORTED,
+           "mx_gdn_recurrence: head dims must be 128");
+  MX_CHECK(conv_stride >= int64_t(2) * d.hk * d.dk + int64_t(d.hv) * d.dv, MX_EINVAL,
+           "mx_gdn_recurrence: conv row stride too small");
+  return finish(gdn_recurrence(conv_out, conv_stride, z, a, b, zab_stride, a_log, dt_bias, norm_w,
+                               eps, d, groups, t, slots, state, history, y, hipStream_t(stream)),
+                "mx_gdn_recurrence");
+}
+
+MX_ABI mx_status mx_gdn_scan(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                             const float* g, const uint16_t* beta, const mx_gdn_dims* dims,
+                             int32_t groups, int32_t t, const int32_t* slots, float* state,
+                             float* history, uint16_t* y, void* stream) {
+  MX_CHECK(dims != nullptr, MX_EINVAL, "mx_gdn_scan: null dims");
+  MX_CHECK(groups >= 0 && t >= 1, MX_EINVAL, "mx_gdn_scan: bad shape");
+  if (groups == 0) return MX_OK;
+  MX_CHECK(q && k && v && g && beta && slots && state && y, MX_EINVAL,
+           "mx_gdn_scan: null pointer");
+  const GdnDims d{dims->hk, dims->hv, dims->dk, dims->dv, dims->conv_k};
+  MX_CHECK(d.hk > 0 && d.hv > 0 && d.hv % d.hk == 0, MX_EINVAL,
+           "mx_gdn_scan: value heads must be a multiple of key heads");
+  MX_CHECK(d.dk == 128 && d.dv == 128, MX_EUNSUPPORTED, "mx_gdn_scan: head dims must be 128");
+  return finish(gdn_scan(q, k, v, g, beta, d, groups, t, slots, state, history, y,
+                         hipStream_t(stream)),
+                "mx_gdn_scan");
+}

@@ -1,0 +1,270 @@
+// GatedDeltaNet decode / verify kernels for gfx950.
+//
+// Reference: Gdn::forward_reference (src/hybrid.rs:369-455) with the compiled
+// graphs decode_conv / decay / silu (src/compiled.rs:13-21, 88-95) and the
+// recurrence kernel gdn_kernel::recurrent{,_with_history} (src/gdn_kernel.rs:7-142,
+// kernels/gated_delta{,_history}.metal).
+//
+// Rows are organised as `groups` independent sequences of `t` consecutive
+// tokens each (row = g * t + i): decode of B slots is groups = B, t = 1; an
+// MTP verify block or a prefill chunk of one slot is groups = 1, t = T.
+// `slots[g]` selects the recurrent state of group g.
+//
+// State layout (HBM): fp32 [slots, Hv, Dk, Dv] — dk-major, so the 128 lanes
+// that own the 128 value rows of a head read and write it fully coalesced.
+// (MLX keeps [B, Hv, Dv, Dk]; the C ABI documents the transposition.)
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace mx {
+
+namespace {
+
+// bf16 logistic with per-operation bf16 rounding (MLX Sigmoid at bfloat).
+__device__ __forceinline__ float sigmoid_bf16(float x) {
+  const float e = round_bf16(expf_(__builtin_fabsf(x)));
+  const float d = round_bf16(1.0f + e);
+  const float y = round_bf16(1.0f / d);
+  return x < 0.0f ? y : round_bf16(1.0f - y);
+}
+
+// logaddexp(x, 0) at bfloat (MLX LogAddExp with per-operation bf16 rounding).
+__device__ __forceinline__ float softplus_bf16(float x) {
+  if (x != x) return x;
+  const float hi = x > 0.0f ? x : 0.0f;
+  const float lo = x > 0.0f ? 0.0f : x;
+  if (hi == u2f(0x7f800000u) || lo == u2f(0xff800000u)) return hi;
+  const float d = round_bf16(lo - hi);
+  const float e = round_bf16(expf_(d));
+  const float l = round_bf16(log1pf_(e));
+  return round_bf16(hi + l);
+}
+
+// ---------------------------------------------------------------------------
+// Causal depthwise conv over the cached window + SiLU, and the conv-state
+// update.  One thread owns one channel of one group, so the in-place state
+// update never races.  Per token: acc = sum_j fl(x_j * w_j) in j order (f32),
+// out = bf16(acc); silu = bf16(out * sigmoid_bf16(out)).
+__global__ __launch_bounds__(256) void conv_kernel(const uint16_t* __restrict__ qkv,
+                                                   int64_t row_stride, int t,
+                                                   const int32_t* __restrict__ slots,
+                                                   uint16_t* __restrict__ conv_state,
+                                                   const float* __restrict__ w, int channels,
+                                                   int taps, uint16_t* __restrict__ out,
+                                                   int64_t out_stride,
+                                                   uint16_t* __restrict__ window_history) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  const int g = blockIdx.y;
+  if (c >= channels) return;
+  uint16_t* st = conv_state + size_t(slots[g]) * (taps - 1) * channels + c;
+  constexpr int kMaxTaps = 8;
+  float win[kMaxTaps];
+  float wj[kMaxTaps];
+  for (int j = 0; j < taps - 1; ++j) win[j] = bf16_to_f32(st[size_t(j) * channels]);
+  for (int j = 0; j < taps; ++j) wj[j] = w[size_t(j) * channels + c];
+  uint16_t* hist = window_history
+                       ? window_history + size_t(g) * (taps - 1 + t) * channels + c
+                       : nullptr;
+  if (hist)
+    for (int j = 0; j < taps - 1; ++j) hist[size_t(j) * channels] = f32_to_bf16(win[j]);
+  for (int i = 0; i < t; ++i) {
+    const size_t row = size_t(g) * t + i;
+    const uint16_t xr = qkv[row * row_stride + c];
+    win[taps - 1] = bf16_to_f32(xr);
+    if (hist) hist[size_t(taps - 1 + i) * channels] = xr;
+    float acc = 0.0f;
+    for (int j = 0; j < taps; ++j) acc = acc + win[j] * wj[j];
+    const float v = round_bf16(acc);
+    out[row * out_stride + c] = f32_to_bf16(v * sigmoid_bf16(v));
+    for (int j = 0; j < taps - 1; ++j) win[j] = win[j + 1];
+  }
+  for (int j = 0; j < taps - 1; ++j) st[size_t(j) * channels] = f32_to_bf16(win[j]);
+}
+
+// Sum over the 128 threads of the block: xor butterfly inside each wave, then
+// wave 0's total + wave 1's total.  Every thread returns the same bits.
+__device__ __forceinline__ float block_sum128(float v, float* red) {
+  for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o, 64);
+  const int wave = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[wave] = v;
+  __syncthreads();
+  return red[0] + red[1];
+}
+
+constexpr int kD = 128;  // head dim handled by the recurrence kernel (Dk == Dv == 128)
+
+// Inputs of the delta rule for one token: either computed from the conv
+// output and the z/a/b projections (FUSED: L2 norms, beta, decay; the gated
+// RMS norm follows the scan) or read as given (the reference's recurrent
+// kernel interface: normalised q/k, v, fp32 g, bf16 beta).
+struct ScanArgs {
+  // fused form
+  const uint16_t* conv_out;
+  int64_t conv_stride;
+  const uint16_t* z;
+  const uint16_t* a;
+  const uint16_t* b;
+  int64_t zab_stride;
+  const float* a_log;
+  const uint16_t* dt_bias;
+  const uint16_t* norm_w;
+  float eps;
+  // raw form: q, k [rows, hk, 128]; v, y [rows, hv, 128]; g, beta [rows, hv]
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const float* g;
+  const uint16_t* beta;
+  // common
+  int hk_heads, hv_heads, t;
+  const int32_t* slots;
+  float* state;
+  float* history;
+  uint16_t* y;
+};
+
+// ---------------------------------------------------------------------------
+// Delta-rule scan for one (group, value head).  Thread i owns value row i of
+// the head: its 128 state values live in registers for all t tokens.
+template <bool FUSED>
+__global__ __launch_bounds__(kD) void recurrence_kernel(ScanArgs p) {
+  const int hv = blockIdx.x;
+  const int g = blockIdx.y;
+  const int i = threadIdx.x;
+  const int hv_heads = p.hv_heads, hk_heads = p.hk_heads;
+  const int hk = hv / (hv_heads / hk_heads);
+  __shared__ float qs[kD], ks[kD], red[2];
+
+  float* sp = p.state + (size_t(p.slots[g]) * hv_heads + hv) * kD * kD + i;
+  float s[kD];
+#pragma unroll
+  for (int d = 0; d < kD; ++d) s[d] = sp[size_t(d) * kD];
+
+  const float eps_l2 = round_bf16(1e-6f);
+  const float qscale = round_bf16(0.08838834764831845f);  // bf16(Dk^-1/2), Dk = 128
+  float neg_a = 0.0f, dt = 0.0f, nw = 0.0f;
+  if constexpr (FUSED) {
+    neg_a = -expf_(p.a_log[hv]);
+    dt = bf16_to_f32(p.dt_bias[hv]);
+    nw = bf16_to_f32(p.norm_w[i]);
+  }
+
+  for (int step = 0; step < p.t; ++step) {
+    const size_t row = size_t(g) * p.t + step;
+    float vi, beta, gdecay;
+    if constexpr (FUSED) {
+      const uint16_t* cr = p.conv_out + row * p.conv_stride;
+      const float qi = bf16_to_f32(cr[hk * kD + i]);
+      const float ki = bf16_to_f32(cr[(hk_heads + hk) * kD + i]);
+      vi = bf16_to_f32(cr[2 * hk_heads * kD + hv * kD + i]);
+      // x * rsqrt(sum(x^2) + eps) with bf16 operations (hybrid.rs:409-413)
+      const float qss = round_bf16(block_sum128(round_bf16(qi * qi), red));
+      const float kss = round_bf16(block_sum128(round_bf16(ki * ki), red));
+      const float rq = round_bf16(1.0f / __builtin_sqrtf(round_bf16(qss + eps_l2)));
+      const float rk = round_bf16(1.0f / __builtin_sqrtf(round_bf16(kss + eps_l2)));
+      __syncthreads();
+      qs[i] = round_bf16(round_bf16(qi * rq) * qscale);
+      ks[i] = round_bf16(ki * rk);
+      beta = sigmoid_bf16(bf16_to_f32(p.b[row * p.zab_stride + hv]));
+      const float x = round_bf16(bf16_to_f32(p.a[row * p.zab_stride + hv]) + dt);
+      gdecay = expf_(neg_a * softplus_bf16(x));
+    } else {
+      __syncthreads();
+      qs[i] = bf16_to_f32(p.q[(row * hk_heads + hk) * kD + i]);
+      ks[i] = bf16_to_f32(p.k[(row * hk_heads + hk) * kD + i]);
+      vi = bf16_to_f32(p.v[(row * hv_heads + hv) * kD + i]);
+      beta = bf16_to_f32(p.beta[row * hv_heads + hv]);
+      gdecay = p.g[row * hv_heads + hv];
+    }
+    __syncthreads();
+
+    // state *= g; kv = sum_d s[d] k[d] (four interleaved fma chains)
+    float c0 = 0.0f, c1 = 0.0f, c2 = 0.0f, c3 = 0.0f;
+#pragma unroll
+    for (int d = 0; d < kD; d += 4) {
+      s[d] = s[d] * gdecay;
+      s[d + 1] = s[d + 1] * gdecay;
+      s[d + 2] = s[d + 2] * gdecay;
+      s[d + 3] = s[d + 3] * gdecay;
+      c0 = fmaf_(s[d], ks[d], c0);
+      c1 = fmaf_(s[d + 1], ks[d + 1], c1);
+      c2 = fmaf_(s[d + 2], ks[d + 2], c2);
+      c3 = fmaf_(s[d + 3], ks[d + 3], c3);
+    }
+    const float kv = (c0 + c1) + (c2 + c3);
+    const float delta = (vi - kv) * beta;
+    float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f;
+#pragma unroll
+    for (int d = 0; d < kD; d += 4) {
+      s[d] = fmaf_(ks[d], delta, s[d]);
+      s[d + 1] = fmaf_(ks[d + 1], delta, s[d + 1]);
+      s[d + 2] = fmaf_(ks[d + 2], delta, s[d + 2]);
+      s[d + 3] = fmaf_(ks[d + 3], delta, s[d + 3]);
+      o0 = fmaf_(s[d], qs[d], o0);
+      o1 = fmaf_(s[d + 1], qs[d + 1], o1);
+      o2 = fmaf_(s[d + 2], qs[d + 2], o2);
+      o3 = fmaf_(s[d + 3], qs[d + 3], o3);
+    }
+    const float yo = round_bf16((o0 + o1) + (o2 + o3));
+    if (p.history) {
+      float* hp = p.history + ((row * hv_heads + hv) * kD) * kD + i;
+#pragma unroll
+      for (int d = 0; d < kD; ++d) hp[size_t(d) * kD] = s[d];
+    }
+    uint16_t* yp = p.y + row * (size_t(hv_heads) * kD) + hv * kD + i;
+    if constexpr (FUSED) {
+      // fast::rms_norm(y, w, eps) then * sigmoid(z) in f32 (hybrid.rs:447-452)
+      const float ss = block_sum128(yo * yo, red);
+      const float inv = 1.0f / __builtin_sqrtf(ss / float(kD) + p.eps);
+      const float normed = round_bf16(nw * round_bf16(yo * inv));
+      const float zi = bf16_to_f32(p.z[row * p.zab_stride + hv * kD + i]);
+      *yp = f32_to_bf16(normed * sigmoidf_(zi));
+    } else {
+      *yp = f32_to_bf16(yo);
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < kD; ++d) sp[size_t(d) * kD] = s[d];
+}
+
+}  // namespace
+
+int gdn_conv(const uint16_t* qkv, int64_t row_stride, int groups, int t, const int32_t* slots,
+             uint16_t* conv_state, const float* conv_w, int channels, int conv_k, uint16_t* out,
+             int64_t out_stride, uint16_t* window_history, hipStream_t s) {
+  if (conv_k < 2 || conv_k > 8) return MX_EUNSUPPORTED;
+  const dim3 grid((channels + 255) / 256, groups);
+  hipLaunchKernelGGL(conv_kernel, grid, dim3(256), 0, s, qkv, row_stride, t, slots, conv_state,
+                     conv_w, channels, conv_k, out, out_stride, window_history);
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
+int gdn_recurrence(const uint16_t* conv_out, int64_t conv_stride, const uint16_t* z,
+                   const uint16_t* a, const uint16_t* b, int64_t zab_stride, const float* a_log,
+                   const uint16_t* dt_bias, const uint16_t* norm_w, float eps, GdnDims d,
+                   int groups, int t, const int32_t* slots, float* state, float* history,
+                   uint16_t* y, hipStream_t s) {
+  if (d.dk != kD || d.dv != kD || d.hk <= 0 || d.hv % d.hk != 0) return MX_EUNSUPPORTED;
+  ScanArgs p{};
+  p.conv_out = conv_out; p.conv_stride = conv_stride; p.z = z; p.a = a; p.b = b;
+  p.zab_stride = zab_stride; p.a_log = a_log; p.dt_bias = dt_bias; p.norm_w = norm_w; p.eps = eps;
+  p.hk_heads = d.hk; p.hv_heads = d.hv; p.t = t; p.slots = slots; p.state = state;
+  p.history = history; p.y = y;
+  hipLaunchKernelGGL(recurrence_kernel<true>, dim3(d.hv, groups), dim3(kD), 0, s, p);
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
+int gdn_scan(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
+             const uint16_t* beta, GdnDims d, int groups, int t, const int32_t* slots,
+             float* state, float* history, uint16_t* y, hipStream_t s) {
+  if (d.dk != kD || d.dv != kD || d.hk <= 0 || d.hv % d.hk != 0) return MX_EUNSUPPORTED;
+  ScanArgs p{};
+  p.q = q; p.k = k; p.v = v; p.g = g; p.beta = beta;
+  p.hk_heads = d.hk; p.hv_heads = d.hv; p.t = t; p.slots = slots; p.state = state;
+  p.history = history; p.y = y;
+  hipLaunchKernelGGL(recurrence_kernel<false>, dim3(d.hv, groups), dim3(kD), 0, s, p);
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
+}  // namespace mx

@@ -19,12 +19,66 @@ inline QWeight to_qweight(const mx_qweight& w) {
   return QWeight{w.codes, w.scales, w.biases, w.n, w.k, w.bits, w.group_size};
 }
 
+// A bank of `experts` equally shaped quantised matrices stored back to back
+// (MLX SwitchLinear layout: codes [E, n, k*bits/32], scales/biases [E, n, k/gs]).
+struct QBank {
+  const uint32_t* codes;
+  const uint16_t* scales;
+  const uint16_t* biases;
+  int experts, n, k, bits, group_size;
+};
+
+inline QBank to_qbank(const mx_qbank& b) {
+  return QBank{b.codes, b.scales, b.biases, b.experts, b.n, b.k, b.bits, b.group_size};
+}
+
 // Shape rules shared by every quantised projection; returns an error message
 // or nullptr.
 const char* check_qweight(const QWeight& w);
 
 int qmv(const QWeight& w, const uint16_t* x, int m, uint16_t* y, hipStream_t s);
 int dequant_rows(const QWeight& w, const uint32_t* ids, int count, uint16_t* out, hipStream_t s);
+
+// ---- MoE ----
+int moe_route(const uint16_t* logits, int64_t logit_stride, const uint16_t* shared_logit,
+              int64_t shared_stride, int rows, int experts, int top_k, uint32_t* ids,
+              uint16_t* scores, uint16_t* factor, hipStream_t s);
+int moe_experts(const uint16_t* x, const uint32_t* ids, const uint16_t* scores, int rows,
+                int top_k, const QBank& gate, const QBank& up, const QBank& down,
+                const QWeight& sgate, const QWeight& sup, const QWeight& sdown, uint16_t* h,
+                uint16_t* p, hipStream_t s);
+int moe_reduce(const uint16_t* p, int rows, int top_k, int hidden, uint16_t* routed,
+               hipStream_t s);
+int moe_hc_epilogue(const uint16_t* routed, const uint16_t* shared, const uint16_t* factor,
+                    const uint16_t* residual, const uint16_t* gate, int rows, int hc, int hidden,
+                    uint16_t* out, hipStream_t s);
+int moe_reduce_hc_epilogue(const uint16_t* p, const uint16_t* factor, const uint16_t* residual,
+                           const uint16_t* gate, int rows, int top_k, int hc, int hidden,
+                           uint16_t* out, hipStream_t s);
+
+// ---- greedy head ----
+int head_parts(int n, int k);
+int head_partials(const QWeight& w, const uint16_t* x, int m, float* maxima, uint32_t* indices,
+                  int* parts, hipStream_t s);
+int argmax_reduce(const float* maxima, const uint32_t* indices, int rows, int parts,
+                  uint32_t* tokens, hipStream_t s);
+int argmax_bf16(const uint16_t* logits, int rows, int n, uint32_t* tokens, hipStream_t s);
+
+// ---- GatedDeltaNet ----
+struct GdnDims {
+  int hk, hv, dk, dv, conv_k;  // key heads, value heads, head dims, conv taps
+};
+int gdn_conv(const uint16_t* qkv, int64_t row_stride, int groups, int t, const int32_t* slots,
+             uint16_t* conv_state, const float* conv_w, int channels, int conv_k,
+             uint16_t* out, int64_t out_stride, uint16_t* window_history, hipStream_t s);
+int gdn_recurrence(const uint16_t* conv_out, int64_t conv_stride, const uint16_t* z,
+                   const uint16_t* a, const uint16_t* b, int64_t zab_stride, const float* a_log,
+                   const uint16_t* dt_bias, const uint16_t* norm_w, float eps, GdnDims d,
+                   int groups, int t, const int32_t* slots, float* state, float* history,
+                   uint16_t* y, hipStream_t s);
+int gdn_scan(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
+             const uint16_t* beta, GdnDims d, int groups, int t, const int32_t* slots,
+             float* state, float* history, uint16_t* y, hipStream_t s);
 
 int fill_bf16(uint16_t* dst, size_t count, uint64_t seed, int dist, float a, float b,
               hipStream_t s);

@@ -1,0 +1,434 @@
+// Sparse-MoE decode kernels for gfx950: routing tail, gathered expert
+// gate/up (+SwiGLU), gathered down (+score), and the slot reduction fused with
+// the hyper-connection epilogue.
+//
+// Reference: MoE::parts (src/hybrid.rs:192-287), moe_route::tail
+// (src/moe_route.rs:25-70, kernels/moe_route_tail.{h,metal}), moe_kernel::gate_up
+// (src/moe_kernel.rs:10-118, kernels/moe_gate_up{4,5}.metal), moe_down::reduce
+// (src/moe_down.rs:34-137, kernels/moe_down_tail.{h,metal}) and
+// moe_epilogue::apply (src/moe_epilogue.rs:17-73, kernels/moe_hc_epilogue.metal).
+//
+// Expert deduplication: every (row, slot) route of one step that names the same
+// expert is served by the workgroup of the expert's first route, so each
+// selected expert's weights stream from HBM once per step however many rows
+// chose it (the reference gathers per route, moe_kernel.rs:100-113).
+#include "common.hpp"
+#include "kernels.hpp"
+#include "qmv_core.hpp"
+
+namespace mx {
+
+namespace {
+
+constexpr int kWaves = 4;
+
+// bf16 logistic function with MLX's per-operation bf16 rounding
+// (reference kernels/moe_route_tail.metal:119-123).
+__device__ __forceinline__ float sigmoid_bf16(float x) {
+  const float e = round_bf16(expf_(__builtin_fabsf(x)));
+  const float d = round_bf16(1.0f + e);
+  const float y = round_bf16(1.0f / d);
+  return x < 0.0f ? y : round_bf16(1.0f - y);
+}
+
+// ---------------------------------------------------------------------------
+// Routing tail: softmax (fp32, MLX precise) -> bf16 gates -> top-k under the
+// (bf16 value, index) key -> bf16 renormalisation -> bf16 sigmoid of the
+// shared-expert gate.  One wave per row; lane l owns experts PER*l .. PER*l+PER-1.
+template <int PER>
+__global__ __launch_bounds__(64) void route_kernel(const uint16_t* __restrict__ logits,
+                                                   int64_t logit_stride,
+                                                   const uint16_t* __restrict__ shared_logit,
+                                                   int64_t shared_stride, int experts, int top_k,
+                                                   uint32_t* __restrict__ ids,
+                                                   uint16_t* __restrict__ scores,
+                                                   uint16_t* __restrict__ factor) {
+  const int row = blockIdx.x;
+  const int lane = threadIdx.x;
+  const uint16_t* in = logits + size_t(row) * logit_stride + lane * PER;
+  float v[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) v[i] = bf16_to_f32(in[i]);
+  float mx_ = v[0];
+#pragma unroll
+  for (int i = 1; i < PER; ++i) mx_ = v[i] > mx_ ? v[i] : mx_;
+  for (int o = 32; o > 0; o >>= 1) {
+    const float t = __shfl_xor(mx_, o, 64);
+    mx_ = t > mx_ ? t : mx_;
+  }
+  float sum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    v[i] = expf_(v[i] - mx_);
+    sum = sum + v[i];
+  }
+  for (int o = 32; o > 0; o >>= 1) sum = sum + __shfl_xor(sum, o, 64);
+  const float inv = 1.0f / sum;
+  uint32_t key[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const uint32_t g = f32_to_bf16(v[i] * inv);
+    // order-preserving map of the bf16 pattern (moe_route_tail.h:13-16)
+    const uint32_t k16 = (g & 0x8000u) ? (~g & 0xffffu) : (g | 0x8000u);
+    key[i] = (k16 << 16) | uint32_t(lane * PER + i);
+  }
+  uint32_t sel[16];
+  for (int s = 0; s < top_k; ++s) {
+    uint32_t best = 0;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) best = key[i] > best ? key[i] : best;
+    for (int o = 32; o > 0; o >>= 1) {
+      const uint32_t t = uint32_t(__shfl_xor(int(best), o, 64));
+      best = t > best ? t : best;
+    }
+    sel[top_k - 1 - s] = best;  // slot k-1 holds the largest (ascending order)
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      if (key[i] == best) key[i] = 0u;  // keys are unique; real keys are never 0
+  }
+  if (lane == 0) {
+    float picked[16];
+    float total = 0.0f;
+    for (int j = 0; j < top_k; ++j) {
+      const uint32_t k16 = sel[j] >> 16;
+      const uint32_t g = (k16 & 0x8000u) ? (k16 & 0x7fffu) : (~k16 & 0xffffu);
+      picked[j] = bf16_to_f32(uint16_t(g));
+      ids[size_t(row) * top_k + j] = sel[j] & 0xffffu;
+      total = round_bf16(picked[j] + total);  // one bf16 add per slot, ascending
+    }
+    for (int j = 0; j < top_k; ++j)
+      scores[size_t(row) * top_k + j] = f32_to_bf16(picked[j] / total);
+    factor[row] = f32_to_bf16(sigmoid_bf16(bf16_to_f32(shared_logit[size_t(row) * shared_stride])));
+  }
+}
+
+// Gathers the rows served by the workgroup of route `t`.  Returns 0 when an
+// earlier route names the same expert (that workgroup does the work).
+// Route R*top_k is the shared expert, used by every row.
+__device__ __forceinline__ int gather_routes(const uint32_t* __restrict__ ids, int rows, int top_k,
+                                             int t, int* row_of, int* slot_of, int* expert) {
+  const int routes = rows * top_k;
+  if (t == routes) {
+    *expert = -1;
+    for (int r = 0; r < rows; ++r) {
+      row_of[r] = r;
+      slot_of[r] = top_k;
+    }
+    return rows;
+  }
+  const uint32_t e = ids[t];
+  for (int u = 0; u < t; ++u)
+    if (ids[u] == e) return 0;
+  int m = 0;
+  for (int u = t; u < routes; ++u)
+    if (ids[u] == e) {
+      row_of[m] = u / top_k;
+      slot_of[m] = u % top_k;
+      ++m;
+    }
+  *expert = int(e);
+  return m;
+}
+
+struct Bank {
+  const uint32_t* codes;
+  const uint16_t* scales;
+  const uint16_t* biases;
+  size_t code_stride, scale_stride;  // per expert
+};
+
+__device__ __forceinline__ Bank bank_for(const QBank& b, int expert, const QWeight& shared) {
+  if (expert < 0) return Bank{shared.codes, shared.scales, shared.biases, 0, 0};
+  const size_t cs = size_t(b.n) * b.k * b.bits / 32;
+  const size_t ss = size_t(b.n) * (b.k / b.group_size);
+  return Bank{b.codes + cs * expert, b.scales + ss * expert, b.biases + ss * expert, cs, ss};
+}
+
+// ---------------------------------------------------------------------------
+// gate/up + SwiGLU.  h[row][slot][i] = bf16(bf16(g * sigmoid(g)) * u).
+template <int BITS, int M>
+__device__ void gate_up_body(const uint16_t* __restrict__ x, const Bank& gb, const Bank& ub,
+                             int inter, int hidden, int gs, const int* row_of, const int* slot_of,
+                             int top_k, uint16_t* __restrict__ h, int row0, int li, int L) {
+  int rows[kQRows];
+#pragma unroll
+  for (int r = 0; r < kQRows; ++r) rows[r] = min(row0 + r, inter - 1);
+  const uint16_t* xrow[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) xrow[m] = x + size_t(row_of[m]) * hidden;
+  float g[M][kQRows], u[M][kQRows];
+  qmv_core<BITS, M>(gb.codes, gb.scales, gb.biases, hidden, gs, xrow, rows, li, L, g);
+  qmv_core<BITS, M>(ub.codes, ub.scales, ub.biases, hidden, gs, xrow, rows, li, L, u);
+  if (li == 0) {
+#pragma unroll
+    for (int r = 0; r < kQRows; ++r) {
+      if (row0 + r >= inter) continue;
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const float gv = round_bf16(g[m][r]);
+        const float uv = round_bf16(u[m][r]);
+        const float silu = round_bf16(gv * sigmoid_bf16(gv));
+        h[(size_t(row_of[m]) * (top_k + 1) + slot_of[m]) * inter + row0 + r] =
+            f32_to_bf16(silu * uv);
+      }
+    }
+  }
+}
+
+template <int BITS>
+__global__ __launch_bounds__(256) void gate_up_kernel(const uint16_t* __restrict__ x,
+                                                      const uint32_t* __restrict__ ids, int rows,
+                                                      int top_k, QBank gate, QBank up,
+                                                      QWeight sgate, QWeight sup,
+                                                      uint16_t* __restrict__ h, int L) {
+  __shared__ int row_of[8], slot_of[8], info[2];
+  if (threadIdx.x == 0) {
+    int e;
+    info[0] = gather_routes(ids, rows, top_k, blockIdx.y, row_of, slot_of, &e);
+    info[1] = e;
+  }
+  __syncthreads();
+  const int m = info[0];
+  if (m == 0) return;
+  const int expert = info[1];
+  const Bank gb = bank_for(gate, expert, sgate);
+  const Bank ub = bank_for(up, expert, sup);
+  const int inter = expert < 0 ? sgate.n : gate.n;
+  const int hidden = gate.k;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int li = lane & (L - 1), lg = lane / L;
+  const int row0 = ((blockIdx.x * kWaves + wave) * (64 / L) + lg) * kQRows;
+  if (row0 >= inter) return;
+  int ro[8], so[8];
+  for (int i = 0; i < m; ++i) {
+    ro[i] = row_of[i];
+    so[i] = slot_of[i];
+  }
+  switch (m) {
+#define MX_CASE(MM) \
+  case MM: gate_up_body<BITS, MM>(x, gb, ub, inter, hidden, gate.group_size, ro, so, top_k, h, row0, li, L); break;
+    MX_CASE(1) MX_CASE(2) MX_CASE(3) MX_CASE(4) MX_CASE(5) MX_CASE(6) MX_CASE(7) MX_CASE(8)
+#undef MX_CASE
+  }
+}
+
+// ---------------------------------------------------------------------------
+// down + score.  p[row][slot][n] = bf16(bf16(down) * score) for routed slots;
+// the shared slot (top_k) keeps bf16(down).
+template <int BITS, int M>
+__device__ void down_body(const uint16_t* __restrict__ h, const Bank& db, int hidden, int inter,
+                          int gs, const int* row_of, const int* slot_of, int top_k,
+                          const uint16_t* __restrict__ scores, uint16_t* __restrict__ p, int row0,
+                          int li, int L) {
+  int rows[kQRows];
+#pragma unroll
+  for (int r = 0; r < kQRows; ++r) rows[r] = min(row0 + r, hidden - 1);
+  const uint16_t* xrow[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+    xrow[m] = h + (size_t(row_of[m]) * (top_k + 1) + slot_of[m]) * inter;
+  float d[M][kQRows];
+  qmv_core<BITS, M>(db.codes, db.scales, db.biases, inter, gs, xrow, rows, li, L, d);
+  if (li == 0) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const bool routed = slot_of[m] < top_k;
+      const float sc =
+          routed ? bf16_to_f32(scores[size_t(row_of[m]) * top_k + slot_of[m]]) : 1.0f;
+#pragma unroll
+      for (int r = 0; r < kQRows; ++r) {
+        if (row0 + r >= hidden) continue;
+        const float dv = round_bf16(d[m][r]);
+        p[(size_t(row_of[m]) * (top_k + 1) + slot_of[m]) * hidden + row0 + r] =
+            f32_to_bf16(routed ? dv * sc : dv);
+      }
+    }
+  }
+}
+
+template <int BITS>
+__global__ __launch_bounds__(256) void down_kernel(const uint16_t* __restrict__ h,
+                                                   const uint32_t* __restrict__ ids,
+                                                   const uint16_t* __restrict__ scores, int rows,
+                                                   int top_k, QBank down, QWeight sdown,
+                                                   uint16_t* __restrict__ p, int L) {
+  __shared__ int row_of[8], slot_of[8], info[2];
+  if (threadIdx.x == 0) {
+    int e;
+    info[0] = gather_routes(ids, rows, top_k, blockIdx.y, row_of, slot_of, &e);
+    info[1] = e;
+  }
+  __syncthreads();
+  const int m = info[0];
+  if (m == 0) return;
+  const int expert = info[1];
+  const Bank db = bank_for(down, expert, sdown);
+  const int hidden = down.n;
+  const int inter = down.k;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int li = lane & (L - 1), lg = lane / L;
+  const int row0 = ((blockIdx.x * kWaves + wave) * (64 / L) + lg) * kQRows;
+  if (row0 >= hidden) return;
+  int ro[8], so[8];
+  for (int i = 0; i < m; ++i) {
+    ro[i] = row_of[i];
+    so[i] = slot_of[i];
+  }
+  switch (m) {
+#define MX_CASE(MM) \
+  case MM: down_body<BITS, MM>(h, db, hidden, inter, down.group_size, ro, so, top_k, scores, p, row0, li, L); break;
+    MX_CASE(1) MX_CASE(2) MX_CASE(3) MX_CASE(4) MX_CASE(5) MX_CASE(6) MX_CASE(7) MX_CASE(8)
+#undef MX_CASE
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Slot reduction.  routed = bf16 sum of p[row][0..k-1][c] in the reference's
+// order (kernels/moe_down_tail.h:20, moe_down_tail.metal:83-99): slot i
+// accumulates into lane i % 8 with one bf16 add per later slot, then lanes
+// 1..7 are added to lane 0's value one by one.  For k = 10 this is the order
+// {0,8},{1,9},2,3,...,7 of the reference's SLOT_ORDER.
+__device__ __forceinline__ float slot_sum(const uint16_t* __restrict__ pr, int top_k,
+                                          size_t stride) {
+  float acc[8] = {0.0f};
+  const int lanes = top_k < 8 ? top_k : 8;
+  for (int a = 0; a < lanes; ++a) {
+    float v = bf16_to_f32(pr[size_t(a) * stride]);
+    for (int s = a + 8; s < top_k; s += 8) v = round_bf16(v + bf16_to_f32(pr[size_t(s) * stride]));
+    acc[a] = v;
+  }
+  float routed = acc[0];
+  for (int a = 1; a < lanes; ++a) routed = round_bf16(acc[a] + routed);
+  return routed;
+}
+
+// Hyper-connection write of the MoE output (kernels/moe_hc_epilogue.metal:8-11):
+//   weighted = bf16(shared * factor); combined = bf16(routed + weighted)
+//   out[s] = bf16(residual[s] + bf16(combined * gate[s]))
+__device__ __forceinline__ void hc_write(float routed, float shared, float factor,
+                                         const uint16_t* __restrict__ residual,
+                                         const uint16_t* __restrict__ gate, int hc, int hidden,
+                                         uint16_t* __restrict__ out) {
+  const float weighted = round_bf16(shared * factor);
+  const float combined = round_bf16(routed + weighted);
+  for (int s = 0; s < hc; ++s) {
+    const float inj = round_bf16(combined * bf16_to_f32(gate[s]));
+    out[size_t(s) * hidden] = f32_to_bf16(bf16_to_f32(residual[size_t(s) * hidden]) + inj);
+  }
+}
+
+__global__ __launch_bounds__(256) void moe_reduce_kernel(const uint16_t* __restrict__ p,
+                                                         int top_k, int hidden,
+                                                         uint16_t* __restrict__ routed) {
+  const int row = blockIdx.y;
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= hidden) return;
+  const uint16_t* pr = p + size_t(row) * (top_k + 1) * hidden + c;
+  routed[size_t(row) * hidden + c] = f32_to_bf16(slot_sum(pr, top_k, hidden));
+}
+
+__global__ __launch_bounds__(256) void moe_epilogue_kernel(
+    const uint16_t* __restrict__ routed, const uint16_t* __restrict__ shared,
+    const uint16_t* __restrict__ factor, const uint16_t* __restrict__ residual,
+    const uint16_t* __restrict__ gate, int hc, int hidden, uint16_t* __restrict__ out) {
+  const int row = blockIdx.y;
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= hidden) return;
+  const size_t o = size_t(row) * hc * hidden + c;
+  hc_write(bf16_to_f32(routed[size_t(row) * hidden + c]),
+           bf16_to_f32(shared[size_t(row) * hidden + c]), bf16_to_f32(factor[row]),
+           residual + o, gate + size_t(row) * hc, hc, hidden, out + o);
+}
+
+__global__ __launch_bounds__(256) void moe_reduce_epilogue_kernel(
+    const uint16_t* __restrict__ p, const uint16_t* __restrict__ factor,
+    const uint16_t* __restrict__ residual, const uint16_t* __restrict__ gate, int top_k, int hc,
+    int hidden, uint16_t* __restrict__ out) {
+  const int row = blockIdx.y;
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= hidden) return;
+  const uint16_t* pr = p + size_t(row) * (top_k + 1) * hidden + c;
+  // the reduced value is rounded to bf16 exactly as the separate kernels store it
+  const float routed = round_bf16(slot_sum(pr, top_k, hidden));
+  const size_t o = size_t(row) * hc * hidden + c;
+  hc_write(routed, bf16_to_f32(pr[size_t(top_k) * hidden]), bf16_to_f32(factor[row]),
+           residual + o, gate + size_t(row) * hc, hc, hidden, out + o);
+}
+
+}  // namespace
+
+int moe_route(const uint16_t* logits, int64_t logit_stride, const uint16_t* shared_logit,
+              int64_t shared_stride, int rows, int experts, int top_k, uint32_t* ids,
+              uint16_t* scores, uint16_t* factor, hipStream_t s) {
+  const int per = experts / 64;
+#define MX_ROUTE(P)                                                                          \
+  case P:                                                                                    \
+    hipLaunchKernelGGL(route_kernel<P>, dim3(rows), dim3(64), 0, s, logits, logit_stride,    \
+                       shared_logit, shared_stride, experts, top_k, ids, scores, factor);    \
+    break;
+  switch (per) {
+    MX_ROUTE(1) MX_ROUTE(2) MX_ROUTE(4) MX_ROUTE(8) MX_ROUTE(16)
+    default: return MX_EUNSUPPORTED;
+  }
+#undef MX_ROUTE
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+int moe_experts(const uint16_t* x, const uint32_t* ids, const uint16_t* scores, int rows,
+                int top_k, const QBank& gate, const QBank& up, const QBank& down,
+                const QWeight& sgate, const QWeight& sup, const QWeight& sdown, uint16_t* h,
+                uint16_t* p, hipStream_t s) {
+  const int routes = rows * top_k + 1;
+  {
+    const int L = qmv_lanes_per_row(gate.k);
+    const int rows_per_block = kWaves * (64 / L) * kQRows;
+    const int inter = gate.n > sgate.n ? gate.n : sgate.n;
+    const dim3 grid((inter + rows_per_block - 1) / rows_per_block, routes);
+    switch (gate.bits) {
+      case 4: hipLaunchKernelGGL(gate_up_kernel<4>, grid, dim3(256), 0, s, x, ids, rows, top_k, gate, up, sgate, sup, h, L); break;
+      case 5: hipLaunchKernelGGL(gate_up_kernel<5>, grid, dim3(256), 0, s, x, ids, rows, top_k, gate, up, sgate, sup, h, L); break;
+      case 6: hipLaunchKernelGGL(gate_up_kernel<6>, grid, dim3(256), 0, s, x, ids, rows, top_k, gate, up, sgate, sup, h, L); break;
+      case 8: hipLaunchKernelGGL(gate_up_kernel<8>, grid, dim3(256), 0, s, x, ids, rows, top_k, gate, up, sgate, sup, h, L); break;
+      default: return MX_EUNSUPPORTED;
+    }
+  }
+  {
+    const int L = qmv_lanes_per_row(down.k);
+    const int rows_per_block = kWaves * (64 / L) * kQRows;
+    const dim3 grid((down.n + rows_per_block - 1) / rows_per_block, routes);
+    switch (down.bits) {
+      case 4: hipLaunchKernelGGL(down_kernel<4>, grid, dim3(256), 0, s, h, ids, scores, rows, top_k, down, sdown, p, L); break;
+      case 5: hipLaunchKernelGGL(down_kernel<5>, grid, dim3(256), 0, s, h, ids, scores, rows, top_k, down, sdown, p, L); break;
+      case 6: hipLaunchKernelGGL(down_kernel<6>, grid, dim3(256), 0, s, h, ids, scores, rows, top_k, down, sdown, p, L); break;
+      case 8: hipLaunchKernelGGL(down_kernel<8>, grid, dim3(256), 0, s, h, ids, scores, rows, top_k, down, sdown, p, L); break;
+      default: return MX_EUNSUPPORTED;
+    }
+  }
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
+int moe_reduce(const uint16_t* p, int rows, int top_k, int hidden, uint16_t* routed,
+               hipStream_t s) {
+  const dim3 grid((hidden + 255) / 256, rows);
+  hipLaunchKernelGGL(moe_reduce_kernel, grid, dim3(256), 0, s, p, top_k, hidden, routed);
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
+int moe_hc_epilogue(const uint16_t* routed, const uint16_t* shared, const uint16_t* factor,
+                    const uint16_t* residual, const uint16_t* gate, int rows, int hc, int hidden,
+                    uint16_t* out, hipStream_t s) {
+  const dim3 grid((hidden + 255) / 256, rows);
+  hipLaunchKernelGGL(moe_epilogue_kernel, grid, dim3(256), 0, s, routed, shared, factor, residual,
+                     gate, hc, hidden, out);
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
+int moe_reduce_hc_epilogue(const uint16_t* p, const uint16_t* factor, const uint16_t* residual,
+                           const uint16_t* gate, int rows, int top_k, int hc, int hidden,
+                           uint16_t* out, hipStream_t s) {
+  const dim3 grid((hidden + 255) / 256, rows);
+  hipLaunchKernelGGL(moe_reduce_epilogue_kernel, grid, dim3(256), 0, s, p, factor, residual, gate,
+                     top_k, hc, hidden, out);
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
+}  // namespace mx
