@@ -149,7 +149,7 @@ __device__ __forceinline__ Bank bank_for(const QBank& b, int expert, const QWeig
 template <int BITS, int M>
 __device__ void gate_up_body(const uint16_t* __restrict__ x, const Bank& gb, const Bank& ub,
                              int inter, int hidden, int gs, const int* row_of, const int* slot_of,
-                             int top_k, uint16_t* __restrict__ h, int row0, int li, int L) {
+                             int top_k, uint16_t* __restrict__ h, int hs, int row0, int li, int L) {
   int rows[kQRows];
 #pragma unroll
   for (int r = 0; r < kQRows; ++r) rows[r] = min(row0 + r, inter - 1);
@@ -168,7 +168,7 @@ __device__ void gate_up_body(const uint16_t* __restrict__ x, const Bank& gb, con
         const float gv = round_bf16(g[m][r]);
         const float uv = round_bf16(u[m][r]);
         const float silu = round_bf16(gv * sigmoid_bf16(gv));
-        h[(size_t(row_of[m]) * (top_k + 1) + slot_of[m]) * inter + row0 + r] =
+        h[(size_t(row_of[m]) * (top_k + 1) + slot_of[m]) * hs + row0 + r] =
             f32_to_bf16(silu * uv);
       }
     }
@@ -180,7 +180,7 @@ __global__ __launch_bounds__(256) void gate_up_kernel(const uint16_t* __restrict
                                                       const uint32_t* __restrict__ ids, int rows,
                                                       int top_k, QBank gate, QBank up,
                                                       QWeight sgate, QWeight sup,
-                                                      uint16_t* __restrict__ h, int L) {
+                                                      uint16_t* __restrict__ h, int hs) {
   __shared__ int row_of[8], slot_of[8], info[2];
   if (threadIdx.x == 0) {
     int e;
@@ -195,6 +195,7 @@ __global__ __launch_bounds__(256) void gate_up_kernel(const uint16_t* __restrict
   const Bank ub = bank_for(up, expert, sup);
   const int inter = expert < 0 ? sgate.n : gate.n;
   const int hidden = gate.k;
+  const int L = qmv_lanes_per_row(hidden);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int li = lane & (L - 1), lg = lane / L;
   const int row0 = ((blockIdx.x * kWaves + wave) * (64 / L) + lg) * kQRows;
@@ -206,7 +207,7 @@ __global__ __launch_bounds__(256) void gate_up_kernel(const uint16_t* __restrict
   }
   switch (m) {
 #define MX_CASE(MM) \
-  case MM: gate_up_body<BITS, MM>(x, gb, ub, inter, hidden, gate.group_size, ro, so, top_k, h, row0, li, L); break;
+  case MM: gate_up_body<BITS, MM>(x, gb, ub, inter, hidden, gate.group_size, ro, so, top_k, h, hs, row0, li, L); break;
     MX_CASE(1) MX_CASE(2) MX_CASE(3) MX_CASE(4) MX_CASE(5) MX_CASE(6) MX_CASE(7) MX_CASE(8)
 #undef MX_CASE
   }
@@ -218,15 +219,15 @@ __global__ __launch_bounds__(256) void gate_up_kernel(const uint16_t* __restrict
 template <int BITS, int M>
 __device__ void down_body(const uint16_t* __restrict__ h, const Bank& db, int hidden, int inter,
                           int gs, const int* row_of, const int* slot_of, int top_k,
-                          const uint16_t* __restrict__ scores, uint16_t* __restrict__ p, int row0,
-                          int li, int L) {
+                          const uint16_t* __restrict__ scores, uint16_t* __restrict__ p, int hs,
+                          int row0, int li, int L) {
   int rows[kQRows];
 #pragma unroll
   for (int r = 0; r < kQRows; ++r) rows[r] = min(row0 + r, hidden - 1);
   const uint16_t* xrow[M];
 #pragma unroll
   for (int m = 0; m < M; ++m)
-    xrow[m] = h + (size_t(row_of[m]) * (top_k + 1) + slot_of[m]) * inter;
+    xrow[m] = h + (size_t(row_of[m]) * (top_k + 1) + slot_of[m]) * hs;
   float d[M][kQRows];
   qmv_core<BITS, M>(db.codes, db.scales, db.biases, inter, gs, xrow, rows, li, L, d);
   if (li == 0) {
@@ -251,7 +252,7 @@ __global__ __launch_bounds__(256) void down_kernel(const uint16_t* __restrict__ 
                                                    const uint32_t* __restrict__ ids,
                                                    const uint16_t* __restrict__ scores, int rows,
                                                    int top_k, QBank down, QWeight sdown,
-                                                   uint16_t* __restrict__ p, int L) {
+                                                   uint16_t* __restrict__ p, int hs) {
   __shared__ int row_of[8], slot_of[8], info[2];
   if (threadIdx.x == 0) {
     int e;
@@ -264,7 +265,8 @@ __global__ __launch_bounds__(256) void down_kernel(const uint16_t* __restrict__ 
   const int expert = info[1];
   const Bank db = bank_for(down, expert, sdown);
   const int hidden = down.n;
-  const int inter = down.k;
+  const int inter = expert < 0 ? sdown.k : down.k;
+  const int L = qmv_lanes_per_row(inter);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int li = lane & (L - 1), lg = lane / L;
   const int row0 = ((blockIdx.x * kWaves + wave) * (64 / L) + lg) * kQRows;
@@ -276,7 +278,7 @@ __global__ __launch_bounds__(256) void down_kernel(const uint16_t* __restrict__ 
   }
   switch (m) {
 #define MX_CASE(MM) \
-  case MM: down_body<BITS, MM>(h, db, hidden, inter, down.group_size, ro, so, top_k, scores, p, row0, li, L); break;
+  case MM: down_body<BITS, MM>(h, db, hidden, inter, down.group_size, ro, so, top_k, scores, p, hs, row0, li, L); break;
     MX_CASE(1) MX_CASE(2) MX_CASE(3) MX_CASE(4) MX_CASE(5) MX_CASE(6) MX_CASE(7) MX_CASE(8)
 #undef MX_CASE
   }
@@ -378,30 +380,34 @@ int moe_experts(const uint16_t* x, const uint32_t* ids, const uint16_t* scores, 
                 const QWeight& sgate, const QWeight& sup, const QWeight& sdown, uint16_t* h,
                 uint16_t* p, hipStream_t s) {
   const int routes = rows * top_k + 1;
+  const int hs = gate.n > sgate.n ? gate.n : sgate.n;  // h row stride (workspace layout)
   {
+    // rows per workgroup is fixed by K = hidden, shared by routed and shared experts
     const int L = qmv_lanes_per_row(gate.k);
     const int rows_per_block = kWaves * (64 / L) * kQRows;
-    const int inter = gate.n > sgate.n ? gate.n : sgate.n;
-    const dim3 grid((inter + rows_per_block - 1) / rows_per_block, routes);
+    const dim3 grid((hs + rows_per_block - 1) / rows_per_block, routes);
+#define MX_GU(B) \
+  case B: hipLaunchKernelGGL(gate_up_kernel<B>, grid, dim3(256), 0, s, x, ids, rows, top_k, gate, up, sgate, sup, h, hs); break;
     switch (gate.bits) {
-      case 4: hipLaunchKernelGGL(gate_up_kernel<4>, grid, dim3(256), 0, s, x, ids, rows, top_k, gate, up, sgate, sup, h, L); break;
-      case 5: hipLaunchKernelGGL(gate_up_kernel<5>, grid, dim3(256), 0, s, x, ids, rows, top_k, gate, up, sgate, sup, h, L); break;
-      case 6: hipLaunchKernelGGL(gate_up_kernel<6>, grid, dim3(256), 0, s, x, ids, rows, top_k, gate, up, sgate, sup, h, L); break;
-      case 8: hipLaunchKernelGGL(gate_up_kernel<8>, grid, dim3(256), 0, s, x, ids, rows, top_k, gate, up, sgate, sup, h, L); break;
+      MX_GU(4) MX_GU(5) MX_GU(6) MX_GU(8)
       default: return MX_EUNSUPPORTED;
     }
+#undef MX_GU
   }
   {
-    const int L = qmv_lanes_per_row(down.k);
+    // rows per workgroup shrink as K = inter grows: size the grid for the
+    // deeper of the two (workgroups past the end of a shallower route exit)
+    const int kmax = down.k > sdown.k ? down.k : sdown.k;
+    const int L = qmv_lanes_per_row(kmax);
     const int rows_per_block = kWaves * (64 / L) * kQRows;
     const dim3 grid((down.n + rows_per_block - 1) / rows_per_block, routes);
+#define MX_DN(B) \
+  case B: hipLaunchKernelGGL(down_kernel<B>, grid, dim3(256), 0, s, h, ids, scores, rows, top_k, down, sdown, p, hs); break;
     switch (down.bits) {
-      case 4: hipLaunchKernelGGL(down_kernel<4>, grid, dim3(256), 0, s, h, ids, scores, rows, top_k, down, sdown, p, L); break;
-      case 5: hipLaunchKernelGGL(down_kernel<5>, grid, dim3(256), 0, s, h, ids, scores, rows, top_k, down, sdown, p, L); break;
-      case 6: hipLaunchKernelGGL(down_kernel<6>, grid, dim3(256), 0, s, h, ids, scores, rows, top_k, down, sdown, p, L); break;
-      case 8: hipLaunchKernelGGL(down_kernel<8>, grid, dim3(256), 0, s, h, ids, scores, rows, top_k, down, sdown, p, L); break;
+      MX_DN(4) MX_DN(5) MX_DN(6) MX_DN(8)
       default: return MX_EUNSUPPORTED;
     }
+#undef MX_DN
   }
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
