@@ -74,6 +74,35 @@ typedef struct mx_gdn_dims {
   int32_t conv_k;  /* depthwise conv taps */
 } mx_gdn_dims;
 
+/* Synthetic hybrid model (BASELINE config 3 / 4): `layers` layers, layer i a
+ * gated full-attention layer when i % attn_every == attn_every - 1, else a
+ * GatedDeltaNet layer; every layer has attention and MLP hyper-connections
+ * (hc streams, low rank hc_rank) and a sparse MoE with one shared expert;
+ * a mixer hyper-connection and a greedy vocabulary head close the stack
+ * (reference src/hybrid.rs:12-38 HybridConfig, 500-685 HybridModel).
+ * Weights are random affine-quantised tensors drawn from `seed`. */
+typedef struct mx_model_config {
+  int32_t hidden;
+  int32_t layers;
+  int32_t attn_every;
+  int32_t vocab;
+  int32_t hc;
+  int32_t hc_rank;
+  int32_t gdn_hk, gdn_hv, gdn_dk, gdn_dv, conv_k;
+  int32_t heads, kv_heads, head_dim, rotary_dim;
+  float rope_theta;
+  float rms_eps;
+  int32_t experts, top_k, moe_inter, shared_inter;
+  int32_t bits;        /* projections and expert gate/up */
+  int32_t down_bits;   /* expert and shared-expert down */
+  int32_t embed_bits, head_bits, group_size;
+  int32_t mixed_bits;  /* nonzero: per-layer bits drawn from {4,5,6,8} by seed (config 4) */
+  int32_t max_slots, max_context, max_verify;
+  uint64_t seed;
+} mx_model_config;
+
+typedef struct mx_engine mx_engine;
+
 /* ---- errors / version -------------------------------------------------- */
 const char* mx_last_error(void);
 int32_t mx_abi_version(void);
@@ -220,6 +249,49 @@ mx_status mx_gdn_recurrence(const uint16_t* conv_out, int64_t conv_stride, const
                             float eps, const mx_gdn_dims* dims, int32_t groups, int32_t t,
                             const int32_t* slots, float* state, float* history, uint16_t* y,
                             void* stream);
+
+/* ---- A1/A17/A18: the decode engine ---------------------------------------
+ * Owns the model weights, a slot arena of caches (GDN state + conv window, KV)
+ * and one HIP stream; every call is synchronous (one sync per step, like the
+ * reference's eval) and must come from the thread that created the engine.
+ *
+ * mx_engine_decode_batch: one token for each of `rows` (1..8) distinct slots
+ * that sit at the same offset; writes each row's greedy next token and
+ * advances the slots.  Replaces HybridModel::decode_batch (src/batching.rs:34-170);
+ * unequal offsets are rejected with MX_ESTATE as in batching.rs:47-53, and
+ * out-of-vocabulary tokens with MX_EINVAL.
+ * mx_engine_decode_rows: the same step without the equal-offset rule (each
+ * row attends to its own context), for ragged continuous batching.
+ * mx_engine_prefill: feeds `count` tokens to one slot in chunks of up to 8
+ * (speculative::prepare, src/speculative.rs:38-68); *next = greedy token after
+ * the last one.
+ * mx_engine_verify / mx_engine_commit: an MTP verify block of 1..max_verify
+ * tokens (argmax at every position into `argmax`), then accept the first
+ * `keep` (0..count) of them (generate_prepared + HybridCache::commit_verified,
+ * src/speculative.rs:370-416, src/hybrid.rs:699-759).
+ * mx_engine_clone_slot: copy one slot's caches to another (prefix reuse,
+ * PrefixCache src/speculative.rs:70-117). */
+mx_status mx_engine_create(const mx_model_config* cfg, mx_engine** out);
+mx_status mx_engine_destroy(mx_engine* e);
+mx_status mx_engine_reset_slot(mx_engine* e, int32_t slot);
+mx_status mx_engine_clone_slot(mx_engine* e, int32_t src, int32_t dst);
+int32_t mx_engine_offset(mx_engine* e, int32_t slot);
+mx_status mx_engine_decode_batch(mx_engine* e, const int32_t* slots, const uint32_t* tokens,
+                                 int32_t rows, uint32_t* next);
+mx_status mx_engine_decode_rows(mx_engine* e, const int32_t* slots, const uint32_t* tokens,
+                                int32_t rows, uint32_t* next);
+mx_status mx_engine_prefill(mx_engine* e, int32_t slot, const uint32_t* tokens, int32_t count,
+                            uint32_t* next);
+mx_status mx_engine_verify(mx_engine* e, int32_t slot, const uint32_t* tokens, int32_t count,
+                           uint32_t* argmax);
+mx_status mx_engine_commit(mx_engine* e, int32_t slot, int32_t keep);
+/* Test/inspection hooks: flags (bit 0: also write bf16 logits of each step;
+ * bit 1: run eagerly instead of replaying captured HIP graphs), and reads of
+ * the last step's "hidden" (bf16 [rows, hc*hidden]) / "logits" (bf16
+ * [rows, vocab]) or of any named weight/cache tensor into host memory. */
+mx_status mx_engine_set_flags(mx_engine* e, int32_t flags);
+mx_status mx_engine_read(mx_engine* e, const char* what, void* host, size_t bytes);
+mx_status mx_engine_tensor(mx_engine* e, const char* name, void** device_ptr, size_t* bytes);
 
 /* mx_gdn_scan: the delta rule alone, on given inputs — the reference's
  * gdn_kernel::recurrent / recurrent_with_history interface (src/gdn_kernel.rs:7-142):

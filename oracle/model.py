@@ -1,0 +1,251 @@
+"""CPU restatement of the engine's model step (the checker for end-to-end
+parity).  TEST INFRASTRUCTURE ONLY: used by tests/ and smoke(), never by the
+product.
+
+It follows HybridModel::forward_hidden (reference src/hybrid.rs:594-685) layer
+by layer with the oracle's C primitives, in the same arithmetic order as the
+engine's kernels, so tokens, hidden states and caches agree bit for bit.
+Weights are read from the engine under test (fetch(name, dtype, shape)); the
+caches are the oracle's own numpy arrays.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import oracle as orc
+
+_p = orc._p
+
+
+def rope_table(max_ctx: int, rot: int, theta: float):
+    """inv_freq = 1 / powf(theta, 2i/rot) in fp32 (reference src/rope.rs:20-24);
+    angle = pos * inv_freq in float64; cos/sin rounded to fp32 (libm, in C)."""
+    half = rot // 2
+    cs = np.empty((max_ctx, half), np.float32)
+    sn = np.empty((max_ctx, half), np.float32)
+    orc.lib.mxo_rope_table(max_ctx, rot, theta, _p(cs), _p(sn))
+    return cs, sn
+
+
+class Model:
+    def __init__(self, cfg: dict, fetch):
+        self.c = c = dict(cfg)
+        self.fetch = fetch
+        H, hc = c["hidden"], c["hc"]
+        self.H, self.hc = H, hc
+        self.cd = 2 * c["gdn_hk"] * 128 + c["gdn_hv"] * 128
+        self.vd = c["gdn_hv"] * 128
+        self.P = self.cd + self.vd + 2 * c["gdn_hv"]
+        self.Q = c["heads"] * 2 * c["head_dim"] + 2 * c["kv_heads"] * c["head_dim"]
+        self.attn = [(i % c["attn_every"]) == c["attn_every"] - 1 for i in range(c["layers"])]
+        self.cache_index = []
+        ng = na = 0
+        for a in self.attn:
+            self.cache_index.append(na if a else ng)
+            na, ng = (na + 1, ng) if a else (na, ng + 1)
+        self.n_gdn, self.n_attn = ng, na
+        self._keep = []
+        self.embed = self._qw("embed", c["vocab"], H, c["embed_bits"])
+        self.head = self._qw("head", c["vocab"], H, c["head_bits"])
+        self.mixer = self._hc("mixer", -1, False)
+        self.layers = []
+        for i in range(c["layers"]):
+            p = f"layers.{i}"
+            L = {"attn_hc": self._hc(p + ".attn_hc", i, True), "mlp_hc": self._hc(p + ".mlp_hc", i, True)}
+            bits, dbits = self.layer_bits(i)
+            if not self.attn[i]:
+                L["in"] = self._qw(p + ".gdn.in", self.P, H, bits)
+                L["conv_w"] = fetch(p + ".gdn.conv_w", np.float32, (c["conv_k"], self.cd))
+                L["a_log"] = fetch(p + ".gdn.a_log", np.float32, (c["gdn_hv"],))
+                L["dt"] = fetch(p + ".gdn.dt_bias", np.uint16, (c["gdn_hv"],))
+                L["norm"] = fetch(p + ".gdn.norm", np.uint16, (128,))
+                L["out"] = self._qw(p + ".gdn.out", H, self.vd, bits)
+            else:
+                L["in"] = self._qw(p + ".attn.in", self.Q, H, bits)
+                L["q_norm"] = fetch(p + ".attn.q_norm", np.uint16, (c["head_dim"],))
+                L["k_norm"] = fetch(p + ".attn.k_norm", np.uint16, (c["head_dim"],))
+                L["out"] = self._qw(p + ".attn.out", H, c["heads"] * c["head_dim"], bits)
+            E, I, SI = c["experts"], c["moe_inter"], c["shared_inter"]
+            L["router"] = self._qw(p + ".moe.router", E + 1, H, bits)
+            L["gate"] = self._bank(p + ".moe.gate", E, I, H, bits)
+            L["up"] = self._bank(p + ".moe.up", E, I, H, bits)
+            L["down"] = self._bank(p + ".moe.down", E, H, I, dbits)
+            L["sgate"] = self._qw(p + ".moe.shared_gate", SI, H, bits)
+            L["sup"] = self._qw(p + ".moe.shared_up", SI, H, bits)
+            L["sdown"] = self._qw(p + ".moe.shared_down", H, SI, dbits)
+            self.layers.append(L)
+        S = c["max_slots"]
+        self.state = np.zeros((S * self.n_gdn, c["gdn_hv"], 128, 128), np.float32)
+        self.conv = np.zeros((S * self.n_gdn, c["conv_k"] - 1, self.cd), np.uint16)
+        self.kv_slot_stride = self.n_attn * c["kv_heads"] * c["max_context"] * c["head_dim"]
+        self.k = np.zeros(S * self.kv_slot_stride, np.uint16)
+        self.v = np.zeros(S * self.kv_slot_stride, np.uint16)
+        self.offsets = [0] * S
+        self.cos, self.sin = rope_table(c["max_context"], c["rotary_dim"], c["rope_theta"])
+        self.hidden = None
+
+    # ---- weights ----
+    def layer_bits(self, i):
+        """(projection bits, expert-down bits) of layer i: the base widths, or
+        with mixed_bits a seeded draw from {4,5,6,8} (same rule as the engine)."""
+        if not self.c.get("mixed_bits") or i < 0:
+            return self.c["bits"], self.c["down_bits"]
+        choices = (4, 5, 6, 8)
+        key = (self.c["seed"] ^ 0x5BD1E995) & (2**64 - 1)
+        return tuple(choices[orc.lib.mxo_rng_u64(key, i * 2 + w) & 3] for w in (0, 1))
+
+    def _qw(self, name, n, k, bits):
+        gs = self.c["group_size"]
+        codes = self.fetch(name + ".codes", np.uint32, (n, k * bits // 32))
+        s = self.fetch(name + ".scales", np.uint16, (n, k // gs))
+        b = self.fetch(name + ".biases", np.uint16, (n, k // gs))
+        self._keep += [codes, s, b]
+        return orc.qw(codes, s, b, n, k, bits, gs)
+
+    def _bank(self, name, E, n, k, bits):
+        gs = self.c["group_size"]
+        codes = self.fetch(name + ".codes", np.uint32, (E * n, k * bits // 32))
+        s = self.fetch(name + ".scales", np.uint16, (E * n, k // gs))
+        b = self.fetch(name + ".biases", np.uint16, (E * n, k // gs))
+        self._keep += [codes, s, b]
+        return orc.qbank(codes, s, b, E, n, k, bits, gs)
+
+    def _hc(self, p, layer, inject):
+        c = self.c
+        bits = self.layer_bits(layer)[0] if layer >= 0 else c["bits"]
+        scale = self.fetch(p + ".scale", np.uint16, (c["hc"] * c["hidden"],))
+        self._keep.append(scale)
+        down = self._qw(p + ".down", c["hc_rank"] + (c["hc"] if inject else 0), c["hc"] * c["hidden"], bits)
+        up = self._qw(p + ".up", c["hc"] * c["hidden"], c["hc_rank"], bits)
+        return {"scale": scale, "down": down, "up": up, "inject": inject}
+
+    # ---- pieces ----
+    def _hc_forward(self, w, h, rows):
+        c = self.c
+        xn = np.empty_like(h)
+        orc.lib.mxo_hc_norm(_p(h), _p(w["scale"]), rows, c["hc"], c["hidden"], c["rms_eps"], _p(xn))
+        lo = np.empty((rows, c["hc_rank"]), np.uint16)
+        inj = np.empty((rows, c["hc"]), np.uint16)
+        orc.lib.mxo_hc_down(C.byref(w["down"]), _p(xn), rows, c["hc_rank"], c["hc"], _p(lo), _p(inj))
+        mixed = np.empty((rows, c["hidden"]), np.uint16)
+        orc.lib.mxo_hc_up_mix(C.byref(w["up"]), _p(lo), _p(xn), rows, c["hidden"], _p(mixed))
+        return mixed, inj
+
+    def _qmv(self, w, x):
+        x = np.ascontiguousarray(x, np.uint16)
+        y = np.empty((x.shape[0], w.n), np.uint16)
+        orc.lib.mxo_qmv(w.codes, w.scales, w.biases, w.n, w.k, w.bits, w.gs, _p(x), x.shape[0], _p(y))
+        return y
+
+    def step(self, tokens, slots, pos, groups, t, history=None):
+        """One engine step over rows (slot, position); GDN rows grouped as
+        `groups` sequences of `t` tokens.  Returns greedy next tokens."""
+        c = self.c
+        rows = len(tokens)
+        H, hc = self.H, self.hc
+        tok = np.ascontiguousarray(tokens, np.uint32)
+        h = np.empty((rows, hc * H), np.uint16)
+        orc.lib.mxo_embed(C.byref(self.embed), _p(tok), rows, hc, _p(h))
+        slots_a = np.ascontiguousarray(slots, np.int32)
+        pos_a = np.ascontiguousarray(pos, np.int32)
+        gdn_slots = np.array([slots[g * t] * self.n_gdn for g in range(groups)], np.int32)
+        for i, L in enumerate(self.layers):
+            mixed, inj = self._hc_forward(L["attn_hc"], h, rows)
+            if not self.attn[i]:
+                gi = self.cache_index[i]
+                proj = self._qmv(L["in"], mixed)
+                qkv = np.ascontiguousarray(proj[:, :self.cd])
+                sl = gdn_slots + gi
+                conv_out = np.empty((rows, self.cd), np.uint16)
+                win = np.empty((groups, c["conv_k"] - 1 + t, self.cd), np.uint16) if history is not None else None
+                orc.lib.mxo_gdn_conv(_p(qkv), self.cd, groups, t, _p(sl), _p(self.conv), _p(L["conv_w"]),
+                                     self.cd, c["conv_k"], _p(conv_out), self.cd,
+                                     _p(win) if win is not None else None)
+                zab = np.ascontiguousarray(proj[:, self.cd:])
+                zp = zab.ctypes.data
+                hist = np.empty((rows, c["gdn_hv"], 128, 128), np.float32) if history is not None else None
+                y = np.empty((rows, self.vd), np.uint16)
+                orc.lib.mxo_gdn_recurrence(_p(conv_out), self.cd, zp, zp + 2 * self.vd,
+                                           zp + 2 * (self.vd + c["gdn_hv"]), zab.shape[1], _p(L["a_log"]),
+                                           _p(L["dt"]), _p(L["norm"]), c["rms_eps"], c["gdn_hk"],
+                                           c["gdn_hv"], groups, t, _p(sl), _p(self.state),
+                                           _p(hist) if hist is not None else None, _p(y))
+                if history is not None:
+                    history.append((gi, hist, win))
+                orc.lib.mxo_hc_write(C.byref(L["out"]), _p(y), rows, hc, _p(h), _p(inj))
+            else:
+                ai = self.cache_index[i]
+                qkv = self._qmv(L["in"], mixed)
+                layer_off = ai * c["kv_heads"] * c["max_context"] * c["head_dim"]
+                kview = self.k[layer_off:]
+                vview = self.v[layer_off:]
+                q = np.empty((rows, c["heads"] * c["head_dim"]), np.uint16)
+                orc.lib.mxo_attn_prep(_p(qkv), self.Q, rows, _p(slots_a), _p(pos_a), _p(L["q_norm"]),
+                                      _p(L["k_norm"]), c["rms_eps"], _p(self.cos), _p(self.sin),
+                                      c["heads"], c["kv_heads"], c["head_dim"], c["rotary_dim"],
+                                      c["max_context"], self.kv_slot_stride, _p(q), kview.ctypes.data,
+                                      vview.ctypes.data)
+                y = np.empty((rows, c["heads"] * c["head_dim"]), np.uint16)
+                orc.lib.mxo_attention(_p(q), _p(qkv), self.Q, rows, _p(slots_a), _p(pos_a),
+                                      kview.ctypes.data, vview.ctypes.data, c["heads"], c["kv_heads"],
+                                      c["head_dim"], c["max_context"], self.kv_slot_stride, _p(y))
+                orc.lib.mxo_hc_write(C.byref(L["out"]), _p(y), rows, hc, _p(h), _p(inj))
+            mixed, inj = self._hc_forward(L["mlp_hc"], h, rows)
+            logits = self._qmv(L["router"], mixed)
+            E = c["experts"]
+            ids, scores, factor = orc.moe_route(np.ascontiguousarray(logits[:, :E]),
+                                                np.ascontiguousarray(logits[:, E]), c["top_k"])
+            pbuf = np.empty((rows, c["top_k"] + 1, H), np.uint16)
+            orc.lib.mxo_moe_experts(_p(mixed), _p(ids), _p(scores), rows, c["top_k"], C.byref(L["gate"]),
+                                    C.byref(L["up"]), C.byref(L["down"]), C.byref(L["sgate"]),
+                                    C.byref(L["sup"]), C.byref(L["sdown"]), _p(pbuf))
+            routed = orc.moe_reduce(pbuf, c["top_k"])
+            shared = np.ascontiguousarray(pbuf[:, c["top_k"], :])
+            h = orc.moe_hc_epilogue(routed, shared, factor, h, inj, hc)
+        self.hidden = h.copy()
+        mixed, _ = self._hc_forward(self.mixer, h, rows)
+        self.last_mixed = mixed
+        return orc.head_argmax(self.head, mixed)
+
+    # ---- engine-level operations (same contracts as the C ABI) ----
+    def decode_rows(self, slots, tokens):
+        pos = [self.offsets[s] for s in slots]
+        out = self.step(tokens, slots, pos, len(slots), 1)
+        for s in slots:
+            self.offsets[s] += 1
+        return out
+
+    def block(self, slot, tokens, history=None):
+        n = len(tokens)
+        pos = [self.offsets[slot] + i for i in range(n)]
+        out = self.step(tokens, [slot] * n, pos, 1, n, history)
+        self.offsets[slot] += n
+        return out
+
+    def prefill(self, slot, tokens):
+        nxt = None
+        for i in range(0, len(tokens), 8):
+            nxt = self.block(slot, tokens[i:i + 8])[-1]
+        return nxt
+
+    def verify(self, slot, tokens):
+        self._snap = (slot, self.offsets[slot],
+                      self.state[slot * self.n_gdn:(slot + 1) * self.n_gdn].copy(),
+                      self.conv[slot * self.n_gdn:(slot + 1) * self.n_gdn].copy())
+        self._hist = []
+        return self.block(slot, tokens, self._hist)
+
+    def commit(self, slot, keep):
+        s0, base, st, cv = self._snap
+        assert s0 == slot
+        K = self.c["conv_k"]
+        if keep == 0:
+            self.state[slot * self.n_gdn:(slot + 1) * self.n_gdn] = st
+            self.conv[slot * self.n_gdn:(slot + 1) * self.n_gdn] = cv
+        else:
+            for gi, hist, win in self._hist:
+                self.state[slot * self.n_gdn + gi] = hist[keep - 1]
+                self.conv[slot * self.n_gdn + gi] = win[0, keep:keep + K - 1]
+        self.offsets[slot] = base + keep

@@ -93,6 +93,27 @@ void mxo_gdn_scan(const uint16_t* q, const uint16_t* k, const uint16_t* v, const
 void mxo_argmax_bf16(const uint16_t* logits, int rows, int n, uint32_t* tokens);
 void mxo_head_argmax(const mxo_qw* w, const uint16_t* x, int m, uint32_t* tokens, float* scratch);
 
+/* ---- model step pieces (model.c) ---- */
+void mxo_hc_norm(const uint16_t* x, const uint16_t* scale, int rows, int hc, int hidden, float eps,
+                 uint16_t* y);
+void mxo_hc_down(const mxo_qw* w, const uint16_t* xn, int rows, int rank, int hc, uint16_t* lo,
+                 uint16_t* inj);
+void mxo_hc_up_mix(const mxo_qw* w, const uint16_t* lo, const uint16_t* xn, int rows, int hidden,
+                   uint16_t* mixed);
+void mxo_hc_write(const mxo_qw* w, const uint16_t* y, int rows, int hc, uint16_t* residual,
+                  const uint16_t* inj);
+void mxo_embed(const mxo_qw* w, const uint32_t* ids, int count, int hc, uint16_t* out);
+void mxo_attn_prep(const uint16_t* qkv, int64_t qkv_stride, int rows, const int32_t* slots,
+                   const int32_t* pos, const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+                   const float* rope_cos, const float* rope_sin, int heads, int kv_heads, int hd,
+                   int rot, int max_ctx, int64_t slot_stride, uint16_t* q_out, uint16_t* k_cache,
+                   uint16_t* v_cache);
+void mxo_attention(const uint16_t* q, const uint16_t* qkv, int64_t qkv_stride, int rows,
+                   const int32_t* slots, const int32_t* pos, const uint16_t* k_cache,
+                   const uint16_t* v_cache, int heads, int kv_heads, int hd, int max_ctx,
+                   int64_t slot_stride, uint16_t* out);
+void mxo_rope_table(int max_ctx, int rot, float theta, float* cos_out, float* sin_out);
+
 int mxo_num_threads(void);
 
 #ifdef __cplusplus

@@ -48,6 +48,15 @@ def _load() -> C.CDLL:
         "mxo_gdn_scan": ([vp, vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp], None),
         "mxo_argmax_bf16": ([vp, i32, i32, vp], None),
         "mxo_head_argmax": ([vp, vp, i32, vp, vp], None),
+        "mxo_hc_norm": ([vp, vp, i32, i32, i32, f32, vp], None),
+        "mxo_hc_down": ([vp, vp, i32, i32, i32, vp, vp], None),
+        "mxo_hc_up_mix": ([vp, vp, vp, i32, i32, vp], None),
+        "mxo_hc_write": ([vp, vp, i32, i32, vp, vp], None),
+        "mxo_embed": ([vp, vp, i32, i32, vp], None),
+        "mxo_attn_prep": ([vp, i64, i32, vp, vp, vp, vp, f32, vp, vp, i32, i32, i32, i32, i32,
+                           i64, vp, vp, vp], None),
+        "mxo_rope_table": ([i32, i32, f32, vp, vp], None),
+        "mxo_attention": ([vp, vp, i64, i32, vp, vp, vp, vp, i32, i32, i32, i32, i64, vp], None),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)

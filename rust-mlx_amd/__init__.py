@@ -63,6 +63,16 @@ class GdnDimsC(C.Structure):
                 ("conv_k", C.c_int32)]
 
 
+class ModelConfigC(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in (
+        "hidden", "layers", "attn_every", "vocab", "hc", "hc_rank", "gdn_hk", "gdn_hv", "gdn_dk",
+        "gdn_dv", "conv_k", "heads", "kv_heads", "head_dim", "rotary_dim")] + [
+        ("rope_theta", C.c_float), ("rms_eps", C.c_float)] + [(n, C.c_int32) for n in (
+            "experts", "top_k", "moe_inter", "shared_inter", "bits", "down_bits", "embed_bits",
+            "head_bits", "group_size", "mixed_bits", "max_slots", "max_context", "max_verify")] + [
+        ("seed", C.c_uint64)]
+
+
 def _load() -> C.CDLL:
     if not os.path.exists(LIB_PATH):
         raise ImportError(
@@ -108,6 +118,19 @@ def _load() -> C.CDLL:
                                i32, i32, vp, vp, vp, vp, vp], i32),
         "mx_gdn_scan": ([vp, vp, vp, vp, vp, C.POINTER(GdnDimsC), i32, i32, vp, vp, vp, vp,
                          vp], i32),
+        "mx_engine_create": ([C.POINTER(ModelConfigC), C.POINTER(vp)], i32),
+        "mx_engine_destroy": ([vp], i32),
+        "mx_engine_reset_slot": ([vp, i32], i32),
+        "mx_engine_clone_slot": ([vp, i32, i32], i32),
+        "mx_engine_offset": ([vp, i32], i32),
+        "mx_engine_decode_batch": ([vp, vp, vp, i32, vp], i32),
+        "mx_engine_decode_rows": ([vp, vp, vp, i32, vp], i32),
+        "mx_engine_prefill": ([vp, i32, vp, i32, vp], i32),
+        "mx_engine_verify": ([vp, i32, vp, i32, vp], i32),
+        "mx_engine_commit": ([vp, i32, i32], i32),
+        "mx_engine_set_flags": ([vp, i32], i32),
+        "mx_engine_read": ([vp, C.c_char_p, vp, sz], i32),
+        "mx_engine_tensor": ([vp, C.c_char_p, C.POINTER(vp), C.POINTER(sz)], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -250,3 +273,88 @@ def fill_bf16(d: DeviceArray, seed: int, dist: int, a: float, b: float) -> None:
 
 def sync() -> None:
     check(lib.mx_device_sync())
+
+
+# ---- model configurations (BASELINE configs 3 and 4, and a tiny test model) ----
+CONFIG3 = dict(hidden=2048, layers=48, attn_every=4, vocab=151936, hc=4, hc_rank=256, gdn_hk=16,
+               gdn_hv=32, gdn_dk=128, gdn_dv=128, conv_k=4, heads=16, kv_heads=2, head_dim=256,
+               rotary_dim=64, rope_theta=1e7, rms_eps=1e-6, experts=512, top_k=10, moe_inter=512,
+               shared_inter=512, bits=4, down_bits=5, embed_bits=8, head_bits=8, group_size=64,
+               mixed_bits=0, max_slots=8, max_context=4096, max_verify=8, seed=20250)
+
+TINY = dict(hidden=256, layers=4, attn_every=4, vocab=1024, hc=4, hc_rank=64, gdn_hk=1, gdn_hv=2,
+            gdn_dk=128, gdn_dv=128, conv_k=4, heads=2, kv_heads=1, head_dim=128, rotary_dim=32,
+            rope_theta=1e7, rms_eps=1e-6, experts=64, top_k=4, moe_inter=64, shared_inter=128,
+            bits=4, down_bits=5, embed_bits=8, head_bits=8, group_size=64, mixed_bits=0,
+            max_slots=6, max_context=600, max_verify=8, seed=77)
+
+
+class Engine:
+    """Host handle of an mx_engine (synchronous calls, one owning thread)."""
+
+    def __init__(self, cfg: dict):
+        self.cfg = dict(cfg)
+        cc = ModelConfigC(**self.cfg)
+        h = C.c_void_p()
+        check(lib.mx_engine_create(C.byref(cc), C.byref(h)))
+        self.h = h.value
+
+    def close(self):
+        if self.h:
+            lib.mx_engine_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @staticmethod
+    def _u32(a):
+        return np.ascontiguousarray(a, np.uint32)
+
+    def decode_batch(self, slots, tokens, equal=True) -> np.ndarray:
+        s = np.ascontiguousarray(slots, np.int32)
+        t = self._u32(tokens)
+        out = np.empty(len(s), np.uint32)
+        fn = lib.mx_engine_decode_batch if equal else lib.mx_engine_decode_rows
+        check(fn(self.h, s.ctypes.data, t.ctypes.data, len(s), out.ctypes.data))
+        return out
+
+    def prefill(self, slot, tokens) -> int:
+        t = self._u32(tokens)
+        out = np.empty(1, np.uint32)
+        check(lib.mx_engine_prefill(self.h, slot, t.ctypes.data, len(t), out.ctypes.data))
+        return int(out[0])
+
+    def verify(self, slot, tokens) -> np.ndarray:
+        t = self._u32(tokens)
+        out = np.empty(len(t), np.uint32)
+        check(lib.mx_engine_verify(self.h, slot, t.ctypes.data, len(t), out.ctypes.data))
+        return out
+
+    def commit(self, slot, keep):
+        check(lib.mx_engine_commit(self.h, slot, keep))
+
+    def reset(self, slot):
+        check(lib.mx_engine_reset_slot(self.h, slot))
+
+    def clone(self, src, dst):
+        check(lib.mx_engine_clone_slot(self.h, src, dst))
+
+    def offset(self, slot) -> int:
+        return lib.mx_engine_offset(self.h, slot)
+
+    def set_flags(self, logits=False, eager=False):
+        check(lib.mx_engine_set_flags(self.h, (1 if logits else 0) | (2 if eager else 0)))
+
+    def read(self, what: str, dtype, shape) -> np.ndarray:
+        out = np.empty(shape, dtype)
+        check(lib.mx_engine_read(self.h, what.encode(), out.ctypes.data, out.nbytes))
+        return out
+
+    def tensor_bytes(self, name: str) -> int:
+        p, n = C.c_void_p(), C.c_size_t()
+        check(lib.mx_engine_tensor(self.h, name.encode(), C.byref(p), C.byref(n)))
+        return n.value

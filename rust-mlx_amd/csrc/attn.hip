@@ -1,0 +1,282 @@
+// Gated full attention for decode / verify rows (gfx950).
+//
+// Reference: Attention::forward_selection with gated = true (src/dense.rs:139-270):
+// q/gate projection split per head, zero-centred q/k norms (compiled::norm,
+// src/compiled.rs:22-28), partial text RoPE (src/rope.rs:8-57,
+// kernels/text_rope.metal), KV append (KvCache::update, src/dense.rs:46-110),
+// scaled dot-product attention over the cached positions (MLX
+// fast::scaled_dot_product_attention), output * sigmoid(gate).
+//
+// Every row carries its own (slot, position): rows of one decode step may sit
+// at different offsets, and rows of one verify block attend causally (row r
+// sees positions <= pos[r]).  The cache holds K and V as bf16
+// [slot][layer][kv_head][position][head_dim].
+//
+// Decoding splits each row's positions into chunks of kAttnChunk; a workgroup
+// handles one (chunk, kv head, row) for all q heads sharing the kv head, so K
+// and V stream once per group.  A second pass combines the chunks.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace mx {
+
+namespace {
+
+constexpr int kMaxHd = 256;
+constexpr int kMaxGroup = 16;  // q heads per kv head
+
+__device__ __forceinline__ float sigmoid_bf16(float x) {
+  const float e = round_bf16(expf_(__builtin_fabsf(x)));
+  const float d = round_bf16(1.0f + e);
+  const float y = round_bf16(1.0f / d);
+  return x < 0.0f ? y : round_bf16(1.0f - y);
+}
+
+// ---------------------------------------------------------------------------
+// One wave per (row, head): zero-centred RMS norm over head_dim, then RoPE on
+// the first rotary_dim values (halves rotated), written to q_out (q heads) or
+// appended to the cache (k heads; v heads are appended unchanged).
+// Norm: lane l sums x^2 over l, l+64, ... in order, xor butterfly;
+// y = bf16((x * rsqrt(mean + eps)) * (w + 1)).
+// RoPE: out[i] = bf16(x1 c - x2 s), out[i+h] = bf16(x2 c + x1 s), c/s from the
+// fp32 table of the row's position.
+__global__ __launch_bounds__(64) void prep_kernel(const uint16_t* __restrict__ qkv,
+                                                  int64_t qkv_stride,
+                                                  const int32_t* __restrict__ slots,
+                                                  const int32_t* __restrict__ pos,
+                                                  const uint16_t* __restrict__ q_norm,
+                                                  const uint16_t* __restrict__ k_norm, float eps,
+                                                  const float* __restrict__ rope_cos,
+                                                  const float* __restrict__ rope_sin,
+                                                  AttnDims d, uint16_t* __restrict__ q_out,
+                                                  uint16_t* __restrict__ k_cache,
+                                                  uint16_t* __restrict__ v_cache) {
+  __shared__ float buf[kMaxHd];
+  const int head = blockIdx.x;  // [0, heads) q, [heads, heads + kv) k, then v
+  const int row = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int hd = d.head_dim;
+  const uint16_t* xr = qkv + size_t(row) * qkv_stride;
+  const int p = pos[row];
+  const size_t cache_off =
+      size_t(slots[row]) * d.slot_stride;  // + (kvh * max_ctx + p) * hd below
+  if (head >= d.heads + d.kv_heads) {
+    const int kvh = head - d.heads - d.kv_heads;
+    const uint16_t* src = xr + size_t(d.heads) * 2 * hd + size_t(d.kv_heads) * hd + size_t(kvh) * hd;
+    uint16_t* dst = v_cache + cache_off + (size_t(kvh) * d.max_ctx + p) * hd;
+    for (int c = lane; c < hd; c += 64) dst[c] = src[c];
+    return;
+  }
+  const bool is_q = head < d.heads;
+  const int h = is_q ? head : head - d.heads;
+  const uint16_t* src = is_q ? xr + size_t(h) * 2 * hd  // [heads, 2, hd]: q then gate
+                             : xr + size_t(d.heads) * 2 * hd + size_t(h) * hd;
+  const uint16_t* w = is_q ? q_norm : k_norm;
+  float acc = 0.0f;
+  for (int c = lane; c < hd; c += 64) {
+    const float v = bf16_to_f32(src[c]);
+    acc = acc + v * v;
+  }
+  for (int o = 32; o > 0; o >>= 1) acc = acc + __shfl_xor(acc, o, 64);
+  const float inv = 1.0f / __builtin_sqrtf(acc / float(hd) + eps);
+  for (int c = lane; c < hd; c += 64)
+    buf[c] = round_bf16((bf16_to_f32(src[c]) * inv) * (bf16_to_f32(w[c]) + 1.0f));
+  __syncthreads();
+  uint16_t* dst = is_q ? q_out + (size_t(row) * d.heads + h) * hd
+                       : k_cache + cache_off + (size_t(h) * d.max_ctx + p) * hd;
+  const int half = d.rotary_dim / 2;
+  const float* cs = rope_cos + size_t(p) * half;
+  const float* sn = rope_sin + size_t(p) * half;
+  for (int c = lane; c < hd; c += 64) {
+    float v;
+    if (c < half) {
+      v = buf[c] * cs[c] - buf[c + half] * sn[c];
+    } else if (c < 2 * half) {
+      const int i = c - half;
+      v = buf[c] * cs[i] + buf[i] * sn[i];
+    } else {
+      v = buf[c];
+    }
+    dst[c] = f32_to_bf16(v);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Partial attention of one chunk for the G q heads of one kv head.
+// Scores: thread t owns position j = chunk*C + t; s = (q . k_j) * scale, the dot
+// as four interleaved fma chains over d (d mod 4), then (c0+c1)+(c2+c3).
+// m = max_t s; p = e^(s - m); l = sum_t p (xor butterfly per wave, waves in
+// order).  Values: thread t owns dim t; o = sum_j p_j v_j[t] (fma chain, j
+// ascending).  Writes (m, l) and o (fp32) per (row, head, chunk).
+template <int G>
+__global__ __launch_bounds__(kAttnChunk) void decode_kernel(
+    const uint16_t* __restrict__ q, const int32_t* __restrict__ slots,
+    const int32_t* __restrict__ pos, const uint16_t* __restrict__ k_cache,
+    const uint16_t* __restrict__ v_cache, AttnDims d, int max_chunks, float scale,
+    float* __restrict__ o_part, float* __restrict__ ml_part) {
+  __shared__ float qs[G][kMaxHd];
+  __shared__ float ps[G][kAttnChunk];
+  __shared__ float red[G][4];
+  const int chunk = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int row = blockIdx.z;
+  const int t = threadIdx.x;
+  const int n_pos = pos[row] + 1;
+  const int j0 = chunk * kAttnChunk;
+  if (j0 >= n_pos) return;  // uniform per workgroup
+  const int hd = d.head_dim;
+  for (int i = t; i < G * hd; i += kAttnChunk) {
+    const int g = i / hd, c = i - g * hd;
+    qs[g][c] = bf16_to_f32(q[(size_t(row) * d.heads + kvh * G + g) * hd + c]);
+  }
+  __syncthreads();
+  const size_t base = size_t(slots[row]) * d.slot_stride + size_t(kvh) * d.max_ctx * hd;
+  const int j = j0 + t;
+  const bool valid = j < n_pos;
+  if (valid) {
+    const uint16_t* kr = k_cache + base + size_t(j) * hd;
+    float c0[G], c1[G], c2[G], c3[G];
+    for (int g = 0; g < G; ++g) c0[g] = c1[g] = c2[g] = c3[g] = 0.0f;
+    for (int c = 0; c < hd; c += 8) {
+      const uint4 raw = *reinterpret_cast<const uint4*>(kr + c);
+      const float kv[8] = {u2f(raw.x << 16), u2f(raw.x & 0xffff0000u), u2f(raw.y << 16),
+                           u2f(raw.y & 0xffff0000u), u2f(raw.z << 16), u2f(raw.z & 0xffff0000u),
+                           u2f(raw.w << 16), u2f(raw.w & 0xffff0000u)};
+      for (int g = 0; g < G; ++g) {
+        c0[g] = fmaf_(qs[g][c + 0], kv[0], c0[g]);
+        c1[g] = fmaf_(qs[g][c + 1], kv[1], c1[g]);
+        c2[g] = fmaf_(qs[g][c + 2], kv[2], c2[g]);
+        c3[g] = fmaf_(qs[g][c + 3], kv[3], c3[g]);
+        c0[g] = fmaf_(qs[g][c + 4], kv[4], c0[g]);
+        c1[g] = fmaf_(qs[g][c + 5], kv[5], c1[g]);
+        c2[g] = fmaf_(qs[g][c + 6], kv[6], c2[g]);
+        c3[g] = fmaf_(qs[g][c + 7], kv[7], c3[g]);
+      }
+    }
+    for (int g = 0; g < G; ++g) ps[g][t] = ((c0[g] + c1[g]) + (c2[g] + c3[g])) * scale;
+  } else {
+    for (int g = 0; g < G; ++g) ps[g][t] = u2f(0xff800000u);
+  }
+  __syncthreads();
+  // per-head max and sum over the chunk
+  const int wave = t >> 6;
+  for (int g = 0; g < G; ++g) {
+    float m = ps[g][t];
+    for (int o = 32; o > 0; o >>= 1) {
+      const float v = __shfl_xor(m, o, 64);
+      m = v > m ? v : m;
+    }
+    if ((t & 63) == 0) red[g][wave] = m;
+  }
+  __syncthreads();
+  float mg[G];
+  for (int g = 0; g < G; ++g) {
+    float m = red[g][0];
+    for (int w = 1; w < kAttnChunk / 64; ++w) m = red[g][w] > m ? red[g][w] : m;
+    mg[g] = m;
+  }
+  __syncthreads();
+  for (int g = 0; g < G; ++g) {
+    const float pv = valid ? expf_(ps[g][t] - mg[g]) : 0.0f;
+    ps[g][t] = pv;
+    float l = pv;
+    for (int o = 32; o > 0; o >>= 1) l = l + __shfl_xor(l, o, 64);
+    if ((t & 63) == 0) red[g][wave] = l;
+  }
+  __syncthreads();
+  const int heads = d.heads;
+  if (t < G) {
+    const int g = t;
+    float l = red[g][0];
+    for (int w = 1; w < kAttnChunk / 64; ++w) l = l + red[g][w];
+    float* ml = ml_part + ((size_t(row) * heads + kvh * G + g) * max_chunks + chunk) * 2;
+    ml[0] = mg[g];
+    ml[1] = l;
+  }
+  if (t < hd) {
+    const int jend = min(n_pos - j0, kAttnChunk);
+    float o[G];
+    for (int g = 0; g < G; ++g) o[g] = 0.0f;
+    const uint16_t* vr = v_cache + base + size_t(j0) * hd + t;
+    for (int jj = 0; jj < jend; ++jj) {
+      const float v = bf16_to_f32(vr[size_t(jj) * hd]);
+      for (int g = 0; g < G; ++g) o[g] = fmaf_(ps[g][jj], v, o[g]);
+    }
+    for (int g = 0; g < G; ++g)
+      o_part[((size_t(row) * heads + kvh * G + g) * max_chunks + chunk) * hd + t] = o[g];
+  }
+}
+
+// Combines the chunks of one (row, head) and applies the output gate:
+//   M = max m_c; w_c = e^(m_c - M); L = sum l_c w_c; O = sum o_c w_c (fma, c
+//   ascending); y = bf16(bf16(O / L) * sigmoid_bf16(gate)).
+__global__ __launch_bounds__(kMaxHd) void combine_kernel(const float* __restrict__ o_part,
+                                                         const float* __restrict__ ml_part,
+                                                         const uint16_t* __restrict__ qkv,
+                                                         int64_t qkv_stride,
+                                                         const int32_t* __restrict__ pos,
+                                                         AttnDims d, int max_chunks,
+                                                         uint16_t* __restrict__ out) {
+  const int h = blockIdx.x;
+  const int row = blockIdx.y;
+  const int t = threadIdx.x;
+  const int hd = d.head_dim;
+  if (t >= hd) return;
+  const int chunks = (pos[row] + kAttnChunk) / kAttnChunk;
+  const float* ml = ml_part + (size_t(row) * d.heads + h) * max_chunks * 2;
+  const float* op = o_part + (size_t(row) * d.heads + h) * max_chunks * hd + t;
+  float M = ml[0];
+  for (int c = 1; c < chunks; ++c) M = ml[2 * c] > M ? ml[2 * c] : M;
+  float L = 0.0f, O = 0.0f;
+  for (int c = 0; c < chunks; ++c) {
+    const float wc = expf_(ml[2 * c] - M);
+    L = fmaf_(ml[2 * c + 1], wc, L);
+    O = fmaf_(op[size_t(c) * hd], wc, O);
+  }
+  const float attn = round_bf16(O / L);
+  const float gate = bf16_to_f32(qkv[size_t(row) * qkv_stride + size_t(h) * 2 * hd + hd + t]);
+  out[(size_t(row) * d.heads + h) * hd + t] = f32_to_bf16(attn * sigmoid_bf16(gate));
+}
+
+}  // namespace
+
+int attn_prep(const uint16_t* qkv, int64_t qkv_stride, int rows, const int32_t* slots,
+              const int32_t* pos, const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+              const float* rope_cos, const float* rope_sin, AttnDims d, uint16_t* q_out,
+              uint16_t* k_cache, uint16_t* v_cache, hipStream_t s) {
+  if (d.head_dim > kMaxHd || d.head_dim % 8 != 0) return MX_EUNSUPPORTED;
+  hipLaunchKernelGGL(prep_kernel, dim3(d.heads + 2 * d.kv_heads, rows), dim3(64), 0, s, qkv,
+                     qkv_stride, slots, pos, q_norm, k_norm, eps, rope_cos, rope_sin, d, q_out,
+                     k_cache, v_cache);
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
+int attn_decode(const uint16_t* q, int rows, const int32_t* slots, const int32_t* pos,
+                const uint16_t* k_cache, const uint16_t* v_cache, AttnDims d, int max_chunks,
+                float* o_part, float* ml_part, hipStream_t s) {
+  if (d.head_dim > kMaxHd || d.heads % d.kv_heads != 0 || d.heads / d.kv_heads > kMaxGroup)
+    return MX_EUNSUPPORTED;
+  const float scale = 1.0f / __builtin_sqrtf(float(d.head_dim));
+  const dim3 grid(max_chunks, d.kv_heads, rows);
+#define MX_DEC(GG)                                                                         \
+  case GG:                                                                                 \
+    hipLaunchKernelGGL(decode_kernel<GG>, grid, dim3(kAttnChunk), 0, s, q, slots, pos,     \
+                       k_cache, v_cache, d, max_chunks, scale, o_part, ml_part);           \
+    break;
+  switch (d.heads / d.kv_heads) {
+    MX_DEC(1) MX_DEC(2) MX_DEC(4) MX_DEC(8) MX_DEC(16)
+    default: return MX_EUNSUPPORTED;
+  }
+#undef MX_DEC
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
+int attn_combine(const float* o_part, const float* ml_part, const uint16_t* qkv,
+                 int64_t qkv_stride, int rows, const int32_t* pos, AttnDims d, int max_chunks,
+                 uint16_t* out, hipStream_t s) {
+  hipLaunchKernelGGL(combine_kernel, dim3(d.heads, rows), dim3(kMaxHd), 0, s, o_part, ml_part,
+                     qkv, qkv_stride, pos, d, max_chunks, out);
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
+}  // namespace mx

@@ -368,3 +368,173 @@ MX_ABI mx_status mx_gdn_scan(const uint16_t* q, const uint16_t* k, const uint16_
                          hipStream_t(stream)),
                 "mx_gdn_scan");
 }
+
+// ---- engine ---------------------------------------------------------------
+struct mx_engine {
+  mx::Engine* impl;
+};
+
+namespace {
+const char* check_config(const mx_model_config& c) {
+  if (c.hidden <= 0 || c.hidden % 64 != 0) return "hidden must be a positive multiple of 64";
+  if (c.layers <= 0 || c.attn_every <= 0) return "layers and attn_every must be positive";
+  if (c.vocab <= 0) return "vocab must be positive";
+  if (c.hc != 4) return "hc must be 4";
+  if (c.hc_rank <= 0 || c.hc_rank % 64 != 0) return "hc_rank must be a positive multiple of 64";
+  if (c.gdn_dk != 128 || c.gdn_dv != 128) return "GDN head dims must be 128";
+  if (c.gdn_hk <= 0 || c.gdn_hv % c.gdn_hk != 0) return "GDN value heads must be a multiple of key heads";
+  if (c.conv_k < 2 || c.conv_k > 8) return "conv_k must be in 2..8";
+  if (c.kv_heads <= 0 || c.heads % c.kv_heads != 0) return "heads must be a multiple of kv_heads";
+  const int g = c.heads / (c.kv_heads > 0 ? c.kv_heads : 1);
+  if (g != 1 && g != 2 && g != 4 && g != 8 && g != 16) return "heads / kv_heads must be 1, 2, 4, 8 or 16";
+  if (c.head_dim <= 0 || c.head_dim > 256 || c.head_dim % 64 != 0) return "head_dim must be 64, 128, 192 or 256";
+  if (c.rotary_dim <= 0 || c.rotary_dim % 2 != 0 || c.rotary_dim > c.head_dim) return "bad rotary_dim";
+  if (c.experts % 64 != 0 || c.experts / 64 > 16 || (c.experts / 64) & (c.experts / 64 - 1))
+    return "experts must be 64, 128, 256, 512 or 1024";
+  if (c.top_k < 1 || c.top_k > 16) return "top_k must be in 1..16";
+  if (c.moe_inter <= 0 || c.shared_inter <= 0 || c.moe_inter % 64 || c.shared_inter % 64)
+    return "expert intermediate sizes must be positive multiples of 64";
+  if (c.group_size != 32 && c.group_size != 64 && c.group_size != 128) return "bad group_size";
+  for (int b : {c.bits, c.down_bits, c.embed_bits, c.head_bits})
+    if (b != 4 && b != 5 && b != 6 && b != 8) return "bits must be 4, 5, 6 or 8";
+  if (c.max_slots < 1 || c.max_slots > 4096) return "max_slots must be in 1..4096";
+  if (c.max_context < 1) return "max_context must be positive";
+  if (c.max_verify < 1 || c.max_verify > 8) return "max_verify must be in 1..8";
+  return nullptr;
+}
+
+mx_status engine_status(int rc, const std::string& err, const char* what) {
+  if (rc == MX_OK) return MX_OK;
+  if (!err.empty()) {
+    set_error(rc, std::string(what) + ": " + err);
+    return mx_status(rc);
+  }
+  return finish(rc, what);
+}
+
+bool tokens_ok(const mx::Engine& e, const uint32_t* t, int n) {
+  for (int i = 0; i < n; ++i)
+    if (t[i] >= uint32_t(engine_config(e).vocab)) return false;
+  return true;
+}
+bool slot_ok(const mx::Engine& e, int s) { return s >= 0 && s < engine_config(e).max_slots; }
+}  // namespace
+
+MX_ABI mx_status mx_engine_create(const mx_model_config* cfg, mx_engine** out) {
+  MX_CHECK(cfg && out, MX_EINVAL, "mx_engine_create: null pointer");
+  if (const char* err = check_config(*cfg))
+    return mx_status(set_error(MX_EINVAL, std::string("mx_engine_create: ") + err));
+  mx::Engine* e = nullptr;
+  const int rc = engine_create(*cfg, &e);
+  if (rc != MX_OK) return finish(rc, "mx_engine_create");
+  *out = new mx_engine{e};
+  return MX_OK;
+}
+
+MX_ABI mx_status mx_engine_destroy(mx_engine* e) {
+  if (e) {
+    engine_destroy(e->impl);
+    delete e;
+  }
+  return MX_OK;
+}
+
+MX_ABI mx_status mx_engine_reset_slot(mx_engine* e, int32_t slot) {
+  MX_CHECK(e && slot_ok(*e->impl, slot), MX_EINVAL, "mx_engine_reset_slot: bad engine or slot");
+  return finish(engine_reset_slot(*e->impl, slot), "mx_engine_reset_slot");
+}
+
+MX_ABI mx_status mx_engine_clone_slot(mx_engine* e, int32_t src, int32_t dst) {
+  MX_CHECK(e && slot_ok(*e->impl, src) && slot_ok(*e->impl, dst) && src != dst, MX_EINVAL,
+           "mx_engine_clone_slot: bad engine or slots");
+  return finish(engine_clone_slot(*e->impl, src, dst), "mx_engine_clone_slot");
+}
+
+MX_ABI int32_t mx_engine_offset(mx_engine* e, int32_t slot) {
+  if (!e || !slot_ok(*e->impl, slot)) return -1;
+  return engine_offset(*e->impl, slot);
+}
+
+static mx_status decode_common(mx_engine* e, const int32_t* slots, const uint32_t* tokens,
+                               int32_t rows, uint32_t* next, bool equal, const char* what) {
+  MX_CHECK(e && slots && tokens && next, MX_EINVAL, std::string(what) + ": null pointer");
+  MX_CHECK(rows >= 1 && rows <= 8, MX_EUNSUPPORTED, std::string(what) + ": rows must be in 1..8");
+  for (int r = 0; r < rows; ++r)
+    MX_CHECK(slot_ok(*e->impl, slots[r]), MX_EINVAL, std::string(what) + ": slot out of range");
+  MX_CHECK(tokens_ok(*e->impl, tokens, rows), MX_EINVAL,
+           std::string(what) + ": token outside vocabulary");
+  if (equal)
+    for (int r = 1; r < rows; ++r)
+      MX_CHECK(engine_offset(*e->impl, slots[r]) == engine_offset(*e->impl, slots[0]), MX_ESTATE,
+               std::string(what) + ": rows must share one cache offset");
+  std::string err;
+  const int rc = engine_decode_rows(*e->impl, slots, tokens, rows, next, &err);
+  return engine_status(rc, err, what);
+}
+
+MX_ABI mx_status mx_engine_decode_batch(mx_engine* e, const int32_t* slots, const uint32_t* tokens,
+                                        int32_t rows, uint32_t* next) {
+  return decode_common(e, slots, tokens, rows, next, true, "mx_engine_decode_batch");
+}
+
+MX_ABI mx_status mx_engine_decode_rows(mx_engine* e, const int32_t* slots, const uint32_t* tokens,
+                                       int32_t rows, uint32_t* next) {
+  return decode_common(e, slots, tokens, rows, next, false, "mx_engine_decode_rows");
+}
+
+MX_ABI mx_status mx_engine_prefill(mx_engine* e, int32_t slot, const uint32_t* tokens,
+                                   int32_t count, uint32_t* next) {
+  MX_CHECK(e && tokens && next, MX_EINVAL, "mx_engine_prefill: null pointer");
+  MX_CHECK(slot_ok(*e->impl, slot), MX_EINVAL, "mx_engine_prefill: slot out of range");
+  MX_CHECK(count >= 1, MX_EINVAL, "mx_engine_prefill: empty input");
+  MX_CHECK(tokens_ok(*e->impl, tokens, count), MX_EINVAL,
+           "mx_engine_prefill: token outside vocabulary");
+  uint32_t out[8];
+  for (int i = 0; i < count; i += 8) {
+    const int n = count - i < 8 ? count - i : 8;
+    std::string err;
+    const int rc = engine_block(*e->impl, slot, tokens + i, n, false, out, &err);
+    if (rc != MX_OK) return engine_status(rc, err, "mx_engine_prefill");
+    *next = out[n - 1];
+  }
+  return MX_OK;
+}
+
+MX_ABI mx_status mx_engine_verify(mx_engine* e, int32_t slot, const uint32_t* tokens,
+                                  int32_t count, uint32_t* argmax) {
+  MX_CHECK(e && tokens && argmax, MX_EINVAL, "mx_engine_verify: null pointer");
+  MX_CHECK(slot_ok(*e->impl, slot), MX_EINVAL, "mx_engine_verify: slot out of range");
+  MX_CHECK(count >= 1 && count <= engine_config(*e->impl).max_verify, MX_EUNSUPPORTED,
+           "mx_engine_verify: count must be in 1..max_verify");
+  MX_CHECK(tokens_ok(*e->impl, tokens, count), MX_EINVAL,
+           "mx_engine_verify: token outside vocabulary");
+  std::string err;
+  return engine_status(engine_verify(*e->impl, slot, tokens, count, argmax, &err), err,
+                       "mx_engine_verify");
+}
+
+MX_ABI mx_status mx_engine_commit(mx_engine* e, int32_t slot, int32_t keep) {
+  MX_CHECK(e && slot_ok(*e->impl, slot), MX_EINVAL, "mx_engine_commit: bad engine or slot");
+  std::string err;
+  return engine_status(engine_commit(*e->impl, slot, keep, &err), err, "mx_engine_commit");
+}
+
+MX_ABI mx_status mx_engine_set_flags(mx_engine* e, int32_t flags) {
+  MX_CHECK(e != nullptr, MX_EINVAL, "mx_engine_set_flags: null engine");
+  engine_set_flags(*e->impl, flags & 1, (flags & 2) ? 0 : 1);
+  return MX_OK;
+}
+
+MX_ABI mx_status mx_engine_read(mx_engine* e, const char* what, void* host, size_t bytes) {
+  MX_CHECK(e && what && host, MX_EINVAL, "mx_engine_read: null pointer");
+  std::string err;
+  return engine_status(engine_read(*e->impl, what, host, bytes, &err), err, "mx_engine_read");
+}
+
+MX_ABI mx_status mx_engine_tensor(mx_engine* e, const char* name, void** device_ptr,
+                                  size_t* bytes) {
+  MX_CHECK(e && name && device_ptr && bytes, MX_EINVAL, "mx_engine_tensor: null pointer");
+  MX_CHECK(engine_tensor(*e->impl, name, device_ptr, bytes) == MX_OK, MX_EINVAL,
+           std::string("mx_engine_tensor: unknown tensor ") + name);
+  return MX_OK;
+}

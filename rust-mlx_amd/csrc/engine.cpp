@@ -1,0 +1,726 @@
+// The decode engine: a synthetic hybrid GatedDeltaNet / gated-attention MoE
+// model resident in HBM, per-slot recurrent and KV caches, and the batched
+// step that runs every layer's kernels on one HIP stream.
+//
+// Reference: HybridModel / HybridLayer / HybridCache (src/hybrid.rs:500-759),
+// HybridModel::decode_batch (src/batching.rs:34-170) and the generation entry
+// points of src/speculative.rs (prepare 38-68, generate_prepared 225-483).
+//
+// MI355X-first differences from the reference's design:
+//  * caches live in a slot arena (state/conv/KV indexed by slot id) instead of
+//    being concatenated and split around every batched step
+//    (batching.rs:54-90, 138-169): a step names its rows' slots;
+//  * every row carries its own position, so rows at different offsets can
+//    share one step (the reference's equal-offset rule is kept as the
+//    decode_batch contract and checked on the host);
+//  * the whole step is captured once per row shape into a HIP graph and
+//    replayed; only the small per-step row table is copied in before launch.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace mx {
+
+namespace {
+
+struct Buf {
+  void* p = nullptr;
+  size_t bytes = 0;
+};
+
+struct QW {
+  QWeight w{};
+};
+
+struct HcW {
+  uint16_t* scale = nullptr;  // [hc * H]
+  QWeight down{};             // [rank (+ hc inject rows), hc * H]
+  QWeight up{};               // [hc * H, rank]
+  bool inject = false;
+};
+
+struct LayerW {
+  bool attn = false;
+  int cache_index = 0;  // index among GDN layers or among attention layers
+  HcW attn_hc, mlp_hc;
+  // GatedDeltaNet
+  QWeight gdn_in{};  // [cd + vd + 2 hv, H]: qkv | z | a | b
+  float* conv_w = nullptr;
+  float* a_log = nullptr;
+  uint16_t* dt_bias = nullptr;
+  uint16_t* gdn_norm = nullptr;
+  QWeight gdn_out{};
+  // attention
+  QWeight attn_in{};  // [heads*2*hd + 2*kvh*hd, H]: (q, gate) per head | k | v
+  uint16_t* q_norm = nullptr;
+  uint16_t* k_norm = nullptr;
+  QWeight attn_out{};
+  // MoE
+  QWeight router{};  // [E + 1, H]: router rows then the shared-expert gate
+  QBank gate{}, up{}, down{};
+  QWeight sgate{}, sup{}, sdown{};
+};
+
+}  // namespace
+
+struct Engine {
+  mx_model_config cfg{};
+  hipStream_t stream = nullptr;
+  std::vector<Buf> allocs;
+  std::map<std::string, Buf> tensors;
+  std::vector<LayerW> layers;
+  QWeight embed{}, head{};
+  HcW mixer;
+  int n_gdn = 0, n_attn = 0;
+  // dims
+  int H = 0, cd = 0, vd = 0, P = 0, Q = 0, max_chunks = 0;
+  GdnDims gd{};
+  AttnDims ad{};
+  // caches
+  float* gdn_state = nullptr;     // [slots][n_gdn][hv][dk][dv]
+  uint16_t* conv_state = nullptr; // [slots][n_gdn][K-1][cd]
+  uint16_t* k_cache = nullptr;    // [slots][n_attn][kvh][max_ctx][hd]
+  uint16_t* v_cache = nullptr;
+  float* rope_cos = nullptr;      // [max_ctx][rot/2]
+  float* rope_sin = nullptr;
+  // verify history and snapshot of one slot
+  float* hist_state = nullptr;    // [n_gdn][max_verify][hv][dk][dv]
+  uint16_t* hist_conv = nullptr;  // [n_gdn][K-1+max_verify][cd]
+  float* snap_state = nullptr;    // [n_gdn][hv][dk][dv]
+  uint16_t* snap_conv = nullptr;  // [n_gdn][K-1][cd]
+  int verify_slot = -1, verify_count = 0, verify_base = 0;
+  // activations (rows <= 8)
+  uint16_t *h = nullptr, *xn = nullptr, *lo = nullptr, *inj = nullptr, *mixed = nullptr;
+  uint16_t *pbuf = nullptr, *conv_out = nullptr, *y = nullptr, *qrot = nullptr, *attn_y = nullptr;
+  uint16_t *logits_r = nullptr, *scores = nullptr, *factor = nullptr, *moe_p = nullptr;
+  uint16_t *moe_h = nullptr, *logits = nullptr;
+  uint32_t* ids = nullptr;
+  float *o_part = nullptr, *ml_part = nullptr;
+  void* head_ws = nullptr;
+  // per-step row table (device) and its pinned host mirror
+  struct RowTable {
+    uint32_t tokens[8];
+    int32_t slots[8];
+    int32_t pos[8];
+    int32_t gdn_slots[8];
+    uint32_t next[8];
+  };
+  RowTable* dev_rows = nullptr;
+  RowTable* host_rows = nullptr;
+  std::vector<int32_t> offsets;
+  bool want_logits = false;
+  int last_rows = 0;
+  // captured graphs keyed by (rows, groups, t, history, logits)
+  std::map<int, hipGraphExec_t> graphs;
+  bool use_graphs = true;
+
+  ~Engine();
+};
+
+Engine::~Engine() {
+  for (auto& g : graphs) hipGraphExecDestroy(g.second);
+  for (auto& a : allocs) hipFree(a.p);
+  if (host_rows) hipHostFree(host_rows);
+  if (stream) hipStreamDestroy(stream);
+}
+
+namespace {
+
+uint64_t tensor_seed(uint64_t base, int layer, int id) {
+  // distinct streams per (layer, tensor); QWeight-style tensors use seed, +1, +2
+  return base + uint64_t(layer + 1) * 1000ull + uint64_t(id) * 10ull;
+}
+
+int alloc(Engine& e, const std::string& name, size_t bytes, void** out) {
+  void* p = nullptr;
+  const hipError_t err = hipMalloc(&p, bytes ? bytes : 1);
+  if (err != hipSuccess) return hip_error(err, ("hipMalloc " + name).c_str());
+  e.allocs.push_back({p, bytes});
+  if (!name.empty()) e.tensors[name] = {p, bytes};
+  *out = p;
+  return MX_OK;
+}
+
+#define MX_TRY(x)                \
+  do {                           \
+    const int rc_ = (x);         \
+    if (rc_ != MX_OK) return rc_; \
+  } while (0)
+
+int make_qw(Engine& e, const std::string& name, int n, int k, int bits, int layer, int id,
+            QWeight* out, float s_lo = 0.005f, float s_hi = 0.03f) {
+  const int gs = e.cfg.group_size;
+  void *c, *s, *b;
+  MX_TRY(alloc(e, name + ".codes", size_t(n) * k * bits / 8, &c));
+  MX_TRY(alloc(e, name + ".scales", size_t(n) * (k / gs) * 2, &s));
+  MX_TRY(alloc(e, name + ".biases", size_t(n) * (k / gs) * 2, &b));
+  const uint64_t seed = tensor_seed(e.cfg.seed, layer, id);
+  MX_TRY(fill_codes(static_cast<uint32_t*>(c), n, k, bits, seed, e.stream));
+  MX_TRY(fill_bf16(static_cast<uint16_t*>(s), size_t(n) * (k / gs), seed + 1, 0, s_lo, s_hi, e.stream));
+  MX_TRY(fill_bf16(static_cast<uint16_t*>(b), size_t(n) * (k / gs), seed + 2, 0, -0.2f, 0.2f, e.stream));
+  *out = QWeight{static_cast<uint32_t*>(c), static_cast<uint16_t*>(s), static_cast<uint16_t*>(b),
+                 n, k, bits, gs};
+  return MX_OK;
+}
+
+int make_bank(Engine& e, const std::string& name, int experts, int n, int k, int bits, int layer,
+              int id, QBank* out) {
+  QWeight w;
+  MX_TRY(make_qw(e, name, experts * n, k, bits, layer, id, &w));
+  *out = QBank{w.codes, w.scales, w.biases, experts, n, k, bits, w.group_size};
+  return MX_OK;
+}
+
+int make_bf16(Engine& e, const std::string& name, size_t count, int layer, int id, int dist,
+              float a, float b, uint16_t** out) {
+  void* p;
+  MX_TRY(alloc(e, name, count * 2, &p));
+  MX_TRY(fill_bf16(static_cast<uint16_t*>(p), count, tensor_seed(e.cfg.seed, layer, id), dist, a, b,
+                   e.stream));
+  *out = static_cast<uint16_t*>(p);
+  return MX_OK;
+}
+
+// fp32 tensor from a bf16 draw (exact widening), on the host then uploaded.
+int make_f32_from_draw(Engine& e, const std::string& name, size_t count, int layer, int id,
+                       int dist, float a, float b, bool log_of, float** out) {
+  std::vector<uint16_t> tmp(count);
+  // draw on the device, read back, widen (and optionally take log) on the host
+  uint16_t* d16;
+  MX_TRY(make_bf16(e, "", count, layer, id, dist, a, b, &d16));
+  if (hipMemcpyAsync(tmp.data(), d16, count * 2, hipMemcpyDeviceToHost, e.stream) != hipSuccess ||
+      hipStreamSynchronize(e.stream) != hipSuccess)
+    return MX_EHIP;
+  std::vector<float> f(count);
+  for (size_t i = 0; i < count; ++i) {
+    const float v = bf16_to_f32(tmp[i]);
+    f[i] = log_of ? std::log(v) : v;
+  }
+  void* p;
+  MX_TRY(alloc(e, name, count * 4, &p));
+  if (hipMemcpy(p, f.data(), count * 4, hipMemcpyHostToDevice) != hipSuccess) return MX_EHIP;
+  *out = static_cast<float*>(p);
+  return MX_OK;
+}
+
+int layer_bits(const mx_model_config& c, int layer, int which) {
+  // which: 0 = main projections, 1 = expert down; tensors outside the layer
+  // stack (layer < 0) always use the base widths
+  if (!c.mixed_bits || layer < 0) return which == 0 ? c.bits : c.down_bits;
+  static const int choices[4] = {4, 5, 6, 8};
+  const uint64_t r = rng_u64(c.seed ^ 0x5bd1e995ull, uint64_t(layer) * 2 + which);
+  return choices[r & 3];
+}
+
+int make_hc(Engine& e, const std::string& p, int layer, int id0, bool inject, HcW* out) {
+  const auto& c = e.cfg;
+  const int bits = layer_bits(c, layer, 0);
+  out->inject = inject;
+  MX_TRY(make_bf16(e, p + ".scale", size_t(c.hc) * c.hidden, layer, id0, 1, 0.1f, 0.0f, &out->scale));
+  MX_TRY(make_qw(e, p + ".down", c.hc_rank + (inject ? c.hc : 0), c.hc * c.hidden, bits, layer,
+                 id0 + 1, &out->down));
+  MX_TRY(make_qw(e, p + ".up", c.hc * c.hidden, c.hc_rank, bits, layer, id0 + 2, &out->up));
+  return MX_OK;
+}
+
+int build(Engine& e) {
+  const auto& c = e.cfg;
+  e.H = c.hidden;
+  e.gd = GdnDims{c.gdn_hk, c.gdn_hv, c.gdn_dk, c.gdn_dv, c.conv_k};
+  e.cd = 2 * c.gdn_hk * c.gdn_dk + c.gdn_hv * c.gdn_dv;
+  e.vd = c.gdn_hv * c.gdn_dv;
+  e.P = e.cd + e.vd + 2 * c.gdn_hv;
+  e.Q = c.heads * 2 * c.head_dim + 2 * c.kv_heads * c.head_dim;
+  e.max_chunks = (c.max_context + kAttnChunk - 1) / kAttnChunk;
+  for (int i = 0; i < c.layers; ++i) {
+    LayerW L;
+    L.attn = (i % c.attn_every) == c.attn_every - 1;
+    L.cache_index = L.attn ? e.n_attn++ : e.n_gdn++;
+    e.layers.push_back(L);
+  }
+  const int64_t attn_slot_stride = int64_t(e.n_attn) * c.kv_heads * c.max_context * c.head_dim;
+  e.ad = AttnDims{c.heads, c.kv_heads, c.head_dim, c.rotary_dim, c.max_context, attn_slot_stride};
+
+  // ---- weights ----
+  MX_TRY(make_qw(e, "embed", c.vocab, c.hidden, c.embed_bits, -1, 1, &e.embed));
+  MX_TRY(make_qw(e, "head", c.vocab, c.hidden, c.head_bits, -1, 2, &e.head));
+  MX_TRY(make_hc(e, "mixer", -1, 3, false, &e.mixer));
+  for (int i = 0; i < c.layers; ++i) {
+    LayerW& L = e.layers[i];
+    const std::string p = "layers." + std::to_string(i);
+    const int bits = layer_bits(c, i, 0);
+    const int dbits = layer_bits(c, i, 1);
+    MX_TRY(make_hc(e, p + ".attn_hc", i, 1, true, &L.attn_hc));
+    MX_TRY(make_hc(e, p + ".mlp_hc", i, 4, true, &L.mlp_hc));
+    if (!L.attn) {
+      MX_TRY(make_qw(e, p + ".gdn.in", e.P, c.hidden, bits, i, 7, &L.gdn_in));
+      // conv weight ~ N(0, 0.5), A = exp(A_log) ~ U(0, 16), dt ~ U(-1, 1), norm ~ 1 + N(0, .1)
+      MX_TRY(make_f32_from_draw(e, p + ".gdn.conv_w", size_t(c.conv_k) * e.cd, i, 8, 1, 0.5f, 0.0f,
+                                false, &L.conv_w));
+      MX_TRY(make_f32_from_draw(e, p + ".gdn.a_log", c.gdn_hv, i, 9, 0, 0.01f, 16.0f, true, &L.a_log));
+      MX_TRY(make_bf16(e, p + ".gdn.dt_bias", c.gdn_hv, i, 10, 0, -1.0f, 1.0f, &L.dt_bias));
+      MX_TRY(make_bf16(e, p + ".gdn.norm", c.gdn_dv, i, 11, 1, 0.1f, 1.0f, &L.gdn_norm));
+      MX_TRY(make_qw(e, p + ".gdn.out", c.hidden, e.vd, bits, i, 12, &L.gdn_out));
+    } else {
+      MX_TRY(make_qw(e, p + ".attn.in", e.Q, c.hidden, bits, i, 7, &L.attn_in));
+      MX_TRY(make_bf16(e, p + ".attn.q_norm", c.head_dim, i, 8, 1, 0.1f, 0.0f, &L.q_norm));
+      MX_TRY(make_bf16(e, p + ".attn.k_norm", c.head_dim, i, 9, 1, 0.1f, 0.0f, &L.k_norm));
+      MX_TRY(make_qw(e, p + ".attn.out", c.hidden, c.heads * c.head_dim, bits, i, 12, &L.attn_out));
+    }
+    MX_TRY(make_qw(e, p + ".moe.router", c.experts + 1, c.hidden, bits, i, 13, &L.router));
+    MX_TRY(make_bank(e, p + ".moe.gate", c.experts, c.moe_inter, c.hidden, bits, i, 14, &L.gate));
+    MX_TRY(make_bank(e, p + ".moe.up", c.experts, c.moe_inter, c.hidden, bits, i, 15, &L.up));
+    MX_TRY(make_bank(e, p + ".moe.down", c.experts, c.hidden, c.moe_inter, dbits, i, 16, &L.down));
+    MX_TRY(make_qw(e, p + ".moe.shared_gate", c.shared_inter, c.hidden, bits, i, 17, &L.sgate));
+    MX_TRY(make_qw(e, p + ".moe.shared_up", c.shared_inter, c.hidden, bits, i, 18, &L.sup));
+    MX_TRY(make_qw(e, p + ".moe.shared_down", c.hidden, c.shared_inter, dbits, i, 19, &L.sdown));
+  }
+
+  // ---- caches ----
+  void* v;
+  const size_t S = size_t(c.max_slots);
+  const size_t state_per = size_t(c.gdn_hv) * c.gdn_dk * c.gdn_dv;
+  MX_TRY(alloc(e, "cache.gdn_state", S * e.n_gdn * state_per * 4, &v));
+  e.gdn_state = static_cast<float*>(v);
+  MX_TRY(alloc(e, "cache.conv_state", S * e.n_gdn * (c.conv_k - 1) * e.cd * 2, &v));
+  e.conv_state = static_cast<uint16_t*>(v);
+  MX_TRY(alloc(e, "cache.k", S * attn_slot_stride * 2, &v));
+  e.k_cache = static_cast<uint16_t*>(v);
+  MX_TRY(alloc(e, "cache.v", S * attn_slot_stride * 2, &v));
+  e.v_cache = static_cast<uint16_t*>(v);
+  MX_TRY(alloc(e, "verify.state", size_t(e.n_gdn) * c.max_verify * state_per * 4, &v));
+  e.hist_state = static_cast<float*>(v);
+  MX_TRY(alloc(e, "verify.conv", size_t(e.n_gdn) * (c.conv_k - 1 + c.max_verify) * e.cd * 2, &v));
+  e.hist_conv = static_cast<uint16_t*>(v);
+  MX_TRY(alloc(e, "verify.snap_state", size_t(e.n_gdn) * state_per * 4, &v));
+  e.snap_state = static_cast<float*>(v);
+  MX_TRY(alloc(e, "verify.snap_conv", size_t(e.n_gdn) * (c.conv_k - 1) * e.cd * 2, &v));
+  e.snap_conv = static_cast<uint16_t*>(v);
+
+  // RoPE table: inv_freq[i] = 1 / theta^(2i/rot) in fp32 (src/rope.rs:20-24),
+  // angle = pos * inv_freq in double, cos/sin rounded to fp32.
+  {
+    const int half = c.rotary_dim / 2;
+    std::vector<float> cs(size_t(c.max_context) * half), sn(cs.size());
+    for (int i = 0; i < half; ++i) {
+      const float power = float(2 * i) / float(c.rotary_dim);
+      const float inv = 1.0f / ::powf(c.rope_theta, power);  // fp32 pow, as MLX's f32 power
+      for (int p = 0; p < c.max_context; ++p) {
+        const double a = double(p) * double(inv);
+        cs[size_t(p) * half + i] = float(std::cos(a));
+        sn[size_t(p) * half + i] = float(std::sin(a));
+      }
+    }
+    MX_TRY(alloc(e, "rope.cos", cs.size() * 4, &v));
+    e.rope_cos = static_cast<float*>(v);
+    MX_TRY(alloc(e, "rope.sin", sn.size() * 4, &v));
+    e.rope_sin = static_cast<float*>(v);
+    if (hipMemcpy(e.rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(e.rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+      return MX_EHIP;
+  }
+
+  // ---- activations for up to 8 rows ----
+  const size_t R = 8;
+  auto a16 = [&](const char* n, size_t count, uint16_t** out) -> int {
+    void* q;
+    MX_TRY(alloc(e, n, count * 2, &q));
+    *out = static_cast<uint16_t*>(q);
+    return MX_OK;
+  };
+  const int inter_max = c.moe_inter > c.shared_inter ? c.moe_inter : c.shared_inter;
+  MX_TRY(a16("act.h", R * c.hc * c.hidden, &e.h));
+  MX_TRY(a16("act.xn", R * c.hc * c.hidden, &e.xn));
+  MX_TRY(a16("act.lo", R * c.hc_rank, &e.lo));
+  MX_TRY(a16("act.inj", R * c.hc, &e.inj));
+  MX_TRY(a16("act.mixed", R * c.hidden, &e.mixed));
+  MX_TRY(a16("act.proj", R * (e.P > e.Q ? e.P : e.Q), &e.pbuf));
+  MX_TRY(a16("act.conv_out", R * e.cd, &e.conv_out));
+  MX_TRY(a16("act.y", R * (e.vd > c.heads * c.head_dim ? e.vd : c.heads * c.head_dim), &e.y));
+  MX_TRY(a16("act.qrot", R * c.heads * c.head_dim, &e.qrot));
+  MX_TRY(a16("act.router", R * (c.experts + 1), &e.logits_r));
+  MX_TRY(a16("act.scores", R * c.top_k, &e.scores));
+  MX_TRY(a16("act.factor", R, &e.factor));
+  MX_TRY(a16("act.moe_p", R * (c.top_k + 1) * c.hidden, &e.moe_p));
+  MX_TRY(a16("act.moe_h", R * (c.top_k + 1) * inter_max, &e.moe_h));
+  MX_TRY(a16("act.logits", R * size_t(c.vocab), &e.logits));
+  MX_TRY(alloc(e, "act.ids", R * c.top_k * 4, &v));
+  e.ids = static_cast<uint32_t*>(v);
+  MX_TRY(alloc(e, "act.o_part", R * c.heads * e.max_chunks * c.head_dim * 4, &v));
+  e.o_part = static_cast<float*>(v);
+  MX_TRY(alloc(e, "act.ml_part", R * c.heads * e.max_chunks * 2 * 4, &v));
+  e.ml_part = static_cast<float*>(v);
+  size_t hws = size_t(head_parts(c.vocab, c.hidden)) * 8 * 8;
+  MX_TRY(alloc(e, "act.head_ws", hws, &e.head_ws));
+  MX_TRY(alloc(e, "rows", sizeof(Engine::RowTable), &v));
+  e.dev_rows = static_cast<Engine::RowTable*>(v);
+  if (hipHostMalloc(reinterpret_cast<void**>(&e.host_rows), sizeof(Engine::RowTable)) != hipSuccess)
+    return MX_ENOMEM;
+  std::memset(e.host_rows, 0, sizeof(Engine::RowTable));
+  e.offsets.assign(c.max_slots, 0);
+  if (hipStreamSynchronize(e.stream) != hipSuccess) return MX_EHIP;
+  return MX_OK;
+}
+
+int hc_forward(Engine& e, const HcW& w, int rows, uint16_t* mixed_out, uint16_t* inj_out) {
+  const auto& c = e.cfg;
+  MX_TRY(hc_norm(e.h, w.scale, rows, c.hc, c.hidden, c.rms_eps, e.xn, e.stream));
+  ProjEpilogue d{};
+  d.mode = kHcDown;
+  d.y = e.lo;
+  d.y_stride = c.hc_rank;
+  d.aux = inj_out;
+  d.aux_stride = c.hc;
+  d.rank = c.hc_rank;
+  d.hc = c.hc;
+  MX_TRY(proj(w.down, e.xn, int64_t(c.hc) * c.hidden, rows, d, e.stream));
+  ProjEpilogue u{};
+  u.mode = kHcUpMix;
+  u.y = mixed_out;
+  u.y_stride = c.hidden;
+  u.xn = e.xn;
+  u.xn_stride = int64_t(c.hc) * c.hidden;
+  u.hc = c.hc;
+  u.hidden = c.hidden;
+  MX_TRY(proj(w.up, e.lo, c.hc_rank, rows, u, e.stream));
+  return MX_OK;
+}
+
+// Records the kernels of one step for `rows` rows arranged as `groups`
+// sequences of `t` tokens.  Row metadata is read from e.dev_rows.
+int record_step(Engine& e, int rows, int groups, int t, bool history, bool logits) {
+  const auto& c = e.cfg;
+  Engine::RowTable* rt = e.dev_rows;
+  MX_TRY(embed(e.embed, rt->tokens, rows, c.hc, e.h, e.stream));
+  for (size_t li = 0; li < e.layers.size(); ++li) {
+    const LayerW& L = e.layers[li];
+    MX_TRY(hc_forward(e, L.attn_hc, rows, e.mixed, e.inj));
+    ProjEpilogue wr{};
+    wr.mode = kHcWrite;
+    wr.y = e.h;
+    wr.y_stride = int64_t(c.hc) * c.hidden;
+    wr.aux = e.inj;
+    wr.aux_stride = c.hc;
+    wr.hc = c.hc;
+    if (!L.attn) {
+      const int gi = L.cache_index;
+      ProjEpilogue pl{};
+      pl.mode = kPlain;
+      pl.y = e.pbuf;
+      pl.y_stride = e.P;
+      MX_TRY(proj(L.gdn_in, e.mixed, c.hidden, rows, pl, e.stream));
+      const size_t conv_per = size_t(c.conv_k - 1) * e.cd;
+      const size_t state_per = size_t(c.gdn_hv) * c.gdn_dk * c.gdn_dv;
+      // cache layout [slot][gdn layer]: slot index s -> s * n_gdn + gi
+      MX_TRY(gdn_conv(e.pbuf, e.P, groups, t, rt->gdn_slots, e.conv_state + gi * conv_per,
+                      L.conv_w, e.cd, c.conv_k, e.conv_out, e.cd,
+                      history ? e.hist_conv + size_t(gi) * (c.conv_k - 1 + c.max_verify) * e.cd
+                              : nullptr,
+                      e.stream));
+      MX_TRY(gdn_recurrence(e.conv_out, e.cd, e.pbuf + e.cd, e.pbuf + e.cd + e.vd,
+                            e.pbuf + e.cd + e.vd + c.gdn_hv, e.P, L.a_log, L.dt_bias, L.gdn_norm,
+                            c.rms_eps, e.gd, groups, t, rt->gdn_slots,
+                            e.gdn_state + gi * state_per,
+                            history ? e.hist_state + size_t(gi) * c.max_verify * state_per : nullptr,
+                            e.y, e.stream));
+      MX_TRY(proj(L.gdn_out, e.y, e.vd, rows, wr, e.stream));
+    } else {
+      const int ai = L.cache_index;
+      ProjEpilogue pl{};
+      pl.mode = kPlain;
+      pl.y = e.pbuf;
+      pl.y_stride = e.Q;
+      MX_TRY(proj(L.attn_in, e.mixed, c.hidden, rows, pl, e.stream));
+      const size_t layer_off = size_t(ai) * c.kv_heads * c.max_context * c.head_dim;
+      MX_TRY(attn_prep(e.pbuf, e.Q, rows, rt->slots, rt->pos, L.q_norm, L.k_norm, c.rms_eps,
+                       e.rope_cos, e.rope_sin, e.ad, e.qrot, e.k_cache + layer_off,
+                       e.v_cache + layer_off, e.stream));
+      MX_TRY(attn_decode(e.qrot, rows, rt->slots, rt->pos, e.k_cache + layer_off,
+                         e.v_cache + layer_off, e.ad, e.max_chunks, e.o_part, e.ml_part, e.stream));
+      MX_TRY(attn_combine(e.o_part, e.ml_part, e.pbuf, e.Q, rows, rt->pos, e.ad, e.max_chunks,
+                          e.y, e.stream));
+      MX_TRY(proj(L.attn_out, e.y, int64_t(c.heads) * c.head_dim, rows, wr, e.stream));
+    }
+    // MoE sublayer
+    MX_TRY(hc_forward(e, L.mlp_hc, rows, e.mixed, e.inj));
+    ProjEpilogue rl{};
+    rl.mode = kPlain;
+    rl.y = e.logits_r;
+    rl.y_stride = c.experts + 1;
+    MX_TRY(proj(L.router, e.mixed, c.hidden, rows, rl, e.stream));
+    MX_TRY(moe_route(e.logits_r, c.experts + 1, e.logits_r + c.experts, c.experts + 1, rows,
+                     c.experts, c.top_k, e.ids, e.scores, e.factor, e.stream));
+    MX_TRY(moe_experts(e.mixed, e.ids, e.scores, rows, c.top_k, L.gate, L.up, L.down, L.sgate,
+                       L.sup, L.sdown, e.moe_h, e.moe_p, e.stream));
+    MX_TRY(moe_reduce_hc_epilogue(e.moe_p, e.factor, e.h, e.inj, rows, c.top_k, c.hc, c.hidden,
+                                  e.h, e.stream));
+  }
+  // mixer + greedy head
+  MX_TRY(hc_forward(e, e.mixer, rows, e.mixed, nullptr));
+  int parts = 0;
+  float* maxima = static_cast<float*>(e.head_ws);
+  uint32_t* indices = reinterpret_cast<uint32_t*>(maxima + size_t(head_parts(c.vocab, c.hidden)) * 8);
+  MX_TRY(head_partials(e.head, e.mixed, rows, maxima, indices, &parts, e.stream));
+  MX_TRY(argmax_reduce(maxima, indices, rows, parts, rt->next, e.stream));
+  if (logits) {
+    ProjEpilogue pl{};
+    pl.mode = kPlain;
+    pl.y = e.logits;
+    pl.y_stride = c.vocab;
+    MX_TRY(proj(e.head, e.mixed, c.hidden, rows, pl, e.stream));
+  }
+  return MX_OK;
+}
+
+int graph_key(int rows, int groups, int t, bool history, bool logits) {
+  return ((rows * 16 + groups) * 16 + t) * 4 + (history ? 2 : 0) + (logits ? 1 : 0);
+}
+
+// Runs one step: copies the row table in, replays (or captures) the graph and
+// reads back the next tokens.  Synchronises once, like the reference's eval.
+int run_step(Engine& e, int rows, int groups, int t, bool history, uint32_t* next) {
+  if (hipMemcpyAsync(e.dev_rows, e.host_rows, sizeof(Engine::RowTable), hipMemcpyHostToDevice,
+                     e.stream) != hipSuccess)
+    return MX_EHIP;
+  const int key = graph_key(rows, groups, t, history, e.want_logits);
+  if (e.use_graphs) {
+    auto it = e.graphs.find(key);
+    if (it == e.graphs.end()) {
+      hipGraph_t g = nullptr;
+      MX_HIP(hipStreamBeginCapture(e.stream, hipStreamCaptureModeThreadLocal));
+      const int rc = record_step(e, rows, groups, t, history, e.want_logits);
+      hipGraph_t captured = nullptr;
+      const hipError_t end = hipStreamEndCapture(e.stream, &captured);
+      if (rc != MX_OK) {
+        if (captured) hipGraphDestroy(captured);
+        return rc;
+      }
+      MX_HIP(end);
+      g = captured;
+      hipGraphExec_t exec = nullptr;
+      const hipError_t inst = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+      hipGraphDestroy(g);
+      MX_HIP(inst);
+      it = e.graphs.emplace(key, exec).first;
+    }
+    MX_HIP(hipGraphLaunch(it->second, e.stream));
+  } else {
+    MX_TRY(record_step(e, rows, groups, t, history, e.want_logits));
+  }
+  MX_HIP(hipMemcpyAsync(e.host_rows->next, e.dev_rows->next, sizeof(uint32_t) * rows,
+                        hipMemcpyDeviceToHost, e.stream));
+  MX_HIP(hipStreamSynchronize(e.stream));
+  if (next) std::memcpy(next, e.host_rows->next, sizeof(uint32_t) * rows);
+  e.last_rows = rows;
+  return MX_OK;
+}
+
+size_t state_per(const Engine& e) {
+  return size_t(e.cfg.gdn_hv) * e.cfg.gdn_dk * e.cfg.gdn_dv;
+}
+size_t conv_per(const Engine& e) { return size_t(e.cfg.conv_k - 1) * e.cd; }
+
+}  // namespace
+
+// ---- engine operations used by the C ABI --------------------------------
+int engine_create(const mx_model_config& cfg, Engine** out) {
+  auto e = std::make_unique<Engine>();
+  e->cfg = cfg;
+  MX_HIP(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking));
+  MX_TRY(build(*e));
+  // caches start empty (zero state, zero conv window)
+  for (int s = 0; s < cfg.max_slots; ++s) MX_TRY(engine_reset_slot(*e, s));
+  MX_HIP(hipStreamSynchronize(e->stream));
+  *out = e.release();
+  return MX_OK;
+}
+
+void engine_destroy(Engine* e) { delete e; }
+
+int engine_reset_slot(Engine& e, int slot) {
+  const size_t sp = state_per(e), cp = conv_per(e);
+  MX_HIP(hipMemsetAsync(e.gdn_state + size_t(slot) * e.n_gdn * sp, 0, e.n_gdn * sp * 4, e.stream));
+  MX_HIP(hipMemsetAsync(e.conv_state + size_t(slot) * e.n_gdn * cp, 0, e.n_gdn * cp * 2, e.stream));
+  MX_HIP(hipStreamSynchronize(e.stream));
+  e.offsets[slot] = 0;
+  if (e.verify_slot == slot) e.verify_slot = -1;
+  return MX_OK;
+}
+
+int engine_clone_slot(Engine& e, int src, int dst) {
+  const size_t sp = state_per(e), cp = conv_per(e);
+  const int64_t kv = e.ad.slot_stride;
+  MX_HIP(hipMemcpyAsync(e.gdn_state + size_t(dst) * e.n_gdn * sp,
+                        e.gdn_state + size_t(src) * e.n_gdn * sp, e.n_gdn * sp * 4,
+                        hipMemcpyDeviceToDevice, e.stream));
+  MX_HIP(hipMemcpyAsync(e.conv_state + size_t(dst) * e.n_gdn * cp,
+                        e.conv_state + size_t(src) * e.n_gdn * cp, e.n_gdn * cp * 2,
+                        hipMemcpyDeviceToDevice, e.stream));
+  // only the filled positions of each (layer, kv head) need copying
+  const int used = e.offsets[src];
+  if (used > 0) {
+    const size_t row_bytes = size_t(used) * e.cfg.head_dim * 2;
+    const size_t pitch = size_t(e.cfg.max_context) * e.cfg.head_dim * 2;
+    const size_t planes = size_t(e.n_attn) * e.cfg.kv_heads;
+    for (uint16_t* cache : {e.k_cache, e.v_cache})
+      MX_HIP(hipMemcpy2DAsync(cache + size_t(dst) * kv, pitch, cache + size_t(src) * kv, pitch,
+                              row_bytes, planes, hipMemcpyDeviceToDevice, e.stream));
+  }
+  MX_HIP(hipStreamSynchronize(e.stream));
+  e.offsets[dst] = e.offsets[src];
+  return MX_OK;
+}
+
+int engine_offset(const Engine& e, int slot) { return e.offsets[slot]; }
+
+int engine_decode_rows(Engine& e, const int32_t* slots, const uint32_t* tokens, int rows,
+                       uint32_t* next, std::string* err) {
+  for (int r = 0; r < rows; ++r) {
+    for (int q = 0; q < r; ++q)
+      if (slots[q] == slots[r]) {
+        *err = "a slot appears twice in one step";
+        return MX_EINVAL;
+      }
+    if (e.offsets[slots[r]] >= e.cfg.max_context) {
+      *err = "slot context is full";
+      return MX_ESTATE;
+    }
+    e.host_rows->tokens[r] = tokens[r];
+    e.host_rows->slots[r] = slots[r];
+    e.host_rows->gdn_slots[r] = slots[r] * e.n_gdn;
+    e.host_rows->pos[r] = e.offsets[slots[r]];
+  }
+  MX_TRY(run_step(e, rows, rows, 1, false, next));
+  for (int r = 0; r < rows; ++r) e.offsets[slots[r]] += 1;
+  // a decode step invalidates any pending verify block of these slots
+  for (int r = 0; r < rows; ++r)
+    if (slots[r] == e.verify_slot) e.verify_slot = -1;
+  return MX_OK;
+}
+
+// One chunk of up to 8 consecutive tokens of one slot (prefill or verify).
+int engine_block(Engine& e, int slot, const uint32_t* tokens, int count, bool history,
+                 uint32_t* next, std::string* err) {
+  if (e.offsets[slot] + count > e.cfg.max_context) {
+    *err = "slot context is full";
+    return MX_ESTATE;
+  }
+  for (int r = 0; r < count; ++r) {
+    e.host_rows->tokens[r] = tokens[r];
+    e.host_rows->slots[r] = slot;
+    e.host_rows->pos[r] = e.offsets[slot] + r;
+  }
+  e.host_rows->gdn_slots[0] = slot * e.n_gdn;
+  MX_TRY(run_step(e, count, 1, count, history, next));
+  e.offsets[slot] += count;
+  return MX_OK;
+}
+
+int engine_verify(Engine& e, int slot, const uint32_t* tokens, int count, uint32_t* next,
+                  std::string* err) {
+  // snapshot the recurrent state so that keep = 0 can restore it
+  const size_t sp = state_per(e), cp = conv_per(e);
+  MX_HIP(hipMemcpyAsync(e.snap_state, e.gdn_state + size_t(slot) * e.n_gdn * sp, e.n_gdn * sp * 4,
+                        hipMemcpyDeviceToDevice, e.stream));
+  MX_HIP(hipMemcpyAsync(e.snap_conv, e.conv_state + size_t(slot) * e.n_gdn * cp, e.n_gdn * cp * 2,
+                        hipMemcpyDeviceToDevice, e.stream));
+  const int base = e.offsets[slot];
+  MX_TRY(engine_block(e, slot, tokens, count, true, next, err));
+  e.verify_slot = slot;
+  e.verify_count = count;
+  e.verify_base = base;
+  return MX_OK;
+}
+
+// Accept the first `keep` tokens of the last verify block
+// (HybridCache::commit_verified, src/hybrid.rs:699-759): the GDN state after
+// token keep-1 comes from the history, the conv window is re-sliced, and the
+// attention offset is trimmed (later positions are overwritten by later steps).
+int engine_commit(Engine& e, int slot, int keep, std::string* err) {
+  if (slot != e.verify_slot) {
+    *err = "no verify block pending on this slot";
+    return MX_ESTATE;
+  }
+  if (keep < 0 || keep > e.verify_count) {
+    *err = "keep outside the verify block";
+    return MX_EINVAL;
+  }
+  const auto& c = e.cfg;
+  const size_t sp = state_per(e), cp = conv_per(e);
+  float* st = e.gdn_state + size_t(slot) * e.n_gdn * sp;
+  uint16_t* cv = e.conv_state + size_t(slot) * e.n_gdn * cp;
+  if (keep == 0) {
+    MX_HIP(hipMemcpyAsync(st, e.snap_state, e.n_gdn * sp * 4, hipMemcpyDeviceToDevice, e.stream));
+    MX_HIP(hipMemcpyAsync(cv, e.snap_conv, e.n_gdn * cp * 2, hipMemcpyDeviceToDevice, e.stream));
+  } else if (keep < e.verify_count) {
+    for (int g = 0; g < e.n_gdn; ++g) {
+      MX_HIP(hipMemcpyAsync(st + g * sp, e.hist_state + (size_t(g) * c.max_verify + keep - 1) * sp,
+                            sp * 4, hipMemcpyDeviceToDevice, e.stream));
+      // window rows keep .. keep + K - 2 are the conv state after `keep` tokens
+      MX_HIP(hipMemcpyAsync(cv + g * cp,
+                            e.hist_conv + size_t(g) * (c.conv_k - 1 + c.max_verify) * e.cd +
+                                size_t(keep) * e.cd,
+                            cp * 2, hipMemcpyDeviceToDevice, e.stream));
+    }
+  }
+  MX_HIP(hipStreamSynchronize(e.stream));
+  e.offsets[slot] = e.verify_base + keep;
+  e.verify_slot = -1;
+  return MX_OK;
+}
+
+int engine_read(Engine& e, const char* what, void* host, size_t bytes, std::string* err) {
+  const std::string w(what);
+  const void* src = nullptr;
+  size_t avail = 0;
+  if (w == "hidden") {
+    src = e.h;
+    avail = size_t(e.last_rows) * e.cfg.hc * e.cfg.hidden * 2;
+  } else if (w == "logits") {
+    src = e.logits;
+    avail = size_t(e.last_rows) * e.cfg.vocab * 2;
+  } else {
+    auto it = e.tensors.find(w);
+    if (it == e.tensors.end()) {
+      *err = "unknown tensor " + w;
+      return MX_EINVAL;
+    }
+    src = it->second.p;
+    avail = it->second.bytes;
+  }
+  if (bytes > avail) {
+    *err = "read larger than the tensor";
+    return MX_EINVAL;
+  }
+  MX_HIP(hipMemcpyAsync(host, src, bytes, hipMemcpyDeviceToHost, e.stream));
+  MX_HIP(hipStreamSynchronize(e.stream));
+  return MX_OK;
+}
+
+int engine_tensor(Engine& e, const char* name, void** ptr, size_t* bytes) {
+  auto it = e.tensors.find(name);
+  if (it == e.tensors.end()) return MX_EINVAL;
+  *ptr = it->second.p;
+  *bytes = it->second.bytes;
+  return MX_OK;
+}
+
+void engine_set_flags(Engine& e, int want_logits, int use_graphs) {
+  e.want_logits = want_logits != 0;
+  e.use_graphs = use_graphs != 0;
+}
+
+const mx_model_config& engine_config(const Engine& e) { return e.cfg; }
+int engine_gdn_layers(const Engine& e) { return e.n_gdn; }
+int engine_attn_layers(const Engine& e) { return e.n_attn; }
+hipStream_t engine_stream(const Engine& e) { return e.stream; }
+
+}  // namespace mx

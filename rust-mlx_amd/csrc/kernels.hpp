@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <string>
+
 #include "../../include/mx355.h"
 
 namespace mx {
@@ -38,6 +40,44 @@ const char* check_qweight(const QWeight& w);
 
 int qmv(const QWeight& w, const uint16_t* x, int m, uint16_t* y, hipStream_t s);
 int dequant_rows(const QWeight& w, const uint32_t* ids, int count, uint16_t* out, hipStream_t s);
+
+// ---- projections with fused epilogues (proj.hip) ----
+enum ProjMode { kPlain = 0, kHcDown = 1, kHcUpMix = 2, kHcWrite = 3 };
+struct ProjEpilogue {
+  int mode;
+  uint16_t* y;        // output (kPlain/kHcDown/kHcUpMix) or the residual [M, hc*n] (kHcWrite)
+  int64_t y_stride;   // elements between activation rows of y
+  uint16_t* aux;      // injection gates [M, hc]: written by kHcDown, read by kHcWrite
+  int64_t aux_stride;
+  const uint16_t* xn; // normed streams [M, hc*hidden] (kHcUpMix)
+  int64_t xn_stride;
+  int rank;           // kHcDown: rows below rank are the low-rank branch
+  int hc;             // hyper-connection streams
+  int hidden;         // kHcUpMix: stream width H (w.n == 4 * H)
+};
+int proj(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const ProjEpilogue& e,
+         hipStream_t s);
+int hc_norm(const uint16_t* x, const uint16_t* scale, int rows, int hc, int hidden, float eps,
+            uint16_t* y, hipStream_t s);
+int embed(const QWeight& w, const uint32_t* ids, int count, int hc, uint16_t* out, hipStream_t s);
+
+// ---- attention (attn.hip) ----
+struct AttnDims {
+  int heads, kv_heads, head_dim, rotary_dim;
+  int max_ctx;           // positions per (slot, layer, kv head) in the cache
+  int64_t slot_stride;   // elements between slots in the K (and V) cache
+};
+int attn_prep(const uint16_t* qkv, int64_t qkv_stride, int rows, const int32_t* slots,
+              const int32_t* pos, const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+              const float* rope_cos, const float* rope_sin, AttnDims d, uint16_t* q_out,
+              uint16_t* k_cache, uint16_t* v_cache, hipStream_t s);
+int attn_decode(const uint16_t* q, int rows, const int32_t* slots, const int32_t* pos,
+                const uint16_t* k_cache, const uint16_t* v_cache, AttnDims d, int max_chunks,
+                float* o_part, float* ml_part, hipStream_t s);
+int attn_combine(const float* o_part, const float* ml_part, const uint16_t* qkv,
+                 int64_t qkv_stride, int rows, const int32_t* pos, AttnDims d, int max_chunks,
+                 uint16_t* out, hipStream_t s);
+constexpr int kAttnChunk = 256;
 
 // ---- MoE ----
 int moe_route(const uint16_t* logits, int64_t logit_stride, const uint16_t* shared_logit,
@@ -79,6 +119,28 @@ int gdn_recurrence(const uint16_t* conv_out, int64_t conv_stride, const uint16_t
 int gdn_scan(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
              const uint16_t* beta, GdnDims d, int groups, int t, const int32_t* slots,
              float* state, float* history, uint16_t* y, hipStream_t s);
+
+// ---- engine (engine.cpp) ----
+struct Engine;
+int engine_create(const mx_model_config& cfg, Engine** out);
+void engine_destroy(Engine* e);
+int engine_reset_slot(Engine& e, int slot);
+int engine_clone_slot(Engine& e, int src, int dst);
+int engine_offset(const Engine& e, int slot);
+int engine_decode_rows(Engine& e, const int32_t* slots, const uint32_t* tokens, int rows,
+                       uint32_t* next, std::string* err);
+int engine_block(Engine& e, int slot, const uint32_t* tokens, int count, bool history,
+                 uint32_t* next, std::string* err);
+int engine_verify(Engine& e, int slot, const uint32_t* tokens, int count, uint32_t* next,
+                  std::string* err);
+int engine_commit(Engine& e, int slot, int keep, std::string* err);
+int engine_read(Engine& e, const char* what, void* host, size_t bytes, std::string* err);
+int engine_tensor(Engine& e, const char* name, void** ptr, size_t* bytes);
+void engine_set_flags(Engine& e, int want_logits, int use_graphs);
+const mx_model_config& engine_config(const Engine& e);
+int engine_gdn_layers(const Engine& e);
+int engine_attn_layers(const Engine& e);
+hipStream_t engine_stream(const Engine& e);
 
 int fill_bf16(uint16_t* dst, size_t count, uint64_t seed, int dist, float a, float b,
               hipStream_t s);

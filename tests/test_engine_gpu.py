@@ -1,0 +1,177 @@
+"""End-to-end parity of the decode engine (tiny hybrid model) against the CPU
+oracle model: greedy tokens, hidden states and caches bit-exact through
+prefill, equal-offset batched decode, ragged decode, MTP verify + commit and
+slot cloning; plus the reference's rejection rules (batch-parity.rs:161-171)."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def pair(mx):
+    from oracle.model import Model
+
+    cfg = dict(mx.TINY)
+    eng = mx.Engine(cfg)
+
+    def fetch(name, dtype, shape):
+        return eng.read(name, dtype, shape)
+
+    model = Model(cfg, fetch)
+    yield eng, model
+    eng.close()
+
+
+def _hidden(eng, cfg, rows):
+    return eng.read("hidden", np.uint16, (rows, cfg["hc"] * cfg["hidden"]))
+
+
+def test_rope_table_matches(pair):
+    eng, model = pair
+    c = model.c
+    half = c["rotary_dim"] // 2
+    cs = eng.read("rope.cos", np.float32, (c["max_context"], half))
+    sn = eng.read("rope.sin", np.float32, (c["max_context"], half))
+    bad = np.argwhere((cs != model.cos) | (sn != model.sin))
+    assert bad.size == 0, (bad[:4], cs[tuple(bad[0])], model.cos[tuple(bad[0])])
+
+
+def test_prefill_and_equal_offset_batch_decode(pair):
+    eng, model = pair
+    c = model.c
+    rng = np.random.default_rng(1)
+    prompt_len = 13
+    slots = [0, 1, 2]
+    nxt = {}
+    for s in slots:
+        eng.reset(s)
+        model.offsets[s] = 0
+        model.state[s * model.n_gdn:(s + 1) * model.n_gdn] = 0
+        model.conv[s * model.n_gdn:(s + 1) * model.n_gdn] = 0
+        prompt = rng.integers(0, c["vocab"], prompt_len)
+        got = eng.prefill(s, prompt)
+        want = model.prefill(s, list(prompt))
+        assert got == want, (s, got, want)
+        nxt[s] = got
+    hid = _hidden(eng, c, 5)
+    assert (hid == model.hidden).all()  # last chunk had 5 rows
+    hf = (hid.astype(np.uint32) << 16).view(np.float32)
+    assert np.isfinite(hf).all() and np.abs(hf).max() > 0  # a live, finite residual stream
+    toks = np.array([nxt[s] for s in slots], np.uint32)
+    seen = set(int(t) for t in toks)
+    for step in range(6):
+        got = eng.decode_batch(slots, toks)
+        want = model.decode_rows(slots, list(toks))
+        assert (got == want).all(), (step, got, want)
+        assert (_hidden(eng, c, len(slots)) == model.hidden).all(), step
+        toks = got
+        seen.update(int(t) for t in got)
+    for s in slots:
+        assert eng.offset(s) == model.offsets[s] == prompt_len + 6
+    seen.update(int(t) for t in toks)
+    assert len(seen) > 3  # the greedy trajectories are not degenerate
+
+
+def test_batch_rows_equal_singleton_rows(pair):
+    eng, model = pair
+    # slots 0 and 1 are both at offset 19 after the previous test
+    eng.clone(0, 3)
+    eng.clone(1, 4)
+    a = eng.decode_batch([0, 1], [5, 9])
+    b0 = eng.decode_batch([3], [5])
+    b1 = eng.decode_batch([4], [9])
+    assert a[0] == b0[0] and a[1] == b1[0]
+    model.decode_rows([0, 1], [5, 9])  # keep the oracle in step with slots 0 and 1
+
+
+def test_ragged_rows_and_long_context(pair):
+    eng, model = pair
+    c = model.c
+    rng = np.random.default_rng(2)
+    # slot 5 gets a context longer than one attention chunk (256 positions)
+    eng.reset(5)
+    model.offsets[5] = 0
+    model.state[5 * model.n_gdn:6 * model.n_gdn] = 0
+    model.conv[5 * model.n_gdn:6 * model.n_gdn] = 0
+    prompt = rng.integers(0, c["vocab"], 301)
+    assert eng.prefill(5, prompt) == model.prefill(5, list(prompt))
+    slots = [5, 2, 0]
+    toks = [7, 8, 9]
+    with pytest.raises(Exception):
+        eng.decode_batch(slots, toks)  # unequal offsets are rejected
+    for step in range(3):
+        got = eng.decode_batch(slots, toks, equal=False)
+        want = model.decode_rows(slots, toks)
+        assert (got == want).all(), step
+        assert (_hidden(eng, c, 3) == model.hidden).all()
+        toks = list(got)
+
+
+def test_verify_commit_matches_oracle(pair):
+    eng, model = pair
+    c = model.c
+    for keep in (2, 0, 4):
+        block = [11, 22, 33, 44]
+        got = eng.verify(2, block)
+        want = model.verify(2, block)
+        assert (got == want).all(), keep
+        eng.commit(2, keep)
+        model.commit(2, keep)
+        assert eng.offset(2) == model.offsets[2]
+        nxt = eng.decode_batch([2], [got[max(keep - 1, 0)]])
+        assert nxt[0] == model.decode_rows([2], [int(got[max(keep - 1, 0)])])[0], keep
+        assert (_hidden(eng, c, 1) == model.hidden).all()
+
+
+def test_commit_equals_sequential_decode(pair):
+    """Verify invariance: a verify block committed with keep=k leaves the same
+    caches as k sequential decode steps (verify-parity.rs:131-194)."""
+    eng, model = pair
+    eng.clone(0, 3)
+    block = [3, 1, 4, 1, 5]
+    eng.verify(3, block)
+    eng.commit(3, 3)
+    seq = []
+    for t in block[:3]:
+        seq.append(eng.decode_batch([0], [t])[0])
+    assert eng.offset(3) == eng.offset(0)
+    a = eng.decode_batch([3], [9])
+    b = eng.decode_batch([0], [9])
+    assert a[0] == b[0]
+
+
+def test_graph_replay_equals_eager(pair):
+    eng, model = pair
+    eng.clone(1, 3)
+    eng.clone(1, 4)
+    a = eng.decode_batch([3], [17])
+    ha = _hidden(eng, model.c, 1).copy()
+    eng.set_flags(eager=True)
+    b = eng.decode_batch([4], [17])
+    hb = _hidden(eng, model.c, 1).copy()
+    eng.set_flags()
+    assert a[0] == b[0] and (ha == hb).all()
+
+
+def test_logits_argmax_agree(pair):
+    eng, model = pair
+    eng.set_flags(logits=True)
+    eng.clone(1, 4)
+    t = eng.decode_batch([4], [23])
+    lg = eng.read("logits", np.uint16, (1, model.c["vocab"]))
+    eng.set_flags()
+    from oracle import oracle as orc
+
+    assert orc.argmax_bf16(lg)[0] == t[0]
+
+
+def test_rejects_bad_tokens_and_slots(mx, pair):
+    eng, model = pair
+    with pytest.raises(mx.MxError) as e:
+        eng.decode_batch([0], [model.c["vocab"]])
+    assert e.value.code == mx.MX_EINVAL
+    with pytest.raises(mx.MxError):
+        eng.decode_batch([0, 0], [1, 2])
+    with pytest.raises(mx.MxError):
+        eng.commit(1, 1)  # no verify block pending on slot 1
