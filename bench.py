@@ -1,16 +1,28 @@
-"""Benchmark driver (one JSON line on stdout).
+"""Benchmark driver (one JSON line on stdout, progress on stderr).
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 
 Workloads:
-  qmv-config0  BASELINE config 0: affine 4-bit g64 QMV, W [4096, 2048],
-               x [1, 2048].  A step is one QMV launch over a fresh weight copy:
-               the timed loop rotates through >= 2 GiB of distinct weight
-               copies so the 256 MB Infinity Cache cannot serve repeats.
+  config3-b8-decode (default)  BASELINE config 3: the full synthetic hybrid
+      model (48 layers, 3:1 GatedDeltaNet : gated attention, 512-expert top-10
+      MoE with a shared expert, hc = 4 hyper-connections, vocab 151936, 4-bit
+      weights with 5-bit expert down and 8-bit embedding/head), 8 slots
+      prefilled with seeded uniform-random prompts of ragged lengths 10..2048,
+      then batched greedy decode of all 8 rows per step (rows at their own
+      offsets).  A step = one decode token for each of the 8 rows; W + K = 256
+      steps per row by default.  value = aggregate tok/s over the K timed steps.
+  qmv-config0  BASELINE config 0: one affine 4-bit g64 QMV [4096, 2048] per
+      step, rotating >= 2 GiB of weight copies so the 256 MB Infinity Cache
+      cannot serve repeats; value = achieved GB/s.
 
-Timing uses HIP events recorded on the stream the kernels are launched on.
-The CPU baseline is the C oracle (oracle/liboracle.so, a restatement of the
-reference arithmetic) timed on this host's cores over a bounded sample.
+Timing: the decode loop is bracketed by device synchronisation (the engine
+synchronises once per step to read the tokens, as the reference's eval does).
+The roofline object is the MoE expert gate/up kernel (the step's dominant
+kernel): algorithmic bytes (distinct experts' weights + the shared expert)
+over its duration, both from HIP events recorded on the engine's stream
+around every launch of an eager profiled step.
+The CPU baseline is the C oracle (oracle/, a restatement of the reference
+arithmetic) timed on this host over a bounded sample of the same step.
 """
 from __future__ import annotations
 
@@ -35,6 +47,148 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+class ProfilerRegion:
+    """roctxProfilerResume/Pause around the timed loop, so that
+    `rocprofv3 --selected-regions` traces the decode steps only (not the
+    engine build or prefill).  A no-op unless --roctx is given."""
+
+    def __init__(self, enabled: bool):
+        self.lib = None
+        if enabled:
+            path = "/opt/rocm/lib/librocprofiler-sdk-roctx.so"
+            self.lib = C.CDLL(path) if os.path.exists(path) else None
+
+    def __enter__(self):
+        if self.lib:
+            self.lib.roctxProfilerResume(0)
+        return self
+
+    def __exit__(self, *exc):
+        if self.lib:
+            self.lib.roctxProfilerPause(0)
+        return False
+
+
+# --------------------------------------------------------------- config 3 --
+def bench_config3(mx, args):
+    cfg = dict(mx.CONFIG3)
+    cfg["max_context"] = 2048 + args.warmup + args.steps + 16
+    rows = 8
+    t0 = time.perf_counter()
+    eng = mx.Engine(cfg)
+    if args.eager:
+        eng.set_flags(eager=True)
+    log(f"config3: engine built in {time.perf_counter() - t0:.1f}s "
+        f"({cfg['layers']} layers, {cfg['experts']} experts)")
+    rng = np.random.default_rng(3000)
+    lengths = rng.integers(10, 2049, rows)
+    nxt = np.zeros(rows, np.uint32)
+    t0 = time.perf_counter()
+    for s in range(rows):
+        prompt = rng.integers(0, cfg["vocab"], lengths[s])
+        if args.synthetic_context:
+            eng.fill_slot(s, int(lengths[s]), seed=4000 + s)
+            nxt[s] = prompt[-1]
+        else:
+            nxt[s] = eng.prefill(s, prompt)
+    prefill_s = time.perf_counter() - t0
+    log(f"config3: {'filled' if args.synthetic_context else 'prefilled'} {int(lengths.sum())} "
+        f"context positions (lengths {[int(x) for x in lengths]}) in {prefill_s:.1f}s")
+    slots = list(range(rows))
+    toks = nxt
+    # one profiled (eager, instrumented) step: expert-kernel timing and bytes
+    toks, prof = eng.profile_step(slots, toks)
+    for _ in range(max(args.warmup - 1, 0)):
+        toks = eng.decode_batch(slots, toks, equal=False)
+    mx.check(mx.lib.mx_device_sync())
+    with ProfilerRegion(args.roctx):
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            toks = eng.decode_batch(slots, toks, equal=False)
+        mx.check(mx.lib.mx_device_sync())
+        dt = time.perf_counter() - t0
+    tok_s = rows * args.steps / dt
+    ms_step = dt / args.steps * 1e3
+    log(f"config3: {args.steps} steps x {rows} rows in {dt:.3f}s -> {tok_s:.1f} tok/s, "
+        f"{ms_step:.3f} ms/step")
+    # a second profiled step after the timed loop (longer contexts)
+    _, prof2 = eng.profile_step(slots, toks)
+    gu_gbs = (prof["gate_up_bytes"] + prof2["gate_up_bytes"]) / (
+        (prof["gate_up_ms"] + prof2["gate_up_ms"]) * 1e-3) / 1e9
+    dn_gbs = (prof["down_bytes"] + prof2["down_bytes"]) / (
+        (prof["down_ms"] + prof2["down_ms"]) * 1e-3) / 1e9
+    layers = prof["layers"]
+    gu_us = prof2["gate_up_ms"] / layers * 1e3
+    step_bytes = prof2["step_bytes"]
+    step_frac = step_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS
+    log(f"config3: expert gate/up {gu_gbs:.0f} GB/s ({gu_us:.1f} us/launch avg), "
+        f"down {dn_gbs:.0f} GB/s; distinct experts/layer {prof2['distinct_experts'] / layers:.1f}; "
+        f"step bytes {step_bytes / 1e9:.2f} GB -> {step_frac * 100:.1f}% of HBM roofline per step")
+    positions = [eng.offset(s) for s in slots]
+    cpu = None if args.no_cpu_baseline else cpu_baseline_config3(mx, eng, cfg, slots, toks, positions)
+    eng.close()
+    return {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "ms_per_step": ms_step,
+        "dtype": "affine u4/u5/u8 codes x bf16 -> fp32 acc; bf16 activations; fp32 GDN state",
+        "config": {
+            "workload": "config3-b8-decode", "model": "synthetic hybrid GDN/attention MoE",
+            "layers": cfg["layers"], "hidden": cfg["hidden"], "experts": cfg["experts"],
+            "top_k": cfg["top_k"], "vocab": cfg["vocab"], "global_batch": rows,
+            "prompt_lengths": [int(x) for x in lengths], "parallelism": "single GPU",
+            "rows_at_own_offsets": True,
+            "step_bytes_gb": round(step_bytes / 1e9, 3),
+            "step_hbm_roofline_frac": round(step_frac, 4),
+            "distinct_experts_per_layer": round(prof2["distinct_experts"] / layers, 2),
+            "expert_down_gbs": round(dn_gbs, 1),
+            "prefill_s": round(prefill_s, 2),
+            "context": "synthetic" if args.synthetic_context else "prefilled",
+        },
+        "roofline": {"bound": "hbm", "kernel": "moe gate_up_kernel<4>",
+                     "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+    }
+
+
+def cpu_baseline_config3(mx, eng, cfg, slots, toks, positions):
+    """The oracle runs one batch-8 decode step over a sample of the stack
+    (layers 0-3: three GDN layers and one attention layer, plus the mixer and
+    head) at the rows' real positions; the step time is scaled to 48 layers."""
+    from oracle.model import Model
+    from oracle import oracle as orc
+
+    sample = [0, 1, 2, 3]
+
+    def fetch(name, dtype, shape):
+        return eng.read(name, dtype, shape)
+
+    t0 = time.perf_counter()
+    model = Model(cfg, fetch, only_layers=sample)
+    log(f"cpu baseline: fetched {len(sample)} layers in {time.perf_counter() - t0:.1f}s")
+    for s, p in zip(slots, positions):
+        model.offsets[s] = p
+    t0 = time.perf_counter()
+    model.decode_rows(slots, list(toks))
+    layers_s = time.perf_counter() - t0
+    # head alone, to separate it from the per-layer cost
+    t1 = time.perf_counter()
+    orc.head_argmax(model.head, model.last_mixed)
+    head_s = time.perf_counter() - t1
+    per_layer = (layers_s - head_s) / len(sample)
+    step_s = per_layer * cfg["layers"] + head_s
+    tok_s = len(slots) / step_s
+    log(f"cpu baseline: {layers_s:.1f}s for {len(sample)} layers + head; "
+        f"scaled step {step_s:.1f}s -> {tok_s:.4f} tok/s")
+    return {"value": round(tok_s, 5), "unit": "tok/s", "cores": orc.num_threads(), "kind": "port",
+            "sample": f"one batch-8 decode step through layers {sample} (3 GDN + 1 attention) "
+                      f"+ mixer + head = {layers_s:.1f}s, scaled to {cfg['layers']} layers "
+                      f"({step_s:.1f}s/step)"}
+
+
+# ---------------------------------------------------------------- config 0 --
 def qweight_bytes(n: int, k: int, bits: int, gs: int) -> int:
     return n * k * bits // 8 + 4 * n * (k // gs)
 
@@ -44,7 +198,7 @@ def bench_qmv_config0(mx, args):
 
     n, k, bits, gs, m = 4096, 2048, 4, 64, 1
     wbytes = qweight_bytes(n, k, bits, gs)
-    alg_bytes = wbytes + 2 * m * k + 2 * m * n  # weights + x + y, counted once per launch
+    alg_bytes = wbytes + 2 * m * k + 2 * m * n
     copies = max(2, int(np.ceil(2 * 1024**3 / wbytes)))
     log(f"qmv-config0: {copies} weight copies ({copies * wbytes / 1e9:.2f} GB) for MALL rotation")
     ws = [mx.QWeight.random(n, k, bits, gs, seed=100 + 17 * i) for i in range(copies)]
@@ -64,7 +218,6 @@ def bench_qmv_config0(mx, args):
     mx.check(mx.lib.mx_event_create(C.byref(e0)))
     mx.check(mx.lib.mx_event_create(C.byref(e1)))
     mx.check(mx.lib.mx_device_sync())
-    t0 = time.perf_counter()
     mx.check(mx.lib.mx_event_record(e0, stream))
     for i in range(args.steps):
         launch(args.warmup + i)
@@ -72,57 +225,63 @@ def bench_qmv_config0(mx, args):
     ms = C.c_float()
     mx.check(mx.lib.mx_event_elapsed_ms(e0, e1, C.byref(ms)))
     mx.check(mx.lib.mx_device_sync())
-    wall = time.perf_counter() - t0
     avg_s = ms.value / 1e3 / args.steps
     achieved = alg_bytes / avg_s / 1e9
-    log(f"qmv-config0: {avg_s * 1e6:.2f} us/launch (events), wall {wall * 1e3:.1f} ms")
-
-    # correctness of the measured kernel on the last copy
+    log(f"qmv-config0: {avg_s * 1e6:.2f} us/launch (events)")
     codes, s, b = orc.random_qweight(n, k, bits, gs, seed=100 + 17 * ((args.warmup + args.steps - 1) % copies))
     want = orc.qmv(codes, s, b, k, bits, gs, x.numpy())
     if not (y.numpy() == want).all():
         raise SystemExit("bench: QMV output differs from oracle")
-
-    cpu = cpu_baseline_qmv(orc, codes, s, b, k, bits, gs, x.numpy(), alg_bytes)
+    reps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < 10.0:
+        orc.qmv(codes, s, b, k, bits, gs, x.numpy())
+        reps += 1
+    cpu_dt = (time.perf_counter() - t0) / reps
     return {
-        "metric": METRIC,
-        "value": round(achieved, 2),
-        "unit": "GB/s",
-        "ms_per_step": avg_s * 1e3,
+        "metric": METRIC, "value": round(achieved, 2), "unit": "GB/s", "ms_per_step": avg_s * 1e3,
         "dtype": "u4 codes x bf16 -> fp32 acc",
         "config": {"workload": "qmv-config0", "n": n, "k": k, "bits": bits, "group_size": gs,
                    "rows": m, "mall_rotation_copies": copies},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
-        "cpu_baseline": cpu,
+        "roofline": {"bound": "hbm", "kernel": "proj/qmv_kernel<4,1>", "achieved": round(achieved, 2),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None},
+        "cpu_baseline": {"value": round(alg_bytes / cpu_dt / 1e9, 3), "unit": "GB/s",
+                         "cores": orc.num_threads(), "kind": "port",
+                         "sample": f"{reps} oracle QMVs of the config-0 matrix in 10s"},
     }
 
 
-def cpu_baseline_qmv(orc, codes, s, b, k, bits, gs, x, alg_bytes, budget_s=10.0):
-    reps, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < budget_s:
-        orc.qmv(codes, s, b, k, bits, gs, x)
-        reps += 1
-    dt = (time.perf_counter() - t0) / reps
-    return {"value": round(alg_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": orc.num_threads(),
-            "kind": "port",
-            "sample": f"{reps} oracle QMVs of the same config-0 matrix in {budget_s:.0f}s (OpenMP)"}
-
-
-WORKLOADS = {"qmv-config0": bench_qmv_config0}
+WORKLOADS = {"config3-b8-decode": bench_config3, "qmv-config0": bench_qmv_config0}
+DEFAULTS = {"config3-b8-decode": (240, 16), "qmv-config0": (2000, 200)}
 
 
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--workload", default="qmv-config0", choices=sorted(WORKLOADS))
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--workload", default="config3-b8-decode", choices=sorted(WORKLOADS))
+    ap.add_argument("--eager", action="store_true",
+                    help="launch every kernel eagerly instead of replaying captured HIP graphs "
+                         "(same kernels; used under rocprofv3, whose kernel trace does not "
+                         "follow graph replays)")
+    ap.add_argument("--synthetic-context", action="store_true",
+                    help="give the rows random caches of the prompt lengths instead of "
+                         "prefilling them (profiling runs: the decode step's cost depends on "
+                         "the context length only)")
+    ap.add_argument("--roctx", action="store_true",
+                    help="bracket the timed loop with roctxProfilerResume/Pause "
+                         "(for rocprofv3 --selected-regions)")
+    ap.add_argument("--no-cpu-baseline", action="store_true",
+                    help="skip the oracle CPU baseline (profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); multi-GPU runs are "
-              "not part of this build", file=sys.stderr)
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build runs on a "
+              "single MI355X and has no multi-GPU path", file=sys.stderr)
         raise SystemExit(2)
+    steps, warmup = DEFAULTS[args.workload]
+    args.steps = steps if args.steps is None else args.steps
+    args.warmup = warmup if args.warmup is None else args.warmup
     from conftest import load_mx
 
     mx = load_mx()
@@ -131,7 +290,7 @@ def main() -> None:
         "metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": res["ms_per_step"],
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": res["dtype"], "data": "synthetic (seeded counter-based generator)",
+        "dtype": res["dtype"], "data": "synthetic (seeded counter-based generator, random-init weights)",
         "config": res["config"], "roofline": res["roofline"], "cpu_baseline": res["cpu_baseline"],
     }
     print(json.dumps(out), flush=True)

@@ -103,6 +103,20 @@ typedef struct mx_model_config {
 
 typedef struct mx_engine mx_engine;
 
+/* What one profiled decode step measured (HIP events on the engine stream)
+ * and its algorithmic HBM bytes (each distinct weight, state and KV byte once). */
+typedef struct mx_step_profile {
+  int32_t rows;
+  int32_t layers;             /* MoE layers profiled */
+  double distinct_experts;    /* routed experts touched, summed over layers */
+  double gate_up_ms;          /* expert gate/up kernel time, summed over layers */
+  double down_ms;             /* expert down kernel time, summed over layers */
+  double gate_up_bytes;       /* algorithmic bytes of those launches */
+  double down_bytes;
+  double step_ms;             /* the whole (eager, instrumented) step */
+  double step_bytes;          /* algorithmic bytes of the whole step */
+} mx_step_profile;
+
 /* ---- errors / version -------------------------------------------------- */
 const char* mx_last_error(void);
 int32_t mx_abi_version(void);
@@ -145,6 +159,15 @@ mx_status mx_eval_math(int32_t op, const float* in, float* out, int64_t n, void*
 mx_status mx_qmv(const mx_qweight* w, const uint16_t* x, int32_t m, uint16_t* y,
                  void* stream);
 
+/* ---- A3/A15: the same projection on the matrix cores --------------------
+ * y = x . dequant(W)^T for 1 <= m <= 16 rows with v_mfma_f32_16x16x32_bf16:
+ * codes enter as exact bf16 integers, each 64-value group's fp32 partial is
+ * scaled in registers.  Results equal mx_qmv's up to fp32 summation order
+ * (the north star's tolerance, not bit for bit).  Requires group_size 64 and
+ * k <= 8192.  The MFMA verify/prefill slot of the reference
+ * (matrix_kernel::project, src/matrix_kernel.rs:113-254, kernels/matrix_packed.metal). */
+mx_status mx_qmm(const mx_qweight* w, const uint16_t* x, int32_t m, uint16_t* y, void* stream);
+
 /* ---- A4: affine dequantisation of selected rows (embedding) --------------
  * out[i, :] = bf16(s * q + b) of row ids[i].  Replaces Linear::embedding
  * (src/weights.rs:203-226: take_axis + ops::dequantize). */
@@ -182,6 +205,14 @@ mx_status mx_moe_experts(const uint16_t* x, const uint32_t* ids, const uint16_t*
                          const mx_qbank* down, const mx_qweight* shared_gate,
                          const mx_qweight* shared_up, const mx_qweight* shared_down,
                          void* workspace, uint16_t* partial, void* stream);
+/* mx_moe_experts on the matrix cores (same contract, fp32 summation order
+ * within tolerance of the exact kernels). */
+mx_status mx_moe_experts_mfma(const uint16_t* x, const uint32_t* ids, const uint16_t* scores,
+                              int32_t rows, int32_t top_k, const mx_qbank* gate,
+                              const mx_qbank* up, const mx_qbank* down,
+                              const mx_qweight* shared_gate, const mx_qweight* shared_up,
+                              const mx_qweight* shared_down, void* workspace, uint16_t* partial,
+                              void* stream);
 /* routed[r] = bf16 sum of partial[r, 0..top_k-1] in the reference's slot
  * order (kernels/moe_down_tail.h:20, moe_down_tail.metal:83-99). */
 mx_status mx_moe_reduce(const uint16_t* partial, int32_t rows, int32_t top_k, int32_t hidden,
@@ -286,10 +317,21 @@ mx_status mx_engine_verify(mx_engine* e, int32_t slot, const uint32_t* tokens, i
                            uint32_t* argmax);
 mx_status mx_engine_commit(mx_engine* e, int32_t slot, int32_t keep);
 /* Test/inspection hooks: flags (bit 0: also write bf16 logits of each step;
- * bit 1: run eagerly instead of replaying captured HIP graphs), and reads of
+ * bit 1: run eagerly instead of replaying captured HIP graphs; bit 2: exact
+ * mode, every projection on the fixed-order kernels that the CPU oracle
+ * reproduces bit for bit, instead of the matrix-core kernels), and reads of
  * the last step's "hidden" (bf16 [rows, hc*hidden]) / "logits" (bf16
  * [rows, vocab]) or of any named weight/cache tensor into host memory. */
 mx_status mx_engine_set_flags(mx_engine* e, int32_t flags);
+/* Measurement hook (no reference counterpart): gives `slot` a synthetic
+ * context of `length` positions (random K/V, GDN state and conv window drawn
+ * from `seed`) in place of a prefill; decode cost depends on the length only. */
+mx_status mx_engine_fill_slot(mx_engine* e, int32_t slot, int32_t length, uint64_t seed);
+/* One decode step like mx_engine_decode_rows, run eagerly with the expert
+ * kernels timed per layer (no reference counterpart: the reference could not
+ * attribute GPU time per kernel, docs/performance.md:41). */
+mx_status mx_engine_profile_step(mx_engine* e, const int32_t* slots, const uint32_t* tokens,
+                                 int32_t rows, uint32_t* next, mx_step_profile* out);
 mx_status mx_engine_read(mx_engine* e, const char* what, void* host, size_t bytes);
 mx_status mx_engine_tensor(mx_engine* e, const char* name, void** device_ptr, size_t* bytes);
 

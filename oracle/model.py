@@ -30,7 +30,9 @@ def rope_table(max_ctx: int, rot: int, theta: float):
 
 
 class Model:
-    def __init__(self, cfg: dict, fetch):
+    def __init__(self, cfg: dict, fetch, only_layers=None):
+        """only_layers: load and run just these layer indices (a bounded CPU
+        sample of a large model); None runs the whole stack."""
         self.c = c = dict(cfg)
         self.fetch = fetch
         H, hc = c["hidden"], c["hc"]
@@ -51,7 +53,8 @@ class Model:
         self.head = self._qw("head", c["vocab"], H, c["head_bits"])
         self.mixer = self._hc("mixer", -1, False)
         self.layers = []
-        for i in range(c["layers"]):
+        self.layer_ids = list(range(c["layers"])) if only_layers is None else list(only_layers)
+        for i in self.layer_ids:
             p = f"layers.{i}"
             L = {"attn_hc": self._hc(p + ".attn_hc", i, True), "mlp_hc": self._hc(p + ".mlp_hc", i, True)}
             bits, dbits = self.layer_bits(i)
@@ -151,7 +154,7 @@ class Model:
         slots_a = np.ascontiguousarray(slots, np.int32)
         pos_a = np.ascontiguousarray(pos, np.int32)
         gdn_slots = np.array([slots[g * t] * self.n_gdn for g in range(groups)], np.int32)
-        for i, L in enumerate(self.layers):
+        for i, L in zip(self.layer_ids, self.layers):
             mixed, inj = self._hc_forward(L["attn_hc"], h, rows)
             if not self.attn[i]:
                 gi = self.cache_index[i]

@@ -73,6 +73,12 @@ class ModelConfigC(C.Structure):
         ("seed", C.c_uint64)]
 
 
+class StepProfileC(C.Structure):
+    _fields_ = [("rows", C.c_int32), ("layers", C.c_int32)] + [(n, C.c_double) for n in (
+        "distinct_experts", "gate_up_ms", "down_ms", "gate_up_bytes", "down_bytes", "step_ms",
+        "step_bytes")]
+
+
 def _load() -> C.CDLL:
     if not os.path.exists(LIB_PATH):
         raise ImportError(
@@ -129,6 +135,12 @@ def _load() -> C.CDLL:
         "mx_engine_verify": ([vp, i32, vp, i32, vp], i32),
         "mx_engine_commit": ([vp, i32, i32], i32),
         "mx_engine_set_flags": ([vp, i32], i32),
+        "mx_engine_fill_slot": ([vp, i32, i32, u64], i32),
+        "mx_qmm": ([C.POINTER(QWeightC), vp, i32, vp, vp], i32),
+        "mx_moe_experts_mfma": ([vp, vp, vp, i32, i32, C.POINTER(QBankC), C.POINTER(QBankC),
+                                 C.POINTER(QBankC), C.POINTER(QWeightC), C.POINTER(QWeightC),
+                                 C.POINTER(QWeightC), vp, vp, vp], i32),
+        "mx_engine_profile_step": ([vp, vp, vp, i32, vp, C.POINTER(StepProfileC)], i32),
         "mx_engine_read": ([vp, C.c_char_p, vp, sz], i32),
         "mx_engine_tensor": ([vp, C.c_char_p, C.POINTER(vp), C.POINTER(sz)], i32),
     }
@@ -343,11 +355,25 @@ class Engine:
     def clone(self, src, dst):
         check(lib.mx_engine_clone_slot(self.h, src, dst))
 
+    def fill_slot(self, slot, length, seed=1):
+        check(lib.mx_engine_fill_slot(self.h, slot, length, seed))
+
     def offset(self, slot) -> int:
         return lib.mx_engine_offset(self.h, slot)
 
-    def set_flags(self, logits=False, eager=False):
-        check(lib.mx_engine_set_flags(self.h, (1 if logits else 0) | (2 if eager else 0)))
+    def profile_step(self, slots, tokens):
+        """One eager decode step with per-layer expert-kernel timing."""
+        s = np.ascontiguousarray(slots, np.int32)
+        t = self._u32(tokens)
+        out = np.empty(len(s), np.uint32)
+        prof = StepProfileC()
+        check(lib.mx_engine_profile_step(self.h, s.ctypes.data, t.ctypes.data, len(s),
+                                         out.ctypes.data, C.byref(prof)))
+        return out, {f: getattr(prof, f) for f, _ in StepProfileC._fields_}
+
+    def set_flags(self, logits=False, eager=False, exact=False):
+        check(lib.mx_engine_set_flags(self.h, (1 if logits else 0) | (2 if eager else 0)
+                                      | (4 if exact else 0)))
 
     def read(self, what: str, dtype, shape) -> np.ndarray:
         out = np.empty(shape, dtype)

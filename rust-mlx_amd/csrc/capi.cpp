@@ -208,7 +208,7 @@ MX_ABI mx_status mx_moe_route(const uint16_t* logits, int64_t logit_stride,
 
 MX_ABI size_t mx_moe_workspace_bytes(int32_t rows, int32_t top_k, int32_t inter) {
   if (rows <= 0 || top_k <= 0 || inter <= 0) return 0;
-  return size_t(rows) * (top_k + 1) * inter * sizeof(uint16_t);
+  return moe_workspace_bytes(rows, top_k, inter);
 }
 
 MX_ABI mx_status mx_moe_experts(const uint16_t* x, const uint32_t* ids, const uint16_t* scores,
@@ -239,8 +239,8 @@ MX_ABI mx_status mx_moe_experts(const uint16_t* x, const uint32_t* ids, const ui
                sd.group_size == d.group_size && sg.bits == g.bits &&
                sg.group_size == g.group_size,
            MX_EINVAL, "mx_moe_experts: shared expert disagrees with the banks");
-  return finish(moe_experts(x, ids, scores, rows, top_k, g, u, d, sg, su, sd,
-                            static_cast<uint16_t*>(workspace), partial, hipStream_t(stream)),
+  return finish(moe_experts(x, ids, scores, rows, top_k, g, u, d, sg, su, sd, workspace, partial,
+                            hipStream_t(stream)),
                 "mx_moe_experts");
 }
 
@@ -521,7 +521,7 @@ MX_ABI mx_status mx_engine_commit(mx_engine* e, int32_t slot, int32_t keep) {
 
 MX_ABI mx_status mx_engine_set_flags(mx_engine* e, int32_t flags) {
   MX_CHECK(e != nullptr, MX_EINVAL, "mx_engine_set_flags: null engine");
-  engine_set_flags(*e->impl, flags & 1, (flags & 2) ? 0 : 1);
+  engine_set_flags(*e->impl, flags & 1, (flags & 2) ? 0 : 1, (flags & 4) ? 1 : 0);
   return MX_OK;
 }
 
@@ -537,4 +537,73 @@ MX_ABI mx_status mx_engine_tensor(mx_engine* e, const char* name, void** device_
   MX_CHECK(engine_tensor(*e->impl, name, device_ptr, bytes) == MX_OK, MX_EINVAL,
            std::string("mx_engine_tensor: unknown tensor ") + name);
   return MX_OK;
+}
+
+MX_ABI mx_status mx_engine_profile_step(mx_engine* e, const int32_t* slots, const uint32_t* tokens,
+                                        int32_t rows, uint32_t* next, mx_step_profile* out) {
+  MX_CHECK(e && slots && tokens && next && out, MX_EINVAL, "mx_engine_profile_step: null pointer");
+  MX_CHECK(rows >= 1 && rows <= 8, MX_EUNSUPPORTED, "mx_engine_profile_step: rows must be in 1..8");
+  for (int r = 0; r < rows; ++r)
+    MX_CHECK(slot_ok(*e->impl, slots[r]), MX_EINVAL, "mx_engine_profile_step: slot out of range");
+  MX_CHECK(tokens_ok(*e->impl, tokens, rows), MX_EINVAL,
+           "mx_engine_profile_step: token outside vocabulary");
+  std::string err;
+  return engine_status(engine_profile_step(*e->impl, slots, tokens, rows, next, out, &err), err,
+                       "mx_engine_profile_step");
+}
+
+MX_ABI mx_status mx_qmm(const mx_qweight* w, const uint16_t* x, int32_t m, uint16_t* y,
+                        void* stream) {
+  MX_CHECK(w != nullptr && x != nullptr && y != nullptr, MX_EINVAL, "mx_qmm: null pointer");
+  const QWeight q = to_qweight(*w);
+  if (const char* err = check_qweight(q)) return mx_status(set_error(MX_EINVAL, std::string("mx_qmm: ") + err));
+  MX_CHECK(qmm_supported(q), MX_EUNSUPPORTED, "mx_qmm: needs group_size 64 and k <= 8192");
+  MX_CHECK(m >= 1 && m <= 16, MX_EUNSUPPORTED, "mx_qmm: m must be in 1..16");
+  ProjEpilogue e{};
+  e.mode = kPlain;
+  e.y = y;
+  e.y_stride = q.n;
+  return finish(qmm(q, x, q.k, m, e, hipStream_t(stream)), "mx_qmm");
+}
+
+MX_ABI mx_status mx_moe_experts_mfma(const uint16_t* x, const uint32_t* ids, const uint16_t* scores,
+                                     int32_t rows, int32_t top_k, const mx_qbank* gate,
+                                     const mx_qbank* up, const mx_qbank* down,
+                                     const mx_qweight* shared_gate, const mx_qweight* shared_up,
+                                     const mx_qweight* shared_down, void* workspace,
+                                     uint16_t* partial, void* stream) {
+  MX_CHECK(x && ids && scores && gate && up && down && shared_gate && shared_up && shared_down &&
+               workspace && partial,
+           MX_EINVAL, "mx_moe_experts_mfma: null pointer");
+  MX_CHECK(rows >= 1 && rows <= 8, MX_EUNSUPPORTED, "mx_moe_experts_mfma: rows must be in 1..8");
+  MX_CHECK(top_k >= 1 && top_k <= 16, MX_EUNSUPPORTED, "mx_moe_experts_mfma: top_k must be in 1..16");
+  const QBank g = to_qbank(*gate), u = to_qbank(*up), d = to_qbank(*down);
+  const QWeight sg = to_qweight(*shared_gate), su = to_qweight(*shared_up), sd = to_qweight(*shared_down);
+  for (const QBank* b : {&g, &u, &d}) {
+    if (const char* err = check_bank(*b))
+      return mx_status(set_error(MX_EINVAL, std::string("mx_moe_experts_mfma: ") + err));
+    MX_CHECK(qmm_supported(QWeight{b->codes, b->scales, b->biases, b->n, b->k, b->bits, b->group_size}),
+             MX_EUNSUPPORTED, "mx_moe_experts_mfma: banks need group_size 64");
+  }
+  MX_CHECK(g.n == u.n && g.k == u.k && d.k == g.n && d.n == g.k && g.experts == u.experts &&
+               g.experts == d.experts && g.bits == u.bits && sg.n == su.n && sg.k == g.k &&
+               su.k == g.k && sd.k == sg.n && sd.n == g.k && sg.bits == g.bits &&
+               sd.bits == d.bits && qmm_supported(sg) && qmm_supported(sd),
+           MX_EINVAL, "mx_moe_experts_mfma: banks and shared expert disagree in shape");
+  const int inter = g.n > sg.n ? g.n : sg.n;
+  uint16_t* h = static_cast<uint16_t*>(workspace);
+  const size_t hb = size_t(rows) * (top_k + 1) * inter * sizeof(uint16_t);
+  MoePlan* plan = reinterpret_cast<MoePlan*>(static_cast<char*>(workspace) + ((hb + 255) / 256) * 256);
+  hipStream_t s = hipStream_t(stream);
+  int rc = moe_plan(ids, rows, top_k, plan, s);
+  if (rc == MX_OK) rc = qmm_gate_up(x, plan, rows, top_k, g, u, sg, su, h, s);
+  if (rc == MX_OK) rc = qmm_down(h, plan, scores, rows, top_k, g.n, sg.n, d, sd, partial, s);
+  return finish(rc, "mx_moe_experts_mfma");
+}
+
+MX_ABI mx_status mx_engine_fill_slot(mx_engine* e, int32_t slot, int32_t length, uint64_t seed) {
+  MX_CHECK(e && slot_ok(*e->impl, slot), MX_EINVAL, "mx_engine_fill_slot: bad engine or slot");
+  std::string err;
+  return engine_status(engine_fill_slot(*e->impl, slot, length, seed, &err), err,
+                       "mx_engine_fill_slot");
 }

@@ -102,6 +102,8 @@ struct Engine {
   uint16_t *pbuf = nullptr, *conv_out = nullptr, *y = nullptr, *qrot = nullptr, *attn_y = nullptr;
   uint16_t *logits_r = nullptr, *scores = nullptr, *factor = nullptr, *moe_p = nullptr;
   uint16_t *moe_h = nullptr, *logits = nullptr;
+  void* moe_ws = nullptr;
+  MoePlan* moe_plan_buf = nullptr;
   uint32_t* ids = nullptr;
   float *o_part = nullptr, *ml_part = nullptr;
   void* head_ws = nullptr;
@@ -121,12 +123,21 @@ struct Engine {
   // captured graphs keyed by (rows, groups, t, history, logits)
   std::map<int, hipGraphExec_t> graphs;
   bool use_graphs = true;
+  // exact: every projection on the fixed-order VALU kernels (bit-identical to
+  // the CPU oracle); otherwise dense and expert projections run on the matrix
+  // cores (router and vocabulary head stay exact in both modes)
+  bool exact = false;
+  // profiling (eager steps only): events around each layer's expert kernels
+  mx_step_profile* prof = nullptr;
+  hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
 
   ~Engine();
 };
 
 Engine::~Engine() {
   for (auto& g : graphs) hipGraphExecDestroy(g.second);
+  for (auto& v : ev)
+    if (v) hipEventDestroy(v);
   for (auto& a : allocs) hipFree(a.p);
   if (host_rows) hipHostFree(host_rows);
   if (stream) hipStreamDestroy(stream);
@@ -165,7 +176,10 @@ int make_qw(Engine& e, const std::string& name, int n, int k, int bits, int laye
   const uint64_t seed = tensor_seed(e.cfg.seed, layer, id);
   MX_TRY(fill_codes(static_cast<uint32_t*>(c), n, k, bits, seed, e.stream));
   MX_TRY(fill_bf16(static_cast<uint16_t*>(s), size_t(n) * (k / gs), seed + 1, 0, s_lo, s_hi, e.stream));
-  MX_TRY(fill_bf16(static_cast<uint16_t*>(b), size_t(n) * (k / gs), seed + 2, 0, -0.2f, 0.2f, e.stream));
+  // zero-mean weights (b ~ -s * mid): a random model whose rows stay distinct
+  // through the stack, so routing spreads over the experts as in a trained model
+  MX_TRY(fill_bias_centered(static_cast<uint16_t*>(b), static_cast<uint16_t*>(s), size_t(n) * (k / gs),
+                            bits, seed + 2, 0.01f, e.stream));
   *out = QWeight{static_cast<uint32_t*>(c), static_cast<uint16_t*>(s), static_cast<uint16_t*>(b),
                  n, k, bits, gs};
   return MX_OK;
@@ -350,7 +364,12 @@ int build(Engine& e) {
   MX_TRY(a16("act.scores", R * c.top_k, &e.scores));
   MX_TRY(a16("act.factor", R, &e.factor));
   MX_TRY(a16("act.moe_p", R * (c.top_k + 1) * c.hidden, &e.moe_p));
-  MX_TRY(a16("act.moe_h", R * (c.top_k + 1) * inter_max, &e.moe_h));
+  {
+    const size_t ws = moe_workspace_bytes(int(R), c.top_k, inter_max);
+    MX_TRY(alloc(e, "act.moe_ws", ws, &e.moe_ws));
+    e.moe_h = static_cast<uint16_t*>(e.moe_ws);
+    e.moe_plan_buf = reinterpret_cast<MoePlan*>(static_cast<char*>(e.moe_ws) + ws - sizeof(MoePlan));
+  }
   MX_TRY(a16("act.logits", R * size_t(c.vocab), &e.logits));
   MX_TRY(alloc(e, "act.ids", R * c.top_k * 4, &v));
   e.ids = static_cast<uint32_t*>(v);
@@ -370,6 +389,83 @@ int build(Engine& e) {
   return MX_OK;
 }
 
+size_t qw_bytes(const QWeight& w) {
+  return size_t(w.n) * w.k * w.bits / 8 + size_t(w.n) * (w.k / w.group_size) * 4;
+}
+
+bool experts_fast(const Engine& e, const LayerW& L) {
+  const QWeight g{L.gate.codes, L.gate.scales, L.gate.biases, L.gate.n, L.gate.k, L.gate.bits,
+                  L.gate.group_size};
+  const QWeight d{L.down.codes, L.down.scales, L.down.biases, L.down.n, L.down.k, L.down.bits,
+                  L.down.group_size};
+  return !e.exact && qmm_supported(g) && qmm_supported(d) && qmm_supported(L.sgate) &&
+         qmm_supported(L.sdown);
+}
+
+int experts_gate_up(Engine& e, const LayerW& L, int rows) {
+  const auto& c = e.cfg;
+  if (experts_fast(e, L))
+    return qmm_gate_up(e.mixed, e.moe_plan_buf, rows, c.top_k, L.gate, L.up, L.sgate, L.sup,
+                       e.moe_h, e.stream);
+  return moe_gate_up(e.mixed, e.moe_plan_buf, rows, c.top_k, L.gate, L.up, L.sgate, L.sup,
+                     e.moe_h, e.stream);
+}
+
+int experts_down(Engine& e, const LayerW& L, int rows) {
+  const auto& c = e.cfg;
+  if (experts_fast(e, L))
+    return qmm_down(e.moe_h, e.moe_plan_buf, e.scores, rows, c.top_k, L.gate.n, L.sgate.n, L.down,
+                    L.sdown, e.moe_p, e.stream);
+  return moe_down(e.moe_h, e.moe_plan_buf, e.scores, rows, c.top_k, L.gate.n, L.sgate.n, L.down,
+                  L.sdown, e.moe_p, e.stream);
+}
+
+// Profiled (eager) steps: count the layer's distinct routed experts and time
+// the gate/up and down expert kernels with events on the engine stream.
+int profile_experts(Engine& e, const LayerW& L, int rows) {
+  const auto& c = e.cfg;
+  std::vector<uint32_t> ids(size_t(rows) * c.top_k);
+  MX_HIP(hipMemcpyAsync(ids.data(), e.ids, ids.size() * 4, hipMemcpyDeviceToHost, e.stream));
+  MX_HIP(hipStreamSynchronize(e.stream));
+  std::vector<char> seen(c.experts, 0);
+  int distinct = 0;
+  for (uint32_t v : ids)
+    if (v < uint32_t(c.experts) && !seen[v]) {
+      seen[v] = 1;
+      ++distinct;
+    }
+  MX_TRY(moe_plan(e.ids, rows, c.top_k, e.moe_plan_buf, e.stream));
+  MX_HIP(hipEventRecord(e.ev[0], e.stream));
+  MX_TRY(experts_gate_up(e, L, rows));
+  MX_HIP(hipEventRecord(e.ev[1], e.stream));
+  MX_TRY(experts_down(e, L, rows));
+  MX_HIP(hipEventRecord(e.ev[2], e.stream));
+  MX_HIP(hipEventSynchronize(e.ev[2]));
+  float a = 0.0f, b = 0.0f;
+  MX_HIP(hipEventElapsedTime(&a, e.ev[0], e.ev[1]));
+  MX_HIP(hipEventElapsedTime(&b, e.ev[1], e.ev[2]));
+  mx_step_profile& p = *e.prof;
+  p.layers += 1;
+  p.distinct_experts += distinct;
+  p.gate_up_ms += a;
+  p.down_ms += b;
+  const QWeight g{L.gate.codes, L.gate.scales, L.gate.biases, L.gate.n, L.gate.k, L.gate.bits,
+                  L.gate.group_size};
+  const QWeight d{L.down.codes, L.down.scales, L.down.biases, L.down.n, L.down.k, L.down.bits,
+                  L.down.group_size};
+  p.gate_up_bytes += double(distinct) * 2.0 * double(qw_bytes(g)) +
+                     double(qw_bytes(L.sgate) + qw_bytes(L.sup));
+  p.down_bytes += double(distinct) * double(qw_bytes(d)) + double(qw_bytes(L.sdown));
+  return MX_OK;
+}
+
+// Projection on the matrix cores (fast mode) or the exact kernels.
+int project(Engine& e, const QWeight& w, const uint16_t* x, int64_t xs, int rows,
+            const ProjEpilogue& ep) {
+  if (!e.exact && qmm_supported(w)) return qmm(w, x, xs, rows, ep, e.stream);
+  return proj(w, x, xs, rows, ep, e.stream);
+}
+
 int hc_forward(Engine& e, const HcW& w, int rows, uint16_t* mixed_out, uint16_t* inj_out) {
   const auto& c = e.cfg;
   MX_TRY(hc_norm(e.h, w.scale, rows, c.hc, c.hidden, c.rms_eps, e.xn, e.stream));
@@ -381,7 +477,7 @@ int hc_forward(Engine& e, const HcW& w, int rows, uint16_t* mixed_out, uint16_t*
   d.aux_stride = c.hc;
   d.rank = c.hc_rank;
   d.hc = c.hc;
-  MX_TRY(proj(w.down, e.xn, int64_t(c.hc) * c.hidden, rows, d, e.stream));
+  MX_TRY(project(e, w.down, e.xn, int64_t(c.hc) * c.hidden, rows, d));
   ProjEpilogue u{};
   u.mode = kHcUpMix;
   u.y = mixed_out;
@@ -390,7 +486,7 @@ int hc_forward(Engine& e, const HcW& w, int rows, uint16_t* mixed_out, uint16_t*
   u.xn_stride = int64_t(c.hc) * c.hidden;
   u.hc = c.hc;
   u.hidden = c.hidden;
-  MX_TRY(proj(w.up, e.lo, c.hc_rank, rows, u, e.stream));
+  MX_TRY(project(e, w.up, e.lo, c.hc_rank, rows, u));
   return MX_OK;
 }
 
@@ -416,7 +512,7 @@ int record_step(Engine& e, int rows, int groups, int t, bool history, bool logit
       pl.mode = kPlain;
       pl.y = e.pbuf;
       pl.y_stride = e.P;
-      MX_TRY(proj(L.gdn_in, e.mixed, c.hidden, rows, pl, e.stream));
+      MX_TRY(project(e, L.gdn_in, e.mixed, c.hidden, rows, pl));
       const size_t conv_per = size_t(c.conv_k - 1) * e.cd;
       const size_t state_per = size_t(c.gdn_hv) * c.gdn_dk * c.gdn_dv;
       // cache layout [slot][gdn layer]: slot index s -> s * n_gdn + gi
@@ -431,14 +527,14 @@ int record_step(Engine& e, int rows, int groups, int t, bool history, bool logit
                             e.gdn_state + gi * state_per,
                             history ? e.hist_state + size_t(gi) * c.max_verify * state_per : nullptr,
                             e.y, e.stream));
-      MX_TRY(proj(L.gdn_out, e.y, e.vd, rows, wr, e.stream));
+      MX_TRY(project(e, L.gdn_out, e.y, e.vd, rows, wr));
     } else {
       const int ai = L.cache_index;
       ProjEpilogue pl{};
       pl.mode = kPlain;
       pl.y = e.pbuf;
       pl.y_stride = e.Q;
-      MX_TRY(proj(L.attn_in, e.mixed, c.hidden, rows, pl, e.stream));
+      MX_TRY(project(e, L.attn_in, e.mixed, c.hidden, rows, pl));
       const size_t layer_off = size_t(ai) * c.kv_heads * c.max_context * c.head_dim;
       MX_TRY(attn_prep(e.pbuf, e.Q, rows, rt->slots, rt->pos, L.q_norm, L.k_norm, c.rms_eps,
                        e.rope_cos, e.rope_sin, e.ad, e.qrot, e.k_cache + layer_off,
@@ -447,7 +543,7 @@ int record_step(Engine& e, int rows, int groups, int t, bool history, bool logit
                          e.v_cache + layer_off, e.ad, e.max_chunks, e.o_part, e.ml_part, e.stream));
       MX_TRY(attn_combine(e.o_part, e.ml_part, e.pbuf, e.Q, rows, rt->pos, e.ad, e.max_chunks,
                           e.y, e.stream));
-      MX_TRY(proj(L.attn_out, e.y, int64_t(c.heads) * c.head_dim, rows, wr, e.stream));
+      MX_TRY(project(e, L.attn_out, e.y, int64_t(c.heads) * c.head_dim, rows, wr));
     }
     // MoE sublayer
     MX_TRY(hc_forward(e, L.mlp_hc, rows, e.mixed, e.inj));
@@ -455,11 +551,16 @@ int record_step(Engine& e, int rows, int groups, int t, bool history, bool logit
     rl.mode = kPlain;
     rl.y = e.logits_r;
     rl.y_stride = c.experts + 1;
-    MX_TRY(proj(L.router, e.mixed, c.hidden, rows, rl, e.stream));
+    MX_TRY(project(e, L.router, e.mixed, c.hidden, rows, rl));
     MX_TRY(moe_route(e.logits_r, c.experts + 1, e.logits_r + c.experts, c.experts + 1, rows,
                      c.experts, c.top_k, e.ids, e.scores, e.factor, e.stream));
-    MX_TRY(moe_experts(e.mixed, e.ids, e.scores, rows, c.top_k, L.gate, L.up, L.down, L.sgate,
-                       L.sup, L.sdown, e.moe_h, e.moe_p, e.stream));
+    if (e.prof) {
+      MX_TRY(profile_experts(e, L, rows));
+    } else {
+      MX_TRY(moe_plan(e.ids, rows, c.top_k, e.moe_plan_buf, e.stream));
+      MX_TRY(experts_gate_up(e, L, rows));
+      MX_TRY(experts_down(e, L, rows));
+    }
     MX_TRY(moe_reduce_hc_epilogue(e.moe_p, e.factor, e.h, e.inj, rows, c.top_k, c.hc, c.hidden,
                                   e.h, e.stream));
   }
@@ -705,6 +806,97 @@ int engine_read(Engine& e, const char* what, void* host, size_t bytes, std::stri
   return MX_OK;
 }
 
+// Algorithmic bytes of one step over the given rows (each distinct byte once):
+// every weight outside the expert banks, the distinct experts' weights, the
+// embedding rows, GDN state and conv window read + write, and the KV
+// positions each row attends to.
+double step_bytes(const Engine& e, int rows, const int32_t* pos, double distinct_sum) {
+  const auto& c = e.cfg;
+  double dense = 0.0;
+  for (const auto& kv : e.tensors) {
+    const std::string& n = kv.first;
+    if (n.rfind("layers.", 0) != 0 && n.rfind("mixer.", 0) != 0 && n.rfind("head.", 0) != 0)
+      continue;
+    if (n.find(".moe.gate.") != std::string::npos || n.find(".moe.up.") != std::string::npos ||
+        n.find(".moe.down.") != std::string::npos)
+      continue;
+    dense += double(kv.second.bytes);
+  }
+  double experts = 0.0;
+  if (!e.layers.empty()) {
+    const LayerW& L = e.layers[0];
+    const QWeight g{L.gate.codes, L.gate.scales, L.gate.biases, L.gate.n, L.gate.k, L.gate.bits,
+                    L.gate.group_size};
+    const QWeight d{L.down.codes, L.down.scales, L.down.biases, L.down.n, L.down.k, L.down.bits,
+                    L.down.group_size};
+    experts = distinct_sum * double(2 * qw_bytes(g) + qw_bytes(d));
+  }
+  const double embed_rows = double(rows) * double(c.hidden) * (c.embed_bits / 8.0 + 4.0 / c.group_size);
+  const double state = double(rows) * e.n_gdn *
+                       (double(c.gdn_hv) * c.gdn_dk * c.gdn_dv * 4.0 + double(c.conv_k - 1) * e.cd * 2.0) * 2.0;
+  double kv = 0.0;
+  for (int r = 0; r < rows; ++r)
+    kv += double(pos[r] + 1) * e.n_attn * c.kv_heads * c.head_dim * 2.0 * 2.0;
+  return dense + experts + embed_rows + state + kv;
+}
+
+int engine_profile_step(Engine& e, const int32_t* slots, const uint32_t* tokens, int rows,
+                        uint32_t* next, mx_step_profile* out, std::string* err) {
+  std::memset(out, 0, sizeof(*out));
+  out->rows = rows;
+  int32_t pos[8];
+  for (int r = 0; r < rows; ++r) pos[r] = e.offsets[slots[r]];
+  for (auto& ev : e.ev)
+    if (!ev) MX_HIP(hipEventCreate(&ev));
+  hipEvent_t t0, t1;
+  MX_HIP(hipEventCreate(&t0));
+  MX_HIP(hipEventCreate(&t1));
+  const bool graphs = e.use_graphs;
+  e.use_graphs = false;
+  e.prof = out;
+  MX_HIP(hipEventRecord(t0, e.stream));
+  const int rc = engine_decode_rows(e, slots, tokens, rows, next, err);
+  e.prof = nullptr;
+  e.use_graphs = graphs;
+  MX_HIP(hipEventRecord(t1, e.stream));
+  MX_HIP(hipEventSynchronize(t1));
+  float ms = 0.0f;
+  MX_HIP(hipEventElapsedTime(&ms, t0, t1));
+  hipEventDestroy(t0);
+  hipEventDestroy(t1);
+  if (rc != MX_OK) return rc;
+  out->step_ms = ms;
+  out->step_bytes = step_bytes(e, rows, pos, out->distinct_experts);
+  return MX_OK;
+}
+
+// Gives a slot a synthetic context of `length` positions: random K/V for
+// those positions, random GDN state and conv window (decode cost depends on
+// the context length only, so this stands in for a prefill when measuring).
+int engine_fill_slot(Engine& e, int slot, int length, uint64_t seed, std::string* err) {
+  const auto& c = e.cfg;
+  if (length < 0 || length > c.max_context) {
+    *err = "length outside 0..max_context";
+    return MX_EINVAL;
+  }
+  const size_t sp = state_per(e), cp = conv_per(e);
+  MX_TRY(fill_f32(e.gdn_state + size_t(slot) * e.n_gdn * sp, e.n_gdn * sp, seed, -0.05f, 0.05f,
+                  e.stream));
+  MX_TRY(fill_bf16(e.conv_state + size_t(slot) * e.n_gdn * cp, e.n_gdn * cp, seed + 1, 1, 1.0f,
+                   0.0f, e.stream));
+  const size_t plane = size_t(c.max_context) * c.head_dim;
+  for (int p = 0; p < e.n_attn * c.kv_heads; ++p) {
+    uint16_t* kb = e.k_cache + size_t(slot) * e.ad.slot_stride + p * plane;
+    uint16_t* vb = e.v_cache + size_t(slot) * e.ad.slot_stride + p * plane;
+    MX_TRY(fill_bf16(kb, size_t(length) * c.head_dim, seed + 2 + 2 * p, 1, 1.0f, 0.0f, e.stream));
+    MX_TRY(fill_bf16(vb, size_t(length) * c.head_dim, seed + 3 + 2 * p, 1, 1.0f, 0.0f, e.stream));
+  }
+  MX_HIP(hipStreamSynchronize(e.stream));
+  e.offsets[slot] = length;
+  if (e.verify_slot == slot) e.verify_slot = -1;
+  return MX_OK;
+}
+
 int engine_tensor(Engine& e, const char* name, void** ptr, size_t* bytes) {
   auto it = e.tensors.find(name);
   if (it == e.tensors.end()) return MX_EINVAL;
@@ -713,9 +905,15 @@ int engine_tensor(Engine& e, const char* name, void** ptr, size_t* bytes) {
   return MX_OK;
 }
 
-void engine_set_flags(Engine& e, int want_logits, int use_graphs) {
+void engine_set_flags(Engine& e, int want_logits, int use_graphs, int exact) {
   e.want_logits = want_logits != 0;
   e.use_graphs = use_graphs != 0;
+  if (e.exact != (exact != 0)) {
+    // captured graphs bake in the kernel choice
+    for (auto& g : e.graphs) hipGraphExecDestroy(g.second);
+    e.graphs.clear();
+  }
+  e.exact = exact != 0;
 }
 
 const mx_model_config& engine_config(const Engine& e) { return e.cfg; }

@@ -57,6 +57,10 @@ struct ProjEpilogue {
 };
 int proj(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const ProjEpilogue& e,
          hipStream_t s);
+// matrix-core (MFMA) projections, 1..16 rows, group size 64 (qmm.hip)
+bool qmm_supported(const QWeight& w);
+int qmm(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const ProjEpilogue& e,
+        hipStream_t s);
 int hc_norm(const uint16_t* x, const uint16_t* scale, int rows, int hc, int hidden, float eps,
             uint16_t* y, hipStream_t s);
 int embed(const QWeight& w, const uint32_t* ids, int count, int hc, uint16_t* out, hipStream_t s);
@@ -80,13 +84,37 @@ int attn_combine(const float* o_part, const float* ml_part, const uint16_t* qkv,
 constexpr int kAttnChunk = 256;
 
 // ---- MoE ----
+constexpr int kMaxRoutes = 8 * 16 + 1;
+// Work list of one MoE step: distinct routed experts (first appearance order)
+// and the shared expert (-1), each with the (row, slot) routes it serves.
+struct MoePlan {
+  int32_t count;
+  int32_t expert[kMaxRoutes];
+  int32_t m[kMaxRoutes];
+  uint8_t row[kMaxRoutes][8];
+  uint8_t slot[kMaxRoutes][8];
+};
+int moe_plan(const uint32_t* ids, int rows, int top_k, MoePlan* plan, hipStream_t s);
+size_t moe_workspace_bytes(int rows, int top_k, int inter);
 int moe_route(const uint16_t* logits, int64_t logit_stride, const uint16_t* shared_logit,
               int64_t shared_stride, int rows, int experts, int top_k, uint32_t* ids,
               uint16_t* scores, uint16_t* factor, hipStream_t s);
 int moe_experts(const uint16_t* x, const uint32_t* ids, const uint16_t* scores, int rows,
                 int top_k, const QBank& gate, const QBank& up, const QBank& down,
-                const QWeight& sgate, const QWeight& sup, const QWeight& sdown, uint16_t* h,
+                const QWeight& sgate, const QWeight& sup, const QWeight& sdown, void* workspace,
                 uint16_t* p, hipStream_t s);
+int moe_gate_up(const uint16_t* x, const MoePlan* plan, int rows, int top_k, const QBank& gate,
+                const QBank& up, const QWeight& sgate, const QWeight& sup, uint16_t* h,
+                hipStream_t s);
+int moe_down(const uint16_t* h, const MoePlan* plan, const uint16_t* scores, int rows, int top_k,
+             int inter, int shared_inter, const QBank& down, const QWeight& sdown, uint16_t* p,
+             hipStream_t s);
+int qmm_gate_up(const uint16_t* x, const MoePlan* plan, int rows, int top_k, const QBank& gate,
+                const QBank& up, const QWeight& sgate, const QWeight& sup, uint16_t* h,
+                hipStream_t s);
+int qmm_down(const uint16_t* h, const MoePlan* plan, const uint16_t* scores, int rows, int top_k,
+             int inter, int shared_inter, const QBank& down, const QWeight& sdown, uint16_t* p,
+             hipStream_t s);
 int moe_reduce(const uint16_t* p, int rows, int top_k, int hidden, uint16_t* routed,
                hipStream_t s);
 int moe_hc_epilogue(const uint16_t* routed, const uint16_t* shared, const uint16_t* factor,
@@ -136,7 +164,10 @@ int engine_verify(Engine& e, int slot, const uint32_t* tokens, int count, uint32
 int engine_commit(Engine& e, int slot, int keep, std::string* err);
 int engine_read(Engine& e, const char* what, void* host, size_t bytes, std::string* err);
 int engine_tensor(Engine& e, const char* name, void** ptr, size_t* bytes);
-void engine_set_flags(Engine& e, int want_logits, int use_graphs);
+int engine_fill_slot(Engine& e, int slot, int length, uint64_t seed, std::string* err);
+int engine_profile_step(Engine& e, const int32_t* slots, const uint32_t* tokens, int rows,
+                        uint32_t* next, mx_step_profile* out, std::string* err);
+void engine_set_flags(Engine& e, int want_logits, int use_graphs, int exact);
 const mx_model_config& engine_config(const Engine& e);
 int engine_gdn_layers(const Engine& e);
 int engine_attn_layers(const Engine& e);
@@ -145,6 +176,9 @@ hipStream_t engine_stream(const Engine& e);
 int fill_bf16(uint16_t* dst, size_t count, uint64_t seed, int dist, float a, float b,
               hipStream_t s);
 int fill_codes(uint32_t* dst, int64_t rows, int k, int bits, uint64_t seed, hipStream_t s);
+int fill_bias_centered(uint16_t* b, const uint16_t* scales, size_t count, int bits, uint64_t seed,
+                       float noise, hipStream_t s);
+int fill_f32(float* dst, size_t count, uint64_t seed, float a, float b, hipStream_t s);
 int eval_math(int op, const float* in, float* out, int64_t n, hipStream_t s);
 
 }  // namespace mx

@@ -102,32 +102,56 @@ __global__ __launch_bounds__(64) void route_kernel(const uint16_t* __restrict__ 
   }
 }
 
-// Gathers the rows served by the workgroup of route `t`.  Returns 0 when an
-// earlier route names the same expert (that workgroup does the work).
-// Route R*top_k is the shared expert, used by every row.
-__device__ __forceinline__ int gather_routes(const uint32_t* __restrict__ ids, int rows, int top_k,
-                                             int t, int* row_of, int* slot_of, int* expert) {
+// ---------------------------------------------------------------------------
+// Expert work plan: one entry per distinct routed expert (in order of first
+// appearance among the rows' slots) plus one for the shared expert, listing
+// the (row, slot) routes it serves.  One workgroup; routes <= 8 * 16 + 1.
+__global__ __launch_bounds__(256) void plan_kernel(const uint32_t* __restrict__ ids, int rows,
+                                                   int top_k, MoePlan* __restrict__ plan) {
+  __shared__ uint32_t sids[kMaxRoutes];
+  __shared__ int wave_count[4];
+  const int t = threadIdx.x;
   const int routes = rows * top_k;
-  if (t == routes) {
-    *expert = -1;
-    for (int r = 0; r < rows; ++r) {
-      row_of[r] = r;
-      slot_of[r] = top_k;
-    }
-    return rows;
+  if (t < routes) sids[t] = ids[t];
+  __syncthreads();
+  bool first = false;
+  int e = -1;
+  if (t < routes) {
+    e = int(sids[t]);
+    first = true;
+    for (int u = 0; u < t; ++u)
+      if (int(sids[u]) == e) {
+        first = false;
+        break;
+      }
+  } else if (t == routes) {
+    first = true;  // the shared expert
   }
-  const uint32_t e = ids[t];
-  for (int u = 0; u < t; ++u)
-    if (ids[u] == e) return 0;
+  const uint64_t mask = __ballot(first);
+  const int lane = t & 63, wave = t >> 6;
+  if (lane == 0) wave_count[wave] = __popcll(mask);
+  __syncthreads();
+  int idx = __popcll(mask & ((1ull << lane) - 1ull));
+  for (int w = 0; w < wave; ++w) idx += wave_count[w];
+  if (t == 0) plan->count = wave_count[0] + wave_count[1] + wave_count[2] + wave_count[3];
+  if (!first) return;
+  plan->expert[idx] = e;
   int m = 0;
-  for (int u = t; u < routes; ++u)
-    if (ids[u] == e) {
-      row_of[m] = u / top_k;
-      slot_of[m] = u % top_k;
+  if (t == routes) {
+    for (int r = 0; r < rows; ++r) {
+      plan->row[idx][m] = uint8_t(r);
+      plan->slot[idx][m] = uint8_t(top_k);
       ++m;
     }
-  *expert = int(e);
-  return m;
+  } else {
+    for (int u = t; u < routes; ++u)
+      if (int(sids[u]) == e) {
+        plan->row[idx][m] = uint8_t(u / top_k);
+        plan->slot[idx][m] = uint8_t(u % top_k);
+        ++m;
+      }
+  }
+  plan->m[idx] = m;
 }
 
 struct Bank {
@@ -177,20 +201,14 @@ __device__ void gate_up_body(const uint16_t* __restrict__ x, const Bank& gb, con
 
 template <int BITS>
 __global__ __launch_bounds__(256) void gate_up_kernel(const uint16_t* __restrict__ x,
-                                                      const uint32_t* __restrict__ ids, int rows,
+                                                      const MoePlan* __restrict__ plan,
                                                       int top_k, QBank gate, QBank up,
                                                       QWeight sgate, QWeight sup,
                                                       uint16_t* __restrict__ h, int hs) {
-  __shared__ int row_of[8], slot_of[8], info[2];
-  if (threadIdx.x == 0) {
-    int e;
-    info[0] = gather_routes(ids, rows, top_k, blockIdx.y, row_of, slot_of, &e);
-    info[1] = e;
-  }
-  __syncthreads();
-  const int m = info[0];
-  if (m == 0) return;
-  const int expert = info[1];
+  const int entry = blockIdx.y;
+  if (entry >= plan->count) return;
+  const int m = plan->m[entry];
+  const int expert = plan->expert[entry];
   const Bank gb = bank_for(gate, expert, sgate);
   const Bank ub = bank_for(up, expert, sup);
   const int inter = expert < 0 ? sgate.n : gate.n;
@@ -201,9 +219,9 @@ __global__ __launch_bounds__(256) void gate_up_kernel(const uint16_t* __restrict
   const int row0 = ((blockIdx.x * kWaves + wave) * (64 / L) + lg) * kQRows;
   if (row0 >= inter) return;
   int ro[8], so[8];
-  for (int i = 0; i < m; ++i) {
-    ro[i] = row_of[i];
-    so[i] = slot_of[i];
+  for (int i = 0; i < 8; ++i) {
+    ro[i] = plan->row[entry][i];
+    so[i] = plan->slot[entry][i];
   }
   switch (m) {
 #define MX_CASE(MM) \
@@ -249,20 +267,14 @@ __device__ void down_body(const uint16_t* __restrict__ h, const Bank& db, int hi
 
 template <int BITS>
 __global__ __launch_bounds__(256) void down_kernel(const uint16_t* __restrict__ h,
-                                                   const uint32_t* __restrict__ ids,
-                                                   const uint16_t* __restrict__ scores, int rows,
+                                                   const MoePlan* __restrict__ plan,
+                                                   const uint16_t* __restrict__ scores,
                                                    int top_k, QBank down, QWeight sdown,
                                                    uint16_t* __restrict__ p, int hs) {
-  __shared__ int row_of[8], slot_of[8], info[2];
-  if (threadIdx.x == 0) {
-    int e;
-    info[0] = gather_routes(ids, rows, top_k, blockIdx.y, row_of, slot_of, &e);
-    info[1] = e;
-  }
-  __syncthreads();
-  const int m = info[0];
-  if (m == 0) return;
-  const int expert = info[1];
+  const int entry = blockIdx.y;
+  if (entry >= plan->count) return;
+  const int m = plan->m[entry];
+  const int expert = plan->expert[entry];
   const Bank db = bank_for(down, expert, sdown);
   const int hidden = down.n;
   const int inter = expert < 0 ? sdown.k : down.k;
@@ -272,9 +284,9 @@ __global__ __launch_bounds__(256) void down_kernel(const uint16_t* __restrict__ 
   const int row0 = ((blockIdx.x * kWaves + wave) * (64 / L) + lg) * kQRows;
   if (row0 >= hidden) return;
   int ro[8], so[8];
-  for (int i = 0; i < m; ++i) {
-    ro[i] = row_of[i];
-    so[i] = slot_of[i];
+  for (int i = 0; i < 8; ++i) {
+    ro[i] = plan->row[entry][i];
+    so[i] = plan->slot[entry][i];
   }
   switch (m) {
 #define MX_CASE(MM) \
@@ -375,41 +387,69 @@ int moe_route(const uint16_t* logits, int64_t logit_stride, const uint16_t* shar
 #undef MX_ROUTE
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
-int moe_experts(const uint16_t* x, const uint32_t* ids, const uint16_t* scores, int rows,
-                int top_k, const QBank& gate, const QBank& up, const QBank& down,
-                const QWeight& sgate, const QWeight& sup, const QWeight& sdown, uint16_t* h,
-                uint16_t* p, hipStream_t s) {
+int moe_plan(const uint32_t* ids, int rows, int top_k, MoePlan* plan, hipStream_t s) {
+  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(256), 0, s, ids, rows, top_k, plan);
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
+int moe_gate_up(const uint16_t* x, const MoePlan* plan, int rows, int top_k, const QBank& gate,
+                const QBank& up, const QWeight& sgate, const QWeight& sup, uint16_t* h,
+                hipStream_t s) {
   const int routes = rows * top_k + 1;
   const int hs = gate.n > sgate.n ? gate.n : sgate.n;  // h row stride (workspace layout)
-  {
-    // rows per workgroup is fixed by K = hidden, shared by routed and shared experts
-    const int L = qmv_lanes_per_row(gate.k);
-    const int rows_per_block = kWaves * (64 / L) * kQRows;
-    const dim3 grid((hs + rows_per_block - 1) / rows_per_block, routes);
+  // rows per workgroup is fixed by K = hidden, shared by routed and shared experts
+  const int L = qmv_lanes_per_row(gate.k);
+  const int rows_per_block = kWaves * (64 / L) * kQRows;
+  const dim3 grid((hs + rows_per_block - 1) / rows_per_block, routes);
 #define MX_GU(B) \
-  case B: hipLaunchKernelGGL(gate_up_kernel<B>, grid, dim3(256), 0, s, x, ids, rows, top_k, gate, up, sgate, sup, h, hs); break;
-    switch (gate.bits) {
-      MX_GU(4) MX_GU(5) MX_GU(6) MX_GU(8)
-      default: return MX_EUNSUPPORTED;
-    }
+  case B: hipLaunchKernelGGL(gate_up_kernel<B>, grid, dim3(256), 0, s, x, plan, top_k, gate, up, sgate, sup, h, hs); break;
+  switch (gate.bits) {
+    MX_GU(4) MX_GU(5) MX_GU(6) MX_GU(8)
+    default: return MX_EUNSUPPORTED;
+  }
 #undef MX_GU
-  }
-  {
-    // rows per workgroup shrink as K = inter grows: size the grid for the
-    // deeper of the two (workgroups past the end of a shallower route exit)
-    const int kmax = down.k > sdown.k ? down.k : sdown.k;
-    const int L = qmv_lanes_per_row(kmax);
-    const int rows_per_block = kWaves * (64 / L) * kQRows;
-    const dim3 grid((down.n + rows_per_block - 1) / rows_per_block, routes);
-#define MX_DN(B) \
-  case B: hipLaunchKernelGGL(down_kernel<B>, grid, dim3(256), 0, s, h, ids, scores, rows, top_k, down, sdown, p, hs); break;
-    switch (down.bits) {
-      MX_DN(4) MX_DN(5) MX_DN(6) MX_DN(8)
-      default: return MX_EUNSUPPORTED;
-    }
-#undef MX_DN
-  }
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
+int moe_down(const uint16_t* h, const MoePlan* plan, const uint16_t* scores, int rows, int top_k,
+             int inter, int shared_inter, const QBank& down, const QWeight& sdown, uint16_t* p,
+             hipStream_t s) {
+  const int routes = rows * top_k + 1;
+  const int hs = inter > shared_inter ? inter : shared_inter;
+  // rows per workgroup shrink as K = inter grows: size the grid for the
+  // deeper of the two (workgroups past the end of a shallower route exit)
+  const int kmax = down.k > sdown.k ? down.k : sdown.k;
+  const int L = qmv_lanes_per_row(kmax);
+  const int rows_per_block = kWaves * (64 / L) * kQRows;
+  const dim3 grid((down.n + rows_per_block - 1) / rows_per_block, routes);
+#define MX_DN(B) \
+  case B: hipLaunchKernelGGL(down_kernel<B>, grid, dim3(256), 0, s, h, plan, scores, top_k, down, sdown, p, hs); break;
+  switch (down.bits) {
+    MX_DN(4) MX_DN(5) MX_DN(6) MX_DN(8)
+    default: return MX_EUNSUPPORTED;
+  }
+#undef MX_DN
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
+size_t moe_workspace_bytes(int rows, int top_k, int inter) {
+  const size_t h = size_t(rows) * (top_k + 1) * inter * sizeof(uint16_t);
+  return ((h + 255) / 256) * 256 + sizeof(MoePlan);
+}
+
+int moe_experts(const uint16_t* x, const uint32_t* ids, const uint16_t* scores, int rows,
+                int top_k, const QBank& gate, const QBank& up, const QBank& down,
+                const QWeight& sgate, const QWeight& sup, const QWeight& sdown, void* workspace,
+                uint16_t* p, hipStream_t s) {
+  const int inter = gate.n > sgate.n ? gate.n : sgate.n;
+  uint16_t* h = static_cast<uint16_t*>(workspace);
+  const size_t hb = size_t(rows) * (top_k + 1) * inter * sizeof(uint16_t);
+  MoePlan* plan = reinterpret_cast<MoePlan*>(static_cast<char*>(workspace) + ((hb + 255) / 256) * 256);
+  int rc = moe_plan(ids, rows, top_k, plan, s);
+  if (rc != MX_OK) return rc;
+  rc = moe_gate_up(x, plan, rows, top_k, gate, up, sgate, sup, h, s);
+  if (rc != MX_OK) return rc;
+  return moe_down(h, plan, scores, rows, top_k, gate.n, sgate.n, down, sdown, p, s);
 }
 
 int moe_reduce(const uint16_t* p, int rows, int top_k, int hidden, uint16_t* routed,

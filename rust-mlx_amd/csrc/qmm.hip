@@ -1,0 +1,344 @@
+// Fast affine-quantised projections on the gfx950 matrix cores (MFMA), for
+// 1..16 activation rows: decode batches, verify blocks and prefill chunks.
+//
+// Replaces the same reference interfaces as the exact kernels (qmv_kernel /
+// gather_qmm of Linear::forward_rows, src/weights.rs:111-202; the expert
+// gate/up/down of MoE::parts, src/hybrid.rs:192-287) with the arithmetic of
+// qmm_core.hpp: results agree with the exact kernels to fp32 summation-order
+// differences (a bf16 ulp or so after rounding), not bit for bit.
+//
+// A workgroup has four waves.  K is split across SK waves (each takes a
+// contiguous range of 64-value groups); their fp32 partials are added in wave
+// order in LDS before the epilogue, so the result is deterministic.
+#include "common.hpp"
+#include "kernels.hpp"
+#include "qmm_core.hpp"
+
+namespace mx {
+
+namespace {
+
+constexpr int kMaxGroups = 128;  // K <= 8192
+
+__device__ __forceinline__ float sigmoid_bf16(float x) {
+  const float e = round_bf16(expf_(__builtin_fabsf(x)));
+  const float d = round_bf16(1.0f + e);
+  const float y = round_bf16(1.0f / d);
+  return x < 0.0f ? y : round_bf16(1.0f - y);
+}
+
+__host__ __device__ inline int split_k(int k) {
+  const int G = k >> 6;
+  return G >= 16 ? 4 : G >= 8 ? 2 : 1;
+}
+
+// Adds the SK partials of each tile group in wave order; returns true on the
+// waves that hold the sums (k-part 0).
+template <int NT, int SK>
+__device__ __forceinline__ bool reduce_split(floatx4_t (&y)[NT], float* red) {
+  if constexpr (SK == 1) {
+    return true;
+  } else {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int kp = wave % SK;
+    if (kp != 0) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        *reinterpret_cast<floatx4_t*>(red + ((wave * NT + t) * 64 + lane) * 4) = y[t];
+    }
+    __syncthreads();
+    if (kp != 0) return false;
+#pragma unroll
+    for (int p = 1; p < SK; ++p)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const floatx4_t v = *reinterpret_cast<const floatx4_t*>(red + (((wave + p) * NT + t) * 64 + lane) * 4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y[t][r] = y[t][r] + v[r];
+      }
+    return true;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Dense projections with the proj.hip epilogues.  NT = 1 for kPlain, kHcDown
+// and kHcWrite (tile group = 16 rows); NT = 4 for kHcUpMix (the four streams
+// s*H + c of 16 columns c).
+template <int BITS, int NT, int SK>
+__global__ __launch_bounds__(256) void dense_kernel(QWeight w, const uint16_t* __restrict__ x,
+                                                    int64_t x_stride, int M, ProjEpilogue e) {
+  __shared__ float red[(SK > 1 ? 4 * NT * 64 * 4 : 4)];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 15, kq = lane >> 4;
+  const int tg = blockIdx.x * (4 / SK) + wave / SK;
+  const int kp = wave % SK;
+  const int n = w.n;
+  int base, wrow[NT];
+  bool live;
+  if constexpr (NT == 4) {  // kHcUpMix
+    base = tg * 16;
+    live = base < e.hidden;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) wrow[t] = min(t * e.hidden + base + j, n - 1);
+  } else {
+    base = tg * 16 * NT;
+    live = base < n;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) wrow[t] = min(base + 16 * t + j, n - 1);
+  }
+  floatx4_t y[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) y[t] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const int G = w.k >> 6;
+  if (live) {
+    TileRow tr[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) tr[t] = tile_row(w.codes, w.scales, w.biases, w.k, BITS, wrow[t]);
+    qmm_tiles<BITS, NT>(tr, j < M ? x + size_t(j) * x_stride : nullptr, G * kp / SK,
+                        G * (kp + 1) / SK, y);
+  }
+  if (!reduce_split<NT, SK>(y, red) || !live) return;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = 4 * kq + r;
+    if (m >= M) continue;
+    if constexpr (NT == 4) {
+      const int c = base + j;
+      if (c >= e.hidden) continue;
+      float sum = 0.0f;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const float p = round_bf16(y[s][r]);
+        const float xn = bf16_to_f32(e.xn[size_t(m) * e.xn_stride + size_t(s) * e.hidden + c]);
+        sum = sum + round_bf16(sigmoid_bf16(p) * xn);
+      }
+      e.y[size_t(m) * e.y_stride + c] = f32_to_bf16(round_bf16(sum) / 4.0f);
+    } else {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const int row = base + 16 * t + j;
+        if (row >= n) continue;
+        const float v = y[t][r];
+        if (e.mode == kPlain) {
+          e.y[size_t(m) * e.y_stride + row] = f32_to_bf16(v);
+        } else if (e.mode == kHcDown) {
+          const float tt = round_bf16(round_bf16(v) / float(e.hc));
+          if (row < e.rank)
+            e.y[size_t(m) * e.y_stride + row] = f32_to_bf16(tt * sigmoid_bf16(tt));
+          else
+            e.aux[size_t(m) * e.aux_stride + (row - e.rank)] = f32_to_bf16(sigmoid_bf16(tt) * 2.0f);
+        } else {  // kHcWrite
+          const float vb = round_bf16(v);
+          for (int s = 0; s < e.hc; ++s) {
+            uint16_t* res = e.y + size_t(m) * e.y_stride + size_t(s) * n + row;
+            const float inj = round_bf16(vb * bf16_to_f32(e.aux[size_t(m) * e.aux_stride + s]));
+            *res = f32_to_bf16(bf16_to_f32(*res) + inj);
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int BITS, int NT, int SK>
+void launch_dense(const QWeight& w, const uint16_t* x, int64_t xs, int m, const ProjEpilogue& e,
+                  hipStream_t s) {
+  const int tiles = NT == 4 ? (e.hidden + 15) / 16 : (w.n + 16 * NT - 1) / (16 * NT);
+  const int per_block = 4 / SK;
+  const int blocks = (tiles + per_block - 1) / per_block;
+  hipLaunchKernelGGL((dense_kernel<BITS, NT, SK>), dim3(blocks), dim3(256), 0, s, w, x, xs, m, e);
+}
+
+template <int BITS, int NT>
+void dense_sk(const QWeight& w, const uint16_t* x, int64_t xs, int m, const ProjEpilogue& e,
+              hipStream_t s) {
+  switch (split_k(w.k)) {
+    case 4: launch_dense<BITS, NT, 4>(w, x, xs, m, e, s); break;
+    case 2: launch_dense<BITS, NT, 2>(w, x, xs, m, e, s); break;
+    default: launch_dense<BITS, NT, 1>(w, x, xs, m, e, s); break;
+  }
+}
+
+template <int BITS>
+void dense_bits(const QWeight& w, const uint16_t* x, int64_t xs, int m, const ProjEpilogue& e,
+                hipStream_t s) {
+  if (e.mode == kHcUpMix)
+    dense_sk<BITS, 4>(w, x, xs, m, e, s);
+  else
+    dense_sk<BITS, 1>(w, x, xs, m, e, s);
+}
+
+// ---------------------------------------------------------------------------
+// Experts.  One workgroup serves one plan entry (an expert and the rows that
+// chose it) for 4/SK tile groups.  gate/up: NT = 2 (the gate tile and the up
+// tile of the same 16 rows), SwiGLU in the epilogue.  down: NT = 1, the route
+// score product in the epilogue.
+__device__ __forceinline__ QWeight expert_weight(const QBank& b, int expert, const QWeight& shared) {
+  if (expert < 0) return shared;
+  const size_t cs = size_t(b.n) * b.k * b.bits / 32;
+  const size_t ss = size_t(b.n) * (b.k / b.group_size);
+  return QWeight{b.codes + cs * expert, b.scales + ss * expert, b.biases + ss * expert, b.n, b.k,
+                 b.bits, b.group_size};
+}
+
+template <int BITS, int SK>
+__global__ __launch_bounds__(256) void expert_gate_up_kernel(const uint16_t* __restrict__ x,
+                                                             const MoePlan* __restrict__ plan,
+                                                             int top_k, QBank gate, QBank up,
+                                                             QWeight sgate, QWeight sup,
+                                                             uint16_t* __restrict__ h, int hs) {
+  __shared__ float red[(SK > 1 ? 4 * 2 * 64 * 4 : 4)];
+  const int entry = blockIdx.y;
+  if (entry >= plan->count) return;
+  const int M = plan->m[entry];
+  const int expert = plan->expert[entry];
+  const QWeight gw = expert_weight(gate, expert, sgate);
+  const QWeight uw = expert_weight(up, expert, sup);
+  const int hidden = gate.k;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 15, kq = lane >> 4;
+  int row_of[8], slot_of[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    row_of[i] = plan->row[entry][i];
+    slot_of[i] = plan->slot[entry][i];
+  }
+  const int tg = blockIdx.x * (4 / SK) + wave / SK;
+  const int kp = wave % SK;
+  const int inter = gw.n;
+  const int base = tg * 16;
+  const bool live = base < inter;
+  floatx4_t y[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+  const int G = hidden >> 6;
+  if (live) {
+    const int row = min(base + j, inter - 1);
+    const TileRow tr[2] = {tile_row(gw.codes, gw.scales, gw.biases, hidden, BITS, row),
+                           tile_row(uw.codes, uw.scales, uw.biases, hidden, BITS, row)};
+    const uint16_t* xa = j < M ? x + size_t(row_of[j & 7]) * hidden : nullptr;
+    qmm_tiles<BITS, 2>(tr, xa, G * kp / SK, G * (kp + 1) / SK, y);
+  }
+  if (!reduce_split<2, SK>(y, red) || !live) return;
+  const int c = base + j;
+  if (c >= inter) return;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = 4 * kq + r;
+    if (m >= M) continue;
+    const float gv = round_bf16(y[0][r]);
+    const float uv = round_bf16(y[1][r]);
+    const float silu = round_bf16(gv * sigmoid_bf16(gv));
+    h[(size_t(row_of[m]) * (top_k + 1) + slot_of[m]) * hs + c] = f32_to_bf16(silu * uv);
+  }
+}
+
+template <int BITS, int SK>
+__global__ __launch_bounds__(256) void expert_down_kernel(const uint16_t* __restrict__ h,
+                                                          const MoePlan* __restrict__ plan,
+                                                          const uint16_t* __restrict__ scores,
+                                                          int top_k, QBank down, QWeight sdown,
+                                                          uint16_t* __restrict__ p, int hs) {
+  __shared__ float red[(SK > 1 ? 4 * 64 * 4 : 4)];
+  const int entry = blockIdx.y;
+  if (entry >= plan->count) return;
+  const int M = plan->m[entry];
+  const int expert = plan->expert[entry];
+  const QWeight dw = expert_weight(down, expert, sdown);
+  const int hidden = dw.n, inter = dw.k;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 15, kq = lane >> 4;
+  int row_of[8], slot_of[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    row_of[i] = plan->row[entry][i];
+    slot_of[i] = plan->slot[entry][i];
+  }
+  const int tg = blockIdx.x * (4 / SK) + wave / SK;
+  const int kp = wave % SK;
+  const int base = tg * 16;
+  const bool live = base < hidden;
+  floatx4_t y[1] = {{0.0f, 0.0f, 0.0f, 0.0f}};
+  const int G = inter >> 6;
+  if (live) {
+    const TileRow tr[1] = {tile_row(dw.codes, dw.scales, dw.biases, inter, BITS,
+                                    min(base + j, hidden - 1))};
+    const uint16_t* xa =
+        j < M ? h + (size_t(row_of[j & 7]) * (top_k + 1) + slot_of[j & 7]) * hs : nullptr;
+    qmm_tiles<BITS, 1>(tr, xa, G * kp / SK, G * (kp + 1) / SK, y);
+  }
+  if (!reduce_split<1, SK>(y, red) || !live) return;
+  const int c = base + j;
+  if (c >= hidden) return;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = 4 * kq + r;
+    if (m >= M) continue;
+    const bool routed = slot_of[m] < top_k;
+    const float dv = round_bf16(y[0][r]);
+    const float sc = routed ? bf16_to_f32(scores[size_t(row_of[m]) * top_k + slot_of[m]]) : 1.0f;
+    p[(size_t(row_of[m]) * (top_k + 1) + slot_of[m]) * hidden + c] = f32_to_bf16(routed ? dv * sc : dv);
+  }
+}
+
+}  // namespace
+
+bool qmm_supported(const QWeight& w) {
+  return w.group_size == 64 && w.k % 64 == 0 && (w.k >> 6) <= kMaxGroups &&
+         (w.bits == 4 || w.bits == 5 || w.bits == 6 || w.bits == 8);
+}
+
+int qmm(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const ProjEpilogue& e,
+        hipStream_t s) {
+  if (!qmm_supported(w) || m < 1 || m > 16) return MX_EUNSUPPORTED;
+  if (e.mode == kHcUpMix && e.hidden * 4 != w.n) return MX_EUNSUPPORTED;
+  switch (w.bits) {
+    case 4: dense_bits<4>(w, x, x_stride, m, e, s); break;
+    case 5: dense_bits<5>(w, x, x_stride, m, e, s); break;
+    case 6: dense_bits<6>(w, x, x_stride, m, e, s); break;
+    default: dense_bits<8>(w, x, x_stride, m, e, s); break;
+  }
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
+int qmm_gate_up(const uint16_t* x, const MoePlan* plan, int rows, int top_k, const QBank& gate,
+                const QBank& up, const QWeight& sgate, const QWeight& sup, uint16_t* h,
+                hipStream_t s) {
+  const int routes = rows * top_k + 1;
+  const int hs = gate.n > sgate.n ? gate.n : sgate.n;
+  const int SK = split_k(gate.k);
+  const int tiles = (hs + 15) / 16;
+  const dim3 grid((tiles + 4 / SK - 1) / (4 / SK), routes);
+#define MX_GU(B, K)                                                                          \
+  if (gate.bits == B && SK == K) {                                                           \
+    hipLaunchKernelGGL((expert_gate_up_kernel<B, K>), grid, dim3(256), 0, s, x, plan, top_k, \
+                       gate, up, sgate, sup, h, hs);                                         \
+    return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;                               \
+  }
+  MX_GU(4, 4) MX_GU(4, 2) MX_GU(4, 1) MX_GU(5, 4) MX_GU(5, 2) MX_GU(5, 1)
+  MX_GU(6, 4) MX_GU(6, 2) MX_GU(6, 1) MX_GU(8, 4) MX_GU(8, 2) MX_GU(8, 1)
+#undef MX_GU
+  return MX_EUNSUPPORTED;
+}
+
+int qmm_down(const uint16_t* h, const MoePlan* plan, const uint16_t* scores, int rows, int top_k,
+             int inter, int shared_inter, const QBank& down, const QWeight& sdown, uint16_t* p,
+             hipStream_t s) {
+  const int routes = rows * top_k + 1;
+  const int hs = inter > shared_inter ? inter : shared_inter;
+  // one split for both depths: the shallower one's waves cover fewer groups
+  const int kmin = down.k < sdown.k ? down.k : sdown.k;
+  const int SK = split_k(kmin);
+  const int tiles = (down.n + 15) / 16;
+  const dim3 grid((tiles + 4 / SK - 1) / (4 / SK), routes);
+#define MX_DN(B, K)                                                                         \
+  if (down.bits == B && SK == K) {                                                          \
+    hipLaunchKernelGGL((expert_down_kernel<B, K>), grid, dim3(256), 0, s, h, plan, scores,  \
+                       top_k, down, sdown, p, hs);                                          \
+    return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;                              \
+  }
+  MX_DN(4, 4) MX_DN(4, 2) MX_DN(4, 1) MX_DN(5, 4) MX_DN(5, 2) MX_DN(5, 1)
+  MX_DN(6, 4) MX_DN(6, 2) MX_DN(6, 1) MX_DN(8, 4) MX_DN(8, 2) MX_DN(8, 1)
+#undef MX_DN
+  return MX_EUNSUPPORTED;
+}
+
+}  // namespace mx

@@ -54,6 +54,23 @@ __global__ void eval_math_kernel(int op, const float* __restrict__ in, float* __
   }
 }
 
+// Zero-mean affine groups: b = bf16(-s * (2^bits - 1) / 2 + U(-noise, noise)),
+// so that the dequantised weights s*q + b of uniform codes centre on zero.
+__global__ void fill_bias_centered_kernel(uint16_t* __restrict__ b, const uint16_t* __restrict__ s,
+                                          size_t count, int bits, uint64_t seed, float noise) {
+  const float mid = float((1u << bits) - 1u) * 0.5f;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < count;
+       i += size_t(gridDim.x) * blockDim.x)
+    b[i] = f32_to_bf16(fmaf_(-bf16_to_f32(s[i]), mid, rng_uniform(seed, i, -noise, noise)));
+}
+
+__global__ void fill_f32_kernel(float* __restrict__ dst, size_t count, uint64_t seed, float a,
+                                float b) {
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < count;
+       i += size_t(gridDim.x) * blockDim.x)
+    dst[i] = rng_uniform(seed, i, a, b);
+}
+
 int grid_for(int64_t n) {
   const int64_t b = (n + 255) / 256;
   return int(b < 16384 ? (b > 0 ? b : 1) : 16384);
@@ -74,6 +91,21 @@ int fill_codes(uint32_t* dst, int64_t rows, int k, int bits, uint64_t seed, hipS
   if (words == 0) return MX_OK;
   hipLaunchKernelGGL(fill_codes_kernel, dim3(grid_for(words)), dim3(256), 0, s, dst, rows, k, bits,
                      seed);
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
+int fill_bias_centered(uint16_t* b, const uint16_t* scales, size_t count, int bits, uint64_t seed,
+                       float noise, hipStream_t s) {
+  if (count == 0) return MX_OK;
+  hipLaunchKernelGGL(fill_bias_centered_kernel, dim3(grid_for(int64_t(count))), dim3(256), 0, s, b,
+                     scales, count, bits, seed, noise);
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
+int fill_f32(float* dst, size_t count, uint64_t seed, float a, float b, hipStream_t s) {
+  if (count == 0) return MX_OK;
+  hipLaunchKernelGGL(fill_f32_kernel, dim3(grid_for(int64_t(count))), dim3(256), 0, s, dst, count,
+                     seed, a, b);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 

@@ -1,0 +1,61 @@
+"""Matrix-core (MFMA) projections: within the north star's tolerance of the
+float64 closed form and of the exact fixed-order kernels, for every code
+width, depth and row count the engine uses (including partial 16-row tiles)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def bf(h):
+    return (np.asarray(h, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+@pytest.mark.parametrize("bits", [4, 5, 6, 8])
+@pytest.mark.parametrize("k,n", [(256, 72), (512, 2048), (2048, 1000), (4096, 264), (8192, 260)])
+def test_qmm_against_closed_form_and_exact(mx, orc, bits, k, n):
+    gs = 64
+    seed = 7000 + bits * 100 + k // 64
+    w = mx.QWeight.random(n, k, bits, gs, seed)
+    codes, s, b = orc.random_qweight(n, k, bits, gs, seed)
+    for m in (1, 3, 8, 16):
+        x = orc.fill_bf16(m * k, seed + m, 1, 1.0, 0.0).reshape(m, k)
+        dx = mx.DeviceArray.from_numpy(x)
+        dy = mx.DeviceArray((m, n), np.uint16)
+        qc = w.c()
+        mx.check(mx.lib.mx_qmm(C.byref(qc), dx.ptr, m, dy.ptr, None))
+        got = bf(dy.numpy()).astype(np.float64)
+        y64 = orc.qmv_f64(codes, s, b, k, bits, gs, x)
+        mag = np.abs(bf(x)).astype(np.float64).sum(axis=1, keepdims=True) * 0.05
+        assert np.all(np.abs(got - y64) <= 2.0 ** -8 * np.abs(y64) + 2.0 ** -16 * mag + 1e-6), (m,)
+        if m <= 8:
+            ex = mx.DeviceArray((m, n), np.uint16)
+            mx.qmv(w, dx, m, ex)
+            e = bf(ex.numpy()).astype(np.float64)
+            # fp32 summation order only: at most a bf16 ulp or two apart
+            assert np.all(np.abs(got - e) <= 2.0 ** -7 * np.abs(e) + 2.0 ** -16 * mag + 1e-6)
+
+
+def test_moe_experts_mfma_within_tolerance(mx, orc):
+    from test_layers_gpu import Moe, dev
+
+    E, I, H, top_k, rows = 64, 512, 2048, 10, 8
+    m = Moe(mx, orc, E, I, H, seed=800)
+    rng = np.random.default_rng(8)
+    ids = np.stack([rng.choice(12, top_k, replace=False) for _ in range(rows)]).astype(np.uint32)
+    scores = orc.f32_to_bf16(rng.uniform(0.02, 0.3, (rows, top_k)).astype(np.float32))
+    x = orc.fill_bf16(rows * H, 801, 1, 1.0, 0.0).reshape(rows, H)
+    want = bf(m.oracle(orc, x, ids, scores, top_k)).astype(np.float64)
+    p = mx.DeviceArray((rows, top_k + 1, H), np.uint16)
+    qb = [b.c() for b in (m.gate, m.up, m.down)]
+    qs = [w.c() for w in (m.sg, m.su, m.sd)]
+    dx, di, ds = dev(mx, x), dev(mx, ids), dev(mx, scores)
+    mx.check(mx.lib.mx_moe_experts_mfma(dx.ptr, di.ptr, ds.ptr, rows, top_k, C.byref(qb[0]),
+                                        C.byref(qb[1]), C.byref(qb[2]), C.byref(qs[0]),
+                                        C.byref(qs[1]), C.byref(qs[2]), m.ws.ptr, p.ptr, None))
+    got = bf(p.numpy()).astype(np.float64)
+    scale = np.abs(want).max(axis=2, keepdims=True)
+    assert np.all(np.abs(got - want) <= 2e-2 * np.abs(want) + 1e-2 * scale)
+    assert np.mean(got == want) > 0.5  # mostly identical after bf16 rounding
