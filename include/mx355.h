@@ -164,8 +164,10 @@ mx_status mx_qmv(const mx_qweight* w, const uint16_t* x, int32_t m, uint16_t* y,
  * codes enter as exact bf16 integers, each 64-value group's fp32 partial is
  * scaled in registers.  Results equal mx_qmv's up to fp32 summation order
  * (the north star's tolerance, not bit for bit).  Requires group_size 64 and
- * k <= 8192.  The MFMA verify/prefill slot of the reference
- * (matrix_kernel::project, src/matrix_kernel.rs:113-254, kernels/matrix_packed.metal). */
+ * k <= 8192.  Deterministic: a workgroup splits k among its own waves and adds
+ * their sums in a fixed order.  The MFMA verify/prefill slot of the reference
+ * (matrix_kernel::project, src/matrix_kernel.rs:113-254,
+ * kernels/matrix_packed.metal). */
 mx_status mx_qmm(const mx_qweight* w, const uint16_t* x, int32_t m, uint16_t* y, void* stream);
 
 /* ---- A4: affine dequantisation of selected rows (embedding) --------------
@@ -245,6 +247,12 @@ mx_status mx_moe_reduce_hc_epilogue(const uint16_t* partial, const uint16_t* fac
 size_t mx_head_workspace_bytes(int32_t n, int32_t k, int32_t m);
 mx_status mx_head_argmax(const mx_qweight* w, const uint16_t* x, int32_t m, uint32_t* tokens,
                          void* workspace, void* stream);
+/* mx_head_argmax with the head projection on the matrix cores (fp32
+ * summation order differs from the exact kernel, so near-ties may resolve
+ * differently; the selection rule is the same).  Requires group_size 64,
+ * k % 512 == 0 and k <= 2048; same workspace size. */
+mx_status mx_head_argmax_mfma(const mx_qweight* w, const uint16_t* x, int32_t m,
+                              uint32_t* tokens, void* workspace, void* stream);
 /* argmax over bf16 logits [rows, n] with the same rule (MLX argmax_axis). */
 mx_status mx_argmax_bf16(const uint16_t* logits, int32_t rows, int32_t n, uint32_t* tokens,
                          void* stream);

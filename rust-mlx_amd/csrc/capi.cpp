@@ -303,6 +303,25 @@ MX_ABI mx_status mx_head_argmax(const mx_qweight* w, const uint16_t* x, int32_t 
                 "mx_head_argmax");
 }
 
+MX_ABI mx_status mx_head_argmax_mfma(const mx_qweight* w, const uint16_t* x, int32_t m,
+                                     uint32_t* tokens, void* workspace, void* stream) {
+  MX_CHECK(w && x && tokens && workspace, MX_EINVAL, "mx_head_argmax_mfma: null pointer");
+  const QWeight q = to_qweight(*w);
+  if (const char* err = check_qweight(q))
+    return mx_status(set_error(MX_EINVAL, std::string("mx_head_argmax_mfma: ") + err));
+  MX_CHECK(m >= 1 && m <= 8, MX_EUNSUPPORTED, "mx_head_argmax_mfma: m must be in 1..8");
+  MX_CHECK(skinny_supported(q) && q.k % 512 == 0 && q.k <= 2048, MX_EUNSUPPORTED,
+           "mx_head_argmax_mfma: needs group_size 64, k % 512 == 0 and k <= 2048");
+  const int parts = skinny_head_parts(q.n);
+  float* maxima = static_cast<float*>(workspace);
+  uint32_t* indices = reinterpret_cast<uint32_t*>(maxima + size_t(parts) * m);
+  int got = 0;
+  int rc = skinny_head(q, x, m, maxima, indices, &got, hipStream_t(stream));
+  if (rc != MX_OK) return finish(rc, "mx_head_argmax_mfma");
+  return finish(argmax_reduce(maxima, indices, m, parts, tokens, hipStream_t(stream)),
+                "mx_head_argmax_mfma");
+}
+
 MX_ABI mx_status mx_argmax_bf16(const uint16_t* logits, int32_t rows, int32_t n, uint32_t* tokens,
                                 void* stream) {
   MX_CHECK(rows >= 0 && n > 0, MX_EINVAL, "mx_argmax_bf16: bad shape");
@@ -563,6 +582,8 @@ MX_ABI mx_status mx_qmm(const mx_qweight* w, const uint16_t* x, int32_t m, uint1
   e.mode = kPlain;
   e.y = y;
   e.y_stride = q.n;
+  if (m <= 8 && skinny_supported(q))
+    return finish(skinny_dense(q, x, q.k, m, e, hipStream_t(stream)), "mx_qmm");
   return finish(qmm(q, x, q.k, m, e, hipStream_t(stream)), "mx_qmm");
 }
 
@@ -595,7 +616,11 @@ MX_ABI mx_status mx_moe_experts_mfma(const uint16_t* x, const uint32_t* ids, con
   const size_t hb = size_t(rows) * (top_k + 1) * inter * sizeof(uint16_t);
   MoePlan* plan = reinterpret_cast<MoePlan*>(static_cast<char*>(workspace) + ((hb + 255) / 256) * 256);
   hipStream_t s = hipStream_t(stream);
-  int rc = moe_plan(ids, rows, top_k, plan, s);
+  int rc = skinny_gate_up(x, ids, rows, top_k, g, u, sg, su, h, s);
+  if (rc == MX_OK) rc = skinny_down(h, ids, scores, rows, top_k, g.n, sg.n, d, sd, partial, s);
+  if (rc != MX_EUNSUPPORTED) return finish(rc, "mx_moe_experts_mfma");
+  // depths the skinny kernels do not cover: the 16-row-tile kernels with a plan
+  rc = moe_plan(ids, rows, top_k, plan, s);
   if (rc == MX_OK) rc = qmm_gate_up(x, plan, rows, top_k, g, u, sg, su, h, s);
   if (rc == MX_OK) rc = qmm_down(h, plan, scores, rows, top_k, g.n, sg.n, d, sd, partial, s);
   return finish(rc, "mx_moe_experts_mfma");

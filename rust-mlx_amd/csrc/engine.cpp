@@ -17,6 +17,7 @@
 //    replayed; only the small per-step row table is copied in before launch.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <map>
@@ -398,15 +399,15 @@ bool experts_fast(const Engine& e, const LayerW& L) {
                   L.gate.group_size};
   const QWeight d{L.down.codes, L.down.scales, L.down.biases, L.down.n, L.down.k, L.down.bits,
                   L.down.group_size};
-  return !e.exact && qmm_supported(g) && qmm_supported(d) && qmm_supported(L.sgate) &&
-         qmm_supported(L.sdown);
+  return !e.exact && skinny_supported(g) && skinny_supported(d) && skinny_supported(L.sgate) &&
+         skinny_supported(L.sdown);
 }
 
 int experts_gate_up(Engine& e, const LayerW& L, int rows) {
   const auto& c = e.cfg;
   if (experts_fast(e, L))
-    return qmm_gate_up(e.mixed, e.moe_plan_buf, rows, c.top_k, L.gate, L.up, L.sgate, L.sup,
-                       e.moe_h, e.stream);
+    return skinny_gate_up(e.mixed, e.ids, rows, c.top_k, L.gate, L.up, L.sgate, L.sup, e.moe_h,
+                          e.stream);
   return moe_gate_up(e.mixed, e.moe_plan_buf, rows, c.top_k, L.gate, L.up, L.sgate, L.sup,
                      e.moe_h, e.stream);
 }
@@ -414,8 +415,8 @@ int experts_gate_up(Engine& e, const LayerW& L, int rows) {
 int experts_down(Engine& e, const LayerW& L, int rows) {
   const auto& c = e.cfg;
   if (experts_fast(e, L))
-    return qmm_down(e.moe_h, e.moe_plan_buf, e.scores, rows, c.top_k, L.gate.n, L.sgate.n, L.down,
-                    L.sdown, e.moe_p, e.stream);
+    return skinny_down(e.moe_h, e.ids, e.scores, rows, c.top_k, L.gate.n, L.sgate.n, L.down,
+                       L.sdown, e.moe_p, e.stream);
   return moe_down(e.moe_h, e.moe_plan_buf, e.scores, rows, c.top_k, L.gate.n, L.sgate.n, L.down,
                   L.sdown, e.moe_p, e.stream);
 }
@@ -434,7 +435,7 @@ int profile_experts(Engine& e, const LayerW& L, int rows) {
       seen[v] = 1;
       ++distinct;
     }
-  MX_TRY(moe_plan(e.ids, rows, c.top_k, e.moe_plan_buf, e.stream));
+  if (!experts_fast(e, L)) MX_TRY(moe_plan(e.ids, rows, c.top_k, e.moe_plan_buf, e.stream));
   MX_HIP(hipEventRecord(e.ev[0], e.stream));
   MX_TRY(experts_gate_up(e, L, rows));
   MX_HIP(hipEventRecord(e.ev[1], e.stream));
@@ -462,6 +463,8 @@ int profile_experts(Engine& e, const LayerW& L, int rows) {
 // Projection on the matrix cores (fast mode) or the exact kernels.
 int project(Engine& e, const QWeight& w, const uint16_t* x, int64_t xs, int rows,
             const ProjEpilogue& ep) {
+  if (!e.exact && rows <= 8 && skinny_supported(w))
+    return skinny_dense(w, x, xs, rows, ep, e.stream);
   if (!e.exact && qmm_supported(w)) return qmm(w, x, xs, rows, ep, e.stream);
   return proj(w, x, xs, rows, ep, e.stream);
 }
@@ -557,7 +560,7 @@ int record_step(Engine& e, int rows, int groups, int t, bool history, bool logit
     if (e.prof) {
       MX_TRY(profile_experts(e, L, rows));
     } else {
-      MX_TRY(moe_plan(e.ids, rows, c.top_k, e.moe_plan_buf, e.stream));
+      if (!experts_fast(e, L)) MX_TRY(moe_plan(e.ids, rows, c.top_k, e.moe_plan_buf, e.stream));
       MX_TRY(experts_gate_up(e, L, rows));
       MX_TRY(experts_down(e, L, rows));
     }
@@ -569,7 +572,10 @@ int record_step(Engine& e, int rows, int groups, int t, bool history, bool logit
   int parts = 0;
   float* maxima = static_cast<float*>(e.head_ws);
   uint32_t* indices = reinterpret_cast<uint32_t*>(maxima + size_t(head_parts(c.vocab, c.hidden)) * 8);
-  MX_TRY(head_partials(e.head, e.mixed, rows, maxima, indices, &parts, e.stream));
+  if (!e.exact && skinny_supported(e.head) && e.head.k % 512 == 0 && e.head.k <= 2048)
+    MX_TRY(skinny_head(e.head, e.mixed, rows, maxima, indices, &parts, e.stream));
+  else
+    MX_TRY(head_partials(e.head, e.mixed, rows, maxima, indices, &parts, e.stream));
   MX_TRY(argmax_reduce(maxima, indices, rows, parts, rt->next, e.stream));
   if (logits) {
     ProjEpilogue pl{};

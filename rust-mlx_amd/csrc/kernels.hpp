@@ -61,6 +61,19 @@ int proj(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const Pro
 bool qmm_supported(const QWeight& w);
 int qmm(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const ProjEpilogue& e,
         hipStream_t s);
+// matrix-core skinny projections for 1..8 rows (skinny.hip)
+bool skinny_supported(const QWeight& w);
+int skinny_dense(const QWeight& w, const uint16_t* x, int64_t x_stride, int m,
+                 const ProjEpilogue& e, hipStream_t s);
+int skinny_gate_up(const uint16_t* x, const uint32_t* ids, int rows, int top_k,
+                   const QBank& gate, const QBank& up, const QWeight& sgate, const QWeight& sup,
+                   uint16_t* h, hipStream_t s);
+int skinny_down(const uint16_t* h, const uint32_t* ids, const uint16_t* scores, int rows,
+                int top_k, int inter, int shared_inter, const QBank& down, const QWeight& sdown,
+                uint16_t* p, hipStream_t s);
+int skinny_head_parts(int n);
+int skinny_head(const QWeight& w, const uint16_t* x, int m, float* maxima, uint32_t* indices,
+                int* parts_out, hipStream_t s);
 int hc_norm(const uint16_t* x, const uint16_t* scale, int rows, int hc, int hidden, float eps,
             uint16_t* y, hipStream_t s);
 int embed(const QWeight& w, const uint32_t* ids, int count, int hc, uint16_t* out, hipStream_t s);

@@ -1,0 +1,546 @@
+// Decode projections on the gfx950 matrix cores for 1..8 activation rows
+// (the arithmetic of skinny_core.hpp): dense projections with the engine's
+// fused epilogues, the gathered expert gate/up (+SwiGLU) and down (+route
+// score), and the greedy vocabulary head (argmax partials).
+//
+// Replaces the same reference interfaces as the exact kernels: the QMV /
+// gather_qmm rows of Linear::forward_rows (src/weights.rs:111-202,
+// src/qmv_kernel.rs:49-180), the expert gather_qmm of MoE::parts
+// (src/hybrid.rs:245-271, moe_kernel::gate_up src/moe_kernel.rs:10-118,
+// moe_down::reduce src/moe_down.rs:34-137) and greedy_head::project
+// (src/greedy_head.rs:40-126).  Results agree with the exact kernels up to
+// fp32 summation order, not bit for bit.
+//
+// A workgroup holds T tiles of 16 weight rows and splits K among KS waves per
+// tile (T * KS <= 16 waves); the KS partial sums of a tile are added in slice
+// order through LDS, so results are deterministic and no workgroup waits on
+// another.  Matrices with few rows use many slices to fill the chip.  For
+// K <= 2048 the activation rows are staged once per workgroup in LDS; deeper
+// rows are read by each wave straight into registers (group sums of x are
+// always staged).  Every wave issues its first weight loads before the
+// staging, so the two latencies overlap.
+#include "common.hpp"
+#include "kernels.hpp"
+#include "skinny_core.hpp"
+
+namespace mx {
+
+namespace {
+
+using sk::floatx4_t;
+
+__device__ __forceinline__ float sigmoid_bf16(float x) {
+  const float e = round_bf16(expf_(__builtin_fabsf(x)));
+  const float d = round_bf16(1.0f + e);
+  const float y = round_bf16(1.0f / d);
+  return x < 0.0f ? y : round_bf16(1.0f - y);
+}
+
+// Largest K staged in LDS (super-steps); deeper rows stream x into registers,
+// up to kDenseSteps.  Expert down rows are at most kDownSteps deep.
+constexpr int kStageSteps = 16;
+constexpr int kDenseSteps = 64;
+constexpr int kDownSteps = 8;
+
+// Sums the KS slices of each tile into yt[m][t * 16 + j] (fp32 [8][16 T]).
+// red: LDS [KS][T][8][16] (unused when KS == 1).  Ends with a barrier.
+template <int T, int KS>
+__device__ __forceinline__ void reduce_tiles(float (&y)[4], float* red, float* yt) {
+  sk::join_parities(y);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 15, q = lane >> 4;
+  const int t = wave / KS, ks = wave - t * KS;
+  constexpr int NC = 16 * T;
+  if constexpr (KS == 1) {
+    if (q < 2) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) yt[(4 * q + r) * NC + t * 16 + j] = y[r];
+    }
+    __syncthreads();
+  } else {
+    if (q < 2) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[((ks * T + t) * 8 + 4 * q + r) * 16 + j] = y[r];
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < 8 * NC; i += 64 * T * KS) {
+      const int m = i / NC, c = i - m * NC;
+      const int tt = c >> 4, jj = c & 15;
+      float sum = 0.0f;
+#pragma unroll
+      for (int k = 0; k < KS; ++k) sum = sum + red[((k * T + tt) * 8 + m) * 16 + jj];
+      yt[i] = sum;
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Dense projections (modes of ProjEpilogue).  Workgroup tg covers rows
+// tg*16T .. tg*16T + 16T - 1 (tile t: rows tg*16T + 16t + j); for kHcUpMix
+// (T = 4) it covers columns tg*16 .. tg*16 + 15 of the four streams (tile t:
+// rows t*H + tg*16 + j).
+template <int BITS, int MODE, int T, int KS, bool XREG, int SCW>
+__global__ __launch_bounds__(64 * T * KS) void dense_kernel(QWeight w,
+                                                            const uint16_t* __restrict__ x,
+                                                            int64_t x_stride, int M,
+                                                            ProjEpilogue e) {
+  extern __shared__ __align__(16) char lds[];
+  __shared__ float red[KS > 1 ? KS * T * 8 * 16 : 1];
+  __shared__ float yt[8 * 16 * T];
+  constexpr int NC = 16 * T;
+  const int tg = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane & 15;
+  const int t = wave / KS, ks = wave - t * KS;
+  const int total = w.k / sk::kSuper;
+  const int k0 = total * ks / KS, steps = total * (ks + 1) / KS - k0;
+  const int n = w.n;
+  int row;
+  if constexpr (MODE == kHcUpMix)
+    row = t * e.hidden + min(tg * 16 + j, e.hidden - 1);
+  else
+    row = min(tg * NC + t * 16 + j, n - 1);
+  const int G = w.k >> 6;
+  const sk::DenseRows xr{x, x_stride, M};
+  constexpr int NT = 64 * T * KS;
+  // slices of a staged tile hold kStageSteps / KS super-steps at most
+  constexpr int BMAX = XREG ? 1 : (kStageSteps / KS > 1 ? kStageSteps / KS : 1);
+  const int xbytes = XREG ? 0 : total * sk::kStepBytes;
+  const float* sx = reinterpret_cast<const float*>(lds + xbytes + sk::kZeroBytes);
+  sk::Stream<BITS, XREG, sk::DenseRows, BMAX, SCW> st(
+      w.codes + size_t(row) * (size_t(w.k) * BITS / 32), w.scales + size_t(row) * G,
+      w.biases + size_t(row) * G, total, k0, steps, 0, lds, sx, xr, M);
+  float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (XREG) {
+    st.prefetch();
+    st.run(0, y);
+  } else {
+    sk::Stager<NT, sk::stage_per(NT, kStageSteps), sk::DenseRows> stg(xr, M, 0, total);
+    stg.load();
+    st.prefetch();
+    stg.store(lds);
+    st.run(xbytes, y);
+  }
+  reduce_tiles<T, KS>(y, red, yt);
+
+  if constexpr (MODE == kHcUpMix) {
+    // 8 rows x 16 columns; each output mixes the four streams of its column
+    if (threadIdx.x >= 128) return;
+    const int m = threadIdx.x >> 4, cj = threadIdx.x & 15;
+    const int c = tg * 16 + cj;
+    if (m >= M || c >= e.hidden) return;
+    float sum = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const float p = round_bf16(yt[m * NC + s * 16 + cj]);
+      const float xn = bf16_to_f32(e.xn[size_t(m) * e.xn_stride + size_t(s) * e.hidden + c]);
+      sum = sum + round_bf16(sigmoid_bf16(p) * xn);
+    }
+    e.y[size_t(m) * e.y_stride + c] = f32_to_bf16(round_bf16(sum) / 4.0f);
+  } else {
+    for (int i = threadIdx.x; i < 8 * NC; i += 64 * T * KS) {
+      const int m = i / NC, c = i - m * NC;
+      const int r = tg * NC + c;
+      if (m >= M || r >= n) continue;
+      const float v = yt[i];
+      if constexpr (MODE == kPlain) {
+        e.y[size_t(m) * e.y_stride + r] = f32_to_bf16(v);
+      } else if constexpr (MODE == kHcDown) {
+        const float tt = round_bf16(round_bf16(v) / float(e.hc));
+        if (r < e.rank)
+          e.y[size_t(m) * e.y_stride + r] = f32_to_bf16(tt * sigmoid_bf16(tt));
+        else
+          e.aux[size_t(m) * e.aux_stride + (r - e.rank)] = f32_to_bf16(sigmoid_bf16(tt) * 2.0f);
+      } else {  // kHcWrite
+        const float vb = round_bf16(v);
+        for (int s = 0; s < e.hc; ++s) {
+          uint16_t* res = e.y + size_t(m) * e.y_stride + size_t(s) * n + r;
+          const float inj = round_bf16(vb * bf16_to_f32(e.aux[size_t(m) * e.aux_stride + s]));
+          *res = f32_to_bf16(bf16_to_f32(*res) + inj);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Expert routes.  Route r (blockIdx.y < rows*top_k) leads a chunk when the
+// number of earlier routes naming its expert is a multiple of 8; the leader
+// serves itself and the next up to seven routes of that expert, so every
+// selected expert's weights stream once per call (one chunk per distinct
+// expert when rows <= 8).  blockIdx.y == rows*top_k is the shared expert,
+// serving every row.  Expert ids are clamped to the bank.
+struct Routes {
+  int expert;       // -1: shared expert
+  int M;
+  uint64_t packed;  // member m: (row << 5 | slot) at bit 8 m
+};
+
+__device__ __forceinline__ bool resolve_routes(const uint32_t* __restrict__ ids, int rows,
+                                               int top_k, int experts, Routes& rt) {
+  const int routes = rows * top_k;
+  const int r = blockIdx.y;
+  if (r == routes) {
+    rt.expert = -1;
+    rt.M = rows;
+    rt.packed = 0;
+    for (int m = 0; m < rows; ++m) rt.packed |= uint64_t((m << 5) | top_k) << (8 * m);
+    return true;
+  }
+  const uint32_t last = uint32_t(experts - 1);
+  const int lane = threadIdx.x & 63;
+  // unconditional loads at clamped indices (one round trip for all three)
+  const uint32_t raw0 = ids[min(lane, routes - 1)];
+  const uint32_t raw1 = ids[min(64 + lane, routes - 1)];
+  const uint32_t e = min(ids[r], last);
+  const uint32_t id0 = lane < routes ? min(raw0, last) : 0xffffffffu;
+  const uint32_t id1 = 64 + lane < routes ? min(raw1, last) : 0xffffffffu;
+  uint64_t eq0 = __ballot(id0 == e);
+  uint64_t eq1 = __ballot(id1 == e);
+  const int before = r < 64 ? __popcll(eq0 & ((1ull << r) - 1ull))
+                            : __popcll(eq0) + __popcll(eq1 & ((1ull << (r - 64)) - 1ull));
+  if (before % 8 != 0) return false;
+  // members: the first 8 routes u >= r naming e
+  if (r < 64) {
+    eq0 &= ~((1ull << r) - 1ull);
+  } else {
+    eq0 = 0;
+    eq1 &= ~((1ull << (r - 64)) - 1ull);
+  }
+  rt.expert = int(e);
+  rt.M = 0;
+  rt.packed = 0;
+  while (rt.M < 8 && (eq0 | eq1)) {
+    int u;
+    if (eq0) {
+      u = __builtin_ctzll(eq0);
+      eq0 &= eq0 - 1;
+    } else {
+      u = 64 + __builtin_ctzll(eq1);
+      eq1 &= eq1 - 1;
+    }
+    const int row = u / top_k;
+    rt.packed |= uint64_t((row << 5) | (u - row * top_k)) << (8 * rt.M);
+    rt.M += 1;
+  }
+  return true;
+}
+
+__device__ __forceinline__ QWeight expert_weight(const QBank& b, int expert, const QWeight& shared) {
+  if (expert < 0) return shared;
+  const size_t cs = size_t(b.n) * b.k * b.bits / 32;
+  const size_t ss = size_t(b.n) * (b.k / b.group_size);
+  return QWeight{b.codes + cs * expert, b.scales + ss * expert, b.biases + ss * expert, b.n, b.k,
+                 b.bits, b.group_size};
+}
+
+// gate/up + SwiGLU: waves 0,1 = gate rows tg*32 + 16w + j, waves 2,3 = up rows
+// of the same indices.  h[row][slot][i] = bf16(bf16(silu(bf16 g)) * bf16 u).
+template <int BITS>
+__global__ __launch_bounds__(256) void gate_up_kernel(const uint16_t* __restrict__ x,
+                                                      const uint32_t* __restrict__ ids, int rows,
+                                                      int top_k, QBank gate, QBank up,
+                                                      QWeight sgate, QWeight sup,
+                                                      uint16_t* __restrict__ h, int hs) {
+  extern __shared__ __align__(16) char lds[];
+  __shared__ float yt[8 * 64];
+  Routes rt;
+  if (!resolve_routes(ids, rows, top_k, gate.experts, rt)) return;
+  const QWeight gw = expert_weight(gate, rt.expert, sgate);
+  const QWeight uw = expert_weight(up, rt.expert, sup);
+  const int inter = gw.n, hidden = gw.k;
+  const int tg = blockIdx.x;
+  if (tg * 32 >= inter) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane & 15;
+  const bool is_gate = wave < 2;
+  const uint32_t* codes = is_gate ? gw.codes : uw.codes;
+  const uint16_t* scales = is_gate ? gw.scales : uw.scales;
+  const uint16_t* biases = is_gate ? gw.biases : uw.biases;
+  const int row = min(tg * 32 + (wave & 1) * 16 + j, inter - 1);
+  const int G = hidden >> 6;
+  const int steps = hidden / sk::kSuper;
+  const sk::RouteRows xr{x, hidden, 0, rt.packed, rt.M};
+  const int xbytes = steps * sk::kStepBytes;
+  const float* sx = reinterpret_cast<const float*>(lds + xbytes + sk::kZeroBytes);
+  sk::Stream<BITS, false, sk::RouteRows> st(codes + size_t(row) * (size_t(hidden) * BITS / 32),
+                                            scales + size_t(row) * G, biases + size_t(row) * G,
+                                            steps, 0, steps, 0, lds, sx, xr, rt.M);
+  sk::Stager<256, sk::stage_per(256, kStageSteps), sk::RouteRows> stg(xr, rt.M, 0, steps);
+  stg.load();
+  st.prefetch();
+  stg.store(lds);
+  float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  st.run(xbytes, y);
+  reduce_tiles<4, 1>(y, nullptr, yt);
+  const int m = threadIdx.x >> 5, c = threadIdx.x & 31;
+  const int i = tg * 32 + c;
+  if (m >= rt.M || i >= inter) return;
+  const float gv = round_bf16(yt[m * 64 + c]);
+  const float uv = round_bf16(yt[m * 64 + 32 + c]);
+  const float silu = round_bf16(gv * sigmoid_bf16(gv));
+  h[(size_t(xr.row(m)) * (top_k + 1) + xr.slot(m)) * hs + i] = f32_to_bf16(silu * uv);
+}
+
+// down + score: p[row][slot][n] = bf16(bf16(down) * score) (routed slots) or
+// bf16(down) (the shared slot, top_k).
+template <int BITS>
+__global__ __launch_bounds__(256) void down_kernel(const uint16_t* __restrict__ h,
+                                                   const uint32_t* __restrict__ ids,
+                                                   const uint16_t* __restrict__ scores, int rows,
+                                                   int top_k, QBank down, QWeight sdown,
+                                                   uint16_t* __restrict__ p, int hs) {
+  extern __shared__ __align__(16) char lds[];
+  __shared__ float yt[8 * 64];
+  Routes rt;
+  if (!resolve_routes(ids, rows, top_k, down.experts, rt)) return;
+  const QWeight dw = expert_weight(down, rt.expert, sdown);
+  const int hidden = dw.n, inter = dw.k;
+  const int tg = blockIdx.x;
+  if (tg * 64 >= hidden) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane & 15;
+  const int row = min(tg * 64 + wave * 16 + j, hidden - 1);
+  const int G = inter >> 6;
+  const int steps = inter / sk::kSuper;
+  const sk::RouteRows xr{h, int64_t(top_k + 1) * hs, hs, rt.packed, rt.M};
+  const int xbytes = steps * sk::kStepBytes;
+  const float* sx = reinterpret_cast<const float*>(lds + xbytes + sk::kZeroBytes);
+  sk::Stream<BITS, false, sk::RouteRows, kDownSteps / 2, 8> st(
+      dw.codes + size_t(row) * (size_t(inter) * BITS / 32), dw.scales + size_t(row) * G,
+      dw.biases + size_t(row) * G, steps, 0, steps, 0, lds, sx, xr, rt.M);
+  sk::Stager<256, sk::stage_per(256, kDownSteps), sk::RouteRows> stg(xr, rt.M, 0, steps);
+  stg.load();
+  st.prefetch();
+  stg.store(lds);
+  float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  st.run(xbytes, y);
+  reduce_tiles<4, 1>(y, nullptr, yt);
+  for (int t = threadIdx.x; t < 512; t += 256) {
+    const int m = t >> 6, c = t & 63;
+    const int r = tg * 64 + c;
+    if (m >= rt.M || r >= hidden) continue;
+    const int row_m = xr.row(m), slot_m = xr.slot(m);
+    const bool routed = slot_m < top_k;
+    const float dv = round_bf16(yt[t]);
+    const float sc = routed ? bf16_to_f32(scores[size_t(row_m) * top_k + slot_m]) : 1.0f;
+    p[(size_t(row_m) * (top_k + 1) + slot_m) * hidden + r] = f32_to_bf16(routed ? dv * sc : dv);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Greedy head: per activation row, the best (bf16(logit), lowest id) of the
+// workgroup's 64 rows.  NaN never wins; a part with nothing above -inf keeps
+// id 0xffffffff and -inf.
+__device__ __forceinline__ void better(float v, uint32_t id, float& best, uint32_t& best_id) {
+  if (v > best || (v == best && id < best_id)) {
+    best = v;
+    best_id = id;
+  }
+}
+
+template <int BITS>
+__global__ __launch_bounds__(256) void head_kernel(QWeight w, const uint16_t* __restrict__ x,
+                                                   int M, float* __restrict__ maxima,
+                                                   uint32_t* __restrict__ indices) {
+  extern __shared__ __align__(16) char lds[];
+  __shared__ float yt[8 * 64];
+  const int tg = blockIdx.x, parts = gridDim.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane & 15;
+  const int n = w.n, G = w.k >> 6;
+  const int row = min(tg * 64 + wave * 16 + j, n - 1);
+  const int steps = w.k / sk::kSuper;
+  const sk::DenseRows xr{x, w.k, M};
+  const int xbytes = steps * sk::kStepBytes;
+  const float* sx = reinterpret_cast<const float*>(lds + xbytes + sk::kZeroBytes);
+  sk::Stream<BITS, false, sk::DenseRows> st(w.codes + size_t(row) * (size_t(w.k) * BITS / 32),
+                                            w.scales + size_t(row) * G, w.biases + size_t(row) * G,
+                                            steps, 0, steps, 0, lds, sx, xr, M);
+  sk::Stager<256, sk::stage_per(256, kStageSteps), sk::DenseRows> stg(xr, M, 0, steps);
+  stg.load();
+  st.prefetch();
+  stg.store(lds);
+  float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  st.run(xbytes, y);
+  reduce_tiles<4, 1>(y, nullptr, yt);
+  for (int m = wave; m < M; m += 4) {
+    const int r = tg * 64 + lane;
+    float best = u2f(0xff800000u);
+    uint32_t best_id = 0xffffffffu;
+    if (r < n) better(round_bf16(yt[m * 64 + lane]), uint32_t(r), best, best_id);
+    for (int o = 32; o > 0; o >>= 1) {
+      const float v = __shfl_xor(best, o, 64);
+      const uint32_t id = uint32_t(__shfl_xor(int(best_id), o, 64));
+      better(v, id, best, best_id);
+    }
+    if (lane == 0) {
+      maxima[size_t(m) * parts + tg] = best;
+      indices[size_t(m) * parts + tg] = best_id;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Launch geometry of a dense projection: KS = the smallest power of two that
+// gives >= 3072 waves, with >= 1 super-step per slice and at most 16 waves
+// per workgroup; T = 4 tiles when the split allows it (always 4 streams for
+// kHcUpMix).
+struct DenseCfg {
+  int T, KS;
+  bool xreg;
+  int scw;  // scale-load width (16 when a row's scales are 16-byte aligned)
+};
+
+// Whether every slice of `total` super-steps split KS ways keeps its scale
+// words within one load per lane quarter (Stream's coverage rule).
+bool scale_cover(int total, int KS, int scw) {
+  const int sq = scw / 4;
+  for (int ks = 0; ks < KS; ++ks) {
+    const int k0 = total * ks / KS, steps = total * (ks + 1) / KS - k0;
+    if (k0 % sq + steps > 4 * sq) return false;
+  }
+  return true;
+}
+
+DenseCfg dense_cfg(const QWeight& w, const ProjEpilogue& e) {
+  const int total = w.k / sk::kSuper;
+  const bool mix = e.mode == kHcUpMix;
+  const int tiles = mix ? 4 * ((e.hidden + 15) / 16) : (w.n + 15) / 16;
+  const int max_ks = mix ? 4 : 16;
+  // deeper splits measured faster down to one super-step per slice while the
+  // launch has under ~3000 waves
+  const int scw = (w.k % 512 == 0) ? 16 : 8;
+  int KS = 1;
+  // rows with 8-byte scale loads (K % 512 != 0) are at most a few super-steps
+  // deep and run unsplit
+  while (scw == 16 && KS < max_ks && tiles * KS < 3072 && total / (2 * KS) >= 1) KS *= 2;
+  while (KS < max_ks && !scale_cover(total, KS, scw)) KS *= 2;
+  const int T = mix ? 4 : (KS <= 4 ? 4 : 16 / KS);
+  return DenseCfg{T, KS, total > kStageSteps, scw};
+}
+
+template <int BITS, int MODE, int T, int KS, bool XREG, int SCW>
+void launch_dense(const QWeight& w, const uint16_t* x, int64_t xs, int m, const ProjEpilogue& e,
+                  hipStream_t s) {
+  const int groups = MODE == kHcUpMix ? (e.hidden + 15) / 16 : (w.n + 16 * T - 1) / (16 * T);
+  const int total = w.k / sk::kSuper;
+  hipLaunchKernelGGL((dense_kernel<BITS, MODE, T, KS, XREG, SCW>), dim3(groups),
+                     dim3(64 * T * KS), XREG ? 0 : sk::stage_bytes(total), s, w, x, xs, m, e);
+}
+
+template <int BITS, int MODE>
+int dense_shape(const QWeight& w, const uint16_t* x, int64_t xs, int m, const ProjEpilogue& e,
+                hipStream_t s) {
+  const DenseCfg c = dense_cfg(w, e);
+  if (!scale_cover(w.k / sk::kSuper, c.KS, c.scw)) return MX_EUNSUPPORTED;
+#define MX_SHAPE(T_, KS_, X_, W_)                                             \
+  if (c.T == T_ && c.KS == KS_ && c.xreg == X_ && c.scw == W_) {             \
+    launch_dense<BITS, MODE, T_, KS_, X_, W_>(w, x, xs, m, e, s);            \
+    return MX_OK;                                                            \
+  }
+  MX_SHAPE(4, 1, false, 16) MX_SHAPE(4, 2, false, 16) MX_SHAPE(4, 4, false, 16)
+  MX_SHAPE(4, 1, false, 8)
+  MX_SHAPE(4, 2, true, 16) MX_SHAPE(4, 4, true, 16)
+  if constexpr (MODE != kHcUpMix) {
+    MX_SHAPE(2, 8, false, 16) MX_SHAPE(1, 16, false, 16) MX_SHAPE(2, 8, true, 16)
+    MX_SHAPE(1, 16, true, 16)
+  }
+#undef MX_SHAPE
+  return MX_EUNSUPPORTED;
+}
+
+template <int BITS>
+int dense_mode(const QWeight& w, const uint16_t* x, int64_t xs, int m, const ProjEpilogue& e,
+               hipStream_t s) {
+  switch (e.mode) {
+    case kPlain: return dense_shape<BITS, kPlain>(w, x, xs, m, e, s);
+    case kHcDown: return dense_shape<BITS, kHcDown>(w, x, xs, m, e, s);
+    case kHcUpMix: return dense_shape<BITS, kHcUpMix>(w, x, xs, m, e, s);
+    default: return dense_shape<BITS, kHcWrite>(w, x, xs, m, e, s);
+  }
+}
+
+}  // namespace
+
+// Scale rows must start 16-byte aligned for 16-byte scale loads
+// (K % 512 == 0); rows up to 1024 deep may use 8-byte loads (K % 256 == 0).
+bool skinny_supported(const QWeight& w) {
+  return w.group_size == 64 && (w.k % 512 == 0 || (w.k % 256 == 0 && w.k <= 1024)) &&
+         w.k / sk::kSuper <= kDenseSteps &&
+         (w.bits == 4 || w.bits == 5 || w.bits == 6 || w.bits == 8);
+}
+
+int skinny_dense(const QWeight& w, const uint16_t* x, int64_t x_stride, int m,
+                 const ProjEpilogue& e, hipStream_t s) {
+  if (!skinny_supported(w) || m < 1 || m > 8) return MX_EUNSUPPORTED;
+  if (e.mode == kHcUpMix && e.hidden * 4 != w.n) return MX_EUNSUPPORTED;
+  int rc;
+  switch (w.bits) {
+    case 4: rc = dense_mode<4>(w, x, x_stride, m, e, s); break;
+    case 5: rc = dense_mode<5>(w, x, x_stride, m, e, s); break;
+    case 6: rc = dense_mode<6>(w, x, x_stride, m, e, s); break;
+    default: rc = dense_mode<8>(w, x, x_stride, m, e, s); break;
+  }
+  if (rc != MX_OK) return rc;
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
+int skinny_gate_up(const uint16_t* x, const uint32_t* ids, int rows, int top_k,
+                   const QBank& gate, const QBank& up, const QWeight& sgate, const QWeight& sup,
+                   uint16_t* h, hipStream_t s) {
+  const int hs = gate.n > sgate.n ? gate.n : sgate.n;
+  const int steps = gate.k / sk::kSuper;
+  if (rows < 1 || rows > 8 || top_k < 1 || top_k > 16 || gate.group_size != 64 ||
+      gate.k % 512 != 0 || steps > kStageSteps || up.bits != gate.bits ||
+      sgate.bits != gate.bits || sup.bits != gate.bits || sgate.k != gate.k)
+    return MX_EUNSUPPORTED;
+  const dim3 grid((hs + 31) / 32, rows * top_k + 1);
+  const int lb = sk::stage_bytes(steps);
+#define MX_GU(B) \
+  case B: hipLaunchKernelGGL(gate_up_kernel<B>, grid, dim3(256), lb, s, x, ids, rows, top_k, gate, up, sgate, sup, h, hs); break;
+  switch (gate.bits) {
+    MX_GU(4) MX_GU(5) MX_GU(6) MX_GU(8)
+    default: return MX_EUNSUPPORTED;
+  }
+#undef MX_GU
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
+int skinny_down(const uint16_t* h, const uint32_t* ids, const uint16_t* scores, int rows,
+                int top_k, int inter, int shared_inter, const QBank& down, const QWeight& sdown,
+                uint16_t* p, hipStream_t s) {
+  const int hs = inter > shared_inter ? inter : shared_inter;
+  const int kmax = down.k > sdown.k ? down.k : sdown.k;
+  if (rows < 1 || rows > 8 || top_k < 1 || top_k > 16 || down.group_size != 64 ||
+      down.k % 256 != 0 || sdown.k % 256 != 0 || kmax / sk::kSuper > kDownSteps ||
+      sdown.bits != down.bits || sdown.n != down.n)
+    return MX_EUNSUPPORTED;
+  const dim3 grid((down.n + 63) / 64, rows * top_k + 1);
+  const int lb = sk::stage_bytes(kmax / sk::kSuper);
+#define MX_DN(B) \
+  case B: hipLaunchKernelGGL(down_kernel<B>, grid, dim3(256), lb, s, h, ids, scores, rows, top_k, down, sdown, p, hs); break;
+  switch (down.bits) {
+    MX_DN(4) MX_DN(5) MX_DN(6) MX_DN(8)
+    default: return MX_EUNSUPPORTED;
+  }
+#undef MX_DN
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
+int skinny_head_parts(int n) { return (n + 63) / 64; }
+
+int skinny_head(const QWeight& w, const uint16_t* x, int m, float* maxima, uint32_t* indices,
+                int* parts_out, hipStream_t s) {
+  if (!skinny_supported(w) || m < 1 || m > 8 || w.k % 512 != 0 || w.k / sk::kSuper > kStageSteps)
+    return MX_EUNSUPPORTED;
+  const int parts = skinny_head_parts(w.n);
+  *parts_out = parts;
+  const int lb = sk::stage_bytes(w.k / sk::kSuper);
+  switch (w.bits) {
+    case 4: hipLaunchKernelGGL(head_kernel<4>, dim3(parts), dim3(256), lb, s, w, x, m, maxima, indices); break;
+    case 5: hipLaunchKernelGGL(head_kernel<5>, dim3(parts), dim3(256), lb, s, w, x, m, maxima, indices); break;
+    case 6: hipLaunchKernelGGL(head_kernel<6>, dim3(parts), dim3(256), lb, s, w, x, m, maxima, indices); break;
+    default: hipLaunchKernelGGL(head_kernel<8>, dim3(parts), dim3(256), lb, s, w, x, m, maxima, indices); break;
+  }
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
+}  // namespace mx

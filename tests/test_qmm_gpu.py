@@ -1,6 +1,7 @@
 """Matrix-core (MFMA) projections: within the north star's tolerance of the
 float64 closed form and of the exact fixed-order kernels, for every code
-width, depth and row count the engine uses (including partial 16-row tiles)."""
+width, depth and row count the engine uses (including partial 16-row tiles
+and matrices split along k across workgroups)."""
 import ctypes as C
 
 import numpy as np
@@ -59,3 +60,51 @@ def test_moe_experts_mfma_within_tolerance(mx, orc):
     scale = np.abs(want).max(axis=2, keepdims=True)
     assert np.all(np.abs(got - want) <= 2e-2 * np.abs(want) + 1e-2 * scale)
     assert np.mean(got == want) > 0.5  # mostly identical after bf16 rounding
+
+
+@pytest.mark.parametrize("n,k", [(260, 8192), (2048, 4096), (513, 2048), (12352, 2048)])
+def test_qmm_k_split_shapes_deterministic(mx, orc, n, k):
+    """Shapes whose k is split among a workgroup's waves (the engine's HC,
+    output and router projections): repeated calls give identical bits, and
+    the result is within tolerance of the float64 closed form."""
+    bits, gs, m = 4, 64, 8
+    w = mx.QWeight.random(n, k, bits, gs, 9100 + n)
+    x = orc.fill_bf16(m * k, 9102, 1, 1.0, 0.0).reshape(m, k)
+    dx = mx.DeviceArray.from_numpy(x)
+    outs = []
+    for _ in range(3):
+        dy = mx.DeviceArray((m, n), np.uint16)
+        qc = w.c()
+        mx.check(mx.lib.mx_qmm(C.byref(qc), dx.ptr, m, dy.ptr, None))
+        outs.append(dy.numpy())
+    assert (outs[0] == outs[1]).all() and (outs[1] == outs[2]).all()
+    codes, s, b = orc.random_qweight(n, k, bits, gs, 9100 + n)
+    y64 = orc.qmv_f64(codes, s, b, k, bits, gs, x)
+    got = bf(outs[0]).astype(np.float64)
+    mag = np.abs(bf(x)).astype(np.float64).sum(axis=1, keepdims=True) * 0.05
+    assert np.all(np.abs(got - y64) <= 2.0 ** -8 * np.abs(y64) + 2.0 ** -16 * mag + 1e-6)
+
+
+@pytest.mark.parametrize("m", [1, 5, 8])
+def test_head_argmax_mfma_matches_exact_head(mx, orc, m):
+    """The matrix-core head picks the exact head's token unless the two best
+    bf16 logits of a row are within the summation-order tolerance."""
+    n, k, bits, gs = 151936, 2048, 8, 64
+    w = mx.QWeight.random(n, k, bits, gs, 9200)
+    x = orc.fill_bf16(m * k, 9201 + m, 1, 1.0, 0.0).reshape(m, k)
+    dx = mx.DeviceArray.from_numpy(x)
+    wsb = mx.lib.mx_head_workspace_bytes(n, k, m)
+    ws = mx.DeviceArray((wsb,), np.uint8)
+    got = mx.DeviceArray((m,), np.uint32)
+    exact = mx.DeviceArray((m,), np.uint32)
+    qc = w.c()
+    mx.check(mx.lib.mx_head_argmax_mfma(C.byref(qc), dx.ptr, m, got.ptr, ws.ptr, None))
+    mx.check(mx.lib.mx_head_argmax(C.byref(qc), dx.ptr, m, exact.ptr, ws.ptr, None))
+    logits = mx.DeviceArray((m, n), np.uint16)
+    mx.qmv(w, dx, m, logits)
+    lg = bf(logits.numpy()).astype(np.float64)
+    g, e = got.numpy(), exact.numpy()
+    for r in range(m):
+        if g[r] != e[r]:
+            assert abs(lg[r, g[r]] - lg[r, e[r]]) <= 2.0 ** -7 * abs(lg[r, e[r]]) + 1e-3, r
+    assert np.mean(g == e) >= 0.5
