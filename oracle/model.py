@@ -143,6 +143,7 @@ class Model:
         return y
 
     def step(self, tokens, slots, pos, groups, t, history=None):
+        self.last_ids = []  # routing of each MoE layer in this step (test inspection)
         """One engine step over rows (slot, position); GDN rows grouped as
         `groups` sequences of `t` tokens.  Returns greedy next tokens."""
         c = self.c
@@ -200,6 +201,7 @@ class Model:
             E = c["experts"]
             ids, scores, factor = orc.moe_route(np.ascontiguousarray(logits[:, :E]),
                                                 np.ascontiguousarray(logits[:, E]), c["top_k"])
+            self.last_ids.append(ids.copy())
             pbuf = np.empty((rows, c["top_k"] + 1, H), np.uint16)
             orc.lib.mxo_moe_experts(_p(mixed), _p(ids), _p(scores), rows, c["top_k"], C.byref(L["gate"]),
                                     C.byref(L["up"]), C.byref(L["down"]), C.byref(L["sgate"]),

@@ -108,6 +108,7 @@ struct Engine {
   uint32_t* ids = nullptr;
   float *o_part = nullptr, *ml_part = nullptr;
   void* head_ws = nullptr;
+  float* hc_part = nullptr;  // partial sums of the fused HC projection
   // per-step row table (device) and its pinned host mirror
   struct RowTable {
     uint32_t tokens[8];
@@ -380,6 +381,8 @@ int build(Engine& e) {
   e.ml_part = static_cast<float*>(v);
   size_t hws = size_t(head_parts(c.vocab, c.hidden)) * 8 * 8;
   MX_TRY(alloc(e, "act.head_ws", hws, &e.head_ws));
+  MX_TRY(alloc(e, "act.hc_part", hc_fused_part_bytes(c.hc_rank + c.hc), &v));
+  e.hc_part = static_cast<float*>(v);
   MX_TRY(alloc(e, "rows", sizeof(Engine::RowTable), &v));
   e.dev_rows = static_cast<Engine::RowTable*>(v);
   if (hipHostMalloc(reinterpret_cast<void**>(&e.host_rows), sizeof(Engine::RowTable)) != hipSuccess)
@@ -471,6 +474,9 @@ int project(Engine& e, const QWeight& w, const uint16_t* x, int64_t xs, int rows
 
 int hc_forward(Engine& e, const HcW& w, int rows, uint16_t* mixed_out, uint16_t* inj_out) {
   const auto& c = e.cfg;
+  if (!e.exact && hc_fused_supported(w.down, w.up, c.hc, c.hidden, c.hc_rank))
+    return hc_fused(w.down, w.up, e.h, w.scale, rows, c.hc, c.hidden, c.hc_rank, c.rms_eps, e.xn,
+                    e.hc_part, mixed_out, inj_out, e.stream);
   MX_TRY(hc_norm(e.h, w.scale, rows, c.hc, c.hidden, c.rms_eps, e.xn, e.stream));
   ProjEpilogue d{};
   d.mode = kHcDown;

@@ -41,6 +41,9 @@ __device__ __forceinline__ float sigmoid_bf16(float x) {
 constexpr int kStageSteps = 16;
 constexpr int kDenseSteps = 64;
 constexpr int kDownSteps = 8;
+// Waves per gate/up tile (K split inside the workgroup): halves each wave's
+// registers so more workgroups stay resident.
+constexpr int kGateUpSplit = 2;
 
 // Sums the KS slices of each tile into yt[m][t * 16 + j] (fp32 [8][16 T]).
 // red: LDS [KS][T][8][16] (unused when KS == 1).  Ends with a barrier.
@@ -234,15 +237,15 @@ __device__ __forceinline__ QWeight expert_weight(const QBank& b, int expert, con
                  b.bits, b.group_size};
 }
 
-// gate/up + SwiGLU: waves 0,1 = gate rows tg*32 + 16w + j, waves 2,3 = up rows
-// of the same indices.  h[row][slot][i] = bf16(bf16(silu(bf16 g)) * bf16 u).
-template <int BITS>
-__global__ __launch_bounds__(256) void gate_up_kernel(const uint16_t* __restrict__ x,
-                                                      const uint32_t* __restrict__ ids, int rows,
-                                                      int top_k, QBank gate, QBank up,
-                                                      QWeight sgate, QWeight sup,
-                                                      uint16_t* __restrict__ h, int hs) {
+// gate/up + SwiGLU: tile 0,1 = gate rows tg*32 + 16t + j, tiles 2,3 = up rows
+// of the same indices, each split along K among KS waves (wave = 4-tile
+// index * KS + slice).  h[row][slot][i] = bf16(bf16(silu(bf16 g)) * bf16 u).
+template <int BITS, int KS>
+__global__ __launch_bounds__(256 * KS, 2) void gate_up_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ ids, int rows, int top_k,
+    QBank gate, QBank up, QWeight sgate, QWeight sup, uint16_t* __restrict__ h, int hs) {
   extern __shared__ __align__(16) char lds[];
+  __shared__ float red[KS > 1 ? KS * 4 * 8 * 16 : 1];
   __shared__ float yt[8 * 64];
   Routes rt;
   if (!resolve_routes(ids, rows, top_k, gate.experts, rt)) return;
@@ -252,26 +255,30 @@ __global__ __launch_bounds__(256) void gate_up_kernel(const uint16_t* __restrict
   const int tg = blockIdx.x;
   if (tg * 32 >= inter) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane & 15;
-  const bool is_gate = wave < 2;
+  const int t = wave / KS, ks = wave - t * KS;
+  const bool is_gate = t < 2;
   const uint32_t* codes = is_gate ? gw.codes : uw.codes;
   const uint16_t* scales = is_gate ? gw.scales : uw.scales;
   const uint16_t* biases = is_gate ? gw.biases : uw.biases;
-  const int row = min(tg * 32 + (wave & 1) * 16 + j, inter - 1);
+  const int row = min(tg * 32 + (t & 1) * 16 + j, inter - 1);
   const int G = hidden >> 6;
   const int steps = hidden / sk::kSuper;
+  const int k0 = steps * ks / KS, n = steps * (ks + 1) / KS - k0;
   const sk::RouteRows xr{x, hidden, 0, rt.packed, rt.M};
   const int xbytes = steps * sk::kStepBytes;
   const float* sx = reinterpret_cast<const float*>(lds + xbytes + sk::kZeroBytes);
-  sk::Stream<BITS, false, sk::RouteRows> st(codes + size_t(row) * (size_t(hidden) * BITS / 32),
-                                            scales + size_t(row) * G, biases + size_t(row) * G,
-                                            steps, 0, steps, 0, lds, sx, xr, rt.M);
-  sk::Stager<256, sk::stage_per(256, kStageSteps), sk::RouteRows> stg(xr, rt.M, 0, steps);
+  sk::Stream<BITS, false, sk::RouteRows, kStageSteps / KS> st(
+      codes + size_t(row) * (size_t(hidden) * BITS / 32), scales + size_t(row) * G,
+      biases + size_t(row) * G, steps, k0, n, 0, lds, sx, xr, rt.M);
+  sk::Stager<256 * KS, sk::stage_per(256 * KS, kStageSteps), sk::RouteRows> stg(xr, rt.M, 0,
+                                                                               steps);
   stg.load();
   st.prefetch();
   stg.store(lds);
   float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   st.run(xbytes, y);
-  reduce_tiles<4, 1>(y, nullptr, yt);
+  reduce_tiles<4, KS>(y, red, yt);
+  if (threadIdx.x >= 256) return;
   const int m = threadIdx.x >> 5, c = threadIdx.x & 31;
   const int i = tg * 32 + c;
   if (m >= rt.M || i >= inter) return;
@@ -284,7 +291,7 @@ __global__ __launch_bounds__(256) void gate_up_kernel(const uint16_t* __restrict
 // down + score: p[row][slot][n] = bf16(bf16(down) * score) (routed slots) or
 // bf16(down) (the shared slot, top_k).
 template <int BITS>
-__global__ __launch_bounds__(256) void down_kernel(const uint16_t* __restrict__ h,
+__global__ __launch_bounds__(256, 4) void down_kernel(const uint16_t* __restrict__ h,
                                                    const uint32_t* __restrict__ ids,
                                                    const uint16_t* __restrict__ scores, int rows,
                                                    int top_k, QBank down, QWeight sdown,
@@ -495,7 +502,7 @@ int skinny_gate_up(const uint16_t* x, const uint32_t* ids, int rows, int top_k,
   const dim3 grid((hs + 31) / 32, rows * top_k + 1);
   const int lb = sk::stage_bytes(steps);
 #define MX_GU(B) \
-  case B: hipLaunchKernelGGL(gate_up_kernel<B>, grid, dim3(256), lb, s, x, ids, rows, top_k, gate, up, sgate, sup, h, hs); break;
+  case B: hipLaunchKernelGGL((gate_up_kernel<B, kGateUpSplit>), grid, dim3(256 * kGateUpSplit), lb, s, x, ids, rows, top_k, gate, up, sgate, sup, h, hs); break;
   switch (gate.bits) {
     MX_GU(4) MX_GU(5) MX_GU(6) MX_GU(8)
     default: return MX_EUNSUPPORTED;
