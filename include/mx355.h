@@ -289,6 +289,32 @@ mx_status mx_gdn_recurrence(const uint16_t* conv_out, int64_t conv_stride, const
                             const int32_t* slots, float* state, float* history, uint16_t* y,
                             void* stream);
 
+/* ---- gated full attention (decode / verify rows) ---------------------------
+ * mx_attn_decode: scaled dot-product attention of each row's normalised and
+ * rotated q heads (q bf16 [rows, heads, head_dim]) over the cached positions
+ * 0..pos[r] of its slot, then the output gate:
+ *   out[r, h] = bf16(bf16(softmax(q k^T / sqrt(head_dim)) v) * sigmoid(gate[r, h]))
+ * with gate[r, h] = qkv[r * qkv_stride + h * 2 * head_dim + head_dim ..] (the
+ * projected rows, [heads][q | gate][head_dim] per row).  Caches are bf16
+ * [slot][kv_head][max_ctx][head_dim] with slot_stride elements between slots.
+ * flags bit 0: the matrix-core kernel (fp32 sums in another order, within
+ * tolerance) instead of the fixed-order kernel that the CPU oracle restates.
+ * workspace: mx_attn_workspace_bytes(rows, heads, head_dim, max_ctx) bytes.
+ * Replaces the fast::scaled_dot_product_attention call and output gate of
+ * Attention::forward_selection (src/dense.rs:139-270, 249-256). */
+typedef struct mx_attn_dims {
+  int32_t heads;     /* q heads */
+  int32_t kv_heads;  /* heads of the cache (heads is a multiple) */
+  int32_t head_dim;  /* <= 256, a multiple of 8 */
+  int32_t max_ctx;   /* positions per (slot, kv head) in the cache */
+  int64_t slot_stride;
+} mx_attn_dims;
+size_t mx_attn_workspace_bytes(int32_t rows, int32_t heads, int32_t head_dim, int32_t max_ctx);
+mx_status mx_attn_decode(const uint16_t* q, const uint16_t* qkv, int64_t qkv_stride, int32_t rows,
+                         const int32_t* slots, const int32_t* pos, const uint16_t* k_cache,
+                         const uint16_t* v_cache, const mx_attn_dims* dims, int32_t flags,
+                         void* workspace, uint16_t* out, void* stream);
+
 /* ---- A1/A17/A18: the decode engine ---------------------------------------
  * Owns the model weights, a slot arena of caches (GDN state + conv window, KV)
  * and one HIP stream; every call is synchronous (one sync per step, like the

@@ -63,6 +63,11 @@ class GdnDimsC(C.Structure):
                 ("conv_k", C.c_int32)]
 
 
+class AttnDimsC(C.Structure):
+    _fields_ = [("heads", C.c_int32), ("kv_heads", C.c_int32), ("head_dim", C.c_int32),
+                ("max_ctx", C.c_int32), ("slot_stride", C.c_int64)]
+
+
 class ModelConfigC(C.Structure):
     _fields_ = [(n, C.c_int32) for n in (
         "hidden", "layers", "attn_every", "vocab", "hc", "hc_rank", "gdn_hk", "gdn_hv", "gdn_dk",
@@ -124,6 +129,9 @@ def _load() -> C.CDLL:
                                i32, i32, vp, vp, vp, vp, vp], i32),
         "mx_gdn_scan": ([vp, vp, vp, vp, vp, C.POINTER(GdnDimsC), i32, i32, vp, vp, vp, vp,
                          vp], i32),
+        "mx_attn_workspace_bytes": ([i32, i32, i32, i32], sz),
+        "mx_attn_decode": ([vp, vp, i64, i32, vp, vp, vp, vp, C.POINTER(AttnDimsC), i32, vp, vp,
+                            vp], i32),
         "mx_engine_create": ([C.POINTER(ModelConfigC), C.POINTER(vp)], i32),
         "mx_engine_destroy": ([vp], i32),
         "mx_engine_reset_slot": ([vp, i32], i32),

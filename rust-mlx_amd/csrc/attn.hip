@@ -17,6 +17,7 @@
 // and V stream once per group.  A second pass combines the chunks.
 #include "common.hpp"
 #include "kernels.hpp"
+#include "skinny_core.hpp"
 
 namespace mx {
 
@@ -207,6 +208,146 @@ __global__ __launch_bounds__(kAttnChunk) void decode_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Matrix-core decode (fast mode): a workgroup of four waves handles
+// kAttnFastChunk = 64 positions of one (row, kv head), 16 per wave, for all G
+// q heads of the kv head.
+// Scores: one v_mfma_f32_16x16x32_bf16 per 32 dims with A = the q heads (row
+// = head, rows >= G zero) and B = the wave's 16 K rows (column = position),
+// both read straight from memory as 16-byte pieces: lane l = 16 qd + j loads
+// dims 32 kk + 8 qd .. +7 of q head j and of position j, so one MFMA step
+// covers 16 positions x 64 bytes of K.  Lane l then holds the scores of heads
+// 4 qd .. +3 at position j.
+// Softmax: max and sum per head over the 16 lanes of a quarter (xor
+// butterfly), then over the four waves through LDS; p = e^(s - m) into LDS.
+// Values: wave w owns dims [w HD/4, (w+1) HD/4) in 8-dim blocks; lane
+// (position group pg, block db) accumulates o[g][8] over positions pg,
+// pg + NPG, ... (one 16-byte V load each, all issued together), and the
+// position groups are summed with xor shuffles.  Positions past the row's
+// length load the last valid row (always in bounds) and weigh it 0.
+template <int G, int HD>
+__global__ __launch_bounds__(256) void decode_fast_kernel(
+    const uint16_t* __restrict__ q, const int32_t* __restrict__ slots,
+    const int32_t* __restrict__ pos, const uint16_t* __restrict__ k_cache,
+    const uint16_t* __restrict__ v_cache, AttnDims d, int max_chunks, float scale,
+    float* __restrict__ o_part, float* __restrict__ ml_part) {
+  constexpr int C = kAttnFastChunk;
+  constexpr int KS = HD / 32;  // MFMA steps over the head dim
+  __shared__ float ps[16][C];
+  __shared__ float red[2][4][16];
+  const int chunk = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int row = blockIdx.z;
+  const int t = threadIdx.x;
+  const int wave = t >> 6, lane = t & 63;
+  const int j = lane & 15, qd = lane >> 4;
+  const int n_pos = pos[row] + 1;
+  const int j0 = chunk * C;
+  if (j0 >= n_pos) return;  // uniform per workgroup
+  const size_t base = size_t(slots[row]) * d.slot_stride + size_t(kvh) * d.max_ctx * HD;
+
+  const int p = j0 + 16 * wave + j;
+  const bool valid = p < n_pos;
+  const uint16_t* kr = k_cache + base + size_t(valid ? p : n_pos - 1) * HD + qd * 8;
+  const uint16_t* qr = q + (size_t(row) * d.heads + kvh * G + (j < G ? j : 0)) * HD + qd * 8;
+  uint4 kb[KS], qa[KS];
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk) kb[kk] = *reinterpret_cast<const uint4*>(kr + kk * 32);
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk) {
+    const uint4 v = *reinterpret_cast<const uint4*>(qr + kk * 32);
+    qa[kk] = j < G ? v : make_uint4(0u, 0u, 0u, 0u);
+  }
+  sk::floatx4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk) acc = sk::mfma(qa[kk], kb[kk], acc);
+
+  float s[4], e[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    s[i] = valid ? acc[i] * scale : u2f(0xff800000u);
+    float m = s[i];
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) {
+      const float v = __shfl_xor(m, o, 64);
+      m = v > m ? v : m;
+    }
+    if (j == 0) red[0][wave][4 * qd + i] = m;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int h = 4 * qd + i;
+    float m = red[0][0][h];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) m = red[0][w][h] > m ? red[0][w][h] : m;
+    e[i] = valid ? expf_(s[i] - m) : 0.0f;
+    ps[h][16 * wave + j] = e[i];
+    float l = e[i];
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) l = l + __shfl_xor(l, o, 64);
+    if (j == 0) red[1][wave][h] = l;
+  }
+  __syncthreads();
+  if (t < G) {
+    float m = red[0][0][t], l = red[1][0][t];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) {
+      m = red[0][w][t] > m ? red[0][w][t] : m;
+      l = l + red[1][w][t];
+    }
+    float* ml = ml_part + ((size_t(row) * d.heads + kvh * G + t) * max_chunks + chunk) * 2;
+    ml[0] = m;
+    ml[1] = l;
+  }
+
+  constexpr int DB = HD / 32;   // 8-dim blocks per wave
+  constexpr int NPG = 64 / DB;  // position groups per wave
+  constexpr int PPL = C / NPG;  // positions per lane
+  const int db = lane % DB, pg = lane / DB;
+  const int dim0 = wave * (HD / 4) + db * 8;
+  uint4 vv[PPL];
+#pragma unroll
+  for (int i = 0; i < PPL; ++i) {
+    const int pp = j0 + pg + NPG * i;
+    vv[i] = *reinterpret_cast<const uint4*>(v_cache + base + size_t(pp < n_pos ? pp : n_pos - 1) * HD +
+                                            dim0);
+  }
+  float o[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int c = 0; c < 8; ++c) o[g][c] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < PPL; ++i) {
+    const uint4 r = vv[i];
+    const float v[8] = {u2f(r.x << 16), u2f(r.x & 0xffff0000u), u2f(r.y << 16),
+                        u2f(r.y & 0xffff0000u), u2f(r.z << 16), u2f(r.z & 0xffff0000u),
+                        u2f(r.w << 16), u2f(r.w & 0xffff0000u)};
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float pr = ps[g][pg + NPG * i];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) o[g][c] = fmaf_(pr, v[c], o[g][c]);
+    }
+  }
+#pragma unroll
+  for (int off = DB; off < 64; off <<= 1)
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int c = 0; c < 8; ++c) o[g][c] = o[g][c] + __shfl_xor(o[g][c], off, 64);
+  if (pg == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float4* dst = reinterpret_cast<float4*>(
+          o_part + ((size_t(row) * d.heads + kvh * G + g) * max_chunks + chunk) * HD + dim0);
+      dst[0] = make_float4(o[g][0], o[g][1], o[g][2], o[g][3]);
+      dst[1] = make_float4(o[g][4], o[g][5], o[g][6], o[g][7]);
+    }
+  }
+}
+
 // Combines the chunks of one (row, head) and applies the output gate:
 //   M = max m_c; w_c = e^(m_c - M); L = sum l_c w_c; O = sum o_c w_c (fma, c
 //   ascending); y = bf16(bf16(O / L) * sigmoid_bf16(gate)).
@@ -216,13 +357,14 @@ __global__ __launch_bounds__(kMaxHd) void combine_kernel(const float* __restrict
                                                          int64_t qkv_stride,
                                                          const int32_t* __restrict__ pos,
                                                          AttnDims d, int max_chunks,
+                                                         int chunk,
                                                          uint16_t* __restrict__ out) {
   const int h = blockIdx.x;
   const int row = blockIdx.y;
   const int t = threadIdx.x;
   const int hd = d.head_dim;
   if (t >= hd) return;
-  const int chunks = (pos[row] + kAttnChunk) / kAttnChunk;
+  const int chunks = (pos[row] + chunk) / chunk;
   const float* ml = ml_part + (size_t(row) * d.heads + h) * max_chunks * 2;
   const float* op = o_part + (size_t(row) * d.heads + h) * max_chunks * hd + t;
   float M = ml[0];
@@ -251,13 +393,38 @@ int attn_prep(const uint16_t* qkv, int64_t qkv_stride, int rows, const int32_t* 
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 
+bool attn_fast_supported(AttnDims d) {
+  if (d.kv_heads <= 0 || d.heads % d.kv_heads != 0) return false;
+  const int g = d.heads / d.kv_heads;
+  return (d.head_dim == 128 || d.head_dim == 256) && (g == 1 || g == 2 || g == 4 || g == 8) &&
+         d.slot_stride % 8 == 0;
+}
+
 int attn_decode(const uint16_t* q, int rows, const int32_t* slots, const int32_t* pos,
                 const uint16_t* k_cache, const uint16_t* v_cache, AttnDims d, int max_chunks,
-                float* o_part, float* ml_part, hipStream_t s) {
+                bool fast, float* o_part, float* ml_part, hipStream_t s) {
   if (d.head_dim > kMaxHd || d.heads % d.kv_heads != 0 || d.heads / d.kv_heads > kMaxGroup)
     return MX_EUNSUPPORTED;
   const float scale = 1.0f / __builtin_sqrtf(float(d.head_dim));
-  const dim3 grid(max_chunks, d.kv_heads, rows);
+  if (fast) {
+    if (!attn_fast_supported(d)) return MX_EUNSUPPORTED;
+    const int chunks = (d.max_ctx + kAttnFastChunk - 1) / kAttnFastChunk;
+    if (chunks > max_chunks) return MX_EINVAL;
+    const dim3 grid(chunks, d.kv_heads, rows);
+#define MX_FDEC(GG, HH)                                                                       \
+  if (d.heads / d.kv_heads == GG && d.head_dim == HH) {                                       \
+    hipLaunchKernelGGL((decode_fast_kernel<GG, HH>), grid, dim3(256), 0, s, q, slots, pos,    \
+                       k_cache, v_cache, d, max_chunks, scale, o_part, ml_part);              \
+    return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;                                 \
+  }
+    MX_FDEC(1, 128) MX_FDEC(2, 128) MX_FDEC(4, 128) MX_FDEC(8, 128)
+    MX_FDEC(1, 256) MX_FDEC(2, 256) MX_FDEC(4, 256) MX_FDEC(8, 256)
+#undef MX_FDEC
+    return MX_EUNSUPPORTED;
+  }
+  const int chunks = (d.max_ctx + kAttnChunk - 1) / kAttnChunk;
+  if (chunks > max_chunks) return MX_EINVAL;
+  const dim3 grid(chunks, d.kv_heads, rows);
 #define MX_DEC(GG)                                                                         \
   case GG:                                                                                 \
     hipLaunchKernelGGL(decode_kernel<GG>, grid, dim3(kAttnChunk), 0, s, q, slots, pos,     \
@@ -273,9 +440,9 @@ int attn_decode(const uint16_t* q, int rows, const int32_t* slots, const int32_t
 
 int attn_combine(const float* o_part, const float* ml_part, const uint16_t* qkv,
                  int64_t qkv_stride, int rows, const int32_t* pos, AttnDims d, int max_chunks,
-                 uint16_t* out, hipStream_t s) {
+                 bool fast, uint16_t* out, hipStream_t s) {
   hipLaunchKernelGGL(combine_kernel, dim3(d.heads, rows), dim3(kMaxHd), 0, s, o_part, ml_part,
-                     qkv, qkv_stride, pos, d, max_chunks, out);
+                     qkv, qkv_stride, pos, d, max_chunks, fast ? kAttnFastChunk : kAttnChunk, out);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 

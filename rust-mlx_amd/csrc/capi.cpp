@@ -388,6 +388,47 @@ MX_ABI mx_status mx_gdn_scan(const uint16_t* q, const uint16_t* k, const uint16_
                 "mx_gdn_scan");
 }
 
+// ---- attention --------------------------------------------------------------
+MX_ABI size_t mx_attn_workspace_bytes(int32_t rows, int32_t heads, int32_t head_dim,
+                                      int32_t max_ctx) {
+  if (rows <= 0 || heads <= 0 || head_dim <= 0 || max_ctx <= 0) return 0;
+  const size_t chunks = (size_t(max_ctx) + kAttnFastChunk - 1) / kAttnFastChunk;
+  const size_t o = size_t(rows) * heads * chunks * head_dim * 4;
+  return o + size_t(rows) * heads * chunks * 2 * 4;
+}
+
+MX_ABI mx_status mx_attn_decode(const uint16_t* q, const uint16_t* qkv, int64_t qkv_stride,
+                                int32_t rows, const int32_t* slots, const int32_t* pos,
+                                const uint16_t* k_cache, const uint16_t* v_cache,
+                                const mx_attn_dims* dims, int32_t flags, void* workspace,
+                                uint16_t* out, void* stream) {
+  MX_CHECK(dims != nullptr, MX_EINVAL, "mx_attn_decode: null dims");
+  MX_CHECK(rows >= 0, MX_EINVAL, "mx_attn_decode: negative rows");
+  if (rows == 0) return MX_OK;
+  MX_CHECK(q && qkv && slots && pos && k_cache && v_cache && workspace && out, MX_EINVAL,
+           "mx_attn_decode: null pointer");
+  const AttnDims d{dims->heads, dims->kv_heads, dims->head_dim, 0, dims->max_ctx,
+                   dims->slot_stride};
+  MX_CHECK(d.heads > 0 && d.kv_heads > 0 && d.heads % d.kv_heads == 0, MX_EINVAL,
+           "mx_attn_decode: heads must be a positive multiple of kv_heads");
+  MX_CHECK(d.head_dim > 0 && d.head_dim <= 256 && d.head_dim % 8 == 0 && d.max_ctx > 0,
+           MX_EUNSUPPORTED, "mx_attn_decode: head_dim must be a multiple of 8 up to 256");
+  MX_CHECK(d.slot_stride >= int64_t(d.kv_heads) * d.max_ctx * d.head_dim &&
+               d.slot_stride % 8 == 0 && qkv_stride >= int64_t(2) * d.heads * d.head_dim,
+           MX_EINVAL, "mx_attn_decode: bad strides");
+  const bool fast = (flags & 1) != 0;
+  MX_CHECK(!fast || attn_fast_supported(d), MX_EUNSUPPORTED,
+           "mx_attn_decode: matrix-core kernel needs head_dim 128/256 and 1..8 q heads per kv head");
+  const int chunks = (d.max_ctx + kAttnFastChunk - 1) / kAttnFastChunk;
+  float* o_part = static_cast<float*>(workspace);
+  float* ml_part = o_part + size_t(rows) * d.heads * chunks * d.head_dim;
+  const hipStream_t s = hipStream_t(stream);
+  int rc = attn_decode(q, rows, slots, pos, k_cache, v_cache, d, chunks, fast, o_part, ml_part, s);
+  if (rc == MX_OK)
+    rc = attn_combine(o_part, ml_part, qkv, qkv_stride, rows, pos, d, chunks, fast, out, s);
+  return finish(rc, "mx_attn_decode");
+}
+
 // ---- engine ---------------------------------------------------------------
 struct mx_engine {
   mx::Engine* impl;

@@ -255,7 +255,7 @@ int build(Engine& e) {
   e.vd = c.gdn_hv * c.gdn_dv;
   e.P = e.cd + e.vd + 2 * c.gdn_hv;
   e.Q = c.heads * 2 * c.head_dim + 2 * c.kv_heads * c.head_dim;
-  e.max_chunks = (c.max_context + kAttnChunk - 1) / kAttnChunk;
+  e.max_chunks = (c.max_context + kAttnFastChunk - 1) / kAttnFastChunk;
   for (int i = 0; i < c.layers; ++i) {
     LayerW L;
     L.attn = (i % c.attn_every) == c.attn_every - 1;
@@ -548,9 +548,12 @@ int record_step(Engine& e, int rows, int groups, int t, bool history, bool logit
       MX_TRY(attn_prep(e.pbuf, e.Q, rows, rt->slots, rt->pos, L.q_norm, L.k_norm, c.rms_eps,
                        e.rope_cos, e.rope_sin, e.ad, e.qrot, e.k_cache + layer_off,
                        e.v_cache + layer_off, e.stream));
+      const bool fast_attn = !e.exact && attn_fast_supported(e.ad);
       MX_TRY(attn_decode(e.qrot, rows, rt->slots, rt->pos, e.k_cache + layer_off,
-                         e.v_cache + layer_off, e.ad, e.max_chunks, e.o_part, e.ml_part, e.stream));
+                         e.v_cache + layer_off, e.ad, e.max_chunks, fast_attn, e.o_part,
+                         e.ml_part, e.stream));
       MX_TRY(attn_combine(e.o_part, e.ml_part, e.pbuf, e.Q, rows, rt->pos, e.ad, e.max_chunks,
+                          fast_attn,
                           e.y, e.stream));
       MX_TRY(project(e, L.attn_out, e.y, int64_t(c.heads) * c.head_dim, rows, wr));
     }

@@ -94,13 +94,19 @@ int attn_prep(const uint16_t* qkv, int64_t qkv_stride, int rows, const int32_t* 
               const int32_t* pos, const uint16_t* q_norm, const uint16_t* k_norm, float eps,
               const float* rope_cos, const float* rope_sin, AttnDims d, uint16_t* q_out,
               uint16_t* k_cache, uint16_t* v_cache, hipStream_t s);
+// fast: the matrix-core kernel (64-position chunks, within tolerance) instead
+// of the fixed-order one (256-position chunks).  o_part / ml_part hold
+// max_chunks chunks per (row, head); max_chunks must cover max_ctx in chunks
+// of the chosen kernel.
+bool attn_fast_supported(AttnDims d);
 int attn_decode(const uint16_t* q, int rows, const int32_t* slots, const int32_t* pos,
                 const uint16_t* k_cache, const uint16_t* v_cache, AttnDims d, int max_chunks,
-                float* o_part, float* ml_part, hipStream_t s);
+                bool fast, float* o_part, float* ml_part, hipStream_t s);
 int attn_combine(const float* o_part, const float* ml_part, const uint16_t* qkv,
                  int64_t qkv_stride, int rows, const int32_t* pos, AttnDims d, int max_chunks,
-                 uint16_t* out, hipStream_t s);
+                 bool fast, uint16_t* out, hipStream_t s);
 constexpr int kAttnChunk = 256;
+constexpr int kAttnFastChunk = 64;
 
 // ---- MoE ----
 constexpr int kMaxRoutes = 8 * 16 + 1;
