@@ -475,7 +475,7 @@ int project(Engine& e, const QWeight& w, const uint16_t* x, int64_t xs, int rows
 int hc_forward(Engine& e, const HcW& w, int rows, uint16_t* mixed_out, uint16_t* inj_out) {
   const auto& c = e.cfg;
   if (!e.exact && hc_fused_supported(w.down, w.up, c.hc, c.hidden, c.hc_rank))
-    return hc_fused(w.down, w.up, e.h, w.scale, rows, c.hc, c.hidden, c.hc_rank, c.rms_eps, e.xn,
+    return hc_fused(w.down, w.up, e.h, w.scale, rows, c.hc, c.hidden, c.hc_rank, c.rms_eps,
                     e.hc_part, mixed_out, inj_out, e.stream);
   MX_TRY(hc_norm(e.h, w.scale, rows, c.hc, c.hidden, c.rms_eps, e.xn, e.stream));
   ProjEpilogue d{};

@@ -1,23 +1,34 @@
 // Hyper-connection input projection on the matrix cores (decode, 1..8 rows):
-// grouped RMS norm -> down (low rank + inject rows) -> activation -> up -> mix,
-// in two launches (reference HyperConnection::forward_reference,
+// per-stream RMS norm -> down (low rank + inject rows) -> activation -> up ->
+// mix, in two launches (reference HyperConnection::forward_reference,
 // src/hybrid.rs:78-99; compiled::activate / injection / mix,
 // src/compiled.rs:46-86).
 //
-//  hc_down_kernel: grid (row groups of 64, S K-slices).  Each K-slice lies in
-//    one stream; the workgroup loads that stream of every activation row,
-//    forms its RMS norm, stages the normalised slice (written out as xn by row
-//    group 0, for the mix) and streams 4 tiles of down rows over it, writing
-//    fp32 partial sums part[slice][m][row].
-//  hc_up_kernel: grid (16-column groups).  Every workgroup adds the S partials
-//    of all down rows in slice order, applies the activation in registers
-//    (low-rank rows -> silu(v / hc) into the MFMA staging; inject rows ->
-//    2 sigmoid(v / hc), written by group 0), then streams the 4 stream tiles of
-//    up rows and mixes: mixed[c] = mean_s sigmoid(p_s) * xn_s[c].
+// The norm is a per-(row, stream) factor, so it is taken out of the down
+// projection: for down row r and activation row m
+//   down[m, r] = sum_s inv[m, s] * sum_{k in stream s} W[r, k] * bf16(h[m, k] (w[k] + 1))
+// with inv[m, s] = 1 / sqrt(mean_{k in s} h[m, k]^2 + eps).
 //
-// Arithmetic: matrix-core sums (skinny_core.hpp) and the element-wise steps of
-// the exact kernels (bf16 rounding per operation); results agree with the
-// exact path within summation-order tolerance.
+//  hc_down_kernel: grid (16-row tiles of the down matrix, streams).  Each of
+//    the workgroup's waves takes SPW super-steps (128 values) of the stream and
+//    builds its matrix-core A operands in registers straight from h and the
+//    norm weights (no LDS staging, no barrier before the products); the same
+//    operands give the group sums of x (an MFMA against ones) and the sums of
+//    squares of h (the diagonal of H H^T, one more MFMA).  The waves' partial
+//    sums are added in LDS in wave order and written as part[stream][m][row];
+//    the tile-0 workgroup of each stream also writes the stream's sums of
+//    squares.
+//  hc_up_kernel: grid (16-column groups).  Every workgroup forms inv, adds the
+//    stream partials of all down rows weighted by inv (stream order), applies
+//    the activation (low-rank rows -> silu(v / hc) into the MFMA staging;
+//    inject rows -> 2 sigmoid(v / hc), written by group 0; sigmoid and the
+//    norm factor from the hardware exp2 / reciprocal / rsqrt), streams the 4
+//    stream tiles of up rows, and mixes:
+//      mixed[c] = mean_s sigmoid(p_s) * bf16((h_s[c] inv_s) (w_s[c] + 1)).
+//
+// Arithmetic: matrix-core sums (skinny_core.hpp) in another order than the
+// exact kernels; results agree with the exact path within summation-order
+// tolerance.
 #include "common.hpp"
 #include "kernels.hpp"
 #include "skinny_core.hpp"
@@ -26,33 +37,53 @@ namespace mx {
 
 namespace {
 
-constexpr int kSlices = 8;
+constexpr int kMaxDownWaves = 8;
 
-__device__ __forceinline__ float sigmoid_bf16(float x) {
-  const float e = round_bf16(expf_(__builtin_fabsf(x)));
-  const float d = round_bf16(1.0f + e);
-  const float y = round_bf16(1.0f / d);
-  return x < 0.0f ? y : round_bf16(1.0f - y);
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// sigmoid with the hardware exp2 and reciprocal (about 1 ulp; fast mode).
+__device__ __forceinline__ float sigmoid_fast(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
 }
 
-// Writes one staged 8-value unit (value v of row m, unit u of the slice) in
-// operand order, and its group sum when this lane leads its group of 8 lanes.
-__device__ __forceinline__ void stage_unit(char* lds, int steps, uint4 val, int m, int u,
-                                           bool live) {
+// Two fp32 values -> packed bf16 pair (round to nearest even).
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  const bf16x2_t v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// A operand of one MFMA step: bf16(h * (w + 1)) for 8 values, in operand order.
+__device__ __forceinline__ uint4 scaled_operand(const uint4& hv, const uint4& wv) {
+  const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
+  const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float a = u2f(hw[i] << 16) * (u2f(ww[i] << 16) + 1.0f);
+    const float b = u2f(hw[i] & 0xffff0000u) * (u2f(ww[i] & 0xffff0000u) + 1.0f);
+    o[i] = pack_bf16(a, b);
+  }
+  return sk::permute_x(make_uint4(o[0], o[1], o[2], o[3]));
+}
+
+// Writes one staged 8-value unit (value unit u of row m) in operand order, and
+// its group sum when this lane leads its group.  The lanes of a wave hold unit
+// u = (lane / 8) + 8 c of row m = lane % 8: the eight units of a group lie 8
+// lanes apart, and consecutive lanes write different rows (no LDS bank
+// conflicts).  All 64 lanes take part in the shuffles.
+__device__ __forceinline__ void stage_unit(char* lds, int steps, uint4 val, int m, int u) {
   uint4* xs = reinterpret_cast<uint4*>(lds);
   float* sx = reinterpret_cast<float*>(lds + steps * sk::kStepBytes + sk::kZeroBytes);
   const uint32_t d[4] = {val.x, val.y, val.z, val.w};
   float sum = 0.0f;
 #pragma unroll
   for (int h = 0; h < 4; ++h) sum = sum + u2f(d[h] << 16) + u2f(d[h] & 0xffff0000u);
-  sum = sum + __shfl_xor(sum, 1, 64);
-  sum = sum + __shfl_xor(sum, 2, 64);
-  sum = sum + __shfl_xor(sum, 4, 64);
-  if (live) {
-    if ((u & 7) == 0) sx[(u >> 3) * 8 + m] = sum;
-    const int s = u >> 4, o = u & 15;
-    xs[(s * 4 + (o & 3)) * 32 + (o >> 2) * 8 + m] = sk::permute_x(val);
-  }
+  sum = sum + __shfl_xor(sum, 8, 64);
+  sum = sum + __shfl_xor(sum, 16, 64);
+  sum = sum + __shfl_xor(sum, 32, 64);
+  if ((u & 7) == 0) sx[(u >> 3) * 8 + m] = sum;
+  const int s = u >> 4, o = u & 15;
+  xs[(s * 4 + (o & 3)) * 32 + (o >> 2) * 8 + m] = sk::permute_x(val);
 }
 
 __device__ __forceinline__ void zero_block(char* lds, int steps, int nthreads) {
@@ -61,146 +92,130 @@ __device__ __forceinline__ void zero_block(char* lds, int steps, int nthreads) {
 }
 
 // ---------------------------------------------------------------------------
-// hidden <= 2048 and hidden % (kSlices / hc * 128) == 0 (checked on the host).
-template <int BITS>
-__global__ __launch_bounds__(256) void hc_down_kernel(QWeight w, const uint16_t* __restrict__ h,
-                                                      const uint16_t* __restrict__ scale, int M,
-                                                      int hidden, int hc, float eps,
-                                                      uint16_t* __restrict__ xn,
-                                                      float* __restrict__ part, int npad) {
-  extern __shared__ __align__(16) char lds[];
-  __shared__ float ssq[4][8];
-  const int tg = blockIdx.x, slice = blockIdx.y;
+// Block: (hidden / 128) / SPW waves (<= kMaxDownWaves).  Lane l = 16 q + j:
+// weight row j of the tile; A row j (activation m = j % 8) when the lane is
+// live for its group parity (j < 8 == q < 2), values 32 q .. +31 of the
+// super-step.
+template <int BITS, int SPW>
+__global__ __launch_bounds__(64 * kMaxDownWaves) void hc_down_kernel(
+    QWeight w, const uint16_t* __restrict__ h, const uint16_t* __restrict__ scale, int M,
+    int hidden, float* __restrict__ part, float* __restrict__ ssq, int npad) {
+  __shared__ float red[kMaxDownWaves][8][16];
+  __shared__ float sred[kMaxDownWaves][8];
+  const int tile = blockIdx.x, stream = blockIdx.y;
+  const int waves = blockDim.x >> 6;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane & 15, q = lane >> 4;
-  const int K = w.k;                     // hc * hidden
-  const int slen = K / kSlices;          // values per slice
-  const int stream = (slice * slen) / hidden;
-  const int sstart = slice * slen - stream * hidden;  // slice offset within the stream
-  const int steps = slen / sk::kSuper;
-  const int ks0 = slice * steps;
-  const int n = w.n, G = K >> 6;
-  const int row = min(tg * 64 + wave * 16 + j, n - 1);
-  // stream rows: M x hidden values, units of 8; thread t holds unit t + 256 k
-  const int units = hidden / 8;          // per row
-  const int total = M * units;
-  constexpr int PER = 8;                 // 8 rows x 2048 / 8 / 256
-  uint4 v[PER];
-  uint4 sc[PER];
+  const int K = w.k, n = w.n, G = K >> 6;
+  const int row = min(tile * 16 + j, n - 1);
+  const int ks0 = stream * (hidden / sk::kSuper) + wave * SPW;  // super-step within K
+  const int m = j & 7;
+  const bool live = ((j < 8) == (q < 2)) && m < M;
+  const uint16_t* hrow = h + size_t(m < M ? m : M - 1) * K + 32 * q;
+  const uint16_t* wrow = scale + 32 * q;
+  const uint32_t* crow = w.codes + size_t(row) * (size_t(K) * BITS / 32);
+  // every load up front: codes, scale/bias words, h and norm weights
+  uint32_t wc[SPW][BITS];
+  uint32_t sw[SPW], bw[SPW];
+  uint4 hx[SPW][4], wx[SPW][4];
 #pragma unroll
-  for (int k = 0; k < PER; ++k) {
-    const int i = min(int(threadIdx.x) + k * 256, total - 1);
-    const int m = i / units, u = i - m * units;
-    v[k] = *reinterpret_cast<const uint4*>(h + size_t(m) * K + size_t(stream) * hidden + u * 8);
-    sc[k] = *reinterpret_cast<const uint4*>(scale + size_t(stream) * hidden + u * 8);
-  }
-  const sk::DenseRows none{h, 0, 1};
-  sk::Stream<BITS, false, sk::DenseRows, 8> st(w.codes + size_t(row) * (size_t(K) * BITS / 32),
-                                               w.scales + size_t(row) * G,
-                                               w.biases + size_t(row) * G, K / sk::kSuper, ks0,
-                                               steps, ks0, lds,
-                                               reinterpret_cast<const float*>(
-                                                   lds + steps * sk::kStepBytes + sk::kZeroBytes),
-                                               none, 1);
-  st.prefetch();
-  // sums of squares per row (thread order, then waves 0..3)
-  float acc[8];
+  for (int i = 0; i < SPW; ++i) {
+    const int ks = ks0 + i;
+    sk::load_codes<BITS>(crow, ks, q, wc[i]);
+    sw[i] = *reinterpret_cast<const uint32_t*>(w.scales + size_t(row) * G + 2 * ks);
+    bw[i] = *reinterpret_cast<const uint32_t*>(w.biases + size_t(row) * G + 2 * ks);
 #pragma unroll
-  for (int m = 0; m < 8; ++m) acc[m] = 0.0f;
-#pragma unroll
-  for (int k = 0; k < PER; ++k) {
-    const int i = int(threadIdx.x) + k * 256;
-    if (i < total) {
-      const int m = i / units;
-      const uint32_t d[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
-      float s2 = 0.0f;
-#pragma unroll
-      for (int hh = 0; hh < 4; ++hh) {
-        const float a = u2f(d[hh] << 16), b = u2f(d[hh] & 0xffff0000u);
-        s2 = s2 + a * a + b * b;
-      }
-#pragma unroll
-      for (int mm = 0; mm < 8; ++mm)
-        if (mm == m) acc[mm] = acc[mm] + s2;
+    for (int u = 0; u < 4; ++u) {
+      hx[i][u] = *reinterpret_cast<const uint4*>(hrow + size_t(ks) * sk::kSuper + 8 * u);
+      wx[i][u] = *reinterpret_cast<const uint4*>(wrow + size_t(ks) * sk::kSuper + 8 * u);
     }
   }
-#pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    float a = acc[m];
-    for (int o = 32; o > 0; o >>= 1) a = a + __shfl_xor(a, o, 64);
-    if (lane == 0) ssq[wave][m] = a;
-  }
-  zero_block(lds, steps, 256);
-  __syncthreads();
-  // normalised slice values, staged (and written out by row group 0)
-  const int sunits = slen / 8;
-#pragma unroll
-  for (int k = 0; k < PER; ++k) {
-    const int i = int(threadIdx.x) + k * 256;
-    const int ic = min(i, total - 1);
-    const int m = ic / units, u = ic - m * units;
-    const int su = u - sstart / 8;  // unit within the slice
-    const bool in_slice = i < total && su >= 0 && su < sunits;
-    const float tot = ((ssq[0][m] + ssq[1][m]) + ssq[2][m]) + ssq[3][m];
-    const float inv = 1.0f / __builtin_sqrtf(tot / float(hidden) + eps);
-    const uint32_t d[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
-    const uint32_t e[4] = {sc[k].x, sc[k].y, sc[k].z, sc[k].w};
-    uint32_t o[4];
-#pragma unroll
-    for (int hh = 0; hh < 4; ++hh) {
-      const float a = u2f(d[hh] << 16), b = u2f(d[hh] & 0xffff0000u);
-      const float ea = u2f(e[hh] << 16), eb = u2f(e[hh] & 0xffff0000u);
-      const uint32_t ya = f32_to_bf16((a * inv) * (ea + 1.0f));
-      const uint32_t yb = f32_to_bf16((b * inv) * (eb + 1.0f));
-      o[hh] = ya | (yb << 16);
-    }
-    const uint4 val = make_uint4(o[0], o[1], o[2], o[3]);
-    // every lane of a wave takes part in the group-sum shuffles; only slice
-    // units are stored (a group of 8 lanes is wholly inside or outside)
-    if ((k * 256 + int(threadIdx.x & ~63)) < total)
-      stage_unit(lds, steps, val, m, su < 0 ? 0 : su, in_slice);
-    if (in_slice && tg == 0)
-      *reinterpret_cast<uint4*>(xn + size_t(m) * K + size_t(stream) * hidden + u * 8) = val;
-  }
-  // rows M..7 of the slice are zero
-  {
-    uint4* xs = reinterpret_cast<uint4*>(lds);
-    float* sxp = reinterpret_cast<float*>(lds + steps * sk::kStepBytes + sk::kZeroBytes);
-    for (int i = threadIdx.x; i < (8 - M) * sunits; i += 256) {
-      const int m = M + i / sunits, u = i % sunits;
-      const int s = u >> 4, o = u & 15;
-      xs[(s * 4 + (o & 3)) * 32 + (o >> 2) * 8 + m] = make_uint4(0, 0, 0, 0);
-      if ((u & 7) == 0) sxp[(u >> 3) * 8 + m] = 0.0f;
-    }
-  }
-  __syncthreads();
+  const uint4 zero = make_uint4(0u, 0u, 0u, 0u);
+  const uint4 ones = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
+  const float off = sk::code_offset<BITS>();
+  const int hi = q >> 1;
   float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  st.run(steps * sk::kStepBytes, y);
-  sk::join_parities(y);
-  const int r = tg * 64 + wave * 16 + j;
-  if (q < 2 && r < n) {
+  sk::floatx4_t sq = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) part[(size_t(slice) * 8 + 4 * q + rr) * npad + r] = y[rr];
+  for (int i = 0; i < SPW; ++i) {
+    uint4 a[4];
+    sk::floatx4_t sa = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      // select the input, then convert unconditionally (a select, not a branch)
+      const uint4 raw = live ? hx[i][u] : zero;
+      sq = sk::mfma(raw, raw, sq);
+      a[u] = scaled_operand(raw, wx[i][u]);
+      sa = sk::mfma(a[u], ones, sa);
+    }
+    sk::floatx4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    acc = sk::mfma(a[0], sk::b_operand<BITS, 0>(wc[i]), acc);
+    acc = sk::mfma(a[1], sk::b_operand<BITS, 1>(wc[i]), acc);
+    acc = sk::mfma(a[2], sk::b_operand<BITS, 2>(wc[i]), acc);
+    acc = sk::mfma(a[3], sk::b_operand<BITS, 3>(wc[i]), acc);
+    const float sc = u2f(hi ? (sw[i] & 0xffff0000u) : (sw[i] << 16));
+    const float bi = fmaf_(-off, sc, u2f(hi ? (bw[i] & 0xffff0000u) : (bw[i] << 16)));
+#pragma unroll
+    for (int r = 0; r < 4; ++r) y[r] = fmaf_(sc, acc[r], fmaf_(bi, sa[r], y[r]));
+  }
+  sk::join_parities(y);
+  if (q < 2) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave][4 * q + r][j] = y[r];
+  }
+  // sum of squares of row m: D[m][m] + D[m+8][m+8] of H H^T, held by lanes
+  // 16 (m / 4) + m and 16 (m / 4) + m + 40, element m % 4
+  const int e = j & 3;
+  const float dg = e == 0 ? sq[0] : e == 1 ? sq[1] : e == 2 ? sq[2] : sq[3];
+  const float dg2 = __shfl(dg, (lane + 40) & 63, 64);
+  if (j < 8 && q == (j >> 2)) sred[wave][j] = dg + dg2;
+  __syncthreads();
+  if (threadIdx.x < 128) {
+    const int mm = threadIdx.x >> 4, jj = threadIdx.x & 15;
+    float v = red[0][mm][jj];
+    for (int wv = 1; wv < waves; ++wv) v = v + red[wv][mm][jj];
+    const int r = tile * 16 + jj;
+    if (r < n) part[(size_t(stream) * 8 + mm) * npad + r] = v;
+    if (tile == 0 && jj == 0) {
+      float s2 = sred[0][mm];
+      for (int wv = 1; wv < waves; ++wv) s2 = s2 + sred[wv][mm];
+      ssq[stream * 8 + mm] = s2;
+    }
   }
 }
 
 // ---------------------------------------------------------------------------
-// n_down = rank (+ hc inject rows); rank % 256 == 0 is not required, but
-// rank <= 512 and rank % 128 == 0 (checked on the host).
-template <int BITS>
+// n_down = rank (+ hc inject rows); rank = 128 STEPS with STEPS 2 or 4.
+// hc == 4.
+template <int BITS, int STEPS>
 __global__ __launch_bounds__(1024) void hc_up_kernel(QWeight up, const float* __restrict__ part,
-                                                     int npad, int n_down, int rank, int M,
-                                                     int hidden, int hc,
-                                                     const uint16_t* __restrict__ xn,
+                                                     const float* __restrict__ ssq, int npad,
+                                                     int n_down, int rank, int M, int hidden,
+                                                     float eps, const uint16_t* __restrict__ h,
+                                                     const uint16_t* __restrict__ scale,
                                                      uint16_t* __restrict__ mixed,
                                                      uint16_t* __restrict__ inj) {
+  constexpr int HC = 4;
   extern __shared__ __align__(16) char lds[];
   __shared__ __align__(16) uint16_t lo[8 * 512];
   __shared__ float yt[8 * 64];
   const int tg = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane & 15;
-  const int steps = rank / sk::kSuper;
+  constexpr int steps = STEPS;
   const int G = rank >> 6;
-  // the up tiles (waves 0..3: stream t) prefetch their weights first
+  const int K = HC * hidden;
+  // 1. stream partials -> down outputs -> activation, one quad of 4 down rows
+  //    per thread (8 * npad / 4 <= 1024); the partial loads go out first
+  const int quads = npad / 4;
+  const int qi = min(int(threadIdx.x), 8 * quads - 1);
+  const int qm = qi / quads, qd = qi - qm * quads;
+  float4 pv[HC];
+  float sv[HC];
+#pragma unroll
+  for (int s = 0; s < HC; ++s) {
+    pv[s] = *reinterpret_cast<const float4*>(part + (size_t(s) * 8 + qm) * npad + 4 * qd);
+    sv[s] = ssq[s * 8 + qm];
+  }
+  // the up tiles (waves 0..3: stream t) prefetch their weights
   const int t = wave & 3;
   const int urow = t * hidden + min(tg * 16 + j, hidden - 1);
   const sk::DenseRows none{mixed, 0, 1};
@@ -209,32 +224,38 @@ __global__ __launch_bounds__(1024) void hc_up_kernel(QWeight up, const float* __
       up.biases + size_t(urow) * G, steps, 0, steps, 0, lds,
       reinterpret_cast<const float*>(lds + steps * sk::kStepBytes + sk::kZeroBytes), none, 1);
   if (wave < 4) st.prefetch();
-  // 1. partial sums -> activation (quads of 4 down rows per thread)
-  const int quads = npad / 4;
-  if (int(threadIdx.x) < 8 * quads) {
-    const int m = threadIdx.x / quads, qd = threadIdx.x - m * quads;
-    float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    float4 pv[kSlices];
+  // the mix inputs of this thread (threads < 128: row mm, column c)
+  const int mm = (threadIdx.x >> 4) & 7, cj = threadIdx.x & 15;
+  const int c = min(tg * 16 + cj, hidden - 1);
+  uint16_t hv[HC], wv[HC];
+  if (threadIdx.x < 128) {  // waves 0 and 1
 #pragma unroll
-    for (int i = 0; i < kSlices; ++i)
-      pv[i] = *reinterpret_cast<const float4*>(part + (size_t(i) * 8 + m) * npad + 4 * qd);
-#pragma unroll
-    for (int i = 0; i < kSlices; ++i) {
-      s.x = s.x + pv[i].x;
-      s.y = s.y + pv[i].y;
-      s.z = s.z + pv[i].z;
-      s.w = s.w + pv[i].w;
+    for (int s = 0; s < HC; ++s) {
+      hv[s] = h[size_t(mm < M ? mm : M - 1) * K + size_t(s) * hidden + c];
+      wv[s] = scale[size_t(s) * hidden + c];
     }
-    const float vals[4] = {s.x, s.y, s.z, s.w};
+  }
+  const float inv_hidden = 1.0f / float(hidden);
+  if (int(threadIdx.x) < 8 * quads) {
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int s = 0; s < HC; ++s) {
+      const float inv = __builtin_amdgcn_rsqf(fmaf_(sv[s], inv_hidden, eps));
+      acc.x = fmaf_(inv, pv[s].x, acc.x);
+      acc.y = fmaf_(inv, pv[s].y, acc.y);
+      acc.z = fmaf_(inv, pv[s].z, acc.z);
+      acc.w = fmaf_(inv, pv[s].w, acc.w);
+    }
+    const float vals[4] = {acc.x, acc.y, acc.z, acc.w};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int r = 4 * qd + k;
       if (r >= n_down) continue;
-      const float tt = round_bf16(round_bf16(vals[k]) / float(hc));
+      const float tt = round_bf16(round_bf16(vals[k]) * (1.0f / HC));
       if (r < rank) {
-        lo[m * rank + r] = m < M ? f32_to_bf16(tt * sigmoid_bf16(tt)) : uint16_t(0);
-      } else if (inj && tg == 0 && m < M) {
-        inj[size_t(m) * hc + (r - rank)] = f32_to_bf16(sigmoid_bf16(tt) * 2.0f);
+        lo[qm * rank + r] = qm < M ? f32_to_bf16(tt * sigmoid_fast(tt)) : uint16_t(0);
+      } else if (inj && tg == 0 && qm < M) {
+        inj[size_t(qm) * HC + (r - rank)] = f32_to_bf16(sigmoid_fast(tt) * 2.0f);
       }
     }
   }
@@ -243,12 +264,12 @@ __global__ __launch_bounds__(1024) void hc_up_kernel(QWeight up, const float* __
   // 2. stage lo (8 rows x rank) in operand order with its group sums
   {
     const int units = rank / 8;
-    const int i = threadIdx.x;  // 8 * units <= 512 <= 1024 threads
-    const bool live = i < 8 * units;
-    const int ic = live ? i : 0;
-    const int m = ic / units, u = ic - m * units;
-    const uint4 val = *reinterpret_cast<const uint4*>(lo + m * rank + u * 8);
-    if (int(threadIdx.x & ~63) < 8 * units) stage_unit(lds, steps, val, m, u, live);
+    const int i = threadIdx.x;  // 8 * units <= 512 <= 1024 threads, a multiple of 64
+    if (i < 8 * units) {        // uniform per wave
+      const int m = i & 7, u = i >> 3;
+      const uint4 val = *reinterpret_cast<const uint4*>(lo + m * rank + u * 8);
+      stage_unit(lds, steps, val, m, u);
+    }
   }
   __syncthreads();
   // 3. up tiles (waves 0..3) and the mix
@@ -263,56 +284,73 @@ __global__ __launch_bounds__(1024) void hc_up_kernel(QWeight up, const float* __
     }
   }
   __syncthreads();
-  if (threadIdx.x >= 128) return;
-  const int m = threadIdx.x >> 4, cj = threadIdx.x & 15;
-  const int c = tg * 16 + cj;
-  if (m >= M || c >= hidden) return;
+  if (threadIdx.x >= 128 || mm >= M || tg * 16 + cj >= hidden) return;
   float sum = 0.0f;
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const float p = round_bf16(yt[m * 64 + s * 16 + cj]);
-    const float x = bf16_to_f32(xn[size_t(m) * hc * hidden + size_t(s) * hidden + c]);
-    sum = sum + round_bf16(sigmoid_bf16(p) * x);
+  for (int s = 0; s < HC; ++s) {
+    const float inv = __builtin_amdgcn_rsqf(fmaf_(ssq[s * 8 + mm], inv_hidden, eps));
+    const float x = round_bf16((bf16_to_f32(hv[s]) * inv) * (bf16_to_f32(wv[s]) + 1.0f));
+    const float p = round_bf16(yt[mm * 64 + s * 16 + cj]);
+    sum = sum + round_bf16(sigmoid_fast(p) * x);
   }
-  mixed[size_t(m) * hidden + c] = f32_to_bf16(round_bf16(sum) / 4.0f);
+  mixed[size_t(mm) * hidden + c] = f32_to_bf16(round_bf16(sum) * 0.25f);
+}
+
+int down_waves(int hidden) {
+  const int sps = hidden / sk::kSuper;
+  return sps < kMaxDownWaves ? sps : kMaxDownWaves;
 }
 
 }  // namespace
 
 int hc_fused_npad(int n_down) { return ((n_down + 63) / 64) * 64; }
 size_t hc_fused_part_bytes(int n_down) {
-  return size_t(kSlices) * 8 * hc_fused_npad(n_down) * sizeof(float);
+  return (size_t(4) * 8 * hc_fused_npad(n_down) + 4 * 8) * sizeof(float);
 }
 
 bool hc_fused_supported(const QWeight& down, const QWeight& up, int hc, int hidden, int rank) {
-  const int slen = down.k / kSlices;
-  return hc == 4 && down.k == hc * hidden && hidden <= 2048 && slen % sk::kSuper == 0 &&
-         hidden % slen == 0 && down.group_size == 64 && up.group_size == 64 &&
-         down.k % 512 == 0 && down.bits == up.bits && up.k == rank && up.n == hc * hidden &&
-         rank % sk::kSuper == 0 && rank <= 512 && (rank % 512 == 0 || rank <= 1024) &&
-         rank % 256 == 0 && hc_fused_npad(down.n) * 2 <= 1024 &&
+  if (hc != 4 || hidden % sk::kSuper != 0 || hidden > 2048) return false;
+  const int sps = hidden / sk::kSuper;
+  const int spw = sps / down_waves(hidden);
+  return sps % down_waves(hidden) == 0 && (spw == 1 || spw == 2) && down.k == hc * hidden &&
+         down.group_size == 64 && up.group_size == 64 && down.bits == up.bits && up.k == rank &&
+         up.n == hc * hidden && rank % 256 == 0 && rank <= 512 &&
+         (down.n == rank || down.n == rank + hc) &&
+         hc_fused_npad(down.n) * 2 <= 1024 &&
          (down.bits == 4 || down.bits == 5 || down.bits == 6 || down.bits == 8);
 }
 
 int hc_fused(const QWeight& down, const QWeight& up, const uint16_t* h, const uint16_t* scale,
-             int M, int hc, int hidden, int rank, float eps, uint16_t* xn, float* part,
-             uint16_t* mixed, uint16_t* inj, hipStream_t s) {
+             int M, int hc, int hidden, int rank, float eps, float* part, uint16_t* mixed,
+             uint16_t* inj, hipStream_t s) {
   if (M < 1 || M > 8 || !hc_fused_supported(down, up, hc, hidden, rank)) return MX_EUNSUPPORTED;
   const int npad = hc_fused_npad(down.n);
-  const int steps = down.k / kSlices / sk::kSuper;
-  const dim3 g1((down.n + 63) / 64, kSlices);
-  const int lb1 = sk::stage_bytes(steps);
+  float* ssq = part + size_t(4) * 8 * npad;
+  const int waves = down_waves(hidden);
+  const int spw = (hidden / sk::kSuper) / waves;
+  const dim3 g1((down.n + 15) / 16, hc);
   const int lb2 = sk::stage_bytes(rank / sk::kSuper);
-  switch (down.bits) {
-#define MX_HC(B)                                                                               \
-  case B:                                                                                      \
-    hipLaunchKernelGGL(hc_down_kernel<B>, g1, dim3(256), lb1, s, down, h, scale, M, hidden, hc, \
-                       eps, xn, part, npad);                                                   \
-    hipLaunchKernelGGL(hc_up_kernel<B>, dim3((hidden + 15) / 16), dim3(1024), lb2, s, up, part, \
-                       npad, down.n, rank, M, hidden, hc, xn, mixed, inj);                     \
+  switch (down.bits * 4 + spw) {
+#define MX_HC(B, W)                                                                           \
+  case B * 4 + W:                                                                             \
+    hipLaunchKernelGGL((hc_down_kernel<B, W>), g1, dim3(64 * waves), 0, s, down, h, scale, M, \
+                       hidden, part, ssq, npad);                                              \
     break;
-    MX_HC(4) MX_HC(5) MX_HC(6) MX_HC(8)
+    MX_HC(4, 1) MX_HC(4, 2) MX_HC(5, 1) MX_HC(5, 2) MX_HC(6, 1) MX_HC(6, 2) MX_HC(8, 1)
+    MX_HC(8, 2)
 #undef MX_HC
+    default: return MX_EUNSUPPORTED;
+  }
+  const dim3 g2((hidden + 15) / 16);
+  switch (down.bits * 8 + rank / sk::kSuper) {
+#define MX_UP(B, S)                                                                           \
+  case B * 8 + S:                                                                             \
+    hipLaunchKernelGGL((hc_up_kernel<B, S>), g2, dim3(1024), lb2, s, up, part, ssq, npad,       \
+                       down.n, rank, M, hidden, eps, h, scale, mixed, inj);                   \
+    break;
+    MX_UP(4, 2) MX_UP(4, 4) MX_UP(5, 2) MX_UP(5, 4) MX_UP(6, 2) MX_UP(6, 4) MX_UP(8, 2)
+    MX_UP(8, 4)
+#undef MX_UP
     default: return MX_EUNSUPPORTED;
   }
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;

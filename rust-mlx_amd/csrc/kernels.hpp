@@ -78,8 +78,8 @@ int skinny_head(const QWeight& w, const uint16_t* x, int m, float* maxima, uint3
 bool hc_fused_supported(const QWeight& down, const QWeight& up, int hc, int hidden, int rank);
 size_t hc_fused_part_bytes(int n_down);
 int hc_fused(const QWeight& down, const QWeight& up, const uint16_t* h, const uint16_t* scale,
-             int M, int hc, int hidden, int rank, float eps, uint16_t* xn, float* part,
-             uint16_t* mixed, uint16_t* inj, hipStream_t s);
+             int M, int hc, int hidden, int rank, float eps, float* part, uint16_t* mixed,
+             uint16_t* inj, hipStream_t s);
 int hc_norm(const uint16_t* x, const uint16_t* scale, int rows, int hc, int hidden, float eps,
             uint16_t* y, hipStream_t s);
 int embed(const QWeight& w, const uint32_t* ids, int count, int hc, uint16_t* out, hipStream_t s);

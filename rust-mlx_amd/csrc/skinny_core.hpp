@@ -171,29 +171,31 @@ struct RouteRows {
 // Stages, for the workgroup's super-steps [ks0, ks0 + steps) of K-long rows:
 // the x tile in operand order, the zero block and the group sums of x (fp32
 // [group][m] after the zero block).  Rows past the first M stage as zeros.
-// load() issues every global load of the staging (unconditionally, at clamped
-// indices); store() waits for them, sums each 64-value group across the 8
-// lanes that hold it, writes LDS and ends with a barrier.  Loads issued between
-// the two (the weight prefetch) stay in flight, because the hardware retires
-// loads in order and store() only needs the older ones.  One pass covers
-// NT * PER 16-byte units; the staging must fit one pass.
+// Unit i (16 bytes) of the staging is value unit u = i / 8 of row m = i % 8,
+// so the 64 lanes of a wave hold the eight units of one 64-value group for
+// all eight rows: their LDS stores spread over the banks (consecutive lanes
+// write different rows), and each group's sum is a butterfly over lanes 8
+// apart.  load() issues every global load of the staging (unconditionally:
+// rows past M load row M - 1, whose address the wave already touches);
+// store() waits for them, writes LDS and ends with a barrier.  Loads issued
+// between the two (the weight prefetch) stay in flight, because the hardware
+// retires loads in order and store() only needs the older ones.  One pass
+// covers NT * PER 16-byte units; the staging must fit one pass.
 template <int NT, int PER, class Rows>
 struct Stager {
   const Rows& xr;
-  int ks0, steps, units, total, live_total;
+  int live, ks0, steps, total;
   uint4 v[PER];
 
   // M: rows xr(0..M-1) exist (the others stage as zeros and are not loaded).
   __device__ __forceinline__ Stager(const Rows& r, int M, int k0, int n)
-      : xr(r), ks0(k0), steps(n), units(n * 16), total(8 * n * 16), live_total(M * n * 16) {}
+      : xr(r), live(M), ks0(k0), steps(n), total(8 * n * 16) {}
 
   __device__ __forceinline__ void load() {
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
-      // indices past the live rows repeat the last live unit: one address for
-      // the whole wave, so they cost the memory pipeline almost nothing
-      const int i = min(int(threadIdx.x) + k * NT, live_total - 1);
-      const int m = i / units, u = i - m * units;
+      const int i = min(int(threadIdx.x) + k * NT, total - 1);
+      const int m = min(i & 7, live - 1), u = i >> 3;
       v[k] = *reinterpret_cast<const uint4*>(xr(m) + size_t(ks0) * kSuper + u * 8);
     }
   }
@@ -206,23 +208,19 @@ struct Stager {
     for (int k = 0; k < PER; ++k) {
       if (k * NT >= total) break;  // uniform
       const int i = int(threadIdx.x) + k * NT;
-      const bool in = i < total;
-      const int ic = in ? i : total - 1;
-      const int m = ic / units, u = ic - m * units;
-      const uint4 val = ic < live_total ? v[k] : make_uint4(0, 0, 0, 0);
+      if (i - int(threadIdx.x & 63) >= total) break;  // uniform per wave (total % 64 == 0)
+      const int m = i & 7, u = i >> 3;
+      const uint4 val = m < live ? v[k] : make_uint4(0, 0, 0, 0);
       const uint32_t d[4] = {val.x, val.y, val.z, val.w};
       float sum = 0.0f;
 #pragma unroll
       for (int h = 0; h < 4; ++h) sum = sum + u2f(d[h] << 16) + u2f(d[h] & 0xffff0000u);
-      // lanes 8c .. 8c+7 hold the eight units of one group (total % 8 == 0)
-      sum = sum + __shfl_xor(sum, 1, 64);
-      sum = sum + __shfl_xor(sum, 2, 64);
-      sum = sum + __shfl_xor(sum, 4, 64);
-      if (in) {
-        if ((u & 7) == 0) sx[(u >> 3) * 8 + m] = sum;
-        const int s = u >> 4, o = u & 15;
-        xs[(s * 4 + (o & 3)) * 32 + (o >> 2) * 8 + m] = permute_x(val);
-      }
+      sum = sum + __shfl_xor(sum, 8, 64);
+      sum = sum + __shfl_xor(sum, 16, 64);
+      sum = sum + __shfl_xor(sum, 32, 64);
+      if ((u & 7) == 0) sx[(u >> 3) * 8 + m] = sum;
+      const int s = u >> 4, o = u & 15;
+      xs[(s * 4 + (o & 3)) * 32 + (o >> 2) * 8 + m] = permute_x(val);
     }
     uint2* zero = reinterpret_cast<uint2*>(lds + xbytes);
     for (int t = threadIdx.x; t < kZeroBytes / 8; t += NT) zero[t] = make_uint2(0, 0);
