@@ -380,6 +380,63 @@ __global__ __launch_bounds__(kMaxHd) void combine_kernel(const float* __restrict
   out[(size_t(row) * d.heads + h) * hd + t] = f32_to_bf16(attn * sigmoid_bf16(gate));
 }
 
+// Fast-mode combine (matrix-core decode partials, 64-position chunks): the
+// chunk weights w_c = e^(m_c - M) are formed once per chunk by threads c and
+// shared through LDS (hardware exp2); L = sum_c l_c w_c as a block sum;
+// O[d] = sum_c o_c[d] w_c (fma, c ascending); y = bf16(bf16(O / L) * sigmoid(gate)).
+// chunks <= 256 (max_ctx <= 16384, checked on the host).
+__global__ __launch_bounds__(256) void combine_fast_kernel(const float* __restrict__ o_part,
+                                                           const float* __restrict__ ml_part,
+                                                           const uint16_t* __restrict__ qkv,
+                                                           int64_t qkv_stride,
+                                                           const int32_t* __restrict__ pos,
+                                                           AttnDims d, int max_chunks,
+                                                           uint16_t* __restrict__ out) {
+  __shared__ float wsh[256];
+  __shared__ float red[2][4];
+  const int h = blockIdx.x;
+  const int row = blockIdx.y;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int hd = d.head_dim;
+  const int chunks = (pos[row] + kAttnFastChunk) / kAttnFastChunk;
+  const float* ml = ml_part + (size_t(row) * d.heads + h) * max_chunks * 2;
+  const float* op = o_part + (size_t(row) * d.heads + h) * max_chunks * hd + min(t, hd - 1);
+  const float gate =
+      bf16_to_f32(qkv[size_t(row) * qkv_stride + size_t(h) * 2 * hd + hd + min(t, hd - 1)]);
+  const float mc = t < chunks ? ml[2 * t] : u2f(0xff800000u);
+  const float lc = t < chunks ? ml[2 * t + 1] : 0.0f;
+  float m = mc;
+  for (int o = 32; o > 0; o >>= 1) {
+    const float v = __shfl_xor(m, o, 64);
+    m = v > m ? v : m;
+  }
+  if (lane == 0) red[0][wave] = m;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+  const float wc = t < chunks ? __builtin_amdgcn_exp2f((mc - M) * 1.4426950408889634f) : 0.0f;
+  wsh[t] = wc;
+  float l = lc * wc;
+  for (int o = 32; o > 0; o >>= 1) l = l + __shfl_xor(l, o, 64);
+  if (lane == 0) red[1][wave] = l;
+  __syncthreads();
+  if (t >= hd) return;
+  const float L = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+  float O = 0.0f;
+  int c = 0;
+  for (; c + 4 <= chunks; c += 4) {
+    const float a0 = op[size_t(c) * hd], a1 = op[size_t(c + 1) * hd];
+    const float a2 = op[size_t(c + 2) * hd], a3 = op[size_t(c + 3) * hd];
+    O = fmaf_(a0, wsh[c], O);
+    O = fmaf_(a1, wsh[c + 1], O);
+    O = fmaf_(a2, wsh[c + 2], O);
+    O = fmaf_(a3, wsh[c + 3], O);
+  }
+  for (; c < chunks; ++c) O = fmaf_(op[size_t(c) * hd], wsh[c], O);
+  const float attn = round_bf16(O * __builtin_amdgcn_rcpf(L));
+  const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gate * 1.4426950408889634f));
+  out[(size_t(row) * d.heads + h) * hd + t] = f32_to_bf16(attn * sg);
+}
+
 }  // namespace
 
 int attn_prep(const uint16_t* qkv, int64_t qkv_stride, int rows, const int32_t* slots,
@@ -397,7 +454,7 @@ bool attn_fast_supported(AttnDims d) {
   if (d.kv_heads <= 0 || d.heads % d.kv_heads != 0) return false;
   const int g = d.heads / d.kv_heads;
   return (d.head_dim == 128 || d.head_dim == 256) && (g == 1 || g == 2 || g == 4 || g == 8) &&
-         d.slot_stride % 8 == 0;
+         d.slot_stride % 8 == 0 && d.max_ctx <= 256 * kAttnFastChunk;
 }
 
 int attn_decode(const uint16_t* q, int rows, const int32_t* slots, const int32_t* pos,
@@ -441,8 +498,14 @@ int attn_decode(const uint16_t* q, int rows, const int32_t* slots, const int32_t
 int attn_combine(const float* o_part, const float* ml_part, const uint16_t* qkv,
                  int64_t qkv_stride, int rows, const int32_t* pos, AttnDims d, int max_chunks,
                  bool fast, uint16_t* out, hipStream_t s) {
-  hipLaunchKernelGGL(combine_kernel, dim3(d.heads, rows), dim3(kMaxHd), 0, s, o_part, ml_part,
-                     qkv, qkv_stride, pos, d, max_chunks, fast ? kAttnFastChunk : kAttnChunk, out);
+  if (fast) {
+    if ((d.max_ctx + kAttnFastChunk - 1) / kAttnFastChunk > 256) return MX_EUNSUPPORTED;
+    hipLaunchKernelGGL(combine_fast_kernel, dim3(d.heads, rows), dim3(256), 0, s, o_part,
+                       ml_part, qkv, qkv_stride, pos, d, max_chunks, out);
+  } else {
+    hipLaunchKernelGGL(combine_kernel, dim3(d.heads, rows), dim3(kMaxHd), 0, s, o_part, ml_part,
+                       qkv, qkv_stride, pos, d, max_chunks, kAttnChunk, out);
+  }
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 

@@ -288,6 +288,158 @@ __global__ __launch_bounds__(256 * KS, 2) void gate_up_kernel(
   h[(size_t(xr.row(m)) * (top_k + 1) + xr.slot(m)) * hs + i] = f32_to_bf16(silu * uv);
 }
 
+// ---------------------------------------------------------------------------
+// Persistent gate/up + SwiGLU over the distinct experts of a step.
+//
+// Every workgroup (4 waves) stages all rows of x once, and builds in LDS the
+// list of distinct experts named by the routes (first route naming an expert
+// leads; each leader carries a row mask and the slot of every member row) plus
+// the shared expert.  Work items are (list entry, 32-column group); workgroup
+// w takes items w, w + P, w + 2P, ... and loads the next item's weights
+// before it computes the current one, so the memory system keeps streaming
+// while the matrix cores and VALUs work.  Waves 2 t and 2 t + 1 compute tile t
+// of the item (0, 1: gate rows 32 g + 16 t + j; 2, 3: the same up rows), one
+// half of the depth each, for all eight staged rows; only member rows are
+// written:
+// h[row][slot][i] = bf16(bf16(silu(bf16 g)) * bf16 u), silu with the hardware
+// exp2 / reciprocal.
+constexpr int kPersistMaxExperts = 512;
+constexpr int kPersistMaxRoutes = 128;
+
+__device__ __forceinline__ float sigmoid_fast(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
+}
+
+// Builds the leader list (lead_e: expert or -1 for the shared expert;
+// lead_info: bit m = row m is a member, bits 8 + 5 m .. : its slot).  Returns
+// the entry count.  Ends with a barrier.
+__device__ __forceinline__ int build_leaders(const uint32_t* __restrict__ ids, int rows,
+                                             int top_k, int experts, int* first,
+                                             unsigned long long* info, int* lead_e,
+                                             unsigned long long* lead_info, int* count) {
+  const int routes = rows * top_k;
+  for (int e = threadIdx.x; e < experts; e += blockDim.x) {
+    first[e] = 0x7fffffff;
+    info[e] = 0ull;
+  }
+  __syncthreads();
+  if (int(threadIdx.x) < routes) {
+    const int u = threadIdx.x;
+    const int e = int(min(ids[u], uint32_t(experts - 1)));
+    const int row = u / top_k, slot = u - row * top_k;
+    atomicMin(&first[e], u);
+    atomicOr(&info[e], (1ull << row) | (static_cast<unsigned long long>(slot) << (8 + 5 * row)));
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    int base = 0;
+    for (int u0 = 0; u0 < routes; u0 += 64) {
+      const int u = u0 + lane;
+      const int e = u < routes ? int(min(ids[u], uint32_t(experts - 1))) : 0;
+      const bool lead = u < routes && first[e] == u;
+      const uint64_t bal = __ballot(lead);
+      if (lead) {
+        const int pos = base + __popcll(bal & ((1ull << lane) - 1ull));
+        lead_e[pos] = e;
+        lead_info[pos] = info[e];
+      }
+      base += __popcll(bal);
+    }
+    if (lane == 0) {
+      unsigned long long all = 0;
+      for (int m = 0; m < rows; ++m)
+        all |= (1ull << m) | (static_cast<unsigned long long>(top_k) << (8 + 5 * m));
+      lead_e[base] = -1;
+      lead_info[base] = all;
+      *count = base + 1;
+    }
+  }
+  __syncthreads();
+  return *count;
+}
+
+template <int BITS, int STEPS>
+__global__ __launch_bounds__(512) void gate_up_persist_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ ids, int rows, int top_k,
+    QBank gate, QBank up, QWeight sgate, QWeight sup, uint16_t* __restrict__ h, int hs) {
+  constexpr int KS = 2;  // waves per tile: each takes half of the depth
+  extern __shared__ __align__(16) char lds[];
+  __shared__ int first[kPersistMaxExperts];
+  __shared__ unsigned long long info[kPersistMaxExperts];
+  __shared__ int lead_e[kPersistMaxRoutes + 1];
+  __shared__ unsigned long long lead_info[kPersistMaxRoutes + 1];
+  __shared__ int count;
+  __shared__ float red[KS * 4 * 8 * 16];
+  __shared__ float yt[8 * 64];
+  constexpr int steps = STEPS;  // hidden = 128 STEPS
+  constexpr int hidden = STEPS * sk::kSuper;
+  constexpr int G = hidden / 64;
+  constexpr int xbytes = steps * sk::kStepBytes;
+  const int inter = gate.n;
+  const float* sx = reinterpret_cast<const float*>(lds + xbytes + sk::kZeroBytes);
+  const sk::DenseRows xr{x, hidden, rows};
+  sk::Stager<512, sk::stage_per(512, STEPS), sk::DenseRows> stg(xr, rows, 0, steps);
+  stg.load();
+  const int nlead =
+      build_leaders(ids, rows, top_k, gate.experts, first, info, lead_e, lead_info, &count);
+  stg.store(lds);
+  const int groups = inter / 32;
+  const int items = nlead * groups;
+  const int P = gridDim.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane & 15;
+  const int t = wave / KS, ks = wave - t * KS;
+  constexpr int n = steps / KS;
+  const int k0 = n * ks;
+  // weight rows of item `it` for this wave (tile t, depth half ks)
+  auto stream_for = [&](int it) {
+    const int lead = it / groups, g = it - lead * groups;
+    const int e = lead_e[lead];
+    const QWeight w = expert_weight(t < 2 ? gate : up, e, t < 2 ? sgate : sup);
+    const int row = g * 32 + (t & 1) * 16 + j;
+    return sk::Stream<BITS, false, sk::DenseRows, n, 16>(
+        w.codes + size_t(row) * (size_t(hidden) * BITS / 32), w.scales + size_t(row) * G,
+        w.biases + size_t(row) * G, steps, k0, n, 0, lds, sx, xr, rows);
+  };
+  auto finish = [&](int it, float (&y)[4]) {
+    reduce_tiles<4, KS>(y, red, yt);
+    const int lead = it / groups, g = it - lead * groups;
+    const unsigned long long inf = lead_info[lead];
+    if (threadIdx.x < 256) {
+      const int m = threadIdx.x >> 5, c = threadIdx.x & 31;
+      if ((inf >> m) & 1ull) {
+        const int slot = int((inf >> (8 + 5 * m)) & 31ull);
+        const float gv = round_bf16(yt[m * 64 + c]);
+        const float uv = round_bf16(yt[m * 64 + 32 + c]);
+        const float silu = round_bf16(gv * sigmoid_fast(gv));
+        h[(size_t(m) * (top_k + 1) + slot) * hs + g * 32 + c] = f32_to_bf16(silu * uv);
+      }
+    }
+    __syncthreads();
+  };
+  if (int(blockIdx.x) >= items) return;  // uniform
+  auto sa = stream_for(blockIdx.x);
+  sa.prefetch();
+  for (int it = blockIdx.x; it < items; it += 2 * P) {
+    const int ib = it + P;
+    // the next item's weights (this item again when there is none: its lines
+    // are in the cache, and the loads stay unconditional)
+    auto sb = stream_for(ib < items ? ib : it);
+    sb.prefetch();
+    float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    sa.run(xbytes, y);
+    finish(it, y);
+    const int ia = it + 2 * P;
+    sa = stream_for(ia < items ? ia : (ib < items ? ib : it));
+    sa.prefetch();
+    if (ib < items) {
+      float yb[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      sb.run(xbytes, yb);
+      finish(ib, yb);
+    }
+  }
+}
+
 // down + score: p[row][slot][n] = bf16(bf16(down) * score) (routed slots) or
 // bf16(down) (the shared slot, top_k).
 template <int BITS>
@@ -499,8 +651,38 @@ int skinny_gate_up(const uint16_t* x, const uint32_t* ids, int rows, int top_k,
       gate.k % 512 != 0 || steps > kStageSteps || up.bits != gate.bits ||
       sgate.bits != gate.bits || sup.bits != gate.bits || sgate.k != gate.k)
     return MX_EUNSUPPORTED;
-  const dim3 grid((hs + 31) / 32, rows * top_k + 1);
   const int lb = sk::stage_bytes(steps);
+  if (gate.experts <= kPersistMaxExperts && rows * top_k <= kPersistMaxRoutes &&
+      sgate.n == gate.n && up.n == gate.n && gate.n % 32 == 0 && steps == kStageSteps) {
+    // one workgroup per resident slot: every workgroup is on the chip from the start
+    static int slots[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
+    const void* fn = nullptr;
+    switch (gate.bits) {
+      case 4: fn = reinterpret_cast<const void*>(gate_up_persist_kernel<4, kStageSteps>); break;
+      case 5: fn = reinterpret_cast<const void*>(gate_up_persist_kernel<5, kStageSteps>); break;
+      case 6: fn = reinterpret_cast<const void*>(gate_up_persist_kernel<6, kStageSteps>); break;
+      default: fn = reinterpret_cast<const void*>(gate_up_persist_kernel<8, kStageSteps>); break;
+    }
+    int& grid_n = slots[gate.bits];
+    if (grid_n == 0) {
+      int dev = 0, cus = 0, per_cu = 0;
+      if (hipGetDevice(&dev) != hipSuccess ||
+          hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+          hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 512, lb) != hipSuccess ||
+          cus <= 0 || per_cu <= 0)
+        return MX_EHIP;
+      grid_n = cus * per_cu;
+    }
+    const dim3 pgrid(grid_n);
+    switch (gate.bits) {
+      case 4: hipLaunchKernelGGL((gate_up_persist_kernel<4, kStageSteps>), pgrid, dim3(512), lb, s, x, ids, rows, top_k, gate, up, sgate, sup, h, hs); break;
+      case 5: hipLaunchKernelGGL((gate_up_persist_kernel<5, kStageSteps>), pgrid, dim3(512), lb, s, x, ids, rows, top_k, gate, up, sgate, sup, h, hs); break;
+      case 6: hipLaunchKernelGGL((gate_up_persist_kernel<6, kStageSteps>), pgrid, dim3(512), lb, s, x, ids, rows, top_k, gate, up, sgate, sup, h, hs); break;
+      default: hipLaunchKernelGGL((gate_up_persist_kernel<8, kStageSteps>), pgrid, dim3(512), lb, s, x, ids, rows, top_k, gate, up, sgate, sup, h, hs); break;
+    }
+    return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+  }
+  const dim3 grid((hs + 31) / 32, rows * top_k + 1);
 #define MX_GU(B) \
   case B: hipLaunchKernelGGL((gate_up_kernel<B, kGateUpSplit>), grid, dim3(256 * kGateUpSplit), lb, s, x, ids, rows, top_k, gate, up, sgate, sup, h, hs); break;
   switch (gate.bits) {

@@ -119,11 +119,16 @@ template <int BITS, int U>
 __device__ __forceinline__ uint4 b_operand(const uint32_t (&w)[BITS]) {
   uint4 r;
   if constexpr (BITS == 4) {
+    // nibbles as bytes (lo: n0 n2 n4 n6, hi: n1 n3 n5 n7), then one byte
+    // permute per operand word places two of them under 0x43 high bytes
     const uint32_t x = w[U];
-    r.x = (x & 0x000F000Fu) | 0x43004300u;
-    r.y = ((x >> 4) & 0x000F000Fu) | 0x43004300u;
-    r.z = ((x >> 8) & 0x000F000Fu) | 0x43004300u;
-    r.w = ((x >> 12) & 0x000F000Fu) | 0x43004300u;
+    const uint32_t lo = x & 0x0F0F0F0Fu;
+    const uint32_t hi = (x >> 4) & 0x0F0F0F0Fu;
+    constexpr uint32_t c43 = 0x43434343u;
+    r.x = __builtin_amdgcn_perm(lo, c43, 0x00060004u);  // n0, n4
+    r.y = __builtin_amdgcn_perm(hi, c43, 0x00060004u);  // n1, n5
+    r.z = __builtin_amdgcn_perm(lo, c43, 0x00070005u);  // n2, n6
+    r.w = __builtin_amdgcn_perm(hi, c43, 0x00070005u);  // n3, n7
   } else if constexpr (BITS == 8) {
     const uint32_t lo = w[2 * U], hi = w[2 * U + 1];
     auto pair = [](float a, float b) { return __builtin_amdgcn_perm(f2u(b), f2u(a), 0x07060302u); };
@@ -273,6 +278,7 @@ struct Stream {
   uint32_t wa[B][BITS], wb[B][BITS];
   uint4 xa[XREG ? B : 1][4], xb[XREG ? B : 1][4];
   int j, q, xoff, zoff;
+  uint32_t half_sel;  // byte permute that moves this lane's group half to the top
   bool act;
 
   // rs: super-steps in the whole row (K / 128, a multiple of SQ).
@@ -284,6 +290,7 @@ struct Stream {
     j = lane & 15;
     q = lane >> 4;
     base = ks0 - ks0 % SQ;
+    half_sel = (q >> 1) ? 0x07060c0cu : 0x05040c0cu;
     act = (j < 8) == (q < 2);
     xoff = (q * 8 + (j & 7)) * 16;
     xlive = false;
@@ -352,8 +359,8 @@ struct Stream {
         acc = mfma(a[1], b_operand<BITS, 1>(w[i]), acc);
         acc = mfma(a[2], b_operand<BITS, 2>(w[i]), acc);
         acc = mfma(a[3], b_operand<BITS, 3>(w[i]), acc);
-        const float sc = u2f(hi ? (sw & 0xffff0000u) : (sw << 16));
-        const float bi = fmaf_(-off, sc, u2f(hi ? (bw & 0xffff0000u) : (bw << 16)));
+        const float sc = u2f(__builtin_amdgcn_perm(sw, sw, half_sel));
+        const float bi = fmaf_(-off, sc, u2f(__builtin_amdgcn_perm(bw, bw, half_sel)));
 #pragma unroll
         for (int r = 0; r < 4; ++r) y[r] = fmaf_(sc, acc[r], fmaf_(bi, sv[r], y[r]));
       }
