@@ -86,20 +86,27 @@ __global__ __launch_bounds__(64) void route_kernel(const uint16_t* __restrict__ 
     for (int i = 0; i < PER; ++i)
       if (key[i] == best) key[i] = 0u;  // keys are unique; real keys are never 0
   }
-  if (lane == 0) {
-    float picked[16];
-    float total = 0.0f;
-    for (int j = 0; j < top_k; ++j) {
-      const uint32_t k16 = sel[j] >> 16;
-      const uint32_t g = (k16 & 0x8000u) ? (k16 & 0x7fffu) : (~k16 & 0xffffu);
-      picked[j] = bf16_to_f32(uint16_t(g));
-      ids[size_t(row) * top_k + j] = sel[j] & 0xffffu;
-      total = round_bf16(picked[j] + total);  // one bf16 add per slot, ascending
+  // every lane holds the selection: the renormalising total is formed in all
+  // lanes (one bf16 add per slot, ascending), then lane j writes slot j
+  float total = 0.0f;
+  float mine = 0.0f;
+  uint32_t mine_id = 0;
+  for (int j = 0; j < top_k; ++j) {
+    const uint32_t k16 = sel[j] >> 16;
+    const uint32_t g = (k16 & 0x8000u) ? (k16 & 0x7fffu) : (~k16 & 0xffffu);
+    const float picked = bf16_to_f32(uint16_t(g));
+    total = round_bf16(picked + total);
+    if (j == lane) {
+      mine = picked;
+      mine_id = sel[j] & 0xffffu;
     }
-    for (int j = 0; j < top_k; ++j)
-      scores[size_t(row) * top_k + j] = f32_to_bf16(picked[j] / total);
-    factor[row] = f32_to_bf16(sigmoid_bf16(bf16_to_f32(shared_logit[size_t(row) * shared_stride])));
   }
+  if (lane < top_k) {
+    ids[size_t(row) * top_k + lane] = mine_id;
+    scores[size_t(row) * top_k + lane] = f32_to_bf16(mine / total);
+  }
+  if (lane == 0)
+    factor[row] = f32_to_bf16(sigmoid_bf16(bf16_to_f32(shared_logit[size_t(row) * shared_stride])));
 }
 
 // ---------------------------------------------------------------------------
@@ -369,6 +376,68 @@ __global__ __launch_bounds__(256) void moe_reduce_epilogue_kernel(
            residual + o, gate + size_t(row) * hc, hc, hidden, out + o);
 }
 
+// The same arithmetic for 4 consecutive columns per thread, with every load
+// issued before the first add (slot values for k <= 15 at clamped slot
+// indices, the shared slot, residual and gates); hc == 4.
+constexpr int kRedMaxK = 16;
+__global__ __launch_bounds__(256) void moe_reduce_epilogue4_kernel(
+    const uint16_t* __restrict__ p, const uint16_t* __restrict__ factor,
+    const uint16_t* __restrict__ residual, const uint16_t* __restrict__ gate, int top_k,
+    int hidden, uint16_t* __restrict__ out) {
+  constexpr int HC = 4;
+  const int row = blockIdx.y;
+  const int c = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (c >= hidden) return;
+  const uint16_t* pr = p + size_t(row) * (top_k + 1) * hidden + c;
+  uint2 pv[kRedMaxK];
+#pragma unroll
+  for (int sl = 0; sl < kRedMaxK; ++sl)
+    pv[sl] = *reinterpret_cast<const uint2*>(pr + size_t(sl < top_k ? sl : top_k) * hidden);
+  const uint2 sh = *reinterpret_cast<const uint2*>(pr + size_t(top_k) * hidden);
+  const size_t o = size_t(row) * HC * hidden + c;
+  uint2 rv[HC];
+  float gv[HC];
+#pragma unroll
+  for (int s2 = 0; s2 < HC; ++s2) {
+    rv[s2] = *reinterpret_cast<const uint2*>(residual + o + size_t(s2) * hidden);
+    gv[s2] = bf16_to_f32(gate[size_t(row) * HC + s2]);
+  }
+  const float f = bf16_to_f32(factor[row]);
+  const int lanes = top_k < 8 ? top_k : 8;
+  uint16_t res[HC][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    auto col = [&](const uint2& v) {
+      return bf16_to_f32(uint16_t(i < 2 ? (v.x >> (16 * i)) : (v.y >> (16 * (i - 2)))));
+    };
+    // slot_sum with compile-time register indices (predicated by top_k)
+    float acc[8];
+#pragma unroll
+    for (int a = 0; a < 8; ++a) {
+      float v = col(pv[a]);
+      if (a + 8 < top_k) v = round_bf16(v + col(pv[a + 8]));
+      acc[a] = v;
+    }
+    float routed = acc[0];
+#pragma unroll
+    for (int a = 1; a < 8; ++a)
+      if (a < lanes) routed = round_bf16(acc[a] + routed);
+    routed = round_bf16(routed);
+    const float weighted = round_bf16(col(sh) * f);
+    const float combined = round_bf16(routed + weighted);
+#pragma unroll
+    for (int s2 = 0; s2 < HC; ++s2) {
+      const float inj = round_bf16(combined * gv[s2]);
+      res[s2][i] = f32_to_bf16(col(rv[s2]) + inj);
+    }
+  }
+#pragma unroll
+  for (int s2 = 0; s2 < HC; ++s2)
+    *reinterpret_cast<uint2*>(out + o + size_t(s2) * hidden) =
+        make_uint2(uint32_t(res[s2][0]) | (uint32_t(res[s2][1]) << 16),
+                   uint32_t(res[s2][2]) | (uint32_t(res[s2][3]) << 16));
+}
+
 }  // namespace
 
 int moe_route(const uint16_t* logits, int64_t logit_stride, const uint16_t* shared_logit,
@@ -471,6 +540,12 @@ int moe_hc_epilogue(const uint16_t* routed, const uint16_t* shared, const uint16
 int moe_reduce_hc_epilogue(const uint16_t* p, const uint16_t* factor, const uint16_t* residual,
                            const uint16_t* gate, int rows, int top_k, int hc, int hidden,
                            uint16_t* out, hipStream_t s) {
+  if (hc == 4 && top_k < kRedMaxK && hidden % 4 == 0) {
+    const dim3 grid4((hidden / 4 + 63) / 64, rows);
+    hipLaunchKernelGGL(moe_reduce_epilogue4_kernel, grid4, dim3(64), 0, s, p, factor, residual,
+                       gate, top_k, hidden, out);
+    return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+  }
   const dim3 grid((hidden + 255) / 256, rows);
   hipLaunchKernelGGL(moe_reduce_epilogue_kernel, grid, dim3(256), 0, s, p, factor, residual, gate,
                      top_k, hc, hidden, out);

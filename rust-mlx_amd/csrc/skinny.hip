@@ -304,6 +304,7 @@ __global__ __launch_bounds__(256 * KS, 2) void gate_up_kernel(
 // h[row][slot][i] = bf16(bf16(silu(bf16 g)) * bf16 u), silu with the hardware
 // exp2 / reciprocal.
 constexpr int kPersistMaxExperts = 512;
+
 constexpr int kPersistMaxRoutes = 128;
 
 __device__ __forceinline__ float sigmoid_fast(float x) {
@@ -313,10 +314,12 @@ __device__ __forceinline__ float sigmoid_fast(float x) {
 // Builds the leader list (lead_e: expert or -1 for the shared expert;
 // lead_info: bit m = row m is a member, bits 8 + 5 m .. : its slot).  Returns
 // the entry count.  Ends with a barrier.
-__device__ __forceinline__ int build_leaders(const uint32_t* __restrict__ ids, int rows,
-                                             int top_k, int experts, int* first,
-                                             unsigned long long* info, int* lead_e,
-                                             unsigned long long* lead_info, int* count) {
+// my_id: ids[threadIdx.x] for threads below rows * top_k (loaded by the caller
+// at kernel start).  route_e: LDS [kPersistMaxRoutes] for the clamped ids.
+__device__ __forceinline__ int build_leaders(uint32_t my_id, int rows, int top_k, int experts,
+                                             int* first, unsigned long long* info, int* route_e,
+                                             int* lead_e, unsigned long long* lead_info,
+                                             int* count) {
   const int routes = rows * top_k;
   for (int e = threadIdx.x; e < experts; e += blockDim.x) {
     first[e] = 0x7fffffff;
@@ -325,8 +328,9 @@ __device__ __forceinline__ int build_leaders(const uint32_t* __restrict__ ids, i
   __syncthreads();
   if (int(threadIdx.x) < routes) {
     const int u = threadIdx.x;
-    const int e = int(min(ids[u], uint32_t(experts - 1)));
+    const int e = int(min(my_id, uint32_t(experts - 1)));
     const int row = u / top_k, slot = u - row * top_k;
+    route_e[u] = e;
     atomicMin(&first[e], u);
     atomicOr(&info[e], (1ull << row) | (static_cast<unsigned long long>(slot) << (8 + 5 * row)));
   }
@@ -336,7 +340,7 @@ __device__ __forceinline__ int build_leaders(const uint32_t* __restrict__ ids, i
     int base = 0;
     for (int u0 = 0; u0 < routes; u0 += 64) {
       const int u = u0 + lane;
-      const int e = u < routes ? int(min(ids[u], uint32_t(experts - 1))) : 0;
+      const int e = u < routes ? route_e[u] : 0;
       const bool lead = u < routes && first[e] == u;
       const uint64_t bal = __ballot(lead);
       if (lead) {
@@ -367,6 +371,7 @@ __global__ __launch_bounds__(512) void gate_up_persist_kernel(
   extern __shared__ __align__(16) char lds[];
   __shared__ int first[kPersistMaxExperts];
   __shared__ unsigned long long info[kPersistMaxExperts];
+  __shared__ int route_e[kPersistMaxRoutes];
   __shared__ int lead_e[kPersistMaxRoutes + 1];
   __shared__ unsigned long long lead_info[kPersistMaxRoutes + 1];
   __shared__ int count;
@@ -379,11 +384,12 @@ __global__ __launch_bounds__(512) void gate_up_persist_kernel(
   const int inter = gate.n;
   const float* sx = reinterpret_cast<const float*>(lds + xbytes + sk::kZeroBytes);
   const sk::DenseRows xr{x, hidden, rows};
+  // route ids first (the expert list needs them), then the x staging loads
+  const uint32_t my_id = ids[min(int(threadIdx.x), rows * top_k - 1)];
   sk::Stager<512, sk::stage_per(512, STEPS), sk::DenseRows> stg(xr, rows, 0, steps);
   stg.load();
-  const int nlead =
-      build_leaders(ids, rows, top_k, gate.experts, first, info, lead_e, lead_info, &count);
-  stg.store(lds);
+  const int nlead = build_leaders(my_id, rows, top_k, gate.experts, first, info, route_e, lead_e,
+                                  lead_info, &count);
   const int groups = inter / 32;
   const int items = nlead * groups;
   const int P = gridDim.x;
@@ -418,8 +424,10 @@ __global__ __launch_bounds__(512) void gate_up_persist_kernel(
     __syncthreads();
   };
   if (int(blockIdx.x) >= items) return;  // uniform
+  // the first item's weights go out before the staged x is written
   auto sa = stream_for(blockIdx.x);
   sa.prefetch();
+  stg.store(lds);
   for (int it = blockIdx.x; it < items; it += 2 * P) {
     const int ib = it + P;
     // the next item's weights (this item again when there is none: its lines
