@@ -14,6 +14,12 @@ Workloads:
   qmv-config0  BASELINE config 0: one affine 4-bit g64 QMV [4096, 2048] per
       step, rotating >= 2 GiB of weight copies so the 256 MB Infinity Cache
       cannot serve repeats; value = achieved GB/s.
+  gdn-prefill-config1  BASELINE config 1 prefill: the chunked GatedDeltaNet
+      scan over T = 2048 tokens of one sequence (16 key / 32 value heads, head
+      dim 128, config-1 inputs); a step = one whole scan (prep + chunk walk);
+      value = tokens/s.  Roofline: fp32 matrix-core FLOPs of the chunked
+      algorithm per scan over the scan time (MI355X fp32 MFMA 157.3 TFLOP/s);
+      the sequential GPU scan (mx_gdn_scan) is timed beside it.
 
 Timing: the decode loop is bracketed by device synchronisation (the engine
 synchronises once per step to read the tokens, as the reference's eval does).
@@ -146,7 +152,7 @@ def bench_config3(mx, args):
             "prefill_s": round(prefill_s, 2),
             "context": "synthetic" if args.synthetic_context else "prefilled",
         },
-        "roofline": {"bound": "hbm", "kernel": "moe gate_up_kernel<4>",
+        "roofline": {"bound": "hbm", "kernel": "moe gate_up_persist_kernel<4, 16>",
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None},
         "cpu_baseline": cpu,
@@ -251,8 +257,100 @@ def bench_qmv_config0(mx, args):
     }
 
 
-WORKLOADS = {"config3-b8-decode": bench_config3, "qmv-config0": bench_qmv_config0}
-DEFAULTS = {"config3-b8-decode": (240, 16), "qmv-config0": (2000, 200)}
+# --------------------------------------------------------------- config 1 --
+FP32_MFMA_PEAK_TFLOPS = 157.3
+
+
+def prefill_flops(t: int, hv: int) -> float:
+    """fp32-equivalent FLOPs of the chunked scan per sequence: per 64-token
+    chunk and value head, K K^T and Q K^T (2 x 64x64x128), W and U (2 x
+    64x64x128), D = U - W S and (gamma Q) S (2 x 64x128x128), P D (64x64x128)
+    and K'^T D (128x64x128), 2 FLOPs per multiply-add."""
+    c, d = 64, 128
+    per_chunk = 2 * (2 * c * c * d + 2 * c * c * d + 2 * c * d * d + c * c * d + d * c * d)
+    return per_chunk * ((t + c - 1) // c) * hv
+
+
+def bench_gdn_prefill_config1(mx, args):
+    from oracle import oracle as orc
+    from test_gdn_prefill_gpu import inputs
+
+    hk, hv, t = 16, 32, 2048
+    q, k, v, g, beta = inputs(orc, t, hk, hv, 2048)
+    state0 = np.zeros((1, hv, 128, 128), np.float32)
+    slots = np.zeros(1, np.int32)
+    dims = mx.GdnDimsC(hk, hv, 128, 128, 4)
+    dq, dk, dv_, dg, db, dsl, dst = (mx.DeviceArray.from_numpy(np.ascontiguousarray(a))
+                                     for a in (q, k, v, g, beta, slots, state0))
+    y = mx.DeviceArray((t, hv, 128), np.uint16)
+    ws = mx.DeviceArray((mx.lib.mx_gdn_prefill_workspace_bytes(1, hv, t),), np.uint8)
+    stream = C.c_void_p()
+    mx.check(mx.lib.mx_stream_create(C.byref(stream)))
+
+    def chunked():
+        mx.check(mx.lib.mx_gdn_prefill_chunked(dq.ptr, dk.ptr, dv_.ptr, dg.ptr, db.ptr,
+                                               C.byref(dims), 1, t, dsl.ptr, dst.ptr, y.ptr,
+                                               ws.ptr, stream))
+
+    def sequential():
+        mx.check(mx.lib.mx_gdn_scan(dq.ptr, dk.ptr, dv_.ptr, dg.ptr, db.ptr, C.byref(dims), 1, t,
+                                    dsl.ptr, dst.ptr, None, y.ptr, stream))
+
+    def timed(fn, n):
+        e0, e1 = C.c_void_p(), C.c_void_p()
+        mx.check(mx.lib.mx_event_create(C.byref(e0)))
+        mx.check(mx.lib.mx_event_create(C.byref(e1)))
+        mx.check(mx.lib.mx_device_sync())
+        mx.check(mx.lib.mx_event_record(e0, stream))
+        for _ in range(n):
+            fn()
+        mx.check(mx.lib.mx_event_record(e1, stream))
+        ms = C.c_float()
+        mx.check(mx.lib.mx_stream_sync(stream))
+        mx.check(mx.lib.mx_event_elapsed_ms(e0, e1, C.byref(ms)))
+        return ms.value / 1e3 / n
+
+    # parity of the measured configuration against the oracle first
+    chunked()
+    mx.check(mx.lib.mx_stream_sync(stream))
+    t0 = time.perf_counter()
+    y_w, st_w, _ = orc.gdn_scan(q, k, v, g, beta, hk, hv, 1, t, slots, state0)
+    cpu_s = time.perf_counter() - t0
+    err = np.abs(dst.numpy() - st_w).max() / np.abs(st_w).max()
+    log(f"gdn-prefill-config1: state max rel err vs oracle {err:.2e}")
+    if err > 1e-4:
+        raise SystemExit("bench: chunked prefill state differs from the oracle")
+    for _ in range(args.warmup):
+        chunked()
+    avg = timed(chunked, args.steps)
+    seq = timed(sequential, max(1, min(5, args.steps)))
+    flops = prefill_flops(t, hv)
+    tflops = flops / avg / 1e12
+    log(f"gdn-prefill-config1: chunked {avg * 1e6:.1f} us/scan ({t / avg:.0f} tok/s, "
+        f"{tflops:.2f} TFLOP/s); sequential GPU scan {seq * 1e6:.1f} us; "
+        f"oracle (sequential, {orc.num_threads()} threads) {cpu_s:.2f} s")
+    return {
+        "metric": METRIC, "value": round(t / avg, 1), "unit": "tok/s", "ms_per_step": avg * 1e3,
+        "dtype": "bf16 q/k/v -> fp32 state, fp32 matrix-core products",
+        "config": {"workload": "gdn-prefill-config1", "t": t, "batch": 1, "key_heads": hk,
+                   "value_heads": hv, "head_dim": 128, "chunk": 64,
+                   "sequential_gpu_scan_us": round(seq * 1e6, 1),
+                   "state_rel_err_vs_oracle": float(f"{err:.3e}")},
+        "roofline": {"bound": "mfma", "kernel": "chunk_prep_kernel + chunk_scan_kernel",
+                     "achieved": round(tflops, 3), "peak": FP32_MFMA_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4),
+                     "traffic": None},
+        "cpu_baseline": {"value": round(t / cpu_s, 1), "unit": "tok/s",
+                         "cores": orc.num_threads(), "kind": "port",
+                         "sample": f"one sequential oracle scan of the same T={t} input "
+                                   f"({cpu_s:.2f}s)"},
+    }
+
+
+WORKLOADS = {"config3-b8-decode": bench_config3, "qmv-config0": bench_qmv_config0,
+             "gdn-prefill-config1": bench_gdn_prefill_config1}
+DEFAULTS = {"config3-b8-decode": (240, 16), "qmv-config0": (2000, 200),
+            "gdn-prefill-config1": (50, 5)}
 
 
 def main() -> None:

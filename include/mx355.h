@@ -379,6 +379,21 @@ mx_status mx_gdn_scan(const uint16_t* q, const uint16_t* k, const uint16_t* v, c
                       const int32_t* slots, float* state, float* history, uint16_t* y,
                       void* stream);
 
+/* mx_gdn_prefill_chunked: the delta rule of mx_gdn_scan over `t` tokens of each
+ * of `groups` sequences, in the chunked form (64-token chunks; per chunk the
+ * triangular transform T = (I + A)^-1 with A[t][s] = beta_t (gamma_t/gamma_s)
+ * k_t.k_s, then D = U - W S, y = (gamma Q) S + P D, S' = gamma_C S + K'^T D, all
+ * products that touch the fp32 state on fp32 matrix cores).  Inputs, state
+ * and y as for mx_gdn_scan (no history).  workspace:
+ * mx_gdn_prefill_workspace_bytes(groups, hv, t) bytes of device memory.
+ * Replaces the T-token call of gdn_kernel::recurrent (src/gdn_kernel.rs:7-71,
+ * kernels/gated_delta.metal), which the reference runs token by token. */
+size_t mx_gdn_prefill_workspace_bytes(int32_t groups, int32_t hv, int32_t t);
+mx_status mx_gdn_prefill_chunked(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                 const float* g, const uint16_t* beta, const mx_gdn_dims* dims,
+                                 int32_t groups, int32_t t, const int32_t* slots, float* state,
+                                 uint16_t* y, void* workspace, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

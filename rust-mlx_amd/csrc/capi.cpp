@@ -388,6 +388,31 @@ MX_ABI mx_status mx_gdn_scan(const uint16_t* q, const uint16_t* k, const uint16_
                 "mx_gdn_scan");
 }
 
+MX_ABI size_t mx_gdn_prefill_workspace_bytes(int32_t groups, int32_t hv, int32_t t) {
+  if (groups <= 0 || hv <= 0 || t <= 0) return 0;
+  return gdn_chunk_workspace_bytes(groups, hv, t);
+}
+
+MX_ABI mx_status mx_gdn_prefill_chunked(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                        const float* g, const uint16_t* beta,
+                                        const mx_gdn_dims* dims, int32_t groups, int32_t t,
+                                        const int32_t* slots, float* state, uint16_t* y,
+                                        void* workspace, void* stream) {
+  MX_CHECK(dims != nullptr, MX_EINVAL, "mx_gdn_prefill_chunked: null dims");
+  MX_CHECK(groups >= 0 && t >= 1, MX_EINVAL, "mx_gdn_prefill_chunked: bad shape");
+  if (groups == 0) return MX_OK;
+  MX_CHECK(q && k && v && g && beta && slots && state && y && workspace, MX_EINVAL,
+           "mx_gdn_prefill_chunked: null pointer");
+  const GdnDims d{dims->hk, dims->hv, dims->dk, dims->dv, dims->conv_k};
+  MX_CHECK(d.hk > 0 && d.hv > 0 && d.hv % d.hk == 0, MX_EINVAL,
+           "mx_gdn_prefill_chunked: value heads must be a multiple of key heads");
+  MX_CHECK(d.dk == 128 && d.dv == 128, MX_EUNSUPPORTED,
+           "mx_gdn_prefill_chunked: head dims must be 128");
+  return finish(gdn_prefill_chunked(q, k, v, g, beta, d, groups, t, slots, state, y,
+                                    static_cast<float*>(workspace), hipStream_t(stream)),
+                "mx_gdn_prefill_chunked");
+}
+
 // ---- attention --------------------------------------------------------------
 MX_ABI size_t mx_attn_workspace_bytes(int32_t rows, int32_t heads, int32_t head_dim,
                                       int32_t max_ctx) {

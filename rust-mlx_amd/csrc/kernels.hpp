@@ -172,6 +172,13 @@ int gdn_recurrence(const uint16_t* conv_out, int64_t conv_stride, const uint16_t
 int gdn_scan(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
              const uint16_t* beta, GdnDims d, int groups, int t, const int32_t* slots,
              float* state, float* history, uint16_t* y, hipStream_t s);
+// chunked prefill form of gdn_scan (gdn_chunk.hip): same inputs and outputs,
+// fp32 matrix-core products over 64-token chunks; workspace from
+// gdn_chunk_workspace_bytes.
+size_t gdn_chunk_workspace_bytes(int groups, int hv, int t);
+int gdn_prefill_chunked(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
+                        const uint16_t* beta, GdnDims d, int groups, int t, const int32_t* slots,
+                        float* state, uint16_t* y, float* workspace, hipStream_t s);
 
 // ---- engine (engine.cpp) ----
 struct Engine;
