@@ -394,6 +394,68 @@ mx_status mx_gdn_prefill_chunked(const uint16_t* q, const uint16_t* k, const uin
                                  int32_t groups, int32_t t, const int32_t* slots, float* state,
                                  uint16_t* y, void* workspace, void* stream);
 
+/* ---- A18: cooperative equal-offset scheduler with a prefix cache -----------
+ * Host-side serving loop over the engine (or any backend with the same three
+ * operations).  Replaces batch::serve / admit / Row::emit
+ * (src/bin/server/batch.rs:240-349, 28-140) and PrefixCache::get_or_prepare
+ * (src/speculative.rs:70-117):
+ *  - up to batch_size rows are active; queued jobs are admitted in submission
+ *    order while a row is free (admission prefills the prompt, or copies the
+ *    cached state of an identical prompt, and emits its greedy token);
+ *  - each mx_sched_step decodes, together, the active rows at the smallest
+ *    cache offset among active rows;
+ *  - a row ends on a stop token (reported, not emitted) or after max_tokens
+ *    emitted tokens; prompt + max_tokens > max_context is rejected;
+ *  - the prefix cache keeps up to prefix_entries prepared prompts within
+ *    prefix_tokens tokens, least recently used evicted first, each in its own
+ *    cache slot (a hit is a slot copy).
+ * The scheduler is not thread safe; one owning thread, like the engine. */
+typedef struct mx_sched mx_sched;
+typedef struct mx_sched_backend {
+  void* ctx;
+  /* fresh cache in `slot`, then the prompt; *next = greedy token after it */
+  mx_status (*prefill)(void* ctx, int32_t slot, const uint32_t* tokens, int32_t count,
+                       uint32_t* next);
+  /* one token for each of `rows` slots at equal offsets */
+  mx_status (*decode)(void* ctx, const int32_t* slots, const uint32_t* tokens, int32_t rows,
+                      uint32_t* next);
+  mx_status (*clone)(void* ctx, int32_t src, int32_t dst);
+} mx_sched_backend;
+typedef struct mx_sched_config {
+  int32_t batch_size;      /* rows decoded together, 1..8 */
+  int32_t slots;           /* cache slots for rows and prefix entries (>= batch_size) */
+  int32_t prefix_entries;  /* prefix-cache entries (0: no cache) */
+  int32_t prefix_tokens;   /* token budget of the prefix cache */
+  int32_t max_context;     /* prompt + max_tokens limit */
+  int32_t n_stop;          /* stop tokens used (0..8) */
+  uint32_t stop[8];
+} mx_sched_config;
+enum {
+  MX_SCHED_TOKEN = 0,   /* `token` emitted; detail = 1 on a prompt's first token after a cache hit */
+  MX_SCHED_STOP = 1,    /* finished on stop token `token` (not emitted) */
+  MX_SCHED_LENGTH = 2,  /* finished after max_tokens tokens */
+  MX_SCHED_ERROR = 3    /* rejected or failed; detail = mx_status */
+};
+typedef struct mx_sched_event {
+  uint64_t job;
+  uint32_t token;
+  int32_t kind;
+  int32_t detail;
+} mx_sched_event;
+mx_status mx_sched_create(const mx_sched_config* cfg, const mx_sched_backend* backend,
+                          mx_sched** out);
+mx_status mx_sched_create_for_engine(mx_engine* e, const mx_sched_config* cfg, mx_sched** out);
+mx_status mx_sched_destroy(mx_sched* s);
+mx_status mx_sched_submit(mx_sched* s, uint64_t job, const uint32_t* prompt, int32_t count,
+                          int32_t max_tokens, int32_t use_prefix_cache);
+/* drops a queued or active job (its slot is freed); MX_EINVAL if unknown */
+mx_status mx_sched_cancel(mx_sched* s, uint64_t job);
+/* one scheduler iteration; `capacity` >= 4 * batch_size events */
+mx_status mx_sched_step(mx_sched* s, mx_sched_event* events, int32_t capacity, int32_t* count,
+                        int32_t* decoded_rows);
+int32_t mx_sched_pending(const mx_sched* s);  /* queued + active jobs */
+int32_t mx_sched_cached(const mx_sched* s);   /* prefix-cache entries */
+
 #ifdef __cplusplus
 }
 #endif

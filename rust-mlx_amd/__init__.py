@@ -84,6 +84,31 @@ class StepProfileC(C.Structure):
         "step_bytes")]
 
 
+SCHED_PREFILL = C.CFUNCTYPE(C.c_int32, C.c_void_p, C.c_int32, C.POINTER(C.c_uint32), C.c_int32,
+                            C.POINTER(C.c_uint32))
+SCHED_DECODE = C.CFUNCTYPE(C.c_int32, C.c_void_p, C.POINTER(C.c_int32), C.POINTER(C.c_uint32),
+                           C.c_int32, C.POINTER(C.c_uint32))
+SCHED_CLONE = C.CFUNCTYPE(C.c_int32, C.c_void_p, C.c_int32, C.c_int32)
+
+
+class SchedBackendC(C.Structure):
+    _fields_ = [("ctx", C.c_void_p), ("prefill", SCHED_PREFILL), ("decode", SCHED_DECODE),
+                ("clone", SCHED_CLONE)]
+
+
+class SchedConfigC(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("batch_size", "slots", "prefix_entries", "prefix_tokens",
+                                         "max_context", "n_stop")] + [("stop", C.c_uint32 * 8)]
+
+
+class SchedEventC(C.Structure):
+    _fields_ = [("job", C.c_uint64), ("token", C.c_uint32), ("kind", C.c_int32),
+                ("detail", C.c_int32)]
+
+
+SCHED_TOKEN, SCHED_STOP, SCHED_LENGTH, SCHED_ERROR = 0, 1, 2, 3
+
+
 def _load() -> C.CDLL:
     if not os.path.exists(LIB_PATH):
         raise ImportError(
@@ -154,6 +179,14 @@ def _load() -> C.CDLL:
                                  C.POINTER(QWeightC), vp, vp, vp], i32),
         "mx_engine_profile_step": ([vp, vp, vp, i32, vp, C.POINTER(StepProfileC)], i32),
         "mx_engine_read": ([vp, C.c_char_p, vp, sz], i32),
+        "mx_sched_create": ([C.POINTER(SchedConfigC), C.POINTER(SchedBackendC), C.POINTER(vp)], i32),
+        "mx_sched_create_for_engine": ([vp, C.POINTER(SchedConfigC), C.POINTER(vp)], i32),
+        "mx_sched_destroy": ([vp], i32),
+        "mx_sched_submit": ([vp, u64, vp, i32, i32, i32], i32),
+        "mx_sched_cancel": ([vp, u64], i32),
+        "mx_sched_step": ([vp, C.POINTER(SchedEventC), i32, C.POINTER(i32), C.POINTER(i32)], i32),
+        "mx_sched_pending": ([vp], i32),
+        "mx_sched_cached": ([vp], i32),
         "mx_engine_tensor": ([vp, C.c_char_p, C.POINTER(vp), C.POINTER(sz)], i32),
     }
     for name, (args, res) in sig.items():
@@ -176,7 +209,9 @@ def declared_symbols(header: str) -> list[str]:
     import re
 
     text = open(header).read()
-    return sorted(set(re.findall(r"\b(mx_[a-z0-9_]+)\s*\(", text)))
+    # a name followed by "(" declares a function; "mx_status (*field)" is a
+    # function-pointer member of a struct
+    return sorted(set(re.findall(r"\b(mx_[a-z0-9_]+)\s*\((?!\*)", text)))
 
 
 class DeviceArray:
@@ -396,3 +431,74 @@ class Engine:
         p, n = C.c_void_p(), C.c_size_t()
         check(lib.mx_engine_tensor(self.h, name.encode(), C.byref(p), C.byref(n)))
         return n.value
+
+
+class Scheduler:
+    """Host handle of an mx_sched: the equal-offset serving loop over an Engine
+    (engine=...) or over a backend given as Python callables (prefill(slot,
+    tokens) -> next, decode(slots, tokens) -> nexts, clone(src, dst))."""
+
+    def __init__(self, batch_size, slots, max_context, prefix_entries=0, prefix_tokens=0,
+                 stop=(), engine=None, prefill=None, decode=None, clone=None):
+        stop = list(stop)
+        cfg = SchedConfigC(batch_size, slots, prefix_entries, prefix_tokens, max_context,
+                           len(stop), (C.c_uint32 * 8)(*stop))
+        h = C.c_void_p()
+        self._keep = None
+        if engine is not None:
+            check(lib.mx_sched_create_for_engine(engine.h, C.byref(cfg), C.byref(h)))
+        else:
+            def pf(ctx, slot, toks, n, out):
+                try:
+                    out[0] = int(prefill(slot, [toks[i] for i in range(n)]))
+                    return MX_OK
+                except Exception:
+                    return 1
+
+            def dc(ctx, slots_p, toks, n, out):
+                try:
+                    nxt = decode([slots_p[i] for i in range(n)], [toks[i] for i in range(n)])
+                    for i in range(n):
+                        out[i] = int(nxt[i])
+                    return MX_OK
+                except Exception:
+                    return 5
+
+            def cl(ctx, src, dst):
+                try:
+                    clone(src, dst)
+                    return MX_OK
+                except Exception:
+                    return 1
+
+            be = SchedBackendC(None, SCHED_PREFILL(pf), SCHED_DECODE(dc), SCHED_CLONE(cl))
+            self._keep = be
+            check(lib.mx_sched_create(C.byref(cfg), C.byref(be), C.byref(h)))
+        self.h = h.value
+        self.batch_size = batch_size
+
+    def submit(self, job, prompt, max_tokens, prefix_cache=True):
+        p = np.ascontiguousarray(prompt, np.uint32)
+        check(lib.mx_sched_submit(self.h, job, p.ctypes.data if len(p) else None, len(p),
+                                  max_tokens, int(prefix_cache)))
+
+    def cancel(self, job) -> bool:
+        return lib.mx_sched_cancel(self.h, job) == MX_OK
+
+    def step(self):
+        cap = 4 * self.batch_size
+        ev = (SchedEventC * cap)()
+        n, rows = C.c_int32(), C.c_int32()
+        check(lib.mx_sched_step(self.h, ev, cap, C.byref(n), C.byref(rows)))
+        return [(e.job, e.token, e.kind, e.detail) for e in ev[: n.value]], rows.value
+
+    def pending(self) -> int:
+        return lib.mx_sched_pending(self.h)
+
+    def cached(self) -> int:
+        return lib.mx_sched_cached(self.h)
+
+    def close(self):
+        if self.h:
+            lib.mx_sched_destroy(self.h)
+            self.h = None
