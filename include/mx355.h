@@ -289,6 +289,16 @@ mx_status mx_gdn_recurrence(const uint16_t* conv_out, int64_t conv_stride, const
                             const int32_t* slots, float* state, float* history, uint16_t* y,
                             void* stream);
 
+/* ---- A16: unquantised bf16 GEMV for short rows ------------------------------
+ * mx_gemv_bf16: y[r, o] = bf16(sum_k w[o, k] x[r, k]) for rows 1..8, w bf16
+ * [n, k] row-major, x bf16 [rows, k], k % 128 == 0.  Each row keeps the order
+ * of a single-row call (32 partial sums over 128-value blocks, fma per
+ * product, then a shuffle-down tree 16, 8, 4, 2, 1), so batching never
+ * changes a row's result.  Replaces gemv_kernel::project
+ * (src/gemv_kernel.rs:30-90, kernels/shared_gemv.metal). */
+mx_status mx_gemv_bf16(const uint16_t* w, int32_t n, int32_t k, const uint16_t* x, int32_t rows,
+                       uint16_t* y, void* stream);
+
 /* ---- gated full attention (decode / verify rows) ---------------------------
  * mx_attn_decode: scaled dot-product attention of each row's normalised and
  * rotated q heads (q bf16 [rows, heads, head_dim]) over the cached positions

@@ -398,3 +398,30 @@ void mxo_head_argmax(const mxo_qw* w, const uint16_t* x, int m, uint32_t* tokens
     tokens[mm] = select_best(scratch, w->n);
   }
 }
+
+/* Unquantised bf16 GEMV for 1..8 rows (reference src/gemv_kernel.rs:30-90,
+ * kernels/shared_gemv.metal): per output column, 32 lanes; lane l accumulates,
+ * over k-blocks of 128 in order, values k0 + 4l + c (c = 0..3) as
+ * acc = fma(w, x, acc); then a shuffle-down tree over lanes with offsets 16, 8,
+ * 4, 2, 1 (lane l += lane l + d); lane 0's sum is rounded to bf16.  Every row
+ * uses the same order, so a row's result does not depend on the others. */
+void mxo_gemv_bf16(const uint16_t* w, int n, int k, const uint16_t* x, int rows, uint16_t* y) {
+#pragma omp parallel for schedule(static)
+  for (int o = 0; o < n; ++o) {
+    for (int r = 0; r < rows; ++r) {
+      float acc[32];
+      for (int l = 0; l < 32; ++l) {
+        float a = 0.0f;
+        for (int k0 = 0; k0 < k; k0 += 128)
+          for (int c = 0; c < 4; ++c) {
+            const int kk = k0 + 4 * l + c;
+            a = fmaf(bf(w[(int64_t)o * k + kk]), bf(x[(int64_t)r * k + kk]), a);
+          }
+        acc[l] = a;
+      }
+      for (int d = 16; d >= 1; d >>= 1)
+        for (int l = 0; l < d; ++l) acc[l] = acc[l] + acc[l + d];
+      y[(int64_t)r * n + o] = mxo_f32_to_bf16(acc[0]);
+    }
+  }
+}

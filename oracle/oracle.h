@@ -89,6 +89,9 @@ void mxo_gdn_scan(const uint16_t* q, const uint16_t* k, const uint16_t* v, const
                   const uint16_t* beta, int hk_heads, int hv_heads, int groups, int t,
                   const int32_t* slots, float* state, float* history, uint16_t* y);
 
+/* ---- A16: unquantised bf16 GEMV for short rows ---- */
+void mxo_gemv_bf16(const uint16_t* w, int n, int k, const uint16_t* x, int rows, uint16_t* y);
+
 /* ---- A14: greedy head ---- */
 void mxo_argmax_bf16(const uint16_t* logits, int rows, int n, uint32_t* tokens);
 void mxo_head_argmax(const mxo_qw* w, const uint16_t* x, int m, uint32_t* tokens, float* scratch);

@@ -47,6 +47,7 @@ def _load() -> C.CDLL:
                                 vp, vp, vp, vp], None),
         "mxo_gdn_scan": ([vp, vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp], None),
         "mxo_argmax_bf16": ([vp, i32, i32, vp], None),
+        "mxo_gemv_bf16": ([vp, i32, i32, vp, i32, vp], None),
         "mxo_head_argmax": ([vp, vp, i32, vp, vp], None),
         "mxo_hc_norm": ([vp, vp, i32, i32, i32, f32, vp], None),
         "mxo_hc_down": ([vp, vp, i32, i32, i32, vp, vp], None),
@@ -281,6 +282,17 @@ def gdn_scan(q, k, v, g, beta, hk, hv, groups, t, slots, state, history=False):
     lib.mxo_gdn_scan(_p(q), _p(k), _p(v), _p(g), _p(beta), hk, hv, groups, t, _p(slots),
                      _p(state), _p(hist) if hist is not None else None, _p(y))
     return y, state, hist
+
+
+# ---- unquantised GEMV ----
+def gemv_bf16(w: np.ndarray, x: np.ndarray) -> np.ndarray:
+    w = np.ascontiguousarray(w, np.uint16)
+    x = np.ascontiguousarray(x, np.uint16)
+    n, k = w.shape
+    rows = x.shape[0]
+    y = np.empty((rows, n), np.uint16)
+    lib.mxo_gemv_bf16(_p(w), n, k, _p(x), rows, _p(y))
+    return y
 
 
 # ---- head ----

@@ -157,6 +157,7 @@ def _load() -> C.CDLL:
         "mx_gdn_prefill_workspace_bytes": ([i32, i32, i32], sz),
         "mx_gdn_prefill_chunked": ([vp, vp, vp, vp, vp, C.POINTER(GdnDimsC), i32, i32, vp, vp, vp,
                                     vp, vp], i32),
+        "mx_gemv_bf16": ([vp, i32, i32, vp, i32, vp, vp], i32),
         "mx_attn_workspace_bytes": ([i32, i32, i32, i32], sz),
         "mx_attn_decode": ([vp, vp, i64, i32, vp, vp, vp, vp, C.POINTER(AttnDimsC), i32, vp, vp,
                             vp], i32),

@@ -413,6 +413,16 @@ MX_ABI mx_status mx_gdn_prefill_chunked(const uint16_t* q, const uint16_t* k, co
                 "mx_gdn_prefill_chunked");
 }
 
+MX_ABI mx_status mx_gemv_bf16(const uint16_t* w, int32_t n, int32_t k, const uint16_t* x,
+                              int32_t rows, uint16_t* y, void* stream) {
+  MX_CHECK(rows >= 0 && n >= 0 && k >= 0, MX_EINVAL, "mx_gemv_bf16: negative size");
+  if (rows == 0 || n == 0) return MX_OK;
+  MX_CHECK(w && x && y, MX_EINVAL, "mx_gemv_bf16: null pointer");
+  MX_CHECK(rows <= 8 && k >= 128 && k % 128 == 0, MX_EUNSUPPORTED,
+           "mx_gemv_bf16: needs 1..8 rows and k a positive multiple of 128");
+  return finish(gemv_bf16(w, n, k, x, rows, y, hipStream_t(stream)), "mx_gemv_bf16");
+}
+
 // ---- attention --------------------------------------------------------------
 MX_ABI size_t mx_attn_workspace_bytes(int32_t rows, int32_t heads, int32_t head_dim,
                                       int32_t max_ctx) {

@@ -172,6 +172,9 @@ int gdn_recurrence(const uint16_t* conv_out, int64_t conv_stride, const uint16_t
 int gdn_scan(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
              const uint16_t* beta, GdnDims d, int groups, int t, const int32_t* slots,
              float* state, float* history, uint16_t* y, hipStream_t s);
+// unquantised bf16 GEMV, 1..8 rows, k % 128 == 0 (gemv.hip)
+int gemv_bf16(const uint16_t* w, int n, int k, const uint16_t* x, int rows, uint16_t* y,
+              hipStream_t s);
 // chunked prefill form of gdn_scan (gdn_chunk.hip): same inputs and outputs,
 // fp32 matrix-core products over 64-token chunks; workspace from
 // gdn_chunk_workspace_bytes.
