@@ -25,8 +25,11 @@ Timing: the decode loop is bracketed by device synchronisation (the engine
 synchronises once per step to read the tokens, as the reference's eval does).
 The roofline object is the MoE expert gate/up kernel (the step's dominant
 kernel): algorithmic bytes (distinct experts' weights + the shared expert)
-over its duration, both from HIP events recorded on the engine's stream
-around every launch of an eager profiled step.
+over its duration, from HIP events on the engine's stream around the 48
+layers' gate/up launches run back to back on the routing of the last step
+(each launch reads its own layer's weights from HBM).  `traffic` is the
+measured HBM bytes per launch from the committed rocprofv3 counter summary
+profiles/config3-b8-decode_hbm-traffic.md.
 The CPU baseline is the C oracle (oracle/, a restatement of the reference
 arithmetic) timed on this host over a bounded sample of the same step.
 """
@@ -117,14 +120,15 @@ def bench_config3(mx, args):
     ms_step = dt / args.steps * 1e3
     log(f"config3: {args.steps} steps x {rows} rows in {dt:.3f}s -> {tok_s:.1f} tok/s, "
         f"{ms_step:.3f} ms/step")
-    # a second profiled step after the timed loop (longer contexts)
+    # a second profiled step after the timed loop (longer contexts), then the
+    # expert kernels of all 48 layers back to back on that step's routing
     _, prof2 = eng.profile_step(slots, toks)
-    gu_gbs = (prof["gate_up_bytes"] + prof2["gate_up_bytes"]) / (
-        (prof["gate_up_ms"] + prof2["gate_up_ms"]) * 1e-3) / 1e9
-    dn_gbs = (prof["down_bytes"] + prof2["down_bytes"]) / (
-        (prof["down_ms"] + prof2["down_ms"]) * 1e-3) / 1e9
+    et = eng.time_experts(rows)
+    gu_gbs = et["gate_up_bytes"] / (et["gate_up_ms"] * 1e-3) / 1e9
+    dn_gbs = et["down_bytes"] / (et["down_ms"] * 1e-3) / 1e9
     layers = prof["layers"]
-    gu_us = prof2["gate_up_ms"] / layers * 1e3
+    gu_us = et["gate_up_ms"] / et["launches"] * 1e3
+    gu_launch_bytes = et["gate_up_bytes"] / et["launches"]
     step_bytes = prof2["step_bytes"]
     step_frac = step_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS
     log(f"config3: expert gate/up {gu_gbs:.0f} GB/s ({gu_us:.1f} us/launch avg), "
@@ -154,9 +158,24 @@ def bench_config3(mx, args):
         },
         "roofline": {"bound": "hbm", "kernel": "moe gate_up_persist_kernel<4, 16>",
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic("config3-b8-decode_hbm-traffic.md"),
+                     "algorithmic_bytes_per_launch": int(gu_launch_bytes),
+                     "us_per_launch": round(gu_us, 2)},
         "cpu_baseline": cpu,
     }
+
+
+def measured_traffic(summary: str):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3
+    counter summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated), or None."""
+    path = os.path.join(ROOT, "profiles", summary)
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch ="):
+            return int(line.split("=")[1])
+    return None
 
 
 def cpu_baseline_config3(mx, eng, cfg, slots, toks, positions):
@@ -347,10 +366,41 @@ def bench_gdn_prefill_config1(mx, args):
     }
 
 
+# ------------------------------------------------------- copy calibration --
+COPY_BYTES = 256 << 20
+
+
+def bench_copy_calibration(mx, args):
+    """Device-to-device copies of 256 MiB (the runtime's copy kernel): the
+    reference point that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to
+    bytes (a copy fetches and writes exactly COPY_BYTES)."""
+    src = mx.DeviceArray((COPY_BYTES,), np.uint8)
+    dst = mx.DeviceArray((COPY_BYTES,), np.uint8)
+    stream = C.c_void_p()
+    mx.check(mx.lib.mx_stream_create(C.byref(stream)))
+    for _ in range(args.warmup):
+        mx.check(mx.lib.mx_memcpy_dtod(dst.ptr, src.ptr, COPY_BYTES, stream))
+    mx.check(mx.lib.mx_stream_sync(stream))
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        mx.check(mx.lib.mx_memcpy_dtod(dst.ptr, src.ptr, COPY_BYTES, stream))
+    mx.check(mx.lib.mx_stream_sync(stream))
+    dt = (time.perf_counter() - t0) / args.steps
+    gbs = 2 * COPY_BYTES / dt / 1e9
+    log(f"copy-calibration: {COPY_BYTES >> 20} MiB copy in {dt * 1e6:.1f} us ({gbs:.0f} GB/s read+write)")
+    return {"metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": dt * 1e3,
+            "dtype": "u8", "config": {"workload": "copy-calibration", "bytes": COPY_BYTES},
+            "roofline": {"bound": "hbm", "kernel": "runtime copy", "achieved": round(gbs, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "traffic": 2 * COPY_BYTES},
+            "cpu_baseline": None}
+
+
 WORKLOADS = {"config3-b8-decode": bench_config3, "qmv-config0": bench_qmv_config0,
-             "gdn-prefill-config1": bench_gdn_prefill_config1}
+             "gdn-prefill-config1": bench_gdn_prefill_config1,
+             "copy-calibration": bench_copy_calibration}
 DEFAULTS = {"config3-b8-decode": (240, 16), "qmv-config0": (2000, 200),
-            "gdn-prefill-config1": (50, 5)}
+            "gdn-prefill-config1": (50, 5), "copy-calibration": (10, 2)}
 
 
 def main() -> None:

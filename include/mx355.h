@@ -117,6 +117,17 @@ typedef struct mx_step_profile {
   double step_bytes;          /* algorithmic bytes of the whole step */
 } mx_step_profile;
 
+/* Expert kernels of every MoE layer timed back to back (HIP events): totals
+ * over `launches` launches of each kernel and their algorithmic bytes. */
+typedef struct mx_expert_timing {
+  int32_t launches;
+  double distinct_experts;  /* routed experts of the routing used (per launch) */
+  double gate_up_ms;
+  double gate_up_bytes;
+  double down_ms;
+  double down_bytes;
+} mx_expert_timing;
+
 /* ---- errors / version -------------------------------------------------- */
 const char* mx_last_error(void);
 int32_t mx_abi_version(void);
@@ -376,6 +387,11 @@ mx_status mx_engine_fill_slot(mx_engine* e, int32_t slot, int32_t length, uint64
  * attribute GPU time per kernel, docs/performance.md:41). */
 mx_status mx_engine_profile_step(mx_engine* e, const int32_t* slots, const uint32_t* tokens,
                                  int32_t rows, uint32_t* next, mx_step_profile* out);
+/* Measurement hook (no reference counterpart): the expert gate/up kernels of
+ * all MoE layers launched back to back on the routing and activations of the
+ * last step, then all down kernels, each group between two events on the
+ * engine stream.  Caches are not changed. */
+mx_status mx_engine_time_experts(mx_engine* e, int32_t rows, mx_expert_timing* out);
 mx_status mx_engine_read(mx_engine* e, const char* what, void* host, size_t bytes);
 mx_status mx_engine_tensor(mx_engine* e, const char* name, void** device_ptr, size_t* bytes);
 

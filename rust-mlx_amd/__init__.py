@@ -96,6 +96,11 @@ class SchedBackendC(C.Structure):
                 ("clone", SCHED_CLONE)]
 
 
+class ExpertTimingC(C.Structure):
+    _fields_ = [("launches", C.c_int32)] + [(n, C.c_double) for n in (
+        "distinct_experts", "gate_up_ms", "gate_up_bytes", "down_ms", "down_bytes")]
+
+
 class SchedConfigC(C.Structure):
     _fields_ = [(n, C.c_int32) for n in ("batch_size", "slots", "prefix_entries", "prefix_tokens",
                                          "max_context", "n_stop")] + [("stop", C.c_uint32 * 8)]
@@ -180,6 +185,7 @@ def _load() -> C.CDLL:
                                  C.POINTER(QWeightC), vp, vp, vp], i32),
         "mx_engine_profile_step": ([vp, vp, vp, i32, vp, C.POINTER(StepProfileC)], i32),
         "mx_engine_read": ([vp, C.c_char_p, vp, sz], i32),
+        "mx_engine_time_experts": ([vp, i32, C.POINTER(ExpertTimingC)], i32),
         "mx_sched_create": ([C.POINTER(SchedConfigC), C.POINTER(SchedBackendC), C.POINTER(vp)], i32),
         "mx_sched_create_for_engine": ([vp, C.POINTER(SchedConfigC), C.POINTER(vp)], i32),
         "mx_sched_destroy": ([vp], i32),
@@ -418,6 +424,12 @@ class Engine:
         check(lib.mx_engine_profile_step(self.h, s.ctypes.data, t.ctypes.data, len(s),
                                          out.ctypes.data, C.byref(prof)))
         return out, {f: getattr(prof, f) for f, _ in StepProfileC._fields_}
+
+    def time_experts(self, rows):
+        """Expert kernels of all MoE layers back to back (totals and bytes)."""
+        t = ExpertTimingC()
+        check(lib.mx_engine_time_experts(self.h, rows, C.byref(t)))
+        return {f: getattr(t, f) for f, _ in ExpertTimingC._fields_}
 
     def set_flags(self, logits=False, eager=False, exact=False):
         check(lib.mx_engine_set_flags(self.h, (1 if logits else 0) | (2 if eager else 0)

@@ -634,6 +634,13 @@ MX_ABI mx_status mx_engine_tensor(mx_engine* e, const char* name, void** device_
   return MX_OK;
 }
 
+MX_ABI mx_status mx_engine_time_experts(mx_engine* e, int32_t rows, mx_expert_timing* out) {
+  MX_CHECK(e && out, MX_EINVAL, "mx_engine_time_experts: null pointer");
+  std::string err;
+  return engine_status(engine_time_experts(*e->impl, rows, out, &err), err,
+                       "mx_engine_time_experts");
+}
+
 MX_ABI mx_status mx_engine_profile_step(mx_engine* e, const int32_t* slots, const uint32_t* tokens,
                                         int32_t rows, uint32_t* next, mx_step_profile* out) {
   MX_CHECK(e && slots && tokens && next && out, MX_EINVAL, "mx_engine_profile_step: null pointer");

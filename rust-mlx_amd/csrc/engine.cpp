@@ -885,6 +885,57 @@ int engine_profile_step(Engine& e, const int32_t* slots, const uint32_t* tokens,
   return MX_OK;
 }
 
+// Times the expert kernels of every MoE layer back to back on the routing
+// and activations of the last step: all gate/up launches between two events,
+// then all down launches.  Each launch reads its own layer's weights, so the
+// weights come from HBM as in a step; back-to-back launches keep the events'
+// own dispatch overhead out of the per-launch average.  Caches are untouched.
+int engine_time_experts(Engine& e, int rows, mx_expert_timing* out, std::string* err) {
+  const auto& c = e.cfg;
+  std::memset(out, 0, sizeof(*out));
+  if (rows < 1 || rows > 8) {
+    *err = "rows must be in 1..8";
+    return MX_EINVAL;
+  }
+  std::vector<uint32_t> ids(size_t(rows) * c.top_k);
+  MX_HIP(hipMemcpyAsync(ids.data(), e.ids, ids.size() * 4, hipMemcpyDeviceToHost, e.stream));
+  MX_HIP(hipStreamSynchronize(e.stream));
+  std::vector<char> seen(c.experts, 0);
+  int distinct = 0;
+  for (uint32_t v : ids)
+    if (v < uint32_t(c.experts) && !seen[v]) {
+      seen[v] = 1;
+      ++distinct;
+    }
+  for (auto& ev : e.ev)
+    if (!ev) MX_HIP(hipEventCreate(&ev));
+  if (!e.layers.empty() && !experts_fast(e, e.layers[0]))
+    MX_TRY(moe_plan(e.ids, rows, c.top_k, e.moe_plan_buf, e.stream));
+  MX_HIP(hipEventRecord(e.ev[0], e.stream));
+  for (const LayerW& L : e.layers) MX_TRY(experts_gate_up(e, L, rows));
+  MX_HIP(hipEventRecord(e.ev[1], e.stream));
+  for (const LayerW& L : e.layers) MX_TRY(experts_down(e, L, rows));
+  MX_HIP(hipEventRecord(e.ev[2], e.stream));
+  MX_HIP(hipEventSynchronize(e.ev[2]));
+  float a = 0.0f, b = 0.0f;
+  MX_HIP(hipEventElapsedTime(&a, e.ev[0], e.ev[1]));
+  MX_HIP(hipEventElapsedTime(&b, e.ev[1], e.ev[2]));
+  out->launches = int32_t(e.layers.size());
+  out->distinct_experts = distinct;
+  out->gate_up_ms = a;
+  out->down_ms = b;
+  for (const LayerW& L : e.layers) {
+    const QWeight g{L.gate.codes, L.gate.scales, L.gate.biases, L.gate.n, L.gate.k, L.gate.bits,
+                    L.gate.group_size};
+    const QWeight d{L.down.codes, L.down.scales, L.down.biases, L.down.n, L.down.k, L.down.bits,
+                    L.down.group_size};
+    out->gate_up_bytes += double(distinct) * 2.0 * double(qw_bytes(g)) +
+                          double(qw_bytes(L.sgate) + qw_bytes(L.sup));
+    out->down_bytes += double(distinct) * double(qw_bytes(d)) + double(qw_bytes(L.sdown));
+  }
+  return MX_OK;
+}
+
 // Gives a slot a synthetic context of `length` positions: random K/V for
 // those positions, random GDN state and conv window (decode cost depends on
 // the context length only, so this stands in for a prefill when measuring).

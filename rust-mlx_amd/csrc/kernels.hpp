@@ -200,6 +200,7 @@ int engine_commit(Engine& e, int slot, int keep, std::string* err);
 int engine_read(Engine& e, const char* what, void* host, size_t bytes, std::string* err);
 int engine_tensor(Engine& e, const char* name, void** ptr, size_t* bytes);
 int engine_fill_slot(Engine& e, int slot, int length, uint64_t seed, std::string* err);
+int engine_time_experts(Engine& e, int rows, mx_expert_timing* out, std::string* err);
 int engine_profile_step(Engine& e, const int32_t* slots, const uint32_t* tokens, int rows,
                         uint32_t* next, mx_step_profile* out, std::string* err);
 void engine_set_flags(Engine& e, int want_logits, int use_graphs, int exact);
