@@ -530,12 +530,20 @@ int record_step(Engine& e, int rows, int groups, int t, bool history, bool logit
                       history ? e.hist_conv + size_t(gi) * (c.conv_k - 1 + c.max_verify) * e.cd
                               : nullptr,
                       e.stream));
-      MX_TRY(gdn_recurrence(e.conv_out, e.cd, e.pbuf + e.cd, e.pbuf + e.cd + e.vd,
-                            e.pbuf + e.cd + e.vd + c.gdn_hv, e.P, L.a_log, L.dt_bias, L.gdn_norm,
-                            c.rms_eps, e.gd, groups, t, rt->gdn_slots,
-                            e.gdn_state + gi * state_per,
-                            history ? e.hist_state + size_t(gi) * c.max_verify * state_per : nullptr,
-                            e.y, e.stream));
+      if (!e.exact && t == 1 && !history) {
+        MX_TRY(gdn_recurrence_fast(e.conv_out, e.cd, e.pbuf + e.cd, e.pbuf + e.cd + e.vd,
+                                   e.pbuf + e.cd + e.vd + c.gdn_hv, e.P, L.a_log, L.dt_bias,
+                                   L.gdn_norm, c.rms_eps, e.gd, groups, rt->gdn_slots,
+                                   e.gdn_state + gi * state_per, e.y, e.stream));
+      } else {
+        MX_TRY(gdn_recurrence(e.conv_out, e.cd, e.pbuf + e.cd, e.pbuf + e.cd + e.vd,
+                              e.pbuf + e.cd + e.vd + c.gdn_hv, e.P, L.a_log, L.dt_bias,
+                              L.gdn_norm, c.rms_eps, e.gd, groups, t, rt->gdn_slots,
+                              e.gdn_state + gi * state_per,
+                              history ? e.hist_state + size_t(gi) * c.max_verify * state_per
+                                      : nullptr,
+                              e.y, e.stream));
+      }
       MX_TRY(project(e, L.gdn_out, e.y, e.vd, rows, wr));
     } else {
       const int ai = L.cache_index;

@@ -228,7 +228,140 @@ __global__ __launch_bounds__(kD) void recurrence_kernel(ScanArgs p) {
   for (int d = 0; d < kD; ++d) sp[size_t(d) * kD] = s[d];
 }
 
+// ---------------------------------------------------------------------------
+// Fast-mode single-token step (decode, t = 1, no history), same inputs and
+// outputs as recurrence_kernel<true>: each wave forms the q / k L2 norms itself
+// with lane shuffles (no barrier), q and k reach the 128 value-row threads
+// through LDS as float4, the output RMS norm is the only exchange between the
+// two waves, and the scalar functions use the hardware exp2 / log2 /
+// reciprocal / rsqrt.  The bf16 rounding points of the exact step (the
+// reference's bf16 operations) are kept, so the step stays within the north
+// star's tolerances of the exact one layer after layer.
+__device__ __forceinline__ float exp_fast(float x) {
+  return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+}
+__device__ __forceinline__ float sigmoid_fast(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + exp_fast(-x));
+}
+// The bf16-rounded logistic and softplus of the exact step (the reference's
+// bf16 operations), with the hardware exp2 / log2 / reciprocal inside.
+__device__ __forceinline__ float sigmoid_bf16_fast(float x) {
+  const float e = round_bf16(exp_fast(__builtin_fabsf(x)));
+  const float d = round_bf16(1.0f + e);
+  const float y = round_bf16(__builtin_amdgcn_rcpf(d));
+  return x < 0.0f ? y : round_bf16(1.0f - y);
+}
+__device__ __forceinline__ float softplus_bf16_fast(float x) {
+  const float hi = x > 0.0f ? x : 0.0f;
+  const float lo = x > 0.0f ? 0.0f : x;
+  const float e = round_bf16(exp_fast(round_bf16(lo - hi)));
+  // log1p(e): series below 2^-10, where log2(1 + e) would lose the low bits
+  const float l = e < 0x1p-10f ? e - 0.5f * e * e
+                               : __builtin_amdgcn_logf(1.0f + e) * 0.6931471805599453f;
+  return round_bf16(hi + round_bf16(l));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o, 64);
+  return v;
+}
+
+__global__ __launch_bounds__(kD) void recurrence_fast_kernel(ScanArgs p) {
+  const int hv = blockIdx.x;
+  const int row = blockIdx.y;  // one token per group
+  const int i = threadIdx.x, lane = i & 63, wave = i >> 6;
+  const int hv_heads = p.hv_heads, hk_heads = p.hk_heads;
+  const int hk = hv / (hv_heads / hk_heads);
+  __shared__ float4 qs4[kD / 4], ks4[kD / 4];
+  __shared__ float red[2];
+  float* sp = p.state + (size_t(p.slots[row]) * hv_heads + hv) * kD * kD + i;
+  float s[kD];
+#pragma unroll
+  for (int d = 0; d < kD; ++d) s[d] = sp[size_t(d) * kD];
+  const uint16_t* cr = p.conv_out + size_t(row) * p.conv_stride;
+  const float q0 = bf16_to_f32(cr[hk * kD + lane]), q1 = bf16_to_f32(cr[hk * kD + 64 + lane]);
+  const float k0 = bf16_to_f32(cr[(hk_heads + hk) * kD + lane]);
+  const float k1 = bf16_to_f32(cr[(hk_heads + hk) * kD + 64 + lane]);
+  const float vi = bf16_to_f32(cr[2 * hk_heads * kD + hv * kD + i]);
+  const float bv = bf16_to_f32(p.b[size_t(row) * p.zab_stride + hv]);
+  const float av = bf16_to_f32(p.a[size_t(row) * p.zab_stride + hv]);
+  const float eps_l2 = round_bf16(1e-6f);
+  const float qscale = round_bf16(0.08838834764831845f);  // bf16(Dk^-1/2), Dk = 128
+  const float qss = round_bf16(wave_sum(round_bf16(q0 * q0) + round_bf16(q1 * q1)));
+  const float kss = round_bf16(wave_sum(round_bf16(k0 * k0) + round_bf16(k1 * k1)));
+  const float rq = round_bf16(__builtin_amdgcn_rsqf(round_bf16(qss + eps_l2)));
+  const float rk = round_bf16(__builtin_amdgcn_rsqf(round_bf16(kss + eps_l2)));
+  if (wave == 0) {
+    float* qs = reinterpret_cast<float*>(qs4);
+    float* ks = reinterpret_cast<float*>(ks4);
+    qs[lane] = round_bf16(round_bf16(q0 * rq) * qscale);
+    qs[64 + lane] = round_bf16(round_bf16(q1 * rq) * qscale);
+    ks[lane] = round_bf16(k0 * rk);
+    ks[64 + lane] = round_bf16(k1 * rk);
+  }
+  const float beta = sigmoid_bf16_fast(bv);
+  const float x = round_bf16(av + bf16_to_f32(p.dt_bias[hv]));
+  const float gdecay = exp_fast(-exp_fast(p.a_log[hv]) * softplus_bf16_fast(x));
+  __syncthreads();
+  float c0 = 0.0f, c1 = 0.0f, c2 = 0.0f, c3 = 0.0f;
+#pragma unroll
+  for (int d4 = 0; d4 < kD / 4; ++d4) {
+    const float4 kv4 = ks4[d4];
+    const int d = 4 * d4;
+    s[d] = s[d] * gdecay;
+    s[d + 1] = s[d + 1] * gdecay;
+    s[d + 2] = s[d + 2] * gdecay;
+    s[d + 3] = s[d + 3] * gdecay;
+    c0 = fmaf_(s[d], kv4.x, c0);
+    c1 = fmaf_(s[d + 1], kv4.y, c1);
+    c2 = fmaf_(s[d + 2], kv4.z, c2);
+    c3 = fmaf_(s[d + 3], kv4.w, c3);
+  }
+  const float delta = (vi - ((c0 + c1) + (c2 + c3))) * beta;
+  float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f;
+#pragma unroll
+  for (int d4 = 0; d4 < kD / 4; ++d4) {
+    const float4 kv4 = ks4[d4], qv4 = qs4[d4];
+    const int d = 4 * d4;
+    s[d] = fmaf_(kv4.x, delta, s[d]);
+    s[d + 1] = fmaf_(kv4.y, delta, s[d + 1]);
+    s[d + 2] = fmaf_(kv4.z, delta, s[d + 2]);
+    s[d + 3] = fmaf_(kv4.w, delta, s[d + 3]);
+    o0 = fmaf_(s[d], qv4.x, o0);
+    o1 = fmaf_(s[d + 1], qv4.y, o1);
+    o2 = fmaf_(s[d + 2], qv4.z, o2);
+    o3 = fmaf_(s[d + 3], qv4.w, o3);
+  }
+#pragma unroll
+  for (int d = 0; d < kD; ++d) sp[size_t(d) * kD] = s[d];
+  const float zi = bf16_to_f32(p.z[size_t(row) * p.zab_stride + hv * kD + i]);
+  const float nw = bf16_to_f32(p.norm_w[i]);
+  const float yo = round_bf16((o0 + o1) + (o2 + o3));
+  const float ws = wave_sum(yo * yo);
+  if (lane == 0) red[wave] = ws;
+  __syncthreads();
+  const float inv = __builtin_amdgcn_rsqf((red[0] + red[1]) * (1.0f / kD) + p.eps);
+  const float normed = round_bf16(nw * round_bf16(yo * inv));
+  p.y[size_t(row) * (size_t(hv_heads) * kD) + hv * kD + i] = f32_to_bf16(normed * sigmoid_fast(zi));
+}
+
 }  // namespace
+
+int gdn_recurrence_fast(const uint16_t* conv_out, int64_t conv_stride, const uint16_t* z,
+                        const uint16_t* a, const uint16_t* b, int64_t zab_stride,
+                        const float* a_log, const uint16_t* dt_bias, const uint16_t* norm_w,
+                        float eps, GdnDims d, int rows, const int32_t* slots, float* state,
+                        uint16_t* y, hipStream_t s) {
+  if (d.dk != kD || d.dv != kD || d.hk <= 0 || d.hv % d.hk != 0) return MX_EUNSUPPORTED;
+  if (rows <= 0) return MX_OK;
+  ScanArgs p{};
+  p.conv_out = conv_out; p.conv_stride = conv_stride; p.z = z; p.a = a; p.b = b;
+  p.zab_stride = zab_stride; p.a_log = a_log; p.dt_bias = dt_bias; p.norm_w = norm_w; p.eps = eps;
+  p.hk_heads = d.hk; p.hv_heads = d.hv; p.t = 1; p.slots = slots; p.state = state;
+  p.history = nullptr; p.y = y;
+  hipLaunchKernelGGL(recurrence_fast_kernel, dim3(d.hv, rows), dim3(kD), 0, s, p);
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
 
 int gdn_conv(const uint16_t* qkv, int64_t row_stride, int groups, int t, const int32_t* slots,
              uint16_t* conv_state, const float* conv_w, int channels, int conv_k, uint16_t* out,

@@ -270,3 +270,31 @@ def test_argmax_extremes(mx, orc):
     tok = mx.DeviceArray((4,), np.uint32)
     mx.check(mx.lib.mx_argmax_bf16(d.ptr, 4, n, tok.ptr, None))
     assert list(tok.numpy()) == [0, 777, 50, 0]
+
+
+@pytest.mark.parametrize("groups", [1, 8])
+def test_gdn_recurrence_fast_within_tolerance(mx, orc, groups):
+    """Fast-mode single-token step (hardware exp2 / log2 / rsqrt, wave-local q/k
+    norms) against the oracle's fixed-order step: fp32 state within 1e-4
+    relative (max norm), y within 2e-2 relative / 1e-2 absolute."""
+    hk, hv, S = 16, 32, 9
+    conv, z, a, b, a_log, dt, norm_w = _gdn_inputs(orc, groups, hk, hv, 900 + groups)
+    rng = np.random.default_rng(98)
+    state = (rng.standard_normal((S, hv, 128, 128)) * 0.05).astype(np.float32)
+    slots = rng.choice(S, groups, replace=False).astype(np.int32)
+    eps = 1e-6
+    y_w, st_w, _ = orc.gdn_recurrence(conv, z, a, b, a_log, dt, norm_w, eps, hk, hv, groups, 1,
+                                      slots, state)
+    zab = np.ascontiguousarray(np.concatenate([z, a, b], axis=1))
+    dzab = dev(mx, zab)
+    dconv, dal, ddt, dnw, dsl, dst = (dev(mx, v) for v in (conv, a_log, dt, norm_w, slots, state))
+    y = mx.DeviceArray((groups, hv * 128), np.uint16)
+    dims = gdn_dims(mx, hk, hv)
+    mx.check(mx.lib.mx_gdn_recurrence_fast(dconv.ptr, conv.shape[1], dzab.ptr,
+                                           dzab.ptr + 2 * hv * 128, dzab.ptr + 2 * (hv * 128 + hv),
+                                           zab.shape[1], dal.ptr, ddt.ptr, dnw.ptr, eps,
+                                           C.byref(dims), groups, dsl.ptr, dst.ptr, y.ptr, None))
+    st = dst.numpy()
+    assert np.abs(st - st_w).max() <= 1e-4 * np.abs(st_w).max()
+    got, want = bf(y.numpy()).astype(np.float64), bf(y_w).astype(np.float64)
+    assert np.all(np.abs(got - want) <= 2e-2 * np.abs(want) + 1e-2)
