@@ -140,6 +140,19 @@ __global__ __launch_bounds__(64 * T * KS) void dense_kernel(QWeight w,
       sum = sum + round_bf16(sigmoid_bf16(p) * xn);
     }
     e.y[size_t(m) * e.y_stride + c] = f32_to_bf16(round_bf16(sum) / 4.0f);
+  } else if constexpr (MODE == kHcWrite) {
+    // one residual stream per thread: the read-modify-writes of a column's
+    // streams are independent, so none waits on another's load
+    for (int i = threadIdx.x; i < 8 * NC * e.hc; i += 64 * T * KS) {
+      const int s = i / (8 * NC), mc = i - s * (8 * NC);
+      const int m = mc / NC, c = mc - m * NC;
+      const int r = tg * NC + c;
+      if (m >= M || r >= n) continue;
+      const float vb = round_bf16(yt[mc]);
+      uint16_t* res = e.y + size_t(m) * e.y_stride + size_t(s) * n + r;
+      const float inj = round_bf16(vb * bf16_to_f32(e.aux[size_t(m) * e.aux_stride + s]));
+      *res = f32_to_bf16(bf16_to_f32(*res) + inj);
+    }
   } else {
     for (int i = threadIdx.x; i < 8 * NC; i += 64 * T * KS) {
       const int m = i / NC, c = i - m * NC;
@@ -148,19 +161,12 @@ __global__ __launch_bounds__(64 * T * KS) void dense_kernel(QWeight w,
       const float v = yt[i];
       if constexpr (MODE == kPlain) {
         e.y[size_t(m) * e.y_stride + r] = f32_to_bf16(v);
-      } else if constexpr (MODE == kHcDown) {
+      } else {  // kHcDown
         const float tt = round_bf16(round_bf16(v) / float(e.hc));
         if (r < e.rank)
           e.y[size_t(m) * e.y_stride + r] = f32_to_bf16(tt * sigmoid_bf16(tt));
         else
           e.aux[size_t(m) * e.aux_stride + (r - e.rank)] = f32_to_bf16(sigmoid_bf16(tt) * 2.0f);
-      } else {  // kHcWrite
-        const float vb = round_bf16(v);
-        for (int s = 0; s < e.hc; ++s) {
-          uint16_t* res = e.y + size_t(m) * e.y_stride + size_t(s) * n + r;
-          const float inj = round_bf16(vb * bf16_to_f32(e.aux[size_t(m) * e.aux_stride + s]));
-          *res = f32_to_bf16(bf16_to_f32(*res) + inj);
-        }
       }
     }
   }
@@ -572,16 +578,23 @@ DenseCfg dense_cfg(const QWeight& w, const ProjEpilogue& e) {
   const bool mix = e.mode == kHcUpMix;
   const int tiles = mix ? 4 * ((e.hidden + 15) / 16) : (w.n + 15) / 16;
   const int max_ks = mix ? 4 : 16;
-  // deeper splits measured faster down to one super-step per slice while the
-  // launch has under ~3000 waves
+  // Measured at 8 rows on 4-bit weights: launches of 512+ column tiles run
+  // fastest as four tiles x four K-splits per workgroup (GDN-in 8.6 us,
+  // attention-in 8.3 us at K=2048); narrower ones as one tile split 8-16
+  // ways, down to one super-step per slice staged or four from registers
+  // (router 4.8 us, 4096x2048 5.3 us, 2048x4096 8.1 us).  Splits beyond
+  // ~3000 waves per launch measured slower.
   const int scw = (w.k % 512 == 0) ? 16 : 8;
+  const bool xreg = total > kStageSteps;
+  const int min_steps = xreg ? 4 : 1;
+  const int ks_cap = tiles >= 512 ? 4 : max_ks;
   int KS = 1;
   // rows with 8-byte scale loads (K % 512 != 0) are at most a few super-steps
   // deep and run unsplit
-  while (scw == 16 && KS < max_ks && tiles * KS < 3072 && total / (2 * KS) >= 1) KS *= 2;
+  while (scw == 16 && KS < ks_cap && tiles * KS < 3072 && total / (2 * KS) >= min_steps) KS *= 2;
   while (KS < max_ks && !scale_cover(total, KS, scw)) KS *= 2;
-  const int T = mix ? 4 : (KS <= 4 ? 4 : 16 / KS);
-  return DenseCfg{T, KS, total > kStageSteps, scw};
+  const int T = (mix || KS <= 4) ? 4 : 1;
+  return DenseCfg{T, KS, xreg, scw};
 }
 
 template <int BITS, int MODE, int T, int KS, bool XREG, int SCW>
@@ -607,7 +620,7 @@ int dense_shape(const QWeight& w, const uint16_t* x, int64_t xs, int m, const Pr
   MX_SHAPE(4, 1, false, 8)
   MX_SHAPE(4, 2, true, 16) MX_SHAPE(4, 4, true, 16)
   if constexpr (MODE != kHcUpMix) {
-    MX_SHAPE(2, 8, false, 16) MX_SHAPE(1, 16, false, 16) MX_SHAPE(2, 8, true, 16)
+    MX_SHAPE(1, 8, false, 16) MX_SHAPE(1, 16, false, 16) MX_SHAPE(1, 8, true, 16)
     MX_SHAPE(1, 16, true, 16)
   }
 #undef MX_SHAPE
