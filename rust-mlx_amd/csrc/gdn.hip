@@ -230,11 +230,11 @@ __global__ __launch_bounds__(kD) void recurrence_kernel(ScanArgs p) {
 
 // ---------------------------------------------------------------------------
 // Fast-mode single-token step (decode, t = 1, no history), same inputs and
-// outputs as recurrence_kernel<true>: each wave forms the q / k L2 norms itself
-// with lane shuffles (no barrier), q and k reach the 128 value-row threads
-// through LDS as float4, the output RMS norm is the only exchange between the
-// two waves, and the scalar functions use the hardware exp2 / log2 /
-// reciprocal / rsqrt.  The bf16 rounding points of the exact step (the
+// outputs as recurrence_kernel<true>: wave 0 forms the q / k L2 norms with lane
+// shuffles, q and k reach the threads through LDS as float4, the state's key
+// rows are split four ways among lanes (fp32 dot products summed in another
+// order than the exact step), and the scalar functions use the hardware exp2 /
+// log2 / reciprocal / rsqrt.  The bf16 rounding points of the exact step (the
 // reference's bf16 operations) are kept, so the step stays within the north
 // star's tolerances of the exact one layer after layer.
 __device__ __forceinline__ float exp_fast(float x) {
@@ -266,18 +266,29 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-__global__ __launch_bounds__(kD) void recurrence_fast_kernel(ScanArgs p) {
+// 512 threads per (value head, row): wave w owns value columns 16 w .. 16 w
+// + 15, lane l = 16 part + c column 16 w + c over the key rows 32 part .. 32
+// part + 31, so a thread holds 32 state values and every key-row dot product
+// ends in an exchange over the four parts (lanes l ^ 16, l ^ 32).  State
+// loads stay coalesced in 64-byte runs per part.
+constexpr int kFastParts = 4;
+constexpr int kFastRows = kD / kFastParts;  // key rows per thread
+
+__global__ __launch_bounds__(kD * kFastParts) void recurrence_fast_kernel(ScanArgs p) {
   const int hv = blockIdx.x;
   const int row = blockIdx.y;  // one token per group
-  const int i = threadIdx.x, lane = i & 63, wave = i >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 15, part = lane >> 4;
+  const int i = wave * 16 + c;  // value column
   const int hv_heads = p.hv_heads, hk_heads = p.hk_heads;
   const int hk = hv / (hv_heads / hk_heads);
   __shared__ float4 qs4[kD / 4], ks4[kD / 4];
-  __shared__ float red[2];
-  float* sp = p.state + (size_t(p.slots[row]) * hv_heads + hv) * kD * kD + i;
-  float s[kD];
+  __shared__ float red[kD * kFastParts / 64];
+  float* sp = p.state + (size_t(p.slots[row]) * hv_heads + hv) * kD * kD +
+              size_t(part * kFastRows) * kD + i;
+  float s[kFastRows];
 #pragma unroll
-  for (int d = 0; d < kD; ++d) s[d] = sp[size_t(d) * kD];
+  for (int d = 0; d < kFastRows; ++d) s[d] = sp[size_t(d) * kD];
   const uint16_t* cr = p.conv_out + size_t(row) * p.conv_stride;
   const float q0 = bf16_to_f32(cr[hk * kD + lane]), q1 = bf16_to_f32(cr[hk * kD + 64 + lane]);
   const float k0 = bf16_to_f32(cr[(hk_heads + hk) * kD + lane]);
@@ -285,13 +296,15 @@ __global__ __launch_bounds__(kD) void recurrence_fast_kernel(ScanArgs p) {
   const float vi = bf16_to_f32(cr[2 * hk_heads * kD + hv * kD + i]);
   const float bv = bf16_to_f32(p.b[size_t(row) * p.zab_stride + hv]);
   const float av = bf16_to_f32(p.a[size_t(row) * p.zab_stride + hv]);
+  const float zi = bf16_to_f32(p.z[size_t(row) * p.zab_stride + hv * kD + i]);
+  const float nw = bf16_to_f32(p.norm_w[i]);
   const float eps_l2 = round_bf16(1e-6f);
   const float qscale = round_bf16(0.08838834764831845f);  // bf16(Dk^-1/2), Dk = 128
-  const float qss = round_bf16(wave_sum(round_bf16(q0 * q0) + round_bf16(q1 * q1)));
-  const float kss = round_bf16(wave_sum(round_bf16(k0 * k0) + round_bf16(k1 * k1)));
-  const float rq = round_bf16(__builtin_amdgcn_rsqf(round_bf16(qss + eps_l2)));
-  const float rk = round_bf16(__builtin_amdgcn_rsqf(round_bf16(kss + eps_l2)));
   if (wave == 0) {
+    const float qss = round_bf16(wave_sum(round_bf16(q0 * q0) + round_bf16(q1 * q1)));
+    const float kss = round_bf16(wave_sum(round_bf16(k0 * k0) + round_bf16(k1 * k1)));
+    const float rq = round_bf16(__builtin_amdgcn_rsqf(round_bf16(qss + eps_l2)));
+    const float rk = round_bf16(__builtin_amdgcn_rsqf(round_bf16(kss + eps_l2)));
     float* qs = reinterpret_cast<float*>(qs4);
     float* ks = reinterpret_cast<float*>(ks4);
     qs[lane] = round_bf16(round_bf16(q0 * rq) * qscale);
@@ -303,10 +316,12 @@ __global__ __launch_bounds__(kD) void recurrence_fast_kernel(ScanArgs p) {
   const float x = round_bf16(av + bf16_to_f32(p.dt_bias[hv]));
   const float gdecay = exp_fast(-exp_fast(p.a_log[hv]) * softplus_bf16_fast(x));
   __syncthreads();
+  const float4* kp = ks4 + part * (kFastRows / 4);
+  const float4* qp = qs4 + part * (kFastRows / 4);
   float c0 = 0.0f, c1 = 0.0f, c2 = 0.0f, c3 = 0.0f;
 #pragma unroll
-  for (int d4 = 0; d4 < kD / 4; ++d4) {
-    const float4 kv4 = ks4[d4];
+  for (int d4 = 0; d4 < kFastRows / 4; ++d4) {
+    const float4 kv4 = kp[d4];
     const int d = 4 * d4;
     s[d] = s[d] * gdecay;
     s[d + 1] = s[d + 1] * gdecay;
@@ -317,11 +332,14 @@ __global__ __launch_bounds__(kD) void recurrence_fast_kernel(ScanArgs p) {
     c2 = fmaf_(s[d + 2], kv4.z, c2);
     c3 = fmaf_(s[d + 3], kv4.w, c3);
   }
-  const float delta = (vi - ((c0 + c1) + (c2 + c3))) * beta;
+  float cs = (c0 + c1) + (c2 + c3);
+  cs = cs + __shfl_xor(cs, 16, 64);
+  cs = cs + __shfl_xor(cs, 32, 64);
+  const float delta = (vi - cs) * beta;
   float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f;
 #pragma unroll
-  for (int d4 = 0; d4 < kD / 4; ++d4) {
-    const float4 kv4 = ks4[d4], qv4 = qs4[d4];
+  for (int d4 = 0; d4 < kFastRows / 4; ++d4) {
+    const float4 kv4 = kp[d4], qv4 = qp[d4];
     const int d = 4 * d4;
     s[d] = fmaf_(kv4.x, delta, s[d]);
     s[d + 1] = fmaf_(kv4.y, delta, s[d + 1]);
@@ -333,17 +351,26 @@ __global__ __launch_bounds__(kD) void recurrence_fast_kernel(ScanArgs p) {
     o3 = fmaf_(s[d + 3], qv4.w, o3);
   }
 #pragma unroll
-  for (int d = 0; d < kD; ++d) sp[size_t(d) * kD] = s[d];
-  const float zi = bf16_to_f32(p.z[size_t(row) * p.zab_stride + hv * kD + i]);
-  const float nw = bf16_to_f32(p.norm_w[i]);
-  const float yo = round_bf16((o0 + o1) + (o2 + o3));
-  const float ws = wave_sum(yo * yo);
+  for (int d = 0; d < kFastRows; ++d) sp[size_t(d) * kD] = s[d];
+  float os = (o0 + o1) + (o2 + o3);
+  os = os + __shfl_xor(os, 16, 64);
+  os = os + __shfl_xor(os, 32, 64);
+  const float yo = round_bf16(os);
+  // the four parts of a column hold the same yo: part 0 enters the norm
+  const float ws = wave_sum(part == 0 ? yo * yo : 0.0f);
   if (lane == 0) red[wave] = ws;
   __syncthreads();
-  const float inv = __builtin_amdgcn_rsqf((red[0] + red[1]) * (1.0f / kD) + p.eps);
-  const float normed = round_bf16(nw * round_bf16(yo * inv));
-  p.y[size_t(row) * (size_t(hv_heads) * kD) + hv * kD + i] = f32_to_bf16(normed * sigmoid_fast(zi));
+  float tot = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kD * kFastParts / 64; ++w) tot = tot + red[w];
+  const float inv = __builtin_amdgcn_rsqf(tot * (1.0f / kD) + p.eps);
+  if (part == 0) {
+    const float normed = round_bf16(nw * round_bf16(yo * inv));
+    p.y[size_t(row) * (size_t(hv_heads) * kD) + hv * kD + i] =
+        f32_to_bf16(normed * sigmoid_fast(zi));
+  }
 }
+
 
 }  // namespace
 
@@ -359,7 +386,7 @@ int gdn_recurrence_fast(const uint16_t* conv_out, int64_t conv_stride, const uin
   p.zab_stride = zab_stride; p.a_log = a_log; p.dt_bias = dt_bias; p.norm_w = norm_w; p.eps = eps;
   p.hk_heads = d.hk; p.hv_heads = d.hv; p.t = 1; p.slots = slots; p.state = state;
   p.history = nullptr; p.y = y;
-  hipLaunchKernelGGL(recurrence_fast_kernel, dim3(d.hv, rows), dim3(kD), 0, s, p);
+  hipLaunchKernelGGL(recurrence_fast_kernel, dim3(d.hv, rows), dim3(kD * kFastParts), 0, s, p);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 

@@ -110,23 +110,27 @@ __global__ __launch_bounds__(64 * kMaxDownWaves) void hc_down_kernel(
   const int ks0 = stream * (hidden / sk::kSuper) + wave * SPW;  // super-step within K
   const int m = j & 7;
   const bool live = ((j < 8) == (q < 2)) && m < M;
-  const uint16_t* hrow = h + size_t(m < M ? m : M - 1) * K + 32 * q;
-  const uint16_t* wrow = scale + 32 * q;
-  const uint32_t* crow = w.codes + size_t(row) * (size_t(K) * BITS / 32);
+  // the lane's data at super-step ks0; super-step ks0 + i sits a constant
+  // offset further
+  const uint16_t* hrow = h + size_t(m < M ? m : M - 1) * K + size_t(ks0) * sk::kSuper + 32 * q;
+  const uint16_t* wrow = scale + size_t(ks0) * sk::kSuper + 32 * q;
+  const uint32_t* clane =
+      w.codes + size_t(row) * (size_t(K) * BITS / 32) + size_t(4 * BITS) * ks0 + BITS * q;
+  const uint16_t* srow = w.scales + size_t(row) * G + 2 * ks0;
+  const uint16_t* brow = w.biases + size_t(row) * G + 2 * ks0;
   // every load up front: codes, scale/bias words, h and norm weights
   uint32_t wc[SPW][BITS];
   uint32_t sw[SPW], bw[SPW];
   uint4 hx[SPW][4], wx[SPW][4];
 #pragma unroll
   for (int i = 0; i < SPW; ++i) {
-    const int ks = ks0 + i;
-    sk::load_codes<BITS>(crow, ks, q, wc[i]);
-    sw[i] = *reinterpret_cast<const uint32_t*>(w.scales + size_t(row) * G + 2 * ks);
-    bw[i] = *reinterpret_cast<const uint32_t*>(w.biases + size_t(row) * G + 2 * ks);
+    sk::load_codes<BITS>(clane, i, wc[i]);
+    sw[i] = *reinterpret_cast<const uint32_t*>(srow + 2 * i);
+    bw[i] = *reinterpret_cast<const uint32_t*>(brow + 2 * i);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      hx[i][u] = *reinterpret_cast<const uint4*>(hrow + size_t(ks) * sk::kSuper + 8 * u);
-      wx[i][u] = *reinterpret_cast<const uint4*>(wrow + size_t(ks) * sk::kSuper + 8 * u);
+      hx[i][u] = *reinterpret_cast<const uint4*>(hrow + i * sk::kSuper + 8 * u);
+      wx[i][u] = *reinterpret_cast<const uint4*>(wrow + i * sk::kSuper + 8 * u);
     }
   }
   const uint4 zero = make_uint4(0u, 0u, 0u, 0u);

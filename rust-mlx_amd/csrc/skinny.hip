@@ -44,6 +44,9 @@ constexpr int kDownSteps = 8;
 // Waves per gate/up tile (K split inside the workgroup): halves each wave's
 // registers so more workgroups stay resident.
 constexpr int kGateUpSplit = 2;
+// persistent gate/up: 16-row tiles per item and waves per tile (depth split)
+constexpr int kPersistTiles = 4;
+constexpr int kPersistSplit = 2;
 
 // Sums the KS slices of each tile into yt[m][t * 16 + j] (fp32 [8][16 T]).
 // red: LDS [KS][T][8][16] (unused when KS == 1).  Ends with a barrier.
@@ -369,11 +372,21 @@ __device__ __forceinline__ int build_leaders(uint32_t my_id, int rows, int top_k
   return *count;
 }
 
-template <int BITS, int STEPS>
-__global__ __launch_bounds__(512) void gate_up_persist_kernel(
+// Persistent expert gate/up.  An item is one leader expert's 16 * TPI / 2
+// intermediate rows of gate and the same rows of up: TPI 16-row tiles, the
+// first half gate, the second up.  KS waves share a tile, each taking 1/KS of
+// the depth; a workgroup is TPI * KS waves and walks the items
+// blockIdx.x, blockIdx.x + P, ... with the next item's weights in flight
+// while the current one computes.
+template <int BITS, int STEPS, int TPI, int KS>
+__global__ __launch_bounds__(64 * TPI * KS) void gate_up_persist_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ ids, int rows, int top_k,
     QBank gate, QBank up, QWeight sgate, QWeight sup, uint16_t* __restrict__ h, int hs) {
-  constexpr int KS = 2;  // waves per tile: each takes half of the depth
+  static_assert(TPI == 2 || TPI == 4, "tiles per item");
+  constexpr int HALF = TPI / 2;   // tiles of gate (and of up) per item
+  constexpr int C = 16 * HALF;    // intermediate rows (h columns) per item
+  constexpr int RED = KS * TPI * 8 * 16;
+  constexpr int NT = 64 * TPI * KS;
   extern __shared__ __align__(16) char lds[];
   __shared__ int first[kPersistMaxExperts];
   __shared__ unsigned long long info[kPersistMaxExperts];
@@ -381,8 +394,10 @@ __global__ __launch_bounds__(512) void gate_up_persist_kernel(
   __shared__ int lead_e[kPersistMaxRoutes + 1];
   __shared__ unsigned long long lead_info[kPersistMaxRoutes + 1];
   __shared__ int count;
-  __shared__ float red[KS * 4 * 8 * 16];
-  __shared__ float yt[8 * 64];
+  // partial sums, alternating between two halves item by item: an item's
+  // epilogue reads one half while the next item writes the other, so one
+  // barrier per item separates writers from readers
+  __shared__ float red[2 * RED];
   constexpr int steps = STEPS;  // hidden = 128 STEPS
   constexpr int hidden = STEPS * sk::kSuper;
   constexpr int G = hidden / 64;
@@ -392,71 +407,88 @@ __global__ __launch_bounds__(512) void gate_up_persist_kernel(
   const sk::DenseRows xr{x, hidden, rows};
   // route ids first (the expert list needs them), then the x staging loads
   const uint32_t my_id = ids[min(int(threadIdx.x), rows * top_k - 1)];
-  sk::Stager<512, sk::stage_per(512, STEPS), sk::DenseRows> stg(xr, rows, 0, steps);
+  sk::Stager<NT, sk::stage_per(NT, STEPS), sk::DenseRows> stg(xr, rows, 0, steps);
   stg.load();
   const int nlead = build_leaders(my_id, rows, top_k, gate.experts, first, info, route_e, lead_e,
                                   lead_info, &count);
-  const int groups = inter / 32;
+  const int groups = inter / C;
   const int items = nlead * groups;
   const int P = gridDim.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane & 15;
   const int t = wave / KS, ks = wave - t * KS;
   constexpr int n = steps / KS;
   const int k0 = n * ks;
-  // weight rows of item `it` for this wave (tile t, depth half ks)
+  // weight rows of item `it` for this wave (tile t, depth slice ks); past the
+  // last item the workgroup's first item again (its lines are cached, and the
+  // loads stay unconditional)
   auto stream_for = [&](int it) {
+    if (it >= items) it = blockIdx.x;
     const int lead = it / groups, g = it - lead * groups;
     const int e = lead_e[lead];
-    const QWeight w = expert_weight(t < 2 ? gate : up, e, t < 2 ? sgate : sup);
-    const int row = g * 32 + (t & 1) * 16 + j;
+    const QWeight w = expert_weight(t < HALF ? gate : up, e, t < HALF ? sgate : sup);
+    const int row = g * C + (t % HALF) * 16 + j;
     return sk::Stream<BITS, false, sk::DenseRows, n, 16>(
         w.codes + size_t(row) * (size_t(hidden) * BITS / 32), w.scales + size_t(row) * G,
         w.biases + size_t(row) * G, steps, k0, n, 0, lds, sx, xr, rows);
   };
+  int half = 0;
   auto finish = [&](int it, float (&y)[4]) {
-    reduce_tiles<4, KS>(y, red, yt);
-    const int lead = it / groups, g = it - lead * groups;
-    const unsigned long long inf = lead_info[lead];
-    if (threadIdx.x < 256) {
-      const int m = threadIdx.x >> 5, c = threadIdx.x & 31;
-      if ((inf >> m) & 1ull) {
-        const int slot = int((inf >> (8 + 5 * m)) & 31ull);
-        const float gv = round_bf16(yt[m * 64 + c]);
-        const float uv = round_bf16(yt[m * 64 + 32 + c]);
-        const float silu = round_bf16(gv * sigmoid_fast(gv));
-        h[(size_t(m) * (top_k + 1) + slot) * hs + g * 32 + c] = f32_to_bf16(silu * uv);
-      }
+    sk::join_parities(y);
+    float* rb = red + half * RED;
+    if ((lane >> 4) < 2) {
+      const int q = lane >> 4;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) rb[((ks * TPI + t) * 8 + 4 * q + r) * 16 + j] = y[r];
     }
     __syncthreads();
+    const int lead = it / groups, g = it - lead * groups;
+    const unsigned long long inf = lead_info[lead];
+    if (threadIdx.x < 8 * C) {
+      const int m = threadIdx.x / C, c = threadIdx.x % C;
+      if ((inf >> m) & 1ull) {
+        const int slot = int((inf >> (8 + 5 * m)) & 31ull);
+        const int tt = c >> 4, jj = c & 15;
+        float gs = 0.0f, us = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+          gs = gs + rb[((k * TPI + tt) * 8 + m) * 16 + jj];
+          us = us + rb[((k * TPI + HALF + tt) * 8 + m) * 16 + jj];
+        }
+        const float gv = round_bf16(gs);
+        const float uv = round_bf16(us);
+        const float silu = round_bf16(gv * sigmoid_fast(gv));
+        h[(size_t(m) * (top_k + 1) + slot) * hs + g * C + c] = f32_to_bf16(silu * uv);
+      }
+    }
+    half ^= 1;
+  };
+  auto step = [&](auto& st, int it) {
+    float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    st.run(xbytes, y);
+    finish(it, y);
   };
   if (int(blockIdx.x) >= items) return;  // uniform
   // the first item's weights go out before the staged x is written
   auto sa = stream_for(blockIdx.x);
   sa.prefetch();
   stg.store(lds);
+  auto sb = stream_for(blockIdx.x + P);
+  sb.prefetch();
   for (int it = blockIdx.x; it < items; it += 2 * P) {
-    const int ib = it + P;
-    // the next item's weights (this item again when there is none: its lines
-    // are in the cache, and the loads stay unconditional)
-    auto sb = stream_for(ib < items ? ib : it);
-    sb.prefetch();
-    float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    sa.run(xbytes, y);
-    finish(it, y);
-    const int ia = it + 2 * P;
-    sa = stream_for(ia < items ? ia : (ib < items ? ib : it));
+    step(sa, it);
+    sa = stream_for(it + 2 * P);
     sa.prefetch();
-    if (ib < items) {
-      float yb[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      sb.run(xbytes, yb);
-      finish(ib, yb);
-    }
+    if (it + P < items) step(sb, it + P);
+    sb = stream_for(it + 3 * P);
+    sb.prefetch();
   }
 }
 
 // down + score: p[row][slot][n] = bf16(bf16(down) * score) (routed slots) or
-// bf16(down) (the shared slot, top_k).
-template <int BITS>
+// bf16(down) (the shared slot, top_k).  STEPS > 0: every expert (shared one
+// included) is STEPS super-steps deep, all loaded in one batch; STEPS == 0:
+// depths up to kDownSteps read from the bank.
+template <int BITS, int STEPS>
 __global__ __launch_bounds__(256, 4) void down_kernel(const uint16_t* __restrict__ h,
                                                    const uint32_t* __restrict__ ids,
                                                    const uint16_t* __restrict__ scores, int rows,
@@ -473,14 +505,15 @@ __global__ __launch_bounds__(256, 4) void down_kernel(const uint16_t* __restrict
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane & 15;
   const int row = min(tg * 64 + wave * 16 + j, hidden - 1);
   const int G = inter >> 6;
-  const int steps = inter / sk::kSuper;
+  const int steps = STEPS > 0 ? STEPS : inter / sk::kSuper;
   const sk::RouteRows xr{h, int64_t(top_k + 1) * hs, hs, rt.packed, rt.M};
   const int xbytes = steps * sk::kStepBytes;
   const float* sx = reinterpret_cast<const float*>(lds + xbytes + sk::kZeroBytes);
-  sk::Stream<BITS, false, sk::RouteRows, kDownSteps / 2, 8> st(
+  sk::Stream<BITS, false, sk::RouteRows, (STEPS > 0 ? STEPS : kDownSteps / 2), 8> st(
       dw.codes + size_t(row) * (size_t(inter) * BITS / 32), dw.scales + size_t(row) * G,
       dw.biases + size_t(row) * G, steps, 0, steps, 0, lds, sx, xr, rt.M);
-  sk::Stager<256, sk::stage_per(256, kDownSteps), sk::RouteRows> stg(xr, rt.M, 0, steps);
+  sk::Stager<256, sk::stage_per(256, (STEPS > 0 ? STEPS : kDownSteps)), sk::RouteRows> stg(
+      xr, rt.M, 0, steps);
   stg.load();
   st.prefetch();
   stg.store(lds);
@@ -674,32 +707,33 @@ int skinny_gate_up(const uint16_t* x, const uint32_t* ids, int rows, int top_k,
     return MX_EUNSUPPORTED;
   const int lb = sk::stage_bytes(steps);
   if (gate.experts <= kPersistMaxExperts && rows * top_k <= kPersistMaxRoutes &&
-      sgate.n == gate.n && up.n == gate.n && gate.n % 32 == 0 && steps == kStageSteps) {
+      sgate.n == gate.n && up.n == gate.n && gate.n % (8 * kPersistTiles) == 0 &&
+      steps == kStageSteps) {
     // one workgroup per resident slot: every workgroup is on the chip from the start
     static int slots[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
     const void* fn = nullptr;
     switch (gate.bits) {
-      case 4: fn = reinterpret_cast<const void*>(gate_up_persist_kernel<4, kStageSteps>); break;
-      case 5: fn = reinterpret_cast<const void*>(gate_up_persist_kernel<5, kStageSteps>); break;
-      case 6: fn = reinterpret_cast<const void*>(gate_up_persist_kernel<6, kStageSteps>); break;
-      default: fn = reinterpret_cast<const void*>(gate_up_persist_kernel<8, kStageSteps>); break;
+      case 4: fn = reinterpret_cast<const void*>(gate_up_persist_kernel<4, kStageSteps, kPersistTiles, kPersistSplit>); break;
+      case 5: fn = reinterpret_cast<const void*>(gate_up_persist_kernel<5, kStageSteps, kPersistTiles, kPersistSplit>); break;
+      case 6: fn = reinterpret_cast<const void*>(gate_up_persist_kernel<6, kStageSteps, kPersistTiles, kPersistSplit>); break;
+      default: fn = reinterpret_cast<const void*>(gate_up_persist_kernel<8, kStageSteps, kPersistTiles, kPersistSplit>); break;
     }
     int& grid_n = slots[gate.bits];
     if (grid_n == 0) {
       int dev = 0, cus = 0, per_cu = 0;
       if (hipGetDevice(&dev) != hipSuccess ||
           hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-          hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 512, lb) != hipSuccess ||
+          hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 64 * kPersistTiles * kPersistSplit, lb) != hipSuccess ||
           cus <= 0 || per_cu <= 0)
         return MX_EHIP;
       grid_n = cus * per_cu;
     }
     const dim3 pgrid(grid_n);
     switch (gate.bits) {
-      case 4: hipLaunchKernelGGL((gate_up_persist_kernel<4, kStageSteps>), pgrid, dim3(512), lb, s, x, ids, rows, top_k, gate, up, sgate, sup, h, hs); break;
-      case 5: hipLaunchKernelGGL((gate_up_persist_kernel<5, kStageSteps>), pgrid, dim3(512), lb, s, x, ids, rows, top_k, gate, up, sgate, sup, h, hs); break;
-      case 6: hipLaunchKernelGGL((gate_up_persist_kernel<6, kStageSteps>), pgrid, dim3(512), lb, s, x, ids, rows, top_k, gate, up, sgate, sup, h, hs); break;
-      default: hipLaunchKernelGGL((gate_up_persist_kernel<8, kStageSteps>), pgrid, dim3(512), lb, s, x, ids, rows, top_k, gate, up, sgate, sup, h, hs); break;
+      case 4: hipLaunchKernelGGL((gate_up_persist_kernel<4, kStageSteps, kPersistTiles, kPersistSplit>), pgrid, dim3(64 * kPersistTiles * kPersistSplit), lb, s, x, ids, rows, top_k, gate, up, sgate, sup, h, hs); break;
+      case 5: hipLaunchKernelGGL((gate_up_persist_kernel<5, kStageSteps, kPersistTiles, kPersistSplit>), pgrid, dim3(64 * kPersistTiles * kPersistSplit), lb, s, x, ids, rows, top_k, gate, up, sgate, sup, h, hs); break;
+      case 6: hipLaunchKernelGGL((gate_up_persist_kernel<6, kStageSteps, kPersistTiles, kPersistSplit>), pgrid, dim3(64 * kPersistTiles * kPersistSplit), lb, s, x, ids, rows, top_k, gate, up, sgate, sup, h, hs); break;
+      default: hipLaunchKernelGGL((gate_up_persist_kernel<8, kStageSteps, kPersistTiles, kPersistSplit>), pgrid, dim3(64 * kPersistTiles * kPersistSplit), lb, s, x, ids, rows, top_k, gate, up, sgate, sup, h, hs); break;
     }
     return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
   }
@@ -725,8 +759,19 @@ int skinny_down(const uint16_t* h, const uint32_t* ids, const uint16_t* scores, 
     return MX_EUNSUPPORTED;
   const dim3 grid((down.n + 63) / 64, rows * top_k + 1);
   const int lb = sk::stage_bytes(kmax / sk::kSuper);
-#define MX_DN(B) \
-  case B: hipLaunchKernelGGL(down_kernel<B>, grid, dim3(256), lb, s, h, ids, scores, rows, top_k, down, sdown, p, hs); break;
+  // 512-deep experts (the common MoE shape) run with their depth fixed at
+  // compile time: one batch of loads and, at 4-8 bits, 60-66 VGPRs (twice
+  // the resident waves of the general form)
+  const bool d4 = down.k == 4 * sk::kSuper && sdown.k == 4 * sk::kSuper;
+#define MX_DN(B)                                                                            \
+  case B:                                                                                   \
+    if (d4)                                                                                 \
+      hipLaunchKernelGGL((down_kernel<B, 4>), grid, dim3(256), lb, s, h, ids, scores, rows, \
+                         top_k, down, sdown, p, hs);                                        \
+    else                                                                                    \
+      hipLaunchKernelGGL((down_kernel<B, 0>), grid, dim3(256), lb, s, h, ids, scores, rows, \
+                         top_k, down, sdown, p, hs);                                        \
+    break;
   switch (down.bits) {
     MX_DN(4) MX_DN(5) MX_DN(6) MX_DN(8)
     default: return MX_EUNSUPPORTED;

@@ -78,9 +78,11 @@ constexpr float code_offset() {
 
 // The lane's BITS words of super-step s (values 128 s + 32 q .. +31 of the row).
 template <int BITS>
-__device__ __forceinline__ void load_codes(const uint32_t* __restrict__ row, int s, int q,
+// lane: the lane's words of its slice's first super-step (row + 4 BITS ks0
+// + BITS q); s: super-step within the slice (a constant offset once unrolled).
+__device__ __forceinline__ void load_codes(const uint32_t* __restrict__ lane, int s,
                                            uint32_t (&w)[BITS]) {
-  const uint32_t* p = row + (4 * BITS) * s + BITS * q;
+  const uint32_t* p = lane + (4 * BITS) * s;
   if constexpr (BITS == 4) {
     const uint4 v = *reinterpret_cast<const uint4*>(p);
     w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
@@ -266,13 +268,13 @@ struct Stream {
       XREG ? 1 : (batch_steps<BITS>() < BMAX ? batch_steps<BITS>() : BMAX);
   static constexpr int SQ = SCW / 4;
   typedef typename std::conditional<SCW == 16, uint4, uint2>::type Quad;
-  const uint32_t* crow;
+  const uint32_t* cq;     // the lane's words of the slice's first super-step
   const uint16_t* srow;
   const uint16_t* brow;
   int ks0, steps, wks0, base, row_steps;
   const char* lds;   // staged x tile (XREG = false)
   const float* sx;   // staged group sums (XREG = false)
-  const uint16_t* xrow;  // this lane's activation row (XREG = true; always valid)
+  const uint16_t* xrow;  // the lane's activations of the slice's first super-step (XREG = true)
   bool xlive;            // the lane's A operand is live (XREG = true)
   Quad scq, bcq;
   uint32_t wa[B][BITS], wb[B][BITS];
@@ -285,10 +287,11 @@ struct Stream {
   __device__ __forceinline__ Stream(const uint32_t* c, const uint16_t* sr, const uint16_t* br,
                                     int rs, int k0, int n, int w0, const char* l, const float* s,
                                     const Rows& xr, int M)
-      : crow(c), srow(sr), brow(br), ks0(k0), steps(n), wks0(w0), row_steps(rs), lds(l), sx(s) {
+      : srow(sr), brow(br), ks0(k0), steps(n), wks0(w0), row_steps(rs), lds(l), sx(s) {
     const int lane = threadIdx.x & 63;
     j = lane & 15;
     q = lane >> 4;
+    cq = c + size_t(4 * BITS) * ks0 + BITS * q;
     base = ks0 - ks0 % SQ;
     half_sel = (q >> 1) ? 0x07060c0cu : 0x05040c0cu;
     act = (j < 8) == (q < 2);
@@ -297,7 +300,7 @@ struct Stream {
     xrow = nullptr;
     if constexpr (XREG) {
       xlive = act && (j & 7) < M;
-      xrow = xr((j & 7) < M ? (j & 7) : 0);
+      xrow = xr((j & 7) < M ? (j & 7) : 0) + size_t(ks0) * kSuper + 32 * q;
     }
   }
 
@@ -305,10 +308,11 @@ struct Stream {
                                        int s0) {
 #pragma unroll
     for (int i = 0; i < B; ++i) {
-      const int ks = ks0 + min(s0 + i, steps - 1);
-      load_codes<BITS>(crow, ks, q, w[i]);
+      // super-steps past the slice are clamped to its last one
+      const int ls = min(s0 + i, steps - 1);
+      load_codes<BITS>(cq, ls, w[i]);
       if constexpr (XREG) {
-        const uint4* p = reinterpret_cast<const uint4*>(xrow + size_t(ks) * kSuper + 32 * q);
+        const uint4* p = reinterpret_cast<const uint4*>(xrow + ls * kSuper);
 #pragma unroll
         for (int u = 0; u < 4; ++u) xv[i][u] = p[u];
       }

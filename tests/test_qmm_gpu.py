@@ -62,6 +62,60 @@ def test_moe_experts_mfma_within_tolerance(mx, orc):
     assert np.mean(got == want) > 0.5  # mostly identical after bf16 rounding
 
 
+def _experts_mfma(mx, m, x, ids, scores, top_k):
+    from test_layers_gpu import dev
+
+    rows = x.shape[0]
+    p = mx.DeviceArray((rows, top_k + 1, m.H), np.uint16)
+    qb = [b.c() for b in (m.gate, m.up, m.down)]
+    qs = [w.c() for w in (m.sg, m.su, m.sd)]
+    dx, di, ds = dev(mx, x), dev(mx, ids), dev(mx, scores)
+    mx.check(mx.lib.mx_moe_experts_mfma(dx.ptr, di.ptr, ds.ptr, rows, top_k, C.byref(qb[0]),
+                                        C.byref(qb[1]), C.byref(qb[2]), C.byref(qs[0]),
+                                        C.byref(qs[1]), C.byref(qs[2]), m.ws.ptr, p.ptr, None))
+    return p.numpy()
+
+
+@pytest.mark.parametrize("bits", [4, 5, 6, 8])
+def test_moe_experts_mfma_every_width(mx, orc, bits):
+    """Hidden 2048 takes the persistent gate/up kernel (three items in flight
+    per wave at <= 5-bit codes, two above) and 512-deep experts the
+    fixed-depth down kernel."""
+    from test_layers_gpu import Moe
+
+    E, I, H, top_k, rows = 40, 512, 2048, 8, 8
+    m = Moe(mx, orc, E, I, H, seed=700 + bits, gbits=bits, dbits=bits)
+    rng = np.random.default_rng(bits)
+    ids = np.stack([rng.choice(E, top_k, replace=False) for _ in range(rows)]).astype(np.uint32)
+    scores = orc.f32_to_bf16(rng.uniform(0.05, 0.5, (rows, top_k)).astype(np.float32))
+    x = orc.fill_bf16(rows * H, 710 + bits, 1, 1.0, 0.0).reshape(rows, H)
+    want = bf(m.run(mx, x, ids, scores, top_k)).astype(np.float64)
+    got = bf(_experts_mfma(mx, m, x, ids, scores, top_k)).astype(np.float64)
+    scale = np.abs(want).max(axis=2, keepdims=True)
+    assert np.all(np.abs(got - want) <= 2e-2 * np.abs(want) + 1e-2 * scale)
+    assert np.mean(got == want) > 0.5
+
+
+@pytest.mark.parametrize("I,sI", [(1024, 512), (256, 768), (512, 512)])
+def test_moe_experts_mfma_mixed_depths(mx, orc, I, sI):
+    """Routed and shared experts of different 256-multiple depths (the down
+    kernel's general form, depth read per expert) and of equal 512 depth (its
+    fixed-depth form), at hidden 512 (the per-route gate/up kernel)."""
+    from test_layers_gpu import Moe
+
+    E, H, top_k, rows = 32, 512, 6, 8
+    m = Moe(mx, orc, E, I, H, seed=600 + I, sI=sI)
+    rng = np.random.default_rng(I + sI)
+    ids = np.stack([rng.choice(E, top_k, replace=False) for _ in range(rows)]).astype(np.uint32)
+    scores = orc.f32_to_bf16(rng.uniform(0.05, 0.5, (rows, top_k)).astype(np.float32))
+    x = orc.fill_bf16(rows * H, 610, 1, 1.0, 0.0).reshape(rows, H)
+    want = bf(m.run(mx, x, ids, scores, top_k)).astype(np.float64)
+    got = bf(_experts_mfma(mx, m, x, ids, scores, top_k)).astype(np.float64)
+    scale = np.abs(want).max(axis=2, keepdims=True)
+    assert np.all(np.abs(got - want) <= 2e-2 * np.abs(want) + 1e-2 * scale)
+    assert np.mean(got == want) > 0.5
+
+
 @pytest.mark.parametrize("n,k", [(260, 8192), (2048, 4096), (513, 2048), (12352, 2048)])
 def test_qmm_k_split_shapes_deterministic(mx, orc, n, k):
     """Shapes whose k is split among a workgroup's waves (the engine's HC,
