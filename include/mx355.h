@@ -226,6 +226,20 @@ mx_status mx_moe_experts_mfma(const uint16_t* x, const uint32_t* ids, const uint
                               const mx_qweight* shared_gate, const mx_qweight* shared_up,
                               const mx_qweight* shared_down, void* workspace, uint16_t* partial,
                               void* stream);
+/* The routing tail and the matrix-core experts in one call: mx_moe_route's
+ * contract for ids / scores / factor (bit-identical results), then
+ * mx_moe_experts_mfma's for partial.  With 512 routed experts and hidden 2048
+ * the expert gate/up kernel routes its rows itself, saving the routing launch.
+ * Replaces moe_route::tail (src/moe_route.rs:25-70) followed by the expert
+ * MLPs of MoE::parts (src/hybrid.rs:217-271). */
+mx_status mx_moe_routed_experts_mfma(const uint16_t* logits, int64_t logit_stride,
+                                     const uint16_t* shared_logit, int64_t shared_stride,
+                                     int32_t experts, const uint16_t* x, int32_t rows,
+                                     int32_t top_k, const mx_qbank* gate, const mx_qbank* up,
+                                     const mx_qbank* down, const mx_qweight* shared_gate,
+                                     const mx_qweight* shared_up, const mx_qweight* shared_down,
+                                     void* workspace, uint32_t* ids, uint16_t* scores,
+                                     uint16_t* factor, uint16_t* partial, void* stream);
 /* routed[r] = bf16 sum of partial[r, 0..top_k-1] in the reference's slot
  * order (kernels/moe_down_tail.h:20, moe_down_tail.metal:83-99). */
 mx_status mx_moe_reduce(const uint16_t* partial, int32_t rows, int32_t top_k, int32_t hidden,

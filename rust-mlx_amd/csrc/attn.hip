@@ -26,13 +26,6 @@ namespace {
 constexpr int kMaxHd = 256;
 constexpr int kMaxGroup = 16;  // q heads per kv head
 
-__device__ __forceinline__ float sigmoid_bf16(float x) {
-  const float e = round_bf16(expf_(__builtin_fabsf(x)));
-  const float d = round_bf16(1.0f + e);
-  const float y = round_bf16(1.0f / d);
-  return x < 0.0f ? y : round_bf16(1.0f - y);
-}
-
 // ---------------------------------------------------------------------------
 // One wave per (row, head): zero-centred RMS norm over head_dim, then RoPE on
 // the first rotary_dim values (halves rotated), written to q_out (q heads) or

@@ -65,6 +65,15 @@ MX_HD float expf_(float x) {
   return p * u2f(uint32_t(ni + 127) << 23);
 }
 
+// bf16 logistic function with MLX's per-operation bf16 rounding
+// (reference kernels/moe_route_tail.metal:119-123).
+__device__ __forceinline__ float sigmoid_bf16(float x) {
+  const float e = round_bf16(expf_(__builtin_fabsf(x)));
+  const float d = round_bf16(1.0f + e);
+  const float y = round_bf16(1.0f / d);
+  return x < 0.0f ? y : round_bf16(1.0f - y);
+}
+
 // log(1 + u) for u > -1: w = 1 + u split as m * 2^e with m in [sqrt(1/2),
 // sqrt(2)); log m from the atanh series in s = (m-1)/(m+1); first-order
 // correction for the rounding of w.

@@ -572,14 +572,23 @@ int record_step(Engine& e, int rows, int groups, int t, bool history, bool logit
     rl.y = e.logits_r;
     rl.y_stride = c.experts + 1;
     MX_TRY(project(e, L.router, e.mixed, c.hidden, rows, rl));
-    MX_TRY(moe_route(e.logits_r, c.experts + 1, e.logits_r + c.experts, c.experts + 1, rows,
-                     c.experts, c.top_k, e.ids, e.scores, e.factor, e.stream));
-    if (e.prof) {
-      MX_TRY(profile_experts(e, L, rows));
-    } else {
-      if (!experts_fast(e, L)) MX_TRY(moe_plan(e.ids, rows, c.top_k, e.moe_plan_buf, e.stream));
-      MX_TRY(experts_gate_up(e, L, rows));
+    if (!e.prof && experts_fast(e, L)) {
+      // the expert gate/up kernel routes the rows itself
+      const RouteIO ro{e.logits_r, c.experts + 1, e.logits_r + c.experts, c.experts + 1,
+                       e.ids, e.scores, e.factor};
+      MX_TRY(skinny_route_gate_up(ro, c.experts, e.mixed, rows, c.top_k, L.gate, L.up, L.sgate,
+                                  L.sup, e.moe_h, e.stream));
       MX_TRY(experts_down(e, L, rows));
+    } else {
+      MX_TRY(moe_route(e.logits_r, c.experts + 1, e.logits_r + c.experts, c.experts + 1, rows,
+                       c.experts, c.top_k, e.ids, e.scores, e.factor, e.stream));
+      if (e.prof) {
+        MX_TRY(profile_experts(e, L, rows));
+      } else {
+        MX_TRY(moe_plan(e.ids, rows, c.top_k, e.moe_plan_buf, e.stream));
+        MX_TRY(experts_gate_up(e, L, rows));
+        MX_TRY(experts_down(e, L, rows));
+      }
     }
     MX_TRY(moe_reduce_hc_epilogue(e.moe_p, e.factor, e.h, e.inj, rows, c.top_k, c.hc, c.hidden,
                                   e.h, e.stream));

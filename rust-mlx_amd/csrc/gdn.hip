@@ -20,14 +20,6 @@ namespace mx {
 
 namespace {
 
-// bf16 logistic with per-operation bf16 rounding (MLX Sigmoid at bfloat).
-__device__ __forceinline__ float sigmoid_bf16(float x) {
-  const float e = round_bf16(expf_(__builtin_fabsf(x)));
-  const float d = round_bf16(1.0f + e);
-  const float y = round_bf16(1.0f / d);
-  return x < 0.0f ? y : round_bf16(1.0f - y);
-}
-
 // logaddexp(x, 0) at bfloat (MLX LogAddExp with per-operation bf16 rounding).
 __device__ __forceinline__ float softplus_bf16(float x) {
   if (x != x) return x;

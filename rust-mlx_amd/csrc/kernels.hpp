@@ -68,6 +68,23 @@ int skinny_dense(const QWeight& w, const uint16_t* x, int64_t x_stride, int m,
 int skinny_gate_up(const uint16_t* x, const uint32_t* ids, int rows, int top_k,
                    const QBank& gate, const QBank& up, const QWeight& sgate, const QWeight& sup,
                    uint16_t* h, hipStream_t s);
+
+// Router outputs and where the routes go (skinny_route_gate_up).
+struct RouteIO {
+  const uint16_t* logits;        // [rows, logit_stride]: experts' logits first
+  int64_t logit_stride;
+  const uint16_t* shared_logit;  // [rows, shared_stride]: the shared-expert gate logit
+  int64_t shared_stride;
+  uint32_t* ids;                 // [rows, top_k] out
+  uint16_t* scores;              // [rows, top_k] out
+  uint16_t* factor;              // [rows] out
+};
+// Routing tail + expert gate/up (+SwiGLU) in one: for 512 routed experts the
+// persistent kernel routes its rows itself (bit-identical to moe_route) and
+// writes ids / scores / factor; otherwise moe_route then skinny_gate_up.
+int skinny_route_gate_up(const RouteIO& ro, int experts, const uint16_t* x, int rows, int top_k,
+                         const QBank& gate, const QBank& up, const QWeight& sgate,
+                         const QWeight& sup, uint16_t* h, hipStream_t s);
 int skinny_down(const uint16_t* h, const uint32_t* ids, const uint16_t* scores, int rows,
                 int top_k, int inter, int shared_inter, const QBank& down, const QWeight& sdown,
                 uint16_t* p, hipStream_t s);

@@ -15,6 +15,7 @@
 #include "common.hpp"
 #include "kernels.hpp"
 #include "qmv_core.hpp"
+#include "route_core.hpp"
 
 namespace mx {
 
@@ -22,19 +23,10 @@ namespace {
 
 constexpr int kWaves = 4;
 
-// bf16 logistic function with MLX's per-operation bf16 rounding
-// (reference kernels/moe_route_tail.metal:119-123).
-__device__ __forceinline__ float sigmoid_bf16(float x) {
-  const float e = round_bf16(expf_(__builtin_fabsf(x)));
-  const float d = round_bf16(1.0f + e);
-  const float y = round_bf16(1.0f / d);
-  return x < 0.0f ? y : round_bf16(1.0f - y);
-}
-
 // ---------------------------------------------------------------------------
 // Routing tail: softmax (fp32, MLX precise) -> bf16 gates -> top-k under the
 // (bf16 value, index) key -> bf16 renormalisation -> bf16 sigmoid of the
-// shared-expert gate.  One wave per row; lane l owns experts PER*l .. PER*l+PER-1.
+// shared-expert gate.  One wave per row (rt::route_row).
 template <int PER>
 __global__ __launch_bounds__(64) void route_kernel(const uint16_t* __restrict__ logits,
                                                    int64_t logit_stride,
@@ -45,65 +37,10 @@ __global__ __launch_bounds__(64) void route_kernel(const uint16_t* __restrict__ 
                                                    uint16_t* __restrict__ factor) {
   const int row = blockIdx.x;
   const int lane = threadIdx.x;
-  const uint16_t* in = logits + size_t(row) * logit_stride + lane * PER;
-  float v[PER];
-#pragma unroll
-  for (int i = 0; i < PER; ++i) v[i] = bf16_to_f32(in[i]);
-  float mx_ = v[0];
-#pragma unroll
-  for (int i = 1; i < PER; ++i) mx_ = v[i] > mx_ ? v[i] : mx_;
-  for (int o = 32; o > 0; o >>= 1) {
-    const float t = __shfl_xor(mx_, o, 64);
-    mx_ = t > mx_ ? t : mx_;
-  }
-  float sum = 0.0f;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    v[i] = expf_(v[i] - mx_);
-    sum = sum + v[i];
-  }
-  for (int o = 32; o > 0; o >>= 1) sum = sum + __shfl_xor(sum, o, 64);
-  const float inv = 1.0f / sum;
-  uint32_t key[PER];
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const uint32_t g = f32_to_bf16(v[i] * inv);
-    // order-preserving map of the bf16 pattern (moe_route_tail.h:13-16)
-    const uint32_t k16 = (g & 0x8000u) ? (~g & 0xffffu) : (g | 0x8000u);
-    key[i] = (k16 << 16) | uint32_t(lane * PER + i);
-  }
-  uint32_t sel[16];
-  for (int s = 0; s < top_k; ++s) {
-    uint32_t best = 0;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) best = key[i] > best ? key[i] : best;
-    for (int o = 32; o > 0; o >>= 1) {
-      const uint32_t t = uint32_t(__shfl_xor(int(best), o, 64));
-      best = t > best ? t : best;
-    }
-    sel[top_k - 1 - s] = best;  // slot k-1 holds the largest (ascending order)
-#pragma unroll
-    for (int i = 0; i < PER; ++i)
-      if (key[i] == best) key[i] = 0u;  // keys are unique; real keys are never 0
-  }
-  // every lane holds the selection: the renormalising total is formed in all
-  // lanes (one bf16 add per slot, ascending), then lane j writes slot j
-  float total = 0.0f;
-  float mine = 0.0f;
-  uint32_t mine_id = 0;
-  for (int j = 0; j < top_k; ++j) {
-    const uint32_t k16 = sel[j] >> 16;
-    const uint32_t g = (k16 & 0x8000u) ? (k16 & 0x7fffu) : (~k16 & 0xffffu);
-    const float picked = bf16_to_f32(uint16_t(g));
-    total = round_bf16(picked + total);
-    if (j == lane) {
-      mine = picked;
-      mine_id = sel[j] & 0xffffu;
-    }
-  }
+  const rt::RouteLane r = rt::route_row<PER>(logits + size_t(row) * logit_stride, top_k);
   if (lane < top_k) {
-    ids[size_t(row) * top_k + lane] = mine_id;
-    scores[size_t(row) * top_k + lane] = f32_to_bf16(mine / total);
+    ids[size_t(row) * top_k + lane] = r.id;
+    scores[size_t(row) * top_k + lane] = r.score;
   }
   if (lane == 0)
     factor[row] = f32_to_bf16(sigmoid_bf16(bf16_to_f32(shared_logit[size_t(row) * shared_stride])));

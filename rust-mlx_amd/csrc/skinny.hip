@@ -22,19 +22,13 @@
 #include "common.hpp"
 #include "kernels.hpp"
 #include "skinny_core.hpp"
+#include "route_core.hpp"
 
 namespace mx {
 
 namespace {
 
 using sk::floatx4_t;
-
-__device__ __forceinline__ float sigmoid_bf16(float x) {
-  const float e = round_bf16(expf_(__builtin_fabsf(x)));
-  const float d = round_bf16(1.0f + e);
-  const float y = round_bf16(1.0f / d);
-  return x < 0.0f ? y : round_bf16(1.0f - y);
-}
 
 // Largest K staged in LDS (super-steps); deeper rows stream x into registers,
 // up to kDenseSteps.  Expert down rows are at most kDownSteps deep.
@@ -378,11 +372,18 @@ __device__ __forceinline__ int build_leaders(uint32_t my_id, int rows, int top_k
 // the depth; a workgroup is TPI * KS waves and walks the items
 // blockIdx.x, blockIdx.x + P, ... with the next item's weights in flight
 // while the current one computes.
-template <int BITS, int STEPS, int TPI, int KS>
+//
+// PER > 0: the kernel routes its rows itself from the router logits (wave r
+// routes row r with rt::route_row<PER>, PER * 64 experts); workgroup 0 writes
+// the ids, scores and shared-expert factors for the kernels after it.
+// PER == 0: the routes come in `ids`.
+template <int BITS, int STEPS, int TPI, int KS, int PER>
 __global__ __launch_bounds__(64 * TPI * KS) void gate_up_persist_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ ids, int rows, int top_k,
-    QBank gate, QBank up, QWeight sgate, QWeight sup, uint16_t* __restrict__ h, int hs) {
+    QBank gate, QBank up, QWeight sgate, QWeight sup, uint16_t* __restrict__ h, int hs,
+    RouteIO ro) {
   static_assert(TPI == 2 || TPI == 4, "tiles per item");
+  static_assert(PER == 0 || TPI * KS >= 8, "a routing wave per row");
   constexpr int HALF = TPI / 2;   // tiles of gate (and of up) per item
   constexpr int C = 16 * HALF;    // intermediate rows (h columns) per item
   constexpr int RED = KS * TPI * 8 * 16;
@@ -405,8 +406,30 @@ __global__ __launch_bounds__(64 * TPI * KS) void gate_up_persist_kernel(
   const int inter = gate.n;
   const float* sx = reinterpret_cast<const float*>(lds + xbytes + sk::kZeroBytes);
   const sk::DenseRows xr{x, hidden, rows};
-  // route ids first (the expert list needs them), then the x staging loads
-  const uint32_t my_id = ids[min(int(threadIdx.x), rows * top_k - 1)];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane & 15;
+  uint32_t my_id;
+  if constexpr (PER > 0) {
+    // every row is routed by a wave (its logit loads are the first ones out)
+    __shared__ uint32_t routed[kPersistMaxRoutes];
+    if (wave < rows) {
+      const rt::RouteLane r = rt::route_row<PER>(ro.logits + size_t(wave) * ro.logit_stride, top_k);
+      if (lane < top_k) {
+        routed[wave * top_k + lane] = r.id;
+        if (blockIdx.x == 0) {
+          ro.ids[wave * top_k + lane] = r.id;
+          ro.scores[wave * top_k + lane] = r.score;
+        }
+      }
+      if (lane == 0 && blockIdx.x == 0)
+        ro.factor[wave] = f32_to_bf16(
+            sigmoid_bf16(bf16_to_f32(ro.shared_logit[size_t(wave) * ro.shared_stride])));
+    }
+    __syncthreads();
+    my_id = routed[min(int(threadIdx.x), rows * top_k - 1)];
+  } else {
+    // route ids first (the expert list needs them), then the x staging loads
+    my_id = ids[min(int(threadIdx.x), rows * top_k - 1)];
+  }
   sk::Stager<NT, sk::stage_per(NT, STEPS), sk::DenseRows> stg(xr, rows, 0, steps);
   stg.load();
   const int nlead = build_leaders(my_id, rows, top_k, gate.experts, first, info, route_e, lead_e,
@@ -414,7 +437,6 @@ __global__ __launch_bounds__(64 * TPI * KS) void gate_up_persist_kernel(
   const int groups = inter / C;
   const int items = nlead * groups;
   const int P = gridDim.x;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane & 15;
   const int t = wave / KS, ks = wave - t * KS;
   constexpr int n = steps / KS;
   const int k0 = n * ks;
@@ -696,47 +718,70 @@ int skinny_dense(const QWeight& w, const uint16_t* x, int64_t x_stride, int m,
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 
-int skinny_gate_up(const uint16_t* x, const uint32_t* ids, int rows, int top_k,
-                   const QBank& gate, const QBank& up, const QWeight& sgate, const QWeight& sup,
-                   uint16_t* h, hipStream_t s) {
-  const int hs = gate.n > sgate.n ? gate.n : sgate.n;
+namespace {
+
+bool persist_ok(const QBank& gate, const QBank& up, const QWeight& sgate, int rows, int top_k) {
+  return gate.experts <= kPersistMaxExperts && rows * top_k <= kPersistMaxRoutes &&
+         sgate.n == gate.n && up.n == gate.n && gate.n % (8 * kPersistTiles) == 0 &&
+         gate.k / sk::kSuper == kStageSteps;
+}
+
+// One workgroup per resident slot: every workgroup is on the chip from the start.
+template <int BITS, int PER>
+int launch_persist(const uint16_t* x, const uint32_t* ids, int rows, int top_k, const QBank& gate,
+                   const QBank& up, const QWeight& sgate, const QWeight& sup, uint16_t* h, int hs,
+                   const RouteIO& ro, hipStream_t s) {
+  constexpr int NT = 64 * kPersistTiles * kPersistSplit;
+  const auto fn = gate_up_persist_kernel<BITS, kStageSteps, kPersistTiles, kPersistSplit, PER>;
+  const int lb = sk::stage_bytes(kStageSteps);
+  static int grid_n = 0;
+  if (grid_n == 0) {
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn),
+                                                     NT, lb) != hipSuccess ||
+        cus <= 0 || per_cu <= 0)
+      return MX_EHIP;
+    grid_n = cus * per_cu;
+  }
+  hipLaunchKernelGGL(fn, dim3(grid_n), dim3(NT), lb, s, x, ids, rows, top_k, gate, up, sgate, sup,
+                     h, hs, ro);
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
+template <int PER>
+int dispatch_persist(const uint16_t* x, const uint32_t* ids, int rows, int top_k,
+                     const QBank& gate, const QBank& up, const QWeight& sgate, const QWeight& sup,
+                     uint16_t* h, int hs, const RouteIO& ro, hipStream_t s) {
+  switch (gate.bits) {
+    case 4: return launch_persist<4, PER>(x, ids, rows, top_k, gate, up, sgate, sup, h, hs, ro, s);
+    case 5: return launch_persist<5, PER>(x, ids, rows, top_k, gate, up, sgate, sup, h, hs, ro, s);
+    case 6: return launch_persist<6, PER>(x, ids, rows, top_k, gate, up, sgate, sup, h, hs, ro, s);
+    default: return launch_persist<8, PER>(x, ids, rows, top_k, gate, up, sgate, sup, h, hs, ro, s);
+  }
+}
+
+int gate_up_check(int rows, int top_k, const QBank& gate, const QBank& up, const QWeight& sgate,
+                  const QWeight& sup) {
   const int steps = gate.k / sk::kSuper;
   if (rows < 1 || rows > 8 || top_k < 1 || top_k > 16 || gate.group_size != 64 ||
       gate.k % 512 != 0 || steps > kStageSteps || up.bits != gate.bits ||
       sgate.bits != gate.bits || sup.bits != gate.bits || sgate.k != gate.k)
     return MX_EUNSUPPORTED;
-  const int lb = sk::stage_bytes(steps);
-  if (gate.experts <= kPersistMaxExperts && rows * top_k <= kPersistMaxRoutes &&
-      sgate.n == gate.n && up.n == gate.n && gate.n % (8 * kPersistTiles) == 0 &&
-      steps == kStageSteps) {
-    // one workgroup per resident slot: every workgroup is on the chip from the start
-    static int slots[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
-    const void* fn = nullptr;
-    switch (gate.bits) {
-      case 4: fn = reinterpret_cast<const void*>(gate_up_persist_kernel<4, kStageSteps, kPersistTiles, kPersistSplit>); break;
-      case 5: fn = reinterpret_cast<const void*>(gate_up_persist_kernel<5, kStageSteps, kPersistTiles, kPersistSplit>); break;
-      case 6: fn = reinterpret_cast<const void*>(gate_up_persist_kernel<6, kStageSteps, kPersistTiles, kPersistSplit>); break;
-      default: fn = reinterpret_cast<const void*>(gate_up_persist_kernel<8, kStageSteps, kPersistTiles, kPersistSplit>); break;
-    }
-    int& grid_n = slots[gate.bits];
-    if (grid_n == 0) {
-      int dev = 0, cus = 0, per_cu = 0;
-      if (hipGetDevice(&dev) != hipSuccess ||
-          hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-          hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 64 * kPersistTiles * kPersistSplit, lb) != hipSuccess ||
-          cus <= 0 || per_cu <= 0)
-        return MX_EHIP;
-      grid_n = cus * per_cu;
-    }
-    const dim3 pgrid(grid_n);
-    switch (gate.bits) {
-      case 4: hipLaunchKernelGGL((gate_up_persist_kernel<4, kStageSteps, kPersistTiles, kPersistSplit>), pgrid, dim3(64 * kPersistTiles * kPersistSplit), lb, s, x, ids, rows, top_k, gate, up, sgate, sup, h, hs); break;
-      case 5: hipLaunchKernelGGL((gate_up_persist_kernel<5, kStageSteps, kPersistTiles, kPersistSplit>), pgrid, dim3(64 * kPersistTiles * kPersistSplit), lb, s, x, ids, rows, top_k, gate, up, sgate, sup, h, hs); break;
-      case 6: hipLaunchKernelGGL((gate_up_persist_kernel<6, kStageSteps, kPersistTiles, kPersistSplit>), pgrid, dim3(64 * kPersistTiles * kPersistSplit), lb, s, x, ids, rows, top_k, gate, up, sgate, sup, h, hs); break;
-      default: hipLaunchKernelGGL((gate_up_persist_kernel<8, kStageSteps, kPersistTiles, kPersistSplit>), pgrid, dim3(64 * kPersistTiles * kPersistSplit), lb, s, x, ids, rows, top_k, gate, up, sgate, sup, h, hs); break;
-    }
-    return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
-  }
+  return MX_OK;
+}
+
+}  // namespace
+
+int skinny_gate_up(const uint16_t* x, const uint32_t* ids, int rows, int top_k,
+                   const QBank& gate, const QBank& up, const QWeight& sgate, const QWeight& sup,
+                   uint16_t* h, hipStream_t s) {
+  const int hs = gate.n > sgate.n ? gate.n : sgate.n;
+  if (gate_up_check(rows, top_k, gate, up, sgate, sup) != MX_OK) return MX_EUNSUPPORTED;
+  if (persist_ok(gate, up, sgate, rows, top_k))
+    return dispatch_persist<0>(x, ids, rows, top_k, gate, up, sgate, sup, h, hs, RouteIO{}, s);
+  const int lb = sk::stage_bytes(gate.k / sk::kSuper);
   const dim3 grid((hs + 31) / 32, rows * top_k + 1);
 #define MX_GU(B) \
   case B: hipLaunchKernelGGL((gate_up_kernel<B, kGateUpSplit>), grid, dim3(256 * kGateUpSplit), lb, s, x, ids, rows, top_k, gate, up, sgate, sup, h, hs); break;
@@ -746,6 +791,19 @@ int skinny_gate_up(const uint16_t* x, const uint32_t* ids, int rows, int top_k,
   }
 #undef MX_GU
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
+int skinny_route_gate_up(const RouteIO& ro, int experts, const uint16_t* x, int rows, int top_k,
+                         const QBank& gate, const QBank& up, const QWeight& sgate,
+                         const QWeight& sup, uint16_t* h, hipStream_t s) {
+  const int hs = gate.n > sgate.n ? gate.n : sgate.n;
+  if (gate_up_check(rows, top_k, gate, up, sgate, sup) != MX_OK) return MX_EUNSUPPORTED;
+  if (experts == 8 * 64 && experts <= gate.experts && persist_ok(gate, up, sgate, rows, top_k))
+    return dispatch_persist<8>(x, ro.ids, rows, top_k, gate, up, sgate, sup, h, hs, ro, s);
+  const int rc = moe_route(ro.logits, ro.logit_stride, ro.shared_logit, ro.shared_stride, rows,
+                           experts, top_k, ro.ids, ro.scores, ro.factor, s);
+  if (rc != MX_OK) return rc;
+  return skinny_gate_up(x, ro.ids, rows, top_k, gate, up, sgate, sup, h, s);
 }
 
 int skinny_down(const uint16_t* h, const uint32_t* ids, const uint16_t* scores, int rows,

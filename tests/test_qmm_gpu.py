@@ -162,3 +162,58 @@ def test_head_argmax_mfma_matches_exact_head(mx, orc, m):
         if g[r] != e[r]:
             assert abs(lg[r, g[r]] - lg[r, e[r]]) <= 2.0 ** -7 * abs(lg[r, e[r]]) + 1e-3, r
     assert np.mean(g == e) >= 0.5
+
+
+@pytest.mark.parametrize("E,rows", [(512, 8), (512, 1), (512, 5), (256, 8)])
+def test_moe_routed_experts_mfma_matches_route_then_experts(mx, orc, E, rows):
+    """The fused routing + matrix-core experts call gives the bits of
+    mx_moe_route (bit-exact with the oracle) followed by mx_moe_experts_mfma:
+    with 512 routed experts the persistent gate/up kernel routes its rows
+    itself, with 256 the call routes first."""
+    from test_layers_gpu import dev
+
+    I, H, top_k = 256, 2048, 10
+    gate = mx.QBank.random(E, I, H, 4, 64, 900)
+    up = mx.QBank.random(E, I, H, 4, 64, 910)
+    down = mx.QBank.random(E, H, I, 5, 64, 920)
+    sg = mx.QWeight.random(I, H, 4, 64, 930)
+    su = mx.QWeight.random(I, H, 4, 64, 940)
+    sd = mx.QWeight.random(H, I, 5, 64, 950)
+    stride = E + 1
+    lg = orc.fill_bf16(rows * stride, 960 + rows, 1, 2.0, 0.0).reshape(rows, stride)
+    lg[0, :E] = 0  # an all-tied row
+    x = orc.fill_bf16(rows * H, 970 + rows, 1, 1.0, 0.0).reshape(rows, H)
+    d_lg, dx = dev(mx, lg), dev(mx, x)
+    ws = mx.DeviceArray((mx.lib.mx_moe_workspace_bytes(8, 16, I),), np.uint8)
+    qb = [b.c() for b in (gate, up, down)]
+    qs = [w.c() for w in (sg, su, sd)]
+    lg_ptr, sh_ptr = d_lg.ptr, d_lg.ptr + 2 * E
+
+    ids_w = mx.DeviceArray((rows, top_k), np.uint32)
+    sc_w = mx.DeviceArray((rows, top_k), np.uint16)
+    fa_w = mx.DeviceArray((rows,), np.uint16)
+    mx.check(mx.lib.mx_moe_route(lg_ptr, stride, sh_ptr, stride, rows, E, top_k, ids_w.ptr,
+                                 sc_w.ptr, fa_w.ptr, None))
+    p_w = mx.DeviceArray((rows, top_k + 1, H), np.uint16)
+    mx.check(mx.lib.mx_moe_experts_mfma(dx.ptr, ids_w.ptr, sc_w.ptr, rows, top_k,
+                                        C.byref(qb[0]), C.byref(qb[1]), C.byref(qb[2]),
+                                        C.byref(qs[0]), C.byref(qs[1]), C.byref(qs[2]), ws.ptr,
+                                        p_w.ptr, None))
+
+    ids = mx.DeviceArray((rows, top_k), np.uint32)
+    sc = mx.DeviceArray((rows, top_k), np.uint16)
+    fa = mx.DeviceArray((rows,), np.uint16)
+    p = mx.DeviceArray((rows, top_k + 1, H), np.uint16)
+    mx.check(mx.lib.mx_moe_routed_experts_mfma(lg_ptr, stride, sh_ptr, stride, E, dx.ptr, rows,
+                                               top_k, C.byref(qb[0]), C.byref(qb[1]),
+                                               C.byref(qb[2]), C.byref(qs[0]), C.byref(qs[1]),
+                                               C.byref(qs[2]), ws.ptr, ids.ptr, sc.ptr, fa.ptr,
+                                               p.ptr, None))
+    assert (ids.numpy() == ids_w.numpy()).all()
+    assert (sc.numpy() == sc_w.numpy()).all()
+    assert (fa.numpy() == fa_w.numpy()).all()
+    assert (p.numpy() == p_w.numpy()).all()
+    # and the routes themselves are the oracle's
+    want_ids, want_sc, want_fa = orc.moe_route(np.ascontiguousarray(lg[:, :E]), lg[:, E], top_k)
+    assert (ids.numpy() == want_ids).all() and (sc.numpy() == want_sc).all()
+    assert (fa.numpy() == want_fa).all()
