@@ -180,6 +180,19 @@ mx_status mx_qmv(const mx_qweight* w, const uint16_t* x, int32_t m, uint16_t* y,
  * (matrix_kernel::project, src/matrix_kernel.rs:113-254,
  * kernels/matrix_packed.metal). */
 mx_status mx_qmm(const mx_qweight* w, const uint16_t* x, int32_t m, uint16_t* y, void* stream);
+/* mx_qmm_conv: mx_qmm (4-bit, 1..8 rows, one token per row) with the GDN
+ * causal conv fused into its output: columns below conv_channels are conv
+ * channels, convolved with the slot's cached window (conv_state bf16 [slots,
+ * conv_k-1, conv_channels], updated in place; conv_w fp32 [conv_k,
+ * conv_channels]; conv_k in 2..4) and written as bf16(silu(bf16(conv))) to
+ * conv_out — mx_gdn_conv's arithmetic on the projection's bf16 outputs, bit
+ * for bit; columns from conv_channels on go to y.  Rows' slots must be
+ * distinct.  Replaces the in_proj + decode_conv pair of Gdn::forward
+ * (src/hybrid.rs:374-400, src/compiled.rs:88-95). */
+mx_status mx_qmm_conv(const mx_qweight* w, const uint16_t* x, int32_t m, int32_t conv_channels,
+                      int32_t conv_k, const int32_t* slots, uint16_t* conv_state,
+                      const float* conv_w, uint16_t* conv_out, int64_t conv_stride, uint16_t* y,
+                      int64_t y_stride, void* stream);
 
 /* ---- A4: affine dequantisation of selected rows (embedding) --------------
  * out[i, :] = bf16(s * q + b) of row ids[i].  Replaces Linear::embedding

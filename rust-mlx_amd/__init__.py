@@ -181,6 +181,8 @@ def _load() -> C.CDLL:
         "mx_engine_set_flags": ([vp, i32], i32),
         "mx_engine_fill_slot": ([vp, i32, i32, u64], i32),
         "mx_qmm": ([C.POINTER(QWeightC), vp, i32, vp, vp], i32),
+        "mx_qmm_conv": ([C.POINTER(QWeightC), vp, i32, i32, i32, vp, vp, vp, vp, i64, vp, i64, vp],
+                        i32),
         "mx_head_argmax_mfma": ([C.POINTER(QWeightC), vp, i32, vp, vp, vp], i32),
         "mx_moe_experts_mfma": ([vp, vp, vp, i32, i32, C.POINTER(QBankC), C.POINTER(QBankC),
                                  C.POINTER(QBankC), C.POINTER(QWeightC), C.POINTER(QWeightC),

@@ -692,6 +692,37 @@ MX_ABI mx_status mx_qmm(const mx_qweight* w, const uint16_t* x, int32_t m, uint1
   return finish(qmm(q, x, q.k, m, e, hipStream_t(stream)), "mx_qmm");
 }
 
+MX_ABI mx_status mx_qmm_conv(const mx_qweight* w, const uint16_t* x, int32_t m,
+                             int32_t conv_channels, int32_t conv_k, const int32_t* slots,
+                             uint16_t* conv_state, const float* conv_w, uint16_t* conv_out,
+                             int64_t conv_stride, uint16_t* y, int64_t y_stride, void* stream) {
+  MX_CHECK(w && x && slots && conv_state && conv_w && conv_out && y, MX_EINVAL,
+           "mx_qmm_conv: null pointer");
+  const QWeight q = to_qweight(*w);
+  if (const char* err = check_qweight(q))
+    return mx_status(set_error(MX_EINVAL, std::string("mx_qmm_conv: ") + err));
+  MX_CHECK(m >= 1 && m <= 8, MX_EUNSUPPORTED, "mx_qmm_conv: m must be in 1..8");
+  MX_CHECK(q.bits == 4 && skinny_supported(q), MX_EUNSUPPORTED,
+           "mx_qmm_conv: needs 4-bit codes, group_size 64 and k a multiple of 512");
+  MX_CHECK(conv_k >= 2 && conv_k <= kConvMaxTaps, MX_EUNSUPPORTED,
+           "mx_qmm_conv: conv_k must be in 2..4");
+  MX_CHECK(conv_channels >= 1 && conv_channels <= q.n && conv_stride >= conv_channels &&
+               y_stride >= q.n,
+           MX_EINVAL, "mx_qmm_conv: bad channel count or strides");
+  ProjEpilogue e{};
+  e.mode = kConv;
+  e.y = y;
+  e.y_stride = y_stride;
+  e.conv_state = conv_state;
+  e.conv_w = conv_w;
+  e.slots = slots;
+  e.conv_out = conv_out;
+  e.conv_stride = conv_stride;
+  e.conv_ch = conv_channels;
+  e.taps = conv_k;
+  return finish(skinny_dense(q, x, q.k, m, e, hipStream_t(stream)), "mx_qmm_conv");
+}
+
 MX_ABI mx_status mx_moe_experts_mfma(const uint16_t* x, const uint32_t* ids, const uint16_t* scores,
                                      int32_t rows, int32_t top_k, const mx_qbank* gate,
                                      const mx_qbank* up, const mx_qbank* down,

@@ -521,15 +521,29 @@ int record_step(Engine& e, int rows, int groups, int t, bool history, bool logit
       pl.mode = kPlain;
       pl.y = e.pbuf;
       pl.y_stride = e.P;
-      MX_TRY(project(e, L.gdn_in, e.mixed, c.hidden, rows, pl));
       const size_t conv_per = size_t(c.conv_k - 1) * e.cd;
       const size_t state_per = size_t(c.gdn_hv) * c.gdn_dk * c.gdn_dv;
       // cache layout [slot][gdn layer]: slot index s -> s * n_gdn + gi
-      MX_TRY(gdn_conv(e.pbuf, e.P, groups, t, rt->gdn_slots, e.conv_state + gi * conv_per,
-                      L.conv_w, e.cd, c.conv_k, e.conv_out, e.cd,
-                      history ? e.hist_conv + size_t(gi) * (c.conv_k - 1 + c.max_verify) * e.cd
-                              : nullptr,
-                      e.stream));
+      if (!e.exact && t == 1 && !history && rows <= 8 && L.gdn_in.bits == 4 &&
+          skinny_supported(L.gdn_in) && c.conv_k <= kConvMaxTaps) {
+        // the conv runs in the projection's epilogue
+        pl.mode = kConv;
+        pl.conv_state = e.conv_state + gi * conv_per;
+        pl.conv_w = L.conv_w;
+        pl.slots = rt->gdn_slots;
+        pl.conv_out = e.conv_out;
+        pl.conv_stride = e.cd;
+        pl.conv_ch = int(e.cd);
+        pl.taps = c.conv_k;
+        MX_TRY(skinny_dense(L.gdn_in, e.mixed, c.hidden, rows, pl, e.stream));
+      } else {
+        MX_TRY(project(e, L.gdn_in, e.mixed, c.hidden, rows, pl));
+        MX_TRY(gdn_conv(e.pbuf, e.P, groups, t, rt->gdn_slots, e.conv_state + gi * conv_per,
+                        L.conv_w, e.cd, c.conv_k, e.conv_out, e.cd,
+                        history ? e.hist_conv + size_t(gi) * (c.conv_k - 1 + c.max_verify) * e.cd
+                                : nullptr,
+                        e.stream));
+      }
       if (!e.exact && t == 1 && !history) {
         MX_TRY(gdn_recurrence_fast(e.conv_out, e.cd, e.pbuf + e.cd, e.pbuf + e.cd + e.vd,
                                    e.pbuf + e.cd + e.vd + c.gdn_hv, e.P, L.a_log, L.dt_bias,

@@ -265,49 +265,46 @@ __device__ __forceinline__ float wave_sum(float v) {
 // loads stay coalesced in 64-byte runs per part.
 constexpr int kFastParts = 4;
 constexpr int kFastRows = kD / kFastParts;  // key rows per thread
+constexpr int kFastThreads = kD * kFastParts;
 
-__global__ __launch_bounds__(kD * kFastParts) void recurrence_fast_kernel(ScanArgs p) {
-  const int hv = blockIdx.x;
-  const int row = blockIdx.y;  // one token per group
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int c = lane & 15, part = lane >> 4;
-  const int i = wave * 16 + c;  // value column
-  const int hv_heads = p.hv_heads, hk_heads = p.hk_heads;
-  const int hk = hv / (hv_heads / hk_heads);
-  __shared__ float4 qs4[kD / 4], ks4[kD / 4];
-  __shared__ float red[kD * kFastParts / 64];
-  float* sp = p.state + (size_t(p.slots[row]) * hv_heads + hv) * kD * kD +
-              size_t(part * kFastRows) * kD + i;
-  float s[kFastRows];
-#pragma unroll
-  for (int d = 0; d < kFastRows; ++d) s[d] = sp[size_t(d) * kD];
-  const uint16_t* cr = p.conv_out + size_t(row) * p.conv_stride;
-  const float q0 = bf16_to_f32(cr[hk * kD + lane]), q1 = bf16_to_f32(cr[hk * kD + 64 + lane]);
-  const float k0 = bf16_to_f32(cr[(hk_heads + hk) * kD + lane]);
-  const float k1 = bf16_to_f32(cr[(hk_heads + hk) * kD + 64 + lane]);
-  const float vi = bf16_to_f32(cr[2 * hk_heads * kD + hv * kD + i]);
-  const float bv = bf16_to_f32(p.b[size_t(row) * p.zab_stride + hv]);
-  const float av = bf16_to_f32(p.a[size_t(row) * p.zab_stride + hv]);
-  const float zi = bf16_to_f32(p.z[size_t(row) * p.zab_stride + hv * kD + i]);
-  const float nw = bf16_to_f32(p.norm_w[i]);
+// Wave 0: the key head's q and k, L2-normalised (q also scaled by
+// bf16(dk^-1/2)) at the exact step's bf16 rounding points, into LDS as
+// float4.  q0 / q1 are q[lane] / q[64 + lane], k likewise.
+__device__ __forceinline__ void fast_qk_norm(float q0, float q1, float k0, float k1, float4* qs4,
+                                             float4* ks4) {
+  const int lane = threadIdx.x & 63;
   const float eps_l2 = round_bf16(1e-6f);
   const float qscale = round_bf16(0.08838834764831845f);  // bf16(Dk^-1/2), Dk = 128
-  if (wave == 0) {
-    const float qss = round_bf16(wave_sum(round_bf16(q0 * q0) + round_bf16(q1 * q1)));
-    const float kss = round_bf16(wave_sum(round_bf16(k0 * k0) + round_bf16(k1 * k1)));
-    const float rq = round_bf16(__builtin_amdgcn_rsqf(round_bf16(qss + eps_l2)));
-    const float rk = round_bf16(__builtin_amdgcn_rsqf(round_bf16(kss + eps_l2)));
-    float* qs = reinterpret_cast<float*>(qs4);
-    float* ks = reinterpret_cast<float*>(ks4);
-    qs[lane] = round_bf16(round_bf16(q0 * rq) * qscale);
-    qs[64 + lane] = round_bf16(round_bf16(q1 * rq) * qscale);
-    ks[lane] = round_bf16(k0 * rk);
-    ks[64 + lane] = round_bf16(k1 * rk);
-  }
-  const float beta = sigmoid_bf16_fast(bv);
+  const float qss = round_bf16(wave_sum(round_bf16(q0 * q0) + round_bf16(q1 * q1)));
+  const float kss = round_bf16(wave_sum(round_bf16(k0 * k0) + round_bf16(k1 * k1)));
+  const float rq = round_bf16(__builtin_amdgcn_rsqf(round_bf16(qss + eps_l2)));
+  const float rk = round_bf16(__builtin_amdgcn_rsqf(round_bf16(kss + eps_l2)));
+  float* qs = reinterpret_cast<float*>(qs4);
+  float* ks = reinterpret_cast<float*>(ks4);
+  qs[lane] = round_bf16(round_bf16(q0 * rq) * qscale);
+  qs[64 + lane] = round_bf16(round_bf16(q1 * rq) * qscale);
+  ks[lane] = round_bf16(k0 * rk);
+  ks[64 + lane] = round_bf16(k1 * rk);
+}
+
+// The decay gate exp(-exp(a_log) softplus(bf16(a + dt_bias))) and beta =
+// sigmoid(b) of value head hv, row `row`.
+__device__ __forceinline__ void fast_gates(const ScanArgs& p, int hv, int row, float& beta,
+                                           float& gdecay) {
+  const float bv = bf16_to_f32(p.b[size_t(row) * p.zab_stride + hv]);
+  const float av = bf16_to_f32(p.a[size_t(row) * p.zab_stride + hv]);
+  beta = sigmoid_bf16_fast(bv);
   const float x = round_bf16(av + bf16_to_f32(p.dt_bias[hv]));
-  const float gdecay = exp_fast(-exp_fast(p.a_log[hv]) * softplus_bf16_fast(x));
-  __syncthreads();
+  gdecay = exp_fast(-exp_fast(p.a_log[hv]) * softplus_bf16_fast(x));
+}
+
+// One thread's share of the delta rule: its 32 state values s (key rows
+// 32 part .. of value column i) are decayed, their k dot product is summed
+// over the four parts, the column's delta applied, the new values stored
+// through sp; returns the column's q dot product (summed over the parts).
+__device__ __forceinline__ float fast_delta(float (&s)[kFastRows], float* sp, const float4* ks4,
+                                            const float4* qs4, int part, float gdecay,
+                                            float beta, float vi) {
   const float4* kp = ks4 + part * (kFastRows / 4);
   const float4* qp = qs4 + part * (kFastRows / 4);
   float c0 = 0.0f, c1 = 0.0f, c2 = 0.0f, c3 = 0.0f;
@@ -347,14 +344,48 @@ __global__ __launch_bounds__(kD * kFastParts) void recurrence_fast_kernel(ScanAr
   float os = (o0 + o1) + (o2 + o3);
   os = os + __shfl_xor(os, 16, 64);
   os = os + __shfl_xor(os, 32, 64);
-  const float yo = round_bf16(os);
-  // the four parts of a column hold the same yo: part 0 enters the norm
-  const float ws = wave_sum(part == 0 ? yo * yo : 0.0f);
+  return os;
+}
+
+// Wave w's share of a value head's output sum of squares (part 0 of each
+// column enters: the four parts hold the same value).
+__device__ __forceinline__ float fast_sq_part(float yo, int part) {
+  return wave_sum(part == 0 ? yo * yo : 0.0f);
+}
+
+__global__ __launch_bounds__(kFastThreads) void recurrence_fast_kernel(ScanArgs p) {
+  const int hv = blockIdx.x;
+  const int row = blockIdx.y;  // one token per group
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 15, part = lane >> 4;
+  const int i = wave * 16 + c;  // value column
+  const int hv_heads = p.hv_heads, hk_heads = p.hk_heads;
+  const int hk = hv / (hv_heads / hk_heads);
+  __shared__ float4 qs4[kD / 4], ks4[kD / 4];
+  __shared__ float red[kFastThreads / 64];
+  float* sp = p.state + (size_t(p.slots[row]) * hv_heads + hv) * kD * kD +
+              size_t(part * kFastRows) * kD + i;
+  float s[kFastRows];
+#pragma unroll
+  for (int d = 0; d < kFastRows; ++d) s[d] = sp[size_t(d) * kD];
+  const uint16_t* cr = p.conv_out + size_t(row) * p.conv_stride;
+  const float vi = bf16_to_f32(cr[2 * hk_heads * kD + hv * kD + i]);
+  const float zi = bf16_to_f32(p.z[size_t(row) * p.zab_stride + hv * kD + i]);
+  const float nw = bf16_to_f32(p.norm_w[i]);
+  if (wave == 0)
+    fast_qk_norm(bf16_to_f32(cr[hk * kD + lane]), bf16_to_f32(cr[hk * kD + 64 + lane]),
+                 bf16_to_f32(cr[(hk_heads + hk) * kD + lane]),
+                 bf16_to_f32(cr[(hk_heads + hk) * kD + 64 + lane]), qs4, ks4);
+  float beta, gdecay;
+  fast_gates(p, hv, row, beta, gdecay);
+  __syncthreads();
+  const float yo = round_bf16(fast_delta(s, sp, ks4, qs4, part, gdecay, beta, vi));
+  const float ws = fast_sq_part(yo, part);
   if (lane == 0) red[wave] = ws;
   __syncthreads();
   float tot = 0.0f;
 #pragma unroll
-  for (int w = 0; w < kD * kFastParts / 64; ++w) tot = tot + red[w];
+  for (int w = 0; w < kFastThreads / 64; ++w) tot = tot + red[w];
   const float inv = __builtin_amdgcn_rsqf(tot * (1.0f / kD) + p.eps);
   if (part == 0) {
     const float normed = round_bf16(nw * round_bf16(yo * inv));
@@ -362,7 +393,6 @@ __global__ __launch_bounds__(kD * kFastParts) void recurrence_fast_kernel(ScanAr
         f32_to_bf16(normed * sigmoid_fast(zi));
   }
 }
-
 
 }  // namespace
 
@@ -378,7 +408,7 @@ int gdn_recurrence_fast(const uint16_t* conv_out, int64_t conv_stride, const uin
   p.zab_stride = zab_stride; p.a_log = a_log; p.dt_bias = dt_bias; p.norm_w = norm_w; p.eps = eps;
   p.hk_heads = d.hk; p.hv_heads = d.hv; p.t = 1; p.slots = slots; p.state = state;
   p.history = nullptr; p.y = y;
-  hipLaunchKernelGGL(recurrence_fast_kernel, dim3(d.hv, rows), dim3(kD * kFastParts), 0, s, p);
+  hipLaunchKernelGGL(recurrence_fast_kernel, dim3(d.hv, rows), dim3(kFastThreads), 0, s, p);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 

@@ -42,7 +42,7 @@ int qmv(const QWeight& w, const uint16_t* x, int m, uint16_t* y, hipStream_t s);
 int dequant_rows(const QWeight& w, const uint32_t* ids, int count, uint16_t* out, hipStream_t s);
 
 // ---- projections with fused epilogues (proj.hip) ----
-enum ProjMode { kPlain = 0, kHcDown = 1, kHcUpMix = 2, kHcWrite = 3 };
+enum ProjMode { kPlain = 0, kHcDown = 1, kHcUpMix = 2, kHcWrite = 3, kConv = 4 };
 struct ProjEpilogue {
   int mode;
   uint16_t* y;        // output (kPlain/kHcDown/kHcUpMix) or the residual [M, hc*n] (kHcWrite)
@@ -54,7 +54,20 @@ struct ProjEpilogue {
   int rank;           // kHcDown: rows below rank are the low-rank branch
   int hc;             // hyper-connection streams
   int hidden;         // kHcUpMix: stream width H (w.n == 4 * H)
+  // kConv (matrix-core 4-bit projections, one token per row, rows' slots
+  // distinct): columns below conv_ch are causal-conv channels; their
+  // bf16(silu(bf16(conv))) goes to conv_out and the window [slots, taps-1,
+  // conv_ch] shifts in place (gdn_conv's arithmetic), columns from conv_ch on
+  // go to y as in kPlain.  taps in 2..kConvMaxTaps.
+  uint16_t* conv_state;
+  const float* conv_w;       // [taps, conv_ch]
+  const int32_t* slots;      // [M]
+  uint16_t* conv_out;
+  int64_t conv_stride;
+  int conv_ch;
+  int taps;
 };
+constexpr int kConvMaxTaps = 4;
 int proj(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const ProjEpilogue& e,
          hipStream_t s);
 // matrix-core (MFMA) projections, 1..16 rows, group size 64 (qmm.hip)

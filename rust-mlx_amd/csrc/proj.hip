@@ -207,6 +207,7 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint32_t* __restrict__
 int proj(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const ProjEpilogue& e,
          hipStream_t s) {
   if (e.mode == kHcUpMix && (e.hidden * kQRows != w.n)) return MX_EUNSUPPORTED;
+  if (e.mode == kConv) return MX_EUNSUPPORTED;
   switch (w.bits) {
     case 4: proj_m<4>(w, x, x_stride, m, e, s); break;
     case 5: proj_m<5>(w, x, x_stride, m, e, s); break;

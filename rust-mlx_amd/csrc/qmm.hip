@@ -290,6 +290,7 @@ int qmm(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const Proj
         hipStream_t s) {
   if (!qmm_supported(w) || m < 1 || m > 16) return MX_EUNSUPPORTED;
   if (e.mode == kHcUpMix && e.hidden * 4 != w.n) return MX_EUNSUPPORTED;
+  if (e.mode == kConv) return MX_EUNSUPPORTED;
   switch (w.bits) {
     case 4: dense_bits<4>(w, x, x_stride, m, e, s); break;
     case 5: dense_bits<5>(w, x, x_stride, m, e, s); break;

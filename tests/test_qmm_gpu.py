@@ -217,3 +217,41 @@ def test_moe_routed_experts_mfma_matches_route_then_experts(mx, orc, E, rows):
     want_ids, want_sc, want_fa = orc.moe_route(np.ascontiguousarray(lg[:, :E]), lg[:, E], top_k)
     assert (ids.numpy() == want_ids).all() and (sc.numpy() == want_sc).all()
     assert (fa.numpy() == want_fa).all()
+
+
+@pytest.mark.parametrize("n,k,ch,taps,m", [(12352, 2048, 8192, 4, 8), (640, 512, 384, 3, 3),
+                                           (300, 1024, 300, 2, 1), (49152, 512, 1000, 4, 2)])
+def test_qmm_conv_matches_qmm_then_conv(mx, orc, n, k, ch, taps, m):
+    """The projection with the GDN conv in its epilogue gives the bits of
+    mx_qmm followed by mx_gdn_conv: conv outputs, the updated window (other
+    slots untouched) and the plain columns.  The last shape has more outputs
+    per workgroup than threads (conv operands fetched in the epilogue)."""
+    from test_layers_gpu import dev
+
+    w = mx.QWeight.random(n, k, 4, 64, 9300 + n)
+    qc = w.c()
+    x = orc.fill_bf16(m * k, 9301 + m, 1, 1.0, 0.0).reshape(m, k)
+    S = 10
+    rng = np.random.default_rng(n + taps)
+    slots = rng.choice(S, m, replace=False).astype(np.int32)
+    state = orc.f32_to_bf16(rng.standard_normal((S, taps - 1, ch)).astype(np.float32))
+    cw = (rng.standard_normal((taps, ch)) * 0.4).astype(np.float32)
+    dx, dsl, dcw = dev(mx, x), dev(mx, slots), dev(mx, cw)
+    y_ref = mx.DeviceArray((m, n), np.uint16)
+    mx.check(mx.lib.mx_qmm(C.byref(qc), dx.ptr, m, y_ref.ptr, None))
+    st1 = dev(mx, state)
+    conv_ref = mx.DeviceArray((m, ch), np.uint16)
+    mx.check(mx.lib.mx_gdn_conv(y_ref.ptr, n, m, 1, dsl.ptr, st1.ptr, dcw.ptr, ch, taps,
+                                conv_ref.ptr, ch, None, None))
+    st2 = dev(mx, state)
+    y2 = dev(mx, np.zeros((m, n), np.uint16))
+    conv2 = mx.DeviceArray((m, ch), np.uint16)
+    mx.check(mx.lib.mx_qmm_conv(C.byref(qc), dx.ptr, m, ch, taps, dsl.ptr, st2.ptr, dcw.ptr,
+                                conv2.ptr, ch, y2.ptr, n, None))
+    assert (conv2.numpy() == conv_ref.numpy()).all()
+    assert (st2.numpy() == st1.numpy()).all()
+    got = y2.numpy()
+    assert (got[:, ch:] == y_ref.numpy()[:, ch:]).all()
+    assert (got[:, :ch] == 0).all()  # conv channels are not written to y
+    other = np.setdiff1d(np.arange(S), slots)
+    assert (st2.numpy()[other] == state[other]).all()
