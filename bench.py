@@ -156,7 +156,7 @@ def bench_config3(mx, args):
             "prefill_s": round(prefill_s, 2),
             "context": "synthetic" if args.synthetic_context else "prefilled",
         },
-        "roofline": {"bound": "hbm", "kernel": "moe gate_up_persist_kernel<4, 16>",
+        "roofline": {"bound": "hbm", "kernel": "moe gate_up_persist_kernel<4, 16, 4, 2, 0>",
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic("config3-b8-decode_hbm-traffic.md"),

@@ -497,10 +497,10 @@ __global__ __launch_bounds__(64 * TPI * KS) void gate_up_persist_kernel(
   constexpr int n = steps / KS;
   const int k0 = n * ks;
   // weight rows of item `it` for this wave (tile t, depth slice ks); past the
-  // last item the workgroup's first item again (its lines are cached, and the
-  // loads stay unconditional)
-  auto stream_for = [&](int it) {
-    if (it >= items) it = blockIdx.x;
+  // last item, item `near` again: one just loaded, so its lines are still in
+  // the cache and the loads stay unconditional without new HBM traffic
+  auto stream_for = [&](int it, int near) {
+    if (it >= items) it = near;
     const int lead = it / groups, g = it - lead * groups;
     const int e = lead_e[lead];
     const QWeight w = expert_weight(t < HALF ? gate : up, e, t < HALF ? sgate : sup);
@@ -547,17 +547,18 @@ __global__ __launch_bounds__(64 * TPI * KS) void gate_up_persist_kernel(
   };
   if (int(blockIdx.x) >= items) return;  // uniform
   // the first item's weights go out before the staged x is written
-  auto sa = stream_for(blockIdx.x);
+  auto sa = stream_for(blockIdx.x, blockIdx.x);
   sa.prefetch();
   stg.store(lds);
-  auto sb = stream_for(blockIdx.x + P);
+  auto sb = stream_for(blockIdx.x + P, blockIdx.x);
   sb.prefetch();
   for (int it = blockIdx.x; it < items; it += 2 * P) {
+    const int ib = it + P < items ? it + P : it;  // the last item loaded
     step(sa, it);
-    sa = stream_for(it + 2 * P);
+    sa = stream_for(it + 2 * P, ib);
     sa.prefetch();
     if (it + P < items) step(sb, it + P);
-    sb = stream_for(it + 3 * P);
+    sb = stream_for(it + 3 * P, it + 2 * P < items ? it + 2 * P : ib);
     sb.prefetch();
   }
 }

@@ -76,10 +76,15 @@ constexpr float code_offset() {
   return BITS == 8 ? 0.0f : 128.0f;
 }
 
-// The lane's BITS words of super-step s (values 128 s + 32 q .. +31 of the row).
+// Four dwords at a dword-aligned address (one 16-byte load; dword-aligned
+// vector accesses are legal on gfx950).
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+// The lane's BITS words of super-step s (values 128 s + 32 q .. +31 of the
+// row).  lane: the lane's words of its slice's first super-step (row + 4 BITS
+// ks0 + BITS q); s: super-step within the slice (a constant offset once
+// unrolled).
 template <int BITS>
-// lane: the lane's words of its slice's first super-step (row + 4 BITS ks0
-// + BITS q); s: super-step within the slice (a constant offset once unrolled).
 __device__ __forceinline__ void load_codes(const uint32_t* __restrict__ lane, int s,
                                            uint32_t (&w)[BITS]) {
   const uint32_t* p = lane + (4 * BITS) * s;
@@ -92,10 +97,14 @@ __device__ __forceinline__ void load_codes(const uint32_t* __restrict__ lane, in
     w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
     w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
   } else if constexpr (BITS == 6) {
-    const uint2 a = *reinterpret_cast<const uint2*>(p);
-    const uint2 b = *reinterpret_cast<const uint2*>(p + 2);
-    const uint2 c = *reinterpret_cast<const uint2*>(p + 4);
-    w[0] = a.x; w[1] = a.y; w[2] = b.x; w[3] = b.y; w[4] = c.x; w[5] = c.y;
+    // 24 bytes at an 8-byte aligned offset: a 16-byte and an 8-byte load
+    const u32x4_a4 a = *reinterpret_cast<const u32x4_a4*>(p);
+    const uint2 b = *reinterpret_cast<const uint2*>(p + 4);
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w; w[4] = b.x; w[5] = b.y;
+  } else if constexpr (BITS == 5) {
+    // 20 bytes at a 4-byte aligned offset: a 16-byte load and a dword
+    const u32x4_a4 a = *reinterpret_cast<const u32x4_a4*>(p);
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w; w[4] = p[4];
   } else {
 #pragma unroll
     for (int i = 0; i < BITS; ++i) w[i] = p[i];
