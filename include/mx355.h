@@ -258,6 +258,22 @@ mx_status mx_moe_routed_experts_mfma(const uint16_t* logits, int64_t logit_strid
 mx_status mx_moe_reduce(const uint16_t* partial, int32_t rows, int32_t top_k, int32_t hidden,
                         uint16_t* routed, void* stream);
 
+/* ---- A3: hyper-connection input projection on the matrix cores ----------
+ * mixed[r] = mean_s sigmoid(up_s(lo)) * bf16(norm_s(h[r]) (scale_s + 1)), with
+ * lo = silu(down(norm(h)) / hc) over the first `rank` down rows and inj =
+ * 2 sigmoid(down(norm(h)) / hc) over the hc inject rows (down rows rank ..
+ * rank + hc - 1, when present): the per-stream RMS norm is factored out of
+ * the down projection.  Matrix-core sums and the hardware exp2 / reciprocal /
+ * rsqrt (the fast mode's arithmetic, within the north star's tolerance of the
+ * fixed-order path), in two launches.  workspace: mx_hc_workspace_bytes(down
+ * rows).  Replaces HyperConnection::forward_reference (src/hybrid.rs:78-99)
+ * and compiled::activate / injection / mix (src/compiled.rs:46-86). */
+size_t mx_hc_workspace_bytes(int32_t n_down);
+mx_status mx_hc_forward_mfma(const mx_qweight* down, const mx_qweight* up, const uint16_t* h,
+                             const uint16_t* scale, int32_t rows, int32_t hc, int32_t hidden,
+                             int32_t rank, float eps, void* workspace, uint16_t* mixed,
+                             uint16_t* inj, void* stream);
+
 /* ---- A9: MoE hyper-connection epilogue ------------------------------------
  * out[r, s, c] = bf16(residual[r, s, c] + bf16(bf16(routed + bf16(shared * factor[r]))
  *                                               * gate[r, s]))

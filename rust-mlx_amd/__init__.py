@@ -181,6 +181,9 @@ def _load() -> C.CDLL:
         "mx_engine_set_flags": ([vp, i32], i32),
         "mx_engine_fill_slot": ([vp, i32, i32, u64], i32),
         "mx_qmm": ([C.POINTER(QWeightC), vp, i32, vp, vp], i32),
+        "mx_hc_workspace_bytes": ([i32], sz),
+        "mx_hc_forward_mfma": ([C.POINTER(QWeightC), C.POINTER(QWeightC), vp, vp, i32, i32, i32,
+                                i32, f32, vp, vp, vp, vp], i32),
         "mx_qmm_conv": ([C.POINTER(QWeightC), vp, i32, i32, i32, vp, vp, vp, vp, i64, vp, i64, vp],
                         i32),
         "mx_head_argmax_mfma": ([C.POINTER(QWeightC), vp, i32, vp, vp, vp], i32),

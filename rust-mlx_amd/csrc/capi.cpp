@@ -723,6 +723,31 @@ MX_ABI mx_status mx_qmm_conv(const mx_qweight* w, const uint16_t* x, int32_t m,
   return finish(skinny_dense(q, x, q.k, m, e, hipStream_t(stream)), "mx_qmm_conv");
 }
 
+MX_ABI size_t mx_hc_workspace_bytes(int32_t n_down) {
+  return n_down > 0 ? hc_fused_part_bytes(n_down) : 0;
+}
+
+MX_ABI mx_status mx_hc_forward_mfma(const mx_qweight* down, const mx_qweight* up,
+                                    const uint16_t* h, const uint16_t* scale, int32_t rows,
+                                    int32_t hc, int32_t hidden, int32_t rank, float eps,
+                                    void* workspace, uint16_t* mixed, uint16_t* inj,
+                                    void* stream) {
+  MX_CHECK(down && up && h && scale && workspace && mixed, MX_EINVAL,
+           "mx_hc_forward_mfma: null pointer");
+  MX_CHECK(rows >= 1 && rows <= 8, MX_EUNSUPPORTED, "mx_hc_forward_mfma: rows must be in 1..8");
+  const QWeight d = to_qweight(*down), u = to_qweight(*up);
+  for (const QWeight* q : {&d, &u})
+    if (const char* err = check_qweight(*q))
+      return mx_status(set_error(MX_EINVAL, std::string("mx_hc_forward_mfma: ") + err));
+  MX_CHECK(hc_fused_supported(d, u, hc, hidden, rank), MX_EUNSUPPORTED,
+           "mx_hc_forward_mfma: needs hc 4, hidden <= 2048, rank 256 or 512, down rows rank "
+           "(+ hc inject rows), group_size 64");
+  MX_CHECK(d.n == rank || inj != nullptr, MX_EINVAL, "mx_hc_forward_mfma: inject rows need inj");
+  return finish(hc_fused(d, u, h, scale, rows, hc, hidden, rank, eps,
+                         static_cast<float*>(workspace), mixed, inj, hipStream_t(stream)),
+                "mx_hc_forward_mfma");
+}
+
 MX_ABI mx_status mx_moe_experts_mfma(const uint16_t* x, const uint32_t* ids, const uint16_t* scores,
                                      int32_t rows, int32_t top_k, const mx_qbank* gate,
                                      const mx_qbank* up, const mx_qbank* down,

@@ -255,3 +255,52 @@ def test_qmm_conv_matches_qmm_then_conv(mx, orc, n, k, ch, taps, m):
     assert (got[:, :ch] == 0).all()  # conv channels are not written to y
     other = np.setdiff1d(np.arange(S), slots)
     assert (st2.numpy()[other] == state[other]).all()
+
+
+@pytest.mark.parametrize("hidden,rank,inject,rows", [(2048, 256, True, 8), (2048, 256, False, 3),
+                                                     (1024, 256, True, 5), (512, 256, True, 1),
+                                                     (2048, 512, False, 2)])
+def test_hc_forward_mfma_within_tolerance_of_oracle(mx, orc, hidden, rank, inject, rows):
+    """The matrix-core hyper-connection projection (norm factored out of the
+    down projection, hardware exp2 / rsqrt) against the oracle's fixed-order
+    HC (norm, down + activation, up + mix): the north star's 2e-2 relative /
+    1e-2 of the row's largest magnitude; repeated calls give the same bits."""
+    from test_layers_gpu import dev
+
+    hc = 4
+    n_down = rank + (hc if inject else 0)
+    down = mx.QWeight.random(n_down, hc * hidden, 4, 64, 9500 + hidden + rows)
+    up = mx.QWeight.random(hc * hidden, rank, 4, 64, 9501 + hidden)
+    rng = np.random.default_rng(hidden + rows)
+    h = orc.f32_to_bf16(rng.standard_normal((rows, hc * hidden)).astype(np.float32))
+    scale = orc.f32_to_bf16(rng.uniform(-0.5, 0.5, hc * hidden).astype(np.float32))
+    eps = 1e-6
+    dh, ds = dev(mx, h), dev(mx, scale)
+    ws = mx.DeviceArray((mx.lib.mx_hc_workspace_bytes(n_down),), np.uint8)
+    dc, uc = down.c(), up.c()
+    outs = []
+    for _ in range(2):
+        mixed = mx.DeviceArray((rows, hidden), np.uint16)
+        inj = mx.DeviceArray((rows, hc), np.uint16)
+        mx.check(mx.lib.mx_hc_forward_mfma(C.byref(dc), C.byref(uc), dh.ptr, ds.ptr, rows, hc,
+                                           hidden, rank, eps, ws.ptr, mixed.ptr, inj.ptr, None))
+        outs.append((mixed.numpy(), inj.numpy()))
+    assert (outs[0][0] == outs[1][0]).all()
+    m1, i1 = outs[0]
+    dcodes, dsc, dbi = down.host()
+    ucodes, usc, ubi = up.host()
+    dq = orc.qw(dcodes, dsc, dbi, n_down, hc * hidden, 4, 64)
+    uq = orc.qw(ucodes, usc, ubi, hc * hidden, rank, 4, 64)
+    xn = np.empty_like(h)
+    orc.lib.mxo_hc_norm(orc._p(h), orc._p(scale), rows, hc, hidden, eps, orc._p(xn))
+    lo = np.empty((rows, rank), np.uint16)
+    inj_w = np.zeros((rows, hc), np.uint16)
+    orc.lib.mxo_hc_down(C.byref(dq), orc._p(xn), rows, rank, hc, orc._p(lo), orc._p(inj_w))
+    mixed_w = np.empty((rows, hidden), np.uint16)
+    orc.lib.mxo_hc_up_mix(C.byref(uq), orc._p(lo), orc._p(xn), rows, hidden, orc._p(mixed_w))
+    got, want = bf(m1).astype(np.float64), bf(mixed_w).astype(np.float64)
+    scale_w = np.abs(want).max(axis=1, keepdims=True)
+    assert np.all(np.abs(got - want) <= 2e-2 * np.abs(want) + 1e-2 * scale_w)
+    if inject:
+        gi, wi = bf(i1).astype(np.float64), bf(inj_w).astype(np.float64)
+        assert np.all(np.abs(gi - wi) <= 2e-2 * np.abs(wi) + 1e-2)
