@@ -253,6 +253,24 @@ mx_status mx_moe_routed_experts_mfma(const uint16_t* logits, int64_t logit_strid
                                      const mx_qweight* shared_up, const mx_qweight* shared_down,
                                      void* workspace, uint32_t* ids, uint16_t* scores,
                                      uint16_t* factor, uint16_t* partial, void* stream);
+/* The whole MoE sublayer after the router projection, in two launches:
+ * mx_moe_routed_experts_mfma, then mx_moe_reduce_hc_epilogue(partial, factor,
+ * residual = out = hcs, gate = hc_gate), with the down projection, the slot
+ * sum and the stream write in one kernel (ids / scores / factor / hcs
+ * bit-identical to those two calls).  hc == 4, top_k <= 15 and 512-deep
+ * experts (routed and shared) only; MX_EUNSUPPORTED otherwise.  hcs:
+ * [rows][4][hidden] residual streams, updated in place; hc_gate: [rows][4].
+ * workspace: mx_moe_workspace_bytes.  Replaces moe_route::tail
+ * (src/moe_route.rs:25-70), the expert MLPs and slot sum of MoE::parts
+ * (src/hybrid.rs:217-271, kernels/moe_down_tail.metal:83-99) and
+ * moe_epilogue::apply (src/moe_epilogue.rs:17-73). */
+mx_status mx_moe_routed_experts_hc_mfma(
+    const uint16_t* logits, int64_t logit_stride, const uint16_t* shared_logit,
+    int64_t shared_stride, int32_t experts, const uint16_t* x, int32_t rows, int32_t top_k,
+    int32_t hc, const mx_qbank* gate, const mx_qbank* up, const mx_qbank* down,
+    const mx_qweight* shared_gate, const mx_qweight* shared_up, const mx_qweight* shared_down,
+    void* workspace, uint32_t* ids, uint16_t* scores, uint16_t* factor, const uint16_t* hc_gate,
+    uint16_t* hcs, void* stream);
 /* routed[r] = bf16 sum of partial[r, 0..top_k-1] in the reference's slot
  * order (kernels/moe_down_tail.h:20, moe_down_tail.metal:83-99). */
 mx_status mx_moe_reduce(const uint16_t* partial, int32_t rows, int32_t top_k, int32_t hidden,

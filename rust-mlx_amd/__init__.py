@@ -194,6 +194,11 @@ def _load() -> C.CDLL:
                                         C.POINTER(QBankC), C.POINTER(QBankC),
                                         C.POINTER(QWeightC), C.POINTER(QWeightC),
                                         C.POINTER(QWeightC), vp, vp, vp, vp, vp, vp], i32),
+        "mx_moe_routed_experts_hc_mfma": ([vp, i64, vp, i64, i32, vp, i32, i32, i32,
+                                           C.POINTER(QBankC), C.POINTER(QBankC),
+                                           C.POINTER(QBankC), C.POINTER(QWeightC),
+                                           C.POINTER(QWeightC), C.POINTER(QWeightC), vp, vp, vp,
+                                           vp, vp, vp, vp], i32),
         "mx_engine_profile_step": ([vp, vp, vp, i32, vp, C.POINTER(StepProfileC)], i32),
         "mx_engine_read": ([vp, C.c_char_p, vp, sz], i32),
         "mx_engine_time_experts": ([vp, i32, C.POINTER(ExpertTimingC)], i32),

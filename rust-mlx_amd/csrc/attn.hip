@@ -251,6 +251,20 @@ __global__ __launch_bounds__(256) void decode_fast_kernel(
     const uint4 v = *reinterpret_cast<const uint4*>(qr + kk * 32);
     qa[kk] = j < G ? v : make_uint4(0u, 0u, 0u, 0u);
   }
+  // the value rows go out with the keys: their addresses do not depend on
+  // the scores, so one memory round trip serves both
+  constexpr int DB = HD / 32;   // 8-dim blocks per wave
+  constexpr int NPG = 64 / DB;  // position groups per wave
+  constexpr int PPL = C / NPG;  // positions per lane
+  const int db = lane % DB, pg = lane / DB;
+  const int dim0 = wave * (HD / 4) + db * 8;
+  uint4 vv[PPL];
+#pragma unroll
+  for (int i = 0; i < PPL; ++i) {
+    const int pp = j0 + pg + NPG * i;
+    vv[i] = *reinterpret_cast<const uint4*>(v_cache + base + size_t(pp < n_pos ? pp : n_pos - 1) * HD +
+                                            dim0);
+  }
   sk::floatx4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int kk = 0; kk < KS; ++kk) acc = sk::mfma(qa[kk], kb[kk], acc);
@@ -294,18 +308,6 @@ __global__ __launch_bounds__(256) void decode_fast_kernel(
     ml[1] = l;
   }
 
-  constexpr int DB = HD / 32;   // 8-dim blocks per wave
-  constexpr int NPG = 64 / DB;  // position groups per wave
-  constexpr int PPL = C / NPG;  // positions per lane
-  const int db = lane % DB, pg = lane / DB;
-  const int dim0 = wave * (HD / 4) + db * 8;
-  uint4 vv[PPL];
-#pragma unroll
-  for (int i = 0; i < PPL; ++i) {
-    const int pp = j0 + pg + NPG * i;
-    vv[i] = *reinterpret_cast<const uint4*>(v_cache + base + size_t(pp < n_pos ? pp : n_pos - 1) * HD +
-                                            dim0);
-  }
   float o[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g)

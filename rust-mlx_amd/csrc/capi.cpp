@@ -824,6 +824,52 @@ MX_ABI mx_status mx_moe_routed_experts_mfma(
   return finish(rc, "mx_moe_routed_experts_mfma");
 }
 
+MX_ABI mx_status mx_moe_routed_experts_hc_mfma(
+    const uint16_t* logits, int64_t logit_stride, const uint16_t* shared_logit,
+    int64_t shared_stride, int32_t experts, const uint16_t* x, int32_t rows, int32_t top_k,
+    int32_t hc, const mx_qbank* gate, const mx_qbank* up, const mx_qbank* down,
+    const mx_qweight* shared_gate, const mx_qweight* shared_up, const mx_qweight* shared_down,
+    void* workspace, uint32_t* ids, uint16_t* scores, uint16_t* factor, const uint16_t* hc_gate,
+    uint16_t* hcs, void* stream) {
+  MX_CHECK(logits && shared_logit && x && gate && up && down && shared_gate && shared_up &&
+               shared_down && workspace && ids && scores && factor && hc_gate && hcs,
+           MX_EINVAL, "mx_moe_routed_experts_hc_mfma: null pointer");
+  MX_CHECK(rows >= 1 && rows <= 8, MX_EUNSUPPORTED,
+           "mx_moe_routed_experts_hc_mfma: rows must be in 1..8");
+  MX_CHECK(top_k >= 1 && top_k <= 15, MX_EUNSUPPORTED,
+           "mx_moe_routed_experts_hc_mfma: top_k must be in 1..15");
+  MX_CHECK(hc == 4, MX_EUNSUPPORTED, "mx_moe_routed_experts_hc_mfma: hc must be 4");
+  MX_CHECK(experts % 64 == 0 && (experts / 64 == 1 || experts / 64 == 2 || experts / 64 == 4 ||
+                                 experts / 64 == 8 || experts / 64 == 16),
+           MX_EUNSUPPORTED,
+           "mx_moe_routed_experts_hc_mfma: experts must be 64, 128, 256, 512 or 1024");
+  MX_CHECK(logit_stride >= experts && shared_stride >= 1, MX_EINVAL,
+           "mx_moe_routed_experts_hc_mfma: row strides too small");
+  const QBank g = to_qbank(*gate), u = to_qbank(*up), d = to_qbank(*down);
+  const QWeight sg = to_qweight(*shared_gate), su = to_qweight(*shared_up), sd = to_qweight(*shared_down);
+  for (const QBank* b : {&g, &u, &d}) {
+    if (const char* err = check_bank(*b))
+      return mx_status(set_error(MX_EINVAL, std::string("mx_moe_routed_experts_hc_mfma: ") + err));
+  }
+  MX_CHECK(experts <= g.experts, MX_EINVAL,
+           "mx_moe_routed_experts_hc_mfma: more logits than experts");
+  MX_CHECK(g.n == u.n && g.k == u.k && d.k == g.n && d.n == g.k && g.experts == u.experts &&
+               g.experts == d.experts && g.bits == u.bits && sg.n == su.n && sg.k == g.k &&
+               su.k == g.k && sd.k == sg.n && sd.n == g.k && sg.bits == g.bits && sd.bits == d.bits,
+           MX_EINVAL, "mx_moe_routed_experts_hc_mfma: banks and shared expert disagree in shape");
+  MX_CHECK(skinny_down_hc_supported(rows, top_k, hc, d, sd), MX_EUNSUPPORTED,
+           "mx_moe_routed_experts_hc_mfma: experts must be 512 deep (routed and shared), "
+           "group_size 64, 4/5/6/8 bits, hidden a multiple of 16");
+  uint16_t* h = static_cast<uint16_t*>(workspace);
+  hipStream_t s = hipStream_t(stream);
+  const RouteIO ro{logits, logit_stride, shared_logit, shared_stride, ids, scores, factor};
+  int rc = skinny_route_gate_up(ro, experts, x, rows, top_k, g, u, sg, su, h, s);
+  if (rc == MX_OK)
+    rc = skinny_down_hc(h, ids, scores, factor, hc_gate, rows, top_k, hc, g.n, sg.n, d, sd, hcs,
+                        s);
+  return finish(rc, "mx_moe_routed_experts_hc_mfma");
+}
+
 MX_ABI mx_status mx_engine_fill_slot(mx_engine* e, int32_t slot, int32_t length, uint64_t seed) {
   MX_CHECK(e && slot_ok(*e->impl, slot), MX_EINVAL, "mx_engine_fill_slot: bad engine or slot");
   std::string err;

@@ -586,13 +586,22 @@ int record_step(Engine& e, int rows, int groups, int t, bool history, bool logit
     rl.y = e.logits_r;
     rl.y_stride = c.experts + 1;
     MX_TRY(project(e, L.router, e.mixed, c.hidden, rows, rl));
+    bool summed = false;  // slots summed and the streams written
     if (!e.prof && experts_fast(e, L)) {
       // the expert gate/up kernel routes the rows itself
       const RouteIO ro{e.logits_r, c.experts + 1, e.logits_r + c.experts, c.experts + 1,
                        e.ids, e.scores, e.factor};
       MX_TRY(skinny_route_gate_up(ro, c.experts, e.mixed, rows, c.top_k, L.gate, L.up, L.sgate,
                                   L.sup, e.moe_h, e.stream));
-      MX_TRY(experts_down(e, L, rows));
+      // 512-deep experts: the down kernel sums the slots and writes the
+      // residual streams itself
+      if (skinny_down_hc_supported(rows, c.top_k, c.hc, L.down, L.sdown)) {
+        MX_TRY(skinny_down_hc(e.moe_h, e.ids, e.scores, e.factor, e.inj, rows, c.top_k, c.hc,
+                              L.gate.n, L.sgate.n, L.down, L.sdown, e.h, e.stream));
+        summed = true;
+      } else {
+        MX_TRY(experts_down(e, L, rows));
+      }
     } else {
       MX_TRY(moe_route(e.logits_r, c.experts + 1, e.logits_r + c.experts, c.experts + 1, rows,
                        c.experts, c.top_k, e.ids, e.scores, e.factor, e.stream));
@@ -604,8 +613,9 @@ int record_step(Engine& e, int rows, int groups, int t, bool history, bool logit
         MX_TRY(experts_down(e, L, rows));
       }
     }
-    MX_TRY(moe_reduce_hc_epilogue(e.moe_p, e.factor, e.h, e.inj, rows, c.top_k, c.hc, c.hidden,
-                                  e.h, e.stream));
+    if (!summed)
+      MX_TRY(moe_reduce_hc_epilogue(e.moe_p, e.factor, e.h, e.inj, rows, c.top_k, c.hc,
+                                    c.hidden, e.h, e.stream));
   }
   // mixer + greedy head
   MX_TRY(hc_forward(e, e.mixer, rows, e.mixed, nullptr));

@@ -101,6 +101,15 @@ int skinny_route_gate_up(const RouteIO& ro, int experts, const uint16_t* x, int 
 int skinny_down(const uint16_t* h, const uint32_t* ids, const uint16_t* scores, int rows,
                 int top_k, int inter, int shared_inter, const QBank& down, const QWeight& sdown,
                 uint16_t* p, hipStream_t s);
+// Expert down + score + slot sum + hyper-connection write (hc == 4, 512-deep
+// experts); bit-identical to skinny_down then moe_reduce_hc_epilogue with out
+// = hcs.  MX_EUNSUPPORTED outside those shapes.
+bool skinny_down_hc_supported(int rows, int top_k, int hc, const QBank& down,
+                              const QWeight& sdown);
+int skinny_down_hc(const uint16_t* h, const uint32_t* ids, const uint16_t* scores,
+                   const uint16_t* factor, const uint16_t* hc_gate, int rows, int top_k, int hc,
+                   int inter, int shared_inter, const QBank& down, const QWeight& sdown,
+                   uint16_t* hcs, hipStream_t s);
 int skinny_head_parts(int n);
 int skinny_head(const QWeight& w, const uint16_t* x, int m, float* maxima, uint32_t* indices,
                 int* parts_out, hipStream_t s);

@@ -612,6 +612,118 @@ __global__ __launch_bounds__(256, 4) void down_kernel(const uint16_t* __restrict
 }
 
 // ---------------------------------------------------------------------------
+// Expert down + score + slot sum + hyper-connection write for 512-deep experts
+// and hc == 4: one workgroup per (16 output columns, token row), so the slot
+// sum of a column never leaves the workgroup.  The row's slots 0..7 and
+// 8..top_k (the last one the shared expert) are staged as the eight
+// activation rows of two stagings; wave w streams the 16 weight rows of the
+// experts of slots w, w + 4, .. (all loads issued together) over the staging
+// of its slot and keeps the slot's own D row.  Every matrix-core output row
+// depends only on its own activation row, so each slot value is the one
+// down_kernel computes; the slot sum and the write follow
+// moe_reduce_epilogue4_kernel (reference order of moe_down_tail.metal:83-99,
+// then moe_epilogue.rs:17-73): the result is bit-identical to down_kernel
+// followed by that kernel.  All rows of a column tile share an XCD (grid x is
+// the tile), so experts chosen by several rows and the shared expert are
+// fetched from HBM once per tile.  hcs: the residual streams, updated in
+// place (row r, stream s at hcs + (4 r + s) hidden).
+template <int BITS, int NSL>
+__global__ __launch_bounds__(256, BITS * NSL <= 18 ? 4 : 2) void down_hc_kernel(
+    const uint16_t* __restrict__ h, const uint32_t* __restrict__ ids,
+    const uint16_t* __restrict__ scores, const uint16_t* __restrict__ factor,
+    const uint16_t* __restrict__ hc_gate, int top_k, QBank down, QWeight sdown, int hs,
+    uint16_t* __restrict__ hcs) {
+  constexpr int STEPS = 4;
+  constexpr int G = 2 * STEPS;  // 64-value groups per weight row
+  constexpr int SB = sk::stage_bytes(STEPS);
+  constexpr int XB = STEPS * sk::kStepBytes;
+  extern __shared__ __align__(16) char lds[];
+  __shared__ float pl[4 * NSL][16];
+  const int tg = blockIdx.x, row = blockIdx.y;
+  const int S = top_k + 1;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane & 15, q = lane >> 4;
+  const int hidden = sdown.n;
+  const int col = tg * 16 + j;  // hidden % 16 == 0 (host)
+  // the row's routes: one clamped slot per lane (vector loads)
+  const int ls = min(lane, top_k - 1);
+  const uint32_t idl = min(ids[size_t(row) * top_k + ls], uint32_t(down.experts - 1));
+  const uint32_t scl = scores[size_t(row) * top_k + ls];
+  // the epilogue's inputs (thread (stream es, column ec) of the first wave)
+  // go out with the first loads
+  const int es = (threadIdx.x >> 4) & 3, ec = threadIdx.x & 15;
+  uint16_t* o = hcs + (size_t(row) * 4 + es) * hidden + tg * 16 + ec;
+  const uint16_t rv = *o;
+  const uint16_t fv = factor[row];
+  const uint16_t gv = hc_gate[size_t(row) * 4 + es];
+  const sk::DenseRows xa{h + size_t(row) * S * hs, hs, S < 8 ? S : 8};
+  const sk::DenseRows xb{h + (size_t(row) * S + 8) * hs, hs, S > 8 ? S - 8 : 1};
+  sk::Stager<256, sk::stage_per(256, STEPS), sk::DenseRows> sta(xa, xa.M, 0, STEPS);
+  sk::Stager<256, sk::stage_per(256, STEPS), sk::DenseRows> stb(xb, xb.M, 0, STEPS);
+  sta.load();
+  if (S > 8) stb.load();  // uniform
+  typedef sk::Stream<BITS, false, sk::DenseRows, STEPS, 8> St;
+  // slot i of this wave (clamped to the last slot: a wave with fewer slots
+  // re-reads the shared expert's rows and discards them)
+  auto make = [&](int i) {
+    const int sl = min(wave + 4 * i, S - 1);
+    const int e = sl < top_k ? __shfl(int(idl), sl, 64) : -1;
+    const QWeight dw = expert_weight(down, e, sdown);
+    const char* base = lds + (sl >= 8 ? SB : 0);
+    return St(dw.codes + size_t(col) * (size_t(STEPS) * sk::kSuper * BITS / 32),
+              dw.scales + size_t(col) * G, dw.biases + size_t(col) * G, STEPS, 0, STEPS, 0,
+              base, reinterpret_cast<const float*>(base + XB + sk::kZeroBytes), xa, 8);
+  };
+  St s0 = make(0);
+  s0.prefetch();
+  St s1 = make(NSL > 1 ? 1 : 0);
+  if constexpr (NSL > 1) s1.prefetch();
+  St s2 = make(NSL > 2 ? 2 : 0);
+  if constexpr (NSL > 2) s2.prefetch();
+  St s3 = make(NSL > 3 ? 3 : 0);
+  if constexpr (NSL > 3) s3.prefetch();
+  sta.store(lds);
+  if (S > 8) stb.store(lds + SB);
+  // the slot's D row m = slot % 8 sits, after the parity join, in lane
+  // 16 (m / 4) + j, element m % 4; p = bf16(bf16(down) * score) for routed
+  // slots, bf16(down) for the shared one
+  auto finish = [&](St& st, int i) {
+    const int sl = wave + 4 * i;
+    if (sl >= S) return;  // uniform
+    float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    st.run(XB, y);
+    sk::join_parities(y);
+    const int m = sl & 7, r = m & 3;
+    const float v = r == 0 ? y[0] : r == 1 ? y[1] : r == 2 ? y[2] : y[3];
+    // the score shuffle runs on every lane: its source lane may lie outside
+    // the writing lanes
+    const uint32_t sc = uint32_t(__shfl(int(scl), sl < top_k ? sl : 0, 64));
+    if (q == (m >> 2)) {
+      const float dv = round_bf16(v);
+      pl[sl][j] = sl < top_k ? round_bf16(dv * bf16_to_f32(uint16_t(sc))) : dv;
+    }
+  };
+  finish(s0, 0);
+  if constexpr (NSL > 1) finish(s1, 1);
+  if constexpr (NSL > 2) finish(s2, 2);
+  if constexpr (NSL > 3) finish(s3, 3);
+  __syncthreads();
+  if (threadIdx.x >= 64) return;
+  // thread (stream es, column ec): the slot sum, then the stream's write
+  const int c = ec;
+  const int lanes = top_k < 8 ? top_k : 8;
+  float routed = 0.0f;
+  for (int a = 0; a < lanes; ++a) {
+    float v = pl[a][c];
+    if (a + 8 < top_k) v = round_bf16(v + pl[a + 8][c]);
+    routed = a == 0 ? v : round_bf16(v + routed);
+  }
+  routed = round_bf16(routed);
+  const float combined = round_bf16(routed + round_bf16(pl[top_k][c] * bf16_to_f32(fv)));
+  const float inj = round_bf16(combined * bf16_to_f32(gv));
+  *o = f32_to_bf16(bf16_to_f32(rv) + inj);
+}
+
+// ---------------------------------------------------------------------------
 // Greedy head: per activation row, the best (bf16(logit), lowest id) of the
 // workgroup's 64 rows.  NaN never wins; a part with nothing above -inf keeps
 // id 0xffffffff and -inf.
@@ -900,6 +1012,39 @@ int skinny_down(const uint16_t* h, const uint32_t* ids, const uint16_t* scores, 
     default: return MX_EUNSUPPORTED;
   }
 #undef MX_DN
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
+bool skinny_down_hc_supported(int rows, int top_k, int hc, const QBank& down,
+                              const QWeight& sdown) {
+  return rows >= 1 && rows <= 8 && top_k >= 1 && top_k + 1 <= 16 && hc == 4 &&
+         down.group_size == 64 && sdown.group_size == 64 && down.k == 4 * sk::kSuper &&
+         sdown.k == 4 * sk::kSuper && sdown.bits == down.bits && sdown.n == down.n &&
+         down.n % 16 == 0 && down.experts >= 1 &&
+         (down.bits == 4 || down.bits == 5 || down.bits == 6 || down.bits == 8);
+}
+
+int skinny_down_hc(const uint16_t* h, const uint32_t* ids, const uint16_t* scores,
+                   const uint16_t* factor, const uint16_t* hc_gate, int rows, int top_k, int hc,
+                   int inter, int shared_inter, const QBank& down, const QWeight& sdown,
+                   uint16_t* hcs, hipStream_t s) {
+  if (!skinny_down_hc_supported(rows, top_k, hc, down, sdown)) return MX_EUNSUPPORTED;
+  const int hs = inter > shared_inter ? inter : shared_inter;
+  const int nsl = (top_k + 1 + 3) / 4;
+  const dim3 grid(down.n / 16, rows);
+  const int lb = 2 * sk::stage_bytes(4);
+  switch (down.bits * 8 + nsl) {
+#define MX_DH(B, N)                                                                          \
+  case B * 8 + N:                                                                            \
+    hipLaunchKernelGGL((down_hc_kernel<B, N>), grid, dim3(256), lb, s, h, ids, scores, factor, \
+                       hc_gate, top_k, down, sdown, hs, hcs);                                 \
+    break;
+    MX_DH(4, 1) MX_DH(4, 2) MX_DH(4, 3) MX_DH(4, 4) MX_DH(5, 1) MX_DH(5, 2) MX_DH(5, 3)
+    MX_DH(5, 4) MX_DH(6, 1) MX_DH(6, 2) MX_DH(6, 3) MX_DH(6, 4) MX_DH(8, 1) MX_DH(8, 2)
+    MX_DH(8, 3) MX_DH(8, 4)
+#undef MX_DH
+    default: return MX_EUNSUPPORTED;
+  }
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 

@@ -125,6 +125,29 @@ __device__ __forceinline__ uint32_t code_at(const uint32_t (&w)[BITS]) {
   }
 }
 
+// 0x43004300 in a vector register: with the mask in a scalar register,
+// (p & mask) | c is then one v_and_or_b32 (a VOP3 instruction takes neither
+// literal operands nor two scalar registers on this architecture).
+__device__ __forceinline__ uint32_t vconst_43004300() {
+  uint32_t c;
+  asm("v_mov_b32 %0, 0x43004300" : "=v"(c));
+  return c;
+}
+
+// The 32 bits of the lane's words starting at bit BIT (bits past the last
+// word read as zeros).
+template <int BITS, int BIT>
+__device__ __forceinline__ uint32_t window(const uint32_t (&w)[BITS]) {
+  constexpr int k = BIT >> 5, o = BIT & 31;
+  if constexpr (o == 0) {
+    return w[k];
+  } else if constexpr (k + 1 < BITS) {
+    return __builtin_amdgcn_alignbit(w[k + 1], w[k], uint32_t(o));
+  } else {
+    return w[k] >> o;
+  }
+}
+
 // B operand of MFMA step U (values 8U .. 8U+7 of the lane's 32) in operand order.
 template <int BITS, int U>
 __device__ __forceinline__ uint4 b_operand(const uint32_t (&w)[BITS]) {
@@ -147,6 +170,32 @@ __device__ __forceinline__ uint4 b_operand(const uint32_t (&w)[BITS]) {
     r.y = pair(float((lo >> 8) & 0xffu), float((hi >> 8) & 0xffu));
     r.z = pair(float((lo >> 16) & 0xffu), float((hi >> 16) & 0xffu));
     r.w = pair(float(lo >> 24), float(hi >> 24));
+  } else if constexpr (BITS == 5) {
+    // the operand's codes are the 40 bits at b = 40 U and each operand word
+    // pairs codes i and i + 4, 20 bits apart: one word p holding bits
+    // b .. b+15 low and b+20 .. b+35 high yields pairs 0..2 as
+    // (p >> 5 i) & 0x001F001F; pair 3 comes from windows at b+15 and b+19
+    constexpr int b = 40 * U;
+    constexpr uint32_t m = 0x001F001Fu;
+    const uint32_t c = vconst_43004300();
+    const uint32_t p = (window<5, b>(w) & 0xFFFFu) | (window<5, b + 4>(w) & 0xFFFF0000u);
+    const uint32_t p3 = (window<5, b + 15>(w) & 0xFFFFu) | (window<5, b + 19>(w) & 0xFFFF0000u);
+    r.x = (p & m) | c;
+    r.y = ((p >> 5) & m) | c;
+    r.z = ((p >> 10) & m) | c;
+    r.w = (p3 & m) | c;
+  } else if constexpr (BITS == 6) {
+    // 48 bits at b = 48 U, pairs 24 bits apart: words holding bits b .. +15
+    // with b+24 .. +39 (pairs 0, 1) and b+12 .. +27 with b+36 .. +51 (2, 3)
+    constexpr int b = 48 * U;
+    constexpr uint32_t m = 0x003F003Fu;
+    const uint32_t c = vconst_43004300();
+    const uint32_t p = (window<6, b>(w) & 0xFFFFu) | (window<6, b + 8>(w) & 0xFFFF0000u);
+    const uint32_t p2 = (window<6, b + 12>(w) & 0xFFFFu) | (window<6, b + 20>(w) & 0xFFFF0000u);
+    r.x = (p & m) | c;
+    r.y = ((p >> 6) & m) | c;
+    r.z = (p2 & m) | c;
+    r.w = ((p2 >> 6) & m) | c;
   } else {
     r.x = (code_at<BITS, 8 * U + 0>(w) | (code_at<BITS, 8 * U + 4>(w) << 16)) | 0x43004300u;
     r.y = (code_at<BITS, 8 * U + 1>(w) | (code_at<BITS, 8 * U + 5>(w) << 16)) | 0x43004300u;

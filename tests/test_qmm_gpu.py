@@ -219,6 +219,66 @@ def test_moe_routed_experts_mfma_matches_route_then_experts(mx, orc, E, rows):
     assert (fa.numpy() == want_fa).all()
 
 
+@pytest.mark.parametrize("E,rows,top_k,dbits", [(512, 8, 10, 5), (512, 1, 10, 5), (512, 5, 10, 4),
+                                                (256, 8, 8, 6), (256, 3, 15, 8), (128, 8, 3, 4),
+                                                (64, 2, 4, 5)])
+def test_moe_routed_experts_hc_mfma_matches_experts_then_epilogue(mx, orc, E, rows, top_k, dbits):
+    """The MoE sublayer call (down projection, slot sum and stream write in
+    one kernel) gives the bits of mx_moe_routed_experts_mfma followed by
+    mx_moe_reduce_hc_epilogue: ids, scores, factor and the updated streams.
+    top_k 3 .. 15 covers one to four slots per wave."""
+    from test_layers_gpu import dev
+
+    I, H = 512, 2048
+    sd0 = 1000 * top_k + E
+    gate = mx.QBank.random(E, I, H, 4, 64, sd0)
+    up = mx.QBank.random(E, I, H, 4, 64, sd0 + 1)
+    down = mx.QBank.random(E, H, I, dbits, 64, sd0 + 2)
+    sg = mx.QWeight.random(I, H, 4, 64, sd0 + 3)
+    su = mx.QWeight.random(I, H, 4, 64, sd0 + 4)
+    sd = mx.QWeight.random(H, I, dbits, 64, sd0 + 5)
+    stride = E + 1
+    lg = orc.fill_bf16(rows * stride, sd0 + 6, 1, 2.0, 0.0).reshape(rows, stride)
+    x = orc.fill_bf16(rows * H, sd0 + 7, 1, 1.0, 0.0).reshape(rows, H)
+    res = orc.fill_bf16(rows * 4 * H, sd0 + 8, 1, 1.0, 0.0).reshape(rows, 4, H)
+    hg = orc.fill_bf16(rows * 4, sd0 + 9, 1, 1.0, 1.0).reshape(rows, 4)
+    d_lg, dx, dhg = dev(mx, lg), dev(mx, x), dev(mx, hg)
+    ws = mx.DeviceArray((mx.lib.mx_moe_workspace_bytes(8, 16, I),), np.uint8)
+    qb = [b.c() for b in (gate, up, down)]
+    qs = [w.c() for w in (sg, su, sd)]
+    lg_ptr, sh_ptr = d_lg.ptr, d_lg.ptr + 2 * E
+
+    ids_w = mx.DeviceArray((rows, top_k), np.uint32)
+    sc_w = mx.DeviceArray((rows, top_k), np.uint16)
+    fa_w = mx.DeviceArray((rows,), np.uint16)
+    p_w = mx.DeviceArray((rows, top_k + 1, H), np.uint16)
+    mx.check(mx.lib.mx_moe_routed_experts_mfma(lg_ptr, stride, sh_ptr, stride, E, dx.ptr, rows,
+                                               top_k, C.byref(qb[0]), C.byref(qb[1]),
+                                               C.byref(qb[2]), C.byref(qs[0]), C.byref(qs[1]),
+                                               C.byref(qs[2]), ws.ptr, ids_w.ptr, sc_w.ptr,
+                                               fa_w.ptr, p_w.ptr, None))
+    dres = dev(mx, res)
+    out_w = mx.DeviceArray((rows, 4, H), np.uint16)
+    mx.check(mx.lib.mx_moe_reduce_hc_epilogue(p_w.ptr, fa_w.ptr, dres.ptr, dhg.ptr, rows, top_k,
+                                              4, H, out_w.ptr, None))
+
+    ids = mx.DeviceArray((rows, top_k), np.uint32)
+    sc = mx.DeviceArray((rows, top_k), np.uint16)
+    fa = mx.DeviceArray((rows,), np.uint16)
+    hcs = dev(mx, res)
+    mx.check(mx.lib.mx_moe_routed_experts_hc_mfma(lg_ptr, stride, sh_ptr, stride, E, dx.ptr, rows,
+                                                  top_k, 4, C.byref(qb[0]), C.byref(qb[1]),
+                                                  C.byref(qb[2]), C.byref(qs[0]), C.byref(qs[1]),
+                                                  C.byref(qs[2]), ws.ptr, ids.ptr, sc.ptr, fa.ptr,
+                                                  dhg.ptr, hcs.ptr, None))
+    assert (ids.numpy() == ids_w.numpy()).all()
+    assert (sc.numpy() == sc_w.numpy()).all()
+    assert (fa.numpy() == fa_w.numpy()).all()
+    got, want = hcs.numpy(), out_w.numpy()
+    assert (got == want).all(), np.argwhere(got != want)[:8]
+    assert not (got == res).all()
+
+
 @pytest.mark.parametrize("n,k,ch,taps,m", [(12352, 2048, 8192, 4, 8), (640, 512, 384, 3, 3),
                                            (300, 1024, 300, 2, 1), (49152, 512, 1000, 4, 2)])
 def test_qmm_conv_matches_qmm_then_conv(mx, orc, n, k, ch, taps, m):
