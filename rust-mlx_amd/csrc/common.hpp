@@ -23,11 +23,12 @@ MX_HD float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
 MX_HD float bf16_to_f32(uint16_t h) { return u2f(uint32_t(h) << 16); }
 
 // fp32 -> bf16, round to nearest even; NaN becomes the canonical quiet NaN.
+// (Written as selects: no branch on the device.)
 MX_HD uint16_t f32_to_bf16(float f) {
-  uint32_t u = f2u(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t(0x7fc0u | ((u >> 16) & 0x8000u));
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return uint16_t(u >> 16);
+  const uint32_t u = f2u(f);
+  const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t q = 0x7fc0u | ((u >> 16) & 0x8000u);
+  return uint16_t((u & 0x7fffffffu) > 0x7f800000u ? q : r);
 }
 
 // Round an fp32 value to the nearest bf16 value, keeping fp32 storage.
@@ -37,13 +38,15 @@ MX_HD float fmaf_(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
 
 // e^x: Cody-Waite reduction x = n*ln2 + r, |r| <= ln2/2, degree-7 Taylor
 // polynomial for e^r, then exact scaling by 2^n (two steps below 2^-126).
+// Branch-free: the reduction runs on x clamped to [-104, 89] (a no-op inside
+// the finite range), and NaN, overflow (x > 88.7228...: +inf) and underflow
+// (x < -103.972...: 0) are selected at the end; the same bits as handling
+// them first, for every fp32 input.
 MX_HD float expf_(float x) {
-  if (x != x) return x;
-  if (x > 88.72283935546875f) return u2f(0x7f800000u);
-  if (x < -103.972084045410156f) return 0.0f;
-  const float t = x * 1.44269502162933349609375f;
+  const float xc = __builtin_fminf(__builtin_fmaxf(x, -104.0f), 89.0f);
+  const float t = xc * 1.44269502162933349609375f;
   const float n = __builtin_rintf(t);
-  float r = fmaf_(-n, 0.693145751953125f, x);
+  float r = fmaf_(-n, 0.693145751953125f, xc);
   r = fmaf_(-n, 1.428606765330187045e-06f, r);
   float p = 1.98412698e-04f;          // 1/5040
   p = fmaf_(p, r, 1.38888889e-03f);   // 1/720
@@ -54,15 +57,15 @@ MX_HD float expf_(float x) {
   p = fmaf_(p, r, 1.0f);
   p = fmaf_(p, r, 1.0f);
   int ni = int(n);
-  if (ni > 127) {
-    p = p * 2.0f;
-    ni -= 1;
-  }
-  if (ni < -126) {
-    p = p * u2f(uint32_t(ni + 64 + 127) << 23);
-    return p * 5.42101086242752217004e-20f;  // 2^-64
-  }
-  return p * u2f(uint32_t(ni + 127) << 23);
+  const bool big = ni > 127;
+  p = big ? p * 2.0f : p;
+  ni = big ? ni - 1 : ni;
+  const float lo = (p * u2f(uint32_t(ni + 64 + 127) << 23)) * 5.42101086242752217004e-20f;  // 2^-64
+  const float hi = p * u2f(uint32_t(ni + 127) << 23);
+  float res = ni < -126 ? lo : hi;
+  res = x > 88.72283935546875f ? u2f(0x7f800000u) : res;
+  res = x < -103.972084045410156f ? 0.0f : res;
+  return x != x ? x : res;
 }
 
 // bf16 logistic function with MLX's per-operation bf16 rounding
