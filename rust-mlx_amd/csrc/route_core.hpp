@@ -17,18 +17,23 @@ __device__ __forceinline__ uint32_t dpp(uint32_t v) {
   return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), CTRL, 0xF, 0xF, false));
 }
 
-// Wave-wide maxima through DPP row permutes (VALU, no LDS round trip) and one
-// read of each 16-lane row's result; a maximum is the same in any order.
+// DPP with a row mask: rows outside ROWS keep v.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp_rows(uint32_t v) {
+  return uint32_t(__builtin_amdgcn_update_dpp(int(v), int(v), CTRL, ROWS, 0xF, false));
+}
+
+// Wave-wide maxima in VALU (no LDS round trip): within rows by quad and
+// mirror permutes, across rows by row_bcast:15 and row_bcast:31, then one read
+// of lane 63; a maximum is the same in any order.
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-  v = max(v, dpp<0xB1>(v));   // quad_perm [1,0,3,2]
-  v = max(v, dpp<0x4E>(v));   // quad_perm [2,3,0,1]
-  v = max(v, dpp<0x141>(v));  // row_half_mirror
-  v = max(v, dpp<0x140>(v));  // row_mirror: every lane of a row holds its max
-  const uint32_t r0 = uint32_t(__builtin_amdgcn_readlane(int(v), 0));
-  const uint32_t r1 = uint32_t(__builtin_amdgcn_readlane(int(v), 16));
-  const uint32_t r2 = uint32_t(__builtin_amdgcn_readlane(int(v), 32));
-  const uint32_t r3 = uint32_t(__builtin_amdgcn_readlane(int(v), 48));
-  return max(max(r0, r1), max(r2, r3));
+  v = max(v, dpp<0xB1>(v));             // quad_perm [1,0,3,2]
+  v = max(v, dpp<0x4E>(v));             // quad_perm [2,3,0,1]
+  v = max(v, dpp<0x141>(v));            // row_half_mirror
+  v = max(v, dpp<0x140>(v));            // row_mirror: every lane of a row holds its max
+  v = max(v, dpp_rows<0x142, 0xA>(v));  // row_bcast:15 into rows 1, 3
+  v = max(v, dpp_rows<0x143, 0xC>(v));  // row_bcast:31 into rows 2, 3
+  return uint32_t(__builtin_amdgcn_readlane(int(v), 63));
 }
 
 // Largest of the lanes' values under `b > a ? b : a` (any order gives the
@@ -39,11 +44,33 @@ __device__ __forceinline__ float wave_max_f32(float x) {
   x = mx2(x, __uint_as_float(dpp<0x4E>(__float_as_uint(x))));
   x = mx2(x, __uint_as_float(dpp<0x141>(__float_as_uint(x))));
   x = mx2(x, __uint_as_float(dpp<0x140>(__float_as_uint(x))));
-  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
-  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
-  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
-  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
-  return mx2(mx2(r0, r1), mx2(r2, r3));
+  x = mx2(x, __uint_as_float(dpp_rows<0x142, 0xA>(__float_as_uint(x))));
+  x = mx2(x, __uint_as_float(dpp_rows<0x143, 0xC>(__float_as_uint(x))));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+}
+
+// The xor-butterfly wave sum (levels 32, 16, 8, 4, 2, 1; each lane adds its
+// partner's value) with the butterfly's own tree, in VALU: levels 32 and 16
+// by lane swaps, 8 by row_ror:8 (= xor 8 within a row), 4 by row_ror:4 (after
+// level 8, lanes l and l ^ 8 hold equal values, so lane (l + 4) mod 16 holds
+// what lane l ^ 4 holds), 2 and 1 by quad permutes.  Addition is commutative,
+// so every lane gets the bits of the shuffle form.
+__device__ __forceinline__ float wave_sum_xor(float s) {
+  {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false,
+                                                    false);
+    s = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  }
+  {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(s), __float_as_uint(s), false,
+                                                    false);
+    s = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  }
+  s = s + __uint_as_float(dpp<0x128>(__float_as_uint(s)));  // row_ror:8
+  s = s + __uint_as_float(dpp<0x124>(__float_as_uint(s)));  // row_ror:4
+  s = s + __uint_as_float(dpp<0x4E>(__float_as_uint(s)));   // quad_perm [2,3,0,1]
+  s = s + __uint_as_float(dpp<0xB1>(__float_as_uint(s)));   // quad_perm [1,0,3,2]
+  return s;
 }
 
 struct RouteLane {
@@ -71,7 +98,7 @@ __device__ __forceinline__ RouteLane route_row(const uint16_t* __restrict__ logi
     sum = sum + v[i];
   }
   // the softmax total: xor butterfly (its order fixes the bits)
-  for (int o = 32; o > 0; o >>= 1) sum = sum + __shfl_xor(sum, o, 64);
+  sum = wave_sum_xor(sum);
   const float inv = 1.0f / sum;
   uint32_t key[PER];
 #pragma unroll
