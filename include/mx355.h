@@ -99,9 +99,17 @@ typedef struct mx_model_config {
   int32_t mixed_bits;  /* nonzero: per-layer bits drawn from {4,5,6,8} by seed (config 4) */
   int32_t max_slots, max_context, max_verify;
   uint64_t seed;
+  int32_t mtp;         /* nonzero: one MTP draft layer for speculative generation (config 4) */
 } mx_model_config;
 
 typedef struct mx_engine mx_engine;
+
+/* Speculative generation counters (mx_engine_generate). */
+typedef struct mx_generate_stats {
+  int32_t rounds;    /* verify blocks run */
+  int32_t drafted;   /* draft tokens proposed */
+  int32_t accepted;  /* draft tokens accepted */
+} mx_generate_stats;
 
 /* What one profiled decode step measured (HIP events on the engine stream)
  * and its algorithmic HBM bytes (each distinct weight, state and KV byte once). */
@@ -444,6 +452,23 @@ mx_status mx_engine_prefill(mx_engine* e, int32_t slot, const uint32_t* tokens, 
 mx_status mx_engine_verify(mx_engine* e, int32_t slot, const uint32_t* tokens, int32_t count,
                            uint32_t* argmax);
 mx_status mx_engine_commit(mx_engine* e, int32_t slot, int32_t keep);
+/* Greedy generation from an empty slot: prefill `prompt`, then emit up to
+ * `max_tokens` tokens (the first is the prefill's greedy token).  depth 0:
+ * one decode step per token.  depth 1..min(7, max_verify - 1): MTP
+ * speculation (the model needs mtp = 1): the draft layer proposes `depth`
+ * tokens, a verify block accepts the matching prefix plus the target's next
+ * token, and the draft layer is resynchronised on the target's hidden states;
+ * the tokens equal the depth-0 ones wherever verify and decode agree (always
+ * in exact mode).  Replaces speculative::generate_prepared
+ * (src/speculative.rs:225-483) with the draft model Mtp::forward
+ * (src/mtp.rs:72-127), default policies (full-vocabulary greedy draft head,
+ * fixed depth, no EOS).  drafts (optional, max_tokens * depth entries): every
+ * round's drafted tokens in order (stats->drafted of them), like the
+ * reference's recorded draft tokens. */
+mx_status mx_engine_generate(mx_engine* e, int32_t slot, const uint32_t* prompt,
+                             int32_t n_prompt, int32_t max_tokens, int32_t depth,
+                             uint32_t* tokens, int32_t* n_tokens, mx_generate_stats* stats,
+                             uint32_t* drafts);
 /* Test/inspection hooks: flags (bit 0: also write bf16 logits of each step;
  * bit 1: run eagerly instead of replaying captured HIP graphs; bit 2: exact
  * mode, every projection on the fixed-order kernels that the CPU oracle

@@ -55,34 +55,28 @@ class Model:
         self.layers = []
         self.layer_ids = list(range(c["layers"])) if only_layers is None else list(only_layers)
         for i in self.layer_ids:
-            p = f"layers.{i}"
-            L = {"attn_hc": self._hc(p + ".attn_hc", i, True), "mlp_hc": self._hc(p + ".mlp_hc", i, True)}
-            bits, dbits = self.layer_bits(i)
-            if not self.attn[i]:
-                L["in"] = self._qw(p + ".gdn.in", self.P, H, bits)
-                L["conv_w"] = fetch(p + ".gdn.conv_w", np.float32, (c["conv_k"], self.cd))
-                L["a_log"] = fetch(p + ".gdn.a_log", np.float32, (c["gdn_hv"],))
-                L["dt"] = fetch(p + ".gdn.dt_bias", np.uint16, (c["gdn_hv"],))
-                L["norm"] = fetch(p + ".gdn.norm", np.uint16, (128,))
-                L["out"] = self._qw(p + ".gdn.out", H, self.vd, bits)
-            else:
-                L["in"] = self._qw(p + ".attn.in", self.Q, H, bits)
-                L["q_norm"] = fetch(p + ".attn.q_norm", np.uint16, (c["head_dim"],))
-                L["k_norm"] = fetch(p + ".attn.k_norm", np.uint16, (c["head_dim"],))
-                L["out"] = self._qw(p + ".attn.out", H, c["heads"] * c["head_dim"], bits)
-            E, I, SI = c["experts"], c["moe_inter"], c["shared_inter"]
-            L["router"] = self._qw(p + ".moe.router", E + 1, H, bits)
-            L["gate"] = self._bank(p + ".moe.gate", E, I, H, bits)
-            L["up"] = self._bank(p + ".moe.up", E, I, H, bits)
-            L["down"] = self._bank(p + ".moe.down", E, H, I, dbits)
-            L["sgate"] = self._qw(p + ".moe.shared_gate", SI, H, bits)
-            L["sup"] = self._qw(p + ".moe.shared_up", SI, H, bits)
-            L["sdown"] = self._qw(p + ".moe.shared_down", H, SI, dbits)
-            self.layers.append(L)
+            self.layers.append(self._load_layer(f"layers.{i}", i, self.attn[i]))
+        # the MTP draft layer (src/mtp.rs:39-70): its tensors are drawn as layer
+        # index `layers`; its KV plane follows the model's attention layers
+        self.mtp = None
+        if c.get("mtp"):
+            m = c["layers"]
+            bits = self.layer_bits(m)[0]
+            self.mtp = {
+                "layer": self._load_layer("mtp.layer", m, True),
+                "norm_emb": fetch("mtp.norm_emb", np.uint16, (H,)),
+                "norm_hid": fetch("mtp.norm_hidden", np.uint16, (hc * H,)),
+                "fc_emb": self._qw("mtp.fc_emb", H, H, bits),
+                "fc_hid": self._qw("mtp.fc_hidden", H, H, bits),
+                "mixer": self._hc("mtp.mixer", m, False),
+                "cache": self.n_attn,
+            }
+            self._keep += [self.mtp["norm_emb"], self.mtp["norm_hid"]]
+        self.n_kv = self.n_attn + (1 if self.mtp is not None else 0)
         S = c["max_slots"]
         self.state = np.zeros((S * self.n_gdn, c["gdn_hv"], 128, 128), np.float32)
         self.conv = np.zeros((S * self.n_gdn, c["conv_k"] - 1, self.cd), np.uint16)
-        self.kv_slot_stride = self.n_attn * c["kv_heads"] * c["max_context"] * c["head_dim"]
+        self.kv_slot_stride = self.n_kv * c["kv_heads"] * c["max_context"] * c["head_dim"]
         self.k = np.zeros(S * self.kv_slot_stride, np.uint16)
         self.v = np.zeros(S * self.kv_slot_stride, np.uint16)
         self.offsets = [0] * S
@@ -98,6 +92,32 @@ class Model:
         choices = (4, 5, 6, 8)
         key = (self.c["seed"] ^ 0x5BD1E995) & (2**64 - 1)
         return tuple(choices[orc.lib.mxo_rng_u64(key, i * 2 + w) & 3] for w in (0, 1))
+
+    def _load_layer(self, p, i, attn):
+        c, H, fetch = self.c, self.H, self.fetch
+        L = {"attn_hc": self._hc(p + ".attn_hc", i, True), "mlp_hc": self._hc(p + ".mlp_hc", i, True)}
+        bits, dbits = self.layer_bits(i)
+        if not attn:
+            L["in"] = self._qw(p + ".gdn.in", self.P, H, bits)
+            L["conv_w"] = fetch(p + ".gdn.conv_w", np.float32, (c["conv_k"], self.cd))
+            L["a_log"] = fetch(p + ".gdn.a_log", np.float32, (c["gdn_hv"],))
+            L["dt"] = fetch(p + ".gdn.dt_bias", np.uint16, (c["gdn_hv"],))
+            L["norm"] = fetch(p + ".gdn.norm", np.uint16, (128,))
+            L["out"] = self._qw(p + ".gdn.out", H, self.vd, bits)
+        else:
+            L["in"] = self._qw(p + ".attn.in", self.Q, H, bits)
+            L["q_norm"] = fetch(p + ".attn.q_norm", np.uint16, (c["head_dim"],))
+            L["k_norm"] = fetch(p + ".attn.k_norm", np.uint16, (c["head_dim"],))
+            L["out"] = self._qw(p + ".attn.out", H, c["heads"] * c["head_dim"], bits)
+        E, I, SI = c["experts"], c["moe_inter"], c["shared_inter"]
+        L["router"] = self._qw(p + ".moe.router", E + 1, H, bits)
+        L["gate"] = self._bank(p + ".moe.gate", E, I, H, bits)
+        L["up"] = self._bank(p + ".moe.up", E, I, H, bits)
+        L["down"] = self._bank(p + ".moe.down", E, H, I, dbits)
+        L["sgate"] = self._qw(p + ".moe.shared_gate", SI, H, bits)
+        L["sup"] = self._qw(p + ".moe.shared_up", SI, H, bits)
+        L["sdown"] = self._qw(p + ".moe.shared_down", H, SI, dbits)
+        return L
 
     def _qw(self, name, n, k, bits):
         gs = self.c["group_size"]
@@ -142,6 +162,66 @@ class Model:
         orc.lib.mxo_qmv(w.codes, w.scales, w.biases, w.n, w.k, w.bits, w.gs, _p(x), x.shape[0], _p(y))
         return y
 
+    def _run_layer(self, L, attn, ci, h, rows, slots_a, pos_a, gdn_slots, groups, t, history):
+        """One layer (GDN or attention sublayer, then the MoE sublayer) on the
+        hc streams h; ci: the layer's GDN or attention cache index."""
+        c = self.c
+        H, hc = self.H, self.hc
+        mixed, inj = self._hc_forward(L["attn_hc"], h, rows)
+        if not attn:
+            gi = ci
+            proj = self._qmv(L["in"], mixed)
+            qkv = np.ascontiguousarray(proj[:, :self.cd])
+            sl = gdn_slots + gi
+            conv_out = np.empty((rows, self.cd), np.uint16)
+            win = np.empty((groups, c["conv_k"] - 1 + t, self.cd), np.uint16) if history is not None else None
+            orc.lib.mxo_gdn_conv(_p(qkv), self.cd, groups, t, _p(sl), _p(self.conv), _p(L["conv_w"]),
+                                 self.cd, c["conv_k"], _p(conv_out), self.cd,
+                                 _p(win) if win is not None else None)
+            zab = np.ascontiguousarray(proj[:, self.cd:])
+            zp = zab.ctypes.data
+            hist = np.empty((rows, c["gdn_hv"], 128, 128), np.float32) if history is not None else None
+            y = np.empty((rows, self.vd), np.uint16)
+            orc.lib.mxo_gdn_recurrence(_p(conv_out), self.cd, zp, zp + 2 * self.vd,
+                                       zp + 2 * (self.vd + c["gdn_hv"]), zab.shape[1], _p(L["a_log"]),
+                                       _p(L["dt"]), _p(L["norm"]), c["rms_eps"], c["gdn_hk"],
+                                       c["gdn_hv"], groups, t, _p(sl), _p(self.state),
+                                       _p(hist) if hist is not None else None, _p(y))
+            if history is not None:
+                history.append((gi, hist, win))
+            orc.lib.mxo_hc_write(C.byref(L["out"]), _p(y), rows, hc, _p(h), _p(inj))
+        else:
+            ai = ci
+            qkv = self._qmv(L["in"], mixed)
+            layer_off = ai * c["kv_heads"] * c["max_context"] * c["head_dim"]
+            kview = self.k[layer_off:]
+            vview = self.v[layer_off:]
+            q = np.empty((rows, c["heads"] * c["head_dim"]), np.uint16)
+            orc.lib.mxo_attn_prep(_p(qkv), self.Q, rows, _p(slots_a), _p(pos_a), _p(L["q_norm"]),
+                                  _p(L["k_norm"]), c["rms_eps"], _p(self.cos), _p(self.sin),
+                                  c["heads"], c["kv_heads"], c["head_dim"], c["rotary_dim"],
+                                  c["max_context"], self.kv_slot_stride, _p(q), kview.ctypes.data,
+                                  vview.ctypes.data)
+            y = np.empty((rows, c["heads"] * c["head_dim"]), np.uint16)
+            orc.lib.mxo_attention(_p(q), _p(qkv), self.Q, rows, _p(slots_a), _p(pos_a),
+                                  kview.ctypes.data, vview.ctypes.data, c["heads"], c["kv_heads"],
+                                  c["head_dim"], c["max_context"], self.kv_slot_stride, _p(y))
+            orc.lib.mxo_hc_write(C.byref(L["out"]), _p(y), rows, hc, _p(h), _p(inj))
+        mixed, inj = self._hc_forward(L["mlp_hc"], h, rows)
+        logits = self._qmv(L["router"], mixed)
+        E = c["experts"]
+        ids, scores, factor = orc.moe_route(np.ascontiguousarray(logits[:, :E]),
+                                            np.ascontiguousarray(logits[:, E]), c["top_k"])
+        self.last_ids.append(ids.copy())
+        pbuf = np.empty((rows, c["top_k"] + 1, H), np.uint16)
+        orc.lib.mxo_moe_experts(_p(mixed), _p(ids), _p(scores), rows, c["top_k"], C.byref(L["gate"]),
+                                C.byref(L["up"]), C.byref(L["down"]), C.byref(L["sgate"]),
+                                C.byref(L["sup"]), C.byref(L["sdown"]), _p(pbuf))
+        routed = orc.moe_reduce(pbuf, c["top_k"])
+        shared = np.ascontiguousarray(pbuf[:, c["top_k"], :])
+        h = orc.moe_hc_epilogue(routed, shared, factor, h, inj, hc)
+        return h
+
     def step(self, tokens, slots, pos, groups, t, history=None):
         self.last_ids = []  # routing of each MoE layer in this step (test inspection)
         """One engine step over rows (slot, position); GDN rows grouped as
@@ -156,63 +236,104 @@ class Model:
         pos_a = np.ascontiguousarray(pos, np.int32)
         gdn_slots = np.array([slots[g * t] * self.n_gdn for g in range(groups)], np.int32)
         for i, L in zip(self.layer_ids, self.layers):
-            mixed, inj = self._hc_forward(L["attn_hc"], h, rows)
-            if not self.attn[i]:
-                gi = self.cache_index[i]
-                proj = self._qmv(L["in"], mixed)
-                qkv = np.ascontiguousarray(proj[:, :self.cd])
-                sl = gdn_slots + gi
-                conv_out = np.empty((rows, self.cd), np.uint16)
-                win = np.empty((groups, c["conv_k"] - 1 + t, self.cd), np.uint16) if history is not None else None
-                orc.lib.mxo_gdn_conv(_p(qkv), self.cd, groups, t, _p(sl), _p(self.conv), _p(L["conv_w"]),
-                                     self.cd, c["conv_k"], _p(conv_out), self.cd,
-                                     _p(win) if win is not None else None)
-                zab = np.ascontiguousarray(proj[:, self.cd:])
-                zp = zab.ctypes.data
-                hist = np.empty((rows, c["gdn_hv"], 128, 128), np.float32) if history is not None else None
-                y = np.empty((rows, self.vd), np.uint16)
-                orc.lib.mxo_gdn_recurrence(_p(conv_out), self.cd, zp, zp + 2 * self.vd,
-                                           zp + 2 * (self.vd + c["gdn_hv"]), zab.shape[1], _p(L["a_log"]),
-                                           _p(L["dt"]), _p(L["norm"]), c["rms_eps"], c["gdn_hk"],
-                                           c["gdn_hv"], groups, t, _p(sl), _p(self.state),
-                                           _p(hist) if hist is not None else None, _p(y))
-                if history is not None:
-                    history.append((gi, hist, win))
-                orc.lib.mxo_hc_write(C.byref(L["out"]), _p(y), rows, hc, _p(h), _p(inj))
-            else:
-                ai = self.cache_index[i]
-                qkv = self._qmv(L["in"], mixed)
-                layer_off = ai * c["kv_heads"] * c["max_context"] * c["head_dim"]
-                kview = self.k[layer_off:]
-                vview = self.v[layer_off:]
-                q = np.empty((rows, c["heads"] * c["head_dim"]), np.uint16)
-                orc.lib.mxo_attn_prep(_p(qkv), self.Q, rows, _p(slots_a), _p(pos_a), _p(L["q_norm"]),
-                                      _p(L["k_norm"]), c["rms_eps"], _p(self.cos), _p(self.sin),
-                                      c["heads"], c["kv_heads"], c["head_dim"], c["rotary_dim"],
-                                      c["max_context"], self.kv_slot_stride, _p(q), kview.ctypes.data,
-                                      vview.ctypes.data)
-                y = np.empty((rows, c["heads"] * c["head_dim"]), np.uint16)
-                orc.lib.mxo_attention(_p(q), _p(qkv), self.Q, rows, _p(slots_a), _p(pos_a),
-                                      kview.ctypes.data, vview.ctypes.data, c["heads"], c["kv_heads"],
-                                      c["head_dim"], c["max_context"], self.kv_slot_stride, _p(y))
-                orc.lib.mxo_hc_write(C.byref(L["out"]), _p(y), rows, hc, _p(h), _p(inj))
-            mixed, inj = self._hc_forward(L["mlp_hc"], h, rows)
-            logits = self._qmv(L["router"], mixed)
-            E = c["experts"]
-            ids, scores, factor = orc.moe_route(np.ascontiguousarray(logits[:, :E]),
-                                                np.ascontiguousarray(logits[:, E]), c["top_k"])
-            self.last_ids.append(ids.copy())
-            pbuf = np.empty((rows, c["top_k"] + 1, H), np.uint16)
-            orc.lib.mxo_moe_experts(_p(mixed), _p(ids), _p(scores), rows, c["top_k"], C.byref(L["gate"]),
-                                    C.byref(L["up"]), C.byref(L["down"]), C.byref(L["sgate"]),
-                                    C.byref(L["sup"]), C.byref(L["sdown"]), _p(pbuf))
-            routed = orc.moe_reduce(pbuf, c["top_k"])
-            shared = np.ascontiguousarray(pbuf[:, c["top_k"], :])
-            h = orc.moe_hc_epilogue(routed, shared, factor, h, inj, hc)
+            h = self._run_layer(L, self.attn[i], self.cache_index[i], h, rows, slots_a, pos_a,
+                                gdn_slots, groups, t, history)
         self.hidden = h.copy()
         mixed, _ = self._hc_forward(self.mixer, h, rows)
         self.last_mixed = mixed
         return orc.head_argmax(self.head, mixed)
+
+    def mtp_step(self, slot, tokens, pos0, prev):
+        """Mtp::forward (src/mtp.rs:72-127) over rows of one slot: token r is the
+        token after MTP position pos0 + r, prev the previous hidden streams
+        [rows, hc*H].  Returns the draft tokens; self.mtp_hidden holds the new
+        hidden streams.  Both norms are compiled::norm (src/compiled.rs:22-28)
+        in the hyper-connection norm's order, over H and over all hc*H values."""
+        c, m = self.c, self.mtp
+        H, hc = self.H, self.hc
+        rows = len(tokens)
+        self.last_ids = []
+        tok = np.ascontiguousarray(tokens, np.uint32)
+        emb = np.empty((rows, H), np.uint16)
+        orc.lib.mxo_embed(C.byref(self.embed), _p(tok), rows, 1, _p(emb))
+        a = np.empty_like(emb)
+        orc.lib.mxo_hc_norm(_p(emb), _p(m["norm_emb"]), rows, 1, H, c["rms_eps"], _p(a))
+        e = self._qmv(m["fc_emb"], a)
+        prev = np.ascontiguousarray(prev, np.uint16).reshape(rows, hc * H)
+        hn = np.empty_like(prev)
+        orc.lib.mxo_hc_norm(_p(prev), _p(m["norm_hid"]), rows, 1, hc * H, c["rms_eps"], _p(hn))
+        f = self._qmv(m["fc_hid"], hn.reshape(rows * hc, H))
+        s32 = orc.bf16_to_f32(e).astype(np.float32)[:, None, :] + \
+            orc.bf16_to_f32(f).astype(np.float32).reshape(rows, hc, H)
+        h = orc.f32_to_bf16(s32.astype(np.float32)).reshape(rows, hc * H)
+        slots_a = np.full(rows, slot, np.int32)
+        pos_a = np.arange(pos0, pos0 + rows, dtype=np.int32)
+        gdn_slots = np.array([slot * self.n_gdn], np.int32)
+        h = self._run_layer(m["layer"], True, m["cache"], h, rows, slots_a, pos_a, gdn_slots, 1,
+                            rows, None)
+        self.mtp_hidden = h.copy()
+        mixed, _ = self._hc_forward(m["mixer"], h, rows)
+        return orc.head_argmax(self.head, mixed)
+
+    def generate(self, slot, prompt, max_tokens, depth=0):
+        """mx_engine_generate's contract (speculative::generate_prepared,
+        src/speculative.rs:225-483, default policies): returns (tokens, stats)."""
+        assert self.offsets[slot] == 0
+        n = len(prompt)
+        stats = {"rounds": 0, "drafted": 0, "accepted": 0, "drafts": []}
+        bonus = seed = dh = None
+        for a in range(0, n, 8):
+            chunk = [int(x) for x in prompt[a:a + 8]]
+            nxt = self.block(slot, chunk)
+            bonus = int(nxt[-1])
+            if depth > 0:
+                toks = [int(prompt[a + r + 1]) if a + r + 1 < n else bonus for r in range(len(chunk))]
+                d = self.mtp_step(slot, toks, a, self.hidden.copy())
+                seed = int(d[-1])
+                dh = self.mtp_hidden[-1:].copy()
+        out = [bonus]
+        if depth == 0:
+            while len(out) < max_tokens:
+                out.append(int(self.decode_rows([slot], [out[-1]])[0]))
+            return out, stats
+        mtp_len = n
+        while len(out) < max_tokens:
+            k = min(depth, max_tokens - len(out))
+            drafted = [seed]
+            base = mtp_len
+            for i in range(1, k):
+                d = self.mtp_step(slot, [drafted[i - 1]], base + i - 1, dh)
+                drafted.append(int(d[0]))
+                dh = self.mtp_hidden[-1:].copy()
+            stats["drafts"] += drafted
+            pred = [int(x) for x in self.verify(slot, [bonus] + drafted)]
+            vh = self.hidden.copy()
+            accepted = 0
+            while accepted < k and drafted[accepted] == pred[accepted]:
+                accepted += 1
+            nxt = pred[accepted]
+            emitted_now, ending = 0, False
+            for i in range(accepted + 1):
+                if len(out) == max_tokens:
+                    ending = True
+                    break
+                out.append(drafted[i] if i < accepted else nxt)
+                emitted_now += 1
+            self.commit(slot, (min(emitted_now, accepted) + 1) if ending else accepted + 1)
+            stats["rounds"] += 1
+            stats["drafted"] += k
+            stats["accepted"] += accepted
+            if ending or len(out) == max_tokens:
+                break
+            bonus = nxt
+            kept = min(accepted, k - 1)
+            mtp_len = base + kept
+            toks = drafted[kept:accepted] + [nxt]
+            d = self.mtp_step(slot, toks, mtp_len, vh[kept:accepted + 1])
+            seed = int(d[-1])
+            dh = self.mtp_hidden[-1:].copy()
+            mtp_len += len(toks)
+        return out, stats
 
     # ---- engine-level operations (same contracts as the C ABI) ----
     def decode_rows(self, slots, tokens):

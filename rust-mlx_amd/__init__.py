@@ -75,7 +75,11 @@ class ModelConfigC(C.Structure):
         ("rope_theta", C.c_float), ("rms_eps", C.c_float)] + [(n, C.c_int32) for n in (
             "experts", "top_k", "moe_inter", "shared_inter", "bits", "down_bits", "embed_bits",
             "head_bits", "group_size", "mixed_bits", "max_slots", "max_context", "max_verify")] + [
-        ("seed", C.c_uint64)]
+        ("seed", C.c_uint64), ("mtp", C.c_int32)]
+
+
+class GenerateStatsC(C.Structure):
+    _fields_ = [("rounds", C.c_int32), ("drafted", C.c_int32), ("accepted", C.c_int32)]
 
 
 class StepProfileC(C.Structure):
@@ -178,6 +182,8 @@ def _load() -> C.CDLL:
         "mx_engine_prefill": ([vp, i32, vp, i32, vp], i32),
         "mx_engine_verify": ([vp, i32, vp, i32, vp], i32),
         "mx_engine_commit": ([vp, i32, i32], i32),
+        "mx_engine_generate": ([vp, i32, vp, i32, i32, i32, vp, vp, C.POINTER(GenerateStatsC), vp],
+                               i32),
         "mx_engine_set_flags": ([vp, i32], i32),
         "mx_engine_fill_slot": ([vp, i32, i32, u64], i32),
         "mx_qmm": ([C.POINTER(QWeightC), vp, i32, vp, vp], i32),
@@ -418,6 +424,20 @@ class Engine:
 
     def commit(self, slot, keep):
         check(lib.mx_engine_commit(self.h, slot, keep))
+
+    def generate(self, slot, prompt, max_tokens, depth=0):
+        """Greedy generation from an empty slot (mx_engine_generate): returns
+        (tokens, {"rounds", "drafted", "accepted", "drafts"})."""
+        t = self._u32(prompt)
+        out = np.empty(max_tokens, np.uint32)
+        n = C.c_int32(0)
+        st = GenerateStatsC()
+        drafts = np.empty(max(max_tokens * depth, 1), np.uint32)
+        check(lib.mx_engine_generate(self.h, slot, t.ctypes.data, len(t), max_tokens, depth,
+                                     out.ctypes.data, C.byref(n), C.byref(st), drafts.ctypes.data))
+        return out[:n.value].copy(), {"rounds": st.rounds, "drafted": st.drafted,
+                                      "accepted": st.accepted,
+                                      "drafts": drafts[:st.drafted].copy()}
 
     def reset(self, slot):
         check(lib.mx_engine_reset_slot(self.h, slot))

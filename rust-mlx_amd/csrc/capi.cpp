@@ -630,6 +630,23 @@ MX_ABI mx_status mx_engine_verify(mx_engine* e, int32_t slot, const uint32_t* to
                        "mx_engine_verify");
 }
 
+MX_ABI mx_status mx_engine_generate(mx_engine* e, int32_t slot, const uint32_t* prompt,
+                                    int32_t n_prompt, int32_t max_tokens, int32_t depth,
+                                    uint32_t* tokens, int32_t* n_tokens,
+                                    mx_generate_stats* stats, uint32_t* drafts) {
+  MX_CHECK(e && prompt && tokens && n_tokens, MX_EINVAL, "mx_engine_generate: null pointer");
+  MX_CHECK(slot_ok(*e->impl, slot), MX_EINVAL, "mx_engine_generate: slot out of range");
+  for (int32_t i = 0; i < n_prompt; ++i)
+    MX_CHECK(prompt[i] < uint32_t(engine_config(*e->impl).vocab), MX_EINVAL,
+             "mx_engine_generate: token outside vocabulary");
+  std::string err;
+  int n = 0;
+  const int rc = engine_generate(*e->impl, slot, prompt, n_prompt, max_tokens, depth, tokens, &n,
+                                 stats, drafts, &err);
+  *n_tokens = n;
+  return engine_status(rc, err, "mx_engine_generate");
+}
+
 MX_ABI mx_status mx_engine_commit(mx_engine* e, int32_t slot, int32_t keep) {
   MX_CHECK(e && slot_ok(*e->impl, slot), MX_EINVAL, "mx_engine_commit: bad engine or slot");
   std::string err;

@@ -81,6 +81,20 @@ struct Engine {
   QWeight embed{}, head{};
   HcW mixer;
   int n_gdn = 0, n_attn = 0;
+  int n_kv = 0;  // attention cache planes per slot: n_attn (+ 1 for the MTP layer)
+  // MTP draft layer (src/mtp.rs:10-127): norms, the two input projections,
+  // one attention + MoE layer with hyper-connections, and its mixer
+  struct Mtp {
+    uint16_t* norm_emb = nullptr;  // [H]
+    uint16_t* norm_hid = nullptr;  // [hc * H]
+    QWeight fc_emb{}, fc_hid{};    // [H, H]
+    LayerW layer;
+    HcW mixer;
+  } mtp;
+  bool has_mtp = false;
+  uint16_t *mtp_emb = nullptr, *mtp_a = nullptr, *mtp_e = nullptr;   // [8][H]
+  uint16_t *mtp_prev = nullptr, *mtp_hn = nullptr, *mtp_f = nullptr;  // [8][hc H]
+  uint16_t* mtp_dh = nullptr;                                          // [hc H]
   // dims
   int H = 0, cd = 0, vd = 0, P = 0, Q = 0, max_chunks = 0;
   GdnDims gd{};
@@ -247,31 +261,11 @@ int make_hc(Engine& e, const std::string& p, int layer, int id0, bool inject, Hc
   return MX_OK;
 }
 
-int build(Engine& e) {
+// One layer's tensors (p: name prefix, i: layer index of the draws).
+int make_layer(Engine& e, const std::string& p, int i, LayerW* out) {
   const auto& c = e.cfg;
-  e.H = c.hidden;
-  e.gd = GdnDims{c.gdn_hk, c.gdn_hv, c.gdn_dk, c.gdn_dv, c.conv_k};
-  e.cd = 2 * c.gdn_hk * c.gdn_dk + c.gdn_hv * c.gdn_dv;
-  e.vd = c.gdn_hv * c.gdn_dv;
-  e.P = e.cd + e.vd + 2 * c.gdn_hv;
-  e.Q = c.heads * 2 * c.head_dim + 2 * c.kv_heads * c.head_dim;
-  e.max_chunks = (c.max_context + kAttnFastChunk - 1) / kAttnFastChunk;
-  for (int i = 0; i < c.layers; ++i) {
-    LayerW L;
-    L.attn = (i % c.attn_every) == c.attn_every - 1;
-    L.cache_index = L.attn ? e.n_attn++ : e.n_gdn++;
-    e.layers.push_back(L);
-  }
-  const int64_t attn_slot_stride = int64_t(e.n_attn) * c.kv_heads * c.max_context * c.head_dim;
-  e.ad = AttnDims{c.heads, c.kv_heads, c.head_dim, c.rotary_dim, c.max_context, attn_slot_stride};
-
-  // ---- weights ----
-  MX_TRY(make_qw(e, "embed", c.vocab, c.hidden, c.embed_bits, -1, 1, &e.embed));
-  MX_TRY(make_qw(e, "head", c.vocab, c.hidden, c.head_bits, -1, 2, &e.head));
-  MX_TRY(make_hc(e, "mixer", -1, 3, false, &e.mixer));
-  for (int i = 0; i < c.layers; ++i) {
-    LayerW& L = e.layers[i];
-    const std::string p = "layers." + std::to_string(i);
+  LayerW& L = *out;
+  {
     const int bits = layer_bits(c, i, 0);
     const int dbits = layer_bits(c, i, 1);
     MX_TRY(make_hc(e, p + ".attn_hc", i, 1, true, &L.attn_hc));
@@ -298,6 +292,51 @@ int build(Engine& e) {
     MX_TRY(make_qw(e, p + ".moe.shared_gate", c.shared_inter, c.hidden, bits, i, 17, &L.sgate));
     MX_TRY(make_qw(e, p + ".moe.shared_up", c.shared_inter, c.hidden, bits, i, 18, &L.sup));
     MX_TRY(make_qw(e, p + ".moe.shared_down", c.hidden, c.shared_inter, dbits, i, 19, &L.sdown));
+  }
+  return MX_OK;
+}
+
+int build(Engine& e) {
+  const auto& c = e.cfg;
+  e.H = c.hidden;
+  e.gd = GdnDims{c.gdn_hk, c.gdn_hv, c.gdn_dk, c.gdn_dv, c.conv_k};
+  e.cd = 2 * c.gdn_hk * c.gdn_dk + c.gdn_hv * c.gdn_dv;
+  e.vd = c.gdn_hv * c.gdn_dv;
+  e.P = e.cd + e.vd + 2 * c.gdn_hv;
+  e.Q = c.heads * 2 * c.head_dim + 2 * c.kv_heads * c.head_dim;
+  e.max_chunks = (c.max_context + kAttnFastChunk - 1) / kAttnFastChunk;
+  for (int i = 0; i < c.layers; ++i) {
+    LayerW L;
+    L.attn = (i % c.attn_every) == c.attn_every - 1;
+    L.cache_index = L.attn ? e.n_attn++ : e.n_gdn++;
+    e.layers.push_back(L);
+  }
+  e.n_kv = e.n_attn + (c.mtp ? 1 : 0);
+  const int64_t attn_slot_stride = int64_t(e.n_kv) * c.kv_heads * c.max_context * c.head_dim;
+  e.ad = AttnDims{c.heads, c.kv_heads, c.head_dim, c.rotary_dim, c.max_context, attn_slot_stride};
+
+  // ---- weights ----
+  MX_TRY(make_qw(e, "embed", c.vocab, c.hidden, c.embed_bits, -1, 1, &e.embed));
+  MX_TRY(make_qw(e, "head", c.vocab, c.hidden, c.head_bits, -1, 2, &e.head));
+  MX_TRY(make_hc(e, "mixer", -1, 3, false, &e.mixer));
+  for (int i = 0; i < c.layers; ++i)
+    MX_TRY(make_layer(e, "layers." + std::to_string(i), i, &e.layers[i]));
+  if (c.mtp) {
+    // the MTP layer draws its tensors as layer index `layers`
+    // (mtp.rs:39-70: pre_fc_norm_embedding / _hidden, fc_embedding / _hidden,
+    // one attention layer with its two hyper-connections, the mixer)
+    const int m = c.layers;
+    const int bits = layer_bits(c, m, 0);
+    e.has_mtp = true;
+    e.mtp.layer.attn = true;
+    e.mtp.layer.cache_index = e.n_attn;  // the plane after the model's attention layers
+    MX_TRY(make_layer(e, "mtp.layer", m, &e.mtp.layer));
+    MX_TRY(make_bf16(e, "mtp.norm_emb", c.hidden, m, 20, 1, 0.1f, 0.0f, &e.mtp.norm_emb));
+    MX_TRY(make_bf16(e, "mtp.norm_hidden", size_t(c.hc) * c.hidden, m, 21, 1, 0.1f, 0.0f,
+                     &e.mtp.norm_hid));
+    MX_TRY(make_qw(e, "mtp.fc_emb", c.hidden, c.hidden, bits, m, 22, &e.mtp.fc_emb));
+    MX_TRY(make_qw(e, "mtp.fc_hidden", c.hidden, c.hidden, bits, m, 23, &e.mtp.fc_hid));
+    MX_TRY(make_hc(e, "mtp.mixer", m, 24, false, &e.mtp.mixer));
   }
 
   // ---- caches ----
@@ -373,6 +412,15 @@ int build(Engine& e) {
     e.moe_plan_buf = reinterpret_cast<MoePlan*>(static_cast<char*>(e.moe_ws) + ws - sizeof(MoePlan));
   }
   MX_TRY(a16("act.logits", R * size_t(c.vocab), &e.logits));
+  if (c.mtp) {
+    MX_TRY(a16("mtp.act.emb", R * c.hidden, &e.mtp_emb));
+    MX_TRY(a16("mtp.act.a", R * c.hidden, &e.mtp_a));
+    MX_TRY(a16("mtp.act.e", R * c.hidden, &e.mtp_e));
+    MX_TRY(a16("mtp.act.prev", R * c.hc * c.hidden, &e.mtp_prev));
+    MX_TRY(a16("mtp.act.hn", R * c.hc * c.hidden, &e.mtp_hn));
+    MX_TRY(a16("mtp.act.f", R * c.hc * c.hidden, &e.mtp_f));
+    MX_TRY(a16("mtp.act.dh", size_t(c.hc) * c.hidden, &e.mtp_dh));
+  }
   MX_TRY(alloc(e, "act.ids", R * c.top_k * 4, &v));
   e.ids = static_cast<uint32_t*>(v);
   MX_TRY(alloc(e, "act.o_part", R * c.heads * e.max_chunks * c.head_dim * 4, &v));
@@ -501,12 +549,12 @@ int hc_forward(Engine& e, const HcW& w, int rows, uint16_t* mixed_out, uint16_t*
 
 // Records the kernels of one step for `rows` rows arranged as `groups`
 // sequences of `t` tokens.  Row metadata is read from e.dev_rows.
-int record_step(Engine& e, int rows, int groups, int t, bool history, bool logits) {
+// Records one layer (attention or GDN sublayer, then the MoE sublayer) on the
+// hc streams e.h of `rows` rows arranged as `groups` sequences of `t` tokens.
+int record_layer(Engine& e, const LayerW& L, int rows, int groups, int t, bool history) {
   const auto& c = e.cfg;
   Engine::RowTable* rt = e.dev_rows;
-  MX_TRY(embed(e.embed, rt->tokens, rows, c.hc, e.h, e.stream));
-  for (size_t li = 0; li < e.layers.size(); ++li) {
-    const LayerW& L = e.layers[li];
+  {
     MX_TRY(hc_forward(e, L.attn_hc, rows, e.mixed, e.inj));
     ProjEpilogue wr{};
     wr.mode = kHcWrite;
@@ -617,8 +665,26 @@ int record_step(Engine& e, int rows, int groups, int t, bool history, bool logit
       MX_TRY(moe_reduce_hc_epilogue(e.moe_p, e.factor, e.h, e.inj, rows, c.top_k, c.hc,
                                     c.hidden, e.h, e.stream));
   }
+  return MX_OK;
+}
+
+// Greedy head over e.mixed: next tokens into the device row table; with
+// `logits`, the bf16 logits too.
+int record_head(Engine& e, int rows, bool logits);
+
+int record_step(Engine& e, int rows, int groups, int t, bool history, bool logits) {
+  const auto& c = e.cfg;
+  Engine::RowTable* rt = e.dev_rows;
+  MX_TRY(embed(e.embed, rt->tokens, rows, c.hc, e.h, e.stream));
+  for (const LayerW& L : e.layers) MX_TRY(record_layer(e, L, rows, groups, t, history));
   // mixer + greedy head
   MX_TRY(hc_forward(e, e.mixer, rows, e.mixed, nullptr));
+  return record_head(e, rows, logits);
+}
+
+int record_head(Engine& e, int rows, bool logits) {
+  const auto& c = e.cfg;
+  Engine::RowTable* rt = e.dev_rows;
   int parts = 0;
   float* maxima = static_cast<float*>(e.head_ws);
   uint32_t* indices = reinterpret_cast<uint32_t*>(maxima + size_t(head_parts(c.vocab, c.hidden)) * 8);
@@ -677,6 +743,59 @@ int run_step(Engine& e, int rows, int groups, int t, bool history, uint32_t* nex
   MX_HIP(hipStreamSynchronize(e.stream));
   if (next) std::memcpy(next, e.host_rows->next, sizeof(uint32_t) * rows);
   e.last_rows = rows;
+  return MX_OK;
+}
+
+// MTP forward (Mtp::forward, src/mtp.rs:72-127) over `rows` rows of one slot:
+// the token ids (the token after each MTP position) and positions come from
+// the row table, the previous hidden streams from e.mtp_prev; the draft
+// tokens go to the row table's `next` and the new hidden streams stay in e.h.
+//   e = fc_embedding(norm(embedding, pre_fc_norm_embedding))
+//   h = fc_hidden(norm(previous hidden over all hc streams)) per stream
+//   h = bf16(e + h) -> attention layer + MoE layer -> mixer -> greedy head
+// Both norms are compiled::norm (src/compiled.rs:22-28), run by the
+// hyper-connection norm kernel with one stream of H or hc * H values.
+int record_mtp(Engine& e, int rows) {
+  const auto& c = e.cfg;
+  Engine::RowTable* rt = e.dev_rows;
+  const int H = c.hidden, hc = c.hc;
+  MX_TRY(embed(e.embed, rt->tokens, rows, 1, e.mtp_emb, e.stream));
+  MX_TRY(hc_norm(e.mtp_emb, e.mtp.norm_emb, rows, 1, H, c.rms_eps, e.mtp_a, e.stream));
+  ProjEpilogue pe{};
+  pe.mode = kPlain;
+  pe.y = e.mtp_e;
+  pe.y_stride = H;
+  MX_TRY(project(e, e.mtp.fc_emb, e.mtp_a, H, rows, pe));
+  MX_TRY(hc_norm(e.mtp_prev, e.mtp.norm_hid, rows, 1, hc * H, c.rms_eps, e.mtp_hn, e.stream));
+  for (int r0 = 0; r0 < rows * hc; r0 += 8) {
+    const int n = rows * hc - r0 < 8 ? rows * hc - r0 : 8;
+    ProjEpilogue ph{};
+    ph.mode = kPlain;
+    ph.y = e.mtp_f + size_t(r0) * H;
+    ph.y_stride = H;
+    MX_TRY(project(e, e.mtp.fc_hid, e.mtp_hn + size_t(r0) * H, H, n, ph));
+  }
+  MX_TRY(mtp_combine(e.mtp_e, e.mtp_f, rows, hc, H, e.h, e.stream));
+  MX_TRY(record_layer(e, e.mtp.layer, rows, 1, rows, false));
+  MX_TRY(hc_forward(e, e.mtp.mixer, rows, e.mixed, nullptr));
+  return record_head(e, rows, false);
+}
+
+// One eager MTP pass over `rows` rows of `slot` at MTP positions pos0 + r.
+int mtp_step(Engine& e, int slot, const uint32_t* tokens, int rows, int pos0, uint32_t* next) {
+  for (int r = 0; r < rows; ++r) {
+    e.host_rows->tokens[r] = tokens[r];
+    e.host_rows->slots[r] = slot;
+    e.host_rows->pos[r] = pos0 + r;
+    e.host_rows->gdn_slots[r] = slot * e.n_gdn;
+  }
+  MX_HIP(hipMemcpyAsync(e.dev_rows, e.host_rows, sizeof(Engine::RowTable), hipMemcpyHostToDevice,
+                        e.stream));
+  MX_TRY(record_mtp(e, rows));
+  MX_HIP(hipMemcpyAsync(e.host_rows->next, e.dev_rows->next, sizeof(uint32_t) * rows,
+                        hipMemcpyDeviceToHost, e.stream));
+  MX_HIP(hipStreamSynchronize(e.stream));
+  std::memcpy(next, e.host_rows->next, sizeof(uint32_t) * rows);
   return MX_OK;
 }
 
@@ -831,6 +950,128 @@ int engine_commit(Engine& e, int slot, int keep, std::string* err) {
   MX_HIP(hipStreamSynchronize(e.stream));
   e.offsets[slot] = e.verify_base + keep;
   e.verify_slot = -1;
+  return MX_OK;
+}
+
+// Greedy generation from an empty slot (speculative::generate_prepared,
+// src/speculative.rs:225-483, with its default policies: full-vocabulary
+// greedy draft head, fixed depth, no EOS).  depth 0: prefill, then one decode
+// step per token.  depth k >= 1: the MTP layer drafts k tokens (the first from
+// the previous pass), a (k + 1)-token verify block checks them, the accepted
+// prefix and the target's next token are emitted, the block is committed, and
+// the draft layer is resynchronised on the target's hidden states of the
+// accepted positions.  The MTP KV positions past the kept ones are
+// overwritten before they are read again, so a snapshot is just a length.
+int engine_generate(Engine& e, int slot, const uint32_t* prompt, int n_prompt, int max_tokens,
+                    int depth, uint32_t* out, int* n_out, mx_generate_stats* stats,
+                    uint32_t* drafts_out, std::string* err) {
+  const auto& c = e.cfg;
+  if (e.offsets[slot] != 0) {
+    *err = "generate needs an empty slot";
+    return MX_ESTATE;
+  }
+  if (n_prompt < 1 || max_tokens < 1) {
+    *err = "empty prompt or no tokens requested";
+    return MX_EINVAL;
+  }
+  if (depth < 0 || depth > 7 || depth + 1 > c.max_verify) {
+    *err = "depth must be in 0..min(7, max_verify - 1)";
+    return MX_EINVAL;
+  }
+  if (depth > 0 && !e.has_mtp) {
+    *err = "the model has no MTP layer (mtp = 0)";
+    return MX_EUNSUPPORTED;
+  }
+  if (int64_t(n_prompt) + max_tokens + depth + 1 > c.max_context) {
+    *err = "prompt + tokens exceed max_context";
+    return MX_EINVAL;
+  }
+  const size_t HS = size_t(c.hc) * c.hidden;
+  mx_generate_stats st{};
+  uint32_t nxt[8], drafts[8], toks[8];
+  uint32_t bonus = 0, seed = 0;
+  // prefill in blocks of 8; with a draft layer, each block's MTP pass follows
+  // it (MTP position i reads token i + 1 and the target's hidden state at i;
+  // the last position reads the target's first greedy token)
+  for (int a = 0; a < n_prompt; a += 8) {
+    const int cnt = n_prompt - a < 8 ? n_prompt - a : 8;
+    MX_TRY(engine_block(e, slot, prompt + a, cnt, false, nxt, err));
+    bonus = nxt[cnt - 1];
+    if (depth > 0) {
+      MX_HIP(hipMemcpyAsync(e.mtp_prev, e.h, cnt * HS * 2, hipMemcpyDeviceToDevice, e.stream));
+      for (int r = 0; r < cnt; ++r) toks[r] = a + r + 1 < n_prompt ? prompt[a + r + 1] : bonus;
+      MX_TRY(mtp_step(e, slot, toks, cnt, a, drafts));
+      seed = drafts[cnt - 1];
+      MX_HIP(hipMemcpyAsync(e.mtp_dh, e.h + (cnt - 1) * HS, HS * 2, hipMemcpyDeviceToDevice,
+                            e.stream));
+    }
+  }
+  int emitted = 0;
+  out[emitted++] = bonus;
+  if (depth == 0) {
+    while (emitted < max_tokens) {
+      const int32_t sl = slot;
+      const uint32_t tok = out[emitted - 1];
+      MX_TRY(engine_decode_rows(e, &sl, &tok, 1, nxt, err));
+      out[emitted++] = nxt[0];
+    }
+  } else {
+    int mtp_len = n_prompt;
+    while (emitted < max_tokens) {
+      const int k = depth < max_tokens - emitted ? depth : max_tokens - emitted;
+      uint32_t drafted[8], block[8], pred[8];
+      drafted[0] = seed;
+      const int base = mtp_len;
+      for (int i = 1; i < k; ++i) {
+        MX_HIP(hipMemcpyAsync(e.mtp_prev, e.mtp_dh, HS * 2, hipMemcpyDeviceToDevice, e.stream));
+        MX_TRY(mtp_step(e, slot, &drafted[i - 1], 1, base + i - 1, &drafted[i]));
+        MX_HIP(hipMemcpyAsync(e.mtp_dh, e.h, HS * 2, hipMemcpyDeviceToDevice, e.stream));
+      }
+      block[0] = bonus;
+      for (int i = 0; i < k; ++i) block[i + 1] = drafted[i];
+      if (drafts_out)
+        for (int i = 0; i < k; ++i) drafts_out[st.drafted + i] = drafted[i];
+      MX_TRY(engine_verify(e, slot, block, k + 1, pred, err));
+      int accepted = 0;
+      while (accepted < k && drafted[accepted] == pred[accepted]) ++accepted;
+      const uint32_t next = pred[accepted];
+      int emitted_now = 0;
+      bool ending = false;
+      for (int i = 0; i <= accepted; ++i) {
+        if (emitted == max_tokens) {
+          ending = true;
+          break;
+        }
+        out[emitted++] = i < accepted ? drafted[i] : next;
+        ++emitted_now;
+      }
+      const int committed = ending ? (emitted_now < accepted ? emitted_now : accepted) + 1
+                                   : accepted + 1;
+      MX_TRY(engine_commit(e, slot, committed, err));
+      st.rounds += 1;
+      st.drafted += k;
+      st.accepted += accepted;
+      if (ending || emitted == max_tokens) break;
+      bonus = next;
+      // resynchronise: keep the draft positions of the first `kept` drafts,
+      // then run the accepted tokens and the next one on the target's hidden
+      // states (verify rows kept .. accepted, still in e.h after the commit)
+      const int kept = accepted < k - 1 ? accepted : k - 1;
+      mtp_len = base + kept;
+      const int sync = accepted - kept + 1;
+      for (int i = 0; i < sync - 1; ++i) toks[i] = drafted[kept + i];
+      toks[sync - 1] = next;
+      MX_HIP(hipMemcpyAsync(e.mtp_prev, e.h + size_t(kept) * HS, sync * HS * 2,
+                            hipMemcpyDeviceToDevice, e.stream));
+      MX_TRY(mtp_step(e, slot, toks, sync, mtp_len, drafts));
+      seed = drafts[sync - 1];
+      MX_HIP(hipMemcpyAsync(e.mtp_dh, e.h + size_t(sync - 1) * HS, HS * 2,
+                            hipMemcpyDeviceToDevice, e.stream));
+      mtp_len += sync;
+    }
+  }
+  *n_out = emitted;
+  if (stats) *stats = st;
   return MX_OK;
 }
 

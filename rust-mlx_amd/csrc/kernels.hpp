@@ -122,6 +122,9 @@ int hc_fused(const QWeight& down, const QWeight& up, const uint16_t* h, const ui
 int hc_norm(const uint16_t* x, const uint16_t* scale, int rows, int hc, int hidden, float eps,
             uint16_t* y, hipStream_t s);
 int embed(const QWeight& w, const uint32_t* ids, int count, int hc, uint16_t* out, hipStream_t s);
+// y[r][s][c] = bf16(e[r][c] + f[r hc + s][c]) (the MTP input, src/mtp.rs:103-106).
+int mtp_combine(const uint16_t* e, const uint16_t* f, int rows, int hc, int hidden, uint16_t* y,
+                hipStream_t s);
 
 // ---- attention (attn.hip) ----
 struct AttnDims {
@@ -242,6 +245,9 @@ int engine_block(Engine& e, int slot, const uint32_t* tokens, int count, bool hi
 int engine_verify(Engine& e, int slot, const uint32_t* tokens, int count, uint32_t* next,
                   std::string* err);
 int engine_commit(Engine& e, int slot, int keep, std::string* err);
+int engine_generate(Engine& e, int slot, const uint32_t* prompt, int n_prompt, int max_tokens,
+                    int depth, uint32_t* out, int* n_out, mx_generate_stats* stats,
+                    uint32_t* drafts, std::string* err);
 int engine_read(Engine& e, const char* what, void* host, size_t bytes, std::string* err);
 int engine_tensor(Engine& e, const char* name, void** ptr, size_t* bytes);
 int engine_fill_slot(Engine& e, int slot, int length, uint64_t seed, std::string* err);

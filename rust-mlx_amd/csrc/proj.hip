@@ -202,7 +202,28 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint32_t* __restrict__
   }
 }
 
+// The MTP layer's input: the embedding projection added to every stream's
+// hidden projection in bf16 (src/mtp.rs:103-106).
+__global__ __launch_bounds__(256) void mtp_combine_kernel(const uint16_t* __restrict__ e,
+                                                          const uint16_t* __restrict__ f,
+                                                          int hc, int hidden,
+                                                          uint16_t* __restrict__ y) {
+  const int r = blockIdx.y;
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < hc * hidden; i += gridDim.x * 256) {
+    const int c = i % hidden;
+    y[size_t(r) * hc * hidden + i] = f32_to_bf16(bf16_to_f32(e[size_t(r) * hidden + c]) +
+                                                 bf16_to_f32(f[size_t(r) * hc * hidden + i]));
+  }
+}
+
 }  // namespace
+
+int mtp_combine(const uint16_t* e, const uint16_t* f, int rows, int hc, int hidden, uint16_t* y,
+                hipStream_t s) {
+  const int bx = (hc * hidden + 255) / 256;
+  hipLaunchKernelGGL(mtp_combine_kernel, dim3(bx, rows), dim3(256), 0, s, e, f, hc, hidden, y);
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
 
 int proj(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const ProjEpilogue& e,
          hipStream_t s) {

@@ -1,0 +1,81 @@
+"""The MTP draft layer and speculative generation (config 4's draft model and
+acceptance loop: Mtp::forward, src/mtp.rs:72-127; generate_prepared,
+src/speculative.rs:225-483) on the tiny model with mtp = 1.
+
+Exact mode: the tokens, every round's draft tokens and the acceptance counts
+are bit-exact with the CPU oracle model running the same loop, and
+speculation is lossless (the tokens equal plain greedy decoding's).  With a
+16-token vocabulary the draft layer's guesses are accepted now and then, so
+the accept / commit / resynchronise paths with accepted > 0 run too.
+Fast mode: the loop runs end to end on the matrix-core kernels (its verify
+blocks and decode steps sum in different orders, so it is not compared with
+plain decoding token for token)."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+# (vocab, mixed widths, depth, seed): seed 60 draws every width in both roles;
+# with 16 tokens, seed 6 (prompt drawn from the same seed) accepts 5-6 drafts
+# in 9-10 rounds at depths 2, 3 and 7
+@pytest.mark.parametrize("vocab,mixed,depth,seed", [(1024, 0, 3, 77), (1024, 1, 1, 60),
+                                                    (16, 0, 3, 6), (16, 0, 7, 6), (16, 0, 2, 6),
+                                                    (16, 1, 3, 60)])
+def test_exact_speculation_matches_oracle_and_plain_greedy(mx, vocab, mixed, depth, seed):
+    from oracle.model import Model
+
+    cfg = dict(mx.TINY, mtp=1, vocab=vocab, mixed_bits=mixed, seed=seed)
+    eng = mx.Engine(cfg)
+    try:
+        eng.set_flags(exact=True)
+        model = Model(cfg, lambda name, dtype, shape: eng.read(name, dtype, shape))
+        prompt = [int(t) for t in np.random.default_rng(seed).integers(0, vocab, 19)]
+        toks, st = eng.generate(1, prompt, 16, depth)
+        want, wst = model.generate(1, prompt, 16, depth)
+        assert [int(t) for t in toks] == want
+        assert [int(d) for d in st["drafts"]] == wst["drafts"]
+        assert (st["rounds"], st["drafted"], st["accepted"]) == \
+            (wst["rounds"], wst["drafted"], wst["accepted"])
+        plain, pst = eng.generate(2, prompt, 16, 0)
+        assert [int(t) for t in plain] == [int(t) for t in toks]
+        assert pst["rounds"] == 0
+        if seed == 6:
+            assert st["accepted"] > 0, st  # the accept path ran
+    finally:
+        eng.close()
+
+
+def test_generate_rejects_bad_requests(mx):
+    cfg = dict(mx.TINY, mtp=0)
+    eng = mx.Engine(cfg)
+    try:
+        with pytest.raises(Exception):
+            eng.generate(0, [1, 2, 3], 4, 3)  # no draft layer
+        eng.generate(0, [1, 2, 3], 2, 0)
+        with pytest.raises(Exception):
+            eng.generate(0, [1, 2, 3], 2, 0)  # the slot is no longer empty
+    finally:
+        eng.close()
+
+
+MID = dict(hidden=512, layers=4, attn_every=4, vocab=4096, hc=4, hc_rank=256, gdn_hk=2, gdn_hv=4,
+           gdn_dk=128, gdn_dv=128, conv_k=4, heads=4, kv_heads=1, head_dim=128, rotary_dim=32,
+           rope_theta=1e7, rms_eps=1e-6, experts=64, top_k=4, moe_inter=512, shared_inter=512,
+           bits=4, down_bits=5, embed_bits=8, head_bits=8, group_size=64, mixed_bits=0,
+           max_slots=4, max_context=128, max_verify=8, seed=4242, mtp=1)
+
+
+def test_fast_speculation_runs_on_the_matrix_cores(mx):
+    eng = mx.Engine(dict(MID))
+    try:
+        eng.set_flags(exact=False)
+        prompt = [int(t) for t in np.random.default_rng(3).integers(0, MID["vocab"], 21)]
+        toks, st = eng.generate(0, prompt, 24, 3)
+        assert len(toks) == 24 and all(0 <= int(t) < MID["vocab"] for t in toks)
+        assert st["rounds"] >= 1 and st["drafted"] == len(st["drafts"])
+        assert 0 <= st["accepted"] <= st["drafted"]
+        plain, _ = eng.generate(1, prompt, 24, 0)
+        assert int(plain[0]) == int(toks[0])  # the prefill's greedy token
+    finally:
+        eng.close()
