@@ -20,6 +20,17 @@ Workloads:
       value = tokens/s.  Roofline: fp32 matrix-core FLOPs of the chunked
       algorithm per scan over the scan time (MI355X fp32 MFMA 157.3 TFLOP/s);
       the sequential GPU scan (mx_gdn_scan) is timed beside it.
+  gdn-decode-config1  BASELINE config 1 decode: one fast-mode GatedDeltaNet
+      step (mx_gdn_recurrence_fast) at B = 1, 2, 4, 8 rows over a rotated 1 GiB
+      fp32 state arena; value = B = 8 rows per second, roofline = state and
+      q/k/v/y bytes over the step time.
+  moe-config2  BASELINE config 2: the decode MoE sublayer (router projection,
+      routing, gathered expert gate/up and down, slot sum into the residual
+      streams) at B = 1..8 rows; 32 rotated input batches; value = B = 8 rows
+      per second, roofline = router + shared + distinct experts' bytes.
+  mtp-config4  BASELINE config 4: MTP speculative generation (depth 3) on the
+      mixed-width config-3 model, batch 1, 4096-token prompt, 256 tokens, timed
+      against plain greedy decoding of the same prompt.
 
 Timing: the decode loop is bracketed by device synchronisation (the engine
 synchronises once per step to read the tokens, as the reference's eval does).
@@ -366,6 +377,272 @@ def bench_gdn_prefill_config1(mx, args):
     }
 
 
+def timed_launches(mx, stream, fn, n):
+    """Average seconds per call of fn() over n calls, HIP events on `stream`
+    (the stream the kernels are launched on)."""
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    mx.check(mx.lib.mx_event_create(C.byref(e0)))
+    mx.check(mx.lib.mx_event_create(C.byref(e1)))
+    mx.check(mx.lib.mx_device_sync())
+    mx.check(mx.lib.mx_event_record(e0, stream))
+    for i in range(n):
+        fn(i)
+    mx.check(mx.lib.mx_event_record(e1, stream))
+    ms = C.c_float()
+    mx.check(mx.lib.mx_stream_sync(stream))
+    mx.check(mx.lib.mx_event_elapsed_ms(e0, e1, C.byref(ms)))
+    mx.check(mx.lib.mx_event_destroy(e0))
+    mx.check(mx.lib.mx_event_destroy(e1))
+    return ms.value / 1e3 / n
+
+
+# per row: fp32 state read + written (2 Hv Dk Dv 4) plus q, k, v (8192 bf16),
+# y (4096 bf16), g (32 fp32) and beta (32 bf16)
+GDN_DECODE_BYTES_PER_ROW = 2 * 32 * 128 * 128 * 4 + 16384 + 8192 + 128 + 64
+
+
+def bench_gdn_decode_config1(mx, args):
+    """Config 1 decode: one fast-mode GatedDeltaNet step (q/k L2 norm, beta,
+    decay, delta rule, gated RMS norm) for B = 1, 2, 4, 8 rows, each row on its
+    own slot of a 1 GiB fp32 state arena (rotated so the 256 MB last-level cache
+    cannot serve repeats).  `value` is the B = 8 step's rows per second."""
+    from oracle import oracle as orc
+
+    hk, hv, d = 16, 32, 128
+    slots_n = 512  # 2 MiB of state per slot
+    dims = mx.GdnDimsC(hk, hv, d, d, 4)
+    rng = np.random.default_rng(1001)
+    rows_max = 8
+    conv = orc.f32_to_bf16(rng.standard_normal((rows_max, 2 * hk * d + hv * d)).astype(np.float32))
+    z = orc.f32_to_bf16(rng.standard_normal((rows_max, hv * d)).astype(np.float32))
+    a = orc.f32_to_bf16(rng.standard_normal((rows_max, hv)).astype(np.float32))
+    b = orc.f32_to_bf16(rng.standard_normal((rows_max, hv)).astype(np.float32))
+    a_log = np.log(rng.uniform(1e-3, 16, hv)).astype(np.float32)  # A ~ U(0, 16)
+    dt = orc.f32_to_bf16(rng.uniform(-1, 1, hv).astype(np.float32))
+    norm_w = orc.f32_to_bf16(rng.uniform(0.5, 1.5, d).astype(np.float32))
+    eps = 1e-6
+    zab = np.ascontiguousarray(np.concatenate([z, a, b], axis=1))
+    dconv, dzab = mx.DeviceArray.from_numpy(conv), mx.DeviceArray.from_numpy(zab)
+    dal, ddt, dnw = (mx.DeviceArray.from_numpy(v) for v in (a_log, dt, norm_w))
+    state = mx.DeviceArray((slots_n, hv, d, d), np.float32, zero=True)
+    lists = np.arange(slots_n * rows_max, dtype=np.int32).reshape(-1, rows_max) % slots_n
+    dlists = mx.DeviceArray.from_numpy(np.ascontiguousarray(lists))
+    y = mx.DeviceArray((rows_max, hv * d), np.uint16)
+    stream = C.c_void_p()
+    mx.check(mx.lib.mx_stream_create(C.byref(stream)))
+    zp = dzab.ptr
+
+    def launch(rows, i):
+        lst = dlists.ptr + 4 * rows * (i % (slots_n // rows))  # `rows` consecutive slots
+        mx.check(mx.lib.mx_gdn_recurrence_fast(dconv.ptr, conv.shape[1], zp, zp + 2 * hv * d,
+                                               zp + 2 * (hv * d + hv), zab.shape[1], dal.ptr,
+                                               ddt.ptr, dnw.ptr, eps, C.byref(dims), rows, 1,
+                                               lst, state.ptr, None, y.ptr, stream))
+
+    # parity first: one B = 8 step from the zero state against the oracle
+    launch(rows_max, 0)
+    mx.check(mx.lib.mx_stream_sync(stream))
+    st0 = np.zeros((rows_max, hv, d, d), np.float32)
+    sl = np.arange(rows_max, dtype=np.int32)
+    t0 = time.perf_counter()
+    y_w, st_w, _ = orc.gdn_recurrence(conv, z, a, b, a_log, dt, norm_w, eps, hk, hv, rows_max, 1,
+                                      sl, st0)
+    cpu_once = time.perf_counter() - t0
+    got_st = np.empty((rows_max, hv, d, d), np.float32)
+    mx.check(mx.lib.mx_memcpy_dtoh(got_st.ctypes.data, state.ptr, got_st.nbytes))
+    st_err = np.abs(got_st - st_w).max() / np.abs(st_w).max()
+    got_y = orc.bf16_to_f32(y.numpy()).astype(np.float64)
+    want_y = orc.bf16_to_f32(y_w).astype(np.float64)
+    y_ok = bool(np.all(np.abs(got_y - want_y) <= 2e-2 * np.abs(want_y) + 1e-2))
+    log(f"gdn-decode-config1: B=8 state max rel err vs oracle {st_err:.2e}, y within tolerance {y_ok}")
+    if st_err > 1e-4 or not y_ok:
+        raise SystemExit("bench: GDN decode step differs from the oracle")
+    per_b = {}
+    for rows in (1, 2, 4, 8):
+        for i in range(args.warmup):
+            launch(rows, i)
+        sec = timed_launches(mx, stream, lambda i, r=rows: launch(r, args.warmup + i), args.steps)
+        gbs = rows * GDN_DECODE_BYTES_PER_ROW / sec / 1e9
+        per_b[rows] = {"us": round(sec * 1e6, 2), "rows_per_s": round(rows / sec, 1),
+                       "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        log(f"gdn-decode-config1: B={rows} {sec * 1e6:.2f} us/step, {gbs:.0f} GB/s")
+    reps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < 10.0:
+        orc.gdn_recurrence(conv, z, a, b, a_log, dt, norm_w, eps, hk, hv, rows_max, 1, sl, st0)
+        reps += 1
+    cpu_dt = (time.perf_counter() - t0) / reps
+    b8 = per_b[8]
+    return {
+        "metric": METRIC, "value": b8["rows_per_s"], "unit": "tok/s (rows stepped per second)",
+        "ms_per_step": b8["us"] / 1e3,
+        "dtype": "bf16 q/k/v/z -> fp32 state and arithmetic",
+        "config": {"workload": "gdn-decode-config1", "key_heads": hk, "value_heads": hv,
+                   "head_dim": d, "state_slots_rotated": slots_n,
+                   "per_batch": {str(k): v for k, v in per_b.items()},
+                   "state_rel_err_vs_oracle": float(f"{st_err:.3e}")},
+        "roofline": {"bound": "hbm", "kernel": "recurrence_fast_kernel (B=8)",
+                     "achieved": b8["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": b8["frac"], "traffic": None,
+                     "algorithmic_bytes_per_launch": 8 * GDN_DECODE_BYTES_PER_ROW},
+        "cpu_baseline": {"value": round(rows_max / cpu_dt, 2), "unit": "tok/s",
+                         "cores": orc.num_threads(), "kind": "port",
+                         "sample": f"{reps} oracle B=8 steps in 10s (first {cpu_once:.3f}s)"},
+    }
+
+
+def bench_moe_config2(mx, args):
+    """Config 2: the sparse MoE block at decode for B = 1..8 rows: the router
+    projection (512 experts + the shared-expert gate, 4-bit), routing (softmax,
+    top-10, renormalisation) inside the expert gate/up kernel, the 4-bit
+    gate/up and 5-bit down projections of the selected and shared experts, and
+    the slot sum written into 4 residual streams (the decode step's MoE
+    sublayer).  32 input batches rotate so that consecutive calls select
+    different experts.  Bytes per call: router + shared expert + U distinct
+    experts x (2 q(512,2048,4) + q(2048,512,5)), U counted per input batch."""
+    from oracle import oracle as orc
+
+    E, H, I, k = 512, 2048, 512, 10
+    n_x = 32
+    gate = mx.QBank.random(E, I, H, 4, 64, 2001)
+    up = mx.QBank.random(E, I, H, 4, 64, 2002)
+    down = mx.QBank.random(E, H, I, 5, 64, 2003)
+    sg = mx.QWeight.random(I, H, 4, 64, 2004)
+    su = mx.QWeight.random(I, H, 4, 64, 2005)
+    sd = mx.QWeight.random(H, I, 5, 64, 2006)
+    router = mx.QWeight.random(E + 1, H, 4, 64, 2007)
+    xs = orc.fill_bf16(n_x * 8 * H, 2008, 1, 1.0, 0.0).reshape(n_x, 8, H)
+    res = orc.fill_bf16(8 * 4 * H, 2009, 1, 1.0, 0.0).reshape(8, 4, H)
+    hg = orc.fill_bf16(8 * 4, 2010, 1, 1.0, 1.0).reshape(8, 4)
+    dx, dres, dhg = (mx.DeviceArray.from_numpy(v) for v in (xs, res, hg))
+    logits = mx.DeviceArray((8, E + 1), np.uint16)
+    ids = mx.DeviceArray((8, k), np.uint32)
+    sc = mx.DeviceArray((8, k), np.uint16)
+    fa = mx.DeviceArray((8,), np.uint16)
+    ws = mx.DeviceArray((mx.lib.mx_moe_workspace_bytes(8, 16, I),), np.uint8)
+    qb = [bk.c() for bk in (gate, up, down)]
+    qs = [w.c() for w in (sg, su, sd)]
+    rc = router.c()
+    stream = C.c_void_p()
+    mx.check(mx.lib.mx_stream_create(C.byref(stream)))
+
+    def launch(rows, i):
+        xp = dx.ptr + 2 * 8 * H * (i % n_x)
+        mx.check(mx.lib.mx_qmm(C.byref(rc), xp, rows, logits.ptr, stream))
+        mx.check(mx.lib.mx_moe_routed_experts_hc_mfma(
+            logits.ptr, E + 1, logits.ptr + 2 * E, E + 1, E, xp, rows, k, 4, C.byref(qb[0]),
+            C.byref(qb[1]), C.byref(qb[2]), C.byref(qs[0]), C.byref(qs[1]), C.byref(qs[2]),
+            ws.ptr, ids.ptr, sc.ptr, fa.ptr, dhg.ptr, dres.ptr, stream))
+
+    ex_bytes = 2 * qweight_bytes(I, H, 4, 64) + qweight_bytes(H, I, 5, 64)
+    fixed_bytes = qweight_bytes(E + 1, H, 4, 64) + ex_bytes  # router + shared expert
+    # parity first (B = 8): the routing of the GPU's router logits is the
+    # oracle's, bit for bit; then the distinct experts of every input batch
+    launch(8, 0)
+    mx.check(mx.lib.mx_stream_sync(stream))
+    lg = logits.numpy()
+    ids_w, sc_w, fa_w = orc.moe_route(lg[:, :E], lg[:, E], k)
+    if not ((ids.numpy() == ids_w).all() and (sc.numpy() == sc_w).all()
+            and (fa.numpy() == fa_w).all()):
+        raise SystemExit("bench: MoE routing differs from the oracle")
+    per_b = {}
+    for rows in range(1, 9):
+        distinct = []
+        for i in range(n_x):
+            launch(rows, i)
+            mx.check(mx.lib.mx_stream_sync(stream))
+            distinct.append(len(np.unique(ids.numpy()[:rows])))
+        u = float(np.mean(distinct))
+        for i in range(args.warmup):
+            launch(rows, i)
+        sec = timed_launches(mx, stream, lambda i, r=rows: launch(r, args.warmup + i), args.steps)
+        alg = fixed_bytes + u * ex_bytes
+        gbs = alg / sec / 1e9
+        per_b[rows] = {"us": round(sec * 1e6, 2), "distinct_experts": round(u, 2),
+                       "bytes": int(alg), "gbs": round(gbs, 1),
+                       "frac": round(gbs / HBM_PEAK_GBS, 4), "rows_per_s": round(rows / sec, 1)}
+        log(f"moe-config2: B={rows} {sec * 1e6:.2f} us/block, U={u:.1f}, {gbs:.0f} GB/s")
+    # CPU baseline: the oracle's B = 8 block (router QMV, route, experts, slot sum)
+    # the oracle's structs view host arrays: keep the arrays alive beside them
+    host_b = [bk.host() for bk in (gate, up, down)]
+    host_s = [w.host() for w in (sg, su, sd)]
+    hb = [orc.qbank(*a, E, bk.n, bk.k, bk.bits, 64) for a, bk in zip(host_b, (gate, up, down))]
+    hs = [orc.qw(*a, w.n, w.k, w.bits, 64) for a, w in zip(host_s, (sg, su, sd))]
+    rcodes, rs, rb = router.host()
+    reps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < 10.0 or reps == 0:
+        x8 = xs[reps % n_x]
+        lgc = orc.qmv(rcodes, rs, rb, H, 4, 64, x8)
+        i_c, s_c, f_c = orc.moe_route(lgc[:, :E], lgc[:, E], k)
+        p = orc.moe_experts(x8, i_c, s_c, k, hb[0], hb[1], hb[2], hs[0], hs[1], hs[2], H)
+        orc.moe_reduce(p, k)
+        reps += 1
+    cpu_dt = (time.perf_counter() - t0) / reps
+    b8 = per_b[8]
+    return {
+        "metric": METRIC, "value": b8["rows_per_s"], "unit": "tok/s (rows per second)",
+        "ms_per_step": b8["us"] / 1e3,
+        "dtype": "affine u4 (gate/up, router) / u5 (down) codes x bf16 -> fp32 acc",
+        "config": {"workload": "moe-config2", "experts": E, "top_k": k, "hidden": H,
+                   "inter": I, "shared_inter": I, "rotated_input_batches": n_x,
+                   "per_batch": {str(b_): v for b_, v in per_b.items()}},
+        "roofline": {"bound": "hbm",
+                     "kernel": "router dense_kernel + gate_up_persist_kernel + down_hc_kernel (B=8)",
+                     "achieved": b8["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": b8["frac"], "traffic": None,
+                     "algorithmic_bytes_per_launch": b8["bytes"]},
+        "cpu_baseline": {"value": round(8 / cpu_dt, 2), "unit": "tok/s",
+                         "cores": orc.num_threads(), "kind": "port",
+                         "sample": f"{reps} oracle B=8 MoE blocks (router, route, experts, "
+                                   f"slot sum) in {reps * cpu_dt:.1f}s"},
+    }
+
+
+def bench_mtp_config4(mx, args):
+    """Config 4: MTP speculative generation on the config-3 model with per-layer
+    widths {4,5,6,8} from the seeded schedule and one draft layer: batch 1, a
+    4096-token prompt, 256 generated tokens, draft depth 3 (4-token verify
+    blocks, greedy acceptance, state and KV rollback).  Timed against plain
+    greedy decoding (depth 0) of the same prompt; each figure is the generate
+    call minus the same call stopped after its first token (prompt and drafter
+    prefill).  Random weights make drafts rarely right: the acceptance rate is
+    reported, and the tokens must equal plain greedy decoding's."""
+    n_tok, ctx, depth = 256, 4096, 3
+    cfg = dict(mx.CONFIG3, mixed_bits=1, mtp=1, max_slots=2,
+               max_context=ctx + n_tok + 64)
+    eng = mx.Engine(cfg)
+    prompt = np.random.default_rng(4004).integers(0, cfg["vocab"], ctx)
+    res = {}
+    for d in (0, depth):
+        eng.reset(0)
+        t0 = time.perf_counter()
+        eng.generate(0, prompt, 1, depth=d)
+        t_first = time.perf_counter() - t0
+        eng.reset(0)
+        t0 = time.perf_counter()
+        toks, st = eng.generate(0, prompt, n_tok + 1, depth=d)
+        t_all = time.perf_counter() - t0
+        res[d] = (toks, st, t_all - t_first, t_first)
+        log(f"mtp-config4: depth {d}: {n_tok} tokens in {t_all - t_first:.3f}s after a "
+            f"{t_first:.2f}s prompt; rounds {st['rounds']}, accepted {st['accepted']}/{st['drafted']}")
+    eng.close()
+    if not (res[0][0] == res[depth][0]).all():
+        raise SystemExit("bench: speculative tokens differ from greedy decoding")
+    toks, st, dt, t_first = res[depth]
+    _, _, dt0, _ = res[0]
+    return {
+        "metric": METRIC, "value": round(n_tok / dt, 2), "unit": "tok/s", "ms_per_step": dt / n_tok * 1e3,
+        "dtype": "affine u4/u5/u6/u8 codes x bf16 -> fp32 acc; bf16 activations; fp32 GDN state",
+        "config": {"workload": "mtp-config4", "model": "synthetic hybrid GDN/attention MoE, mixed widths",
+                   "batch": 1, "context": ctx, "generated": n_tok, "draft_depth": depth,
+                   "rounds": st["rounds"], "drafted": st["drafted"], "accepted": st["accepted"],
+                   "ms_per_round": round(dt / max(st["rounds"], 1) * 1e3, 3),
+                   "greedy_decode_tok_s": round(n_tok / dt0, 2), "prompt_s": round(t_first, 2),
+                   "tokens_equal_greedy": True},
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+
+
 # ------------------------------------------------------- copy calibration --
 COPY_BYTES = 256 << 20
 
@@ -398,9 +675,11 @@ def bench_copy_calibration(mx, args):
 
 WORKLOADS = {"config3-b8-decode": bench_config3, "qmv-config0": bench_qmv_config0,
              "gdn-prefill-config1": bench_gdn_prefill_config1,
-             "copy-calibration": bench_copy_calibration}
+             "gdn-decode-config1": bench_gdn_decode_config1, "moe-config2": bench_moe_config2,
+             "mtp-config4": bench_mtp_config4, "copy-calibration": bench_copy_calibration}
 DEFAULTS = {"config3-b8-decode": (240, 16), "qmv-config0": (2000, 200),
-            "gdn-prefill-config1": (50, 5), "copy-calibration": (10, 2)}
+            "gdn-prefill-config1": (50, 5), "gdn-decode-config1": (200, 20),
+            "moe-config2": (200, 20), "mtp-config4": (1, 0), "copy-calibration": (10, 2)}
 
 
 def main() -> None:

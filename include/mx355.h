@@ -405,17 +405,21 @@ mx_status mx_attn_decode(const uint16_t* q, const uint16_t* qkv, int64_t qkv_str
                          const uint16_t* v_cache, const mx_attn_dims* dims, int32_t flags,
                          void* workspace, uint16_t* out, void* stream);
 
-/* mx_gdn_recurrence_fast: the single-token form of mx_gdn_recurrence (t = 1 for
- * each of `rows` groups, no history) with the matrix-core engine's fast-mode
+/* mx_gdn_recurrence_fast: mx_gdn_recurrence's contract (groups of t tokens,
+ * optional per-token history) with the matrix-core engine's fast-mode
  * arithmetic: the same fp32 delta rule, hardware exp2 / log2 / reciprocal /
  * rsqrt for beta, the decay, the L2 and RMS norms and the gate, within the
- * north star's tolerances of the fixed-order kernel. */
+ * north star's tolerances of the fixed-order kernel.  Every token's
+ * arithmetic is independent of t, so a t-token verify block gives the bits
+ * of t one-token calls (the decode step) and greedy acceptance stays
+ * lossless.  Replaces the same reference interfaces as mx_gdn_recurrence
+ * (src/gdn_kernel.rs:7-142, src/hybrid.rs:401-453). */
 mx_status mx_gdn_recurrence_fast(const uint16_t* conv_out, int64_t conv_stride,
                                  const uint16_t* z, const uint16_t* a, const uint16_t* b,
                                  int64_t zab_stride, const float* a_log, const uint16_t* dt_bias,
                                  const uint16_t* norm_w, float eps, const mx_gdn_dims* dims,
-                                 int32_t rows, const int32_t* slots, float* state, uint16_t* y,
-                                 void* stream);
+                                 int32_t groups, int32_t t, const int32_t* slots, float* state,
+                                 float* history, uint16_t* y, void* stream);
 
 /* ---- A1/A17/A18: the decode engine ---------------------------------------
  * Owns the model weights, a slot arena of caches (GDN state + conv window, KV)

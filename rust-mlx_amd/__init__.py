@@ -164,7 +164,7 @@ def _load() -> C.CDLL:
         "mx_gdn_scan": ([vp, vp, vp, vp, vp, C.POINTER(GdnDimsC), i32, i32, vp, vp, vp, vp,
                          vp], i32),
         "mx_gdn_recurrence_fast": ([vp, i64, vp, vp, vp, i64, vp, vp, vp, f32,
-                                    C.POINTER(GdnDimsC), i32, vp, vp, vp, vp], i32),
+                                    C.POINTER(GdnDimsC), i32, i32, vp, vp, vp, vp, vp], i32),
         "mx_gdn_prefill_workspace_bytes": ([i32, i32, i32], sz),
         "mx_gdn_prefill_chunked": ([vp, vp, vp, vp, vp, C.POINTER(GdnDimsC), i32, i32, vp, vp, vp,
                                     vp, vp], i32),

@@ -374,12 +374,12 @@ MX_ABI mx_status mx_gdn_recurrence_fast(const uint16_t* conv_out, int64_t conv_s
                                         const uint16_t* z, const uint16_t* a, const uint16_t* b,
                                         int64_t zab_stride, const float* a_log,
                                         const uint16_t* dt_bias, const uint16_t* norm_w,
-                                        float eps, const mx_gdn_dims* dims, int32_t rows,
-                                        const int32_t* slots, float* state, uint16_t* y,
-                                        void* stream) {
+                                        float eps, const mx_gdn_dims* dims, int32_t groups,
+                                        int32_t t, const int32_t* slots, float* state,
+                                        float* history, uint16_t* y, void* stream) {
   MX_CHECK(dims != nullptr, MX_EINVAL, "mx_gdn_recurrence_fast: null dims");
-  MX_CHECK(rows >= 0, MX_EINVAL, "mx_gdn_recurrence_fast: negative rows");
-  if (rows == 0) return MX_OK;
+  MX_CHECK(groups >= 0 && t >= 1, MX_EINVAL, "mx_gdn_recurrence_fast: bad shape");
+  if (groups == 0) return MX_OK;
   MX_CHECK(conv_out && z && a && b && a_log && dt_bias && norm_w && slots && state && y,
            MX_EINVAL, "mx_gdn_recurrence_fast: null pointer");
   const GdnDims d{dims->hk, dims->hv, dims->dk, dims->dv, dims->conv_k};
@@ -387,8 +387,11 @@ MX_ABI mx_status mx_gdn_recurrence_fast(const uint16_t* conv_out, int64_t conv_s
            "mx_gdn_recurrence_fast: value heads must be a multiple of key heads");
   MX_CHECK(d.dk == 128 && d.dv == 128, MX_EUNSUPPORTED,
            "mx_gdn_recurrence_fast: head dims must be 128");
+  MX_CHECK(conv_stride >= int64_t(2) * d.hk * d.dk + int64_t(d.hv) * d.dv, MX_EINVAL,
+           "mx_gdn_recurrence_fast: conv row stride too small");
   return finish(gdn_recurrence_fast(conv_out, conv_stride, z, a, b, zab_stride, a_log, dt_bias,
-                                    norm_w, eps, d, rows, slots, state, y, hipStream_t(stream)),
+                                    norm_w, eps, d, groups, t, slots, state, history, y,
+                                    hipStream_t(stream)),
                 "mx_gdn_recurrence_fast");
 }
 

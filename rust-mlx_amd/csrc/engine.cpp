@@ -592,19 +592,19 @@ int record_layer(Engine& e, const LayerW& L, int rows, int groups, int t, bool h
                                 : nullptr,
                         e.stream));
       }
-      if (!e.exact && t == 1 && !history) {
+      float* hist = history ? e.hist_state + size_t(gi) * c.max_verify * state_per : nullptr;
+      if (!e.exact) {
+        // decode, verify and prefill blocks alike: a verify block's tokens
+        // get the bits of one-token decode steps (lossless speculation)
         MX_TRY(gdn_recurrence_fast(e.conv_out, e.cd, e.pbuf + e.cd, e.pbuf + e.cd + e.vd,
                                    e.pbuf + e.cd + e.vd + c.gdn_hv, e.P, L.a_log, L.dt_bias,
-                                   L.gdn_norm, c.rms_eps, e.gd, groups, rt->gdn_slots,
-                                   e.gdn_state + gi * state_per, e.y, e.stream));
+                                   L.gdn_norm, c.rms_eps, e.gd, groups, t, rt->gdn_slots,
+                                   e.gdn_state + gi * state_per, hist, e.y, e.stream));
       } else {
         MX_TRY(gdn_recurrence(e.conv_out, e.cd, e.pbuf + e.cd, e.pbuf + e.cd + e.vd,
                               e.pbuf + e.cd + e.vd + c.gdn_hv, e.P, L.a_log, L.dt_bias,
                               L.gdn_norm, c.rms_eps, e.gd, groups, t, rt->gdn_slots,
-                              e.gdn_state + gi * state_per,
-                              history ? e.hist_state + size_t(gi) * c.max_verify * state_per
-                                      : nullptr,
-                              e.y, e.stream));
+                              e.gdn_state + gi * state_per, hist, e.y, e.stream));
       }
       MX_TRY(project(e, L.gdn_out, e.y, e.vd, rows, wr));
     } else {

@@ -221,9 +221,11 @@ __global__ __launch_bounds__(kD) void recurrence_kernel(ScanArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-// Fast-mode single-token step (decode, t = 1, no history), same inputs and
-// outputs as recurrence_kernel<true>: wave 0 forms the q / k L2 norms with lane
-// shuffles, q and k reach the threads through LDS as float4, the state's key
+// Fast-mode step, same inputs and outputs as recurrence_kernel<true> (t tokens
+// per group, optional per-token history; each token's arithmetic is the same
+// whatever t is, so a verify block matches one-token decode steps bit for
+// bit): wave 0 forms the q / k L2 norms with lane shuffles, q and k reach the
+// threads through LDS as float4, the state's key
 // rows are split four ways among lanes (fp32 dot products summed in another
 // order than the exact step), and the scalar functions use the hardware exp2 /
 // log2 / reciprocal / rsqrt.  The bf16 rounding points of the exact step (the
@@ -301,7 +303,8 @@ __device__ __forceinline__ void fast_gates(const ScanArgs& p, int hv, int row, f
 // One thread's share of the delta rule: its 32 state values s (key rows
 // 32 part .. of value column i) are decayed, their k dot product is summed
 // over the four parts, the column's delta applied, the new values stored
-// through sp; returns the column's q dot product (summed over the parts).
+// through sp when it is not null; returns the column's q dot product (summed
+// over the parts).
 __device__ __forceinline__ float fast_delta(float (&s)[kFastRows], float* sp, const float4* ks4,
                                             const float4* qs4, int part, float gdecay,
                                             float beta, float vi) {
@@ -339,8 +342,10 @@ __device__ __forceinline__ float fast_delta(float (&s)[kFastRows], float* sp, co
     o2 = fmaf_(s[d + 2], qv4.z, o2);
     o3 = fmaf_(s[d + 3], qv4.w, o3);
   }
+  if (sp) {
 #pragma unroll
-  for (int d = 0; d < kFastRows; ++d) sp[size_t(d) * kD] = s[d];
+    for (int d = 0; d < kFastRows; ++d) sp[size_t(d) * kD] = s[d];
+  }
   float os = (o0 + o1) + (o2 + o3);
   os = os + __shfl_xor(os, 16, 64);
   os = os + __shfl_xor(os, 32, 64);
@@ -355,7 +360,7 @@ __device__ __forceinline__ float fast_sq_part(float yo, int part) {
 
 __global__ __launch_bounds__(kFastThreads) void recurrence_fast_kernel(ScanArgs p) {
   const int hv = blockIdx.x;
-  const int row = blockIdx.y;  // one token per group
+  const int g = blockIdx.y;  // group: p.t consecutive tokens of one slot
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 15, part = lane >> 4;
   const int i = wave * 16 + c;  // value column
@@ -363,34 +368,49 @@ __global__ __launch_bounds__(kFastThreads) void recurrence_fast_kernel(ScanArgs 
   const int hk = hv / (hv_heads / hk_heads);
   __shared__ float4 qs4[kD / 4], ks4[kD / 4];
   __shared__ float red[kFastThreads / 64];
-  float* sp = p.state + (size_t(p.slots[row]) * hv_heads + hv) * kD * kD +
-              size_t(part * kFastRows) * kD + i;
+  const size_t my_off = size_t(part * kFastRows) * kD + i;
+  float* sp = p.state + (size_t(p.slots[g]) * hv_heads + hv) * kD * kD + my_off;
   float s[kFastRows];
 #pragma unroll
   for (int d = 0; d < kFastRows; ++d) s[d] = sp[size_t(d) * kD];
-  const uint16_t* cr = p.conv_out + size_t(row) * p.conv_stride;
-  const float vi = bf16_to_f32(cr[2 * hk_heads * kD + hv * kD + i]);
-  const float zi = bf16_to_f32(p.z[size_t(row) * p.zab_stride + hv * kD + i]);
   const float nw = bf16_to_f32(p.norm_w[i]);
-  if (wave == 0)
-    fast_qk_norm(bf16_to_f32(cr[hk * kD + lane]), bf16_to_f32(cr[hk * kD + 64 + lane]),
-                 bf16_to_f32(cr[(hk_heads + hk) * kD + lane]),
-                 bf16_to_f32(cr[(hk_heads + hk) * kD + 64 + lane]), qs4, ks4);
-  float beta, gdecay;
-  fast_gates(p, hv, row, beta, gdecay);
-  __syncthreads();
-  const float yo = round_bf16(fast_delta(s, sp, ks4, qs4, part, gdecay, beta, vi));
-  const float ws = fast_sq_part(yo, part);
-  if (lane == 0) red[wave] = ws;
-  __syncthreads();
-  float tot = 0.0f;
+  // Every token runs the single-token step's arithmetic on the registers'
+  // state, so a block of t tokens gives the bits of t one-token launches.
+  // LDS reuse across tokens: qs4 / ks4 are rewritten only after the barrier
+  // that follows every wave's reads of them, red only after the next
+  // token's first barrier, which every wave reaches after reading it.
+  for (int step = 0; step < p.t; ++step) {
+    const size_t row = size_t(g) * p.t + step;
+    const uint16_t* cr = p.conv_out + row * p.conv_stride;
+    const float vi = bf16_to_f32(cr[2 * hk_heads * kD + hv * kD + i]);
+    const float zi = bf16_to_f32(p.z[row * p.zab_stride + hv * kD + i]);
+    if (wave == 0)
+      fast_qk_norm(bf16_to_f32(cr[hk * kD + lane]), bf16_to_f32(cr[hk * kD + 64 + lane]),
+                   bf16_to_f32(cr[(hk_heads + hk) * kD + lane]),
+                   bf16_to_f32(cr[(hk_heads + hk) * kD + 64 + lane]), qs4, ks4);
+    float beta, gdecay;
+    fast_gates(p, hv, int(row), beta, gdecay);
+    __syncthreads();
+    // the state after this token: into the history row when there is one,
+    // else into the cache after the last token
+    float* dst = p.history ? p.history + (row * hv_heads + hv) * kD * kD + my_off
+                           : (step == p.t - 1 ? sp : nullptr);
+    const float yo = round_bf16(fast_delta(s, dst, ks4, qs4, part, gdecay, beta, vi));
+    const float ws = fast_sq_part(yo, part);
+    if (lane == 0) red[wave] = ws;
+    __syncthreads();
+    float tot = 0.0f;
 #pragma unroll
-  for (int w = 0; w < kFastThreads / 64; ++w) tot = tot + red[w];
-  const float inv = __builtin_amdgcn_rsqf(tot * (1.0f / kD) + p.eps);
-  if (part == 0) {
-    const float normed = round_bf16(nw * round_bf16(yo * inv));
-    p.y[size_t(row) * (size_t(hv_heads) * kD) + hv * kD + i] =
-        f32_to_bf16(normed * sigmoid_fast(zi));
+    for (int w = 0; w < kFastThreads / 64; ++w) tot = tot + red[w];
+    const float inv = __builtin_amdgcn_rsqf(tot * (1.0f / kD) + p.eps);
+    if (part == 0) {
+      const float normed = round_bf16(nw * round_bf16(yo * inv));
+      p.y[row * (size_t(hv_heads) * kD) + hv * kD + i] = f32_to_bf16(normed * sigmoid_fast(zi));
+    }
+  }
+  if (p.history) {
+#pragma unroll
+    for (int d = 0; d < kFastRows; ++d) sp[size_t(d) * kD] = s[d];
   }
 }
 
@@ -399,16 +419,17 @@ __global__ __launch_bounds__(kFastThreads) void recurrence_fast_kernel(ScanArgs 
 int gdn_recurrence_fast(const uint16_t* conv_out, int64_t conv_stride, const uint16_t* z,
                         const uint16_t* a, const uint16_t* b, int64_t zab_stride,
                         const float* a_log, const uint16_t* dt_bias, const uint16_t* norm_w,
-                        float eps, GdnDims d, int rows, const int32_t* slots, float* state,
-                        uint16_t* y, hipStream_t s) {
+                        float eps, GdnDims d, int groups, int t, const int32_t* slots,
+                        float* state, float* history, uint16_t* y, hipStream_t s) {
   if (d.dk != kD || d.dv != kD || d.hk <= 0 || d.hv % d.hk != 0) return MX_EUNSUPPORTED;
-  if (rows <= 0) return MX_OK;
+  if (groups <= 0) return MX_OK;
+  if (t < 1) return MX_EINVAL;
   ScanArgs p{};
   p.conv_out = conv_out; p.conv_stride = conv_stride; p.z = z; p.a = a; p.b = b;
   p.zab_stride = zab_stride; p.a_log = a_log; p.dt_bias = dt_bias; p.norm_w = norm_w; p.eps = eps;
-  p.hk_heads = d.hk; p.hv_heads = d.hv; p.t = 1; p.slots = slots; p.state = state;
-  p.history = nullptr; p.y = y;
-  hipLaunchKernelGGL(recurrence_fast_kernel, dim3(d.hv, rows), dim3(kFastThreads), 0, s, p);
+  p.hk_heads = d.hk; p.hv_heads = d.hv; p.t = t; p.slots = slots; p.state = state;
+  p.history = history; p.y = y;
+  hipLaunchKernelGGL(recurrence_fast_kernel, dim3(d.hv, groups), dim3(kFastThreads), 0, s, p);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 

@@ -206,12 +206,13 @@ struct GdnDims {
 int gdn_conv(const uint16_t* qkv, int64_t row_stride, int groups, int t, const int32_t* slots,
              uint16_t* conv_state, const float* conv_w, int channels, int conv_k,
              uint16_t* out, int64_t out_stride, uint16_t* window_history, hipStream_t s);
-// fast-mode single-token step (t = 1 per group, no history), gdn.hip
+// fast-mode step (t tokens per group, optional history; every token gives the
+// bits of a one-token call), gdn.hip
 int gdn_recurrence_fast(const uint16_t* conv_out, int64_t conv_stride, const uint16_t* z,
                         const uint16_t* a, const uint16_t* b, int64_t zab_stride,
                         const float* a_log, const uint16_t* dt_bias, const uint16_t* norm_w,
-                        float eps, GdnDims d, int rows, const int32_t* slots, float* state,
-                        uint16_t* y, hipStream_t s);
+                        float eps, GdnDims d, int groups, int t, const int32_t* slots,
+                        float* state, float* history, uint16_t* y, hipStream_t s);
 int gdn_recurrence(const uint16_t* conv_out, int64_t conv_stride, const uint16_t* z,
                    const uint16_t* a, const uint16_t* b, int64_t zab_stride, const float* a_log,
                    const uint16_t* dt_bias, const uint16_t* norm_w, float eps, GdnDims d,

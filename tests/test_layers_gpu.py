@@ -293,8 +293,54 @@ def test_gdn_recurrence_fast_within_tolerance(mx, orc, groups):
     mx.check(mx.lib.mx_gdn_recurrence_fast(dconv.ptr, conv.shape[1], dzab.ptr,
                                            dzab.ptr + 2 * hv * 128, dzab.ptr + 2 * (hv * 128 + hv),
                                            zab.shape[1], dal.ptr, ddt.ptr, dnw.ptr, eps,
-                                           C.byref(dims), groups, dsl.ptr, dst.ptr, y.ptr, None))
+                                           C.byref(dims), groups, 1, dsl.ptr, dst.ptr, None, y.ptr,
+                                           None))
     st = dst.numpy()
     assert np.abs(st - st_w).max() <= 1e-4 * np.abs(st_w).max()
     got, want = bf(y.numpy()).astype(np.float64), bf(y_w).astype(np.float64)
     assert np.all(np.abs(got - want) <= 2e-2 * np.abs(want) + 1e-2)
+
+
+@pytest.mark.parametrize("groups,t", [(1, 4), (2, 3), (1, 8)])
+def test_gdn_recurrence_fast_block_equals_one_token_steps(mx, orc, groups, t):
+    """A fast-mode block of t tokens per group (the engine's verify and prefill
+    form) gives the bits of t one-token fast calls (the decode step): every y
+    row, the history's state after every token, and the final cached state.
+    Speculative decoding's greedy acceptance is lossless only with this."""
+    hk, hv, S = 16, 32, 6
+    rows = groups * t
+    conv, z, a, b, a_log, dt, norm_w = _gdn_inputs(orc, rows, hk, hv, 700 + rows)
+    rng = np.random.default_rng(97)
+    state = (rng.standard_normal((S, hv, 128, 128)) * 0.05).astype(np.float32)
+    slots = rng.choice(S, groups, replace=False).astype(np.int32)
+    zab = np.ascontiguousarray(np.concatenate([z, a, b], axis=1))
+    cs, zs = conv.shape[1], zab.shape[1]
+    dims = gdn_dims(mx, hk, hv)
+    eps = 1e-6
+    dconv, dzab, dal, ddt, dnw, dsl = (dev(mx, v) for v in (conv, zab, a_log, dt, norm_w, slots))
+
+    def call(r0, g, tt, slot_ptr, st, hist, y):
+        zp = dzab.ptr + 2 * r0 * zs
+        mx.check(mx.lib.mx_gdn_recurrence_fast(dconv.ptr + 2 * r0 * cs, cs, zp, zp + 2 * hv * 128,
+                                               zp + 2 * (hv * 128 + hv), zs, dal.ptr, ddt.ptr,
+                                               dnw.ptr, eps, C.byref(dims), g, tt, slot_ptr,
+                                               st.ptr, hist, y.ptr, None))
+
+    st_b = dev(mx, state)
+    hist = mx.DeviceArray((rows, hv, 128, 128), np.float32)
+    y_b = mx.DeviceArray((rows, hv * 128), np.uint16)
+    call(0, groups, t, dsl.ptr, st_b, hist.ptr, y_b)
+    st_s = dev(mx, state)
+    y_s = mx.DeviceArray((1, hv * 128), np.uint16)
+    y_want = np.empty((rows, hv * 128), np.uint16)
+    h_want = np.empty((rows, hv, 128, 128), np.float32)
+    for step in range(t):
+        for g in range(groups):
+            r = g * t + step
+            call(r, 1, 1, dsl.ptr + 4 * g, st_s, None, y_s)
+            y_want[r] = y_s.numpy()[0]
+            h_want[r] = st_s.numpy()[slots[g]]
+    assert (y_b.numpy() == y_want).all()
+    assert (hist.numpy() == h_want).all()
+    assert (st_b.numpy() == st_s.numpy()).all()
+    assert not (st_b.numpy()[slots] == state[slots]).all()
