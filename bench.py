@@ -466,12 +466,16 @@ def bench_gdn_decode_config1(mx, args):
         per_b[rows] = {"us": round(sec * 1e6, 2), "rows_per_s": round(rows / sec, 1),
                        "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
         log(f"gdn-decode-config1: B={rows} {sec * 1e6:.2f} us/step, {gbs:.0f} GB/s")
-    reps, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < 10.0:
-        orc.gdn_recurrence(conv, z, a, b, a_log, dt, norm_w, eps, hk, hv, rows_max, 1, sl, st0)
-        reps += 1
-    cpu_dt = (time.perf_counter() - t0) / reps
     b8 = per_b[8]
+    cpu = None
+    if not args.no_cpu_baseline:
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < 10.0:
+            orc.gdn_recurrence(conv, z, a, b, a_log, dt, norm_w, eps, hk, hv, rows_max, 1, sl, st0)
+            reps += 1
+        cpu_dt = (time.perf_counter() - t0) / reps
+        cpu = {"value": round(rows_max / cpu_dt, 2), "unit": "tok/s", "cores": orc.num_threads(),
+               "kind": "port", "sample": f"{reps} oracle B=8 steps in 10s (first {cpu_once:.3f}s)"}
     return {
         "metric": METRIC, "value": b8["rows_per_s"], "unit": "tok/s (rows stepped per second)",
         "ms_per_step": b8["us"] / 1e3,
@@ -484,9 +488,7 @@ def bench_gdn_decode_config1(mx, args):
                      "achieved": b8["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": b8["frac"], "traffic": None,
                      "algorithmic_bytes_per_launch": 8 * GDN_DECODE_BYTES_PER_ROW},
-        "cpu_baseline": {"value": round(rows_max / cpu_dt, 2), "unit": "tok/s",
-                         "cores": orc.num_threads(), "kind": "port",
-                         "sample": f"{reps} oracle B=8 steps in 10s (first {cpu_once:.3f}s)"},
+        "cpu_baseline": cpu,
     }
 
 
@@ -561,7 +563,30 @@ def bench_moe_config2(mx, args):
                        "bytes": int(alg), "gbs": round(gbs, 1),
                        "frac": round(gbs / HBM_PEAK_GBS, 4), "rows_per_s": round(rows / sec, 1)}
         log(f"moe-config2: B={rows} {sec * 1e6:.2f} us/block, U={u:.1f}, {gbs:.0f} GB/s")
-    # CPU baseline: the oracle's B = 8 block (router QMV, route, experts, slot sum)
+    b8 = per_b[8]
+    cpu = None if args.no_cpu_baseline else moe_cpu_baseline(orc, gate, up, down, sg, su, sd,
+                                                             router, xs)
+    return {
+        "metric": METRIC, "value": b8["rows_per_s"], "unit": "tok/s (rows per second)",
+        "ms_per_step": b8["us"] / 1e3,
+        "dtype": "affine u4 (gate/up, router) / u5 (down) codes x bf16 -> fp32 acc",
+        "config": {"workload": "moe-config2", "experts": E, "top_k": k, "hidden": H,
+                   "inter": I, "shared_inter": I, "rotated_input_batches": n_x,
+                   "per_batch": {str(b_): v for b_, v in per_b.items()}},
+        "roofline": {"bound": "hbm",
+                     "kernel": "router dense_kernel + gate_up_persist_kernel + down_hc_kernel (B=8)",
+                     "achieved": b8["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": b8["frac"], "traffic": None,
+                     "algorithmic_bytes_per_launch": b8["bytes"]},
+        "cpu_baseline": cpu,
+    }
+
+
+def moe_cpu_baseline(orc, gate, up, down, sg, su, sd, router, xs):
+    """The oracle's B = 8 MoE block (router QMV, route, experts, slot sum),
+    repeated for about 10 s on this host."""
+    E, H, k = gate.experts, gate.k, 10
+    n_x = xs.shape[0]
     # the oracle's structs view host arrays: keep the arrays alive beside them
     host_b = [bk.host() for bk in (gate, up, down)]
     host_s = [w.host() for w in (sg, su, sd)]
@@ -577,24 +602,9 @@ def bench_moe_config2(mx, args):
         orc.moe_reduce(p, k)
         reps += 1
     cpu_dt = (time.perf_counter() - t0) / reps
-    b8 = per_b[8]
-    return {
-        "metric": METRIC, "value": b8["rows_per_s"], "unit": "tok/s (rows per second)",
-        "ms_per_step": b8["us"] / 1e3,
-        "dtype": "affine u4 (gate/up, router) / u5 (down) codes x bf16 -> fp32 acc",
-        "config": {"workload": "moe-config2", "experts": E, "top_k": k, "hidden": H,
-                   "inter": I, "shared_inter": I, "rotated_input_batches": n_x,
-                   "per_batch": {str(b_): v for b_, v in per_b.items()}},
-        "roofline": {"bound": "hbm",
-                     "kernel": "router dense_kernel + gate_up_persist_kernel + down_hc_kernel (B=8)",
-                     "achieved": b8["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": b8["frac"], "traffic": None,
-                     "algorithmic_bytes_per_launch": b8["bytes"]},
-        "cpu_baseline": {"value": round(8 / cpu_dt, 2), "unit": "tok/s",
-                         "cores": orc.num_threads(), "kind": "port",
-                         "sample": f"{reps} oracle B=8 MoE blocks (router, route, experts, "
-                                   f"slot sum) in {reps * cpu_dt:.1f}s"},
-    }
+    return {"value": round(8 / cpu_dt, 2), "unit": "tok/s", "cores": orc.num_threads(),
+            "kind": "port", "sample": f"{reps} oracle B=8 MoE blocks (router, route, experts, "
+                                      f"slot sum) in {reps * cpu_dt:.1f}s"}
 
 
 def bench_mtp_config4(mx, args):
