@@ -358,6 +358,10 @@ __device__ __forceinline__ float fast_sq_part(float yo, int part) {
   return wave_sum(part == 0 ? yo * yo : 0.0f);
 }
 
+// BLOCK = false: the one-token decode form (t = 1, no history), with no token
+// loop in the code; BLOCK = true: t tokens per group and optional history.
+// Both run the same per-token arithmetic, so their bits agree.
+template <bool BLOCK>
 __global__ __launch_bounds__(kFastThreads) void recurrence_fast_kernel(ScanArgs p) {
   const int hv = blockIdx.x;
   const int g = blockIdx.y;  // group: p.t consecutive tokens of one slot
@@ -379,8 +383,10 @@ __global__ __launch_bounds__(kFastThreads) void recurrence_fast_kernel(ScanArgs 
   // LDS reuse across tokens: qs4 / ks4 are rewritten only after the barrier
   // that follows every wave's reads of them, red only after the next
   // token's first barrier, which every wave reaches after reading it.
-  for (int step = 0; step < p.t; ++step) {
-    const size_t row = size_t(g) * p.t + step;
+  const int T = BLOCK ? p.t : 1;
+  float* const history = BLOCK ? p.history : nullptr;
+  for (int step = 0; step < T; ++step) {
+    const size_t row = size_t(g) * T + step;
     const uint16_t* cr = p.conv_out + row * p.conv_stride;
     const float vi = bf16_to_f32(cr[2 * hk_heads * kD + hv * kD + i]);
     const float zi = bf16_to_f32(p.z[row * p.zab_stride + hv * kD + i]);
@@ -393,8 +399,8 @@ __global__ __launch_bounds__(kFastThreads) void recurrence_fast_kernel(ScanArgs 
     __syncthreads();
     // the state after this token: into the history row when there is one,
     // else into the cache after the last token
-    float* dst = p.history ? p.history + (row * hv_heads + hv) * kD * kD + my_off
-                           : (step == p.t - 1 ? sp : nullptr);
+    float* dst = history ? history + (row * hv_heads + hv) * kD * kD + my_off
+                         : (step == T - 1 ? sp : nullptr);
     const float yo = round_bf16(fast_delta(s, dst, ks4, qs4, part, gdecay, beta, vi));
     const float ws = fast_sq_part(yo, part);
     if (lane == 0) red[wave] = ws;
@@ -408,7 +414,7 @@ __global__ __launch_bounds__(kFastThreads) void recurrence_fast_kernel(ScanArgs 
       p.y[row * (size_t(hv_heads) * kD) + hv * kD + i] = f32_to_bf16(normed * sigmoid_fast(zi));
     }
   }
-  if (p.history) {
+  if (history) {
 #pragma unroll
     for (int d = 0; d < kFastRows; ++d) sp[size_t(d) * kD] = s[d];
   }
@@ -429,7 +435,12 @@ int gdn_recurrence_fast(const uint16_t* conv_out, int64_t conv_stride, const uin
   p.zab_stride = zab_stride; p.a_log = a_log; p.dt_bias = dt_bias; p.norm_w = norm_w; p.eps = eps;
   p.hk_heads = d.hk; p.hv_heads = d.hv; p.t = t; p.slots = slots; p.state = state;
   p.history = history; p.y = y;
-  hipLaunchKernelGGL(recurrence_fast_kernel, dim3(d.hv, groups), dim3(kFastThreads), 0, s, p);
+  if (t == 1 && !history)
+    hipLaunchKernelGGL(recurrence_fast_kernel<false>, dim3(d.hv, groups), dim3(kFastThreads), 0, s,
+                       p);
+  else
+    hipLaunchKernelGGL(recurrence_fast_kernel<true>, dim3(d.hv, groups), dim3(kFastThreads), 0, s,
+                       p);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 

@@ -304,9 +304,10 @@ def test_gdn_recurrence_fast_within_tolerance(mx, orc, groups):
 @pytest.mark.parametrize("groups,t", [(1, 4), (2, 3), (1, 8)])
 def test_gdn_recurrence_fast_block_equals_one_token_steps(mx, orc, groups, t):
     """A fast-mode block of t tokens per group (the engine's verify and prefill
-    form) gives the bits of t one-token fast calls (the decode step): every y
-    row, the history's state after every token, and the final cached state.
-    Speculative decoding's greedy acceptance is lossless only with this."""
+    form, the kernel's looping instance) gives the bits of t one-token fast
+    calls (the decode step, its loop-free instance): every y row, the history's
+    state after every token, and the final cached state.  Speculative
+    decoding's greedy acceptance is lossless only with this."""
     hk, hv, S = 16, 32, 6
     rows = groups * t
     conv, z, a, b, a_log, dt, norm_w = _gdn_inputs(orc, rows, hk, hv, 700 + rows)
