@@ -451,6 +451,16 @@ mx_status mx_engine_decode_batch(mx_engine* e, const int32_t* slots, const uint3
                                  int32_t rows, uint32_t* next);
 mx_status mx_engine_decode_rows(mx_engine* e, const int32_t* slots, const uint32_t* tokens,
                                 int32_t rows, uint32_t* next);
+/* mx_engine_decode_batch that also returns what HybridModel::decode_batch
+ * returns (src/batching.rs:34-170, `Ok((logits, hidden))` at 169): the
+ * step's bf16 logits [rows, vocab] and final hidden streams bf16
+ * [rows, hc * hidden] (before the mixer), written to caller-owned device
+ * buffers; either may be NULL.  `next` holds the greedy tokens, which are
+ * the argmax of these logits (largest, lowest id on ties).  Same equal-offset
+ * rule as mx_engine_decode_batch. */
+mx_status mx_engine_decode_batch_outputs(mx_engine* e, const int32_t* slots,
+                                         const uint32_t* tokens, int32_t rows, uint32_t* next,
+                                         uint16_t* logits, uint16_t* hidden);
 mx_status mx_engine_prefill(mx_engine* e, int32_t slot, const uint32_t* tokens, int32_t count,
                             uint32_t* next);
 mx_status mx_engine_verify(mx_engine* e, int32_t slot, const uint32_t* tokens, int32_t count,
@@ -495,6 +505,18 @@ mx_status mx_engine_profile_step(mx_engine* e, const int32_t* slots, const uint3
  * engine stream.  Caches are not changed. */
 mx_status mx_engine_time_experts(mx_engine* e, int32_t rows, mx_expert_timing* out);
 mx_status mx_engine_read(mx_engine* e, const char* what, void* host, size_t bytes);
+/* Test hook (no reference counterpart): one eager decode step of `rows`
+ * rows at their own offsets in which every layer i takes its input streams
+ * from h_in[i] (host bf16 [layers + 1][rows][hc * hidden]) instead of the
+ * previous layer's output, so each layer can be compared with a CPU model
+ * fed the same inputs ("teacher forcing").  Layer i's output streams go to
+ * h_out[i] (host, [layers][rows][hc * hidden]) and its top-k expert ids to
+ * ids_out[i] (host uint32 [layers][rows][top_k]); the mixer and the head run
+ * on h_in[layers] and write `next`.  Caches and offsets advance as in
+ * mx_engine_decode_rows. */
+mx_status mx_engine_decode_forced(mx_engine* e, const int32_t* slots, const uint32_t* tokens,
+                                  int32_t rows, const uint16_t* h_in, uint16_t* h_out,
+                                  uint32_t* ids_out, uint32_t* next);
 mx_status mx_engine_tensor(mx_engine* e, const char* name, void** device_ptr, size_t* bytes);
 
 /* mx_gdn_scan: the delta rule alone, on given inputs — the reference's

@@ -258,16 +258,20 @@ void mxo_attention(const uint16_t* q, const uint16_t* qkv, int64_t qkv_stride, i
 }
 
 /* RoPE table (reference src/rope.rs:20-24): inv_freq[i] = 1 / powf(theta, 2i/rot)
- * in fp32, angle = pos * inv_freq in double, cos/sin rounded to fp32. */
+ * in fp32; the angle is the fp32 product pos * inv_freq, as
+ * kernels/text_rope.metal computes it (`float angle = pos*float(inv_freq)`),
+ * so its rounding error grows with the position; cos/sin of that fp32 angle
+ * are evaluated in double and rounded to fp32 (the last ulp of metal::cos is
+ * parity unpinned). */
 void mxo_rope_table(int max_ctx, int rot, float theta, float* cos_out, float* sin_out) {
   const int half = rot / 2;
   for (int i = 0; i < half; ++i) {
     const float power = (float)(2 * i) / (float)rot;
     const float inv = 1.0f / powf(theta, power);
     for (int p = 0; p < max_ctx; ++p) {
-      const double a = (double)p * (double)inv;
-      cos_out[(int64_t)p * half + i] = (float)cos(a);
-      sin_out[(int64_t)p * half + i] = (float)sin(a);
+      const float a = (float)p * inv;
+      cos_out[(int64_t)p * half + i] = (float)cos((double)a);
+      sin_out[(int64_t)p * half + i] = (float)sin((double)a);
     }
   }
 }

@@ -21,7 +21,8 @@ _p = orc._p
 
 def rope_table(max_ctx: int, rot: int, theta: float):
     """inv_freq = 1 / powf(theta, 2i/rot) in fp32 (reference src/rope.rs:20-24);
-    angle = pos * inv_freq in float64; cos/sin rounded to fp32 (libm, in C)."""
+    angle = the fp32 product pos * inv_freq (kernels/text_rope.metal); cos/sin
+    of that angle rounded to fp32 (libm, in C)."""
     half = rot // 2
     cs = np.empty((max_ctx, half), np.float32)
     sn = np.empty((max_ctx, half), np.float32)
@@ -209,6 +210,7 @@ class Model:
             orc.lib.mxo_hc_write(C.byref(L["out"]), _p(y), rows, hc, _p(h), _p(inj))
         mixed, inj = self._hc_forward(L["mlp_hc"], h, rows)
         logits = self._qmv(L["router"], mixed)
+        self.last_router.append(logits.copy())
         E = c["experts"]
         ids, scores, factor = orc.moe_route(np.ascontiguousarray(logits[:, :E]),
                                             np.ascontiguousarray(logits[:, E]), c["top_k"])
@@ -223,9 +225,14 @@ class Model:
         return h
 
     def step(self, tokens, slots, pos, groups, t, history=None):
-        self.last_ids = []  # routing of each MoE layer in this step (test inspection)
         """One engine step over rows (slot, position); GDN rows grouped as
-        `groups` sequences of `t` tokens.  Returns greedy next tokens."""
+        `groups` sequences of `t` tokens.  Returns greedy next tokens.  For
+        inspection by tests, the step keeps each MoE layer's routing
+        (last_ids), router logits (last_router) and each layer's input
+        streams, then the final ones (layer_in, len(layers) + 1 entries)."""
+        self.last_ids = []
+        self.last_router = []
+        self.layer_in = []
         c = self.c
         rows = len(tokens)
         H, hc = self.H, self.hc
@@ -236,8 +243,10 @@ class Model:
         pos_a = np.ascontiguousarray(pos, np.int32)
         gdn_slots = np.array([slots[g * t] * self.n_gdn for g in range(groups)], np.int32)
         for i, L in zip(self.layer_ids, self.layers):
+            self.layer_in.append(h.copy())
             h = self._run_layer(L, self.attn[i], self.cache_index[i], h, rows, slots_a, pos_a,
                                 gdn_slots, groups, t, history)
+        self.layer_in.append(h.copy())
         self.hidden = h.copy()
         mixed, _ = self._hc_forward(self.mixer, h, rows)
         self.last_mixed = mixed
@@ -253,6 +262,7 @@ class Model:
         H, hc = self.H, self.hc
         rows = len(tokens)
         self.last_ids = []
+        self.last_router = []
         tok = np.ascontiguousarray(tokens, np.uint32)
         emb = np.empty((rows, H), np.uint16)
         orc.lib.mxo_embed(C.byref(self.embed), _p(tok), rows, 1, _p(emb))

@@ -179,6 +179,8 @@ def _load() -> C.CDLL:
         "mx_engine_offset": ([vp, i32], i32),
         "mx_engine_decode_batch": ([vp, vp, vp, i32, vp], i32),
         "mx_engine_decode_rows": ([vp, vp, vp, i32, vp], i32),
+        "mx_engine_decode_batch_outputs": ([vp, vp, vp, i32, vp, vp, vp], i32),
+        "mx_engine_decode_forced": ([vp, vp, vp, i32, vp, vp, vp, vp], i32),
         "mx_engine_prefill": ([vp, i32, vp, i32, vp], i32),
         "mx_engine_verify": ([vp, i32, vp, i32, vp], i32),
         "mx_engine_commit": ([vp, i32, i32], i32),
@@ -409,6 +411,39 @@ class Engine:
         fn = lib.mx_engine_decode_batch if equal else lib.mx_engine_decode_rows
         check(fn(self.h, s.ctypes.data, t.ctypes.data, len(s), out.ctypes.data))
         return out
+
+    def decode_batch_outputs(self, slots, tokens, logits=True, hidden=True):
+        """mx_engine_decode_batch_outputs: (next tokens, bf16 logits [rows, vocab]
+        or None, bf16 hidden streams [rows, hc*hidden] or None)."""
+        s = np.ascontiguousarray(slots, np.int32)
+        t = self._u32(tokens)
+        rows = len(s)
+        out = np.empty(rows, np.uint32)
+        c = self.cfg
+        lg = DeviceArray((rows, c["vocab"]), np.uint16) if logits else None
+        hd = DeviceArray((rows, c["hc"] * c["hidden"]), np.uint16) if hidden else None
+        check(lib.mx_engine_decode_batch_outputs(self.h, s.ctypes.data, t.ctypes.data, rows,
+                                                 out.ctypes.data, lg.ptr if lg else None,
+                                                 hd.ptr if hd else None))
+        return out, (lg.numpy() if lg else None), (hd.numpy() if hd else None)
+
+    def decode_forced(self, slots, tokens, h_in):
+        """mx_engine_decode_forced: h_in bf16 [layers + 1, rows, hc*hidden];
+        returns (next tokens, per-layer outputs [layers, rows, hc*hidden],
+        per-layer expert ids [layers, rows, top_k])."""
+        s = np.ascontiguousarray(slots, np.int32)
+        t = self._u32(tokens)
+        rows = len(s)
+        c = self.cfg
+        h_in = np.ascontiguousarray(h_in, np.uint16)
+        assert h_in.shape == (c["layers"] + 1, rows, c["hc"] * c["hidden"]), h_in.shape
+        h_out = np.empty((c["layers"], rows, c["hc"] * c["hidden"]), np.uint16)
+        ids = np.empty((c["layers"], rows, c["top_k"]), np.uint32)
+        out = np.empty(rows, np.uint32)
+        check(lib.mx_engine_decode_forced(self.h, s.ctypes.data, t.ctypes.data, rows,
+                                          h_in.ctypes.data, h_out.ctypes.data, ids.ctypes.data,
+                                          out.ctypes.data))
+        return out, h_out, ids
 
     def prefill(self, slot, tokens) -> int:
         t = self._u32(tokens)

@@ -576,7 +576,8 @@ MX_ABI int32_t mx_engine_offset(mx_engine* e, int32_t slot) {
 }
 
 static mx_status decode_common(mx_engine* e, const int32_t* slots, const uint32_t* tokens,
-                               int32_t rows, uint32_t* next, bool equal, const char* what) {
+                               int32_t rows, uint32_t* next, bool equal, const char* what,
+                               uint16_t* logits = nullptr, uint16_t* hidden = nullptr) {
   MX_CHECK(e && slots && tokens && next, MX_EINVAL, std::string(what) + ": null pointer");
   MX_CHECK(rows >= 1 && rows <= 8, MX_EUNSUPPORTED, std::string(what) + ": rows must be in 1..8");
   for (int r = 0; r < rows; ++r)
@@ -588,8 +589,34 @@ static mx_status decode_common(mx_engine* e, const int32_t* slots, const uint32_
       MX_CHECK(engine_offset(*e->impl, slots[r]) == engine_offset(*e->impl, slots[0]), MX_ESTATE,
                std::string(what) + ": rows must share one cache offset");
   std::string err;
-  const int rc = engine_decode_rows(*e->impl, slots, tokens, rows, next, &err);
+  const int rc = (logits || hidden)
+                     ? engine_decode_outputs(*e->impl, slots, tokens, rows, next, logits, hidden, &err)
+                     : engine_decode_rows(*e->impl, slots, tokens, rows, next, &err);
   return engine_status(rc, err, what);
+}
+
+MX_ABI mx_status mx_engine_decode_batch_outputs(mx_engine* e, const int32_t* slots,
+                                                const uint32_t* tokens, int32_t rows,
+                                                uint32_t* next, uint16_t* logits,
+                                                uint16_t* hidden) {
+  return decode_common(e, slots, tokens, rows, next, true, "mx_engine_decode_batch_outputs",
+                       logits, hidden);
+}
+
+MX_ABI mx_status mx_engine_decode_forced(mx_engine* e, const int32_t* slots,
+                                         const uint32_t* tokens, int32_t rows,
+                                         const uint16_t* h_in, uint16_t* h_out,
+                                         uint32_t* ids_out, uint32_t* next) {
+  MX_CHECK(e && slots && tokens && h_in && h_out && ids_out && next, MX_EINVAL,
+           "mx_engine_decode_forced: null pointer");
+  MX_CHECK(rows >= 1 && rows <= 8, MX_EUNSUPPORTED, "mx_engine_decode_forced: rows must be in 1..8");
+  for (int r = 0; r < rows; ++r)
+    MX_CHECK(slot_ok(*e->impl, slots[r]), MX_EINVAL, "mx_engine_decode_forced: slot out of range");
+  MX_CHECK(tokens_ok(*e->impl, tokens, rows), MX_EINVAL,
+           "mx_engine_decode_forced: token outside vocabulary");
+  std::string err;
+  const int rc = engine_decode_forced(*e->impl, slots, tokens, rows, h_in, h_out, ids_out, next, &err);
+  return engine_status(rc, err, "mx_engine_decode_forced");
 }
 
 MX_ABI mx_status mx_engine_decode_batch(mx_engine* e, const int32_t* slots, const uint32_t* tokens,

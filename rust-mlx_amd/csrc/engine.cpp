@@ -360,8 +360,9 @@ int build(Engine& e) {
   MX_TRY(alloc(e, "verify.snap_conv", size_t(e.n_gdn) * (c.conv_k - 1) * e.cd * 2, &v));
   e.snap_conv = static_cast<uint16_t*>(v);
 
-  // RoPE table: inv_freq[i] = 1 / theta^(2i/rot) in fp32 (src/rope.rs:20-24),
-  // angle = pos * inv_freq in double, cos/sin rounded to fp32.
+  // RoPE table: inv_freq[i] = 1 / theta^(2i/rot) in fp32 (src/rope.rs:20-24);
+  // the angle is the fp32 product pos * inv_freq (kernels/text_rope.metal),
+  // cos/sin of that fp32 angle rounded to fp32.
   {
     const int half = c.rotary_dim / 2;
     std::vector<float> cs(size_t(c.max_context) * half), sn(cs.size());
@@ -369,9 +370,9 @@ int build(Engine& e) {
       const float power = float(2 * i) / float(c.rotary_dim);
       const float inv = 1.0f / ::powf(c.rope_theta, power);  // fp32 pow, as MLX's f32 power
       for (int p = 0; p < c.max_context; ++p) {
-        const double a = double(p) * double(inv);
-        cs[size_t(p) * half + i] = float(std::cos(a));
-        sn[size_t(p) * half + i] = float(std::sin(a));
+        const float a = float(p) * inv;
+        cs[size_t(p) * half + i] = float(std::cos(double(a)));
+        sn[size_t(p) * half + i] = float(std::sin(double(a)));
       }
     }
     MX_TRY(alloc(e, "rope.cos", cs.size() * 4, &v));
@@ -688,12 +689,14 @@ int record_head(Engine& e, int rows, bool logits) {
   int parts = 0;
   float* maxima = static_cast<float*>(e.head_ws);
   uint32_t* indices = reinterpret_cast<uint32_t*>(maxima + size_t(head_parts(c.vocab, c.hidden)) * 8);
-  if (!e.exact && skinny_supported(e.head) && e.head.k % 512 == 0 && e.head.k <= 2048)
-    MX_TRY(skinny_head(e.head, e.mixed, rows, maxima, indices, &parts, e.stream));
+  const bool fast = !e.exact && skinny_supported(e.head) && e.head.k % 512 == 0 && e.head.k <= 2048;
+  if (fast)  // the matrix-core head writes the logits it ranks
+    MX_TRY(skinny_head(e.head, e.mixed, rows, maxima, indices, &parts, e.stream,
+                       logits ? e.logits : nullptr));
   else
     MX_TRY(head_partials(e.head, e.mixed, rows, maxima, indices, &parts, e.stream));
   MX_TRY(argmax_reduce(maxima, indices, rows, parts, rt->next, e.stream));
-  if (logits) {
+  if (logits && !fast) {  // the exact projection's bf16 logits (same order as the exact head)
     ProjEpilogue pl{};
     pl.mode = kPlain;
     pl.y = e.logits;
@@ -852,6 +855,8 @@ int engine_clone_slot(Engine& e, int src, int dst) {
   }
   MX_HIP(hipStreamSynchronize(e.stream));
   e.offsets[dst] = e.offsets[src];
+  // the copy replaces the caches a pending verify block of dst would roll back
+  if (dst == e.verify_slot) e.verify_slot = -1;
   return MX_OK;
 }
 
@@ -882,6 +887,78 @@ int engine_decode_rows(Engine& e, const int32_t* slots, const uint32_t* tokens, 
   return MX_OK;
 }
 
+// decode_rows, then the step's logits (bf16 [rows, vocab]) and final hidden
+// streams (bf16 [rows, hc * hidden]) into caller device buffers (either may be
+// null), as HybridModel::decode_batch returns them (src/batching.rs:34-170).
+int engine_decode_outputs(Engine& e, const int32_t* slots, const uint32_t* tokens, int rows,
+                          uint32_t* next, uint16_t* logits, uint16_t* hidden, std::string* err) {
+  const auto& c = e.cfg;
+  const bool saved = e.want_logits;
+  e.want_logits = saved || logits != nullptr;
+  const int rc = engine_decode_rows(e, slots, tokens, rows, next, err);
+  e.want_logits = saved;
+  MX_TRY(rc);
+  if (logits)
+    MX_HIP(hipMemcpyAsync(logits, e.logits, size_t(rows) * c.vocab * 2, hipMemcpyDeviceToDevice,
+                          e.stream));
+  if (hidden)
+    MX_HIP(hipMemcpyAsync(hidden, e.h, size_t(rows) * c.hc * c.hidden * 2,
+                          hipMemcpyDeviceToDevice, e.stream));
+  MX_HIP(hipStreamSynchronize(e.stream));
+  return MX_OK;
+}
+
+// Teacher-forced decode step (a test hook): each layer i runs eagerly on the
+// given input streams h_in[i] (host bf16 [layers + 1][rows][hc * hidden])
+// instead of the previous layer's output; its output streams go to h_out[i]
+// and its routing to ids_out[i] ([layers][rows][top_k]); the mixer and head
+// run on h_in[layers].  Caches are updated and offsets advance as in a step.
+int engine_decode_forced(Engine& e, const int32_t* slots, const uint32_t* tokens, int rows,
+                         const uint16_t* h_in, uint16_t* h_out, uint32_t* ids_out,
+                         uint32_t* next, std::string* err) {
+  const auto& c = e.cfg;
+  for (int r = 0; r < rows; ++r) {
+    for (int q = 0; q < r; ++q)
+      if (slots[q] == slots[r]) {
+        *err = "a slot appears twice in one step";
+        return MX_EINVAL;
+      }
+    if (e.offsets[slots[r]] >= c.max_context) {
+      *err = "slot context is full";
+      return MX_ESTATE;
+    }
+    e.host_rows->tokens[r] = tokens[r];
+    e.host_rows->slots[r] = slots[r];
+    e.host_rows->gdn_slots[r] = slots[r] * e.n_gdn;
+    e.host_rows->pos[r] = e.offsets[slots[r]];
+  }
+  const size_t HS = size_t(rows) * c.hc * c.hidden;
+  MX_HIP(hipMemcpyAsync(e.dev_rows, e.host_rows, sizeof(Engine::RowTable), hipMemcpyHostToDevice,
+                        e.stream));
+  for (size_t i = 0; i < e.layers.size(); ++i) {
+    MX_HIP(hipMemcpyAsync(e.h, h_in + i * HS, HS * 2, hipMemcpyHostToDevice, e.stream));
+    MX_TRY(record_layer(e, e.layers[i], rows, rows, 1, false));
+    MX_HIP(hipMemcpyAsync(h_out + i * HS, e.h, HS * 2, hipMemcpyDeviceToHost, e.stream));
+    MX_HIP(hipMemcpyAsync(ids_out + i * size_t(rows) * c.top_k, e.ids,
+                          size_t(rows) * c.top_k * 4, hipMemcpyDeviceToHost, e.stream));
+    MX_HIP(hipStreamSynchronize(e.stream));
+  }
+  MX_HIP(hipMemcpyAsync(e.h, h_in + e.layers.size() * HS, HS * 2, hipMemcpyHostToDevice,
+                        e.stream));
+  MX_TRY(hc_forward(e, e.mixer, rows, e.mixed, nullptr));
+  MX_TRY(record_head(e, rows, e.want_logits));
+  MX_HIP(hipMemcpyAsync(e.host_rows->next, e.dev_rows->next, sizeof(uint32_t) * rows,
+                        hipMemcpyDeviceToHost, e.stream));
+  MX_HIP(hipStreamSynchronize(e.stream));
+  std::memcpy(next, e.host_rows->next, sizeof(uint32_t) * rows);
+  e.last_rows = rows;
+  for (int r = 0; r < rows; ++r) {
+    e.offsets[slots[r]] += 1;
+    if (slots[r] == e.verify_slot) e.verify_slot = -1;
+  }
+  return MX_OK;
+}
+
 // One chunk of up to 8 consecutive tokens of one slot (prefill or verify).
 int engine_block(Engine& e, int slot, const uint32_t* tokens, int count, bool history,
                  uint32_t* next, std::string* err) {
@@ -895,6 +972,9 @@ int engine_block(Engine& e, int slot, const uint32_t* tokens, int count, bool hi
     e.host_rows->pos[r] = e.offsets[slot] + r;
   }
   e.host_rows->gdn_slots[0] = slot * e.n_gdn;
+  // a prefill block (no history) moves the caches past any pending verify
+  // block of this slot, whose snapshot and history no longer apply
+  if (!history && slot == e.verify_slot) e.verify_slot = -1;
   MX_TRY(run_step(e, count, 1, count, history, next));
   e.offsets[slot] += count;
   return MX_OK;

@@ -111,8 +111,9 @@ int skinny_down_hc(const uint16_t* h, const uint32_t* ids, const uint16_t* score
                    int inter, int shared_inter, const QBank& down, const QWeight& sdown,
                    uint16_t* hcs, hipStream_t s);
 int skinny_head_parts(int n);
+// logits (nullable): also writes the bf16 logits [m, n] that the argmax ranks
 int skinny_head(const QWeight& w, const uint16_t* x, int m, float* maxima, uint32_t* indices,
-                int* parts_out, hipStream_t s);
+                int* parts_out, hipStream_t s, uint16_t* logits = nullptr);
 // hyper-connection input projection on the matrix cores, two launches (hc.hip)
 bool hc_fused_supported(const QWeight& down, const QWeight& up, int hc, int hidden, int rank);
 size_t hc_fused_part_bytes(int n_down);
@@ -241,6 +242,11 @@ int engine_clone_slot(Engine& e, int src, int dst);
 int engine_offset(const Engine& e, int slot);
 int engine_decode_rows(Engine& e, const int32_t* slots, const uint32_t* tokens, int rows,
                        uint32_t* next, std::string* err);
+int engine_decode_outputs(Engine& e, const int32_t* slots, const uint32_t* tokens, int rows,
+                          uint32_t* next, uint16_t* logits, uint16_t* hidden, std::string* err);
+int engine_decode_forced(Engine& e, const int32_t* slots, const uint32_t* tokens, int rows,
+                         const uint16_t* h_in, uint16_t* h_out, uint32_t* ids_out,
+                         uint32_t* next, std::string* err);
 int engine_block(Engine& e, int slot, const uint32_t* tokens, int count, bool history,
                  uint32_t* next, std::string* err);
 int engine_verify(Engine& e, int slot, const uint32_t* tokens, int count, uint32_t* next,

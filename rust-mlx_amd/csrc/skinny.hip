@@ -737,7 +737,8 @@ __device__ __forceinline__ void better(float v, uint32_t id, float& best, uint32
 template <int BITS>
 __global__ __launch_bounds__(256) void head_kernel(QWeight w, const uint16_t* __restrict__ x,
                                                    int M, float* __restrict__ maxima,
-                                                   uint32_t* __restrict__ indices) {
+                                                   uint32_t* __restrict__ indices,
+                                                   uint16_t* __restrict__ logits) {
   extern __shared__ __align__(16) char lds[];
   __shared__ float yt[8 * 64];
   const int tg = blockIdx.x, parts = gridDim.x;
@@ -762,7 +763,11 @@ __global__ __launch_bounds__(256) void head_kernel(QWeight w, const uint16_t* __
     const int r = tg * 64 + lane;
     float best = u2f(0xff800000u);
     uint32_t best_id = 0xffffffffu;
-    if (r < n) better(round_bf16(yt[m * 64 + lane]), uint32_t(r), best, best_id);
+    if (r < n) {
+      better(round_bf16(yt[m * 64 + lane]), uint32_t(r), best, best_id);
+      // the bf16 logit the argmax ranks, when the caller wants the logits
+      if (logits) logits[size_t(m) * n + r] = f32_to_bf16(yt[m * 64 + lane]);
+    }
     for (int o = 32; o > 0; o >>= 1) {
       const float v = __shfl_xor(best, o, 64);
       const uint32_t id = uint32_t(__shfl_xor(int(best_id), o, 64));
@@ -1051,17 +1056,17 @@ int skinny_down_hc(const uint16_t* h, const uint32_t* ids, const uint16_t* score
 int skinny_head_parts(int n) { return (n + 63) / 64; }
 
 int skinny_head(const QWeight& w, const uint16_t* x, int m, float* maxima, uint32_t* indices,
-                int* parts_out, hipStream_t s) {
+                int* parts_out, hipStream_t s, uint16_t* logits) {
   if (!skinny_supported(w) || m < 1 || m > 8 || w.k % 512 != 0 || w.k / sk::kSuper > kStageSteps)
     return MX_EUNSUPPORTED;
   const int parts = skinny_head_parts(w.n);
   *parts_out = parts;
   const int lb = sk::stage_bytes(w.k / sk::kSuper);
   switch (w.bits) {
-    case 4: hipLaunchKernelGGL(head_kernel<4>, dim3(parts), dim3(256), lb, s, w, x, m, maxima, indices); break;
-    case 5: hipLaunchKernelGGL(head_kernel<5>, dim3(parts), dim3(256), lb, s, w, x, m, maxima, indices); break;
-    case 6: hipLaunchKernelGGL(head_kernel<6>, dim3(parts), dim3(256), lb, s, w, x, m, maxima, indices); break;
-    default: hipLaunchKernelGGL(head_kernel<8>, dim3(parts), dim3(256), lb, s, w, x, m, maxima, indices); break;
+    case 4: hipLaunchKernelGGL(head_kernel<4>, dim3(parts), dim3(256), lb, s, w, x, m, maxima, indices, logits); break;
+    case 5: hipLaunchKernelGGL(head_kernel<5>, dim3(parts), dim3(256), lb, s, w, x, m, maxima, indices, logits); break;
+    case 6: hipLaunchKernelGGL(head_kernel<6>, dim3(parts), dim3(256), lb, s, w, x, m, maxima, indices, logits); break;
+    default: hipLaunchKernelGGL(head_kernel<8>, dim3(parts), dim3(256), lb, s, w, x, m, maxima, indices, logits); break;
   }
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }

@@ -142,6 +142,24 @@ def test_commit_equals_sequential_decode(pair):
     assert a[0] == b[0]
 
 
+def test_commit_rejected_after_prefill_or_clone(mx, pair):
+    """A pending verify block is dropped by a later prefill of the slot or a
+    clone onto it: commit then reports MX_ESTATE instead of rolling the
+    caches back to a snapshot that no longer applies."""
+    eng, model = pair
+    eng.clone(0, 3)
+    eng.verify(3, [1, 2, 3])
+    eng.prefill(3, [4, 5])
+    with pytest.raises(mx.MxError) as e:
+        eng.commit(3, 1)
+    assert e.value.code == mx.MX_ESTATE
+    eng.verify(3, [1, 2])
+    eng.clone(0, 3)
+    with pytest.raises(mx.MxError) as e:
+        eng.commit(3, 1)
+    assert e.value.code == mx.MX_ESTATE
+
+
 def test_graph_replay_equals_eager(pair):
     eng, model = pair
     eng.clone(1, 3)

@@ -7,9 +7,10 @@ are bit-exact with the CPU oracle model running the same loop, and
 speculation is lossless (the tokens equal plain greedy decoding's).  With a
 16-token vocabulary the draft layer's guesses are accepted now and then, so
 the accept / commit / resynchronise paths with accepted > 0 run too.
-Fast mode: the loop runs end to end on the matrix-core kernels (its verify
-blocks and decode steps sum in different orders, so it is not compared with
-plain decoding token for token)."""
+Fast mode: the loop runs end to end on the matrix-core kernels; a fast verify
+block gives every position the bits of a one-token fast decode step, so the
+fast loop's tokens are checked against plain fast greedy decoding token for
+token (test_fast_speculation_is_lossless)."""
 import numpy as np
 import pytest
 

@@ -6,6 +6,9 @@ Each check is chosen so that a plausible slip (a dropped (1 + scale), a
 missing 1 / hc, a wrong stream or head mapping, a rotation sign) fails it."""
 import ctypes as C
 
+import ctypes as C
+import ctypes.util
+
 import numpy as np
 
 HC, EPS = 4, 1e-6
@@ -123,11 +126,23 @@ def _prep(orc, rows, pos, seed):
     return qkv, qn, kn, kc, vc, slots, pos, q_out, width, slot_stride
 
 
+def _inv_freq32(theta, rot):
+    """inv_freq[i] = 1 / powf(theta, 2i/rot) in fp32 (src/rope.rs:20-24), with
+    the C library's powf."""
+    libm = C.CDLL(ctypes.util.find_library("m"))
+    libm.powf.restype = C.c_float
+    libm.powf.argtypes = [C.c_float, C.c_float]
+    half = rot // 2
+    return np.array([np.float32(1.0) / np.float32(libm.powf(theta, np.float32(2 * i) / np.float32(rot)))
+                     for i in range(half)], np.float32)
+
+
 def _rope64(x, p):
-    """Rotate-half RoPE on the first ROT dims (kernels/text_rope.metal), float64."""
+    """Rotate-half RoPE on the first ROT dims (kernels/text_rope.metal): the
+    angle is the fp32 product pos * inv_freq, the rotation in float64."""
     half = ROT // 2
-    inv = THETA ** (-np.arange(half) * 2.0 / ROT)
-    a = p * inv
+    inv = _inv_freq32(THETA, ROT)
+    a = (np.float32(p) * inv).astype(np.float64)
     c, s = np.cos(a), np.sin(a)
     out = x.copy()
     out[..., :half] = x[..., :half] * c - x[..., half:ROT] * s
@@ -193,3 +208,27 @@ def test_attention_against_float64_softmax(orc):
             so = ko @ bf(q_out[r, h]) / np.sqrt(HD)
             wo = np.exp(so - so.max())
             assert not within(bf(out[r, h]), ((wo / wo.sum()) @ other) * sigmoid(gate[h]))
+
+
+def test_rope_angle_is_the_fp32_product(orc):
+    """kernels/text_rope.metal computes `float angle = pos*float(inv_freq)`:
+    the angle is rounded to fp32 before cos/sin, an error that grows with the
+    position (about 2.4e-4 rad at 4k, 1.6e-2 rad at 262k).  The oracle's table
+    equals cos/sin of that fp32 angle at positions near 4000 and 200000, and
+    differs there from the exact (float64) angle, so a table built from the
+    float64 product fails this test."""
+    rot, theta = 64, 1e7
+    half = rot // 2
+    maxc = 200_008
+    cos = np.empty((maxc, half), np.float32)
+    sin = np.empty((maxc, half), np.float32)
+    orc.lib.mxo_rope_table(maxc, rot, theta, orc._p(cos), orc._p(sin))
+    inv = _inv_freq32(theta, rot)
+    pos = np.array([0, 1, 3999, 4000, 4097, 199_999, 200_003], np.int64)
+    a32 = (pos.astype(np.float32)[:, None] * inv[None, :]).astype(np.float64)
+    assert (cos[pos] == np.cos(a32).astype(np.float32)).all()
+    assert (sin[pos] == np.sin(a32).astype(np.float32)).all()
+    a64 = pos.astype(np.float64)[:, None] * inv.astype(np.float64)[None, :]
+    far = pos >= 199_999
+    assert (sin[pos[far]] != np.sin(a64[far]).astype(np.float32)).any()
+    assert np.abs(a32[far] - a64[far]).max() > 1e-3
