@@ -108,12 +108,15 @@ static const uint32_t* qw_row_codes(const mxo_qw* w, int64_t row) {
 static const uint16_t* qw_row_s(const mxo_qw* w, int64_t row) { return w->scales + row * (w->k / w->gs); }
 static const uint16_t* qw_row_b(const mxo_qw* w, int64_t row) { return w->biases + row * (w->k / w->gs); }
 static float qw_dot(const mxo_qw* w, int64_t row, const uint16_t* x) {
+  if (w->mode == 1)
+    return mxo_xq_row(qw_row_codes(w, row), qw_row_s(w, row), qw_row_b(w, row), w->k, w->bits, x);
   return mxo_qmv_row(qw_row_codes(w, row), qw_row_s(w, row), qw_row_b(w, row), w->k, w->bits, w->gs, x);
 }
 static mxo_qw bank_expert(const mxo_qbank* b, int e) {
   const int64_t cs = (int64_t)b->n * b->k * b->bits / 32;
   const int64_t ss = (int64_t)b->n * (b->k / b->gs);
-  mxo_qw w = {b->codes + cs * e, b->scales + ss * e, b->biases + ss * e, b->n, b->k, b->bits, b->gs};
+  mxo_qw w = {b->codes + cs * e, b->scales + ss * e, b->biases + ss * e, b->n, b->k, b->bits, b->gs,
+              b->mode};
   return w;
 }
 

@@ -27,6 +27,9 @@ static float butterfly64(float* v) {
 static float row_dot(const mxo_qw* w, int64_t row, const uint16_t* x) {
   const int64_t wpr = ((int64_t)w->k * w->bits) >> 5;
   const int gpr = w->k / w->gs;
+  if (w->mode == 1)
+    return mxo_xq_row(w->codes + row * wpr, w->scales + row * gpr, w->biases + row * gpr, w->k,
+                      w->bits, x);
   return mxo_qmv_row(w->codes + row * wpr, w->scales + row * gpr, w->biases + row * gpr, w->k,
                      w->bits, w->gs, x);
 }

@@ -47,18 +47,29 @@ void mxo_qmv(const uint32_t* codes, const uint16_t* scales, const uint16_t* bias
 void mxo_qmv_f64(const uint32_t* codes, const uint16_t* scales, const uint16_t* biases, int n,
                  int k, int bits, int gs, const uint16_t* x, int m, double* y);
 
-/* ---- quantised weights as plain structs ---- */
+/* ---- exact-integer affine projection (xq.c): the engine's bit-exact path ---- */
+int mxo_xq_slices(int k);
+int64_t mxo_xq_int(uint16_t h, int eb);
+int mxo_xq_group_exp(const uint16_t* x);
+float mxo_xq_row(const uint32_t* row_words, const uint16_t* scale_row, const uint16_t* bias_row,
+                 int k, int bits, const uint16_t* x);
+void mxo_xq(const uint32_t* codes, const uint16_t* scales, const uint16_t* biases, int n, int k,
+            int bits, const uint16_t* x, int m, float* y);
+
+/* ---- quantised weights as plain structs ----
+ * mode 0: projections in the fixed fp32 order of mxo_qmv_row; mode 1: the
+ * exact-integer projection of mxo_xq_row (group size 64). */
 typedef struct mxo_qw {
   const uint32_t* codes;
   const uint16_t* scales;
   const uint16_t* biases;
-  int n, k, bits, gs;
+  int n, k, bits, gs, mode;
 } mxo_qw;
 typedef struct mxo_qbank {
   const uint32_t* codes;
   const uint16_t* scales;
   const uint16_t* biases;
-  int experts, n, k, bits, gs;
+  int experts, n, k, bits, gs, mode;
 } mxo_qbank;
 
 /* ---- A6-A9: MoE ---- */

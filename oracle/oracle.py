@@ -36,6 +36,11 @@ def _load() -> C.CDLL:
         "mxo_qmv_f64": ([vp, vp, vp, i32, i32, i32, i32, vp, i32, vp], None),
         "mxo_num_threads": ([], i32),
         "mxo_qmv_row": ([vp, vp, vp, i32, i32, i32, vp], f32),
+        "mxo_xq_slices": ([i32], i32),
+        "mxo_xq_int": ([C.c_uint16, i32], i64),
+        "mxo_xq_group_exp": ([vp], i32),
+        "mxo_xq_row": ([vp, vp, vp, i32, i32, vp], f32),
+        "mxo_xq": ([vp, vp, vp, i32, i32, i32, vp, i32, vp], None),
         "mxo_sigmoid_bf16": ([f32], f32),
         "mxo_softplus_bf16": ([f32], f32),
         "mxo_moe_route": ([vp, i64, vp, i64, i32, i32, i32, vp, vp, vp], None),
@@ -69,28 +74,37 @@ def _load() -> C.CDLL:
 lib = _load()
 
 
+# projection arithmetic of a weight struct: the fixed fp32 order of
+# mxo_qmv_row, or the exact-integer projection of mxo_xq_row
+FIXED, XQ = 0, 1
+
+
 class QW(C.Structure):
     _fields_ = [("codes", C.c_void_p), ("scales", C.c_void_p), ("biases", C.c_void_p),
-                ("n", C.c_int), ("k", C.c_int), ("bits", C.c_int), ("gs", C.c_int)]
+                ("n", C.c_int), ("k", C.c_int), ("bits", C.c_int), ("gs", C.c_int),
+                ("mode", C.c_int)]
 
 
 class QBank(C.Structure):
     _fields_ = [("codes", C.c_void_p), ("scales", C.c_void_p), ("biases", C.c_void_p),
                 ("experts", C.c_int), ("n", C.c_int), ("k", C.c_int), ("bits", C.c_int),
-                ("gs", C.c_int)]
+                ("gs", C.c_int), ("mode", C.c_int)]
 
 
-def qw(codes, scales, biases, n, k, bits, gs) -> QW:
+def qw(codes, scales, biases, n, k, bits, gs, mode=FIXED) -> QW:
     """Struct view of host arrays (the caller keeps the arrays alive)."""
     for a in (codes, scales, biases):
         assert a.flags["C_CONTIGUOUS"]
-    return QW(codes.ctypes.data, scales.ctypes.data, biases.ctypes.data, n, k, bits, gs)
+    assert mode == FIXED or gs == 64
+    return QW(codes.ctypes.data, scales.ctypes.data, biases.ctypes.data, n, k, bits, gs, mode)
 
 
-def qbank(codes, scales, biases, experts, n, k, bits, gs) -> QBank:
+def qbank(codes, scales, biases, experts, n, k, bits, gs, mode=FIXED) -> QBank:
     for a in (codes, scales, biases):
         assert a.flags["C_CONTIGUOUS"]
-    return QBank(codes.ctypes.data, scales.ctypes.data, biases.ctypes.data, experts, n, k, bits, gs)
+    assert mode == FIXED or gs == 64
+    return QBank(codes.ctypes.data, scales.ctypes.data, biases.ctypes.data, experts, n, k, bits, gs,
+                 mode)
 
 
 def _p(a: np.ndarray):
@@ -169,6 +183,16 @@ def qmv(codes, scales, biases, k, bits, gs, x) -> np.ndarray:
     n = codes.shape[0]
     y = np.empty((m, n), np.uint16)
     lib.mxo_qmv(_p(codes), _p(scales), _p(biases), n, k, bits, gs, _p(x), m, _p(y))
+    return y
+
+
+def xq(codes, scales, biases, k, bits, x) -> np.ndarray:
+    """Exact-integer projection (mxo_xq): fp32 y [m, n] before bf16 rounding."""
+    x = np.ascontiguousarray(x, np.uint16)
+    m = x.shape[0]
+    n = codes.shape[0]
+    y = np.empty((m, n), np.float32)
+    lib.mxo_xq(_p(codes), _p(scales), _p(biases), n, k, bits, _p(x), m, _p(y))
     return y
 
 
