@@ -96,8 +96,7 @@ def bench_config3(mx, args):
     rows = 8
     t0 = time.perf_counter()
     eng = mx.Engine(cfg)
-    if args.eager:
-        eng.set_flags(eager=True)
+    eng.set_flags(eager=args.eager, exact=args.exact)
     log(f"config3: engine built in {time.perf_counter() - t0:.1f}s "
         f"({cfg['layers']} layers, {cfg['experts']} experts)")
     rng = np.random.default_rng(3000)
@@ -131,6 +130,22 @@ def bench_config3(mx, args):
     ms_step = dt / args.steps * 1e3
     log(f"config3: {args.steps} steps x {rows} rows in {dt:.3f}s -> {tok_s:.1f} tok/s, "
         f"{ms_step:.3f} ms/step")
+    # the bit-exact path (exact mode: the fixed-order kernels the CPU oracle
+    # reproduces bit for bit) timed the same way on the same rows
+    exact_steps = max(args.steps // 4, 4)
+    eng.set_flags(exact=not args.exact, eager=args.eager)
+    for _ in range(2):
+        toks = eng.decode_batch(slots, toks, equal=False)
+    mx.check(mx.lib.mx_device_sync())
+    t0 = time.perf_counter()
+    for _ in range(exact_steps):
+        toks = eng.decode_batch(slots, toks, equal=False)
+    mx.check(mx.lib.mx_device_sync())
+    other_dt = (time.perf_counter() - t0) / exact_steps
+    other_tok_s = rows / other_dt
+    eng.set_flags(exact=args.exact, eager=args.eager)
+    log(f"config3: {'fast' if args.exact else 'exact'} mode {exact_steps} steps: "
+        f"{other_tok_s:.1f} tok/s, {other_dt * 1e3:.3f} ms/step")
     # a second profiled step after the timed loop (longer contexts), then the
     # expert kernels of all 48 layers back to back on that step's routing
     _, prof2 = eng.profile_step(slots, toks)
@@ -166,6 +181,8 @@ def bench_config3(mx, args):
             "expert_down_gbs": round(dn_gbs, 1),
             "prefill_s": round(prefill_s, 2),
             "context": "synthetic" if args.synthetic_context else "prefilled",
+            "mode": "exact" if args.exact else "fast",
+            ("fast_tok_s" if args.exact else "exact_tok_s"): round(other_tok_s, 2),
         },
         "roofline": {"bound": "hbm", "kernel": "moe gate_up_persist_kernel<4, 16, 4, 2, 0>",
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -709,6 +726,9 @@ def main() -> None:
     ap.add_argument("--roctx", action="store_true",
                     help="bracket the timed loop with roctxProfilerResume/Pause "
                          "(for rocprofv3 --selected-regions)")
+    ap.add_argument("--exact", action="store_true",
+                    help="time the exact (bit-exact, fixed-order) kernels as the headline "
+                         "path, and the matrix-core path beside it")
     ap.add_argument("--no-cpu-baseline", action="store_true",
                     help="skip the oracle CPU baseline (profiling runs)")
     args = ap.parse_args()

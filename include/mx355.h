@@ -188,6 +188,21 @@ mx_status mx_qmv(const mx_qweight* w, const uint16_t* x, int32_t m, uint16_t* y,
  * (matrix_kernel::project, src/matrix_kernel.rs:113-254,
  * kernels/matrix_packed.metal). */
 mx_status mx_qmm(const mx_qweight* w, const uint16_t* x, int32_t m, uint16_t* y, void* stream);
+/* ---- A3/A15: the exact-integer projection on the int8 matrix cores -------
+ * y[m, n] = bf16 of the affine projection computed exactly: per 64-value
+ * group, x is put on an integer grid anchored at the group's largest bf16
+ * exponent (X = trunc(x 2^(156 - Eb)), |X| < 2^30), P = sum X q and
+ * Q = sum X are exact integer sums (signed int8 digits of X against the
+ * codes on v_mfma_i32_16x16x64_i8), v = fma(P, s, Q b) 2^(Eb - 156) in fp64,
+ * groups added in fp64 in order within fixed slices of eight groups (one
+ * slice below k = 1024), slices in order, one rounding to fp32, then bf16.
+ * Bit-exact with the CPU oracle (oracle/xq.c); no result depends on the
+ * number of rows or the launch shape.  1 <= m <= 8, group_size 64, k a
+ * multiple of 64 up to 512 or of 512 up to 8192.  The product path of the
+ * decode engine's exact mode.  Replaces the same reference interfaces as
+ * mx_qmv (src/qmv_kernel.rs:49-180, kernels/verify_qmv.{h,metal}: the
+ * affine formula of verify_qmv.h:112). */
+mx_status mx_xq(const mx_qweight* w, const uint16_t* x, int32_t m, uint16_t* y, void* stream);
 /* mx_qmm_conv: mx_qmm (4-bit, 1..8 rows, one token per row) with the GDN
  * causal conv fused into its output: columns below conv_channels are conv
  * channels, convolved with the slot's cached window (conv_state bf16 [slots,
@@ -486,7 +501,11 @@ mx_status mx_engine_generate(mx_engine* e, int32_t slot, const uint32_t* prompt,
 /* Test/inspection hooks: flags (bit 0: also write bf16 logits of each step;
  * bit 1: run eagerly instead of replaying captured HIP graphs; bit 2: exact
  * mode, every projection on the fixed-order kernels that the CPU oracle
- * reproduces bit for bit, instead of the matrix-core kernels), and reads of
+ * reproduces bit for bit, instead of the matrix-core kernels; bits 3..9, a
+ * diagnostic mask of the components that run exact while the rest stays on
+ * the matrix cores: 3 hyper-connections, 4 GDN projections, 5 GDN
+ * recurrence, 6 attention projections, 7 attention core, 8 router + routing
+ * + experts, 9 vocabulary head), and reads of
  * the last step's "hidden" (bf16 [rows, hc*hidden]) / "logits" (bf16
  * [rows, vocab]) or of any named weight/cache tensor into host memory. */
 mx_status mx_engine_set_flags(mx_engine* e, int32_t flags);

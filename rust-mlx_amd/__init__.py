@@ -189,6 +189,7 @@ def _load() -> C.CDLL:
         "mx_engine_set_flags": ([vp, i32], i32),
         "mx_engine_fill_slot": ([vp, i32, i32, u64], i32),
         "mx_qmm": ([C.POINTER(QWeightC), vp, i32, vp, vp], i32),
+        "mx_xq": ([C.POINTER(QWeightC), vp, i32, vp, vp], i32),
         "mx_hc_workspace_bytes": ([i32], sz),
         "mx_hc_forward_mfma": ([C.POINTER(QWeightC), C.POINTER(QWeightC), vp, vp, i32, i32, i32,
                                 i32, f32, vp, vp, vp, vp], i32),
@@ -502,9 +503,12 @@ class Engine:
         check(lib.mx_engine_time_experts(self.h, rows, C.byref(t)))
         return {f: getattr(t, f) for f, _ in ExpertTimingC._fields_}
 
-    def set_flags(self, logits=False, eager=False, exact=False):
+    # components for set_flags(exact_parts=...): run exact while the rest stays fast
+    EX_HC, EX_GDN_PROJ, EX_GDN, EX_ATTN_PROJ, EX_ATTN, EX_MOE, EX_HEAD = 1, 2, 4, 8, 16, 32, 64
+
+    def set_flags(self, logits=False, eager=False, exact=False, exact_parts=0):
         check(lib.mx_engine_set_flags(self.h, (1 if logits else 0) | (2 if eager else 0)
-                                      | (4 if exact else 0)))
+                                      | (4 if exact else 0) | (exact_parts << 3)))
 
     def read(self, what: str, dtype, shape) -> np.ndarray:
         out = np.empty(shape, dtype)

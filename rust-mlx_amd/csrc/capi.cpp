@@ -685,7 +685,8 @@ MX_ABI mx_status mx_engine_commit(mx_engine* e, int32_t slot, int32_t keep) {
 
 MX_ABI mx_status mx_engine_set_flags(mx_engine* e, int32_t flags) {
   MX_CHECK(e != nullptr, MX_EINVAL, "mx_engine_set_flags: null engine");
-  engine_set_flags(*e->impl, flags & 1, (flags & 2) ? 0 : 1, (flags & 4) ? 1 : 0);
+  engine_set_flags(*e->impl, flags & 1, (flags & 2) ? 0 : 1, (flags & 4) ? 1 : 0,
+                   (flags >> 3) & 127);
   return MX_OK;
 }
 
@@ -737,6 +738,21 @@ MX_ABI mx_status mx_qmm(const mx_qweight* w, const uint16_t* x, int32_t m, uint1
   if (m <= 8 && skinny_supported(q))
     return finish(skinny_dense(q, x, q.k, m, e, hipStream_t(stream)), "mx_qmm");
   return finish(qmm(q, x, q.k, m, e, hipStream_t(stream)), "mx_qmm");
+}
+
+MX_ABI mx_status mx_xq(const mx_qweight* w, const uint16_t* x, int32_t m, uint16_t* y,
+                       void* stream) {
+  MX_CHECK(w != nullptr && x != nullptr && y != nullptr, MX_EINVAL, "mx_xq: null pointer");
+  const QWeight q = to_qweight(*w);
+  if (const char* err = check_qweight(q)) return mx_status(set_error(MX_EINVAL, std::string("mx_xq: ") + err));
+  MX_CHECK(xq_supported(q), MX_EUNSUPPORTED,
+           "mx_xq: needs group_size 64 and k a multiple of 64 up to 512 or of 512 up to 8192");
+  MX_CHECK(m >= 1 && m <= 8, MX_EUNSUPPORTED, "mx_xq: m must be in 1..8");
+  ProjEpilogue e{};
+  e.mode = kPlain;
+  e.y = y;
+  e.y_stride = q.n;
+  return finish(xq_dense(q, x, q.k, m, e, hipStream_t(stream)), "mx_xq");
 }
 
 MX_ABI mx_status mx_qmm_conv(const mx_qweight* w, const uint16_t* x, int32_t m,

@@ -143,6 +143,9 @@ struct Engine {
   // the CPU oracle); otherwise dense and expert projections run on the matrix
   // cores (router and vocabulary head stay exact in both modes)
   bool exact = false;
+  // finer diagnostic switch: components (kEx* bits) that run on the exact
+  // kernels while the rest stays on the matrix cores
+  int exact_parts = 0;
   // profiling (eager steps only): events around each layer's expert kernels
   mx_step_profile* prof = nullptr;
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
@@ -160,6 +163,19 @@ Engine::~Engine() {
 }
 
 namespace {
+
+// Components of a layer that the diagnostic mask can move to the exact kernels.
+enum : int {
+  kExHc = 1,        // hyper-connection projections (and their norm / mix)
+  kExGdnProj = 2,   // GDN input and output projections
+  kExGdn = 4,       // GDN recurrence
+  kExAttnProj = 8,  // attention input and output projections
+  kExAttn = 16,     // attention core
+  kExMoe = 32,      // router projection, routing and experts
+  kExHead = 64,     // vocabulary head
+};
+
+bool ex(const Engine& e, int part) { return e.exact || (e.exact_parts & part) != 0; }
 
 uint64_t tensor_seed(uint64_t base, int layer, int id) {
   // distinct streams per (layer, tensor); QWeight-style tensors use seed, +1, +2
@@ -451,7 +467,7 @@ bool experts_fast(const Engine& e, const LayerW& L) {
                   L.gate.group_size};
   const QWeight d{L.down.codes, L.down.scales, L.down.biases, L.down.n, L.down.k, L.down.bits,
                   L.down.group_size};
-  return !e.exact && skinny_supported(g) && skinny_supported(d) && skinny_supported(L.sgate) &&
+  return !ex(e, kExMoe) && skinny_supported(g) && skinny_supported(d) && skinny_supported(L.sgate) &&
          skinny_supported(L.sdown);
 }
 
@@ -514,16 +530,17 @@ int profile_experts(Engine& e, const LayerW& L, int rows) {
 
 // Projection on the matrix cores (fast mode) or the exact kernels.
 int project(Engine& e, const QWeight& w, const uint16_t* x, int64_t xs, int rows,
-            const ProjEpilogue& ep) {
-  if (!e.exact && rows <= 8 && skinny_supported(w))
+            const ProjEpilogue& ep, int part) {
+  const bool exact = ex(e, part);
+  if (!exact && rows <= 8 && skinny_supported(w))
     return skinny_dense(w, x, xs, rows, ep, e.stream);
-  if (!e.exact && qmm_supported(w)) return qmm(w, x, xs, rows, ep, e.stream);
+  if (!exact && qmm_supported(w)) return qmm(w, x, xs, rows, ep, e.stream);
   return proj(w, x, xs, rows, ep, e.stream);
 }
 
 int hc_forward(Engine& e, const HcW& w, int rows, uint16_t* mixed_out, uint16_t* inj_out) {
   const auto& c = e.cfg;
-  if (!e.exact && hc_fused_supported(w.down, w.up, c.hc, c.hidden, c.hc_rank))
+  if (!ex(e, kExHc) && hc_fused_supported(w.down, w.up, c.hc, c.hidden, c.hc_rank))
     return hc_fused(w.down, w.up, e.h, w.scale, rows, c.hc, c.hidden, c.hc_rank, c.rms_eps,
                     e.hc_part, mixed_out, inj_out, e.stream);
   MX_TRY(hc_norm(e.h, w.scale, rows, c.hc, c.hidden, c.rms_eps, e.xn, e.stream));
@@ -535,7 +552,7 @@ int hc_forward(Engine& e, const HcW& w, int rows, uint16_t* mixed_out, uint16_t*
   d.aux_stride = c.hc;
   d.rank = c.hc_rank;
   d.hc = c.hc;
-  MX_TRY(project(e, w.down, e.xn, int64_t(c.hc) * c.hidden, rows, d));
+  MX_TRY(project(e, w.down, e.xn, int64_t(c.hc) * c.hidden, rows, d, kExHc));
   ProjEpilogue u{};
   u.mode = kHcUpMix;
   u.y = mixed_out;
@@ -544,7 +561,7 @@ int hc_forward(Engine& e, const HcW& w, int rows, uint16_t* mixed_out, uint16_t*
   u.xn_stride = int64_t(c.hc) * c.hidden;
   u.hc = c.hc;
   u.hidden = c.hidden;
-  MX_TRY(project(e, w.up, e.lo, c.hc_rank, rows, u));
+  MX_TRY(project(e, w.up, e.lo, c.hc_rank, rows, u, kExHc));
   return MX_OK;
 }
 
@@ -573,7 +590,7 @@ int record_layer(Engine& e, const LayerW& L, int rows, int groups, int t, bool h
       const size_t conv_per = size_t(c.conv_k - 1) * e.cd;
       const size_t state_per = size_t(c.gdn_hv) * c.gdn_dk * c.gdn_dv;
       // cache layout [slot][gdn layer]: slot index s -> s * n_gdn + gi
-      if (!e.exact && t == 1 && !history && rows <= 8 && L.gdn_in.bits == 4 &&
+      if (!ex(e, kExGdnProj) && t == 1 && !history && rows <= 8 && L.gdn_in.bits == 4 &&
           skinny_supported(L.gdn_in) && c.conv_k <= kConvMaxTaps) {
         // the conv runs in the projection's epilogue
         pl.mode = kConv;
@@ -586,7 +603,7 @@ int record_layer(Engine& e, const LayerW& L, int rows, int groups, int t, bool h
         pl.taps = c.conv_k;
         MX_TRY(skinny_dense(L.gdn_in, e.mixed, c.hidden, rows, pl, e.stream));
       } else {
-        MX_TRY(project(e, L.gdn_in, e.mixed, c.hidden, rows, pl));
+        MX_TRY(project(e, L.gdn_in, e.mixed, c.hidden, rows, pl, kExGdnProj));
         MX_TRY(gdn_conv(e.pbuf, e.P, groups, t, rt->gdn_slots, e.conv_state + gi * conv_per,
                         L.conv_w, e.cd, c.conv_k, e.conv_out, e.cd,
                         history ? e.hist_conv + size_t(gi) * (c.conv_k - 1 + c.max_verify) * e.cd
@@ -594,7 +611,7 @@ int record_layer(Engine& e, const LayerW& L, int rows, int groups, int t, bool h
                         e.stream));
       }
       float* hist = history ? e.hist_state + size_t(gi) * c.max_verify * state_per : nullptr;
-      if (!e.exact) {
+      if (!ex(e, kExGdn)) {
         // decode, verify and prefill blocks alike: a verify block's tokens
         // get the bits of one-token decode steps (lossless speculation)
         MX_TRY(gdn_recurrence_fast(e.conv_out, e.cd, e.pbuf + e.cd, e.pbuf + e.cd + e.vd,
@@ -607,26 +624,26 @@ int record_layer(Engine& e, const LayerW& L, int rows, int groups, int t, bool h
                               L.gdn_norm, c.rms_eps, e.gd, groups, t, rt->gdn_slots,
                               e.gdn_state + gi * state_per, hist, e.y, e.stream));
       }
-      MX_TRY(project(e, L.gdn_out, e.y, e.vd, rows, wr));
+      MX_TRY(project(e, L.gdn_out, e.y, e.vd, rows, wr, kExGdnProj));
     } else {
       const int ai = L.cache_index;
       ProjEpilogue pl{};
       pl.mode = kPlain;
       pl.y = e.pbuf;
       pl.y_stride = e.Q;
-      MX_TRY(project(e, L.attn_in, e.mixed, c.hidden, rows, pl));
+      MX_TRY(project(e, L.attn_in, e.mixed, c.hidden, rows, pl, kExAttnProj));
       const size_t layer_off = size_t(ai) * c.kv_heads * c.max_context * c.head_dim;
       MX_TRY(attn_prep(e.pbuf, e.Q, rows, rt->slots, rt->pos, L.q_norm, L.k_norm, c.rms_eps,
                        e.rope_cos, e.rope_sin, e.ad, e.qrot, e.k_cache + layer_off,
                        e.v_cache + layer_off, e.stream));
-      const bool fast_attn = !e.exact && attn_fast_supported(e.ad);
+      const bool fast_attn = !ex(e, kExAttn) && attn_fast_supported(e.ad);
       MX_TRY(attn_decode(e.qrot, rows, rt->slots, rt->pos, e.k_cache + layer_off,
                          e.v_cache + layer_off, e.ad, e.max_chunks, fast_attn, e.o_part,
                          e.ml_part, e.stream));
       MX_TRY(attn_combine(e.o_part, e.ml_part, e.pbuf, e.Q, rows, rt->pos, e.ad, e.max_chunks,
                           fast_attn,
                           e.y, e.stream));
-      MX_TRY(project(e, L.attn_out, e.y, int64_t(c.heads) * c.head_dim, rows, wr));
+      MX_TRY(project(e, L.attn_out, e.y, int64_t(c.heads) * c.head_dim, rows, wr, kExAttnProj));
     }
     // MoE sublayer
     MX_TRY(hc_forward(e, L.mlp_hc, rows, e.mixed, e.inj));
@@ -634,7 +651,7 @@ int record_layer(Engine& e, const LayerW& L, int rows, int groups, int t, bool h
     rl.mode = kPlain;
     rl.y = e.logits_r;
     rl.y_stride = c.experts + 1;
-    MX_TRY(project(e, L.router, e.mixed, c.hidden, rows, rl));
+    MX_TRY(project(e, L.router, e.mixed, c.hidden, rows, rl, kExMoe));
     bool summed = false;  // slots summed and the streams written
     if (!e.prof && experts_fast(e, L)) {
       // the expert gate/up kernel routes the rows itself
@@ -689,7 +706,8 @@ int record_head(Engine& e, int rows, bool logits) {
   int parts = 0;
   float* maxima = static_cast<float*>(e.head_ws);
   uint32_t* indices = reinterpret_cast<uint32_t*>(maxima + size_t(head_parts(c.vocab, c.hidden)) * 8);
-  const bool fast = !e.exact && skinny_supported(e.head) && e.head.k % 512 == 0 && e.head.k <= 2048;
+  const bool fast = !ex(e, kExHead) && skinny_supported(e.head) && e.head.k % 512 == 0 &&
+                    e.head.k <= 2048;
   if (fast)  // the matrix-core head writes the logits it ranks
     MX_TRY(skinny_head(e.head, e.mixed, rows, maxima, indices, &parts, e.stream,
                        logits ? e.logits : nullptr));
@@ -768,7 +786,7 @@ int record_mtp(Engine& e, int rows) {
   pe.mode = kPlain;
   pe.y = e.mtp_e;
   pe.y_stride = H;
-  MX_TRY(project(e, e.mtp.fc_emb, e.mtp_a, H, rows, pe));
+  MX_TRY(project(e, e.mtp.fc_emb, e.mtp_a, H, rows, pe, kExAttnProj));
   MX_TRY(hc_norm(e.mtp_prev, e.mtp.norm_hid, rows, 1, hc * H, c.rms_eps, e.mtp_hn, e.stream));
   for (int r0 = 0; r0 < rows * hc; r0 += 8) {
     const int n = rows * hc - r0 < 8 ? rows * hc - r0 : 8;
@@ -776,7 +794,7 @@ int record_mtp(Engine& e, int rows) {
     ph.mode = kPlain;
     ph.y = e.mtp_f + size_t(r0) * H;
     ph.y_stride = H;
-    MX_TRY(project(e, e.mtp.fc_hid, e.mtp_hn + size_t(r0) * H, H, n, ph));
+    MX_TRY(project(e, e.mtp.fc_hid, e.mtp_hn + size_t(r0) * H, H, n, ph, kExAttnProj));
   }
   MX_TRY(mtp_combine(e.mtp_e, e.mtp_f, rows, hc, H, e.h, e.stream));
   MX_TRY(record_layer(e, e.mtp.layer, rows, 1, rows, false));
@@ -1333,15 +1351,16 @@ int engine_tensor(Engine& e, const char* name, void** ptr, size_t* bytes) {
   return MX_OK;
 }
 
-void engine_set_flags(Engine& e, int want_logits, int use_graphs, int exact) {
+void engine_set_flags(Engine& e, int want_logits, int use_graphs, int exact, int exact_parts) {
   e.want_logits = want_logits != 0;
   e.use_graphs = use_graphs != 0;
-  if (e.exact != (exact != 0)) {
+  if (e.exact != (exact != 0) || e.exact_parts != exact_parts) {
     // captured graphs bake in the kernel choice
     for (auto& g : e.graphs) hipGraphExecDestroy(g.second);
     e.graphs.clear();
   }
   e.exact = exact != 0;
+  e.exact_parts = exact_parts;
 }
 
 const mx_model_config& engine_config(const Engine& e) { return e.cfg; }

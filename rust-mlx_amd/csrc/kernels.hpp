@@ -74,6 +74,11 @@ int proj(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const Pro
 bool qmm_supported(const QWeight& w);
 int qmm(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const ProjEpilogue& e,
         hipStream_t s);
+// exact-integer projections for 1..8 rows (xq.hip): the CPU oracle's
+// mxo_xq arithmetic bit for bit, on the int8 matrix cores
+bool xq_supported(const QWeight& w);
+int xq_dense(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const ProjEpilogue& e,
+             hipStream_t s);
 // matrix-core skinny projections for 1..8 rows (skinny.hip)
 bool skinny_supported(const QWeight& w);
 int skinny_dense(const QWeight& w, const uint16_t* x, int64_t x_stride, int m,
@@ -261,7 +266,7 @@ int engine_fill_slot(Engine& e, int slot, int length, uint64_t seed, std::string
 int engine_time_experts(Engine& e, int rows, mx_expert_timing* out, std::string* err);
 int engine_profile_step(Engine& e, const int32_t* slots, const uint32_t* tokens, int rows,
                         uint32_t* next, mx_step_profile* out, std::string* err);
-void engine_set_flags(Engine& e, int want_logits, int use_graphs, int exact);
+void engine_set_flags(Engine& e, int want_logits, int use_graphs, int exact, int exact_parts);
 const mx_model_config& engine_config(const Engine& e);
 int engine_gdn_layers(const Engine& e);
 int engine_attn_layers(const Engine& e);

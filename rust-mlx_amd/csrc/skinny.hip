@@ -23,6 +23,7 @@
 #include "kernels.hpp"
 #include "skinny_core.hpp"
 #include "route_core.hpp"
+#include "proj_epilogue.hpp"
 
 namespace mx {
 
@@ -103,13 +104,8 @@ __global__ __launch_bounds__(64 * T * KS) void dense_kernel(QWeight w,
   const int G = w.k >> 6;
   const sk::DenseRows xr{x, x_stride, M};
   constexpr int NT = 64 * T * KS;
-  // kConv: the thread's first epilogue output (row cm, column cr); its slot
-  // is read before the weight stream, its window and conv weights right after
-  constexpr bool kConvPre = MODE == kConv && 8 * NC <= NT;
-  const int cm = threadIdx.x / NC, cr = tg * NC + threadIdx.x % NC;
-  const bool conv_item = kConvPre && cm < M && cr < min(n, e.conv_ch);
-  int cslot = 0;
-  if (conv_item) cslot = e.slots[cm];
+  ProjFinish<MODE, NC, NT> fin;
+  fin.begin(e, tg, M, n);
   // slices of a staged tile hold kStageSteps / KS super-steps at most
   constexpr int BMAX = XREG ? 1 : (kStageSteps / KS > 1 ? kStageSteps / KS : 1);
   const int xbytes = XREG ? 0 : total * sk::kStepBytes;
@@ -118,111 +114,20 @@ __global__ __launch_bounds__(64 * T * KS) void dense_kernel(QWeight w,
       w.codes + size_t(row) * (size_t(w.k) * BITS / 32), w.scales + size_t(row) * G,
       w.biases + size_t(row) * G, total, k0, steps, 0, lds, sx, xr, M);
   float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  uint16_t cwin[kConvMaxTaps - 1] = {};
-  float cw[kConvMaxTaps] = {};
-  // window taps and weights at indices clamped to the last real one, so the
-  // loads stay unconditional within the item
-  auto conv_fetch = [&](int slot, int r, uint16_t (&win)[kConvMaxTaps - 1],
-                        float (&wt)[kConvMaxTaps]) {
-    const uint16_t* stp = e.conv_state + size_t(slot) * (e.taps - 1) * e.conv_ch + r;
-#pragma unroll
-    for (int j = 0; j < kConvMaxTaps - 1; ++j) win[j] = stp[size_t(min(j, e.taps - 2)) * e.conv_ch];
-#pragma unroll
-    for (int j = 0; j < kConvMaxTaps; ++j) wt[j] = e.conv_w[size_t(min(j, e.taps - 1)) * e.conv_ch + r];
-  };
   if constexpr (XREG) {
     st.prefetch();
-    if (conv_item) conv_fetch(cslot, cr, cwin, cw);
+    fin.prefetch(e);
     st.run(0, y);
   } else {
     sk::Stager<NT, sk::stage_per(NT, kStageSteps), sk::DenseRows> stg(xr, M, 0, total);
     stg.load();
     st.prefetch();
-    if (conv_item) conv_fetch(cslot, cr, cwin, cw);
+    fin.prefetch(e);
     stg.store(lds);
     st.run(xbytes, y);
   }
   reduce_tiles<T, KS>(y, red, yt);
-
-  if constexpr (MODE == kHcUpMix) {
-    // 8 rows x 16 columns; each output mixes the four streams of its column
-    if (threadIdx.x >= 128) return;
-    const int m = threadIdx.x >> 4, cj = threadIdx.x & 15;
-    const int c = tg * 16 + cj;
-    if (m >= M || c >= e.hidden) return;
-    float sum = 0.0f;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const float p = round_bf16(yt[m * NC + s * 16 + cj]);
-      const float xn = bf16_to_f32(e.xn[size_t(m) * e.xn_stride + size_t(s) * e.hidden + c]);
-      sum = sum + round_bf16(sigmoid_bf16(p) * xn);
-    }
-    e.y[size_t(m) * e.y_stride + c] = f32_to_bf16(round_bf16(sum) / 4.0f);
-  } else if constexpr (MODE == kConv) {
-    for (int i = threadIdx.x; i < 8 * NC; i += NT) {
-      const int m = i / NC, c = i - m * NC;
-      const int r = tg * NC + c;
-      if (m >= M || r >= n) continue;
-      const uint16_t xb = f32_to_bf16(yt[i]);
-      if (r >= e.conv_ch) {
-        e.y[size_t(m) * e.y_stride + r] = xb;
-        continue;
-      }
-      uint16_t win[kConvMaxTaps - 1];
-      float wt[kConvMaxTaps];
-      const int slot = kConvPre ? cslot : e.slots[m];
-      if constexpr (kConvPre) {
-#pragma unroll
-        for (int j = 0; j < kConvMaxTaps - 1; ++j) win[j] = cwin[j];
-#pragma unroll
-        for (int j = 0; j < kConvMaxTaps; ++j) wt[j] = cw[j];
-      } else {
-        conv_fetch(slot, r, win, wt);
-      }
-      // acc = sum_j fl(x_j * w_j) over the window then the new value
-      float acc = 0.0f;
-#pragma unroll
-      for (int j = 0; j < kConvMaxTaps - 1; ++j)
-        if (j < e.taps - 1) acc = acc + bf16_to_f32(win[j]) * wt[j];
-      acc = acc + bf16_to_f32(xb) * wt[kConvMaxTaps - 1];
-      const float v = round_bf16(acc);
-      e.conv_out[size_t(m) * e.conv_stride + r] = f32_to_bf16(v * sigmoid_bf16(v));
-      uint16_t* stp = e.conv_state + size_t(slot) * (e.taps - 1) * e.conv_ch + r;
-#pragma unroll
-      for (int j = 0; j < kConvMaxTaps - 2; ++j)
-        if (j < e.taps - 2) stp[size_t(j) * e.conv_ch] = win[j + 1];
-      stp[size_t(e.taps - 2) * e.conv_ch] = xb;
-    }
-  } else if constexpr (MODE == kHcWrite) {
-    // one residual stream per thread: the read-modify-writes of a column's
-    // streams are independent, so none waits on another's load
-    for (int i = threadIdx.x; i < 8 * NC * e.hc; i += 64 * T * KS) {
-      const int s = i / (8 * NC), mc = i - s * (8 * NC);
-      const int m = mc / NC, c = mc - m * NC;
-      const int r = tg * NC + c;
-      if (m >= M || r >= n) continue;
-      const float vb = round_bf16(yt[mc]);
-      uint16_t* res = e.y + size_t(m) * e.y_stride + size_t(s) * n + r;
-      const float inj = round_bf16(vb * bf16_to_f32(e.aux[size_t(m) * e.aux_stride + s]));
-      *res = f32_to_bf16(bf16_to_f32(*res) + inj);
-    }
-  } else {
-    for (int i = threadIdx.x; i < 8 * NC; i += 64 * T * KS) {
-      const int m = i / NC, c = i - m * NC;
-      const int r = tg * NC + c;
-      if (m >= M || r >= n) continue;
-      const float v = yt[i];
-      if constexpr (MODE == kPlain) {
-        e.y[size_t(m) * e.y_stride + r] = f32_to_bf16(v);
-      } else {  // kHcDown
-        const float tt = round_bf16(round_bf16(v) / float(e.hc));
-        if (r < e.rank)
-          e.y[size_t(m) * e.y_stride + r] = f32_to_bf16(tt * sigmoid_bf16(tt));
-        else
-          e.aux[size_t(m) * e.aux_stride + (r - e.rank)] = f32_to_bf16(sigmoid_bf16(tt) * 2.0f);
-      }
-    }
-  }
+  fin.finish(yt, e, tg, M, n);
 }
 
 // ---------------------------------------------------------------------------

@@ -275,8 +275,10 @@ def test_argmax_extremes(mx, orc):
 @pytest.mark.parametrize("groups", [1, 8])
 def test_gdn_recurrence_fast_within_tolerance(mx, orc, groups):
     """Fast-mode single-token step (hardware exp2 / log2 / rsqrt, wave-local q/k
-    norms) against the oracle's fixed-order step: fp32 state within 1e-4
-    relative (max norm), y within 2e-2 relative / 1e-2 absolute."""
+    norms) against the oracle's fixed-order step on the same inputs: the fp32
+    state within 1e-4 relative per element (|d| <= 1e-4 max(|w|, 1e-2 rms)
+    per head, the floor covering entries that cancel to near zero), y within
+    2e-2 relative / 1e-2 absolute."""
     hk, hv, S = 16, 32, 9
     conv, z, a, b, a_log, dt, norm_w = _gdn_inputs(orc, groups, hk, hv, 900 + groups)
     rng = np.random.default_rng(98)
@@ -295,8 +297,13 @@ def test_gdn_recurrence_fast_within_tolerance(mx, orc, groups):
                                            zab.shape[1], dal.ptr, ddt.ptr, dnw.ptr, eps,
                                            C.byref(dims), groups, 1, dsl.ptr, dst.ptr, None, y.ptr,
                                            None))
-    st = dst.numpy()
-    assert np.abs(st - st_w).max() <= 1e-4 * np.abs(st_w).max()
+    st = dst.numpy().astype(np.float64)
+    w64 = st_w.astype(np.float64)
+    rms = np.sqrt((w64 ** 2).mean(axis=(2, 3), keepdims=True))
+    ratio = np.abs(st - w64) / (1e-4 * np.maximum(np.abs(w64), 1e-2 * rms))
+    print(f"fast GDN state: worst error / bound {ratio.max():.3f}, "
+          f"entries above 1e-4 relative {(np.abs(st - w64) > 1e-4 * np.abs(w64)).mean():.2e}")
+    assert ratio.max() <= 1.0
     got, want = bf(y.numpy()).astype(np.float64), bf(y_w).astype(np.float64)
     assert np.all(np.abs(got - want) <= 2e-2 * np.abs(want) + 1e-2)
 
