@@ -4,7 +4,9 @@ product.
 
 It follows HybridModel::forward_hidden (reference src/hybrid.rs:594-685) layer
 by layer with the oracle's C primitives, in the same arithmetic order as the
-engine's kernels, so tokens, hidden states and caches agree bit for bit.
+engine's exact mode, so tokens, hidden states and caches agree bit for bit.
+Every projection is the exact-integer affine projection (oracle/xq.c, the
+engine's int8 matrix-core kernels): weights are viewed with mode XQ.
 Weights are read from the engine under test (fetch(name, dtype, shape)); the
 caches are the oracle's own numpy arrays.
 """
@@ -36,6 +38,7 @@ class Model:
         sample of a large model); None runs the whole stack."""
         self.c = c = dict(cfg)
         self.fetch = fetch
+        self.mode = orc.XQ
         H, hc = c["hidden"], c["hc"]
         self.H, self.hc = H, hc
         self.cd = 2 * c["gdn_hk"] * 128 + c["gdn_hv"] * 128
@@ -126,7 +129,7 @@ class Model:
         s = self.fetch(name + ".scales", np.uint16, (n, k // gs))
         b = self.fetch(name + ".biases", np.uint16, (n, k // gs))
         self._keep += [codes, s, b]
-        return orc.qw(codes, s, b, n, k, bits, gs)
+        return orc.qw(codes, s, b, n, k, bits, gs, self.mode)
 
     def _bank(self, name, E, n, k, bits):
         gs = self.c["group_size"]
@@ -134,7 +137,7 @@ class Model:
         s = self.fetch(name + ".scales", np.uint16, (E * n, k // gs))
         b = self.fetch(name + ".biases", np.uint16, (E * n, k // gs))
         self._keep += [codes, s, b]
-        return orc.qbank(codes, s, b, E, n, k, bits, gs)
+        return orc.qbank(codes, s, b, E, n, k, bits, gs, self.mode)
 
     def _hc(self, p, layer, inject):
         c = self.c
@@ -158,9 +161,15 @@ class Model:
         return mixed, inj
 
     def _qmv(self, w, x):
+        """bf16 projection of rows x by the weight struct w (its mode's arithmetic)."""
         x = np.ascontiguousarray(x, np.uint16)
-        y = np.empty((x.shape[0], w.n), np.uint16)
-        orc.lib.mxo_qmv(w.codes, w.scales, w.biases, w.n, w.k, w.bits, w.gs, _p(x), x.shape[0], _p(y))
+        m = x.shape[0]
+        if w.mode == orc.XQ:
+            yf = np.empty((m, w.n), np.float32)
+            orc.lib.mxo_xq(w.codes, w.scales, w.biases, w.n, w.k, w.bits, _p(x), m, _p(yf))
+            return orc.f32_to_bf16(yf)
+        y = np.empty((m, w.n), np.uint16)
+        orc.lib.mxo_qmv(w.codes, w.scales, w.biases, w.n, w.k, w.bits, w.gs, _p(x), m, _p(y))
         return y
 
     def _run_layer(self, L, attn, ci, h, rows, slots_a, pos_a, gdn_slots, groups, t, history):

@@ -476,8 +476,8 @@ int experts_gate_up(Engine& e, const LayerW& L, int rows) {
   if (experts_fast(e, L))
     return skinny_gate_up(e.mixed, e.ids, rows, c.top_k, L.gate, L.up, L.sgate, L.sup, e.moe_h,
                           e.stream);
-  return moe_gate_up(e.mixed, e.moe_plan_buf, rows, c.top_k, L.gate, L.up, L.sgate, L.sup,
-                     e.moe_h, e.stream);
+  return xq_gate_up(e.mixed, e.moe_plan_buf, rows, c.top_k, L.gate, L.up, L.sgate, L.sup,
+                    e.moe_h, e.stream);
 }
 
 int experts_down(Engine& e, const LayerW& L, int rows) {
@@ -485,8 +485,8 @@ int experts_down(Engine& e, const LayerW& L, int rows) {
   if (experts_fast(e, L))
     return skinny_down(e.moe_h, e.ids, e.scores, rows, c.top_k, L.gate.n, L.sgate.n, L.down,
                        L.sdown, e.moe_p, e.stream);
-  return moe_down(e.moe_h, e.moe_plan_buf, e.scores, rows, c.top_k, L.gate.n, L.sgate.n, L.down,
-                  L.sdown, e.moe_p, e.stream);
+  return xq_down(e.moe_h, e.moe_plan_buf, e.scores, rows, c.top_k, L.gate.n, L.sgate.n, L.down,
+                 L.sdown, e.moe_p, e.stream);
 }
 
 // Profiled (eager) steps: count the layer's distinct routed experts and time
@@ -529,13 +529,14 @@ int profile_experts(Engine& e, const LayerW& L, int rows) {
 }
 
 // Projection on the matrix cores (fast mode) or the exact kernels.
+// Exact components take the exact-integer projection (bit for bit the CPU
+// oracle's); a weight it does not cover is an error, never another path.
 int project(Engine& e, const QWeight& w, const uint16_t* x, int64_t xs, int rows,
             const ProjEpilogue& ep, int part) {
-  const bool exact = ex(e, part);
-  if (!exact && rows <= 8 && skinny_supported(w))
-    return skinny_dense(w, x, xs, rows, ep, e.stream);
-  if (!exact && qmm_supported(w)) return qmm(w, x, xs, rows, ep, e.stream);
-  return proj(w, x, xs, rows, ep, e.stream);
+  if (ex(e, part)) return xq_dense(w, x, xs, rows, ep, e.stream);
+  if (rows <= 8 && skinny_supported(w)) return skinny_dense(w, x, xs, rows, ep, e.stream);
+  if (qmm_supported(w)) return qmm(w, x, xs, rows, ep, e.stream);
+  return xq_dense(w, x, xs, rows, ep, e.stream);
 }
 
 int hc_forward(Engine& e, const HcW& w, int rows, uint16_t* mixed_out, uint16_t* inj_out) {
@@ -706,22 +707,15 @@ int record_head(Engine& e, int rows, bool logits) {
   int parts = 0;
   float* maxima = static_cast<float*>(e.head_ws);
   uint32_t* indices = reinterpret_cast<uint32_t*>(maxima + size_t(head_parts(c.vocab, c.hidden)) * 8);
-  const bool fast = !ex(e, kExHead) && skinny_supported(e.head) && e.head.k % 512 == 0 &&
-                    e.head.k <= 2048;
-  if (fast)  // the matrix-core head writes the logits it ranks
+  // either head writes the bf16 logits it ranks when they are wanted; heads
+  // the matrix-core kernel does not cover take the exact-integer one
+  if (!ex(e, kExHead) && skinny_supported(e.head) && e.head.k % 512 == 0 && e.head.k <= 2048)
     MX_TRY(skinny_head(e.head, e.mixed, rows, maxima, indices, &parts, e.stream,
                        logits ? e.logits : nullptr));
   else
-    MX_TRY(head_partials(e.head, e.mixed, rows, maxima, indices, &parts, e.stream));
-  MX_TRY(argmax_reduce(maxima, indices, rows, parts, rt->next, e.stream));
-  if (logits && !fast) {  // the exact projection's bf16 logits (same order as the exact head)
-    ProjEpilogue pl{};
-    pl.mode = kPlain;
-    pl.y = e.logits;
-    pl.y_stride = c.vocab;
-    MX_TRY(proj(e.head, e.mixed, c.hidden, rows, pl, e.stream));
-  }
-  return MX_OK;
+    MX_TRY(xq_head(e.head, e.mixed, rows, maxima, indices, logits ? e.logits : nullptr, &parts,
+                   e.stream));
+  return argmax_reduce(maxima, indices, rows, parts, rt->next, e.stream);
 }
 
 int graph_key(int rows, int groups, int t, bool history, bool logits) {

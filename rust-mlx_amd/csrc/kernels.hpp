@@ -79,6 +79,19 @@ int qmm(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const Proj
 bool xq_supported(const QWeight& w);
 int xq_dense(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const ProjEpilogue& e,
              hipStream_t s);
+struct MoePlan;
+// exact-integer expert MLPs over a MoePlan (same contracts as moe_gate_up /
+// moe_down) and greedy-head partials (same layout as head_partials, parts =
+// xq_head_parts(n); logits, when non-null, receives the bf16 logits)
+int xq_gate_up(const uint16_t* x, const MoePlan* plan, int rows, int top_k, const QBank& gate,
+               const QBank& up, const QWeight& sgate, const QWeight& sup, uint16_t* h,
+               hipStream_t s);
+int xq_down(const uint16_t* h, const MoePlan* plan, const uint16_t* scores, int rows, int top_k,
+            int inter, int shared_inter, const QBank& down, const QWeight& sdown, uint16_t* p,
+            hipStream_t s);
+int xq_head_parts(int n);
+int xq_head(const QWeight& w, const uint16_t* x, int m, float* maxima, uint32_t* indices,
+            uint16_t* logits, int* parts_out, hipStream_t s);
 // matrix-core skinny projections for 1..8 rows (skinny.hip)
 bool skinny_supported(const QWeight& w);
 int skinny_dense(const QWeight& w, const uint16_t* x, int64_t x_stride, int m,
