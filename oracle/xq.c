@@ -14,10 +14,10 @@
  *  - P = sum_k X_k q_k and Q = sum_k X_k are exact integers (|P| < 2^44);
  *  - the group's value is v_g = fma(P, s_g, Q b_g) * 2^(Eb - 156) in double
  *    (P s_g and Q b_g are exact products; one rounding in the fma);
- *  - the groups are added in double, in order, within each of S contiguous
- *    slices of the row (S = K / 512 when K >= 1024, else 1), each sum
- *    starting from +0; the slice sums are added in order from +0; the total
- *    is rounded once to fp32.
+ *  - the groups are added in double, in order, within each slice of two
+ *    consecutive groups (the last slice of an odd count holds one), each
+ *    slice sum starting from +0; the slice sums are added in order from +0;
+ *    the total is rounded once to fp32.
  *
  * On the GPU the integer sums are int8 matrix-core products of the signed
  * base-256 digits of X_k with the codes (exact in int32), so the result
@@ -27,7 +27,7 @@
 
 #include "oracle.h"
 
-int mxo_xq_slices(int k) { return k >= 1024 ? k / 512 : 1; }
+int mxo_xq_slices(int k) { return (k / 64 + 1) / 2; }
 
 /* X_k of one bf16 value on the grid of exponent field eb. */
 int64_t mxo_xq_int(uint16_t h, int eb) {
@@ -50,11 +50,11 @@ int mxo_xq_group_exp(const uint16_t* x) {
 
 float mxo_xq_row(const uint32_t* rw, const uint16_t* srow, const uint16_t* brow, int k, int bits,
                  const uint16_t* x) {
-  const int G = k / 64, S = mxo_xq_slices(k), per = G / S;
+  const int G = k / 64, S = mxo_xq_slices(k);
   double total = 0.0;
   for (int sl = 0; sl < S; ++sl) {
     double acc = 0.0;
-    for (int g = sl * per; g < (sl + 1) * per; ++g) {
+    for (int g = 2 * sl; g < 2 * sl + 2 && g < G; ++g) {
       const int eb = mxo_xq_group_exp(x + 64 * g);
       int64_t P = 0, Q = 0;
       for (int j = 0; j < 64; ++j) {

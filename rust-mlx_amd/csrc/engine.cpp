@@ -123,6 +123,11 @@ struct Engine {
   float *o_part = nullptr, *ml_part = nullptr;
   void* head_ws = nullptr;
   float* hc_part = nullptr;  // partial sums of the fused HC projection
+  // exact-integer operand planes of the normed streams xn and of `mixed`,
+  // written by their producers (exact mode) and read by every projection of
+  // those activations
+  char* xn_plane = nullptr;
+  char* mixed_plane = nullptr;
   // per-step row table (device) and its pinned host mirror
   struct RowTable {
     uint32_t tokens[8];
@@ -176,6 +181,13 @@ enum : int {
 };
 
 bool ex(const Engine& e, int part) { return e.exact || (e.exact_parts & part) != 0; }
+
+// The operand plane of e.mixed when its producer wrote one (the exact
+// hyper-connection path), else null (the consumer stages its operands).
+const char* mixed_plane(const Engine& e, int rows) {
+  return ex(e, kExHc) && rows <= 8 ? e.mixed_plane : nullptr;
+}
+
 
 uint64_t tensor_seed(uint64_t base, int layer, int id) {
   // distinct streams per (layer, tensor); QWeight-style tensors use seed, +1, +2
@@ -448,6 +460,10 @@ int build(Engine& e) {
   MX_TRY(alloc(e, "act.head_ws", hws, &e.head_ws));
   MX_TRY(alloc(e, "act.hc_part", hc_fused_part_bytes(c.hc_rank + c.hc), &v));
   e.hc_part = static_cast<float*>(v);
+  MX_TRY(alloc(e, "act.xn_plane", xq_plane_bytes(c.hc * c.hidden), &v));
+  e.xn_plane = static_cast<char*>(v);
+  MX_TRY(alloc(e, "act.mixed_plane", xq_plane_bytes(c.hidden), &v));
+  e.mixed_plane = static_cast<char*>(v);
   MX_TRY(alloc(e, "rows", sizeof(Engine::RowTable), &v));
   e.dev_rows = static_cast<Engine::RowTable*>(v);
   if (hipHostMalloc(reinterpret_cast<void**>(&e.host_rows), sizeof(Engine::RowTable)) != hipSuccess)
@@ -476,8 +492,8 @@ int experts_gate_up(Engine& e, const LayerW& L, int rows) {
   if (experts_fast(e, L))
     return skinny_gate_up(e.mixed, e.ids, rows, c.top_k, L.gate, L.up, L.sgate, L.sup, e.moe_h,
                           e.stream);
-  return xq_gate_up(e.mixed, e.moe_plan_buf, rows, c.top_k, L.gate, L.up, L.sgate, L.sup,
-                    e.moe_h, e.stream);
+  return xq_gate_up(e.mixed, mixed_plane(e, rows), e.moe_plan_buf, rows, c.top_k, L.gate, L.up,
+                    L.sgate, L.sup, e.moe_h, e.stream);
 }
 
 int experts_down(Engine& e, const LayerW& L, int rows) {
@@ -532,8 +548,8 @@ int profile_experts(Engine& e, const LayerW& L, int rows) {
 // Exact components take the exact-integer projection (bit for bit the CPU
 // oracle's); a weight it does not cover is an error, never another path.
 int project(Engine& e, const QWeight& w, const uint16_t* x, int64_t xs, int rows,
-            const ProjEpilogue& ep, int part) {
-  if (ex(e, part)) return xq_dense(w, x, xs, rows, ep, e.stream);
+            const ProjEpilogue& ep, int part, const char* plane = nullptr) {
+  if (ex(e, part)) return xq_dense(w, x, xs, rows, ep, e.stream, plane);
   if (rows <= 8 && skinny_supported(w)) return skinny_dense(w, x, xs, rows, ep, e.stream);
   if (qmm_supported(w)) return qmm(w, x, xs, rows, ep, e.stream);
   return xq_dense(w, x, xs, rows, ep, e.stream);
@@ -544,7 +560,11 @@ int hc_forward(Engine& e, const HcW& w, int rows, uint16_t* mixed_out, uint16_t*
   if (!ex(e, kExHc) && hc_fused_supported(w.down, w.up, c.hc, c.hidden, c.hc_rank))
     return hc_fused(w.down, w.up, e.h, w.scale, rows, c.hc, c.hidden, c.hc_rank, c.rms_eps,
                     e.hc_part, mixed_out, inj_out, e.stream);
-  MX_TRY(hc_norm(e.h, w.scale, rows, c.hc, c.hidden, c.rms_eps, e.xn, e.stream));
+  // exact: the norm writes the down projection's operand plane, and the
+  // up-projection + mix writes the plane of `mixed` for its consumers
+  const bool exact = ex(e, kExHc) && rows <= 8;
+  MX_TRY(hc_norm(e.h, w.scale, rows, c.hc, c.hidden, c.rms_eps, e.xn, e.stream,
+                 exact ? e.xn_plane : nullptr));
   ProjEpilogue d{};
   d.mode = kHcDown;
   d.y = e.lo;
@@ -553,7 +573,10 @@ int hc_forward(Engine& e, const HcW& w, int rows, uint16_t* mixed_out, uint16_t*
   d.aux_stride = c.hc;
   d.rank = c.hc_rank;
   d.hc = c.hc;
-  MX_TRY(project(e, w.down, e.xn, int64_t(c.hc) * c.hidden, rows, d, kExHc));
+  MX_TRY(project(e, w.down, e.xn, int64_t(c.hc) * c.hidden, rows, d, kExHc,
+                 exact ? e.xn_plane : nullptr));
+  if (exact && mixed_out == e.mixed)
+    return xq_upmix(w.up, e.lo, rows, e.xn, c.hidden, mixed_out, e.mixed_plane, e.stream);
   ProjEpilogue u{};
   u.mode = kHcUpMix;
   u.y = mixed_out;
@@ -591,8 +614,9 @@ int record_layer(Engine& e, const LayerW& L, int rows, int groups, int t, bool h
       const size_t conv_per = size_t(c.conv_k - 1) * e.cd;
       const size_t state_per = size_t(c.gdn_hv) * c.gdn_dk * c.gdn_dv;
       // cache layout [slot][gdn layer]: slot index s -> s * n_gdn + gi
-      if (!ex(e, kExGdnProj) && t == 1 && !history && rows <= 8 && L.gdn_in.bits == 4 &&
-          skinny_supported(L.gdn_in) && c.conv_k <= kConvMaxTaps) {
+      const bool exact_in = ex(e, kExGdnProj);
+      if (t == 1 && !history && rows <= 8 && L.gdn_in.bits == 4 && c.conv_k <= kConvMaxTaps &&
+          (exact_in ? xq_supported(L.gdn_in) : skinny_supported(L.gdn_in))) {
         // the conv runs in the projection's epilogue
         pl.mode = kConv;
         pl.conv_state = e.conv_state + gi * conv_per;
@@ -602,9 +626,12 @@ int record_layer(Engine& e, const LayerW& L, int rows, int groups, int t, bool h
         pl.conv_stride = e.cd;
         pl.conv_ch = int(e.cd);
         pl.taps = c.conv_k;
-        MX_TRY(skinny_dense(L.gdn_in, e.mixed, c.hidden, rows, pl, e.stream));
+        if (exact_in)
+          MX_TRY(xq_dense(L.gdn_in, e.mixed, c.hidden, rows, pl, e.stream, mixed_plane(e, rows)));
+        else
+          MX_TRY(skinny_dense(L.gdn_in, e.mixed, c.hidden, rows, pl, e.stream));
       } else {
-        MX_TRY(project(e, L.gdn_in, e.mixed, c.hidden, rows, pl, kExGdnProj));
+        MX_TRY(project(e, L.gdn_in, e.mixed, c.hidden, rows, pl, kExGdnProj, mixed_plane(e, rows)));
         MX_TRY(gdn_conv(e.pbuf, e.P, groups, t, rt->gdn_slots, e.conv_state + gi * conv_per,
                         L.conv_w, e.cd, c.conv_k, e.conv_out, e.cd,
                         history ? e.hist_conv + size_t(gi) * (c.conv_k - 1 + c.max_verify) * e.cd
@@ -632,7 +659,7 @@ int record_layer(Engine& e, const LayerW& L, int rows, int groups, int t, bool h
       pl.mode = kPlain;
       pl.y = e.pbuf;
       pl.y_stride = e.Q;
-      MX_TRY(project(e, L.attn_in, e.mixed, c.hidden, rows, pl, kExAttnProj));
+      MX_TRY(project(e, L.attn_in, e.mixed, c.hidden, rows, pl, kExAttnProj, mixed_plane(e, rows)));
       const size_t layer_off = size_t(ai) * c.kv_heads * c.max_context * c.head_dim;
       MX_TRY(attn_prep(e.pbuf, e.Q, rows, rt->slots, rt->pos, L.q_norm, L.k_norm, c.rms_eps,
                        e.rope_cos, e.rope_sin, e.ad, e.qrot, e.k_cache + layer_off,
@@ -652,7 +679,7 @@ int record_layer(Engine& e, const LayerW& L, int rows, int groups, int t, bool h
     rl.mode = kPlain;
     rl.y = e.logits_r;
     rl.y_stride = c.experts + 1;
-    MX_TRY(project(e, L.router, e.mixed, c.hidden, rows, rl, kExMoe));
+    MX_TRY(project(e, L.router, e.mixed, c.hidden, rows, rl, kExMoe, mixed_plane(e, rows)));
     bool summed = false;  // slots summed and the streams written
     if (!e.prof && experts_fast(e, L)) {
       // the expert gate/up kernel routes the rows itself
@@ -713,7 +740,8 @@ int record_head(Engine& e, int rows, bool logits) {
     MX_TRY(skinny_head(e.head, e.mixed, rows, maxima, indices, &parts, e.stream,
                        logits ? e.logits : nullptr));
   else
-    MX_TRY(xq_head(e.head, e.mixed, rows, maxima, indices, logits ? e.logits : nullptr, &parts,
+    MX_TRY(xq_head(e.head, e.mixed, mixed_plane(e, rows), rows, maxima, indices,
+                   logits ? e.logits : nullptr, &parts,
                    e.stream));
   return argmax_reduce(maxima, indices, rows, parts, rt->next, e.stream);
 }

@@ -76,22 +76,29 @@ int qmm(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const Proj
         hipStream_t s);
 // exact-integer projections for 1..8 rows (xq.hip): the CPU oracle's
 // mxo_xq arithmetic bit for bit, on the int8 matrix cores
+// plane (nullable): the activation operands of x, written by its producer in
+// the layout of xq_plane_bytes(K) (xq_core.hpp), in place of a staging
 bool xq_supported(const QWeight& w);
+size_t xq_plane_bytes(int k);
 int xq_dense(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const ProjEpilogue& e,
-             hipStream_t s);
+             hipStream_t s, const char* plane = nullptr);
+// exact hyper-connection up-projection + stream mix (kHcUpMix arithmetic)
+// that also writes the operand plane of its output `mixed`
+int xq_upmix(const QWeight& up, const uint16_t* lo, int m, const uint16_t* xn, int hidden,
+             uint16_t* mixed, char* mixed_plane, hipStream_t s);
 struct MoePlan;
 // exact-integer expert MLPs over a MoePlan (same contracts as moe_gate_up /
 // moe_down) and greedy-head partials (same layout as head_partials, parts =
 // xq_head_parts(n); logits, when non-null, receives the bf16 logits)
-int xq_gate_up(const uint16_t* x, const MoePlan* plan, int rows, int top_k, const QBank& gate,
-               const QBank& up, const QWeight& sgate, const QWeight& sup, uint16_t* h,
-               hipStream_t s);
+int xq_gate_up(const uint16_t* x, const char* plane, const MoePlan* plan, int rows, int top_k,
+               const QBank& gate, const QBank& up, const QWeight& sgate, const QWeight& sup,
+               uint16_t* h, hipStream_t s);
 int xq_down(const uint16_t* h, const MoePlan* plan, const uint16_t* scores, int rows, int top_k,
             int inter, int shared_inter, const QBank& down, const QWeight& sdown, uint16_t* p,
             hipStream_t s);
 int xq_head_parts(int n);
-int xq_head(const QWeight& w, const uint16_t* x, int m, float* maxima, uint32_t* indices,
-            uint16_t* logits, int* parts_out, hipStream_t s);
+int xq_head(const QWeight& w, const uint16_t* x, const char* plane, int m, float* maxima,
+            uint32_t* indices, uint16_t* logits, int* parts_out, hipStream_t s);
 // matrix-core skinny projections for 1..8 rows (skinny.hip)
 bool skinny_supported(const QWeight& w);
 int skinny_dense(const QWeight& w, const uint16_t* x, int64_t x_stride, int m,
@@ -138,8 +145,9 @@ size_t hc_fused_part_bytes(int n_down);
 int hc_fused(const QWeight& down, const QWeight& up, const uint16_t* h, const uint16_t* scale,
              int M, int hc, int hidden, int rank, float eps, float* part, uint16_t* mixed,
              uint16_t* inj, hipStream_t s);
+// plane (nullable, rows <= 8): also the exact-integer operand plane of y
 int hc_norm(const uint16_t* x, const uint16_t* scale, int rows, int hc, int hidden, float eps,
-            uint16_t* y, hipStream_t s);
+            uint16_t* y, hipStream_t s, char* plane = nullptr);
 int embed(const QWeight& w, const uint32_t* ids, int count, int hc, uint16_t* out, hipStream_t s);
 // y[r][s][c] = bf16(e[r][c] + f[r hc + s][c]) (the MTP input, src/mtp.rs:103-106).
 int mtp_combine(const uint16_t* e, const uint16_t* f, int rows, int hc, int hidden, uint16_t* y,

@@ -14,6 +14,7 @@
 // steps follow MLX's bf16 graphs with one bf16 rounding per operation.
 #include "common.hpp"
 #include "kernels.hpp"
+#include "xq_core.hpp"
 #include "qmv_core.hpp"
 
 namespace mx {
@@ -149,10 +150,13 @@ void proj_m(const QWeight& w, const uint16_t* x, int64_t xs, int m, const ProjEp
 //   y = bf16((x * rsqrt(mean(x^2) + eps)) * (scale + 1))   in f32.
 // One workgroup (256 threads) per (row, stream); thread t sums x^2 over
 // columns t, t+256, ... in order; xor butterfly per wave; waves summed in order.
+// plane (nullable, rows <= 8): also writes the exact-integer operand plane of
+// y (xq_core.hpp), the hc * hidden values of row blockIdx.y as one K-long row
 __global__ __launch_bounds__(256) void hc_norm_kernel(const uint16_t* __restrict__ x,
                                                       const uint16_t* __restrict__ scale,
                                                       int hidden, float eps,
-                                                      uint16_t* __restrict__ y) {
+                                                      uint16_t* __restrict__ y,
+                                                      char* __restrict__ plane) {
   __shared__ float red[4];
   const int s = blockIdx.x;
   const int row = blockIdx.y;
@@ -170,9 +174,32 @@ __global__ __launch_bounds__(256) void hc_norm_kernel(const uint16_t* __restrict
   const float inv = 1.0f / __builtin_sqrtf(total / float(hidden) + eps);
   uint16_t* yr = y + (size_t(row) * hc + s) * hidden;
   const uint16_t* sc = scale + size_t(s) * hidden;
-  for (int c = threadIdx.x; c < hidden; c += 256) {
-    const float v = bf16_to_f32(xr[c]);
-    yr[c] = f32_to_bf16((v * inv) * (bf16_to_f32(sc[c]) + 1.0f));
+  if (!plane) {
+    for (int c = threadIdx.x; c < hidden; c += 256) {
+      const float v = bf16_to_f32(xr[c]);
+      yr[c] = f32_to_bf16((v * inv) * (bf16_to_f32(sc[c]) + 1.0f));
+    }
+    return;
+  }
+  // lane l of wave w takes values 16 (l / 16) .. +15 of group w * 16 + l % 16
+  // (and of every 64th group after it), writes them and their operands
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kb = lane >> 4;
+  const int ng = hidden / xq::kGroup;
+  for (int g0 = wave * 16; g0 < ng; g0 += 64) {
+    const int gl = g0 + (lane & 15);
+    const bool live = gl < ng;
+    float f[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      f[i] = 0.0f;
+      if (live) {
+        const int c = gl * xq::kGroup + 16 * kb + i;
+        const uint16_t o = f32_to_bf16((bf16_to_f32(xr[c]) * inv) * (bf16_to_f32(sc[c]) + 1.0f));
+        yr[c] = o;
+        f[i] = bf16_to_f32(o);
+      }
+    }
+    xq::digitize_unit(f, row, s * ng + gl, kb, live, plane, hc * ng);
   }
 }
 
@@ -240,8 +267,10 @@ int proj(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const Pro
 }
 
 int hc_norm(const uint16_t* x, const uint16_t* scale, int rows, int hc, int hidden, float eps,
-            uint16_t* y, hipStream_t s) {
-  hipLaunchKernelGGL(hc_norm_kernel, dim3(hc, rows), dim3(256), 0, s, x, scale, hidden, eps, y);
+            uint16_t* y, hipStream_t s, char* plane) {
+  if (plane && (rows > 8 || hidden % xq::kGroup != 0)) return MX_EUNSUPPORTED;
+  hipLaunchKernelGGL(hc_norm_kernel, dim3(hc, rows), dim3(256), 0, s, x, scale, hidden, eps, y,
+                     plane);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 

@@ -29,8 +29,6 @@ namespace mx {
 
 namespace {
 
-constexpr int kXqStageGroups = 64;  // groups staged in LDS (K <= 4096)
-
 struct XRows {
   const uint16_t* x;
   int64_t stride;
@@ -46,24 +44,17 @@ int raise_lds(F fn, int lb) {
   return MX_OK;
 }
 
-// Register-built A operand of one group for this lane (XREG): block bk's row
-// r = 4 bk + (l % 16) / 4, digit l % 4, values 16 (l / 16) .. +15 in
-// perm<BITS>() order; q and eb of the row this lane supplies.
-template <int BITS>
-__device__ __forceinline__ xq::v4i reg_operand(const XRows& xr, int M, int bk, int g, double& q,
+// Register-built A operand of one group for this lane (operands from
+// registers): block bk's row r = 4 bk + (l % 16) / 4, digit l % 4, values
+// 16 (l / 16) .. +15 in perm() order; q and eb of the row this lane supplies.
+template <class Rows>
+__device__ __forceinline__ xq::v4i reg_operand(const Rows& xr, int M, int bk, int g, double& q,
                                                int& eb) {
   const int lane = threadIdx.x & 63, kb = lane >> 4, d = lane & 3;
   const int r = 4 * bk + ((lane & 15) >> 2);
   float f[16];
   if (r < M) {
-    const uint4* src = reinterpret_cast<const uint4*>(xr(r) + size_t(g) * xq::kGroup + 16 * kb);
-    const uint4 a = src[0], b = src[1];
-    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      f[2 * i] = u2f(w[i] << 16);
-      f[2 * i + 1] = u2f(w[i] & 0xffff0000u);
-    }
+    xq::load16(xr(r) + size_t(g) * xq::kGroup + 16 * kb, f);
   } else {
 #pragma unroll
     for (int i = 0; i < 16; ++i) f[i] = 0.0f;
@@ -88,8 +79,7 @@ __device__ __forceinline__ xq::v4i reg_operand(const XRows& xr, int M, int bk, i
   for (int pw = 0; pw < 4; ++pw) {
     uint32_t v = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      v |= ((xq::digits(X[xq::perm<BITS>(4 * pw + i)]) >> sh) & 0xffu) << (8 * i);
+    for (int i = 0; i < 4; ++i) v |= ((xq::digits(X[xq::perm(4 * pw + i)]) >> sh) & 0xffu) << (8 * i);
     o[pw] = v;
   }
   xq::v4i op;
@@ -97,82 +87,151 @@ __device__ __forceinline__ xq::v4i reg_operand(const XRows& xr, int M, int bk, i
   return op;
 }
 
-// The projection values of one workgroup: wave (t, ks) streams the weight
-// row of its lane (crow / srow / brow: tile t's row l % 16) over slice ks's
-// groups against activation rows xr(0..M-1) (staged in LDS, or built in
-// registers when XREG), and yt[m][t * 16 + j] receives the fp32 result of
-// activation row m and tile row j.  `pre` runs once the slice's weight loads
-// are issued (the caller's own prefetches).  Ends with a barrier.
-template <int BITS, int T, int KS, bool XREG, class Rows, class Pre>
+// Where a kernel's activation operands come from.
+enum : int {
+  kSrcStage = 0,     // staged by the workgroup into LDS from the bf16 rows
+  kSrcReg = 1,       // built by each wave in registers (deep rows, no plane)
+  kSrcPlane = 2,     // read by each wave from the producer's plane in global memory
+  kSrcPlaneLds = 3,  // the producer's plane copied once per workgroup into LDS
+};
+
+template <int BITS>
+constexpr int batch_groups() {
+  return BITS == 8 ? 4 : 8;  // groups per load batch (8-bit codes are twice as wide)
+}
+
+// LDS bytes of xq_tiles: the staged or copied operands of G groups, and the
+// slice sums of T tiles when KS > 1 (they reuse the operand area).
+__host__ __device__ constexpr int tiles_lds(int G, int T, int KS, int SRC) {
+  const int ops = (SRC == kSrcStage || SRC == kSrcPlaneLds) ? xq::stage_bytes(G) : 0;
+  const int sums = KS > 1 ? ((G + 1) / 2) * T * 8 * 16 * 8 : 0;
+  const int b = ops > sums ? ops : sums;
+  return b > 16 ? b : 16;
+}
+
+// The projection values of one workgroup.  Wave (t, ks) streams the weight
+// row of its lane (crow / srow / brow: tile t's row l % 16) over slices
+// [ks SPW, ks SPW + SPW) (two groups each) against activation rows
+// xr(0..M-1), in load batches kept two deep; `blocks` says which four-row
+// blocks of activation rows to compute (bit 0: rows 0-3, bit 1: rows 4-7).
+// With KS == 1 the wave adds its slice sums in order itself; otherwise the
+// slice sums meet in LDS and are added in slice order.  yt[m][t * 16 + j]
+// receives the fp32 result of activation row m and tile row j.  `pre` runs
+// once the first weight loads are issued.  Ends with a barrier.
+template <int BITS, int T, int KS, int SPW, int SRC, class Rows, class Pre>
 __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
                                          const uint16_t* __restrict__ srow,
                                          const uint16_t* __restrict__ brow, int K, int M,
-                                         const Rows& xr, char* lds, double* red, float* yt,
-                                         Pre&& pre) {
+                                         int blocks, const Rows& xr, const char* plane, char* lds,
+                                         float* yt, Pre&& pre) {
   constexpr int NC = 16 * T, NT = 64 * T * KS;
+  constexpr int NG = 2 * SPW;
+  constexpr int B = NG < batch_groups<BITS>() ? NG : batch_groups<BITS>();
+  constexpr int NB = NG / B;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane & 15, kb = lane >> 4;
   const int t = wave / KS, ks = wave - t * KS;
-  const int G = K / xq::kGroup, gps = G / KS, g0 = ks * gps;
-  // the slice's code words, scales and biases, all issued up front
-  xq::Codes<BITS> c[xq::kGroupsPerSlice];
-  uint16_t sv[xq::kGroupsPerSlice], bv[xq::kGroupsPerSlice];
+  const int G = K / xq::kGroup, S = (G + 1) / 2;
+  const int gbeg = 2 * ks * SPW, gend = min(gbeg + NG, G);
+  xq::Codes<BITS> c[2][B];
+  uint16_t sv[2][B], bv[2][B];
+  auto load_batch = [&](int buf, int bi) {
 #pragma unroll
-  for (int i = 0; i < xq::kGroupsPerSlice; ++i) {
-    const int g = g0 + min(i, gps - 1);
-    xq::load_codes<BITS>(crow, g, kb, c[i]);
-    sv[i] = srow[g];
-    bv[i] = brow[g];
-  }
+    for (int i = 0; i < B; ++i) {
+      const int g = min(gbeg + bi * B + i, gend - 1);
+      xq::load_codes<BITS>(crow, g, kb, c[buf][i]);
+      sv[buf][i] = srow[g];
+      bv[buf][i] = brow[g];
+    }
+  };
+  load_batch(0, 0);
+  if constexpr (NB > 1) load_batch(1, 1);
   pre();
-  const bool two = M > 4;
-  double acc[2] = {0.0, 0.0};
-  if constexpr (!XREG) {
-    xq::stage<BITS, NT>(lds, xr, M, 0, G);
-    const double* qs = reinterpret_cast<const double*>(lds + G * xq::kGroupBytes);
-    const int* es = reinterpret_cast<const int*>(lds + G * (xq::kGroupBytes + 64));
-#pragma unroll
-    for (int i = 0; i < xq::kGroupsPerSlice; ++i) {
-      if (i < gps) {
-        const int g = g0 + i;
-        const char* ab = lds + g * xq::kGroupBytes + lane * 16;
-        const xq::v4i a0 = *reinterpret_cast<const xq::v4i*>(ab);
-        const xq::v4i a1 = *reinterpret_cast<const xq::v4i*>(ab + xq::kBlockBytes);
-        xq::group_step<BITS>(a0, a1, two, xq::b_operand<BITS>(c[i]), qs[g * 8 + kb],
-                             qs[g * 8 + 4 + kb], es[g * 8 + kb], es[g * 8 + 4 + kb],
-                             double(bf16_to_f32(sv[i])), double(bf16_to_f32(bv[i])), acc);
-      }
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < xq::kGroupsPerSlice; ++i) {
-      if (i < gps) {
-        const int g = g0 + i;
-        double q0, q1 = 0.0;
-        int e0, e1 = 1;
-        const xq::v4i a0 = reg_operand<BITS>(xr, M, 0, g, q0, e0);
-        xq::v4i a1 = {0, 0, 0, 0};
-        if (two) a1 = reg_operand<BITS>(xr, M, 1, g, q1, e1);
-        // this lane receives activation row kb of each block: the Q and Eb
-        // of that row sit in the lanes that supplied it (l % 16 = 4 kb)
-        const int src = 4 * kb;
-        const double rq0 = __shfl(q0, src, 64), rq1 = __shfl(q1, src, 64);
-        const int re0 = __shfl(e0, src, 64), re1 = __shfl(e1, src, 64);
-        xq::group_step<BITS>(a0, a1, two, xq::b_operand<BITS>(c[i]), rq0, rq1, re0, re1,
-                             double(bf16_to_f32(sv[i])), double(bf16_to_f32(bv[i])), acc);
-      }
-    }
+  const char* src = lds;
+  if constexpr (SRC == kSrcStage) {
+    xq::stage<NT>(lds, xr, M, 0, G);
+  } else if constexpr (SRC == kSrcPlaneLds) {
+    const int n16 = xq::stage_bytes(G) / 16;
+    for (int i = threadIdx.x; i < n16; i += NT)
+      reinterpret_cast<uint4*>(lds)[i] = reinterpret_cast<const uint4*>(plane)[i];
+    __syncthreads();
+  } else if constexpr (SRC == kSrcPlane) {
+    src = plane;
   }
-  // slice sums in slice order, from +0, then one rounding to fp32
-  red[((ks * T + t) * 8 + kb) * 16 + j] = acc[0];
-  red[((ks * T + t) * 8 + 4 + kb) * 16 + j] = acc[1];
-  __syncthreads();
-  for (int i = threadIdx.x; i < 8 * NC; i += NT) {
-    const int m = i / NC, cc = i - m * NC;
-    const int tt = cc >> 4, jj = cc & 15;
-    double total = 0.0;
+  const double* qs = reinterpret_cast<const double*>(src + xq::plane_q_offset(G));
+  const int* es = reinterpret_cast<const int*>(src + xq::plane_e_offset(G));
+  double acc[2] = {0.0, 0.0}, tot[2] = {0.0, 0.0}, ss[KS > 1 ? SPW : 1][2];
 #pragma unroll
-    for (int k = 0; k < KS; ++k) total = total + red[((k * T + tt) * 8 + m) * 16 + jj];
-    yt[i] = float(total);
+  for (int bi = 0; bi < NB; ++bi) {
+    const int buf = bi & 1;
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+      const int gl = bi * B + i, g = gbeg + gl;
+      if (g < gend) {
+        xq::v4i a0, a1;
+        double q0 = 0.0, q1 = 0.0;
+        int e0 = 1, e1 = 1;
+        if constexpr (SRC == kSrcReg) {
+          a0 = reg_operand(xr, M, 0, g, q0, e0);
+          a1 = (blocks & 2) ? reg_operand(xr, M, 1, g, q1, e1) : a0;
+          // this lane receives activation row kb of each block: the Q and Eb
+          // of that row sit in the lanes that supplied it (l % 16 = 4 kb)
+          q0 = __shfl(q0, 4 * kb, 64);
+          e0 = __shfl(e0, 4 * kb, 64);
+          q1 = __shfl(q1, 4 * kb, 64);
+          e1 = __shfl(e1, 4 * kb, 64);
+        } else {
+          const char* ab = src + g * xq::kGroupBytes + lane * 16;
+          a0 = *reinterpret_cast<const xq::v4i*>(ab);
+          a1 = *reinterpret_cast<const xq::v4i*>(ab + xq::kBlockBytes);
+          q0 = qs[g * 8 + kb];
+          q1 = qs[g * 8 + 4 + kb];
+          e0 = es[g * 8 + kb];
+          e1 = es[g * 8 + 4 + kb];
+        }
+        xq::group_step<BITS>(a0, a1, blocks, xq::b_operand<BITS>(c[buf][i]), q0, q1, e0, e1,
+                             double(bf16_to_f32(sv[buf][i])), double(bf16_to_f32(bv[buf][i])),
+                             acc);
+        // a slice ends after its second group, or after the last group of an
+        // odd count
+        if ((gl & 1) || g + 1 == gend) {
+          if constexpr (KS == 1) {
+            tot[0] = tot[0] + acc[0];
+            tot[1] = tot[1] + acc[1];
+          } else {
+            ss[gl >> 1][0] = acc[0];
+            ss[gl >> 1][1] = acc[1];
+          }
+          acc[0] = 0.0;
+          acc[1] = 0.0;
+        }
+      }
+    }
+    if (bi + 2 < NB) load_batch(buf, bi + 2);
+  }
+  if constexpr (KS == 1) {
+    if constexpr (SRC == kSrcStage || SRC == kSrcPlaneLds) __syncthreads();
+    yt[kb * NC + t * 16 + j] = float(tot[0]);
+    yt[(4 + kb) * NC + t * 16 + j] = float(tot[1]);
+  } else {
+    // slice sums in slice order, from +0, then one rounding to fp32
+    if constexpr (SRC == kSrcStage || SRC == kSrcPlaneLds) __syncthreads();
+    double* red = reinterpret_cast<double*>(lds);
+#pragma unroll
+    for (int sl = 0; sl < SPW; ++sl) {
+      const int gs = ks * SPW + sl;
+      if (gs < S) {
+        red[((gs * T + t) * 8 + kb) * 16 + j] = ss[sl][0];
+        red[((gs * T + t) * 8 + 4 + kb) * 16 + j] = ss[sl][1];
+      }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < 8 * NC; i += NT) {
+      const int m = i / NC, cc = i - m * NC;
+      const int tt = cc >> 4, jj = cc & 15;
+      double total = 0.0;
+      for (int k = 0; k < S; ++k) total = total + red[((k * T + tt) * 8 + m) * 16 + jj];
+      yt[i] = float(total);
+    }
   }
   __syncthreads();
 }
@@ -181,13 +240,13 @@ __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
 // tg*16T .. tg*16T + 16T - 1 (tile t: rows tg*16T + 16t + j); for kHcUpMix
 // (T = 4) it covers columns tg*16 .. tg*16 + 15 of the four streams (tile t:
 // rows t*H + tg*16 + j).
-template <int BITS, int MODE, int T, int KS, bool XREG>
+template <int BITS, int MODE, int T, int KS, int SPW, int SRC>
 __global__ __launch_bounds__(64 * T * KS) void xq_dense_kernel(QWeight w,
                                                                const uint16_t* __restrict__ x,
                                                                int64_t x_stride, int M,
+                                                               const char* __restrict__ plane,
                                                                ProjEpilogue e) {
   extern __shared__ __align__(16) char lds[];
-  __shared__ double red[KS * T * 8 * 16];
   __shared__ float yt[8 * 16 * T];
   constexpr int NC = 16 * T, NT = 64 * T * KS;
   const int tg = blockIdx.x;
@@ -200,9 +259,10 @@ __global__ __launch_bounds__(64 * T * KS) void xq_dense_kernel(QWeight w,
     row = min(tg * NC + t * 16 + j, n - 1);
   ProjFinish<MODE, NC, NT> fin;
   fin.begin(e, tg, M, n);
-  xq_tiles<BITS, T, KS, XREG>(w.codes + size_t(row) * (size_t(w.k) * BITS / 32),
-                              w.scales + size_t(row) * G, w.biases + size_t(row) * G, w.k, M,
-                              XRows{x, x_stride}, lds, red, yt, [&] { fin.prefetch(e); });
+  xq_tiles<BITS, T, KS, SPW, SRC>(w.codes + size_t(row) * (size_t(w.k) * BITS / 32),
+                                  w.scales + size_t(row) * G, w.biases + size_t(row) * G, w.k, M,
+                                  M > 4 ? 3 : 1, XRows{x, x_stride}, plane, lds, yt,
+                                  [&] { fin.prefetch(e); });
   fin.finish(yt, e, tg, M, n);
 }
 
@@ -227,59 +287,142 @@ __device__ __forceinline__ QWeight bank_matrix(const QBank& b, int expert, const
                  b.bits, b.group_size};
 }
 
-// Expert gate/up + SwiGLU for one plan entry (blockIdx.y) and 32
-// intermediate rows (blockIdx.x): tiles 0-1 are gate rows, tiles 2-3 the same
-// up rows; h[row][slot][i] = bf16(bf16(silu(bf16(g))) * bf16(u)) for the
-// entry's member routes (the exact kernels' SwiGLU, moe.hip gate_up_body).
-template <int BITS, int KS>
-__global__ __launch_bounds__(64 * 4 * KS) void xq_gate_up_kernel(
-    const uint16_t* __restrict__ x, const MoePlan* __restrict__ plan, int top_k, QBank gate,
-    QBank up, QWeight sgate, QWeight sup, uint16_t* __restrict__ h, int hs) {
+// Copies a plane of G groups (xq_core.hpp layout) into LDS: every thread
+// issues all of its loads before its first store.  Ends with a barrier.
+template <int NT>
+__device__ __forceinline__ void copy_plane(char* lds, const char* plane, int G) {
+  constexpr int kMaxPer = 12;  // 68.6 KiB (K = 2048) over 512 threads
+  const int n16 = xq::stage_bytes(G) / 16;
+  uint4 v[kMaxPer];
+#pragma unroll
+  for (int k = 0; k < kMaxPer; ++k) {
+    const int i = int(threadIdx.x) + k * NT;
+    if (i < n16) v[k] = reinterpret_cast<const uint4*>(plane)[i];
+  }
+#pragma unroll
+  for (int k = 0; k < kMaxPer; ++k) {
+    const int i = int(threadIdx.x) + k * NT;
+    if (i < n16) reinterpret_cast<uint4*>(lds)[i] = v[k];
+  }
+  __syncthreads();
+}
+
+// Expert gate/up + SwiGLU for one plan entry (blockIdx.y) and 128
+// intermediate rows (blockIdx.x).  Every wave is independent: it owns 16
+// intermediate rows, streams their gate rows and then their up rows over the
+// whole depth (load batches kept D deep across both passes, so the memory
+// system streams while the matrix cores and VALUs work), adds each pass's
+// slice sums in order in registers, and writes h[row][slot][i] =
+// bf16(bf16(silu(bf16 g)) * bf16 u) for the member routes (the exact
+// kernels' SwiGLU, moe.hip gate_up_body).  Operands: the plane of x copied
+// into LDS (every row of x by index), or the members staged in order.
+template <int BITS, int SPW, int SRC>
+__global__ __launch_bounds__(512) void xq_gate_up_kernel(
+    const uint16_t* __restrict__ x, const char* __restrict__ plane,
+    const MoePlan* __restrict__ plan, int top_k, QBank gate, QBank up, QWeight sgate, QWeight sup,
+    uint16_t* __restrict__ h, int hs) {
   extern __shared__ __align__(16) char lds[];
-  __shared__ double red[KS * 4 * 8 * 16];
-  __shared__ float yt[8 * 64];
   __shared__ int ro[8], so[8];
+  constexpr int NG = 2 * SPW;                       // groups per pass (at most)
+  constexpr int B = NG < batch_groups<BITS>() ? NG : batch_groups<BITS>();
+  constexpr int NBP = NG / B;                       // batches per pass
+  constexpr int NB = 2 * NBP;                       // gate pass, then up pass
+  constexpr int D = NB < 3 ? NB : 3;                // batches in flight
   const int entry = blockIdx.y;
   if (entry >= plan->count) return;
   const int expert = plan->expert[entry];
   const QWeight gw = bank_matrix(gate, expert, sgate);
   const QWeight uw = bank_matrix(up, expert, sup);
   const int inter = gw.n, hidden = gw.k;
-  const int i0 = blockIdx.x * 32;
+  const int i0 = blockIdx.x * 128;
   if (i0 >= inter) return;
   const int M = plan->m[entry];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane & 15, kb = lane >> 4;
+  const int G = hidden / xq::kGroup;
+  const int row = min(i0 + 16 * wave + j, inter - 1);
+  const size_t wpr = size_t(hidden) * BITS / 32;
+  const uint32_t* crow[2] = {gw.codes + row * wpr, uw.codes + row * wpr};
+  const uint16_t* srow[2] = {gw.scales + size_t(row) * G, uw.scales + size_t(row) * G};
+  const uint16_t* brow[2] = {gw.biases + size_t(row) * G, uw.biases + size_t(row) * G};
+  xq::Codes<BITS> c[D][B];
+  uint16_t sv[D][B], bv[D][B];
+  auto load_batch = [&](int buf, int bi) {
+    const int pass = bi / NBP;
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+      const int g = min((bi % NBP) * B + i, G - 1);
+      xq::load_codes<BITS>(crow[pass], g, kb, c[buf][i]);
+      sv[buf][i] = srow[pass][g];
+      bv[buf][i] = brow[pass][g];
+    }
+  };
+#pragma unroll
+  for (int d = 0; d < D; ++d) load_batch(d, d);
   if (threadIdx.x < 8) {
     ro[threadIdx.x] = plan->row[entry][threadIdx.x];
     so[threadIdx.x] = plan->slot[entry][threadIdx.x];
   }
-  __syncthreads();
-  const int j = threadIdx.x & 15, t = (threadIdx.x >> 6) / KS;
-  const QWeight& mw = t < 2 ? gw : uw;
-  const int row = min(i0 + 16 * (t & 1) + j, inter - 1);
-  const int G = hidden / xq::kGroup;
-  xq_tiles<BITS, 4, KS, false>(mw.codes + size_t(row) * (size_t(hidden) * BITS / 32),
-                               mw.scales + size_t(row) * G, mw.biases + size_t(row) * G, hidden,
-                               M, MemberRows{x, hidden, 0, ro, so}, lds, red, yt, [] {});
-  for (int i = threadIdx.x; i < 8 * 32; i += 64 * 4 * KS) {
-    const int m = i >> 5, c = i & 31;
-    if (m >= M || i0 + c >= inter) continue;
-    const float gv = round_bf16(yt[m * 64 + c]);
-    const float uv = round_bf16(yt[m * 64 + 32 + c]);
-    const float silu = round_bf16(gv * sigmoid_bf16(gv));
-    h[(size_t(ro[m]) * (top_k + 1) + so[m]) * hs + i0 + c] = f32_to_bf16(silu * uv);
+  int blocks = 0;
+  if constexpr (SRC == kSrcPlaneLds) {
+    for (int m = 0; m < M; ++m) blocks |= plan->row[entry][m] < 4 ? 1 : 2;
+    copy_plane<512>(lds, plane, G);
+  } else {
+    blocks = M > 4 ? 3 : 1;
+    __syncthreads();
+    xq::stage<512>(lds, MemberRows{x, hidden, 0, ro, so}, M, 0, G);
+  }
+  const double* qs = reinterpret_cast<const double*>(lds + xq::plane_q_offset(G));
+  const int* es = reinterpret_cast<const int*>(lds + xq::plane_e_offset(G));
+  double acc[2] = {0.0, 0.0}, tot[2][2] = {{0.0, 0.0}, {0.0, 0.0}};
+#pragma unroll
+  for (int bi = 0; bi < NB; ++bi) {
+    const int buf = bi % D, pass = bi / NBP;
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+      const int gl = (bi % NBP) * B + i;
+      if (gl < G) {
+        const char* ab = lds + gl * xq::kGroupBytes + lane * 16;
+        xq::group_step<BITS>(*reinterpret_cast<const xq::v4i*>(ab),
+                             *reinterpret_cast<const xq::v4i*>(ab + xq::kBlockBytes), blocks,
+                             xq::b_operand<BITS>(c[buf][i]), qs[gl * 8 + kb], qs[gl * 8 + 4 + kb],
+                             es[gl * 8 + kb], es[gl * 8 + 4 + kb], double(bf16_to_f32(sv[buf][i])),
+                             double(bf16_to_f32(bv[buf][i])), acc);
+        // a slice ends after its second group, or after the last of an odd count
+        if ((gl & 1) || gl + 1 == G) {
+          tot[pass][0] = tot[pass][0] + acc[0];
+          tot[pass][1] = tot[pass][1] + acc[1];
+          acc[0] = 0.0;
+          acc[1] = 0.0;
+        }
+      }
+    }
+    if (bi + D < NB) load_batch(buf, bi + D);
+  }
+  // lane (kb, j) holds activation rows kb and 4 + kb of column i0 + 16 w + j
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+    const int xr = 4 * blk + kb;  // row of x (plane) or member index (staged)
+    for (int m = 0; m < M; ++m) {
+      const bool hit = SRC == kSrcPlaneLds ? ro[m] == xr : m == xr;
+      if (!hit || i0 + 16 * wave + j >= inter) continue;
+      const float gv = round_bf16(float(tot[0][blk]));
+      const float uv = round_bf16(float(tot[1][blk]));
+      const float silu = round_bf16(gv * sigmoid_bf16(gv));
+      h[(size_t(ro[m]) * (top_k + 1) + so[m]) * hs + i0 + 16 * wave + j] = f32_to_bf16(silu * uv);
+    }
   }
 }
 
 // Expert down + route score for one plan entry (blockIdx.y) and 64 output
 // columns (blockIdx.x): p[row][slot][c] = bf16(bf16(down h) * score) for
 // routed slots, bf16(down h) for the shared slot (moe.hip down_body).
-template <int BITS, int KS>
-__global__ __launch_bounds__(64 * 4 * KS) void xq_down_kernel(
-    const uint16_t* __restrict__ h, const MoePlan* __restrict__ plan,
-    const uint16_t* __restrict__ scores, int top_k, QBank down, QWeight sdown,
-    uint16_t* __restrict__ p, int hs) {
+template <int BITS, int SPW>
+__global__ __launch_bounds__(256) void xq_down_kernel(const uint16_t* __restrict__ h,
+                                                      const MoePlan* __restrict__ plan,
+                                                      const uint16_t* __restrict__ scores,
+                                                      int top_k, QBank down, QWeight sdown,
+                                                      uint16_t* __restrict__ p, int hs) {
   extern __shared__ __align__(16) char lds[];
-  __shared__ double red[KS * 4 * 8 * 16];
   __shared__ float yt[8 * 64];
   __shared__ int ro[8], so[8];
   const int entry = blockIdx.y;
@@ -295,20 +438,72 @@ __global__ __launch_bounds__(64 * 4 * KS) void xq_down_kernel(
     so[threadIdx.x] = plan->slot[entry][threadIdx.x];
   }
   __syncthreads();
-  const int j = threadIdx.x & 15, t = (threadIdx.x >> 6) / KS;
+  const int j = threadIdx.x & 15, t = threadIdx.x >> 6;
   const int row = min(c0 + 16 * t + j, hidden - 1);
   const int G = inter / xq::kGroup;
-  xq_tiles<BITS, 4, KS, false>(dw.codes + size_t(row) * (size_t(inter) * BITS / 32),
-                               dw.scales + size_t(row) * G, dw.biases + size_t(row) * G, inter,
-                               M, MemberRows{h, int64_t(top_k + 1) * hs, hs, ro, so}, lds, red, yt,
-                               [] {});
-  for (int i = threadIdx.x; i < 8 * 64; i += 64 * 4 * KS) {
+  xq_tiles<BITS, 4, 1, SPW, kSrcStage>(dw.codes + size_t(row) * (size_t(inter) * BITS / 32),
+                                       dw.scales + size_t(row) * G, dw.biases + size_t(row) * G,
+                                       inter, M, M > 4 ? 3 : 1,
+                                       MemberRows{h, int64_t(top_k + 1) * hs, hs, ro, so}, nullptr,
+                                       lds, yt, [] {});
+  for (int i = threadIdx.x; i < 8 * 64; i += 256) {
     const int m = i >> 6, c = i & 63;
     if (m >= M || c0 + c >= hidden) continue;
     const bool routed = so[m] < top_k;
     const float dv = round_bf16(yt[i]);
     const float sc = routed ? bf16_to_f32(scores[size_t(ro[m]) * top_k + so[m]]) : 1.0f;
     p[(size_t(ro[m]) * (top_k + 1) + so[m]) * hidden + c0 + c] = f32_to_bf16(routed ? dv * sc : dv);
+  }
+}
+
+// Hyper-connection up-projection and stream mix for one 64-column group of
+// `mixed` (blockIdx.x = tg): tile t = 4 s + ct holds up rows
+// s * H + 64 tg + 16 ct + j (K = the rank); each column takes the kHcUpMix
+// arithmetic of ProjFinish, then wave 0 writes the group's operand plane, so
+// every consumer of `mixed` reads its operands ready-made.
+template <int BITS, int SPW>
+__global__ __launch_bounds__(1024) void xq_upmix_kernel(QWeight w, const uint16_t* __restrict__ lo,
+                                                        int M, const uint16_t* __restrict__ xn,
+                                                        int hidden, uint16_t* __restrict__ mixed,
+                                                        char* __restrict__ plane) {
+  extern __shared__ __align__(16) char lds[];
+  __shared__ float yt[8 * 256];
+  __shared__ float mix[8 * 64];
+  const int tg = blockIdx.x;
+  const int j = threadIdx.x & 15, t = threadIdx.x >> 6;
+  const int row = (t >> 2) * hidden + tg * 64 + (t & 3) * 16 + j;
+  const int G = w.k / xq::kGroup;
+  xq_tiles<BITS, 16, 1, SPW, kSrcStage>(w.codes + size_t(row) * (size_t(w.k) * BITS / 32),
+                                        w.scales + size_t(row) * G, w.biases + size_t(row) * G,
+                                        w.k, M, M > 4 ? 3 : 1, XRows{lo, w.k}, nullptr, lds, yt,
+                                        [] {});
+  for (int i = threadIdx.x; i < 8 * 64; i += 1024) {
+    const int m = i >> 6, c = i & 63;
+    float v = 0.0f;
+    if (m < M) {
+      float sum = 0.0f;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const float p = round_bf16(yt[m * 256 + s * 64 + c]);
+        const float x = bf16_to_f32(xn[size_t(m) * 4 * hidden + size_t(s) * hidden + tg * 64 + c]);
+        sum = sum + round_bf16(sigmoid_bf16(p) * x);
+      }
+      const uint16_t o = f32_to_bf16(round_bf16(sum) / 4.0f);
+      mixed[size_t(m) * hidden + tg * 64 + c] = o;
+      v = bf16_to_f32(o);
+    }
+    mix[i] = v;
+  }
+  if (!plane) return;
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    // lane l: row l % 8 (lanes with l % 16 >= 8 repeat a row and only join
+    // the butterflies), values 16 (l / 16) .. +15 of the group
+    const int lane = threadIdx.x, m = lane & 7, kb = lane >> 4;
+    float f[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) f[i] = mix[m * 64 + 16 * kb + i];
+    xq::digitize_unit(f, m, tg, kb, (lane & 15) < 8 && m < M, plane, hidden / xq::kGroup);
   }
 }
 
@@ -320,199 +515,289 @@ __device__ __forceinline__ void better_of(float v, uint32_t id, float& best, uin
 }
 
 // Greedy head: per activation row, the best (bf16 logit, lowest id) of the
-// workgroup's 64 vocabulary rows (NaN never wins; nothing above -inf keeps id
+// workgroup's 256 vocabulary rows (16 waves, each streaming a 16-row tile
+// over the whole depth; NaN never wins; nothing above -inf keeps id
 // 0xffffffff), and, when asked, the bf16 logits themselves.
-template <int BITS, int KS>
-__global__ __launch_bounds__(64 * 4 * KS) void xq_head_kernel(QWeight w,
-                                                              const uint16_t* __restrict__ x,
-                                                              int M, float* __restrict__ maxima,
-                                                              uint32_t* __restrict__ indices,
-                                                              uint16_t* __restrict__ logits) {
+template <int BITS, int SPW, int SRC>
+__global__ __launch_bounds__(1024) void xq_head_kernel(QWeight w, const uint16_t* __restrict__ x,
+                                                       const char* __restrict__ plane, int M,
+                                                       float* __restrict__ maxima,
+                                                       uint32_t* __restrict__ indices,
+                                                       uint16_t* __restrict__ logits) {
   extern __shared__ __align__(16) char lds[];
-  __shared__ double red[KS * 4 * 8 * 16];
-  __shared__ float yt[8 * 64];
+  __shared__ float yt[8 * 256];
+  __shared__ float bv[16][8];
+  __shared__ uint32_t bi[16][8];
   const int tg = blockIdx.x, parts = gridDim.x;
-  const int j = threadIdx.x & 15, t = (threadIdx.x >> 6) / KS;
+  const int j = threadIdx.x & 15, t = threadIdx.x >> 6;
   const int n = w.n, G = w.k / xq::kGroup;
-  const int row = min(tg * 64 + 16 * t + j, n - 1);
-  xq_tiles<BITS, 4, KS, false>(w.codes + size_t(row) * (size_t(w.k) * BITS / 32),
-                               w.scales + size_t(row) * G, w.biases + size_t(row) * G, w.k, M,
-                               XRows{x, w.k}, lds, red, yt, [] {});
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int m = wave; m < M; m += 4 * KS) {
-    const int r = tg * 64 + lane;
+  const int row = min(tg * 256 + 16 * t + j, n - 1);
+  xq_tiles<BITS, 16, 1, SPW, SRC>(w.codes + size_t(row) * (size_t(w.k) * BITS / 32),
+                                  w.scales + size_t(row) * G, w.biases + size_t(row) * G, w.k, M,
+                                  M > 4 ? 3 : 1, XRows{x, w.k}, plane, lds, yt, [] {});
+  // wave t ranks columns 16 t .. +15 for every row (lane = 16 m' + c, two
+  // passes of four rows), then wave 0 ranks the 16 wave bests per row
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    const int m = 4 * half + (lane >> 4), c = 16 * t + (lane & 15);
+    const int r = tg * 256 + c;
     float best = u2f(0xff800000u);
     uint32_t best_id = 0xffffffffu;
-    if (r < n) {
-      better_of(round_bf16(yt[m * 64 + lane]), uint32_t(r), best, best_id);
-      if (logits) logits[size_t(m) * n + r] = f32_to_bf16(yt[m * 64 + lane]);
+    if (m < M && r < n) {
+      better_of(round_bf16(yt[m * 256 + c]), uint32_t(r), best, best_id);
+      if (logits) logits[size_t(m) * n + r] = f32_to_bf16(yt[m * 256 + c]);
     }
-    for (int o = 32; o > 0; o >>= 1) {
+    for (int o = 8; o > 0; o >>= 1) {
       const float v = __shfl_xor(best, o, 64);
       const uint32_t id = uint32_t(__shfl_xor(int(best_id), o, 64));
       better_of(v, id, best, best_id);
     }
-    if (lane == 0) {
-      maxima[size_t(m) * parts + tg] = best;
-      indices[size_t(m) * parts + tg] = best_id;
+    if ((lane & 15) == 0) {
+      bv[t][m] = best;
+      bi[t][m] = best_id;
     }
+  }
+  __syncthreads();
+  if (threadIdx.x < 8 && int(threadIdx.x) < M) {
+    const int m = threadIdx.x;
+    float best = bv[0][m];
+    uint32_t best_id = bi[0][m];
+    for (int w2 = 1; w2 < 16; ++w2) better_of(bv[w2][m], bi[w2][m], best, best_id);
+    maxima[size_t(m) * parts + tg] = best;
+    indices[size_t(m) * parts + tg] = best_id;
   }
 }
 
-template <int BITS, int MODE, int T, int KS, bool XREG>
-int launch_xq(const QWeight& w, const uint16_t* x, int64_t xs, int m, const ProjEpilogue& e,
-              hipStream_t s) {
+template <int BITS, int MODE, int T, int KS, int SPW, int SRC>
+int launch_xq(const QWeight& w, const uint16_t* x, int64_t xs, int m, const char* plane,
+              const ProjEpilogue& e, hipStream_t s) {
   const int groups = MODE == kHcUpMix ? (e.hidden + 15) / 16 : (w.n + 16 * T - 1) / (16 * T);
-  const int lb = XREG ? 0 : xq::stage_bytes(w.k / xq::kGroup);
-  const auto fn = xq_dense_kernel<BITS, MODE, T, KS, XREG>;
+  const int lb = tiles_lds(w.k / xq::kGroup, T, KS, SRC);
+  const auto fn = xq_dense_kernel<BITS, MODE, T, KS, SPW, SRC>;
   MX_TRY_RC(raise_lds(fn, lb));
-  hipLaunchKernelGGL(fn, dim3(groups), dim3(64 * T * KS), lb, s, w, x, xs, m, e);
+  hipLaunchKernelGGL(fn, dim3(groups), dim3(64 * T * KS), lb, s, w, x, xs, m, plane, e);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 
-// Slices are fixed by K; tiles per workgroup fill up to 16 waves (kHcUpMix
-// always takes the four streams as four tiles).
+// Slices of two groups: S = 1..4 slices run in one wave (four tiles per
+// workgroup); deeper rows split their slices over KS waves of one tile (16
+// waves at K = 2048 for up to 2048 rows, so short matrices still fill the
+// chip) or of four tiles (long matrices).  Operands come from the caller's
+// plane when there is one (read in place by one-tile shapes, copied to LDS
+// by four-tile ones), else from an LDS staging (up to 64 groups) or from
+// registers.
 template <int BITS, int MODE>
-int xq_shape(const QWeight& w, const uint16_t* x, int64_t xs, int m, const ProjEpilogue& e,
-             hipStream_t s) {
-  const int KS = xq::slices(w.k);
-  const bool xreg = w.k / xq::kGroup > kXqStageGroups;
-#define MX_XQ(T_, KS_, X_)                                                   \
-  if (KS == KS_ && xreg == X_) return launch_xq<BITS, MODE, T_, KS_, X_>(w, x, xs, m, e, s);
-  if constexpr (MODE == kHcUpMix) {
-    MX_XQ(4, 1, false) MX_XQ(4, 2, false) MX_XQ(4, 4, false)
-  } else {
-    MX_XQ(4, 1, false) MX_XQ(4, 2, false) MX_XQ(4, 3, false) MX_XQ(4, 4, false)
-    MX_XQ(2, 5, false) MX_XQ(2, 6, false) MX_XQ(2, 7, false) MX_XQ(2, 8, false)
-    MX_XQ(1, 16, true) MX_XQ(1, 12, true) MX_XQ(1, 10, true) MX_XQ(1, 9, true)
+int xq_shape(const QWeight& w, const uint16_t* x, int64_t xs, int m, const char* plane,
+             const ProjEpilogue& e, hipStream_t s) {
+  const int G = w.k / xq::kGroup, S = (G + 1) / 2;
+#define MX_XQ(T_, KS_, SPW_, SRC_) \
+  return launch_xq<BITS, MODE, T_, KS_, SPW_, SRC_>(w, x, xs, m, plane, e, s)
+  if (S <= 4) {
+    if (S == 1) MX_XQ(4, 1, 1, kSrcStage);
+    if (S == 2) MX_XQ(4, 1, 2, kSrcStage);
+    MX_XQ(4, 1, 4, kSrcStage);
+  }
+  if constexpr (MODE != kHcUpMix) {
+    if (S == 8) {
+      if (plane) MX_XQ(4, 2, 4, kSrcPlaneLds);
+      MX_XQ(4, 2, 4, kSrcStage);
+    }
+    if (S == 16) {
+      if (w.n > 2048) {
+        if (plane) MX_XQ(4, 4, 4, kSrcPlaneLds);
+        MX_XQ(4, 4, 4, kSrcStage);
+      }
+      if (plane) MX_XQ(1, 16, 1, kSrcPlane);
+      MX_XQ(1, 16, 1, kSrcStage);
+    }
+    if (S == 32) {
+      if (plane) MX_XQ(1, 16, 2, kSrcPlane);
+      MX_XQ(1, 8, 4, kSrcStage);
+    }
+    if (S == 64) {
+      if (plane) MX_XQ(1, 16, 4, kSrcPlane);
+      MX_XQ(1, 16, 4, kSrcReg);
+    }
   }
 #undef MX_XQ
   return MX_EUNSUPPORTED;
 }
 
 template <int BITS>
-int xq_mode(const QWeight& w, const uint16_t* x, int64_t xs, int m, const ProjEpilogue& e,
-            hipStream_t s) {
+int xq_mode(const QWeight& w, const uint16_t* x, int64_t xs, int m, const char* plane,
+            const ProjEpilogue& e, hipStream_t s) {
   switch (e.mode) {
-    case kPlain: return xq_shape<BITS, kPlain>(w, x, xs, m, e, s);
-    case kHcDown: return xq_shape<BITS, kHcDown>(w, x, xs, m, e, s);
-    case kHcUpMix: return xq_shape<BITS, kHcUpMix>(w, x, xs, m, e, s);
-    case kConv: return xq_shape<BITS, kConv>(w, x, xs, m, e, s);
-    default: return xq_shape<BITS, kHcWrite>(w, x, xs, m, e, s);
+    case kPlain: return xq_shape<BITS, kPlain>(w, x, xs, m, plane, e, s);
+    case kHcDown: return xq_shape<BITS, kHcDown>(w, x, xs, m, plane, e, s);
+    case kHcUpMix: return xq_shape<BITS, kHcUpMix>(w, x, xs, m, plane, e, s);
+    case kConv:
+      if constexpr (BITS == 4) return xq_shape<BITS, kConv>(w, x, xs, m, plane, e, s);
+      return MX_EUNSUPPORTED;
+    default: return xq_shape<BITS, kHcWrite>(w, x, xs, m, plane, e, s);
   }
 }
 
-template <int BITS, int KS>
-int launch_gate_up(const uint16_t* x, const MoePlan* plan, int routes, int top_k,
-                   const QBank& gate, const QBank& up, const QWeight& sgate, const QWeight& sup,
-                   uint16_t* h, int hs, hipStream_t s) {
-  const auto fn = xq_gate_up_kernel<BITS, KS>;
+// Slices per wave of a whole-depth shape: S rounded up to a power of two.
+int whole_spw(int k) {
+  const int S = (k / xq::kGroup + 1) / 2;
+  int spw = 1;
+  while (spw < S) spw *= 2;
+  return spw;
+}
+
+template <int BITS, int SPW>
+int launch_gate_up(const uint16_t* x, const char* plane, const MoePlan* plan, int routes,
+                   int top_k, const QBank& gate, const QBank& up, const QWeight& sgate,
+                   const QWeight& sup, uint16_t* h, int hs, hipStream_t s) {
+  const dim3 grid((hs + 127) / 128, routes);
   const int lb = xq::stage_bytes(gate.k / xq::kGroup);
+  const auto fn = plane ? xq_gate_up_kernel<BITS, SPW, kSrcPlaneLds>
+                        : xq_gate_up_kernel<BITS, SPW, kSrcStage>;
   MX_TRY_RC(raise_lds(fn, lb));
-  hipLaunchKernelGGL(fn, dim3((hs + 31) / 32, routes), dim3(64 * 4 * KS), lb, s, x, plan, top_k,
-                     gate, up, sgate, sup, h, hs);
+  hipLaunchKernelGGL(fn, grid, dim3(512), lb, s, x, plane, plan, top_k, gate, up, sgate, sup, h,
+                     hs);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 
-template <int BITS, int KS>
+template <int BITS, int SPW>
 int launch_down(const uint16_t* h, const MoePlan* plan, int routes, const uint16_t* scores,
                 int top_k, const QBank& down, const QWeight& sdown, uint16_t* p, int hs,
                 hipStream_t s) {
-  const auto fn = xq_down_kernel<BITS, KS>;
+  const auto fn = xq_down_kernel<BITS, SPW>;
   const int kmax = down.k > sdown.k ? down.k : sdown.k;
-  const int lb = xq::stage_bytes(kmax / xq::kGroup);
+  const int lb = tiles_lds(kmax / xq::kGroup, 4, 1, kSrcStage);
   MX_TRY_RC(raise_lds(fn, lb));
-  hipLaunchKernelGGL(fn, dim3((down.n + 63) / 64, routes), dim3(64 * 4 * KS), lb, s, h, plan,
-                     scores, top_k, down, sdown, p, hs);
+  hipLaunchKernelGGL(fn, dim3((down.n + 63) / 64, routes), dim3(256), lb, s, h, plan, scores,
+                     top_k, down, sdown, p, hs);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 
-template <int BITS, int KS>
-int launch_head(const QWeight& w, const uint16_t* x, int m, float* maxima, uint32_t* indices,
-                uint16_t* logits, int parts, hipStream_t s) {
-  const auto fn = xq_head_kernel<BITS, KS>;
-  const int lb = xq::stage_bytes(w.k / xq::kGroup);
-  MX_TRY_RC(raise_lds(fn, lb));
-  hipLaunchKernelGGL(fn, dim3(parts), dim3(64 * 4 * KS), lb, s, w, x, m, maxima, indices, logits);
+template <int BITS, int SPW>
+int launch_head(const QWeight& w, const uint16_t* x, const char* plane, int m, float* maxima,
+                uint32_t* indices, uint16_t* logits, int parts, hipStream_t s) {
+  const int G = w.k / xq::kGroup;
+  if (plane) {
+    const auto fn = xq_head_kernel<BITS, SPW, kSrcPlaneLds>;
+    const int lb = tiles_lds(G, 16, 1, kSrcPlaneLds);
+    MX_TRY_RC(raise_lds(fn, lb));
+    hipLaunchKernelGGL(fn, dim3(parts), dim3(1024), lb, s, w, x, plane, m, maxima, indices, logits);
+  } else {
+    const auto fn = xq_head_kernel<BITS, SPW, kSrcStage>;
+    const int lb = tiles_lds(G, 16, 1, kSrcStage);
+    MX_TRY_RC(raise_lds(fn, lb));
+    hipLaunchKernelGGL(fn, dim3(parts), dim3(1024), lb, s, w, x, plane, m, maxima, indices, logits);
+  }
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 
-// Expert matrices take K in {64 .. 512} (one slice), 1024 or 2048.
-bool xq_bank_ok(int k) { return (k % 64 == 0 && k <= 512) || k == 1024 || k == 2048; }
+// Expert and head matrices: K a multiple of 64 up to 2048 (one whole-depth
+// wave per tile, operands staged or copied into LDS).
+bool xq_whole_ok(int k) { return k % 64 == 0 && k >= 64 && k <= 2048; }
+
+#define MX_SPW_DISPATCH(B_, FN, ...)                          \
+  switch (spw) {                                              \
+    case 1: return FN<B_, 1>(__VA_ARGS__);                    \
+    case 2: return FN<B_, 2>(__VA_ARGS__);                    \
+    case 4: return FN<B_, 4>(__VA_ARGS__);                    \
+    case 8: return FN<B_, 8>(__VA_ARGS__);                    \
+    default: return FN<B_, 16>(__VA_ARGS__);                  \
+  }
 
 }  // namespace
 
-int xq_gate_up(const uint16_t* x, const MoePlan* plan, int rows, int top_k, const QBank& gate,
-               const QBank& up, const QWeight& sgate, const QWeight& sup, uint16_t* h,
-               hipStream_t s) {
+int xq_gate_up(const uint16_t* x, const char* plane, const MoePlan* plan, int rows, int top_k,
+               const QBank& gate, const QBank& up, const QWeight& sgate, const QWeight& sup,
+               uint16_t* h, hipStream_t s) {
   if (gate.group_size != 64 || up.group_size != 64 || sgate.group_size != 64 ||
-      sup.group_size != 64 || !xq_bank_ok(gate.k) || sgate.k != gate.k || up.k != gate.k ||
+      sup.group_size != 64 || !xq_whole_ok(gate.k) || sgate.k != gate.k || up.k != gate.k ||
       gate.bits != up.bits || sgate.bits != gate.bits || sup.bits != gate.bits)
     return MX_EUNSUPPORTED;
   const int routes = rows * top_k + 1;
   const int hs = gate.n > sgate.n ? gate.n : sgate.n;
-  const int ks = xq::slices(gate.k);
-#define MX_GU(B, K_) \
-  if (gate.bits == B && ks == K_) return launch_gate_up<B, K_>(x, plan, routes, top_k, gate, up, sgate, sup, h, hs, s);
-  MX_GU(4, 1) MX_GU(4, 2) MX_GU(4, 4) MX_GU(5, 1) MX_GU(5, 2) MX_GU(5, 4)
-  MX_GU(6, 1) MX_GU(6, 2) MX_GU(6, 4) MX_GU(8, 1) MX_GU(8, 2) MX_GU(8, 4)
-#undef MX_GU
-  return MX_EUNSUPPORTED;
+  const int spw = whole_spw(gate.k);
+  switch (gate.bits) {
+    case 4: MX_SPW_DISPATCH(4, launch_gate_up, x, plane, plan, routes, top_k, gate, up, sgate, sup, h, hs, s)
+    case 5: MX_SPW_DISPATCH(5, launch_gate_up, x, plane, plan, routes, top_k, gate, up, sgate, sup, h, hs, s)
+    case 6: MX_SPW_DISPATCH(6, launch_gate_up, x, plane, plan, routes, top_k, gate, up, sgate, sup, h, hs, s)
+    default: MX_SPW_DISPATCH(8, launch_gate_up, x, plane, plan, routes, top_k, gate, up, sgate, sup, h, hs, s)
+  }
 }
 
 int xq_down(const uint16_t* h, const MoePlan* plan, const uint16_t* scores, int rows, int top_k,
             int inter, int shared_inter, const QBank& down, const QWeight& sdown, uint16_t* p,
             hipStream_t s) {
-  if (down.group_size != 64 || sdown.group_size != 64 || !xq_bank_ok(down.k) ||
-      !xq_bank_ok(sdown.k) || xq::slices(down.k) != xq::slices(sdown.k) ||
-      sdown.bits != down.bits || sdown.n != down.n)
+  if (down.group_size != 64 || sdown.group_size != 64 || !xq_whole_ok(down.k) ||
+      !xq_whole_ok(sdown.k) || sdown.bits != down.bits || sdown.n != down.n)
     return MX_EUNSUPPORTED;
   const int routes = rows * top_k + 1;
   const int hs = inter > shared_inter ? inter : shared_inter;
-  const int ks = xq::slices(down.k);
-#define MX_DN(B, K_) \
-  if (down.bits == B && ks == K_) return launch_down<B, K_>(h, plan, routes, scores, top_k, down, sdown, p, hs, s);
-  MX_DN(4, 1) MX_DN(4, 2) MX_DN(4, 4) MX_DN(5, 1) MX_DN(5, 2) MX_DN(5, 4)
-  MX_DN(6, 1) MX_DN(6, 2) MX_DN(6, 4) MX_DN(8, 1) MX_DN(8, 2) MX_DN(8, 4)
-#undef MX_DN
+  const int spw = whole_spw(down.k > sdown.k ? down.k : sdown.k);
+  switch (down.bits) {
+    case 4: MX_SPW_DISPATCH(4, launch_down, h, plan, routes, scores, top_k, down, sdown, p, hs, s)
+    case 5: MX_SPW_DISPATCH(5, launch_down, h, plan, routes, scores, top_k, down, sdown, p, hs, s)
+    case 6: MX_SPW_DISPATCH(6, launch_down, h, plan, routes, scores, top_k, down, sdown, p, hs, s)
+    default: MX_SPW_DISPATCH(8, launch_down, h, plan, routes, scores, top_k, down, sdown, p, hs, s)
+  }
+}
+
+int xq_upmix(const QWeight& up, const uint16_t* lo, int m, const uint16_t* xn, int hidden,
+             uint16_t* mixed, char* mixed_plane, hipStream_t s) {
+  if (up.group_size != 64 || up.k % 64 != 0 || up.k > 512 || up.n != 4 * hidden ||
+      hidden % 64 != 0 || m < 1 || m > 8)
+    return MX_EUNSUPPORTED;
+  const int G = up.k / xq::kGroup;
+  const int lb = tiles_lds(G, 16, 1, kSrcStage);
+  const dim3 grid(hidden / 64);
+  const int spw = whole_spw(up.k);
+#define MX_UM(B, SPW)                                                                           \
+  if (up.bits == B && spw == SPW) {                                                             \
+    hipLaunchKernelGGL((xq_upmix_kernel<B, SPW>), grid, dim3(1024), lb, s, up, lo, m, xn, hidden, \
+                       mixed, mixed_plane);                                                     \
+    return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;                                   \
+  }
+  MX_UM(4, 1) MX_UM(4, 2) MX_UM(4, 4) MX_UM(5, 1) MX_UM(5, 2) MX_UM(5, 4)
+  MX_UM(6, 1) MX_UM(6, 2) MX_UM(6, 4) MX_UM(8, 1) MX_UM(8, 2) MX_UM(8, 4)
+#undef MX_UM
   return MX_EUNSUPPORTED;
 }
 
-int xq_head_parts(int n) { return (n + 63) / 64; }
+size_t xq_plane_bytes(int k) { return size_t(xq::stage_bytes(k / xq::kGroup)); }
 
-int xq_head(const QWeight& w, const uint16_t* x, int m, float* maxima, uint32_t* indices,
-            uint16_t* logits, int* parts_out, hipStream_t s) {
-  if (w.group_size != 64 || !xq_bank_ok(w.k) || m < 1 || m > 8) return MX_EUNSUPPORTED;
+int xq_head_parts(int n) { return (n + 255) / 256; }
+
+int xq_head(const QWeight& w, const uint16_t* x, const char* plane, int m, float* maxima,
+            uint32_t* indices, uint16_t* logits, int* parts_out, hipStream_t s) {
+  if (w.group_size != 64 || !xq_whole_ok(w.k) || m < 1 || m > 8) return MX_EUNSUPPORTED;
   const int parts = xq_head_parts(w.n);
   *parts_out = parts;
-  const int ks = xq::slices(w.k);
-#define MX_HD(B, K_) \
-  if (w.bits == B && ks == K_) return launch_head<B, K_>(w, x, m, maxima, indices, logits, parts, s);
-  MX_HD(4, 1) MX_HD(4, 2) MX_HD(4, 4) MX_HD(5, 1) MX_HD(5, 2) MX_HD(5, 4)
-  MX_HD(6, 1) MX_HD(6, 2) MX_HD(6, 4) MX_HD(8, 1) MX_HD(8, 2) MX_HD(8, 4)
-#undef MX_HD
-  return MX_EUNSUPPORTED;
+  const int spw = whole_spw(w.k);
+  switch (w.bits) {
+    case 4: MX_SPW_DISPATCH(4, launch_head, w, x, plane, m, maxima, indices, logits, parts, s)
+    case 5: MX_SPW_DISPATCH(5, launch_head, w, x, plane, m, maxima, indices, logits, parts, s)
+    case 6: MX_SPW_DISPATCH(6, launch_head, w, x, plane, m, maxima, indices, logits, parts, s)
+    default: MX_SPW_DISPATCH(8, launch_head, w, x, plane, m, maxima, indices, logits, parts, s)
+  }
 }
 
-// Group size 64; K a multiple of 64 up to 512, or a multiple of 512 up to
-// 8192 (slices of eight groups); 16-byte aligned activation rows.
+// Group size 64; K a multiple of 64 with at most four slices (K <= 512), or
+// K = 1024, 2048, 4096 or 8192.
 bool xq_supported(const QWeight& w) {
-  const int ks = xq::slices(w.k);
-  const bool shape = (w.k % 64 == 0 && w.k <= 512) ||
-                     (w.k % 512 == 0 && (ks <= 10 || ks == 12 || ks == 16));
+  const bool shape = w.k % 64 == 0 && w.k >= 64 &&
+                     (w.k <= 512 || w.k == 1024 || w.k == 2048 || w.k == 4096 || w.k == 8192);
   return w.group_size == 64 && shape && (w.bits == 4 || w.bits == 5 || w.bits == 6 || w.bits == 8);
 }
 
 int xq_dense(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const ProjEpilogue& e,
-             hipStream_t s) {
+             hipStream_t s, const char* plane) {
   if (!xq_supported(w) || m < 1 || m > 8) return MX_EUNSUPPORTED;
   if (e.mode == kHcUpMix && e.hidden * 4 != w.n) return MX_EUNSUPPORTED;
   if (e.mode == kConv && (e.taps < 2 || e.taps > kConvMaxTaps)) return MX_EUNSUPPORTED;
   switch (w.bits) {
-    case 4: return xq_mode<4>(w, x, x_stride, m, e, s);
-    case 5: return xq_mode<5>(w, x, x_stride, m, e, s);
-    case 6: return xq_mode<6>(w, x, x_stride, m, e, s);
-    default: return xq_mode<8>(w, x, x_stride, m, e, s);
+    case 4: return xq_mode<4>(w, x, x_stride, m, plane, e, s);
+    case 5: return xq_mode<5>(w, x, x_stride, m, plane, e, s);
+    case 6: return xq_mode<6>(w, x, x_stride, m, plane, e, s);
+    default: return xq_mode<8>(w, x, x_stride, m, plane, e, s);
   }
 }
 

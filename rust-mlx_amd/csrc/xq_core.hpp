@@ -6,8 +6,8 @@
 //   field of the group (at least 1) and X_k = trunc(x_k 2^(156 - Eb)), an
 //   integer below 2^30 in magnitude; P = sum X_k q_k and Q = sum X_k are
 //   exact; v_g = fma(P, s_g, Q b_g) 2^(Eb - 156) in fp64; the groups of each
-//   of S = k >= 1024 ? k / 512 : 1 contiguous slices are added in order from
-//   +0 in fp64, the slice sums likewise, and the total is rounded to fp32.
+//   slice of two consecutive groups are added in order from +0 in fp64, the
+//   slice sums likewise, and the total is rounded to fp32.
 //
 // P comes from the matrix core exactly: X_k = sum_d D_d 256^d with signed
 // digits D_d in [-128, 127] (the bytes of (X + 0x808080) ^ 0x808080), and
@@ -21,8 +21,10 @@
 // activation row r of a four-row block (rows 0-3 or 4-7), so lane l ends with
 // the four digit sums of activation row l / 16 (+ 4 for the second block)
 // against weight row l % 16 of the tile, and combines them in registers.
-// Within each lane's 16 k-slots both operands use the k order perm<BITS>():
-// 4-bit codes split into low and high nibbles with two masks per word.
+// Within each lane's 16 k-slots both operands use one k order, perm(): the
+// order in which 4-bit codes split into low and high nibbles with two masks
+// per word (other widths are permuted into it), so an activation plane built
+// once serves every consumer whatever its code width.
 #pragma once
 
 #include "common.hpp"
@@ -36,18 +38,25 @@ typedef uint32_t u32x3_a4 __attribute__((ext_vector_type(3), aligned(4)));
 constexpr int kGroup = 64;
 constexpr int kBlockBytes = 1024;            // A operands of one (group, 4-row block)
 constexpr int kGroupBytes = 2 * kBlockBytes; // both blocks of a group
-constexpr int kGroupsPerSlice = 8;           // slices of deep rows (k >= 1024)
 
-__host__ __device__ constexpr int slices(int k) { return k >= 1024 ? k / 512 : 1; }
+// Slices of the arithmetic: two consecutive groups each (the last of an odd
+// count holds one).
+__host__ __device__ constexpr int slices(int k) { return (k / kGroup + 1) / 2; }
 
 __device__ __forceinline__ v4i mfma(const v4i& a, const v4i& b, const v4i& c) {
   return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
-// Value of the lane's 16 held in operand byte e.
-template <int BITS>
-__host__ __device__ constexpr int perm(int e) {
-  return BITS == 4 ? (e / 8) * 8 + (e % 4) * 2 + (e / 4) % 2 : e;
+// Value of the lane's 16 held in operand byte e: bytes 0-3 hold values
+// 0, 2, 4, 6; 4-7 values 1, 3, 5, 7; 8-11 values 8 .. 14; 12-15 values 9 .. 15.
+__host__ __device__ constexpr int perm(int e) { return (e / 8) * 8 + (e % 4) * 2 + (e / 4) % 2; }
+
+// Words of values (0..3, 4..7) -> (0, 2, 4, 6) and (1, 3, 5, 7).
+__device__ __forceinline__ int even_of(uint32_t lo, uint32_t hi) {
+  return int(__builtin_amdgcn_perm(hi, lo, 0x06040200u));
+}
+__device__ __forceinline__ int odd_of(uint32_t lo, uint32_t hi) {
+  return int(__builtin_amdgcn_perm(hi, lo, 0x07050301u));
 }
 
 // The lane's code words of one group: 16 codes of value 64 g + 16 kb on.
@@ -102,8 +111,8 @@ __device__ __forceinline__ uint32_t spread4(uint32_t v) {
          ((v << (3 * d)) & (m << 24));
 }
 
-// B operand: the lane's 16 codes as int8 in perm<BITS>() order (8-bit codes
-// as q - 128, the offset restored through Q in the epilogue).
+// B operand: the lane's 16 codes as int8 in perm() order (8-bit codes as
+// q - 128, the offset restored through Q in the epilogue).
 template <int BITS>
 __device__ __forceinline__ v4i b_operand(const Codes<BITS>& c) {
   v4i r;
@@ -112,16 +121,21 @@ __device__ __forceinline__ v4i b_operand(const Codes<BITS>& c) {
     r.y = int((c.w[0] >> 4) & 0x0F0F0F0Fu);
     r.z = int(c.w[1] & 0x0F0F0F0Fu);
     r.w = int((c.w[1] >> 4) & 0x0F0F0F0Fu);
-  } else if constexpr (BITS == 8) {
-    r.x = int(c.w[0] ^ 0x80808080u);
-    r.y = int(c.w[1] ^ 0x80808080u);
-    r.z = int(c.w[2] ^ 0x80808080u);
-    r.w = int(c.w[3] ^ 0x80808080u);
   } else {
-    r.x = int(spread4<BITS>(bits_at<BITS, 0>(c)));
-    r.y = int(spread4<BITS>(bits_at<BITS, 4 * BITS>(c)));
-    r.z = int(spread4<BITS>(bits_at<BITS, 8 * BITS>(c)));
-    r.w = int(spread4<BITS>(bits_at<BITS, 12 * BITS>(c)));
+    uint32_t q[4];
+    if constexpr (BITS == 8) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) q[i] = c.w[i] ^ 0x80808080u;
+    } else {
+      q[0] = spread4<BITS>(bits_at<BITS, 0>(c));
+      q[1] = spread4<BITS>(bits_at<BITS, 4 * BITS>(c));
+      q[2] = spread4<BITS>(bits_at<BITS, 8 * BITS>(c));
+      q[3] = spread4<BITS>(bits_at<BITS, 12 * BITS>(c));
+    }
+    r.x = even_of(q[0], q[1]);
+    r.y = odd_of(q[0], q[1]);
+    r.z = even_of(q[2], q[3]);
+    r.w = odd_of(q[2], q[3]);
   }
   return r;
 }
@@ -150,101 +164,115 @@ __device__ __forceinline__ void transpose4(const uint32_t (&z)[4], uint32_t (&o)
   o[3] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
 }
 
-// LDS layout of a staging of `ng` groups: A operands [g][block][lane] x 16 B,
-// then Q fp64 [g][8], then Eb int [g][8].
+// Layout of the activation operands of `ng` groups, in LDS (a staging) or in
+// global memory (a plane written by the producer of the activations):
+// A operands [g][block][lane] x 16 B, then Q fp64 [g][8], then Eb int [g][8].
 __host__ __device__ constexpr int stage_bytes(int ng) { return ng * (kGroupBytes + 8 * 8 + 8 * 4); }
+__host__ __device__ constexpr int plane_q_offset(int ng) { return ng * kGroupBytes; }
+__host__ __device__ constexpr int plane_e_offset(int ng) { return ng * (kGroupBytes + 64); }
 
-// Stages groups [g0, g0 + ng) of activation rows xr(0..M-1) (rows past M as
-// zeros): the A operands of both four-row blocks in perm<BITS>() order, Q and
-// Eb.  All NT threads of the workgroup call it; ends with a barrier.  Each
-// wave takes two groups at a time: lane l handles row l % 8 of group
-// 2 i + (l % 16) / 8, values 16 (l / 16) .. +15, so the four lanes of one
-// (group, row) are 16 apart and share Eb and Q through two butterfly steps.
-template <int BITS, int NT, class Rows>
+// One 16-value unit of activation row m (< 8), values 16 kb .. +15 of group
+// g: f holds them widened to fp32.  The four lanes holding one (group, row)
+// must be 16 apart in the wave (kb = lane / 16): they share Eb and Q through
+// two butterfly steps.  Writes the unit's four digit operands, and (kb == 0)
+// Q and Eb, into the layout of `ng` groups at dst; `write` false still joins
+// the butterflies.
+__device__ __forceinline__ void digitize_unit(const float (&f)[16], int m, int g, int kb,
+                                              bool write, char* dst, int ng) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(f[i]));
+  int eb = max(int((f2u(amax) >> 23) & 0xffu), 1);
+  eb = max(eb, __shfl_xor(eb, 16, 64));
+  eb = max(eb, __shfl_xor(eb, 32, 64));
+  int X[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) X[i] = grid_int(f[i], eb);
+  double q = 0.0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) q += double(X[2 * i] + X[2 * i + 1]);  // pairs < 2^31
+  q += __shfl_xor(q, 16, 64);
+  q += __shfl_xor(q, 32, 64);
+  if (!write) return;
+  // operand word p of digit d: byte i = digit d of value perm(4 p + i)
+  uint32_t op[4][4];
+#pragma unroll
+  for (int pw = 0; pw < 4; ++pw) {
+    const uint32_t z[4] = {digits(X[perm(4 * pw + 0)]), digits(X[perm(4 * pw + 1)]),
+                           digits(X[perm(4 * pw + 2)]), digits(X[perm(4 * pw + 3)])};
+    uint32_t t[4];
+    transpose4(z, t);
+#pragma unroll
+    for (int d = 0; d < 4; ++d) op[d][pw] = t[d];
+  }
+  char* base = dst + g * kGroupBytes + (m >> 2) * kBlockBytes;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const int slot = 4 * (m & 3) + d + 16 * kb;
+    *reinterpret_cast<uint4*>(base + slot * 16) = make_uint4(op[d][0], op[d][1], op[d][2], op[d][3]);
+  }
+  if (kb == 0) {
+    reinterpret_cast<double*>(dst + plane_q_offset(ng))[g * 8 + m] = q;
+    reinterpret_cast<int*>(dst + plane_e_offset(ng))[g * 8 + m] = eb;
+  }
+}
+
+// Widens 16 bf16 values (two 16-byte loads) to fp32.
+__device__ __forceinline__ void load16(const uint16_t* src, float (&f)[16]) {
+  const uint4 a = reinterpret_cast<const uint4*>(src)[0], b = reinterpret_cast<const uint4*>(src)[1];
+  const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    f[2 * i] = u2f(w[i] << 16);
+    f[2 * i + 1] = u2f(w[i] & 0xffff0000u);
+  }
+}
+
+// Stages groups [g0, g0 + ng) of activation rows xr(0..M-1) into LDS.  Rows
+// past M are left unwritten: their matrix-core sums land in D rows that no
+// epilogue reads.  All NT threads of the workgroup call it; ends with a
+// barrier.  Each wave takes 16 / R groups at a time (R = 8 rows rounded up to
+// a power of two >= M): lane l handles row (l % 16) % R of group
+// i + (l % 16) / R, values 16 (l / 16) .. +15.
+template <int NT, class Rows>
 __device__ __forceinline__ void stage(char* lds, const Rows& xr, int M, int g0, int ng) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   constexpr int NW = NT / 64;
-  const int m = lane & 7, kb = lane >> 4, half = (lane >> 3) & 1;
-  double* qs = reinterpret_cast<double*>(lds + ng * kGroupBytes);
-  int* es = reinterpret_cast<int*>(lds + ng * (kGroupBytes + 64));
-  for (int p = wave; 2 * p < ng; p += NW) {
-    const int g = 2 * p + half;
+  const int R = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
+  const int per = 16 / R;  // groups per wave step
+  const int m = (lane & 15) % R, kb = lane >> 4, sub = (lane & 15) / R;
+  for (int p = wave; p * per < ng; p += NW) {
+    const int g = p * per + sub;
     const bool live = g < ng && m < M;
     float f[16];
     if (live) {
-      const uint4* src = reinterpret_cast<const uint4*>(xr(m) + size_t(g0 + g) * kGroup + 16 * kb);
-      const uint4 a = src[0], b = src[1];
-      const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        f[2 * i] = u2f(w[i] << 16);
-        f[2 * i + 1] = u2f(w[i] & 0xffff0000u);
-      }
+      load16(xr(m) + size_t(g0 + g) * kGroup + 16 * kb, f);
     } else {
 #pragma unroll
       for (int i = 0; i < 16; ++i) f[i] = 0.0f;
     }
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(f[i]));
-    int eb = max(int((f2u(amax) >> 23) & 0xffu), 1);
-    eb = max(eb, __shfl_xor(eb, 16, 64));
-    eb = max(eb, __shfl_xor(eb, 32, 64));
-    int X[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) X[i] = grid_int(f[i], eb);
-    double q = 0.0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) q += double(X[2 * i] + X[2 * i + 1]);  // pairs < 2^31
-    q += __shfl_xor(q, 16, 64);
-    q += __shfl_xor(q, 32, 64);
-    // operand word p of digit d: bytes i = digit d of value perm(4 p + i)
-    uint32_t op[4][4];
-#pragma unroll
-    for (int pw = 0; pw < 4; ++pw) {
-      const uint32_t z[4] = {digits(X[perm<BITS>(4 * pw + 0)]), digits(X[perm<BITS>(4 * pw + 1)]),
-                             digits(X[perm<BITS>(4 * pw + 2)]), digits(X[perm<BITS>(4 * pw + 3)])};
-      uint32_t t[4];
-      transpose4(z, t);
-#pragma unroll
-      for (int d = 0; d < 4; ++d) op[d][pw] = t[d];
-    }
-    if (g < ng) {
-      char* base = lds + g * kGroupBytes + (m >> 2) * kBlockBytes;
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const int slot = 4 * (m & 3) + d + 16 * kb;
-        *reinterpret_cast<uint4*>(base + slot * 16) = make_uint4(op[d][0], op[d][1], op[d][2], op[d][3]);
-      }
-      if (kb == 0) {
-        qs[g * 8 + m] = q;
-        es[g * 8 + m] = eb;
-      }
-    }
+    digitize_unit(f, m, g, kb, live, lds, ng);
   }
   __syncthreads();
 }
 
 // One group of a tile row into the two fp64 row accumulators of this lane
-// (activation rows l / 16 and 4 + l / 16 against tile row l % 16): a, Q and
-// Eb from the staging (or from registers), s and b the row's scale and bias.
+// (activation rows l / 16 and 4 + l / 16 against tile row l % 16) for the
+// four-row blocks in `blocks` (bit 0: rows 0-3, bit 1: rows 4-7): a, Q and Eb
+// of each block's row, s and b the tile row's scale and bias.
 template <int BITS>
-__device__ __forceinline__ void group_step(const v4i& a0, const v4i& a1, bool two, const v4i& bop,
-                                           double q0, double q1, int e0, int e1, double s,
-                                           double b, double (&acc)[2]) {
+__device__ __forceinline__ void group_step(const v4i& a0, const v4i& a1, int blocks,
+                                           const v4i& bop, double q0, double q1, int e0, int e1,
+                                           double s, double b, double (&acc)[2]) {
   const v4i zero = {0, 0, 0, 0};
-  const v4i d0 = mfma(a0, bop, zero);
   auto fold = [&](const v4i& d, double q, int e) {
     double p = fma(fma(fma(double(d.w), 256.0, double(d.z)), 256.0, double(d.y)), 256.0,
                    double(d.x));
     if constexpr (BITS == 8) p = p + 128.0 * q;  // codes entered as q - 128
     return __builtin_amdgcn_ldexp(fma(p, s, q * b), e - 156);
   };
-  acc[0] = acc[0] + fold(d0, q0, e0);
-  if (two) {
-    const v4i d1 = mfma(a1, bop, zero);
-    acc[1] = acc[1] + fold(d1, q1, e1);
-  }
+  if (blocks & 1) acc[0] = acc[0] + fold(mfma(a0, bop, zero), q0, e0);
+  if (blocks & 2) acc[1] = acc[1] + fold(mfma(a1, bop, zero), q1, e1);
 }
 
 }  // namespace xq

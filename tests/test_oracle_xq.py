@@ -109,7 +109,7 @@ def test_xq_grid_integers_fit_four_int8_digits(orc):
 
 
 def test_xq_planted_mistakes_fail(orc):
-    """A dropped bias term misses the closed form; merging the two slices of a
+    """A dropped bias term misses the closed form; merging the slices of a
     K = 1024 row into one sequential double sum, and anchoring the grid at the
     row's largest exponent, give other bits on inputs built to show them."""
     n, k, bits = 4, 1024, 4
@@ -119,7 +119,8 @@ def test_xq_planted_mistakes_fail(orc):
     w = _dense_w(orc, codes, s, b, k, bits)
     no_bias = _bf(x) @ (w - np.repeat(_bf(b), 64, axis=1)).T
     assert np.max(np.abs(y - no_bias)) > 1e-2
-    # slices: group 0 = +2^60, group 8 (slice 1) = -2^60, group 9 = +1
+    # slices of two groups: group 0 = +2^60 (slice 0); groups 8 = -2^60 and
+    # 9 = +1 share slice 4
     codes1 = np.zeros((1, k * 8 // 32), np.uint32)
     for g in (0, 8, 9):
         codes1[0, g * 16] = 1  # q at value 64 g = 1 (8-bit codes: 4 per word)
@@ -128,8 +129,9 @@ def test_xq_planted_mistakes_fail(orc):
     xf = np.zeros((1, k), np.float32)
     xf[0, 0], xf[0, 512], xf[0, 576] = 2.0 ** 60, -(2.0 ** 60), 1.0
     y1 = float(orc.xq(codes1, s1, b1, k, 8, orc.f32_to_bf16(xf))[0, 0])
-    assert orc.lib.mxo_xq_slices(k) == 2
-    assert y1 == 0.0  # slice 1 rounds -2^60 + 1 to -2^60; one sequential sum would give 1
+    assert orc.lib.mxo_xq_slices(k) == 8
+    assert orc.lib.mxo_xq_slices(448) == 4 and orc.lib.mxo_xq_slices(64) == 1
+    assert y1 == 0.0  # slice 4 rounds -2^60 + 1 to -2^60; one sequential sum would give 1
     # grid per group, not per row: a group of small values next to a group
     # holding 2^20 keeps all its bits
     xg = np.full((1, 128), 1.0 + 2 ** -7, np.float32)
