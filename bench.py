@@ -34,13 +34,19 @@ Workloads:
 
 Timing: the decode loop is bracketed by device synchronisation (the engine
 synchronises once per step to read the tokens, as the reference's eval does).
+Config 3 times the exact mode by default: the exact-integer kernels, whose
+tokens, routing and every layer output equal the CPU oracle's bit for bit
+(tests/test_config3_gpu.py).  `--fast` times the bf16 matrix-core mode
+instead; the other mode is always timed beside the headline one.
 The roofline object is the MoE expert gate/up kernel (the step's dominant
-kernel): algorithmic bytes (distinct experts' weights + the shared expert)
-over its duration, from HIP events on the engine's stream around the 48
-layers' gate/up launches run back to back on the routing of the last step
-(each launch reads its own layer's weights from HBM).  `traffic` is the
-measured HBM bytes per launch from the committed rocprofv3 counter summary
-profiles/config3-b8-decode_hbm-traffic.md.
+kernel), in the form the step launches: algorithmic bytes (distinct experts'
+weights + the shared expert) over its duration, from HIP events on the
+engine's stream around the 48 layers' gate/up launches run back to back on
+the routing of the last step (each launch reads its own layer's weights from
+HBM).  `traffic` is the measured HBM bytes per launch from the committed
+rocprofv3 counter summary of that kernel
+(profiles/config3-b8-decode-exact_hbm-traffic.md, or
+profiles/config3-b8-decode_hbm-traffic.md for --fast).
 The CPU baseline is the C oracle (oracle/, a restatement of the reference
 arithmetic) timed on this host over a bounded sample of the same step.
 """
@@ -57,7 +63,6 @@ import numpy as np
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
-sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "batch-8 decode tok/s (aggregate) + QMV/MoE achieved HBM GB/s vs 8 TB/s peak"
@@ -65,6 +70,30 @@ METRIC = "batch-8 decode tok/s (aggregate) + QMV/MoE achieved HBM GB/s vs 8 TB/s
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
+
+
+def to_bf16(x) -> np.ndarray:
+    """float32 -> bf16 bits, round to nearest even (synthetic inputs)."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def bf16_to_f32(h) -> np.ndarray:
+    return (np.asarray(h, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def load_package():
+    """Import rust-mlx_amd (a hyphenated directory) as module rust_mlx_amd."""
+    import importlib.util
+
+    if "rust_mlx_amd" in sys.modules:
+        return sys.modules["rust_mlx_amd"]
+    spec = importlib.util.spec_from_file_location(
+        "rust_mlx_amd", os.path.join(ROOT, "rust-mlx_amd", "__init__.py"))
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["rust_mlx_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
 
 
 class ProfilerRegion:
@@ -96,7 +125,8 @@ def bench_config3(mx, args):
     rows = 8
     t0 = time.perf_counter()
     eng = mx.Engine(cfg)
-    eng.set_flags(eager=args.eager, exact=args.exact)
+    exact = not args.fast
+    eng.set_flags(eager=args.eager, exact=exact)
     log(f"config3: engine built in {time.perf_counter() - t0:.1f}s "
         f"({cfg['layers']} layers, {cfg['experts']} experts)")
     rng = np.random.default_rng(3000)
@@ -130,10 +160,11 @@ def bench_config3(mx, args):
     ms_step = dt / args.steps * 1e3
     log(f"config3: {args.steps} steps x {rows} rows in {dt:.3f}s -> {tok_s:.1f} tok/s, "
         f"{ms_step:.3f} ms/step")
-    # the bit-exact path (exact mode: the fixed-order kernels the CPU oracle
-    # reproduces bit for bit) timed the same way on the same rows
+    # the other mode timed the same way on the same rows (exact: the
+    # exact-integer kernels the CPU oracle reproduces bit for bit; fast: the
+    # bf16 matrix-core kernels, within tolerance of it)
     exact_steps = max(args.steps // 4, 4)
-    eng.set_flags(exact=not args.exact, eager=args.eager)
+    eng.set_flags(exact=not exact, eager=args.eager)
     for _ in range(2):
         toks = eng.decode_batch(slots, toks, equal=False)
     mx.check(mx.lib.mx_device_sync())
@@ -143,8 +174,8 @@ def bench_config3(mx, args):
     mx.check(mx.lib.mx_device_sync())
     other_dt = (time.perf_counter() - t0) / exact_steps
     other_tok_s = rows / other_dt
-    eng.set_flags(exact=args.exact, eager=args.eager)
-    log(f"config3: {'fast' if args.exact else 'exact'} mode {exact_steps} steps: "
+    eng.set_flags(exact=exact, eager=args.eager)
+    log(f"config3: {'fast' if exact else 'exact'} mode {exact_steps} steps: "
         f"{other_tok_s:.1f} tok/s, {other_dt * 1e3:.3f} ms/step")
     # a second profiled step after the timed loop (longer contexts), then the
     # expert kernels of all 48 layers back to back on that step's routing
@@ -181,13 +212,18 @@ def bench_config3(mx, args):
             "expert_down_gbs": round(dn_gbs, 1),
             "prefill_s": round(prefill_s, 2),
             "context": "synthetic" if args.synthetic_context else "prefilled",
-            "mode": "exact" if args.exact else "fast",
-            ("fast_tok_s" if args.exact else "exact_tok_s"): round(other_tok_s, 2),
+            "mode": "exact" if exact else "fast",
+            ("fast_tok_s" if exact else "exact_tok_s"): round(other_tok_s, 2),
         },
-        "roofline": {"bound": "hbm", "kernel": "moe gate_up_persist_kernel<4, 16, 4, 2, 0>",
+        "roofline": {"bound": "hbm",
+                     "kernel": ("xq_gate_up_kernel<4, 16, 3> (exact-integer expert gate/up + SwiGLU, "
+                                "the form the step launches)") if exact else
+                               ("gate_up_persist_kernel<4, 16, 4, 2, 0> (route-taking form; the "
+                                "step launches the self-routing <4, 16, 4, 2, 8>)"),
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic("config3-b8-decode_hbm-traffic.md"),
+                     "traffic": measured_traffic("config3-b8-decode-exact_hbm-traffic.md" if exact
+                                                 else "config3-b8-decode_hbm-traffic.md"),
                      "algorithmic_bytes_per_launch": int(gu_launch_bytes),
                      "us_per_launch": round(gu_us, 2)},
         "cpu_baseline": cpu,
@@ -247,15 +283,14 @@ def qweight_bytes(n: int, k: int, bits: int, gs: int) -> int:
 
 
 def bench_qmv_config0(mx, args):
-    from oracle import oracle as orc
-
     n, k, bits, gs, m = 4096, 2048, 4, 64, 1
     wbytes = qweight_bytes(n, k, bits, gs)
     alg_bytes = wbytes + 2 * m * k + 2 * m * n
     copies = max(2, int(np.ceil(2 * 1024**3 / wbytes)))
     log(f"qmv-config0: {copies} weight copies ({copies * wbytes / 1e9:.2f} GB) for MALL rotation")
     ws = [mx.QWeight.random(n, k, bits, gs, seed=100 + 17 * i) for i in range(copies)]
-    x = mx.DeviceArray.from_numpy(orc.fill_bf16(m * k, 101, 1, 1.0, 0.0).reshape(m, k))
+    x = mx.DeviceArray((m, k), np.uint16)
+    mx.fill_bf16(x, 101, 1, 1.0, 0.0)
     y = mx.DeviceArray((m, n), np.uint16)
     stream = C.c_void_p()
     mx.check(mx.lib.mx_stream_create(C.byref(stream)))
@@ -281,15 +316,25 @@ def bench_qmv_config0(mx, args):
     avg_s = ms.value / 1e3 / args.steps
     achieved = alg_bytes / avg_s / 1e9
     log(f"qmv-config0: {avg_s * 1e6:.2f} us/launch (events)")
-    codes, s, b = orc.random_qweight(n, k, bits, gs, seed=100 + 17 * ((args.warmup + args.steps - 1) % copies))
-    want = orc.qmv(codes, s, b, k, bits, gs, x.numpy())
-    if not (y.numpy() == want).all():
-        raise SystemExit("bench: QMV output differs from oracle")
-    reps, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < 10.0:
-        orc.qmv(codes, s, b, k, bits, gs, x.numpy())
-        reps += 1
-    cpu_dt = (time.perf_counter() - t0) / reps
+    cpu = None
+    if not args.no_cpu_baseline:
+        # CPU baseline leg: the oracle checks the last launch bit for bit, then
+        # repeats the same QMV for about 10 s
+        from oracle import oracle as orc
+
+        seed = 100 + 17 * ((args.warmup + args.steps - 1) % copies)
+        codes, s, b = orc.random_qweight(n, k, bits, gs, seed=seed)
+        xh = x.numpy()
+        if not (y.numpy() == orc.qmv(codes, s, b, k, bits, gs, xh)).all():
+            raise SystemExit("bench: QMV output differs from oracle")
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < 10.0:
+            orc.qmv(codes, s, b, k, bits, gs, xh)
+            reps += 1
+        cpu_dt = (time.perf_counter() - t0) / reps
+        cpu = {"value": round(alg_bytes / cpu_dt / 1e9, 3), "unit": "GB/s",
+               "cores": orc.num_threads(), "kind": "port",
+               "sample": f"{reps} oracle QMVs of the config-0 matrix in 10s"}
     return {
         "metric": METRIC, "value": round(achieved, 2), "unit": "GB/s", "ms_per_step": avg_s * 1e3,
         "dtype": "u4 codes x bf16 -> fp32 acc",
@@ -298,9 +343,7 @@ def bench_qmv_config0(mx, args):
         "roofline": {"bound": "hbm", "kernel": "proj/qmv_kernel<4,1>", "achieved": round(achieved, 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": None},
-        "cpu_baseline": {"value": round(alg_bytes / cpu_dt / 1e9, 3), "unit": "GB/s",
-                         "cores": orc.num_threads(), "kind": "port",
-                         "sample": f"{reps} oracle QMVs of the config-0 matrix in 10s"},
+        "cpu_baseline": cpu,
     }
 
 
@@ -318,12 +361,26 @@ def prefill_flops(t: int, hv: int) -> float:
     return per_chunk * ((t + c - 1) // c) * hv
 
 
-def bench_gdn_prefill_config1(mx, args):
-    from oracle import oracle as orc
-    from test_gdn_prefill_gpu import inputs
+def gdn_config1_inputs(rows, hk, hv, seed):
+    """Config-1 style scan inputs: L2-normalised q, k; beta = sigmoid(N(0,1));
+    g = exp(-softplus(N(0,1)) * A) with A ~ U(0, 16) per head."""
+    rng = np.random.default_rng(seed)
 
+    def l2n(x):
+        return x / np.linalg.norm(x, axis=-1, keepdims=True)
+
+    q = to_bf16(l2n(rng.standard_normal((rows, hk, 128))).astype(np.float32))
+    k = to_bf16(l2n(rng.standard_normal((rows, hk, 128))).astype(np.float32))
+    v = to_bf16(rng.standard_normal((rows, hv, 128)).astype(np.float32))
+    beta = to_bf16((1 / (1 + np.exp(-rng.standard_normal((rows, hv))))).astype(np.float32))
+    A = rng.uniform(0, 16, hv)
+    g = np.exp(-np.log1p(np.exp(rng.standard_normal((rows, hv)))) * A).astype(np.float32)
+    return q, k, v, g, beta
+
+
+def bench_gdn_prefill_config1(mx, args):
     hk, hv, t = 16, 32, 2048
-    q, k, v, g, beta = inputs(orc, t, hk, hv, 2048)
+    q, k, v, g, beta = gdn_config1_inputs(t, hk, hv, 2048)
     state0 = np.zeros((1, hv, 128, 128), np.float32)
     slots = np.zeros(1, np.int32)
     dims = mx.GdnDimsC(hk, hv, 128, 128, 4)
@@ -357,16 +414,25 @@ def bench_gdn_prefill_config1(mx, args):
         mx.check(mx.lib.mx_event_elapsed_ms(e0, e1, C.byref(ms)))
         return ms.value / 1e3 / n
 
-    # parity of the measured configuration against the oracle first
     chunked()
     mx.check(mx.lib.mx_stream_sync(stream))
-    t0 = time.perf_counter()
-    y_w, st_w, _ = orc.gdn_scan(q, k, v, g, beta, hk, hv, 1, t, slots, state0)
-    cpu_s = time.perf_counter() - t0
-    err = np.abs(dst.numpy() - st_w).max() / np.abs(st_w).max()
-    log(f"gdn-prefill-config1: state max rel err vs oracle {err:.2e}")
-    if err > 1e-4:
-        raise SystemExit("bench: chunked prefill state differs from the oracle")
+    err = cpu = None
+    if not args.no_cpu_baseline:
+        # CPU baseline leg: one sequential oracle scan of the same input,
+        # timed, and the checker of the first chunked scan's state
+        from oracle import oracle as orc
+
+        t0 = time.perf_counter()
+        y_w, st_w, _ = orc.gdn_scan(q, k, v, g, beta, hk, hv, 1, t, slots, state0)
+        cpu_s = time.perf_counter() - t0
+        err = float(np.abs(dst.numpy() - st_w).max() / np.abs(st_w).max())
+        log(f"gdn-prefill-config1: state max rel err vs oracle {err:.2e}; oracle (sequential, "
+            f"{orc.num_threads()} threads) {cpu_s:.2f} s")
+        if err > 1e-4:
+            raise SystemExit("bench: chunked prefill state differs from the oracle")
+        cpu = {"value": round(t / cpu_s, 1), "unit": "tok/s", "cores": orc.num_threads(),
+               "kind": "port", "sample": f"one sequential oracle scan of the same T={t} input "
+                                         f"({cpu_s:.2f}s)"}
     for _ in range(args.warmup):
         chunked()
     avg = timed(chunked, args.steps)
@@ -374,23 +440,19 @@ def bench_gdn_prefill_config1(mx, args):
     flops = prefill_flops(t, hv)
     tflops = flops / avg / 1e12
     log(f"gdn-prefill-config1: chunked {avg * 1e6:.1f} us/scan ({t / avg:.0f} tok/s, "
-        f"{tflops:.2f} TFLOP/s); sequential GPU scan {seq * 1e6:.1f} us; "
-        f"oracle (sequential, {orc.num_threads()} threads) {cpu_s:.2f} s")
+        f"{tflops:.2f} TFLOP/s); sequential GPU scan {seq * 1e6:.1f} us")
     return {
         "metric": METRIC, "value": round(t / avg, 1), "unit": "tok/s", "ms_per_step": avg * 1e3,
         "dtype": "bf16 q/k/v -> fp32 state, fp32 matrix-core products",
         "config": {"workload": "gdn-prefill-config1", "t": t, "batch": 1, "key_heads": hk,
                    "value_heads": hv, "head_dim": 128, "chunk": 64,
                    "sequential_gpu_scan_us": round(seq * 1e6, 1),
-                   "state_rel_err_vs_oracle": float(f"{err:.3e}")},
+                   "state_rel_err_vs_oracle": None if err is None else float(f"{err:.3e}")},
         "roofline": {"bound": "mfma", "kernel": "chunk_prep_kernel + chunk_scan_kernel",
                      "achieved": round(tflops, 3), "peak": FP32_MFMA_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4),
                      "traffic": None},
-        "cpu_baseline": {"value": round(t / cpu_s, 1), "unit": "tok/s",
-                         "cores": orc.num_threads(), "kind": "port",
-                         "sample": f"one sequential oracle scan of the same T={t} input "
-                                   f"({cpu_s:.2f}s)"},
+        "cpu_baseline": cpu,
     }
 
 
@@ -423,20 +485,18 @@ def bench_gdn_decode_config1(mx, args):
     decay, delta rule, gated RMS norm) for B = 1, 2, 4, 8 rows, each row on its
     own slot of a 1 GiB fp32 state arena (rotated so the 256 MB last-level cache
     cannot serve repeats).  `value` is the B = 8 step's rows per second."""
-    from oracle import oracle as orc
-
     hk, hv, d = 16, 32, 128
     slots_n = 512  # 2 MiB of state per slot
     dims = mx.GdnDimsC(hk, hv, d, d, 4)
     rng = np.random.default_rng(1001)
     rows_max = 8
-    conv = orc.f32_to_bf16(rng.standard_normal((rows_max, 2 * hk * d + hv * d)).astype(np.float32))
-    z = orc.f32_to_bf16(rng.standard_normal((rows_max, hv * d)).astype(np.float32))
-    a = orc.f32_to_bf16(rng.standard_normal((rows_max, hv)).astype(np.float32))
-    b = orc.f32_to_bf16(rng.standard_normal((rows_max, hv)).astype(np.float32))
+    conv = to_bf16(rng.standard_normal((rows_max, 2 * hk * d + hv * d)).astype(np.float32))
+    z = to_bf16(rng.standard_normal((rows_max, hv * d)).astype(np.float32))
+    a = to_bf16(rng.standard_normal((rows_max, hv)).astype(np.float32))
+    b = to_bf16(rng.standard_normal((rows_max, hv)).astype(np.float32))
     a_log = np.log(rng.uniform(1e-3, 16, hv)).astype(np.float32)  # A ~ U(0, 16)
-    dt = orc.f32_to_bf16(rng.uniform(-1, 1, hv).astype(np.float32))
-    norm_w = orc.f32_to_bf16(rng.uniform(0.5, 1.5, d).astype(np.float32))
+    dt = to_bf16(rng.uniform(-1, 1, hv).astype(np.float32))
+    norm_w = to_bf16(rng.uniform(0.5, 1.5, d).astype(np.float32))
     eps = 1e-6
     zab = np.ascontiguousarray(np.concatenate([z, a, b], axis=1))
     dconv, dzab = mx.DeviceArray.from_numpy(conv), mx.DeviceArray.from_numpy(zab)
@@ -456,24 +516,12 @@ def bench_gdn_decode_config1(mx, args):
                                                ddt.ptr, dnw.ptr, eps, C.byref(dims), rows, 1,
                                                lst, state.ptr, None, y.ptr, stream))
 
-    # parity first: one B = 8 step from the zero state against the oracle
+    # one B = 8 step from the zero state: the CPU baseline leg checks it
     launch(rows_max, 0)
     mx.check(mx.lib.mx_stream_sync(stream))
-    st0 = np.zeros((rows_max, hv, d, d), np.float32)
-    sl = np.arange(rows_max, dtype=np.int32)
-    t0 = time.perf_counter()
-    y_w, st_w, _ = orc.gdn_recurrence(conv, z, a, b, a_log, dt, norm_w, eps, hk, hv, rows_max, 1,
-                                      sl, st0)
-    cpu_once = time.perf_counter() - t0
     got_st = np.empty((rows_max, hv, d, d), np.float32)
     mx.check(mx.lib.mx_memcpy_dtoh(got_st.ctypes.data, state.ptr, got_st.nbytes))
-    st_err = np.abs(got_st - st_w).max() / np.abs(st_w).max()
-    got_y = orc.bf16_to_f32(y.numpy()).astype(np.float64)
-    want_y = orc.bf16_to_f32(y_w).astype(np.float64)
-    y_ok = bool(np.all(np.abs(got_y - want_y) <= 2e-2 * np.abs(want_y) + 1e-2))
-    log(f"gdn-decode-config1: B=8 state max rel err vs oracle {st_err:.2e}, y within tolerance {y_ok}")
-    if st_err > 1e-4 or not y_ok:
-        raise SystemExit("bench: GDN decode step differs from the oracle")
+    got_y = bf16_to_f32(y.numpy()).astype(np.float64)
     per_b = {}
     for rows in (1, 2, 4, 8):
         for i in range(args.warmup):
@@ -484,8 +532,25 @@ def bench_gdn_decode_config1(mx, args):
                        "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
         log(f"gdn-decode-config1: B={rows} {sec * 1e6:.2f} us/step, {gbs:.0f} GB/s")
     b8 = per_b[8]
-    cpu = None
+    cpu = st_err = None
     if not args.no_cpu_baseline:
+        # CPU baseline leg: the oracle's B = 8 step from the zero state checks
+        # the GPU's first step, then repeats for about 10 s
+        from oracle import oracle as orc
+
+        st0 = np.zeros((rows_max, hv, d, d), np.float32)
+        sl = np.arange(rows_max, dtype=np.int32)
+        t0 = time.perf_counter()
+        y_w, st_w, _ = orc.gdn_recurrence(conv, z, a, b, a_log, dt, norm_w, eps, hk, hv, rows_max,
+                                          1, sl, st0)
+        cpu_once = time.perf_counter() - t0
+        st_err = float(np.abs(got_st - st_w).max() / np.abs(st_w).max())
+        want_y = bf16_to_f32(y_w).astype(np.float64)
+        y_ok = bool(np.all(np.abs(got_y - want_y) <= 2e-2 * np.abs(want_y) + 1e-2))
+        log(f"gdn-decode-config1: B=8 state max rel err vs oracle {st_err:.2e}, "
+            f"y within tolerance {y_ok}")
+        if st_err > 1e-4 or not y_ok:
+            raise SystemExit("bench: GDN decode step differs from the oracle")
         reps, t0 = 0, time.perf_counter()
         while time.perf_counter() - t0 < 10.0:
             orc.gdn_recurrence(conv, z, a, b, a_log, dt, norm_w, eps, hk, hv, rows_max, 1, sl, st0)
@@ -500,7 +565,7 @@ def bench_gdn_decode_config1(mx, args):
         "config": {"workload": "gdn-decode-config1", "key_heads": hk, "value_heads": hv,
                    "head_dim": d, "state_slots_rotated": slots_n,
                    "per_batch": {str(k): v for k, v in per_b.items()},
-                   "state_rel_err_vs_oracle": float(f"{st_err:.3e}")},
+                   "state_rel_err_vs_oracle": None if st_err is None else float(f"{st_err:.3e}")},
         "roofline": {"bound": "hbm", "kernel": "recurrence_fast_kernel (B=8)",
                      "achieved": b8["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": b8["frac"], "traffic": None,
@@ -518,8 +583,6 @@ def bench_moe_config2(mx, args):
     sublayer).  32 input batches rotate so that consecutive calls select
     different experts.  Bytes per call: router + shared expert + U distinct
     experts x (2 q(512,2048,4) + q(2048,512,5)), U counted per input batch."""
-    from oracle import oracle as orc
-
     E, H, I, k = 512, 2048, 512, 10
     n_x = 32
     gate = mx.QBank.random(E, I, H, 4, 64, 2001)
@@ -529,10 +592,11 @@ def bench_moe_config2(mx, args):
     su = mx.QWeight.random(I, H, 4, 64, 2005)
     sd = mx.QWeight.random(H, I, 5, 64, 2006)
     router = mx.QWeight.random(E + 1, H, 4, 64, 2007)
-    xs = orc.fill_bf16(n_x * 8 * H, 2008, 1, 1.0, 0.0).reshape(n_x, 8, H)
-    res = orc.fill_bf16(8 * 4 * H, 2009, 1, 1.0, 0.0).reshape(8, 4, H)
-    hg = orc.fill_bf16(8 * 4, 2010, 1, 1.0, 1.0).reshape(8, 4)
-    dx, dres, dhg = (mx.DeviceArray.from_numpy(v) for v in (xs, res, hg))
+    dx = mx.DeviceArray((n_x, 8, H), np.uint16)
+    dres = mx.DeviceArray((8, 4, H), np.uint16)
+    dhg = mx.DeviceArray((8, 4), np.uint16)
+    for arr, seed, base in ((dx, 2008, 0.0), (dres, 2009, 0.0), (dhg, 2010, 1.0)):
+        mx.fill_bf16(arr, seed, 1, 1.0, base)
     logits = mx.DeviceArray((8, E + 1), np.uint16)
     ids = mx.DeviceArray((8, k), np.uint32)
     sc = mx.DeviceArray((8, k), np.uint16)
@@ -554,15 +618,11 @@ def bench_moe_config2(mx, args):
 
     ex_bytes = 2 * qweight_bytes(I, H, 4, 64) + qweight_bytes(H, I, 5, 64)
     fixed_bytes = qweight_bytes(E + 1, H, 4, 64) + ex_bytes  # router + shared expert
-    # parity first (B = 8): the routing of the GPU's router logits is the
-    # oracle's, bit for bit; then the distinct experts of every input batch
+    # one B = 8 block whose routing the CPU baseline leg checks; then the
+    # distinct experts of every input batch
     launch(8, 0)
     mx.check(mx.lib.mx_stream_sync(stream))
-    lg = logits.numpy()
-    ids_w, sc_w, fa_w = orc.moe_route(lg[:, :E], lg[:, E], k)
-    if not ((ids.numpy() == ids_w).all() and (sc.numpy() == sc_w).all()
-            and (fa.numpy() == fa_w).all()):
-        raise SystemExit("bench: MoE routing differs from the oracle")
+    first = (logits.numpy(), ids.numpy(), sc.numpy(), fa.numpy())
     per_b = {}
     for rows in range(1, 9):
         distinct = []
@@ -581,8 +641,8 @@ def bench_moe_config2(mx, args):
                        "frac": round(gbs / HBM_PEAK_GBS, 4), "rows_per_s": round(rows / sec, 1)}
         log(f"moe-config2: B={rows} {sec * 1e6:.2f} us/block, U={u:.1f}, {gbs:.0f} GB/s")
     b8 = per_b[8]
-    cpu = None if args.no_cpu_baseline else moe_cpu_baseline(orc, gate, up, down, sg, su, sd,
-                                                             router, xs)
+    cpu = None if args.no_cpu_baseline else moe_cpu_baseline(gate, up, down, sg, su, sd, router,
+                                                             dx.numpy(), first)
     return {
         "metric": METRIC, "value": b8["rows_per_s"], "unit": "tok/s (rows per second)",
         "ms_per_step": b8["us"] / 1e3,
@@ -599,10 +659,18 @@ def bench_moe_config2(mx, args):
     }
 
 
-def moe_cpu_baseline(orc, gate, up, down, sg, su, sd, router, xs):
+def moe_cpu_baseline(gate, up, down, sg, su, sd, router, xs, first):
     """The oracle's B = 8 MoE block (router QMV, route, experts, slot sum),
-    repeated for about 10 s on this host."""
+    repeated for about 10 s on this host, after it checks the routing of the
+    GPU's first block (`first`: its router logits, ids, scores and shared
+    factors) bit for bit."""
+    from oracle import oracle as orc
+
     E, H, k = gate.experts, gate.k, 10
+    lg, ids_g, sc_g, fa_g = first
+    ids_w, sc_w, fa_w = orc.moe_route(lg[:, :E], lg[:, E], k)
+    if not ((ids_g == ids_w).all() and (sc_g == sc_w).all() and (fa_g == fa_w).all()):
+        raise SystemExit("bench: MoE routing differs from the oracle")
     n_x = xs.shape[0]
     # the oracle's structs view host arrays: keep the arrays alive beside them
     host_b = [bk.host() for bk in (gate, up, down)]
@@ -726,9 +794,13 @@ def main() -> None:
     ap.add_argument("--roctx", action="store_true",
                     help="bracket the timed loop with roctxProfilerResume/Pause "
                          "(for rocprofv3 --selected-regions)")
+    ap.add_argument("--fast", action="store_true",
+                    help="config3: time the bf16 matrix-core kernels (within tolerance of the "
+                         "oracle, not bit-exact) as the headline path, and the exact path "
+                         "beside it")
     ap.add_argument("--exact", action="store_true",
-                    help="time the exact (bit-exact, fixed-order) kernels as the headline "
-                         "path, and the matrix-core path beside it")
+                    help="config3: the exact-integer kernels (bit-exact with the oracle) as "
+                         "the headline path, the matrix-core path beside it (the default)")
     ap.add_argument("--no-cpu-baseline", action="store_true",
                     help="skip the oracle CPU baseline (profiling runs)")
     args = ap.parse_args()
@@ -739,9 +811,7 @@ def main() -> None:
     steps, warmup = DEFAULTS[args.workload]
     args.steps = steps if args.steps is None else args.steps
     args.warmup = warmup if args.warmup is None else args.warmup
-    from conftest import load_mx
-
-    mx = load_mx()
+    mx = load_package()
     res = WORKLOADS[args.workload](mx, args)
     out = {
         "metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1,

@@ -100,6 +100,18 @@ constexpr int batch_groups() {
   return BITS == 8 ? 4 : 8;  // groups per load batch (8-bit codes are twice as wide)
 }
 
+// Groups per load batch of a wave covering 2 SPW groups.
+template <int BITS, int SPW>
+constexpr int tile_batch() {
+  return 2 * SPW < batch_groups<BITS>() ? 2 * SPW : batch_groups<BITS>();
+}
+
+// sb_vector_ok for the batches of xq_tiles over matrix w.
+template <int BITS, int SPW>
+__device__ __forceinline__ bool tiles_sbv(const QWeight& w) {
+  return xq::sb_vector_ok<tile_batch<BITS, SPW>()>(w.scales, w.biases, w.k / xq::kGroup);
+}
+
 // LDS bytes of xq_tiles: the staged or copied operands of G groups, and the
 // slice sums of T tiles when KS > 1 (they reuse the operand area).
 __host__ __device__ constexpr int tiles_lds(int G, int T, int KS, int SRC) {
@@ -121,27 +133,25 @@ __host__ __device__ constexpr int tiles_lds(int G, int T, int KS, int SRC) {
 template <int BITS, int T, int KS, int SPW, int SRC, class Rows, class Pre>
 __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
                                          const uint16_t* __restrict__ srow,
-                                         const uint16_t* __restrict__ brow, int K, int M,
-                                         int blocks, const Rows& xr, const char* plane, char* lds,
-                                         float* yt, Pre&& pre) {
+                                         const uint16_t* __restrict__ brow, bool sbv, int K,
+                                         int M, int blocks, const Rows& xr, const char* plane,
+                                         char* lds, float* yt, Pre&& pre) {
   constexpr int NC = 16 * T, NT = 64 * T * KS;
   constexpr int NG = 2 * SPW;
-  constexpr int B = NG < batch_groups<BITS>() ? NG : batch_groups<BITS>();
+  constexpr int B = tile_batch<BITS, SPW>();
   constexpr int NB = NG / B;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane & 15, kb = lane >> 4;
+  const int lane = threadIdx.x & 63, j = lane & 15, kb = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int t = wave / KS, ks = wave - t * KS;
   const int G = K / xq::kGroup, S = (G + 1) / 2;
   const int gbeg = 2 * ks * SPW, gend = min(gbeg + NG, G);
   xq::Codes<BITS> c[2][B];
-  uint16_t sv[2][B], bv[2][B];
+  xq::ScaleBias<B> sb[2];
   auto load_batch = [&](int buf, int bi) {
 #pragma unroll
-    for (int i = 0; i < B; ++i) {
-      const int g = min(gbeg + bi * B + i, gend - 1);
-      xq::load_codes<BITS>(crow, g, kb, c[buf][i]);
-      sv[buf][i] = srow[g];
-      bv[buf][i] = brow[g];
-    }
+    for (int i = 0; i < B; ++i)
+      xq::load_codes<BITS>(crow, min(gbeg + bi * B + i, gend - 1), kb, c[buf][i]);
+    xq::load_scale_bias<B>(srow, brow, gbeg + bi * B, gend, sbv, sb[buf]);
   };
   load_batch(0, 0);
   if constexpr (NB > 1) load_batch(1, 1);
@@ -150,10 +160,7 @@ __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
   if constexpr (SRC == kSrcStage) {
     xq::stage<NT>(lds, xr, M, 0, G);
   } else if constexpr (SRC == kSrcPlaneLds) {
-    const int n16 = xq::stage_bytes(G) / 16;
-    for (int i = threadIdx.x; i < n16; i += NT)
-      reinterpret_cast<uint4*>(lds)[i] = reinterpret_cast<const uint4*>(plane)[i];
-    __syncthreads();
+    xq::dma_plane<NT>(lds, plane, G);
   } else if constexpr (SRC == kSrcPlane) {
     src = plane;
   }
@@ -189,8 +196,7 @@ __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
           e1 = es[g * 8 + 4 + kb];
         }
         xq::group_step<BITS>(a0, a1, blocks, xq::b_operand<BITS>(c[buf][i]), q0, q1, e0, e1,
-                             double(bf16_to_f32(sv[buf][i])), double(bf16_to_f32(bv[buf][i])),
-                             acc);
+                             sb[buf].scale(i), sb[buf].bias(i), acc);
         // a slice ends after its second group, or after the last group of an
         // odd count
         if ((gl & 1) || g + 1 == gend) {
@@ -260,8 +266,9 @@ __global__ __launch_bounds__(64 * T * KS) void xq_dense_kernel(QWeight w,
   ProjFinish<MODE, NC, NT> fin;
   fin.begin(e, tg, M, n);
   xq_tiles<BITS, T, KS, SPW, SRC>(w.codes + size_t(row) * (size_t(w.k) * BITS / 32),
-                                  w.scales + size_t(row) * G, w.biases + size_t(row) * G, w.k, M,
-                                  M > 4 ? 3 : 1, XRows{x, x_stride}, plane, lds, yt,
+                                  w.scales + size_t(row) * G, w.biases + size_t(row) * G,
+                                  tiles_sbv<BITS, SPW>(w), w.k, M, M > 4 ? 3 : 1,
+                                  XRows{x, x_stride}, plane, lds, yt,
                                   [&] { fin.prefetch(e); });
   fin.finish(yt, e, tg, M, n);
 }
@@ -289,24 +296,6 @@ __device__ __forceinline__ QWeight bank_matrix(const QBank& b, int expert, const
 
 // Copies a plane of G groups (xq_core.hpp layout) into LDS: every thread
 // issues all of its loads before its first store.  Ends with a barrier.
-template <int NT>
-__device__ __forceinline__ void copy_plane(char* lds, const char* plane, int G) {
-  constexpr int kMaxPer = 12;  // 68.6 KiB (K = 2048) over 512 threads
-  const int n16 = xq::stage_bytes(G) / 16;
-  uint4 v[kMaxPer];
-#pragma unroll
-  for (int k = 0; k < kMaxPer; ++k) {
-    const int i = int(threadIdx.x) + k * NT;
-    if (i < n16) v[k] = reinterpret_cast<const uint4*>(plane)[i];
-  }
-#pragma unroll
-  for (int k = 0; k < kMaxPer; ++k) {
-    const int i = int(threadIdx.x) + k * NT;
-    if (i < n16) reinterpret_cast<uint4*>(lds)[i] = v[k];
-  }
-  __syncthreads();
-}
-
 // Expert gate/up + SwiGLU for one plan entry (blockIdx.y) and 128
 // intermediate rows (blockIdx.x).  Every wave is independent: it owns 16
 // intermediate rows, streams their gate rows and then their up rows over the
@@ -324,7 +313,7 @@ __global__ __launch_bounds__(512) void xq_gate_up_kernel(
   extern __shared__ __align__(16) char lds[];
   __shared__ int ro[8], so[8];
   constexpr int NG = 2 * SPW;                       // groups per pass (at most)
-  constexpr int B = NG < batch_groups<BITS>() ? NG : batch_groups<BITS>();
+  constexpr int B = tile_batch<BITS, SPW>();
   constexpr int NBP = NG / B;                       // batches per pass
   constexpr int NB = 2 * NBP;                       // gate pass, then up pass
   constexpr int D = NB < 3 ? NB : 3;                // batches in flight
@@ -337,37 +326,43 @@ __global__ __launch_bounds__(512) void xq_gate_up_kernel(
   const int i0 = blockIdx.x * 128;
   if (i0 >= inter) return;
   const int M = plan->m[entry];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane & 15, kb = lane >> 4;
+  const int lane = threadIdx.x & 63, j = lane & 15, kb = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int G = hidden / xq::kGroup;
   const int row = min(i0 + 16 * wave + j, inter - 1);
+  const bool sbv[2] = {xq::sb_vector_ok<B>(gw.scales, gw.biases, G),
+                       xq::sb_vector_ok<B>(uw.scales, uw.biases, G)};
   const size_t wpr = size_t(hidden) * BITS / 32;
   const uint32_t* crow[2] = {gw.codes + row * wpr, uw.codes + row * wpr};
   const uint16_t* srow[2] = {gw.scales + size_t(row) * G, uw.scales + size_t(row) * G};
   const uint16_t* brow[2] = {gw.biases + size_t(row) * G, uw.biases + size_t(row) * G};
   xq::Codes<BITS> c[D][B];
-  uint16_t sv[D][B], bv[D][B];
+  xq::ScaleBias<B> sb[D];
   auto load_batch = [&](int buf, int bi) {
-    const int pass = bi / NBP;
+    const int pass = bi / NBP, g0 = (bi % NBP) * B;
 #pragma unroll
-    for (int i = 0; i < B; ++i) {
-      const int g = min((bi % NBP) * B + i, G - 1);
-      xq::load_codes<BITS>(crow[pass], g, kb, c[buf][i]);
-      sv[buf][i] = srow[pass][g];
-      bv[buf][i] = brow[pass][g];
-    }
+    for (int i = 0; i < B; ++i) xq::load_codes<BITS>(crow[pass], min(g0 + i, G - 1), kb, c[buf][i]);
+    xq::load_scale_bias<B>(srow[pass], brow[pass], g0, G, sbv[pass], sb[buf]);
   };
+  // member rows and slots: loaded before the weights, stored after them, so
+  // no wait for them holds the weight loads back
+  int r8 = 0, s8 = 0;
+  if (threadIdx.x < 8) {
+    r8 = plan->row[entry][threadIdx.x];
+    s8 = plan->slot[entry][threadIdx.x];
+  }
 #pragma unroll
   for (int d = 0; d < D; ++d) load_batch(d, d);
   if (threadIdx.x < 8) {
-    ro[threadIdx.x] = plan->row[entry][threadIdx.x];
-    so[threadIdx.x] = plan->slot[entry][threadIdx.x];
+    ro[threadIdx.x] = r8;
+    so[threadIdx.x] = s8;
   }
-  int blocks = 0;
+  int blocks = M > 4 ? 3 : 1;
   if constexpr (SRC == kSrcPlaneLds) {
-    for (int m = 0; m < M; ++m) blocks |= plan->row[entry][m] < 4 ? 1 : 2;
-    copy_plane<512>(lds, plane, G);
+    xq::dma_plane<512>(lds, plane, G);
+    blocks = 0;
+    for (int m = 0; m < M; ++m) blocks |= ro[m] < 4 ? 1 : 2;
   } else {
-    blocks = M > 4 ? 3 : 1;
     __syncthreads();
     xq::stage<512>(lds, MemberRows{x, hidden, 0, ro, so}, M, 0, G);
   }
@@ -385,8 +380,8 @@ __global__ __launch_bounds__(512) void xq_gate_up_kernel(
         xq::group_step<BITS>(*reinterpret_cast<const xq::v4i*>(ab),
                              *reinterpret_cast<const xq::v4i*>(ab + xq::kBlockBytes), blocks,
                              xq::b_operand<BITS>(c[buf][i]), qs[gl * 8 + kb], qs[gl * 8 + 4 + kb],
-                             es[gl * 8 + kb], es[gl * 8 + 4 + kb], double(bf16_to_f32(sv[buf][i])),
-                             double(bf16_to_f32(bv[buf][i])), acc);
+                             es[gl * 8 + kb], es[gl * 8 + 4 + kb], sb[buf].scale(i),
+                             sb[buf].bias(i), acc);
         // a slice ends after its second group, or after the last of an odd count
         if ((gl & 1) || gl + 1 == G) {
           tot[pass][0] = tot[pass][0] + acc[0];
@@ -443,7 +438,7 @@ __global__ __launch_bounds__(256) void xq_down_kernel(const uint16_t* __restrict
   const int G = inter / xq::kGroup;
   xq_tiles<BITS, 4, 1, SPW, kSrcStage>(dw.codes + size_t(row) * (size_t(inter) * BITS / 32),
                                        dw.scales + size_t(row) * G, dw.biases + size_t(row) * G,
-                                       inter, M, M > 4 ? 3 : 1,
+                                       tiles_sbv<BITS, SPW>(dw), inter, M, M > 4 ? 3 : 1,
                                        MemberRows{h, int64_t(top_k + 1) * hs, hs, ro, so}, nullptr,
                                        lds, yt, [] {});
   for (int i = threadIdx.x; i < 8 * 64; i += 256) {
@@ -475,7 +470,8 @@ __global__ __launch_bounds__(1024) void xq_upmix_kernel(QWeight w, const uint16_
   const int G = w.k / xq::kGroup;
   xq_tiles<BITS, 16, 1, SPW, kSrcStage>(w.codes + size_t(row) * (size_t(w.k) * BITS / 32),
                                         w.scales + size_t(row) * G, w.biases + size_t(row) * G,
-                                        w.k, M, M > 4 ? 3 : 1, XRows{lo, w.k}, nullptr, lds, yt,
+                                        tiles_sbv<BITS, SPW>(w), w.k, M, M > 4 ? 3 : 1,
+                                        XRows{lo, w.k}, nullptr, lds, yt,
                                         [] {});
   for (int i = threadIdx.x; i < 8 * 64; i += 1024) {
     const int m = i >> 6, c = i & 63;
@@ -533,8 +529,9 @@ __global__ __launch_bounds__(1024) void xq_head_kernel(QWeight w, const uint16_t
   const int n = w.n, G = w.k / xq::kGroup;
   const int row = min(tg * 256 + 16 * t + j, n - 1);
   xq_tiles<BITS, 16, 1, SPW, SRC>(w.codes + size_t(row) * (size_t(w.k) * BITS / 32),
-                                  w.scales + size_t(row) * G, w.biases + size_t(row) * G, w.k, M,
-                                  M > 4 ? 3 : 1, XRows{x, w.k}, plane, lds, yt, [] {});
+                                  w.scales + size_t(row) * G, w.biases + size_t(row) * G,
+                                  tiles_sbv<BITS, SPW>(w), w.k, M, M > 4 ? 3 : 1, XRows{x, w.k},
+                                  plane, lds, yt, [] {});
   // wave t ranks columns 16 t .. +15 for every row (lane = 16 m' + c, two
   // passes of four rows), then wave 0 ranks the 16 wave bests per row
   const int lane = threadIdx.x & 63;

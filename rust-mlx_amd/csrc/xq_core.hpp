@@ -256,6 +256,82 @@ __device__ __forceinline__ void stage(char* lds, const Rows& xr, int M, int g0, 
   __syncthreads();
 }
 
+// Copies an activation plane of G groups (the layout above) into LDS with
+// direct global-to-LDS loads, 16 bytes per lane, no registers held; all NT
+// threads of the workgroup call it.  Ends with every load landed and a
+// barrier.
+template <int NT>
+__device__ __forceinline__ void dma_plane(char* lds, const char* __restrict__ plane, int G) {
+  const int n16 = stage_bytes(G) / 16;
+  const int lane = threadIdx.x & 63;
+  for (int i = threadIdx.x; i < n16; i += NT) {
+    // the wave's lanes land at consecutive 16-byte slots from its first index
+    __builtin_amdgcn_global_load_lds(
+        plane + size_t(i) * 16,
+        reinterpret_cast<__attribute__((address_space(3))) void*>(
+            reinterpret_cast<uintptr_t>(lds + size_t(i - lane) * 16)),
+        16, 0, 0);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+}
+
+// Scales and biases of B consecutive groups of one weight row, as bf16 pairs.
+template <int B>
+struct ScaleBias {
+  static constexpr int W = (B + 1) / 2;
+  uint32_t s[W], b[W];
+  __device__ __forceinline__ double scale(int i) const { return half(s[i >> 1], i); }
+  __device__ __forceinline__ double bias(int i) const { return half(b[i >> 1], i); }
+  __device__ __forceinline__ static double half(uint32_t w, int i) {
+    return double(u2f((i & 1) ? (w & 0xffff0000u) : (w << 16)));
+  }
+};
+
+// Whether the scale and bias rows of a matrix with G groups per row can be
+// read B values at a time: G a multiple of B and both arrays starting on a
+// 2B-byte boundary (then every row and every batch start on one too).
+template <int B>
+__host__ __device__ __forceinline__ bool sb_vector_ok(const uint16_t* scales,
+                                                      const uint16_t* biases, int G) {
+  const uintptr_t at = reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(biases);
+  return B > 1 && G % B == 0 && (at & uintptr_t(2 * B - 1)) == 0;
+}
+
+// Groups g0 .. g0 + B - 1 of the row's scales and biases, indices clamped to
+// gend - 1: one vector load each when `vec` (sb_vector_ok of the matrix) and
+// the batch starts on a multiple of B and lies below gend.  Every argument
+// but the row pointers is the same across the wave, so the choice is too.
+template <int B>
+__device__ __forceinline__ void load_scale_bias(const uint16_t* __restrict__ srow,
+                                                const uint16_t* __restrict__ brow, int g0,
+                                                int gend, bool vec, ScaleBias<B>& o) {
+  static_assert(B == 1 || B == 2 || B == 4 || B == 8, "batch");
+  if (B > 1 && vec && g0 % B == 0 && g0 + B <= gend) {
+    if constexpr (B == 8) {
+      const uint4 sv = *reinterpret_cast<const uint4*>(srow + g0);
+      const uint4 bv = *reinterpret_cast<const uint4*>(brow + g0);
+      o.s[0] = sv.x; o.s[1] = sv.y; o.s[2] = sv.z; o.s[3] = sv.w;
+      o.b[0] = bv.x; o.b[1] = bv.y; o.b[2] = bv.z; o.b[3] = bv.w;
+    } else if constexpr (B == 4) {
+      const uint2 sv = *reinterpret_cast<const uint2*>(srow + g0);
+      const uint2 bv = *reinterpret_cast<const uint2*>(brow + g0);
+      o.s[0] = sv.x; o.s[1] = sv.y;
+      o.b[0] = bv.x; o.b[1] = bv.y;
+    } else if constexpr (B == 2) {
+      o.s[0] = *reinterpret_cast<const uint32_t*>(srow + g0);
+      o.b[0] = *reinterpret_cast<const uint32_t*>(brow + g0);
+    }
+  } else {
+#pragma unroll
+    for (int w = 0; w < ScaleBias<B>::W; ++w) {
+      const int ga = min(g0 + 2 * w, gend - 1), gb = min(g0 + 2 * w + 1, gend - 1);
+      o.s[w] = uint32_t(srow[ga]) | (uint32_t(srow[gb]) << 16);
+      o.b[w] = uint32_t(brow[ga]) | (uint32_t(brow[gb]) << 16);
+    }
+  }
+}
+
 // One group of a tile row into the two fp64 row accumulators of this lane
 // (activation rows l / 16 and 4 + l / 16 against tile row l % 16) for the
 // four-row blocks in `blocks` (bit 0: rows 0-3, bit 1: rows 4-7): a, Q and Eb
@@ -266,9 +342,11 @@ __device__ __forceinline__ void group_step(const v4i& a0, const v4i& a1, int blo
                                            double s, double b, double (&acc)[2]) {
   const v4i zero = {0, 0, 0, 0};
   auto fold = [&](const v4i& d, double q, int e) {
-    double p = fma(fma(fma(double(d.w), 256.0, double(d.z)), 256.0, double(d.y)), 256.0,
-                   double(d.x));
-    if constexpr (BITS == 8) p = p + 128.0 * q;  // codes entered as q - 128
+    // P = (D0 + 256 D1) + 65536 (D2 + 256 D3): each pair is exact in int32
+    // (|D| < 2^21) and the fp64 combination is exact (|P| < 2^47)
+    const int lo = d.x + d.y * 256, hi = d.z + d.w * 256;
+    double p = fma(double(hi), 65536.0, double(lo));
+    if constexpr (BITS == 8) p = fma(q, 128.0, p);  // codes entered as q - 128
     return __builtin_amdgcn_ldexp(fma(p, s, q * b), e - 156);
   };
   if (blocks & 1) acc[0] = acc[0] + fold(mfma(a0, bop, zero), q0, e0);
