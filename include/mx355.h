@@ -342,6 +342,19 @@ mx_status mx_moe_reduce_hc_epilogue(const uint16_t* partial, const uint16_t* fac
 size_t mx_head_workspace_bytes(int32_t n, int32_t k, int32_t m);
 mx_status mx_head_argmax(const mx_qweight* w, const uint16_t* x, int32_t m, uint32_t* tokens,
                          void* workspace, void* stream);
+/* mx_head_argmax for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc): no
+ * workspace argument and no allocation of any kind.  The partials live in a
+ * static device array of 1 MiB per GPU, held until the process ends; the
+ * call returns MX_EUNSUPPORTED when mx_head_workspace_bytes(n, k, m) exceeds
+ * mx_head_noalloc_max_bytes() (1 MiB: a 262144-row head at k >= 2048 and
+ * m = 8).  Every call on one GPU shares that array: calls that overlap on
+ * one GPU (different streams or threads) race.  Same tokens as
+ * mx_head_argmax bit for bit (same kernels).  No counterpart in the
+ * reference: an addition for callers that cannot allocate. */
+size_t mx_head_noalloc_max_bytes(void);
+mx_status mx_head_argmax_noalloc(const mx_qweight* w, const uint16_t* x, int32_t m,
+                                 uint32_t* tokens, void* stream);
 /* mx_head_argmax with the head projection on the matrix cores (fp32
  * summation order differs from the exact kernel, so near-ties may resolve
  * differently; the selection rule is the same).  Requires group_size 64,

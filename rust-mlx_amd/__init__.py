@@ -196,6 +196,8 @@ def _load() -> C.CDLL:
         "mx_qmm_conv": ([C.POINTER(QWeightC), vp, i32, i32, i32, vp, vp, vp, vp, i64, vp, i64, vp],
                         i32),
         "mx_head_argmax_mfma": ([C.POINTER(QWeightC), vp, i32, vp, vp, vp], i32),
+        "mx_head_noalloc_max_bytes": ([], C.c_size_t),
+        "mx_head_argmax_noalloc": ([C.POINTER(QWeightC), vp, i32, vp, vp], i32),
         "mx_moe_experts_mfma": ([vp, vp, vp, i32, i32, C.POINTER(QBankC), C.POINTER(QBankC),
                                  C.POINTER(QBankC), C.POINTER(QWeightC), C.POINTER(QWeightC),
                                  C.POINTER(QWeightC), vp, vp, vp], i32),

@@ -303,6 +303,22 @@ MX_ABI mx_status mx_head_argmax(const mx_qweight* w, const uint16_t* x, int32_t 
                 "mx_head_argmax");
 }
 
+MX_ABI size_t mx_head_noalloc_max_bytes(void) { return kHeadNoAllocScratchBytes; }
+
+MX_ABI mx_status mx_head_argmax_noalloc(const mx_qweight* w, const uint16_t* x, int32_t m,
+                                        uint32_t* tokens, void* stream) {
+  MX_CHECK(w && x && tokens, MX_EINVAL, "mx_head_argmax_noalloc: null pointer");
+  const QWeight q = to_qweight(*w);
+  if (const char* err = check_qweight(q))
+    return mx_status(set_error(MX_EINVAL, std::string("mx_head_argmax_noalloc: ") + err));
+  MX_CHECK(m >= 1 && m <= 8, MX_EUNSUPPORTED, "mx_head_argmax_noalloc: m must be in 1..8");
+  MX_CHECK(head_noalloc_bytes(q.n, q.k, m) <= kHeadNoAllocScratchBytes, MX_EUNSUPPORTED,
+           "mx_head_argmax_noalloc: the partials of this head (mx_head_workspace_bytes) exceed "
+           "the static scratch (mx_head_noalloc_max_bytes)");
+  return finish(head_argmax_noalloc(q, x, m, tokens, hipStream_t(stream)),
+                "mx_head_argmax_noalloc");
+}
+
 MX_ABI mx_status mx_head_argmax_mfma(const mx_qweight* w, const uint16_t* x, int32_t m,
                                      uint32_t* tokens, void* workspace, void* stream) {
   MX_CHECK(w && x && tokens && workspace, MX_EINVAL, "mx_head_argmax_mfma: null pointer");

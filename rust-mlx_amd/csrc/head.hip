@@ -8,6 +8,8 @@
 // The default reference path, argmax_axis(head.forward_rows(x))
 // (src/bin/batch-bench.rs:118-120), selects the same token: the selection
 // rule below is a total order, so the split into partials cannot change it.
+#include <mutex>
+
 #include "common.hpp"
 #include "kernels.hpp"
 #include "qmv_core.hpp"
@@ -189,6 +191,54 @@ int argmax_reduce(const float* maxima, const uint32_t* indices, int rows, int pa
                   uint32_t* tokens, hipStream_t s) {
   hipLaunchKernelGGL(reduce_kernel, dim3(rows), dim3(256), 0, s, maxima, indices, parts, tokens);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
+// Partials of head_argmax_noalloc: a file-scope device array, one copy per
+// GPU, shared by every call on that GPU (calls that overlap on one GPU race).
+// Host code never passes `scratch` itself to a kernel: in host code the name
+// stands for a host-side shadow, so kernels receive the device address that
+// hipGetSymbolAddress returns for the current device.
+namespace {
+__device__ __align__(256) unsigned char scratch[kHeadNoAllocScratchBytes];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
+}  // namespace
+
+// The current device's copy of `scratch`: looked up on the first call on each
+// device (with that device current) and kept.
+static int noalloc_scratch(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return MX_EHIP;
+  if (dev < 0 || dev >= kMaxDevices) return MX_EUNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return MX_EHIP;
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return MX_OK;
+}
+
+size_t head_noalloc_bytes(int n, int k, int m) {
+  return size_t(head_parts(n, k)) * size_t(m) * (sizeof(float) + sizeof(uint32_t));
+}
+
+// head_partials + argmax_reduce with the partials in this device's `scratch`
+// instead of a workspace.  Every partial the reduction reads is written by
+// the partials launch of the same call, so nothing needs clearing.
+int head_argmax_noalloc(const QWeight& w, const uint16_t* x, int m, uint32_t* tokens,
+                        hipStream_t s) {
+  if (head_noalloc_bytes(w.n, w.k, m) > kHeadNoAllocScratchBytes) return MX_EUNSUPPORTED;
+  void* base = nullptr;
+  if (int rc = noalloc_scratch(&base); rc != MX_OK) return rc;
+  const int parts = head_parts(w.n, w.k);
+  float* maxima = static_cast<float*>(base);
+  uint32_t* indices = reinterpret_cast<uint32_t*>(maxima + size_t(parts) * m);
+  int got = 0;
+  if (int rc = head_partials(w, x, m, maxima, indices, &got, s); rc != MX_OK) return rc;
+  return argmax_reduce(maxima, indices, m, parts, tokens, s);
 }
 
 int argmax_bf16(const uint16_t* logits, int rows, int n, uint32_t* tokens, hipStream_t s) {

@@ -222,6 +222,13 @@ int moe_reduce_hc_epilogue(const uint16_t* p, const uint16_t* factor, const uint
 int head_parts(int n, int k);
 int head_partials(const QWeight& w, const uint16_t* x, int m, float* maxima, uint32_t* indices,
                   int* parts, hipStream_t s);
+// Greedy head without a workspace: the partials live in a static device
+// array of kHeadNoAllocScratchBytes per GPU (head.hip); MX_EUNSUPPORTED when
+// head_noalloc_bytes(n, k, m) exceeds it.
+constexpr size_t kHeadNoAllocScratchBytes = size_t(1) << 20;
+size_t head_noalloc_bytes(int n, int k, int m);
+int head_argmax_noalloc(const QWeight& w, const uint16_t* x, int m, uint32_t* tokens,
+                        hipStream_t s);
 int argmax_reduce(const float* maxima, const uint32_t* indices, int rows, int parts,
                   uint32_t* tokens, hipStream_t s);
 int argmax_bf16(const uint16_t* logits, int rows, int n, uint32_t* tokens, hipStream_t s);

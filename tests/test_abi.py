@@ -61,3 +61,17 @@ def test_layer_entry_points_reject_bad_geometry_without_device(mx):
     assert mx.lib.mx_head_argmax(C.byref(head), fake, 0, fake, fake, None) == mx.MX_EUNSUPPORTED
     assert mx.lib.mx_head_workspace_bytes(151936, 2048, 8) > 0
     assert mx.lib.mx_moe_workspace_bytes(8, 10, 512) >= 8 * 11 * 512 * 2
+
+
+def test_noalloc_head_refuses_oversized_heads_without_device(mx):
+    """The static-scratch head rejects a head whose partials exceed its
+    1 MiB array before any launch (pointers are never dereferenced)."""
+    fake = 256
+    assert mx.lib.mx_head_noalloc_max_bytes() == 1 << 20
+    big = mx.QWeightC(fake, fake, fake, 300000, 2048, 8, 64)
+    assert mx.lib.mx_head_workspace_bytes(300000, 2048, 8) > mx.lib.mx_head_noalloc_max_bytes()
+    assert mx.lib.mx_head_argmax_noalloc(C.byref(big), fake, 8, fake, None) == mx.MX_EUNSUPPORTED
+    assert b"static scratch" in mx.lib.mx_last_error()
+    ok = mx.QWeightC(fake, fake, fake, 1000, 512, 8, 64)
+    assert mx.lib.mx_head_argmax_noalloc(C.byref(ok), fake, 9, fake, None) == mx.MX_EUNSUPPORTED
+    assert mx.lib.mx_head_argmax_noalloc(C.byref(ok), None, 1, fake, None) == mx.MX_EINVAL
