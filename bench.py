@@ -177,6 +177,26 @@ def bench_config3(mx, args):
     eng.set_flags(exact=exact, eager=args.eager)
     log(f"config3: {'fast' if exact else 'exact'} mode {exact_steps} steps: "
         f"{other_tok_s:.1f} tok/s, {other_dt * 1e3:.3f} ms/step")
+    # the reference's batching policy (src/bin/server/batch.rs:274-289): only
+    # rows at equal offsets share a decode step (mx_engine_decode_batch); the
+    # ragged rows here all differ, so each row steps alone
+    toks = np.asarray(toks, np.uint32).copy()
+    groups = {}
+    for i, s_ in enumerate(slots):
+        groups.setdefault(eng.offset(s_), []).append(i)
+    ref_steps = max(args.steps // 8, 4)
+    for _ in range(2):
+        for idx in groups.values():
+            toks[idx] = eng.decode_batch([slots[i] for i in idx], toks[idx], equal=True)
+    mx.check(mx.lib.mx_device_sync())
+    t0 = time.perf_counter()
+    for _ in range(ref_steps):
+        for idx in groups.values():
+            toks[idx] = eng.decode_batch([slots[i] for i in idx], toks[idx], equal=True)
+    mx.check(mx.lib.mx_device_sync())
+    ref_tok_s = rows * ref_steps / (time.perf_counter() - t0)
+    log(f"config3: reference batching policy ({len(groups)} equal-offset groups per step): "
+        f"{ref_tok_s:.1f} tok/s over {ref_steps} steps")
     # a second profiled step after the timed loop (longer contexts), then the
     # expert kernels of all 48 layers back to back on that step's routing
     _, prof2 = eng.profile_step(slots, toks)
@@ -214,6 +234,8 @@ def bench_config3(mx, args):
             "context": "synthetic" if args.synthetic_context else "prefilled",
             "mode": "exact" if exact else "fast",
             ("fast_tok_s" if exact else "exact_tok_s"): round(other_tok_s, 2),
+            "reference_policy_tok_s": round(ref_tok_s, 2),
+            "reference_policy_groups": len(groups),
         },
         "roofline": {"bound": "hbm",
                      "kernel": ("xq_gate_up_kernel<4, 16, 3> (exact-integer expert gate/up + SwiGLU, "

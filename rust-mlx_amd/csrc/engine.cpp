@@ -697,12 +697,14 @@ int record_layer(Engine& e, const LayerW& L, int rows, int groups, int t, bool h
         MX_TRY(experts_down(e, L, rows));
       }
     } else {
-      MX_TRY(moe_route(e.logits_r, c.experts + 1, e.logits_r + c.experts, c.experts + 1, rows,
-                       c.experts, c.top_k, e.ids, e.scores, e.factor, e.stream));
       if (e.prof) {
+        MX_TRY(moe_route(e.logits_r, c.experts + 1, e.logits_r + c.experts, c.experts + 1, rows,
+                         c.experts, c.top_k, e.ids, e.scores, e.factor, e.stream));
         MX_TRY(profile_experts(e, L, rows));
       } else {
-        MX_TRY(moe_plan(e.ids, rows, c.top_k, e.moe_plan_buf, e.stream));
+        MX_TRY(moe_route_plan(e.logits_r, c.experts + 1, e.logits_r + c.experts, c.experts + 1,
+                              rows, c.experts, c.top_k, e.ids, e.scores, e.factor,
+                              e.moe_plan_buf, e.stream));
         MX_TRY(experts_gate_up(e, L, rows));
         MX_TRY(experts_down(e, L, rows));
       }

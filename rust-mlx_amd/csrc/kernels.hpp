@@ -181,14 +181,22 @@ constexpr int kAttnFastChunk = 64;
 constexpr int kMaxRoutes = 8 * 16 + 1;
 // Work list of one MoE step: distinct routed experts (first appearance order)
 // and the shared expert (-1), each with the (row, slot) routes it serves.
+// item[]: the (entry, four-row block of rows) pairs that have a member, as
+// 2 entry + block, entries in order (the exact gate/up kernel's work list).
 struct MoePlan {
   int32_t count;
   int32_t expert[kMaxRoutes];
   int32_t m[kMaxRoutes];
   uint8_t row[kMaxRoutes][8];
   uint8_t slot[kMaxRoutes][8];
+  int32_t nitems;
+  uint16_t item[2 * kMaxRoutes];
 };
 int moe_plan(const uint32_t* ids, int rows, int top_k, MoePlan* plan, hipStream_t s);
+// moe_route then moe_plan of its ids, in one launch (rows <= 8)
+int moe_route_plan(const uint16_t* logits, int64_t logit_stride, const uint16_t* shared_logit,
+                   int64_t shared_stride, int rows, int experts, int top_k, uint32_t* ids,
+                   uint16_t* scores, uint16_t* factor, MoePlan* plan, hipStream_t s);
 size_t moe_workspace_bytes(int rows, int top_k, int inter);
 int moe_route(const uint16_t* logits, int64_t logit_stride, const uint16_t* shared_logit,
               int64_t shared_stride, int rows, int experts, int top_k, uint32_t* ids,

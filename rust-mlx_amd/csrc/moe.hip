@@ -50,52 +50,115 @@ __global__ __launch_bounds__(64) void route_kernel(const uint16_t* __restrict__ 
 // Expert work plan: one entry per distinct routed expert (in order of first
 // appearance among the rows' slots) plus one for the shared expert, listing
 // the (row, slot) routes it serves.  One workgroup; routes <= 8 * 16 + 1.
-__global__ __launch_bounds__(256) void plan_kernel(const uint32_t* __restrict__ ids, int rows,
-                                                   int top_k, MoePlan* __restrict__ plan) {
-  __shared__ uint32_t sids[kMaxRoutes];
-  __shared__ int wave_count[4];
+// The plan from the route ids in sids (LDS); every thread of the workgroup
+// calls it (NT threads, at most 8 waves; routes <= 8 * 16 + 1).
+template <int NT>
+__device__ __forceinline__ void plan_body(const uint32_t* sids, int rows, int top_k,
+                                          MoePlan* __restrict__ plan) {
+  __shared__ int entry_of[kMaxRoutes];  // entry index, by its first route
+  __shared__ int wave_count[8], wave_items[8];
+  constexpr int NW = NT / 64;
   const int t = threadIdx.x;
   const int routes = rows * top_k;
-  if (t < routes) sids[t] = ids[t];
-  __syncthreads();
-  bool first = false;
-  int e = -1;
-  if (t < routes) {
-    e = int(sids[t]);
-    first = true;
-    for (int u = 0; u < t; ++u)
-      if (int(sids[u]) == e) {
-        first = false;
-        break;
+  // one pass over every route: the first route of this route's expert, this
+  // route's place among the expert's routes (route order), how many there
+  // are, and which four-row blocks of rows they come from
+  const bool routed = t < routes;
+  const uint32_t e = routed ? sids[t] : 0u;
+  int first_u = t, pos = 0, cnt = 0, blkmask = 0;
+  if (routed) {
+    for (int r = 0, u = 0; r < rows; ++r) {
+      int hit = 0;
+#pragma unroll 4
+      for (int k = 0; k < top_k; ++k, ++u) {
+        const bool match = sids[u] == e;
+        first_u = match && u < first_u ? u : first_u;
+        pos += match && u < t;
+        hit += match;
       }
-  } else if (t == routes) {
-    first = true;  // the shared expert
+      cnt += hit;
+      blkmask |= hit ? 1 << (r >> 2) : 0;
+    }
+  } else if (t == routes) {  // the shared expert: every row, slot top_k
+    cnt = rows;
+    blkmask = rows > 4 ? 3 : 1;
   }
+  const bool first = routed ? first_u == t : t == routes;
   const uint64_t mask = __ballot(first);
   const int lane = t & 63, wave = t >> 6;
   if (lane == 0) wave_count[wave] = __popcll(mask);
+  // items, (entry, block with a member) pairs in entry order
+  const int nb = first ? __popc(blkmask) : 0;
+  const uint64_t one = __ballot(nb >= 1), two = __ballot(nb == 2);
+  const uint64_t below = (1ull << lane) - 1ull;
+  int pos_item = __popcll(one & below) + __popcll(two & below);
+  if (lane == 0) wave_items[wave] = __popcll(one) + __popcll(two);
   __syncthreads();
-  int idx = __popcll(mask & ((1ull << lane) - 1ull));
-  for (int w = 0; w < wave; ++w) idx += wave_count[w];
-  if (t == 0) plan->count = wave_count[0] + wave_count[1] + wave_count[2] + wave_count[3];
-  if (!first) return;
-  plan->expert[idx] = e;
-  int m = 0;
-  if (t == routes) {
-    for (int r = 0; r < rows; ++r) {
-      plan->row[idx][m] = uint8_t(r);
-      plan->slot[idx][m] = uint8_t(top_k);
-      ++m;
+  int idx = __popcll(mask & below), count = 0, nitems = 0;
+  for (int w = 0; w < NW; ++w) {
+    if (w < wave) {
+      idx += wave_count[w];
+      pos_item += wave_items[w];
     }
-  } else {
-    for (int u = t; u < routes; ++u)
-      if (int(sids[u]) == e) {
-        plan->row[idx][m] = uint8_t(u / top_k);
-        plan->slot[idx][m] = uint8_t(u % top_k);
-        ++m;
-      }
+    count += wave_count[w];
+    nitems += wave_items[w];
   }
-  plan->m[idx] = m;
+  if (t == 0) {
+    plan->count = count;
+    plan->nitems = nitems;
+  }
+  if (first) {
+    entry_of[t] = idx;
+    plan->expert[idx] = routed ? int(e) : -1;
+    plan->m[idx] = cnt;
+    for (int b = 0; b < 2; ++b)
+      if ((blkmask >> b) & 1) plan->item[pos_item++] = uint16_t(2 * idx + b);
+  }
+  if (t == routes)
+    for (int r = 0; r < rows; ++r) {
+      plan->row[idx][r] = uint8_t(r);
+      plan->slot[idx][r] = uint8_t(top_k);
+    }
+  __syncthreads();
+  if (routed) {
+    const int en = entry_of[first_u];
+    plan->row[en][pos] = uint8_t(t / top_k);
+    plan->slot[en][pos] = uint8_t(t % top_k);
+  }
+}
+
+__global__ __launch_bounds__(256) void plan_kernel(const uint32_t* __restrict__ ids, int rows,
+                                                   int top_k, MoePlan* __restrict__ plan) {
+  __shared__ uint32_t sids[kMaxRoutes];
+  const int t = threadIdx.x;
+  if (t < rows * top_k) sids[t] = ids[t];
+  __syncthreads();
+  plan_body<256>(sids, rows, top_k, plan);
+}
+
+// Routing tail (route_kernel's arithmetic, wave r routing row r) and the plan
+// of its routes in one workgroup.
+template <int PER>
+__global__ __launch_bounds__(512) void route_plan_kernel(
+    const uint16_t* __restrict__ logits, int64_t logit_stride,
+    const uint16_t* __restrict__ shared_logit, int64_t shared_stride, int rows, int top_k,
+    uint32_t* __restrict__ ids, uint16_t* __restrict__ scores, uint16_t* __restrict__ factor,
+    MoePlan* __restrict__ plan) {
+  __shared__ uint32_t sids[kMaxRoutes];
+  const int lane = threadIdx.x & 63, row = threadIdx.x >> 6;
+  if (row < rows) {
+    const rt::RouteLane r = rt::route_row<PER>(logits + size_t(row) * logit_stride, top_k);
+    if (lane < top_k) {
+      ids[size_t(row) * top_k + lane] = r.id;
+      scores[size_t(row) * top_k + lane] = r.score;
+      sids[row * top_k + lane] = r.id;
+    }
+    if (lane == 0)
+      factor[row] =
+          f32_to_bf16(sigmoid_bf16(bf16_to_f32(shared_logit[size_t(row) * shared_stride])));
+  }
+  __syncthreads();
+  plan_body<512>(sids, rows, top_k, plan);
 }
 
 struct Bank {
@@ -385,6 +448,30 @@ int moe_route(const uint16_t* logits, int64_t logit_stride, const uint16_t* shar
   case P:                                                                                    \
     hipLaunchKernelGGL(route_kernel<P>, dim3(rows), dim3(64), 0, s, logits, logit_stride,    \
                        shared_logit, shared_stride, experts, top_k, ids, scores, factor);    \
+    break;
+  switch (per) {
+    MX_ROUTE(1) MX_ROUTE(2) MX_ROUTE(4) MX_ROUTE(8) MX_ROUTE(16)
+    default: return MX_EUNSUPPORTED;
+  }
+#undef MX_ROUTE
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+int moe_route_plan(const uint16_t* logits, int64_t logit_stride, const uint16_t* shared_logit,
+                   int64_t shared_stride, int rows, int experts, int top_k, uint32_t* ids,
+                   uint16_t* scores, uint16_t* factor, MoePlan* plan, hipStream_t s) {
+  if (rows > 8) {  // one wave per row: two launches beyond eight rows
+    if (int rc = moe_route(logits, logit_stride, shared_logit, shared_stride, rows, experts,
+                           top_k, ids, scores, factor, s);
+        rc != MX_OK)
+      return rc;
+    return moe_plan(ids, rows, top_k, plan, s);
+  }
+  if (rows < 1) return MX_EINVAL;
+  const int per = experts / 64;
+#define MX_ROUTE(P)                                                                           \
+  case P:                                                                                     \
+    hipLaunchKernelGGL(route_plan_kernel<P>, dim3(1), dim3(512), 0, s, logits, logit_stride,  \
+                       shared_logit, shared_stride, rows, top_k, ids, scores, factor, plan);  \
     break;
   switch (per) {
     MX_ROUTE(1) MX_ROUTE(2) MX_ROUTE(4) MX_ROUTE(8) MX_ROUTE(16)

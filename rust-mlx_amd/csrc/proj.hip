@@ -152,52 +152,80 @@ void proj_m(const QWeight& w, const uint16_t* x, int64_t xs, int m, const ProjEp
 // columns t, t+256, ... in order; xor butterfly per wave; waves summed in order.
 // plane (nullable, rows <= 8): also writes the exact-integer operand plane of
 // y (xq_core.hpp), the hc * hidden values of row blockIdx.y as one K-long row
+template <int K>
 __global__ __launch_bounds__(256) void hc_norm_kernel(const uint16_t* __restrict__ x,
                                                       const uint16_t* __restrict__ scale,
                                                       int hidden, float eps,
                                                       uint16_t* __restrict__ y,
                                                       char* __restrict__ plane) {
+  // K > 0: hidden == 256 K, every value loaded once into registers (thread t
+  // holds columns t, t + 256, ...); K == 0: any hidden, loops over columns
   __shared__ float red[4];
+  extern __shared__ __align__(16) uint16_t ys[];  // the normalised stream (plane only)
   const int s = blockIdx.x;
   const int row = blockIdx.y;
   const int hc = gridDim.x;
+  const int t = threadIdx.x;
   const uint16_t* xr = x + (size_t(row) * hc + s) * hidden;
+  const uint16_t* sc = scale + size_t(s) * hidden;
+  uint16_t* yr = y + (size_t(row) * hc + s) * hidden;
+  float xv[K > 0 ? K : 1], sv[K > 0 ? K : 1];
   float acc = 0.0f;
-  for (int c = threadIdx.x; c < hidden; c += 256) {
-    const float v = bf16_to_f32(xr[c]);
-    acc = acc + v * v;
+  if constexpr (K > 0) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      xv[k] = bf16_to_f32(xr[t + 256 * k]);
+      sv[k] = bf16_to_f32(sc[t + 256 * k]);
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) acc = acc + xv[k] * xv[k];
+  } else {
+    for (int c = t; c < hidden; c += 256) {
+      const float v = bf16_to_f32(xr[c]);
+      acc = acc + v * v;
+    }
   }
   for (int o = 32; o > 0; o >>= 1) acc = acc + __shfl_xor(acc, o, 64);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  if ((t & 63) == 0) red[t >> 6] = acc;
   __syncthreads();
   const float total = ((red[0] + red[1]) + red[2]) + red[3];
   const float inv = 1.0f / __builtin_sqrtf(total / float(hidden) + eps);
-  uint16_t* yr = y + (size_t(row) * hc + s) * hidden;
-  const uint16_t* sc = scale + size_t(s) * hidden;
-  if (!plane) {
-    for (int c = threadIdx.x; c < hidden; c += 256) {
-      const float v = bf16_to_f32(xr[c]);
-      yr[c] = f32_to_bf16((v * inv) * (bf16_to_f32(sc[c]) + 1.0f));
+  if constexpr (K > 0) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const uint16_t o = f32_to_bf16((xv[k] * inv) * (sv[k] + 1.0f));
+      yr[t + 256 * k] = o;
+      if (plane) ys[t + 256 * k] = o;
     }
-    return;
+  } else {
+    for (int c = t; c < hidden; c += 256) {
+      const uint16_t o = f32_to_bf16((bf16_to_f32(xr[c]) * inv) * (bf16_to_f32(sc[c]) + 1.0f));
+      yr[c] = o;
+      if (plane) ys[c] = o;
+    }
   }
+  if (!plane) return;
+  __syncthreads();
   // lane l of wave w takes values 16 (l / 16) .. +15 of group w * 16 + l % 16
-  // (and of every 64th group after it), writes them and their operands
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kb = lane >> 4;
+  // (and of every 64th group after it) and writes their operands
+  const int lane = t & 63, wave = t >> 6, kb = lane >> 4;
   const int ng = hidden / xq::kGroup;
   for (int g0 = wave * 16; g0 < ng; g0 += 64) {
     const int gl = g0 + (lane & 15);
     const bool live = gl < ng;
     float f[16];
+    if (live) {
+      const uint4 a = *reinterpret_cast<const uint4*>(ys + gl * xq::kGroup + 16 * kb);
+      const uint4 b = *reinterpret_cast<const uint4*>(ys + gl * xq::kGroup + 16 * kb + 8);
+      const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      f[i] = 0.0f;
-      if (live) {
-        const int c = gl * xq::kGroup + 16 * kb + i;
-        const uint16_t o = f32_to_bf16((bf16_to_f32(xr[c]) * inv) * (bf16_to_f32(sc[c]) + 1.0f));
-        yr[c] = o;
-        f[i] = bf16_to_f32(o);
+      for (int i = 0; i < 8; ++i) {
+        f[2 * i] = u2f(w[i] << 16);
+        f[2 * i + 1] = u2f(w[i] & 0xffff0000u);
       }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) f[i] = 0.0f;
     }
     xq::digitize_unit(f, row, s * ng + gl, kb, live, plane, hc * ng);
   }
@@ -269,8 +297,22 @@ int proj(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const Pro
 int hc_norm(const uint16_t* x, const uint16_t* scale, int rows, int hc, int hidden, float eps,
             uint16_t* y, hipStream_t s, char* plane) {
   if (plane && (rows > 8 || hidden % xq::kGroup != 0)) return MX_EUNSUPPORTED;
-  hipLaunchKernelGGL(hc_norm_kernel, dim3(hc, rows), dim3(256), 0, s, x, scale, hidden, eps, y,
-                     plane);
+  const int lb = plane ? hidden * 2 : 0;
+  if (hidden == 2048)
+    hipLaunchKernelGGL(hc_norm_kernel<8>, dim3(hc, rows), dim3(256), lb, s, x, scale, hidden, eps,
+                       y, plane);
+  else if (hidden == 4096)
+    hipLaunchKernelGGL(hc_norm_kernel<16>, dim3(hc, rows), dim3(256), lb, s, x, scale, hidden,
+                       eps, y, plane);
+  else if (hidden % 256 == 0 && hidden <= 1024)
+    hipLaunchKernelGGL(hidden == 256 ? hc_norm_kernel<1>
+                                     : hidden == 512 ? hc_norm_kernel<2>
+                                                     : hidden == 768 ? hc_norm_kernel<3>
+                                                                     : hc_norm_kernel<4>,
+                       dim3(hc, rows), dim3(256), lb, s, x, scale, hidden, eps, y, plane);
+  else
+    hipLaunchKernelGGL(hc_norm_kernel<0>, dim3(hc, rows), dim3(256), lb, s, x, scale, hidden, eps,
+                       y, plane);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 

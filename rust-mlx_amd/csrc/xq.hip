@@ -296,40 +296,68 @@ __device__ __forceinline__ QWeight bank_matrix(const QBank& b, int expert, const
 
 // Copies a plane of G groups (xq_core.hpp layout) into LDS: every thread
 // issues all of its loads before its first store.  Ends with a barrier.
-// Expert gate/up + SwiGLU for one plan entry (blockIdx.y) and 128
-// intermediate rows (blockIdx.x).  Every wave is independent: it owns 16
-// intermediate rows, streams their gate rows and then their up rows over the
-// whole depth (load batches kept D deep across both passes, so the memory
-// system streams while the matrix cores and VALUs work), adds each pass's
-// slice sums in order in registers, and writes h[row][slot][i] =
-// bf16(bf16(silu(bf16 g)) * bf16 u) for the member routes (the exact
-// kernels' SwiGLU, moe.hip gate_up_body).  Operands: the plane of x copied
-// into LDS (every row of x by index), or the members staged in order.
-template <int BITS, int SPW, int SRC>
-__global__ __launch_bounds__(512) void xq_gate_up_kernel(
+// Expert gate/up + SwiGLU for 64 intermediate rows (blockIdx.x) of one plan
+// entry and one four-row block of activation rows: with the plane, blockIdx.y
+// is an item of the plan (an entry and a block of rows 4b .. 4b + 3 of x that
+// holds a member; past the items a workgroup returns at once, so the active
+// ones come first in dispatch order); staged, blockIdx.y is the entry and
+// blockIdx.z the block of members 4z .. 4z + 3.  Wave (t, ks) owns the 16
+// intermediate rows of tile t and the depth half ks (2 SPW groups): it
+// streams their gate rows and then their up rows (load batches kept D deep
+// across both passes, so the memory system streams while the matrix cores
+// and VALUs work).  The ks = 1 wave leaves its slice sums in LDS; the ks = 0
+// wave adds its own in order from +0 and then those, in slice order, and
+// writes h[row][slot][i] = bf16(bf16(silu(bf16 g)) * bf16 u) for the block's
+// member routes (the exact kernels' SwiGLU, moe.hip gate_up_body).
+// Operands: the block of the plane of x copied into LDS, or the members
+// staged in order.  FULL: each half is exactly 2 SPW groups and the scales
+// and biases load B at a time (the launcher checks their alignment), so the
+// group loop is straight-line code whose scheduler overlaps one group's
+// operand reads, matrix-core pass and fp64 fold with the next group's.
+constexpr int kGuTiles = 4;  // 16-row tiles per gate/up workgroup (2 waves each)
+
+__host__ __device__ constexpr int gate_up_red_bytes(int spw) { return kGuTiles * 2 * spw * 64 * 8; }
+
+template <int BITS, int SPW, int SRC, bool FULL>
+__global__ __launch_bounds__(128 * kGuTiles) __attribute__((amdgpu_waves_per_eu(4)))
+void xq_gate_up_kernel(
     const uint16_t* __restrict__ x, const char* __restrict__ plane,
     const MoePlan* __restrict__ plan, int top_k, QBank gate, QBank up, QWeight sgate, QWeight sup,
     uint16_t* __restrict__ h, int hs) {
   extern __shared__ __align__(16) char lds[];
   __shared__ int ro[8], so[8];
-  constexpr int NG = 2 * SPW;                       // groups per pass (at most)
+  constexpr int NT = 128 * kGuTiles;
+  constexpr int NG = 2 * SPW;                       // groups per wave and pass (at most)
   constexpr int B = tile_batch<BITS, SPW>();
   constexpr int NBP = NG / B;                       // batches per pass
   constexpr int NB = 2 * NBP;                       // gate pass, then up pass
-  constexpr int D = NB < 3 ? NB : 3;                // batches in flight
-  const int entry = blockIdx.y;
-  if (entry >= plan->count) return;
+  constexpr int D = NB < 2 ? NB : 2;                // batches in flight
+  int entry, blk;
+  if constexpr (SRC == kSrcPlaneLds) {
+    // blockIdx.y: an item of the plan, (entry, block of rows with a member)
+    if (int(blockIdx.y) >= plan->nitems) return;
+    const int item = plan->item[blockIdx.y];
+    entry = item >> 1;
+    blk = item & 1;
+  } else {
+    entry = blockIdx.y;
+    blk = blockIdx.z;
+    if (entry >= plan->count || 4 * blk >= plan->m[entry]) return;
+  }
+  const int M = plan->m[entry];
   const int expert = plan->expert[entry];
   const QWeight gw = bank_matrix(gate, expert, sgate);
   const QWeight uw = bank_matrix(up, expert, sup);
   const int inter = gw.n, hidden = gw.k;
-  const int i0 = blockIdx.x * 128;
+  const int i0 = blockIdx.x * 16 * kGuTiles;
   if (i0 >= inter) return;
-  const int M = plan->m[entry];
   const int lane = threadIdx.x & 63, j = lane & 15, kb = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int t = wave >> 1, ks = wave & 1;
   const int G = hidden / xq::kGroup;
-  const int row = min(i0 + 16 * wave + j, inter - 1);
+  const int gbeg = ks * NG, gend = min(gbeg + NG, G);
+  const int col = i0 + 16 * t + j;
+  const int row = min(col, inter - 1);
   const bool sbv[2] = {xq::sb_vector_ok<B>(gw.scales, gw.biases, G),
                        xq::sb_vector_ok<B>(uw.scales, uw.biases, G)};
   const size_t wpr = size_t(hidden) * BITS / 32;
@@ -339,71 +367,113 @@ __global__ __launch_bounds__(512) void xq_gate_up_kernel(
   xq::Codes<BITS> c[D][B];
   xq::ScaleBias<B> sb[D];
   auto load_batch = [&](int buf, int bi) {
-    const int pass = bi / NBP, g0 = (bi % NBP) * B;
+    const int pass = bi / NBP, g0 = gbeg + (bi % NBP) * B;
+    const int last = max(gend - 1, 0);
 #pragma unroll
-    for (int i = 0; i < B; ++i) xq::load_codes<BITS>(crow[pass], min(g0 + i, G - 1), kb, c[buf][i]);
-    xq::load_scale_bias<B>(srow[pass], brow[pass], g0, G, sbv[pass], sb[buf]);
+    for (int i = 0; i < B; ++i)
+      xq::load_codes<BITS>(crow[pass], min(g0 + i, last), kb, c[buf][i]);
+    if constexpr (FULL)
+      xq::load_scale_bias_vec<B>(srow[pass], brow[pass], g0, sb[buf]);
+    else
+      xq::load_scale_bias<B>(srow[pass], brow[pass], min(g0, last), max(gend, 1), sbv[pass],
+                             sb[buf]);
   };
-  // member rows and slots: loaded before the weights, stored after them, so
-  // no wait for them holds the weight loads back
-  int r8 = 0, s8 = 0;
-  if (threadIdx.x < 8) {
-    r8 = plan->row[entry][threadIdx.x];
-    s8 = plan->slot[entry][threadIdx.x];
-  }
-#pragma unroll
-  for (int d = 0; d < D; ++d) load_batch(d, d);
-  if (threadIdx.x < 8) {
-    ro[threadIdx.x] = r8;
-    so[threadIdx.x] = s8;
-  }
-  int blocks = M > 4 ? 3 : 1;
+  // operand addresses: group g's A operand at ab + g * gstride; Q and Eb of
+  // the lane's activation row at qb[8 g], eb[8 g]
+  const char* ab;
+  const double* qb;
+  const int* eb;
+  int gstride, red_at;
   if constexpr (SRC == kSrcPlaneLds) {
-    xq::dma_plane<512>(lds, plane, G);
-    blocks = 0;
-    for (int m = 0; m < M; ++m) blocks |= ro[m] < 4 ? 1 : 2;
+    // the plane block (from the L2) lands first; the weight batches go out
+    // after it, so the group loop starts when its first batch arrives rather
+    // than after all of them
+    xq::dma_plane_block<NT>(lds, plane, G, blk, blockIdx.x + 7 * blockIdx.y);
+#pragma unroll
+    for (int d = 0; d < D; ++d) load_batch(d, d);
+    ab = lds + lane * 16;
+    gstride = xq::kBlockBytes;
+    qb = reinterpret_cast<const double*>(lds + xq::block_q_offset(G)) + 4 * blk + kb;
+    eb = reinterpret_cast<const int*>(lds + xq::block_e_offset(G)) + 4 * blk + kb;
+    red_at = xq::block_bytes(G);
   } else {
+    // member rows and slots: loaded before the weights, stored after them,
+    // so no wait for them holds the weight loads back
+    int r8 = 0, s8 = 0;
+    if (threadIdx.x < 8) {
+      r8 = plan->row[entry][threadIdx.x];
+      s8 = plan->slot[entry][threadIdx.x];
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) load_batch(d, d);
+    if (threadIdx.x < 8) {
+      ro[threadIdx.x] = r8;
+      so[threadIdx.x] = s8;
+    }
     __syncthreads();
-    xq::stage<512>(lds, MemberRows{x, hidden, 0, ro, so}, M, 0, G);
+    xq::stage<NT>(lds, MemberRows{x, hidden, 0, ro, so}, M, 0, G);
+    ab = lds + blk * xq::kBlockBytes + lane * 16;
+    gstride = xq::kGroupBytes;
+    qb = reinterpret_cast<const double*>(lds + xq::plane_q_offset(G)) + 4 * blk + kb;
+    eb = reinterpret_cast<const int*>(lds + xq::plane_e_offset(G)) + 4 * blk + kb;
+    red_at = xq::stage_bytes(G);
   }
-  const double* qs = reinterpret_cast<const double*>(lds + xq::plane_q_offset(G));
-  const int* es = reinterpret_cast<const int*>(lds + xq::plane_e_offset(G));
-  double acc[2] = {0.0, 0.0}, tot[2][2] = {{0.0, 0.0}, {0.0, 0.0}};
+  // slice sums of the ks = 1 waves: [tile][pass][slice][lane]
+  double* red = reinterpret_cast<double*>(lds + ((red_at + 15) & ~15));
+  double tot[2] = {0.0, 0.0}, acc = 0.0;  // [gate/up]
 #pragma unroll
   for (int bi = 0; bi < NB; ++bi) {
     const int buf = bi % D, pass = bi / NBP;
 #pragma unroll
     for (int i = 0; i < B; ++i) {
-      const int gl = (bi % NBP) * B + i;
-      if (gl < G) {
-        const char* ab = lds + gl * xq::kGroupBytes + lane * 16;
-        xq::group_step<BITS>(*reinterpret_cast<const xq::v4i*>(ab),
-                             *reinterpret_cast<const xq::v4i*>(ab + xq::kBlockBytes), blocks,
-                             xq::b_operand<BITS>(c[buf][i]), qs[gl * 8 + kb], qs[gl * 8 + 4 + kb],
-                             es[gl * 8 + kb], es[gl * 8 + 4 + kb], sb[buf].scale(i),
-                             sb[buf].bias(i), acc);
+      const int gi = (bi % NBP) * B + i, gl = gbeg + gi;
+      if (FULL || gl < gend) {
+        xq::group_step1<BITS>(*reinterpret_cast<const xq::v4i*>(ab + gl * gstride),
+                              xq::b_operand<BITS>(c[buf][i]), qb[gl * 8], eb[gl * 8],
+                              sb[buf].scale(i), sb[buf].bias(i), acc);
         // a slice ends after its second group, or after the last of an odd count
-        if ((gl & 1) || gl + 1 == G) {
-          tot[pass][0] = tot[pass][0] + acc[0];
-          tot[pass][1] = tot[pass][1] + acc[1];
-          acc[0] = 0.0;
-          acc[1] = 0.0;
+        if ((gl & 1) || (!FULL && gl + 1 == G)) {
+          if (ks == 0) {
+            tot[pass] = tot[pass] + acc;
+          } else {
+            red[((t * 2 + pass) * SPW + (gi >> 1)) * 64 + lane] = acc;
+          }
+          acc = 0.0;
+          if constexpr (FULL) {
+            // the slice's total exists here (the empty asm reads it), so its
+            // folds stay within the slice, and the scheduler overlaps the
+            // groups of one slice, no more
+            asm volatile("" : "+v"(tot[pass]));
+            __builtin_amdgcn_sched_barrier(0);
+          }
         }
       }
     }
     if (bi + D < NB) load_batch(buf, bi + D);
   }
-  // lane (kb, j) holds activation rows kb and 4 + kb of column i0 + 16 w + j
+  __syncthreads();
+  if (ks != 0) return;
+  // the second half's slices, in slice order
+  const int s1 = ((G - NG) + 1) / 2;
 #pragma unroll
-  for (int blk = 0; blk < 2; ++blk) {
-    const int xr = 4 * blk + kb;  // row of x (plane) or member index (staged)
+  for (int pass = 0; pass < 2; ++pass)
+    for (int sl = 0; sl < s1 && sl < SPW; ++sl)
+      tot[pass] = tot[pass] + red[((t * 2 + pass) * SPW + sl) * 64 + lane];
+  // lane (kb, j) holds activation row (plane) or member (staged) 4 blk + kb
+  // of column col
+  const int xr = 4 * blk + kb;
+  if (col < inter) {
+    const float gv = round_bf16(float(tot[0]));
+    const float uv = round_bf16(float(tot[1]));
+    const float silu = round_bf16(gv * sigmoid_bf16(gv));
+    const uint16_t out = f32_to_bf16(silu * uv);
     for (int m = 0; m < M; ++m) {
-      const bool hit = SRC == kSrcPlaneLds ? ro[m] == xr : m == xr;
-      if (!hit || i0 + 16 * wave + j >= inter) continue;
-      const float gv = round_bf16(float(tot[0][blk]));
-      const float uv = round_bf16(float(tot[1][blk]));
-      const float silu = round_bf16(gv * sigmoid_bf16(gv));
-      h[(size_t(ro[m]) * (top_k + 1) + so[m]) * hs + i0 + 16 * wave + j] = f32_to_bf16(silu * uv);
+      if constexpr (SRC == kSrcPlaneLds) {
+        const int r = plan->row[entry][m];
+        if (r == xr) h[(size_t(r) * (top_k + 1) + plan->slot[entry][m]) * hs + col] = out;
+      } else {
+        if (m == xr) h[(size_t(ro[m]) * (top_k + 1) + so[m]) * hs + col] = out;
+      }
     }
   }
 }
@@ -647,13 +717,27 @@ template <int BITS, int SPW>
 int launch_gate_up(const uint16_t* x, const char* plane, const MoePlan* plan, int routes,
                    int top_k, const QBank& gate, const QBank& up, const QWeight& sgate,
                    const QWeight& sup, uint16_t* h, int hs, hipStream_t s) {
-  const dim3 grid((hs + 127) / 128, routes);
-  const int lb = xq::stage_bytes(gate.k / xq::kGroup);
-  const auto fn = plane ? xq_gate_up_kernel<BITS, SPW, kSrcPlaneLds>
-                        : xq_gate_up_kernel<BITS, SPW, kSrcStage>;
+  const int gx = (hs + 16 * kGuTiles - 1) / (16 * kGuTiles);
+  // plane: one workgroup row per plan item (at most two per entry); staged:
+  // entries by blocks of members
+  const dim3 grid = plane ? dim3(gx, 2 * routes, 1) : dim3(gx, routes, 2);
+  const int G = gate.k / xq::kGroup;
+  const int lb = ((plane ? xq::block_bytes(G) : xq::stage_bytes(G)) + 15) / 16 * 16 +
+                 gate_up_red_bytes(SPW);
+  // FULL also needs every expert's scale/bias rows on 2B-byte boundaries
+  constexpr int B = tile_batch<BITS, SPW>();
+  const bool full = G == 4 * SPW && xq::sb_vector_ok<B>(gate.scales, gate.biases, G) &&
+                    xq::sb_vector_ok<B>(up.scales, up.biases, G) &&
+                    xq::sb_vector_ok<B>(sgate.scales, sgate.biases, G) &&
+                    xq::sb_vector_ok<B>(sup.scales, sup.biases, G) &&
+                    (size_t(gate.n) * G) % B == 0 && (size_t(up.n) * G) % B == 0;
+  const auto fn = plane ? (full ? xq_gate_up_kernel<BITS, SPW, kSrcPlaneLds, true>
+                                : xq_gate_up_kernel<BITS, SPW, kSrcPlaneLds, false>)
+                        : (full ? xq_gate_up_kernel<BITS, SPW, kSrcStage, true>
+                                : xq_gate_up_kernel<BITS, SPW, kSrcStage, false>);
   MX_TRY_RC(raise_lds(fn, lb));
-  hipLaunchKernelGGL(fn, grid, dim3(512), lb, s, x, plane, plan, top_k, gate, up, sgate, sup, h,
-                     hs);
+  hipLaunchKernelGGL(fn, grid, dim3(128 * kGuTiles), lb, s, x, plane, plan, top_k, gate, up,
+                     sgate, sup, h, hs);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 
@@ -712,7 +796,8 @@ int xq_gate_up(const uint16_t* x, const char* plane, const MoePlan* plan, int ro
     return MX_EUNSUPPORTED;
   const int routes = rows * top_k + 1;
   const int hs = gate.n > sgate.n ? gate.n : sgate.n;
-  const int spw = whole_spw(gate.k);
+  // two waves per tile, each half the depth (rounded up to whole slices)
+  const int spw = whole_spw(gate.k) > 1 ? whole_spw(gate.k) / 2 : 1;
   switch (gate.bits) {
     case 4: MX_SPW_DISPATCH(4, launch_gate_up, x, plane, plan, routes, top_k, gate, up, sgate, sup, h, hs, s)
     case 5: MX_SPW_DISPATCH(5, launch_gate_up, x, plane, plan, routes, top_k, gate, up, sgate, sup, h, hs, s)

@@ -276,6 +276,42 @@ __device__ __forceinline__ void dma_plane(char* lds, const char* __restrict__ pl
   __syncthreads();
 }
 
+// One four-row block of an activation plane in LDS: the A operands of block
+// `blk` of every group (1 KB a group), then Q [g][8], then Eb [g][8] of all
+// eight rows, copied like dma_plane.
+__host__ __device__ constexpr int block_bytes(int ng) { return ng * (kBlockBytes + 8 * 8 + 8 * 4); }
+__host__ __device__ constexpr int block_q_offset(int ng) { return ng * kBlockBytes; }
+__host__ __device__ constexpr int block_e_offset(int ng) { return ng * (kBlockBytes + 64); }
+
+// `rot` (any value) rotates the order of the 1 KB pieces: workgroups that
+// copy the same plane at once start at different places, so their requests
+// spread over the cache channels instead of queueing on the same lines.
+template <int NT>
+__device__ __forceinline__ void dma_plane_block(char* lds, const char* __restrict__ plane, int G,
+                                                int blk, int rot = 0) {
+  const int na = G * (kBlockBytes / 16), n16 = block_bytes(G) / 16;
+  const int pieces = (n16 + 63) / 64;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  rot = rot % pieces;
+  for (int p = wave; p < pieces; p += NT / 64) {
+    int q = p + rot;
+    q = q >= pieces ? q - pieces : q;  // this instruction's 1 KB piece
+    const int i = q * 64 + lane;
+    if (i < n16) {
+      const char* src = i < na ? plane + size_t(i >> 6) * kGroupBytes + blk * kBlockBytes +
+                                     (i & 63) * 16
+                               : plane + plane_q_offset(G) + size_t(i - na) * 16;
+      __builtin_amdgcn_global_load_lds(
+          src,
+          reinterpret_cast<__attribute__((address_space(3))) void*>(
+              reinterpret_cast<uintptr_t>(lds + size_t(q) * 1024)),
+          16, 0, 0);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+}
+
 // Scales and biases of B consecutive groups of one weight row, as bf16 pairs.
 template <int B>
 struct ScaleBias {
@@ -296,6 +332,29 @@ __host__ __device__ __forceinline__ bool sb_vector_ok(const uint16_t* scales,
                                                       const uint16_t* biases, int G) {
   const uintptr_t at = reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(biases);
   return B > 1 && G % B == 0 && (at & uintptr_t(2 * B - 1)) == 0;
+}
+
+// Groups g0 .. g0 + B - 1 of the row's scales and biases with one vector load
+// each: the caller guarantees g0 % B == 0, g0 + B <= G and sb_vector_ok.
+template <int B>
+__device__ __forceinline__ void load_scale_bias_vec(const uint16_t* __restrict__ srow,
+                                                    const uint16_t* __restrict__ brow, int g0,
+                                                    ScaleBias<B>& o) {
+  static_assert(B == 2 || B == 4 || B == 8, "batch");
+  if constexpr (B == 8) {
+    const uint4 sv = *reinterpret_cast<const uint4*>(srow + g0);
+    const uint4 bv = *reinterpret_cast<const uint4*>(brow + g0);
+    o.s[0] = sv.x; o.s[1] = sv.y; o.s[2] = sv.z; o.s[3] = sv.w;
+    o.b[0] = bv.x; o.b[1] = bv.y; o.b[2] = bv.z; o.b[3] = bv.w;
+  } else if constexpr (B == 4) {
+    const uint2 sv = *reinterpret_cast<const uint2*>(srow + g0);
+    const uint2 bv = *reinterpret_cast<const uint2*>(brow + g0);
+    o.s[0] = sv.x; o.s[1] = sv.y;
+    o.b[0] = bv.x; o.b[1] = bv.y;
+  } else {
+    o.s[0] = *reinterpret_cast<const uint32_t*>(srow + g0);
+    o.b[0] = *reinterpret_cast<const uint32_t*>(brow + g0);
+  }
 }
 
 // Groups g0 .. g0 + B - 1 of the row's scales and biases, indices clamped to
@@ -336,10 +395,10 @@ __device__ __forceinline__ void load_scale_bias(const uint16_t* __restrict__ sro
 // (activation rows l / 16 and 4 + l / 16 against tile row l % 16) for the
 // four-row blocks in `blocks` (bit 0: rows 0-3, bit 1: rows 4-7): a, Q and Eb
 // of each block's row, s and b the tile row's scale and bias.
-template <int BITS>
-__device__ __forceinline__ void group_step(const v4i& a0, const v4i& a1, int blocks,
-                                           const v4i& bop, double q0, double q1, int e0, int e1,
-                                           double s, double b, double (&acc)[2]) {
+template <int BITS, int BLK>
+__device__ __forceinline__ void group_step(const v4i& a0, const v4i& a1, const v4i& bop,
+                                           double q0, double q1, int e0, int e1, double s,
+                                           double b, double (&acc)[2]) {
   const v4i zero = {0, 0, 0, 0};
   auto fold = [&](const v4i& d, double q, int e) {
     // P = (D0 + 256 D1) + 65536 (D2 + 256 D3): each pair is exact in int32
@@ -349,8 +408,27 @@ __device__ __forceinline__ void group_step(const v4i& a0, const v4i& a1, int blo
     if constexpr (BITS == 8) p = fma(q, 128.0, p);  // codes entered as q - 128
     return __builtin_amdgcn_ldexp(fma(p, s, q * b), e - 156);
   };
-  if (blocks & 1) acc[0] = acc[0] + fold(mfma(a0, bop, zero), q0, e0);
-  if (blocks & 2) acc[1] = acc[1] + fold(mfma(a1, bop, zero), q1, e1);
+  if constexpr (BLK & 1) acc[0] = acc[0] + fold(mfma(a0, bop, zero), q0, e0);
+  if constexpr (BLK & 2) acc[1] = acc[1] + fold(mfma(a1, bop, zero), q1, e1);
+}
+
+// One group of one four-row block: a, Q and Eb of the lane's activation row
+// of that block, s and b the tile row's scale and bias.
+template <int BITS>
+__device__ __forceinline__ void group_step1(const v4i& a, const v4i& bop, double q, int e,
+                                            double s, double b, double& acc) {
+  double pair[2] = {acc, 0.0};
+  group_step<BITS, 1>(a, a, bop, q, q, e, e, s, b, pair);
+  acc = pair[0];
+}
+
+// The same with the blocks chosen at run time (uniform across the wave).
+template <int BITS>
+__device__ __forceinline__ void group_step(const v4i& a0, const v4i& a1, int blocks,
+                                           const v4i& bop, double q0, double q1, int e0, int e1,
+                                           double s, double b, double (&acc)[2]) {
+  if (blocks & 1) group_step<BITS, 1>(a0, a1, bop, q0, q1, e0, e1, s, b, acc);
+  if (blocks & 2) group_step<BITS, 2>(a0, a1, bop, q0, q1, e0, e1, s, b, acc);
 }
 
 }  // namespace xq
