@@ -305,6 +305,11 @@ def qweight_bytes(n: int, k: int, bits: int, gs: int) -> int:
 
 
 def bench_qmv_config0(mx, args):
+    """Config 0: one affine 4-bit g64 QMV [4096, 2048] x 1 row per step, over
+    rotated weight copies.  Headline: the exact-integer kernel (mx_xq, the
+    engine's exact mode, bit-exact with the oracle's mxo_xq); the fixed-order
+    VALU kernel (mx_qmv, bit-exact with the oracle's mxo_qmv) and the bf16
+    matrix-core kernel (mx_qmm) are timed beside it."""
     n, k, bits, gs, m = 4096, 2048, 4, 64, 1
     wbytes = qweight_bytes(n, k, bits, gs)
     alg_bytes = wbytes + 2 * m * k + 2 * m * n
@@ -313,58 +318,57 @@ def bench_qmv_config0(mx, args):
     ws = [mx.QWeight.random(n, k, bits, gs, seed=100 + 17 * i) for i in range(copies)]
     x = mx.DeviceArray((m, k), np.uint16)
     mx.fill_bf16(x, 101, 1, 1.0, 0.0)
-    y = mx.DeviceArray((m, n), np.uint16)
+    ys = {name: mx.DeviceArray((m, n), np.uint16) for name in ("xq", "qmv", "qmm")}
     stream = C.c_void_p()
     mx.check(mx.lib.mx_stream_create(C.byref(stream)))
     qcs = [w.c() for w in ws]
+    fns = {"xq": mx.lib.mx_xq, "qmv": mx.lib.mx_qmv, "qmm": mx.lib.mx_qmm}
+    per = {}
+    for name, fn in fns.items():
+        y = ys[name]
 
-    def launch(i):
-        mx.check(mx.lib.mx_qmv(C.byref(qcs[i % copies]), x.ptr, m, y.ptr, stream))
+        def launch(i, fn=fn, y=y):
+            mx.check(fn(C.byref(qcs[i % copies]), x.ptr, m, y.ptr, stream))
 
-    for i in range(args.warmup):
-        launch(i)
-    mx.check(mx.lib.mx_stream_sync(stream))
-    e0, e1 = C.c_void_p(), C.c_void_p()
-    mx.check(mx.lib.mx_event_create(C.byref(e0)))
-    mx.check(mx.lib.mx_event_create(C.byref(e1)))
-    mx.check(mx.lib.mx_device_sync())
-    mx.check(mx.lib.mx_event_record(e0, stream))
-    for i in range(args.steps):
-        launch(args.warmup + i)
-    mx.check(mx.lib.mx_event_record(e1, stream))
-    ms = C.c_float()
-    mx.check(mx.lib.mx_event_elapsed_ms(e0, e1, C.byref(ms)))
-    mx.check(mx.lib.mx_device_sync())
-    avg_s = ms.value / 1e3 / args.steps
+        for i in range(args.warmup):
+            launch(i)
+        mx.check(mx.lib.mx_stream_sync(stream))
+        sec = timed_launches(mx, stream, lambda i: launch(args.warmup + i), args.steps)
+        per[name] = {"us": round(sec * 1e6, 3), "gbs": round(alg_bytes / sec / 1e9, 2)}
+        log(f"qmv-config0: {name} {sec * 1e6:.2f} us/launch (events), "
+            f"{alg_bytes / sec / 1e9:.0f} GB/s")
+    avg_s = per["xq"]["us"] * 1e-6
     achieved = alg_bytes / avg_s / 1e9
-    log(f"qmv-config0: {avg_s * 1e6:.2f} us/launch (events)")
     cpu = None
     if not args.no_cpu_baseline:
-        # CPU baseline leg: the oracle checks the last launch bit for bit, then
-        # repeats the same QMV for about 10 s
+        # CPU baseline leg: the oracle checks each kernel's last launch bit for
+        # bit, then repeats the exact-integer QMV for about 10 s
         from oracle import oracle as orc
 
         seed = 100 + 17 * ((args.warmup + args.steps - 1) % copies)
         codes, s, b = orc.random_qweight(n, k, bits, gs, seed=seed)
         xh = x.numpy()
-        if not (y.numpy() == orc.qmv(codes, s, b, k, bits, gs, xh)).all():
-            raise SystemExit("bench: QMV output differs from oracle")
+        if not (ys["xq"].numpy() == orc.f32_to_bf16(orc.xq(codes, s, b, k, bits, xh))).all():
+            raise SystemExit("bench: exact-integer QMV differs from the oracle")
+        if not (ys["qmv"].numpy() == orc.qmv(codes, s, b, k, bits, gs, xh)).all():
+            raise SystemExit("bench: fixed-order QMV differs from the oracle")
         reps, t0 = 0, time.perf_counter()
         while time.perf_counter() - t0 < 10.0:
-            orc.qmv(codes, s, b, k, bits, gs, xh)
+            orc.xq(codes, s, b, k, bits, xh)
             reps += 1
         cpu_dt = (time.perf_counter() - t0) / reps
         cpu = {"value": round(alg_bytes / cpu_dt / 1e9, 3), "unit": "GB/s",
                "cores": orc.num_threads(), "kind": "port",
-               "sample": f"{reps} oracle QMVs of the config-0 matrix in 10s"}
+               "sample": f"{reps} oracle exact-integer QMVs of the config-0 matrix in 10s"}
     return {
         "metric": METRIC, "value": round(achieved, 2), "unit": "GB/s", "ms_per_step": avg_s * 1e3,
-        "dtype": "u4 codes x bf16 -> fp32 acc",
+        "dtype": "u4 codes x bf16 activations on a per-group integer grid -> exact int32 sums, "
+                 "fp64 group combination",
         "config": {"workload": "qmv-config0", "n": n, "k": k, "bits": bits, "group_size": gs,
-                   "rows": m, "mall_rotation_copies": copies},
-        "roofline": {"bound": "hbm", "kernel": "proj/qmv_kernel<4,1>", "achieved": round(achieved, 2),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None},
+                   "rows": m, "mall_rotation_copies": copies, "kernels": per},
+        "roofline": {"bound": "hbm", "kernel": "xq_dense_kernel (mx_xq, exact-integer)",
+                     "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
         "cpu_baseline": cpu,
     }
 
@@ -722,11 +726,14 @@ def bench_mtp_config4(mx, args):
     greedy decoding (depth 0) of the same prompt; each figure is the generate
     call minus the same call stopped after its first token (prompt and drafter
     prefill).  Random weights make drafts rarely right: the acceptance rate is
-    reported, and the tokens must equal plain greedy decoding's."""
+    reported, and the tokens must equal plain greedy decoding's.  Exact mode
+    unless --fast."""
     n_tok, ctx, depth = 256, 4096, 3
     cfg = dict(mx.CONFIG3, mixed_bits=1, mtp=1, max_slots=2,
                max_context=ctx + n_tok + 64)
     eng = mx.Engine(cfg)
+    exact = not args.fast
+    eng.set_flags(exact=exact)
     prompt = np.random.default_rng(4004).integers(0, cfg["vocab"], ctx)
     res = {}
     for d in (0, depth):
@@ -754,7 +761,7 @@ def bench_mtp_config4(mx, args):
                    "rounds": st["rounds"], "drafted": st["drafted"], "accepted": st["accepted"],
                    "ms_per_round": round(dt / max(st["rounds"], 1) * 1e3, 3),
                    "greedy_decode_tok_s": round(n_tok / dt0, 2), "prompt_s": round(t_first, 2),
-                   "tokens_equal_greedy": True},
+                   "tokens_equal_greedy": True, "mode": "exact" if exact else "fast"},
         "roofline": None,
         "cpu_baseline": None,
     }

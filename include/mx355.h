@@ -551,6 +551,46 @@ mx_status mx_engine_decode_forced(mx_engine* e, const int32_t* slots, const uint
                                   uint32_t* ids_out, uint32_t* next);
 mx_status mx_engine_tensor(mx_engine* e, const char* name, void** device_ptr, size_t* bytes);
 
+/* ---- checkpoint loading (§8(f)#3) ------------------------------------------
+ * Tensor dtypes as safetensors names them. */
+#define MX_DT_U32 0
+#define MX_DT_BF16 1
+#define MX_DT_F16 2
+#define MX_DT_F32 3
+/* Writes one checkpoint tensor, named as in an MLX checkpoint of the hybrid
+ * model (the names Weights / HybridModel::load / Mtp::load read:
+ * src/weights.rs:22-99, src/hybrid.rs:56-66, 130-142, 335-352, 529-567,
+ * src/mtp.rs:39-70; an optional "language_model." prefix), into the engine's
+ * matrices: in_proj_qkv / z / a / b fill rows of the fused GDN input
+ * projection, mlp.gate and mlp.shared_expert_gate the router's rows,
+ * input_mix_weight_down and block_inject_weight the hyper-connection's down
+ * rows, q_proj / k_proj / v_proj the attention input rows; conv1d.weight
+ * [channels, taps, 1] is stored as the engine's fp32 [taps, channels].
+ * ".weight" (U32 packed codes), ".scales", ".biases" of a quantised linear
+ * must match the engine's width and group size (MX_EUNSUPPORTED names the
+ * difference); float tensors of any listed dtype are converted (to bf16 with
+ * round-to-nearest-even, or to fp32).  MX_EUNSUPPORTED for modules the
+ * engine does not build (per-layer n-gram embeddings "ple.", the attention
+ * indexer "self_attn.indexer."), MX_EINVAL for unknown names or shapes.  The
+ * engine is created from the checkpoint's config.json first (mx_model_config
+ * field for field); tensors not loaded keep their seeded values. */
+mx_status mx_engine_load_tensor(mx_engine* e, const char* name, int32_t dtype,
+                                const int64_t* shape, int32_t ndim, const void* data,
+                                size_t bytes);
+/* The mapping of mx_engine_load_tensor without an engine or a device: where
+ * `name` goes for configuration `cfg`.  tensor receives the engine tensor's
+ * name (at most cap bytes with the terminator); info[0..7] = kind (0
+ * quantised rows, 1 bf16 vector, 2 fp32 vector, 3 conv weight), part (0
+ * codes, 1 scales, 2 biases), first row, rows, matrix rows n, matrix depth
+ * k, bits, vector length.  Same statuses as mx_engine_load_tensor. */
+mx_status mx_checkpoint_target(const mx_model_config* cfg, const char* name, char* tensor,
+                               size_t cap, int32_t* info);
+/* Every tensor of one .safetensors file through mx_engine_load_tensor (the
+ * file read in order; vision towers and n-gram table row shards skipped, as
+ * the reference's loader does); *loaded = tensors written.  Stops at the
+ * first error. */
+mx_status mx_engine_load_safetensors(mx_engine* e, const char* path, int32_t* loaded);
+
 /* mx_gdn_scan: the delta rule alone, on given inputs — the reference's
  * gdn_kernel::recurrent / recurrent_with_history interface (src/gdn_kernel.rs:7-142):
  * q, k bf16 [groups*t, hk, dk] (already normalised), v bf16 [groups*t, hv, dv],

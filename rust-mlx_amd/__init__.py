@@ -222,6 +222,10 @@ def _load() -> C.CDLL:
         "mx_sched_pending": ([vp], i32),
         "mx_sched_cached": ([vp], i32),
         "mx_engine_tensor": ([vp, C.c_char_p, C.POINTER(vp), C.POINTER(sz)], i32),
+        "mx_engine_load_tensor": ([vp, C.c_char_p, i32, C.POINTER(C.c_int64), i32, vp, sz], i32),
+        "mx_engine_load_safetensors": ([vp, C.c_char_p, C.POINTER(i32)], i32),
+        "mx_checkpoint_target": ([C.POINTER(ModelConfigC), C.c_char_p, C.c_char_p, sz,
+                                  C.POINTER(i32)], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -369,11 +373,68 @@ def sync() -> None:
 
 
 # ---- model configurations (BASELINE configs 3 and 4, and a tiny test model) ----
+MX_DT_U32, MX_DT_BF16, MX_DT_F16, MX_DT_F32 = 0, 1, 2, 3
+
 CONFIG3 = dict(hidden=2048, layers=48, attn_every=4, vocab=151936, hc=4, hc_rank=256, gdn_hk=16,
                gdn_hv=32, gdn_dk=128, gdn_dv=128, conv_k=4, heads=16, kv_heads=2, head_dim=256,
                rotary_dim=64, rope_theta=1e7, rms_eps=1e-6, experts=512, top_k=10, moe_inter=512,
                shared_inter=512, bits=4, down_bits=5, embed_bits=8, head_bits=8, group_size=64,
                mixed_bits=0, max_slots=8, max_context=4096, max_verify=8, seed=20250)
+
+def checkpoint_target(cfg: dict, name: str):
+    """mx_checkpoint_target: (status, engine tensor name, info dict) for an
+    MLX tensor name under configuration cfg, no device needed."""
+    cc = ModelConfigC(**cfg)
+    buf = C.create_string_buffer(256)
+    info = (C.c_int32 * 8)()
+    rc = lib.mx_checkpoint_target(C.byref(cc), name.encode(), buf, 256, info)
+    keys = ("kind", "part", "row0", "rows", "n", "k", "bits", "count")
+    return rc, buf.value.decode(), dict(zip(keys, list(info)))
+
+
+def config_from_mlx(config: dict, max_slots=8, max_context=4096, max_verify=8, seed=1,
+                    mtp=0) -> dict:
+    """Engine configuration of an MLX checkpoint's config.json (the fields
+    HybridConfig reads, src/hybrid.rs; rope defaults as src/qsa.rs:35-40):
+    the layer pattern must repeat k-1 linear-attention layers then one full
+    attention layer; widths come from "quantization" (per-module entries
+    override the default for the expert down, embedding and head)."""
+    t = config.get("text_config", config)
+    q = config.get("quantization") or config.get("quantization_config")
+    if not q:
+        raise ValueError("config.json has no quantization (the engine runs quantised weights)")
+    types = t["layer_types"]
+    n = t["num_hidden_layers"]
+    k = types.index("full_attention") + 1
+    if n % k or types != (["linear_attention"] * (k - 1) + ["full_attention"]) * (n // k):
+        raise ValueError("layer pattern is not (k-1 linear attention, 1 full attention) repeated")
+
+    def bits_of(*prefixes):
+        for p in prefixes:
+            if isinstance(q.get(p), dict):
+                return q[p]["bits"]
+        return q["bits"]
+
+    rope = t.get("rope_parameters") or {}
+    head_dim = t["head_dim"]
+    return dict(
+        hidden=t["hidden_size"], layers=n, attn_every=k, vocab=t["vocab_size"], hc=t["hc_count"],
+        hc_rank=t["hc_lowrank"], gdn_hk=t["linear_num_key_heads"], gdn_hv=t["linear_num_value_heads"],
+        gdn_dk=t["linear_key_head_dim"], gdn_dv=t["linear_value_head_dim"],
+        conv_k=t["linear_conv_kernel_dim"], heads=t["num_attention_heads"],
+        kv_heads=t["num_key_value_heads"], head_dim=head_dim,
+        rotary_dim=int(head_dim * rope.get("partial_rotary_factor", 0.25)),
+        rope_theta=float(rope.get("rope_theta", 1e7)), rms_eps=t["rms_norm_eps"],
+        experts=t["num_experts"], top_k=t["num_experts_per_tok"],
+        moe_inter=t["moe_intermediate_size"], shared_inter=t["shared_expert_intermediate_size"],
+        bits=q["bits"],
+        down_bits=bits_of("language_model.model.layers.0.mlp.switch_mlp.down_proj",
+                          "model.layers.0.mlp.switch_mlp.down_proj"),
+        embed_bits=bits_of("language_model.model.embed_tokens", "model.embed_tokens"),
+        head_bits=bits_of("language_model.lm_head", "lm_head"),
+        group_size=q["group_size"], mixed_bits=0, max_slots=max_slots, max_context=max_context,
+        max_verify=max_verify, seed=seed, mtp=mtp)
+
 
 TINY = dict(hidden=256, layers=4, attn_every=4, vocab=1024, hc=4, hc_rank=64, gdn_hk=1, gdn_hv=2,
             gdn_dk=128, gdn_dv=128, conv_k=4, heads=2, kv_heads=1, head_dim=128, rotary_dim=32,
@@ -520,6 +581,27 @@ class Engine:
     def tensor_bytes(self, name: str) -> int:
         p, n = C.c_void_p(), C.c_size_t()
         check(lib.mx_engine_tensor(self.h, name.encode(), C.byref(p), C.byref(n)))
+        return n.value
+
+    # numpy dtype of a checkpoint array -> MX_DT_*; uint16 arrays carry bf16 bits
+    _DT = {np.dtype(np.uint32): MX_DT_U32, np.dtype(np.uint16): MX_DT_BF16,
+           np.dtype(np.float16): MX_DT_F16, np.dtype(np.float32): MX_DT_F32}
+
+    def load_tensor(self, name: str, array: np.ndarray, raise_on_error=True) -> int:
+        """mx_engine_load_tensor of one MLX-named checkpoint array; returns the
+        status (raises on error unless raise_on_error is False)."""
+        a = np.ascontiguousarray(array)
+        shape = (C.c_int64 * a.ndim)(*a.shape)
+        rc = lib.mx_engine_load_tensor(self.h, name.encode(), self._DT[a.dtype], shape, a.ndim,
+                                       a.ctypes.data, a.nbytes)
+        if raise_on_error:
+            check(rc)
+        return rc
+
+    def load_safetensors(self, path: str) -> int:
+        """mx_engine_load_safetensors: every tensor of the file; returns the count."""
+        n = C.c_int32()
+        check(lib.mx_engine_load_safetensors(self.h, os.fspath(path).encode(), C.byref(n)))
         return n.value
 
 

@@ -1,6 +1,7 @@
 // C ABI: argument validation, error reporting and dispatch to the launchers.
 #include <hip/hip_runtime.h>
 
+#include <cstring>
 #include <string>
 
 #include "common.hpp"
@@ -718,6 +719,43 @@ MX_ABI mx_status mx_engine_tensor(mx_engine* e, const char* name, void** device_
   MX_CHECK(engine_tensor(*e->impl, name, device_ptr, bytes) == MX_OK, MX_EINVAL,
            std::string("mx_engine_tensor: unknown tensor ") + name);
   return MX_OK;
+}
+
+MX_ABI mx_status mx_engine_load_tensor(mx_engine* e, const char* name, int32_t dtype,
+                                       const int64_t* shape, int32_t ndim, const void* data,
+                                       size_t bytes) {
+  MX_CHECK(e && name && shape && data, MX_EINVAL, "mx_engine_load_tensor: null pointer");
+  MX_CHECK(dtype >= MX_DT_U32 && dtype <= MX_DT_F32, MX_EINVAL, "mx_engine_load_tensor: bad dtype");
+  std::string err;
+  return engine_status(engine_load_tensor(*e->impl, name, dtype, shape, ndim, data, bytes, &err),
+                       err, "mx_engine_load_tensor");
+}
+
+MX_ABI mx_status mx_checkpoint_target(const mx_model_config* cfg, const char* name, char* tensor,
+                                      size_t cap, int32_t* info) {
+  MX_CHECK(cfg && name && tensor && info && cap > 0, MX_EINVAL,
+           "mx_checkpoint_target: null pointer");
+  CheckpointTarget t;
+  const int rc = checkpoint_target(*cfg, name, &t);
+  if (rc == MX_EUNSUPPORTED)
+    return mx_status(set_error(MX_EUNSUPPORTED, std::string("mx_checkpoint_target: the engine has "
+                                                            "no module for tensor ") + name));
+  MX_CHECK(rc == MX_OK, MX_EINVAL, std::string("mx_checkpoint_target: unknown tensor name ") + name);
+  MX_CHECK(t.tensor.size() < cap, MX_EINVAL, "mx_checkpoint_target: name buffer too small");
+  std::memcpy(tensor, t.tensor.c_str(), t.tensor.size() + 1);
+  const int32_t v[8] = {int32_t(t.kind), t.part, t.row0, t.rows, t.n, t.k, t.bits,
+                        int32_t(t.count)};
+  std::memcpy(info, v, sizeof(v));
+  return MX_OK;
+}
+
+MX_ABI mx_status mx_engine_load_safetensors(mx_engine* e, const char* path, int32_t* loaded) {
+  MX_CHECK(e && path && loaded, MX_EINVAL, "mx_engine_load_safetensors: null pointer");
+  std::string err;
+  int n = 0;
+  const int rc = engine_load_safetensors(*e->impl, path, &n, &err);
+  *loaded = n;
+  return engine_status(rc, err, "mx_engine_load_safetensors");
 }
 
 MX_ABI mx_status mx_engine_time_experts(mx_engine* e, int32_t rows, mx_expert_timing* out) {

@@ -19,6 +19,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -1385,6 +1386,436 @@ void engine_set_flags(Engine& e, int want_logits, int use_graphs, int exact, int
   }
   e.exact = exact != 0;
   e.exact_parts = exact_parts;
+}
+
+// ---------------------------------------------------------------------------
+// Checkpoint loading: MLX tensor names (the reference's Weights / HybridModel
+// loaders, src/weights.rs:22-99, src/hybrid.rs:56-66, 130-142, 335-352,
+// 529-567, src/mtp.rs:39-70) onto the engine's matrices, several of which fuse
+// reference modules: the GDN input projection is qkv | z | a | b, the router
+// carries the shared-expert gate as its last row, a hyper-connection's down
+// projection carries the block-inject rows after the low-rank rows, and the
+// attention input projection is q_proj (query and gate per head) | k | v.
+namespace {
+
+bool take(std::string& s, const char* prefix) {
+  const size_t n = std::strlen(prefix);
+  if (s.compare(0, n, prefix) != 0) return false;
+  s.erase(0, n);
+  return true;
+}
+
+}  // namespace
+
+// Where one MLX tensor goes, from the model configuration alone: rows
+// [row0, row0 + rows) of the engine matrix `tensor` (its codes, scales or
+// biases), or the whole bf16 / fp32 vector `tensor`, or the GDN conv weight
+// (fp32 [taps][channels] from MLX's [channels][taps][1]).
+int checkpoint_target(const mx_model_config& c, std::string name, CheckpointTarget* t) {
+  using T = CheckpointTarget;
+  auto quant = [&](const std::string& tensor, int n, int k, int bits, int row0, int rows,
+                   const std::string& rest) -> int {
+    t->kind = T::kQuant;
+    t->tensor = tensor;
+    t->n = n;
+    t->k = k;
+    t->bits = bits;
+    t->row0 = row0;
+    t->rows = rows;
+    if (rest == "weight") t->part = 0;
+    else if (rest == "scales") t->part = 1;
+    else if (rest == "biases") t->part = 2;
+    else return MX_EINVAL;
+    return MX_OK;
+  };
+  auto vec = [&](const std::string& tensor, T::Kind kind, size_t count) -> int {
+    t->kind = kind;
+    t->tensor = tensor;
+    t->count = count;
+    return MX_OK;
+  };
+  const int H = c.hidden, hc = c.hc, r = c.hc_rank;
+  const int cd = 2 * c.gdn_hk * c.gdn_dk + c.gdn_hv * c.gdn_dv, vd = c.gdn_hv * c.gdn_dv;
+  const int P = cd + vd + 2 * c.gdn_hv;
+  const int qr = c.heads * 2 * c.head_dim, kv = c.kv_heads * c.head_dim, Q = qr + 2 * kv;
+  auto hcw = [&](const std::string& e, int layer, bool inject, std::string rest) -> int {
+    const int bits = layer_bits(c, layer, 0), nd = r + (inject ? hc : 0);
+    if (rest == "hc_norm.weight") return vec(e + ".scale", T::kBf16, size_t(hc) * H);
+    if (take(rest, "input_mix_weight_down.")) return quant(e + ".down", nd, hc * H, bits, 0, r, rest);
+    if (inject && take(rest, "block_inject_weight.")) return quant(e + ".down", nd, hc * H, bits, r, hc, rest);
+    if (take(rest, "input_mix_weight_up.")) return quant(e + ".up", hc * H, r, bits, 0, hc * H, rest);
+    return int(MX_EINVAL);
+  };
+  auto layer = [&](const std::string& e, int i, bool attn, std::string rest) -> int {
+    const int bits = layer_bits(c, i, 0), db = layer_bits(c, i, 1);
+    if (take(rest, "attn_hyper_connection.")) return hcw(e + ".attn_hc", i, true, rest);
+    if (take(rest, "mlp_hyper_connection.")) return hcw(e + ".mlp_hc", i, true, rest);
+    if (take(rest, "ple.")) return int(MX_EUNSUPPORTED);  // per-layer n-gram embeddings: not built
+    if (!attn && take(rest, "linear_attn.")) {
+      const std::string g = e + ".gdn.in";
+      if (take(rest, "in_proj_qkv.")) return quant(g, P, H, bits, 0, cd, rest);
+      if (take(rest, "in_proj_z.")) return quant(g, P, H, bits, cd, vd, rest);
+      if (take(rest, "in_proj_a.")) return quant(g, P, H, bits, cd + vd, c.gdn_hv, rest);
+      if (take(rest, "in_proj_b.")) return quant(g, P, H, bits, cd + vd + c.gdn_hv, c.gdn_hv, rest);
+      if (take(rest, "out_proj.")) return quant(e + ".gdn.out", H, vd, bits, 0, H, rest);
+      if (rest == "conv1d.weight") {
+        t->conv_ch = cd;
+        t->taps = c.conv_k;
+        return vec(e + ".gdn.conv_w", T::kConvW, size_t(cd) * c.conv_k);
+      }
+      if (rest == "A_log") return vec(e + ".gdn.a_log", T::kF32, size_t(c.gdn_hv));
+      if (rest == "dt_bias") return vec(e + ".gdn.dt_bias", T::kBf16, size_t(c.gdn_hv));
+      if (rest == "norm.weight") return vec(e + ".gdn.norm", T::kBf16, size_t(c.gdn_dv));
+      return int(MX_EINVAL);
+    }
+    if (attn && take(rest, "self_attn.")) {
+      if (take(rest, "indexer.")) return int(MX_EUNSUPPORTED);  // sparse-attention indexer: not built
+      const std::string a = e + ".attn.in";
+      if (take(rest, "q_proj.")) return quant(a, Q, H, bits, 0, qr, rest);
+      if (take(rest, "k_proj.")) return quant(a, Q, H, bits, qr, kv, rest);
+      if (take(rest, "v_proj.")) return quant(a, Q, H, bits, qr + kv, kv, rest);
+      if (take(rest, "o_proj.")) return quant(e + ".attn.out", H, c.heads * c.head_dim, bits, 0, H, rest);
+      if (rest == "q_norm.weight") return vec(e + ".attn.q_norm", T::kBf16, size_t(c.head_dim));
+      if (rest == "k_norm.weight") return vec(e + ".attn.k_norm", T::kBf16, size_t(c.head_dim));
+      return int(MX_EINVAL);
+    }
+    if (take(rest, "mlp.")) {
+      const std::string m = e + ".moe.";
+      const int E = c.experts, I = c.moe_inter, SI = c.shared_inter;
+      if (take(rest, "gate.")) return quant(m + "router", E + 1, H, bits, 0, E, rest);
+      if (take(rest, "shared_expert_gate.")) return quant(m + "router", E + 1, H, bits, E, 1, rest);
+      if (take(rest, "switch_mlp.gate_proj.")) return quant(m + "gate", E * I, H, bits, 0, E * I, rest);
+      if (take(rest, "switch_mlp.up_proj.")) return quant(m + "up", E * I, H, bits, 0, E * I, rest);
+      if (take(rest, "switch_mlp.down_proj.")) return quant(m + "down", E * H, I, db, 0, E * H, rest);
+      if (take(rest, "shared_expert.gate_proj.")) return quant(m + "shared_gate", SI, H, bits, 0, SI, rest);
+      if (take(rest, "shared_expert.up_proj.")) return quant(m + "shared_up", SI, H, bits, 0, SI, rest);
+      if (take(rest, "shared_expert.down_proj.")) return quant(m + "shared_down", H, SI, db, 0, H, rest);
+      return int(MX_EINVAL);
+    }
+    return int(MX_EINVAL);
+  };
+  take(name, "language_model.");
+  if (take(name, "model.embed_tokens.")) return quant("embed", c.vocab, H, c.embed_bits, 0, c.vocab, name);
+  if (take(name, "lm_head.")) return quant("head", c.vocab, H, c.head_bits, 0, c.vocab, name);
+  if (take(name, "model.hyper_connection_mixer.")) return hcw("mixer", -1, false, name);
+  if (take(name, "model.layers.")) {
+    const size_t dot = name.find('.');
+    if (dot == std::string::npos || dot == 0) return MX_EINVAL;
+    const int i = std::atoi(name.substr(0, dot).c_str());
+    if (i < 0 || i >= c.layers) return MX_EINVAL;
+    const bool attn = i % c.attn_every == c.attn_every - 1;
+    return layer("layers." + std::to_string(i), i, attn, name.substr(dot + 1));
+  }
+  if (take(name, "mtp.")) {
+    if (!c.mtp) return MX_EUNSUPPORTED;  // configuration without the draft layer
+    const int m = c.layers, bits = layer_bits(c, m, 0);
+    if (take(name, "layers.0.")) return layer("mtp.layer", m, true, name);
+    if (name == "pre_fc_norm_embedding.weight") return vec("mtp.norm_emb", T::kBf16, size_t(H));
+    if (name == "pre_fc_norm_hidden.weight") return vec("mtp.norm_hidden", T::kBf16, size_t(hc) * H);
+    if (take(name, "fc_embedding.")) return quant("mtp.fc_emb", H, H, bits, 0, H, name);
+    if (take(name, "fc_hidden.")) return quant("mtp.fc_hidden", H, H, bits, 0, H, name);
+    if (take(name, "hyper_connection_mixer.")) return hcw("mtp.mixer", m, false, name);
+    return MX_EINVAL;
+  }
+  return MX_EINVAL;
+}
+
+namespace {
+
+float load_value(const void* data, int dtype, size_t i) {
+  switch (dtype) {
+    case MX_DT_BF16: return bf16_to_f32(static_cast<const uint16_t*>(data)[i]);
+    case MX_DT_F16: {
+      _Float16 h;
+      std::memcpy(&h, static_cast<const uint16_t*>(data) + i, 2);
+      return float(h);
+    }
+    default: return static_cast<const float*>(data)[i];
+  }
+}
+
+bool float_dtype(int dtype) { return dtype == MX_DT_BF16 || dtype == MX_DT_F16 || dtype == MX_DT_F32; }
+
+int copy_bf16(const void* data, int dtype, size_t count, uint16_t* dst) {
+  std::vector<uint16_t> v(count);
+  for (size_t i = 0; i < count; ++i)
+    v[i] = dtype == MX_DT_BF16 ? static_cast<const uint16_t*>(data)[i]
+                               : f32_to_bf16(load_value(data, dtype, i));
+  return hipMemcpy(dst, v.data(), count * 2, hipMemcpyHostToDevice) == hipSuccess ? MX_OK : MX_EHIP;
+}
+
+}  // namespace
+
+int engine_load_tensor(Engine& e, const char* name, int dtype, const int64_t* shape, int ndim,
+                       const void* data, size_t bytes, std::string* err) {
+  CheckpointTarget t;
+  const int rc = checkpoint_target(e.cfg, name, &t);
+  if (rc == MX_EUNSUPPORTED) {
+    *err = std::string("the engine has no module for tensor ") + name;
+    return MX_EUNSUPPORTED;
+  }
+  if (rc != MX_OK) {
+    *err = std::string("unknown tensor name ") + name;
+    return MX_EINVAL;
+  }
+  if (ndim < 1 || ndim > 4) {
+    *err = std::string(name) + ": bad rank";
+    return MX_EINVAL;
+  }
+  size_t count = 1;
+  for (int i = 0; i < ndim; ++i) count *= size_t(shape[i]);
+  const size_t esize = dtype == MX_DT_F32 || dtype == MX_DT_U32 ? 4 : 2;
+  if (bytes != count * esize) {
+    *err = std::string(name) + ": byte count does not match shape and dtype";
+    return MX_EINVAL;
+  }
+  auto ptr = [&](const std::string& n) -> void* {
+    auto it = e.tensors.find(n);
+    return it == e.tensors.end() ? nullptr : it->second.p;
+  };
+  if (t.kind != CheckpointTarget::kQuant) {
+    if (!float_dtype(dtype) || count != t.count) {
+      *err = std::string(name) + ": expected " + std::to_string(t.count) + " float values";
+      return MX_EINVAL;
+    }
+    void* dst = ptr(t.tensor);
+    if (!dst) {
+      *err = "engine tensor " + t.tensor + " missing";
+      return MX_EINVAL;
+    }
+    if (t.kind == CheckpointTarget::kBf16)
+      return copy_bf16(data, dtype, count, static_cast<uint16_t*>(dst));
+    std::vector<float> v(count);
+    if (t.kind == CheckpointTarget::kF32) {
+      for (size_t i = 0; i < count; ++i) v[i] = load_value(data, dtype, i);
+    } else {  // MLX conv1d weight [channels, taps, 1] -> [taps][channels]
+      if (shape[0] != t.conv_ch) {
+        *err = std::string(name) + ": conv channels differ from the engine's";
+        return MX_EINVAL;
+      }
+      for (int ch = 0; ch < t.conv_ch; ++ch)
+        for (int j = 0; j < t.taps; ++j)
+          v[size_t(j) * t.conv_ch + ch] = load_value(data, dtype, size_t(ch) * t.taps + j);
+    }
+    return hipMemcpy(dst, v.data(), count * 4, hipMemcpyHostToDevice) == hipSuccess ? MX_OK
+                                                                                  : MX_EHIP;
+  }
+  // quantised matrix rows: leading dims flatten into rows (an expert bank is
+  // [experts, n, width]), the last dim is the packed or per-group width
+  const int64_t width = shape[ndim - 1];
+  const int64_t rows = int64_t(count / size_t(width));
+  if (rows != t.rows) {
+    *err = std::string(name) + ": " + std::to_string(rows) + " rows, the engine's matrix takes " +
+           std::to_string(t.rows);
+    return MX_EINVAL;
+  }
+  const int gs = e.cfg.group_size;
+  const int64_t words = int64_t(t.k) * t.bits / 32, groups = t.k / gs;
+  if (t.part == 0) {
+    if (dtype != MX_DT_U32) {
+      *err = std::string(name) + ": packed codes must be U32 (unquantised matrices are not supported)";
+      return MX_EUNSUPPORTED;
+    }
+    if (width != words) {
+      *err = std::string(name) + ": " + std::to_string(width * 32 / t.k) +
+             "-bit codes, the engine's matrix is " + std::to_string(t.bits) + "-bit";
+      return MX_EUNSUPPORTED;
+    }
+    char* dst = static_cast<char*>(ptr(t.tensor + ".codes"));
+    if (!dst) {
+      *err = "engine tensor " + t.tensor + " missing";
+      return MX_EINVAL;
+    }
+    dst += size_t(t.row0) * words * 4;
+    return hipMemcpy(dst, data, bytes, hipMemcpyHostToDevice) == hipSuccess ? MX_OK : MX_EHIP;
+  }
+  if (!float_dtype(dtype) || width != groups) {
+    *err = std::string(name) + ": " + std::to_string(width) +
+           " groups per row, the engine's matrix has " + std::to_string(groups) +
+           " (group size " + std::to_string(gs) + ")";
+    return MX_EUNSUPPORTED;
+  }
+  uint16_t* base = static_cast<uint16_t*>(ptr(t.tensor + (t.part == 1 ? ".scales" : ".biases")));
+  if (!base) {
+    *err = "engine tensor " + t.tensor + " missing";
+    return MX_EINVAL;
+  }
+  return copy_bf16(data, dtype, count, base + size_t(t.row0) * groups);
+}
+
+namespace {
+
+// A minimal JSON reader for safetensors headers: objects of names to
+// {"dtype": str, "shape": [int...], "data_offsets": [int, int]}, plus
+// "__metadata__" (skipped).
+struct JsonIn {
+  const char* p;
+  const char* end;
+  void ws() { while (p < end && (*p == ' ' || *p == '\n' || *p == '\r' || *p == '\t')) ++p; }
+  bool eat(char ch) {
+    ws();
+    if (p < end && *p == ch) { ++p; return true; }
+    return false;
+  }
+  bool str(std::string* out) {
+    ws();
+    if (p >= end || *p != '"') return false;
+    ++p;
+    out->clear();
+    while (p < end && *p != '"') {
+      if (*p == '\\' && p + 1 < end) {
+        ++p;
+        const char ch = *p;
+        out->push_back(ch == 'n' ? '\n' : ch == 't' ? '\t' : ch);
+      } else {
+        out->push_back(*p);
+      }
+      ++p;
+    }
+    if (p >= end) return false;
+    ++p;
+    return true;
+  }
+  bool num(int64_t* v) {
+    ws();
+    char* q = nullptr;
+    *v = std::strtoll(p, &q, 10);
+    if (q == p) return false;
+    p = q;
+    return true;
+  }
+  bool skip() {  // any value
+    ws();
+    if (p >= end) return false;
+    if (*p == '"') { std::string s; return str(&s); }
+    if (*p == '{' || *p == '[') {
+      const char open = *p, close = open == '{' ? '}' : ']';
+      ++p;
+      if (eat(close)) return true;
+      do {
+        if (open == '{') {
+          std::string k;
+          if (!str(&k) || !eat(':')) return false;
+        }
+        if (!skip()) return false;
+      } while (eat(','));
+      return eat(close);
+    }
+    while (p < end && *p != ',' && *p != '}' && *p != ']') ++p;
+    return true;
+  }
+};
+
+struct StEntry {
+  std::string name, dtype;
+  std::vector<int64_t> shape;
+  int64_t begin = 0, end = 0;
+};
+
+bool parse_header(const char* p, size_t n, std::vector<StEntry>* out) {
+  JsonIn in{p, p + n};
+  if (!in.eat('{')) return false;
+  if (in.eat('}')) return true;
+  do {
+    StEntry en;
+    if (!in.str(&en.name) || !in.eat(':')) return false;
+    if (en.name == "__metadata__") {
+      if (!in.skip()) return false;
+      continue;
+    }
+    if (!in.eat('{')) return false;
+    do {
+      std::string key;
+      if (!in.str(&key) || !in.eat(':')) return false;
+      if (key == "dtype") {
+        if (!in.str(&en.dtype)) return false;
+      } else if (key == "shape" || key == "data_offsets") {
+        std::vector<int64_t> v;
+        if (!in.eat('[')) return false;
+        if (!in.eat(']')) {
+          do {
+            int64_t x;
+            if (!in.num(&x)) return false;
+            v.push_back(x);
+          } while (in.eat(','));
+          if (!in.eat(']')) return false;
+        }
+        if (key == "shape") {
+          en.shape = v;
+        } else {
+          if (v.size() != 2) return false;
+          en.begin = v[0];
+          en.end = v[1];
+        }
+      } else if (!in.skip()) {
+        return false;
+      }
+    } while (in.eat(','));
+    if (!in.eat('}')) return false;
+    out->push_back(std::move(en));
+  } while (in.eat(','));
+  return in.eat('}');
+}
+
+}  // namespace
+
+int engine_load_safetensors(Engine& e, const char* path, int* loaded, std::string* err) {
+  *loaded = 0;
+  FILE* f = std::fopen(path, "rb");
+  if (!f) {
+    *err = std::string("cannot open ") + path;
+    return MX_EINVAL;
+  }
+  std::unique_ptr<FILE, int (*)(FILE*)> guard(f, std::fclose);
+  uint64_t hlen = 0;
+  if (std::fread(&hlen, 8, 1, f) != 1 || hlen > (100ull << 20)) {
+    *err = std::string(path) + ": not a safetensors file";
+    return MX_EINVAL;
+  }
+  std::string header(size_t(hlen), '\0');
+  if (std::fread(&header[0], 1, header.size(), f) != header.size()) {
+    *err = std::string(path) + ": truncated header";
+    return MX_EINVAL;
+  }
+  std::vector<StEntry> entries;
+  if (!parse_header(header.data(), header.size(), &entries)) {
+    *err = std::string(path) + ": unreadable header";
+    return MX_EINVAL;
+  }
+  const long base = long(8 + hlen);
+  std::vector<char> buf;
+  for (const StEntry& en : entries) {
+    // the reference's loader skips vision towers and the n-gram tables'
+    // row shards (src/weights.rs:48-54)
+    if (en.name.rfind("visual.", 0) == 0 || en.name.rfind("vision_tower.", 0) == 0 ||
+        en.name.find(".ngram_embedding.shards.") != std::string::npos)
+      continue;
+    int dt;
+    if (en.dtype == "U32") dt = MX_DT_U32;
+    else if (en.dtype == "BF16") dt = MX_DT_BF16;
+    else if (en.dtype == "F16") dt = MX_DT_F16;
+    else if (en.dtype == "F32") dt = MX_DT_F32;
+    else {
+      *err = en.name + ": unsupported dtype " + en.dtype;
+      return MX_EUNSUPPORTED;
+    }
+    const int64_t nbytes = en.end - en.begin;
+    if (nbytes < 0 || en.shape.empty()) {
+      *err = en.name + ": bad offsets or shape";
+      return MX_EINVAL;
+    }
+    buf.resize(size_t(nbytes));
+    if (std::fseek(f, base + long(en.begin), SEEK_SET) != 0 ||
+        std::fread(buf.data(), 1, buf.size(), f) != buf.size()) {
+      *err = en.name + ": truncated data";
+      return MX_EINVAL;
+    }
+    const int rc = engine_load_tensor(e, en.name.c_str(), dt, en.shape.data(), int(en.shape.size()),
+                                      buf.data(), buf.size(), err);
+    if (rc != MX_OK) return rc;
+    ++*loaded;
+  }
+  return MX_OK;
 }
 
 const mx_model_config& engine_config(const Engine& e) { return e.cfg; }

@@ -298,6 +298,21 @@ int engine_generate(Engine& e, int slot, const uint32_t* prompt, int n_prompt, i
                     uint32_t* drafts, std::string* err);
 int engine_read(Engine& e, const char* what, void* host, size_t bytes, std::string* err);
 int engine_tensor(Engine& e, const char* name, void** ptr, size_t* bytes);
+// Where an MLX-named checkpoint tensor goes (engine.cpp): rows [row0, row0 +
+// rows) of the engine matrix `tensor` (n x k at `bits`; part 0 codes, 1
+// scales, 2 biases), or `count` values of a bf16 / fp32 vector, or the GDN
+// conv weight.  MX_EUNSUPPORTED for modules the engine does not build.
+struct CheckpointTarget {
+  enum Kind { kQuant = 0, kBf16 = 1, kF32 = 2, kConvW = 3 } kind = kQuant;
+  std::string tensor;
+  int n = 0, k = 0, bits = 0, row0 = 0, rows = 0, part = 0;
+  size_t count = 0;
+  int conv_ch = 0, taps = 0;
+};
+int checkpoint_target(const mx_model_config& c, std::string name, CheckpointTarget* t);
+int engine_load_tensor(Engine& e, const char* name, int dtype, const int64_t* shape, int ndim,
+                       const void* data, size_t bytes, std::string* err);
+int engine_load_safetensors(Engine& e, const char* path, int* loaded, std::string* err);
 int engine_fill_slot(Engine& e, int slot, int length, uint64_t seed, std::string* err);
 int engine_time_experts(Engine& e, int rows, mx_expert_timing* out, std::string* err);
 int engine_profile_step(Engine& e, const int32_t* slots, const uint32_t* tokens, int rows,
