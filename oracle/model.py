@@ -9,6 +9,12 @@ Every projection is the exact-integer affine projection (oracle/xq.c, the
 engine's int8 matrix-core kernels): weights are viewed with mode XQ.
 Weights are read from the engine under test (fetch(name, dtype, shape)); the
 caches are the oracle's own numpy arrays.
+
+The composition (which stream feeds which projection; injections, gates,
+shared expert, caches, mixer; the draft layer) is checked against the float32
+restatement oracle/hybrid.py -- itself pinned by the reference's end-to-end
+fixture -- on one synthetic MLX checkpoint mapped through
+mx_checkpoint_target (tests/test_oracle_composition.py).
 """
 from __future__ import annotations
 
@@ -292,6 +298,7 @@ class Model:
                             rows, None)
         self.mtp_hidden = h.copy()
         mixed, _ = self._hc_forward(m["mixer"], h, rows)
+        self.last_mixed = mixed
         return orc.head_argmax(self.head, mixed)
 
     def generate(self, slot, prompt, max_tokens, depth=0):

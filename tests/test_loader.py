@@ -1,7 +1,7 @@
 """Checkpoint loading on the CPU, against the reference's own end-to-end
-fixture (tests/fixtures/hybrid: config.json and the safetensors tensor names,
-dtypes and shapes, copied as data into tests/golden/hybrid_fixture_header.json
-by make_hybrid_fixture_header.py):
+fixture (tests/fixtures/hybrid, copied byte for byte into tests/golden/hybrid
+by copy_hybrid_fixture.py: config.json and the safetensors tensor names,
+dtypes and shapes):
   * the engine configuration from config.json (rust_mlx_amd.config_from_mlx);
   * where every fixture tensor goes (mx_checkpoint_target, the mapping that
     mx_engine_load_tensor applies): its shape matches the engine matrix's
@@ -13,6 +13,7 @@ by make_hybrid_fixture_header.py):
     embedding's codes and is refused at load time (codes must be U32)."""
 import json
 import os
+import struct
 from collections import defaultdict
 
 import numpy as np
@@ -23,8 +24,15 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 
 
 def fixture():
-    with open(os.path.join(HERE, "golden", "hybrid_fixture_header.json")) as f:
-        return json.load(f)
+    d = os.path.join(HERE, "golden", "hybrid")
+    with open(os.path.join(d, "config.json")) as f:
+        config = json.load(f)
+    with open(os.path.join(d, "model.safetensors"), "rb") as f:
+        (n,) = struct.unpack("<Q", f.read(8))
+        header = json.loads(f.read(n))
+    header.pop("__metadata__", None)
+    tensors = {k: {"dtype": v["dtype"], "shape": v["shape"]} for k, v in header.items()}
+    return {"config": config, "tensors": tensors}
 
 
 def test_config_from_the_reference_fixture(mx):
