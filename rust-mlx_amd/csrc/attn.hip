@@ -101,7 +101,9 @@ __global__ __launch_bounds__(64) void prep_kernel(const uint16_t* __restrict__ q
 // as four interleaved fma chains over d (d mod 4), then (c0+c1)+(c2+c3).
 // m = max_t s; p = e^(s - m); l = sum_t p (xor butterfly per wave, waves in
 // order).  Values: thread t owns dim t; o = sum_j p_j v_j[t] (fma chain, j
-// ascending).  Writes (m, l) and o (fp32) per (row, head, chunk).
+// ascending).  Writes (m, l) and o (fp32) per (row, head, chunk).  A
+// workgroup takes G of the kv head's q heads (blockIdx.y = kv head * splits +
+// split), so short contexts still spread over many workgroups.
 template <int G>
 __global__ __launch_bounds__(kAttnChunk) void decode_kernel(
     const uint16_t* __restrict__ q, const int32_t* __restrict__ slots,
@@ -112,7 +114,9 @@ __global__ __launch_bounds__(kAttnChunk) void decode_kernel(
   __shared__ float ps[G][kAttnChunk];
   __shared__ float red[G][4];
   const int chunk = blockIdx.x;
-  const int kvh = blockIdx.y;
+  const int splits = d.heads / d.kv_heads / G;
+  const int kvh = blockIdx.y / splits;
+  const int h0 = kvh * (G * splits) + (blockIdx.y - kvh * splits) * G;  // first q head
   const int row = blockIdx.z;
   const int t = threadIdx.x;
   const int n_pos = pos[row] + 1;
@@ -121,30 +125,43 @@ __global__ __launch_bounds__(kAttnChunk) void decode_kernel(
   const int hd = d.head_dim;
   for (int i = t; i < G * hd; i += kAttnChunk) {
     const int g = i / hd, c = i - g * hd;
-    qs[g][c] = bf16_to_f32(q[(size_t(row) * d.heads + kvh * G + g) * hd + c]);
+    qs[g][c] = bf16_to_f32(q[(size_t(row) * d.heads + h0 + g) * hd + c]);
   }
   __syncthreads();
   const size_t base = size_t(slots[row]) * d.slot_stride + size_t(kvh) * d.max_ctx * hd;
   const int j = j0 + t;
   const bool valid = j < n_pos;
   if (valid) {
-    const uint16_t* kr = k_cache + base + size_t(j) * hd;
+    // the row's K pieces are all requested before the first is used (one
+    // memory round trip per 16 pieces, not one per piece); the fma order is
+    // unchanged: chain d mod 4, dims ascending
+    const uint4* kr = reinterpret_cast<const uint4*>(k_cache + base + size_t(j) * hd);
+    const int n8 = hd >> 3;
     float c0[G], c1[G], c2[G], c3[G];
     for (int g = 0; g < G; ++g) c0[g] = c1[g] = c2[g] = c3[g] = 0.0f;
-    for (int c = 0; c < hd; c += 8) {
-      const uint4 raw = *reinterpret_cast<const uint4*>(kr + c);
-      const float kv[8] = {u2f(raw.x << 16), u2f(raw.x & 0xffff0000u), u2f(raw.y << 16),
-                           u2f(raw.y & 0xffff0000u), u2f(raw.z << 16), u2f(raw.z & 0xffff0000u),
-                           u2f(raw.w << 16), u2f(raw.w & 0xffff0000u)};
-      for (int g = 0; g < G; ++g) {
-        c0[g] = fmaf_(qs[g][c + 0], kv[0], c0[g]);
-        c1[g] = fmaf_(qs[g][c + 1], kv[1], c1[g]);
-        c2[g] = fmaf_(qs[g][c + 2], kv[2], c2[g]);
-        c3[g] = fmaf_(qs[g][c + 3], kv[3], c3[g]);
-        c0[g] = fmaf_(qs[g][c + 4], kv[4], c0[g]);
-        c1[g] = fmaf_(qs[g][c + 5], kv[5], c1[g]);
-        c2[g] = fmaf_(qs[g][c + 6], kv[6], c2[g]);
-        c3[g] = fmaf_(qs[g][c + 7], kv[7], c3[g]);
+    for (int b0 = 0; b0 < n8; b0 += 16) {
+      uint4 raw[16];
+#pragma unroll
+      for (int b = 0; b < 16; ++b)
+        if (b0 + b < n8) raw[b] = kr[b0 + b];
+#pragma unroll
+      for (int b = 0; b < 16; ++b) {
+        if (b0 + b >= n8) break;
+        const int c = (b0 + b) * 8;
+        const float kv[8] = {u2f(raw[b].x << 16), u2f(raw[b].x & 0xffff0000u),
+                             u2f(raw[b].y << 16), u2f(raw[b].y & 0xffff0000u),
+                             u2f(raw[b].z << 16), u2f(raw[b].z & 0xffff0000u),
+                             u2f(raw[b].w << 16), u2f(raw[b].w & 0xffff0000u)};
+        for (int g = 0; g < G; ++g) {
+          c0[g] = fmaf_(qs[g][c + 0], kv[0], c0[g]);
+          c1[g] = fmaf_(qs[g][c + 1], kv[1], c1[g]);
+          c2[g] = fmaf_(qs[g][c + 2], kv[2], c2[g]);
+          c3[g] = fmaf_(qs[g][c + 3], kv[3], c3[g]);
+          c0[g] = fmaf_(qs[g][c + 4], kv[4], c0[g]);
+          c1[g] = fmaf_(qs[g][c + 5], kv[5], c1[g]);
+          c2[g] = fmaf_(qs[g][c + 6], kv[6], c2[g]);
+          c3[g] = fmaf_(qs[g][c + 7], kv[7], c3[g]);
+        }
       }
     }
     for (int g = 0; g < G; ++g) ps[g][t] = ((c0[g] + c1[g]) + (c2[g] + c3[g])) * scale;
@@ -183,21 +200,44 @@ __global__ __launch_bounds__(kAttnChunk) void decode_kernel(
     const int g = t;
     float l = red[g][0];
     for (int w = 1; w < kAttnChunk / 64; ++w) l = l + red[g][w];
-    float* ml = ml_part + ((size_t(row) * heads + kvh * G + g) * max_chunks + chunk) * 2;
+    float* ml = ml_part + ((size_t(row) * heads + h0 + g) * max_chunks + chunk) * 2;
     ml[0] = mg[g];
     ml[1] = l;
   }
   if (t < hd) {
+    // values in batches of 32 positions, the next batch requested before the
+    // current one is consumed; per dim one fma chain over j ascending
     const int jend = min(n_pos - j0, kAttnChunk);
     float o[G];
     for (int g = 0; g < G; ++g) o[g] = 0.0f;
     const uint16_t* vr = v_cache + base + size_t(j0) * hd + t;
-    for (int jj = 0; jj < jend; ++jj) {
+    constexpr int PB = 32;
+    uint16_t cur[PB], nxt[PB];
+    const int full = jend / PB;  // whole batches (uniform over the workgroup)
+    if (full > 0) {
+#pragma unroll
+      for (int b = 0; b < PB; ++b) cur[b] = vr[size_t(b) * hd];
+    }
+    for (int i = 0; i < full; ++i) {
+      const int jj = i * PB;
+      if (i + 1 < full) {
+#pragma unroll
+        for (int b = 0; b < PB; ++b) nxt[b] = vr[size_t(jj + PB + b) * hd];
+      }
+#pragma unroll
+      for (int b = 0; b < PB; ++b) {
+        const float v = bf16_to_f32(cur[b]);
+        for (int g = 0; g < G; ++g) o[g] = fmaf_(ps[g][jj + b], v, o[g]);
+      }
+#pragma unroll
+      for (int b = 0; b < PB; ++b) cur[b] = nxt[b];
+    }
+    for (int jj = full * PB; jj < jend; ++jj) {
       const float v = bf16_to_f32(vr[size_t(jj) * hd]);
       for (int g = 0; g < G; ++g) o[g] = fmaf_(ps[g][jj], v, o[g]);
     }
     for (int g = 0; g < G; ++g)
-      o_part[((size_t(row) * heads + kvh * G + g) * max_chunks + chunk) * hd + t] = o[g];
+      o_part[((size_t(row) * heads + h0 + g) * max_chunks + chunk) * hd + t] = o[g];
   }
 }
 
@@ -476,17 +516,16 @@ int attn_decode(const uint16_t* q, int rows, const int32_t* slots, const int32_t
   }
   const int chunks = (d.max_ctx + kAttnChunk - 1) / kAttnChunk;
   if (chunks > max_chunks) return MX_EINVAL;
-  const dim3 grid(chunks, d.kv_heads, rows);
-#define MX_DEC(GG)                                                                         \
-  case GG:                                                                                 \
-    hipLaunchKernelGGL(decode_kernel<GG>, grid, dim3(kAttnChunk), 0, s, q, slots, pos,     \
-                       k_cache, v_cache, d, max_chunks, scale, o_part, ml_part);           \
-    break;
-  switch (d.heads / d.kv_heads) {
-    MX_DEC(1) MX_DEC(2) MX_DEC(4) MX_DEC(8) MX_DEC(16)
-    default: return MX_EUNSUPPORTED;
-  }
-#undef MX_DEC
+  // two q heads per workgroup (one when the kv head has one)
+  const int grp = d.heads / d.kv_heads;
+  if (grp != 1 && grp != 2 && grp != 4 && grp != 8 && grp != 16) return MX_EUNSUPPORTED;
+  const dim3 grid(chunks, d.kv_heads * (grp == 1 ? 1 : grp / 2), rows);
+  if (grp == 1)
+    hipLaunchKernelGGL(decode_kernel<1>, grid, dim3(kAttnChunk), 0, s, q, slots, pos, k_cache,
+                       v_cache, d, max_chunks, scale, o_part, ml_part);
+  else
+    hipLaunchKernelGGL(decode_kernel<2>, grid, dim3(kAttnChunk), 0, s, q, slots, pos, k_cache,
+                       v_cache, d, max_chunks, scale, o_part, ml_part);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 

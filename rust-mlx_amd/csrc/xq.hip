@@ -167,6 +167,28 @@ __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
   const double* qs = reinterpret_cast<const double*>(src + xq::plane_q_offset(G));
   const int* es = reinterpret_cast<const int*>(src + xq::plane_e_offset(G));
   double acc[2] = {0.0, 0.0}, tot[2] = {0.0, 0.0}, ss[KS > 1 ? SPW : 1][2];
+  // A plane read in place: each group's operands are requested PD groups
+  // ahead of their use, so the wave waits for memory once, not per group.
+  constexpr int PD = SRC == kSrcPlane ? (NG < 4 ? NG : 4) : 1;
+  struct PlaneOp {
+    xq::v4i a0, a1;
+    double q0, q1;
+    int e0, e1;
+  } pf[PD];
+  auto load_op = [&](int gl, PlaneOp& o) {
+    const int g = min(gbeg + gl, gend - 1);
+    const char* ab = src + g * xq::kGroupBytes + lane * 16;
+    o.a0 = *reinterpret_cast<const xq::v4i*>(ab);
+    o.a1 = *reinterpret_cast<const xq::v4i*>(ab + xq::kBlockBytes);
+    o.q0 = qs[g * 8 + kb];
+    o.q1 = qs[g * 8 + 4 + kb];
+    o.e0 = es[g * 8 + kb];
+    o.e1 = es[g * 8 + 4 + kb];
+  };
+  if constexpr (SRC == kSrcPlane) {
+#pragma unroll
+    for (int i = 0; i < PD; ++i) load_op(i, pf[i]);
+  }
 #pragma unroll
   for (int bi = 0; bi < NB; ++bi) {
     const int buf = bi & 1;
@@ -177,7 +199,15 @@ __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
         xq::v4i a0, a1;
         double q0 = 0.0, q1 = 0.0;
         int e0 = 1, e1 = 1;
-        if constexpr (SRC == kSrcReg) {
+        if constexpr (SRC == kSrcPlane) {
+          const PlaneOp& o = pf[gl % PD];
+          a0 = o.a0;
+          a1 = o.a1;
+          q0 = o.q0;
+          q1 = o.q1;
+          e0 = o.e0;
+          e1 = o.e1;
+        } else if constexpr (SRC == kSrcReg) {
           a0 = reg_operand(xr, M, 0, g, q0, e0);
           a1 = (blocks & 2) ? reg_operand(xr, M, 1, g, q1, e1) : a0;
           // this lane receives activation row kb of each block: the Q and Eb
@@ -197,6 +227,9 @@ __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
         }
         xq::group_step<BITS>(a0, a1, blocks, xq::b_operand<BITS>(c[buf][i]), q0, q1, e0, e1,
                              sb[buf].scale(i), sb[buf].bias(i), acc);
+        if constexpr (SRC == kSrcPlane) {
+          if (gl + PD < NG) load_op(gl + PD, pf[gl % PD]);
+        }
         // a slice ends after its second group, or after the last group of an
         // odd count
         if ((gl & 1) || g + 1 == gend) {
