@@ -24,6 +24,8 @@ struct ProjFinish {
   // kConv with one output per thread: the thread's slot is read before the
   // weight stream, its window and conv weights right after it
   static constexpr bool kConvPre = MODE == kConv && 8 * NC <= NT;
+  // activation rows this workgroup writes: [m_lo, min(m_hi, M))
+  int m_lo = 0, m_hi = 8;
   int cm = 0, cr = 0, cslot = 0;
   bool conv_item = false;
   uint16_t cwin[kConvMaxTaps - 1] = {};
@@ -45,7 +47,7 @@ struct ProjFinish {
     if constexpr (kConvPre) {
       cm = threadIdx.x / NC;
       cr = tg * NC + threadIdx.x % NC;
-      conv_item = cm < M && cr < min(n, e.conv_ch);
+      conv_item = cm >= m_lo && cm < min(M, m_hi) && cr < min(n, e.conv_ch);
       if (conv_item) cslot = e.slots[cm];
     }
   }
@@ -64,7 +66,7 @@ struct ProjFinish {
       if (threadIdx.x >= 128) return;
       const int m = threadIdx.x >> 4, cj = threadIdx.x & 15;
       const int c = tg * 16 + cj;
-      if (m >= M || c >= e.hidden) return;
+      if (m < m_lo || m >= min(M, m_hi) || c >= e.hidden) return;
       float sum = 0.0f;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
@@ -77,7 +79,7 @@ struct ProjFinish {
       for (int i = threadIdx.x; i < 8 * NC; i += NT) {
         const int m = i / NC, c = i - m * NC;
         const int r = tg * NC + c;
-        if (m >= M || r >= n) continue;
+        if (m < m_lo || m >= min(M, m_hi) || r >= n) continue;
         const uint16_t xb = f32_to_bf16(yt[i]);
         if (r >= e.conv_ch) {
           e.y[size_t(m) * e.y_stride + r] = xb;
@@ -115,7 +117,7 @@ struct ProjFinish {
         const int s = i / (8 * NC), mc = i - s * (8 * NC);
         const int m = mc / NC, c = mc - m * NC;
         const int r = tg * NC + c;
-        if (m >= M || r >= n) continue;
+        if (m < m_lo || m >= min(M, m_hi) || r >= n) continue;
         const float vb = round_bf16(yt[mc]);
         uint16_t* res = e.y + size_t(m) * e.y_stride + size_t(s) * n + r;
         const float inj = round_bf16(vb * bf16_to_f32(e.aux[size_t(m) * e.aux_stride + s]));
@@ -125,7 +127,7 @@ struct ProjFinish {
       for (int i = threadIdx.x; i < 8 * NC; i += NT) {
         const int m = i / NC, c = i - m * NC;
         const int r = tg * NC + c;
-        if (m >= M || r >= n) continue;
+        if (m < m_lo || m >= min(M, m_hi) || r >= n) continue;
         const float v = yt[i];
         if constexpr (MODE == kPlain) {
           e.y[size_t(m) * e.y_stride + r] = f32_to_bf16(v);

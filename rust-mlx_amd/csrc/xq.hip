@@ -93,6 +93,7 @@ enum : int {
   kSrcReg = 1,       // built by each wave in registers (deep rows, no plane)
   kSrcPlane = 2,     // read by each wave from the producer's plane in global memory
   kSrcPlaneLds = 3,  // the producer's plane copied once per workgroup into LDS
+  kSrcBlockLds = 4,  // one four-row block of the plane copied into LDS (blockIdx.y)
 };
 
 template <int BITS>
@@ -115,7 +116,9 @@ __device__ __forceinline__ bool tiles_sbv(const QWeight& w) {
 // LDS bytes of xq_tiles: the staged or copied operands of G groups, and the
 // slice sums of T tiles when KS > 1 (they reuse the operand area).
 __host__ __device__ constexpr int tiles_lds(int G, int T, int KS, int SRC) {
-  const int ops = (SRC == kSrcStage || SRC == kSrcPlaneLds) ? xq::stage_bytes(G) : 0;
+  const int ops = (SRC == kSrcStage || SRC == kSrcPlaneLds) ? xq::stage_bytes(G)
+                  : SRC == kSrcBlockLds                       ? xq::block_bytes(G)
+                                                              : 0;
   const int sums = KS > 1 ? ((G + 1) / 2) * T * 8 * 16 * 8 : 0;
   const int b = ops > sums ? ops : sums;
   return b > 16 ? b : 16;
@@ -161,11 +164,16 @@ __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
     xq::stage<NT>(lds, xr, M, 0, G);
   } else if constexpr (SRC == kSrcPlaneLds) {
     xq::dma_plane<NT>(lds, plane, G);
+  } else if constexpr (SRC == kSrcBlockLds) {
+    xq::dma_plane_block<NT>(lds, plane, G, blocks >> 1);
   } else if constexpr (SRC == kSrcPlane) {
     src = plane;
   }
-  const double* qs = reinterpret_cast<const double*>(src + xq::plane_q_offset(G));
-  const int* es = reinterpret_cast<const int*>(src + xq::plane_e_offset(G));
+  const double* qs = reinterpret_cast<const double*>(
+      src + (SRC == kSrcBlockLds ? xq::block_q_offset(G) : xq::plane_q_offset(G)));
+  const int* es = reinterpret_cast<const int*>(
+      src + (SRC == kSrcBlockLds ? xq::block_e_offset(G) : xq::plane_e_offset(G)));
+  const int bq = 4 * (blocks >> 1) + kb;  // kSrcBlockLds: the lane's activation row
   double acc[2] = {0.0, 0.0}, tot[2] = {0.0, 0.0}, ss[KS > 1 ? SPW : 1][2];
   // A plane read in place: each group's operands are requested PD groups
   // ahead of their use, so the wave waits for memory once, not per group.
@@ -207,6 +215,12 @@ __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
           q1 = o.q1;
           e0 = o.e0;
           e1 = o.e1;
+        } else if constexpr (SRC == kSrcBlockLds) {
+          // one block: its operand feeds the accumulator of that block
+          a0 = *reinterpret_cast<const xq::v4i*>(src + g * xq::kBlockBytes + lane * 16);
+          a1 = a0;
+          q0 = q1 = qs[g * 8 + bq];
+          e0 = e1 = es[g * 8 + bq];
         } else if constexpr (SRC == kSrcReg) {
           a0 = reg_operand(xr, M, 0, g, q0, e0);
           a1 = (blocks & 2) ? reg_operand(xr, M, 1, g, q1, e1) : a0;
@@ -248,12 +262,12 @@ __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
     if (bi + 2 < NB) load_batch(buf, bi + 2);
   }
   if constexpr (KS == 1) {
-    if constexpr (SRC == kSrcStage || SRC == kSrcPlaneLds) __syncthreads();
+    if constexpr (SRC == kSrcStage || SRC == kSrcPlaneLds || SRC == kSrcBlockLds) __syncthreads();
     yt[kb * NC + t * 16 + j] = float(tot[0]);
     yt[(4 + kb) * NC + t * 16 + j] = float(tot[1]);
   } else {
     // slice sums in slice order, from +0, then one rounding to fp32
-    if constexpr (SRC == kSrcStage || SRC == kSrcPlaneLds) __syncthreads();
+    if constexpr (SRC == kSrcStage || SRC == kSrcPlaneLds || SRC == kSrcBlockLds) __syncthreads();
     double* red = reinterpret_cast<double*>(lds);
 #pragma unroll
     for (int sl = 0; sl < SPW; ++sl) {
@@ -297,10 +311,17 @@ __global__ __launch_bounds__(64 * T * KS) void xq_dense_kernel(QWeight w,
   else
     row = min(tg * NC + t * 16 + j, n - 1);
   ProjFinish<MODE, NC, NT> fin;
+  int blocks = M > 4 ? 3 : 1;
+  if constexpr (SRC == kSrcBlockLds) {
+    // this workgroup's four activation rows: block blockIdx.y
+    blocks = 1 << blockIdx.y;
+    fin.m_lo = 4 * blockIdx.y;
+    fin.m_hi = fin.m_lo + 4;
+  }
   fin.begin(e, tg, M, n);
   xq_tiles<BITS, T, KS, SPW, SRC>(w.codes + size_t(row) * (size_t(w.k) * BITS / 32),
                                   w.scales + size_t(row) * G, w.biases + size_t(row) * G,
-                                  tiles_sbv<BITS, SPW>(w), w.k, M, M > 4 ? 3 : 1,
+                                  tiles_sbv<BITS, SPW>(w), w.k, M, blocks,
                                   XRows{x, x_stride}, plane, lds, yt,
                                   [&] { fin.prefetch(e); });
   fin.finish(yt, e, tg, M, n);
@@ -676,7 +697,8 @@ int launch_xq(const QWeight& w, const uint16_t* x, int64_t xs, int m, const char
   const int lb = tiles_lds(w.k / xq::kGroup, T, KS, SRC);
   const auto fn = xq_dense_kernel<BITS, MODE, T, KS, SPW, SRC>;
   MX_TRY_RC(raise_lds(fn, lb));
-  hipLaunchKernelGGL(fn, dim3(groups), dim3(64 * T * KS), lb, s, w, x, xs, m, plane, e);
+  const int nblk = SRC == kSrcBlockLds && m > 4 ? 2 : 1;
+  hipLaunchKernelGGL(fn, dim3(groups, nblk), dim3(64 * T * KS), lb, s, w, x, xs, m, plane, e);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 
@@ -716,7 +738,8 @@ int xq_shape(const QWeight& w, const uint16_t* x, int64_t xs, int m, const char*
       MX_XQ(1, 8, 4, kSrcStage);
     }
     if (S == 64) {
-      if (plane) MX_XQ(1, 16, 4, kSrcPlane);
+      // each workgroup copies one block of the plane (about 140 KB) into LDS
+      if (plane) MX_XQ(1, 16, 4, kSrcBlockLds);
       MX_XQ(1, 16, 4, kSrcReg);
     }
   }
