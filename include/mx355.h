@@ -194,11 +194,12 @@ mx_status mx_qmm(const mx_qweight* w, const uint16_t* x, int32_t m, uint16_t* y,
  * exponent (X = trunc(x 2^(156 - Eb)), |X| < 2^30), P = sum X q and
  * Q = sum X are exact integer sums (signed int8 digits of X against the
  * codes on v_mfma_i32_16x16x64_i8), v = fma(P, s, Q b) 2^(Eb - 156) in fp64,
- * groups added in fp64 in order within fixed slices of eight groups (one
- * slice below k = 1024), slices in order, one rounding to fp32, then bf16.
- * Bit-exact with the CPU oracle (oracle/xq.c); no result depends on the
- * number of rows or the launch shape.  1 <= m <= 8, group_size 64, k a
- * multiple of 64 up to 512 or of 512 up to 8192.  The product path of the
+ * groups added in fp64 in order within slices of two consecutive groups
+ * (the last slice of an odd count holds one), the slice sums in order, one
+ * rounding to fp32, then bf16.  Bit-exact with the CPU oracle (oracle/xq.c);
+ * no result depends on the number of rows or the launch shape.  1 <= m <= 8,
+ * group_size 64, k a multiple of 64 up to 512, or 1024, 2048, 4096, 8192.
+ * The product path of the
  * decode engine's exact mode.  Replaces the same reference interfaces as
  * mx_qmv (src/qmv_kernel.rs:49-180, kernels/verify_qmv.{h,metal}: the
  * affine formula of verify_qmv.h:112). */
