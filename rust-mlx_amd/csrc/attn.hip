@@ -18,6 +18,7 @@
 #include "common.hpp"
 #include "kernels.hpp"
 #include "skinny_core.hpp"
+#include "xq_core.hpp"
 
 namespace mx {
 
@@ -393,12 +394,14 @@ __global__ __launch_bounds__(kMaxHd) void combine_kernel(const float* __restrict
                                                          const int32_t* __restrict__ pos,
                                                          AttnDims d, int max_chunks,
                                                          int chunk,
-                                                         uint16_t* __restrict__ out) {
+                                                         uint16_t* __restrict__ out,
+                                                         char* __restrict__ plane) {
+  __shared__ __align__(16) uint16_t ob[kMaxHd];  // the head's output row (plane only)
   const int h = blockIdx.x;
   const int row = blockIdx.y;
   const int t = threadIdx.x;
   const int hd = d.head_dim;
-  if (t >= hd) return;
+  if (t < hd) {
   const int chunks = (pos[row] + chunk) / chunk;
   const float* ml = ml_part + (size_t(row) * d.heads + h) * max_chunks * 2;
   const float* op = o_part + (size_t(row) * d.heads + h) * max_chunks * hd + t;
@@ -412,7 +415,22 @@ __global__ __launch_bounds__(kMaxHd) void combine_kernel(const float* __restrict
   }
   const float attn = round_bf16(O / L);
   const float gate = bf16_to_f32(qkv[size_t(row) * qkv_stride + size_t(h) * 2 * hd + hd + t]);
-  out[(size_t(row) * d.heads + h) * hd + t] = f32_to_bf16(attn * sigmoid_bf16(gate));
+  const uint16_t o = f32_to_bf16(attn * sigmoid_bf16(gate));
+  out[(size_t(row) * d.heads + h) * hd + t] = o;
+  ob[t] = o;
+  }
+  if (!plane) return;
+  // the head's hd / 64 groups of this row, digitised by wave 0 (lanes
+  // 16 kb + gl, gl < hd / 64), for the output projection
+  __syncthreads();
+  if (t < 64) {
+    const int kb = t >> 4, gl = t & 15, ng = hd / xq::kGroup;
+    const bool unit = gl < ng;
+    float f[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) f[q] = unit ? bf16_to_f32(ob[gl * xq::kGroup + 16 * kb + q]) : 0.0f;
+    xq::digitize_unit(f, row, h * ng + (unit ? gl : 0), kb, unit, plane, d.heads * ng);
+  }
 }
 
 // Fast-mode combine (matrix-core decode partials, 64-position chunks): the
@@ -531,14 +549,16 @@ int attn_decode(const uint16_t* q, int rows, const int32_t* slots, const int32_t
 
 int attn_combine(const float* o_part, const float* ml_part, const uint16_t* qkv,
                  int64_t qkv_stride, int rows, const int32_t* pos, AttnDims d, int max_chunks,
-                 bool fast, uint16_t* out, hipStream_t s) {
+                 bool fast, uint16_t* out, hipStream_t s, char* plane) {
   if (fast) {
     if ((d.max_ctx + kAttnFastChunk - 1) / kAttnFastChunk > 256) return MX_EUNSUPPORTED;
     hipLaunchKernelGGL(combine_fast_kernel, dim3(d.heads, rows), dim3(256), 0, s, o_part,
                        ml_part, qkv, qkv_stride, pos, d, max_chunks, out);
   } else {
+    const bool pl = plane && rows <= 8 && d.head_dim % xq::kGroup == 0;
     hipLaunchKernelGGL(combine_kernel, dim3(d.heads, rows), dim3(kMaxHd), 0, s, o_part, ml_part,
-                       qkv, qkv_stride, pos, d, max_chunks, kAttnChunk, out);
+                       qkv, qkv_stride, pos, d, max_chunks, kAttnChunk, out,
+                       pl ? plane : nullptr);
   }
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }

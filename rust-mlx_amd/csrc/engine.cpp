@@ -129,6 +129,7 @@ struct Engine {
   // those activations
   char* xn_plane = nullptr;
   char* mixed_plane = nullptr;
+  char* y_plane = nullptr;  // operand plane of the GDN / attention output (exact mode)
   // per-step row table (device) and its pinned host mirror
   struct RowTable {
     uint32_t tokens[8];
@@ -465,6 +466,9 @@ int build(Engine& e) {
   e.xn_plane = static_cast<char*>(v);
   MX_TRY(alloc(e, "act.mixed_plane", xq_plane_bytes(c.hidden), &v));
   e.mixed_plane = static_cast<char*>(v);
+  MX_TRY(alloc(e, "act.y_plane",
+               xq_plane_bytes(std::max(c.gdn_hv * c.gdn_dv, c.heads * c.head_dim)), &v));
+  e.y_plane = static_cast<char*>(v);
   MX_TRY(alloc(e, "rows", sizeof(Engine::RowTable), &v));
   e.dev_rows = static_cast<Engine::RowTable*>(v);
   if (hipHostMalloc(reinterpret_cast<void**>(&e.host_rows), sizeof(Engine::RowTable)) != hipSuccess)
@@ -647,13 +651,16 @@ int record_layer(Engine& e, const LayerW& L, int rows, int groups, int t, bool h
                                    e.pbuf + e.cd + e.vd + c.gdn_hv, e.P, L.a_log, L.dt_bias,
                                    L.gdn_norm, c.rms_eps, e.gd, groups, t, rt->gdn_slots,
                                    e.gdn_state + gi * state_per, hist, e.y, e.stream));
-      } else {
+      }
+      // exact recurrence + exact projection: the recurrence writes the
+      // projection's operand plane
+      char* yp = ex(e, kExGdn) && ex(e, kExGdnProj) && rows <= 8 ? e.y_plane : nullptr;
+      if (ex(e, kExGdn))
         MX_TRY(gdn_recurrence(e.conv_out, e.cd, e.pbuf + e.cd, e.pbuf + e.cd + e.vd,
                               e.pbuf + e.cd + e.vd + c.gdn_hv, e.P, L.a_log, L.dt_bias,
                               L.gdn_norm, c.rms_eps, e.gd, groups, t, rt->gdn_slots,
-                              e.gdn_state + gi * state_per, hist, e.y, e.stream));
-      }
-      MX_TRY(project(e, L.gdn_out, e.y, e.vd, rows, wr, kExGdnProj));
+                              e.gdn_state + gi * state_per, hist, e.y, e.stream, yp));
+      MX_TRY(project(e, L.gdn_out, e.y, e.vd, rows, wr, kExGdnProj, yp));
     } else {
       const int ai = L.cache_index;
       ProjEpilogue pl{};
@@ -669,10 +676,11 @@ int record_layer(Engine& e, const LayerW& L, int rows, int groups, int t, bool h
       MX_TRY(attn_decode(e.qrot, rows, rt->slots, rt->pos, e.k_cache + layer_off,
                          e.v_cache + layer_off, e.ad, e.max_chunks, fast_attn, e.o_part,
                          e.ml_part, e.stream));
+      char* yp = !fast_attn && ex(e, kExAttnProj) && rows <= 8 ? e.y_plane : nullptr;
       MX_TRY(attn_combine(e.o_part, e.ml_part, e.pbuf, e.Q, rows, rt->pos, e.ad, e.max_chunks,
-                          fast_attn,
-                          e.y, e.stream));
-      MX_TRY(project(e, L.attn_out, e.y, int64_t(c.heads) * c.head_dim, rows, wr, kExAttnProj));
+                          fast_attn, e.y, e.stream, yp));
+      MX_TRY(project(e, L.attn_out, e.y, int64_t(c.heads) * c.head_dim, rows, wr, kExAttnProj,
+                     yp));
     }
     // MoE sublayer
     MX_TRY(hc_forward(e, L.mlp_hc, rows, e.mixed, e.inj));

@@ -15,6 +15,7 @@
 // (MLX keeps [B, Hv, Dv, Dk]; the C ABI documents the transposition.)
 #include "common.hpp"
 #include "kernels.hpp"
+#include "xq_core.hpp"
 
 namespace mx {
 
@@ -114,6 +115,7 @@ struct ScanArgs {
   float* state;
   float* history;
   uint16_t* y;
+  char* plane;  // nullable: the exact-integer operand plane of y (rows <= 8)
 };
 
 // ---------------------------------------------------------------------------
@@ -127,6 +129,7 @@ __global__ __launch_bounds__(kD) void recurrence_kernel(ScanArgs p) {
   const int hv_heads = p.hv_heads, hk_heads = p.hk_heads;
   const int hk = hv / (hv_heads / hk_heads);
   __shared__ float qs[kD], ks[kD], red[2];
+  __shared__ __align__(16) uint16_t yb[kD];  // the head's y row (plane only)
 
   float* sp = p.state + (size_t(p.slots[g]) * hv_heads + hv) * kD * kD + i;
   float s[kD];
@@ -211,7 +214,25 @@ __global__ __launch_bounds__(kD) void recurrence_kernel(ScanArgs p) {
       const float inv = 1.0f / __builtin_sqrtf(ss / float(kD) + p.eps);
       const float normed = round_bf16(nw * round_bf16(yo * inv));
       const float zi = bf16_to_f32(p.z[row * p.zab_stride + hv * kD + i]);
-      *yp = f32_to_bf16(normed * sigmoidf_(zi));
+      const uint16_t yv = f32_to_bf16(normed * sigmoidf_(zi));
+      *yp = yv;
+      if (p.plane) {
+        // the head's two 64-value groups of this row, digitised by wave 0
+        // (lanes 16 kb + gl, gl < 2), for the output projection
+        yb[i] = yv;
+        __syncthreads();
+        const int lane = i & 63, kb = lane >> 4, gl = lane & 15;
+        if (i < 64) {
+          float f[16];
+          const bool unit = gl < kD / xq::kGroup;
+#pragma unroll
+          for (int q = 0; q < 16; ++q)
+            f[q] = unit ? bf16_to_f32(yb[gl * xq::kGroup + 16 * kb + q]) : 0.0f;
+          xq::digitize_unit(f, int(row), hv * (kD / xq::kGroup) + (unit ? gl : 0), kb, unit,
+                            p.plane, hv_heads * (kD / xq::kGroup));
+        }
+        __syncthreads();
+      }
     } else {
       *yp = f32_to_bf16(yo);
     }
@@ -458,13 +479,14 @@ int gdn_recurrence(const uint16_t* conv_out, int64_t conv_stride, const uint16_t
                    const uint16_t* a, const uint16_t* b, int64_t zab_stride, const float* a_log,
                    const uint16_t* dt_bias, const uint16_t* norm_w, float eps, GdnDims d,
                    int groups, int t, const int32_t* slots, float* state, float* history,
-                   uint16_t* y, hipStream_t s) {
+                   uint16_t* y, hipStream_t s, char* plane) {
   if (d.dk != kD || d.dv != kD || d.hk <= 0 || d.hv % d.hk != 0) return MX_EUNSUPPORTED;
   ScanArgs p{};
   p.conv_out = conv_out; p.conv_stride = conv_stride; p.z = z; p.a = a; p.b = b;
   p.zab_stride = zab_stride; p.a_log = a_log; p.dt_bias = dt_bias; p.norm_w = norm_w; p.eps = eps;
   p.hk_heads = d.hk; p.hv_heads = d.hv; p.t = t; p.slots = slots; p.state = state;
   p.history = history; p.y = y;
+  p.plane = groups * t <= 8 ? plane : nullptr;
   hipLaunchKernelGGL(recurrence_kernel<true>, dim3(d.hv, groups), dim3(kD), 0, s, p);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }

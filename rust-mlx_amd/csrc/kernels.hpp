@@ -171,9 +171,11 @@ bool attn_fast_supported(AttnDims d);
 int attn_decode(const uint16_t* q, int rows, const int32_t* slots, const int32_t* pos,
                 const uint16_t* k_cache, const uint16_t* v_cache, AttnDims d, int max_chunks,
                 bool fast, float* o_part, float* ml_part, hipStream_t s);
+// plane (exact form only, rows <= 8): also writes the exact-integer operand
+// plane of `out` (xq_plane_bytes(heads * head_dim) layout)
 int attn_combine(const float* o_part, const float* ml_part, const uint16_t* qkv,
                  int64_t qkv_stride, int rows, const int32_t* pos, AttnDims d, int max_chunks,
-                 bool fast, uint16_t* out, hipStream_t s);
+                 bool fast, uint16_t* out, hipStream_t s, char* plane = nullptr);
 constexpr int kAttnChunk = 256;
 constexpr int kAttnFastChunk = 64;
 
@@ -255,11 +257,13 @@ int gdn_recurrence_fast(const uint16_t* conv_out, int64_t conv_stride, const uin
                         const float* a_log, const uint16_t* dt_bias, const uint16_t* norm_w,
                         float eps, GdnDims d, int groups, int t, const int32_t* slots,
                         float* state, float* history, uint16_t* y, hipStream_t s);
+// plane (rows <= 8): also writes the exact-integer operand plane of y
+// (xq_plane_bytes(hv * 128) layout)
 int gdn_recurrence(const uint16_t* conv_out, int64_t conv_stride, const uint16_t* z,
                    const uint16_t* a, const uint16_t* b, int64_t zab_stride, const float* a_log,
                    const uint16_t* dt_bias, const uint16_t* norm_w, float eps, GdnDims d,
                    int groups, int t, const int32_t* slots, float* state, float* history,
-                   uint16_t* y, hipStream_t s);
+                   uint16_t* y, hipStream_t s, char* plane = nullptr);
 int gdn_scan(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
              const uint16_t* beta, GdnDims d, int groups, int t, const int32_t* slots,
              float* state, float* history, uint16_t* y, hipStream_t s);
