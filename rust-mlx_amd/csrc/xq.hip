@@ -350,7 +350,7 @@ __device__ __forceinline__ QWeight bank_matrix(const QBank& b, int expert, const
 
 // Copies a plane of G groups (xq_core.hpp layout) into LDS: every thread
 // issues all of its loads before its first store.  Ends with a barrier.
-// Expert gate/up + SwiGLU for 64 intermediate rows (blockIdx.x) of one plan
+// Expert gate/up + SwiGLU for 16 kGuTiles intermediate rows (blockIdx.x) of one plan
 // entry and one four-row block of activation rows: with the plane, blockIdx.y
 // is an item of the plan (an entry and a block of rows 4b .. 4b + 3 of x that
 // holds a member; past the items a workgroup returns at once, so the active
@@ -368,7 +368,7 @@ __device__ __forceinline__ QWeight bank_matrix(const QBank& b, int expert, const
 // and biases load B at a time (the launcher checks their alignment), so the
 // group loop is straight-line code whose scheduler overlaps one group's
 // operand reads, matrix-core pass and fp64 fold with the next group's.
-constexpr int kGuTiles = 4;  // 16-row tiles per gate/up workgroup (2 waves each)
+constexpr int kGuTiles = 2;  // 16-row tiles per gate/up workgroup (2 waves each)
 
 __host__ __device__ constexpr int gate_up_red_bytes(int spw) { return kGuTiles * 2 * spw * 64 * 8; }
 
@@ -532,24 +532,26 @@ void xq_gate_up_kernel(
   }
 }
 
-// Expert down + route score for one plan entry (blockIdx.y) and 64 output
+constexpr int kDnTiles = 4;  // 16-column tiles per expert down workgroup (one wave each)
+
+// Expert down + route score for one plan entry (blockIdx.y) and 16 kDnTiles output
 // columns (blockIdx.x): p[row][slot][c] = bf16(bf16(down h) * score) for
 // routed slots, bf16(down h) for the shared slot (moe.hip down_body).
 template <int BITS, int SPW>
-__global__ __launch_bounds__(256) void xq_down_kernel(const uint16_t* __restrict__ h,
+__global__ __launch_bounds__(64 * kDnTiles) void xq_down_kernel(const uint16_t* __restrict__ h,
                                                       const MoePlan* __restrict__ plan,
                                                       const uint16_t* __restrict__ scores,
                                                       int top_k, QBank down, QWeight sdown,
                                                       uint16_t* __restrict__ p, int hs) {
   extern __shared__ __align__(16) char lds[];
-  __shared__ float yt[8 * 64];
+  __shared__ float yt[8 * 16 * kDnTiles];
   __shared__ int ro[8], so[8];
   const int entry = blockIdx.y;
   if (entry >= plan->count) return;
   const int expert = plan->expert[entry];
   const QWeight dw = bank_matrix(down, expert, sdown);
   const int hidden = dw.n, inter = dw.k;
-  const int c0 = blockIdx.x * 64;
+  const int c0 = blockIdx.x * 16 * kDnTiles;
   if (c0 >= hidden) return;
   const int M = plan->m[entry];
   if (threadIdx.x < 8) {
@@ -560,13 +562,14 @@ __global__ __launch_bounds__(256) void xq_down_kernel(const uint16_t* __restrict
   const int j = threadIdx.x & 15, t = threadIdx.x >> 6;
   const int row = min(c0 + 16 * t + j, hidden - 1);
   const int G = inter / xq::kGroup;
-  xq_tiles<BITS, 4, 1, SPW, kSrcStage>(dw.codes + size_t(row) * (size_t(inter) * BITS / 32),
+  xq_tiles<BITS, kDnTiles, 1, SPW, kSrcStage>(dw.codes + size_t(row) * (size_t(inter) * BITS / 32),
                                        dw.scales + size_t(row) * G, dw.biases + size_t(row) * G,
                                        tiles_sbv<BITS, SPW>(dw), inter, M, M > 4 ? 3 : 1,
                                        MemberRows{h, int64_t(top_k + 1) * hs, hs, ro, so}, nullptr,
                                        lds, yt, [] {});
-  for (int i = threadIdx.x; i < 8 * 64; i += 256) {
-    const int m = i >> 6, c = i & 63;
+  constexpr int NC = 16 * kDnTiles;
+  for (int i = threadIdx.x; i < 8 * NC; i += 64 * kDnTiles) {
+    const int m = i / NC, c = i % NC;
     if (m >= M || c0 + c >= hidden) continue;
     const bool routed = so[m] < top_k;
     const float dv = round_bf16(yt[i]);
@@ -803,10 +806,11 @@ int launch_down(const uint16_t* h, const MoePlan* plan, int routes, const uint16
                 hipStream_t s) {
   const auto fn = xq_down_kernel<BITS, SPW>;
   const int kmax = down.k > sdown.k ? down.k : sdown.k;
-  const int lb = tiles_lds(kmax / xq::kGroup, 4, 1, kSrcStage);
+  const int lb = tiles_lds(kmax / xq::kGroup, kDnTiles, 1, kSrcStage);
   MX_TRY_RC(raise_lds(fn, lb));
-  hipLaunchKernelGGL(fn, dim3((down.n + 63) / 64, routes), dim3(256), lb, s, h, plan, scores,
-                     top_k, down, sdown, p, hs);
+  constexpr int NC = 16 * kDnTiles;
+  hipLaunchKernelGGL(fn, dim3((down.n + NC - 1) / NC, routes), dim3(64 * kDnTiles), lb, s, h,
+                     plan, scores, top_k, down, sdown, p, hs);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 
