@@ -579,7 +579,8 @@ __global__ __launch_bounds__(64 * kDnTiles) void xq_down_kernel(const uint16_t* 
 }
 
 // Hyper-connection up-projection and stream mix for one 64-column group of
-// `mixed` (blockIdx.x = tg): tile t = 4 s + ct holds up rows
+// `mixed` (blockIdx.x = tg) and, with more than four activation rows, one
+// four-row block of them (blockIdx.y): tile t = 4 s + ct holds up rows
 // s * H + 64 tg + 16 ct + j (K = the rank); each column takes the kHcUpMix
 // arithmetic of ProjFinish, then wave 0 writes the group's operand plane, so
 // every consumer of `mixed` reads its operands ready-made.
@@ -595,15 +596,20 @@ __global__ __launch_bounds__(1024) void xq_upmix_kernel(QWeight w, const uint16_
   const int j = threadIdx.x & 15, t = threadIdx.x >> 6;
   const int row = (t >> 2) * hidden + tg * 64 + (t & 3) * 16 + j;
   const int G = w.k / xq::kGroup;
+  // two workgroups per column group when there are two four-row blocks of
+  // activation rows: blockIdx.y = the block this one computes and writes
+  const bool split = gridDim.y > 1;
+  const int mlo = split ? 4 * int(blockIdx.y) : 0, mhi = split ? mlo + 4 : 8;
   xq_tiles<BITS, 16, 1, SPW, kSrcStage>(w.codes + size_t(row) * (size_t(w.k) * BITS / 32),
                                         w.scales + size_t(row) * G, w.biases + size_t(row) * G,
-                                        tiles_sbv<BITS, SPW>(w), w.k, M, M > 4 ? 3 : 1,
+                                        tiles_sbv<BITS, SPW>(w), w.k, M,
+                                        split ? 1 << blockIdx.y : (M > 4 ? 3 : 1),
                                         XRows{lo, w.k}, nullptr, lds, yt,
                                         [] {});
   for (int i = threadIdx.x; i < 8 * 64; i += 1024) {
     const int m = i >> 6, c = i & 63;
     float v = 0.0f;
-    if (m < M) {
+    if (m < M && m >= mlo && m < mhi) {
       float sum = 0.0f;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
@@ -626,7 +632,8 @@ __global__ __launch_bounds__(1024) void xq_upmix_kernel(QWeight w, const uint16_
     float f[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) f[i] = mix[m * 64 + 16 * kb + i];
-    xq::digitize_unit(f, m, tg, kb, (lane & 15) < 8 && m < M, plane, hidden / xq::kGroup);
+    xq::digitize_unit(f, m, tg, kb, (lane & 15) < 8 && m < M && m >= mlo && m < mhi, plane,
+                      hidden / xq::kGroup);
   }
 }
 
@@ -890,7 +897,7 @@ int xq_upmix(const QWeight& up, const uint16_t* lo, int m, const uint16_t* xn, i
     return MX_EUNSUPPORTED;
   const int G = up.k / xq::kGroup;
   const int lb = tiles_lds(G, 16, 1, kSrcStage);
-  const dim3 grid(hidden / 64);
+  const dim3 grid(hidden / 64, m > 4 ? 2 : 1);
   const int spw = whole_spw(up.k);
 #define MX_UM(B, SPW)                                                                           \
   if (up.bits == B && spw == SPW) {                                                             \
