@@ -355,22 +355,21 @@ __device__ __forceinline__ QWeight bank_matrix(const QBank& b, int expert, const
 // is an item of the plan (an entry and a block of rows 4b .. 4b + 3 of x that
 // holds a member; past the items a workgroup returns at once, so the active
 // ones come first in dispatch order); staged, blockIdx.y is the entry and
-// blockIdx.z the block of members 4z .. 4z + 3.  Wave (t, ks) owns the 16
-// intermediate rows of tile t and the depth half ks (2 SPW groups): it
-// streams their gate rows and then their up rows (load batches kept D deep
-// across both passes, so the memory system streams while the matrix cores
-// and VALUs work).  The ks = 1 wave leaves its slice sums in LDS; the ks = 0
-// wave adds its own in order from +0 and then those, in slice order, and
-// writes h[row][slot][i] = bf16(bf16(silu(bf16 g)) * bf16 u) for the block's
-// member routes (the exact kernels' SwiGLU, moe.hip gate_up_body).
+// blockIdx.z the block of members 4z .. 4z + 3.  Wave (t, p) owns the 16
+// intermediate rows of tile t in matrix p (0: gate, 1: up) and streams them
+// over the whole depth (load batches kept D deep, so the memory system
+// streams while the matrix cores and VALUs work), adding its slice sums in
+// slice order from +0.  The up wave leaves its rounded value in LDS; the gate
+// wave writes h[row][slot][i] = bf16(bf16(silu(bf16 g)) * bf16 u) for the
+// block's member routes (the exact kernels' SwiGLU, moe.hip gate_up_body).
 // Operands: the block of the plane of x copied into LDS, or the members
-// staged in order.  FULL: each half is exactly 2 SPW groups and the scales
+// staged in order.  FULL: the depth is exactly 2 SPW groups and the scales
 // and biases load B at a time (the launcher checks their alignment), so the
 // group loop is straight-line code whose scheduler overlaps one group's
 // operand reads, matrix-core pass and fp64 fold with the next group's.
 constexpr int kGuTiles = 2;  // 16-row tiles per gate/up workgroup (2 waves each)
 
-__host__ __device__ constexpr int gate_up_red_bytes(int spw) { return kGuTiles * 2 * spw * 64 * 8; }
+__host__ __device__ constexpr int gate_up_xch_bytes() { return kGuTiles * 64 * 4; }
 
 template <int BITS, int SPW, int SRC, bool FULL>
 __global__ __launch_bounds__(128 * kGuTiles) __attribute__((amdgpu_waves_per_eu(4)))
@@ -381,10 +380,9 @@ void xq_gate_up_kernel(
   extern __shared__ __align__(16) char lds[];
   __shared__ int ro[8], so[8];
   constexpr int NT = 128 * kGuTiles;
-  constexpr int NG = 2 * SPW;                       // groups per wave and pass (at most)
+  constexpr int NG = 2 * SPW;                       // groups per wave (at most)
   constexpr int B = tile_batch<BITS, SPW>();
-  constexpr int NBP = NG / B;                       // batches per pass
-  constexpr int NB = 2 * NBP;                       // gate pass, then up pass
+  constexpr int NB = NG / B;                        // load batches per wave
   constexpr int D = NB < 2 ? NB : 2;                // batches in flight
   int entry, blk;
   if constexpr (SRC == kSrcPlaneLds) {
@@ -400,44 +398,38 @@ void xq_gate_up_kernel(
   }
   const int M = plan->m[entry];
   const int expert = plan->expert[entry];
-  const QWeight gw = bank_matrix(gate, expert, sgate);
-  const QWeight uw = bank_matrix(up, expert, sup);
-  const int inter = gw.n, hidden = gw.k;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int t = wave >> 1, p = wave & 1;
+  // the gate and up matrices of an expert have one shape (the launcher checks)
+  const QWeight mw = bank_matrix(p ? up : gate, expert, p ? sup : sgate);
+  const int inter = mw.n, hidden = mw.k;
   const int i0 = blockIdx.x * 16 * kGuTiles;
   if (i0 >= inter) return;
   const int lane = threadIdx.x & 63, j = lane & 15, kb = lane >> 4;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int t = wave >> 1, ks = wave & 1;
   const int G = hidden / xq::kGroup;
-  const int gbeg = ks * NG, gend = min(gbeg + NG, G);
   const int col = i0 + 16 * t + j;
   const int row = min(col, inter - 1);
-  const bool sbv[2] = {xq::sb_vector_ok<B>(gw.scales, gw.biases, G),
-                       xq::sb_vector_ok<B>(uw.scales, uw.biases, G)};
-  const size_t wpr = size_t(hidden) * BITS / 32;
-  const uint32_t* crow[2] = {gw.codes + row * wpr, uw.codes + row * wpr};
-  const uint16_t* srow[2] = {gw.scales + size_t(row) * G, uw.scales + size_t(row) * G};
-  const uint16_t* brow[2] = {gw.biases + size_t(row) * G, uw.biases + size_t(row) * G};
+  const bool sbv = xq::sb_vector_ok<B>(mw.scales, mw.biases, G);
+  const uint32_t* crow = mw.codes + row * (size_t(hidden) * BITS / 32);
+  const uint16_t* srow = mw.scales + size_t(row) * G;
+  const uint16_t* brow = mw.biases + size_t(row) * G;
   xq::Codes<BITS> c[D][B];
   xq::ScaleBias<B> sb[D];
   auto load_batch = [&](int buf, int bi) {
-    const int pass = bi / NBP, g0 = gbeg + (bi % NBP) * B;
-    const int last = max(gend - 1, 0);
+    const int g0 = bi * B;
 #pragma unroll
-    for (int i = 0; i < B; ++i)
-      xq::load_codes<BITS>(crow[pass], min(g0 + i, last), kb, c[buf][i]);
+    for (int i = 0; i < B; ++i) xq::load_codes<BITS>(crow, min(g0 + i, G - 1), kb, c[buf][i]);
     if constexpr (FULL)
-      xq::load_scale_bias_vec<B>(srow[pass], brow[pass], g0, sb[buf]);
+      xq::load_scale_bias_vec<B>(srow, brow, g0, sb[buf]);
     else
-      xq::load_scale_bias<B>(srow[pass], brow[pass], min(g0, last), max(gend, 1), sbv[pass],
-                             sb[buf]);
+      xq::load_scale_bias<B>(srow, brow, min(g0, G - 1), G, sbv, sb[buf]);
   };
   // operand addresses: group g's A operand at ab + g * gstride; Q and Eb of
   // the lane's activation row at qb[8 g], eb[8 g]
   const char* ab;
   const double* qb;
   const int* eb;
-  int gstride, red_at;
+  int gstride, xch_at;
   if constexpr (SRC == kSrcPlaneLds) {
     // the plane block (from the L2) lands first; the weight batches go out
     // after it, so the group loop starts when its first batch arrives rather
@@ -449,7 +441,7 @@ void xq_gate_up_kernel(
     gstride = xq::kBlockBytes;
     qb = reinterpret_cast<const double*>(lds + xq::block_q_offset(G)) + 4 * blk + kb;
     eb = reinterpret_cast<const int*>(lds + xq::block_e_offset(G)) + 4 * blk + kb;
-    red_at = xq::block_bytes(G);
+    xch_at = xq::block_bytes(G);
   } else {
     // member rows and slots: loaded before the weights, stored after them,
     // so no wait for them holds the weight loads back
@@ -470,34 +462,30 @@ void xq_gate_up_kernel(
     gstride = xq::kGroupBytes;
     qb = reinterpret_cast<const double*>(lds + xq::plane_q_offset(G)) + 4 * blk + kb;
     eb = reinterpret_cast<const int*>(lds + xq::plane_e_offset(G)) + 4 * blk + kb;
-    red_at = xq::stage_bytes(G);
+    xch_at = xq::stage_bytes(G);
   }
-  // slice sums of the ks = 1 waves: [tile][pass][slice][lane]
-  double* red = reinterpret_cast<double*>(lds + ((red_at + 15) & ~15));
-  double tot[2] = {0.0, 0.0}, acc = 0.0;  // [gate/up]
+  // the up waves' rounded values: [tile][lane]
+  float* xch = reinterpret_cast<float*>(lds + ((xch_at + 15) & ~15));
+  double tot = 0.0, acc = 0.0;
 #pragma unroll
   for (int bi = 0; bi < NB; ++bi) {
-    const int buf = bi % D, pass = bi / NBP;
+    const int buf = bi % D;
 #pragma unroll
     for (int i = 0; i < B; ++i) {
-      const int gi = (bi % NBP) * B + i, gl = gbeg + gi;
-      if (FULL || gl < gend) {
+      const int gl = bi * B + i;
+      if (FULL || gl < G) {
         xq::group_step1<BITS>(*reinterpret_cast<const xq::v4i*>(ab + gl * gstride),
                               xq::b_operand<BITS>(c[buf][i]), qb[gl * 8], eb[gl * 8],
                               sb[buf].scale(i), sb[buf].bias(i), acc);
         // a slice ends after its second group, or after the last of an odd count
         if ((gl & 1) || (!FULL && gl + 1 == G)) {
-          if (ks == 0) {
-            tot[pass] = tot[pass] + acc;
-          } else {
-            red[((t * 2 + pass) * SPW + (gi >> 1)) * 64 + lane] = acc;
-          }
+          tot = tot + acc;
           acc = 0.0;
           if constexpr (FULL) {
             // the slice's total exists here (the empty asm reads it), so its
             // folds stay within the slice, and the scheduler overlaps the
             // groups of one slice, no more
-            asm volatile("" : "+v"(tot[pass]));
+            asm volatile("" : "+v"(tot));
             __builtin_amdgcn_sched_barrier(0);
           }
         }
@@ -505,21 +493,16 @@ void xq_gate_up_kernel(
     }
     if (bi + D < NB) load_batch(buf, bi + D);
   }
+  const float v = round_bf16(float(tot));
+  if (p) xch[t * 64 + lane] = v;
   __syncthreads();
-  if (ks != 0) return;
-  // the second half's slices, in slice order
-  const int s1 = ((G - NG) + 1) / 2;
-#pragma unroll
-  for (int pass = 0; pass < 2; ++pass)
-    for (int sl = 0; sl < s1 && sl < SPW; ++sl)
-      tot[pass] = tot[pass] + red[((t * 2 + pass) * SPW + sl) * 64 + lane];
+  if (p) return;
   // lane (kb, j) holds activation row (plane) or member (staged) 4 blk + kb
   // of column col
   const int xr = 4 * blk + kb;
   if (col < inter) {
-    const float gv = round_bf16(float(tot[0]));
-    const float uv = round_bf16(float(tot[1]));
-    const float silu = round_bf16(gv * sigmoid_bf16(gv));
+    const float uv = xch[t * 64 + lane];
+    const float silu = round_bf16(v * sigmoid_bf16(v));
     const uint16_t out = f32_to_bf16(silu * uv);
     for (int m = 0; m < M; ++m) {
       if constexpr (SRC == kSrcPlaneLds) {
@@ -789,10 +772,10 @@ int launch_gate_up(const uint16_t* x, const char* plane, const MoePlan* plan, in
   const dim3 grid = plane ? dim3(gx, 2 * routes, 1) : dim3(gx, routes, 2);
   const int G = gate.k / xq::kGroup;
   const int lb = ((plane ? xq::block_bytes(G) : xq::stage_bytes(G)) + 15) / 16 * 16 +
-                 gate_up_red_bytes(SPW);
+                 gate_up_xch_bytes();
   // FULL also needs every expert's scale/bias rows on 2B-byte boundaries
   constexpr int B = tile_batch<BITS, SPW>();
-  const bool full = G == 4 * SPW && xq::sb_vector_ok<B>(gate.scales, gate.biases, G) &&
+  const bool full = G == 2 * SPW && xq::sb_vector_ok<B>(gate.scales, gate.biases, G) &&
                     xq::sb_vector_ok<B>(up.scales, up.biases, G) &&
                     xq::sb_vector_ok<B>(sgate.scales, sgate.biases, G) &&
                     xq::sb_vector_ok<B>(sup.scales, sup.biases, G) &&
@@ -859,12 +842,13 @@ int xq_gate_up(const uint16_t* x, const char* plane, const MoePlan* plan, int ro
                uint16_t* h, hipStream_t s) {
   if (gate.group_size != 64 || up.group_size != 64 || sgate.group_size != 64 ||
       sup.group_size != 64 || !xq_whole_ok(gate.k) || sgate.k != gate.k || up.k != gate.k ||
-      gate.bits != up.bits || sgate.bits != gate.bits || sup.bits != gate.bits)
+      gate.bits != up.bits || sgate.bits != gate.bits || sup.bits != gate.bits ||
+      up.n != gate.n || sup.n != sgate.n)
     return MX_EUNSUPPORTED;
   const int routes = rows * top_k + 1;
   const int hs = gate.n > sgate.n ? gate.n : sgate.n;
-  // two waves per tile, each half the depth (rounded up to whole slices)
-  const int spw = whole_spw(gate.k) > 1 ? whole_spw(gate.k) / 2 : 1;
+  // two waves per tile (gate and up), each over the whole depth
+  const int spw = whole_spw(gate.k);
   switch (gate.bits) {
     case 4: MX_SPW_DISPATCH(4, launch_gate_up, x, plane, plan, routes, top_k, gate, up, sgate, sup, h, hs, s)
     case 5: MX_SPW_DISPATCH(5, launch_gate_up, x, plane, plan, routes, top_k, gate, up, sgate, sup, h, hs, s)
