@@ -383,7 +383,7 @@ void xq_gate_up_kernel(
   constexpr int NG = 2 * SPW;                       // groups per wave (at most)
   constexpr int B = tile_batch<BITS, SPW>();
   constexpr int NB = NG / B;                        // load batches per wave
-  constexpr int D = NB < 2 ? NB : 2;                // batches in flight
+  constexpr int D = NB < 3 ? NB : 3;                // batches in flight
   int entry, blk;
   if constexpr (SRC == kSrcPlaneLds) {
     // blockIdx.y: an item of the plan, (entry, block of rows with a member)
