@@ -238,7 +238,7 @@ def bench_config3(mx, args):
             "reference_policy_groups": len(groups),
         },
         "roofline": {"bound": "hbm",
-                     "kernel": ("xq_gate_up_kernel<4, 8, 3, true> (exact-integer expert gate/up + "
+                     "kernel": ("xq_gate_up_kernel<4, 16, 3, true> (exact-integer expert gate/up + "
                                 "SwiGLU over the plan's work items, the form the step launches)") if exact else
                                ("gate_up_persist_kernel<4, 16, 4, 2, 0> (route-taking form; the "
                                 "step launches the self-routing <4, 16, 4, 2, 8>)"),
