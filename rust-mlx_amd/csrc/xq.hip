@@ -767,9 +767,11 @@ int launch_gate_up(const uint16_t* x, const char* plane, const MoePlan* plan, in
                    int top_k, const QBank& gate, const QBank& up, const QWeight& sgate,
                    const QWeight& sup, uint16_t* h, int hs, hipStream_t s) {
   const int gx = (hs + 16 * kGuTiles - 1) / (16 * kGuTiles);
-  // plane: one workgroup row per plan item (at most two per entry); staged:
-  // entries by blocks of members
-  const dim3 grid = plane ? dim3(gx, 2 * routes, 1) : dim3(gx, routes, 2);
+  // plane: one workgroup row per plan item (an entry's items are the blocks
+  // its routes come from, so there are at most routes + 1 of them: the shared
+  // entry's two blocks and at most one per routed route); staged: entries by
+  // blocks of members
+  const dim3 grid = plane ? dim3(gx, routes + 1, 1) : dim3(gx, routes, 2);
   const int G = gate.k / xq::kGroup;
   const int lb = ((plane ? xq::block_bytes(G) : xq::stage_bytes(G)) + 15) / 16 * 16 +
                  gate_up_xch_bytes();
