@@ -48,7 +48,9 @@ rocprofv3 counter summary of that kernel
 (profiles/config3-b8-decode-exact_hbm-traffic.md, or
 profiles/config3-b8-decode_hbm-traffic.md for --fast).
 The CPU baseline is the C oracle (oracle/, a restatement of the reference
-arithmetic) timed on this host over a bounded sample of the same step.
+arithmetic) timed on this host: for config 3, one whole batch-8 step on the
+engine's weights and caches, whose next tokens must equal the exact engine's
+for the same step; for the component workloads, a bounded sample.
 """
 from __future__ import annotations
 
@@ -212,7 +214,16 @@ def bench_config3(mx, args):
         f"down {dn_gbs:.0f} GB/s; distinct experts/layer {prof2['distinct_experts'] / layers:.1f}; "
         f"step bytes {step_bytes / 1e9:.2f} GB -> {step_frac * 100:.1f}% of HBM roofline per step")
     positions = [eng.offset(s) for s in slots]
-    cpu = None if args.no_cpu_baseline else cpu_baseline_config3(mx, eng, cfg, slots, toks, positions)
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu, cpu_next = cpu_baseline_config3(mx, eng, cfg, slots, toks, positions)
+        # the engine's own step on the same rows, tokens and caches
+        eng_next = np.asarray(eng.decode_batch(slots, toks, equal=False), np.uint32)
+        same = bool((np.asarray(cpu_next, np.uint32).reshape(-1)[:rows] == eng_next).all())
+        log(f"cpu baseline: oracle next tokens {'equal' if same else 'DIFFER FROM'} the engine's")
+        if exact and not same:
+            raise SystemExit("bench: the oracle's step and the exact engine step disagree")
+        cpu["tokens_equal_engine"] = same
     eng.close()
     return {
         "metric": METRIC,
@@ -265,38 +276,36 @@ def measured_traffic(summary: str):
 
 
 def cpu_baseline_config3(mx, eng, cfg, slots, toks, positions):
-    """The oracle runs one batch-8 decode step over a sample of the stack
-    (layers 0-3: three GDN layers and one attention layer, plus the mixer and
-    head) at the rows' real positions; the step time is scaled to 48 layers."""
+    """The oracle runs one whole batch-8 decode step (all layers, the mixer and
+    the head, the engine's weights and caches read back from the device) at
+    the rows' real positions, and its next tokens are checked against the
+    engine's for the same step."""
     from oracle.model import Model
     from oracle import oracle as orc
-
-    sample = [0, 1, 2, 3]
 
     def fetch(name, dtype, shape):
         return eng.read(name, dtype, shape)
 
     t0 = time.perf_counter()
-    model = Model(cfg, fetch, only_layers=sample)
-    log(f"cpu baseline: fetched {len(sample)} layers in {time.perf_counter() - t0:.1f}s")
+    model = Model(cfg, fetch)
+    # the engine's caches (the oracle keeps them in the same layout)
+    model.state[...] = eng.read("cache.gdn_state", np.float32, model.state.shape)
+    model.conv[...] = eng.read("cache.conv_state", np.uint16, model.conv.shape)
+    model.k[...] = eng.read("cache.k", np.uint16, model.k.shape)
+    model.v[...] = eng.read("cache.v", np.uint16, model.v.shape)
+    log(f"cpu baseline: fetched {cfg['layers']} layers and the caches in "
+        f"{time.perf_counter() - t0:.1f}s")
     for s, p in zip(slots, positions):
         model.offsets[s] = p
     t0 = time.perf_counter()
-    model.decode_rows(slots, list(toks))
-    layers_s = time.perf_counter() - t0
-    # head alone, to separate it from the per-layer cost
-    t1 = time.perf_counter()
-    orc.head_argmax(model.head, model.last_mixed)
-    head_s = time.perf_counter() - t1
-    per_layer = (layers_s - head_s) / len(sample)
-    step_s = per_layer * cfg["layers"] + head_s
+    nxt = model.decode_rows(slots, list(toks))
+    step_s = time.perf_counter() - t0
     tok_s = len(slots) / step_s
-    log(f"cpu baseline: {layers_s:.1f}s for {len(sample)} layers + head; "
-        f"scaled step {step_s:.1f}s -> {tok_s:.4f} tok/s")
+    log(f"cpu baseline: one step {step_s:.1f}s -> {tok_s:.4f} tok/s")
+    del model
     return {"value": round(tok_s, 5), "unit": "tok/s", "cores": orc.num_threads(), "kind": "port",
-            "sample": f"one batch-8 decode step through layers {sample} (3 GDN + 1 attention) "
-                      f"+ mixer + head = {layers_s:.1f}s, scaled to {cfg['layers']} layers "
-                      f"({step_s:.1f}s/step)"}
+            "sample": f"one whole batch-8 decode step ({cfg['layers']} layers + mixer + head) "
+                      f"= {step_s:.1f}s"}, nxt
 
 
 # ---------------------------------------------------------------- config 0 --
