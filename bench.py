@@ -742,7 +742,7 @@ def bench_mtp_config4(mx, args):
                max_context=ctx + n_tok + 64)
     eng = mx.Engine(cfg)
     exact = not args.fast
-    eng.set_flags(exact=exact)
+    eng.set_flags(exact=exact, eager=args.eager)
     prompt = np.random.default_rng(4004).integers(0, cfg["vocab"], ctx)
     res = {}
     for d in (0, depth):
@@ -757,23 +757,102 @@ def bench_mtp_config4(mx, args):
         res[d] = (toks, st, t_all - t_first, t_first)
         log(f"mtp-config4: depth {d}: {n_tok} tokens in {t_all - t_first:.3f}s after a "
             f"{t_first:.2f}s prompt; rounds {st['rounds']}, accepted {st['accepted']}/{st['drafted']}")
-    eng.close()
     if not (res[0][0] == res[depth][0]).all():
         raise SystemExit("bench: speculative tokens differ from greedy decoding")
     toks, st, dt, t_first = res[depth]
     _, _, dt0, _ = res[0]
+    ms_round = dt / max(st["rounds"], 1) * 1e3
+    tok_per_round = n_tok / max(st["rounds"], 1)
+    # one more verify round at the end of the generated context: the caches
+    # as they stand (read by the CPU leg first), one profiled verify block of
+    # depth + 1 tokens (its algorithmic bytes), a commit, and the bytes of the
+    # round's depth draft-layer steps (depth - 1 drafts before the block and
+    # one resynchronisation after it)
+    pos = eng.offset(0)
+    block = [int(t) for t in toks[-(depth + 1):]]
+    cpu_model = None
+    if not args.no_cpu_baseline:
+        cpu_model = mtp_cpu_model(mx, eng, cfg, pos)
+    with ProfilerRegion(args.roctx):
+        pred, vprof = eng.profile_verify(0, block)
+    eng.commit(0, 1)
+    draft_b = eng.draft_bytes(pos)
+    round_bytes = vprof["step_bytes"] + depth * draft_b
+    gbs = round_bytes / (ms_round * 1e-3) / 1e9
+    log(f"mtp-config4: verify block {vprof['step_bytes'] / 1e9:.3f} GB "
+        f"({vprof['distinct_experts'] / max(vprof['layers'], 1):.1f} distinct experts/layer), "
+        f"draft step {draft_b / 1e9:.3f} GB; round {round_bytes / 1e9:.3f} GB in {ms_round:.3f} ms "
+        f"-> {gbs:.0f} GB/s")
+    cpu = None
+    if cpu_model is not None:
+        cpu = mtp_cpu_round(cpu_model, block, pred, depth, tok_per_round, exact)
+        del cpu_model
+    eng.close()
     return {
         "metric": METRIC, "value": round(n_tok / dt, 2), "unit": "tok/s", "ms_per_step": dt / n_tok * 1e3,
         "dtype": "affine u4/u5/u6/u8 codes x bf16 -> fp32 acc; bf16 activations; fp32 GDN state",
         "config": {"workload": "mtp-config4", "model": "synthetic hybrid GDN/attention MoE, mixed widths",
                    "batch": 1, "context": ctx, "generated": n_tok, "draft_depth": depth,
                    "rounds": st["rounds"], "drafted": st["drafted"], "accepted": st["accepted"],
-                   "ms_per_round": round(dt / max(st["rounds"], 1) * 1e3, 3),
+                   "ms_per_round": round(ms_round, 3),
+                   "verify_block_bytes_gb": round(vprof["step_bytes"] / 1e9, 4),
+                   "draft_step_bytes_gb": round(draft_b / 1e9, 4),
+                   "round_bytes_gb": round(round_bytes / 1e9, 4),
                    "greedy_decode_tok_s": round(n_tok / dt0, 2), "prompt_s": round(t_first, 2),
                    "tokens_equal_greedy": True, "mode": "exact" if exact else "fast"},
-        "roofline": None,
-        "cpu_baseline": None,
+        "roofline": {"bound": "hbm",
+                     "kernel": f"whole verify round, graph-replayed: one {depth + 1}-token verify "
+                               f"block through all {cfg['layers']} layers + {depth} MTP draft-layer "
+                               "steps with the greedy head",
+                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_round": int(round_bytes),
+                     "ms_per_round": round(ms_round, 3)},
+        "cpu_baseline": cpu,
     }
+
+
+def mtp_cpu_model(mx, eng, cfg, pos):
+    """The oracle model on the engine's weights (mixed widths, the MTP layer)
+    and its caches as they stand, slot 0 at position pos."""
+    from oracle.model import Model
+
+    t0 = time.perf_counter()
+    model = Model(cfg, lambda name, dtype, shape: eng.read(name, dtype, shape))
+    model.state[...] = eng.read("cache.gdn_state", np.float32, model.state.shape)
+    model.conv[...] = eng.read("cache.conv_state", np.uint16, model.conv.shape)
+    model.k[...] = eng.read("cache.k", np.uint16, model.k.shape)
+    model.v[...] = eng.read("cache.v", np.uint16, model.v.shape)
+    model.offsets[0] = pos
+    log(f"cpu baseline: fetched {cfg['layers']} layers + the MTP layer and the caches in "
+        f"{time.perf_counter() - t0:.1f}s")
+    return model
+
+
+def mtp_cpu_round(model, block, pred, depth, tok_per_round, exact):
+    """One verify round on the CPU oracle: the same verify block as the
+    engine's (its predictions must equal the engine's in exact mode), a
+    commit, and depth draft-layer steps on the block's hidden streams."""
+    from oracle import oracle as orc
+
+    t0 = time.perf_counter()
+    cpu_pred = np.asarray(model.verify(0, block), np.uint32)
+    hid = model.hidden.copy()
+    model.commit(0, 1)
+    pos = model.offsets[0]
+    for i in range(depth):
+        model.mtp_step(0, [block[-1]], pos + i, hid[-1:])
+    round_s = time.perf_counter() - t0
+    same = bool((cpu_pred == np.asarray(pred, np.uint32)).all())
+    log(f"cpu baseline: one verify round {round_s:.1f}s; verify predictions "
+        f"{'equal' if same else 'DIFFER FROM'} the engine's")
+    if exact and not same:
+        raise SystemExit("bench: the oracle's verify block and the exact engine's disagree")
+    return {"value": round(tok_per_round / round_s, 5), "unit": "tok/s", "cores": orc.num_threads(),
+            "kind": "port", "tokens_equal_engine": same,
+            "sample": f"one whole verify round ({len(block)}-token verify block through all layers "
+                      f"+ commit + {depth} MTP draft steps) = {round_s:.1f}s, at the engine's "
+                      f"{tok_per_round:.2f} tokens per round"}
 
 
 # ------------------------------------------------------- copy calibration --

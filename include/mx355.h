@@ -532,6 +532,19 @@ mx_status mx_engine_fill_slot(mx_engine* e, int32_t slot, int32_t length, uint64
  * attribute GPU time per kernel, docs/performance.md:41). */
 mx_status mx_engine_profile_step(mx_engine* e, const int32_t* slots, const uint32_t* tokens,
                                  int32_t rows, uint32_t* next, mx_step_profile* out);
+/* Measurement hook (no reference counterpart): one MTP verify block like
+ * mx_engine_verify (a commit must follow, as after mx_engine_verify), run
+ * eagerly with the expert kernels timed per layer; out->step_bytes holds the
+ * block's algorithmic bytes (weights outside the expert banks, the routed
+ * experts the block touches, the GDN state read once and written after every
+ * token, conv windows, the KV positions up to the block's last). */
+mx_status mx_engine_profile_verify(mx_engine* e, int32_t slot, const uint32_t* tokens,
+                                   int32_t count, uint32_t* argmax, mx_step_profile* out);
+/* Measurement hook (no reference counterpart): algorithmic bytes of one MTP
+ * draft step of one row at cache position `pos` (the draft layer outside its
+ * expert banks, top_k of its experts, one embedding row, the greedy head, the
+ * draft layer's KV positions).  MX_EUNSUPPORTED without an MTP layer. */
+mx_status mx_engine_draft_bytes(mx_engine* e, int32_t pos, double* bytes);
 /* Measurement hook (no reference counterpart): the expert gate/up kernels of
  * all MoE layers launched back to back on the routing and activations of the
  * last step, then all down kernels, each group between two events on the

@@ -211,6 +211,8 @@ def _load() -> C.CDLL:
                                            C.POINTER(QWeightC), C.POINTER(QWeightC), vp, vp, vp,
                                            vp, vp, vp, vp], i32),
         "mx_engine_profile_step": ([vp, vp, vp, i32, vp, C.POINTER(StepProfileC)], i32),
+        "mx_engine_profile_verify": ([vp, i32, vp, i32, vp, C.POINTER(StepProfileC)], i32),
+        "mx_engine_draft_bytes": ([vp, i32, C.POINTER(C.c_double)], i32),
         "mx_engine_read": ([vp, C.c_char_p, vp, sz], i32),
         "mx_engine_time_experts": ([vp, i32, C.POINTER(ExpertTimingC)], i32),
         "mx_sched_create": ([C.POINTER(SchedConfigC), C.POINTER(SchedBackendC), C.POINTER(vp)], i32),
@@ -559,6 +561,22 @@ class Engine:
         check(lib.mx_engine_profile_step(self.h, s.ctypes.data, t.ctypes.data, len(s),
                                          out.ctypes.data, C.byref(prof)))
         return out, {f: getattr(prof, f) for f, _ in StepProfileC._fields_}
+
+    def profile_verify(self, slot, tokens):
+        """One eager verify block with per-layer expert-kernel timing; the
+        profile's step_bytes are the block's algorithmic bytes."""
+        t = self._u32(tokens)
+        out = np.empty(len(t), np.uint32)
+        prof = StepProfileC()
+        check(lib.mx_engine_profile_verify(self.h, slot, t.ctypes.data, len(t), out.ctypes.data,
+                                           C.byref(prof)))
+        return out, {f: getattr(prof, f) for f, _ in StepProfileC._fields_}
+
+    def draft_bytes(self, pos) -> float:
+        """Algorithmic bytes of one MTP draft step at cache position pos."""
+        b = C.c_double(0.0)
+        check(lib.mx_engine_draft_bytes(self.h, pos, C.byref(b)))
+        return b.value
 
     def time_experts(self, rows):
         """Expert kernels of all MoE layers back to back (totals and bytes)."""

@@ -778,6 +778,27 @@ MX_ABI mx_status mx_engine_profile_step(mx_engine* e, const int32_t* slots, cons
                        "mx_engine_profile_step");
 }
 
+MX_ABI mx_status mx_engine_profile_verify(mx_engine* e, int32_t slot, const uint32_t* tokens,
+                                          int32_t count, uint32_t* argmax, mx_step_profile* out) {
+  MX_CHECK(e && tokens && argmax && out, MX_EINVAL, "mx_engine_profile_verify: null pointer");
+  MX_CHECK(slot_ok(*e->impl, slot), MX_EINVAL, "mx_engine_profile_verify: slot out of range");
+  MX_CHECK(count >= 1 && count <= engine_config(*e->impl).max_verify, MX_EUNSUPPORTED,
+           "mx_engine_profile_verify: count must be in 1..max_verify");
+  MX_CHECK(tokens_ok(*e->impl, tokens, count), MX_EINVAL,
+           "mx_engine_profile_verify: token outside vocabulary");
+  std::string err;
+  return engine_status(engine_profile_verify(*e->impl, slot, tokens, count, argmax, out, &err),
+                       err, "mx_engine_profile_verify");
+}
+
+MX_ABI mx_status mx_engine_draft_bytes(mx_engine* e, int32_t pos, double* bytes) {
+  MX_CHECK(e && bytes, MX_EINVAL, "mx_engine_draft_bytes: null pointer");
+  MX_CHECK(pos >= 0, MX_EINVAL, "mx_engine_draft_bytes: negative position");
+  std::string err;
+  return engine_status(engine_draft_bytes(*e->impl, pos, bytes, &err), err,
+                       "mx_engine_draft_bytes");
+}
+
 MX_ABI mx_status mx_qmm(const mx_qweight* w, const uint16_t* x, int32_t m, uint16_t* y,
                         void* stream) {
   MX_CHECK(w != nullptr && x != nullptr && y != nullptr, MX_EINVAL, "mx_qmm: null pointer");

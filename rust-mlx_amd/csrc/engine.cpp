@@ -155,6 +155,7 @@ struct Engine {
   int exact_parts = 0;
   // profiling (eager steps only): events around each layer's expert kernels
   mx_step_profile* prof = nullptr;
+  double prof_routed = 0.0;  // profiled steps: routed expert bytes, summed over layers
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
 
   ~Engine();
@@ -546,6 +547,7 @@ int profile_experts(Engine& e, const LayerW& L, int rows) {
   p.gate_up_bytes += double(distinct) * 2.0 * double(qw_bytes(g)) +
                      double(qw_bytes(L.sgate) + qw_bytes(L.sup));
   p.down_bytes += double(distinct) * double(qw_bytes(d)) + double(qw_bytes(L.sdown));
+  e.prof_routed += double(distinct) * (2.0 * double(qw_bytes(g)) + double(qw_bytes(d)));
   return MX_OK;
 }
 
@@ -1238,18 +1240,23 @@ int engine_read(Engine& e, const char* what, void* host, size_t bytes, std::stri
 // every weight outside the expert banks, the distinct experts' weights, the
 // embedding rows, GDN state and conv window read + write, and the KV
 // positions each row attends to.
-double step_bytes(const Engine& e, int rows, const int32_t* pos, double distinct_sum) {
-  const auto& c = e.cfg;
+// Bytes of the tensors under `prefix` outside the routed expert banks.
+double dense_bytes(const Engine& e, const char* prefix) {
   double dense = 0.0;
   for (const auto& kv : e.tensors) {
     const std::string& n = kv.first;
-    if (n.rfind("layers.", 0) != 0 && n.rfind("mixer.", 0) != 0 && n.rfind("head.", 0) != 0)
-      continue;
+    if (n.rfind(prefix, 0) != 0) continue;
     if (n.find(".moe.gate.") != std::string::npos || n.find(".moe.up.") != std::string::npos ||
         n.find(".moe.down.") != std::string::npos)
       continue;
     dense += double(kv.second.bytes);
   }
+  return dense;
+}
+
+double step_bytes(const Engine& e, int rows, const int32_t* pos, double distinct_sum) {
+  const auto& c = e.cfg;
+  const double dense = dense_bytes(e, "layers.") + dense_bytes(e, "mixer.") + dense_bytes(e, "head.");
   double experts = 0.0;
   if (!e.layers.empty()) {
     const LayerW& L = e.layers[0];
@@ -1295,6 +1302,80 @@ int engine_profile_step(Engine& e, const int32_t* slots, const uint32_t* tokens,
   if (rc != MX_OK) return rc;
   out->step_ms = ms;
   out->step_bytes = step_bytes(e, rows, pos, out->distinct_experts);
+  return MX_OK;
+}
+
+// Algorithmic bytes of one verify block of `count` tokens of one slot that
+// starts at position `base` (each distinct byte once): every weight outside
+// the expert banks, the routed experts the block touches (`routed`), the
+// embedding rows, the GDN state read once and written after every token (the
+// verify history), the conv window read and written, and the KV positions up
+// to the block's last.
+double verify_bytes(const Engine& e, int count, int base, double routed) {
+  const auto& c = e.cfg;
+  const double dense = dense_bytes(e, "layers.") + dense_bytes(e, "mixer.") + dense_bytes(e, "head.");
+  const double embed_rows = double(count) * double(c.hidden) * (c.embed_bits / 8.0 + 4.0 / c.group_size);
+  const double state = double(e.n_gdn) * (double(c.gdn_hv) * c.gdn_dk * c.gdn_dv * 4.0 * (1 + count) +
+                                          double(c.conv_k - 1) * e.cd * 2.0 * 2.0);
+  const double kv = double(base + count) * e.n_attn * c.kv_heads * c.head_dim * 2.0 * 2.0;
+  return dense + routed + embed_rows + state + kv;
+}
+
+// Algorithmic bytes of one MTP draft step of one row at position `pos`: the
+// draft layer's weights outside its expert banks, top_k routed experts of its
+// bank, the embedding row, the shared greedy head and the draft layer's KV
+// positions.
+double draft_bytes(const Engine& e, int pos) {
+  const auto& c = e.cfg;
+  const LayerW& L = e.mtp.layer;
+  const QWeight g{L.gate.codes, L.gate.scales, L.gate.biases, L.gate.n, L.gate.k, L.gate.bits,
+                  L.gate.group_size};
+  const QWeight d{L.down.codes, L.down.scales, L.down.biases, L.down.n, L.down.k, L.down.bits,
+                  L.down.group_size};
+  const double layer = dense_bytes(e, "mtp.layer.") + dense_bytes(e, "mtp.norm_") +
+                       dense_bytes(e, "mtp.fc_") + dense_bytes(e, "mtp.mixer.");
+  const double experts = double(c.top_k) * (2.0 * double(qw_bytes(g)) + double(qw_bytes(d)));
+  const double embed_row = double(c.hidden) * (c.embed_bits / 8.0 + 4.0 / c.group_size);
+  const double kv = double(pos + 1) * c.kv_heads * c.head_dim * 2.0 * 2.0;
+  return layer + experts + embed_row + dense_bytes(e, "head.") + kv;
+}
+
+int engine_profile_verify(Engine& e, int slot, const uint32_t* tokens, int count, uint32_t* next,
+                          mx_step_profile* out, std::string* err) {
+  std::memset(out, 0, sizeof(*out));
+  out->rows = count;
+  const int base = e.offsets[slot];
+  for (auto& ev : e.ev)
+    if (!ev) MX_HIP(hipEventCreate(&ev));
+  hipEvent_t t0, t1;
+  MX_HIP(hipEventCreate(&t0));
+  MX_HIP(hipEventCreate(&t1));
+  const bool graphs = e.use_graphs;
+  e.use_graphs = false;
+  e.prof = out;
+  e.prof_routed = 0.0;
+  MX_HIP(hipEventRecord(t0, e.stream));
+  const int rc = engine_verify(e, slot, tokens, count, next, err);
+  e.prof = nullptr;
+  e.use_graphs = graphs;
+  MX_HIP(hipEventRecord(t1, e.stream));
+  MX_HIP(hipEventSynchronize(t1));
+  float ms = 0.0f;
+  MX_HIP(hipEventElapsedTime(&ms, t0, t1));
+  hipEventDestroy(t0);
+  hipEventDestroy(t1);
+  if (rc != MX_OK) return rc;
+  out->step_ms = ms;
+  out->step_bytes = verify_bytes(e, count, base, e.prof_routed);
+  return MX_OK;
+}
+
+int engine_draft_bytes(const Engine& e, int pos, double* bytes, std::string* err) {
+  if (!e.has_mtp) {
+    *err = "the model has no MTP layer (mtp = 0)";
+    return MX_EUNSUPPORTED;
+  }
+  *bytes = draft_bytes(e, pos);
   return MX_OK;
 }
 

@@ -321,6 +321,9 @@ int engine_fill_slot(Engine& e, int slot, int length, uint64_t seed, std::string
 int engine_time_experts(Engine& e, int rows, mx_expert_timing* out, std::string* err);
 int engine_profile_step(Engine& e, const int32_t* slots, const uint32_t* tokens, int rows,
                         uint32_t* next, mx_step_profile* out, std::string* err);
+int engine_profile_verify(Engine& e, int slot, const uint32_t* tokens, int count, uint32_t* next,
+                          mx_step_profile* out, std::string* err);
+int engine_draft_bytes(const Engine& e, int pos, double* bytes, std::string* err);
 void engine_set_flags(Engine& e, int want_logits, int use_graphs, int exact, int exact_parts);
 const mx_model_config& engine_config(const Engine& e);
 int engine_gdn_layers(const Engine& e);
