@@ -74,17 +74,6 @@ __global__ __launch_bounds__(256) void conv_kernel(const uint16_t* __restrict__ 
   for (int j = 0; j < taps - 1; ++j) st[size_t(j) * channels] = f32_to_bf16(win[j]);
 }
 
-// Sum over the 128 threads of the block: xor butterfly inside each wave, then
-// wave 0's total + wave 1's total.  Every thread returns the same bits.
-__device__ __forceinline__ float block_sum128(float v, float* red) {
-  for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o, 64);
-  const int wave = threadIdx.x >> 6;
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[wave] = v;
-  __syncthreads();
-  return red[0] + red[1];
-}
-
 constexpr int kD = 128;  // head dim handled by the recurrence kernel (Dk == Dv == 128)
 
 // Inputs of the delta rule for one token: either computed from the conv
@@ -119,22 +108,44 @@ struct ScanArgs {
 };
 
 // ---------------------------------------------------------------------------
-// Delta-rule scan for one (group, value head).  Thread i owns value row i of
-// the head: its 128 state values live in registers for all t tokens.
+// Delta-rule scan for one (group, value head), in the fixed order of the CPU
+// oracle: per value column i, the key-row dot products are four fma chains
+// c_r over the key rows d = r mod 4 (ascending), joined as (c0 + c1) +
+// (c2 + c3).  512 threads: wave w owns value columns 16 w .. 16 w + 15, lane
+// l = 16 r + c column 16 w + c over the key rows d = 4 m + r, m = 0 .. 31
+// (chain r), so each thread holds 32 state values and the two joins are the
+// lane exchanges l ^ 16 then l ^ 32 (fp32 addition commutes, so all four
+// parts end with the oracle's bits).  Sums over 128 values (the q / k L2
+// norms, the gated norm) are the oracle's two 64-lane xor butterflies, over
+// values 0 .. 63 and 64 .. 127, added.  State loads stay coalesced in 64-byte
+// runs (four key rows of 16 columns per wave load).
+constexpr int kExactParts = 4;
+constexpr int kExactRows = kD / kExactParts;  // key rows per thread
+constexpr int kExactThreads = kD * kExactParts;
+
+__device__ __forceinline__ float xor_butterfly64(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o, 64);
+  return v;
+}
+
 template <bool FUSED>
-__global__ __launch_bounds__(kD) void recurrence_kernel(ScanArgs p) {
+__global__ __launch_bounds__(kExactThreads) void recurrence_kernel(ScanArgs p) {
   const int hv = blockIdx.x;
   const int g = blockIdx.y;
-  const int i = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 15, part = lane >> 4;
+  const int i = wave * 16 + c;  // value column
   const int hv_heads = p.hv_heads, hk_heads = p.hk_heads;
   const int hk = hv / (hv_heads / hk_heads);
-  __shared__ float qs[kD], ks[kD], red[2];
+  __shared__ float qs[kD], ks[kD], ys[kD], red[1];
   __shared__ __align__(16) uint16_t yb[kD];  // the head's y row (plane only)
 
-  float* sp = p.state + (size_t(p.slots[g]) * hv_heads + hv) * kD * kD + i;
-  float s[kD];
+  const size_t my_off = size_t(part) * kD + i;
+  float* sp = p.state + (size_t(p.slots[g]) * hv_heads + hv) * kD * kD + my_off;
+  float s[kExactRows];  // s[m]: key row 4 m + part of column i
 #pragma unroll
-  for (int d = 0; d < kD; ++d) s[d] = sp[size_t(d) * kD];
+  for (int m = 0; m < kExactRows; ++m) s[m] = sp[size_t(m) * kExactParts * kD];
 
   const float eps_l2 = round_bf16(1e-6f);
   const float qscale = round_bf16(0.08838834764831845f);  // bf16(Dk^-1/2), Dk = 128
@@ -148,81 +159,94 @@ __global__ __launch_bounds__(kD) void recurrence_kernel(ScanArgs p) {
   for (int step = 0; step < p.t; ++step) {
     const size_t row = size_t(g) * p.t + step;
     float vi, beta, gdecay;
+    // LDS of the previous token (qs, ks, ys, red, yb) is read by every wave
+    // before this barrier
+    __syncthreads();
     if constexpr (FUSED) {
       const uint16_t* cr = p.conv_out + row * p.conv_stride;
-      const float qi = bf16_to_f32(cr[hk * kD + i]);
-      const float ki = bf16_to_f32(cr[(hk_heads + hk) * kD + i]);
+      if (wave == 0) {
+        const float q0 = bf16_to_f32(cr[hk * kD + lane]);
+        const float q1 = bf16_to_f32(cr[hk * kD + 64 + lane]);
+        const float k0 = bf16_to_f32(cr[(hk_heads + hk) * kD + lane]);
+        const float k1 = bf16_to_f32(cr[(hk_heads + hk) * kD + 64 + lane]);
+        // x * rsqrt(sum(x^2) + eps) with bf16 operations (hybrid.rs:409-413)
+        const float qss = round_bf16(xor_butterfly64(round_bf16(q0 * q0)) +
+                                     xor_butterfly64(round_bf16(q1 * q1)));
+        const float kss = round_bf16(xor_butterfly64(round_bf16(k0 * k0)) +
+                                     xor_butterfly64(round_bf16(k1 * k1)));
+        const float rq = round_bf16(1.0f / __builtin_sqrtf(round_bf16(qss + eps_l2)));
+        const float rk = round_bf16(1.0f / __builtin_sqrtf(round_bf16(kss + eps_l2)));
+        qs[lane] = round_bf16(round_bf16(q0 * rq) * qscale);
+        qs[64 + lane] = round_bf16(round_bf16(q1 * rq) * qscale);
+        ks[lane] = round_bf16(k0 * rk);
+        ks[64 + lane] = round_bf16(k1 * rk);
+      }
       vi = bf16_to_f32(cr[2 * hk_heads * kD + hv * kD + i]);
-      // x * rsqrt(sum(x^2) + eps) with bf16 operations (hybrid.rs:409-413)
-      const float qss = round_bf16(block_sum128(round_bf16(qi * qi), red));
-      const float kss = round_bf16(block_sum128(round_bf16(ki * ki), red));
-      const float rq = round_bf16(1.0f / __builtin_sqrtf(round_bf16(qss + eps_l2)));
-      const float rk = round_bf16(1.0f / __builtin_sqrtf(round_bf16(kss + eps_l2)));
-      __syncthreads();
-      qs[i] = round_bf16(round_bf16(qi * rq) * qscale);
-      ks[i] = round_bf16(ki * rk);
       beta = sigmoid_bf16(bf16_to_f32(p.b[row * p.zab_stride + hv]));
       const float x = round_bf16(bf16_to_f32(p.a[row * p.zab_stride + hv]) + dt);
       gdecay = expf_(neg_a * softplus_bf16(x));
     } else {
-      __syncthreads();
-      qs[i] = bf16_to_f32(p.q[(row * hk_heads + hk) * kD + i]);
-      ks[i] = bf16_to_f32(p.k[(row * hk_heads + hk) * kD + i]);
+      if (wave == 0) {
+        const uint16_t* qr = p.q + (row * hk_heads + hk) * kD;
+        const uint16_t* kr = p.k + (row * hk_heads + hk) * kD;
+        qs[lane] = bf16_to_f32(qr[lane]);
+        qs[64 + lane] = bf16_to_f32(qr[64 + lane]);
+        ks[lane] = bf16_to_f32(kr[lane]);
+        ks[64 + lane] = bf16_to_f32(kr[64 + lane]);
+      }
       vi = bf16_to_f32(p.v[(row * hv_heads + hv) * kD + i]);
       beta = bf16_to_f32(p.beta[row * hv_heads + hv]);
       gdecay = p.g[row * hv_heads + hv];
     }
     __syncthreads();
 
-    // state *= g; kv = sum_d s[d] k[d] (four interleaved fma chains)
-    float c0 = 0.0f, c1 = 0.0f, c2 = 0.0f, c3 = 0.0f;
+    // state *= g; chain `part` of kv = sum_d s[d] k[d]
+    float cp = 0.0f;
 #pragma unroll
-    for (int d = 0; d < kD; d += 4) {
-      s[d] = s[d] * gdecay;
-      s[d + 1] = s[d + 1] * gdecay;
-      s[d + 2] = s[d + 2] * gdecay;
-      s[d + 3] = s[d + 3] * gdecay;
-      c0 = fmaf_(s[d], ks[d], c0);
-      c1 = fmaf_(s[d + 1], ks[d + 1], c1);
-      c2 = fmaf_(s[d + 2], ks[d + 2], c2);
-      c3 = fmaf_(s[d + 3], ks[d + 3], c3);
+    for (int m = 0; m < kExactRows; ++m) {
+      s[m] = s[m] * gdecay;
+      cp = fmaf_(s[m], ks[kExactParts * m + part], cp);
     }
-    const float kv = (c0 + c1) + (c2 + c3);
+    float kv = cp + __shfl_xor(cp, 16, 64);  // c0 + c1 (parts 0, 1), c2 + c3 (parts 2, 3)
+    kv = kv + __shfl_xor(kv, 32, 64);        // (c0 + c1) + (c2 + c3)
     const float delta = (vi - kv) * beta;
-    float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f;
+    float op = 0.0f;
 #pragma unroll
-    for (int d = 0; d < kD; d += 4) {
-      s[d] = fmaf_(ks[d], delta, s[d]);
-      s[d + 1] = fmaf_(ks[d + 1], delta, s[d + 1]);
-      s[d + 2] = fmaf_(ks[d + 2], delta, s[d + 2]);
-      s[d + 3] = fmaf_(ks[d + 3], delta, s[d + 3]);
-      o0 = fmaf_(s[d], qs[d], o0);
-      o1 = fmaf_(s[d + 1], qs[d + 1], o1);
-      o2 = fmaf_(s[d + 2], qs[d + 2], o2);
-      o3 = fmaf_(s[d + 3], qs[d + 3], o3);
+    for (int m = 0; m < kExactRows; ++m) {
+      s[m] = fmaf_(ks[kExactParts * m + part], delta, s[m]);
+      op = fmaf_(s[m], qs[kExactParts * m + part], op);
     }
-    const float yo = round_bf16((o0 + o1) + (o2 + o3));
+    float os = op + __shfl_xor(op, 16, 64);
+    os = os + __shfl_xor(os, 32, 64);
+    const float yo = round_bf16(os);
     if (p.history) {
-      float* hp = p.history + ((row * hv_heads + hv) * kD) * kD + i;
+      float* hp = p.history + ((row * hv_heads + hv) * kD) * kD + my_off;
 #pragma unroll
-      for (int d = 0; d < kD; ++d) hp[size_t(d) * kD] = s[d];
+      for (int m = 0; m < kExactRows; ++m) hp[size_t(m) * kExactParts * kD] = s[m];
     }
     uint16_t* yp = p.y + row * (size_t(hv_heads) * kD) + hv * kD + i;
     if constexpr (FUSED) {
       // fast::rms_norm(y, w, eps) then * sigmoid(z) in f32 (hybrid.rs:447-452)
-      const float ss = block_sum128(yo * yo, red);
-      const float inv = 1.0f / __builtin_sqrtf(ss / float(kD) + p.eps);
+      if (part == 0) ys[i] = yo;
+      __syncthreads();
+      if (wave == 0) {
+        const float y0 = ys[lane], y1 = ys[64 + lane];
+        const float ss = xor_butterfly64(y0 * y0) + xor_butterfly64(y1 * y1);
+        if (lane == 0) red[0] = ss;
+      }
+      __syncthreads();
+      const float inv = 1.0f / __builtin_sqrtf(red[0] / float(kD) + p.eps);
       const float normed = round_bf16(nw * round_bf16(yo * inv));
       const float zi = bf16_to_f32(p.z[row * p.zab_stride + hv * kD + i]);
       const uint16_t yv = f32_to_bf16(normed * sigmoidf_(zi));
-      *yp = yv;
+      if (part == 0) *yp = yv;
       if (p.plane) {
         // the head's two 64-value groups of this row, digitised by wave 0
         // (lanes 16 kb + gl, gl < 2), for the output projection
-        yb[i] = yv;
+        if (part == 0) yb[i] = yv;
         __syncthreads();
-        const int lane = i & 63, kb = lane >> 4, gl = lane & 15;
-        if (i < 64) {
+        if (wave == 0) {
+          const int kb = lane >> 4, gl = lane & 15;
           float f[16];
           const bool unit = gl < kD / xq::kGroup;
 #pragma unroll
@@ -231,14 +255,13 @@ __global__ __launch_bounds__(kD) void recurrence_kernel(ScanArgs p) {
           xq::digitize_unit(f, int(row), hv * (kD / xq::kGroup) + (unit ? gl : 0), kb, unit,
                             p.plane, hv_heads * (kD / xq::kGroup));
         }
-        __syncthreads();
       }
     } else {
-      *yp = f32_to_bf16(yo);
+      if (part == 0) *yp = f32_to_bf16(yo);
     }
   }
 #pragma unroll
-  for (int d = 0; d < kD; ++d) sp[size_t(d) * kD] = s[d];
+  for (int m = 0; m < kExactRows; ++m) sp[size_t(m) * kExactParts * kD] = s[m];
 }
 
 // ---------------------------------------------------------------------------
@@ -487,7 +510,7 @@ int gdn_recurrence(const uint16_t* conv_out, int64_t conv_stride, const uint16_t
   p.hk_heads = d.hk; p.hv_heads = d.hv; p.t = t; p.slots = slots; p.state = state;
   p.history = history; p.y = y;
   p.plane = groups * t <= 8 ? plane : nullptr;
-  hipLaunchKernelGGL(recurrence_kernel<true>, dim3(d.hv, groups), dim3(kD), 0, s, p);
+  hipLaunchKernelGGL(recurrence_kernel<true>, dim3(d.hv, groups), dim3(kExactThreads), 0, s, p);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 
@@ -499,7 +522,7 @@ int gdn_scan(const uint16_t* q, const uint16_t* k, const uint16_t* v, const floa
   p.q = q; p.k = k; p.v = v; p.g = g; p.beta = beta;
   p.hk_heads = d.hk; p.hv_heads = d.hv; p.t = t; p.slots = slots; p.state = state;
   p.history = history; p.y = y;
-  hipLaunchKernelGGL(recurrence_kernel<false>, dim3(d.hv, groups), dim3(kD), 0, s, p);
+  hipLaunchKernelGGL(recurrence_kernel<false>, dim3(d.hv, groups), dim3(kExactThreads), 0, s, p);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 
