@@ -61,6 +61,12 @@ def test_layer_entry_points_reject_bad_geometry_without_device(mx):
     assert mx.lib.mx_head_argmax(C.byref(head), fake, 0, fake, fake, None) == mx.MX_EUNSUPPORTED
     assert mx.lib.mx_head_workspace_bytes(151936, 2048, 8) > 0
     assert mx.lib.mx_moe_workspace_bytes(8, 10, 512) >= 8 * 11 * 512 * 2
+    # engine measurement hooks: null engine or outputs are refused
+    prof = mx.StepProfileC()
+    tok = (C.c_uint32 * 4)(1, 2, 3, 4)
+    out = (C.c_uint32 * 4)()
+    assert mx.lib.mx_engine_profile_verify(None, 0, tok, 4, out, C.byref(prof)) == mx.MX_EINVAL
+    assert mx.lib.mx_engine_draft_bytes(None, 0, None) == mx.MX_EINVAL
 
 
 def test_noalloc_head_refuses_oversized_heads_without_device(mx):

@@ -88,3 +88,46 @@ def test_fast_speculation_is_lossless(mx, vocab, depth):
             assert st["accepted"] > 0, st
     finally:
         eng.close()
+
+
+def test_verify_profile_and_draft_bytes(mx):
+    """The measurement hooks of the config-4 bench line: a profiled verify
+    block predicts what an unprofiled one does, a one-token profiled verify
+    counts the bytes of a one-row profiled decode step on the same state and
+    routing (weights, routed experts, embedding row, state read + one state
+    write, KV), and a draft step's bytes grow by one KV position per
+    position."""
+    cfg = dict(mx.TINY, mtp=1, seed=5)
+    eng = mx.Engine(cfg)
+    try:
+        eng.set_flags(exact=True)
+        prompt = [int(t) for t in np.random.default_rng(5).integers(0, cfg["vocab"], 21)]
+        nxt = eng.prefill(0, prompt)
+        eng.clone(0, 1)
+        eng.clone(0, 2)
+        block = [nxt, 3, 7, 11]
+        want = eng.verify(0, block)
+        eng.commit(0, 2)
+        got, prof = eng.profile_verify(1, block)
+        eng.commit(1, 2)
+        assert [int(t) for t in got] == [int(t) for t in want]
+        assert prof["layers"] == cfg["layers"] and prof["step_bytes"] > 0
+        assert prof["distinct_experts"] <= cfg["layers"] * min(len(block) * cfg["top_k"],
+                                                              cfg["experts"])
+        assert eng.offset(0) == eng.offset(1) == len(prompt) + 2
+        # one token: the verify block's bytes equal a decode step's
+        _, one = eng.profile_verify(2, [nxt])
+        eng.commit(2, 1)
+        eng.reset(2)
+        nxt2 = eng.prefill(2, prompt)
+        assert nxt2 == nxt
+        _, step = eng.profile_step([2], [nxt])
+        assert step["distinct_experts"] == one["distinct_experts"]
+        assert step["step_bytes"] == pytest.approx(one["step_bytes"], rel=1e-12)
+        # draft steps: the KV term grows by kv_heads * head_dim * 2 tensors * 2 B
+        # per position
+        d0, d1 = eng.draft_bytes(100), eng.draft_bytes(150)
+        assert d1 - d0 == pytest.approx(50 * cfg["kv_heads"] * cfg["head_dim"] * 4, rel=1e-12)
+        assert 0 < d0 < prof["step_bytes"]
+    finally:
+        eng.close()
