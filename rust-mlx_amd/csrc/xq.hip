@@ -413,16 +413,41 @@ void xq_gate_up_kernel(
   const uint32_t* crow = mw.codes + row * (size_t(hidden) * BITS / 32);
   const uint16_t* srow = mw.scales + size_t(row) * G;
   const uint16_t* brow = mw.biases + size_t(row) * G;
-  xq::Codes<BITS> c[D][B];
-  xq::ScaleBias<B> sb[D];
+  // RM (4-bit, whole batches of 8 groups): the weight stream is read in
+  // row-major lane order, lane 4 r + q taking 16 bytes of tile row r (piece q
+  // of a pair of groups) and the scale and bias words of groups 2q, 2q + 1 of
+  // the batch, so each four adjacent lanes read contiguous bytes of one row;
+  // ds_bpermute then gives lane 16 kb + j the matrix-core operand of row j
+  // (the words load_codes would have read), so every product is unchanged.
+  constexpr bool RM = BITS == 4 && FULL && B == 8;
+  const int q4 = lane & 3;
+  const int lrow = min(i0 + 16 * t + (lane >> 2), inter - 1);
+  const uint32_t* lcrow = mw.codes + lrow * (size_t(hidden) * BITS / 32);
+  const uint16_t* lsrow = mw.scales + size_t(lrow) * G;
+  const uint16_t* lbrow = mw.biases + size_t(lrow) * G;
+  xq::Codes<BITS> c[RM ? 1 : D][B];
+  xq::ScaleBias<B> sb[RM ? 1 : D];
+  uint4 rc[RM ? D : 1][B / 2];
+  uint32_t rs[RM ? D : 1], rb[RM ? D : 1];
   auto load_batch = [&](int buf, int bi) {
     const int g0 = bi * B;
+    if constexpr (RM) {
 #pragma unroll
-    for (int i = 0; i < B; ++i) xq::load_codes<BITS>(crow, min(g0 + i, G - 1), kb, c[buf][i]);
-    if constexpr (FULL)
-      xq::load_scale_bias_vec<B>(srow, brow, g0, sb[buf]);
-    else
-      xq::load_scale_bias<B>(srow, brow, min(g0, G - 1), G, sbv, sb[buf]);
+      for (int pp = 0; pp < B / 2; ++pp)
+        rc[buf][pp] = *reinterpret_cast<const uint4*>(lcrow + 8 * (g0 + 2 * pp) + 4 * q4);
+      rs[buf] = *reinterpret_cast<const uint32_t*>(lsrow + g0 + 2 * q4);
+      rb[buf] = *reinterpret_cast<const uint32_t*>(lbrow + g0 + 2 * q4);
+    } else {
+#pragma unroll
+      for (int i = 0; i < B; ++i) xq::load_codes<BITS>(crow, min(g0 + i, G - 1), kb, c[buf][i]);
+      if constexpr (FULL)
+        xq::load_scale_bias_vec<B>(srow, brow, g0, sb[buf]);
+      else
+        xq::load_scale_bias<B>(srow, brow, min(g0, G - 1), G, sbv, sb[buf]);
+    }
+  };
+  auto bperm = [](int src_lane, uint32_t v) {
+    return uint32_t(__builtin_amdgcn_ds_bpermute(src_lane << 2, int(v)));
   };
   // operand addresses: group g's A operand at ab + g * gstride; Q and Eb of
   // the lane's activation row at qb[8 g], eb[8 g]
@@ -467,6 +492,8 @@ void xq_gate_up_kernel(
   // the up waves' rounded values: [tile][lane]
   float* xch = reinterpret_cast<float*>(lds + ((xch_at + 15) & ~15));
   double tot = 0.0, acc = 0.0;
+  xq::ScaleBias<B> sbr;   // RM: the batch's scales and biases of row j
+  xq::Codes<BITS> cp[2];  // RM: the current pair of groups' codes of row j
 #pragma unroll
   for (int bi = 0; bi < NB; ++bi) {
     const int buf = bi % D;
@@ -474,9 +501,41 @@ void xq_gate_up_kernel(
     for (int i = 0; i < B; ++i) {
       const int gl = bi * B + i;
       if (FULL || gl < G) {
+        xq::Codes<BITS> ci;
+        double sc, bs;
+        if constexpr (RM) {
+          if (i == 0) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+              sbr.s[w] = bperm(4 * j + w, rs[buf]);
+              sbr.b[w] = bperm(4 * j + w, rb[buf]);
+            }
+          }
+          if ((i & 1) == 0) {
+            // group gl: words 2 kb, 2 kb + 1 of the row's 32 bytes, in piece
+            // kb / 2 (lane 4 j + kb / 2); group gl + 1 in piece 2 + kb / 2
+            const uint4 r = rc[buf][i >> 1];
+            const int s0 = 4 * j + (kb >> 1), s1 = s0 + 2;
+            const bool odd = kb & 1;
+            const uint32_t a0 = bperm(s0, r.x), a1 = bperm(s0, r.y);
+            const uint32_t a2 = bperm(s0, r.z), a3 = bperm(s0, r.w);
+            const uint32_t b0 = bperm(s1, r.x), b1 = bperm(s1, r.y);
+            const uint32_t b2 = bperm(s1, r.z), b3 = bperm(s1, r.w);
+            cp[0].w[0] = odd ? a2 : a0;
+            cp[0].w[1] = odd ? a3 : a1;
+            cp[1].w[0] = odd ? b2 : b0;
+            cp[1].w[1] = odd ? b3 : b1;
+          }
+          ci = cp[i & 1];
+          sc = sbr.scale(i);
+          bs = sbr.bias(i);
+        } else {
+          ci = c[buf][i];
+          sc = sb[buf].scale(i);
+          bs = sb[buf].bias(i);
+        }
         xq::group_step1<BITS>(*reinterpret_cast<const xq::v4i*>(ab + gl * gstride),
-                              xq::b_operand<BITS>(c[buf][i]), qb[gl * 8], eb[gl * 8],
-                              sb[buf].scale(i), sb[buf].bias(i), acc);
+                              xq::b_operand<BITS>(ci), qb[gl * 8], eb[gl * 8], sc, bs, acc);
         // a slice ends after its second group, or after the last of an odd count
         if ((gl & 1) || (!FULL && gl + 1 == G)) {
           tot = tot + acc;
