@@ -124,6 +124,14 @@ __host__ __device__ constexpr int tiles_lds(int G, int T, int KS, int SRC) {
   return b > 16 ? b : 16;
 }
 
+// The weight row read by a lane in row-major order (lane 4 r + q: row r of
+// its tile), for the RM form of xq_tiles.
+struct RmRows {
+  const uint32_t* codes = nullptr;
+  const uint16_t* scales = nullptr;
+  const uint16_t* biases = nullptr;
+};
+
 // The projection values of one workgroup.  Wave (t, ks) streams the weight
 // row of its lane (crow / srow / brow: tile t's row l % 16) over slices
 // [ks SPW, ks SPW + SPW) (two groups each) against activation rows
@@ -133,29 +141,56 @@ __host__ __device__ constexpr int tiles_lds(int G, int T, int KS, int SRC) {
 // slice sums meet in LDS and are added in slice order.  yt[m][t * 16 + j]
 // receives the fp32 result of activation row m and tile row j.  `pre` runs
 // once the first weight loads are issued.  Ends with a barrier.
-template <int BITS, int T, int KS, int SPW, int SRC, class Rows, class Pre>
+// RM (4-bit codes, batches of 8 groups; the launcher checks that every wave's
+// groups are whole batches and the scale/bias rows 16-byte aligned): the
+// weight stream is read in row-major lane order through `rm` (lane 4 r + q:
+// 16 bytes of row r, piece q of a pair of groups, and the scale and bias
+// words of groups 2q, 2q + 1 of the batch), so each four adjacent lanes read
+// contiguous bytes, and ds_bpermute hands lane 16 kb + j the words that
+// load_codes / load_scale_bias would have read for row j: the products are
+// unchanged.
+template <int BITS, int T, int KS, int SPW, int SRC, bool RM = false, class Rows, class Pre>
 __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
                                          const uint16_t* __restrict__ srow,
                                          const uint16_t* __restrict__ brow, bool sbv, int K,
                                          int M, int blocks, const Rows& xr, const char* plane,
-                                         char* lds, float* yt, Pre&& pre) {
+                                         char* lds, float* yt, Pre&& pre,
+                                         const RmRows& rm = RmRows{}) {
   constexpr int NC = 16 * T, NT = 64 * T * KS;
   constexpr int NG = 2 * SPW;
   constexpr int B = tile_batch<BITS, SPW>();
   constexpr int NB = NG / B;
+  constexpr bool R = RM && BITS == 4 && B == 8;
   const int lane = threadIdx.x & 63, j = lane & 15, kb = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int t = wave / KS, ks = wave - t * KS;
   const int G = K / xq::kGroup, S = (G + 1) / 2;
   const int gbeg = 2 * ks * SPW, gend = min(gbeg + NG, G);
-  xq::Codes<BITS> c[2][B];
-  xq::ScaleBias<B> sb[2];
+  const int q4 = lane & 3;
+  xq::Codes<BITS> c[R ? 1 : 2][B];
+  xq::ScaleBias<B> sb[R ? 1 : 2];
+  uint4 rc[R ? 2 : 1][B / 2 > 0 ? B / 2 : 1];
+  uint32_t rs[R ? 2 : 1], rb[R ? 2 : 1];
   auto load_batch = [&](int buf, int bi) {
+    if constexpr (R) {
+      const int g0 = gbeg + bi * B;
 #pragma unroll
-    for (int i = 0; i < B; ++i)
-      xq::load_codes<BITS>(crow, min(gbeg + bi * B + i, gend - 1), kb, c[buf][i]);
-    xq::load_scale_bias<B>(srow, brow, gbeg + bi * B, gend, sbv, sb[buf]);
+      for (int pp = 0; pp < B / 2; ++pp)
+        rc[buf][pp] = *reinterpret_cast<const uint4*>(rm.codes + 8 * (g0 + 2 * pp) + 4 * q4);
+      rs[buf] = *reinterpret_cast<const uint32_t*>(rm.scales + g0 + 2 * q4);
+      rb[buf] = *reinterpret_cast<const uint32_t*>(rm.biases + g0 + 2 * q4);
+    } else {
+#pragma unroll
+      for (int i = 0; i < B; ++i)
+        xq::load_codes<BITS>(crow, min(gbeg + bi * B + i, gend - 1), kb, c[buf][i]);
+      xq::load_scale_bias<B>(srow, brow, gbeg + bi * B, gend, sbv, sb[buf]);
+    }
   };
+  auto bperm = [](int src_lane, uint32_t v) {
+    return uint32_t(__builtin_amdgcn_ds_bpermute(src_lane << 2, int(v)));
+  };
+  xq::ScaleBias<B> sbr;   // R: the batch's scales and biases of row j
+  xq::Codes<BITS> cp[2];  // R: the current pair of groups' codes of row j
   load_batch(0, 0);
   if constexpr (NB > 1) load_batch(1, 1);
   pre();
@@ -239,8 +274,41 @@ __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
           e0 = es[g * 8 + kb];
           e1 = es[g * 8 + 4 + kb];
         }
-        xq::group_step<BITS>(a0, a1, blocks, xq::b_operand<BITS>(c[buf][i]), q0, q1, e0, e1,
-                             sb[buf].scale(i), sb[buf].bias(i), acc);
+        xq::Codes<BITS> ci;
+        double sc, bs;
+        if constexpr (R) {
+          if (i == 0) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+              sbr.s[w] = bperm(4 * j + w, rs[buf]);
+              sbr.b[w] = bperm(4 * j + w, rb[buf]);
+            }
+          }
+          if ((i & 1) == 0) {
+            // group g: words 2 kb, 2 kb + 1 of the row's 32 bytes, in piece
+            // kb / 2 (lane 4 j + kb / 2); group g + 1 in piece 2 + kb / 2
+            const uint4 r = rc[buf][i >> 1];
+            const int s0 = 4 * j + (kb >> 1), s1 = s0 + 2;
+            const bool odd = kb & 1;
+            const uint32_t x0 = bperm(s0, r.x), x1 = bperm(s0, r.y);
+            const uint32_t x2 = bperm(s0, r.z), x3 = bperm(s0, r.w);
+            const uint32_t y0 = bperm(s1, r.x), y1 = bperm(s1, r.y);
+            const uint32_t y2 = bperm(s1, r.z), y3 = bperm(s1, r.w);
+            cp[0].w[0] = odd ? x2 : x0;
+            cp[0].w[1] = odd ? x3 : x1;
+            cp[1].w[0] = odd ? y2 : y0;
+            cp[1].w[1] = odd ? y3 : y1;
+          }
+          ci = cp[i & 1];
+          sc = sbr.scale(i);
+          bs = sbr.bias(i);
+        } else {
+          ci = c[buf][i];
+          sc = sb[buf].scale(i);
+          bs = sb[buf].bias(i);
+        }
+        xq::group_step<BITS>(a0, a1, blocks, xq::b_operand<BITS>(ci), q0, q1, e0, e1, sc, bs,
+                             acc);
         if constexpr (SRC == kSrcPlane) {
           if (gl + PD < NG) load_op(gl + PD, pf[gl % PD]);
         }
@@ -293,7 +361,7 @@ __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
 // tg*16T .. tg*16T + 16T - 1 (tile t: rows tg*16T + 16t + j); for kHcUpMix
 // (T = 4) it covers columns tg*16 .. tg*16 + 15 of the four streams (tile t:
 // rows t*H + tg*16 + j).
-template <int BITS, int MODE, int T, int KS, int SPW, int SRC>
+template <int BITS, int MODE, int T, int KS, int SPW, int SRC, bool RM = false>
 __global__ __launch_bounds__(64 * T * KS) void xq_dense_kernel(QWeight w,
                                                                const uint16_t* __restrict__ x,
                                                                int64_t x_stride, int M,
@@ -305,11 +373,21 @@ __global__ __launch_bounds__(64 * T * KS) void xq_dense_kernel(QWeight w,
   const int tg = blockIdx.x;
   const int j = threadIdx.x & 15, t = (threadIdx.x >> 6) / KS;
   const int n = w.n, G = w.k / xq::kGroup;
-  int row;
-  if constexpr (MODE == kHcUpMix)
+  int row, lrow;  // the lane's tile row, and its row-major load row (RM)
+  const int jr = (threadIdx.x & 63) >> 2;
+  if constexpr (MODE == kHcUpMix) {
     row = t * e.hidden + min(tg * 16 + j, e.hidden - 1);
-  else
+    lrow = t * e.hidden + min(tg * 16 + jr, e.hidden - 1);
+  } else {
     row = min(tg * NC + t * 16 + j, n - 1);
+    lrow = min(tg * NC + t * 16 + jr, n - 1);
+  }
+  RmRows rm;
+  if constexpr (RM) {
+    rm.codes = w.codes + size_t(lrow) * (size_t(w.k) * BITS / 32);
+    rm.scales = w.scales + size_t(lrow) * G;
+    rm.biases = w.biases + size_t(lrow) * G;
+  }
   ProjFinish<MODE, NC, NT> fin;
   int blocks = M > 4 ? 3 : 1;
   if constexpr (SRC == kSrcBlockLds) {
@@ -319,11 +397,11 @@ __global__ __launch_bounds__(64 * T * KS) void xq_dense_kernel(QWeight w,
     fin.m_hi = fin.m_lo + 4;
   }
   fin.begin(e, tg, M, n);
-  xq_tiles<BITS, T, KS, SPW, SRC>(w.codes + size_t(row) * (size_t(w.k) * BITS / 32),
-                                  w.scales + size_t(row) * G, w.biases + size_t(row) * G,
-                                  tiles_sbv<BITS, SPW>(w), w.k, M, blocks,
-                                  XRows{x, x_stride}, plane, lds, yt,
-                                  [&] { fin.prefetch(e); });
+  xq_tiles<BITS, T, KS, SPW, SRC, RM>(w.codes + size_t(row) * (size_t(w.k) * BITS / 32),
+                                      w.scales + size_t(row) * G, w.biases + size_t(row) * G,
+                                      tiles_sbv<BITS, SPW>(w), w.k, M, blocks,
+                                      XRows{x, x_stride}, plane, lds, yt,
+                                      [&] { fin.prefetch(e); }, rm);
   fin.finish(yt, e, tg, M, n);
 }
 
@@ -747,7 +825,16 @@ int launch_xq(const QWeight& w, const uint16_t* x, int64_t xs, int m, const char
               const ProjEpilogue& e, hipStream_t s) {
   const int groups = MODE == kHcUpMix ? (e.hidden + 15) / 16 : (w.n + 16 * T - 1) / (16 * T);
   const int lb = tiles_lds(w.k / xq::kGroup, T, KS, SRC);
-  const auto fn = xq_dense_kernel<BITS, MODE, T, KS, SPW, SRC>;
+  auto fn = xq_dense_kernel<BITS, MODE, T, KS, SPW, SRC, false>;
+  if constexpr (BITS == 4 && tile_batch<BITS, SPW>() == 8) {
+    // row-major weight reads: the KS waves of a tile cover the depth in whole
+    // batches of 8 groups (no wave reads past its row), rows and scale/bias
+    // rows on 16-byte boundaries
+    const int G = w.k / xq::kGroup;
+    const bool rm = G == KS * 2 * SPW && (reinterpret_cast<uintptr_t>(w.codes) & 15) == 0 &&
+                    (size_t(w.k) * BITS / 8) % 16 == 0 && xq::sb_vector_ok<8>(w.scales, w.biases, G);
+    if (rm) fn = xq_dense_kernel<BITS, MODE, T, KS, SPW, SRC, true>;
+  }
   MX_TRY_RC(raise_lds(fn, lb));
   const int nblk = SRC == kSrcBlockLds && m > 4 ? 2 : 1;
   hipLaunchKernelGGL(fn, dim3(groups, nblk), dim3(64 * T * KS), lb, s, w, x, xs, m, plane, e);
