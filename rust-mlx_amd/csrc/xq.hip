@@ -141,11 +141,12 @@ struct RmRows {
 // slice sums meet in LDS and are added in slice order.  yt[m][t * 16 + j]
 // receives the fp32 result of activation row m and tile row j.  `pre` runs
 // once the first weight loads are issued.  Ends with a barrier.
-// RM (4-bit codes, batches of 8 groups; the launcher checks that every wave's
-// groups are whole batches and the scale/bias rows 16-byte aligned): the
-// weight stream is read in row-major lane order through `rm` (lane 4 r + q:
-// 16 bytes of row r, piece q of a pair of groups, and the scale and bias
-// words of groups 2q, 2q + 1 of the batch), so each four adjacent lanes read
+// RM (4-bit codes, batches of an even number of groups; the launcher checks
+// that every wave's groups are whole batches and the scale/bias rows
+// aligned): the weight stream is read in row-major lane order through `rm`
+// (lane 4 r + q: 16 bytes of row r, piece q of a pair of groups, and the
+// scale and bias words of groups 2q, 2q + 1 of the batch), so each four
+// adjacent lanes read
 // contiguous bytes, and ds_bpermute hands lane 16 kb + j the words that
 // load_codes / load_scale_bias would have read for row j: the products are
 // unchanged.
@@ -160,7 +161,7 @@ __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
   constexpr int NG = 2 * SPW;
   constexpr int B = tile_batch<BITS, SPW>();
   constexpr int NB = NG / B;
-  constexpr bool R = RM && BITS == 4 && B == 8;
+  constexpr bool R = RM && BITS == 4 && B % 2 == 0;
   const int lane = threadIdx.x & 63, j = lane & 15, kb = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int t = wave / KS, ks = wave - t * KS;
@@ -177,8 +178,10 @@ __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
 #pragma unroll
       for (int pp = 0; pp < B / 2; ++pp)
         rc[buf][pp] = *reinterpret_cast<const uint4*>(rm.codes + 8 * (g0 + 2 * pp) + 4 * q4);
-      rs[buf] = *reinterpret_cast<const uint32_t*>(rm.scales + g0 + 2 * q4);
-      rb[buf] = *reinterpret_cast<const uint32_t*>(rm.biases + g0 + 2 * q4);
+      // B / 2 scale (bias) words per row; lanes past them repeat the last
+      const int qw = q4 & (B / 2 > 0 ? B / 2 - 1 : 0);
+      rs[buf] = *reinterpret_cast<const uint32_t*>(rm.scales + g0 + 2 * qw);
+      rb[buf] = *reinterpret_cast<const uint32_t*>(rm.biases + g0 + 2 * qw);
     } else {
 #pragma unroll
       for (int i = 0; i < B; ++i)
@@ -279,7 +282,7 @@ __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
         if constexpr (R) {
           if (i == 0) {
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
+            for (int w = 0; w < B / 2; ++w) {
               sbr.s[w] = bperm(4 * j + w, rs[buf]);
               sbr.b[w] = bperm(4 * j + w, rb[buf]);
             }
@@ -704,7 +707,7 @@ __global__ __launch_bounds__(64 * kDnTiles) void xq_down_kernel(const uint16_t* 
 // s * H + 64 tg + 16 ct + j (K = the rank); each column takes the kHcUpMix
 // arithmetic of ProjFinish, then wave 0 writes the group's operand plane, so
 // every consumer of `mixed` reads its operands ready-made.
-template <int BITS, int SPW>
+template <int BITS, int SPW, bool RM = false>
 __global__ __launch_bounds__(1024) void xq_upmix_kernel(QWeight w, const uint16_t* __restrict__ lo,
                                                         int M, const uint16_t* __restrict__ xn,
                                                         int hidden, uint16_t* __restrict__ mixed,
@@ -716,16 +719,23 @@ __global__ __launch_bounds__(1024) void xq_upmix_kernel(QWeight w, const uint16_
   const int j = threadIdx.x & 15, t = threadIdx.x >> 6;
   const int row = (t >> 2) * hidden + tg * 64 + (t & 3) * 16 + j;
   const int G = w.k / xq::kGroup;
+  RmRows rm;
+  if constexpr (RM) {
+    // the lane's row-major load row: tile row (lane & 63) / 4
+    const int lrow = (t >> 2) * hidden + tg * 64 + (t & 3) * 16 + ((threadIdx.x & 63) >> 2);
+    rm.codes = w.codes + size_t(lrow) * (size_t(w.k) * BITS / 32);
+    rm.scales = w.scales + size_t(lrow) * G;
+    rm.biases = w.biases + size_t(lrow) * G;
+  }
   // two workgroups per column group when there are two four-row blocks of
   // activation rows: blockIdx.y = the block this one computes and writes
   const bool split = gridDim.y > 1;
   const int mlo = split ? 4 * int(blockIdx.y) : 0, mhi = split ? mlo + 4 : 8;
-  xq_tiles<BITS, 16, 1, SPW, kSrcStage>(w.codes + size_t(row) * (size_t(w.k) * BITS / 32),
-                                        w.scales + size_t(row) * G, w.biases + size_t(row) * G,
-                                        tiles_sbv<BITS, SPW>(w), w.k, M,
-                                        split ? 1 << blockIdx.y : (M > 4 ? 3 : 1),
-                                        XRows{lo, w.k}, nullptr, lds, yt,
-                                        [] {});
+  xq_tiles<BITS, 16, 1, SPW, kSrcStage, RM>(w.codes + size_t(row) * (size_t(w.k) * BITS / 32),
+                                            w.scales + size_t(row) * G, w.biases + size_t(row) * G,
+                                            tiles_sbv<BITS, SPW>(w), w.k, M,
+                                            split ? 1 << blockIdx.y : (M > 4 ? 3 : 1),
+                                            XRows{lo, w.k}, nullptr, lds, yt, [] {}, rm);
   for (int i = threadIdx.x; i < 8 * 64; i += 1024) {
     const int m = i >> 6, c = i & 63;
     float v = 0.0f;
@@ -826,13 +836,14 @@ int launch_xq(const QWeight& w, const uint16_t* x, int64_t xs, int m, const char
   const int groups = MODE == kHcUpMix ? (e.hidden + 15) / 16 : (w.n + 16 * T - 1) / (16 * T);
   const int lb = tiles_lds(w.k / xq::kGroup, T, KS, SRC);
   auto fn = xq_dense_kernel<BITS, MODE, T, KS, SPW, SRC, false>;
-  if constexpr (BITS == 4 && tile_batch<BITS, SPW>() == 8) {
+  constexpr int B = tile_batch<BITS, SPW>();
+  if constexpr (BITS == 4 && B % 2 == 0) {
     // row-major weight reads: the KS waves of a tile cover the depth in whole
-    // batches of 8 groups (no wave reads past its row), rows and scale/bias
-    // rows on 16-byte boundaries
+    // batches (no wave reads past its row), rows on 16-byte boundaries, the
+    // scale/bias rows aligned for B-group reads
     const int G = w.k / xq::kGroup;
     const bool rm = G == KS * 2 * SPW && (reinterpret_cast<uintptr_t>(w.codes) & 15) == 0 &&
-                    (size_t(w.k) * BITS / 8) % 16 == 0 && xq::sb_vector_ok<8>(w.scales, w.biases, G);
+                    (size_t(w.k) * BITS / 8) % 16 == 0 && xq::sb_vector_ok<B>(w.scales, w.biases, G);
     if (rm) fn = xq_dense_kernel<BITS, MODE, T, KS, SPW, SRC, true>;
   }
   MX_TRY_RC(raise_lds(fn, lb));
@@ -1031,10 +1042,19 @@ int xq_upmix(const QWeight& up, const uint16_t* lo, int m, const uint16_t* xn, i
   const int lb = tiles_lds(G, 16, 1, kSrcStage);
   const dim3 grid(hidden / 64, m > 4 ? 2 : 1);
   const int spw = whole_spw(up.k);
+  // row-major weight reads (4-bit): the tile's waves cover the depth in whole
+  // batches, rows on 16-byte boundaries, scale/bias rows aligned
+  const bool rm = up.bits == 4 && G == 2 * spw && (reinterpret_cast<uintptr_t>(up.codes) & 15) == 0 &&
+                  (size_t(up.k) * 4 / 8) % 16 == 0;
 #define MX_UM(B, SPW)                                                                           \
   if (up.bits == B && spw == SPW) {                                                             \
-    hipLaunchKernelGGL((xq_upmix_kernel<B, SPW>), grid, dim3(1024), lb, s, up, lo, m, xn, hidden, \
-                       mixed, mixed_plane);                                                     \
+    if (B == 4 && rm &&                                                                         \
+        xq::sb_vector_ok<tile_batch<B, SPW>()>(up.scales, up.biases, G))                         \
+      hipLaunchKernelGGL((xq_upmix_kernel<B, SPW, B == 4>), grid, dim3(1024), lb, s, up, lo, m,  \
+                         xn, hidden, mixed, mixed_plane);                                       \
+    else                                                                                        \
+      hipLaunchKernelGGL((xq_upmix_kernel<B, SPW, false>), grid, dim3(1024), lb, s, up, lo, m,   \
+                         xn, hidden, mixed, mixed_plane);                                       \
     return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;                                   \
   }
   MX_UM(4, 1) MX_UM(4, 2) MX_UM(4, 4) MX_UM(5, 1) MX_UM(5, 2) MX_UM(5, 4)
