@@ -161,7 +161,9 @@ __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
   constexpr int NG = 2 * SPW;
   constexpr int B = tile_batch<BITS, SPW>();
   constexpr int NB = NG / B;
-  constexpr bool R = RM && BITS == 4 && B % 2 == 0;
+  // 4-bit: pairs of groups per 16-byte piece; 8-bit: one group's 16 bytes
+  // per lane, so the move is a pure lane permutation
+  constexpr bool R = RM && ((BITS == 4 && B % 2 == 0) || BITS == 8);
   const int lane = threadIdx.x & 63, j = lane & 15, kb = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int t = wave / KS, ks = wave - t * KS;
@@ -170,14 +172,19 @@ __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
   const int q4 = lane & 3;
   xq::Codes<BITS> c[R ? 1 : 2][B];
   xq::ScaleBias<B> sb[R ? 1 : 2];
-  uint4 rc[R ? 2 : 1][B / 2 > 0 ? B / 2 : 1];
+  constexpr int NP = BITS == 8 ? B : (B / 2 > 0 ? B / 2 : 1);  // 16-byte pieces per batch
+  uint4 rc[R ? 2 : 1][NP];
   uint32_t rs[R ? 2 : 1], rb[R ? 2 : 1];
   auto load_batch = [&](int buf, int bi) {
     if constexpr (R) {
       const int g0 = gbeg + bi * B;
 #pragma unroll
-      for (int pp = 0; pp < B / 2; ++pp)
-        rc[buf][pp] = *reinterpret_cast<const uint4*>(rm.codes + 8 * (g0 + 2 * pp) + 4 * q4);
+      for (int pp = 0; pp < NP; ++pp) {
+        if constexpr (BITS == 8)  // piece q of group g0 + pp
+          rc[buf][pp] = *reinterpret_cast<const uint4*>(rm.codes + 16 * (g0 + pp) + 4 * q4);
+        else  // piece q of groups g0 + 2 pp, + 1
+          rc[buf][pp] = *reinterpret_cast<const uint4*>(rm.codes + 8 * (g0 + 2 * pp) + 4 * q4);
+      }
       // B / 2 scale (bias) words per row; lanes past them repeat the last
       const int qw = q4 & (B / 2 > 0 ? B / 2 - 1 : 0);
       rs[buf] = *reinterpret_cast<const uint32_t*>(rm.scales + g0 + 2 * qw);
@@ -287,7 +294,15 @@ __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
               sbr.b[w] = bperm(4 * j + w, rb[buf]);
             }
           }
-          if ((i & 1) == 0) {
+          if constexpr (BITS == 8) {
+            // group g: piece kb of row j (lane 4 j + kb)
+            const uint4 r = rc[buf][i];
+            const int s0 = 4 * j + kb;
+            ci.w[0] = bperm(s0, r.x);
+            ci.w[1] = bperm(s0, r.y);
+            ci.w[2] = bperm(s0, r.z);
+            ci.w[3] = bperm(s0, r.w);
+          } else if ((i & 1) == 0) {
             // group g: words 2 kb, 2 kb + 1 of the row's 32 bytes, in piece
             // kb / 2 (lane 4 j + kb / 2); group g + 1 in piece 2 + kb / 2
             const uint4 r = rc[buf][i >> 1];
@@ -302,7 +317,7 @@ __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
             cp[1].w[0] = odd ? y2 : y0;
             cp[1].w[1] = odd ? y3 : y1;
           }
-          ci = cp[i & 1];
+          if constexpr (BITS == 4) ci = cp[i & 1];
           sc = sbr.scale(i);
           bs = sbr.bias(i);
         } else {
@@ -778,7 +793,7 @@ __device__ __forceinline__ void better_of(float v, uint32_t id, float& best, uin
 // workgroup's 256 vocabulary rows (16 waves, each streaming a 16-row tile
 // over the whole depth; NaN never wins; nothing above -inf keeps id
 // 0xffffffff), and, when asked, the bf16 logits themselves.
-template <int BITS, int SPW, int SRC>
+template <int BITS, int SPW, int SRC, bool RM = false>
 __global__ __launch_bounds__(1024) void xq_head_kernel(QWeight w, const uint16_t* __restrict__ x,
                                                        const char* __restrict__ plane, int M,
                                                        float* __restrict__ maxima,
@@ -792,10 +807,18 @@ __global__ __launch_bounds__(1024) void xq_head_kernel(QWeight w, const uint16_t
   const int j = threadIdx.x & 15, t = threadIdx.x >> 6;
   const int n = w.n, G = w.k / xq::kGroup;
   const int row = min(tg * 256 + 16 * t + j, n - 1);
-  xq_tiles<BITS, 16, 1, SPW, SRC>(w.codes + size_t(row) * (size_t(w.k) * BITS / 32),
-                                  w.scales + size_t(row) * G, w.biases + size_t(row) * G,
-                                  tiles_sbv<BITS, SPW>(w), w.k, M, M > 4 ? 3 : 1, XRows{x, w.k},
-                                  plane, lds, yt, [] {});
+  RmRows rm;
+  if constexpr (RM) {
+    // the lane's row-major load row: tile row (lane & 63) / 4
+    const int lrow = min(tg * 256 + 16 * t + ((threadIdx.x & 63) >> 2), n - 1);
+    rm.codes = w.codes + size_t(lrow) * (size_t(w.k) * BITS / 32);
+    rm.scales = w.scales + size_t(lrow) * G;
+    rm.biases = w.biases + size_t(lrow) * G;
+  }
+  xq_tiles<BITS, 16, 1, SPW, SRC, RM>(w.codes + size_t(row) * (size_t(w.k) * BITS / 32),
+                                      w.scales + size_t(row) * G, w.biases + size_t(row) * G,
+                                      tiles_sbv<BITS, SPW>(w), w.k, M, M > 4 ? 3 : 1,
+                                      XRows{x, w.k}, plane, lds, yt, [] {}, rm);
   // wave t ranks columns 16 t .. +15 for every row (lane = 16 m' + c, two
   // passes of four rows), then wave 0 ranks the 16 wave bests per row
   const int lane = threadIdx.x & 63;
@@ -967,7 +990,19 @@ template <int BITS, int SPW>
 int launch_head(const QWeight& w, const uint16_t* x, const char* plane, int m, float* maxima,
                 uint32_t* indices, uint16_t* logits, int parts, hipStream_t s) {
   const int G = w.k / xq::kGroup;
-  if (plane) {
+  constexpr int B = tile_batch<BITS, SPW>();
+  // row-major weight reads (8-bit; 4-bit with even batches): whole batches
+  // over the depth, rows on 16-byte boundaries, scale/bias rows aligned
+  const bool rm = (BITS == 8 || (BITS == 4 && B % 2 == 0)) && G == 2 * SPW &&
+                  (reinterpret_cast<uintptr_t>(w.codes) & 15) == 0 &&
+                  (size_t(w.k) * BITS / 8) % 16 == 0 && B > 1 &&
+                  xq::sb_vector_ok<(B > 1 ? B : 2)>(w.scales, w.biases, G);
+  if (plane && rm && (BITS == 8 || BITS == 4)) {
+    const auto fn = xq_head_kernel<BITS, SPW, kSrcPlaneLds, BITS == 8 || BITS == 4>;
+    const int lb = tiles_lds(G, 16, 1, kSrcPlaneLds);
+    MX_TRY_RC(raise_lds(fn, lb));
+    hipLaunchKernelGGL(fn, dim3(parts), dim3(1024), lb, s, w, x, plane, m, maxima, indices, logits);
+  } else if (plane) {
     const auto fn = xq_head_kernel<BITS, SPW, kSrcPlaneLds>;
     const int lb = tiles_lds(G, 16, 1, kSrcPlaneLds);
     MX_TRY_RC(raise_lds(fn, lb));
