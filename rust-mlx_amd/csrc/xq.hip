@@ -860,7 +860,7 @@ int launch_xq(const QWeight& w, const uint16_t* x, int64_t xs, int m, const char
   const int lb = tiles_lds(w.k / xq::kGroup, T, KS, SRC);
   auto fn = xq_dense_kernel<BITS, MODE, T, KS, SPW, SRC, false>;
   constexpr int B = tile_batch<BITS, SPW>();
-  if constexpr (BITS == 4 && B % 2 == 0) {
+  if constexpr ((BITS == 4 && B % 2 == 0) || (BITS == 8 && B > 1)) {
     // row-major weight reads: the KS waves of a tile cover the depth in whole
     // batches (no wave reads past its row), rows on 16-byte boundaries, the
     // scale/bias rows aligned for B-group reads
