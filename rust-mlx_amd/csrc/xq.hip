@@ -163,7 +163,11 @@ __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
   constexpr int NB = NG / B;
   // 4-bit: pairs of groups per 16-byte piece; 8-bit: one group's 16 bytes
   // per lane, so the move is a pure lane permutation
-  constexpr bool R = RM && ((BITS == 4 && B % 2 == 0) || BITS == 8);
+  // 5 / 6-bit (RG): lane 4 r + q reads the code window load_codes gives
+  // row r and k-block q (adjacent lanes: contiguous bytes of one row), then
+  // the window's words move to lane 16 q + r
+  constexpr bool RG = RM && (BITS == 5 || BITS == 6) && B % 2 == 0;
+  constexpr bool R = RM && ((BITS == 4 && B % 2 == 0) || BITS == 8 || RG);
   const int lane = threadIdx.x & 63, j = lane & 15, kb = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int t = wave / KS, ks = wave - t * KS;
@@ -173,17 +177,22 @@ __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
   xq::Codes<BITS> c[R ? 1 : 2][B];
   xq::ScaleBias<B> sb[R ? 1 : 2];
   constexpr int NP = BITS == 8 ? B : (B / 2 > 0 ? B / 2 : 1);  // 16-byte pieces per batch
-  uint4 rc[R ? 2 : 1][NP];
+  uint4 rc[R && !RG ? 2 : 1][NP];
+  xq::Codes<BITS> rw[RG ? 2 : 1][RG ? B : 1];
   uint32_t rs[R ? 2 : 1], rb[R ? 2 : 1];
   auto load_batch = [&](int buf, int bi) {
     if constexpr (R) {
       const int g0 = gbeg + bi * B;
 #pragma unroll
-      for (int pp = 0; pp < NP; ++pp) {
+      for (int pp = 0; pp < (RG ? 0 : NP); ++pp) {
         if constexpr (BITS == 8)  // piece q of group g0 + pp
           rc[buf][pp] = *reinterpret_cast<const uint4*>(rm.codes + 16 * (g0 + pp) + 4 * q4);
         else  // piece q of groups g0 + 2 pp, + 1
           rc[buf][pp] = *reinterpret_cast<const uint4*>(rm.codes + 8 * (g0 + 2 * pp) + 4 * q4);
+      }
+      if constexpr (RG) {
+#pragma unroll
+        for (int i = 0; i < B; ++i) xq::load_codes<BITS>(rm.codes, g0 + i, q4, rw[buf][i]);
       }
       // B / 2 scale (bias) words per row; lanes past them repeat the last
       const int qw = q4 & (B / 2 > 0 ? B / 2 - 1 : 0);
@@ -294,7 +303,12 @@ __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
               sbr.b[w] = bperm(4 * j + w, rb[buf]);
             }
           }
-          if constexpr (BITS == 8) {
+          if constexpr (RG) {
+            // group g: the window of row j, k-block kb (lane 4 j + kb)
+#pragma unroll
+            for (int w = 0; w < xq::Codes<BITS>::W; ++w)
+              ci.w[w] = bperm(4 * j + kb, rw[buf][i].w[w]);
+          } else if constexpr (BITS == 8) {
             // group g: piece kb of row j (lane 4 j + kb)
             const uint4 r = rc[buf][i];
             const int s0 = 4 * j + kb;
@@ -515,7 +529,11 @@ void xq_gate_up_kernel(
   // the batch, so each four adjacent lanes read contiguous bytes of one row;
   // ds_bpermute then gives lane 16 kb + j the matrix-core operand of row j
   // (the words load_codes would have read), so every product is unchanged.
-  constexpr bool RM = BITS == 4 && FULL && B == 8;
+  // 8-bit: one group's 16 bytes per lane (a pure lane permutation); 5 / 6-bit
+  // (RMG): lane 4 r + q reads the code window load_codes gives row r and
+  // k-block q, and the window's words move to lane 16 q + r
+  constexpr bool RMG = (BITS == 5 || BITS == 6) && FULL && B % 2 == 0;
+  constexpr bool RM = (BITS == 4 && FULL && B == 8) || (BITS == 8 && FULL && B % 2 == 0) || RMG;
   const int q4 = lane & 3;
   const int lrow = min(i0 + 16 * t + (lane >> 2), inter - 1);
   const uint32_t* lcrow = mw.codes + lrow * (size_t(hidden) * BITS / 32);
@@ -523,16 +541,29 @@ void xq_gate_up_kernel(
   const uint16_t* lbrow = mw.biases + size_t(lrow) * G;
   xq::Codes<BITS> c[RM ? 1 : D][B];
   xq::ScaleBias<B> sb[RM ? 1 : D];
-  uint4 rc[RM ? D : 1][B / 2];
+  constexpr int NP = BITS == 8 ? B : B / 2;  // 16-byte pieces per batch (4 / 8-bit)
+  uint4 rc[RM && !RMG ? D : 1][NP > 0 ? NP : 1];
+  xq::Codes<BITS> rw[RMG ? D : 1][RMG ? B : 1];
   uint32_t rs[RM ? D : 1], rb[RM ? D : 1];
   auto load_batch = [&](int buf, int bi) {
     const int g0 = bi * B;
     if constexpr (RM) {
+      if constexpr (RMG) {
 #pragma unroll
-      for (int pp = 0; pp < B / 2; ++pp)
-        rc[buf][pp] = *reinterpret_cast<const uint4*>(lcrow + 8 * (g0 + 2 * pp) + 4 * q4);
-      rs[buf] = *reinterpret_cast<const uint32_t*>(lsrow + g0 + 2 * q4);
-      rb[buf] = *reinterpret_cast<const uint32_t*>(lbrow + g0 + 2 * q4);
+        for (int i = 0; i < B; ++i) xq::load_codes<BITS>(lcrow, g0 + i, q4, rw[buf][i]);
+      } else {
+#pragma unroll
+        for (int pp = 0; pp < NP; ++pp) {
+          if constexpr (BITS == 8)  // piece q of group g0 + pp
+            rc[buf][pp] = *reinterpret_cast<const uint4*>(lcrow + 16 * (g0 + pp) + 4 * q4);
+          else  // piece q of groups g0 + 2 pp, + 1
+            rc[buf][pp] = *reinterpret_cast<const uint4*>(lcrow + 8 * (g0 + 2 * pp) + 4 * q4);
+        }
+      }
+      // B / 2 scale (bias) words per row; lanes past them repeat the last
+      const int qw = q4 & (B / 2 - 1);
+      rs[buf] = *reinterpret_cast<const uint32_t*>(lsrow + g0 + 2 * qw);
+      rb[buf] = *reinterpret_cast<const uint32_t*>(lbrow + g0 + 2 * qw);
     } else {
 #pragma unroll
       for (int i = 0; i < B; ++i) xq::load_codes<BITS>(crow, min(g0 + i, G - 1), kb, c[buf][i]);
@@ -602,12 +633,25 @@ void xq_gate_up_kernel(
         if constexpr (RM) {
           if (i == 0) {
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
+            for (int w = 0; w < B / 2; ++w) {
               sbr.s[w] = bperm(4 * j + w, rs[buf]);
               sbr.b[w] = bperm(4 * j + w, rb[buf]);
             }
           }
-          if ((i & 1) == 0) {
+          if constexpr (RMG) {
+            // group gl: the window of row j, k-block kb (lane 4 j + kb)
+#pragma unroll
+            for (int w = 0; w < xq::Codes<BITS>::W; ++w)
+              ci.w[w] = bperm(4 * j + kb, rw[buf][i].w[w]);
+          } else if constexpr (BITS == 8) {
+            // group gl: piece kb of row j (lane 4 j + kb)
+            const uint4 r = rc[buf][i];
+            const int s0 = 4 * j + kb;
+            ci.w[0] = bperm(s0, r.x);
+            ci.w[1] = bperm(s0, r.y);
+            ci.w[2] = bperm(s0, r.z);
+            ci.w[3] = bperm(s0, r.w);
+          } else if ((i & 1) == 0) {
             // group gl: words 2 kb, 2 kb + 1 of the row's 32 bytes, in piece
             // kb / 2 (lane 4 j + kb / 2); group gl + 1 in piece 2 + kb / 2
             const uint4 r = rc[buf][i >> 1];
@@ -622,7 +666,7 @@ void xq_gate_up_kernel(
             cp[1].w[0] = odd ? b2 : b0;
             cp[1].w[1] = odd ? b3 : b1;
           }
-          ci = cp[i & 1];
+          if constexpr (BITS == 4) ci = cp[i & 1];
           sc = sbr.scale(i);
           bs = sbr.bias(i);
         } else {
@@ -860,13 +904,16 @@ int launch_xq(const QWeight& w, const uint16_t* x, int64_t xs, int m, const char
   const int lb = tiles_lds(w.k / xq::kGroup, T, KS, SRC);
   auto fn = xq_dense_kernel<BITS, MODE, T, KS, SPW, SRC, false>;
   constexpr int B = tile_batch<BITS, SPW>();
-  if constexpr ((BITS == 4 && B % 2 == 0) || (BITS == 8 && B > 1)) {
+  if constexpr (B % 2 == 0) {
     // row-major weight reads: the KS waves of a tile cover the depth in whole
     // batches (no wave reads past its row), rows on 16-byte boundaries, the
     // scale/bias rows aligned for B-group reads
     const int G = w.k / xq::kGroup;
-    const bool rm = G == KS * 2 * SPW && (reinterpret_cast<uintptr_t>(w.codes) & 15) == 0 &&
-                    (size_t(w.k) * BITS / 8) % 16 == 0 && xq::sb_vector_ok<B>(w.scales, w.biases, G);
+    const bool rm = G == KS * 2 * SPW &&
+                    (BITS == 5 || BITS == 6 ||
+                     ((reinterpret_cast<uintptr_t>(w.codes) & 15) == 0 &&
+                      (size_t(w.k) * BITS / 8) % 16 == 0)) &&
+                    xq::sb_vector_ok<B>(w.scales, w.biases, G);
     if (rm) fn = xq_dense_kernel<BITS, MODE, T, KS, SPW, SRC, true>;
   }
   MX_TRY_RC(raise_lds(fn, lb));
@@ -961,7 +1008,11 @@ int launch_gate_up(const uint16_t* x, const char* plane, const MoePlan* plan, in
                     xq::sb_vector_ok<B>(up.scales, up.biases, G) &&
                     xq::sb_vector_ok<B>(sgate.scales, sgate.biases, G) &&
                     xq::sb_vector_ok<B>(sup.scales, sup.biases, G) &&
-                    (size_t(gate.n) * G) % B == 0 && (size_t(up.n) * G) % B == 0;
+                    (size_t(gate.n) * G) % B == 0 && (size_t(up.n) * G) % B == 0 &&
+                    // FULL 4- and 8-bit forms read 16-byte code pieces
+                    ((reinterpret_cast<uintptr_t>(gate.codes) | reinterpret_cast<uintptr_t>(up.codes) |
+                      reinterpret_cast<uintptr_t>(sgate.codes) | reinterpret_cast<uintptr_t>(sup.codes)) &
+                     15) == 0;
   const auto fn = plane ? (full ? xq_gate_up_kernel<BITS, SPW, kSrcPlaneLds, true>
                                 : xq_gate_up_kernel<BITS, SPW, kSrcPlaneLds, false>)
                         : (full ? xq_gate_up_kernel<BITS, SPW, kSrcStage, true>
