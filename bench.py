@@ -98,28 +98,6 @@ def load_package():
     return mod
 
 
-class ProfilerRegion:
-    """roctxProfilerResume/Pause around the timed loop, so that
-    `rocprofv3 --selected-regions` traces the decode steps only (not the
-    engine build or prefill).  A no-op unless --roctx is given."""
-
-    def __init__(self, enabled: bool):
-        self.lib = None
-        if enabled:
-            path = "/opt/rocm/lib/librocprofiler-sdk-roctx.so"
-            self.lib = C.CDLL(path) if os.path.exists(path) else None
-
-    def __enter__(self):
-        if self.lib:
-            self.lib.roctxProfilerResume(0)
-        return self
-
-    def __exit__(self, *exc):
-        if self.lib:
-            self.lib.roctxProfilerPause(0)
-        return False
-
-
 # --------------------------------------------------------------- config 3 --
 def bench_config3(mx, args):
     cfg = dict(mx.CONFIG3)
@@ -152,12 +130,11 @@ def bench_config3(mx, args):
     for _ in range(max(args.warmup - 1, 0)):
         toks = eng.decode_batch(slots, toks, equal=False)
     mx.check(mx.lib.mx_device_sync())
-    with ProfilerRegion(args.roctx):
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            toks = eng.decode_batch(slots, toks, equal=False)
-        mx.check(mx.lib.mx_device_sync())
-        dt = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        toks = eng.decode_batch(slots, toks, equal=False)
+    mx.check(mx.lib.mx_device_sync())
+    dt = time.perf_counter() - t0
     tok_s = rows * args.steps / dt
     ms_step = dt / args.steps * 1e3
     log(f"config3: {args.steps} steps x {rows} rows in {dt:.3f}s -> {tok_s:.1f} tok/s, "
@@ -230,7 +207,7 @@ def bench_config3(mx, args):
         "value": round(tok_s, 2),
         "unit": "tok/s",
         "ms_per_step": ms_step,
-        "dtype": "affine u4/u5/u8 codes x bf16 -> fp32 acc; bf16 activations; fp32 GDN state",
+        "dtype": step_dtype(exact, "u4/u5/u8"),
         "config": {
             "workload": "config3-b8-decode", "model": "synthetic hybrid GDN/attention MoE",
             "layers": cfg["layers"], "hidden": cfg["hidden"], "experts": cfg["experts"],
@@ -261,6 +238,16 @@ def bench_config3(mx, args):
                      "us_per_launch": round(gu_us, 2)},
         "cpu_baseline": cpu,
     }
+
+
+def step_dtype(exact: bool, widths: str) -> str:
+    """The arithmetic the timed step computes in, by mode."""
+    if exact:
+        return (f"affine {widths} codes; bf16 activations as exact integers on a per-group grid "
+                "(int8 matrix-core digits, exact int32 sums), fp64 group combination, one fp32 "
+                "rounding; fp32 GDN state")
+    return (f"affine {widths} codes x bf16 matrix-core products -> fp32 sums; bf16 activations; "
+            "fp32 GDN state")
 
 
 def measured_traffic(summary: str):
@@ -681,7 +668,8 @@ def bench_moe_config2(mx, args):
     return {
         "metric": METRIC, "value": b8["rows_per_s"], "unit": "tok/s (rows per second)",
         "ms_per_step": b8["us"] / 1e3,
-        "dtype": "affine u4 (gate/up, router) / u5 (down) codes x bf16 -> fp32 acc",
+        "dtype": "affine u4 (gate/up, router) / u5 (down) codes x bf16 matrix-core products "
+                 "-> fp32 sums (fast mode)",
         "config": {"workload": "moe-config2", "experts": E, "top_k": k, "hidden": H,
                    "inter": I, "shared_inter": I, "rotated_input_batches": n_x,
                    "per_batch": {str(b_): v for b_, v in per_b.items()}},
@@ -773,8 +761,7 @@ def bench_mtp_config4(mx, args):
     cpu_model = None
     if not args.no_cpu_baseline:
         cpu_model = mtp_cpu_model(mx, eng, cfg, pos)
-    with ProfilerRegion(args.roctx):
-        pred, vprof = eng.profile_verify(0, block)
+    pred, vprof = eng.profile_verify(0, block)
     eng.commit(0, 1)
     draft_b = eng.draft_bytes(pos)
     round_bytes = vprof["step_bytes"] + depth * draft_b
@@ -790,7 +777,7 @@ def bench_mtp_config4(mx, args):
     eng.close()
     return {
         "metric": METRIC, "value": round(n_tok / dt, 2), "unit": "tok/s", "ms_per_step": dt / n_tok * 1e3,
-        "dtype": "affine u4/u5/u6/u8 codes x bf16 -> fp32 acc; bf16 activations; fp32 GDN state",
+        "dtype": step_dtype(exact, "u4/u5/u6/u8"),
         "config": {"workload": "mtp-config4", "model": "synthetic hybrid GDN/attention MoE, mixed widths",
                    "batch": 1, "context": ctx, "generated": n_tok, "draft_depth": depth,
                    "rounds": st["rounds"], "drafted": st["drafted"], "accepted": st["accepted"],
@@ -908,9 +895,6 @@ def main() -> None:
                     help="give the rows random caches of the prompt lengths instead of "
                          "prefilling them (profiling runs: the decode step's cost depends on "
                          "the context length only)")
-    ap.add_argument("--roctx", action="store_true",
-                    help="bracket the timed loop with roctxProfilerResume/Pause "
-                         "(for rocprofv3 --selected-regions)")
     ap.add_argument("--fast", action="store_true",
                     help="config3: time the bf16 matrix-core kernels (within tolerance of the "
                          "oracle, not bit-exact) as the headline path, and the exact path "

@@ -81,6 +81,7 @@ typedef struct mx_gdn_dims {
  * a mixer hyper-connection and a greedy vocabulary head close the stack
  * (reference src/hybrid.rs:12-38 HybridConfig, 500-685 HybridModel).
  * Weights are random affine-quantised tensors drawn from `seed`. */
+#define MX_MAX_LAYERS 128
 typedef struct mx_model_config {
   int32_t hidden;
   int32_t layers;
@@ -100,6 +101,14 @@ typedef struct mx_model_config {
   int32_t max_slots, max_context, max_verify;
   uint64_t seed;
   int32_t mtp;         /* nonzero: one MTP draft layer for speculative generation (config 4) */
+  /* Per-layer widths read from a checkpoint's per-module quantization
+   * (src/weights.rs:70-90), 0 = not given.  Entry 2 i: layer i's projections,
+   * hyper-connections, router and expert / shared-expert gate and up; entry
+   * 2 i + 1: its expert and shared-expert down.  Index `layers` is the MTP
+   * draft layer (its fc_embedding / fc_hidden and draft mixer take entry
+   * 2 layers).  A nonzero entry overrides bits / down_bits and the
+   * mixed_bits draw for that layer. */
+  uint8_t layer_widths[2 * (MX_MAX_LAYERS + 1)];
 } mx_model_config;
 
 typedef struct mx_engine mx_engine;
@@ -582,8 +591,11 @@ mx_status mx_engine_tensor(mx_engine* e, const char* name, void** device_ptr, si
  * [channels, taps, 1] is stored as the engine's fp32 [taps, channels].
  * ".weight" (U32 packed codes), ".scales", ".biases" of a quantised linear
  * must match the engine's width and group size (MX_EUNSUPPORTED names the
- * difference); float tensors of any listed dtype are converted (to bf16 with
- * round-to-nearest-even, or to fp32).  MX_EUNSUPPORTED for modules the
+ * difference).  Float tensors are taken only where the engine keeps their
+ * exact values: into an fp32 tensor (A_log, conv1d.weight) any float dtype;
+ * into a bf16 tensor (scales, biases, norm weights, dt_bias) BF16, or F16 /
+ * F32 whose every value is a bf16 value -- otherwise MX_EUNSUPPORTED names
+ * the tensor and the first value that would round.  MX_EUNSUPPORTED for modules the
  * engine does not build (per-layer n-gram embeddings "ple.", the attention
  * indexer "self_attn.indexer."), MX_EINVAL for unknown names or shapes.  The
  * engine is created from the checkpoint's config.json first (mx_model_config
@@ -604,6 +616,15 @@ mx_status mx_checkpoint_target(const mx_model_config* cfg, const char* name, cha
  * the reference's loader does); *loaded = tensors written.  Stops at the
  * first error. */
 mx_status mx_engine_load_safetensors(mx_engine* e, const char* path, int32_t* loaded);
+/* Every check of mx_engine_load_safetensors without an engine or a device:
+ * the file's header (offsets inside the file, positive dims, bytes matching
+ * shape and dtype), each tensor's target, width, group count and exact float
+ * values for configuration cfg.  *checked = tensors that pass; the first
+ * failure returns its status and names the tensor (mx_last_error).  The
+ * reference loads through MLX (src/weights.rs:22-99) and fails at its first
+ * bad tensor too; this entry lets a caller refuse a checkpoint before it
+ * allocates an engine. */
+mx_status mx_checkpoint_check(const mx_model_config* cfg, const char* path, int32_t* checked);
 
 /* mx_gdn_scan: the delta rule alone, on given inputs — the reference's
  * gdn_kernel::recurrent / recurrent_with_history interface (src/gdn_kernel.rs:7-142):

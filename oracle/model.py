@@ -95,13 +95,19 @@ class Model:
 
     # ---- weights ----
     def layer_bits(self, i):
-        """(projection bits, expert-down bits) of layer i: the base widths, or
-        with mixed_bits a seeded draw from {4,5,6,8} (same rule as the engine)."""
-        if not self.c.get("mixed_bits") or i < 0:
-            return self.c["bits"], self.c["down_bits"]
-        choices = (4, 5, 6, 8)
-        key = (self.c["seed"] ^ 0x5BD1E995) & (2**64 - 1)
-        return tuple(choices[orc.lib.mxo_rng_u64(key, i * 2 + w) & 3] for w in (0, 1))
+        """(projection bits, expert-down bits) of layer i: a checkpoint's width
+        table entry (layer_widths, nonzero), else the base widths, or with
+        mixed_bits a seeded draw from {4,5,6,8} (same rule as the engine)."""
+        table = self.c.get("layer_widths") or []
+
+        def width(w):
+            if i >= 0 and 2 * i + w < len(table) and table[2 * i + w]:
+                return int(table[2 * i + w])
+            if not self.c.get("mixed_bits") or i < 0:
+                return (self.c["bits"], self.c["down_bits"])[w]
+            key = (self.c["seed"] ^ 0x5BD1E995) & (2**64 - 1)
+            return (4, 5, 6, 8)[orc.lib.mxo_rng_u64(key, i * 2 + w) & 3]
+        return width(0), width(1)
 
     def _load_layer(self, p, i, attn):
         c, H, fetch = self.c, self.H, self.fetch
@@ -274,10 +280,28 @@ class Model:
         hidden streams.  Both norms are compiled::norm (src/compiled.rs:22-28)
         in the hyper-connection norm's order, over H and over all hc*H values."""
         c, m = self.c, self.mtp
-        H, hc = self.H, self.hc
         rows = len(tokens)
         self.last_ids = []
         self.last_router = []
+        h = self.mtp_compose(tokens, prev)
+        slots_a = np.full(rows, slot, np.int32)
+        pos_a = np.arange(pos0, pos0 + rows, dtype=np.int32)
+        gdn_slots = np.array([slot * self.n_gdn], np.int32)
+        h = self._run_layer(m["layer"], True, m["cache"], h, rows, slots_a, pos_a, gdn_slots, 1,
+                            rows, None)
+        self.mtp_hidden = h.copy()
+        mixed, _ = self._hc_forward(m["mixer"], h, rows)
+        self.last_mixed = mixed
+        return orc.head_argmax(self.head, mixed)
+
+    def mtp_compose(self, tokens, prev):
+        """The draft layer's input streams (src/mtp.rs:88-104): e =
+        fc_embedding(norm(embedding)) over H; the previous hidden streams
+        normalised together over all hc*H values, then fc_hidden on each
+        stream; h[s] = bf16(e + f[s]).  Also kept as self.mtp_input."""
+        c, m = self.c, self.mtp
+        H, hc = self.H, self.hc
+        rows = len(tokens)
         tok = np.ascontiguousarray(tokens, np.uint32)
         emb = np.empty((rows, H), np.uint16)
         orc.lib.mxo_embed(C.byref(self.embed), _p(tok), rows, 1, _p(emb))
@@ -291,15 +315,8 @@ class Model:
         s32 = orc.bf16_to_f32(e).astype(np.float32)[:, None, :] + \
             orc.bf16_to_f32(f).astype(np.float32).reshape(rows, hc, H)
         h = orc.f32_to_bf16(s32.astype(np.float32)).reshape(rows, hc * H)
-        slots_a = np.full(rows, slot, np.int32)
-        pos_a = np.arange(pos0, pos0 + rows, dtype=np.int32)
-        gdn_slots = np.array([slot * self.n_gdn], np.int32)
-        h = self._run_layer(m["layer"], True, m["cache"], h, rows, slots_a, pos_a, gdn_slots, 1,
-                            rows, None)
-        self.mtp_hidden = h.copy()
-        mixed, _ = self._hc_forward(m["mixer"], h, rows)
-        self.last_mixed = mixed
-        return orc.head_argmax(self.head, mixed)
+        self.mtp_input = h.copy()
+        return h
 
     def generate(self, slot, prompt, max_tokens, depth=0):
         """mx_engine_generate's contract (speculative::generate_prepared,

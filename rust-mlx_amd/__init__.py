@@ -68,6 +68,9 @@ class AttnDimsC(C.Structure):
                 ("max_ctx", C.c_int32), ("slot_stride", C.c_int64)]
 
 
+MAX_LAYERS = 128  # MX_MAX_LAYERS
+
+
 class ModelConfigC(C.Structure):
     _fields_ = [(n, C.c_int32) for n in (
         "hidden", "layers", "attn_every", "vocab", "hc", "hc_rank", "gdn_hk", "gdn_hv", "gdn_dk",
@@ -75,7 +78,21 @@ class ModelConfigC(C.Structure):
         ("rope_theta", C.c_float), ("rms_eps", C.c_float)] + [(n, C.c_int32) for n in (
             "experts", "top_k", "moe_inter", "shared_inter", "bits", "down_bits", "embed_bits",
             "head_bits", "group_size", "mixed_bits", "max_slots", "max_context", "max_verify")] + [
-        ("seed", C.c_uint64), ("mtp", C.c_int32)]
+        ("seed", C.c_uint64), ("mtp", C.c_int32),
+        ("layer_widths", C.c_uint8 * (2 * (MAX_LAYERS + 1)))]
+
+
+def config_c(cfg: dict) -> ModelConfigC:
+    """The mx_model_config of an engine configuration dict (its optional
+    "layer_widths" list fills the per-layer width table, zeros elsewhere)."""
+    d = dict(cfg)
+    widths = d.pop("layer_widths", None) or []
+    cc = ModelConfigC(**d)
+    if len(widths) > 2 * (MAX_LAYERS + 1):
+        raise ValueError("layer_widths longer than the engine's table")
+    for i, w in enumerate(widths):
+        cc.layer_widths[i] = int(w)
+    return cc
 
 
 class GenerateStatsC(C.Structure):
@@ -386,7 +403,7 @@ CONFIG3 = dict(hidden=2048, layers=48, attn_every=4, vocab=151936, hc=4, hc_rank
 def checkpoint_target(cfg: dict, name: str):
     """mx_checkpoint_target: (status, engine tensor name, info dict) for an
     MLX tensor name under configuration cfg, no device needed."""
-    cc = ModelConfigC(**cfg)
+    cc = config_c(cfg)
     buf = C.create_string_buffer(256)
     info = (C.c_int32 * 8)()
     rc = lib.mx_checkpoint_target(C.byref(cc), name.encode(), buf, 256, info)
@@ -394,13 +411,49 @@ def checkpoint_target(cfg: dict, name: str):
     return rc, buf.value.decode(), dict(zip(keys, list(info)))
 
 
+# The quantised modules of one layer by width role (0: projections,
+# hyper-connections, router, expert and shared-expert gate/up; 1: expert and
+# shared-expert down), as the reference names them (src/hybrid.rs:56-66,
+# 130-142, 335-352, 529-567; src/mtp.rs:39-70).  The engine fuses each
+# role's modules of a layer at one width.
+_HC_MODULES = ("input_mix_weight_down", "input_mix_weight_up")
+_ROLE0 = {
+    "linear_attention": ("linear_attn.in_proj_qkv", "linear_attn.in_proj_z", "linear_attn.in_proj_a",
+                         "linear_attn.in_proj_b", "linear_attn.out_proj"),
+    "full_attention": ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj",
+                       "self_attn.o_proj"),
+}
+_MOE0 = ("mlp.gate", "mlp.shared_expert_gate", "mlp.switch_mlp.gate_proj", "mlp.switch_mlp.up_proj",
+         "mlp.shared_expert.gate_proj", "mlp.shared_expert.up_proj")
+_MOE1 = ("mlp.switch_mlp.down_proj", "mlp.shared_expert.down_proj")
+
+
+def _layer_modules(prefix: str, kind: str):
+    """(role, module prefix) of every quantised module of one layer."""
+    out = []
+    for hc in ("attn_hyper_connection", "mlp_hyper_connection"):
+        out += [(0, f"{prefix}.{hc}.{m}") for m in _HC_MODULES + ("block_inject_weight",)]
+    out += [(0, f"{prefix}.{m}") for m in _ROLE0[kind] + _MOE0]
+    out += [(1, f"{prefix}.{m}") for m in _MOE1]
+    return out
+
+
 def config_from_mlx(config: dict, max_slots=8, max_context=4096, max_verify=8, seed=1,
                     mtp=0) -> dict:
     """Engine configuration of an MLX checkpoint's config.json (the fields
     HybridConfig reads, src/hybrid.rs; rope defaults as src/qsa.rs:35-40):
     the layer pattern must repeat k-1 linear-attention layers then one full
-    attention layer; widths come from "quantization" (per-module entries
-    override the default for the expert down, embedding and head)."""
+    attention layer.  Widths come from "quantization": its default, and the
+    per-module entries that override it (src/weights.rs:70-90) for the
+    embedding, the head, and each layer's width table entries
+    (`layer_widths`; the MTP draft layer at index `layers`).  Raises
+    ValueError naming the module when the engine cannot hold a width as
+    given: two modules the engine fuses at one width differ (one width per
+    layer for its projections, hyper-connections, router and expert gate/up;
+    one for its expert and shared-expert down), the mixer differs from the
+    default width, a module's group size differs from the default's, or the
+    mode is not affine.  (The engine itself takes group size 64 only:
+    mx_engine_create refuses others.)"""
     t = config.get("text_config", config)
     q = config.get("quantization") or config.get("quantization_config")
     if not q:
@@ -410,13 +463,51 @@ def config_from_mlx(config: dict, max_slots=8, max_context=4096, max_verify=8, s
     k = types.index("full_attention") + 1
     if n % k or types != (["linear_attention"] * (k - 1) + ["full_attention"]) * (n // k):
         raise ValueError("layer pattern is not (k-1 linear attention, 1 full attention) repeated")
+    if n > MAX_LAYERS:
+        raise ValueError(f"{n} layers: the engine holds at most {MAX_LAYERS}")
+    gs0 = q["group_size"]
+    if q.get("mode", "affine") != "affine":
+        raise ValueError(f"quantization mode {q.get('mode')}: the engine runs affine weights")
 
-    def bits_of(*prefixes):
-        for p in prefixes:
-            if isinstance(q.get(p), dict):
-                return q[p]["bits"]
+    def quant_of(module):
+        """(bits, group size) of a module: its own entry (with or without the
+        language_model. prefix) or the default."""
+        for key in (module, "language_model." + module):
+            e = q.get(key)
+            if isinstance(e, dict):
+                if e.get("mode", "affine") != "affine":
+                    raise ValueError(f"{module}: quantization mode {e.get('mode')} is not affine")
+                if e["group_size"] != gs0:
+                    raise ValueError(f"{module}: group size {e['group_size']}, the engine uses one "
+                                     f"group size for every module ({gs0})")
+                return e["bits"]
         return q["bits"]
 
+    def one_width(modules, what):
+        widths = {}
+        for m in modules:
+            widths.setdefault(quant_of(m), m)
+        if len(widths) > 1:
+            (a, ma), (b, mb) = list(widths.items())[:2]
+            raise ValueError(f"{what}: {ma} is {a}-bit and {mb} is {b}-bit; the engine fuses them "
+                             "at one width")
+        return next(iter(widths))
+
+    table = [0] * (2 * (MAX_LAYERS + 1))
+    for i in range(n):
+        mods = _layer_modules(f"model.layers.{i}", types[i])
+        for role in (0, 1):
+            table[2 * i + role] = one_width([m for r, m in mods if r == role], f"layer {i}")
+    if mtp:
+        mods = _layer_modules("mtp.layers.0", "full_attention")
+        extra = ["mtp.fc_embedding", "mtp.fc_hidden"] + \
+            [f"mtp.hyper_connection_mixer.{m}" for m in _HC_MODULES]
+        table[2 * n] = one_width([m for r, m in mods if r == 0] + extra, "MTP layer")
+        table[2 * n + 1] = one_width([m for r, m in mods if r == 1], "MTP layer")
+    mixer = one_width([f"model.hyper_connection_mixer.{m}" for m in _HC_MODULES], "mixer")
+    if mixer != q["bits"]:
+        raise ValueError(f"model.hyper_connection_mixer: {mixer}-bit, the engine runs the mixer at "
+                         f"the default width ({q['bits']}-bit)")
     rope = t.get("rope_parameters") or {}
     head_dim = t["head_dim"]
     return dict(
@@ -429,13 +520,19 @@ def config_from_mlx(config: dict, max_slots=8, max_context=4096, max_verify=8, s
         rope_theta=float(rope.get("rope_theta", 1e7)), rms_eps=t["rms_norm_eps"],
         experts=t["num_experts"], top_k=t["num_experts_per_tok"],
         moe_inter=t["moe_intermediate_size"], shared_inter=t["shared_expert_intermediate_size"],
-        bits=q["bits"],
-        down_bits=bits_of("language_model.model.layers.0.mlp.switch_mlp.down_proj",
-                          "model.layers.0.mlp.switch_mlp.down_proj"),
-        embed_bits=bits_of("language_model.model.embed_tokens", "model.embed_tokens"),
-        head_bits=bits_of("language_model.lm_head", "lm_head"),
-        group_size=q["group_size"], mixed_bits=0, max_slots=max_slots, max_context=max_context,
-        max_verify=max_verify, seed=seed, mtp=mtp)
+        bits=q["bits"], down_bits=table[1],
+        embed_bits=quant_of("model.embed_tokens"), head_bits=quant_of("lm_head"),
+        group_size=gs0, mixed_bits=0, max_slots=max_slots, max_context=max_context,
+        max_verify=max_verify, seed=seed, mtp=mtp, layer_widths=table)
+
+
+def checkpoint_check(cfg: dict, path) -> int:
+    """mx_checkpoint_check: every check of loading `path` into an engine of
+    configuration cfg, without a device; returns the tensors checked
+    (raises MxError naming the first failing tensor)."""
+    n = C.c_int32()
+    check(lib.mx_checkpoint_check(C.byref(config_c(cfg)), os.fspath(path).encode(), C.byref(n)))
+    return n.value
 
 
 TINY = dict(hidden=256, layers=4, attn_every=4, vocab=1024, hc=4, hc_rank=64, gdn_hk=1, gdn_hv=2,
@@ -450,7 +547,7 @@ class Engine:
 
     def __init__(self, cfg: dict):
         self.cfg = dict(cfg)
-        cc = ModelConfigC(**self.cfg)
+        cc = config_c(self.cfg)
         h = C.c_void_p()
         check(lib.mx_engine_create(C.byref(cc), C.byref(h)))
         self.h = h.value

@@ -2,6 +2,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstring>
+#include <new>
 #include <string>
 
 #include "common.hpp"
@@ -531,9 +532,13 @@ const char* check_config(const mx_model_config& c) {
   if (c.top_k < 1 || c.top_k > 16) return "top_k must be in 1..16";
   if (c.moe_inter <= 0 || c.shared_inter <= 0 || c.moe_inter % 64 || c.shared_inter % 64)
     return "expert intermediate sizes must be positive multiples of 64";
-  if (c.group_size != 32 && c.group_size != 64 && c.group_size != 128) return "bad group_size";
+  if (c.group_size != 64)
+    return "group_size must be 64 (the engine's exact-integer kernels combine 64-value groups)";
+  if (c.layers > MX_MAX_LAYERS) return "layers must be at most MX_MAX_LAYERS";
   for (int b : {c.bits, c.down_bits, c.embed_bits, c.head_bits})
     if (b != 4 && b != 5 && b != 6 && b != 8) return "bits must be 4, 5, 6 or 8";
+  for (int b : c.layer_widths)
+    if (b != 0 && b != 4 && b != 5 && b != 6 && b != 8) return "layer_widths entries must be 0, 4, 5, 6 or 8";
   if (c.max_slots < 1 || c.max_slots > 4096) return "max_slots must be in 1..4096";
   if (c.max_context < 1) return "max_context must be positive";
   if (c.max_verify < 1 || c.max_verify > 8) return "max_verify must be in 1..8";
@@ -727,8 +732,14 @@ MX_ABI mx_status mx_engine_load_tensor(mx_engine* e, const char* name, int32_t d
   MX_CHECK(e && name && shape && data, MX_EINVAL, "mx_engine_load_tensor: null pointer");
   MX_CHECK(dtype >= MX_DT_U32 && dtype <= MX_DT_F32, MX_EINVAL, "mx_engine_load_tensor: bad dtype");
   std::string err;
-  return engine_status(engine_load_tensor(*e->impl, name, dtype, shape, ndim, data, bytes, &err),
-                       err, "mx_engine_load_tensor");
+  try {
+    return engine_status(engine_load_tensor(*e->impl, name, dtype, shape, ndim, data, bytes, &err),
+                         err, "mx_engine_load_tensor");
+  } catch (const std::bad_alloc&) {
+    return mx_status(set_error(MX_ENOMEM, "mx_engine_load_tensor: out of host memory"));
+  } catch (...) {
+    return mx_status(set_error(MX_EINVAL, "mx_engine_load_tensor: failed"));
+  }
 }
 
 MX_ABI mx_status mx_checkpoint_target(const mx_model_config* cfg, const char* name, char* tensor,
@@ -753,9 +764,39 @@ MX_ABI mx_status mx_engine_load_safetensors(mx_engine* e, const char* path, int3
   MX_CHECK(e && path && loaded, MX_EINVAL, "mx_engine_load_safetensors: null pointer");
   std::string err;
   int n = 0;
-  const int rc = engine_load_safetensors(*e->impl, path, &n, &err);
+  int rc;
+  try {
+    rc = engine_load_safetensors(*e->impl, path, &n, &err);
+  } catch (const std::bad_alloc&) {
+    rc = MX_ENOMEM;
+    err = "out of host memory";
+  } catch (...) {
+    rc = MX_EINVAL;
+    err = "failed";
+  }
   *loaded = n;
   return engine_status(rc, err, "mx_engine_load_safetensors");
+}
+
+MX_ABI mx_status mx_checkpoint_check(const mx_model_config* cfg, const char* path,
+                                     int32_t* checked) {
+  MX_CHECK(cfg && path && checked, MX_EINVAL, "mx_checkpoint_check: null pointer");
+  if (const char* err = check_config(*cfg))
+    return mx_status(set_error(MX_EINVAL, std::string("mx_checkpoint_check: ") + err));
+  std::string err;
+  int n = 0;
+  int rc;
+  try {
+    rc = checkpoint_check(*cfg, path, &n, &err);
+  } catch (const std::bad_alloc&) {
+    rc = MX_ENOMEM;
+    err = "out of host memory";
+  } catch (...) {
+    rc = MX_EINVAL;
+    err = "failed";
+  }
+  *checked = n;
+  return engine_status(rc, err, "mx_checkpoint_check");
 }
 
 MX_ABI mx_status mx_engine_time_experts(mx_engine* e, int32_t rows, mx_expert_timing* out) {

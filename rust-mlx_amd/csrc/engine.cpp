@@ -19,6 +19,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <map>
@@ -274,7 +275,10 @@ int make_f32_from_draw(Engine& e, const std::string& name, size_t count, int lay
 
 int layer_bits(const mx_model_config& c, int layer, int which) {
   // which: 0 = main projections, 1 = expert down; tensors outside the layer
-  // stack (layer < 0) always use the base widths
+  // stack (layer < 0) always use the base widths; a checkpoint's width table
+  // overrides the base widths and the mixed_bits draw
+  if (layer >= 0 && layer <= MX_MAX_LAYERS && c.layer_widths[2 * layer + which] != 0)
+    return c.layer_widths[2 * layer + which];
   if (!c.mixed_bits || layer < 0) return which == 0 ? c.bits : c.down_bits;
   static const int choices[4] = {4, 5, 6, 8};
   const uint64_t r = rng_u64(c.seed ^ 0x5bd1e995ull, uint64_t(layer) * 2 + which);
@@ -1625,20 +1629,39 @@ float load_value(const void* data, int dtype, size_t i) {
 
 bool float_dtype(int dtype) { return dtype == MX_DT_BF16 || dtype == MX_DT_F16 || dtype == MX_DT_F32; }
 
-int copy_bf16(const void* data, int dtype, size_t count, uint16_t* dst) {
-  std::vector<uint16_t> v(count);
-  for (size_t i = 0; i < count; ++i)
-    v[i] = dtype == MX_DT_BF16 ? static_cast<const uint16_t*>(data)[i]
-                               : f32_to_bf16(load_value(data, dtype, i));
-  return hipMemcpy(dst, v.data(), count * 2, hipMemcpyHostToDevice) == hipSuccess ? MX_OK : MX_EHIP;
+// The first value of an F16 / F32 tensor that bf16 cannot hold exactly, or -1.
+int64_t first_inexact_bf16(const void* data, int dtype, size_t count) {
+  if (dtype == MX_DT_BF16) return -1;
+  for (size_t i = 0; i < count; ++i) {
+    const float v = load_value(data, dtype, i);
+    uint32_t u;
+    std::memcpy(&u, &v, 4);
+    if (u & 0xffffu) return int64_t(i);
+  }
+  return -1;
 }
 
-}  // namespace
+std::vector<uint16_t> to_bf16(const void* data, int dtype, size_t count) {
+  std::vector<uint16_t> v(count);
+  for (size_t i = 0; i < count; ++i) {
+    if (dtype == MX_DT_BF16) {
+      v[i] = static_cast<const uint16_t*>(data)[i];
+    } else {
+      const float f = load_value(data, dtype, i);
+      uint32_t u;
+      std::memcpy(&u, &f, 4);
+      v[i] = uint16_t(u >> 16);  // exact: first_inexact_bf16 passed
+    }
+  }
+  return v;
+}
 
-int engine_load_tensor(Engine& e, const char* name, int dtype, const int64_t* shape, int ndim,
-                       const void* data, size_t bytes, std::string* err) {
-  CheckpointTarget t;
-  const int rc = checkpoint_target(e.cfg, name, &t);
+// Every check of one tensor that needs no engine: its target, rank, dims,
+// byte count, dtype, width, group count and (with data) exact float values.
+int plan_tensor(const mx_model_config& c, const char* name, int dtype, const int64_t* shape,
+                int ndim, const void* data, size_t bytes, CheckpointTarget* t, size_t* count_out,
+                std::string* err) {
+  const int rc = checkpoint_target(c, name, t);
   if (rc == MX_EUNSUPPORTED) {
     *err = std::string("the engine has no module for tensor ") + name;
     return MX_EUNSUPPORTED;
@@ -1652,84 +1675,129 @@ int engine_load_tensor(Engine& e, const char* name, int dtype, const int64_t* sh
     return MX_EINVAL;
   }
   size_t count = 1;
-  for (int i = 0; i < ndim; ++i) count *= size_t(shape[i]);
+  for (int i = 0; i < ndim; ++i) {
+    if (shape[i] <= 0 || shape[i] > (int64_t(1) << 40)) {
+      *err = std::string(name) + ": dim " + std::to_string(i) + " is " + std::to_string(shape[i]);
+      return MX_EINVAL;
+    }
+    if (count > (size_t(1) << 42) / size_t(shape[i])) {
+      *err = std::string(name) + ": shape too large";
+      return MX_EINVAL;
+    }
+    count *= size_t(shape[i]);
+  }
   const size_t esize = dtype == MX_DT_F32 || dtype == MX_DT_U32 ? 4 : 2;
   if (bytes != count * esize) {
     *err = std::string(name) + ": byte count does not match shape and dtype";
     return MX_EINVAL;
   }
+  *count_out = count;
+  if (t->kind != CheckpointTarget::kQuant) {
+    if (!float_dtype(dtype) || count != t->count) {
+      *err = std::string(name) + ": expected " + std::to_string(t->count) + " float values";
+      return MX_EINVAL;
+    }
+    if (t->kind == CheckpointTarget::kConvW && shape[0] != t->conv_ch) {
+      *err = std::string(name) + ": conv channels differ from the engine's";
+      return MX_EINVAL;
+    }
+  } else {
+    // quantised matrix rows: leading dims flatten into rows (an expert bank
+    // is [experts, n, width]), the last dim is the packed or per-group width
+    const int64_t width = shape[ndim - 1];
+    const int64_t rows = int64_t(count / size_t(width));
+    if (rows != t->rows) {
+      *err = std::string(name) + ": " + std::to_string(rows) + " rows, the engine's matrix takes " +
+             std::to_string(t->rows);
+      return MX_EINVAL;
+    }
+    const int gs = c.group_size;
+    const int64_t words = int64_t(t->k) * t->bits / 32, groups = t->k / gs;
+    if (t->part == 0) {
+      if (dtype != MX_DT_U32) {
+        *err = std::string(name) + ": packed codes must be U32 (unquantised matrices are not supported)";
+        return MX_EUNSUPPORTED;
+      }
+      if (width != words) {
+        *err = std::string(name) + ": " + std::to_string(width * 32 / t->k) +
+               "-bit codes, the engine's matrix is " + std::to_string(t->bits) + "-bit";
+        return MX_EUNSUPPORTED;
+      }
+      return MX_OK;
+    }
+    if (!float_dtype(dtype) || width != groups) {
+      *err = std::string(name) + ": " + std::to_string(width) +
+             " groups per row, the engine's matrix has " + std::to_string(groups) +
+             " (group size " + std::to_string(gs) + ")";
+      return MX_EUNSUPPORTED;
+    }
+  }
+  // bf16 targets keep values exactly or refuse them (never a silent rounding)
+  const bool to_bf16_target = t->kind == CheckpointTarget::kQuant || t->kind == CheckpointTarget::kBf16;
+  if (data && to_bf16_target) {
+    const int64_t bad = first_inexact_bf16(data, dtype, count);
+    if (bad >= 0) {
+      char v[64];
+      std::snprintf(v, sizeof v, "%.9g", double(load_value(data, dtype, size_t(bad))));
+      *err = std::string(name) + ": value " + v + " at index " + std::to_string(bad) +
+             " is not a bf16 value (the engine keeps this tensor in bf16 and does not round it)";
+      return MX_EUNSUPPORTED;
+    }
+  }
+  return MX_OK;
+}
+
+}  // namespace
+
+int engine_load_tensor(Engine& e, const char* name, int dtype, const int64_t* shape, int ndim,
+                       const void* data, size_t bytes, std::string* err) {
+  CheckpointTarget t;
+  size_t count = 0;
+  MX_TRY(plan_tensor(e.cfg, name, dtype, shape, ndim, data, bytes, &t, &count, err));
   auto ptr = [&](const std::string& n) -> void* {
     auto it = e.tensors.find(n);
     return it == e.tensors.end() ? nullptr : it->second.p;
   };
-  if (t.kind != CheckpointTarget::kQuant) {
-    if (!float_dtype(dtype) || count != t.count) {
-      *err = std::string(name) + ": expected " + std::to_string(t.count) + " float values";
-      return MX_EINVAL;
-    }
-    void* dst = ptr(t.tensor);
-    if (!dst) {
-      *err = "engine tensor " + t.tensor + " missing";
-      return MX_EINVAL;
-    }
-    if (t.kind == CheckpointTarget::kBf16)
-      return copy_bf16(data, dtype, count, static_cast<uint16_t*>(dst));
-    std::vector<float> v(count);
-    if (t.kind == CheckpointTarget::kF32) {
-      for (size_t i = 0; i < count; ++i) v[i] = load_value(data, dtype, i);
-    } else {  // MLX conv1d weight [channels, taps, 1] -> [taps][channels]
-      if (shape[0] != t.conv_ch) {
-        *err = std::string(name) + ": conv channels differ from the engine's";
-        return MX_EINVAL;
-      }
-      for (int ch = 0; ch < t.conv_ch; ++ch)
-        for (int j = 0; j < t.taps; ++j)
-          v[size_t(j) * t.conv_ch + ch] = load_value(data, dtype, size_t(ch) * t.taps + j);
-    }
-    return hipMemcpy(dst, v.data(), count * 4, hipMemcpyHostToDevice) == hipSuccess ? MX_OK
-                                                                                  : MX_EHIP;
-  }
-  // quantised matrix rows: leading dims flatten into rows (an expert bank is
-  // [experts, n, width]), the last dim is the packed or per-group width
-  const int64_t width = shape[ndim - 1];
-  const int64_t rows = int64_t(count / size_t(width));
-  if (rows != t.rows) {
-    *err = std::string(name) + ": " + std::to_string(rows) + " rows, the engine's matrix takes " +
-           std::to_string(t.rows);
-    return MX_EINVAL;
-  }
-  const int gs = e.cfg.group_size;
-  const int64_t words = int64_t(t.k) * t.bits / 32, groups = t.k / gs;
-  if (t.part == 0) {
-    if (dtype != MX_DT_U32) {
-      *err = std::string(name) + ": packed codes must be U32 (unquantised matrices are not supported)";
-      return MX_EUNSUPPORTED;
-    }
-    if (width != words) {
-      *err = std::string(name) + ": " + std::to_string(width * 32 / t.k) +
-             "-bit codes, the engine's matrix is " + std::to_string(t.bits) + "-bit";
-      return MX_EUNSUPPORTED;
-    }
-    char* dst = static_cast<char*>(ptr(t.tensor + ".codes"));
-    if (!dst) {
-      *err = "engine tensor " + t.tensor + " missing";
-      return MX_EINVAL;
-    }
-    dst += size_t(t.row0) * words * 4;
-    return hipMemcpy(dst, data, bytes, hipMemcpyHostToDevice) == hipSuccess ? MX_OK : MX_EHIP;
-  }
-  if (!float_dtype(dtype) || width != groups) {
-    *err = std::string(name) + ": " + std::to_string(width) +
-           " groups per row, the engine's matrix has " + std::to_string(groups) +
-           " (group size " + std::to_string(gs) + ")";
-    return MX_EUNSUPPORTED;
-  }
-  uint16_t* base = static_cast<uint16_t*>(ptr(t.tensor + (t.part == 1 ? ".scales" : ".biases")));
-  if (!base) {
+  const char* suffix = t.kind != CheckpointTarget::kQuant ? ""
+                       : t.part == 0                      ? ".codes"
+                       : t.part == 1                      ? ".scales"
+                                                          : ".biases";
+  char* dst = static_cast<char*>(ptr(t.tensor + suffix));
+  if (!dst) {
     *err = "engine tensor " + t.tensor + " missing";
     return MX_EINVAL;
   }
-  return copy_bf16(data, dtype, count, base + size_t(t.row0) * groups);
+  auto put = [&](const void* src, size_t n) {
+    return hipMemcpy(dst, src, n, hipMemcpyHostToDevice) == hipSuccess ? MX_OK : MX_EHIP;
+  };
+  switch (t.kind) {
+    case CheckpointTarget::kBf16: {
+      const std::vector<uint16_t> v = to_bf16(data, dtype, count);
+      return put(v.data(), count * 2);
+    }
+    case CheckpointTarget::kF32: {
+      std::vector<float> v(count);
+      for (size_t i = 0; i < count; ++i) v[i] = load_value(data, dtype, i);
+      return put(v.data(), count * 4);
+    }
+    case CheckpointTarget::kConvW: {  // MLX conv1d weight [channels, taps, 1] -> [taps][channels]
+      std::vector<float> v(count);
+      for (int ch = 0; ch < t.conv_ch; ++ch)
+        for (int j = 0; j < t.taps; ++j)
+          v[size_t(j) * t.conv_ch + ch] = load_value(data, dtype, size_t(ch) * t.taps + j);
+      return put(v.data(), count * 4);
+    }
+    case CheckpointTarget::kQuant:
+      break;
+  }
+  const int64_t words = int64_t(t.k) * t.bits / 32, groups = t.k / e.cfg.group_size;
+  if (t.part == 0) {
+    dst += size_t(t.row0) * words * 4;
+    return put(data, bytes);
+  }
+  dst += size_t(t.row0) * groups * 2;
+  const std::vector<uint16_t> v = to_bf16(data, dtype, count);
+  return put(v.data(), count * 2);
 }
 
 namespace {
@@ -1767,15 +1835,23 @@ struct JsonIn {
   }
   bool num(int64_t* v) {
     ws();
-    char* q = nullptr;
-    *v = std::strtoll(p, &q, 10);
-    if (q == p) return false;
-    p = q;
+    if (p >= end || !(*p == '-' || (*p >= '0' && *p <= '9'))) return false;
+    int64_t x = 0;
+    bool neg = false;
+    if (*p == '-') { neg = true; ++p; }
+    const char* first = p;
+    while (p < end && *p >= '0' && *p <= '9') {
+      if (x > (INT64_MAX - 9) / 10) return false;  // out of range
+      x = x * 10 + (*p - '0');
+      ++p;
+    }
+    if (p == first) return false;
+    *v = neg ? -x : x;
     return true;
   }
-  bool skip() {  // any value
+  bool skip(int depth = 0) {  // any value
     ws();
-    if (p >= end) return false;
+    if (p >= end || depth > 64) return false;
     if (*p == '"') { std::string s; return str(&s); }
     if (*p == '{' || *p == '[') {
       const char open = *p, close = open == '{' ? '}' : ']';
@@ -1786,7 +1862,7 @@ struct JsonIn {
           std::string k;
           if (!str(&k) || !eat(':')) return false;
         }
-        if (!skip()) return false;
+        if (!skip(depth + 1)) return false;
       } while (eat(','));
       return eat(close);
     }
@@ -1798,7 +1874,7 @@ struct JsonIn {
 struct StEntry {
   std::string name, dtype;
   std::vector<int64_t> shape;
-  int64_t begin = 0, end = 0;
+  int64_t begin = -1, end = -1;
 };
 
 bool parse_header(const char* p, size_t n, std::vector<StEntry>* out) {
@@ -1824,7 +1900,7 @@ bool parse_header(const char* p, size_t n, std::vector<StEntry>* out) {
         if (!in.eat(']')) {
           do {
             int64_t x;
-            if (!in.num(&x)) return false;
+            if (!in.num(&x) || v.size() >= 8) return false;
             v.push_back(x);
           } while (in.eat(','));
           if (!in.eat(']')) return false;
@@ -1846,18 +1922,28 @@ bool parse_header(const char* p, size_t n, std::vector<StEntry>* out) {
   return in.eat('}');
 }
 
-}  // namespace
-
-int engine_load_safetensors(Engine& e, const char* path, int* loaded, std::string* err) {
-  *loaded = 0;
+// Reads a .safetensors file and calls fn(name, dtype, shape, ndim, data, bytes)
+// for each tensor the reference's loader keeps (it skips vision towers and
+// the n-gram tables' row shards, src/weights.rs:48-54), stopping at the first
+// nonzero status.  Offsets are checked against the file before any read.
+template <class Fn>
+int read_safetensors(const char* path, int* done, std::string* err, Fn fn) {
+  *done = 0;
   FILE* f = std::fopen(path, "rb");
   if (!f) {
     *err = std::string("cannot open ") + path;
     return MX_EINVAL;
   }
   std::unique_ptr<FILE, int (*)(FILE*)> guard(f, std::fclose);
+  if (std::fseek(f, 0, SEEK_END) != 0) {
+    *err = std::string(path) + ": cannot seek";
+    return MX_EINVAL;
+  }
+  const long fsize = std::ftell(f);
+  std::rewind(f);
   uint64_t hlen = 0;
-  if (std::fread(&hlen, 8, 1, f) != 1 || hlen > (100ull << 20)) {
+  if (fsize < 8 || std::fread(&hlen, 8, 1, f) != 1 || hlen > (100ull << 20) ||
+      hlen > uint64_t(fsize) - 8) {
     *err = std::string(path) + ": not a safetensors file";
     return MX_EINVAL;
   }
@@ -1871,11 +1957,9 @@ int engine_load_safetensors(Engine& e, const char* path, int* loaded, std::strin
     *err = std::string(path) + ": unreadable header";
     return MX_EINVAL;
   }
-  const long base = long(8 + hlen);
+  const int64_t base = int64_t(8 + hlen), data_size = int64_t(fsize) - base;
   std::vector<char> buf;
   for (const StEntry& en : entries) {
-    // the reference's loader skips vision towers and the n-gram tables'
-    // row shards (src/weights.rs:48-54)
     if (en.name.rfind("visual.", 0) == 0 || en.name.rfind("vision_tower.", 0) == 0 ||
         en.name.find(".ngram_embedding.shards.") != std::string::npos)
       continue;
@@ -1888,23 +1972,54 @@ int engine_load_safetensors(Engine& e, const char* path, int* loaded, std::strin
       *err = en.name + ": unsupported dtype " + en.dtype;
       return MX_EUNSUPPORTED;
     }
-    const int64_t nbytes = en.end - en.begin;
-    if (nbytes < 0 || en.shape.empty()) {
-      *err = en.name + ": bad offsets or shape";
+    if (en.begin < 0 || en.end < en.begin || en.end > data_size) {
+      *err = en.name + ": data_offsets [" + std::to_string(en.begin) + ", " +
+             std::to_string(en.end) + "] outside the file's " + std::to_string(data_size) +
+             " data bytes";
       return MX_EINVAL;
     }
-    buf.resize(size_t(nbytes));
-    if (std::fseek(f, base + long(en.begin), SEEK_SET) != 0 ||
+    if (en.shape.empty()) {
+      *err = en.name + ": empty shape";
+      return MX_EINVAL;
+    }
+    for (int64_t d : en.shape)
+      if (d <= 0) {
+        *err = en.name + ": dim " + std::to_string(d);
+        return MX_EINVAL;
+      }
+    buf.resize(size_t(en.end - en.begin));
+    if (std::fseek(f, long(base + en.begin), SEEK_SET) != 0 ||
         std::fread(buf.data(), 1, buf.size(), f) != buf.size()) {
       *err = en.name + ": truncated data";
       return MX_EINVAL;
     }
-    const int rc = engine_load_tensor(e, en.name.c_str(), dt, en.shape.data(), int(en.shape.size()),
-                                      buf.data(), buf.size(), err);
+    const int rc = fn(en.name.c_str(), dt, en.shape.data(), int(en.shape.size()), buf.data(),
+                      buf.size());
     if (rc != MX_OK) return rc;
-    ++*loaded;
+    ++*done;
   }
   return MX_OK;
+}
+
+}  // namespace
+
+int engine_load_safetensors(Engine& e, const char* path, int* loaded, std::string* err) {
+  return read_safetensors(path, loaded, err,
+                          [&](const char* name, int dt, const int64_t* shape, int ndim,
+                              const void* data, size_t bytes) {
+                            return engine_load_tensor(e, name, dt, shape, ndim, data, bytes, err);
+                          });
+}
+
+int checkpoint_check(const mx_model_config& c, const char* path, int* checked, std::string* err) {
+  return read_safetensors(path, checked, err,
+                          [&](const char* name, int dt, const int64_t* shape, int ndim,
+                              const void* data, size_t bytes) {
+                            CheckpointTarget t;
+                            size_t count = 0;
+                            return plan_tensor(c, name, dt, shape, ndim, data, bytes, &t, &count,
+                                               err);
+                          });
 }
 
 const mx_model_config& engine_config(const Engine& e) { return e.cfg; }

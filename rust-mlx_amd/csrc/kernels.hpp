@@ -317,6 +317,7 @@ int checkpoint_target(const mx_model_config& c, std::string name, CheckpointTarg
 int engine_load_tensor(Engine& e, const char* name, int dtype, const int64_t* shape, int ndim,
                        const void* data, size_t bytes, std::string* err);
 int engine_load_safetensors(Engine& e, const char* path, int* loaded, std::string* err);
+int checkpoint_check(const mx_model_config& c, const char* path, int* checked, std::string* err);
 int engine_fill_slot(Engine& e, int slot, int length, uint64_t seed, std::string* err);
 int engine_time_experts(Engine& e, int rows, mx_expert_timing* out, std::string* err);
 int engine_profile_step(Engine& e, const int32_t* slots, const uint32_t* tokens, int rows,

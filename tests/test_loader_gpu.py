@@ -167,3 +167,64 @@ def a_names(mx, eng):
         for m in ("router", "gate", "up", "down", "shared_gate", "shared_up", "shared_down"):
             out += qw(f"{s}.moe.{m}")
     return out
+
+
+def test_mixed_width_checkpoint_runs_bit_exact_with_the_oracle(mx, tmp_path):
+    """A synthetic MLX checkpoint whose layers are quantised at their own
+    widths (per-module quantization entries, src/weights.rs:70-90): its
+    config.json gives the engine's width table (config_from_mlx), the file
+    loads into the engine, every engine weight equals the file's mapping
+    through mx_checkpoint_target, and the exact engine's speculative
+    generation (prefill, verify blocks, the MTP draft layer) and batched
+    decode equal the oracle model's on the same tensors bit for bit."""
+    from mlx_ckpt import engine_tensors, make_fetch, synth_checkpoint, write_safetensors
+    from oracle.model import Model
+
+    base = dict(mx.TINY, mtp=1, vocab=16)
+    widths = {0: (8, 6), 1: (5, 4), 2: (6, 8), 3: (5, 5), 4: (8, 4)}  # index 4: the MTP layer
+    T, config = synth_checkpoint(base, 21, widths)
+    cfg = mx.config_from_mlx(config, max_slots=3, max_context=96, seed=9, mtp=1)
+    assert cfg["layer_widths"][:10] == [8, 6, 5, 4, 6, 8, 5, 5, 8, 4]
+    path = tmp_path / "mixed.safetensors"
+    n = write_safetensors(path, T)
+    assert mx.checkpoint_check(cfg, path) == n
+    E = engine_tensors(mx, cfg, T)
+    eng = mx.Engine(cfg)
+    try:
+        assert eng.load_safetensors(str(path)) == n
+        for name, a in E.items():
+            assert (eng.read(name, a.dtype, a.shape) == a).all(), name
+        eng.set_flags(exact=True)
+        model = Model(cfg, make_fetch(E))
+        prompt = [int(t) for t in np.random.default_rng(6).integers(0, 16, 13)]
+        toks, st = eng.generate(0, prompt, 12, 3)
+        want, wst = model.generate(0, prompt, 12, 3)
+        assert [int(t) for t in toks] == want
+        assert [int(d) for d in st["drafts"]] == wst["drafts"]
+        assert (st["rounds"], st["accepted"]) == (wst["rounds"], wst["accepted"])
+        # two more slots decoded together, at their own offsets
+        for s, p in ((1, prompt[:5]), (2, prompt[3:12])):
+            assert eng.prefill(s, p) == int(model.prefill(s, p))
+        t = [int(x) for x in model.decode_rows([1, 2], [3, 7])]
+        assert [int(x) for x in eng.decode_batch([1, 2], [3, 7], equal=False)] == t
+    finally:
+        eng.close()
+
+
+def test_a_checkpoint_value_that_would_round_is_refused(mx, tmp_path):
+    """An fp32 scale that bf16 cannot hold stops the load with its name."""
+    from mlx_ckpt import synth_checkpoint, write_safetensors
+
+    T, config = synth_checkpoint(dict(mx.TINY), 5)
+    cfg = mx.config_from_mlx(config, max_slots=1, max_context=32)
+    name = "language_model.model.layers.1.mlp.switch_mlp.up_proj.scales"
+    T[name] = T[name].copy()
+    T[name].reshape(-1)[3] += np.float32(1e-5)
+    path = tmp_path / "inexact.safetensors"
+    write_safetensors(path, T, dtypes={name: "F32"})
+    eng = mx.Engine(cfg)
+    try:
+        with pytest.raises(mx.MxError, match="up_proj.scales: value"):
+            eng.load_safetensors(str(path))
+    finally:
+        eng.close()

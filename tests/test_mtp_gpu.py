@@ -1,6 +1,11 @@
 """The MTP draft layer and speculative generation (config 4's draft model and
 acceptance loop: Mtp::forward, src/mtp.rs:72-127; generate_prepared,
-src/speculative.rs:225-483) on the tiny model with mtp = 1.
+src/speculative.rs:225-483) on the tiny model with mtp = 1, at config 3's
+geometry (four layers, mixed widths, a 16-token vocabulary slice: bit-exact
+with the oracle, drafts accepted) and over the whole 48-layer config-4 model
+(lossless against plain greedy decoding).  The oracle's draft step itself is
+pinned on the CPU by a float64 closed form and a reduction to a trunk layer
+(tests/test_oracle_mtp.py).
 
 Exact mode: the tokens, every round's draft tokens and the acceptance counts
 are bit-exact with the CPU oracle model running the same loop, and
@@ -129,5 +134,63 @@ def test_verify_profile_and_draft_bytes(mx):
         d0, d1 = eng.draft_bytes(100), eng.draft_bytes(150)
         assert d1 - d0 == pytest.approx(50 * cfg["kv_heads"] * cfg["head_dim"] * 4, rel=1e-12)
         assert 0 < d0 < prof["step_bytes"]
+    finally:
+        eng.close()
+
+
+def test_exact_speculation_at_config3_geometry_matches_oracle(mx):
+    """Config 4 at config 3's geometry (hidden 2048, 512 experts top-10,
+    hc 4 / rank 256, GDN 16/32 heads, attention 16/2 heads of 256) with the
+    mixed per-layer widths and the MTP draft layer, four layers and a
+    16-token vocabulary slice so that drafts are accepted now and then: the
+    exact engine's speculative generation (prompt prefill with the drafter's
+    prefill, drafts, 4-token verify blocks, greedy acceptance, commit,
+    resynchronisation) equals the oracle model's bit for bit -- tokens, every
+    draft, rounds and accepted counts -- and plain greedy decoding's tokens."""
+    from oracle.model import Model
+
+    cfg = dict(mx.CONFIG3, layers=4, vocab=16, mtp=1, mixed_bits=1, max_slots=3, max_context=96)
+    eng = mx.Engine(cfg)
+    try:
+        eng.set_flags(exact=True)
+        chosen = None
+        for seed in range(12):  # the engine alone finds a prompt with accepted drafts
+            prompt = [int(t) for t in np.random.default_rng(100 + seed).integers(0, 16, 17)]
+            eng.reset(0)
+            toks, st = eng.generate(0, prompt, 24, 3)
+            if st["accepted"] > 0:
+                chosen = (prompt, toks, st)
+                break
+        assert chosen is not None, "no accepted draft in 12 prompts"
+        prompt, toks, st = chosen
+        print(f"prompt seed {100 + seed}: rounds {st['rounds']}, accepted "
+              f"{st['accepted']}/{st['drafted']}", flush=True)
+        model = Model(cfg, lambda name, dtype, shape: eng.read(name, dtype, shape))
+        want, wst = model.generate(0, prompt, 24, 3)
+        assert [int(t) for t in toks] == want
+        assert [int(d) for d in st["drafts"]] == wst["drafts"]
+        assert (st["rounds"], st["drafted"], st["accepted"]) == \
+            (wst["rounds"], wst["drafted"], wst["accepted"])
+        plain, pst = eng.generate(1, prompt, 24, 0)
+        assert [int(t) for t in plain] == [int(t) for t in toks] and pst["rounds"] == 0
+    finally:
+        eng.close()
+
+
+def test_exact_speculation_over_all_48_layers_is_lossless(mx):
+    """The whole config-4 model (48 mixed-width layers, vocabulary 151936,
+    the MTP draft layer): speculative generation of 40 tokens in depth-3
+    rounds gives plain greedy decoding's tokens, over at least 8 rounds."""
+    cfg = dict(mx.CONFIG3, mtp=1, mixed_bits=1, max_slots=2, max_context=160)
+    eng = mx.Engine(cfg)
+    try:
+        eng.set_flags(exact=True)
+        prompt = [int(t) for t in np.random.default_rng(44).integers(0, cfg["vocab"], 41)]
+        toks, st = eng.generate(0, prompt, 40, 3)
+        plain, _ = eng.generate(1, prompt, 40, 0)
+        print(f"48 layers: rounds {st['rounds']}, accepted {st['accepted']}/{st['drafted']}",
+              flush=True)
+        assert len(toks) == 40 and st["rounds"] >= 8
+        assert [int(t) for t in toks] == [int(t) for t in plain]
     finally:
         eng.close()
