@@ -254,7 +254,9 @@ mx_status mx_moe_route(const uint16_t* logits, int64_t logit_stride, const uint1
  * partial is bf16 [rows, top_k + 1, hidden]; workspace holds
  * mx_moe_workspace_bytes(rows, top_k, max(inter, shared inter)) bytes.
  * Routes naming the same expert are served together, so each selected
- * expert's weights stream once per call.  Replaces moe_kernel::gate_up
+ * expert's weights stream once per call.  ids are expert indices below the
+ * banks' expert count (at most 1024), distinct within a row, as a top-k
+ * routing gives them.  Replaces moe_kernel::gate_up
  * (src/moe_kernel.rs:10-118), the gather_qmm gate/up/down of MoE::parts
  * (src/hybrid.rs:245-271), moe_down::reduce's expert QMV + score product
  * (src/moe_down.rs:34-137) and the shared Mlp (src/dense.rs:292-298). */

@@ -103,22 +103,30 @@ __global__ __launch_bounds__(64) void prep_kernel(const uint16_t* __restrict__ q
 // m = max_t s; p = e^(s - m); l = sum_t p (xor butterfly per wave, waves in
 // order).  Values: thread t owns dim t; o = sum_j p_j v_j[t] (fma chain, j
 // ascending).  Writes (m, l) and o (fp32) per (row, head, chunk).  A
-// workgroup takes G of the kv head's q heads (blockIdx.y = kv head * splits +
-// split), so short contexts still spread over many workgroups.
+// workgroup takes G of the kv head's q heads (`splits` workgroups per kv
+// head), so short contexts still spread over many workgroups.
 template <int G>
 __global__ __launch_bounds__(kAttnChunk) void decode_kernel(
     const uint16_t* __restrict__ q, const int32_t* __restrict__ slots,
     const int32_t* __restrict__ pos, const uint16_t* __restrict__ k_cache,
     const uint16_t* __restrict__ v_cache, AttnDims d, int max_chunks, float scale,
-    float* __restrict__ o_part, float* __restrict__ ml_part) {
+    float* __restrict__ o_part, float* __restrict__ ml_part, int chunks, int rows) {
   __shared__ float qs[G][kMaxHd];
   __shared__ float ps[G][kAttnChunk];
   __shared__ float red[G][4];
-  const int chunk = blockIdx.x;
+  // one-dimensional grid placed by XCD: workgroups go to the eight XCDs in
+  // turn (id mod 8), so the `splits` workgroups of one (chunk, kv head, row)
+  // -- which read the same K and V rows -- take ids congruent mod 8 and
+  // share one L2
   const int splits = d.heads / d.kv_heads / G;
-  const int kvh = blockIdx.y / splits;
-  const int h0 = kvh * (G * splits) + (blockIdx.y - kvh * splits) * G;  // first q head
-  const int row = blockIdx.z;
+  const int b = blockIdx.x, xcd = b & 7, k8 = b >> 3;
+  const int group = (k8 / splits) * 8 + xcd;  // (chunk, kv head, row)
+  const int split = k8 - (k8 / splits) * splits;
+  if (group >= chunks * d.kv_heads * rows) return;  // padding (uniform)
+  const int chunk = group % chunks;
+  const int kvh = (group / chunks) % d.kv_heads;
+  const int h0 = kvh * (G * splits) + split * G;  // first q head
+  const int row = group / (chunks * d.kv_heads);
   const int t = threadIdx.x;
   const int n_pos = pos[row] + 1;
   const int j0 = chunk * kAttnChunk;
@@ -537,13 +545,15 @@ int attn_decode(const uint16_t* q, int rows, const int32_t* slots, const int32_t
   // two q heads per workgroup (one when the kv head has one)
   const int grp = d.heads / d.kv_heads;
   if (grp != 1 && grp != 2 && grp != 4 && grp != 8 && grp != 16) return MX_EUNSUPPORTED;
-  const dim3 grid(chunks, d.kv_heads * (grp == 1 ? 1 : grp / 2), rows);
+  const int splits = grp == 1 ? 1 : grp / 2;
+  const int groups = chunks * d.kv_heads * rows;
+  const dim3 grid((groups + 7) / 8 * 8 * splits);
   if (grp == 1)
     hipLaunchKernelGGL(decode_kernel<1>, grid, dim3(kAttnChunk), 0, s, q, slots, pos, k_cache,
-                       v_cache, d, max_chunks, scale, o_part, ml_part);
+                       v_cache, d, max_chunks, scale, o_part, ml_part, chunks, rows);
   else
     hipLaunchKernelGGL(decode_kernel<2>, grid, dim3(kAttnChunk), 0, s, q, slots, pos, k_cache,
-                       v_cache, d, max_chunks, scale, o_part, ml_part);
+                       v_cache, d, max_chunks, scale, o_part, ml_part, chunks, rows);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 

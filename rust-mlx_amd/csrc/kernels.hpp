@@ -66,6 +66,10 @@ struct ProjEpilogue {
   int64_t conv_stride;
   int conv_ch;
   int taps;
+  // set by the launcher: a one-dimensional grid placed by XCD (block-plane
+  // projections over both four-row blocks) with xcd_groups tiles
+  int xcd_blocks = 0;
+  int xcd_groups = 0;
 };
 constexpr int kConvMaxTaps = 4;
 int proj(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const ProjEpilogue& e,

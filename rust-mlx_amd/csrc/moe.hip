@@ -57,28 +57,38 @@ __device__ __forceinline__ void plan_body(const uint32_t* sids, int rows, int to
                                           MoePlan* __restrict__ plan) {
   __shared__ int entry_of[kMaxRoutes];  // entry index, by its first route
   __shared__ int wave_count[8], wave_items[8];
+  // per expert: the rows that route to it (a bit per row) and its first
+  // route; filled with LDS atomics, which need no order, so every route
+  // learns its expert's routes in one pass instead of a scan of all routes
+  constexpr int kTable = 1024;  // experts (at most 1024)
+  __shared__ uint32_t row_mask[kTable];
+  __shared__ int first_route[kTable];
   constexpr int NW = NT / 64;
   const int t = threadIdx.x;
   const int routes = rows * top_k;
-  // one pass over every route: the first route of this route's expert, this
-  // route's place among the expert's routes (route order), how many there
-  // are, and which four-row blocks of rows they come from
+  for (int i = t; i < kTable; i += NT) {
+    row_mask[i] = 0u;
+    first_route[i] = 1 << 30;
+  }
+  __syncthreads();
   const bool routed = t < routes;
-  const uint32_t e = routed ? sids[t] : 0u;
+  const uint32_t e = routed ? sids[t] & uint32_t(kTable - 1) : 0u;
+  const int row = routed ? t / top_k : 0;
+  if (routed) {
+    atomicOr(&row_mask[e], 1u << row);
+    atomicMin(&first_route[e], t);
+  }
+  __syncthreads();
+  // this route's place among its expert's routes (route order: each row
+  // routes to an expert at most once, so by row), how many there are, which
+  // four-row blocks of rows they come from
   int first_u = t, pos = 0, cnt = 0, blkmask = 0;
   if (routed) {
-    for (int r = 0, u = 0; r < rows; ++r) {
-      int hit = 0;
-#pragma unroll 4
-      for (int k = 0; k < top_k; ++k, ++u) {
-        const bool match = sids[u] == e;
-        first_u = match && u < first_u ? u : first_u;
-        pos += match && u < t;
-        hit += match;
-      }
-      cnt += hit;
-      blkmask |= hit ? 1 << (r >> 2) : 0;
-    }
+    const uint32_t mask = row_mask[e];
+    first_u = first_route[e];
+    pos = __popc(mask & ((1u << row) - 1u));
+    cnt = __popc(mask);
+    blkmask = ((mask & 0x0fu) ? 1 : 0) | ((mask & 0xf0u) ? 2 : 0);
   } else if (t == routes) {  // the shared expert: every row, slot top_k
     cnt = rows;
     blkmask = rows > 4 ? 3 : 1;
@@ -147,15 +157,16 @@ __global__ __launch_bounds__(512) void route_plan_kernel(
   __shared__ uint32_t sids[kMaxRoutes];
   const int lane = threadIdx.x & 63, row = threadIdx.x >> 6;
   if (row < rows) {
+    // the shared-expert logit is requested with the row's logits, so its
+    // latency overlaps theirs instead of following the top-k
+    const uint16_t sh = shared_logit[size_t(row) * shared_stride];  // every lane: no branch
     const rt::RouteLane r = rt::route_row<PER>(logits + size_t(row) * logit_stride, top_k);
     if (lane < top_k) {
       ids[size_t(row) * top_k + lane] = r.id;
       scores[size_t(row) * top_k + lane] = r.score;
       sids[row * top_k + lane] = r.id;
     }
-    if (lane == 0)
-      factor[row] =
-          f32_to_bf16(sigmoid_bf16(bf16_to_f32(shared_logit[size_t(row) * shared_stride])));
+    if (lane == 0) factor[row] = f32_to_bf16(sigmoid_bf16(bf16_to_f32(sh)));
   }
   __syncthreads();
   plan_body<512>(sids, rows, top_k, plan);
