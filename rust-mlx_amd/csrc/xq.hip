@@ -520,6 +520,12 @@ void xq_gate_up_kernel(
   }
   const int M = plan->m[entry];
   const int expert = plan->expert[entry];
+  // the entry's member rows and slots, read now (scalar loads that overlap
+  // the weight stream) rather than in the epilogue
+  const uint32_t* rw32 = reinterpret_cast<const uint32_t*>(plan->row[entry]);
+  const uint32_t* sw32 = reinterpret_cast<const uint32_t*>(plan->slot[entry]);
+  const uint64_t mrows = uint64_t(rw32[0]) | (uint64_t(rw32[1]) << 32);
+  const uint64_t mslots = uint64_t(sw32[0]) | (uint64_t(sw32[1]) << 32);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int t = wave >> 1, p = wave & 1;
   // the gate and up matrices of an expert have one shape (the launcher checks)
@@ -712,8 +718,8 @@ void xq_gate_up_kernel(
     const uint16_t out = f32_to_bf16(silu * uv);
     for (int m = 0; m < M; ++m) {
       if constexpr (SRC == kSrcPlaneLds) {
-        const int r = plan->row[entry][m];
-        if (r == xr) h[(size_t(r) * (top_k + 1) + plan->slot[entry][m]) * hs + col] = out;
+        const int r = int((mrows >> (8 * m)) & 0xffu);
+        if (r == xr) h[(size_t(r) * (top_k + 1) + int((mslots >> (8 * m)) & 0xffu)) * hs + col] = out;
       } else {
         if (m == xr) h[(size_t(ro[m]) * (top_k + 1) + so[m]) * hs + col] = out;
       }
@@ -735,6 +741,7 @@ __global__ __launch_bounds__(64 * kDnTiles) void xq_down_kernel(const uint16_t* 
   extern __shared__ __align__(16) char lds[];
   __shared__ float yt[8 * 16 * kDnTiles];
   __shared__ int ro[8], so[8];
+  __shared__ float sco[8];
   const int entry = blockIdx.y;
   if (entry >= plan->count) return;
   const int expert = plan->expert[entry];
@@ -744,8 +751,13 @@ __global__ __launch_bounds__(64 * kDnTiles) void xq_down_kernel(const uint16_t* 
   if (c0 >= hidden) return;
   const int M = plan->m[entry];
   if (threadIdx.x < 8) {
-    ro[threadIdx.x] = plan->row[entry][threadIdx.x];
-    so[threadIdx.x] = plan->slot[entry][threadIdx.x];
+    // member rows, slots and route scores (the epilogue's), read up front
+    const int r = plan->row[entry][threadIdx.x], sl = plan->slot[entry][threadIdx.x];
+    ro[threadIdx.x] = r;
+    so[threadIdx.x] = sl;
+    sco[threadIdx.x] = int(threadIdx.x) < M && sl < top_k
+                           ? bf16_to_f32(scores[size_t(r) * top_k + sl])
+                           : 1.0f;
   }
   __syncthreads();
   const int j = threadIdx.x & 15, t = threadIdx.x >> 6;
@@ -762,8 +774,8 @@ __global__ __launch_bounds__(64 * kDnTiles) void xq_down_kernel(const uint16_t* 
     if (m >= M || c0 + c >= hidden) continue;
     const bool routed = so[m] < top_k;
     const float dv = round_bf16(yt[i]);
-    const float sc = routed ? bf16_to_f32(scores[size_t(ro[m]) * top_k + so[m]]) : 1.0f;
-    p[(size_t(ro[m]) * (top_k + 1) + so[m]) * hidden + c0 + c] = f32_to_bf16(routed ? dv * sc : dv);
+    p[(size_t(ro[m]) * (top_k + 1) + so[m]) * hidden + c0 + c] =
+        f32_to_bf16(routed ? dv * sco[m] : dv);
   }
 }
 
