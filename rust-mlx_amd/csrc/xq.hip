@@ -94,6 +94,7 @@ enum : int {
   kSrcPlane = 2,     // read by each wave from the producer's plane in global memory
   kSrcPlaneLds = 3,  // the producer's plane copied once per workgroup into LDS
   kSrcBlockLds = 4,  // one four-row block of the plane copied into LDS (blockIdx.y)
+  kSrcBlockPlane = 5,  // one four-row block of the plane read in place by each wave
 };
 
 template <int BITS>
@@ -220,18 +221,21 @@ __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
     xq::dma_plane<NT>(lds, plane, G);
   } else if constexpr (SRC == kSrcBlockLds) {
     xq::dma_plane_block<NT>(lds, plane, G, blocks >> 1);
-  } else if constexpr (SRC == kSrcPlane) {
+  } else if constexpr (SRC == kSrcPlane || SRC == kSrcBlockPlane) {
     src = plane;
   }
   const double* qs = reinterpret_cast<const double*>(
       src + (SRC == kSrcBlockLds ? xq::block_q_offset(G) : xq::plane_q_offset(G)));
   const int* es = reinterpret_cast<const int*>(
       src + (SRC == kSrcBlockLds ? xq::block_e_offset(G) : xq::plane_e_offset(G)));
-  const int bq = 4 * (blocks >> 1) + kb;  // kSrcBlockLds: the lane's activation row
+  const int bq = 4 * (blocks >> 1) + kb;  // one-block sources: the lane's activation row
   double acc[2] = {0.0, 0.0}, tot[2] = {0.0, 0.0}, ss[KS > 1 ? SPW : 1][2];
   // A plane read in place: each group's operands are requested PD groups
-  // ahead of their use, so the wave waits for memory once, not per group.
-  constexpr int PD = SRC == kSrcPlane ? (NG < 4 ? NG : 4) : 1;
+  // ahead of their use, so the wave waits for memory once, not per group
+  // (one block: only that block's operands, and only the wave's own groups,
+  // with no copy of the rest into LDS and no barrier before the first group)
+  constexpr bool INPLACE = SRC == kSrcPlane || SRC == kSrcBlockPlane;
+  constexpr int PD = INPLACE ? (NG < 4 ? NG : 4) : 1;
   struct PlaneOp {
     xq::v4i a0, a1;
     double q0, q1;
@@ -239,15 +243,23 @@ __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
   } pf[PD];
   auto load_op = [&](int gl, PlaneOp& o) {
     const int g = min(gbeg + gl, gend - 1);
-    const char* ab = src + g * xq::kGroupBytes + lane * 16;
-    o.a0 = *reinterpret_cast<const xq::v4i*>(ab);
-    o.a1 = *reinterpret_cast<const xq::v4i*>(ab + xq::kBlockBytes);
-    o.q0 = qs[g * 8 + kb];
-    o.q1 = qs[g * 8 + 4 + kb];
-    o.e0 = es[g * 8 + kb];
-    o.e1 = es[g * 8 + 4 + kb];
+    if constexpr (SRC == kSrcBlockPlane) {
+      const char* ab = src + g * xq::kGroupBytes + (blocks >> 1) * xq::kBlockBytes + lane * 16;
+      o.a0 = *reinterpret_cast<const xq::v4i*>(ab);
+      o.a1 = o.a0;
+      o.q0 = o.q1 = qs[g * 8 + bq];
+      o.e0 = o.e1 = es[g * 8 + bq];
+    } else {
+      const char* ab = src + g * xq::kGroupBytes + lane * 16;
+      o.a0 = *reinterpret_cast<const xq::v4i*>(ab);
+      o.a1 = *reinterpret_cast<const xq::v4i*>(ab + xq::kBlockBytes);
+      o.q0 = qs[g * 8 + kb];
+      o.q1 = qs[g * 8 + 4 + kb];
+      o.e0 = es[g * 8 + kb];
+      o.e1 = es[g * 8 + 4 + kb];
+    }
   };
-  if constexpr (SRC == kSrcPlane) {
+  if constexpr (INPLACE) {
 #pragma unroll
     for (int i = 0; i < PD; ++i) load_op(i, pf[i]);
   }
@@ -261,7 +273,7 @@ __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
         xq::v4i a0, a1;
         double q0 = 0.0, q1 = 0.0;
         int e0 = 1, e1 = 1;
-        if constexpr (SRC == kSrcPlane) {
+        if constexpr (INPLACE) {
           const PlaneOp& o = pf[gl % PD];
           a0 = o.a0;
           a1 = o.a1;
@@ -341,7 +353,7 @@ __device__ __forceinline__ void xq_tiles(const uint32_t* __restrict__ crow,
         }
         xq::group_step<BITS>(a0, a1, blocks, xq::b_operand<BITS>(ci), q0, q1, e0, e1, sc, bs,
                              acc);
-        if constexpr (SRC == kSrcPlane) {
+        if constexpr (INPLACE) {
           if (gl + PD < NG) load_op(gl + PD, pf[gl % PD]);
         }
         // a slice ends after its second group, or after the last group of an
@@ -403,7 +415,7 @@ __global__ __launch_bounds__(64 * T * KS) void xq_dense_kernel(QWeight w,
   __shared__ float yt[8 * 16 * T];
   constexpr int NC = 16 * T, NT = 64 * T * KS;
   int tg = blockIdx.x, blk = blockIdx.y;
-  if constexpr (SRC == kSrcBlockLds) {
+  if constexpr (SRC == kSrcBlockLds || SRC == kSrcBlockPlane) {
     if (gridDim.y == 1 && gridDim.x % 8 == 0 && e.xcd_blocks) {
       // both four-row blocks, placed by XCD: workgroups are dispatched to
       // the eight XCDs in turn (id mod 8), so XCDs 0-3 take block 0 and 4-7
@@ -434,7 +446,7 @@ __global__ __launch_bounds__(64 * T * KS) void xq_dense_kernel(QWeight w,
   }
   ProjFinish<MODE, NC, NT> fin;
   int blocks = M > 4 ? 3 : 1;
-  if constexpr (SRC == kSrcBlockLds) {
+  if constexpr (SRC == kSrcBlockLds || SRC == kSrcBlockPlane) {
     // this workgroup's four activation rows: block blk
     blocks = 1 << blk;
     fin.m_lo = 4 * blk;
@@ -809,11 +821,23 @@ __global__ __launch_bounds__(1024) void xq_upmix_kernel(QWeight w, const uint16_
   // activation rows: blockIdx.y = the block this one computes and writes
   const bool split = gridDim.y > 1;
   const int mlo = split ? 4 * int(blockIdx.y) : 0, mhi = split ? mlo + 4 : 8;
-  xq_tiles<BITS, 16, 1, SPW, kSrcStage, RM>(w.codes + size_t(row) * (size_t(w.k) * BITS / 32),
-                                            w.scales + size_t(row) * G, w.biases + size_t(row) * G,
-                                            tiles_sbv<BITS, SPW>(w), w.k, M,
-                                            split ? 1 << blockIdx.y : (M > 4 ? 3 : 1),
-                                            XRows{lo, w.k}, nullptr, lds, yt, [] {}, rm);
+  // the normed streams the mix multiplies, requested once the first weight
+  // loads are out (thread i < 512 mixes row i / 64, column i % 64)
+  const int im = threadIdx.x >> 6, ic = threadIdx.x & 63;
+  const bool mixer = threadIdx.x < 8 * 64 && im < M && im >= mlo && im < mhi;
+  uint16_t xv[4] = {0, 0, 0, 0};
+  xq_tiles<BITS, 16, 1, SPW, kSrcStage, RM>(
+      w.codes + size_t(row) * (size_t(w.k) * BITS / 32), w.scales + size_t(row) * G,
+      w.biases + size_t(row) * G, tiles_sbv<BITS, SPW>(w), w.k, M,
+      split ? 1 << blockIdx.y : (M > 4 ? 3 : 1), XRows{lo, w.k}, nullptr, lds, yt,
+      [&] {
+        if (mixer) {
+#pragma unroll
+          for (int s = 0; s < 4; ++s)
+            xv[s] = xn[size_t(im) * 4 * hidden + size_t(s) * hidden + tg * 64 + ic];
+        }
+      },
+      rm);
   for (int i = threadIdx.x; i < 8 * 64; i += 1024) {
     const int m = i >> 6, c = i & 63;
     float v = 0.0f;
@@ -822,7 +846,7 @@ __global__ __launch_bounds__(1024) void xq_upmix_kernel(QWeight w, const uint16_
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const float p = round_bf16(yt[m * 256 + s * 64 + c]);
-        const float x = bf16_to_f32(xn[size_t(m) * 4 * hidden + size_t(s) * hidden + tg * 64 + c]);
+        const float x = bf16_to_f32(xv[s]);
         sum = sum + round_bf16(sigmoid_bf16(p) * x);
       }
       const uint16_t o = f32_to_bf16(round_bf16(sum) / 4.0f);
@@ -936,7 +960,7 @@ int launch_xq(const QWeight& w, const uint16_t* x, int64_t xs, int m, const char
     if (rm) fn = xq_dense_kernel<BITS, MODE, T, KS, SPW, SRC, true>;
   }
   MX_TRY_RC(raise_lds(fn, lb));
-  const int nblk = SRC == kSrcBlockLds && m > 4 ? 2 : 1;
+  const int nblk = (SRC == kSrcBlockLds || SRC == kSrcBlockPlane) && m > 4 ? 2 : 1;
   if (nblk == 2) {
     // one-dimensional grid placed by XCD (xq_dense_kernel)
     ProjEpilogue ex = e;
@@ -986,8 +1010,9 @@ int xq_shape(const QWeight& w, const uint16_t* x, int64_t xs, int m, const char*
       MX_XQ(1, 8, 4, kSrcStage);
     }
     if (S == 64) {
-      // each workgroup copies one block of the plane (about 140 KB) into LDS
-      if (plane) MX_XQ(1, 16, 4, kSrcBlockLds);
+      // each workgroup takes one block of the plane; each wave reads its own
+      // groups' operands of that block in place
+      if (plane) MX_XQ(1, 16, 4, kSrcBlockPlane);
       MX_XQ(1, 16, 4, kSrcReg);
     }
   }
