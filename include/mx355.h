@@ -487,6 +487,19 @@ mx_status mx_engine_destroy(mx_engine* e);
 mx_status mx_engine_reset_slot(mx_engine* e, int32_t slot);
 mx_status mx_engine_clone_slot(mx_engine* e, int32_t src, int32_t dst);
 int32_t mx_engine_offset(mx_engine* e, int32_t slot);
+/* 1 when a failed step left the slot's caches partly updated (GDN state and
+ * conv windows are advanced in place; the reference's lazy evaluation never
+ * writes a cache before the whole step succeeded, src/batching.rs:136-137):
+ * every step, prefill, verify, commit and clone from that slot then returns
+ * MX_ESTATE until mx_engine_reset_slot or mx_engine_clone_slot (into it)
+ * replaces its caches.  A failed verify block restores its snapshot instead,
+ * so its slot stays usable.  0 otherwise, -1 for a bad slot. */
+int32_t mx_engine_slot_failed(mx_engine* e, int32_t slot);
+/* Test hook with no reference counterpart: the engine's next step stops with
+ * MX_EHIP after launching `after_layers` layers (eager), as a launch that
+ * fails mid-step would, so failure handling can be tested without a device
+ * fault.  0 disarms. */
+mx_status mx_engine_inject_failure(mx_engine* e, int32_t after_layers);
 mx_status mx_engine_decode_batch(mx_engine* e, const int32_t* slots, const uint32_t* tokens,
                                  int32_t rows, uint32_t* next);
 mx_status mx_engine_decode_rows(mx_engine* e, const int32_t* slots, const uint32_t* tokens,

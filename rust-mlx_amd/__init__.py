@@ -245,6 +245,9 @@ def _load() -> C.CDLL:
         "mx_engine_load_safetensors": ([vp, C.c_char_p, C.POINTER(i32)], i32),
         "mx_checkpoint_target": ([C.POINTER(ModelConfigC), C.c_char_p, C.c_char_p, sz,
                                   C.POINTER(i32)], i32),
+        "mx_checkpoint_check": ([C.POINTER(ModelConfigC), C.c_char_p, C.POINTER(i32)], i32),
+        "mx_engine_slot_failed": ([vp, i32], i32),
+        "mx_engine_inject_failure": ([vp, i32], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -648,6 +651,15 @@ class Engine:
 
     def offset(self, slot) -> int:
         return lib.mx_engine_offset(self.h, slot)
+
+    def slot_failed(self, slot) -> bool:
+        """mx_engine_slot_failed: a failed step left this slot's caches partly updated."""
+        return lib.mx_engine_slot_failed(self.h, slot) == 1
+
+    def inject_failure(self, after_layers):
+        """mx_engine_inject_failure (test hook): the next step stops with
+        MX_EHIP after launching `after_layers` layers (eager mode)."""
+        check(lib.mx_engine_inject_failure(self.h, after_layers))
 
     def profile_step(self, slots, tokens):
         """One eager decode step with per-layer expert-kernel timing."""

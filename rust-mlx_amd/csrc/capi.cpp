@@ -589,12 +589,25 @@ MX_ABI mx_status mx_engine_reset_slot(mx_engine* e, int32_t slot) {
 MX_ABI mx_status mx_engine_clone_slot(mx_engine* e, int32_t src, int32_t dst) {
   MX_CHECK(e && slot_ok(*e->impl, src) && slot_ok(*e->impl, dst) && src != dst, MX_EINVAL,
            "mx_engine_clone_slot: bad engine or slots");
+  MX_CHECK(!engine_slot_failed(*e->impl, src), MX_ESTATE,
+           "mx_engine_clone_slot: the source slot was left partly updated by a failed step");
   return finish(engine_clone_slot(*e->impl, src, dst), "mx_engine_clone_slot");
 }
 
 MX_ABI int32_t mx_engine_offset(mx_engine* e, int32_t slot) {
   if (!e || !slot_ok(*e->impl, slot)) return -1;
   return engine_offset(*e->impl, slot);
+}
+
+MX_ABI int32_t mx_engine_slot_failed(mx_engine* e, int32_t slot) {
+  if (!e || !slot_ok(*e->impl, slot)) return -1;
+  return engine_slot_failed(*e->impl, slot);
+}
+
+MX_ABI mx_status mx_engine_inject_failure(mx_engine* e, int32_t after_layers) {
+  MX_CHECK(e && after_layers >= 0, MX_EINVAL, "mx_engine_inject_failure: bad arguments");
+  engine_inject_failure(*e->impl, after_layers);
+  return MX_OK;
 }
 
 static mx_status decode_common(mx_engine* e, const int32_t* slots, const uint32_t* tokens,

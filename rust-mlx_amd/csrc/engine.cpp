@@ -144,6 +144,11 @@ struct Engine {
   std::vector<int32_t> offsets;
   bool want_logits = false;
   int last_rows = 0;
+  // slots whose caches a failed step left partly advanced (refused until a
+  // reset or a clone replaces them); a test hook makes the next step fail
+  // after `fail_after` layers have been launched
+  std::vector<uint8_t> failed;
+  int fail_after = 0;
   // captured graphs keyed by (rows, groups, t, history, logits)
   std::map<int, hipGraphExec_t> graphs;
   bool use_graphs = true;
@@ -480,6 +485,7 @@ int build(Engine& e) {
     return MX_ENOMEM;
   std::memset(e.host_rows, 0, sizeof(Engine::RowTable));
   e.offsets.assign(c.max_slots, 0);
+  e.failed.assign(c.max_slots, 0);
   if (hipStreamSynchronize(e.stream) != hipSuccess) return MX_EHIP;
   return MX_OK;
 }
@@ -739,7 +745,18 @@ int record_step(Engine& e, int rows, int groups, int t, bool history, bool logit
   const auto& c = e.cfg;
   Engine::RowTable* rt = e.dev_rows;
   MX_TRY(embed(e.embed, rt->tokens, rows, c.hc, e.h, e.stream));
-  for (const LayerW& L : e.layers) MX_TRY(record_layer(e, L, rows, groups, t, history));
+  int launched = 0;
+  for (const LayerW& L : e.layers) {
+    MX_TRY(record_layer(e, L, rows, groups, t, history));
+    if (e.fail_after > 0 && ++launched == e.fail_after) {
+      // the injected failure: the launched layers run, then the step stops
+      // as a failed launch would
+      // (under graph capture nothing has run yet: the capture is dropped)
+      e.fail_after = 0;
+      if (!e.use_graphs) (void)hipStreamSynchronize(e.stream);
+      return MX_EHIP;
+    }
+  }
   // mixer + greedy head
   MX_TRY(hc_forward(e, e.mixer, rows, e.mixed, nullptr));
   return record_head(e, rows, logits);
@@ -887,11 +904,13 @@ int engine_reset_slot(Engine& e, int slot) {
   MX_HIP(hipMemsetAsync(e.conv_state + size_t(slot) * e.n_gdn * cp, 0, e.n_gdn * cp * 2, e.stream));
   MX_HIP(hipStreamSynchronize(e.stream));
   e.offsets[slot] = 0;
+  e.failed[slot] = 0;
   if (e.verify_slot == slot) e.verify_slot = -1;
   return MX_OK;
 }
 
 int engine_clone_slot(Engine& e, int src, int dst) {
+  if (e.failed[src]) return MX_ESTATE;  // nothing intact to copy
   const size_t sp = state_per(e), cp = conv_per(e);
   const int64_t kv = e.ad.slot_stride;
   MX_HIP(hipMemcpyAsync(e.gdn_state + size_t(dst) * e.n_gdn * sp,
@@ -912,6 +931,7 @@ int engine_clone_slot(Engine& e, int src, int dst) {
   }
   MX_HIP(hipStreamSynchronize(e.stream));
   e.offsets[dst] = e.offsets[src];
+  e.failed[dst] = 0;
   // the copy replaces the caches a pending verify block of dst would roll back
   if (dst == e.verify_slot) e.verify_slot = -1;
   return MX_OK;
@@ -919,8 +939,38 @@ int engine_clone_slot(Engine& e, int src, int dst) {
 
 int engine_offset(const Engine& e, int slot) { return e.offsets[slot]; }
 
+// A step that fails after its first launch leaves the GDN state and conv
+// windows of its slots partly advanced (they are updated in place; the
+// reference's lazy evaluation never writes a cache before the whole step has
+// succeeded, src/batching.rs:136-137).  Those slots are marked failed and
+// refused until reset_slot or clone_slot replaces their caches, so no later
+// step reads them as if they were intact; their offsets do not advance.
+int step_failed(Engine& e, const int32_t* slots, int n, int rc, std::string* err) {
+  for (int r = 0; r < n; ++r) e.failed[slots[r]] = 1;
+  for (int r = 0; r < n; ++r)
+    if (slots[r] == e.verify_slot) e.verify_slot = -1;
+  if (err->empty())
+    *err = "the step failed after updating its slots' caches in place; reset or clone over "
+           "those slots before using them again";
+  return rc;
+}
+
+int slots_usable(const Engine& e, const int32_t* slots, int n, std::string* err) {
+  for (int r = 0; r < n; ++r)
+    if (e.failed[slots[r]]) {
+      *err = "slot " + std::to_string(slots[r]) +
+             " was left partly updated by a failed step; reset it or clone a prefix into it";
+      return MX_ESTATE;
+    }
+  return MX_OK;
+}
+
+int engine_slot_failed(const Engine& e, int slot) { return e.failed[slot]; }
+void engine_inject_failure(Engine& e, int after_layers) { e.fail_after = after_layers; }
+
 int engine_decode_rows(Engine& e, const int32_t* slots, const uint32_t* tokens, int rows,
                        uint32_t* next, std::string* err) {
+  MX_TRY(slots_usable(e, slots, rows, err));
   for (int r = 0; r < rows; ++r) {
     for (int q = 0; q < r; ++q)
       if (slots[q] == slots[r]) {
@@ -936,7 +986,8 @@ int engine_decode_rows(Engine& e, const int32_t* slots, const uint32_t* tokens, 
     e.host_rows->gdn_slots[r] = slots[r] * e.n_gdn;
     e.host_rows->pos[r] = e.offsets[slots[r]];
   }
-  MX_TRY(run_step(e, rows, rows, 1, false, next));
+  const int rc = run_step(e, rows, rows, 1, false, next);
+  if (rc != MX_OK) return step_failed(e, slots, rows, rc, err);
   for (int r = 0; r < rows; ++r) e.offsets[slots[r]] += 1;
   // a decode step invalidates any pending verify block of these slots
   for (int r = 0; r < rows; ++r)
@@ -974,6 +1025,7 @@ int engine_decode_forced(Engine& e, const int32_t* slots, const uint32_t* tokens
                          const uint16_t* h_in, uint16_t* h_out, uint32_t* ids_out,
                          uint32_t* next, std::string* err) {
   const auto& c = e.cfg;
+  MX_TRY(slots_usable(e, slots, rows, err));
   for (int r = 0; r < rows; ++r) {
     for (int q = 0; q < r; ++q)
       if (slots[q] == slots[r]) {
@@ -1019,6 +1071,7 @@ int engine_decode_forced(Engine& e, const int32_t* slots, const uint32_t* tokens
 // One chunk of up to 8 consecutive tokens of one slot (prefill or verify).
 int engine_block(Engine& e, int slot, const uint32_t* tokens, int count, bool history,
                  uint32_t* next, std::string* err) {
+  MX_TRY(slots_usable(e, &slot, 1, err));
   if (e.offsets[slot] + count > e.cfg.max_context) {
     *err = "slot context is full";
     return MX_ESTATE;
@@ -1032,13 +1085,17 @@ int engine_block(Engine& e, int slot, const uint32_t* tokens, int count, bool hi
   // a prefill block (no history) moves the caches past any pending verify
   // block of this slot, whose snapshot and history no longer apply
   if (!history && slot == e.verify_slot) e.verify_slot = -1;
-  MX_TRY(run_step(e, count, 1, count, history, next));
+  const int rc = run_step(e, count, 1, count, history, next);
+  if (rc != MX_OK) return step_failed(e, &slot, 1, rc, err);
   e.offsets[slot] += count;
   return MX_OK;
 }
 
 int engine_verify(Engine& e, int slot, const uint32_t* tokens, int count, uint32_t* next,
                   std::string* err) {
+  // a failed slot is refused before its (partly updated) caches are
+  // snapshotted, so a failure below always comes from this block's own step
+  MX_TRY(slots_usable(e, &slot, 1, err));
   // snapshot the recurrent state so that keep = 0 can restore it
   const size_t sp = state_per(e), cp = conv_per(e);
   MX_HIP(hipMemcpyAsync(e.snap_state, e.gdn_state + size_t(slot) * e.n_gdn * sp, e.n_gdn * sp * 4,
@@ -1046,7 +1103,22 @@ int engine_verify(Engine& e, int slot, const uint32_t* tokens, int count, uint32
   MX_HIP(hipMemcpyAsync(e.snap_conv, e.conv_state + size_t(slot) * e.n_gdn * cp, e.n_gdn * cp * 2,
                         hipMemcpyDeviceToDevice, e.stream));
   const int base = e.offsets[slot];
-  MX_TRY(engine_block(e, slot, tokens, count, true, next, err));
+  const int rc = engine_block(e, slot, tokens, count, true, next, err);
+  if (rc != MX_OK) {
+    // a failed verify block puts back the snapshot it took: the state and
+    // conv window return to the block's start, the offset never moved, and
+    // the KV rows past it are overwritten before they are read
+    if (e.failed[slot] &&
+        hipMemcpyAsync(e.gdn_state + size_t(slot) * e.n_gdn * sp, e.snap_state, e.n_gdn * sp * 4,
+                       hipMemcpyDeviceToDevice, e.stream) == hipSuccess &&
+        hipMemcpyAsync(e.conv_state + size_t(slot) * e.n_gdn * cp, e.snap_conv, e.n_gdn * cp * 2,
+                       hipMemcpyDeviceToDevice, e.stream) == hipSuccess &&
+        hipStreamSynchronize(e.stream) == hipSuccess) {
+      e.failed[slot] = 0;
+      *err += " (the verify block's snapshot restored the slot)";
+    }
+    return rc;
+  }
   e.verify_slot = slot;
   e.verify_count = count;
   e.verify_base = base;
@@ -1457,6 +1529,7 @@ int engine_fill_slot(Engine& e, int slot, int length, uint64_t seed, std::string
   }
   MX_HIP(hipStreamSynchronize(e.stream));
   e.offsets[slot] = length;
+  e.failed[slot] = 0;
   if (e.verify_slot == slot) e.verify_slot = -1;
   return MX_OK;
 }

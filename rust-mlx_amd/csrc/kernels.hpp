@@ -289,6 +289,8 @@ void engine_destroy(Engine* e);
 int engine_reset_slot(Engine& e, int slot);
 int engine_clone_slot(Engine& e, int src, int dst);
 int engine_offset(const Engine& e, int slot);
+int engine_slot_failed(const Engine& e, int slot);
+void engine_inject_failure(Engine& e, int after_layers);
 int engine_decode_rows(Engine& e, const int32_t* slots, const uint32_t* tokens, int rows,
                        uint32_t* next, std::string* err);
 int engine_decode_outputs(Engine& e, const int32_t* slots, const uint32_t* tokens, int rows,

@@ -226,3 +226,54 @@ def test_fast_mode_within_tolerance_of_oracle(pair):
         from oracle import oracle as orc
         lg = orc.bf16_to_f32(model._qmv(model.head, model.last_mixed))[0]
         assert abs(lg[got[0]] - lg[want[0]]) <= 2e-2 * abs(lg[want[0]]) + 1e-2
+
+
+def test_a_failed_step_leaves_no_slot_silently_corrupted(mx):
+    """A step that fails after some of its layers ran (forced from the host
+    with mx_engine_inject_failure, eager launches) has updated its slots' GDN
+    state and conv windows in place; those slots are marked failed and every
+    later use returns MX_ESTATE until a reset or a clone replaces them.  The
+    offsets do not advance.  A failed verify block restores its snapshot, so
+    its slot stays usable and a later verify equals one on an untouched copy.
+    (The reference's lazy evaluation keeps every caller's cache intact on a
+    GPU error, src/batching.rs:136-137.)"""
+    cfg = dict(mx.TINY)
+    eng = mx.Engine(cfg)
+    try:
+        eng.set_flags(exact=True, eager=True)
+        prompt = [5, 17, 300, 9, 2, 44]
+        nxt = eng.prefill(0, prompt)
+        for s in (1, 2, 3):
+            eng.clone(0, s)
+        base = eng.offset(0)
+        # a decode step failing after two of the four layers
+        eng.inject_failure(2)
+        with pytest.raises(mx.MxError) as ex:
+            eng.decode_batch([0, 1], [nxt, nxt], equal=False)
+        assert ex.value.code == mx.MX_EHIP
+        assert eng.slot_failed(0) and eng.slot_failed(1) and not eng.slot_failed(2)
+        assert eng.offset(0) == base and eng.offset(1) == base
+        for op in (lambda: eng.decode_batch([0], [nxt]), lambda: eng.prefill(1, [3]),
+                   lambda: eng.verify(0, [nxt, 3]), lambda: eng.clone(1, 4)):
+            with pytest.raises(mx.MxError) as ex:
+                op()
+            assert ex.value.code == mx.MX_ESTATE
+        # the untouched slot still decodes; a clone into a failed slot or a
+        # reset makes it usable again, and it then matches the untouched one
+        want = eng.decode_batch([2], [nxt])
+        eng.clone(3, 0)
+        assert not eng.slot_failed(0)
+        assert [int(t) for t in eng.decode_batch([0], [nxt])] == [int(t) for t in want]
+        eng.reset(1)
+        assert not eng.slot_failed(1) and eng.offset(1) == 0
+        assert eng.prefill(1, prompt) == nxt
+        # a failed verify block restores its snapshot: the slot stays usable
+        eng.clone(3, 5)
+        eng.inject_failure(3)
+        with pytest.raises(mx.MxError):
+            eng.verify(3, [nxt, 3, 7])
+        assert not eng.slot_failed(3) and eng.offset(3) == base
+        assert [int(t) for t in eng.verify(3, [nxt, 3, 7])] == \
+            [int(t) for t in eng.verify(5, [nxt, 3, 7])]
+    finally:
+        eng.close()
