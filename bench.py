@@ -179,7 +179,10 @@ def bench_config3(mx, args):
     # a second profiled step after the timed loop (longer contexts), then the
     # expert kernels of all 48 layers back to back on that step's routing
     _, prof2 = eng.profile_step(slots, toks)
-    et = eng.time_experts(rows)
+    reps = [eng.time_experts(rows) for _ in range(EXPERT_REPS)]
+    et = dict(reps[0])
+    et["gate_up_ms"] = sum(r["gate_up_ms"] for r in reps) / len(reps)
+    et["down_ms"] = sum(r["down_ms"] for r in reps) / len(reps)
     gu_gbs = et["gate_up_bytes"] / (et["gate_up_ms"] * 1e-3) / 1e9
     dn_gbs = et["down_bytes"] / (et["down_ms"] * 1e-3) / 1e9
     layers = prof["layers"]
@@ -226,10 +229,14 @@ def bench_config3(mx, args):
             "reference_policy_groups": len(groups),
         },
         "roofline": {"bound": "hbm",
-                     "kernel": ("xq_gate_up_kernel<4, 16, 3, true> (exact-integer expert gate/up + "
-                                "SwiGLU over the plan's work items, the form the step launches)") if exact else
-                               ("gate_up_persist_kernel<4, 16, 4, 2, 0> (route-taking form; the "
-                                "step launches the self-routing <4, 16, 4, 2, 8>)"),
+                     "kernel": (("xq_gate_up_kernel<4, 16, 3, true> (exact-integer expert gate/up + "
+                                 "SwiGLU over the plan's work items, the form the step launches)")
+                                if exact else
+                                ("gate_up_persist_kernel<4, 16, 4, 2, 0> (route-taking form; the "
+                                 "step launches the self-routing <4, 16, 4, 2, 8>)")) +
+                               f"; timing: HIP events on the engine stream around the {layers} "
+                               f"layers' launches run back to back on the last step's routing, "
+                               f"mean of {EXPERT_REPS} such runs, divided by {layers}",
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic("config3-b8-decode-exact_hbm-traffic.md" if exact
@@ -238,6 +245,11 @@ def bench_config3(mx, args):
                      "us_per_launch": round(gu_us, 2)},
         "cpu_baseline": cpu,
     }
+
+
+# back-to-back runs of the 48 expert gate/up (and down) launches averaged for
+# the roofline figure
+EXPERT_REPS = 4
 
 
 def step_dtype(exact: bool, widths: str) -> str:
@@ -881,7 +893,102 @@ DEFAULTS = {"config3-b8-decode": (240, 16), "qmv-config0": (2000, 200),
             "moe-config2": (200, 20), "mtp-config4": (1, 0), "copy-calibration": (10, 2)}
 
 
+def short_kernel_name(name: str) -> str:
+    """A kernel's name without namespaces, return type and argument list."""
+    import re
+    name = name.replace("mx::(anonymous namespace)::", "").replace("void ", "")
+    m = re.match(r"([\w]+(?:<[^>]*>)?)", name)
+    return m.group(1) if m else name[:60]
+
+
+def summarize_trace(path: str, line_path=None, kernel="xq_gate_up_kernel") -> None:
+    """Markdown summary of a rocprofv3 kernel trace of this script
+    (`--kernel-trace --output-format csv`, the *_kernel_trace.csv file):
+
+    * every run of >= 16 consecutive launches of `kernel` (the back-to-back
+      launches behind the roofline figure; inside a step other kernels
+      separate them), with the mean kernel duration and first-start-to-last-end
+      span per launch; with `line_path` (the JSON line the same run printed),
+      `frac` recomputed from the trace's mean beside the line's own;
+    * when the trace holds whole eager steps: one step (the kernels after the
+      third launch of the exact head up to and including the fourth) by
+      kernel and grid, with the hyper-connection kernels (norm, 8192-deep
+      down projection, up-mix) summed."""
+    import csv
+    import gzip
+    import io
+    fh = gzip.open(path) if path.endswith(".gz") else open(path, "rb")
+    rows = list(csv.DictReader(io.TextIOWrapper(fh, "utf-8")))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+
+    def dur(r):
+        return (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+
+    names = [short_kernel_name(r["Kernel_Name"]) for r in rows]
+    runs, i = [], 0
+    while i < len(rows):
+        j = i
+        while j < len(rows) and names[j] == names[i]:
+            j += 1
+        if j - i >= 16 and names[i].startswith(kernel):
+            runs.append((i, j))
+        i = j
+    print(f"## Back-to-back launches of `{kernel}`\n")
+    print("| run | kernel | launches | mean us | span us / launch |")
+    print("|---:|---|---:|---:|---:|")
+    all_d = []
+    for n, (i, j) in enumerate(runs):
+        d = [dur(r) for r in rows[i:j]]
+        all_d += d
+        span = (int(rows[j - 1]["End_Timestamp"]) - int(rows[i]["Start_Timestamp"])) / 1e3
+        print(f"| {n} | `{names[i]}` | {j - i} | {sum(d) / len(d):.2f} | {span / (j - i):.2f} |")
+    if all_d:
+        mean = sum(all_d) / len(all_d)
+        print(f"\nmean over {len(all_d)} back-to-back launches: {mean:.2f} us")
+        if line_path:
+            line = None
+            for text in open(line_path):
+                text = text.strip()
+                if text.startswith("{"):
+                    line = json.loads(text)
+            rf = line["roofline"]
+            b = rf["algorithmic_bytes_per_launch"]
+            frac = b / (mean * 1e-6) / 1e9 / rf["peak"]
+            print(f"algorithmic bytes per launch (the line's): {b}")
+            print(f"frac from the trace: {frac:.4f}; the line's frac: {rf['frac']} "
+                  f"(us_per_launch {rf['us_per_launch']}); ratio {frac / rf['frac']:.4f}")
+    heads = [k for k, nm in enumerate(names) if nm.startswith("xq_head_kernel")]
+    if len(heads) < 4:
+        return
+    a, b = heads[2], heads[3]
+    step = rows[a + 1:b + 1]
+    groups = {}
+    for r, nm in zip(step, names[a + 1:b + 1]):
+        wg = int(r["Workgroup_Size_X"])
+        grid = (int(r["Grid_Size_X"]) // wg, int(r["Grid_Size_Y"]) // int(r["Workgroup_Size_Y"]),
+                int(r["Grid_Size_Z"]) // int(r["Workgroup_Size_Z"]))
+        groups.setdefault((nm, grid, wg), []).append(dur(r))
+    tot = sum(sum(v) for v in groups.values())
+    span = (int(step[-1]["End_Timestamp"]) - int(step[0]["Start_Timestamp"])) / 1e3
+    print(f"\n## One step\n\n{len(step)} launches, {tot / 1e3:.3f} ms of kernel time, "
+          f"{span / 1e3:.3f} ms first start to last end\n")
+    print("| kernel | workgroups (x, y, z) | threads | calls/step | avg us | ms/step | share |")
+    print("|---|---|---:|---:|---:|---:|---:|")
+    for (nm, grid, wg), v in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        print(f"| `{nm}` | {grid} | {wg} | {len(v)} | {sum(v) / len(v):.1f} | "
+              f"{sum(v) / 1e3:.3f} | {sum(v) / tot * 100:.1f} % |")
+    hc = [(k, v) for k, v in groups.items()
+          if k[0].startswith(("hc_norm_kernel", "xq_upmix_kernel", "xq_dense_kernel<4, 1,"))]
+    hc_us = sum(sum(v) for _, v in hc)
+    print(f"\nhyper-connection family (norm + HC down + up-mix): "
+          f"{sum(len(v) for _, v in hc)} launches, {hc_us / 1e3:.3f} ms per step")
+
+
 def main() -> None:
+    if len(sys.argv) >= 3 and sys.argv[1] == "--summarize-trace":
+        # no device work: summarise a rocprofv3 kernel trace of an earlier run
+        summarize_trace(sys.argv[2], sys.argv[3] if len(sys.argv) > 3 else None)
+        return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)

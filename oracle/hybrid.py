@@ -8,8 +8,8 @@ It restates, in numpy float32 and in the reference's own tensor names:
   MoE::parts / forward_write (softmax, top-k, normalised scores, shared
     expert times sigmoid gate)               src/hybrid.rs:192-300
   Gdn::forward_reference, gdn_reference      src/hybrid.rs:369-495
-  Qsa::forward while the sparse indexer is idle (nblocks <= budget/ratio)
-                                             src/qsa.rs:66-105
+  Qsa::forward, dense (nblocks <= budget/ratio) and sparse (indexer block
+    scores, top budget/ratio blocks + causal tail)   src/qsa.rs:66-176
   Attention::forward_selection (gated: q|gate split, norm, text RoPE,
     causal SDPA, sigmoid output gate)        src/dense.rs:139-270
   text RoPE                                  src/rope.rs:8-28, kernels/text_rope.metal
@@ -22,8 +22,8 @@ It restates, in numpy float32 and in the reference's own tensor names:
 
 Pinned by the reference's end-to-end fixture tests/fixtures/hybrid (prefill
 logits within 1e-4 and its greedy tokens, as src/bin/hybrid-parity.rs checks;
-a copy lives under tests/golden/hybrid).  Positions where the reference's QSA
-indexer would select sparse blocks are refused, not approximated.
+a copy lives under tests/golden/hybrid), including the decode steps after
+the QSA indexer has switched to sparse block selection.
 Mtp.forward has no fixture in the reference: parity unpinned (its
 composition is restated from src/mtp.rs:72-127 and cross-checked against the
 oracle's draft step only).
@@ -275,12 +275,13 @@ class Gdn:
 
 
 # -------------------------------------------------------------- attention --
-def rope_text(x, rot, theta, offset):
-    """x [heads, t, d] at positions offset..offset+t-1; the first rot values
-    rotate as two halves (src/rope.rs:16-24, kernels/text_rope.metal)."""
+def rope_text(x, rot, theta, offset, stride=1):
+    """x [heads, t, d] at positions (offset + i) * stride, i < t
+    (runtime_prepare::positions, src/runtime_prepare.rs:61-66); the first rot
+    values rotate as two halves (src/rope.rs:8-57, kernels/text_rope.metal)."""
     half = rot // 2
     inv = (F32(1.0) / np.power(F32(theta), np.arange(0, rot, 2, dtype=F32) / F32(rot))).astype(F32)
-    pos = np.arange(offset, offset + x.shape[1], dtype=F32)
+    pos = (np.arange(offset, offset + x.shape[1]) * stride).astype(F32)
     ang = (pos[:, None] * inv[None, :]).astype(F32)
     c, s = np.cos(ang).astype(F32), np.sin(ang).astype(F32)
     y = x.copy()
@@ -307,16 +308,73 @@ class Attention:
         self.eps = c["rms_norm_eps"]
         self.budget = c.get("indexer_budget")
         self.ratio = c.get("indexer_compress_ratio")
+        self.index = None
+        if w.has(p + ".indexer.index_qk_proj.weight"):
+            # Qsa::load (src/qsa.rs:35-64): the indexer's q|k projection and norms
+            self.index = w.linear(p + ".indexer.index_qk_proj")
+            self.iqs = w.tensor(p + ".indexer.q_layernorm.weight")
+            self.iks = w.tensor(p + ".indexer.k_layernorm.weight")
+            self.ih, self.idim = c["indexer_n_heads"], c["indexer_head_dim"]
 
     def new_cache(self):
         return {"k": np.zeros((self.kvh, 0, self.hd), F32),
-                "v": np.zeros((self.kvh, 0, self.hd), F32), "offset": 0, "len": 0}
+                "v": np.zeros((self.kvh, 0, self.hd), F32), "offset": 0, "len": 0,
+                "raw": None, "blocks": None}
+
+    def index_mask(self, x, cache):
+        """Qsa::forward's indexer (src/qsa.rs:66-176) for rows x [t, H] at the
+        cache's offset: the boolean attention mask [t, L] over all L cached
+        positions, or None while the regime is dense (nblocks <= budget /
+        ratio: plain causal attention).  Raw keys (the projection's last head)
+        accumulate every step; each complete block of `ratio` raw keys is
+        averaged, normed and rotated at position block * ratio once; a query's
+        block score is sum over indexer heads of relu(q . block) / sqrt(dim);
+        a row attends to its top budget / ratio complete blocks plus its own
+        incomplete tail (causal) once more than budget / ratio blocks are
+        complete, else causally."""
+        t, ratio, d = x.shape[0], self.ratio, self.idim
+        offset = cache["offset"]
+        qk = lin(x, self.index).reshape(t, self.ih + 1, d)
+        raw = qk[:, self.ih]
+        cache["raw"] = raw.copy() if cache["raw"] is None else np.concatenate([cache["raw"], raw], 0)
+        raw = cache["raw"]
+        L = raw.shape[0]
+        nb, topk = L // ratio, self.budget // ratio
+        if nb <= topk:
+            return None
+        q = norm(qk[:, :self.ih], self.iqs, self.eps).transpose(1, 0, 2)    # [ih, t, d]
+        q = rope_text(q, self.rot, self.theta, offset)
+        old = 0 if cache["blocks"] is None else cache["blocks"].shape[0]
+        if nb > old:
+            new = raw[old * ratio:nb * ratio].astype(F32).reshape(nb - old, ratio, d).mean(1)
+            new = norm(new.astype(F32), self.iks, self.eps)
+            new = rope_text(new[None], self.rot, self.theta, old, ratio)[0]
+            cache["blocks"] = new if cache["blocks"] is None else np.concatenate([cache["blocks"], new], 0)
+        blocks = cache["blocks"]
+        scores = (np.maximum((q @ blocks.T).astype(F32), F32(0)).sum(0)
+                  / F32(np.sqrt(F32(d)))).astype(F32)                          # [t, nb]
+        ends = offset + 1 + np.arange(t)
+        complete = ends // ratio
+        valid = np.arange(nb)[None, :] < complete[:, None]
+        scores = np.where(valid, scores, -np.inf)
+        selected = np.argpartition(scores, -topk, axis=-1)[:, -topk:]
+        chosen = np.zeros((t, nb), bool)
+        np.put_along_axis(chosen, selected, True, axis=-1)
+        token_blocks = np.minimum(np.arange(L) // ratio, nb - 1)
+        ids = np.arange(L)[None, :]
+        tail = ids >= (complete * ratio)[:, None]
+        causal = ids < ends[:, None]
+        sparse = (chosen[:, token_blocks] | tail) & causal
+        return np.where((complete > topk)[:, None], sparse, causal)
 
     def forward(self, x, cache, rope_offset=None):
         t = x.shape[0]
         cache["len"] += t
-        if self.budget and cache["len"] // self.ratio > self.budget // self.ratio:
-            raise NotImplementedError("the sparse QSA indexer regime is not restated")
+        allowed = None
+        if self.index is not None:
+            allowed = self.index_mask(x, cache)
+        elif self.budget and cache["len"] // self.ratio > self.budget // self.ratio:
+            raise NotImplementedError("the sparse QSA regime needs the indexer's tensors")
         H, hd = self.heads, self.hd
         qg = lin(x, self.q).reshape(t, H, 2, hd)
         q, gate = qg[:, :, 0], qg[:, :, 1]
@@ -337,8 +395,9 @@ class Attention:
         for h in range(H):
             sc = (q[h] @ Kc[h // rep].T * F32(hd ** -0.5)).astype(F32)   # [t, L]
             L = Kc.shape[1]
-            mask = np.arange(L)[None, :] > (old + np.arange(t))[:, None]
-            sc = np.where(mask, -np.inf, sc)
+            if allowed is None:
+                allowed = np.arange(L)[None, :] <= (old + np.arange(t))[:, None]
+            sc = np.where(allowed, sc, -np.inf)
             p = np.exp(sc - sc.max(-1, keepdims=True))
             p = (p / p.sum(-1, keepdims=True)).astype(F32)
             out[:, h] = p @ Vc[h // rep]
