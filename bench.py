@@ -905,13 +905,15 @@ def summarize_trace(path: str, line_path=None, kernel="xq_gate_up_kernel") -> No
     """Markdown summary of a rocprofv3 kernel trace of this script
     (`--kernel-trace --output-format csv`, the *_kernel_trace.csv file):
 
-    * every run of >= 16 consecutive launches of `kernel` (the back-to-back
-      launches behind the roofline figure; inside a step other kernels
-      separate them), with the mean kernel duration and first-start-to-last-end
-      span per launch; with `line_path` (the JSON line the same run printed),
-      `frac` recomputed from the trace's mean beside the line's own;
+    * every run of >= 16 launches of `kernel` each starting within 5 us of
+      the previous one's end (the back-to-back launches behind the roofline
+      figure; inside a step a layer's other kernels separate them, also when
+      the trace was filtered to `kernel` alone), with the mean kernel duration
+      and first-start-to-last-end span per launch; with `line_path` (the JSON
+      line the same run printed), `frac` recomputed from the trace's mean
+      beside the line's own;
     * when the trace holds whole eager steps: one step (the kernels after the
-      third launch of the exact head up to and including the fourth) by
+      third launch of the greedy head up to and including the fourth) by
       kernel and grid, with the hyper-connection kernels (norm, 8192-deep
       down projection, up-mix) summed."""
     import csv
@@ -925,13 +927,15 @@ def summarize_trace(path: str, line_path=None, kernel="xq_gate_up_kernel") -> No
         return (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
 
     names = [short_kernel_name(r["Kernel_Name"]) for r in rows]
+    mine = [k for k, nm in enumerate(names) if nm.startswith(kernel)]
     runs, i = [], 0
-    while i < len(rows):
-        j = i
-        while j < len(rows) and names[j] == names[i]:
+    while i < len(mine):
+        j = i + 1
+        while (j < len(mine) and mine[j] == mine[j - 1] + 1 and
+               int(rows[mine[j]]["Start_Timestamp"]) - int(rows[mine[j - 1]]["End_Timestamp"]) < 5000):
             j += 1
-        if j - i >= 16 and names[i].startswith(kernel):
-            runs.append((i, j))
+        if j - i >= 16:
+            runs.append((mine[i], mine[j - 1] + 1))
         i = j
     print(f"## Back-to-back launches of `{kernel}`\n")
     print("| run | kernel | launches | mean us | span us / launch |")
@@ -957,7 +961,7 @@ def summarize_trace(path: str, line_path=None, kernel="xq_gate_up_kernel") -> No
             print(f"algorithmic bytes per launch (the line's): {b}")
             print(f"frac from the trace: {frac:.4f}; the line's frac: {rf['frac']} "
                   f"(us_per_launch {rf['us_per_launch']}); ratio {frac / rf['frac']:.4f}")
-    heads = [k for k, nm in enumerate(names) if nm.startswith("xq_head_kernel")]
+    heads = [k for k, nm in enumerate(names) if nm.startswith(("xq_head_kernel", "head_kernel"))]
     if len(heads) < 4:
         return
     a, b = heads[2], heads[3]
@@ -984,7 +988,50 @@ def summarize_trace(path: str, line_path=None, kernel="xq_gate_up_kernel") -> No
           f"{sum(len(v) for _, v in hc)} launches, {hc_us / 1e3:.3f} ms per step")
 
 
+def summarize_counters(fetch_csv: str, write_csv: str, fetch_scale: float, write_scale: float,
+                       kernel="xq_gate_up_kernel") -> None:
+    """Markdown table of HBM bytes per dispatch from two rocprofv3 `--pmc`
+    runs of this script (FETCH_SIZE, then WRITE_SIZE; the
+    *_counter_collection.csv files): per (kernel, grid size), the median
+    counter over its dispatches times the copy calibration (bytes per KiB
+    the counter reports for a device copy of known size, the
+    copy-calibration workload), then `traffic_bytes_per_launch` of `kernel`
+    (fetched + written) as the roofline's `traffic` reads it."""
+    import csv
+    import gzip
+    import io
+    import statistics
+
+    def load(path, counter):
+        out = {}
+        fh = gzip.open(path) if path.endswith(".gz") else open(path, "rb")
+        for r in csv.DictReader(io.TextIOWrapper(fh, "utf-8")):
+            if r["Counter_Name"] == counter:
+                key = (short_kernel_name(r["Kernel_Name"]), int(r["Grid_Size"]))
+                out.setdefault(key, []).append(float(r["Counter_Value"]))
+        return out
+
+    f, w = load(fetch_csv, "FETCH_SIZE"), load(write_csv, "WRITE_SIZE")
+    fs, ws = fetch_scale * 1024, write_scale * 1024
+    print("| kernel | grid (threads) | dispatches | fetched MB | written MB |")
+    print("|---|---:|---:|---:|---:|")
+    for key in sorted(f, key=lambda k: -statistics.median(f[k])):
+        fm = statistics.median(f[key]) * fs / 1e6
+        wm = statistics.median(w.get(key, [0.0])) * ws / 1e6
+        if fm + wm >= 0.01:
+            print(f"| `{key[0]}` | {key[1]} | {len(f[key])} | {fm:.2f} | {wm:.3f} |")
+    tops = [k for k in f if k[0].startswith(kernel)]
+    if tops:
+        key = max(tops, key=lambda k: statistics.median(f[k]))  # the batch-8 grid
+        tb = statistics.median(f[key]) * fs + statistics.median(w.get(key, [0.0])) * ws
+        print(f"\ntraffic_bytes_per_launch = {int(tb)}")
+
+
 def main() -> None:
+    if len(sys.argv) >= 6 and sys.argv[1] == "--summarize-counters":
+        # no device work: summarise two rocprofv3 counter runs of this script
+        summarize_counters(sys.argv[2], sys.argv[3], float(sys.argv[4]), float(sys.argv[5]))
+        return
     if len(sys.argv) >= 3 and sys.argv[1] == "--summarize-trace":
         # no device work: summarise a rocprofv3 kernel trace of an earlier run
         summarize_trace(sys.argv[2], sys.argv[3] if len(sys.argv) > 3 else None)
