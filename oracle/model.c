@@ -187,7 +187,8 @@ void mxo_attn_prep(const uint16_t* qkv, int64_t qkv_stride, int rows, const int3
  * the kernels' order (attn.hip), then the output gate:
  *   per chunk: s_j = ((q.k_j) as four fma chains d mod 4, (c0+c1)+(c2+c3)) * scale;
  *   m = max s; p_j = e^(s_j - m); l = per-64 butterflies of p summed in wave order;
- *   o[d] = fma chain over j of p_j v_j[d];
+ *   o[d] = ((o_0 + o_1) + o_2) + o_3, o_w the fma chain over the chunk's
+ *   positions 64 w .. 64 w + 63 (ascending) of p_j v_j[d];
  *   combine: M = max m_c; w_c = e^(m_c - M); L = fma(l_c, w_c, L); O = fma(o_c, w_c, O);
  *   y = bf16(bf16(O / L) * sigmoid_bf16(gate)). */
 void mxo_attention(const uint16_t* q, const uint16_t* qkv, int64_t qkv_stride, int rows,
@@ -235,10 +236,14 @@ void mxo_attention(const uint16_t* q, const uint16_t* qkv, int64_t qkv_stride, i
         ms[2 * c + 1] = ((w4[0] + w4[1]) + w4[2]) + w4[3];
         const int jend = n_pos - j0 < CH ? n_pos - j0 : CH;
         for (int d = 0; d < hd; ++d) {
-          float o = 0.0f;
-          for (int jj = 0; jj < jend; ++jj)
-            o = fmaf(p[jj], bf(v_cache[base + (int64_t)(j0 + jj) * hd + d]), o);
-          os[(int64_t)c * hd + d] = o;
+          float ow[4];
+          for (int w = 0; w < 4; ++w) {
+            ow[w] = 0.0f;
+            const int jb = jend < 64 * w + 64 ? jend : 64 * w + 64;
+            for (int jj = 64 * w; jj < jb; ++jj)
+              ow[w] = fmaf(p[jj], bf(v_cache[base + (int64_t)(j0 + jj) * hd + d]), ow[w]);
+          }
+          os[(int64_t)c * hd + d] = ((ow[0] + ow[1]) + ow[2]) + ow[3];
         }
       }
       float M = ms[0];

@@ -15,6 +15,8 @@
 // Decoding splits each row's positions into chunks of kAttnChunk; a workgroup
 // handles one (chunk, kv head, row) for all q heads sharing the kv head, so K
 // and V stream once per group.  A second pass combines the chunks.
+#include <type_traits>
+
 #include "common.hpp"
 #include "kernels.hpp"
 #include "skinny_core.hpp"
@@ -101,19 +103,24 @@ __global__ __launch_bounds__(64) void prep_kernel(const uint16_t* __restrict__ q
 // Scores: thread t owns position j = chunk*C + t; s = (q . k_j) * scale, the dot
 // as four interleaved fma chains over d (d mod 4), then (c0+c1)+(c2+c3).
 // m = max_t s; p = e^(s - m); l = sum_t p (xor butterfly per wave, waves in
-// order).  Values: thread t owns dim t; o = sum_j p_j v_j[t] (fma chain, j
-// ascending).  Writes (m, l) and o (fp32) per (row, head, chunk).  A
-// workgroup takes G of the kv head's q heads (`splits` workgroups per kv
-// head), so short contexts still spread over many workgroups.
-template <int G>
+// order).  Values: wave w takes the chunk's positions 64 w .. 64 w + 63 and
+// lane l the dims DPL l .. DPL l + DPL - 1 (DPL = head_dim / 64); per (head,
+// dim) one fma chain over the wave's positions ascending, then the four
+// waves' sums added in wave order, ((o0 + o1) + o2) + o3.  Writes (m, l) and
+// o (fp32) per (row, head, chunk).  A workgroup takes G of the kv head's q
+// heads (`splits` workgroups per kv head), so short contexts still spread
+// over many workgroups.
+template <int G, int DPL>
 __global__ __launch_bounds__(kAttnChunk) void decode_kernel(
     const uint16_t* __restrict__ q, const int32_t* __restrict__ slots,
     const int32_t* __restrict__ pos, const uint16_t* __restrict__ k_cache,
     const uint16_t* __restrict__ v_cache, AttnDims d, int max_chunks, float scale,
     float* __restrict__ o_part, float* __restrict__ ml_part, int chunks, int rows) {
+  static_assert(kAttnChunk == 256, "four waves of 64 positions");
   __shared__ float qs[G][kMaxHd];
   __shared__ float ps[G][kAttnChunk];
   __shared__ float red[G][4];
+  __shared__ float ow[4][G][64 * DPL];
   // one-dimensional grid placed by XCD: workgroups go to the eight XCDs in
   // turn (id mod 8), so the `splits` workgroups of one (chunk, kv head, row)
   // -- which read the same K and V rows -- take ids congruent mod 8 and
@@ -131,55 +138,70 @@ __global__ __launch_bounds__(kAttnChunk) void decode_kernel(
   const int n_pos = pos[row] + 1;
   const int j0 = chunk * kAttnChunk;
   if (j0 >= n_pos) return;  // uniform per workgroup
-  const int hd = d.head_dim;
+  const int hd = d.head_dim;  // 64 DPL (checked on the host)
+  const size_t base = size_t(slots[row]) * d.slot_stride + size_t(kvh) * d.max_ctx * hd;
+  const int j = j0 + t;
+  const bool valid = j < n_pos;
+  const int wave = t >> 6, lane = t & 63;
+  // the position's whole K row is requested before the q heads are staged
+  // (one memory round trip); a position past the row's end reads the chunk's
+  // first row, which is in bounds, and ignores it
+  constexpr int N8 = 8 * DPL;  // 16-byte pieces per row
+  uint4 raw[N8];
+  {
+    const uint4* kr = reinterpret_cast<const uint4*>(k_cache + base + size_t(valid ? j : j0) * hd);
+#pragma unroll
+    for (int b = 0; b < N8; ++b) raw[b] = kr[b];
+  }
   for (int i = t; i < G * hd; i += kAttnChunk) {
     const int g = i / hd, c = i - g * hd;
     qs[g][c] = bf16_to_f32(q[(size_t(row) * d.heads + h0 + g) * hd + c]);
   }
   __syncthreads();
-  const size_t base = size_t(slots[row]) * d.slot_stride + size_t(kvh) * d.max_ctx * hd;
-  const int j = j0 + t;
-  const bool valid = j < n_pos;
   if (valid) {
-    // the row's K pieces are all requested before the first is used (one
-    // memory round trip per 16 pieces, not one per piece); the fma order is
-    // unchanged: chain d mod 4, dims ascending
-    const uint4* kr = reinterpret_cast<const uint4*>(k_cache + base + size_t(j) * hd);
-    const int n8 = hd >> 3;
+    // fma order: chain d mod 4, dims ascending
     float c0[G], c1[G], c2[G], c3[G];
     for (int g = 0; g < G; ++g) c0[g] = c1[g] = c2[g] = c3[g] = 0.0f;
-    for (int b0 = 0; b0 < n8; b0 += 16) {
-      uint4 raw[16];
 #pragma unroll
-      for (int b = 0; b < 16; ++b)
-        if (b0 + b < n8) raw[b] = kr[b0 + b];
-#pragma unroll
-      for (int b = 0; b < 16; ++b) {
-        if (b0 + b >= n8) break;
-        const int c = (b0 + b) * 8;
-        const float kv[8] = {u2f(raw[b].x << 16), u2f(raw[b].x & 0xffff0000u),
-                             u2f(raw[b].y << 16), u2f(raw[b].y & 0xffff0000u),
-                             u2f(raw[b].z << 16), u2f(raw[b].z & 0xffff0000u),
-                             u2f(raw[b].w << 16), u2f(raw[b].w & 0xffff0000u)};
-        for (int g = 0; g < G; ++g) {
-          c0[g] = fmaf_(qs[g][c + 0], kv[0], c0[g]);
-          c1[g] = fmaf_(qs[g][c + 1], kv[1], c1[g]);
-          c2[g] = fmaf_(qs[g][c + 2], kv[2], c2[g]);
-          c3[g] = fmaf_(qs[g][c + 3], kv[3], c3[g]);
-          c0[g] = fmaf_(qs[g][c + 4], kv[4], c0[g]);
-          c1[g] = fmaf_(qs[g][c + 5], kv[5], c1[g]);
-          c2[g] = fmaf_(qs[g][c + 6], kv[6], c2[g]);
-          c3[g] = fmaf_(qs[g][c + 7], kv[7], c3[g]);
-        }
+    for (int b = 0; b < N8; ++b) {
+      const int c = b * 8;
+      const float kv[8] = {u2f(raw[b].x << 16), u2f(raw[b].x & 0xffff0000u),
+                           u2f(raw[b].y << 16), u2f(raw[b].y & 0xffff0000u),
+                           u2f(raw[b].z << 16), u2f(raw[b].z & 0xffff0000u),
+                           u2f(raw[b].w << 16), u2f(raw[b].w & 0xffff0000u)};
+      for (int g = 0; g < G; ++g) {
+        c0[g] = fmaf_(qs[g][c + 0], kv[0], c0[g]);
+        c1[g] = fmaf_(qs[g][c + 1], kv[1], c1[g]);
+        c2[g] = fmaf_(qs[g][c + 2], kv[2], c2[g]);
+        c3[g] = fmaf_(qs[g][c + 3], kv[3], c3[g]);
+        c0[g] = fmaf_(qs[g][c + 4], kv[4], c0[g]);
+        c1[g] = fmaf_(qs[g][c + 5], kv[5], c1[g]);
+        c2[g] = fmaf_(qs[g][c + 6], kv[6], c2[g]);
+        c3[g] = fmaf_(qs[g][c + 7], kv[7], c3[g]);
       }
     }
     for (int g = 0; g < G; ++g) ps[g][t] = ((c0[g] + c1[g]) + (c2[g] + c3[g])) * scale;
   } else {
     for (int g = 0; g < G; ++g) ps[g][t] = u2f(0xff800000u);
   }
+  // the wave's V rows (positions 64 wave .. +63 before the row's end; lane:
+  // DPL dims) are requested now and arrive during the softmax
+  using VT = typename std::conditional<DPL == 4, uint2,
+             typename std::conditional<DPL == 2, uint32_t, uint16_t>::type>::type;
+  const int jend = min(n_pos - j0, kAttnChunk);
+  const int ja = wave * 64, jb = min(jend, ja + 64);
+  const int nv = jb > ja ? jb - ja : 0;  // uniform per wave
+  VT vraw[64];
+  {
+    // positions past the wave's last one reload that one (in bounds, unused)
+    const VT* vr = reinterpret_cast<const VT*>(v_cache + base + size_t(j0) * hd) + lane;
+    const size_t vstride = size_t(hd) / DPL;  // VT elements per position
+    const int last = nv > 0 ? jb - 1 : 0;
+#pragma unroll
+    for (int b = 0; b < 64; ++b) vraw[b] = vr[size_t(min(ja + b, last)) * vstride];
+  }
   __syncthreads();
   // per-head max and sum over the chunk
-  const int wave = t >> 6;
   for (int g = 0; g < G; ++g) {
     float m = ps[g][t];
     for (int o = 32; o > 0; o >>= 1) {
@@ -213,40 +235,36 @@ __global__ __launch_bounds__(kAttnChunk) void decode_kernel(
     ml[0] = mg[g];
     ml[1] = l;
   }
-  if (t < hd) {
-    // values in batches of 32 positions, the next batch requested before the
-    // current one is consumed; per dim one fma chain over j ascending
-    const int jend = min(n_pos - j0, kAttnChunk);
-    float o[G];
-    for (int g = 0; g < G; ++g) o[g] = 0.0f;
-    const uint16_t* vr = v_cache + base + size_t(j0) * hd + t;
-    constexpr int PB = 32;
-    uint16_t cur[PB], nxt[PB];
-    const int full = jend / PB;  // whole batches (uniform over the workgroup)
-    if (full > 0) {
+  {
+    // values: per (head, dim) one fma chain over the wave's positions
+    float o[G][DPL];
+    for (int g = 0; g < G; ++g)
+      for (int i = 0; i < DPL; ++i) o[g][i] = 0.0f;
 #pragma unroll
-      for (int b = 0; b < PB; ++b) cur[b] = vr[size_t(b) * hd];
-    }
-    for (int i = 0; i < full; ++i) {
-      const int jj = i * PB;
-      if (i + 1 < full) {
-#pragma unroll
-        for (int b = 0; b < PB; ++b) nxt[b] = vr[size_t(jj + PB + b) * hd];
+    for (int b = 0; b < 64; ++b) {
+      if (b >= nv) continue;  // uniform per wave
+      float v[DPL];
+      if constexpr (DPL == 4) {
+        v[0] = u2f(vraw[b].x << 16), v[1] = u2f(vraw[b].x & 0xffff0000u);
+        v[2] = u2f(vraw[b].y << 16), v[3] = u2f(vraw[b].y & 0xffff0000u);
+      } else if constexpr (DPL == 2) {
+        v[0] = u2f(vraw[b] << 16), v[1] = u2f(vraw[b] & 0xffff0000u);
+      } else {
+        v[0] = bf16_to_f32(vraw[b]);
       }
+      for (int g = 0; g < G; ++g)
 #pragma unroll
-      for (int b = 0; b < PB; ++b) {
-        const float v = bf16_to_f32(cur[b]);
-        for (int g = 0; g < G; ++g) o[g] = fmaf_(ps[g][jj + b], v, o[g]);
-      }
-#pragma unroll
-      for (int b = 0; b < PB; ++b) cur[b] = nxt[b];
-    }
-    for (int jj = full * PB; jj < jend; ++jj) {
-      const float v = bf16_to_f32(vr[size_t(jj) * hd]);
-      for (int g = 0; g < G; ++g) o[g] = fmaf_(ps[g][jj], v, o[g]);
+        for (int i = 0; i < DPL; ++i) o[g][i] = fmaf_(ps[g][ja + b], v[i], o[g][i]);
     }
     for (int g = 0; g < G; ++g)
-      o_part[((size_t(row) * heads + h0 + g) * max_chunks + chunk) * hd + t] = o[g];
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) ow[wave][g][lane * DPL + i] = o[g][i];
+  }
+  __syncthreads();
+  if (t < hd) {
+    for (int g = 0; g < G; ++g)
+      o_part[((size_t(row) * heads + h0 + g) * max_chunks + chunk) * hd + t] =
+          ((ow[0][g][t] + ow[1][g][t]) + ow[2][g][t]) + ow[3][g][t];
   }
 }
 
@@ -548,13 +566,15 @@ int attn_decode(const uint16_t* q, int rows, const int32_t* slots, const int32_t
   const int splits = grp == 1 ? 1 : grp / 2;
   const int groups = chunks * d.kv_heads * rows;
   const dim3 grid((groups + 7) / 8 * 8 * splits);
-  if (grp == 1)
-    hipLaunchKernelGGL(decode_kernel<1>, grid, dim3(kAttnChunk), 0, s, q, slots, pos, k_cache,
-                       v_cache, d, max_chunks, scale, o_part, ml_part, chunks, rows);
-  else
-    hipLaunchKernelGGL(decode_kernel<2>, grid, dim3(kAttnChunk), 0, s, q, slots, pos, k_cache,
-                       v_cache, d, max_chunks, scale, o_part, ml_part, chunks, rows);
-  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+#define MX_DEC(GG, DD)                                                                          \
+  if ((grp == 1 ? 1 : 2) == GG && d.head_dim == 64 * DD) {                                      \
+    hipLaunchKernelGGL((decode_kernel<GG, DD>), grid, dim3(kAttnChunk), 0, s, q, slots, pos,    \
+                       k_cache, v_cache, d, max_chunks, scale, o_part, ml_part, chunks, rows);  \
+    return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;                                   \
+  }
+  MX_DEC(1, 1) MX_DEC(1, 2) MX_DEC(1, 4) MX_DEC(2, 1) MX_DEC(2, 2) MX_DEC(2, 4)
+#undef MX_DEC
+  return MX_EUNSUPPORTED;  // head_dim other than 64, 128 or 256
 }
 
 int attn_combine(const float* o_part, const float* ml_part, const uint16_t* qkv,
