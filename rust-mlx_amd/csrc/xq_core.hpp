@@ -121,21 +121,35 @@ __device__ __forceinline__ v4i b_operand(const Codes<BITS>& c) {
     r.y = int((c.w[0] >> 4) & 0x0F0F0F0Fu);
     r.z = int(c.w[1] & 0x0F0F0F0Fu);
     r.w = int((c.w[1] >> 4) & 0x0F0F0F0Fu);
-  } else {
+  } else if constexpr (BITS == 8) {
     uint32_t q[4];
-    if constexpr (BITS == 8) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) q[i] = c.w[i] ^ 0x80808080u;
-    } else {
-      q[0] = spread4<BITS>(bits_at<BITS, 0>(c));
-      q[1] = spread4<BITS>(bits_at<BITS, 4 * BITS>(c));
-      q[2] = spread4<BITS>(bits_at<BITS, 8 * BITS>(c));
-      q[3] = spread4<BITS>(bits_at<BITS, 12 * BITS>(c));
-    }
+    for (int i = 0; i < 4; ++i) q[i] = c.w[i] ^ 0x80808080u;
     r.x = even_of(q[0], q[1]);
     r.y = odd_of(q[0], q[1]);
     r.z = even_of(q[2], q[3]);
     r.w = odd_of(q[2], q[3]);
+  } else {
+    // 5 / 6 bits: each code extracted from a 32-bit window holding it whole
+    // (w0 = bits 0..31, then bits 30..61 and 60..91 of the lane's codes) and
+    // shifted into its byte: the same bytes as spreading four codes at a
+    // time and interleaving them, in fewer instructions
+    const uint32_t wa = c.w[0];
+    const uint32_t wb = __builtin_amdgcn_alignbit(c.w[1], c.w[0], 30u);
+    const uint32_t wc = __builtin_amdgcn_alignbit(c.w[2], c.w[1], 28u);
+    auto code = [&](int i) -> uint32_t {
+      const int at = BITS * i;  // compile-time after unrolling
+      const uint32_t src = at + BITS <= 32 ? wa : at + BITS <= 62 ? wb : at + BITS <= 92 ? wc : c.w[2];
+      const int off = at + BITS <= 32 ? at : at + BITS <= 62 ? at - 30 : at + BITS <= 92 ? at - 60 : at - 64;
+      return __builtin_amdgcn_ubfe(src, uint32_t(off), uint32_t(BITS));
+    };
+    auto pack = [&](int a) -> int {  // codes a, a + 2, a + 4, a + 6 as bytes 0..3
+      return int(code(a) | (code(a + 2) << 8) | (code(a + 4) << 16) | (code(a + 6) << 24));
+    };
+    r.x = pack(0);
+    r.y = pack(1);
+    r.z = pack(8);
+    r.w = pack(9);
   }
   return r;
 }
