@@ -1030,11 +1030,13 @@ def summarize_counters(fetch_csv: str, write_csv: str, fetch_scale: float, write
 def main() -> None:
     if len(sys.argv) >= 6 and sys.argv[1] == "--summarize-counters":
         # no device work: summarise two rocprofv3 counter runs of this script
-        summarize_counters(sys.argv[2], sys.argv[3], float(sys.argv[4]), float(sys.argv[5]))
+        summarize_counters(sys.argv[2], sys.argv[3], float(sys.argv[4]), float(sys.argv[5]),
+                           *(sys.argv[6:7]))
         return
     if len(sys.argv) >= 3 and sys.argv[1] == "--summarize-trace":
         # no device work: summarise a rocprofv3 kernel trace of an earlier run
-        summarize_trace(sys.argv[2], sys.argv[3] if len(sys.argv) > 3 else None)
+        summarize_trace(sys.argv[2], sys.argv[3] if len(sys.argv) > 3 else None,
+                        *(sys.argv[4:5]))
         return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
