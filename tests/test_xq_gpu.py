@@ -2,7 +2,8 @@
 CPU oracle's mxo_xq bit for bit: config 0's matrix, the decode step's
 projection shapes (router 513 x 2048, GDN input 12352 x 2048, K = 4096 rows
 staged in 137 KiB of LDS, K = 8192 hyper-connection rows built in registers,
-K = 256 up-projections), every code width, 1..8 activation rows, and
+K = 256 up-projections), every code width at each of those depths, 1..8
+activation rows, and
 activations with exponents spread over many binades (the grid truncation)."""
 import ctypes as C
 
@@ -42,6 +43,19 @@ def _run(mx, orc, n, k, bits, m, seed, spread=False):
     (512, 2048, 8, 7),
     (1000, 2048, 8, 1),    # head width, ragged n
     (64, 448, 4, 6),       # short rows: one slice of 7 groups
+    # every width through the other row-major read forms: 8-bit batches of
+    # four and eight (K = 1024, K = 2048 with n > 2048), and 5 / 6 / 8-bit at
+    # K = 4096 (LDS staging) and K = 8192 (register and block operands)
+    (4096, 2048, 8, 8),
+    (640, 1024, 8, 4),
+    (2048, 4096, 6, 3),
+    (2048, 4096, 5, 8),
+    (2048, 4096, 8, 2),
+    (260, 8192, 5, 5),
+    (260, 8192, 6, 8),
+    (260, 8192, 8, 2),
+    (8192, 256, 5, 8),
+    (8192, 256, 6, 3),
 ])
 def test_xq_bit_exact_with_oracle(mx, orc, n, k, bits, m):
     got, want = _run(mx, orc, n, k, bits, m, seed=n + k + bits + m)
