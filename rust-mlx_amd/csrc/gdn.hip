@@ -141,6 +141,45 @@ __global__ __launch_bounds__(kExactThreads) void recurrence_kernel(ScanArgs p) {
   __shared__ float qs[kD], ks[kD], ys[kD], red[1];
   __shared__ __align__(16) uint16_t yb[kD];  // the head's y row (plane only)
 
+  // one token's inputs as raw bits: q, k (two values each, wave 0), v of
+  // column i, beta / g (or b, a) and z; requested ahead of their use, the
+  // first token's before the state, so the q / k norms run while the state
+  // streams in
+  struct In {
+    uint16_t q0, q1, k0, k1, v, b, a, z;
+    float g;
+  };
+  auto load_in = [&](size_t row) {
+    In r{};
+    if constexpr (FUSED) {
+      const uint16_t* cr = p.conv_out + row * p.conv_stride;
+      if (wave == 0) {
+        r.q0 = cr[hk * kD + lane];
+        r.q1 = cr[hk * kD + 64 + lane];
+        r.k0 = cr[(hk_heads + hk) * kD + lane];
+        r.k1 = cr[(hk_heads + hk) * kD + 64 + lane];
+      }
+      r.v = cr[2 * hk_heads * kD + hv * kD + i];
+      r.b = p.b[row * p.zab_stride + hv];
+      r.a = p.a[row * p.zab_stride + hv];
+      r.z = p.z[row * p.zab_stride + hv * kD + i];
+    } else {
+      if (wave == 0) {
+        const uint16_t* qr = p.q + (row * hk_heads + hk) * kD;
+        const uint16_t* kr = p.k + (row * hk_heads + hk) * kD;
+        r.q0 = qr[lane];
+        r.q1 = qr[64 + lane];
+        r.k0 = kr[lane];
+        r.k1 = kr[64 + lane];
+      }
+      r.v = p.v[(row * hv_heads + hv) * kD + i];
+      r.b = p.beta[row * hv_heads + hv];
+      r.g = p.g[row * hv_heads + hv];
+    }
+    return r;
+  };
+  In in = load_in(size_t(g) * p.t);
+
   const size_t my_off = size_t(part) * kD + i;
   float* sp = p.state + (size_t(p.slots[g]) * hv_heads + hv) * kD * kD + my_off;
   float s[kExactRows];  // s[m]: key row 4 m + part of column i
@@ -158,17 +197,18 @@ __global__ __launch_bounds__(kExactThreads) void recurrence_kernel(ScanArgs p) {
 
   for (int step = 0; step < p.t; ++step) {
     const size_t row = size_t(g) * p.t + step;
+    const In cur = in;
+    if (step + 1 < p.t) in = load_in(row + 1);
     float vi, beta, gdecay;
     // LDS of the previous token (qs, ks, ys, red, yb) is read by every wave
     // before this barrier
     __syncthreads();
     if constexpr (FUSED) {
-      const uint16_t* cr = p.conv_out + row * p.conv_stride;
       if (wave == 0) {
-        const float q0 = bf16_to_f32(cr[hk * kD + lane]);
-        const float q1 = bf16_to_f32(cr[hk * kD + 64 + lane]);
-        const float k0 = bf16_to_f32(cr[(hk_heads + hk) * kD + lane]);
-        const float k1 = bf16_to_f32(cr[(hk_heads + hk) * kD + 64 + lane]);
+        const float q0 = bf16_to_f32(cur.q0);
+        const float q1 = bf16_to_f32(cur.q1);
+        const float k0 = bf16_to_f32(cur.k0);
+        const float k1 = bf16_to_f32(cur.k1);
         // x * rsqrt(sum(x^2) + eps) with bf16 operations (hybrid.rs:409-413)
         const float qss = round_bf16(xor_butterfly64(round_bf16(q0 * q0)) +
                                      xor_butterfly64(round_bf16(q1 * q1)));
@@ -181,22 +221,20 @@ __global__ __launch_bounds__(kExactThreads) void recurrence_kernel(ScanArgs p) {
         ks[lane] = round_bf16(k0 * rk);
         ks[64 + lane] = round_bf16(k1 * rk);
       }
-      vi = bf16_to_f32(cr[2 * hk_heads * kD + hv * kD + i]);
-      beta = sigmoid_bf16(bf16_to_f32(p.b[row * p.zab_stride + hv]));
-      const float x = round_bf16(bf16_to_f32(p.a[row * p.zab_stride + hv]) + dt);
+      vi = bf16_to_f32(cur.v);
+      beta = sigmoid_bf16(bf16_to_f32(cur.b));
+      const float x = round_bf16(bf16_to_f32(cur.a) + dt);
       gdecay = expf_(neg_a * softplus_bf16(x));
     } else {
       if (wave == 0) {
-        const uint16_t* qr = p.q + (row * hk_heads + hk) * kD;
-        const uint16_t* kr = p.k + (row * hk_heads + hk) * kD;
-        qs[lane] = bf16_to_f32(qr[lane]);
-        qs[64 + lane] = bf16_to_f32(qr[64 + lane]);
-        ks[lane] = bf16_to_f32(kr[lane]);
-        ks[64 + lane] = bf16_to_f32(kr[64 + lane]);
+        qs[lane] = bf16_to_f32(cur.q0);
+        qs[64 + lane] = bf16_to_f32(cur.q1);
+        ks[lane] = bf16_to_f32(cur.k0);
+        ks[64 + lane] = bf16_to_f32(cur.k1);
       }
-      vi = bf16_to_f32(p.v[(row * hv_heads + hv) * kD + i]);
-      beta = bf16_to_f32(p.beta[row * hv_heads + hv]);
-      gdecay = p.g[row * hv_heads + hv];
+      vi = bf16_to_f32(cur.v);
+      beta = bf16_to_f32(cur.b);
+      gdecay = cur.g;
     }
     __syncthreads();
 
@@ -237,7 +275,7 @@ __global__ __launch_bounds__(kExactThreads) void recurrence_kernel(ScanArgs p) {
       __syncthreads();
       const float inv = 1.0f / __builtin_sqrtf(red[0] / float(kD) + p.eps);
       const float normed = round_bf16(nw * round_bf16(yo * inv));
-      const float zi = bf16_to_f32(p.z[row * p.zab_stride + hv * kD + i]);
+      const float zi = bf16_to_f32(cur.z);
       const uint16_t yv = f32_to_bf16(normed * sigmoidf_(zi));
       if (part == 0) *yp = yv;
       if (p.plane) {
