@@ -57,8 +57,10 @@ def test_prefill_logits(fixture):
 
 
 def greedy(w, n):
+    with open(os.path.join(HERE, "oracle.json")) as f:
+        prompt = json.load(f)["prompt"]
     m = hy.HybridModel(w)
-    tail = m.forward(FIXTURE_PROMPT)[0][-1]
+    tail = m.forward(prompt)[0][-1]
     got = []
     for _ in range(n):
         got.append(int(np.argmax(tail)))
@@ -66,8 +68,6 @@ def greedy(w, n):
             tail = m.forward([got[-1]])[0][-1]
     return got
 
-
-FIXTURE_PROMPT = json.load(open(os.path.join(HERE, "oracle.json")))["prompt"]
 
 
 def test_greedy_tokens_through_the_sparse_indexer_regime(fixture):
