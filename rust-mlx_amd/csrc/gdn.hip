@@ -129,8 +129,19 @@ __device__ __forceinline__ float xor_butterfly64(float v) {
   return v;
 }
 
-template <bool FUSED>
+// Tokens are taken in chunks of up to CH (1 for a decode step, kExactChunk
+// for verify and prefill blocks).  Before a chunk's
+// recurrence, wave w normalises token w's q and k into LDS and every thread
+// holds its column's v, z and the token's gates in registers, so the
+// recurrence itself runs the chunk's tokens with no barrier; the gated norm
+// and the output plane of the chunk's tokens follow it, one wave per token.
+// Every value is computed as in the one-token-at-a-time order (the same
+// butterflies, chains and roundings), only the schedule differs.
+constexpr int kExactChunk = 8;
+
+template <bool FUSED, int CH>
 __global__ __launch_bounds__(kExactThreads) void recurrence_kernel(ScanArgs p) {
+  static_assert(kExactThreads / 64 >= CH, "a wave per token of a chunk");
   const int hv = blockIdx.x;
   const int g = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -138,47 +149,60 @@ __global__ __launch_bounds__(kExactThreads) void recurrence_kernel(ScanArgs p) {
   const int i = wave * 16 + c;  // value column
   const int hv_heads = p.hv_heads, hk_heads = p.hk_heads;
   const int hk = hv / (hv_heads / hk_heads);
-  __shared__ float qs[kD], ks[kD], ys[kD], red[1];
-  __shared__ __align__(16) uint16_t yb[kD];  // the head's y row (plane only)
+  __shared__ float qs[CH][kD], ks[CH][kD], ys[CH][kD];
+  __shared__ float red[CH];
+  __shared__ __align__(16) uint16_t yb[CH][kD];  // y rows (plane only)
 
-  // one token's inputs as raw bits: q, k (two values each, wave 0), v of
-  // column i, beta / g (or b, a) and z; requested ahead of their use, the
-  // first token's before the state, so the q / k norms run while the state
-  // streams in
+  // a token's per-column inputs as raw bits: v of column i, b / a (or beta,
+  // g) and z
   struct In {
-    uint16_t q0, q1, k0, k1, v, b, a, z;
+    uint16_t v, b, a, z;
     float g;
   };
   auto load_in = [&](size_t row) {
     In r{};
     if constexpr (FUSED) {
       const uint16_t* cr = p.conv_out + row * p.conv_stride;
-      if (wave == 0) {
-        r.q0 = cr[hk * kD + lane];
-        r.q1 = cr[hk * kD + 64 + lane];
-        r.k0 = cr[(hk_heads + hk) * kD + lane];
-        r.k1 = cr[(hk_heads + hk) * kD + 64 + lane];
-      }
       r.v = cr[2 * hk_heads * kD + hv * kD + i];
       r.b = p.b[row * p.zab_stride + hv];
       r.a = p.a[row * p.zab_stride + hv];
       r.z = p.z[row * p.zab_stride + hv * kD + i];
     } else {
-      if (wave == 0) {
-        const uint16_t* qr = p.q + (row * hk_heads + hk) * kD;
-        const uint16_t* kr = p.k + (row * hk_heads + hk) * kD;
-        r.q0 = qr[lane];
-        r.q1 = qr[64 + lane];
-        r.k0 = kr[lane];
-        r.k1 = kr[64 + lane];
-      }
       r.v = p.v[(row * hv_heads + hv) * kD + i];
       r.b = p.beta[row * hv_heads + hv];
       r.g = p.g[row * hv_heads + hv];
     }
     return r;
   };
-  In in = load_in(size_t(g) * p.t);
+  // wave w's raw q / k of chunk token w: lanes hold values lane, 64 + lane
+  auto load_qk = [&](size_t row, uint16_t (&qk)[4]) {
+    if constexpr (FUSED) {
+      const uint16_t* cr = p.conv_out + row * p.conv_stride;
+      qk[0] = cr[hk * kD + lane];
+      qk[1] = cr[hk * kD + 64 + lane];
+      qk[2] = cr[(hk_heads + hk) * kD + lane];
+      qk[3] = cr[(hk_heads + hk) * kD + 64 + lane];
+    } else {
+      const uint16_t* qr = p.q + (row * hk_heads + hk) * kD;
+      const uint16_t* kr = p.k + (row * hk_heads + hk) * kD;
+      qk[0] = qr[lane];
+      qk[1] = qr[64 + lane];
+      qk[2] = kr[lane];
+      qk[3] = kr[64 + lane];
+    }
+  };
+  const size_t row0 = size_t(g) * p.t;
+  // the first chunk's inputs are requested before the state, so the q / k
+  // norms run while the state streams in
+  In in[CH];
+  uint16_t qk[4] = {0, 0, 0, 0};
+  {
+    const int n0 = p.t < CH ? p.t : CH;
+    if (wave < n0) load_qk(row0 + wave, qk);
+#pragma unroll
+    for (int k = 0; k < CH; ++k)
+      if (k < n0) in[k] = load_in(row0 + k);
+  }
 
   const size_t my_off = size_t(part) * kD + i;
   float* sp = p.state + (size_t(p.slots[g]) * hv_heads + hv) * kD * kD + my_off;
@@ -195,20 +219,21 @@ __global__ __launch_bounds__(kExactThreads) void recurrence_kernel(ScanArgs p) {
     nw = bf16_to_f32(p.norm_w[i]);
   }
 
-  for (int step = 0; step < p.t; ++step) {
-    const size_t row = size_t(g) * p.t + step;
-    const In cur = in;
-    if (step + 1 < p.t) in = load_in(row + 1);
-    float vi, beta, gdecay;
-    // LDS of the previous token (qs, ks, ys, red, yb) is read by every wave
+  for (int c0 = 0; c0 < p.t; c0 += CH) {
+    const int n = p.t - c0 < CH ? p.t - c0 : CH;
+    // LDS of the previous chunk (qs, ks, ys, red, yb) is read by every wave
     // before this barrier
-    __syncthreads();
-    if constexpr (FUSED) {
-      if (wave == 0) {
-        const float q0 = bf16_to_f32(cur.q0);
-        const float q1 = bf16_to_f32(cur.q1);
-        const float k0 = bf16_to_f32(cur.k0);
-        const float k1 = bf16_to_f32(cur.k1);
+    if (c0 > 0) {
+      __syncthreads();
+      if (wave < n) load_qk(row0 + c0 + wave, qk);
+#pragma unroll
+      for (int k = 0; k < CH; ++k)
+        if (k < n) in[k] = load_in(row0 + c0 + k);
+    }
+    if (wave < n) {
+      const float q0 = bf16_to_f32(qk[0]), q1 = bf16_to_f32(qk[1]);
+      const float k0 = bf16_to_f32(qk[2]), k1 = bf16_to_f32(qk[3]);
+      if constexpr (FUSED) {
         // x * rsqrt(sum(x^2) + eps) with bf16 operations (hybrid.rs:409-413)
         const float qss = round_bf16(xor_butterfly64(round_bf16(q0 * q0)) +
                                      xor_butterfly64(round_bf16(q1 * q1)));
@@ -216,86 +241,104 @@ __global__ __launch_bounds__(kExactThreads) void recurrence_kernel(ScanArgs p) {
                                      xor_butterfly64(round_bf16(k1 * k1)));
         const float rq = round_bf16(1.0f / __builtin_sqrtf(round_bf16(qss + eps_l2)));
         const float rk = round_bf16(1.0f / __builtin_sqrtf(round_bf16(kss + eps_l2)));
-        qs[lane] = round_bf16(round_bf16(q0 * rq) * qscale);
-        qs[64 + lane] = round_bf16(round_bf16(q1 * rq) * qscale);
-        ks[lane] = round_bf16(k0 * rk);
-        ks[64 + lane] = round_bf16(k1 * rk);
+        qs[wave][lane] = round_bf16(round_bf16(q0 * rq) * qscale);
+        qs[wave][64 + lane] = round_bf16(round_bf16(q1 * rq) * qscale);
+        ks[wave][lane] = round_bf16(k0 * rk);
+        ks[wave][64 + lane] = round_bf16(k1 * rk);
+      } else {
+        qs[wave][lane] = q0;
+        qs[wave][64 + lane] = q1;
+        ks[wave][lane] = k0;
+        ks[wave][64 + lane] = k1;
       }
-      vi = bf16_to_f32(cur.v);
-      beta = sigmoid_bf16(bf16_to_f32(cur.b));
-      const float x = round_bf16(bf16_to_f32(cur.a) + dt);
-      gdecay = expf_(neg_a * softplus_bf16(x));
-    } else {
-      if (wave == 0) {
-        qs[lane] = bf16_to_f32(cur.q0);
-        qs[64 + lane] = bf16_to_f32(cur.q1);
-        ks[lane] = bf16_to_f32(cur.k0);
-        ks[64 + lane] = bf16_to_f32(cur.k1);
-      }
-      vi = bf16_to_f32(cur.v);
-      beta = bf16_to_f32(cur.b);
-      gdecay = cur.g;
     }
     __syncthreads();
 
-    // state *= g; chain `part` of kv = sum_d s[d] k[d]
-    float cp = 0.0f;
+    float yo[CH];
 #pragma unroll
-    for (int m = 0; m < kExactRows; ++m) {
-      s[m] = s[m] * gdecay;
-      cp = fmaf_(s[m], ks[kExactParts * m + part], cp);
-    }
-    float kv = cp + __shfl_xor(cp, 16, 64);  // c0 + c1 (parts 0, 1), c2 + c3 (parts 2, 3)
-    kv = kv + __shfl_xor(kv, 32, 64);        // (c0 + c1) + (c2 + c3)
-    const float delta = (vi - kv) * beta;
-    float op = 0.0f;
+    for (int k = 0; k < CH; ++k) {
+      yo[k] = 0.0f;
+      if (k >= n) continue;  // uniform
+      const size_t row = row0 + c0 + k;
+      float vi, beta, gdecay;
+      if constexpr (FUSED) {
+        vi = bf16_to_f32(in[k].v);
+        beta = sigmoid_bf16(bf16_to_f32(in[k].b));
+        const float x = round_bf16(bf16_to_f32(in[k].a) + dt);
+        gdecay = expf_(neg_a * softplus_bf16(x));
+      } else {
+        vi = bf16_to_f32(in[k].v);
+        beta = bf16_to_f32(in[k].b);
+        gdecay = in[k].g;
+      }
+      // state *= g; chain `part` of kv = sum_d s[d] k[d]
+      float cp = 0.0f;
 #pragma unroll
-    for (int m = 0; m < kExactRows; ++m) {
-      s[m] = fmaf_(ks[kExactParts * m + part], delta, s[m]);
-      op = fmaf_(s[m], qs[kExactParts * m + part], op);
-    }
-    float os = op + __shfl_xor(op, 16, 64);
-    os = os + __shfl_xor(os, 32, 64);
-    const float yo = round_bf16(os);
-    if (p.history) {
-      float* hp = p.history + ((row * hv_heads + hv) * kD) * kD + my_off;
+      for (int m = 0; m < kExactRows; ++m) {
+        s[m] = s[m] * gdecay;
+        cp = fmaf_(s[m], ks[k][kExactParts * m + part], cp);
+      }
+      float kv = cp + __shfl_xor(cp, 16, 64);  // c0 + c1 (parts 0, 1), c2 + c3 (parts 2, 3)
+      kv = kv + __shfl_xor(kv, 32, 64);        // (c0 + c1) + (c2 + c3)
+      const float delta = (vi - kv) * beta;
+      float op = 0.0f;
 #pragma unroll
-      for (int m = 0; m < kExactRows; ++m) hp[size_t(m) * kExactParts * kD] = s[m];
+      for (int m = 0; m < kExactRows; ++m) {
+        s[m] = fmaf_(ks[k][kExactParts * m + part], delta, s[m]);
+        op = fmaf_(s[m], qs[k][kExactParts * m + part], op);
+      }
+      float os = op + __shfl_xor(op, 16, 64);
+      os = os + __shfl_xor(os, 32, 64);
+      yo[k] = round_bf16(os);
+      if (p.history) {
+        float* hp = p.history + ((row * hv_heads + hv) * kD) * kD + my_off;
+#pragma unroll
+        for (int m = 0; m < kExactRows; ++m) hp[size_t(m) * kExactParts * kD] = s[m];
+      }
+      if constexpr (FUSED) {
+        if (part == 0) ys[k][i] = yo[k];
+      } else {
+        if (part == 0) p.y[row * (size_t(hv_heads) * kD) + hv * kD + i] = f32_to_bf16(yo[k]);
+      }
     }
-    uint16_t* yp = p.y + row * (size_t(hv_heads) * kD) + hv * kD + i;
     if constexpr (FUSED) {
-      // fast::rms_norm(y, w, eps) then * sigmoid(z) in f32 (hybrid.rs:447-452)
-      if (part == 0) ys[i] = yo;
+      // fast::rms_norm(y, w, eps) then * sigmoid(z) in f32 (hybrid.rs:447-452):
+      // wave w sums token w's squares, then every column normalises
       __syncthreads();
-      if (wave == 0) {
-        const float y0 = ys[lane], y1 = ys[64 + lane];
+      if (wave < n) {
+        const float y0 = ys[wave][lane], y1 = ys[wave][64 + lane];
         const float ss = xor_butterfly64(y0 * y0) + xor_butterfly64(y1 * y1);
-        if (lane == 0) red[0] = ss;
+        if (lane == 0) red[wave] = ss;
       }
       __syncthreads();
-      const float inv = 1.0f / __builtin_sqrtf(red[0] / float(kD) + p.eps);
-      const float normed = round_bf16(nw * round_bf16(yo * inv));
-      const float zi = bf16_to_f32(cur.z);
-      const uint16_t yv = f32_to_bf16(normed * sigmoidf_(zi));
-      if (part == 0) *yp = yv;
+#pragma unroll
+      for (int k = 0; k < CH; ++k) {
+        if (k >= n) continue;
+        const size_t row = row0 + c0 + k;
+        const float inv = 1.0f / __builtin_sqrtf(red[k] / float(kD) + p.eps);
+        const float normed = round_bf16(nw * round_bf16(yo[k] * inv));
+        const float zi = bf16_to_f32(in[k].z);
+        const uint16_t yv = f32_to_bf16(normed * sigmoidf_(zi));
+        if (part == 0) {
+          p.y[row * (size_t(hv_heads) * kD) + hv * kD + i] = yv;
+          yb[k][i] = yv;
+        }
+      }
       if (p.plane) {
-        // the head's two 64-value groups of this row, digitised by wave 0
-        // (lanes 16 kb + gl, gl < 2), for the output projection
-        if (part == 0) yb[i] = yv;
+        // each token's two 64-value groups of this head, digitised by wave
+        // `token` (lanes 16 kb + gl, gl < 2), for the output projection
         __syncthreads();
-        if (wave == 0) {
+        if (wave < n) {
           const int kb = lane >> 4, gl = lane & 15;
           float f[16];
           const bool unit = gl < kD / xq::kGroup;
 #pragma unroll
           for (int q = 0; q < 16; ++q)
-            f[q] = unit ? bf16_to_f32(yb[gl * xq::kGroup + 16 * kb + q]) : 0.0f;
-          xq::digitize_unit(f, int(row), hv * (kD / xq::kGroup) + (unit ? gl : 0), kb, unit,
-                            p.plane, hv_heads * (kD / xq::kGroup));
+            f[q] = unit ? bf16_to_f32(yb[wave][gl * xq::kGroup + 16 * kb + q]) : 0.0f;
+          xq::digitize_unit(f, int(row0 + c0 + wave), hv * (kD / xq::kGroup) + (unit ? gl : 0), kb,
+                            unit, p.plane, hv_heads * (kD / xq::kGroup));
         }
       }
-    } else {
-      if (part == 0) *yp = f32_to_bf16(yo);
     }
   }
 #pragma unroll
@@ -548,7 +591,12 @@ int gdn_recurrence(const uint16_t* conv_out, int64_t conv_stride, const uint16_t
   p.hk_heads = d.hk; p.hv_heads = d.hv; p.t = t; p.slots = slots; p.state = state;
   p.history = history; p.y = y;
   p.plane = groups * t <= 8 ? plane : nullptr;
-  hipLaunchKernelGGL(recurrence_kernel<true>, dim3(d.hv, groups), dim3(kExactThreads), 0, s, p);
+  if (t == 1)
+    hipLaunchKernelGGL((recurrence_kernel<true, 1>), dim3(d.hv, groups), dim3(kExactThreads), 0,
+                       s, p);
+  else
+    hipLaunchKernelGGL((recurrence_kernel<true, kExactChunk>), dim3(d.hv, groups),
+                       dim3(kExactThreads), 0, s, p);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 
@@ -560,7 +608,12 @@ int gdn_scan(const uint16_t* q, const uint16_t* k, const uint16_t* v, const floa
   p.q = q; p.k = k; p.v = v; p.g = g; p.beta = beta;
   p.hk_heads = d.hk; p.hv_heads = d.hv; p.t = t; p.slots = slots; p.state = state;
   p.history = history; p.y = y;
-  hipLaunchKernelGGL(recurrence_kernel<false>, dim3(d.hv, groups), dim3(kExactThreads), 0, s, p);
+  if (t == 1)
+    hipLaunchKernelGGL((recurrence_kernel<false, 1>), dim3(d.hv, groups), dim3(kExactThreads), 0,
+                       s, p);
+  else
+    hipLaunchKernelGGL((recurrence_kernel<false, kExactChunk>), dim3(d.hv, groups),
+                       dim3(kExactThreads), 0, s, p);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 
