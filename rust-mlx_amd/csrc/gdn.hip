@@ -50,28 +50,51 @@ __global__ __launch_bounds__(256) void conv_kernel(const uint16_t* __restrict__ 
   const int g = blockIdx.y;
   if (c >= channels) return;
   uint16_t* st = conv_state + size_t(slots[g]) * (taps - 1) * channels + c;
+  // fixed-size arrays indexed by unrolled loops (taps <= kMaxTaps, checked
+  // on the host), so they stay in registers
   constexpr int kMaxTaps = 8;
+  constexpr int kBlock = 8;  // tokens whose inputs are requested together
   float win[kMaxTaps];
   float wj[kMaxTaps];
-  for (int j = 0; j < taps - 1; ++j) win[j] = bf16_to_f32(st[size_t(j) * channels]);
-  for (int j = 0; j < taps; ++j) wj[j] = w[size_t(j) * channels + c];
+#pragma unroll
+  for (int j = 0; j < kMaxTaps; ++j) {
+    win[j] = j < taps - 1 ? bf16_to_f32(st[size_t(j) * channels]) : 0.0f;
+    wj[j] = j < taps ? w[size_t(j) * channels + c] : 0.0f;
+  }
   uint16_t* hist = window_history
                        ? window_history + size_t(g) * (taps - 1 + t) * channels + c
                        : nullptr;
   if (hist)
     for (int j = 0; j < taps - 1; ++j) hist[size_t(j) * channels] = f32_to_bf16(win[j]);
-  for (int i = 0; i < t; ++i) {
-    const size_t row = size_t(g) * t + i;
-    const uint16_t xr = qkv[row * row_stride + c];
-    win[taps - 1] = bf16_to_f32(xr);
-    if (hist) hist[size_t(taps - 1 + i) * channels] = xr;
-    float acc = 0.0f;
-    for (int j = 0; j < taps; ++j) acc = acc + win[j] * wj[j];
-    const float v = round_bf16(acc);
-    out[row * out_stride + c] = f32_to_bf16(v * sigmoid_bf16(v));
-    for (int j = 0; j < taps - 1; ++j) win[j] = win[j + 1];
+  for (int i0 = 0; i0 < t; i0 += kBlock) {
+    const int n = t - i0 < kBlock ? t - i0 : kBlock;
+    uint16_t xs[kBlock];
+#pragma unroll
+    for (int i = 0; i < kBlock; ++i)
+      xs[i] = i < n ? qkv[(size_t(g) * t + i0 + i) * row_stride + c] : uint16_t(0);
+#pragma unroll
+    for (int i = 0; i < kBlock; ++i) {
+      if (i >= n) continue;  // uniform
+      const size_t row = size_t(g) * t + i0 + i;
+      // the new input sits at tap taps - 1
+#pragma unroll
+      for (int j = 0; j < kMaxTaps; ++j)
+        if (j == taps - 1) win[j] = bf16_to_f32(xs[i]);
+      if (hist) hist[size_t(taps - 1 + i0 + i) * channels] = xs[i];
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < kMaxTaps; ++j)
+        if (j < taps) acc = acc + win[j] * wj[j];
+      const float v = round_bf16(acc);
+      out[row * out_stride + c] = f32_to_bf16(v * sigmoid_bf16(v));
+#pragma unroll
+      for (int j = 0; j < kMaxTaps - 1; ++j)
+        if (j < taps - 1) win[j] = win[j + 1];
+    }
   }
-  for (int j = 0; j < taps - 1; ++j) st[size_t(j) * channels] = f32_to_bf16(win[j]);
+#pragma unroll
+  for (int j = 0; j < kMaxTaps; ++j)
+    if (j < taps - 1) st[size_t(j) * channels] = f32_to_bf16(win[j]);
 }
 
 constexpr int kD = 128;  // head dim handled by the recurrence kernel (Dk == Dv == 128)
