@@ -7,8 +7,9 @@ Workloads:
       model (48 layers, 3:1 GatedDeltaNet : gated attention, 512-expert top-10
       MoE with a shared expert, hc = 4 hyper-connections, vocab 151936, 4-bit
       weights with 5-bit expert down and 8-bit embedding/head), 8 slots
-      prefilled with seeded uniform-random prompts of ragged lengths 10..2048,
-      then batched greedy decode of all 8 rows per step (rows at their own
+      prefilled with seeded uniform-random prompts of ragged lengths 10..2048
+      (128-token chunks on the matrix cores; --block-prefill: the exact
+      eight-token blocks), then batched greedy decode of all 8 rows per step (rows at their own
       offsets).  A step = one decode token for each of the 8 rows; W + K = 256
       steps per row by default.  value = aggregate tok/s over the K timed steps.
   qmv-config0  BASELINE config 0: one affine 4-bit g64 QMV [4096, 2048] per
@@ -119,10 +120,13 @@ def bench_config3(mx, args):
             eng.fill_slot(s, int(lengths[s]), seed=4000 + s)
             nxt[s] = prompt[-1]
         else:
-            nxt[s] = eng.prefill(s, prompt)
+            nxt[s] = eng.prefill(s, prompt, chunked=not args.block_prefill)
     prefill_s = time.perf_counter() - t0
+    prefill_mode = ("synthetic" if args.synthetic_context else
+                    "exact 8-token blocks" if args.block_prefill else "128-token chunks")
     log(f"config3: {'filled' if args.synthetic_context else 'prefilled'} {int(lengths.sum())} "
-        f"context positions (lengths {[int(x) for x in lengths]}) in {prefill_s:.1f}s")
+        f"context positions (lengths {[int(x) for x in lengths]}) in {prefill_s:.2f}s "
+        f"({prefill_mode}, {lengths.sum() / prefill_s:.0f} positions/s)")
     slots = list(range(rows))
     toks = nxt
     # one profiled (eager, instrumented) step: expert-kernel timing and bytes
@@ -222,7 +226,9 @@ def bench_config3(mx, args):
             "distinct_experts_per_layer": round(prof2["distinct_experts"] / layers, 2),
             "expert_down_gbs": round(dn_gbs, 1),
             "prefill_s": round(prefill_s, 2),
+            "prefill_positions": int(lengths.sum()),
             "context": "synthetic" if args.synthetic_context else "prefilled",
+            "prefill": prefill_mode,
             "mode": "exact" if exact else "fast",
             ("fast_tok_s" if exact else "exact_tok_s"): round(other_tok_s, 2),
             "reference_policy_tok_s": round(ref_tok_s, 2),
@@ -1051,6 +1057,10 @@ def main() -> None:
                     help="give the rows random caches of the prompt lengths instead of "
                          "prefilling them (profiling runs: the decode step's cost depends on "
                          "the context length only)")
+    ap.add_argument("--block-prefill", action="store_true",
+                    help="config3: prefill the contexts in exact eight-token blocks "
+                         "(mx_engine_prefill) instead of 128-token matrix-core chunks "
+                         "(mx_engine_prefill_chunked)")
     ap.add_argument("--fast", action="store_true",
                     help="config3: time the bf16 matrix-core kernels (within tolerance of the "
                          "oracle, not bit-exact) as the headline path, and the exact path "

@@ -199,6 +199,7 @@ def _load() -> C.CDLL:
         "mx_engine_decode_batch_outputs": ([vp, vp, vp, i32, vp, vp, vp], i32),
         "mx_engine_decode_forced": ([vp, vp, vp, i32, vp, vp, vp, vp], i32),
         "mx_engine_prefill": ([vp, i32, vp, i32, vp], i32),
+        "mx_engine_prefill_chunked": ([vp, i32, vp, i32, vp], i32),
         "mx_engine_verify": ([vp, i32, vp, i32, vp], i32),
         "mx_engine_commit": ([vp, i32, i32], i32),
         "mx_engine_generate": ([vp, i32, vp, i32, i32, i32, vp, vp, C.POINTER(GenerateStatsC), vp],
@@ -611,10 +612,14 @@ class Engine:
                                           out.ctypes.data))
         return out, h_out, ids
 
-    def prefill(self, slot, tokens) -> int:
+    def prefill(self, slot, tokens, chunked=False) -> int:
+        """Feeds tokens to a slot; returns the greedy token after the last one.
+        chunked: mx_engine_prefill_chunked (128-token chunks on the matrix
+        cores, within tolerance of the exact 8-token blocks)."""
         t = self._u32(tokens)
         out = np.empty(1, np.uint32)
-        check(lib.mx_engine_prefill(self.h, slot, t.ctypes.data, len(t), out.ctypes.data))
+        fn = lib.mx_engine_prefill_chunked if chunked else lib.mx_engine_prefill
+        check(fn(self.h, slot, t.ctypes.data, len(t), out.ctypes.data))
         return int(out[0])
 
     def verify(self, slot, tokens) -> np.ndarray:

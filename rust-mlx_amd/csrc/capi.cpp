@@ -682,6 +682,18 @@ MX_ABI mx_status mx_engine_prefill(mx_engine* e, int32_t slot, const uint32_t* t
   return MX_OK;
 }
 
+MX_ABI mx_status mx_engine_prefill_chunked(mx_engine* e, int32_t slot, const uint32_t* tokens,
+                                           int32_t count, uint32_t* next) {
+  MX_CHECK(e && tokens && next, MX_EINVAL, "mx_engine_prefill_chunked: null pointer");
+  MX_CHECK(slot_ok(*e->impl, slot), MX_EINVAL, "mx_engine_prefill_chunked: slot out of range");
+  MX_CHECK(count >= 1, MX_EINVAL, "mx_engine_prefill_chunked: empty input");
+  MX_CHECK(tokens_ok(*e->impl, tokens, count), MX_EINVAL,
+           "mx_engine_prefill_chunked: token outside vocabulary");
+  std::string err;
+  return engine_status(engine_prefill_chunked(*e->impl, slot, tokens, count, next, &err), err,
+                       "mx_engine_prefill_chunked");
+}
+
 MX_ABI mx_status mx_engine_verify(mx_engine* e, int32_t slot, const uint32_t* tokens,
                                   int32_t count, uint32_t* argmax) {
   MX_CHECK(e && tokens && argmax, MX_EINVAL, "mx_engine_verify: null pointer");
@@ -859,7 +871,7 @@ MX_ABI mx_status mx_qmm(const mx_qweight* w, const uint16_t* x, int32_t m, uint1
   const QWeight q = to_qweight(*w);
   if (const char* err = check_qweight(q)) return mx_status(set_error(MX_EINVAL, std::string("mx_qmm: ") + err));
   MX_CHECK(qmm_supported(q), MX_EUNSUPPORTED, "mx_qmm: needs group_size 64 and k <= 8192");
-  MX_CHECK(m >= 1 && m <= 16, MX_EUNSUPPORTED, "mx_qmm: m must be in 1..16");
+  MX_CHECK(m >= 1 && m <= kQmmMaxRows, MX_EUNSUPPORTED, "mx_qmm: m must be in 1..128");
   ProjEpilogue e{};
   e.mode = kPlain;
   e.y = y;
@@ -949,7 +961,8 @@ MX_ABI mx_status mx_moe_experts_mfma(const uint16_t* x, const uint32_t* ids, con
   MX_CHECK(x && ids && scores && gate && up && down && shared_gate && shared_up && shared_down &&
                workspace && partial,
            MX_EINVAL, "mx_moe_experts_mfma: null pointer");
-  MX_CHECK(rows >= 1 && rows <= 8, MX_EUNSUPPORTED, "mx_moe_experts_mfma: rows must be in 1..8");
+  MX_CHECK(rows >= 1 && rows <= kPrefillChunk, MX_EUNSUPPORTED,
+           "mx_moe_experts_mfma: rows must be in 1..128");
   MX_CHECK(top_k >= 1 && top_k <= 16, MX_EUNSUPPORTED, "mx_moe_experts_mfma: top_k must be in 1..16");
   const QBank g = to_qbank(*gate), u = to_qbank(*up), d = to_qbank(*down);
   const QWeight sg = to_qweight(*shared_gate), su = to_qweight(*shared_up), sd = to_qweight(*shared_down);
@@ -967,8 +980,19 @@ MX_ABI mx_status mx_moe_experts_mfma(const uint16_t* x, const uint32_t* ids, con
   const int inter = g.n > sg.n ? g.n : sg.n;
   uint16_t* h = static_cast<uint16_t*>(workspace);
   const size_t hb = size_t(rows) * (top_k + 1) * inter * sizeof(uint16_t);
-  MoePlan* plan = reinterpret_cast<MoePlan*>(static_cast<char*>(workspace) + ((hb + 255) / 256) * 256);
+  char* list = static_cast<char*>(workspace) + ((hb + 255) / 256) * 256;
   hipStream_t s = hipStream_t(stream);
+  if (rows > 8) {  // a prefill chunk's rows: routes grouped by expert, 16-row tiles
+    MX_CHECK(g.experts <= kChunkMaxExperts, MX_EUNSUPPORTED,
+             "mx_moe_experts_mfma: more than 1023 experts beyond eight rows");
+    ChunkPlan* cp = reinterpret_cast<ChunkPlan*>(list);
+    int rc = chunk_plan(ids, rows, g.experts, top_k, cp, s);
+    if (rc == MX_OK) rc = qmm_chunk_gate_up(x, cp, rows, g.experts, top_k, g, u, sg, su, h, s);
+    if (rc == MX_OK)
+      rc = qmm_chunk_down(h, cp, scores, rows, g.experts, top_k, g.n, sg.n, d, sd, partial, s);
+    return finish(rc, "mx_moe_experts_mfma");
+  }
+  MoePlan* plan = reinterpret_cast<MoePlan*>(list);
   int rc = skinny_gate_up(x, ids, rows, top_k, g, u, sg, su, h, s);
   if (rc == MX_OK) rc = skinny_down(h, ids, scores, rows, top_k, g.n, sg.n, d, sd, partial, s);
   if (rc != MX_EUNSUPPORTED) return finish(rc, "mx_moe_experts_mfma");

@@ -94,8 +94,8 @@ struct Engine {
     HcW mixer;
   } mtp;
   bool has_mtp = false;
-  uint16_t *mtp_emb = nullptr, *mtp_a = nullptr, *mtp_e = nullptr;   // [8][H]
-  uint16_t *mtp_prev = nullptr, *mtp_hn = nullptr, *mtp_f = nullptr;  // [8][hc H]
+  uint16_t *mtp_emb = nullptr, *mtp_a = nullptr, *mtp_e = nullptr;   // [rows][H]
+  uint16_t *mtp_prev = nullptr, *mtp_hn = nullptr, *mtp_f = nullptr;  // [rows][hc H]
   uint16_t* mtp_dh = nullptr;                                          // [hc H]
   // dims
   int H = 0, cd = 0, vd = 0, P = 0, Q = 0, max_chunks = 0;
@@ -114,13 +114,15 @@ struct Engine {
   float* snap_state = nullptr;    // [n_gdn][hv][dk][dv]
   uint16_t* snap_conv = nullptr;  // [n_gdn][K-1][cd]
   int verify_slot = -1, verify_count = 0, verify_base = 0;
-  // activations (rows <= 8)
+  // activations (rows <= kPrefillChunk: a decode step or verify block uses
+  // at most 8, a prefill chunk up to kPrefillChunk)
   uint16_t *h = nullptr, *xn = nullptr, *lo = nullptr, *inj = nullptr, *mixed = nullptr;
   uint16_t *pbuf = nullptr, *conv_out = nullptr, *y = nullptr, *qrot = nullptr, *attn_y = nullptr;
   uint16_t *logits_r = nullptr, *scores = nullptr, *factor = nullptr, *moe_p = nullptr;
   uint16_t *moe_h = nullptr, *logits = nullptr;
   void* moe_ws = nullptr;
   MoePlan* moe_plan_buf = nullptr;
+  ChunkPlan* chunk_plan = nullptr;  // expert work list of a prefill chunk
   uint32_t* ids = nullptr;
   float *o_part = nullptr, *ml_part = nullptr;
   void* head_ws = nullptr;
@@ -133,11 +135,11 @@ struct Engine {
   char* y_plane = nullptr;  // operand plane of the GDN / attention output (exact mode)
   // per-step row table (device) and its pinned host mirror
   struct RowTable {
-    uint32_t tokens[8];
-    int32_t slots[8];
-    int32_t pos[8];
-    int32_t gdn_slots[8];
-    uint32_t next[8];
+    uint32_t tokens[kPrefillChunk];
+    int32_t slots[kPrefillChunk];
+    int32_t pos[kPrefillChunk];
+    int32_t gdn_slots[kPrefillChunk];
+    uint32_t next[kPrefillChunk];
   };
   RowTable* dev_rows = nullptr;
   RowTable* host_rows = nullptr;
@@ -159,6 +161,9 @@ struct Engine {
   // finer diagnostic switch: components (kEx* bits) that run on the exact
   // kernels while the rest stays on the matrix cores
   int exact_parts = 0;
+  // set while a prefill chunk is recorded: every component on the matrix-core
+  // kernels, whatever `exact` says
+  bool chunk = false;
   // profiling (eager steps only): events around each layer's expert kernels
   mx_step_profile* prof = nullptr;
   double prof_routed = 0.0;  // profiled steps: routed expert bytes, summed over layers
@@ -189,7 +194,9 @@ enum : int {
   kExHead = 64,     // vocabulary head
 };
 
-bool ex(const Engine& e, int part) { return e.exact || (e.exact_parts & part) != 0; }
+bool ex(const Engine& e, int part) {
+  return !e.chunk && (e.exact || (e.exact_parts & part) != 0);
+}
 
 // The operand plane of e.mixed when its producer wrote one (the exact
 // hyper-connection path), else null (the consumer stages its operands).
@@ -424,8 +431,8 @@ int build(Engine& e) {
       return MX_EHIP;
   }
 
-  // ---- activations for up to 8 rows ----
-  const size_t R = 8;
+  // ---- activations for up to kPrefillChunk rows ----
+  const size_t R = kPrefillChunk;
   auto a16 = [&](const char* n, size_t count, uint16_t** out) -> int {
     void* q;
     MX_TRY(alloc(e, n, count * 2, &q));
@@ -452,6 +459,8 @@ int build(Engine& e) {
     e.moe_h = static_cast<uint16_t*>(e.moe_ws);
     e.moe_plan_buf = reinterpret_cast<MoePlan*>(static_cast<char*>(e.moe_ws) + ws - sizeof(MoePlan));
   }
+  MX_TRY(alloc(e, "act.chunk_plan", sizeof(ChunkPlan), &v));
+  e.chunk_plan = static_cast<ChunkPlan*>(v);
   MX_TRY(a16("act.logits", R * size_t(c.vocab), &e.logits));
   if (c.mtp) {
     MX_TRY(a16("mtp.act.emb", R * c.hidden, &e.mtp_emb));
@@ -574,7 +583,7 @@ int project(Engine& e, const QWeight& w, const uint16_t* x, int64_t xs, int rows
 
 int hc_forward(Engine& e, const HcW& w, int rows, uint16_t* mixed_out, uint16_t* inj_out) {
   const auto& c = e.cfg;
-  if (!ex(e, kExHc) && hc_fused_supported(w.down, w.up, c.hc, c.hidden, c.hc_rank))
+  if (!ex(e, kExHc) && rows <= 8 && hc_fused_supported(w.down, w.up, c.hc, c.hidden, c.hc_rank))
     return hc_fused(w.down, w.up, e.h, w.scale, rows, c.hc, c.hidden, c.hc_rank, c.rms_eps,
                     e.hc_part, mixed_out, inj_out, e.stream);
   // exact: the norm writes the down projection's operand plane, and the
@@ -702,7 +711,16 @@ int record_layer(Engine& e, const LayerW& L, int rows, int groups, int t, bool h
     rl.y_stride = c.experts + 1;
     MX_TRY(project(e, L.router, e.mixed, c.hidden, rows, rl, kExMoe, mixed_plane(e, rows)));
     bool summed = false;  // slots summed and the streams written
-    if (!e.prof && experts_fast(e, L)) {
+    if (rows > 8) {
+      // a prefill chunk: the routes grouped by expert, on the matrix cores
+      MX_TRY(moe_route(e.logits_r, c.experts + 1, e.logits_r + c.experts, c.experts + 1, rows,
+                       c.experts, c.top_k, e.ids, e.scores, e.factor, e.stream));
+      MX_TRY(chunk_plan(e.ids, rows, c.experts, c.top_k, e.chunk_plan, e.stream));
+      MX_TRY(qmm_chunk_gate_up(e.mixed, e.chunk_plan, rows, c.experts, c.top_k, L.gate, L.up,
+                               L.sgate, L.sup, e.moe_h, e.stream));
+      MX_TRY(qmm_chunk_down(e.moe_h, e.chunk_plan, e.scores, rows, c.experts, c.top_k, L.gate.n,
+                            L.sgate.n, L.down, L.sdown, e.moe_p, e.stream));
+    } else if (!e.prof && experts_fast(e, L)) {
       // the expert gate/up kernel routes the rows itself
       const RouteIO ro{e.logits_r, c.experts + 1, e.logits_r + c.experts, c.experts + 1,
                        e.ids, e.scores, e.factor};
@@ -737,9 +755,10 @@ int record_layer(Engine& e, const LayerW& L, int rows, int groups, int t, bool h
   return MX_OK;
 }
 
-// Greedy head over e.mixed: next tokens into the device row table; with
-// `logits`, the bf16 logits too.
-int record_head(Engine& e, int rows, bool logits);
+// Greedy head over rows first_row .. first_row + rows - 1 of e.mixed: next
+// tokens into the device row table (from entry 0); with `logits`, the bf16
+// logits too.
+int record_head(Engine& e, int rows, bool logits, int first_row = 0);
 
 int record_step(Engine& e, int rows, int groups, int t, bool history, bool logits) {
   const auto& c = e.cfg;
@@ -762,21 +781,21 @@ int record_step(Engine& e, int rows, int groups, int t, bool history, bool logit
   return record_head(e, rows, logits);
 }
 
-int record_head(Engine& e, int rows, bool logits) {
+int record_head(Engine& e, int rows, bool logits, int first_row) {
   const auto& c = e.cfg;
   Engine::RowTable* rt = e.dev_rows;
+  const uint16_t* x = e.mixed + size_t(first_row) * c.hidden;
   int parts = 0;
   float* maxima = static_cast<float*>(e.head_ws);
   uint32_t* indices = reinterpret_cast<uint32_t*>(maxima + size_t(head_parts(c.vocab, c.hidden)) * 8);
   // either head writes the bf16 logits it ranks when they are wanted; heads
   // the matrix-core kernel does not cover take the exact-integer one
   if (!ex(e, kExHead) && skinny_supported(e.head) && e.head.k % 512 == 0 && e.head.k <= 2048)
-    MX_TRY(skinny_head(e.head, e.mixed, rows, maxima, indices, &parts, e.stream,
+    MX_TRY(skinny_head(e.head, x, rows, maxima, indices, &parts, e.stream,
                        logits ? e.logits : nullptr));
   else
-    MX_TRY(xq_head(e.head, e.mixed, mixed_plane(e, rows), rows, maxima, indices,
-                   logits ? e.logits : nullptr, &parts,
-                   e.stream));
+    MX_TRY(xq_head(e.head, x, first_row == 0 ? mixed_plane(e, rows) : nullptr, rows, maxima,
+                   indices, logits ? e.logits : nullptr, &parts, e.stream));
   return argmax_reduce(maxima, indices, rows, parts, rt->next, e.stream);
 }
 
@@ -1088,6 +1107,63 @@ int engine_block(Engine& e, int slot, const uint32_t* tokens, int count, bool hi
   const int rc = run_step(e, count, 1, count, history, next);
   if (rc != MX_OK) return step_failed(e, &slot, 1, rc, err);
   e.offsets[slot] += count;
+  return MX_OK;
+}
+
+// One prefill chunk of `rows` consecutive tokens of one slot (rows from the
+// row table): every layer on the matrix-core kernels with `rows` activation
+// rows (a GDN layer scans the chunk's tokens in order), then the greedy head
+// on the chunk's last row only (its next token lands in entry 0 of `next`).
+static int record_chunk(Engine& e, int rows) {
+  const auto& c = e.cfg;
+  MX_TRY(embed(e.embed, e.dev_rows->tokens, rows, c.hc, e.h, e.stream));
+  for (const LayerW& L : e.layers) MX_TRY(record_layer(e, L, rows, 1, rows, false));
+  MX_TRY(hc_forward(e, e.mixer, rows, e.mixed, nullptr));
+  return record_head(e, 1, false, rows - 1);
+}
+
+// Prefill in chunks of up to kPrefillChunk tokens (speculative::prepare,
+// src/speculative.rs:38-68, which runs the model's forward over each chunk):
+// the projections and experts of a whole chunk on the matrix cores, each
+// weight read once per chunk instead of once per eight tokens.  The chunk's
+// arithmetic is the matrix-core kernels' (fp32 sums in hardware order), so the
+// caches agree with a block-by-block exact prefill to those kernels'
+// tolerance, not bit for bit.  Eager launches (no graph).
+int engine_prefill_chunked(Engine& e, int slot, const uint32_t* tokens, int count,
+                           uint32_t* next, std::string* err) {
+  MX_TRY(slots_usable(e, &slot, 1, err));
+  if (int64_t(e.offsets[slot]) + count > e.cfg.max_context) {
+    *err = "slot context is full";
+    return MX_ESTATE;
+  }
+  if (slot == e.verify_slot) e.verify_slot = -1;
+  for (int a = 0; a < count; a += kPrefillChunk) {
+    const int n = count - a < kPrefillChunk ? count - a : kPrefillChunk;
+    for (int r = 0; r < n; ++r) {
+      e.host_rows->tokens[r] = tokens[a + r];
+      e.host_rows->slots[r] = slot;
+      e.host_rows->pos[r] = e.offsets[slot] + r;
+    }
+    e.host_rows->gdn_slots[0] = slot * e.n_gdn;
+    int rc = MX_OK;
+    if (hipMemcpyAsync(e.dev_rows, e.host_rows, sizeof(Engine::RowTable), hipMemcpyHostToDevice,
+                       e.stream) != hipSuccess)
+      rc = MX_EHIP;
+    if (rc == MX_OK) {
+      e.chunk = true;
+      rc = record_chunk(e, n);
+      e.chunk = false;
+    }
+    if (rc == MX_OK &&
+        (hipMemcpyAsync(e.host_rows->next, e.dev_rows->next, sizeof(uint32_t),
+                        hipMemcpyDeviceToHost, e.stream) != hipSuccess ||
+         hipStreamSynchronize(e.stream) != hipSuccess))
+      rc = MX_EHIP;
+    if (rc != MX_OK) return step_failed(e, &slot, 1, rc, err);
+    e.offsets[slot] += n;
+    *next = e.host_rows->next[0];
+  }
+  e.last_rows = 0;  // the activation buffers hold no step's rows
   return MX_OK;
 }
 

@@ -74,7 +74,11 @@ struct ProjEpilogue {
 constexpr int kConvMaxTaps = 4;
 int proj(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const ProjEpilogue& e,
          hipStream_t s);
-// matrix-core (MFMA) projections, 1..16 rows, group size 64 (qmm.hip)
+// rows of one prefill chunk (the chunk of speculative::prepare,
+// src/speculative.rs:38-68)
+constexpr int kPrefillChunk = 128;
+// matrix-core (MFMA) projections, 1..kQmmMaxRows rows, group size 64 (qmm.hip)
+constexpr int kQmmMaxRows = kPrefillChunk;
 bool qmm_supported(const QWeight& w);
 int qmm(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const ProjEpilogue& e,
         hipStream_t s);
@@ -223,6 +227,33 @@ int qmm_gate_up(const uint16_t* x, const MoePlan* plan, int rows, int top_k, con
 int qmm_down(const uint16_t* h, const MoePlan* plan, const uint16_t* scores, int rows, int top_k,
              int inter, int shared_inter, const QBank& down, const QWeight& sdown, uint16_t* p,
              hipStream_t s);
+// Work list of a prefill chunk's experts (more than eight rows): the routes
+// grouped by expert (experts in index order, then the shared expert -1), each
+// expert's routes in row order, cut into items of at most 16 routes (one
+// 16-row matrix-core tile).  member row / slot: the slot is top_k for the
+// shared expert.
+constexpr int kChunkRoutes = kPrefillChunk * 17;  // top_k <= 16, plus the shared slot
+constexpr int kChunkMaxExperts = 1023;
+struct ChunkPlan {
+  int32_t nitems;
+  int32_t expert[kChunkRoutes];
+  int32_t start[kChunkRoutes];
+  int32_t m[kChunkRoutes];
+  uint8_t row[kChunkRoutes];
+  uint8_t slot[kChunkRoutes];
+};
+// items a chunk of `rows` rows can produce (a bound: the grids' y extent)
+int chunk_max_items(int rows, int experts, int top_k);
+int chunk_plan(const uint32_t* ids, int rows, int experts, int top_k, ChunkPlan* plan,
+               hipStream_t s);
+// matrix-core expert MLPs over a ChunkPlan (qmm.hip): h [rows][top_k + 1][hs]
+// and p [rows][top_k + 1][hidden], the contracts of moe_gate_up / moe_down
+int qmm_chunk_gate_up(const uint16_t* x, const ChunkPlan* plan, int rows, int experts, int top_k,
+                      const QBank& gate, const QBank& up, const QWeight& sgate,
+                      const QWeight& sup, uint16_t* h, hipStream_t s);
+int qmm_chunk_down(const uint16_t* h, const ChunkPlan* plan, const uint16_t* scores, int rows,
+                   int experts, int top_k, int inter, int shared_inter, const QBank& down,
+                   const QWeight& sdown, uint16_t* p, hipStream_t s);
 int moe_reduce(const uint16_t* p, int rows, int top_k, int hidden, uint16_t* routed,
                hipStream_t s);
 int moe_hc_epilogue(const uint16_t* routed, const uint16_t* shared, const uint16_t* factor,
@@ -300,6 +331,8 @@ int engine_decode_forced(Engine& e, const int32_t* slots, const uint32_t* tokens
                          uint32_t* next, std::string* err);
 int engine_block(Engine& e, int slot, const uint32_t* tokens, int count, bool history,
                  uint32_t* next, std::string* err);
+int engine_prefill_chunked(Engine& e, int slot, const uint32_t* tokens, int count,
+                           uint32_t* next, std::string* err);
 int engine_verify(Engine& e, int slot, const uint32_t* tokens, int count, uint32_t* next,
                   std::string* err);
 int engine_commit(Engine& e, int slot, int keep, std::string* err);

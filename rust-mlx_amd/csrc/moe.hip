@@ -172,6 +172,89 @@ __global__ __launch_bounds__(512) void route_plan_kernel(
   plan_body<512>(sids, rows, top_k, plan);
 }
 
+// ---------------------------------------------------------------------------
+// Expert work list of a prefill chunk (up to kPrefillChunk rows): the routes
+// grouped by expert, experts in index order and then the shared expert, each
+// expert's routes in row order (a row names an expert at most once), cut into
+// items of at most 16 routes.  One workgroup of 1024 threads; thread e < 1024
+// owns expert e (the shared expert is index `experts`).
+constexpr int kChunkPlanThreads = 1024;
+
+// Exclusive prefix sum over the workgroup's threads in thread order, and the
+// total (every thread calls it).
+__device__ __forceinline__ int block_exclusive_sum(int v, int* total) {
+  __shared__ int wave_sum[kChunkPlanThreads / 64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int incl = v;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += u;
+  }
+  if (lane == 63) wave_sum[wave] = incl;
+  __syncthreads();
+  int before = 0, all = 0;
+  for (int w = 0; w < kChunkPlanThreads / 64; ++w) {
+    if (w < wave) before += wave_sum[w];
+    all += wave_sum[w];
+  }
+  __syncthreads();  // wave_sum may be reused by the next call
+  *total = all;
+  return before + incl - v;
+}
+
+__global__ __launch_bounds__(kChunkPlanThreads) void chunk_plan_kernel(
+    const uint32_t* __restrict__ ids, int rows, int experts, int top_k,
+    ChunkPlan* __restrict__ plan) {
+  // rows (bits 0..127) that route to each expert
+  __shared__ uint32_t mask[kChunkPlanThreads][kPrefillChunk / 32];
+  __shared__ int first[kChunkPlanThreads];  // each expert's first member
+  const int t = threadIdx.x;
+  constexpr int W = kPrefillChunk / 32;
+#pragma unroll
+  for (int w = 0; w < W; ++w) mask[t][w] = 0u;
+  __syncthreads();
+  const int routes = rows * top_k;
+  for (int r = t; r < routes; r += kChunkPlanThreads) {
+    const uint32_t e = ids[r];
+    const int row = r / top_k;
+    if (e < uint32_t(experts)) atomicOr(&mask[e][row >> 5], 1u << (row & 31));
+  }
+  __syncthreads();
+  int cnt = 0;
+  if (t < experts) {
+#pragma unroll
+    for (int w = 0; w < W; ++w) cnt += __popc(mask[t][w]);
+  } else if (t == experts) {
+    cnt = rows;
+  }
+  const int items = (cnt + 15) / 16;
+  int members = 0, nitems = 0;
+  const int m_off = block_exclusive_sum(cnt, &members);
+  const int i_off = block_exclusive_sum(items, &nitems);
+  first[t] = m_off;
+  if (t == 0) plan->nitems = nitems;
+  for (int i = 0; i < items; ++i) {
+    plan->expert[i_off + i] = t == experts ? -1 : t;
+    plan->start[i_off + i] = m_off + 16 * i;
+    plan->m[i_off + i] = cnt - 16 * i < 16 ? cnt - 16 * i : 16;
+  }
+  __syncthreads();
+  for (int r = t; r < routes; r += kChunkPlanThreads) {
+    const uint32_t e = ids[r];
+    if (e >= uint32_t(experts)) continue;
+    const int row = r / top_k;
+    int rank = __popc(mask[e][row >> 5] & ((1u << (row & 31)) - 1u));
+    for (int w = 0; w < (row >> 5); ++w) rank += __popc(mask[e][w]);
+    const int at = first[e] + rank;
+    plan->row[at] = uint8_t(row);
+    plan->slot[at] = uint8_t(r - row * top_k);
+  }
+  for (int row = t; row < rows; row += kChunkPlanThreads) {
+    plan->row[first[experts] + row] = uint8_t(row);
+    plan->slot[first[experts] + row] = uint8_t(top_k);
+  }
+}
+
 struct Bank {
   const uint32_t* codes;
   const uint16_t* scales;
@@ -496,6 +579,22 @@ int moe_plan(const uint32_t* ids, int rows, int top_k, MoePlan* plan, hipStream_
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 
+int chunk_max_items(int rows, int experts, int top_k) {
+  // an expert with c routes gives ceil(c / 16) <= 1 + (c - 1) / 16 items
+  const int routes = rows * top_k;
+  return (routes < experts ? routes : experts) + (routes + 15) / 16 + (rows + 15) / 16;
+}
+
+int chunk_plan(const uint32_t* ids, int rows, int experts, int top_k, ChunkPlan* plan,
+               hipStream_t s) {
+  if (rows < 1 || rows > kPrefillChunk || top_k < 1 || top_k > 16 || experts < 1 ||
+      experts > kChunkMaxExperts)
+    return MX_EUNSUPPORTED;
+  hipLaunchKernelGGL(chunk_plan_kernel, dim3(1), dim3(kChunkPlanThreads), 0, s, ids, rows,
+                     experts, top_k, plan);
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
 int moe_gate_up(const uint16_t* x, const MoePlan* plan, int rows, int top_k, const QBank& gate,
                 const QBank& up, const QWeight& sgate, const QWeight& sup, uint16_t* h,
                 hipStream_t s) {
@@ -537,8 +636,9 @@ int moe_down(const uint16_t* h, const MoePlan* plan, const uint16_t* scores, int
 }
 
 size_t moe_workspace_bytes(int rows, int top_k, int inter) {
+  // h, then the work list: a MoePlan (<= 8 rows) or a ChunkPlan
   const size_t h = size_t(rows) * (top_k + 1) * inter * sizeof(uint16_t);
-  return ((h + 255) / 256) * 256 + sizeof(MoePlan);
+  return ((h + 255) / 256) * 256 + (rows > 8 ? sizeof(ChunkPlan) : sizeof(MoePlan));
 }
 
 int moe_experts(const uint16_t* x, const uint32_t* ids, const uint16_t* scores, int rows,

@@ -1,5 +1,6 @@
 // Fast affine-quantised projections on the gfx950 matrix cores (MFMA), for
-// 1..16 activation rows: decode batches, verify blocks and prefill chunks.
+// 1..kQmmMaxRows activation rows (blocks of 16 rows): decode batches, verify
+// blocks and prefill chunks.
 //
 // Replaces the same reference interfaces as the exact kernels (qmv_kernel /
 // gather_qmm of Linear::forward_rows, src/weights.rs:111-202; the expert
@@ -64,10 +65,14 @@ __device__ __forceinline__ bool reduce_split(floatx4_t (&y)[NT], float* red) {
 // Dense projections with the proj.hip epilogues.  NT = 1 for kPlain, kHcDown
 // and kHcWrite (tile group = 16 rows); NT = 4 for kHcUpMix (the four streams
 // s*H + c of 16 columns c).
+// blockIdx.y: the block of 16 activation rows (rows 16 blockIdx.y .. +15).
 template <int BITS, int NT, int SK>
 __global__ __launch_bounds__(256) void dense_kernel(QWeight w, const uint16_t* __restrict__ x,
                                                     int64_t x_stride, int M, ProjEpilogue e) {
   __shared__ float red[(SK > 1 ? 4 * NT * 64 * 4 : 4)];
+  const int m0 = 16 * blockIdx.y;
+  x += size_t(m0) * x_stride;
+  M = min(M - m0, 16);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 15, kq = lane >> 4;
   const int tg = blockIdx.x * (4 / SK) + wave / SK;
@@ -100,8 +105,8 @@ __global__ __launch_bounds__(256) void dense_kernel(QWeight w, const uint16_t* _
   if (!reduce_split<NT, SK>(y, red) || !live) return;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int m = 4 * kq + r;
-    if (m >= M) continue;
+    if (4 * kq + r >= M) continue;
+    const int m = m0 + 4 * kq + r;
     if constexpr (NT == 4) {
       const int c = base + j;
       if (c >= e.hidden) continue;
@@ -146,7 +151,8 @@ void launch_dense(const QWeight& w, const uint16_t* x, int64_t xs, int m, const 
   const int tiles = NT == 4 ? (e.hidden + 15) / 16 : (w.n + 16 * NT - 1) / (16 * NT);
   const int per_block = 4 / SK;
   const int blocks = (tiles + per_block - 1) / per_block;
-  hipLaunchKernelGGL((dense_kernel<BITS, NT, SK>), dim3(blocks), dim3(256), 0, s, w, x, xs, m, e);
+  hipLaunchKernelGGL((dense_kernel<BITS, NT, SK>), dim3(blocks, (m + 15) / 16), dim3(256), 0, s, w,
+                     x, xs, m, e);
 }
 
 template <int BITS, int NT>
@@ -279,6 +285,117 @@ __global__ __launch_bounds__(256) void expert_down_kernel(const uint16_t* __rest
   }
 }
 
+// ---------------------------------------------------------------------------
+// Experts of a prefill chunk over a ChunkPlan: one workgroup serves one item
+// (an expert and up to 16 of its routes) for 4/SK tile groups; the
+// arithmetic of expert_gate_up_kernel / expert_down_kernel.  Lane j (of each
+// quarter) holds member j's row and slot; the epilogue's rows 4 kq .. +3 read
+// theirs from those lanes.
+struct ChunkItem {
+  int m, expert;
+  int row, slot;      // this lane's member (j < m; else member m - 1)
+  int erow[4], eslot[4];  // members 4 kq .. 4 kq + 3 (epilogue rows)
+};
+
+__device__ __forceinline__ ChunkItem chunk_item(const ChunkPlan* __restrict__ plan, int item) {
+  ChunkItem it;
+  it.m = plan->m[item];
+  it.expert = plan->expert[item];
+  const int start = plan->start[item];
+  const int lane = threadIdx.x & 63;
+  const int j = lane & 15, kq = lane >> 4;
+  const int mj = j < it.m ? j : it.m - 1;
+  it.row = plan->row[start + mj];
+  it.slot = plan->slot[start + mj];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {  // every lane takes part in the shuffles
+    it.erow[r] = __shfl(it.row, 4 * kq + r, 64);
+    it.eslot[r] = __shfl(it.slot, 4 * kq + r, 64);
+  }
+  return it;
+}
+
+template <int BITS, int SK>
+__global__ __launch_bounds__(256) void chunk_gate_up_kernel(const uint16_t* __restrict__ x,
+                                                            const ChunkPlan* __restrict__ plan,
+                                                            int top_k, QBank gate, QBank up,
+                                                            QWeight sgate, QWeight sup,
+                                                            uint16_t* __restrict__ h, int hs) {
+  __shared__ float red[(SK > 1 ? 4 * 2 * 64 * 4 : 4)];
+  if (int(blockIdx.y) >= plan->nitems) return;
+  const ChunkItem it = chunk_item(plan, blockIdx.y);
+  const QWeight gw = expert_weight(gate, it.expert, sgate);
+  const QWeight uw = expert_weight(up, it.expert, sup);
+  const int hidden = gate.k;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 15, kq = lane >> 4;
+  const int tg = blockIdx.x * (4 / SK) + wave / SK;
+  const int kp = wave % SK;
+  const int inter = gw.n;
+  const int base = tg * 16;
+  const bool live = base < inter;
+  floatx4_t y[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+  const int G = hidden >> 6;
+  if (live) {
+    const int row = min(base + j, inter - 1);
+    const TileRow tr[2] = {tile_row(gw.codes, gw.scales, gw.biases, hidden, BITS, row),
+                           tile_row(uw.codes, uw.scales, uw.biases, hidden, BITS, row)};
+    const uint16_t* xa = j < it.m ? x + size_t(it.row) * hidden : nullptr;
+    qmm_tiles<BITS, 2>(tr, xa, G * kp / SK, G * (kp + 1) / SK, y);
+  }
+  if (!reduce_split<2, SK>(y, red) || !live) return;
+  const int c = base + j;
+  if (c >= inter) return;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    if (4 * kq + r >= it.m) continue;
+    const float gv = round_bf16(y[0][r]);
+    const float uv = round_bf16(y[1][r]);
+    const float silu = round_bf16(gv * sigmoid_bf16(gv));
+    h[(size_t(it.erow[r]) * (top_k + 1) + it.eslot[r]) * hs + c] = f32_to_bf16(silu * uv);
+  }
+}
+
+template <int BITS, int SK>
+__global__ __launch_bounds__(256) void chunk_down_kernel(const uint16_t* __restrict__ h,
+                                                         const ChunkPlan* __restrict__ plan,
+                                                         const uint16_t* __restrict__ scores,
+                                                         int top_k, QBank down, QWeight sdown,
+                                                         uint16_t* __restrict__ p, int hs) {
+  __shared__ float red[(SK > 1 ? 4 * 64 * 4 : 4)];
+  if (int(blockIdx.y) >= plan->nitems) return;
+  const ChunkItem it = chunk_item(plan, blockIdx.y);
+  const QWeight dw = expert_weight(down, it.expert, sdown);
+  const int hidden = dw.n, inter = dw.k;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 15, kq = lane >> 4;
+  const int tg = blockIdx.x * (4 / SK) + wave / SK;
+  const int kp = wave % SK;
+  const int base = tg * 16;
+  const bool live = base < hidden;
+  floatx4_t y[1] = {{0.0f, 0.0f, 0.0f, 0.0f}};
+  const int G = inter >> 6;
+  if (live) {
+    const TileRow tr[1] = {tile_row(dw.codes, dw.scales, dw.biases, inter, BITS,
+                                    min(base + j, hidden - 1))};
+    const uint16_t* xa =
+        j < it.m ? h + (size_t(it.row) * (top_k + 1) + it.slot) * hs : nullptr;
+    qmm_tiles<BITS, 1>(tr, xa, G * kp / SK, G * (kp + 1) / SK, y);
+  }
+  if (!reduce_split<1, SK>(y, red) || !live) return;
+  const int c = base + j;
+  if (c >= hidden) return;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    if (4 * kq + r >= it.m) continue;
+    const int row = it.erow[r], slot = it.eslot[r];
+    const bool routed = slot < top_k;
+    const float dv = round_bf16(y[0][r]);
+    const float sc = routed ? bf16_to_f32(scores[size_t(row) * top_k + slot]) : 1.0f;
+    p[(size_t(row) * (top_k + 1) + slot) * hidden + c] = f32_to_bf16(routed ? dv * sc : dv);
+  }
+}
+
 }  // namespace
 
 bool qmm_supported(const QWeight& w) {
@@ -288,7 +405,7 @@ bool qmm_supported(const QWeight& w) {
 
 int qmm(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const ProjEpilogue& e,
         hipStream_t s) {
-  if (!qmm_supported(w) || m < 1 || m > 16) return MX_EUNSUPPORTED;
+  if (!qmm_supported(w) || m < 1 || m > kQmmMaxRows) return MX_EUNSUPPORTED;
   if (e.mode == kHcUpMix && e.hidden * 4 != w.n) return MX_EUNSUPPORTED;
   if (e.mode == kConv) return MX_EUNSUPPORTED;
   switch (w.bits) {
@@ -335,6 +452,45 @@ int qmm_down(const uint16_t* h, const MoePlan* plan, const uint16_t* scores, int
     hipLaunchKernelGGL((expert_down_kernel<B, K>), grid, dim3(256), 0, s, h, plan, scores,  \
                        top_k, down, sdown, p, hs);                                          \
     return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;                              \
+  }
+  MX_DN(4, 4) MX_DN(4, 2) MX_DN(4, 1) MX_DN(5, 4) MX_DN(5, 2) MX_DN(5, 1)
+  MX_DN(6, 4) MX_DN(6, 2) MX_DN(6, 1) MX_DN(8, 4) MX_DN(8, 2) MX_DN(8, 1)
+#undef MX_DN
+  return MX_EUNSUPPORTED;
+}
+
+int qmm_chunk_gate_up(const uint16_t* x, const ChunkPlan* plan, int rows, int experts, int top_k,
+                      const QBank& gate, const QBank& up, const QWeight& sgate,
+                      const QWeight& sup, uint16_t* h, hipStream_t s) {
+  const int hs = gate.n > sgate.n ? gate.n : sgate.n;
+  const int SK = split_k(gate.k);
+  const int tiles = (hs + 15) / 16;
+  const dim3 grid((tiles + 4 / SK - 1) / (4 / SK), chunk_max_items(rows, experts, top_k));
+#define MX_GU(B, K)                                                                        \
+  if (gate.bits == B && SK == K) {                                                         \
+    hipLaunchKernelGGL((chunk_gate_up_kernel<B, K>), grid, dim3(256), 0, s, x, plan, top_k, \
+                       gate, up, sgate, sup, h, hs);                                       \
+    return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;                             \
+  }
+  MX_GU(4, 4) MX_GU(4, 2) MX_GU(4, 1) MX_GU(5, 4) MX_GU(5, 2) MX_GU(5, 1)
+  MX_GU(6, 4) MX_GU(6, 2) MX_GU(6, 1) MX_GU(8, 4) MX_GU(8, 2) MX_GU(8, 1)
+#undef MX_GU
+  return MX_EUNSUPPORTED;
+}
+
+int qmm_chunk_down(const uint16_t* h, const ChunkPlan* plan, const uint16_t* scores, int rows,
+                   int experts, int top_k, int inter, int shared_inter, const QBank& down,
+                   const QWeight& sdown, uint16_t* p, hipStream_t s) {
+  const int hs = inter > shared_inter ? inter : shared_inter;
+  const int kmin = down.k < sdown.k ? down.k : sdown.k;
+  const int SK = split_k(kmin);
+  const int tiles = (down.n + 15) / 16;
+  const dim3 grid((tiles + 4 / SK - 1) / (4 / SK), chunk_max_items(rows, experts, top_k));
+#define MX_DN(B, K)                                                                          \
+  if (down.bits == B && SK == K) {                                                           \
+    hipLaunchKernelGGL((chunk_down_kernel<B, K>), grid, dim3(256), 0, s, h, plan, scores,    \
+                       top_k, down, sdown, p, hs);                                           \
+    return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;                               \
   }
   MX_DN(4, 4) MX_DN(4, 2) MX_DN(4, 1) MX_DN(5, 4) MX_DN(5, 2) MX_DN(5, 1)
   MX_DN(6, 4) MX_DN(6, 2) MX_DN(6, 1) MX_DN(8, 4) MX_DN(8, 2) MX_DN(8, 1)

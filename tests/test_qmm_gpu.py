@@ -21,7 +21,7 @@ def test_qmm_against_closed_form_and_exact(mx, orc, bits, k, n):
     seed = 7000 + bits * 100 + k // 64
     w = mx.QWeight.random(n, k, bits, gs, seed)
     codes, s, b = orc.random_qweight(n, k, bits, gs, seed)
-    for m in (1, 3, 8, 16):
+    for m in (1, 3, 8, 16, 40, 128):  # beyond 16: blocks of 16 rows (a prefill chunk)
         x = orc.fill_bf16(m * k, seed + m, 1, 1.0, 0.0).reshape(m, k)
         dx = mx.DeviceArray.from_numpy(x)
         dy = mx.DeviceArray((m, n), np.uint16)
@@ -91,6 +91,34 @@ def test_moe_experts_mfma_every_width(mx, orc, bits):
     x = orc.fill_bf16(rows * H, 710 + bits, 1, 1.0, 0.0).reshape(rows, H)
     want = bf(m.run(mx, x, ids, scores, top_k)).astype(np.float64)
     got = bf(_experts_mfma(mx, m, x, ids, scores, top_k)).astype(np.float64)
+    scale = np.abs(want).max(axis=2, keepdims=True)
+    assert np.all(np.abs(got - want) <= 2e-2 * np.abs(want) + 1e-2 * scale)
+    assert np.mean(got == want) > 0.5
+
+
+@pytest.mark.parametrize("rows,E,top_k,H", [(40, 64, 10, 2048), (128, 64, 10, 2048),
+                                            (128, 512, 10, 2048), (17, 32, 6, 512)])
+def test_moe_experts_mfma_prefill_chunk_rows(mx, orc, rows, E, top_k, H):
+    """Beyond eight rows (a prefill chunk): routes grouped by expert into
+    16-route tiles.  At 128 rows over 64 experts most experts take more than
+    16 routes (several tiles each); against the exact kernels run eight rows
+    at a time, within the north star's tolerance."""
+    from test_layers_gpu import Moe
+
+    I = 512
+    m = Moe(mx, orc, E, I, H, seed=650 + rows + E)
+    m.ws = mx.DeviceArray((mx.lib.mx_moe_workspace_bytes(rows, top_k, I),), np.uint8)
+    rng = np.random.default_rng(rows + E)
+    ids = np.stack([rng.choice(E, top_k, replace=False) for _ in range(rows)]).astype(np.uint32)
+    scores = orc.f32_to_bf16(rng.uniform(0.05, 0.5, (rows, top_k)).astype(np.float32))
+    x = orc.fill_bf16(rows * H, 660 + rows, 1, 1.0, 0.0).reshape(rows, H)
+    got = bf(_experts_mfma(mx, m, x, ids, scores, top_k)).astype(np.float64)
+    ws = m.ws
+    m.ws = mx.DeviceArray((mx.lib.mx_moe_workspace_bytes(8, top_k, I),), np.uint8)
+    want = np.concatenate([m.run(mx, x[r:r + 8], ids[r:r + 8], scores[r:r + 8], top_k)
+                           for r in range(0, rows, 8)])
+    m.ws = ws
+    want = bf(want).astype(np.float64)
     scale = np.abs(want).max(axis=2, keepdims=True)
     assert np.all(np.abs(got - want) <= 2e-2 * np.abs(want) + 1e-2 * scale)
     assert np.mean(got == want) > 0.5
