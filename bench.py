@@ -8,7 +8,7 @@ Workloads:
       MoE with a shared expert, hc = 4 hyper-connections, vocab 151936, 4-bit
       weights with 5-bit expert down and 8-bit embedding/head), 8 slots
       prefilled with seeded uniform-random prompts of ragged lengths 10..2048
-      (128-token chunks on the matrix cores; --block-prefill: the exact
+      (256-token chunks on the matrix cores; --block-prefill: the exact
       eight-token blocks), then batched greedy decode of all 8 rows per step (rows at their own
       offsets).  A step = one decode token for each of the 8 rows; W + K = 256
       steps per row by default.  value = aggregate tok/s over the K timed steps.
@@ -123,7 +123,7 @@ def bench_config3(mx, args):
             nxt[s] = eng.prefill(s, prompt, chunked=not args.block_prefill)
     prefill_s = time.perf_counter() - t0
     prefill_mode = ("synthetic" if args.synthetic_context else
-                    "exact 8-token blocks" if args.block_prefill else "128-token chunks")
+                    "exact 8-token blocks" if args.block_prefill else "256-token chunks")
     log(f"config3: {'filled' if args.synthetic_context else 'prefilled'} {int(lengths.sum())} "
         f"context positions (lengths {[int(x) for x in lengths]}) in {prefill_s:.2f}s "
         f"({prefill_mode}, {lengths.sum() / prefill_s:.0f} positions/s)")
@@ -1059,7 +1059,7 @@ def main() -> None:
                          "the context length only)")
     ap.add_argument("--block-prefill", action="store_true",
                     help="config3: prefill the contexts in exact eight-token blocks "
-                         "(mx_engine_prefill) instead of 128-token matrix-core chunks "
+                         "(mx_engine_prefill) instead of 256-token matrix-core chunks "
                          "(mx_engine_prefill_chunked)")
     ap.add_argument("--fast", action="store_true",
                     help="config3: time the bf16 matrix-core kernels (within tolerance of the "

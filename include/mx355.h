@@ -188,8 +188,8 @@ mx_status mx_qmv(const mx_qweight* w, const uint16_t* x, int32_t m, uint16_t* y,
                  void* stream);
 
 /* ---- A3/A15: the same projection on the matrix cores --------------------
- * y = x . dequant(W)^T for 1 <= m <= 128 rows (blocks of 16) with
- * v_mfma_f32_16x16x32_bf16:
+ * y = x . dequant(W)^T for 1 <= m <= 256 rows with v_mfma_f32_16x16x32_bf16
+ * (beyond 16 rows a GEMM staging 128-row blocks of x in LDS):
  * codes enter as exact bf16 integers, each 64-value group's fp32 partial is
  * scaled in registers.  Results equal mx_qmv's up to fp32 summation order
  * (the north star's tolerance, not bit for bit).  Requires group_size 64 and
@@ -268,7 +268,7 @@ mx_status mx_moe_experts(const uint16_t* x, const uint32_t* ids, const uint16_t*
                          const mx_qweight* shared_up, const mx_qweight* shared_down,
                          void* workspace, uint16_t* partial, void* stream);
 /* mx_moe_experts on the matrix cores (same contract, fp32 summation order
- * within tolerance of the exact kernels), for 1..128 rows: beyond eight rows
+ * within tolerance of the exact kernels), for 1..256 rows: beyond eight rows
  * (a prefill chunk) the routes are grouped by expert into 16-route matrix-core
  * tiles, each expert's weights read once per 16 of its routes, and the banks
  * may hold at most 1023 experts. */
@@ -520,9 +520,10 @@ mx_status mx_engine_decode_batch_outputs(mx_engine* e, const int32_t* slots,
                                          uint16_t* logits, uint16_t* hidden);
 mx_status mx_engine_prefill(mx_engine* e, int32_t slot, const uint32_t* tokens, int32_t count,
                             uint32_t* next);
-/* mx_engine_prefill_chunked: the same contract in chunks of up to 128 tokens
- * (the chunk size speculative::prepare is called with; its loop is
- * src/speculative.rs:38-68, one model forward per chunk).  A chunk's
+/* mx_engine_prefill_chunked: the same contract in chunks of up to 256 tokens
+ * (speculative::prepare's loop, src/speculative.rs:38-68, one model forward
+ * per chunk; the reference calls it with 128, twice the chunk here halves the
+ * expert weights read per token).  A chunk's
  * projections and experts run as 16-row matrix-core tiles over all of its
  * rows (each weight read once per chunk), its attention is causal over the
  * chunk, and its GDN layers scan its tokens in order; *next comes from the

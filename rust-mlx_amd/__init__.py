@@ -614,7 +614,7 @@ class Engine:
 
     def prefill(self, slot, tokens, chunked=False) -> int:
         """Feeds tokens to a slot; returns the greedy token after the last one.
-        chunked: mx_engine_prefill_chunked (128-token chunks on the matrix
+        chunked: mx_engine_prefill_chunked (256-token chunks on the matrix
         cores, within tolerance of the exact 8-token blocks)."""
         t = self._u32(tokens)
         out = np.empty(1, np.uint32)

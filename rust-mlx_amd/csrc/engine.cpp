@@ -123,6 +123,10 @@ struct Engine {
   void* moe_ws = nullptr;
   MoePlan* moe_plan_buf = nullptr;
   ChunkPlan* chunk_plan = nullptr;  // expert work list of a prefill chunk
+  float* gemm_part = nullptr;       // a prefill chunk's k-split GEMM partials
+  size_t gemm_part_floats = 0;
+  void* gdn_io = nullptr;           // a prefill chunk's GDN scan inputs
+  float* gdn_ws = nullptr;          // and the chunked scan's workspace
   uint32_t* ids = nullptr;
   float *o_part = nullptr, *ml_part = nullptr;
   void* head_ws = nullptr;
@@ -461,6 +465,14 @@ int build(Engine& e) {
   }
   MX_TRY(alloc(e, "act.chunk_plan", sizeof(ChunkPlan), &v));
   e.chunk_plan = static_cast<ChunkPlan*>(v);
+  e.gemm_part_floats = size_t(4) << 20;  // 16 MB: the projections' k-split partials
+  MX_TRY(alloc(e, "act.gemm_part", e.gemm_part_floats * 4, &v));
+  e.gemm_part = static_cast<float*>(v);
+  if (e.n_gdn > 0) {
+    MX_TRY(alloc(e, "act.gdn_chunk_io", gdn_chunk_io_bytes(int(R), e.gd), &e.gdn_io));
+    MX_TRY(alloc(e, "act.gdn_chunk_ws", gdn_chunk_workspace_bytes(1, c.gdn_hv, int(R)), &v));
+    e.gdn_ws = static_cast<float*>(v);
+  }
   MX_TRY(a16("act.logits", R * size_t(c.vocab), &e.logits));
   if (c.mtp) {
     MX_TRY(a16("mtp.act.emb", R * c.hidden, &e.mtp_emb));
@@ -577,7 +589,12 @@ int project(Engine& e, const QWeight& w, const uint16_t* x, int64_t xs, int rows
             const ProjEpilogue& ep, int part, const char* plane = nullptr) {
   if (ex(e, part)) return xq_dense(w, x, xs, rows, ep, e.stream, plane);
   if (rows <= 8 && skinny_supported(w)) return skinny_dense(w, x, xs, rows, ep, e.stream);
-  if (qmm_supported(w)) return qmm(w, x, xs, rows, ep, e.stream);
+  if (qmm_supported(w)) {
+    ProjEpilogue ek = ep;  // prefill rows may split k across workgroups
+    ek.part = e.gemm_part;
+    ek.part_floats = e.gemm_part_floats;
+    return qmm(w, x, xs, rows, ek, e.stream);
+  }
   return xq_dense(w, x, xs, rows, ep, e.stream);
 }
 
@@ -665,7 +682,14 @@ int record_layer(Engine& e, const LayerW& L, int rows, int groups, int t, bool h
                         e.stream));
       }
       float* hist = history ? e.hist_state + size_t(gi) * c.max_verify * state_per : nullptr;
-      if (!ex(e, kExGdn)) {
+      if (!ex(e, kExGdn) && rows > 8) {
+        // a prefill chunk: the chunked scan (64-token chunks on the matrix
+        // cores) in place of the token-by-token step
+        MX_TRY(gdn_chunk_fast(e.conv_out, e.cd, e.pbuf + e.cd, e.pbuf + e.cd + e.vd,
+                              e.pbuf + e.cd + e.vd + c.gdn_hv, e.P, L.a_log, L.dt_bias,
+                              L.gdn_norm, c.rms_eps, e.gd, groups, t, rt->gdn_slots,
+                              e.gdn_state + gi * state_per, e.y, e.gdn_io, e.gdn_ws, e.stream));
+      } else if (!ex(e, kExGdn)) {
         // decode, verify and prefill blocks alike: a verify block's tokens
         // get the bits of one-token decode steps (lossless speculation)
         MX_TRY(gdn_recurrence_fast(e.conv_out, e.cd, e.pbuf + e.cd, e.pbuf + e.cd + e.vd,
@@ -1124,8 +1148,9 @@ static int record_chunk(Engine& e, int rows) {
 
 // Prefill in chunks of up to kPrefillChunk tokens (speculative::prepare,
 // src/speculative.rs:38-68, which runs the model's forward over each chunk):
-// the projections and experts of a whole chunk on the matrix cores, each
-// weight read once per chunk instead of once per eight tokens.  The chunk's
+// the projections and experts of a whole chunk on the matrix cores (expert
+// weights read once per 16 of an expert's routes in the chunk instead of once
+// per eight tokens), the GDN layers through the chunked scan.  The chunk's
 // arithmetic is the matrix-core kernels' (fp32 sums in hardware order), so the
 // caches agree with a block-by-block exact prefill to those kernels'
 // tolerance, not bit for bit.  Eager launches (no graph).

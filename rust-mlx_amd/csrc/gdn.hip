@@ -97,6 +97,67 @@ __global__ __launch_bounds__(256) void conv_kernel(const uint16_t* __restrict__ 
     if (j < taps - 1) st[size_t(j) * channels] = f32_to_bf16(win[j]);
 }
 
+// The same causal conv for long runs of tokens without a window history (a
+// prefill chunk): the conv has no recurrence, so each thread takes one
+// channel and kConvTok consecutive tokens of one group (grid.y), reading its
+// window from the inputs (and, for the first block, from the cached window).
+// Same arithmetic as conv_kernel, bit for bit.  Block 0 of each group alone
+// reads and rewrites the cached window, so no block reads it after its update.
+constexpr int kConvTok = 16;  // >= taps - 1
+
+__global__ __launch_bounds__(256) void conv_tokens_kernel(const uint16_t* __restrict__ qkv,
+                                                          int64_t row_stride, int t,
+                                                          const int32_t* __restrict__ slots,
+                                                          uint16_t* __restrict__ conv_state,
+                                                          const float* __restrict__ w,
+                                                          int channels, int taps,
+                                                          uint16_t* __restrict__ out,
+                                                          int64_t out_stride) {
+  constexpr int kMaxTaps = 8;
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  const int t0 = blockIdx.y * kConvTok, g = blockIdx.z;
+  if (c >= channels) return;
+  uint16_t* st = conv_state + size_t(slots[g]) * (taps - 1) * channels + c;
+  const uint16_t* xg = qkv + size_t(g) * t * row_stride + c;
+  const int n = t - t0 < kConvTok ? t - t0 : kConvTok;
+  // window: inputs t0 - (taps - 1) .. t0 + n - 1 (negative: the cached window)
+  float x[kConvTok + kMaxTaps - 1];
+#pragma unroll
+  for (int j = 0; j < kConvTok + kMaxTaps - 1; ++j) {
+    const int i = t0 - (taps - 1) + j;  // input index
+    float v = 0.0f;
+    if (j < n + taps - 1) {
+      if (i >= 0)
+        v = bf16_to_f32(xg[size_t(i) * row_stride]);
+      else
+        v = bf16_to_f32(st[size_t(i + taps - 1) * channels]);
+    }
+    x[j] = v;
+  }
+  float wj[kMaxTaps];
+#pragma unroll
+  for (int j = 0; j < kMaxTaps; ++j) wj[j] = j < taps ? w[size_t(j) * channels + c] : 0.0f;
+#pragma unroll
+  for (int k = 0; k < kConvTok; ++k) {
+    if (k >= n) break;
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxTaps; ++j)
+      if (j < taps) acc = acc + x[k + j] * wj[j];
+    const float v = round_bf16(acc);
+    out[(size_t(g) * t + t0 + k) * out_stride + c] = f32_to_bf16(v * sigmoid_bf16(v));
+  }
+  if (blockIdx.y == 0) {
+    // the cached window after the last token: inputs t - (taps - 1) .. t - 1
+    for (int j = 0; j < taps - 1; ++j) {
+      const int i = t - (taps - 1) + j;
+      const float v = i >= 0 ? bf16_to_f32(xg[size_t(i) * row_stride])
+                             : x[i - t0 + taps - 1];  // an old cached value (t0 == 0)
+      st[size_t(j) * channels] = f32_to_bf16(v);
+    }
+  }
+}
+
 constexpr int kD = 128;  // head dim handled by the recurrence kernel (Dk == Dv == 128)
 
 // Inputs of the delta rule for one token: either computed from the conv
@@ -420,21 +481,34 @@ constexpr int kFastThreads = kD * kFastParts;
 // Wave 0: the key head's q and k, L2-normalised (q also scaled by
 // bf16(dk^-1/2)) at the exact step's bf16 rounding points, into LDS as
 // float4.  q0 / q1 are q[lane] / q[64 + lane], k likewise.
-__device__ __forceinline__ void fast_qk_norm(float q0, float q1, float k0, float k1, float4* qs4,
-                                             float4* ks4) {
-  const int lane = threadIdx.x & 63;
+// The fast step's L2 norms of one token's q and k (one key head, one wave:
+// lane l holds dims l and 64 + l of each): qk = {q_l, q_64+l, k_l, k_64+l},
+// bf16 values.
+__device__ __forceinline__ void fast_qk_values(float q0, float q1, float k0, float k1,
+                                               float (&qk)[4]) {
   const float eps_l2 = round_bf16(1e-6f);
   const float qscale = round_bf16(0.08838834764831845f);  // bf16(Dk^-1/2), Dk = 128
   const float qss = round_bf16(wave_sum(round_bf16(q0 * q0) + round_bf16(q1 * q1)));
   const float kss = round_bf16(wave_sum(round_bf16(k0 * k0) + round_bf16(k1 * k1)));
   const float rq = round_bf16(__builtin_amdgcn_rsqf(round_bf16(qss + eps_l2)));
   const float rk = round_bf16(__builtin_amdgcn_rsqf(round_bf16(kss + eps_l2)));
+  qk[0] = round_bf16(round_bf16(q0 * rq) * qscale);
+  qk[1] = round_bf16(round_bf16(q1 * rq) * qscale);
+  qk[2] = round_bf16(k0 * rk);
+  qk[3] = round_bf16(k1 * rk);
+}
+
+__device__ __forceinline__ void fast_qk_norm(float q0, float q1, float k0, float k1, float4* qs4,
+                                             float4* ks4) {
+  const int lane = threadIdx.x & 63;
+  float qk[4];
+  fast_qk_values(q0, q1, k0, k1, qk);
   float* qs = reinterpret_cast<float*>(qs4);
   float* ks = reinterpret_cast<float*>(ks4);
-  qs[lane] = round_bf16(round_bf16(q0 * rq) * qscale);
-  qs[64 + lane] = round_bf16(round_bf16(q1 * rq) * qscale);
-  ks[lane] = round_bf16(k0 * rk);
-  ks[64 + lane] = round_bf16(k1 * rk);
+  qs[lane] = qk[0];
+  qs[64 + lane] = qk[1];
+  ks[lane] = qk[2];
+  ks[64 + lane] = qk[3];
 }
 
 // The decay gate exp(-exp(a_log) softplus(bf16(a + dt_bias))) and beta =
@@ -568,6 +642,72 @@ __global__ __launch_bounds__(kFastThreads) void recurrence_fast_kernel(ScanArgs 
   }
 }
 
+// ---------------------------------------------------------------------------
+// A prefill chunk's fast GDN step through the chunked scan (gdn_chunk.hip).
+// Inputs per token row: normalised q / k of every key head (fast_qk_values)
+// and the decay and beta of every value head (fast_gates); the scan's output
+// then takes the gated RMS norm of the fast step.
+struct ChunkIo {
+  uint16_t* q;     // [rows][hk][kD] bf16
+  uint16_t* k;     // [rows][hk][kD] bf16
+  float* g;        // [rows][hv]
+  uint16_t* beta;  // [rows][hv] bf16
+};
+
+__host__ __device__ inline size_t chunk_io_align(size_t b) { return (b + 255) / 256 * 256; }
+
+__host__ __device__ inline ChunkIo chunk_io(void* io, int rows, int hk, int hv) {
+  char* p = static_cast<char*>(io);
+  ChunkIo c;
+  const size_t qk = chunk_io_align(size_t(rows) * hk * kD * 2);
+  c.q = reinterpret_cast<uint16_t*>(p);
+  c.k = reinterpret_cast<uint16_t*>(p + qk);
+  c.g = reinterpret_cast<float*>(p + 2 * qk);
+  c.beta = reinterpret_cast<uint16_t*>(p + 2 * qk + chunk_io_align(size_t(rows) * hv * 4));
+  return c;
+}
+
+// One workgroup per token row: wave w normalises key heads w, w + 4, ...;
+// threads below hv give the value heads' gates.
+__global__ __launch_bounds__(256) void chunk_inputs_kernel(ScanArgs p, ChunkIo io) {
+  const int row = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint16_t* cr = p.conv_out + size_t(row) * p.conv_stride;
+  for (int kh = wave; kh < p.hk_heads; kh += 4) {
+    float qk[4];
+    fast_qk_values(bf16_to_f32(cr[kh * kD + lane]), bf16_to_f32(cr[kh * kD + 64 + lane]),
+                   bf16_to_f32(cr[(p.hk_heads + kh) * kD + lane]),
+                   bf16_to_f32(cr[(p.hk_heads + kh) * kD + 64 + lane]), qk);
+    uint16_t* qo = io.q + (size_t(row) * p.hk_heads + kh) * kD;
+    uint16_t* ko = io.k + (size_t(row) * p.hk_heads + kh) * kD;
+    qo[lane] = f32_to_bf16(qk[0]);
+    qo[64 + lane] = f32_to_bf16(qk[1]);
+    ko[lane] = f32_to_bf16(qk[2]);
+    ko[64 + lane] = f32_to_bf16(qk[3]);
+  }
+  for (int hv = threadIdx.x; hv < p.hv_heads; hv += 256) {
+    float beta, gdecay;
+    fast_gates(p, hv, row, beta, gdecay);
+    io.g[size_t(row) * p.hv_heads + hv] = gdecay;
+    io.beta[size_t(row) * p.hv_heads + hv] = f32_to_bf16(beta);
+  }
+}
+
+// Gated RMS norm of the scan's output, in place: one wave per (value head,
+// row), lane l holding values l and 64 + l.
+__global__ __launch_bounds__(64) void chunk_norm_kernel(ScanArgs p) {
+  const int hv = blockIdx.x, row = blockIdx.y, lane = threadIdx.x;
+  uint16_t* yr = p.y + (size_t(row) * p.hv_heads + hv) * kD;
+  const float y0 = bf16_to_f32(yr[lane]), y1 = bf16_to_f32(yr[64 + lane]);
+  const float tot = wave_sum(y0 * y0 + y1 * y1);
+  const float inv = __builtin_amdgcn_rsqf(tot * (1.0f / kD) + p.eps);
+  const uint16_t* zr = p.z + size_t(row) * p.zab_stride + hv * kD;
+  const float o0 = round_bf16(bf16_to_f32(p.norm_w[lane]) * round_bf16(y0 * inv));
+  const float o1 = round_bf16(bf16_to_f32(p.norm_w[64 + lane]) * round_bf16(y1 * inv));
+  yr[lane] = f32_to_bf16(o0 * sigmoid_fast(bf16_to_f32(zr[lane])));
+  yr[64 + lane] = f32_to_bf16(o1 * sigmoid_fast(bf16_to_f32(zr[64 + lane])));
+}
+
 }  // namespace
 
 int gdn_recurrence_fast(const uint16_t* conv_out, int64_t conv_stride, const uint16_t* z,
@@ -592,10 +732,46 @@ int gdn_recurrence_fast(const uint16_t* conv_out, int64_t conv_stride, const uin
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 
+size_t gdn_chunk_io_bytes(int rows, GdnDims d) {
+  return 2 * chunk_io_align(size_t(rows) * d.hk * kD * 2) +
+         chunk_io_align(size_t(rows) * d.hv * 4) + chunk_io_align(size_t(rows) * d.hv * 2);
+}
+
+int gdn_chunk_fast(const uint16_t* conv_out, int64_t conv_stride, const uint16_t* z,
+                   const uint16_t* a, const uint16_t* b, int64_t zab_stride, const float* a_log,
+                   const uint16_t* dt_bias, const uint16_t* norm_w, float eps, GdnDims d,
+                   int groups, int t, const int32_t* slots, float* state, uint16_t* y, void* io,
+                   float* workspace, hipStream_t s) {
+  if (d.dk != kD || d.dv != kD || d.hk <= 0 || d.hv % d.hk != 0) return MX_EUNSUPPORTED;
+  if (groups <= 0) return MX_OK;
+  if (t < 1) return MX_EINVAL;
+  const int rows = groups * t;
+  ScanArgs p{};
+  p.conv_out = conv_out; p.conv_stride = conv_stride; p.z = z; p.a = a; p.b = b;
+  p.zab_stride = zab_stride; p.a_log = a_log; p.dt_bias = dt_bias; p.norm_w = norm_w; p.eps = eps;
+  p.hk_heads = d.hk; p.hv_heads = d.hv; p.t = t; p.slots = slots; p.state = state; p.y = y;
+  const ChunkIo c = chunk_io(io, rows, d.hk, d.hv);
+  hipLaunchKernelGGL(chunk_inputs_kernel, dim3(rows), dim3(256), 0, s, p, c);
+  // v: the conv output's value channels, row stride conv_stride
+  if (int rc = gdn_prefill_chunked(c.q, c.k, conv_out + 2 * d.hk * kD, c.g, c.beta, d, groups, t,
+                                   slots, state, y, workspace, s, conv_stride);
+      rc != MX_OK)
+    return rc;
+  hipLaunchKernelGGL(chunk_norm_kernel, dim3(d.hv, rows), dim3(64), 0, s, p);
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
 int gdn_conv(const uint16_t* qkv, int64_t row_stride, int groups, int t, const int32_t* slots,
              uint16_t* conv_state, const float* conv_w, int channels, int conv_k, uint16_t* out,
              int64_t out_stride, uint16_t* window_history, hipStream_t s) {
   if (conv_k < 2 || conv_k > 8) return MX_EUNSUPPORTED;
+  if (groups <= 0) return MX_OK;
+  if (!window_history && t > kConvTok) {  // long runs: tokens spread over workgroups
+    const dim3 grid((channels + 255) / 256, (t + kConvTok - 1) / kConvTok, groups);
+    hipLaunchKernelGGL(conv_tokens_kernel, grid, dim3(256), 0, s, qkv, row_stride, t, slots,
+                       conv_state, conv_w, channels, conv_k, out, out_stride);
+    return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+  }
   const dim3 grid((channels + 255) / 256, groups);
   hipLaunchKernelGGL(conv_kernel, grid, dim3(256), 0, s, qkv, row_stride, t, slots, conv_state,
                      conv_w, channels, conv_k, out, out_stride, window_history);

@@ -73,7 +73,7 @@ __device__ __forceinline__ void store16(float* Z, int ldz, floatx4_t v, float sc
 __global__ __launch_bounds__(256) void chunk_prep_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const float* __restrict__ g,
-    const uint16_t* __restrict__ beta, int hk, int hv, int t, int nchunks,
+    const uint16_t* __restrict__ beta, int hk, int hv, int t, int nchunks, int64_t v_stride,
     float* __restrict__ ws) {
   __shared__ double Ls[kC];            // inclusive prefix sum of log2 g
   __shared__ float bs[kC];             // beta
@@ -97,7 +97,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
     const bool ok = r < len;
     const size_t rr = row0 + (ok ? r : 0);
     uint4 kv = *reinterpret_cast<const uint4*>(k + (rr * hk + kh) * kD + cu * 8);
-    uint4 vv = *reinterpret_cast<const uint4*>(v + (rr * hv + h) * kD + cu * 8);
+    uint4 vv = *reinterpret_cast<const uint4*>(v + rr * v_stride + h * kD + cu * 8);
     if (!ok) kv = vv = make_uint4(0u, 0u, 0u, 0u);
     *reinterpret_cast<uint4*>(Ks + r * kD + cu * 8) = kv;
     *reinterpret_cast<uint4*>(Vs + r * kD + cu * 8) = vv;
@@ -361,12 +361,14 @@ size_t gdn_chunk_workspace_bytes(int groups, int hv, int t) {
 
 int gdn_prefill_chunked(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
                         const uint16_t* beta, GdnDims d, int groups, int t, const int32_t* slots,
-                        float* state, uint16_t* y, float* workspace, hipStream_t s) {
+                        float* state, uint16_t* y, float* workspace, hipStream_t s,
+                        int64_t v_stride) {
   if (d.dk != kD || d.dv != kD || d.hk <= 0 || d.hv % d.hk != 0) return MX_EUNSUPPORTED;
   if (groups <= 0 || t <= 0) return MX_OK;
   const int nchunks = (t + kC - 1) / kC;
+  if (v_stride <= 0) v_stride = int64_t(d.hv) * kD;
   hipLaunchKernelGGL(chunk_prep_kernel, dim3(nchunks, d.hv, groups), dim3(256), 0, s, q, k, v, g,
-                     beta, d.hk, d.hv, t, nchunks, workspace);
+                     beta, d.hk, d.hv, t, nchunks, v_stride, workspace);
   hipLaunchKernelGGL(chunk_scan_kernel, dim3(kD / kSlice, d.hv, groups), dim3(256), 0, s,
                      workspace, d.hv, t, nchunks, slots, state, y);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;

@@ -70,13 +70,18 @@ struct ProjEpilogue {
   // projections over both four-row blocks) with xcd_groups tiles
   int xcd_blocks = 0;
   int xcd_groups = 0;
+  // prefill GEMM (more than 16 rows): fp32 workspace for partial sums when k
+  // is split across workgroups (null: no split)
+  float* part = nullptr;
+  size_t part_floats = 0;
 };
 constexpr int kConvMaxTaps = 4;
 int proj(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const ProjEpilogue& e,
          hipStream_t s);
-// rows of one prefill chunk (the chunk of speculative::prepare,
-// src/speculative.rs:38-68)
-constexpr int kPrefillChunk = 128;
+// rows of one prefill chunk (speculative::prepare's chunks,
+// src/speculative.rs:38-68; the reference passes 128, and twice that halves
+// the expert weights streamed per prompt token)
+constexpr int kPrefillChunk = 256;
 // matrix-core (MFMA) projections, 1..kQmmMaxRows rows, group size 64 (qmm.hip)
 constexpr int kQmmMaxRows = kPrefillChunk;
 bool qmm_supported(const QWeight& w);
@@ -307,11 +312,23 @@ int gemv_bf16(const uint16_t* w, int n, int k, const uint16_t* x, int rows, uint
               hipStream_t s);
 // chunked prefill form of gdn_scan (gdn_chunk.hip): same inputs and outputs,
 // fp32 matrix-core products over 64-token chunks; workspace from
-// gdn_chunk_workspace_bytes.
+// gdn_chunk_workspace_bytes.  v_stride: elements between token rows of v
+// (0: hv * dv, dense).
 size_t gdn_chunk_workspace_bytes(int groups, int hv, int t);
 int gdn_prefill_chunked(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
                         const uint16_t* beta, GdnDims d, int groups, int t, const int32_t* slots,
-                        float* state, uint16_t* y, float* workspace, hipStream_t s);
+                        float* state, uint16_t* y, float* workspace, hipStream_t s,
+                        int64_t v_stride = 0);
+// The fast GDN step of a prefill chunk (t tokens of each group) through the
+// chunked scan: normalised q / k, decay and beta per token (the fast step's
+// arithmetic) into `io`, gdn_prefill_chunked, then the gated RMS norm into y.
+// io: gdn_chunk_io_bytes(rows, d) bytes; workspace as gdn_prefill_chunked.
+size_t gdn_chunk_io_bytes(int rows, GdnDims d);
+int gdn_chunk_fast(const uint16_t* conv_out, int64_t conv_stride, const uint16_t* z,
+                   const uint16_t* a, const uint16_t* b, int64_t zab_stride, const float* a_log,
+                   const uint16_t* dt_bias, const uint16_t* norm_w, float eps, GdnDims d,
+                   int groups, int t, const int32_t* slots, float* state, uint16_t* y, void* io,
+                   float* workspace, hipStream_t s);
 
 // ---- engine (engine.cpp) ----
 struct Engine;

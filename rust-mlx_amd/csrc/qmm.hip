@@ -175,6 +175,207 @@ void dense_bits(const QWeight& w, const uint16_t* x, int64_t xs, int m, const Pr
 }
 
 // ---------------------------------------------------------------------------
+// Prefill GEMM (more than 16 activation rows): a workgroup computes a tile of
+// 64 weight rows x 128 activation rows over the groups [g0, g1) of its k
+// slice (blockIdx.z); wave (wn, wm) of its 2 x 2 waves owns 32 weight rows
+// (two 16-row tiles) x 64 activation rows (four 16-row tiles).  The
+// activations of two groups (128 k) at a time are staged in LDS once for the
+// four waves (eight lanes per 128-byte row piece); the next two groups' loads
+// are in flight while the matrix cores work on these, and the weights of
+// the stage after are requested too.  The per-group arithmetic of qmm_tiles
+// (codes as exact bf16 integers, fp32 sums, the group's scale and bias
+// applied in registers, the group sums of x from a ones operand on the matrix
+// cores).  With a k split the workgroups write fp32 partials
+// and gemm_reduce_kernel adds them in slice order before the epilogue.
+constexpr int kGemmM = 128;          // activation rows per workgroup
+constexpr int kGemmN = 64;           // weight rows per workgroup
+constexpr int kGemmLd = 64 + 8;      // padded LDS row (bf16) of one group
+constexpr int kGemmStage = 2;        // groups staged per barrier pair
+
+// The projection epilogues of one output (activation row m, weight row `row`).
+__device__ __forceinline__ void gemm_epilogue(const ProjEpilogue& e, int n, int m, int row,
+                                              float v) {
+  if (e.mode == kPlain) {
+    e.y[size_t(m) * e.y_stride + row] = f32_to_bf16(v);
+  } else if (e.mode == kHcDown) {
+    const float tt = round_bf16(round_bf16(v) / float(e.hc));
+    if (row < e.rank)
+      e.y[size_t(m) * e.y_stride + row] = f32_to_bf16(tt * sigmoid_bf16(tt));
+    else
+      e.aux[size_t(m) * e.aux_stride + (row - e.rank)] = f32_to_bf16(sigmoid_bf16(tt) * 2.0f);
+  } else {  // kHcWrite
+    const float vb = round_bf16(v);
+    for (int s = 0; s < e.hc; ++s) {
+      uint16_t* res = e.y + size_t(m) * e.y_stride + size_t(s) * n + row;
+      const float inj = round_bf16(vb * bf16_to_f32(e.aux[size_t(m) * e.aux_stride + s]));
+      *res = f32_to_bf16(bf16_to_f32(*res) + inj);
+    }
+  }
+}
+
+template <int BITS, bool SPLIT>
+__global__ __launch_bounds__(256) void gemm_kernel(QWeight w, const uint16_t* __restrict__ x,
+                                                   int64_t x_stride, int M, int per,
+                                                   ProjEpilogue e) {
+  __shared__ __align__(16) uint16_t xs[kGemmStage][kGemmM][kGemmLd];
+  constexpr int NW = group_words<BITS>();
+  const uint4 ones = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 15, kq = lane >> 4;
+  const int wn = wave & 1, wm = wave >> 1;
+  const int n = w.n, G = w.k >> 6;
+  const int nb = blockIdx.x * kGemmN + wn * 32;  // this wave's first weight row
+  const int mb = blockIdx.y * kGemmM;            // this workgroup's first activation row
+  const int gbeg = blockIdx.z * per;
+  const int gend = min(G, gbeg + per);
+  TileRow tr[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+    tr[t] = tile_row(w.codes, w.scales, w.biases, w.k, BITS, min(nb + 16 * t + j, n - 1));
+  const float off = code_offset<BITS>();
+  // staging: piece i of thread t is 16-byte chunk (t % 8) of row t / 8 + 32 (i % 4)
+  // of the stage's group i / 4 (eight lanes per 128-byte row piece)
+  const int sc8 = tid & 7, sr0 = tid >> 3;
+  uint4 xv[8];
+  auto load_x = [&](int g0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = sr0 + 32 * (i & 3), g = g0 + (i >> 2);
+      if (mb + r < M && g < gend)
+        xv[i] = *reinterpret_cast<const uint4*>(x + size_t(mb + r) * x_stride + 64 * g + 8 * sc8);
+      else
+        xv[i] = make_uint4(0u, 0u, 0u, 0u);
+    }
+  };
+  floatx4_t y[2][4];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) y[t][u] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  // a stage's codes and raw scales / biases; weights stream from HBM, so each
+  // stage's are requested two stages ahead of their use
+  struct StageW {
+    uint32_t cw[kGemmStage][2][NW];
+    uint16_t sc[kGemmStage][2], bi[kGemmStage][2];
+  };
+  auto load_w = [&](int g0, StageW& st) {
+#pragma unroll
+    for (int s = 0; s < kGemmStage; ++s) {
+      const int g = min(g0 + s, gend - 1);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        load_group_codes<BITS>(tr[t].codes, g, kq, st.cw[s][t]);
+        st.sc[s][t] = tr[t].scales[g];
+        st.bi[s][t] = tr[t].biases[g];
+      }
+    }
+  };
+  StageW w0, w1;
+  load_w(gbeg, w0);
+  load_w(gbeg + kGemmStage, w1);
+  load_x(gbeg);
+  for (int g0 = gbeg; g0 < gend; g0 += kGemmStage) {
+    StageW w2;
+    load_w(g0 + 2 * kGemmStage, w2);  // two stages ahead (clamped to the slice)
+    const StageW& cur = w0;
+    float sc[kGemmStage][2], bi[kGemmStage][2];
+    __syncthreads();  // every wave is done with the previous stage's LDS
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = sr0 + 32 * (i & 3), gs = i >> 2;
+      *reinterpret_cast<uint4*>(&xs[gs][r][8 * sc8]) = xv[i];
+    }
+    __syncthreads();
+    if (g0 + kGemmStage < gend) load_x(g0 + kGemmStage);  // next stage, in flight
+#pragma unroll
+    for (int s = 0; s < kGemmStage; ++s)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        sc[s][t] = bf16_to_f32(cur.sc[s][t]);
+        bi[s][t] = fmaf_(-off, sc[s][t], bf16_to_f32(cur.bi[s][t]));
+      }
+#pragma unroll
+    for (int s = 0; s < kGemmStage; ++s) {
+      if (g0 + s >= gend) break;  // uniform
+      const uint4 b0[2] = {codes_operand<BITS, 0>(cur.cw[s][0]), codes_operand<BITS, 0>(cur.cw[s][1])};
+      const uint4 b1[2] = {codes_operand<BITS, 1>(cur.cw[s][0]), codes_operand<BITS, 1>(cur.cw[s][1])};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int row = wm * 64 + 16 * u + j;
+        const uint4* xp = reinterpret_cast<const uint4*>(&xs[s][row][16 * kq]);
+        const uint4 a0 = permute_x(xp[0]), a1 = permute_x(xp[1]);
+        // the rows' group sums (D rows) against a ones operand
+        floatx4_t sxr = {0.0f, 0.0f, 0.0f, 0.0f};
+        sxr = mfma_bf16(a0, ones, sxr);
+        sxr = mfma_bf16(a1, ones, sxr);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          floatx4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+          acc = mfma_bf16(a0, b0[t], acc);
+          acc = mfma_bf16(a1, b1[t], acc);
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            y[t][u][r] = fmaf_(sc[s][t], acc[r], fmaf_(bi[s][t], sxr[r], y[t][u][r]));
+        }
+      }
+    }
+    w0 = w1;
+    w1 = w2;
+  }
+  // D row = activation row, column = weight row
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int row = nb + 16 * t + j;
+    if (row >= n) continue;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = mb + wm * 64 + 16 * u + 4 * kq + r;
+        if (m >= M) continue;
+        if constexpr (SPLIT)
+          e.part[(size_t(blockIdx.z) * M + m) * n + row] = y[t][u][r];
+        else
+          gemm_epilogue(e, n, m, row, y[t][u][r]);
+      }
+  }
+}
+
+// The k slices' partial sums added in slice order, then the epilogue.
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(int n, int M, int slices,
+                                                          ProjEpilogue e) {
+  const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= size_t(M) * n) return;
+  const int m = int(i / n), row = int(i - size_t(m) * n);
+  float v = e.part[i];
+  for (int z = 1; z < slices; ++z) v = v + e.part[size_t(z) * M * n + i];
+  gemm_epilogue(e, n, m, row, v);
+}
+
+template <int BITS>
+void launch_gemm(const QWeight& w, const uint16_t* x, int64_t xs, int m, const ProjEpilogue& e,
+                 hipStream_t s) {
+  const int G = w.k >> 6;
+  const int nb = (w.n + kGemmN - 1) / kGemmN, mb = (m + kGemmM - 1) / kGemmM;
+  // split k across workgroups until the grid has about 256 workgroups, each
+  // slice at least four groups, when the workspace holds the partials
+  int slices = 1;
+  while (nb * mb * slices < 256 && G / (2 * slices) >= 4 && e.part &&
+         size_t(2 * slices) * m * w.n <= e.part_floats)
+    slices *= 2;
+  const int per = (G + slices - 1) / slices;
+  const dim3 grid(nb, mb, slices);
+  if (slices == 1) {
+    hipLaunchKernelGGL((gemm_kernel<BITS, false>), grid, dim3(256), 0, s, w, x, xs, m, per, e);
+  } else {
+    hipLaunchKernelGGL((gemm_kernel<BITS, true>), grid, dim3(256), 0, s, w, x, xs, m, per, e);
+    const size_t outs = size_t(m) * w.n;
+    hipLaunchKernelGGL(gemm_reduce_kernel, dim3(unsigned((outs + 255) / 256)), dim3(256), 0, s,
+                       w.n, m, slices, e);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Experts.  One workgroup serves one plan entry (an expert and the rows that
 // chose it) for 4/SK tile groups.  gate/up: NT = 2 (the gate tile and the up
 // tile of the same 16 rows), SwiGLU in the epilogue.  down: NT = 1, the route
@@ -287,10 +488,11 @@ __global__ __launch_bounds__(256) void expert_down_kernel(const uint16_t* __rest
 
 // ---------------------------------------------------------------------------
 // Experts of a prefill chunk over a ChunkPlan: one workgroup serves one item
-// (an expert and up to 16 of its routes) for 4/SK tile groups; the
-// arithmetic of expert_gate_up_kernel / expert_down_kernel.  Lane j (of each
-// quarter) holds member j's row and slot; the epilogue's rows 4 kq .. +3 read
-// theirs from those lanes.
+// (an expert and up to 16 of its routes) for a range of output rows, each
+// wave over the whole depth (qmm_tiles, the arithmetic of expert_gate_up_kernel
+// / expert_down_kernel without the split of k).  Lane j (of each quarter)
+// holds member j's row and slot; the epilogue's rows 4 kq .. +3 read theirs
+// from those lanes.
 struct ChunkItem {
   int m, expert;
   int row, slot;      // this lane's member (j < m; else member m - 1)
@@ -315,13 +517,16 @@ __device__ __forceinline__ ChunkItem chunk_item(const ChunkPlan* __restrict__ pl
   return it;
 }
 
-template <int BITS, int SK>
+// gate/up: wave w of the workgroup takes 32 rows of the gate and the same 32
+// rows of the up matrix (four tiles sharing the activation operands and their
+// group sums) over the whole depth, so a workgroup streams 128 rows of each
+// matrix and the item's plan is read once per 256 KB of 4-bit weights.
+template <int BITS>
 __global__ __launch_bounds__(256) void chunk_gate_up_kernel(const uint16_t* __restrict__ x,
                                                             const ChunkPlan* __restrict__ plan,
                                                             int top_k, QBank gate, QBank up,
                                                             QWeight sgate, QWeight sup,
                                                             uint16_t* __restrict__ h, int hs) {
-  __shared__ float red[(SK > 1 ? 4 * 2 * 64 * 4 : 4)];
   if (int(blockIdx.y) >= plan->nitems) return;
   const ChunkItem it = chunk_item(plan, blockIdx.y);
   const QWeight gw = expert_weight(gate, it.expert, sgate);
@@ -329,70 +534,72 @@ __global__ __launch_bounds__(256) void chunk_gate_up_kernel(const uint16_t* __re
   const int hidden = gate.k;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 15, kq = lane >> 4;
-  const int tg = blockIdx.x * (4 / SK) + wave / SK;
-  const int kp = wave % SK;
   const int inter = gw.n;
-  const int base = tg * 16;
-  const bool live = base < inter;
-  floatx4_t y[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
-  const int G = hidden >> 6;
-  if (live) {
-    const int row = min(base + j, inter - 1);
-    const TileRow tr[2] = {tile_row(gw.codes, gw.scales, gw.biases, hidden, BITS, row),
-                           tile_row(uw.codes, uw.scales, uw.biases, hidden, BITS, row)};
-    const uint16_t* xa = j < it.m ? x + size_t(it.row) * hidden : nullptr;
-    qmm_tiles<BITS, 2>(tr, xa, G * kp / SK, G * (kp + 1) / SK, y);
-  }
-  if (!reduce_split<2, SK>(y, red) || !live) return;
-  const int c = base + j;
-  if (c >= inter) return;
+  const int base = (blockIdx.x * 4 + wave) * 32;
+  if (base >= inter) return;
+  const int r0 = min(base + j, inter - 1), r1 = min(base + 16 + j, inter - 1);
+  const TileRow tr[4] = {tile_row(gw.codes, gw.scales, gw.biases, hidden, BITS, r0),
+                         tile_row(gw.codes, gw.scales, gw.biases, hidden, BITS, r1),
+                         tile_row(uw.codes, uw.scales, uw.biases, hidden, BITS, r0),
+                         tile_row(uw.codes, uw.scales, uw.biases, hidden, BITS, r1)};
+  floatx4_t y[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    if (4 * kq + r >= it.m) continue;
-    const float gv = round_bf16(y[0][r]);
-    const float uv = round_bf16(y[1][r]);
-    const float silu = round_bf16(gv * sigmoid_bf16(gv));
-    h[(size_t(it.erow[r]) * (top_k + 1) + it.eslot[r]) * hs + c] = f32_to_bf16(silu * uv);
+  for (int t = 0; t < 4; ++t) y[t] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const uint16_t* xa = j < it.m ? x + size_t(it.row) * hidden : nullptr;
+  qmm_tiles<BITS, 4>(tr, xa, 0, hidden >> 6, y);
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int c = base + 16 * t + j;
+    if (c >= inter) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if (4 * kq + r >= it.m) continue;
+      const float gv = round_bf16(y[t][r]);
+      const float uv = round_bf16(y[2 + t][r]);
+      const float silu = round_bf16(gv * sigmoid_bf16(gv));
+      h[(size_t(it.erow[r]) * (top_k + 1) + it.eslot[r]) * hs + c] = f32_to_bf16(silu * uv);
+    }
   }
 }
 
-template <int BITS, int SK>
+// down: wave w takes 64 rows (four tiles) over the whole depth; a workgroup
+// streams 256 rows of the expert's down matrix.
+template <int BITS>
 __global__ __launch_bounds__(256) void chunk_down_kernel(const uint16_t* __restrict__ h,
                                                          const ChunkPlan* __restrict__ plan,
                                                          const uint16_t* __restrict__ scores,
                                                          int top_k, QBank down, QWeight sdown,
                                                          uint16_t* __restrict__ p, int hs) {
-  __shared__ float red[(SK > 1 ? 4 * 64 * 4 : 4)];
   if (int(blockIdx.y) >= plan->nitems) return;
   const ChunkItem it = chunk_item(plan, blockIdx.y);
   const QWeight dw = expert_weight(down, it.expert, sdown);
   const int hidden = dw.n, inter = dw.k;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 15, kq = lane >> 4;
-  const int tg = blockIdx.x * (4 / SK) + wave / SK;
-  const int kp = wave % SK;
-  const int base = tg * 16;
-  const bool live = base < hidden;
-  floatx4_t y[1] = {{0.0f, 0.0f, 0.0f, 0.0f}};
-  const int G = inter >> 6;
-  if (live) {
-    const TileRow tr[1] = {tile_row(dw.codes, dw.scales, dw.biases, inter, BITS,
-                                    min(base + j, hidden - 1))};
-    const uint16_t* xa =
-        j < it.m ? h + (size_t(it.row) * (top_k + 1) + it.slot) * hs : nullptr;
-    qmm_tiles<BITS, 1>(tr, xa, G * kp / SK, G * (kp + 1) / SK, y);
-  }
-  if (!reduce_split<1, SK>(y, red) || !live) return;
-  const int c = base + j;
-  if (c >= hidden) return;
+  const int base = (blockIdx.x * 4 + wave) * 64;
+  if (base >= hidden) return;
+  TileRow tr[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+    tr[t] = tile_row(dw.codes, dw.scales, dw.biases, inter, BITS, min(base + 16 * t + j, hidden - 1));
+  floatx4_t y[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) y[t] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const uint16_t* xa = j < it.m ? h + (size_t(it.row) * (top_k + 1) + it.slot) * hs : nullptr;
+  qmm_tiles<BITS, 4>(tr, xa, 0, inter >> 6, y);
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     if (4 * kq + r >= it.m) continue;
     const int row = it.erow[r], slot = it.eslot[r];
     const bool routed = slot < top_k;
-    const float dv = round_bf16(y[0][r]);
     const float sc = routed ? bf16_to_f32(scores[size_t(row) * top_k + slot]) : 1.0f;
-    p[(size_t(row) * (top_k + 1) + slot) * hidden + c] = f32_to_bf16(routed ? dv * sc : dv);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int c = base + 16 * t + j;
+      if (c >= hidden) continue;
+      const float dv = round_bf16(y[t][r]);
+      p[(size_t(row) * (top_k + 1) + slot) * hidden + c] = f32_to_bf16(routed ? dv * sc : dv);
+    }
   }
 }
 
@@ -408,6 +615,15 @@ int qmm(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const Proj
   if (!qmm_supported(w) || m < 1 || m > kQmmMaxRows) return MX_EUNSUPPORTED;
   if (e.mode == kHcUpMix && e.hidden * 4 != w.n) return MX_EUNSUPPORTED;
   if (e.mode == kConv) return MX_EUNSUPPORTED;
+  if (m > 16 && e.mode != kHcUpMix) {  // prefill rows: the staged GEMM
+    switch (w.bits) {
+      case 4: launch_gemm<4>(w, x, x_stride, m, e, s); break;
+      case 5: launch_gemm<5>(w, x, x_stride, m, e, s); break;
+      case 6: launch_gemm<6>(w, x, x_stride, m, e, s); break;
+      default: launch_gemm<8>(w, x, x_stride, m, e, s); break;
+    }
+    return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+  }
   switch (w.bits) {
     case 4: dense_bits<4>(w, x, x_stride, m, e, s); break;
     case 5: dense_bits<5>(w, x, x_stride, m, e, s); break;
@@ -463,39 +679,36 @@ int qmm_chunk_gate_up(const uint16_t* x, const ChunkPlan* plan, int rows, int ex
                       const QBank& gate, const QBank& up, const QWeight& sgate,
                       const QWeight& sup, uint16_t* h, hipStream_t s) {
   const int hs = gate.n > sgate.n ? gate.n : sgate.n;
-  const int SK = split_k(gate.k);
-  const int tiles = (hs + 15) / 16;
-  const dim3 grid((tiles + 4 / SK - 1) / (4 / SK), chunk_max_items(rows, experts, top_k));
-#define MX_GU(B, K)                                                                        \
-  if (gate.bits == B && SK == K) {                                                         \
-    hipLaunchKernelGGL((chunk_gate_up_kernel<B, K>), grid, dim3(256), 0, s, x, plan, top_k, \
-                       gate, up, sgate, sup, h, hs);                                       \
-    return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;                             \
-  }
-  MX_GU(4, 4) MX_GU(4, 2) MX_GU(4, 1) MX_GU(5, 4) MX_GU(5, 2) MX_GU(5, 1)
-  MX_GU(6, 4) MX_GU(6, 2) MX_GU(6, 1) MX_GU(8, 4) MX_GU(8, 2) MX_GU(8, 1)
+  const dim3 grid((hs + 127) / 128, chunk_max_items(rows, experts, top_k));
+  switch (gate.bits) {
+#define MX_GU(B)                                                                          \
+  case B:                                                                                 \
+    hipLaunchKernelGGL((chunk_gate_up_kernel<B>), grid, dim3(256), 0, s, x, plan, top_k,  \
+                       gate, up, sgate, sup, h, hs);                                      \
+    break;
+    MX_GU(4) MX_GU(5) MX_GU(6) MX_GU(8)
 #undef MX_GU
-  return MX_EUNSUPPORTED;
+    default: return MX_EUNSUPPORTED;
+  }
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 
 int qmm_chunk_down(const uint16_t* h, const ChunkPlan* plan, const uint16_t* scores, int rows,
                    int experts, int top_k, int inter, int shared_inter, const QBank& down,
                    const QWeight& sdown, uint16_t* p, hipStream_t s) {
   const int hs = inter > shared_inter ? inter : shared_inter;
-  const int kmin = down.k < sdown.k ? down.k : sdown.k;
-  const int SK = split_k(kmin);
-  const int tiles = (down.n + 15) / 16;
-  const dim3 grid((tiles + 4 / SK - 1) / (4 / SK), chunk_max_items(rows, experts, top_k));
-#define MX_DN(B, K)                                                                          \
-  if (down.bits == B && SK == K) {                                                           \
-    hipLaunchKernelGGL((chunk_down_kernel<B, K>), grid, dim3(256), 0, s, h, plan, scores,    \
-                       top_k, down, sdown, p, hs);                                           \
-    return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;                               \
-  }
-  MX_DN(4, 4) MX_DN(4, 2) MX_DN(4, 1) MX_DN(5, 4) MX_DN(5, 2) MX_DN(5, 1)
-  MX_DN(6, 4) MX_DN(6, 2) MX_DN(6, 1) MX_DN(8, 4) MX_DN(8, 2) MX_DN(8, 1)
+  const dim3 grid((down.n + 255) / 256, chunk_max_items(rows, experts, top_k));
+  switch (down.bits) {
+#define MX_DN(B)                                                                             \
+  case B:                                                                                    \
+    hipLaunchKernelGGL((chunk_down_kernel<B>), grid, dim3(256), 0, s, h, plan, scores, top_k, \
+                       down, sdown, p, hs);                                                  \
+    break;
+    MX_DN(4) MX_DN(5) MX_DN(6) MX_DN(8)
 #undef MX_DN
-  return MX_EUNSUPPORTED;
+    default: return MX_EUNSUPPORTED;
+  }
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 
 }  // namespace mx

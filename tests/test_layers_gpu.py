@@ -170,6 +170,27 @@ def test_gdn_conv_bit_exact(mx, orc, groups, t):
     assert (hist.numpy() == hist_w).all()
 
 
+@pytest.mark.parametrize("groups,t,K", [(1, 256, 4), (2, 100, 4), (1, 17, 8), (1, 40, 2)])
+def test_gdn_conv_long_runs_bit_exact(mx, orc, groups, t, K):
+    """Runs longer than 16 tokens without a window history (prefill chunks)
+    spread their tokens over workgroups; same bits as the oracle's sequential
+    conv, cached window included."""
+    C_, S = 8192, 6
+    rng = np.random.default_rng(groups * 1000 + t + K)
+    stride = C_ + 32
+    qkv = orc.f32_to_bf16(rng.standard_normal((groups * t, stride)).astype(np.float32))
+    state = orc.f32_to_bf16(rng.standard_normal((S, K - 1, C_)).astype(np.float32))
+    w = (rng.standard_normal((K, C_)) * 0.4).astype(np.float32)
+    slots = rng.choice(S, groups, replace=False).astype(np.int32)
+    out_w, st_w, _ = orc.gdn_conv(np.ascontiguousarray(qkv[:, :C_]), groups, t, slots, state, w)
+    dq, dst, dw, ds = dev(mx, qkv), dev(mx, state), dev(mx, w), dev(mx, slots)
+    out = mx.DeviceArray((groups * t, C_), np.uint16)
+    mx.check(mx.lib.mx_gdn_conv(dq.ptr, stride, groups, t, ds.ptr, dst.ptr, dw.ptr, C_, K, out.ptr,
+                                C_, None, None))
+    assert (out.numpy() == out_w).all()
+    assert (dst.numpy() == st_w).all()
+
+
 def _gdn_inputs(orc, rows, hk, hv, seed):
     rng = np.random.default_rng(seed)
     conv = orc.f32_to_bf16(rng.standard_normal((rows, 2 * hk * 128 + hv * 128)).astype(np.float32))

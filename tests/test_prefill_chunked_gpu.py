@@ -1,4 +1,4 @@
-"""Chunked prefill (mx_engine_prefill_chunked: 128-token chunks whose
+"""Chunked prefill (mx_engine_prefill_chunked: 256-token chunks whose
 projections and experts run as 16-row matrix-core tiles) against the
 block prefill (mx_engine_prefill, eight tokens per step).
 
@@ -71,8 +71,9 @@ def test_short_chunk_equals_matrix_core_block(tiny, n):
 
 @pytest.mark.parametrize("n", [300, 128, 9])
 def test_chunked_prefill_within_tolerance_of_block_prefill(tiny, n):
-    """n = 300: two full chunks and one of 44 tokens; 128: exactly one chunk;
-    9: the smallest chunk beyond the eight-row kernels."""
+    """n = 300: a full chunk and one of 44 tokens; 128: one chunk with a
+    partial 16-row tile of the expert lists; 9: the smallest chunk beyond the
+    eight-row kernels."""
     eng, cfg = tiny
     prompt = np.random.default_rng(100 + n).integers(0, cfg["vocab"], n)
     ex = prefill(eng, 0, prompt, exact=True, chunked=False)

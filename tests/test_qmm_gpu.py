@@ -21,7 +21,7 @@ def test_qmm_against_closed_form_and_exact(mx, orc, bits, k, n):
     seed = 7000 + bits * 100 + k // 64
     w = mx.QWeight.random(n, k, bits, gs, seed)
     codes, s, b = orc.random_qweight(n, k, bits, gs, seed)
-    for m in (1, 3, 8, 16, 40, 128):  # beyond 16: blocks of 16 rows (a prefill chunk)
+    for m in (1, 3, 8, 16, 40, 200):  # beyond 16: the staged prefill GEMM
         x = orc.fill_bf16(m * k, seed + m, 1, 1.0, 0.0).reshape(m, k)
         dx = mx.DeviceArray.from_numpy(x)
         dy = mx.DeviceArray((m, n), np.uint16)
