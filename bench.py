@@ -736,7 +736,9 @@ def moe_cpu_baseline(gate, up, down, sg, su, sd, router, xs, first):
 def bench_mtp_config4(mx, args):
     """Config 4: MTP speculative generation on the config-3 model with per-layer
     widths {4,5,6,8} from the seeded schedule and one draft layer: batch 1, a
-    4096-token prompt, 256 generated tokens, draft depth 3 (4-token verify
+    4096-token prompt (prefilled in 256-token matrix-core chunks, the draft
+    layer's prompt pass too; --block-prefill: exact eight-token blocks), 256
+    generated tokens, draft depth 3 (4-token verify
     blocks, greedy acceptance, state and KV rollback).  Timed against plain
     greedy decoding (depth 0) of the same prompt; each figure is the generate
     call minus the same call stopped after its first token (prompt and drafter
@@ -748,7 +750,7 @@ def bench_mtp_config4(mx, args):
                max_context=ctx + n_tok + 64)
     eng = mx.Engine(cfg)
     exact = not args.fast
-    eng.set_flags(exact=exact, eager=args.eager)
+    eng.set_flags(exact=exact, eager=args.eager, chunked_generate=not args.block_prefill)
     prompt = np.random.default_rng(4004).integers(0, cfg["vocab"], ctx)
     res = {}
     for d in (0, depth):
@@ -804,6 +806,8 @@ def bench_mtp_config4(mx, args):
                    "draft_step_bytes_gb": round(draft_b / 1e9, 4),
                    "round_bytes_gb": round(round_bytes / 1e9, 4),
                    "greedy_decode_tok_s": round(n_tok / dt0, 2), "prompt_s": round(t_first, 2),
+                   "prompt_prefill": "exact 8-token blocks" if args.block_prefill
+                                     else "256-token chunks",
                    "tokens_equal_greedy": True, "mode": "exact" if exact else "fast"},
         "roofline": {"bound": "hbm",
                      "kernel": f"whole verify round, graph-replayed: one {depth + 1}-token verify "
@@ -1058,7 +1062,7 @@ def main() -> None:
                          "prefilling them (profiling runs: the decode step's cost depends on "
                          "the context length only)")
     ap.add_argument("--block-prefill", action="store_true",
-                    help="config3: prefill the contexts in exact eight-token blocks "
+                    help="config3 / mtp-config4: prefill the contexts (prompt) in exact eight-token blocks "
                          "(mx_engine_prefill) instead of 256-token matrix-core chunks "
                          "(mx_engine_prefill_chunked)")
     ap.add_argument("--fast", action="store_true",

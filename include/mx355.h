@@ -523,10 +523,11 @@ mx_status mx_engine_prefill(mx_engine* e, int32_t slot, const uint32_t* tokens, 
 /* mx_engine_prefill_chunked: the same contract in chunks of up to 256 tokens
  * (speculative::prepare's loop, src/speculative.rs:38-68, one model forward
  * per chunk; the reference calls it with 128, twice the chunk here halves the
- * expert weights read per token).  A chunk's
- * projections and experts run as 16-row matrix-core tiles over all of its
- * rows (each weight read once per chunk), its attention is causal over the
- * chunk, and its GDN layers scan its tokens in order; *next comes from the
+ * expert weights read per token).  A chunk's projections run as a
+ * matrix-core GEMM over all of its rows, its routes grouped by expert into
+ * 16-route tiles (each expert's weights read once per 16 of its routes), its
+ * attention is causal over the chunk, and its GDN layers take the chunked
+ * scan (64-token sub-chunks on the fp32 matrix cores); *next comes from the
  * last row's logits.  The matrix-core arithmetic agrees with
  * mx_engine_prefill's exact kernels to fp32 summation order, not bit for bit
  * (whatever mx_engine_set_flags chose for decode steps).  A failure marks the
@@ -549,7 +550,9 @@ mx_status mx_engine_commit(mx_engine* e, int32_t slot, int32_t keep);
  * (src/mtp.rs:72-127), default policies (full-vocabulary greedy draft head,
  * fixed depth, no EOS).  drafts (optional, max_tokens * depth entries): every
  * round's drafted tokens in order (stats->drafted of them), like the
- * reference's recorded draft tokens. */
+ * reference's recorded draft tokens.  With flag bit 10 (mx_engine_set_flags)
+ * the prompt is prefilled as mx_engine_prefill_chunked does, the draft
+ * layer's pass over the prompt running chunk by chunk on the same kernels. */
 mx_status mx_engine_generate(mx_engine* e, int32_t slot, const uint32_t* prompt,
                              int32_t n_prompt, int32_t max_tokens, int32_t depth,
                              uint32_t* tokens, int32_t* n_tokens, mx_generate_stats* stats,
@@ -561,7 +564,8 @@ mx_status mx_engine_generate(mx_engine* e, int32_t slot, const uint32_t* prompt,
  * diagnostic mask of the components that run exact while the rest stays on
  * the matrix cores: 3 hyper-connections, 4 GDN projections, 5 GDN
  * recurrence, 6 attention projections, 7 attention core, 8 router + routing
- * + experts, 9 vocabulary head), and reads of
+ * + experts, 9 vocabulary head); bit 10: mx_engine_generate prefills its
+ * prompt in matrix-core chunks), and reads of
  * the last step's "hidden" (bf16 [rows, hc*hidden]) / "logits" (bf16
  * [rows, vocab]) or of any named weight/cache tensor into host memory. */
 mx_status mx_engine_set_flags(mx_engine* e, int32_t flags);

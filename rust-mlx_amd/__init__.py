@@ -701,9 +701,11 @@ class Engine:
     # components for set_flags(exact_parts=...): run exact while the rest stays fast
     EX_HC, EX_GDN_PROJ, EX_GDN, EX_ATTN_PROJ, EX_ATTN, EX_MOE, EX_HEAD = 1, 2, 4, 8, 16, 32, 64
 
-    def set_flags(self, logits=False, eager=False, exact=False, exact_parts=0):
+    def set_flags(self, logits=False, eager=False, exact=False, exact_parts=0,
+                  chunked_generate=False):
         check(lib.mx_engine_set_flags(self.h, (1 if logits else 0) | (2 if eager else 0)
-                                      | (4 if exact else 0) | (exact_parts << 3)))
+                                      | (4 if exact else 0) | (exact_parts << 3)
+                                      | (1024 if chunked_generate else 0)))
 
     def read(self, what: str, dtype, shape) -> np.ndarray:
         out = np.empty(shape, dtype)

@@ -733,7 +733,7 @@ MX_ABI mx_status mx_engine_commit(mx_engine* e, int32_t slot, int32_t keep) {
 MX_ABI mx_status mx_engine_set_flags(mx_engine* e, int32_t flags) {
   MX_CHECK(e != nullptr, MX_EINVAL, "mx_engine_set_flags: null engine");
   engine_set_flags(*e->impl, flags & 1, (flags & 2) ? 0 : 1, (flags & 4) ? 1 : 0,
-                   (flags >> 3) & 127);
+                   (flags >> 3) & 127, (flags >> 10) & 1);
   return MX_OK;
 }
 

@@ -168,6 +168,9 @@ struct Engine {
   // set while a prefill chunk is recorded: every component on the matrix-core
   // kernels, whatever `exact` says
   bool chunk = false;
+  // engine_generate prefills its prompt in chunks (and runs the draft layer's
+  // prompt pass chunk by chunk)
+  bool chunked_generate = false;
   // profiling (eager steps only): events around each layer's expert kernels
   mx_step_profile* prof = nullptr;
   double prof_routed = 0.0;  // profiled steps: routed expert bytes, summed over layers
@@ -887,8 +890,9 @@ int record_mtp(Engine& e, int rows) {
   pe.y_stride = H;
   MX_TRY(project(e, e.mtp.fc_emb, e.mtp_a, H, rows, pe, kExAttnProj));
   MX_TRY(hc_norm(e.mtp_prev, e.mtp.norm_hid, rows, 1, hc * H, c.rms_eps, e.mtp_hn, e.stream));
-  for (int r0 = 0; r0 < rows * hc; r0 += 8) {
-    const int n = rows * hc - r0 < 8 ? rows * hc - r0 : 8;
+  const int piece = e.chunk ? kQmmMaxRows : 8;  // stream rows per projection
+  for (int r0 = 0; r0 < rows * hc; r0 += piece) {
+    const int n = rows * hc - r0 < piece ? rows * hc - r0 : piece;
     ProjEpilogue ph{};
     ph.mode = kPlain;
     ph.y = e.mtp_f + size_t(r0) * H;
@@ -898,11 +902,15 @@ int record_mtp(Engine& e, int rows) {
   MX_TRY(mtp_combine(e.mtp_e, e.mtp_f, rows, hc, H, e.h, e.stream));
   MX_TRY(record_layer(e, e.mtp.layer, rows, 1, rows, false));
   MX_TRY(hc_forward(e, e.mtp.mixer, rows, e.mixed, nullptr));
-  return record_head(e, rows, false);
+  // a prompt chunk's pass needs only its last row's draft (into entry 0)
+  return rows > 8 ? record_head(e, 1, false, rows - 1) : record_head(e, rows, false);
 }
 
 // One eager MTP pass over `rows` rows of `slot` at MTP positions pos0 + r.
-int mtp_step(Engine& e, int slot, const uint32_t* tokens, int rows, int pos0, uint32_t* next) {
+// chunk: a prompt chunk's pass on the matrix-core kernels (rows up to
+// kPrefillChunk); beyond eight rows only next[rows - 1] is written.
+int mtp_step(Engine& e, int slot, const uint32_t* tokens, int rows, int pos0, uint32_t* next,
+             bool chunk = false) {
   for (int r = 0; r < rows; ++r) {
     e.host_rows->tokens[r] = tokens[r];
     e.host_rows->slots[r] = slot;
@@ -911,11 +919,18 @@ int mtp_step(Engine& e, int slot, const uint32_t* tokens, int rows, int pos0, ui
   }
   MX_HIP(hipMemcpyAsync(e.dev_rows, e.host_rows, sizeof(Engine::RowTable), hipMemcpyHostToDevice,
                         e.stream));
-  MX_TRY(record_mtp(e, rows));
-  MX_HIP(hipMemcpyAsync(e.host_rows->next, e.dev_rows->next, sizeof(uint32_t) * rows,
+  e.chunk = chunk;
+  const int rc = record_mtp(e, rows);
+  e.chunk = false;
+  MX_TRY(rc);
+  const int got = rows > 8 ? 1 : rows;
+  MX_HIP(hipMemcpyAsync(e.host_rows->next, e.dev_rows->next, sizeof(uint32_t) * got,
                         hipMemcpyDeviceToHost, e.stream));
   MX_HIP(hipStreamSynchronize(e.stream));
-  std::memcpy(next, e.host_rows->next, sizeof(uint32_t) * rows);
+  if (rows > 8)
+    next[rows - 1] = e.host_rows->next[0];
+  else
+    std::memcpy(next, e.host_rows->next, sizeof(uint32_t) * rows);
   return MX_OK;
 }
 
@@ -1298,19 +1313,26 @@ int engine_generate(Engine& e, int slot, const uint32_t* prompt, int n_prompt, i
   }
   const size_t HS = size_t(c.hc) * c.hidden;
   mx_generate_stats st{};
-  uint32_t nxt[8], drafts[8], toks[8];
+  uint32_t nxt[8], drafts[kPrefillChunk], toks[kPrefillChunk];
   uint32_t bonus = 0, seed = 0;
-  // prefill in blocks of 8; with a draft layer, each block's MTP pass follows
-  // it (MTP position i reads token i + 1 and the target's hidden state at i;
-  // the last position reads the target's first greedy token)
-  for (int a = 0; a < n_prompt; a += 8) {
-    const int cnt = n_prompt - a < 8 ? n_prompt - a : 8;
-    MX_TRY(engine_block(e, slot, prompt + a, cnt, false, nxt, err));
-    bonus = nxt[cnt - 1];
+  // prefill in blocks of 8 (or matrix-core chunks); with a draft layer, each
+  // block's MTP pass follows it (MTP position i reads token i + 1 and the
+  // target's hidden state at i; the last position reads the target's first
+  // greedy token)
+  const bool chunked = e.chunked_generate;
+  const int block = chunked ? kPrefillChunk : 8;
+  for (int a = 0; a < n_prompt; a += block) {
+    const int cnt = n_prompt - a < block ? n_prompt - a : block;
+    if (chunked) {
+      MX_TRY(engine_prefill_chunked(e, slot, prompt + a, cnt, &bonus, err));
+    } else {
+      MX_TRY(engine_block(e, slot, prompt + a, cnt, false, nxt, err));
+      bonus = nxt[cnt - 1];
+    }
     if (depth > 0) {
       MX_HIP(hipMemcpyAsync(e.mtp_prev, e.h, cnt * HS * 2, hipMemcpyDeviceToDevice, e.stream));
       for (int r = 0; r < cnt; ++r) toks[r] = a + r + 1 < n_prompt ? prompt[a + r + 1] : bonus;
-      MX_TRY(mtp_step(e, slot, toks, cnt, a, drafts));
+      MX_TRY(mtp_step(e, slot, toks, cnt, a, drafts, chunked));
       seed = drafts[cnt - 1];
       MX_HIP(hipMemcpyAsync(e.mtp_dh, e.h + (cnt - 1) * HS, HS * 2, hipMemcpyDeviceToDevice,
                             e.stream));
@@ -1643,8 +1665,10 @@ int engine_tensor(Engine& e, const char* name, void** ptr, size_t* bytes) {
   return MX_OK;
 }
 
-void engine_set_flags(Engine& e, int want_logits, int use_graphs, int exact, int exact_parts) {
+void engine_set_flags(Engine& e, int want_logits, int use_graphs, int exact, int exact_parts,
+                      int chunked_generate) {
   e.want_logits = want_logits != 0;
+  e.chunked_generate = chunked_generate != 0;
   e.use_graphs = use_graphs != 0;
   if (e.exact != (exact != 0) || e.exact_parts != exact_parts) {
     // captured graphs bake in the kernel choice

@@ -381,7 +381,8 @@ int engine_profile_step(Engine& e, const int32_t* slots, const uint32_t* tokens,
 int engine_profile_verify(Engine& e, int slot, const uint32_t* tokens, int count, uint32_t* next,
                           mx_step_profile* out, std::string* err);
 int engine_draft_bytes(const Engine& e, int pos, double* bytes, std::string* err);
-void engine_set_flags(Engine& e, int want_logits, int use_graphs, int exact, int exact_parts);
+void engine_set_flags(Engine& e, int want_logits, int use_graphs, int exact, int exact_parts,
+                      int chunked_generate);
 const mx_model_config& engine_config(const Engine& e);
 int engine_gdn_layers(const Engine& e);
 int engine_attn_layers(const Engine& e);

@@ -121,3 +121,36 @@ def test_chunked_prefill_then_exact_decode_and_rejections(mx, tiny):
         eng.prefill(3, too_long, chunked=True)
     assert eng.offset(3) == 151
     assert eng.slot_failed(3) == 0
+
+
+def test_generate_with_chunked_prompt_and_drafter_pass(mx):
+    """mx_engine_generate with flag bit 10: the prompt is prefilled in chunks
+    and the draft layer's prompt pass runs chunk by chunk.  Speculation stays
+    lossless (depth 3 gives plain greedy decoding's tokens from the same
+    chunked prompt, drafts accepted now and then with a 16-token vocabulary),
+    and the draft layer's KV rows over the prompt agree with the block
+    prefill's within the block prefill's own tolerance."""
+    cfg = dict(mx.TINY, mtp=1, vocab=16, seed=6)
+    eng = mx.Engine(cfg)
+    try:
+        prompt = [int(t) for t in np.random.default_rng(6).integers(0, 16, 300)]
+        out = {}
+        for chunked in (False, True):
+            for depth in (0, 3):
+                eng.reset(0)
+                eng.set_flags(exact=True, chunked_generate=chunked)
+                toks, st = eng.generate(0, prompt, 16, depth)
+                out[chunked, depth] = (toks, st)
+            # the draft layer's K / V plane (after the model's attention layers)
+            n_gdn, n_attn, _, _ = dims(cfg)
+            shape = (cfg["max_slots"], n_attn + 1, cfg["kv_heads"], cfg["max_context"],
+                     cfg["head_dim"])
+            out[chunked, "kv"] = [bf(eng.read(name, np.uint16, shape)[0, n_attn, :, :300])
+                                  for name in ("cache.k", "cache.v")]
+        for chunked in (False, True):
+            assert np.array_equal(out[chunked, 0][0], out[chunked, 3][0]), chunked
+        print(f"chunked prompt: {out[True, 3][1]}; blocks: {out[False, 3][1]}", flush=True)
+        for g, w in zip(out[True, "kv"], out[False, "kv"]):
+            assert rel(g, w) <= 5e-2, rel(g, w)
+    finally:
+        eng.close()
