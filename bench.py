@@ -8,7 +8,7 @@ Workloads:
       MoE with a shared expert, hc = 4 hyper-connections, vocab 151936, 4-bit
       weights with 5-bit expert down and 8-bit embedding/head), 8 slots
       prefilled with seeded uniform-random prompts of ragged lengths 10..2048
-      (256-token chunks on the matrix cores; --block-prefill: the exact
+      (512-token chunks on the matrix cores; --block-prefill: the exact
       eight-token blocks), then batched greedy decode of all 8 rows per step (rows at their own
       offsets).  A step = one decode token for each of the 8 rows; W + K = 256
       steps per row by default.  value = aggregate tok/s over the K timed steps.
@@ -29,6 +29,8 @@ Workloads:
       routing, gathered expert gate/up and down, slot sum into the residual
       streams) at B = 1..8 rows; 32 rotated input batches; value = B = 8 rows
       per second, roofline = router + shared + distinct experts' bytes.
+  prefill-config3  chunked prefill of one 2048-token prompt on the config-3
+      model (512-token chunks on the matrix cores); value = prompt tokens/s.
   mtp-config4  BASELINE config 4: MTP speculative generation (depth 3) on the
       mixed-width config-3 model, batch 1, 4096-token prompt, 256 tokens, timed
       against plain greedy decoding of the same prompt.
@@ -123,7 +125,7 @@ def bench_config3(mx, args):
             nxt[s] = eng.prefill(s, prompt, chunked=not args.block_prefill)
     prefill_s = time.perf_counter() - t0
     prefill_mode = ("synthetic" if args.synthetic_context else
-                    "exact 8-token blocks" if args.block_prefill else "256-token chunks")
+                    "exact 8-token blocks" if args.block_prefill else f"{mx.PREFILL_CHUNK}-token chunks")
     log(f"config3: {'filled' if args.synthetic_context else 'prefilled'} {int(lengths.sum())} "
         f"context positions (lengths {[int(x) for x in lengths]}) in {prefill_s:.2f}s "
         f"({prefill_mode}, {lengths.sum() / prefill_s:.0f} positions/s)")
@@ -736,7 +738,7 @@ def moe_cpu_baseline(gate, up, down, sg, su, sd, router, xs, first):
 def bench_mtp_config4(mx, args):
     """Config 4: MTP speculative generation on the config-3 model with per-layer
     widths {4,5,6,8} from the seeded schedule and one draft layer: batch 1, a
-    4096-token prompt (prefilled in 256-token matrix-core chunks, the draft
+    4096-token prompt (prefilled in 512-token matrix-core chunks, the draft
     layer's prompt pass too; --block-prefill: exact eight-token blocks), 256
     generated tokens, draft depth 3 (4-token verify
     blocks, greedy acceptance, state and KV rollback).  Timed against plain
@@ -807,7 +809,7 @@ def bench_mtp_config4(mx, args):
                    "round_bytes_gb": round(round_bytes / 1e9, 4),
                    "greedy_decode_tok_s": round(n_tok / dt0, 2), "prompt_s": round(t_first, 2),
                    "prompt_prefill": "exact 8-token blocks" if args.block_prefill
-                                     else "256-token chunks",
+                                     else f"{mx.PREFILL_CHUNK}-token chunks",
                    "tokens_equal_greedy": True, "mode": "exact" if exact else "fast"},
         "roofline": {"bound": "hbm",
                      "kernel": f"whole verify round, graph-replayed: one {depth + 1}-token verify "
@@ -894,13 +896,90 @@ def bench_copy_calibration(mx, args):
             "cpu_baseline": None}
 
 
+def model_weight_bytes(eng, cfg):
+    """Bytes of every layer weight of the engine (projections, expert banks,
+    hyper-connections; not the embedding or the head)."""
+    total = 0
+    for i in range(cfg["layers"]):
+        p = f"layers.{i}"
+        mats = [".attn_hc.down", ".attn_hc.up", ".mlp_hc.down", ".mlp_hc.up", ".moe.router",
+                ".moe.gate", ".moe.up", ".moe.down", ".moe.shared_gate", ".moe.shared_up",
+                ".moe.shared_down"]
+        attn = (i % cfg["attn_every"]) == cfg["attn_every"] - 1
+        mats += [".attn.in", ".attn.out"] if attn else [".gdn.in", ".gdn.out"]
+        for m in mats:
+            for part in (".codes", ".scales", ".biases"):
+                total += eng.tensor_bytes(p + m + part)
+    return total
+
+
+def bench_prefill_config3(mx, args):
+    """Chunked prefill on the config-3 model: a step = one 2048-token prompt of
+    one slot through mx_engine_prefill_chunked (four 512-token chunks: the
+    projections as matrix-core GEMMs, routes grouped by expert, causal
+    attention over each chunk, the GDN layers through the chunked scan).
+    value = prompt tokens/s.  Roofline: a chunk of 512 tokens routes 5120
+    tokens over 512 experts, so every expert's weights stream once per chunk
+    (at least); the bound is every layer weight once per chunk at 8 TB/s.  The
+    exact eight-token block prefill (mx_engine_prefill) of 256 tokens is timed
+    beside it."""
+    cfg = dict(mx.CONFIG3, max_slots=2, max_context=2048 + 64)
+    eng = mx.Engine(cfg)
+    eng.set_flags(eager=args.eager)
+    rng = np.random.default_rng(5005)
+    t = 2048
+    prompt = rng.integers(0, cfg["vocab"], t)
+    for _ in range(max(args.warmup, 1)):
+        eng.reset(0)
+        eng.prefill(0, prompt[:256], chunked=True)
+    mx.check(mx.lib.mx_device_sync())
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        eng.reset(0)
+        eng.prefill(0, prompt, chunked=True)
+    mx.check(mx.lib.mx_device_sync())
+    dt = (time.perf_counter() - t0) / args.steps
+    tok_s = t / dt
+    chunk = mx.PREFILL_CHUNK
+    chunks = (t + chunk - 1) // chunk
+    wbytes = model_weight_bytes(eng, cfg)
+    gbs = wbytes * chunks / dt / 1e9
+    block_tok_s = None
+    if not args.eager:  # profiled (eager) runs trace the chunked prefill alone
+        eng.reset(1)
+        eng.set_flags(exact=True)
+        t0 = time.perf_counter()
+        eng.prefill(1, prompt[:256])
+        block_tok_s = 256 / (time.perf_counter() - t0)
+    log(f"prefill-config3: {t} tokens in {dt * 1e3:.1f} ms -> {tok_s:.0f} tok/s "
+        f"({dt / chunks * 1e3:.2f} ms per {chunk}-token chunk; layer weights {wbytes / 1e9:.2f} GB "
+        f"once per chunk -> {gbs:.0f} GB/s)"
+        + (f"; exact 8-token blocks: {block_tok_s:.0f} tok/s" if block_tok_s else ""))
+    eng.close()
+    return {"metric": "chunked prefill tok/s (one 2048-token prompt, config-3 model)",
+            "value": round(tok_s, 1), "unit": "tok/s", "ms_per_step": dt * 1e3,
+            "dtype": "u4/u5 codes x bf16 on the bf16 matrix cores, fp32 sums",
+            "config": {"workload": "prefill-config3", "prompt": t, "chunk": chunk,
+                       "layers": cfg["layers"], "experts": cfg["experts"],
+                       "ms_per_chunk": round(dt / chunks * 1e3, 3),
+                       "block_prefill_tok_s": round(block_tok_s, 1) if block_tok_s else None},
+            "roofline": {"bound": "hbm",
+                         "kernel": f"whole chunk: every layer weight once per {chunk}-token chunk",
+                         "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                         "algorithmic_bytes_per_chunk": int(wbytes)},
+            "cpu_baseline": None}
+
+
 WORKLOADS = {"config3-b8-decode": bench_config3, "qmv-config0": bench_qmv_config0,
              "gdn-prefill-config1": bench_gdn_prefill_config1,
              "gdn-decode-config1": bench_gdn_decode_config1, "moe-config2": bench_moe_config2,
-             "mtp-config4": bench_mtp_config4, "copy-calibration": bench_copy_calibration}
+             "mtp-config4": bench_mtp_config4, "copy-calibration": bench_copy_calibration,
+             "prefill-config3": bench_prefill_config3}
 DEFAULTS = {"config3-b8-decode": (240, 16), "qmv-config0": (2000, 200),
             "gdn-prefill-config1": (50, 5), "gdn-decode-config1": (200, 20),
-            "moe-config2": (200, 20), "mtp-config4": (1, 0), "copy-calibration": (10, 2)}
+            "moe-config2": (200, 20), "mtp-config4": (1, 0), "copy-calibration": (10, 2),
+            "prefill-config3": (3, 1)}
 
 
 def short_kernel_name(name: str) -> str:
@@ -1063,7 +1142,7 @@ def main() -> None:
                          "the context length only)")
     ap.add_argument("--block-prefill", action="store_true",
                     help="config3 / mtp-config4: prefill the contexts (prompt) in exact eight-token blocks "
-                         "(mx_engine_prefill) instead of 256-token matrix-core chunks "
+                         "(mx_engine_prefill) instead of 512-token matrix-core chunks "
                          "(mx_engine_prefill_chunked)")
     ap.add_argument("--fast", action="store_true",
                     help="config3: time the bf16 matrix-core kernels (within tolerance of the "

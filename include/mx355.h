@@ -148,6 +148,10 @@ typedef struct mx_expert_timing {
 /* ---- errors / version -------------------------------------------------- */
 const char* mx_last_error(void);
 int32_t mx_abi_version(void);
+/* Tokens per chunk of mx_engine_prefill_chunked (and of mx_engine_generate's
+ * chunked prompt): the most rows any matrix-core entry takes.  No reference
+ * counterpart (speculative::prepare takes the chunk as an argument). */
+int32_t mx_prefill_chunk_tokens(void);
 
 /* ---- device plumbing used by hosts and tests (no reference counterpart:
  *      MLX owns memory in the reference) ---------------------------------- */
@@ -188,7 +192,7 @@ mx_status mx_qmv(const mx_qweight* w, const uint16_t* x, int32_t m, uint16_t* y,
                  void* stream);
 
 /* ---- A3/A15: the same projection on the matrix cores --------------------
- * y = x . dequant(W)^T for 1 <= m <= 256 rows with v_mfma_f32_16x16x32_bf16
+ * y = x . dequant(W)^T for 1 <= m <= 512 rows with v_mfma_f32_16x16x32_bf16
  * (beyond 16 rows a GEMM staging 128-row blocks of x in LDS):
  * codes enter as exact bf16 integers, each 64-value group's fp32 partial is
  * scaled in registers.  Results equal mx_qmv's up to fp32 summation order
@@ -268,7 +272,7 @@ mx_status mx_moe_experts(const uint16_t* x, const uint32_t* ids, const uint16_t*
                          const mx_qweight* shared_up, const mx_qweight* shared_down,
                          void* workspace, uint16_t* partial, void* stream);
 /* mx_moe_experts on the matrix cores (same contract, fp32 summation order
- * within tolerance of the exact kernels), for 1..256 rows: beyond eight rows
+ * within tolerance of the exact kernels), for 1..512 rows: beyond eight rows
  * (a prefill chunk) the routes are grouped by expert into 16-route matrix-core
  * tiles, each expert's weights read once per 16 of its routes, and the banks
  * may hold at most 1023 experts. */
@@ -520,10 +524,11 @@ mx_status mx_engine_decode_batch_outputs(mx_engine* e, const int32_t* slots,
                                          uint16_t* logits, uint16_t* hidden);
 mx_status mx_engine_prefill(mx_engine* e, int32_t slot, const uint32_t* tokens, int32_t count,
                             uint32_t* next);
-/* mx_engine_prefill_chunked: the same contract in chunks of up to 256 tokens
- * (speculative::prepare's loop, src/speculative.rs:38-68, one model forward
- * per chunk; the reference calls it with 128, twice the chunk here halves the
- * expert weights read per token).  A chunk's projections run as a
+/* mx_engine_prefill_chunked: the same contract in chunks of up to 512 tokens
+ * (mx_prefill_chunk_tokens; speculative::prepare's loop,
+ * src/speculative.rs:38-68, one model forward per chunk: the reference calls
+ * it with 128, and a chunk four times longer reads each expert's weights once
+ * per 512 prompt tokens instead of once per 128).  A chunk's projections run as a
  * matrix-core GEMM over all of its rows, its routes grouped by expert into
  * 16-route tiles (each expert's weights read once per 16 of its routes), its
  * attention is causal over the chunk, and its GDN layers take the chunked

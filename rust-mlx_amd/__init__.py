@@ -145,6 +145,7 @@ def _load() -> C.CDLL:
     sig = {
         "mx_last_error": ([], C.c_char_p),
         "mx_abi_version": ([], i32),
+        "mx_prefill_chunk_tokens": ([], i32),
         "mx_malloc": ([C.POINTER(vp), sz], i32),
         "mx_free": ([vp], i32),
         "mx_memcpy_htod": ([vp, vp, sz], i32),
@@ -258,6 +259,8 @@ def _load() -> C.CDLL:
 
 
 lib = _load()
+# tokens per chunk of mx_engine_prefill_chunked
+PREFILL_CHUNK = int(lib.mx_prefill_chunk_tokens())
 
 
 def check(rc: int) -> None:
@@ -614,7 +617,7 @@ class Engine:
 
     def prefill(self, slot, tokens, chunked=False) -> int:
         """Feeds tokens to a slot; returns the greedy token after the last one.
-        chunked: mx_engine_prefill_chunked (256-token chunks on the matrix
+        chunked: mx_engine_prefill_chunked (512-token chunks on the matrix
         cores, within tolerance of the exact 8-token blocks)."""
         t = self._u32(tokens)
         out = np.empty(1, np.uint32)

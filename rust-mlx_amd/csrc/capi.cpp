@@ -57,6 +57,7 @@ using namespace mx;
 
 MX_ABI const char* mx_last_error(void) { return last_error(); }
 MX_ABI int32_t mx_abi_version(void) { return 1; }
+MX_ABI int32_t mx_prefill_chunk_tokens(void) { return kPrefillChunk; }
 
 MX_ABI mx_status mx_malloc(void** ptr, size_t bytes) {
   MX_CHECK(ptr != nullptr, MX_EINVAL, "mx_malloc: null out pointer");
@@ -871,7 +872,7 @@ MX_ABI mx_status mx_qmm(const mx_qweight* w, const uint16_t* x, int32_t m, uint1
   const QWeight q = to_qweight(*w);
   if (const char* err = check_qweight(q)) return mx_status(set_error(MX_EINVAL, std::string("mx_qmm: ") + err));
   MX_CHECK(qmm_supported(q), MX_EUNSUPPORTED, "mx_qmm: needs group_size 64 and k <= 8192");
-  MX_CHECK(m >= 1 && m <= kQmmMaxRows, MX_EUNSUPPORTED, "mx_qmm: m must be in 1..256");
+  MX_CHECK(m >= 1 && m <= kQmmMaxRows, MX_EUNSUPPORTED, "mx_qmm: m must be in 1..512");
   ProjEpilogue e{};
   e.mode = kPlain;
   e.y = y;
@@ -962,7 +963,7 @@ MX_ABI mx_status mx_moe_experts_mfma(const uint16_t* x, const uint32_t* ids, con
                workspace && partial,
            MX_EINVAL, "mx_moe_experts_mfma: null pointer");
   MX_CHECK(rows >= 1 && rows <= kPrefillChunk, MX_EUNSUPPORTED,
-           "mx_moe_experts_mfma: rows must be in 1..256");
+           "mx_moe_experts_mfma: rows must be in 1..512");
   MX_CHECK(top_k >= 1 && top_k <= 16, MX_EUNSUPPORTED, "mx_moe_experts_mfma: top_k must be in 1..16");
   const QBank g = to_qbank(*gate), u = to_qbank(*up), d = to_qbank(*down);
   const QWeight sg = to_qweight(*shared_gate), su = to_qweight(*shared_up), sd = to_qweight(*shared_down);

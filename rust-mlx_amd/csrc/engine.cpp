@@ -476,7 +476,8 @@ int build(Engine& e) {
     MX_TRY(alloc(e, "act.gdn_chunk_ws", gdn_chunk_workspace_bytes(1, c.gdn_hv, int(R)), &v));
     e.gdn_ws = static_cast<float*>(v);
   }
-  MX_TRY(a16("act.logits", R * size_t(c.vocab), &e.logits));
+  // bf16 logits of a decode step or verify block (at most 8 rows)
+  MX_TRY(a16("act.logits", size_t(8) * c.vocab, &e.logits));
   if (c.mtp) {
     MX_TRY(a16("mtp.act.emb", R * c.hidden, &e.mtp_emb));
     MX_TRY(a16("mtp.act.a", R * c.hidden, &e.mtp_a));

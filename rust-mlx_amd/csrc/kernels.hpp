@@ -79,9 +79,9 @@ constexpr int kConvMaxTaps = 4;
 int proj(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const ProjEpilogue& e,
          hipStream_t s);
 // rows of one prefill chunk (speculative::prepare's chunks,
-// src/speculative.rs:38-68; the reference passes 128, and twice that halves
-// the expert weights streamed per prompt token)
-constexpr int kPrefillChunk = 256;
+// src/speculative.rs:38-68; the reference passes 128: a 512-token chunk routes
+// 5120 tokens, so each expert's weights stream once per 512 prompt tokens)
+constexpr int kPrefillChunk = 512;
 // matrix-core (MFMA) projections, 1..kQmmMaxRows rows, group size 64 (qmm.hip)
 constexpr int kQmmMaxRows = kPrefillChunk;
 bool qmm_supported(const QWeight& w);
@@ -244,7 +244,7 @@ struct ChunkPlan {
   int32_t expert[kChunkRoutes];
   int32_t start[kChunkRoutes];
   int32_t m[kChunkRoutes];
-  uint8_t row[kChunkRoutes];
+  uint16_t row[kChunkRoutes];
   uint8_t slot[kChunkRoutes];
 };
 // items a chunk of `rows` rows can produce (a bound: the grids' y extent)

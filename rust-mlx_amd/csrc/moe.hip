@@ -246,11 +246,11 @@ __global__ __launch_bounds__(kChunkPlanThreads) void chunk_plan_kernel(
     int rank = __popc(mask[e][row >> 5] & ((1u << (row & 31)) - 1u));
     for (int w = 0; w < (row >> 5); ++w) rank += __popc(mask[e][w]);
     const int at = first[e] + rank;
-    plan->row[at] = uint8_t(row);
+    plan->row[at] = uint16_t(row);
     plan->slot[at] = uint8_t(r - row * top_k);
   }
   for (int row = t; row < rows; row += kChunkPlanThreads) {
-    plan->row[first[experts] + row] = uint8_t(row);
+    plan->row[first[experts] + row] = uint16_t(row);
     plan->slot[first[experts] + row] = uint8_t(top_k);
   }
 }
