@@ -1077,6 +1077,30 @@ def summarize_trace(path: str, line_path=None, kernel="xq_gate_up_kernel") -> No
           f"{sum(len(v) for _, v in hc)} launches, {hc_us / 1e3:.3f} ms per step")
 
 
+def summarize_kernels(path: str) -> None:
+    """Markdown table of a rocprofv3 kernel trace grouped by kernel and grid
+    (workgroups): launches, average and total duration.  Weight fills of
+    engine creation and runtime copies are left out."""
+    import collections
+    import csv
+
+    agg = collections.defaultdict(lambda: [0, 0.0])
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            name = r["Kernel_Name"]
+            if name.startswith("mx::(anonymous namespace)::fill") or "rocclr" in name:
+                continue
+            key = (short_kernel_name(name), int(r["Grid_Size_X"]) // int(r["Workgroup_Size_X"]),
+                   int(r["Grid_Size_Y"]), int(r["Grid_Size_Z"]))
+            agg[key][0] += 1
+            agg[key][1] += (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+    rows = sorted(agg.items(), key=lambda kv: -kv[1][1])
+    print("| kernel | workgroups (x, y, z) | launches | avg us | total ms |")
+    print("|---|---|---:|---:|---:|")
+    for (name, gx, gy, gz), (n, us) in rows:
+        print(f"| `{name}` | ({gx}, {gy}, {gz}) | {n} | {us / n:.1f} | {us / 1e3:.2f} |")
+
+
 def summarize_counters(fetch_csv: str, write_csv: str, fetch_scale: float, write_scale: float,
                        kernel="xq_gate_up_kernel") -> None:
     """Markdown table of HBM bytes per dispatch from two rocprofv3 `--pmc`
@@ -1121,6 +1145,10 @@ def main() -> None:
         # no device work: summarise two rocprofv3 counter runs of this script
         summarize_counters(sys.argv[2], sys.argv[3], float(sys.argv[4]), float(sys.argv[5]),
                            *(sys.argv[6:7]))
+        return
+    if len(sys.argv) >= 3 and sys.argv[1] == "--summarize-kernels":
+        # no device work: group a rocprofv3 kernel trace by kernel and grid
+        summarize_kernels(sys.argv[2])
         return
     if len(sys.argv) >= 3 and sys.argv[1] == "--summarize-trace":
         # no device work: summarise a rocprofv3 kernel trace of an earlier run
