@@ -1162,6 +1162,41 @@ static int record_chunk(Engine& e, int rows) {
   return record_head(e, 1, false, rows - 1);
 }
 
+// Whether every layer of the model has a matrix-core kernel for a prefill
+// chunk (checked before any launch, so an unsupported model is refused
+// without touching a slot): projections and expert banks of group size 64
+// and depth <= 8192, at most 1023 experts with a routing width the routing
+// kernel covers, top-k <= 16, 128-wide GDN heads and a conv of <= 8 taps.
+static bool chunk_supported(const Engine& e, std::string* err) {
+  const auto& c = e.cfg;
+  auto bank = [](const QBank& b) {
+    return qmm_supported(QWeight{b.codes, b.scales, b.biases, b.n, b.k, b.bits, b.group_size});
+  };
+  const int per = c.experts / 64;
+  bool ok = c.experts <= kChunkMaxExperts && c.experts % 64 == 0 &&
+            (per == 1 || per == 2 || per == 4 || per == 8 || per == 16) && c.top_k <= 16 &&
+            c.gdn_dk == 128 && c.gdn_dv == 128 && c.conv_k >= 2 && c.conv_k <= 8 &&
+            qmm_supported(e.mixer.down) && qmm_supported(e.mixer.up);
+  auto layer_ok = [&](const LayerW& L) {
+    bool r = qmm_supported(L.attn_hc.down) && qmm_supported(L.attn_hc.up) &&
+             qmm_supported(L.mlp_hc.down) && qmm_supported(L.mlp_hc.up) &&
+             qmm_supported(L.router) && bank(L.gate) && bank(L.up) && bank(L.down) &&
+             qmm_supported(L.sgate) && qmm_supported(L.sup) && qmm_supported(L.sdown);
+    return r && (L.attn ? qmm_supported(L.attn_in) && qmm_supported(L.attn_out)
+                        : qmm_supported(L.gdn_in) && qmm_supported(L.gdn_out));
+  };
+  for (const LayerW& L : e.layers) ok = ok && layer_ok(L);
+  if (e.has_mtp)
+    ok = ok && layer_ok(e.mtp.layer) && qmm_supported(e.mtp.fc_emb) &&
+         qmm_supported(e.mtp.fc_hid) && qmm_supported(e.mtp.mixer.down) &&
+         qmm_supported(e.mtp.mixer.up);
+  if (!ok)
+    *err = "the model has no matrix-core prefill kernel for some layer (group size 64, depth "
+           "<= 8192, <= 1023 experts in 64..1024 steps of powers of two, top-k <= 16, 128-wide "
+           "GDN heads needed); use mx_engine_prefill";
+  return ok;
+}
+
 // Prefill in chunks of up to kPrefillChunk tokens (speculative::prepare,
 // src/speculative.rs:38-68, which runs the model's forward over each chunk):
 // the projections and experts of a whole chunk on the matrix cores (expert
@@ -1177,6 +1212,7 @@ int engine_prefill_chunked(Engine& e, int slot, const uint32_t* tokens, int coun
     *err = "slot context is full";
     return MX_ESTATE;
   }
+  if (!chunk_supported(e, err)) return MX_EUNSUPPORTED;
   if (slot == e.verify_slot) e.verify_slot = -1;
   for (int a = 0; a < count; a += kPrefillChunk) {
     const int n = count - a < kPrefillChunk ? count - a : kPrefillChunk;

@@ -155,3 +155,22 @@ def test_generate_with_chunked_prompt_and_drafter_pass(mx):
             assert rel(g, w) <= 5e-2, rel(g, w)
     finally:
         eng.close()
+
+
+def test_chunked_prefill_refuses_unsupported_models_before_any_launch(mx):
+    """A model the chunk kernels do not cover (1024 experts: the chunk's expert
+    lists hold at most 1023) is refused with MX_EUNSUPPORTED before any
+    launch: the slot is not marked failed, its offset does not move, and the
+    block prefill still serves it."""
+    cfg = dict(mx.TINY, experts=1024, max_slots=2)
+    eng = mx.Engine(cfg)
+    try:
+        prompt = np.random.default_rng(3).integers(0, cfg["vocab"], 40)
+        with pytest.raises(mx.MxError) as exc:
+            eng.prefill(0, prompt, chunked=True)
+        assert exc.value.code == mx.MX_EUNSUPPORTED
+        assert eng.offset(0) == 0 and eng.slot_failed(0) == 0
+        eng.prefill(0, prompt)
+        assert eng.offset(0) == 40
+    finally:
+        eng.close()
