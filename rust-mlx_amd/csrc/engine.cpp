@@ -171,6 +171,10 @@ struct Engine {
   // engine_generate prefills its prompt in chunks (and runs the draft layer's
   // prompt pass chunk by chunk)
   bool chunked_generate = false;
+  // set while recording: the last MoE slot sum also normed the streams for
+  // the next hyper-connection (xn and its plane are written), whose own norm
+  // launch is then skipped
+  bool xn_ready = false;
   // profiling (eager steps only): events around each layer's expert kernels
   mx_step_profile* prof = nullptr;
   double prof_routed = 0.0;  // profiled steps: routed expert bytes, summed over layers
@@ -610,8 +614,11 @@ int hc_forward(Engine& e, const HcW& w, int rows, uint16_t* mixed_out, uint16_t*
   // exact: the norm writes the down projection's operand plane, and the
   // up-projection + mix writes the plane of `mixed` for its consumers
   const bool exact = ex(e, kExHc) && rows <= 8;
-  MX_TRY(hc_norm(e.h, w.scale, rows, c.hc, c.hidden, c.rms_eps, e.xn, e.stream,
-                 exact ? e.xn_plane : nullptr));
+  if (e.xn_ready)
+    e.xn_ready = false;  // the slot sum before normed the streams with this scale
+  else
+    MX_TRY(hc_norm(e.h, w.scale, rows, c.hc, c.hidden, c.rms_eps, e.xn, e.stream,
+                   exact ? e.xn_plane : nullptr));
   ProjEpilogue d{};
   d.mode = kHcDown;
   d.y = e.lo;
@@ -640,7 +647,10 @@ int hc_forward(Engine& e, const HcW& w, int rows, uint16_t* mixed_out, uint16_t*
 // sequences of `t` tokens.  Row metadata is read from e.dev_rows.
 // Records one layer (attention or GDN sublayer, then the MoE sublayer) on the
 // hc streams e.h of `rows` rows arranged as `groups` sequences of `t` tokens.
-int record_layer(Engine& e, const LayerW& L, int rows, int groups, int t, bool history) {
+// next_scale (nullable): the norm scale of the hyper-connection that follows
+// the layer, which the exact slot sum then applies in the same launch.
+int record_layer(Engine& e, const LayerW& L, int rows, int groups, int t, bool history,
+                 const uint16_t* next_scale = nullptr) {
   const auto& c = e.cfg;
   Engine::RowTable* rt = e.dev_rows;
   {
@@ -776,9 +786,16 @@ int record_layer(Engine& e, const LayerW& L, int rows, int groups, int t, bool h
         MX_TRY(experts_down(e, L, rows));
       }
     }
-    if (!summed)
-      MX_TRY(moe_reduce_hc_epilogue(e.moe_p, e.factor, e.h, e.inj, rows, c.top_k, c.hc,
-                                    c.hidden, e.h, e.stream));
+    if (!summed) {
+      if (next_scale && ex(e, kExHc) && moe_reduce_norm_supported(rows, c.top_k, c.hc, c.hidden)) {
+        MX_TRY(moe_reduce_norm(e.moe_p, e.factor, e.h, e.inj, rows, c.top_k, c.hc, c.hidden,
+                               next_scale, c.rms_eps, e.xn, e.xn_plane, e.stream));
+        e.xn_ready = true;
+      } else {
+        MX_TRY(moe_reduce_hc_epilogue(e.moe_p, e.factor, e.h, e.inj, rows, c.top_k, c.hc,
+                                      c.hidden, e.h, e.stream));
+      }
+    }
   }
   return MX_OK;
 }
@@ -793,8 +810,11 @@ int record_step(Engine& e, int rows, int groups, int t, bool history, bool logit
   Engine::RowTable* rt = e.dev_rows;
   MX_TRY(embed(e.embed, rt->tokens, rows, c.hc, e.h, e.stream));
   int launched = 0;
-  for (const LayerW& L : e.layers) {
-    MX_TRY(record_layer(e, L, rows, groups, t, history));
+  e.xn_ready = false;
+  for (size_t i = 0; i < e.layers.size(); ++i) {
+    const LayerW& L = e.layers[i];
+    const uint16_t* next = i + 1 < e.layers.size() ? e.layers[i + 1].attn_hc.scale : e.mixer.scale;
+    MX_TRY(record_layer(e, L, rows, groups, t, history, next));
     if (e.fail_after > 0 && ++launched == e.fail_after) {
       // the injected failure: the launched layers run, then the step stops
       // as a failed launch would
@@ -901,7 +921,8 @@ int record_mtp(Engine& e, int rows) {
     MX_TRY(project(e, e.mtp.fc_hid, e.mtp_hn + size_t(r0) * H, H, n, ph, kExAttnProj));
   }
   MX_TRY(mtp_combine(e.mtp_e, e.mtp_f, rows, hc, H, e.h, e.stream));
-  MX_TRY(record_layer(e, e.mtp.layer, rows, 1, rows, false));
+  e.xn_ready = false;
+  MX_TRY(record_layer(e, e.mtp.layer, rows, 1, rows, false, e.mtp.mixer.scale));
   MX_TRY(hc_forward(e, e.mtp.mixer, rows, e.mixed, nullptr));
   // a prompt chunk's pass needs only its last row's draft (into entry 0)
   return rows > 8 ? record_head(e, 1, false, rows - 1) : record_head(e, rows, false);
@@ -1103,6 +1124,7 @@ int engine_decode_forced(Engine& e, const int32_t* slots, const uint32_t* tokens
   const size_t HS = size_t(rows) * c.hc * c.hidden;
   MX_HIP(hipMemcpyAsync(e.dev_rows, e.host_rows, sizeof(Engine::RowTable), hipMemcpyHostToDevice,
                         e.stream));
+  e.xn_ready = false;
   for (size_t i = 0; i < e.layers.size(); ++i) {
     MX_HIP(hipMemcpyAsync(e.h, h_in + i * HS, HS * 2, hipMemcpyHostToDevice, e.stream));
     MX_TRY(record_layer(e, e.layers[i], rows, rows, 1, false));
@@ -1157,6 +1179,7 @@ int engine_block(Engine& e, int slot, const uint32_t* tokens, int count, bool hi
 static int record_chunk(Engine& e, int rows) {
   const auto& c = e.cfg;
   MX_TRY(embed(e.embed, e.dev_rows->tokens, rows, c.hc, e.h, e.stream));
+  e.xn_ready = false;
   for (const LayerW& L : e.layers) MX_TRY(record_layer(e, L, rows, 1, rows, false));
   MX_TRY(hc_forward(e, e.mixer, rows, e.mixed, nullptr));
   return record_head(e, 1, false, rows - 1);

@@ -267,6 +267,12 @@ int moe_hc_epilogue(const uint16_t* routed, const uint16_t* shared, const uint16
 int moe_reduce_hc_epilogue(const uint16_t* p, const uint16_t* factor, const uint16_t* residual,
                            const uint16_t* gate, int rows, int top_k, int hc, int hidden,
                            uint16_t* out, hipStream_t s);
+// moe_reduce_hc_epilogue in place on h, then hc_norm of the result with
+// `scale` into xn and its operand plane, in one launch (same bits)
+bool moe_reduce_norm_supported(int rows, int top_k, int hc, int hidden);
+int moe_reduce_norm(const uint16_t* p, const uint16_t* factor, uint16_t* h, const uint16_t* gate,
+                    int rows, int top_k, int hc, int hidden, const uint16_t* scale, float eps,
+                    uint16_t* xn, char* plane, hipStream_t s);
 
 // ---- greedy head ----
 int head_parts(int n, int k);

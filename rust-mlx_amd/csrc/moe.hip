@@ -16,6 +16,7 @@
 #include "kernels.hpp"
 #include "qmv_core.hpp"
 #include "route_core.hpp"
+#include "xq_core.hpp"
 
 namespace mx {
 
@@ -532,6 +533,132 @@ __global__ __launch_bounds__(256) void moe_reduce_epilogue4_kernel(
                    uint32_t(res[s2][2]) | (uint32_t(res[s2][3]) << 16));
 }
 
+// moe_reduce_epilogue4_kernel's slot sum and stream write fused with the next
+// hyper-connection's norm (hc_norm_kernel's arithmetic, with the operand
+// plane): one workgroup per (stream, row) as the norm kernel has, each
+// summing the row's slots again for its own stream (K consecutive columns per
+// thread); the written stream goes through LDS so that thread t then takes
+// columns t + 256 k, and the stream's sum of squares runs over the same
+// columns in the same order as the norm kernel's thread t.
+// Same bits as the two launches; hc == 4, hidden = 256 K.
+template <int K>
+__global__ __launch_bounds__(256) void moe_reduce_norm_kernel(
+    const uint16_t* __restrict__ p, const uint16_t* __restrict__ factor,
+    uint16_t* __restrict__ h, const uint16_t* __restrict__ gate, int top_k,
+    const uint16_t* __restrict__ scale, float eps, uint16_t* __restrict__ xn,
+    char* __restrict__ plane) {
+  constexpr int HC = 4;
+  constexpr int hidden = 256 * K;
+  constexpr int CPT = K;  // consecutive columns per thread in the slot sum
+  __shared__ float red[4];
+  __shared__ __align__(16) uint16_t hs_[hidden];  // the written stream
+  __shared__ __align__(16) uint16_t ys[hidden];
+  const int s = blockIdx.x, row = blockIdx.y, t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const uint16_t* pr = p + size_t(row) * (top_k + 1) * hidden;
+  uint16_t* hr = h + (size_t(row) * HC + s) * hidden;
+  const float f = bf16_to_f32(factor[row]);
+  const float gv = bf16_to_f32(gate[size_t(row) * HC + s]);
+  const int lanes = top_k < 8 ? top_k : 8;
+  // slot sum of columns CPT t .. CPT t + CPT - 1 (every load issued first)
+  {
+    const int c0 = CPT * t;
+    uint16_t pv[kRedMaxK][CPT], sh[CPT], rv[CPT];
+    // CPT consecutive bf16 values, as one load when they fill 8 or 16 bytes
+    auto load = [&](const uint16_t* src, uint16_t (&dst)[CPT]) {
+      if constexpr (CPT == 8) {
+        const uint4 v = *reinterpret_cast<const uint4*>(src);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          dst[2 * i] = uint16_t(w[i]);
+          dst[2 * i + 1] = uint16_t(w[i] >> 16);
+        }
+      } else if constexpr (CPT == 4) {
+        const uint2 v = *reinterpret_cast<const uint2*>(src);
+        dst[0] = uint16_t(v.x);
+        dst[1] = uint16_t(v.x >> 16);
+        dst[2] = uint16_t(v.y);
+        dst[3] = uint16_t(v.y >> 16);
+      } else {
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) dst[i] = src[i];
+      }
+    };
+#pragma unroll
+    for (int sl = 0; sl < kRedMaxK; ++sl)
+      load(pr + size_t(sl < top_k ? sl : top_k) * hidden + c0, pv[sl]);
+    load(pr + size_t(top_k) * hidden + c0, sh);
+    load(hr + c0, rv);
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      float acc[8];
+#pragma unroll
+      for (int a = 0; a < 8; ++a) {
+        float v = bf16_to_f32(pv[a][i]);
+        if (a + 8 < top_k) v = round_bf16(v + bf16_to_f32(pv[a + 8][i]));
+        acc[a] = v;
+      }
+      float routed = acc[0];
+#pragma unroll
+      for (int a = 1; a < 8; ++a)
+        if (a < lanes) routed = round_bf16(acc[a] + routed);
+      routed = round_bf16(routed);
+      const float weighted = round_bf16(bf16_to_f32(sh[i]) * f);
+      const float combined = round_bf16(routed + weighted);
+      const float inj = round_bf16(combined * gv);
+      const uint16_t o = f32_to_bf16(bf16_to_f32(rv[i]) + inj);
+      hr[c0 + i] = o;
+      hs_[c0 + i] = o;
+    }
+  }
+  __syncthreads();
+  float xv[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) xv[k] = bf16_to_f32(hs_[t + 256 * k]);
+  // the stream's norm (hc_norm_kernel<K>'s order)
+  float acc = 0.0f;
+#pragma unroll
+  for (int k = 0; k < K; ++k) acc = acc + xv[k] * xv[k];
+  for (int o = 32; o > 0; o >>= 1) acc = acc + __shfl_xor(acc, o, 64);
+  if (lane == 0) red[wave] = acc;
+  __syncthreads();
+  const float total = ((red[0] + red[1]) + red[2]) + red[3];
+  const float inv = 1.0f / __builtin_sqrtf(total / float(hidden) + eps);
+  uint16_t* xr = xn + (size_t(row) * HC + s) * hidden;
+  const uint16_t* sc = scale + size_t(s) * hidden;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int c = t + 256 * k;
+    const uint16_t o = f32_to_bf16((xv[k] * inv) * (bf16_to_f32(sc[c]) + 1.0f));
+    xr[c] = o;
+    ys[c] = o;
+  }
+  __syncthreads();
+  // the stream's groups of the row's plane (hc_norm_kernel's group split)
+  const int kb = lane >> 4;
+  constexpr int ng = hidden / xq::kGroup;
+  for (int g0 = wave * 16; g0 < ng; g0 += 64) {
+    const int gl = g0 + (lane & 15);
+    const bool live = gl < ng;
+    float fv[16];
+    if (live) {
+      const uint4 a = *reinterpret_cast<const uint4*>(ys + gl * xq::kGroup + 16 * kb);
+      const uint4 b = *reinterpret_cast<const uint4*>(ys + gl * xq::kGroup + 16 * kb + 8);
+      const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        fv[2 * i] = u2f(w[i] << 16);
+        fv[2 * i + 1] = u2f(w[i] & 0xffff0000u);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) fv[i] = 0.0f;
+    }
+    xq::digitize_unit(fv, row, s * ng + gl, kb, live, plane, HC * ng);
+  }
+}
+
 }  // namespace
 
 int moe_route(const uint16_t* logits, int64_t logit_stride, const uint16_t* shared_logit,
@@ -669,6 +796,27 @@ int moe_hc_epilogue(const uint16_t* routed, const uint16_t* shared, const uint16
   const dim3 grid((hidden + 255) / 256, rows);
   hipLaunchKernelGGL(moe_epilogue_kernel, grid, dim3(256), 0, s, routed, shared, factor, residual,
                      gate, hc, hidden, out);
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
+bool moe_reduce_norm_supported(int rows, int top_k, int hc, int hidden) {
+  return rows >= 1 && rows <= 8 && top_k >= 1 && top_k < kRedMaxK && hc == 4 &&
+         hidden % 256 == 0 && hidden / 256 >= 1 && hidden / 256 <= 8;
+}
+
+int moe_reduce_norm(const uint16_t* p, const uint16_t* factor, uint16_t* h, const uint16_t* gate,
+                    int rows, int top_k, int hc, int hidden, const uint16_t* scale, float eps,
+                    uint16_t* xn, char* plane, hipStream_t s) {
+  if (!moe_reduce_norm_supported(rows, top_k, hc, hidden)) return MX_EUNSUPPORTED;
+  switch (hidden / 256) {
+#define MX_RN(KK)                                                                              \
+  case KK:                                                                                     \
+    hipLaunchKernelGGL(moe_reduce_norm_kernel<KK>, dim3(4, rows), dim3(256), 0, s, p, factor, h, \
+                       gate, top_k, scale, eps, xn, plane);                                    \
+    break;
+    MX_RN(1) MX_RN(2) MX_RN(3) MX_RN(4) MX_RN(5) MX_RN(6) MX_RN(7) MX_RN(8)
+#undef MX_RN
+  }
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 
