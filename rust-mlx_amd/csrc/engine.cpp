@@ -493,9 +493,10 @@ int build(Engine& e) {
   }
   MX_TRY(alloc(e, "act.ids", R * c.top_k * 4, &v));
   e.ids = static_cast<uint32_t*>(v);
-  MX_TRY(alloc(e, "act.o_part", R * c.heads * e.max_chunks * c.head_dim * 4, &v));
+  const size_t AR = R < size_t(kAttnRows) ? R : size_t(kAttnRows);  // attention rows per launch
+  MX_TRY(alloc(e, "act.o_part", AR * c.heads * e.max_chunks * c.head_dim * 4, &v));
   e.o_part = static_cast<float*>(v);
-  MX_TRY(alloc(e, "act.ml_part", R * c.heads * e.max_chunks * 2 * 4, &v));
+  MX_TRY(alloc(e, "act.ml_part", AR * c.heads * e.max_chunks * 2 * 4, &v));
   e.ml_part = static_cast<float*>(v);
   size_t hws = size_t(head_parts(c.vocab, c.hidden)) * 8 * 8;
   MX_TRY(alloc(e, "act.head_ws", hws, &e.head_ws));
@@ -732,12 +733,19 @@ int record_layer(Engine& e, const LayerW& L, int rows, int groups, int t, bool h
                        e.rope_cos, e.rope_sin, e.ad, e.qrot, e.k_cache + layer_off,
                        e.v_cache + layer_off, e.stream));
       const bool fast_attn = !ex(e, kExAttn) && attn_fast_supported(e.ad);
-      MX_TRY(attn_decode(e.qrot, rows, rt->slots, rt->pos, e.k_cache + layer_off,
-                         e.v_cache + layer_off, e.ad, e.max_chunks, fast_attn, e.o_part,
-                         e.ml_part, e.stream));
       char* yp = !fast_attn && ex(e, kExAttnProj) && rows <= 8 ? e.y_plane : nullptr;
-      MX_TRY(attn_combine(e.o_part, e.ml_part, e.pbuf, e.Q, rows, rt->pos, e.ad, e.max_chunks,
-                          fast_attn, e.y, e.stream, yp));
+      // a prefill chunk's query rows go through in blocks of kAttnRows, so
+      // the per-chunk partials stay sized for kAttnRows rows
+      const size_t qd = size_t(c.heads) * c.head_dim;
+      for (int r0 = 0; r0 < rows; r0 += kAttnRows) {
+        const int n = rows - r0 < kAttnRows ? rows - r0 : kAttnRows;
+        MX_TRY(attn_decode(e.qrot + r0 * qd, n, rt->slots + r0, rt->pos + r0,
+                           e.k_cache + layer_off, e.v_cache + layer_off, e.ad, e.max_chunks,
+                           fast_attn, e.o_part, e.ml_part, e.stream));
+        MX_TRY(attn_combine(e.o_part, e.ml_part, e.pbuf + size_t(r0) * e.Q, e.Q, n,
+                            rt->pos + r0, e.ad, e.max_chunks, fast_attn, e.y + r0 * qd,
+                            e.stream, yp));
+      }
       MX_TRY(project(e, L.attn_out, e.y, int64_t(c.heads) * c.head_dim, rows, wr, kExAttnProj,
                      yp));
     }

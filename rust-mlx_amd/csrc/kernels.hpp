@@ -191,6 +191,7 @@ int attn_combine(const float* o_part, const float* ml_part, const uint16_t* qkv,
                  bool fast, uint16_t* out, hipStream_t s, char* plane = nullptr);
 constexpr int kAttnChunk = 256;
 constexpr int kAttnFastChunk = 64;
+constexpr int kAttnRows = 128;  // query rows per attention launch of a prefill chunk
 
 // ---- MoE ----
 constexpr int kMaxRoutes = 8 * 16 + 1;

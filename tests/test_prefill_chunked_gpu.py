@@ -174,3 +174,24 @@ def test_chunked_prefill_refuses_unsupported_models_before_any_launch(mx):
         assert eng.offset(0) == 40
     finally:
         eng.close()
+
+
+def test_chunked_prefill_continues_an_existing_context(tiny):
+    """A chunked prefill after 100 positions of block prefill (a prefix reused,
+    then the rest of the prompt): the chunk reads the slot's cached conv
+    window, GDN state and K/V, and its queries attend to the earlier
+    positions.  The caches agree with a whole-prompt block prefill as closely
+    as the matrix-core block prefill does."""
+    eng, cfg = tiny
+    prompt = np.random.default_rng(41).integers(0, cfg["vocab"], 400)
+    prefill(eng, 0, prompt, exact=True, chunked=False)
+    prefill(eng, 1, prompt, exact=False, chunked=False)
+    prefill(eng, 2, prompt[:100], exact=True, chunked=False)
+    eng.set_flags(exact=False)
+    eng.prefill(2, prompt[100:], chunked=True)
+    assert eng.offset(2) == 400
+    exact, fast, got = (caches(eng, cfg, s, 400) for s in (0, 1, 2))
+    base = [rel(f, e) for f, e in zip(fast, exact)]
+    errs = [rel(g, e) for g, e in zip(got, exact)]
+    print(f"continued chunk vs exact: {errs}; fast blocks vs exact: {base}", flush=True)
+    assert all(e <= 2.0 * b + 1e-2 for e, b in zip(errs, base)), (errs, base)
