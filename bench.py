@@ -1140,7 +1140,52 @@ def summarize_counters(fetch_csv: str, write_csv: str, fetch_scale: float, write
         print(f"\ntraffic_bytes_per_launch = {int(tb)}")
 
 
+def summarize_pmc(paths, kernels=("xq_gate_up_kernel", "xq_down_kernel", "xq_head_kernel")) -> None:
+    """Markdown table of every counter in rocprofv3 `--pmc` runs of this script
+    (their *_counter_collection.csv files, one pass each): per kernel name
+    prefix in `kernels`, its largest grid (the batch-8 step's), the median of
+    each counter over that grid's dispatches."""
+    import csv
+    import gzip
+    import io
+    import statistics
+
+    vals = {}  # (short name, grid) -> counter -> values
+    for path in paths:
+        fh = gzip.open(path) if path.endswith(".gz") else open(path, "rb")
+        for r in csv.DictReader(io.TextIOWrapper(fh, "utf-8")):
+            key = (short_kernel_name(r["Kernel_Name"]), int(r["Grid_Size"]))
+            vals.setdefault(key, {}).setdefault(r["Counter_Name"], []).append(
+                float(r["Counter_Value"]))
+    picked = []
+    for prefix in kernels:
+        keys = [k for k in vals if k[0].startswith(prefix)]
+        if keys:
+            picked.append(max(keys, key=lambda k: k[1]))
+    counters = sorted({c for k in picked for c in vals[k]})
+    print("| counter | " + " | ".join(f"`{k[0]}` ({k[1]} threads)" for k in picked) + " |")
+    print("|---|" + "---:|" * len(picked))
+    for c in counters:
+        cells = []
+        for k in picked:
+            v = vals[k].get(c)
+            cells.append(f"{statistics.median(v):.6g}" if v else "")
+        print(f"| {c} | " + " | ".join(cells) + " |")
+    print("\n| dispatches | " + " | ".join(
+        str(max(len(v) for v in vals[k].values())) for k in picked) + " |")
+
+
 def main() -> None:
+    if len(sys.argv) >= 3 and sys.argv[1] == "--summarize-pmc":
+        # no device work: medians of every counter of rocprofv3 --pmc runs
+        # (optionally `--kernels a,b,c`: the kernel name prefixes to report)
+        args = sys.argv[2:]
+        if "--kernels" in args:
+            i = args.index("--kernels")
+            summarize_pmc(args[:i] + args[i + 2:], tuple(args[i + 1].split(",")))
+        else:
+            summarize_pmc(args)
+        return
     if len(sys.argv) >= 6 and sys.argv[1] == "--summarize-counters":
         # no device work: summarise two rocprofv3 counter runs of this script
         summarize_counters(sys.argv[2], sys.argv[3], float(sys.argv[4]), float(sys.argv[5]),
