@@ -192,11 +192,13 @@ mx_status mx_qmv(const mx_qweight* w, const uint16_t* x, int32_t m, uint16_t* y,
                  void* stream);
 
 /* ---- A3/A15: the same projection on the matrix cores --------------------
- * y = x . dequant(W)^T for 1 <= m <= 512 rows with v_mfma_f32_16x16x32_bf16
- * (beyond 16 rows a GEMM staging 128-row blocks of x in LDS):
- * codes enter as exact bf16 integers, each 64-value group's fp32 partial is
- * scaled in registers.  Results equal mx_qmv's up to fp32 summation order
- * (the north star's tolerance, not bit for bit).  Requires group_size 64 and
+ * y = x . dequant(W)^T for 1 <= m <= 512 rows with v_mfma_f32_16x16x32_bf16.
+ * Up to 16 rows the codes enter as exact bf16 integers and each 64-value
+ * group's fp32 partial is scaled in registers; beyond 16 rows a GEMM stages
+ * 128-row blocks of x in LDS and dequantises each workgroup's weight rows
+ * there as w = s q + b split into two bf16 parts (hi + lo within 2^-17 of w).
+ * Results equal mx_qmv's up to fp32 summation order and that split (the
+ * north star's tolerance, not bit for bit).  Requires group_size 64 and
  * k <= 8192.  Deterministic: a workgroup splits k among its own waves and adds
  * their sums in a fixed order.  The MFMA verify/prefill slot of the reference
  * (matrix_kernel::project, src/matrix_kernel.rs:113-254,

@@ -180,13 +180,12 @@ void dense_bits(const QWeight& w, const uint16_t* x, int64_t xs, int m, const Pr
 // slice (blockIdx.z); wave (wn, wm) of its 2 x 2 waves owns 32 weight rows
 // (two 16-row tiles) x 64 activation rows (four 16-row tiles).  The
 // activations of two groups (128 k) at a time are staged in LDS once for the
-// four waves (eight lanes per 128-byte row piece); the next two groups' loads
-// are in flight while the matrix cores work on these, and the weights of
-// the stage after are requested too.  The per-group arithmetic of qmm_tiles
-// (codes as exact bf16 integers, fp32 sums, the group's scale and bias
-// applied in registers, the group sums of x from a ones operand on the matrix
-// cores).  With a k split the workgroups write fp32 partials
-// and gemm_reduce_kernel adds them in slice order before the epilogue.
+// four waves (eight lanes per 128-byte row piece), and so are the weights of
+// those groups, dequantised (gemm_dq_kernel); the next two groups'
+// activations are in flight while the matrix cores work on these, and the
+// weights of the stage after are requested too.  With a k split the
+// workgroups write fp32 partials and gemm_reduce_kernel adds them in slice
+// order before the epilogue.
 constexpr int kGemmM = 128;          // activation rows per workgroup
 constexpr int kGemmN = 64;           // weight rows per workgroup
 constexpr int kGemmLd = 64 + 8;      // padded LDS row (bf16) of one group
@@ -213,28 +212,54 @@ __device__ __forceinline__ void gemm_epilogue(const ProjEpilogue& e, int n, int 
   }
 }
 
+// Prefill projections: the weights dequantised once per workgroup.  Each
+// stage, thread t turns 32 codes of weight row t / 4 (k piece t % 4 of the
+// stage's 128; BITS 32-bit words) into w = s q + b in fp32 and stores two bf16 parts in LDS,
+// hi = bf16(w) and lo = bf16(w - hi) (w - hi is exact in fp32; hi + lo is w
+// to within 2^-17 |w|).  The waves then multiply plain tiles, x hi + x lo
+// into fp32 accumulators over the whole slice, with no per-group scale work
+// per output (the exact-code form applies s and b to every output of every
+// group, and its 128 q offset cancels in fp32).  Lane quarter kq of MFMA step
+// st covers k = 16 kq + 8 st .. + 7 of a group on both operands.
+constexpr int kDqLd = 2 * 64 + 8;  // padded LDS row (bf16) of a stage's weights
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+__host__ __device__ constexpr int gemm_dq_lds() {
+  return (kGemmStage * kGemmM * kGemmLd + 2 * kGemmN * kDqLd) * 2;
+}
+
+// Code v (0..31) of a 32-code piece held in BITS words, value v at bit BITS v.
+template <int BITS, int V>
+__device__ __forceinline__ uint32_t piece_code(const uint32_t (&w)[BITS]) {
+  constexpr int bit = BITS * V, word = bit >> 5, off = bit & 31;
+  constexpr uint32_t mask = (1u << BITS) - 1u;
+  if constexpr (off + BITS <= 32)
+    return (w[word] >> off) & mask;
+  else
+    return __builtin_amdgcn_alignbit(w[word + 1], w[word], uint32_t(off)) & mask;
+}
+
 template <int BITS, bool SPLIT>
-__global__ __launch_bounds__(256) void gemm_kernel(QWeight w, const uint16_t* __restrict__ x,
-                                                   int64_t x_stride, int M, int per,
-                                                   ProjEpilogue e) {
-  __shared__ __align__(16) uint16_t xs[kGemmStage][kGemmM][kGemmLd];
-  constexpr int NW = group_words<BITS>();
-  const uint4 ones = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
+__global__ __launch_bounds__(256) void gemm_dq_kernel(QWeight w, const uint16_t* __restrict__ x,
+                                                      int64_t x_stride, int M, int per,
+                                                      ProjEpilogue e) {
+  extern __shared__ __align__(16) uint16_t dq_lds[];
+  auto xs = reinterpret_cast<uint16_t (*)[kGemmM][kGemmLd]>(dq_lds);
+  auto wh = reinterpret_cast<uint16_t (*)[kDqLd]>(dq_lds + kGemmStage * kGemmM * kGemmLd);
+  auto wl = wh + kGemmN;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j = lane & 15, kq = lane >> 4;
   const int wn = wave & 1, wm = wave >> 1;
   const int n = w.n, G = w.k >> 6;
-  const int nb = blockIdx.x * kGemmN + wn * 32;  // this wave's first weight row
-  const int mb = blockIdx.y * kGemmM;            // this workgroup's first activation row
+  const int mb = blockIdx.y * kGemmM;
   const int gbeg = blockIdx.z * per;
   const int gend = min(G, gbeg + per);
-  TileRow tr[2];
-#pragma unroll
-  for (int t = 0; t < 2; ++t)
-    tr[t] = tile_row(w.codes, w.scales, w.biases, w.k, BITS, min(nb + 16 * t + j, n - 1));
-  const float off = code_offset<BITS>();
-  // staging: piece i of thread t is 16-byte chunk (t % 8) of row t / 8 + 32 (i % 4)
-  // of the stage's group i / 4 (eight lanes per 128-byte row piece)
+  // dequantising role: weight row dr of the workgroup, 32-value piece dp
+  const int dr = tid >> 2, dp = tid & 3;
+  const int wrow = min(int(blockIdx.x) * kGemmN + dr, n - 1);
+  const uint32_t* crow = w.codes + size_t(wrow) * (size_t(w.k) * BITS / 32);
+  const uint16_t* srow = w.scales + size_t(wrow) * G;
+  const uint16_t* brow = w.biases + size_t(wrow) * G;
   const int sc8 = tid & 7, sr0 = tid >> 3;
   uint4 xv[8];
   auto load_x = [&](int g0) {
@@ -247,29 +272,34 @@ __global__ __launch_bounds__(256) void gemm_kernel(QWeight w, const uint16_t* __
         xv[i] = make_uint4(0u, 0u, 0u, 0u);
     }
   };
+  struct StageW {
+    uint32_t c[BITS];  // 32 codes of row dr, group g0 + dp / 2, half dp % 2
+    uint16_t sc, bi;
+  };
+  auto load_w = [&](int g0, StageW& st) {
+    const int g = min(g0 + (dp >> 1), gend - 1);
+    const uint32_t* src = crow + 2 * BITS * g + BITS * (dp & 1);
+    if constexpr (BITS % 4 == 0) {  // 16-byte aligned pieces
+#pragma unroll
+      for (int i = 0; i < BITS / 4; ++i) {
+        const uint4 v = reinterpret_cast<const uint4*>(src)[i];
+        st.c[4 * i] = v.x;
+        st.c[4 * i + 1] = v.y;
+        st.c[4 * i + 2] = v.z;
+        st.c[4 * i + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < BITS; ++i) st.c[i] = src[i];
+    }
+    st.sc = srow[g];
+    st.bi = brow[g];
+  };
   floatx4_t y[2][4];
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int u = 0; u < 4; ++u) y[t][u] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  // a stage's codes and raw scales / biases; weights stream from HBM, so each
-  // stage's are requested two stages ahead of their use
-  struct StageW {
-    uint32_t cw[kGemmStage][2][NW];
-    uint16_t sc[kGemmStage][2], bi[kGemmStage][2];
-  };
-  auto load_w = [&](int g0, StageW& st) {
-#pragma unroll
-    for (int s = 0; s < kGemmStage; ++s) {
-      const int g = min(g0 + s, gend - 1);
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        load_group_codes<BITS>(tr[t].codes, g, kq, st.cw[s][t]);
-        st.sc[s][t] = tr[t].scales[g];
-        st.bi[s][t] = tr[t].biases[g];
-      }
-    }
-  };
   StageW w0, w1;
   load_w(gbeg, w0);
   load_w(gbeg + kGemmStage, w1);
@@ -277,52 +307,68 @@ __global__ __launch_bounds__(256) void gemm_kernel(QWeight w, const uint16_t* __
   for (int g0 = gbeg; g0 < gend; g0 += kGemmStage) {
     StageW w2;
     load_w(g0 + 2 * kGemmStage, w2);  // two stages ahead (clamped to the slice)
-    const StageW& cur = w0;
-    float sc[kGemmStage][2], bi[kGemmStage][2];
-    __syncthreads();  // every wave is done with the previous stage's LDS
+    __syncthreads();                  // every wave is done with the previous stage's LDS
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int r = sr0 + 32 * (i & 3), gs = i >> 2;
       *reinterpret_cast<uint4*>(&xs[gs][r][8 * sc8]) = xv[i];
     }
+    {
+      const float sc = bf16_to_f32(w0.sc), bi = bf16_to_f32(w0.bi);
+      uint32_t qv[32];
+      [&]<int... V>(std::integer_sequence<int, V...>) {
+        ((qv[V] = piece_code<BITS, V>(w0.c)), ...);
+      }(std::make_integer_sequence<int, 32>{});
+#pragma unroll
+      for (int q8 = 0; q8 < 4; ++q8) {  // codes 8 q8 .. + 7
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float v0 = fmaf_(sc, float(qv[8 * q8 + 2 * i]), bi);
+          const float v1 = fmaf_(sc, float(qv[8 * q8 + 2 * i + 1]), bi);
+          const bf16x2_t h = {__bf16(v0), __bf16(v1)};
+          const uint32_t hb = __builtin_bit_cast(uint32_t, h);
+          const bf16x2_t l = {__bf16(v0 - u2f(hb << 16)), __bf16(v1 - u2f(hb & 0xffff0000u))};
+          hw[i] = hb;
+          lw[i] = __builtin_bit_cast(uint32_t, l);
+        }
+        const int col = 32 * dp + 8 * q8;
+        *reinterpret_cast<uint4*>(&wh[dr][col]) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        *reinterpret_cast<uint4*>(&wl[dr][col]) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+      }
+    }
     __syncthreads();
     if (g0 + kGemmStage < gend) load_x(g0 + kGemmStage);  // next stage, in flight
 #pragma unroll
-    for (int s = 0; s < kGemmStage; ++s)
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        sc[s][t] = bf16_to_f32(cur.sc[s][t]);
-        bi[s][t] = fmaf_(-off, sc[s][t], bf16_to_f32(cur.bi[s][t]));
-      }
-#pragma unroll
     for (int s = 0; s < kGemmStage; ++s) {
       if (g0 + s >= gend) break;  // uniform
-      const uint4 b0[2] = {codes_operand<BITS, 0>(cur.cw[s][0]), codes_operand<BITS, 0>(cur.cw[s][1])};
-      const uint4 b1[2] = {codes_operand<BITS, 1>(cur.cw[s][0]), codes_operand<BITS, 1>(cur.cw[s][1])};
+      uint4 bh[2][2], bl[2][2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+          const int nr = wn * 32 + 16 * t + j, col = 64 * s + 16 * kq + 8 * st;
+          bh[t][st] = *reinterpret_cast<const uint4*>(&wh[nr][col]);
+          bl[t][st] = *reinterpret_cast<const uint4*>(&wl[nr][col]);
+        }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int row = wm * 64 + 16 * u + j;
         const uint4* xp = reinterpret_cast<const uint4*>(&xs[s][row][16 * kq]);
-        const uint4 a0 = permute_x(xp[0]), a1 = permute_x(xp[1]);
-        // the rows' group sums (D rows) against a ones operand
-        floatx4_t sxr = {0.0f, 0.0f, 0.0f, 0.0f};
-        sxr = mfma_bf16(a0, ones, sxr);
-        sxr = mfma_bf16(a1, ones, sxr);
+        const uint4 a0 = xp[0], a1 = xp[1];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-          floatx4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-          acc = mfma_bf16(a0, b0[t], acc);
-          acc = mfma_bf16(a1, b1[t], acc);
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            y[t][u][r] = fmaf_(sc[s][t], acc[r], fmaf_(bi[s][t], sxr[r], y[t][u][r]));
+          y[t][u] = mfma_bf16(a0, bh[t][0], y[t][u]);
+          y[t][u] = mfma_bf16(a1, bh[t][1], y[t][u]);
+          y[t][u] = mfma_bf16(a0, bl[t][0], y[t][u]);
+          y[t][u] = mfma_bf16(a1, bl[t][1], y[t][u]);
         }
       }
     }
     w0 = w1;
     w1 = w2;
   }
-  // D row = activation row, column = weight row
+  const int nb = blockIdx.x * kGemmN + wn * 32;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int row = nb + 16 * t + j;
@@ -365,10 +411,19 @@ void launch_gemm(const QWeight& w, const uint16_t* x, int64_t xs, int m, const P
     slices *= 2;
   const int per = (G + slices - 1) / slices;
   const dim3 grid(nb, mb, slices);
-  if (slices == 1) {
-    hipLaunchKernelGGL((gemm_kernel<BITS, false>), grid, dim3(256), 0, s, w, x, xs, m, per, e);
-  } else {
-    hipLaunchKernelGGL((gemm_kernel<BITS, true>), grid, dim3(256), 0, s, w, x, xs, m, per, e);
+  // the LDS above the default 64 KiB needs the kernel attribute
+  const void* fn = slices == 1 ? reinterpret_cast<const void*>(gemm_dq_kernel<BITS, false>)
+                               : reinterpret_cast<const void*>(gemm_dq_kernel<BITS, true>);
+  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, gemm_dq_lds()) !=
+      hipSuccess)
+    return;
+  if (slices == 1)
+    hipLaunchKernelGGL((gemm_dq_kernel<BITS, false>), grid, dim3(256), gemm_dq_lds(), s, w, x,
+                       xs, m, per, e);
+  else
+    hipLaunchKernelGGL((gemm_dq_kernel<BITS, true>), grid, dim3(256), gemm_dq_lds(), s, w, x,
+                       xs, m, per, e);
+  if (slices > 1) {
     const size_t outs = size_t(m) * w.n;
     hipLaunchKernelGGL(gemm_reduce_kernel, dim3(unsigned((outs + 255) / 256)), dim3(256), 0, s,
                        w.n, m, slices, e);
