@@ -239,7 +239,11 @@ __device__ __forceinline__ uint32_t piece_code(const uint32_t (&w)[BITS]) {
     return __builtin_amdgcn_alignbit(w[word + 1], w[word], uint32_t(off)) & mask;
 }
 
-template <int BITS, bool SPLIT>
+// MIX (kHcUpMix, no k split): the workgroup's 64 weight rows are the four
+// streams' rows s H + c of 16 columns c (blockIdx.x 16 .. + 15), and the
+// epilogue mixes the four streams of each column through LDS with
+// dense_kernel's kHcUpMix arithmetic.
+template <int BITS, bool SPLIT, bool MIX = false>
 __global__ __launch_bounds__(256) void gemm_dq_kernel(QWeight w, const uint16_t* __restrict__ x,
                                                       int64_t x_stride, int M, int per,
                                                       ProjEpilogue e) {
@@ -256,7 +260,9 @@ __global__ __launch_bounds__(256) void gemm_dq_kernel(QWeight w, const uint16_t*
   const int gend = min(G, gbeg + per);
   // dequantising role: weight row dr of the workgroup, 32-value piece dp
   const int dr = tid >> 2, dp = tid & 3;
-  const int wrow = min(int(blockIdx.x) * kGemmN + dr, n - 1);
+  const int cb = int(blockIdx.x) * 16;  // MIX: the workgroup's first column
+  const int wrow = MIX ? (dr >> 4) * e.hidden + min(cb + (dr & 15), e.hidden - 1)
+                       : min(int(blockIdx.x) * kGemmN + dr, n - 1);
   const uint32_t* crow = w.codes + size_t(wrow) * (size_t(w.k) * BITS / 32);
   const uint16_t* srow = w.scales + size_t(wrow) * G;
   const uint16_t* brow = w.biases + size_t(wrow) * G;
@@ -368,6 +374,32 @@ __global__ __launch_bounds__(256) void gemm_dq_kernel(QWeight w, const uint16_t*
     w0 = w1;
     w1 = w2;
   }
+  if constexpr (MIX) {
+    // stream s = 2 wn + t of column cb + j: bf16(p) into LDS [row][s][column]
+    __syncthreads();  // the last stage's operands are read
+    float* ex = reinterpret_cast<float*>(dq_lds);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          ex[((wm * 64 + 16 * u + 4 * kq + r) * 4 + 2 * wn + t) * 16 + j] = round_bf16(y[t][u][r]);
+    __syncthreads();
+    for (int i = tid; i < kGemmM * 16; i += 256) {
+      const int ml = i >> 4, c = i & 15, m = mb + ml;
+      if (m >= M || cb + c >= e.hidden) continue;
+      float sum = 0.0f;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const float xn =
+            bf16_to_f32(e.xn[size_t(m) * e.xn_stride + size_t(st) * e.hidden + cb + c]);
+        sum = sum + round_bf16(sigmoid_bf16(ex[(ml * 4 + st) * 16 + c]) * xn);
+      }
+      e.y[size_t(m) * e.y_stride + cb + c] = f32_to_bf16(round_bf16(sum) / 4.0f);
+    }
+    return;
+  }
   const int nb = blockIdx.x * kGemmN + wn * 32;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
@@ -402,7 +434,17 @@ template <int BITS>
 void launch_gemm(const QWeight& w, const uint16_t* x, int64_t xs, int m, const ProjEpilogue& e,
                  hipStream_t s) {
   const int G = w.k >> 6;
-  const int nb = (w.n + kGemmN - 1) / kGemmN, mb = (m + kGemmM - 1) / kGemmM;
+  const int mb = (m + kGemmM - 1) / kGemmM;
+  if (e.mode == kHcUpMix) {  // four streams of 16 columns per workgroup, no k split
+    const void* fn = reinterpret_cast<const void*>(gemm_dq_kernel<BITS, false, true>);
+    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, gemm_dq_lds()) !=
+        hipSuccess)
+      return;
+    hipLaunchKernelGGL((gemm_dq_kernel<BITS, false, true>), dim3((e.hidden + 15) / 16, mb, 1),
+                       dim3(256), gemm_dq_lds(), s, w, x, xs, m, G, e);
+    return;
+  }
+  const int nb = (w.n + kGemmN - 1) / kGemmN;
   // split k across workgroups until the grid has about 256 workgroups, each
   // slice at least four groups, when the workspace holds the partials
   int slices = 1;
@@ -670,7 +712,7 @@ int qmm(const QWeight& w, const uint16_t* x, int64_t x_stride, int m, const Proj
   if (!qmm_supported(w) || m < 1 || m > kQmmMaxRows) return MX_EUNSUPPORTED;
   if (e.mode == kHcUpMix && e.hidden * 4 != w.n) return MX_EUNSUPPORTED;
   if (e.mode == kConv) return MX_EUNSUPPORTED;
-  if (m > 16 && e.mode != kHcUpMix) {  // prefill rows: the staged GEMM
+  if (m > 16) {  // prefill rows: the staged GEMM
     switch (w.bits) {
       case 4: launch_gemm<4>(w, x, x_stride, m, e, s); break;
       case 5: launch_gemm<5>(w, x, x_stride, m, e, s); break;
