@@ -16,6 +16,7 @@
 // handles one (chunk, kv head, row) for all q heads sharing the kv head, so K
 // and V stream once per group.  A second pass combines the chunks.
 #include <type_traits>
+#include <utility>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -470,6 +471,7 @@ __global__ __launch_bounds__(256) void combine_fast_kernel(const float* __restri
                                                            int64_t qkv_stride,
                                                            const int32_t* __restrict__ pos,
                                                            AttnDims d, int max_chunks,
+                                                           int chunk_len,
                                                            uint16_t* __restrict__ out) {
   __shared__ float wsh[256];
   __shared__ float red[2][4];
@@ -477,7 +479,7 @@ __global__ __launch_bounds__(256) void combine_fast_kernel(const float* __restri
   const int row = blockIdx.y;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int hd = d.head_dim;
-  const int chunks = (pos[row] + kAttnFastChunk) / kAttnFastChunk;
+  const int chunks = (pos[row] + chunk_len) / chunk_len;
   const float* ml = ml_part + (size_t(row) * d.heads + h) * max_chunks * 2;
   const float* op = o_part + (size_t(row) * d.heads + h) * max_chunks * hd + min(t, hd - 1);
   const float gate =
@@ -514,6 +516,225 @@ __global__ __launch_bounds__(256) void combine_fast_kernel(const float* __restri
   const float attn = round_bf16(O * __builtin_amdgcn_rcpf(L));
   const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gate * 1.4426950408889634f));
   out[(size_t(row) * d.heads + h) * hd + t] = f32_to_bf16(attn * sg);
+}
+
+// ---------------------------------------------------------------------------
+// Prefill attention on the matrix cores (fast mode, a chunk of query rows of
+// one slot): a workgroup of eight waves takes QB = 8 * 16 / G query rows, one
+// kv head and one split of kPfSplit key positions, so the key and value rows
+// of a tile are read once for all QB rows x G heads.  Wave w owns one M tile
+// of 16 (row, head) pairs: pair i = row qb0 + w * 16 / G + i / G, head
+// kvh * G + i % G.  Per tile of kPfKeys keys: K rows and V (transposed) are
+// staged in LDS; S = Q K^T on the matrix cores (Q held as A operands for the
+// whole launch); the online softmax per pair (max and sum over the 16 lanes
+// of a quarter and the tile's four 16-key columns, hardware exp2); P goes
+// through LDS into A-operand order as two bf16 parts (hi + lo), and O += P V
+// on the matrix cores (fp32 accumulators, rescaled by e^(m_old - m_new)).
+// The split's (m, l, O) per pair go to o_part / ml_part at chunk index =
+// split, which combine_fast_kernel merges with chunk length kPfSplit.  Rows of
+// one query block must share a slot (a prefill chunk's rows do).
+constexpr int kPfKeys = 64;     // keys per tile
+constexpr int kPfSplit = 256;   // keys per split (one partial per pair and split)
+constexpr int kPfKLd = kMaxHd + 8;      // padded K row in LDS (bf16)
+constexpr int kPfVLd = kPfKeys + 8;     // padded transposed-V row (bf16)
+
+template <int HD>
+__host__ __device__ constexpr int prefill_attn_lds() {
+  return (kPfKeys * kPfKLd + HD * kPfVLd + 8 * 2 * 16 * kPfVLd) * 2;
+}
+
+template <int G, int HD>
+__global__ __launch_bounds__(512) void prefill_attn_kernel(
+    const uint16_t* __restrict__ q, int rows, const int32_t* __restrict__ slots,
+    const int32_t* __restrict__ pos, const uint16_t* __restrict__ k_cache,
+    const uint16_t* __restrict__ v_cache, AttnDims d, int max_chunks, float scale,
+    float* __restrict__ o_part, float* __restrict__ ml_part) {
+  constexpr int RPW = 16 / G;       // query rows per wave
+  constexpr int QB = 8 * RPW;       // query rows per workgroup
+  constexpr int KS = HD / 32;       // MFMA steps over the head dim
+  constexpr int NO = HD / 16;       // 16-dim output tiles
+  extern __shared__ __align__(16) uint16_t pf_lds[];
+  uint16_t* ks = pf_lds;                              // [kPfKeys][kPfKLd]
+  uint16_t* vt = ks + kPfKeys * kPfKLd;               // [HD][kPfVLd]
+  uint16_t* pw = vt + HD * kPfVLd;                    // [8 waves][hi, lo][16][kPfVLd]
+  __shared__ int blk_max;
+  const int split = blockIdx.x, kvh = blockIdx.y, qb0 = blockIdx.z * QB;
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const int j = lane & 15, kq = lane >> 4;
+  if (t == 0) {
+    int mx = -1;
+    for (int r = qb0; r < min(qb0 + QB, rows); ++r) mx = max(mx, pos[r]);
+    blk_max = mx;
+  }
+  __syncthreads();
+  const int key0 = split * kPfSplit;
+  const int kend = min(key0 + kPfSplit, blk_max + 1);  // keys [key0, kend)
+  if (key0 >= kend) return;                             // uniform
+  const size_t base = size_t(slots[qb0]) * d.slot_stride + size_t(kvh) * d.max_ctx * HD;
+  // this lane's A-operand pair (j) and the D-layout pairs 4 kq + r
+  const int arow = qb0 + wave * RPW + j / G;
+  const bool alive = arow < rows;
+  const uint16_t* qr =
+      q + (size_t(alive ? arow : 0) * d.heads + kvh * G + j % G) * HD + 8 * kq;
+  uint4 qa[KS];
+#pragma unroll
+  for (int k = 0; k < KS; ++k)
+    qa[k] = alive ? *reinterpret_cast<const uint4*>(qr + 32 * k) : make_uint4(0u, 0u, 0u, 0u);
+  int lim[4];  // exclusive key limit of D-layout pair 4 kq + r
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int row = qb0 + wave * RPW + (4 * kq + r) / G;
+    lim[r] = row < rows ? min(pos[row] + 1, kend) : key0;
+  }
+  const float sl2 = scale * 1.4426950408889634f;  // scores in log2 units
+  float m_run[4], l_run[4];
+  sk::floatx4_t o[NO];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    m_run[r] = u2f(0xff800000u);
+    l_run[r] = 0.0f;
+  }
+#pragma unroll
+  for (int n = 0; n < NO; ++n) o[n] = sk::floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  uint16_t* ph = pw + wave * 2 * 16 * kPfVLd;
+  uint16_t* pl = ph + 16 * kPfVLd;
+  // a tile's K pieces and V key pairs per thread, loaded one tile ahead
+  constexpr int KPT = kPfKeys * HD / 8 / 512, VPT = (kPfKeys / 2) * (HD / 8) / 512;
+  static_assert(KPT * 512 == kPfKeys * HD / 8 && VPT * 512 == (kPfKeys / 2) * (HD / 8),
+                "tile pieces divide among 512 threads");
+  uint4 kr[KPT], va[VPT], vb[VPT];
+  // constant indices from the start, so the arrays stay in registers
+  auto load_k = [&](int kt, int u) {
+    const int i = t + 512 * u, key = i / (HD / 8), pc = i % (HD / 8);
+    const int kk = min(kt + key, kend - 1);  // keys past kend: the last valid one
+    return *reinterpret_cast<const uint4*>(k_cache + base + size_t(kk) * HD + 8 * pc);
+  };
+  auto load_v = [&](int kt, int u, int second) {
+    const int i = t + 512 * u;
+    const int kp = i % (kPfKeys / 2), dg = i / (kPfKeys / 2);  // neighbours: keys (banks)
+    const int kk = min(kt + 2 * kp + second, kend - 1);
+    return *reinterpret_cast<const uint4*>(v_cache + base + size_t(kk) * HD + 8 * dg);
+  };
+#define MX_PF_LOAD(KT)                                                                  \
+  {                                                                                     \
+    const int kt_ = (KT);                                                               \
+    [&]<int... U>(std::integer_sequence<int, U...>) {                                   \
+      ((kr[U] = load_k(kt_, U)), ...);                                                  \
+    }(std::make_integer_sequence<int, KPT>{});                                          \
+    [&]<int... U>(std::integer_sequence<int, U...>) {                                   \
+      ((va[U] = load_v(kt_, U, 0), vb[U] = load_v(kt_, U, 1)), ...);                    \
+    }(std::make_integer_sequence<int, VPT>{});                                          \
+  }
+  MX_PF_LOAD(key0)
+  for (int kt = key0; kt < kend; kt += kPfKeys) {
+    __syncthreads();  // the previous tile's K, V and P are consumed
+    // K rows; V transposed, one 32-bit word (two keys) per dim
+#pragma unroll
+    for (int u = 0; u < KPT; ++u) {
+      const int i = t + 512 * u, key = i / (HD / 8), pc = i % (HD / 8);
+      *reinterpret_cast<uint4*>(ks + key * kPfKLd + 8 * pc) = kr[u];
+    }
+#pragma unroll
+    for (int u = 0; u < VPT; ++u) {
+      const int i = t + 512 * u;
+      const int kp = i % (kPfKeys / 2), dg = i / (kPfKeys / 2);
+      const uint32_t av[4] = {va[u].x, va[u].y, va[u].z, va[u].w};
+      const uint32_t bv[4] = {vb[u].x, vb[u].y, vb[u].z, vb[u].w};
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        *reinterpret_cast<uint32_t*>(vt + (8 * dg + 2 * w) * kPfVLd + 2 * kp) =
+            (av[w] & 0xffffu) | (bv[w] << 16);
+        *reinterpret_cast<uint32_t*>(vt + (8 * dg + 2 * w + 1) * kPfVLd + 2 * kp) =
+            (av[w] >> 16) | (bv[w] & 0xffff0000u);
+      }
+    }
+    __syncthreads();
+    if (kt + kPfKeys < kend) MX_PF_LOAD(kt + kPfKeys)  // in flight during this tile's work
+    // S = Q K^T: four 16-key columns; lane (j, kq) gets pairs 4 kq + r at key kt + 16 c + j
+    sk::floatx4_t sc[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      sc[c] = sk::floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int k = 0; k < KS; ++k)
+        sc[c] = sk::mfma(qa[k],
+                         *reinterpret_cast<const uint4*>(ks + (16 * c + j) * kPfKLd + 32 * k + 8 * kq),
+                         sc[c]);
+    }
+    // online softmax per pair
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float mt = u2f(0xff800000u);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const bool v = kt + 16 * c + j < lim[r];
+        sc[c][r] = v ? sc[c][r] * sl2 : u2f(0xff800000u);
+        mt = fmaxf(mt, sc[c][r]);
+      }
+#pragma unroll
+      for (int off = 8; off > 0; off >>= 1) mt = fmaxf(mt, __shfl_xor(mt, off, 64));
+      const float mn = fmaxf(m_run[r], mt);
+      const bool none = mn == u2f(0xff800000u);  // no valid key yet
+      const float alpha = none || m_run[r] == u2f(0xff800000u)
+                              ? 0.0f
+                              : __builtin_amdgcn_exp2f(m_run[r] - mn);
+      float ls = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float pv = none || sc[c][r] == u2f(0xff800000u)
+                             ? 0.0f
+                             : __builtin_amdgcn_exp2f(sc[c][r] - mn);
+        sc[c][r] = pv;
+        ls += pv;
+      }
+#pragma unroll
+      for (int off = 8; off > 0; off >>= 1) ls += __shfl_xor(ls, off, 64);
+      l_run[r] = l_run[r] * alpha + ls;
+      m_run[r] = mn;
+#pragma unroll
+      for (int n = 0; n < NO; ++n) o[n][r] *= alpha;
+    }
+    // P (pair 4 kq + r, key 16 c + j) into LDS as bf16 hi and lo
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pv = sc[c][r];
+        const __bf16 h = __bf16(pv);
+        const float hf = float(h);
+        ph[(4 * kq + r) * kPfVLd + 16 * c + j] = __builtin_bit_cast(uint16_t, h);
+        pl[(4 * kq + r) * kPfVLd + 16 * c + j] = __builtin_bit_cast(uint16_t, __bf16(pv - hf));
+      }
+    __syncthreads();
+    // O += P V: A = P (pair j, keys 32 s + 8 kq ..), B = V^T rows (dim 16 n + j)
+#pragma unroll
+    for (int st = 0; st < kPfKeys / 32; ++st) {
+      const uint4 ah = *reinterpret_cast<const uint4*>(ph + j * kPfVLd + 32 * st + 8 * kq);
+      const uint4 al = *reinterpret_cast<const uint4*>(pl + j * kPfVLd + 32 * st + 8 * kq);
+#pragma unroll
+      for (int n = 0; n < NO; ++n) {
+        const uint4 bv = *reinterpret_cast<const uint4*>(vt + (16 * n + j) * kPfVLd + 32 * st + 8 * kq);
+        o[n] = sk::mfma(ah, bv, o[n]);
+        o[n] = sk::mfma(al, bv, o[n]);
+      }
+    }
+  }
+#undef MX_PF_LOAD
+  // partials of this split (chunk index = split)
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int i = 4 * kq + r;
+    const int row = qb0 + wave * RPW + i / G;
+    if (row >= rows) continue;
+    const size_t ph_ = (size_t(row) * d.heads + kvh * G + i % G) * max_chunks + split;
+#pragma unroll
+    for (int n = 0; n < NO; ++n) o_part[ph_ * HD + 16 * n + j] = o[n][r];
+    if (j == 0) {
+      // m in natural-log units, as the decode kernels write it
+      ml_part[ph_ * 2] = m_run[r] * 0.6931471805599453f;
+      ml_part[ph_ * 2 + 1] = l_run[r];
+    }
+  }
 }
 
 }  // namespace
@@ -583,13 +804,55 @@ int attn_combine(const float* o_part, const float* ml_part, const uint16_t* qkv,
   if (fast) {
     if ((d.max_ctx + kAttnFastChunk - 1) / kAttnFastChunk > 256) return MX_EUNSUPPORTED;
     hipLaunchKernelGGL(combine_fast_kernel, dim3(d.heads, rows), dim3(256), 0, s, o_part,
-                       ml_part, qkv, qkv_stride, pos, d, max_chunks, out);
+                       ml_part, qkv, qkv_stride, pos, d, max_chunks, kAttnFastChunk, out);
   } else {
     const bool pl = plane && rows <= 8 && d.head_dim % xq::kGroup == 0;
     hipLaunchKernelGGL(combine_kernel, dim3(d.heads, rows), dim3(kMaxHd), 0, s, o_part, ml_part,
                        qkv, qkv_stride, pos, d, max_chunks, kAttnChunk, out,
                        pl ? plane : nullptr);
   }
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+}
+
+bool attn_prefill_supported(AttnDims d) {
+  if (!attn_fast_supported(d)) return false;
+  const int g = d.heads / d.kv_heads;
+  return (d.head_dim == 256 || d.head_dim == 128) && (g == 2 || g == 4 || g == 8) &&
+         (d.max_ctx + kPfSplit - 1) / kPfSplit <= 256;
+}
+
+int attn_prefill(const uint16_t* q, int rows, const int32_t* slots, const int32_t* pos,
+                 const uint16_t* k_cache, const uint16_t* v_cache, AttnDims d, int max_chunks,
+                 float* o_part, float* ml_part, hipStream_t s) {
+  if (!attn_prefill_supported(d)) return MX_EUNSUPPORTED;
+  const int splits = (d.max_ctx + kPfSplit - 1) / kPfSplit;
+  if (splits > max_chunks) return MX_EINVAL;
+  const float scale = 1.0f / __builtin_sqrtf(float(d.head_dim));
+  const int g = d.heads / d.kv_heads;
+#define MX_PF(GG, HH)                                                                        \
+  if (g == GG && d.head_dim == HH) {                                                         \
+    const auto fn = prefill_attn_kernel<GG, HH>;                                             \
+    constexpr int lb = prefill_attn_lds<HH>();                                               \
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(fn),                               \
+                            hipFuncAttributeMaxDynamicSharedMemorySize, lb) != hipSuccess)   \
+      return MX_EHIP;                                                                        \
+    constexpr int qb = 8 * 16 / GG;                                                          \
+    hipLaunchKernelGGL(fn, dim3(splits, d.kv_heads, (rows + qb - 1) / qb), dim3(512), lb, s, \
+                       q, rows, slots, pos, k_cache, v_cache, d, max_chunks, scale, o_part,  \
+                       ml_part);                                                             \
+    return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;                                \
+  }
+  MX_PF(2, 128) MX_PF(4, 128) MX_PF(8, 128) MX_PF(2, 256) MX_PF(4, 256) MX_PF(8, 256)
+#undef MX_PF
+  return MX_EUNSUPPORTED;
+}
+
+int attn_combine_splits(const float* o_part, const float* ml_part, const uint16_t* qkv,
+                        int64_t qkv_stride, int rows, const int32_t* pos, AttnDims d,
+                        int max_chunks, uint16_t* out, hipStream_t s) {
+  if ((d.max_ctx + kPfSplit - 1) / kPfSplit > 256) return MX_EUNSUPPORTED;
+  hipLaunchKernelGGL(combine_fast_kernel, dim3(d.heads, rows), dim3(256), 0, s, o_part, ml_part,
+                     qkv, qkv_stride, pos, d, max_chunks, kPfSplit, out);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
 }
 

@@ -737,8 +737,20 @@ int record_layer(Engine& e, const LayerW& L, int rows, int groups, int t, bool h
       // a prefill chunk's query rows go through in blocks of kAttnRows, so
       // the per-chunk partials stay sized for kAttnRows rows
       const size_t qd = size_t(c.heads) * c.head_dim;
+      // (more than 8 rows in fast mode: the rows of one slot's chunk, their
+      // query blocks sharing each key tile)
+      const bool prefill = rows > 8 && fast_attn && attn_prefill_supported(e.ad);
       for (int r0 = 0; r0 < rows; r0 += kAttnRows) {
         const int n = rows - r0 < kAttnRows ? rows - r0 : kAttnRows;
+        if (prefill) {
+          MX_TRY(attn_prefill(e.qrot + r0 * qd, n, rt->slots + r0, rt->pos + r0,
+                              e.k_cache + layer_off, e.v_cache + layer_off, e.ad, e.max_chunks,
+                              e.o_part, e.ml_part, e.stream));
+          MX_TRY(attn_combine_splits(e.o_part, e.ml_part, e.pbuf + size_t(r0) * e.Q, e.Q, n,
+                                     rt->pos + r0, e.ad, e.max_chunks, e.y + r0 * qd,
+                                     e.stream));
+          continue;
+        }
         MX_TRY(attn_decode(e.qrot + r0 * qd, n, rt->slots + r0, rt->pos + r0,
                            e.k_cache + layer_off, e.v_cache + layer_off, e.ad, e.max_chunks,
                            fast_attn, e.o_part, e.ml_part, e.stream));

@@ -191,6 +191,16 @@ int attn_combine(const float* o_part, const float* ml_part, const uint16_t* qkv,
                  bool fast, uint16_t* out, hipStream_t s, char* plane = nullptr);
 constexpr int kAttnChunk = 256;
 constexpr int kAttnFastChunk = 64;
+// Prefill (fast mode): query rows of one slot in blocks that share each key
+// tile, one partial per (row, head) and split of 256 keys at chunk index =
+// split; attn_combine_splits merges them (and applies the output gate).
+bool attn_prefill_supported(AttnDims d);
+int attn_prefill(const uint16_t* q, int rows, const int32_t* slots, const int32_t* pos,
+                 const uint16_t* k_cache, const uint16_t* v_cache, AttnDims d, int max_chunks,
+                 float* o_part, float* ml_part, hipStream_t s);
+int attn_combine_splits(const float* o_part, const float* ml_part, const uint16_t* qkv,
+                        int64_t qkv_stride, int rows, const int32_t* pos, AttnDims d,
+                        int max_chunks, uint16_t* out, hipStream_t s);
 constexpr int kAttnRows = 128;  // query rows per attention launch of a prefill chunk
 
 // ---- MoE ----
