@@ -439,6 +439,11 @@ mx_status mx_gemv_bf16(const uint16_t* w, int32_t n, int32_t k, const uint16_t* 
  * [slot][kv_head][max_ctx][head_dim] with slot_stride elements between slots.
  * flags bit 0: the matrix-core kernel (fp32 sums in another order, within
  * tolerance) instead of the fixed-order kernel that the CPU oracle restates.
+ * flags bit 1: the matrix-core prefill form (within the same tolerance) for
+ * the rows of one slot's prompt chunk: blocks of 8 * 16 / (heads / kv_heads)
+ * rows share each 64-key tile, with partials per 256-key split; every row
+ * must name the same slot; needs head_dim 128 or 256 and 2, 4 or 8 q heads
+ * per kv head (MX_EUNSUPPORTED otherwise).
  * workspace: mx_attn_workspace_bytes(rows, heads, head_dim, max_ctx) bytes.
  * Replaces the fast::scaled_dot_product_attention call and output gate of
  * Attention::forward_selection (src/dense.rs:139-270, 249-256). */

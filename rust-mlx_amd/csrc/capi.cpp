@@ -502,6 +502,14 @@ MX_ABI mx_status mx_attn_decode(const uint16_t* q, const uint16_t* qkv, int64_t 
   float* o_part = static_cast<float*>(workspace);
   float* ml_part = o_part + size_t(rows) * d.heads * chunks * d.head_dim;
   const hipStream_t s = hipStream_t(stream);
+  if (flags & 2) {  // the prefill form: rows of one slot, query blocks sharing key tiles
+    MX_CHECK(attn_prefill_supported(d), MX_EUNSUPPORTED,
+             "mx_attn_decode: prefill form needs head_dim 128/256 and 2, 4 or 8 q heads per kv head");
+    int rc = attn_prefill(q, rows, slots, pos, k_cache, v_cache, d, chunks, o_part, ml_part, s);
+    if (rc == MX_OK)
+      rc = attn_combine_splits(o_part, ml_part, qkv, qkv_stride, rows, pos, d, chunks, out, s);
+    return finish(rc, "mx_attn_decode");
+  }
   int rc = attn_decode(q, rows, slots, pos, k_cache, v_cache, d, chunks, fast, o_part, ml_part, s);
   if (rc == MX_OK)
     rc = attn_combine(o_part, ml_part, qkv, qkv_stride, rows, pos, d, chunks, fast, out, s);
