@@ -535,6 +535,7 @@ __global__ __launch_bounds__(256) void combine_fast_kernel(const float* __restri
 // one query block must share a slot (a prefill chunk's rows do).
 constexpr int kPfKeys = 64;     // keys per tile
 constexpr int kPfSplit = 256;   // keys per split (one partial per pair and split)
+static_assert(attn_prefill_splits(kPfSplit + 1) == 2, "attn_prefill_splits counts kPfSplit keys");
 constexpr int kPfKLd = kMaxHd + 8;      // padded K row in LDS (bf16)
 constexpr int kPfVLd = kPfKeys + 8;     // padded transposed-V row (bf16)
 

@@ -494,9 +494,12 @@ int build(Engine& e) {
   MX_TRY(alloc(e, "act.ids", R * c.top_k * 4, &v));
   e.ids = static_cast<uint32_t*>(v);
   const size_t AR = R < size_t(kAttnRows) ? R : size_t(kAttnRows);  // attention rows per launch
-  MX_TRY(alloc(e, "act.o_part", AR * c.heads * e.max_chunks * c.head_dim * 4, &v));
+  // partials per (row, head): decode chunks for AR rows, or the prefill
+  // form's splits for all R rows of a chunk in one launch
+  const size_t parts = std::max(AR * e.max_chunks, R * size_t(attn_prefill_splits(c.max_context)));
+  MX_TRY(alloc(e, "act.o_part", parts * c.heads * c.head_dim * 4, &v));
   e.o_part = static_cast<float*>(v);
-  MX_TRY(alloc(e, "act.ml_part", AR * c.heads * e.max_chunks * 2 * 4, &v));
+  MX_TRY(alloc(e, "act.ml_part", parts * c.heads * 2 * 4, &v));
   e.ml_part = static_cast<float*>(v);
   size_t hws = size_t(head_parts(c.vocab, c.hidden)) * 8 * 8;
   MX_TRY(alloc(e, "act.head_ws", hws, &e.head_ws));
@@ -734,23 +737,21 @@ int record_layer(Engine& e, const LayerW& L, int rows, int groups, int t, bool h
                        e.v_cache + layer_off, e.stream));
       const bool fast_attn = !ex(e, kExAttn) && attn_fast_supported(e.ad);
       char* yp = !fast_attn && ex(e, kExAttnProj) && rows <= 8 ? e.y_plane : nullptr;
-      // a prefill chunk's query rows go through in blocks of kAttnRows, so
-      // the per-chunk partials stay sized for kAttnRows rows
       const size_t qd = size_t(c.heads) * c.head_dim;
-      // (more than 8 rows in fast mode: the rows of one slot's chunk, their
-      // query blocks sharing each key tile)
+      // more than 8 rows in fast mode: the rows of one slot's chunk in one
+      // launch, their query blocks sharing each key tile; otherwise rows go
+      // through in blocks of kAttnRows, so the per-chunk partials stay sized
+      // for kAttnRows rows
       const bool prefill = rows > 8 && fast_attn && attn_prefill_supported(e.ad);
-      for (int r0 = 0; r0 < rows; r0 += kAttnRows) {
+      if (prefill) {
+        const int splits = attn_prefill_splits(c.max_context);
+        MX_TRY(attn_prefill(e.qrot, rows, rt->slots, rt->pos, e.k_cache + layer_off,
+                            e.v_cache + layer_off, e.ad, splits, e.o_part, e.ml_part, e.stream));
+        MX_TRY(attn_combine_splits(e.o_part, e.ml_part, e.pbuf, e.Q, rows, rt->pos, e.ad, splits,
+                                   e.y, e.stream));
+      }
+      for (int r0 = 0; r0 < rows && !prefill; r0 += kAttnRows) {
         const int n = rows - r0 < kAttnRows ? rows - r0 : kAttnRows;
-        if (prefill) {
-          MX_TRY(attn_prefill(e.qrot + r0 * qd, n, rt->slots + r0, rt->pos + r0,
-                              e.k_cache + layer_off, e.v_cache + layer_off, e.ad, e.max_chunks,
-                              e.o_part, e.ml_part, e.stream));
-          MX_TRY(attn_combine_splits(e.o_part, e.ml_part, e.pbuf + size_t(r0) * e.Q, e.Q, n,
-                                     rt->pos + r0, e.ad, e.max_chunks, e.y + r0 * qd,
-                                     e.stream));
-          continue;
-        }
         MX_TRY(attn_decode(e.qrot + r0 * qd, n, rt->slots + r0, rt->pos + r0,
                            e.k_cache + layer_off, e.v_cache + layer_off, e.ad, e.max_chunks,
                            fast_attn, e.o_part, e.ml_part, e.stream));

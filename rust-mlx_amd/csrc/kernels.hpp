@@ -195,6 +195,7 @@ constexpr int kAttnFastChunk = 64;
 // tile, one partial per (row, head) and split of 256 keys at chunk index =
 // split; attn_combine_splits merges them (and applies the output gate).
 bool attn_prefill_supported(AttnDims d);
+constexpr int attn_prefill_splits(int max_ctx) { return (max_ctx + 255) / 256; }
 int attn_prefill(const uint16_t* q, int rows, const int32_t* slots, const int32_t* pos,
                  const uint16_t* k_cache, const uint16_t* v_cache, AttnDims d, int max_chunks,
                  float* o_part, float* ml_part, hipStream_t s);
