@@ -618,7 +618,10 @@ __device__ __forceinline__ ChunkItem chunk_item(const ChunkPlan* __restrict__ pl
 // rows of the up matrix (four tiles sharing the activation operands and their
 // group sums) over the whole depth, so a workgroup streams 128 rows of each
 // matrix and the item's plan is read once per 256 KB of 4-bit weights.
-template <int BITS>
+// SX: the item's rows pass through LDS once per batch of four groups for the
+// four waves (qmm_tiles_sx) instead of every wave reading them; every wave
+// then takes part in the batches' barriers, past the matrix's rows too.
+template <int BITS, bool SX>
 __global__ __launch_bounds__(256) void chunk_gate_up_kernel(const uint16_t* __restrict__ x,
                                                             const ChunkPlan* __restrict__ plan,
                                                             int top_k, QBank gate, QBank up,
@@ -633,7 +636,7 @@ __global__ __launch_bounds__(256) void chunk_gate_up_kernel(const uint16_t* __re
   const int j = lane & 15, kq = lane >> 4;
   const int inter = gw.n;
   const int base = (blockIdx.x * 4 + wave) * 32;
-  if (base >= inter) return;
+  if (!SX && base >= inter) return;
   const int r0 = min(base + j, inter - 1), r1 = min(base + 16 + j, inter - 1);
   const TileRow tr[4] = {tile_row(gw.codes, gw.scales, gw.biases, hidden, BITS, r0),
                          tile_row(gw.codes, gw.scales, gw.biases, hidden, BITS, r1),
@@ -642,8 +645,17 @@ __global__ __launch_bounds__(256) void chunk_gate_up_kernel(const uint16_t* __re
   floatx4_t y[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) y[t] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  const uint16_t* xa = j < it.m ? x + size_t(it.row) * hidden : nullptr;
-  qmm_tiles<BITS, 4>(tr, xa, 0, hidden >> 6, y);
+  if constexpr (SX) {
+    __shared__ __align__(16) uint16_t xs[16 * kSxLd];
+    const int sr = threadIdx.x >> 4;  // the member this thread stages (lane sr holds its row)
+    const int srow = __shfl(it.row, sr, 64);
+    qmm_tiles_sx<BITS, 4, 256>(tr, sr < it.m ? x + size_t(srow) * hidden : nullptr, xs,
+                               j < it.m ? j : -1, 0, hidden >> 6, y);
+    if (base >= inter) return;
+  } else {
+    const uint16_t* xa = j < it.m ? x + size_t(it.row) * hidden : nullptr;
+    qmm_tiles<BITS, 4>(tr, xa, 0, hidden >> 6, y);
+  }
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int c = base + 16 * t + j;
@@ -661,7 +673,7 @@ __global__ __launch_bounds__(256) void chunk_gate_up_kernel(const uint16_t* __re
 
 // down: wave w takes 64 rows (four tiles) over the whole depth; a workgroup
 // streams 256 rows of the expert's down matrix.
-template <int BITS>
+template <int BITS, bool SX>
 __global__ __launch_bounds__(256) void chunk_down_kernel(const uint16_t* __restrict__ h,
                                                          const ChunkPlan* __restrict__ plan,
                                                          const uint16_t* __restrict__ scores,
@@ -674,7 +686,7 @@ __global__ __launch_bounds__(256) void chunk_down_kernel(const uint16_t* __restr
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 15, kq = lane >> 4;
   const int base = (blockIdx.x * 4 + wave) * 64;
-  if (base >= hidden) return;
+  if (!SX && base >= hidden) return;
   TileRow tr[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t)
@@ -682,8 +694,18 @@ __global__ __launch_bounds__(256) void chunk_down_kernel(const uint16_t* __restr
   floatx4_t y[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) y[t] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  const uint16_t* xa = j < it.m ? h + (size_t(it.row) * (top_k + 1) + it.slot) * hs : nullptr;
-  qmm_tiles<BITS, 4>(tr, xa, 0, inter >> 6, y);
+  if constexpr (SX) {
+    __shared__ __align__(16) uint16_t xs[16 * kSxLd];
+    const int sr = threadIdx.x >> 4;  // the member this thread stages (lane sr holds it)
+    const int srow = __shfl(it.row, sr, 64), sslot = __shfl(it.slot, sr, 64);
+    qmm_tiles_sx<BITS, 4, 256>(
+        tr, sr < it.m ? h + (size_t(srow) * (top_k + 1) + sslot) * hs : nullptr, xs,
+        j < it.m ? j : -1, 0, inter >> 6, y);
+    if (base >= hidden) return;
+  } else {
+    const uint16_t* xa = j < it.m ? h + (size_t(it.row) * (top_k + 1) + it.slot) * hs : nullptr;
+    qmm_tiles<BITS, 4>(tr, xa, 0, inter >> 6, y);
+  }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     if (4 * kq + r >= it.m) continue;
@@ -777,11 +799,16 @@ int qmm_chunk_gate_up(const uint16_t* x, const ChunkPlan* plan, int rows, int ex
                       const QWeight& sup, uint16_t* h, hipStream_t s) {
   const int hs = gate.n > sgate.n ? gate.n : sgate.n;
   const dim3 grid((hs + 127) / 128, chunk_max_items(rows, experts, top_k));
+  const bool sx = (gate.k >> 6) % 4 == 0;  // whole batches of four groups
   switch (gate.bits) {
-#define MX_GU(B)                                                                          \
-  case B:                                                                                 \
-    hipLaunchKernelGGL((chunk_gate_up_kernel<B>), grid, dim3(256), 0, s, x, plan, top_k,  \
-                       gate, up, sgate, sup, h, hs);                                      \
+#define MX_GU(B)                                                                              \
+  case B:                                                                                     \
+    if (sx)                                                                                   \
+      hipLaunchKernelGGL((chunk_gate_up_kernel<B, true>), grid, dim3(256), 0, s, x, plan,     \
+                         top_k, gate, up, sgate, sup, h, hs);                                 \
+    else                                                                                      \
+      hipLaunchKernelGGL((chunk_gate_up_kernel<B, false>), grid, dim3(256), 0, s, x, plan,    \
+                         top_k, gate, up, sgate, sup, h, hs);                                 \
     break;
     MX_GU(4) MX_GU(5) MX_GU(6) MX_GU(8)
 #undef MX_GU
@@ -795,11 +822,16 @@ int qmm_chunk_down(const uint16_t* h, const ChunkPlan* plan, const uint16_t* sco
                    const QWeight& sdown, uint16_t* p, hipStream_t s) {
   const int hs = inter > shared_inter ? inter : shared_inter;
   const dim3 grid((down.n + 255) / 256, chunk_max_items(rows, experts, top_k));
+  const bool sx = (down.k >> 6) % 4 == 0 && (sdown.k >> 6) % 4 == 0;
   switch (down.bits) {
-#define MX_DN(B)                                                                             \
-  case B:                                                                                    \
-    hipLaunchKernelGGL((chunk_down_kernel<B>), grid, dim3(256), 0, s, h, plan, scores, top_k, \
-                       down, sdown, p, hs);                                                  \
+#define MX_DN(B)                                                                              \
+  case B:                                                                                     \
+    if (sx)                                                                                   \
+      hipLaunchKernelGGL((chunk_down_kernel<B, true>), grid, dim3(256), 0, s, h, plan, scores, \
+                         top_k, down, sdown, p, hs);                                          \
+    else                                                                                      \
+      hipLaunchKernelGGL((chunk_down_kernel<B, false>), grid, dim3(256), 0, s, h, plan,       \
+                         scores, top_k, down, sdown, p, hs);                                  \
     break;
     MX_DN(4) MX_DN(5) MX_DN(6) MX_DN(8)
 #undef MX_DN

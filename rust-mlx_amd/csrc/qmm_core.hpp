@@ -237,4 +237,90 @@ __device__ __forceinline__ void qmm_tiles(const TileRow (&tr)[NT], const uint16_
   }
 }
 
+// qmm_tiles for a workgroup of NTH threads whose waves all multiply the same
+// 16 activation rows over the same groups [g0, g1), (g1 - g0) % 4 == 0: the
+// rows pass through LDS once per batch of four groups instead of every wave
+// reading them.  Thread t copies 32 bytes of row t / 16 (`xrow`, nullptr for
+// a row beyond M) per batch, the next batch's piece in flight during this
+// batch's work; `xs` holds one batch (16 rows of 256 values, rows padded to
+// kSxLd so the lanes of one ds_read_b128 pass hit different bank groups);
+// `lrow` is the row this lane's A operand takes (lane % 16), or -1 for zeros.
+// Every wave of the workgroup must call it (it synchronises the workgroup).
+constexpr int kSxLd = 256 + 8;
+
+template <int BITS, int NT, int NTH>
+__device__ __forceinline__ void qmm_tiles_sx(const TileRow (&tr)[NT], const uint16_t* xrow,
+                                             uint16_t* xs, int lrow, int g0, int g1,
+                                             floatx4_t (&y)[NT]) {
+  static_assert(NTH == 256, "16 rows x 16 pieces of 32 bytes per batch");
+  constexpr int GB = 4;
+  constexpr int NW = group_words<BITS>();
+  const int lane = threadIdx.x & 63;
+  const int kq = lane >> 4;
+  const float off = code_offset<BITS>();
+  const uint4 ones = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
+  const int sr = threadIdx.x >> 4, pc = threadIdx.x & 15;  // staged row, 32-byte piece
+  uint4 xn0 = make_uint4(0u, 0u, 0u, 0u), xn1 = xn0;
+  auto load_piece = [&](int g) {
+    if (xrow) {
+      const uint4* p = reinterpret_cast<const uint4*>(xrow + 64 * g + 16 * pc);
+      xn0 = p[0];
+      xn1 = p[1];
+    }
+  };
+  load_piece(g0);
+  for (int g = g0; g < g1; g += GB) {
+    __syncthreads();  // every wave is done with the previous batch's rows
+    *reinterpret_cast<uint4*>(xs + sr * kSxLd + 16 * pc) = xn0;
+    *reinterpret_cast<uint4*>(xs + sr * kSxLd + 16 * pc + 8) = xn1;
+    if (g + GB < g1) load_piece(g + GB);  // in flight during this batch
+    uint32_t w[GB][NT][NW];
+    uint2 sc2[NT], bi2[NT];
+#pragma unroll
+    for (int b = 0; b < GB; ++b)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) load_group_codes<BITS>(tr[t].codes, g + b, kq, w[b][t]);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      if ((reinterpret_cast<uintptr_t>(tr[t].scales + g) & 7u) == 0 &&
+          (reinterpret_cast<uintptr_t>(tr[t].biases + g) & 7u) == 0) {
+        sc2[t] = *reinterpret_cast<const uint2*>(tr[t].scales + g);
+        bi2[t] = *reinterpret_cast<const uint2*>(tr[t].biases + g);
+      } else {
+        sc2[t] = make_uint2(uint32_t(tr[t].scales[g]) | (uint32_t(tr[t].scales[g + 1]) << 16),
+                            uint32_t(tr[t].scales[g + 2]) | (uint32_t(tr[t].scales[g + 3]) << 16));
+        bi2[t] = make_uint2(uint32_t(tr[t].biases[g]) | (uint32_t(tr[t].biases[g + 1]) << 16),
+                            uint32_t(tr[t].biases[g + 2]) | (uint32_t(tr[t].biases[g + 3]) << 16));
+      }
+    }
+    __syncthreads();  // the batch's rows are in LDS
+#pragma unroll
+    for (int b = 0; b < GB; ++b) {
+      uint4 x0 = make_uint4(0u, 0u, 0u, 0u), x1 = x0;
+      if (lrow >= 0) {
+        const uint4* xp = reinterpret_cast<const uint4*>(xs + lrow * kSxLd + 64 * b + 16 * kq);
+        x0 = xp[0];
+        x1 = xp[1];
+      }
+      const uint4 a0 = permute_x(x0);
+      const uint4 a1 = permute_x(x1);
+      floatx4_t sx = {0.0f, 0.0f, 0.0f, 0.0f};
+      sx = mfma_bf16(a0, ones, sx);
+      sx = mfma_bf16(a1, ones, sx);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const uint32_t sw = b < 2 ? sc2[t].x : sc2[t].y;
+        const uint32_t bw = b < 2 ? bi2[t].x : bi2[t].y;
+        const float sc = u2f((b & 1) ? (sw & 0xffff0000u) : (sw << 16));
+        const float bi = fmaf_(-off, sc, u2f((b & 1) ? (bw & 0xffff0000u) : (bw << 16)));
+        floatx4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        acc = mfma_bf16(a0, codes_operand<BITS, 0>(w[b][t]), acc);
+        acc = mfma_bf16(a1, codes_operand<BITS, 1>(w[b][t]), acc);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y[t][r] = fmaf_(sc, acc[r], fmaf_(bi, sx[r], y[t][r]));
+      }
+    }
+  }
+}
+
 }  // namespace mx
