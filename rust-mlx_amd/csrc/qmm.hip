@@ -671,6 +671,53 @@ __global__ __launch_bounds__(256) void chunk_gate_up_kernel(const uint16_t* __re
   }
 }
 
+// The 4-bit gate/up on 32-row tiles (qmm_tiles32_sx): wave w takes gate and
+// up rows base .. base + 31, lane l the row base + l % 32 of both; lane l
+// holds activation rows 8 (i / 4) + 4 (l / 32) + i % 4 (i < 8) of its column.
+__global__ __launch_bounds__(256) void chunk_gate_up32_kernel(const uint16_t* __restrict__ x,
+                                                              const ChunkPlan* __restrict__ plan,
+                                                              int top_k, QBank gate, QBank up,
+                                                              QWeight sgate, QWeight sup,
+                                                              uint16_t* __restrict__ h, int hs) {
+  if (int(blockIdx.y) >= plan->nitems) return;
+  const ChunkItem it = chunk_item(plan, blockIdx.y);
+  const QWeight gw = expert_weight(gate, it.expert, sgate);
+  const QWeight uw = expert_weight(up, it.expert, sup);
+  const int hidden = gate.k;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 31, hf = lane >> 5;
+  const int inter = gw.n;
+  const int base = (blockIdx.x * 4 + wave) * 32;
+  const int r0 = min(base + j, inter - 1);
+  const TileRow tr[2] = {tile_row(gw.codes, gw.scales, gw.biases, hidden, 4, r0),
+                         tile_row(uw.codes, uw.scales, uw.biases, hidden, 4, r0)};
+  // the members of this lane's activation rows (lane m % 16 holds member m)
+  int er[8], es[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int ar = 8 * (i >> 2) + 4 * hf + (i & 3);
+    er[i] = __shfl(it.row, ar, 64);
+    es[i] = __shfl(it.slot, ar, 64);
+  }
+  floatx16_t y[2] = {{}, {}};
+  __shared__ __align__(16) uint16_t xs[16 * kSxLd];
+  const int sr = threadIdx.x >> 4;  // the member this thread stages (lane sr holds its row)
+  const int srow = __shfl(it.row, sr, 64);
+  qmm_tiles32_sx<2, 256>(tr, sr < it.m ? x + size_t(srow) * hidden : nullptr, xs,
+                         (lane & 31) < it.m ? (lane & 31) : -1, 0, hidden >> 6, y);
+  const int c = base + j;
+  if (c >= inter) return;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int ar = 8 * (i >> 2) + 4 * hf + (i & 3);
+    if (ar >= it.m) continue;
+    const float gv = round_bf16(y[0][i]);
+    const float uv = round_bf16(y[1][i]);
+    const float silu = round_bf16(gv * sigmoid_bf16(gv));
+    h[(size_t(er[i]) * (top_k + 1) + es[i]) * hs + c] = f32_to_bf16(silu * uv);
+  }
+}
+
 // down: wave w takes 64 rows (four tiles) over the whole depth; a workgroup
 // streams 256 rows of the expert's down matrix.
 template <int BITS, bool SX>
@@ -800,6 +847,11 @@ int qmm_chunk_gate_up(const uint16_t* x, const ChunkPlan* plan, int rows, int ex
   const int hs = gate.n > sgate.n ? gate.n : sgate.n;
   const dim3 grid((hs + 127) / 128, chunk_max_items(rows, experts, top_k));
   const bool sx = (gate.k >> 6) % 4 == 0;  // whole batches of four groups
+  if (sx && gate.bits == 4) {  // 32-row tiles, 16-byte code reads per lane
+    hipLaunchKernelGGL(chunk_gate_up32_kernel, grid, dim3(256), 0, s, x, plan, top_k, gate, up,
+                       sgate, sup, h, hs);
+    return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+  }
   switch (gate.bits) {
 #define MX_GU(B)                                                                              \
   case B:                                                                                     \

@@ -323,4 +323,104 @@ __device__ __forceinline__ void qmm_tiles_sx(const TileRow (&tr)[NT], const uint
   }
 }
 
+// The 4-bit form of qmm_tiles_sx on v_mfma_f32_32x32x16_bf16, tiles of 32
+// weight rows: lane l takes weight row l % 32 and, in MFMA step s of a
+// group, values 32 h + 8 s .. + 7 of it (h = l / 32) on both operands, so its
+// codes of a group are 16 contiguous bytes (one load; the 16x16 form reads
+// 8 bytes per lane per 16-row tile).  Activation rows 16..31 of the 32-row
+// A tile are zero, so D values i < 8 (rows 8 (i / 4) + 4 h + i % 4) are the
+// real ones and only they are scaled; the arithmetic per product and group
+// is qmm_tiles' (fp32 sums inside the matrix core in another order).
+typedef float floatx16_t __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ floatx16_t mfma32_bf16(const uint4& a, const uint4& b, floatx16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// One 32-bit word of 8 nibble codes as a B operand in permute_x order.
+__device__ __forceinline__ uint4 nibble_operand(uint32_t x) {
+  uint4 r;
+  r.x = (x & 0x000F000Fu) | 0x43004300u;
+  r.y = ((x >> 4) & 0x000F000Fu) | 0x43004300u;
+  r.z = ((x >> 8) & 0x000F000Fu) | 0x43004300u;
+  r.w = ((x >> 12) & 0x000F000Fu) | 0x43004300u;
+  return r;
+}
+
+template <int NT, int NTH>
+__device__ __forceinline__ void qmm_tiles32_sx(const TileRow (&tr)[NT], const uint16_t* xrow,
+                                               uint16_t* xs, int lrow, int g0, int g1,
+                                               floatx16_t (&y)[NT]) {
+  static_assert(NTH == 256, "16 rows x 16 pieces of 32 bytes per batch");
+  constexpr int GB = 4;
+  const int lane = threadIdx.x & 63;
+  const int h = lane >> 5;
+  const uint4 ones = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
+  const int sr = threadIdx.x >> 4, pc = threadIdx.x & 15;
+  uint4 xn0 = make_uint4(0u, 0u, 0u, 0u), xn1 = xn0;
+  auto load_piece = [&](int g) {
+    if (xrow) {
+      const uint4* p = reinterpret_cast<const uint4*>(xrow + 64 * g + 16 * pc);
+      xn0 = p[0];
+      xn1 = p[1];
+    }
+  };
+  load_piece(g0);
+  for (int g = g0; g < g1; g += GB) {
+    __syncthreads();  // every wave is done with the previous batch's rows
+    *reinterpret_cast<uint4*>(xs + sr * kSxLd + 16 * pc) = xn0;
+    *reinterpret_cast<uint4*>(xs + sr * kSxLd + 16 * pc + 8) = xn1;
+    if (g + GB < g1) load_piece(g + GB);  // in flight during this batch
+    uint4 w[GB][NT];
+    uint2 sc2[NT], bi2[NT];
+#pragma unroll
+    for (int b = 0; b < GB; ++b)
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        w[b][t] = *reinterpret_cast<const uint4*>(tr[t].codes + 8 * (g + b) + 4 * h);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      if ((reinterpret_cast<uintptr_t>(tr[t].scales + g) & 7u) == 0 &&
+          (reinterpret_cast<uintptr_t>(tr[t].biases + g) & 7u) == 0) {
+        sc2[t] = *reinterpret_cast<const uint2*>(tr[t].scales + g);
+        bi2[t] = *reinterpret_cast<const uint2*>(tr[t].biases + g);
+      } else {
+        sc2[t] = make_uint2(uint32_t(tr[t].scales[g]) | (uint32_t(tr[t].scales[g + 1]) << 16),
+                            uint32_t(tr[t].scales[g + 2]) | (uint32_t(tr[t].scales[g + 3]) << 16));
+        bi2[t] = make_uint2(uint32_t(tr[t].biases[g]) | (uint32_t(tr[t].biases[g + 1]) << 16),
+                            uint32_t(tr[t].biases[g + 2]) | (uint32_t(tr[t].biases[g + 3]) << 16));
+      }
+    }
+    __syncthreads();  // the batch's rows are in LDS
+#pragma unroll
+    for (int b = 0; b < GB; ++b) {
+      uint4 a[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        uint4 xv = make_uint4(0u, 0u, 0u, 0u);
+        if (lrow >= 0)
+          xv = *reinterpret_cast<const uint4*>(xs + lrow * kSxLd + 64 * b + 32 * h + 8 * s);
+        a[s] = permute_x(xv);
+      }
+      floatx16_t sx = {};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) sx = mfma32_bf16(a[s], ones, sx);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const uint32_t sw = b < 2 ? sc2[t].x : sc2[t].y;
+        const uint32_t bw = b < 2 ? bi2[t].x : bi2[t].y;
+        const float sc = u2f((b & 1) ? (sw & 0xffff0000u) : (sw << 16));
+        const float bi = fmaf_(-128.0f, sc, u2f((b & 1) ? (bw & 0xffff0000u) : (bw << 16)));
+        const uint32_t cw[4] = {w[b][t].x, w[b][t].y, w[b][t].z, w[b][t].w};
+        floatx16_t acc = {};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc = mfma32_bf16(a[s], nibble_operand(cw[s]), acc);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) y[t][i] = fmaf_(sc, acc[i], fmaf_(bi, sx[i], y[t][i]));
+      }
+    }
+  }
+}
+
 }  // namespace mx
