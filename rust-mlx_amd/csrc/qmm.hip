@@ -671,9 +671,10 @@ __global__ __launch_bounds__(256) void chunk_gate_up_kernel(const uint16_t* __re
   }
 }
 
-// The 4-bit gate/up on 32-row tiles (qmm_tiles32_sx): wave w takes gate and
+// The gate/up on 32-row tiles (qmm_tiles32_sx): wave w takes gate and
 // up rows base .. base + 31, lane l the row base + l % 32 of both; lane l
 // holds activation rows 8 (i / 4) + 4 (l / 32) + i % 4 (i < 8) of its column.
+template <int BITS>
 __global__ __launch_bounds__(256) void chunk_gate_up32_kernel(const uint16_t* __restrict__ x,
                                                               const ChunkPlan* __restrict__ plan,
                                                               int top_k, QBank gate, QBank up,
@@ -689,8 +690,8 @@ __global__ __launch_bounds__(256) void chunk_gate_up32_kernel(const uint16_t* __
   const int inter = gw.n;
   const int base = (blockIdx.x * 4 + wave) * 32;
   const int r0 = min(base + j, inter - 1);
-  const TileRow tr[2] = {tile_row(gw.codes, gw.scales, gw.biases, hidden, 4, r0),
-                         tile_row(uw.codes, uw.scales, uw.biases, hidden, 4, r0)};
+  const TileRow tr[2] = {tile_row(gw.codes, gw.scales, gw.biases, hidden, BITS, r0),
+                         tile_row(uw.codes, uw.scales, uw.biases, hidden, BITS, r0)};
   // the members of this lane's activation rows (lane m % 16 holds member m)
   int er[8], es[8];
 #pragma unroll
@@ -703,7 +704,7 @@ __global__ __launch_bounds__(256) void chunk_gate_up32_kernel(const uint16_t* __
   __shared__ __align__(16) uint16_t xs[16 * kSxLd];
   const int sr = threadIdx.x >> 4;  // the member this thread stages (lane sr holds its row)
   const int srow = __shfl(it.row, sr, 64);
-  qmm_tiles32_sx<2, 256>(tr, sr < it.m ? x + size_t(srow) * hidden : nullptr, xs,
+  qmm_tiles32_sx<BITS, 2, 256>(tr, sr < it.m ? x + size_t(srow) * hidden : nullptr, xs,
                          (lane & 31) < it.m ? (lane & 31) : -1, 0, hidden >> 6, y);
   const int c = base + j;
   if (c >= inter) return;
@@ -715,6 +716,55 @@ __global__ __launch_bounds__(256) void chunk_gate_up32_kernel(const uint16_t* __
     const float uv = round_bf16(y[1][i]);
     const float silu = round_bf16(gv * sigmoid_bf16(gv));
     h[(size_t(er[i]) * (top_k + 1) + es[i]) * hs + c] = f32_to_bf16(silu * uv);
+  }
+}
+
+// The down on 32-row tiles (qmm_tiles32_sx): wave w takes rows base .. base +
+// 63 as two tiles, lane l rows base + 32 t + l % 32.
+template <int BITS>
+__global__ __launch_bounds__(256) void chunk_down32_kernel(const uint16_t* __restrict__ h,
+                                                           const ChunkPlan* __restrict__ plan,
+                                                           const uint16_t* __restrict__ scores,
+                                                           int top_k, QBank down, QWeight sdown,
+                                                           uint16_t* __restrict__ p, int hs) {
+  if (int(blockIdx.y) >= plan->nitems) return;
+  const ChunkItem it = chunk_item(plan, blockIdx.y);
+  const QWeight dw = expert_weight(down, it.expert, sdown);
+  const int hidden = dw.n, inter = dw.k;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 31, hf = lane >> 5;
+  const int base = (blockIdx.x * 4 + wave) * 64;
+  TileRow tr[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+    tr[t] = tile_row(dw.codes, dw.scales, dw.biases, inter, BITS, min(base + 32 * t + j, hidden - 1));
+  int er[8], es[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int ar = 8 * (i >> 2) + 4 * hf + (i & 3);
+    er[i] = __shfl(it.row, ar, 64);
+    es[i] = __shfl(it.slot, ar, 64);
+  }
+  floatx16_t y[2] = {{}, {}};
+  __shared__ __align__(16) uint16_t xs[16 * kSxLd];
+  const int sr = threadIdx.x >> 4;  // the member this thread stages (lane sr holds it)
+  const int srow = __shfl(it.row, sr, 64), sslot = __shfl(it.slot, sr, 64);
+  qmm_tiles32_sx<BITS, 2, 256>(
+      tr, sr < it.m ? h + (size_t(srow) * (top_k + 1) + sslot) * hs : nullptr, xs,
+      j < it.m ? j : -1, 0, inter >> 6, y);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int ar = 8 * (i >> 2) + 4 * hf + (i & 3);
+    if (ar >= it.m) continue;
+    const bool routed = es[i] < top_k;
+    const float sc = routed ? bf16_to_f32(scores[size_t(er[i]) * top_k + es[i]]) : 1.0f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int c = base + 32 * t + j;
+      if (c >= hidden) continue;
+      const float dv = round_bf16(y[t][i]);
+      p[(size_t(er[i]) * (top_k + 1) + es[i]) * hidden + c] = f32_to_bf16(routed ? dv * sc : dv);
+    }
   }
 }
 
@@ -841,15 +891,24 @@ int qmm_down(const uint16_t* h, const MoePlan* plan, const uint16_t* scores, int
   return MX_EUNSUPPORTED;
 }
 
+// The 32-row tile forms (4- and 8-bit codes, whole batches of four groups).
+bool chunk_w32_ok(int bits, int k) { return (bits == 4 || bits == 8) && (k >> 6) % 4 == 0; }
+
 int qmm_chunk_gate_up(const uint16_t* x, const ChunkPlan* plan, int rows, int experts, int top_k,
                       const QBank& gate, const QBank& up, const QWeight& sgate,
                       const QWeight& sup, uint16_t* h, hipStream_t s) {
   const int hs = gate.n > sgate.n ? gate.n : sgate.n;
   const dim3 grid((hs + 127) / 128, chunk_max_items(rows, experts, top_k));
   const bool sx = (gate.k >> 6) % 4 == 0;  // whole batches of four groups
-  if (sx && gate.bits == 4) {  // 32-row tiles, 16-byte code reads per lane
-    hipLaunchKernelGGL(chunk_gate_up32_kernel, grid, dim3(256), 0, s, x, plan, top_k, gate, up,
-                       sgate, sup, h, hs);
+  if (sx && gate.bits == sgate.bits && chunk_w32_ok(gate.bits, gate.k) &&
+      chunk_w32_ok(sgate.bits, sgate.k)) {
+    // 32-row tiles: each lane reads a group's 32 codes with 16-byte loads
+    if (gate.bits == 4)
+      hipLaunchKernelGGL((chunk_gate_up32_kernel<4>), grid, dim3(256), 0, s, x, plan, top_k,
+                         gate, up, sgate, sup, h, hs);
+    else
+      hipLaunchKernelGGL((chunk_gate_up32_kernel<8>), grid, dim3(256), 0, s, x, plan, top_k,
+                         gate, up, sgate, sup, h, hs);
     return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
   }
   switch (gate.bits) {
@@ -875,6 +934,16 @@ int qmm_chunk_down(const uint16_t* h, const ChunkPlan* plan, const uint16_t* sco
   const int hs = inter > shared_inter ? inter : shared_inter;
   const dim3 grid((down.n + 255) / 256, chunk_max_items(rows, experts, top_k));
   const bool sx = (down.k >> 6) % 4 == 0 && (sdown.k >> 6) % 4 == 0;
+  if (sx && down.bits == sdown.bits && chunk_w32_ok(down.bits, down.k) &&
+      chunk_w32_ok(sdown.bits, sdown.k)) {
+    if (down.bits == 4)
+      hipLaunchKernelGGL((chunk_down32_kernel<4>), grid, dim3(256), 0, s, h, plan, scores, top_k,
+                         down, sdown, p, hs);
+    else
+      hipLaunchKernelGGL((chunk_down32_kernel<8>), grid, dim3(256), 0, s, h, plan, scores, top_k,
+                         down, sdown, p, hs);
+    return hipGetLastError() == hipSuccess ? MX_OK : MX_EHIP;
+  }
   switch (down.bits) {
 #define MX_DN(B)                                                                              \
   case B:                                                                                     \

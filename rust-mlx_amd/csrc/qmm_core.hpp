@@ -20,6 +20,8 @@
 // the matrix core (hardware order), then s * acc + (b - off*s) * sum(x) in fp32.
 #pragma once
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace mx {
@@ -348,7 +350,44 @@ __device__ __forceinline__ uint4 nibble_operand(uint32_t x) {
   return r;
 }
 
-template <int NT, int NTH>
+// A lane's 32 codes of group g in its half h: BITS words from byte 8 BITS g +
+// 4 BITS h of the row (value v at bit BITS v), in aligned 16-byte loads (4
+// and 8 bits; 5 / 6-bit pieces do not start on 16-byte boundaries, and
+// reading the two aligned pieces around them measured slower than the
+// 16-row form).
+template <int BITS>
+__device__ __forceinline__ void load_half_codes(const uint32_t* __restrict__ row, int g, int h,
+                                                uint32_t (&w)[BITS]) {
+  static_assert(BITS == 4 || BITS == 8, "16-byte pieces");
+#pragma unroll
+  for (int i = 0; i < BITS / 4; ++i) {
+    const uint4 v = reinterpret_cast<const uint4*>(row + 2 * BITS * g + BITS * h)[i];
+    w[4 * i] = v.x;
+    w[4 * i + 1] = v.y;
+    w[4 * i + 2] = v.z;
+    w[4 * i + 3] = v.w;
+  }
+}
+
+// B operand of MFMA step s (codes 8 s .. + 7 of the lane's 32) in permute_x
+// order, codes as exact bf16 integers (128 + q for 4 bits, q for 8 bits).
+template <int BITS, int S>
+__device__ __forceinline__ uint4 half_operand(const uint32_t (&w)[BITS]) {
+  if constexpr (BITS == 4) {
+    return nibble_operand(w[S]);
+  } else {
+    const uint32_t lo = w[2 * S], hi = w[2 * S + 1];
+    auto pair = [](float a, float b) { return __builtin_amdgcn_perm(f2u(b), f2u(a), 0x07060302u); };
+    uint4 r;
+    r.x = pair(float(lo & 0xffu), float(hi & 0xffu));
+    r.y = pair(float((lo >> 8) & 0xffu), float((hi >> 8) & 0xffu));
+    r.z = pair(float((lo >> 16) & 0xffu), float((hi >> 16) & 0xffu));
+    r.w = pair(float(lo >> 24), float(hi >> 24));
+    return r;
+  }
+}
+
+template <int BITS, int NT, int NTH>
 __device__ __forceinline__ void qmm_tiles32_sx(const TileRow (&tr)[NT], const uint16_t* xrow,
                                                uint16_t* xs, int lrow, int g0, int g1,
                                                floatx16_t (&y)[NT]) {
@@ -356,6 +395,7 @@ __device__ __forceinline__ void qmm_tiles32_sx(const TileRow (&tr)[NT], const ui
   constexpr int GB = 4;
   const int lane = threadIdx.x & 63;
   const int h = lane >> 5;
+  const float off = code_offset<BITS>();
   const uint4 ones = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
   const int sr = threadIdx.x >> 4, pc = threadIdx.x & 15;
   uint4 xn0 = make_uint4(0u, 0u, 0u, 0u), xn1 = xn0;
@@ -372,13 +412,12 @@ __device__ __forceinline__ void qmm_tiles32_sx(const TileRow (&tr)[NT], const ui
     *reinterpret_cast<uint4*>(xs + sr * kSxLd + 16 * pc) = xn0;
     *reinterpret_cast<uint4*>(xs + sr * kSxLd + 16 * pc + 8) = xn1;
     if (g + GB < g1) load_piece(g + GB);  // in flight during this batch
-    uint4 w[GB][NT];
+    uint32_t w[GB][NT][BITS];
     uint2 sc2[NT], bi2[NT];
 #pragma unroll
     for (int b = 0; b < GB; ++b)
 #pragma unroll
-      for (int t = 0; t < NT; ++t)
-        w[b][t] = *reinterpret_cast<const uint4*>(tr[t].codes + 8 * (g + b) + 4 * h);
+      for (int t = 0; t < NT; ++t) load_half_codes<BITS>(tr[t].codes, g + b, h, w[b][t]);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       if ((reinterpret_cast<uintptr_t>(tr[t].scales + g) & 7u) == 0 &&
@@ -411,11 +450,12 @@ __device__ __forceinline__ void qmm_tiles32_sx(const TileRow (&tr)[NT], const ui
         const uint32_t sw = b < 2 ? sc2[t].x : sc2[t].y;
         const uint32_t bw = b < 2 ? bi2[t].x : bi2[t].y;
         const float sc = u2f((b & 1) ? (sw & 0xffff0000u) : (sw << 16));
-        const float bi = fmaf_(-128.0f, sc, u2f((b & 1) ? (bw & 0xffff0000u) : (bw << 16)));
-        const uint32_t cw[4] = {w[b][t].x, w[b][t].y, w[b][t].z, w[b][t].w};
+        const float bi = fmaf_(-off, sc, u2f((b & 1) ? (bw & 0xffff0000u) : (bw << 16)));
         floatx16_t acc = {};
-#pragma unroll
-        for (int s = 0; s < 4; ++s) acc = mfma32_bf16(a[s], nibble_operand(cw[s]), acc);
+        acc = mfma32_bf16(a[0], half_operand<BITS, 0>(w[b][t]), acc);
+        acc = mfma32_bf16(a[1], half_operand<BITS, 1>(w[b][t]), acc);
+        acc = mfma32_bf16(a[2], half_operand<BITS, 2>(w[b][t]), acc);
+        acc = mfma32_bf16(a[3], half_operand<BITS, 3>(w[b][t]), acc);
 #pragma unroll
         for (int i = 0; i < 8; ++i) y[t][i] = fmaf_(sc, acc[i], fmaf_(bi, sx[i], y[t][i]));
       }

@@ -124,6 +124,35 @@ def test_moe_experts_mfma_prefill_chunk_rows(mx, orc, rows, E, top_k, H):
     assert np.mean(got == want) > 0.5
 
 
+@pytest.mark.parametrize("gbits,dbits,H,I", [(5, 6, 512, 512), (6, 8, 1024, 256),
+                                              (8, 4, 512, 768), (4, 5, 256, 1280)])
+def test_moe_experts_mfma_prefill_chunk_widths(mx, orc, gbits, dbits, H, I):
+    """The prefill chunk's expert kernels for every code width (4/8-bit: the
+    32-row tile forms, each lane reading a group's 32 codes of its half with
+    16-byte loads; 5/6-bit: the 16-row forms), at depths of 4..20 groups,
+    against the exact kernels eight rows at a time within the north star's
+    tolerance."""
+    from test_layers_gpu import Moe
+
+    E, top_k, rows = 32, 6, 40
+    m = Moe(mx, orc, E, I, H, seed=700 + gbits * 10 + dbits, gbits=gbits, dbits=dbits)
+    m.ws = mx.DeviceArray((mx.lib.mx_moe_workspace_bytes(rows, top_k, I),), np.uint8)
+    rng = np.random.default_rng(gbits * 10 + dbits)
+    ids = np.stack([rng.choice(E, top_k, replace=False) for _ in range(rows)]).astype(np.uint32)
+    scores = orc.f32_to_bf16(rng.uniform(0.05, 0.5, (rows, top_k)).astype(np.float32))
+    x = orc.fill_bf16(rows * H, 710 + gbits, 1, 1.0, 0.0).reshape(rows, H)
+    got = bf(_experts_mfma(mx, m, x, ids, scores, top_k)).astype(np.float64)
+    ws = m.ws
+    m.ws = mx.DeviceArray((mx.lib.mx_moe_workspace_bytes(8, top_k, I),), np.uint8)
+    want = np.concatenate([m.run(mx, x[r:r + 8], ids[r:r + 8], scores[r:r + 8], top_k)
+                           for r in range(0, rows, 8)])
+    m.ws = ws
+    want = bf(want).astype(np.float64)
+    scale = np.abs(want).max(axis=2, keepdims=True)
+    assert np.all(np.abs(got - want) <= 2e-2 * np.abs(want) + 1e-2 * scale)
+    assert np.mean(got == want) > 0.5
+
+
 @pytest.mark.parametrize("I,sI", [(1024, 512), (256, 768), (512, 512)])
 def test_moe_experts_mfma_mixed_depths(mx, orc, I, sI):
     """Routed and shared experts of different 256-multiple depths (the down
