@@ -269,17 +269,48 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const float* __restrict
     Sl[d * 17 + i] = sp[size_t(d) * kD + i];
   }
   __syncthreads();
-  for (int c = 0; c < nchunks; ++c) {
+  // a chunk's workspace operands of this lane; the next chunk's are
+  // requested before this chunk's work (they do not depend on the state)
+  struct ChunkOps {
+    float4 w[8], q[8], p[4], k[2][4];
+    float u[4];
+    float gc;
+  };
+  auto load_ops = [&](int c, ChunkOps& o) {
     const float* in = ws + ((size_t(grp) * hv + h) * nchunks + c) * kWsFloats;
+    const float4* wrow = reinterpret_cast<const float4*>(in + kWOff + (wave * 64 + lane) * 32);
+    const float4* qrow = reinterpret_cast<const float4*>(in + kQOff + (wave * 64 + lane) * 32);
+#pragma unroll
+    for (int k4 = 0; k4 < 8; ++k4) {
+      o.w[k4] = wrow[k4];
+      o.q[k4] = qrow[k4];
+    }
+    const float4* prow = reinterpret_cast<const float4*>(in + kPOff + (wave * 64 + lane) * 16);
+#pragma unroll
+    for (int k4 = 0; k4 < 4; ++k4) o.p[k4] = k4 <= wave ? prow[k4] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const float4* krow =
+          reinterpret_cast<const float4*>(in + kKOff + ((2 * wave + u) * 64 + lane) * 16);
+#pragma unroll
+      for (int k4 = 0; k4 < 4; ++k4) o.k[u][k4] = krow[k4];
+    }
+    const float* uo = in + kUOff;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o.u[r] = uo[(16 * wave + 4 * qd + r) * kD + i0 + j];
+    o.gc = in[kGOff];
+  };
+  ChunkOps cur, nxt;
+  load_ops(0, cur);
+  for (int c = 0; c < nchunks; ++c) {
+    if (c + 1 < nchunks) load_ops(c + 1, nxt);  // in flight during this chunk
     const int t0 = c * kC;
     const int len = min(kC, t - t0);
     // D = U - W S and the first part of O = (gamma Q) S, row tile `wave`
-    const float4* wrow = reinterpret_cast<const float4*>(in + kWOff + (wave * 64 + lane) * 32);
-    const float4* qrow = reinterpret_cast<const float4*>(in + kQOff + (wave * 64 + lane) * 32);
     floatx4_t dacc = {0.0f, 0.0f, 0.0f, 0.0f}, oacc = dacc;
 #pragma unroll
     for (int k4 = 0; k4 < 8; ++k4) {
-      const float4 wv = wrow[k4], qv = qrow[k4];
+      const float4 wv = cur.w[k4], qv = cur.q[k4];
       const float wa[4] = {wv.x, wv.y, wv.z, wv.w}, qa[4] = {qv.x, qv.y, qv.z, qv.w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -289,20 +320,18 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const float* __restrict
         oacc = mfma4(qa[e], sb, oacc);
       }
     }
-    const float* uo = in + kUOff;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int tr = 16 * wave + 4 * qd + r;
-      Dl[tr * 17 + j] = uo[tr * kD + i0 + j] - dacc[r];
+      Dl[tr * 17 + j] = cur.u[r] - dacc[r];
     }
-    const float gc = in[kGOff];
+    const float gc = cur.gc;
     __syncthreads();
     // O += P D (P lower triangular: k-steps up to the tile's diagonal)
-    const float4* prow = reinterpret_cast<const float4*>(in + kPOff + (wave * 64 + lane) * 16);
 #pragma unroll
     for (int k4 = 0; k4 < 4; ++k4) {
       if (k4 > wave) break;  // uniform per wave
-      const float4 pv = prow[k4];
+      const float4 pv = cur.p[k4];
       const float pa[4] = {pv.x, pv.y, pv.z, pv.w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -321,11 +350,10 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const float* __restrict
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int dt = 2 * wave + u;
-      const float4* krow = reinterpret_cast<const float4*>(in + kKOff + (dt * 64 + lane) * 16);
       floatx4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int k4 = 0; k4 < 4; ++k4) {
-        const float4 kv = krow[k4];
+        const float4 kv = cur.k[u][k4];
         const float ka[4] = {kv.x, kv.y, kv.z, kv.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -345,6 +373,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const float* __restrict
       for (int r = 0; r < 4; ++r) Sl[(16 * dt + 4 * qd + r) * 17 + j] = sacc[u][r];
     }
     __syncthreads();
+    cur = nxt;
   }
   for (int e = tid; e < kD * kSlice; e += 256) {
     const int d = e >> 4, i = e & 15;
