@@ -3,7 +3,7 @@
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 
 Workloads:
-  config3-b8-decode (default)  BASELINE config 3: the full synthetic hybrid
+  config3-b8-decode (default)  benchmark config 3: the full synthetic hybrid
       model (48 layers, 3:1 GatedDeltaNet : gated attention, 512-expert top-10
       MoE with a shared expert, hc = 4 hyper-connections, vocab 151936, 4-bit
       weights with 5-bit expert down and 8-bit embedding/head), 8 slots
@@ -12,26 +12,26 @@ Workloads:
       eight-token blocks), then batched greedy decode of all 8 rows per step (rows at their own
       offsets).  A step = one decode token for each of the 8 rows; W + K = 256
       steps per row by default.  value = aggregate tok/s over the K timed steps.
-  qmv-config0  BASELINE config 0: one affine 4-bit g64 QMV [4096, 2048] per
+  qmv-config0  benchmark config 0: one affine 4-bit g64 QMV [4096, 2048] per
       step, rotating >= 2 GiB of weight copies so the 256 MB Infinity Cache
       cannot serve repeats; value = achieved GB/s.
-  gdn-prefill-config1  BASELINE config 1 prefill: the chunked GatedDeltaNet
+  gdn-prefill-config1  benchmark config 1 prefill: the chunked GatedDeltaNet
       scan over T = 2048 tokens of one sequence (16 key / 32 value heads, head
       dim 128, config-1 inputs); a step = one whole scan (prep + chunk walk);
       value = tokens/s.  Roofline: fp32 matrix-core FLOPs of the chunked
       algorithm per scan over the scan time (MI355X fp32 MFMA 157.3 TFLOP/s);
       the sequential GPU scan (mx_gdn_scan) is timed beside it.
-  gdn-decode-config1  BASELINE config 1 decode: one fast-mode GatedDeltaNet
+  gdn-decode-config1  benchmark config 1 decode: one fast-mode GatedDeltaNet
       step (mx_gdn_recurrence_fast) at B = 1, 2, 4, 8 rows over a rotated 1 GiB
       fp32 state arena; value = B = 8 rows per second, roofline = state and
       q/k/v/y bytes over the step time.
-  moe-config2  BASELINE config 2: the decode MoE sublayer (router projection,
+  moe-config2  benchmark config 2: the decode MoE sublayer (router projection,
       routing, gathered expert gate/up and down, slot sum into the residual
       streams) at B = 1..8 rows; 32 rotated input batches; value = B = 8 rows
       per second, roofline = router + shared + distinct experts' bytes.
   prefill-config3  chunked prefill of one 2048-token prompt on the config-3
       model (512-token chunks on the matrix cores); value = prompt tokens/s.
-  mtp-config4  BASELINE config 4: MTP speculative generation (depth 3) on the
+  mtp-config4  benchmark config 4: MTP speculative generation (depth 3) on the
       mixed-width config-3 model, batch 1, 4096-token prompt, 256 tokens, timed
       against plain greedy decoding of the same prompt.
 

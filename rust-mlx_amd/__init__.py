@@ -398,7 +398,7 @@ def sync() -> None:
     check(lib.mx_device_sync())
 
 
-# ---- model configurations (BASELINE configs 3 and 4, and a tiny test model) ----
+# ---- model configurations (benchmark configs 3 and 4, and a tiny test model) ----
 MX_DT_U32, MX_DT_BF16, MX_DT_F16, MX_DT_F32 = 0, 1, 2, 3
 
 CONFIG3 = dict(hidden=2048, layers=48, attn_every=4, vocab=151936, hc=4, hc_rank=256, gdn_hk=16,

@@ -4,7 +4,7 @@ kernel, token by token) and the GPU sequential scan (mx_gdn_scan): the fp32
 state within 1e-4 relative (max norm) and y within 2e-2 relative / 1e-2
 absolute, the north star's tolerances.  Covers a single chunk, a partial last
 chunk, two sequences at once, a non-zero initial state, decays down to zero
-(a reset inside a chunk) and BASELINE config 1's prefill (T = 2048, 16 key /
+(a reset inside a chunk) and benchmark config 1's prefill (T = 2048, 16 key /
 32 value heads)."""
 import ctypes as C
 
@@ -73,7 +73,7 @@ def test_prefill_chunked_matches_sequential_oracle(mx, orc, hk, hv, groups, t, i
 
 
 def test_prefill_chunked_config1_t2048(mx, orc):
-    """BASELINE config 1 prefill: T = 2048, B = 1, 16 key / 32 value heads,
+    """benchmark config 1 prefill: T = 2048, B = 1, 16 key / 32 value heads,
     zero initial state; against the oracle and the GPU sequential scan."""
     hk, hv, t = 16, 32, 2048
     q, k, v, g, beta = inputs(orc, t, hk, hv, 2048)

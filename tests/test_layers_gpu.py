@@ -94,7 +94,7 @@ def test_experts_bit_exact_with_shared_experts_across_rows(mx, orc, rows):
 
 
 def test_experts_config2_shapes_and_batch_invariance(mx, orc):
-    """BASELINE config 2 geometry: 512 experts, inter 512, hidden 2048, top-10,
+    """benchmark config 2 geometry: 512 experts, inter 512, hidden 2048, top-10,
     4-bit gate/up, 5-bit down; rows routed by the router tail."""
     E, I, H, top_k = 512, 512, 2048, 10
     m = Moe(mx, orc, E, I, H, seed=500)

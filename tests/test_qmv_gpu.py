@@ -61,7 +61,7 @@ def test_qmv_bit_exact(mx, orc, bits, gs, k, n):
 
 
 def test_qmv_config0_exact_and_closed_form(mx, orc):
-    """x bf16 [1,2048] ~ N(0,1); W [4096,2048] 4-bit g64."""
+    """benchmark config 0: x bf16 [1,2048] ~ N(0,1); W [4096,2048] 4-bit g64."""
     n, k, bits, gs = 4096, 2048, 4, 64
     w = dev_q(mx, n, k, bits, gs, 100)
     codes, s, b = orc.random_qweight(n, k, bits, gs, 100)
